@@ -1,0 +1,367 @@
+"""fusiongpu_amd -- MI355X-native IVF-PQ search engine.
+
+Python host mirror of the C ABI in include/fusiongpu.h (libfusiongpu.so).
+Device buffers are torch tensors on the HIP device (torch is plumbing for
+memory and streams); every compute call goes to the HIP kernels in
+fusiongpu_amd/csrc.  There is no CPU fallback: importing this package raises
+if the library is not built.
+
+Reference interfaces mirrored (Hello-day/FusionGPU):
+  * Index.load / Index.from_arrays  -> load_ivf_index_to_gpu (search_pipeline.cu:481-529)
+  * Index.coarse_search             -> cuVS CAGRA top_m call (search_pipeline.cu:341)
+  * Index.adc_search                -> run_gpu_batch_logic with p1_lists = nprobe,
+                                       limit_k = rerank_m = k (gpu_global.cu:679-874)
+  * kmeans_fit / l2_topk            -> run_kmeans_gpu / batch_assign_clusters (kmeans_gpu.cuh:197-324)
+  * pq_train                        -> train_residual_pq_codebooks (pq_utils.h:77-138)
+  * pq_encode                       -> encode_residuals_to_pq_gpu (kmeans_gpu.cuh:450-508)
+  * build_ivfpq                     -> build_global main (build_global.cu:21-258), no rebalancing
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import numpy as np
+
+__all__ = [
+    "FgpuError", "lib", "lib_path", "Index", "gen_gmm", "l2_topk", "kmeans_fit", "kmeans_update",
+    "fixed_shift", "pq_train", "pq_encode", "build_ivfpq", "write_ivf_data", "read_ivf_data",
+    "write_fvecs", "read_fvecs", "read_ivecs", "probe_counts",
+]
+
+lib_path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib", "libfusiongpu.so")
+
+_c = ctypes
+_vp, _i32, _i64, _u64, _f32, _f64, _sz = (_c.c_void_p, _c.c_int, _c.c_int64, _c.c_uint64, _c.c_float,
+                                          _c.c_double, _c.c_size_t)
+
+_SIGS = {
+    "fgpu_last_error": (_c.c_char_p, []),
+    "fgpu_abi_version": (_i32, []),
+    "fgpu_index_create": (_i32, [_i32, _i32, _i32, _i64, _vp, _vp, _vp, _vp, _vp, _c.POINTER(_vp)]),
+    "fgpu_index_load": (_i32, [_c.c_char_p, _c.c_char_p, _i32, _i32, _c.POINTER(_vp)]),
+    "fgpu_index_destroy": (None, [_vp]),
+    "fgpu_index_get_info": (_i32, [_vp, _vp]),
+    "fgpu_coarse_workspace_bytes": (_sz, [_i32, _i32]),
+    "fgpu_coarse_search": (_i32, [_vp, _vp, _i32, _i32, _f32, _vp, _vp, _vp, _sz, _vp]),
+    "fgpu_probe_counts": (_i32, [_vp, _vp, _i32, _i32, _vp, _vp, _vp]),
+    "fgpu_adc_search": (_i32, [_vp, _vp, _i32, _vp, _i32, _i32, _vp, _vp, _vp]),
+    "fgpu_search_workspace_bytes": (_sz, [_i32, _i32, _i32]),
+    "fgpu_search": (_i32, [_vp, _vp, _i32, _i32, _i32, _f32, _vp, _vp, _vp, _sz, _vp]),
+    "fgpu_l2_topk_workspace_bytes": (_sz, [_i64, _i32]),
+    "fgpu_l2_topk": (_i32, [_vp, _i64, _vp, _i32, _i32, _i32, _vp, _vp, _vp, _sz, _vp]),
+    "fgpu_kmeans_workspace_bytes": (_sz, [_i32, _i32]),
+    "fgpu_kmeans_update": (_i32, [_vp, _i64, _vp, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _sz, _vp]),
+    "fgpu_fixed_shift": (_i32, [_f32, _i64]),
+    "fgpu_kmeans_fit": (_i32, [_vp, _i64, _i32, _i32, _i32, _i32, _u64, _vp, _vp, _vp]),
+    "fgpu_pq_train": (_i32, [_vp, _i64, _i32, _i32, _vp, _vp, _i32, _i32, _vp, _vp]),
+    "fgpu_pq_encode": (_i32, [_vp, _i64, _i32, _i32, _vp, _vp, _vp, _vp, _vp]),
+    "fgpu_build_ivfpq": (_i32, [_vp, _i64, _i32, _i32, _i32, _i32, _i32, _u64, _i32, _i32,
+                                _vp, _vp, _vp, _vp, _vp, _vp]),
+    "fgpu_write_ivf_data": (_i32, [_c.c_char_p, _i64, _i32, _i32, _i32, _vp, _vp, _vp, _vp]),
+    "fgpu_read_ivf_header": (_i32, [_c.c_char_p, _c.POINTER(_i64), _c.POINTER(_i32)]),
+    "fgpu_read_ivf_data": (_i32, [_c.c_char_p, _i32, _i32, _vp, _vp, _vp, _vp]),
+    "fgpu_write_fvecs": (_i32, [_c.c_char_p, _vp, _i64, _i32]),
+    "fgpu_read_fvecs": (_i32, [_c.c_char_p, _i32, _c.POINTER(_i64), _vp]),
+    "fgpu_read_ivecs": (_i32, [_c.c_char_p, _c.POINTER(_i32), _c.POINTER(_i64), _vp]),
+    "fgpu_gen_gmm": (None, [_i64, _i32, _i32, _f64, _f64, _f64, _f64, _u64, _i32, _vp, _i32]),
+}
+
+
+class FgpuError(RuntimeError):
+    """A libfusiongpu call returned a non-zero fgpu_status."""
+
+    def __init__(self, status: int, msg: str):
+        super().__init__(f"fgpu status {status}: {msg}")
+        self.status = status
+
+
+def _load():
+    if not os.path.exists(lib_path):
+        raise ImportError(f"{lib_path} is not built; run __graft_entry__.build() (hipcc for gfx950)")
+    l = ctypes.CDLL(lib_path)
+    for name, (res, args) in _SIGS.items():
+        f = getattr(l, name)
+        f.restype = res
+        f.argtypes = args
+    return l
+
+
+lib = _load()
+
+
+def _check(st: int):
+    if st != 0:
+        raise FgpuError(st, lib.fgpu_last_error().decode(errors="replace"))
+
+
+def _np_ptr(a: np.ndarray):
+    assert a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data_as(_vp)
+
+
+# --------------------------------------------------------------------------- torch plumbing
+def _torch():
+    import torch  # noqa: PLC0415 -- only needed for device buffers
+    return torch
+
+
+def _dev_ptr(t):
+    assert t.is_cuda and t.is_contiguous(), "expected a contiguous device tensor"
+    return _vp(t.data_ptr())
+
+
+def _stream(stream=None):
+    torch = _torch()
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return _vp(s.cuda_stream)
+
+
+def _workspace(nbytes: int):
+    torch = _torch()
+    return torch.empty(max(int(nbytes), 256), dtype=torch.uint8, device="cuda")
+
+
+def _to_dev(a, dtype=None):
+    torch = _torch()
+    if isinstance(a, np.ndarray):
+        return torch.from_numpy(np.ascontiguousarray(a)).to("cuda")
+    return a.contiguous()
+
+
+# --------------------------------------------------------------------------- synthetic data
+def gen_gmm(n: int, dim: int, ncomp: int, seed: int, set: int = 0, lo: float = -1.0, hi: float = 1.0,
+            sig_lo: float = 0.1, sig_hi: float | None = None, nthreads: int = 0) -> np.ndarray:
+    """Seeded Gaussian-mixture vectors [n][dim] float32 (set 0 = base, 1 = queries)."""
+    out = np.empty((n, dim), np.float32)
+    lib.fgpu_gen_gmm(n, dim, ncomp, lo, hi, sig_lo, sig_lo if sig_hi is None else sig_hi, seed, set,
+                     _np_ptr(out), nthreads)
+    return out
+
+
+# --------------------------------------------------------------------------- files
+def write_ivf_data(path, offsets, ids, codes, centroids):
+    offsets = np.ascontiguousarray(offsets, np.int32)
+    ids = np.ascontiguousarray(ids, np.int32)
+    codes = np.ascontiguousarray(codes, np.uint8)
+    centroids = np.ascontiguousarray(centroids, np.float32)
+    _check(lib.fgpu_write_ivf_data(str(path).encode(), ids.shape[0], offsets.shape[0] - 1, codes.shape[1],
+                                   centroids.shape[1], _np_ptr(offsets), _np_ptr(ids), _np_ptr(codes),
+                                   _np_ptr(centroids)))
+
+
+def read_ivf_data(path, pq_m: int, dim: int):
+    total, nlist = _i64(), _i32()
+    _check(lib.fgpu_read_ivf_header(str(path).encode(), _c.byref(total), _c.byref(nlist)))
+    offs = np.empty(nlist.value + 1, np.int32)
+    ids = np.empty(total.value, np.int32)
+    codes = np.empty((total.value, pq_m), np.uint8)
+    cent = np.empty((nlist.value, dim), np.float32)
+    _check(lib.fgpu_read_ivf_data(str(path).encode(), pq_m, dim, _np_ptr(offs), _np_ptr(ids), _np_ptr(codes),
+                                  _np_ptr(cent)))
+    return offs, ids, codes, cent
+
+
+def write_fvecs(path, v):
+    v = np.ascontiguousarray(v, np.float32)
+    _check(lib.fgpu_write_fvecs(str(path).encode(), _np_ptr(v), v.shape[0], v.shape[1]))
+
+
+def read_fvecs(path, dim: int) -> np.ndarray:
+    n = _i64()
+    _check(lib.fgpu_read_fvecs(str(path).encode(), dim, _c.byref(n), None))
+    out = np.empty((n.value, dim), np.float32)
+    _check(lib.fgpu_read_fvecs(str(path).encode(), dim, _c.byref(n), _np_ptr(out)))
+    return out
+
+
+def read_ivecs(path) -> np.ndarray:
+    d, n = _i32(), _i64()
+    _check(lib.fgpu_read_ivecs(str(path).encode(), _c.byref(d), _c.byref(n), None))
+    out = np.empty((n.value, d.value), np.int32)
+    _check(lib.fgpu_read_ivecs(str(path).encode(), _c.byref(d), _c.byref(n), _np_ptr(out)))
+    return out
+
+
+# --------------------------------------------------------------------------- index + search
+class _Info(ctypes.Structure):
+    _fields_ = [("dim", _i32), ("pq_m", _i32), ("pq_k", _i32), ("nlist", _i32), ("total", _i64),
+                ("d_pq_codebook", _vp), ("d_cluster_offsets", _vp), ("d_all_pq_codes", _vp),
+                ("d_all_vector_ids", _vp), ("d_centroids", _vp), ("max_list_len", _i32)]
+
+
+class Index:
+    """Device-resident IVF-PQ index (the reference's IVFIndexGPU, defs.h:51-58)."""
+
+    def __init__(self, handle):
+        self._h = _vp(handle)
+        info = _Info()
+        _check(lib.fgpu_index_get_info(self._h, _c.byref(info)))
+        self.dim, self.pq_m, self.nlist, self.total = info.dim, info.pq_m, info.nlist, info.total
+        self.max_list_len = info.max_list_len
+        self.info = info
+
+    @classmethod
+    def from_arrays(cls, dim, pq_m, offsets, ids, codes, centroids, codebook) -> "Index":
+        offsets = np.ascontiguousarray(offsets, np.int32)
+        ids = np.ascontiguousarray(ids, np.int32)
+        codes = np.ascontiguousarray(codes, np.uint8)
+        centroids = np.ascontiguousarray(centroids, np.float32)
+        codebook = np.ascontiguousarray(codebook, np.float32)
+        h = _vp()
+        _check(lib.fgpu_index_create(dim, pq_m, offsets.shape[0] - 1, ids.shape[0], _np_ptr(offsets), _np_ptr(ids),
+                                     _np_ptr(codes), _np_ptr(centroids), _np_ptr(codebook), _c.byref(h)))
+        return cls(h.value)
+
+    @classmethod
+    def load(cls, ivf_data_path, codebook_path, dim: int, pq_m: int) -> "Index":
+        h = _vp()
+        _check(lib.fgpu_index_load(str(ivf_data_path).encode(), str(codebook_path).encode(), dim, pq_m,
+                                   _c.byref(h)))
+        return cls(h.value)
+
+    def close(self):
+        if self._h:
+            lib.fgpu_index_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    # -- search
+    def coarse_workspace_bytes(self, nq: int) -> int:
+        return lib.fgpu_coarse_workspace_bytes(nq, self.nlist)
+
+    def coarse_search(self, queries, nprobe: int, prune_ratio: float = 100.0, workspace=None, out=None,
+                      stream=None):
+        """Exact top-nprobe lists: (probe_ids uint32-as-int32 [nq][nprobe], dists [nq][nprobe])."""
+        torch = _torch()
+        q = _to_dev(queries)
+        nq = q.shape[0]
+        ws = workspace if workspace is not None else _workspace(self.coarse_workspace_bytes(nq))
+        ids, d = out if out is not None else (torch.empty((nq, nprobe), dtype=torch.int32, device="cuda"),
+                                              torch.empty((nq, nprobe), dtype=torch.float32, device="cuda"))
+        _check(lib.fgpu_coarse_search(self._h, _dev_ptr(q), nq, nprobe, prune_ratio, _dev_ptr(ids), _dev_ptr(d),
+                                      _dev_ptr(ws), ws.numel(), _stream(stream)))
+        return ids, d
+
+    def adc_search(self, queries, probe_ids, k: int, out=None, stream=None):
+        """LUT + ADC scan + top-k over the probed lists: (ids int32 [nq][k], dists float32 [nq][k])."""
+        torch = _torch()
+        q = _to_dev(queries)
+        p = _to_dev(probe_ids)
+        nq, nprobe = p.shape
+        ids, d = out if out is not None else (torch.empty((nq, k), dtype=torch.int32, device="cuda"),
+                                              torch.empty((nq, k), dtype=torch.float32, device="cuda"))
+        _check(lib.fgpu_adc_search(self._h, _dev_ptr(q), nq, _dev_ptr(p), nprobe, k, _dev_ptr(ids), _dev_ptr(d),
+                                   _stream(stream)))
+        return ids, d
+
+    def search_workspace_bytes(self, nq: int, nprobe: int) -> int:
+        return lib.fgpu_search_workspace_bytes(nq, self.nlist, nprobe)
+
+    def search(self, queries, nprobe: int, k: int, prune_ratio: float = 100.0, workspace=None, out=None,
+               stream=None):
+        torch = _torch()
+        q = _to_dev(queries)
+        nq = q.shape[0]
+        ws = workspace if workspace is not None else _workspace(self.search_workspace_bytes(nq, nprobe))
+        ids, d = out if out is not None else (torch.empty((nq, k), dtype=torch.int32, device="cuda"),
+                                              torch.empty((nq, k), dtype=torch.float32, device="cuda"))
+        _check(lib.fgpu_search(self._h, _dev_ptr(q), nq, nprobe, k, prune_ratio, _dev_ptr(ids), _dev_ptr(d),
+                               _dev_ptr(ws), ws.numel(), _stream(stream)))
+        return ids, d
+
+
+def probe_counts(index: Index, probe_ids, stream=None):
+    torch = _torch()
+    p = _to_dev(probe_ids)
+    nq, nprobe = p.shape
+    counts = torch.empty(nq, dtype=torch.int32, device="cuda")
+    offs = torch.empty(nq + 1, dtype=torch.int32, device="cuda")
+    _check(lib.fgpu_probe_counts(index._h, _dev_ptr(p), nq, nprobe, _dev_ptr(counts), _dev_ptr(offs),
+                                 _stream(stream)))
+    return counts, offs
+
+
+# --------------------------------------------------------------------------- exact selection + build
+def l2_topk(x, c, p: int, stream=None):
+    """p nearest rows of c for each row of x by exact device-form L2: (ids, dists)."""
+    torch = _torch()
+    x, c = _to_dev(x), _to_dev(c)
+    n, dim = x.shape
+    nc = c.shape[0]
+    ws = _workspace(lib.fgpu_l2_topk_workspace_bytes(n, nc))
+    ids = torch.empty((n, p), dtype=torch.int32, device="cuda")
+    d = torch.empty((n, p), dtype=torch.float32, device="cuda")
+    _check(lib.fgpu_l2_topk(_dev_ptr(x), n, _dev_ptr(c), nc, dim, p, _dev_ptr(ids), _dev_ptr(d), _dev_ptr(ws),
+                            ws.numel(), _stream(stream)))
+    return ids, d
+
+
+def fixed_shift(maxabs: float, n: int) -> int:
+    return lib.fgpu_fixed_shift(maxabs, n)
+
+
+def kmeans_update(x, assign, centroids, shift: int, empty_rule: int = 0, stream=None):
+    """One deterministic Lloyd update in place on `centroids` (device); returns counts."""
+    torch = _torch()
+    x, a = _to_dev(x), _to_dev(assign)
+    n, dim = x.shape
+    k = centroids.shape[0]
+    ws = _workspace(lib.fgpu_kmeans_workspace_bytes(k, dim))
+    counts = torch.empty(k, dtype=torch.int32, device="cuda")
+    _check(lib.fgpu_kmeans_update(_dev_ptr(x), n, _dev_ptr(a), k, dim, shift, empty_rule, _dev_ptr(centroids),
+                                  _dev_ptr(counts), _dev_ptr(ws), ws.numel(), _stream(stream)))
+    return counts
+
+
+def kmeans_fit(x, k: int, iters: int, init_mode: int = 0, seed: int = 42, want_assign: bool = True, stream=None):
+    torch = _torch()
+    x = _to_dev(x)
+    n, dim = x.shape
+    cent = torch.empty((k, dim), dtype=torch.float32, device="cuda")
+    assign = torch.empty(n, dtype=torch.int32, device="cuda") if want_assign else None
+    _check(lib.fgpu_kmeans_fit(_dev_ptr(x), n, dim, k, iters, init_mode, seed, _dev_ptr(cent),
+                               _dev_ptr(assign) if want_assign else None, _stream(stream)))
+    return cent, assign
+
+
+def pq_train(x, assign, centroids, pq_m: int, sample_size: int = 50000, iters: int = 8, stream=None):
+    torch = _torch()
+    x, a, c = _to_dev(x), _to_dev(assign), _to_dev(centroids)
+    n, dim = x.shape
+    cb = torch.empty((pq_m, 256, dim // pq_m), dtype=torch.float32, device="cuda")
+    _check(lib.fgpu_pq_train(_dev_ptr(x), n, dim, pq_m, _dev_ptr(a), _dev_ptr(c), sample_size, iters,
+                             _dev_ptr(cb), _stream(stream)))
+    return cb
+
+
+def pq_encode(x, assign, centroids, codebook, stream=None):
+    torch = _torch()
+    x, a, c, cb = _to_dev(x), _to_dev(assign), _to_dev(centroids), _to_dev(codebook)
+    n, dim = x.shape
+    pq_m = cb.shape[0]
+    codes = torch.empty((n, pq_m), dtype=torch.uint8, device="cuda")
+    _check(lib.fgpu_pq_encode(_dev_ptr(x), n, dim, pq_m, _dev_ptr(a), _dev_ptr(c), _dev_ptr(cb), _dev_ptr(codes),
+                              _stream(stream)))
+    return codes
+
+
+def build_ivfpq(x, nlist: int, pq_m: int, kmeans_iters: int = 20, init_mode: int = 0, seed: int = 42,
+                pq_iters: int = 8, sample_size: int = 50000, stream=None):
+    """build_global without rebalancing: host arrays (offsets, ids, codes, centroids, codebook)."""
+    x = _to_dev(x)
+    n, dim = x.shape
+    offs = np.empty(nlist + 1, np.int32)
+    ids = np.empty(n, np.int32)
+    codes = np.empty((n, pq_m), np.uint8)
+    cent = np.empty((nlist, dim), np.float32)
+    cb = np.empty((pq_m, 256, dim // pq_m), np.float32)
+    _check(lib.fgpu_build_ivfpq(_dev_ptr(x), n, dim, nlist, pq_m, kmeans_iters, init_mode, seed, pq_iters,
+                                sample_size, _np_ptr(offs), _np_ptr(ids), _np_ptr(codes), _np_ptr(cent), _np_ptr(cb),
+                                _stream(stream)))
+    return offs, ids, codes, cent, cb

@@ -1,0 +1,560 @@
+// capi.cpp -- the extern "C" boundary (include/fusiongpu.h): index handle,
+// search and build orchestration, file formats and the synthetic generator.
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <fstream>
+#include <numeric>
+#include <random>
+#include <string>
+#include <thread>
+#include <vector>
+
+#include "common.hpp"
+#include "kernels.hpp"
+
+struct fgpu_index {
+  int dim = 0, m = 0, nlist = 0, max_list_len = 0;
+  int64_t total = 0;
+  float* d_codebook = nullptr;
+  int32_t* d_offsets = nullptr;
+  uint8_t* d_codes = nullptr;
+  int32_t* d_ids = nullptr;
+  float* d_centroids = nullptr;
+  float* d_cnorm = nullptr;      // [nlist] ||c||^2
+  float* d_cnorm_max = nullptr;  // [1]
+};
+
+namespace fgpu {
+
+thread_local std::string g_err;
+fgpu_status set_error(fgpu_status st, const std::string& msg) {
+  g_err = msg;
+  return st;
+}
+
+namespace {
+
+// RAII device buffer for the build path (search entry points never allocate).
+template <class T>
+struct DevBuf {
+  T* p = nullptr;
+  DevBuf() = default;
+  DevBuf(const DevBuf&) = delete;
+  DevBuf& operator=(const DevBuf&) = delete;
+  ~DevBuf() { if (p) (void)hipFree(p); }
+  fgpu_status alloc(size_t count) {
+    if (count == 0) count = 1;
+    if (hipMalloc(&p, count * sizeof(T)) != hipSuccess) {
+      p = nullptr;
+      (void)hipGetLastError();
+      return set_error(FGPU_ERR_NOMEM, "hipMalloc failed (" + std::to_string(count * sizeof(T)) + " bytes)");
+    }
+    return FGPU_OK;
+  }
+};
+
+void free_index(fgpu_index* ix) {
+  if (!ix) return;
+  for (void* p : {(void*)ix->d_codebook, (void*)ix->d_offsets, (void*)ix->d_codes, (void*)ix->d_ids,
+                  (void*)ix->d_centroids, (void*)ix->d_cnorm, (void*)ix->d_cnorm_max})
+    if (p) (void)hipFree(p);
+  delete ix;
+}
+
+int64_t topk_batch_rows(int64_t n, int nc) {
+  const size_t budget = 256ull << 20;  // estimate tile budget per batch
+  int64_t b = est_rows_per_batch(budget, nc);
+  if (b < 64) b = 64;
+  return std::min<int64_t>(b, ((n + 63) / 64) * 64);
+}
+
+// splitmix64 finaliser (same definition as the oracle's generator).
+inline uint64_t mix64(uint64_t z) {
+  z += 0x9E3779B97F4A7C15ull;
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}
+inline double u01(uint64_t seed, uint64_t stream, uint64_t idx) {
+  uint64_t h = mix64(seed ^ mix64(stream * 0xD1B54A32D192ED03ull + 0x632BE59BD9B4E019ull) ^ mix64(idx));
+  return (double)(h >> 11) * (1.0 / 9007199254740992.0);
+}
+
+}  // namespace
+}  // namespace fgpu
+
+using namespace fgpu;
+
+extern "C" {
+
+const char* fgpu_last_error(void) { return g_err.c_str(); }
+int fgpu_abi_version(void) { return 1; }
+
+// ---------------------------------------------------------------------------
+fgpu_status fgpu_index_create(int dim, int pq_m, int nlist, int64_t total, const int32_t* h_offsets,
+                              const int32_t* h_ids, const uint8_t* h_codes, const float* h_centroids,
+                              const float* h_codebook, fgpu_index** out) {
+  FGPU_CHECK(out && h_offsets && h_centroids && h_codebook, FGPU_ERR_ARG, "index_create: null argument");
+  FGPU_CHECK(total == 0 || (h_ids && h_codes), FGPU_ERR_ARG, "index_create: null ids/codes");
+  FGPU_CHECK(dim > 0 && pq_m > 0 && dim % pq_m == 0 && nlist > 0 && total >= 0 && total < INT32_MAX,
+             FGPU_ERR_ARG, "index_create: bad geometry");
+  FGPU_CHECK(h_offsets[0] == 0 && h_offsets[nlist] == total, FGPU_ERR_ARG,
+             "index_create: offsets must start at 0 and end at total");
+  int maxlen = 0;
+  for (int l = 0; l < nlist; ++l) {
+    const int len = h_offsets[l + 1] - h_offsets[l];
+    FGPU_CHECK(len >= 0, FGPU_ERR_ARG, "index_create: offsets not monotone");
+    maxlen = std::max(maxlen, len);
+  }
+  fgpu_index* ix = new fgpu_index();
+  ix->dim = dim; ix->m = pq_m; ix->nlist = nlist; ix->total = total; ix->max_list_len = maxlen;
+  auto fail = [&](fgpu_status st) { free_index(ix); return st; };
+  auto alloc = [&](void** p, size_t b) { return hipMalloc(p, b == 0 ? 256 : b) == hipSuccess; };
+  const size_t cb_bytes = (size_t)pq_m * kPQK * (dim / pq_m) * sizeof(float);
+  if (!alloc((void**)&ix->d_codebook, cb_bytes) || !alloc((void**)&ix->d_offsets, sizeof(int32_t) * (nlist + 1)) ||
+      !alloc((void**)&ix->d_codes, (size_t)total * pq_m + 256) || !alloc((void**)&ix->d_ids, sizeof(int32_t) * total) ||
+      !alloc((void**)&ix->d_centroids, sizeof(float) * (size_t)nlist * dim) ||
+      !alloc((void**)&ix->d_cnorm, sizeof(float) * nlist) || !alloc((void**)&ix->d_cnorm_max, 256)) {
+    (void)hipGetLastError();
+    return fail(set_error(FGPU_ERR_NOMEM, "index_create: device allocation failed"));
+  }
+  if (hipMemcpy(ix->d_codebook, h_codebook, cb_bytes, hipMemcpyHostToDevice) != hipSuccess ||
+      hipMemcpy(ix->d_offsets, h_offsets, sizeof(int32_t) * (nlist + 1), hipMemcpyHostToDevice) != hipSuccess ||
+      (total && hipMemcpy(ix->d_codes, h_codes, (size_t)total * pq_m, hipMemcpyHostToDevice) != hipSuccess) ||
+      (total && hipMemcpy(ix->d_ids, h_ids, sizeof(int32_t) * total, hipMemcpyHostToDevice) != hipSuccess) ||
+      hipMemcpy(ix->d_centroids, h_centroids, sizeof(float) * (size_t)nlist * dim, hipMemcpyHostToDevice) != hipSuccess)
+    return fail(set_error(FGPU_ERR_HIP, "index_create: copy to device failed"));
+  fgpu_status st = launch_row_norms(ix->d_centroids, nlist, dim, ix->d_cnorm, nullptr);
+  if (st == FGPU_OK) st = launch_max_reduce(ix->d_cnorm, nlist, ix->d_cnorm_max, nullptr);
+  if (st != FGPU_OK) return fail(st);
+  if (hipStreamSynchronize(nullptr) != hipSuccess) return fail(set_error(FGPU_ERR_HIP, "index_create: sync failed"));
+  *out = ix;
+  return FGPU_OK;
+}
+
+void fgpu_index_destroy(fgpu_index* idx) { free_index(idx); }
+
+fgpu_status fgpu_index_get_info(const fgpu_index* ix, fgpu_index_info* o) {
+  FGPU_CHECK(ix && o, FGPU_ERR_ARG, "index_get_info: null argument");
+  o->dim = ix->dim; o->pq_m = ix->m; o->pq_k = kPQK; o->nlist = ix->nlist; o->total = ix->total;
+  o->d_pq_codebook = ix->d_codebook; o->d_cluster_offsets = ix->d_offsets; o->d_all_pq_codes = ix->d_codes;
+  o->d_all_vector_ids = ix->d_ids; o->d_centroids = ix->d_centroids; o->max_list_len = ix->max_list_len;
+  return FGPU_OK;
+}
+
+fgpu_status fgpu_index_load(const char* ivf_path, const char* cb_path, int dim, int pq_m, fgpu_index** out) {
+  int64_t total = 0;
+  int nlist = 0;
+  FGPU_TRY(fgpu_read_ivf_header(ivf_path, &total, &nlist));
+  FGPU_CHECK(dim > 0 && pq_m > 0 && dim % pq_m == 0, FGPU_ERR_ARG, "index_load: bad geometry");
+  std::vector<int32_t> offs(nlist + 1), ids(total);
+  std::vector<uint8_t> codes((size_t)total * pq_m);
+  std::vector<float> cent((size_t)nlist * dim);
+  FGPU_TRY(fgpu_read_ivf_data(ivf_path, pq_m, dim, offs.data(), ids.data(), codes.data(), cent.data()));
+  std::ifstream f(cb_path, std::ios::binary | std::ios::ate);
+  FGPU_CHECK(f.good(), FGPU_ERR_IO, std::string("cannot open codebook: ") + cb_path);
+  const size_t want = (size_t)pq_m * kPQK * (dim / pq_m) * sizeof(float);
+  FGPU_CHECK((size_t)f.tellg() == want, FGPU_ERR_IO, "codebook file size does not match dim/pq_m");
+  std::vector<float> cb(want / sizeof(float));
+  f.seekg(0);
+  f.read(reinterpret_cast<char*>(cb.data()), want);
+  FGPU_CHECK(f.good(), FGPU_ERR_IO, "short read of codebook");
+  return fgpu_index_create(dim, pq_m, nlist, total, offs.data(), ids.data(), codes.data(), cent.data(), cb.data(), out);
+}
+
+// ---------------------------------------------------------------------------
+size_t fgpu_coarse_workspace_bytes(int nq, int nlist) {
+  return carve_bytes<float>((size_t)nq) + carve_bytes<float>((size_t)std::max(nq, 64) * nlist) + 256;
+}
+
+fgpu_status fgpu_coarse_search(const fgpu_index* ix, const float* dq, int nq, int nprobe, float prune_ratio,
+                               uint32_t* d_ids, float* d_dists, void* ws, size_t ws_bytes, void* stream) {
+  FGPU_CHECK(ix && dq && d_ids && d_dists && ws, FGPU_ERR_ARG, "coarse_search: null argument");
+  FGPU_CHECK(nq >= 0 && nprobe >= 1 && nprobe <= ix->nlist && nprobe <= 64, FGPU_ERR_ARG,
+             "coarse_search: need 1 <= nprobe <= min(nlist, 64)");
+  if (nq == 0) return FGPU_OK;
+  hipStream_t s = as_stream(stream);
+  Carve cv(ws, ws_bytes);
+  float* xn = cv.take<float>(nq);
+  const size_t rest = ws_bytes > cv.used ? ws_bytes - cv.used : 0;
+  int64_t rows = std::min<int64_t>(est_rows_per_batch(rest > 256 ? rest - 256 : 0, ix->nlist), ((nq + 63) / 64) * 64);
+  FGPU_CHECK(xn && rows >= 64, FGPU_ERR_WORKSPACE, "coarse_search: workspace too small");
+  float* est = cv.take<float>((size_t)rows * ix->nlist);
+  FGPU_CHECK(est, FGPU_ERR_WORKSPACE, "coarse_search: workspace too small");
+  FGPU_TRY(launch_row_norms(dq, nq, ix->dim, xn, s));
+  for (int64_t b0 = 0; b0 < nq; b0 += rows) {
+    const int64_t nb = std::min<int64_t>(rows, nq - b0);
+    FGPU_TRY(launch_gemm_est(dq + b0 * ix->dim, nb, ix->d_centroids, ix->nlist, ix->dim, xn + b0, ix->d_cnorm, est,
+                             ix->nlist, s));
+    FGPU_TRY(launch_select_exact(est, ix->nlist, nb, ix->nlist, dq + b0 * ix->dim, ix->d_centroids, ix->dim, xn + b0,
+                                 ix->d_cnorm_max, nprobe, 1, prune_ratio,
+                                 reinterpret_cast<int32_t*>(d_ids) + b0 * nprobe, d_dists + b0 * nprobe, s));
+  }
+  return FGPU_OK;
+}
+
+fgpu_status fgpu_probe_counts(const fgpu_index* ix, const uint32_t* d_probe_ids, int nq, int nprobe, int32_t* d_counts,
+                              int32_t* d_offsets, void* stream) {
+  FGPU_CHECK(ix && d_probe_ids && d_counts && d_offsets && nq >= 0 && nprobe >= 1, FGPU_ERR_ARG,
+             "probe_counts: bad argument");
+  return launch_probe_counts(d_probe_ids, nq, nprobe, ix->nlist, ix->d_offsets, d_counts, d_offsets, as_stream(stream));
+}
+
+fgpu_status fgpu_adc_search(const fgpu_index* ix, const float* dq, int nq, const uint32_t* d_probe_ids, int nprobe,
+                            int k, int32_t* d_out_ids, float* d_out_dists, void* stream) {
+  FGPU_CHECK(ix && dq && d_probe_ids && d_out_ids && d_out_dists, FGPU_ERR_ARG, "adc_search: null argument");
+  FGPU_CHECK(nq >= 0 && nprobe >= 1 && k >= 1, FGPU_ERR_ARG, "adc_search: bad sizes");
+  FGPU_CHECK(adc_supported(ix->dim, ix->m), FGPU_ERR_UNSUPPORTED, "adc_search: no kernel for this (dim, pq_m)");
+  AdcArgs a{dq, ix->d_centroids, ix->d_codebook, ix->d_offsets, ix->d_codes, ix->d_ids, d_probe_ids,
+            nq, nprobe, k, ix->nlist, d_out_ids, d_out_dists};
+  return launch_adc_plain(ix->dim, ix->m, a, as_stream(stream));
+}
+
+size_t fgpu_search_workspace_bytes(int nq, int nlist, int nprobe) {
+  return carve_bytes<uint32_t>((size_t)nq * nprobe) + carve_bytes<float>((size_t)nq * nprobe) +
+         fgpu_coarse_workspace_bytes(nq, nlist);
+}
+
+fgpu_status fgpu_search(const fgpu_index* ix, const float* dq, int nq, int nprobe, int k, float prune_ratio,
+                        int32_t* d_out_ids, float* d_out_dists, void* ws, size_t ws_bytes, void* stream) {
+  FGPU_CHECK(ix && ws, FGPU_ERR_ARG, "search: null argument");
+  Carve cv(ws, ws_bytes);
+  uint32_t* pid = cv.take<uint32_t>((size_t)nq * nprobe);
+  float* pd = cv.take<float>((size_t)nq * nprobe);
+  FGPU_CHECK(cv.ok(), FGPU_ERR_WORKSPACE, "search: workspace too small");
+  FGPU_TRY(fgpu_coarse_search(ix, dq, nq, nprobe, prune_ratio, pid, pd, cv.base + cv.used, ws_bytes - cv.used, stream));
+  return fgpu_adc_search(ix, dq, nq, pid, nprobe, k, d_out_ids, d_out_dists, stream);
+}
+
+// ---------------------------------------------------------------------------
+size_t fgpu_l2_topk_workspace_bytes(int64_t n, int nc) {
+  return carve_bytes<float>(n) + carve_bytes<float>(nc) + 256 + carve_bytes<float>((size_t)topk_batch_rows(n, nc) * nc);
+}
+
+fgpu_status fgpu_l2_topk(const float* dx, int64_t n, const float* dc, int nc, int dim, int p, int32_t* d_ids,
+                         float* d_dists, void* ws, size_t ws_bytes, void* stream) {
+  FGPU_CHECK(dx && dc && d_ids && d_dists && ws, FGPU_ERR_ARG, "l2_topk: null argument");
+  FGPU_CHECK(n >= 0 && nc >= 1 && dim >= 1 && p >= 1 && p <= nc && p <= 64, FGPU_ERR_ARG, "l2_topk: bad sizes");
+  if (n == 0) return FGPU_OK;
+  hipStream_t s = as_stream(stream);
+  Carve cv(ws, ws_bytes);
+  float* xn = cv.take<float>(n);
+  float* cn = cv.take<float>(nc);
+  float* cmax = cv.take<float>(64);
+  FGPU_CHECK(cv.ok(), FGPU_ERR_WORKSPACE, "l2_topk: workspace too small");
+  const size_t rest = ws_bytes - cv.used;
+  const int64_t rows = std::min<int64_t>(est_rows_per_batch(rest, nc), ((n + 63) / 64) * 64);
+  FGPU_CHECK(rows >= 64, FGPU_ERR_WORKSPACE, "l2_topk: workspace too small");
+  float* est = cv.take<float>((size_t)rows * nc);
+  FGPU_TRY(launch_row_norms(dx, n, dim, xn, s));
+  FGPU_TRY(launch_row_norms(dc, nc, dim, cn, s));
+  FGPU_TRY(launch_max_reduce(cn, nc, cmax, s));
+  for (int64_t b0 = 0; b0 < n; b0 += rows) {
+    const int64_t nb = std::min<int64_t>(rows, n - b0);
+    FGPU_TRY(launch_gemm_est(dx + b0 * dim, nb, dc, nc, dim, xn + b0, cn, est, nc, s));
+    FGPU_TRY(launch_select_exact(est, nc, nb, nc, dx + b0 * dim, dc, dim, xn + b0, cmax, p, 0, 0.0f, d_ids + b0 * p,
+                                 d_dists + b0 * p, s));
+  }
+  return FGPU_OK;
+}
+
+// ---------------------------------------------------------------------------
+int fgpu_fixed_shift(float maxabs, int64_t n) {
+  int e = 0;
+  if (maxabs > 0.0f) std::frexp((double)maxabs, &e);
+  int lg = 0;
+  while ((1LL << lg) < (n > 0 ? n : 1)) ++lg;
+  int s = 61 - lg - e;
+  return s < 0 ? 0 : (s > 60 ? 60 : s);
+}
+
+size_t fgpu_kmeans_workspace_bytes(int k, int dim) {
+  return carve_bytes<unsigned long long>((size_t)k * dim) + carve_bytes<int32_t>(k);
+}
+
+fgpu_status fgpu_kmeans_update(const float* dx, int64_t n, const int32_t* d_assign, int k, int dim, int shift,
+                               int empty_rule, float* d_cent, int32_t* d_counts, void* ws, size_t ws_bytes,
+                               void* stream) {
+  FGPU_CHECK(dx && d_assign && d_cent && ws && k >= 1 && dim >= 1 && n >= 0, FGPU_ERR_ARG, "kmeans_update: bad argument");
+  hipStream_t s = as_stream(stream);
+  Carve cv(ws, ws_bytes);
+  auto* sums = cv.take<unsigned long long>((size_t)k * dim);
+  int32_t* cnt = cv.take<int32_t>(k);
+  FGPU_CHECK(cv.ok(), FGPU_ERR_WORKSPACE, "kmeans_update: workspace too small");
+  if (d_counts) cnt = d_counts;
+  FGPU_TRY(launch_kmeans_accumulate(dx, n, d_assign, k, dim, shift, sums, cnt, s));
+  return launch_kmeans_finalize(sums, cnt, k, dim, shift, empty_rule, d_cent, s);
+}
+
+fgpu_status fgpu_kmeans_fit(const float* dx, int64_t n, int dim, int k, int iters, int init_mode, uint64_t seed,
+                            float* d_cent, int32_t* d_assign_out, void* stream) {
+  FGPU_CHECK(dx && d_cent && n >= 1 && dim >= 1 && k >= 1 && k <= n && iters >= 0, FGPU_ERR_ARG,
+             "kmeans_fit: bad argument");
+  FGPU_CHECK(init_mode == 0 || init_mode == 1, FGPU_ERR_ARG, "kmeans_fit: init_mode must be 0 or 1");
+  hipStream_t s = as_stream(stream);
+  // fixed-point shift from max |x|
+  DevBuf<float> scratch;
+  FGPU_TRY(scratch.alloc(1024));
+  FGPU_TRY(launch_maxabs(dx, n * dim, scratch.p, s));
+  float maxabs = 0.0f;
+  FGPU_HIP(hipMemcpyAsync(&maxabs, scratch.p + 1023, sizeof(float), hipMemcpyDeviceToHost, s));
+  FGPU_HIP(hipStreamSynchronize(s));
+  const int shift = fgpu_fixed_shift(maxabs, n);
+
+  DevBuf<int32_t> rows;
+  FGPU_TRY(rows.alloc(k));
+  if (init_mode == 0) {
+    // run_kmeans_gpu's initialisation (kmeans_gpu.cuh:259-267)
+    std::vector<int32_t> h(k);
+    std::mt19937 rng((unsigned)seed);
+    const int64_t stride = std::max<int64_t>(1, n / k);
+    for (int i = 0; i < k; ++i)
+      h[i] = (int32_t)(((int64_t)i * stride + (int64_t)(rng() % (unsigned long long)stride)) % n);
+    FGPU_HIP(hipMemcpyAsync(rows.p, h.data(), sizeof(int32_t) * k, hipMemcpyHostToDevice, s));
+    FGPU_TRY(launch_gather_rows(dx, dim, rows.p, k, d_cent, s));
+    FGPU_HIP(hipStreamSynchronize(s));
+  } else {
+    DevBuf<char> pws;
+    const size_t b = kmeans_pp_ws_bytes(n);
+    FGPU_TRY(pws.alloc(b));
+    FGPU_TRY(launch_kmeans_pp(dx, n, dim, k, seed, d_cent, rows.p, pws.p, b, s));
+    FGPU_HIP(hipStreamSynchronize(s));
+  }
+  DevBuf<int32_t> assign;
+  DevBuf<float> dist;
+  DevBuf<char> tws, kws;
+  const size_t tb = fgpu_l2_topk_workspace_bytes(n, k), kb = fgpu_kmeans_workspace_bytes(k, dim);
+  FGPU_TRY(assign.alloc(n));
+  FGPU_TRY(dist.alloc(n));
+  FGPU_TRY(tws.alloc(tb));
+  FGPU_TRY(kws.alloc(kb));
+  for (int it = 0; it < iters; ++it) {
+    FGPU_TRY(fgpu_l2_topk(dx, n, d_cent, k, dim, 1, assign.p, dist.p, tws.p, tb, stream));
+    FGPU_TRY(fgpu_kmeans_update(dx, n, assign.p, k, dim, shift, 0, d_cent, nullptr, kws.p, kb, stream));
+  }
+  if (d_assign_out) FGPU_TRY(fgpu_l2_topk(dx, n, d_cent, k, dim, 1, d_assign_out, dist.p, tws.p, tb, stream));
+  FGPU_HIP(hipStreamSynchronize(s));
+  return FGPU_OK;
+}
+
+fgpu_status fgpu_pq_train(const float* dx, int64_t n, int dim, int pq_m, const int32_t* d_assign, const float* d_cent,
+                          int sample_size, int iters, float* d_codebook, void* stream) {
+  FGPU_CHECK(dx && d_assign && d_cent && d_codebook && n >= 1 && pq_m >= 1 && dim % pq_m == 0 && iters >= 0,
+             FGPU_ERR_ARG, "pq_train: bad argument");
+  hipStream_t s = as_stream(stream);
+  // sample rows (pq_utils.h:91-97)
+  const int actual = (int)std::min<int64_t>(sample_size, n);
+  FGPU_CHECK(actual >= kPQK, FGPU_ERR_ARG, "pq_train: need at least 256 sample rows");
+  std::vector<int32_t> idx(n);
+  std::iota(idx.begin(), idx.end(), 0);
+  {
+    std::mt19937 rng(12345);
+    std::shuffle(idx.begin(), idx.end(), rng);
+  }
+  idx.resize(actual);
+  // per-subspace initial rows (pq_utils.h:20-31, seed 1234+m)
+  std::vector<int32_t> init((size_t)pq_m * kPQK);
+  {
+    std::vector<int> ind(actual);
+    for (int sub = 0; sub < pq_m; ++sub) {
+      std::iota(ind.begin(), ind.end(), 0);
+      std::mt19937 rng(1234 + sub);
+      std::shuffle(ind.begin(), ind.end(), rng);
+      std::copy(ind.begin(), ind.begin() + kPQK, init.begin() + (size_t)sub * kPQK);
+    }
+  }
+  DevBuf<int32_t> drows, dinit, dassign;
+  DevBuf<float> res;
+  FGPU_TRY(drows.alloc(actual));
+  FGPU_TRY(dinit.alloc(init.size()));
+  FGPU_TRY(dassign.alloc((size_t)actual * pq_m));
+  FGPU_TRY(res.alloc((size_t)actual * dim));
+  FGPU_HIP(hipMemcpyAsync(drows.p, idx.data(), sizeof(int32_t) * actual, hipMemcpyHostToDevice, s));
+  FGPU_HIP(hipMemcpyAsync(dinit.p, init.data(), sizeof(int32_t) * init.size(), hipMemcpyHostToDevice, s));
+  FGPU_TRY(launch_pq_residuals(dx, dim, drows.p, actual, d_assign, d_cent, res.p, s));
+  FGPU_TRY(launch_pq_init(res.p, actual, dim, pq_m, dinit.p, d_codebook, s));
+  for (int it = 0; it < iters; ++it) {
+    FGPU_TRY(launch_pq_estep(res.p, actual, dim, pq_m, d_codebook, dassign.p, s));
+    FGPU_TRY(launch_pq_mstep(res.p, actual, dim, pq_m, dassign.p, d_codebook, s));
+  }
+  FGPU_HIP(hipStreamSynchronize(s));
+  return FGPU_OK;
+}
+
+fgpu_status fgpu_pq_encode(const float* dx, int64_t n, int dim, int pq_m, const int32_t* d_assign,
+                           const float* d_cent, const float* d_codebook, uint8_t* d_codes, void* stream) {
+  FGPU_CHECK(dx && d_assign && d_cent && d_codebook && d_codes && n >= 0 && pq_m >= 1 && dim % pq_m == 0,
+             FGPU_ERR_ARG, "pq_encode: bad argument");
+  return launch_pq_encode(dx, n, dim, pq_m, d_assign, d_cent, d_codebook, d_codes, as_stream(stream));
+}
+
+fgpu_status fgpu_build_ivfpq(const float* dx, int64_t n, int dim, int nlist, int pq_m, int kmeans_iters, int init_mode,
+                             uint64_t seed, int pq_iters, int sample_size, int32_t* h_offsets, int32_t* h_ids,
+                             uint8_t* h_codes, float* h_centroids, float* h_codebook, void* stream) {
+  FGPU_CHECK(dx && h_offsets && h_ids && h_codes && h_centroids && h_codebook, FGPU_ERR_ARG, "build: null argument");
+  FGPU_CHECK(n < INT32_MAX, FGPU_ERR_ARG, "build: more than 2^31-1 vectors");
+  hipStream_t s = as_stream(stream);
+  DevBuf<float> cent, cb;
+  DevBuf<int32_t> assign;
+  DevBuf<uint8_t> codes;
+  FGPU_TRY(cent.alloc((size_t)nlist * dim));
+  FGPU_TRY(cb.alloc((size_t)pq_m * kPQK * (dim / pq_m)));
+  FGPU_TRY(assign.alloc(n));
+  FGPU_TRY(codes.alloc((size_t)n * pq_m));
+  FGPU_TRY(fgpu_kmeans_fit(dx, n, dim, nlist, kmeans_iters, init_mode, seed, cent.p, assign.p, stream));
+  FGPU_TRY(fgpu_pq_train(dx, n, dim, pq_m, assign.p, cent.p, sample_size, pq_iters, cb.p, stream));
+  FGPU_TRY(fgpu_pq_encode(dx, n, dim, pq_m, assign.p, cent.p, cb.p, codes.p, stream));
+  std::vector<int32_t> ha(n);
+  std::vector<uint8_t> hc((size_t)n * pq_m);
+  FGPU_HIP(hipMemcpyAsync(ha.data(), assign.p, sizeof(int32_t) * n, hipMemcpyDeviceToHost, s));
+  FGPU_HIP(hipMemcpyAsync(hc.data(), codes.p, hc.size(), hipMemcpyDeviceToHost, s));
+  FGPU_HIP(hipMemcpyAsync(h_centroids, cent.p, sizeof(float) * (size_t)nlist * dim, hipMemcpyDeviceToHost, s));
+  FGPU_HIP(hipMemcpyAsync(h_codebook, cb.p, sizeof(float) * (size_t)pq_m * kPQK * (dim / pq_m), hipMemcpyDeviceToHost, s));
+  FGPU_HIP(hipStreamSynchronize(s));
+  // inverted lists in cluster order, ids ascending inside a list (build_global.cu:225-240)
+  std::vector<int64_t> cnt(nlist + 1, 0);
+  for (int64_t i = 0; i < n; ++i) cnt[ha[i] + 1]++;
+  for (int l = 0; l < nlist; ++l) cnt[l + 1] += cnt[l];
+  for (int l = 0; l <= nlist; ++l) h_offsets[l] = (int32_t)cnt[l];
+  std::vector<int64_t> pos(cnt.begin(), cnt.end() - 1);
+  for (int64_t i = 0; i < n; ++i) {
+    const int64_t pp = pos[ha[i]]++;
+    h_ids[pp] = (int32_t)i;
+    std::memcpy(h_codes + pp * pq_m, hc.data() + i * pq_m, pq_m);
+  }
+  return FGPU_OK;
+}
+
+// ---------------------------------------------------------------------------
+fgpu_status fgpu_write_ivf_data(const char* path, int64_t total, int nlist, int pq_m, int dim, const int32_t* offsets,
+                                const int32_t* ids, const uint8_t* codes, const float* centroids) {
+  FGPU_CHECK(path && offsets && centroids && total >= 0 && total < INT32_MAX, FGPU_ERR_ARG, "write_ivf_data: bad argument");
+  std::ofstream f(path, std::ios::binary);
+  FGPU_CHECK(f.good(), FGPU_ERR_IO, std::string("cannot create ") + path);
+  const int32_t t32 = (int32_t)total, nl = nlist;
+  f.write(reinterpret_cast<const char*>(&t32), 4);
+  f.write(reinterpret_cast<const char*>(&nl), 4);
+  f.write(reinterpret_cast<const char*>(offsets), sizeof(int32_t) * (nlist + 1));
+  f.write(reinterpret_cast<const char*>(ids), sizeof(int32_t) * total);
+  f.write(reinterpret_cast<const char*>(codes), (size_t)total * pq_m);
+  f.write(reinterpret_cast<const char*>(centroids), sizeof(float) * (size_t)nlist * dim);
+  FGPU_CHECK(f.good(), FGPU_ERR_IO, "write_ivf_data: write failed");
+  return FGPU_OK;
+}
+
+fgpu_status fgpu_read_ivf_header(const char* path, int64_t* total, int* nlist) {
+  std::ifstream f(path, std::ios::binary);
+  FGPU_CHECK(f.good(), FGPU_ERR_IO, std::string("cannot open ") + (path ? path : "(null)"));
+  int32_t t = 0, nl = 0;
+  f.read(reinterpret_cast<char*>(&t), 4);
+  f.read(reinterpret_cast<char*>(&nl), 4);
+  FGPU_CHECK(f.good() && t >= 0 && nl > 0, FGPU_ERR_IO, "ivf_data.bin: bad header");
+  *total = t;
+  *nlist = nl;
+  return FGPU_OK;
+}
+
+fgpu_status fgpu_read_ivf_data(const char* path, int pq_m, int dim, int32_t* offsets, int32_t* ids, uint8_t* codes,
+                               float* centroids) {
+  int64_t total = 0;
+  int nlist = 0;
+  FGPU_TRY(fgpu_read_ivf_header(path, &total, &nlist));
+  std::ifstream f(path, std::ios::binary | std::ios::ate);
+  const int64_t size = (int64_t)f.tellg();
+  const int64_t want = 8 + 4 * (int64_t)(nlist + 1) + 4 * total + total * pq_m + 4 * (int64_t)nlist * dim;
+  FGPU_CHECK(size == want, FGPU_ERR_IO,
+             "ivf_data.bin: size " + std::to_string(size) + " != expected " + std::to_string(want) +
+                 " for the stated dim/pq_m");
+  f.seekg(8);
+  f.read(reinterpret_cast<char*>(offsets), sizeof(int32_t) * (nlist + 1));
+  f.read(reinterpret_cast<char*>(ids), sizeof(int32_t) * total);
+  f.read(reinterpret_cast<char*>(codes), (size_t)total * pq_m);
+  f.read(reinterpret_cast<char*>(centroids), sizeof(float) * (size_t)nlist * dim);
+  FGPU_CHECK(f.good(), FGPU_ERR_IO, "ivf_data.bin: short read");
+  return FGPU_OK;
+}
+
+fgpu_status fgpu_write_fvecs(const char* path, const float* v, int64_t n, int dim) {
+  std::ofstream f(path, std::ios::binary);
+  FGPU_CHECK(f.good(), FGPU_ERR_IO, std::string("cannot create ") + path);
+  for (int64_t i = 0; i < n; ++i) {
+    f.write(reinterpret_cast<const char*>(&dim), 4);
+    f.write(reinterpret_cast<const char*>(v + i * dim), sizeof(float) * dim);
+  }
+  FGPU_CHECK(f.good(), FGPU_ERR_IO, "write_fvecs: write failed");
+  return FGPU_OK;
+}
+
+fgpu_status fgpu_read_fvecs(const char* path, int dim, int64_t* n, float* out) {
+  std::ifstream f(path, std::ios::binary | std::ios::ate);
+  FGPU_CHECK(f.good(), FGPU_ERR_IO, std::string("cannot open ") + (path ? path : "(null)"));
+  const int64_t size = (int64_t)f.tellg();
+  f.seekg(0);
+  int32_t d = 0;
+  f.read(reinterpret_cast<char*>(&d), 4);
+  FGPU_CHECK(f.good() && d == dim, FGPU_ERR_IO,
+             "fvecs dimension mismatch: expected " + std::to_string(dim) + ", got " + std::to_string(d));
+  const int64_t rec = 4 + 4 * (int64_t)dim;
+  *n = size / rec;
+  if (!out) return FGPU_OK;
+  f.seekg(0);
+  for (int64_t i = 0; i < *n; ++i) {
+    f.seekg(4, std::ios::cur);
+    f.read(reinterpret_cast<char*>(out + i * dim), sizeof(float) * dim);
+  }
+  FGPU_CHECK(f.good(), FGPU_ERR_IO, "fvecs: short read");
+  return FGPU_OK;
+}
+
+fgpu_status fgpu_read_ivecs(const char* path, int* dim, int64_t* n, int32_t* out) {
+  std::ifstream f(path, std::ios::binary | std::ios::ate);
+  FGPU_CHECK(f.good(), FGPU_ERR_IO, std::string("cannot open ") + (path ? path : "(null)"));
+  const int64_t size = (int64_t)f.tellg();
+  f.seekg(0);
+  int32_t d = 0;
+  f.read(reinterpret_cast<char*>(&d), 4);
+  FGPU_CHECK(f.good() && d > 0, FGPU_ERR_IO, "ivecs: bad header");
+  *dim = d;
+  *n = size / (4 + 4 * (int64_t)d);
+  if (!out) return FGPU_OK;
+  f.seekg(0);
+  for (int64_t i = 0; i < *n; ++i) {
+    f.seekg(4, std::ios::cur);
+    f.read(reinterpret_cast<char*>(out + i * d), sizeof(int32_t) * d);
+  }
+  FGPU_CHECK(f.good(), FGPU_ERR_IO, "ivecs: short read");
+  return FGPU_OK;
+}
+
+// ---------------------------------------------------------------------------
+void fgpu_gen_gmm(int64_t n, int dim, int ncomp, double lo, double hi, double sig_lo, double sig_hi, uint64_t seed,
+                  int set, float* out, int nthreads) {
+  std::vector<double> centre((size_t)ncomp * dim), sigma(ncomp);
+  for (int64_t j = 0; j < (int64_t)ncomp * dim; ++j) centre[j] = lo + (hi - lo) * u01(seed, 1, j);
+  for (int j = 0; j < ncomp; ++j) sigma[j] = sig_lo + (sig_hi - sig_lo) * u01(seed, 2, j);
+  const uint64_t s_lab = 3 + 2 * (uint64_t)set, s_noise = 4 + 2 * (uint64_t)set;
+  auto rows = [&](int64_t r0, int64_t r1) {
+    for (int64_t i = r0; i < r1; ++i) {
+      int lab = (int)(u01(seed, s_lab, i) * ncomp);
+      if (lab >= ncomp) lab = ncomp - 1;
+      for (int d = 0; d < dim; ++d) {
+        const uint64_t e = (uint64_t)i * dim + d;
+        const uint64_t pr = e >> 1;
+        const double a = u01(seed, s_noise, 2 * pr), b = u01(seed, s_noise, 2 * pr + 1);
+        const double rad = std::sqrt(-2.0 * std::log(1.0 - a));
+        const double ang = 6.283185307179586476925286766559 * b;
+        const double z = (e & 1) ? rad * std::sin(ang) : rad * std::cos(ang);
+        out[e] = (float)(centre[(size_t)lab * dim + d] + sigma[lab] * z);
+      }
+    }
+  };
+  int nt = nthreads > 0 ? nthreads : (int)std::max(1u, std::min(16u, std::thread::hardware_concurrency()));
+  if (n < 4096) nt = 1;
+  std::vector<std::thread> th;
+  for (int t = 0; t < nt; ++t) th.emplace_back(rows, n * t / nt, n * (t + 1) / nt);
+  for (auto& x : th) x.join();
+}
+
+}  // extern "C"

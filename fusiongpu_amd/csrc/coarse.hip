@@ -1,0 +1,327 @@
+// coarse.hip -- exact nearest-centroid selection for the coarse quantizer
+// (A2), the k-means assignment (A13) and exact kNN (A18).
+//
+// The reference ranks centroids with cuVS CAGRA (search_pipeline.cu:341) and
+// assigns k-means points with a cuBLAS -2*X*C^T GEMM plus norms
+// (kmeans_gpu.cuh:197-229).  Here the dense contraction runs on the MFMA
+// units (v_mfma_f32_32x32x2f32), producing an estimate
+//     est = ||x||^2 + ||c||^2 - 2<x,c>
+// whose error against the exact device-form distance (a sequential fused
+// multiply-add over dimensions, tune_parameters.cu:39-46) is bounded by
+//     |est - exact| <= E = kappa * (||x||^2 + max_c ||c||^2),
+//     kappa = 8 * gamma(2*dim + 8),  gamma(n) = n*u / (1 - n*u),  u = 2^-24
+// (standard forward error bounds for dot products in any summation order,
+// with a factor 2 of slack).  With T the p-th smallest estimate, every column
+// of the exact top-p has est <= T + 2E, so re-scoring exactly that superset
+// and sorting by (exact distance, index) yields the exact answer with the tie
+// rule, independent of the GEMM's summation order.
+#include "common.hpp"
+#include "kernels.hpp"
+
+#include <cmath>
+
+namespace fgpu {
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+namespace {
+
+constexpr int kTM = 64, kTN = 64, kTK = 32, kLdsStride = 96;
+
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+__device__ __forceinline__ int lanes_below(uint64_t m) {
+  return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+}
+
+__global__ __launch_bounds__(256) void row_norms_kernel(const float* __restrict__ x, int64_t n, int dim,
+                                                        float* __restrict__ out) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= n) return;
+  const float* r = x + row * dim;
+  float s = 0.0f;
+  for (int d = lane; d < dim; d += kWave) s = __builtin_fmaf(r[d], r[d], s);
+#pragma unroll
+  for (int m = 32; m > 0; m >>= 1) s += __shfl_xor(s, m, kWave);
+  if (lane == 0) out[row] = s;
+}
+
+__global__ __launch_bounds__(1024) void max_reduce_kernel(const float* __restrict__ v, int64_t n,
+                                                          float* __restrict__ out) {
+  __shared__ float part[16];
+  float m = -FLT_MAX;
+  for (int64_t i = threadIdx.x; i < n; i += blockDim.x) m = fmaxf(m, v[i]);
+  m = wave_max_f(m);
+  if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = m;
+  __syncthreads();
+  if (threadIdx.x < 64) {
+    float t = threadIdx.x < (blockDim.x >> 6) ? part[threadIdx.x] : -FLT_MAX;
+    t = wave_max_f(t);
+    if (threadIdx.x == 0) *out = t;
+  }
+}
+
+// 64x64 output tile per workgroup, 4 waves each owning a 32x32 quadrant.
+// Operand tiles are staged k-major in LDS with a 96-float row stride, so the
+// MFMA operand reads (lanes 0-31: k, lanes 32-63: k+1) and the staging writes
+// (one row per lane) both hit distinct banks.
+__global__ __launch_bounds__(256) void gemm_est_kernel(const float* __restrict__ x, int64_t nrows,
+                                                       const float* __restrict__ c, int ncols, int dim,
+                                                       const float* __restrict__ xn,
+                                                       const float* __restrict__ cn,
+                                                       float* __restrict__ est, int64_t ld) {
+  __shared__ float As[kTK][kLdsStride];
+  __shared__ float Bs[kTK][kLdsStride];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t row0 = (int64_t)blockIdx.x * kTM;
+  const int col0 = blockIdx.y * kTN;
+  const int wr = wave >> 1, wc = wave & 1;
+  f32x16 acc;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
+
+  const int64_t ar = row0 + lane;
+  const int bc = col0 + lane;
+  for (int k0 = 0; k0 < dim; k0 += kTK) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int kk = wave * 8 + j * 4;
+      float4 va = make_float4(0.f, 0.f, 0.f, 0.f), vb = va;
+      if (k0 + kk < dim) {
+        if (ar < nrows) va = *reinterpret_cast<const float4*>(x + ar * dim + k0 + kk);
+        if (bc < ncols) vb = *reinterpret_cast<const float4*>(c + (int64_t)bc * dim + k0 + kk);
+      }
+      As[kk + 0][lane] = va.x; As[kk + 1][lane] = va.y; As[kk + 2][lane] = va.z; As[kk + 3][lane] = va.w;
+      Bs[kk + 0][lane] = vb.x; Bs[kk + 1][lane] = vb.y; Bs[kk + 2][lane] = vb.z; Bs[kk + 3][lane] = vb.w;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int kk = 0; kk < kTK; kk += 2) {
+      const float a = As[kk + (lane >> 5)][wr * 32 + (lane & 31)];
+      const float b = Bs[kk + (lane >> 5)][wc * 32 + (lane & 31)];
+      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, acc, 0, 0, 0);
+    }
+    __syncthreads();
+  }
+  // D layout of v_mfma_f32_32x32x2f32: lane l, accumulator r holds
+  // row 8*(r/4) + 4*(l/32) + r%4, column l%32.
+  const int j = col0 + wc * 32 + (lane & 31);
+  if (j >= ncols) return;
+  const float cj = cn[j];
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int64_t i = row0 + wr * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+    if (i < nrows) est[i * ld + j] = (xn[i] + cj) - 2.0f * acc[r];
+  }
+}
+
+constexpr int kCandCap = 256;
+
+// One wave per row: p-th smallest estimate by LDS radix select, margin
+// superset, exact re-score, bitonic sort by (distance, index).
+template <int VPL>
+__global__ __launch_bounds__(256) void select_exact_kernel(
+    const float* __restrict__ est, int64_t ld, int64_t nrows, int ncols,
+    const float* __restrict__ x, const float* __restrict__ c, int dim,
+    const float* __restrict__ xn, const float* __restrict__ cn_max, float kappa, int p, int prune,
+    float prune_ratio, int32_t* __restrict__ out_ids, float* __restrict__ out_d) {
+  __shared__ uint32_t hist_s[4][256];
+  __shared__ int cand_s[4][kCandCap];
+  __shared__ __align__(16) float x_s[4][256];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t row = (int64_t)blockIdx.x * 4 + wave;
+  if (row >= nrows) return;  // whole wave leaves; no workgroup barrier follows
+  uint32_t* hist = hist_s[wave];
+  int* cand = cand_s[wave];
+  float* xs = x_s[wave];
+  for (int d = lane; d < dim; d += kWave) xs[d] = x[row * dim + d];
+
+  float val[VPL];
+  const float* er = est + row * ld;
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) {
+    const int col = j * kWave + lane;
+    val[j] = col < ncols ? er[col] : FLT_MAX;
+  }
+
+  // Threshold T = p-th smallest estimate.
+  float T;
+  if (p == 1) {
+    float m = val[0];
+#pragma unroll
+    for (int j = 1; j < VPL; ++j) m = fminf(m, val[j]);
+    T = wave_min_f(m);
+  } else {
+    uint32_t key[VPL];
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) key[j] = (j * kWave + lane < ncols) ? float_key(val[j]) : 0xFFFFFFFFu;
+    uint32_t prefix = 0, mask = 0;
+    uint32_t rem = (uint32_t)p;
+    for (int shift = 24; shift >= 0; shift -= 8) {
+      for (int b = lane; b < 256; b += kWave) hist[b] = 0u;
+      wave_lds_sync();
+#pragma unroll
+      for (int j = 0; j < VPL; ++j)
+        if ((key[j] & mask) == prefix) atomicAdd(&hist[(key[j] >> shift) & 255u], 1u);
+      wave_lds_sync();
+      const uint32_t h0 = hist[4 * lane], h1 = hist[4 * lane + 1], h2 = hist[4 * lane + 2],
+                     h3 = hist[4 * lane + 3];
+      const uint32_t s = h0 + h1 + h2 + h3;
+      uint32_t inc = s;
+#pragma unroll
+      for (int o = 1; o < kWave; o <<= 1) {
+        uint32_t t = __shfl_up(inc, o, kWave);
+        if (lane >= o) inc += t;
+      }
+      const uint32_t exc = inc - s;
+      const uint64_t bm = __ballot(exc < rem && rem <= inc);
+      const int L = __ffsll((unsigned long long)bm) - 1;
+      int bin = 3;
+      uint32_t below = exc + h0 + h1 + h2;
+      if (rem <= exc + h0) { bin = 0; below = exc; }
+      else if (rem <= exc + h0 + h1) { bin = 1; below = exc + h0; }
+      else if (rem <= exc + h0 + h1 + h2) { bin = 2; below = exc + h0 + h1; }
+      bin = readlane_i(bin, L) + 4 * L;
+      below = (uint32_t)readlane_i((int)below, L);
+      rem -= below;
+      prefix |= (uint32_t)bin << shift;
+      mask |= 0xFFu << shift;
+      wave_lds_sync();
+    }
+    T = key_float(prefix);
+  }
+  const double E = (double)kappa * ((double)xn[row] + (double)(*cn_max));
+  const double thr = (double)T + 2.0 * E;
+
+  // Ordered compaction of the candidate columns.
+  int C = 0;
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) {
+    const int col = j * kWave + lane;
+    const bool f = col < ncols && (double)val[j] <= thr;
+    const uint64_t bm = __ballot(f);
+    const int pos = C + lanes_below(bm);
+    if (f && pos < kCandCap) cand[pos] = col;
+    C += __popcll(bm);
+  }
+  wave_lds_sync();
+  const bool all_cols = C > kCandCap;  // pathological ties: re-score everything
+  const int ncand = all_cols ? ncols : C;
+
+  float ld_ = FLT_MAX;
+  int li = kPadId;
+  bool first = true;
+  for (int base = 0; base < ncand; base += kWave) {
+    float d = FLT_MAX;
+    int id = kPadId;
+    if (base + lane < ncand) {
+      id = all_cols ? base + lane : cand[base + lane];
+      const float* cr = c + (int64_t)id * dim;
+      float acc = 0.0f;
+      if ((dim & 3) == 0) {
+        for (int t = 0; t < dim; t += 4) {
+          const float4 cv = *reinterpret_cast<const float4*>(cr + t);
+          const float4 xv = *reinterpret_cast<const float4*>(xs + t);
+          float df = xv.x - cv.x; acc = __builtin_fmaf(df, df, acc);
+          df = xv.y - cv.y; acc = __builtin_fmaf(df, df, acc);
+          df = xv.z - cv.z; acc = __builtin_fmaf(df, df, acc);
+          df = xv.w - cv.w; acc = __builtin_fmaf(df, df, acc);
+        }
+      } else {
+        for (int t = 0; t < dim; ++t) {
+          const float df = xs[t] - cr[t];
+          acc = __builtin_fmaf(df, df, acc);
+        }
+      }
+      d = acc;
+    }
+    wave_sort64(d, id);
+    if (first) { ld_ = d; li = id; first = false; }
+    else wave_merge_sorted64(ld_, li, d, id);
+  }
+
+  const float best = readlane_f(ld_, 0);
+  const float pthr = best * prune_ratio;
+  if (lane < p) {
+    int32_t oid = li;
+    if (prune && ld_ > pthr) oid = (int32_t)kPruned;
+    out_ids[row * p + lane] = oid;
+    out_d[row * p + lane] = ld_;
+  }
+}
+
+template <int VPL>
+fgpu_status launch_select_t(const float* est, int64_t ld, int64_t nrows, int ncols, const float* x,
+                            const float* c, int dim, const float* xn, const float* cn_max, float kappa,
+                            int p, int prune, float prune_ratio, int32_t* ids, float* d, hipStream_t s) {
+  const int64_t blocks = (nrows + 3) / 4;
+  hipLaunchKernelGGL(select_exact_kernel<VPL>, dim3((unsigned)blocks), dim3(256), 0, s, est, ld, nrows,
+                     ncols, x, c, dim, xn, cn_max, kappa, p, prune, prune_ratio, ids, d);
+  FGPU_HIP(hipGetLastError());
+  return FGPU_OK;
+}
+
+}  // namespace
+
+fgpu_status launch_row_norms(const float* rows, int64_t n, int dim, float* norms, hipStream_t s) {
+  if (n <= 0) return FGPU_OK;
+  hipLaunchKernelGGL(row_norms_kernel, dim3((unsigned)((n + 3) / 4)), dim3(256), 0, s, rows, n, dim, norms);
+  FGPU_HIP(hipGetLastError());
+  return FGPU_OK;
+}
+
+fgpu_status launch_max_reduce(const float* v, int64_t n, float* out, hipStream_t s) {
+  hipLaunchKernelGGL(max_reduce_kernel, dim3(1), dim3(1024), 0, s, v, n, out);
+  FGPU_HIP(hipGetLastError());
+  return FGPU_OK;
+}
+
+fgpu_status launch_gemm_est(const float* x, int64_t nrows, const float* c, int ncols, int dim,
+                            const float* xn, const float* cn, float* est, int64_t ld, hipStream_t s) {
+  FGPU_CHECK(dim % 4 == 0, FGPU_ERR_UNSUPPORTED, "gemm_est: dim must be a multiple of 4");
+  if (nrows <= 0 || ncols <= 0) return FGPU_OK;
+  dim3 grid((unsigned)((nrows + kTM - 1) / kTM), (unsigned)((ncols + kTN - 1) / kTN));
+  FGPU_CHECK(grid.y <= 65535u, FGPU_ERR_UNSUPPORTED, "gemm_est: too many columns");
+  hipLaunchKernelGGL(gemm_est_kernel, grid, dim3(256), 0, s, x, nrows, c, ncols, dim, xn, cn, est, ld);
+  FGPU_HIP(hipGetLastError());
+  return FGPU_OK;
+}
+
+static float coarse_kappa(int dim) {
+  const double u = std::ldexp(1.0, -24);
+  const double n = 2.0 * dim + 8.0;
+  const double gamma = n * u / (1.0 - n * u);
+  return (float)(8.0 * gamma * 1.001);
+}
+
+fgpu_status launch_select_exact(const float* est, int64_t ld, int64_t nrows, int ncols, const float* x,
+                                const float* c, int dim, const float* xn, const float* cn_max, int p,
+                                int prune, float prune_ratio, int32_t* ids, float* d, hipStream_t s) {
+  FGPU_CHECK(p >= 1 && p <= 64 && p <= ncols, FGPU_ERR_UNSUPPORTED, "select: need 1 <= p <= min(64, ncols)");
+  FGPU_CHECK(dim <= 256, FGPU_ERR_UNSUPPORTED, "select: dim must be <= 256");
+  if (nrows <= 0) return FGPU_OK;
+  const float kappa = coarse_kappa(dim);
+#define FGPU_SEL(V) \
+  if (ncols <= (V) * kWave) return launch_select_t<V>(est, ld, nrows, ncols, x, c, dim, xn, cn_max, kappa, p, prune, prune_ratio, ids, d, s)
+  FGPU_SEL(1);
+  FGPU_SEL(2);
+  FGPU_SEL(4);
+  FGPU_SEL(8);
+  FGPU_SEL(16);
+  FGPU_SEL(32);
+  FGPU_SEL(64);
+#undef FGPU_SEL
+  return set_error(FGPU_ERR_UNSUPPORTED, "select: more than 4096 columns");
+}
+
+int64_t est_rows_per_batch(size_t bytes, int ncols) {
+  int64_t r = (int64_t)(bytes / ((size_t)ncols * sizeof(float)));
+  return r - r % 64;
+}
+
+}  // namespace fgpu

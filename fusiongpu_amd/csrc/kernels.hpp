@@ -1,0 +1,73 @@
+// kernels.hpp -- host-side launchers for the HIP kernels (C++ linkage).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "fusiongpu.h"
+
+namespace fgpu {
+
+// ---- coarse.hip -------------------------------------------------------------
+// norms[i] = ||rows[i]||^2 (fp32, any order: it only feeds the GEMM estimate).
+fgpu_status launch_row_norms(const float* rows, int64_t n, int dim, float* norms, hipStream_t s);
+// *out = max(norms[0..n)).
+fgpu_status launch_max_reduce(const float* v, int64_t n, float* out, hipStream_t s);
+// est[i][j] = xn[i] + cn[j] - 2 <x_i, c_j> for i in [0,nrows), j in [0,ncols);
+// est row stride is ld floats.  MFMA f32 32x32x2.
+fgpu_status launch_gemm_est(const float* x, int64_t nrows, const float* c, int ncols, int dim,
+                            const float* xn, const float* cn, float* est, int64_t ld, hipStream_t s);
+// Per row: the p nearest columns by exact device-form L2, chosen from the
+// estimate with a rigorous error margin.  ids are int32 bit patterns; with
+// prune != 0 a column farther than best*prune_ratio gets 0xFFFFFFFF.
+fgpu_status launch_select_exact(const float* est, int64_t ld, int64_t nrows, int ncols,
+                                const float* x, const float* c, int dim, const float* xn,
+                                const float* cn_max, int p, int prune, float prune_ratio,
+                                int32_t* out_ids, float* out_d, hipStream_t s);
+// Rows per batch of the estimate matrix that fit in `bytes`.
+int64_t est_rows_per_batch(size_t bytes, int ncols);
+
+// ---- adc.hip ------------------------------------------------------------------
+struct AdcArgs {
+  const float* queries;     // [nq][dim]
+  const float* centroids;   // [nlist][dim]
+  const float* codebook;    // [m][256][dim/m]
+  const int32_t* offsets;   // [nlist+1]
+  const uint8_t* codes;     // [total][m]
+  const int32_t* vec_ids;   // [total]
+  const uint32_t* probes;   // [nq][nprobe]
+  int nq, nprobe, k, nlist;  // probe ids >= nlist are skipped like pruned ones
+  int32_t* out_ids;         // [nq][k]
+  float* out_d;             // [nq][k]
+};
+bool adc_supported(int dim, int m);
+fgpu_status launch_adc_plain(int dim, int m, const AdcArgs& a, hipStream_t s);
+
+// ---- build.hip ----------------------------------------------------------------
+fgpu_status launch_probe_counts(const uint32_t* probes, int nq, int nprobe, int nlist, const int32_t* offsets,
+                                int32_t* counts, int32_t* offs, hipStream_t s);
+fgpu_status launch_maxabs(const float* x, int64_t count, float* out, hipStream_t s);
+fgpu_status launch_kmeans_accumulate(const float* x, int64_t n, const int32_t* assign, int k,
+                                     int dim, int shift, unsigned long long* sums, int32_t* counts,
+                                     hipStream_t s);
+fgpu_status launch_kmeans_finalize(const unsigned long long* sums, const int32_t* counts, int k,
+                                   int dim, int shift, int empty_rule, float* cent, hipStream_t s);
+fgpu_status launch_gather_rows(const float* x, int dim, const int32_t* rows, int nrows, float* out,
+                               hipStream_t s);
+fgpu_status launch_pq_encode(const float* x, int64_t n, int dim, int m, const int32_t* assign,
+                             const float* cent, const float* codebook, uint8_t* codes, hipStream_t s);
+fgpu_status launch_pq_residuals(const float* x, int dim, const int32_t* rows, int nrows,
+                                const int32_t* assign, const float* cent, float* res, hipStream_t s);
+fgpu_status launch_pq_init(const float* res, int nsample, int dim, int m, const int32_t* init_rows,
+                           float* codebook, hipStream_t s);
+fgpu_status launch_pq_estep(const float* res, int nsample, int dim, int m, const float* codebook,
+                            int32_t* assign_pq, hipStream_t s);
+fgpu_status launch_pq_mstep(const float* res, int nsample, int dim, int m, const int32_t* assign_pq,
+                            float* codebook, hipStream_t s);
+// k-means++ seeding on the device (definition in oracle.cpp orc_kmeans_init_pp).
+fgpu_status launch_kmeans_pp(const float* x, int64_t n, int dim, int k, uint64_t seed, float* cent,
+                             int32_t* rows, void* ws, size_t ws_bytes, hipStream_t s);
+size_t kmeans_pp_ws_bytes(int64_t n);
+
+}  // namespace fgpu

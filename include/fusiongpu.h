@@ -1,0 +1,175 @@
+/* fusiongpu.h -- C ABI of the MI355X-native IVF-PQ engine (libfusiongpu.so).
+ *
+ * Plain C types only: device pointers are `void*`/typed pointers into HBM,
+ * streams are passed as `void*` (a hipStream_t; NULL = the null stream).
+ * Every call returns an fgpu_status (0 = ok) and never exits the process;
+ * fgpu_last_error() returns a thread-local message for the last failure.
+ * Calls that take a stream only enqueue work on it: no hidden host
+ * synchronisation, no static scratch.  Scratch comes from a caller-owned
+ * device workspace whose size the matching *_workspace_bytes() call returns.
+ *
+ * Each entry point names the reference interface it replaces
+ * (Hello-day/FusionGPU, file:line).
+ */
+#ifndef FUSIONGPU_H_
+#define FUSIONGPU_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum {
+  FGPU_OK = 0,
+  FGPU_ERR_ARG = 1,         /* invalid argument (shape, null pointer, range) */
+  FGPU_ERR_UNSUPPORTED = 2, /* geometry (dim, pq_m, k, nprobe) with no kernel instance */
+  FGPU_ERR_HIP = 3,         /* a HIP runtime call failed */
+  FGPU_ERR_IO = 4,          /* missing, short or inconsistent file */
+  FGPU_ERR_NOMEM = 5,       /* device or host allocation failed */
+  FGPU_ERR_WORKSPACE = 6    /* workspace smaller than *_workspace_bytes() */
+} fgpu_status;
+
+typedef struct fgpu_index fgpu_index; /* opaque device-resident IVF-PQ index */
+
+/* Device view of an index: the reference's IVFIndexGPU (defs.h:51-58) plus
+ * the geometry that defs.h fixes at compile time (defs.h:9-12). */
+typedef struct {
+  int dim, pq_m, pq_k, nlist;
+  int64_t total;
+  const float* d_pq_codebook;      /* [pq_m][256][dim/pq_m] */
+  const int32_t* d_cluster_offsets; /* [nlist+1] */
+  const uint8_t* d_all_pq_codes;   /* [total][pq_m], list-major */
+  const int32_t* d_all_vector_ids; /* [total] */
+  const float* d_centroids;        /* [nlist][dim] */
+  int max_list_len;
+} fgpu_index_info;
+
+const char* fgpu_last_error(void);
+int fgpu_abi_version(void);
+
+/* ---- index (A1) ------------------------------------------------------- */
+
+/* Copies host arrays laid out as ivf_data.bin holds them (build_global.cu:242-252)
+ * plus the codebook (global_pq_codebook.bin, build_global.cu:204-206) to HBM.
+ * Replaces load_ivf_index_to_gpu (search_pipeline.cu:481-529). */
+fgpu_status fgpu_index_create(int dim, int pq_m, int nlist, int64_t total, const int32_t* h_offsets,
+                              const int32_t* h_ids, const uint8_t* h_codes, const float* h_centroids,
+                              const float* h_codebook, fgpu_index** out);
+/* Reads ivf_data.bin + global_pq_codebook.bin (search_pipeline.cu:481-503); dim and
+ * pq_m are not stored in the files (defs.h fixes them), so the caller states them. */
+fgpu_status fgpu_index_load(const char* ivf_data_path, const char* codebook_path, int dim, int pq_m,
+                            fgpu_index** out);
+void fgpu_index_destroy(fgpu_index* idx);
+fgpu_status fgpu_index_get_info(const fgpu_index* idx, fgpu_index_info* out);
+
+/* ---- search: coarse quantizer (A2 + A3) -------------------------------- */
+
+/* Exact top-nprobe lists per query, ascending (distance, list id), with the
+ * prune rule of prune_and_count_fused_kernel (gpu_global.cu:43-50): a probe
+ * whose distance exceeds best*prune_ratio becomes 0xFFFFFFFF.  Replaces the
+ * cuVS CAGRA call (search_pipeline.cu:341; cagra_adapter.cuh:38-68) with an
+ * MFMA GEMM plus an exact re-score.  nprobe <= 64. */
+size_t fgpu_coarse_workspace_bytes(int nq, int nlist);
+fgpu_status fgpu_coarse_search(const fgpu_index* idx, const float* d_queries, int nq, int nprobe,
+                               float prune_ratio, uint32_t* d_probe_ids, float* d_probe_dists,
+                               void* d_workspace, size_t workspace_bytes, void* stream);
+
+/* counts[q] = sum of list sizes over surviving probes; offsets = exclusive
+ * scan with offsets[nq] = total (gpu_global.cu:31-77, 704-723). */
+fgpu_status fgpu_probe_counts(const fgpu_index* idx, const uint32_t* d_probe_ids, int nq, int nprobe,
+                              int32_t* d_counts, int32_t* d_offsets, void* stream);
+
+/* ---- search: LUT + ADC scan + top-k (A4-A6, A10, plain IVF-PQ) ---------- */
+
+/* The k best (ADC distance, vector id) over every vector of every surviving
+ * probed list; padding id -1 / distance FLT_MAX.  Equals run_gpu_batch_logic
+ * (gpu_global.cu:679-874) with p1_lists = nprobe, limit_k = k, rerank_m = k.
+ * k <= 64. */
+fgpu_status fgpu_adc_search(const fgpu_index* idx, const float* d_queries, int nq,
+                            const uint32_t* d_probe_ids, int nprobe, int k, int32_t* d_out_ids,
+                            float* d_out_dists, void* stream);
+
+/* coarse + ADC in one call. */
+size_t fgpu_search_workspace_bytes(int nq, int nlist, int nprobe);
+fgpu_status fgpu_search(const fgpu_index* idx, const float* d_queries, int nq, int nprobe, int k,
+                        float prune_ratio, int32_t* d_out_ids, float* d_out_dists,
+                        void* d_workspace, size_t workspace_bytes, void* stream);
+
+/* ---- exact nearest centroids (A13 / A2 core) -------------------------- */
+
+/* For each row x of d_x [n][dim]: the p nearest rows of d_c [nc][dim] by
+ * exact squared L2 in the reference's device form (sequential fused
+ * multiply-add, tune_parameters.cu:39-46), ascending (distance, index).
+ * p = 1 is the k-means assignment (kmeans_gpu.cuh:197-229, lowest index wins
+ * ties).  MFMA GEMM + rigorous-margin re-score.  p <= 64. */
+size_t fgpu_l2_topk_workspace_bytes(int64_t n, int nc);
+fgpu_status fgpu_l2_topk(const float* d_x, int64_t n, const float* d_c, int nc, int dim, int p,
+                         int32_t* d_ids, float* d_dists, void* d_workspace, size_t workspace_bytes,
+                         void* stream);
+
+/* ---- index build (A13-A17) -------------------------------------------- */
+
+/* One Lloyd update (kmeans_gpu.cuh:81-116) with deterministic fixed-point
+ * sums: c = (float)(sum(round(x*2^shift)) * 2^-shift) * (1.0f/count).
+ * empty_rule 0 = empty cluster becomes zero (kmeans_gpu.cuh:293,110), 1 = keeps
+ * its centroid.  Workspace: fgpu_kmeans_workspace_bytes(k, dim). */
+size_t fgpu_kmeans_workspace_bytes(int k, int dim);
+fgpu_status fgpu_kmeans_update(const float* d_x, int64_t n, const int32_t* d_assign, int k, int dim,
+                               int shift, int empty_rule, float* d_centroids, int32_t* d_counts,
+                               void* d_workspace, size_t workspace_bytes, void* stream);
+/* Fixed-point shift for data with max |x| = maxabs and n rows. */
+int fgpu_fixed_shift(float maxabs, int64_t n);
+
+/* Full k-means (run_kmeans_gpu, kmeans_gpu.cuh:234-324): init_mode 0 = the
+ * reference's strided mt19937 init (kmeans_gpu.cuh:259-267), 1 = k-means++
+ * seeding; then iters x (assign, update).  d_centroids [k][dim] out. */
+fgpu_status fgpu_kmeans_fit(const float* d_x, int64_t n, int dim, int k, int iters, int init_mode,
+                            uint64_t seed, float* d_centroids, int32_t* d_assign_out, void* stream);
+
+/* Residual PQ codebook training (train_residual_pq_codebooks, pq_utils.h:77-138):
+ * d_codebook [pq_m][256][dim/pq_m] out. */
+fgpu_status fgpu_pq_train(const float* d_x, int64_t n, int dim, int pq_m, const int32_t* d_assign,
+                          const float* d_centroids, int sample_size, int iters, float* d_codebook,
+                          void* stream);
+/* Residual PQ encoding (encode_residuals_kernel, kmeans_gpu.cuh:403-445). */
+fgpu_status fgpu_pq_encode(const float* d_x, int64_t n, int dim, int pq_m, const int32_t* d_assign,
+                           const float* d_centroids, const float* d_codebook, uint8_t* d_codes,
+                           void* stream);
+
+/* build_global (build_global.cu:21-258) without rebalancing and CAGRA: k-means
+ * (nlist, kmeans_iters), assignment, PQ training (pq_iters, sample_size),
+ * encoding and list assembly.  Outputs are host arrays in ivf_data.bin layout:
+ * h_offsets [nlist+1], h_ids [n], h_codes [n][pq_m], h_centroids [nlist][dim],
+ * h_codebook [pq_m][256][dim/pq_m]. */
+fgpu_status fgpu_build_ivfpq(const float* d_x, int64_t n, int dim, int nlist, int pq_m,
+                             int kmeans_iters, int init_mode, uint64_t seed, int pq_iters,
+                             int sample_size, int32_t* h_offsets, int32_t* h_ids, uint8_t* h_codes,
+                             float* h_centroids, float* h_codebook, void* stream);
+
+/* ---- files (utils.h, build_global.cu:242-252) -------------------------- */
+
+fgpu_status fgpu_write_ivf_data(const char* path, int64_t total, int nlist, int pq_m, int dim,
+                                const int32_t* offsets, const int32_t* ids, const uint8_t* codes,
+                                const float* centroids);
+/* Reads the header: *total, *nlist. */
+fgpu_status fgpu_read_ivf_header(const char* path, int64_t* total, int* nlist);
+fgpu_status fgpu_read_ivf_data(const char* path, int pq_m, int dim, int32_t* offsets, int32_t* ids,
+                               uint8_t* codes, float* centroids);
+fgpu_status fgpu_write_fvecs(const char* path, const float* v, int64_t n, int dim);
+/* fvecs/ivecs readers (utils.h:22-48, 75-95): *n rows of dim; pass out=NULL to query. */
+fgpu_status fgpu_read_fvecs(const char* path, int dim, int64_t* n, float* out);
+fgpu_status fgpu_read_ivecs(const char* path, int* dim, int64_t* n, int32_t* out);
+
+/* ---- synthetic data (no reference counterpart) ------------------------- */
+
+/* Seeded Gaussian mixture, identical on every host (counter-based splitmix64 +
+ * Box-Muller in double).  set 0 = base vectors, 1 = queries. */
+void fgpu_gen_gmm(int64_t n, int dim, int ncomp, double lo, double hi, double sig_lo, double sig_hi,
+                  uint64_t seed, int set, float* out, int nthreads);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* FUSIONGPU_H_ */

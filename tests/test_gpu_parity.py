@@ -1,0 +1,198 @@
+"""GPU parity: the HIP path (through the C ABI) against the CPU oracle on the
+same seeded inputs.  Bar: bit-exact ids, codes, assignments and -- because
+every distance is computed in the reference's exact operation order --
+bit-exact fp32 distances too (the north-star tolerance is 1e-4 relative).
+"""
+import sys
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+if not torch.cuda.is_available():
+    pytest.skip("no HIP device", allow_module_level=True)
+
+import fusiongpu_amd as fg  # noqa: E402
+import oracle  # noqa: E402
+from tests.golden.make_golden import inputs as golden_inputs  # noqa: E402
+
+
+def _say(msg):
+    print(f"[gpu-case] {msg}", flush=True)
+    sys.stdout.flush()
+
+
+def _bits(a):
+    return np.asarray(a, np.float32).view(np.uint32)
+
+
+def _host(t):
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def _random_index(rng, n, dim, m, nlist, empty=(), big=None):
+    """A valid index with arbitrary codes: list sizes skewed, some empty, one very long."""
+    p = rng.random(nlist) + 0.05
+    for e in empty:
+        p[e] = 0.0
+    if big is not None:
+        p[big] *= 40.0
+    assign = rng.choice(nlist, size=n, p=p / p.sum()).astype(np.int32)
+    codes = rng.integers(0, 256, (n, m)).astype(np.uint8)
+    codes[100] = codes[101]            # exact ADC ties ...
+    assign[101] = assign[100]          # ... inside one list
+    offs, ids, lc = oracle.build_lists(assign, nlist, codes)
+    cent = rng.standard_normal((nlist, dim)).astype(np.float32) * 0.7
+    cb = (rng.standard_normal((m, 256, dim // m)) * 0.4).astype(np.float32)
+    return offs, ids, lc, cent, cb
+
+
+# --------------------------------------------------------------------------- exact nearest centroids
+@pytest.mark.parametrize("dim,nc,p", [(128, 1024, 32), (96, 300, 1), (128, 4096, 64), (64, 50, 10), (128, 77, 1)])
+def test_l2_topk_bit_exact(dim, nc, p):
+    _say(f"l2_topk dim={dim} nc={nc} p={p}")
+    rng = np.random.default_rng(dim + nc + p)
+    x = rng.standard_normal((257, dim)).astype(np.float32)
+    c = rng.standard_normal((nc, dim)).astype(np.float32)
+    c[5] = c[2]                      # duplicate centroid -> exact ties
+    x[3] = c[2]                      # distance 0 to two centroids
+    x[4] = c[2] + np.float32(1e-3)   # near-tie region for the GEMM estimate
+    ids, d = fg.l2_topk(torch.from_numpy(x).cuda(), torch.from_numpy(c).cuda(), p)
+    ids, d = _host(ids), _host(d)
+    oid, od = oracle.coarse(x, c, p, prune_ratio=np.inf)  # best*inf never prunes (0*inf is NaN)
+    assert np.array_equal(ids.view(np.uint32), oid)
+    assert np.array_equal(_bits(d), _bits(od))
+    if p == 1:
+        assert np.array_equal(ids[:, 0], oracle.kmeans_assign(x, c))
+
+
+# --------------------------------------------------------------------------- coarse quantizer (A2, A3)
+@pytest.mark.parametrize("prune_ratio", [100.0, 1.3])
+def test_coarse_search_bit_exact(prune_ratio):
+    _say(f"coarse prune_ratio={prune_ratio}")
+    rng = np.random.default_rng(3)
+    offs, ids, lc, cent, cb = _random_index(rng, 4000, 128, 32, 256)
+    cent[9] = cent[4]
+    q = rng.standard_normal((300, 128)).astype(np.float32) * 0.7
+    q[0] = cent[4]
+    idx = fg.Index.from_arrays(128, 32, offs, ids, lc, cent, cb)
+    pid, pd = idx.coarse_search(torch.from_numpy(q).cuda(), 32, prune_ratio)
+    pid, pd = _host(pid).view(np.uint32), _host(pd)
+    oid, od = oracle.coarse(q, cent, 32, prune_ratio)
+    assert np.array_equal(pid, oid)
+    assert np.array_equal(_bits(pd), _bits(od))
+    idx.close()
+
+
+# --------------------------------------------------------------------------- LUT + ADC + top-k (A4-A6, A10)
+@pytest.mark.parametrize("dim,m,k", [(128, 32, 10), (128, 16, 10), (96, 48, 20), (96, 32, 64), (128, 64, 1),
+                                     (96, 16, 7)])
+def test_adc_search_bit_exact(dim, m, k):
+    _say(f"adc dim={dim} m={m} k={k}")
+    rng = np.random.default_rng(dim * m + k)
+    nlist = 40
+    offs, ids, lc, cent, cb = _random_index(rng, 30000, dim, m, nlist, empty=(3, 17), big=8)
+    q = rng.standard_normal((150, dim)).astype(np.float32) * 0.7
+    probes, _ = oracle.coarse(q, cent, 12)
+    probes[5, 2] = 0xFFFFFFFF             # pruned probe mid-list
+    probes[6, :] = 0xFFFFFFFF             # every probe pruned -> padding
+    probes[7, 0] = 3                      # an empty list first
+    probes[8, :] = probes[8, 0]           # the same list probed twice is scanned twice
+    idx = fg.Index.from_arrays(dim, m, offs, ids, lc, cent, cb)
+    assert idx.max_list_len > 1024        # longer than the reference's 1024-item cut
+    gid, gd = idx.adc_search(torch.from_numpy(q).cuda(), torch.from_numpy(probes.view(np.int32)).cuda(), k)
+    gid, gd = _host(gid), _host(gd)
+    oid, od = oracle.search_plain(q, cent, cb, offs, ids, lc, probes, k)
+    bad = np.nonzero(~np.all(gid == oid, axis=1))[0]
+    assert bad.size == 0, f"first mismatching queries {bad[:5]}: gpu {gid[bad[0]]} oracle {oid[bad[0]]}"
+    assert np.array_equal(_bits(gd), _bits(od))
+    assert np.all(gid[6] == -1)
+    idx.close()
+
+
+def test_search_fused_equals_stages():
+    _say("fused search")
+    rng = np.random.default_rng(21)
+    offs, ids, lc, cent, cb = _random_index(rng, 20000, 128, 32, 128)
+    q = torch.from_numpy(rng.standard_normal((500, 128)).astype(np.float32) * 0.7).cuda()
+    idx = fg.Index.from_arrays(128, 32, offs, ids, lc, cent, cb)
+    fid, fd = idx.search(q, 16, 10)
+    pid, _ = idx.coarse_search(q, 16)
+    sid, sd = idx.adc_search(q, pid, 10)
+    assert torch.equal(fid, sid) and torch.equal(fd, sd)
+    qn = q.cpu().numpy()
+    oprobe, _ = oracle.coarse(qn, cent, 16)
+    oid, od = oracle.search_plain(qn, cent, cb, offs, ids, lc, oprobe, 10)
+    assert np.array_equal(_host(fid), oid) and np.array_equal(_bits(_host(fd)), _bits(od))
+    cnt, off = fg.probe_counts(idx, pid)
+    ocnt = oracle.probe_counts(oprobe, offs)
+    assert np.array_equal(_host(cnt), ocnt)
+    assert np.array_equal(_host(off), np.concatenate([[0], np.cumsum(ocnt)]).astype(np.int32))
+    idx.close()
+
+
+# --------------------------------------------------------------------------- k-means (A13, A14)
+def test_kmeans_update_bit_exact():
+    _say("kmeans_update")
+    rng = np.random.default_rng(31)
+    x = rng.standard_normal((20000, 128)).astype(np.float32)
+    k = 50
+    a = rng.integers(0, k - 1, 20000).astype(np.int32)
+    old = rng.standard_normal((k, 128)).astype(np.float32)
+    shift = fg.fixed_shift(float(np.abs(x).max()), x.shape[0])
+    for rule in (0, 1):
+        c = torch.from_numpy(old.copy()).cuda()
+        cnt = fg.kmeans_update(torch.from_numpy(x).cuda(), torch.from_numpy(a).cuda(), c, shift, rule)
+        want, wcnt = oracle.kmeans_update(x, a, old, shift, rule)
+        assert np.array_equal(_host(cnt), wcnt)
+        assert np.array_equal(_bits(_host(c)), _bits(want))
+
+
+@pytest.mark.parametrize("init_mode", [0, 1])
+def test_kmeans_fit_bit_exact(init_mode):
+    _say(f"kmeans_fit init={init_mode}")
+    x = oracle.gen_gmm(6000, 128, 24, seed=5, sig_lo=0.1)
+    cent, assign = fg.kmeans_fit(torch.from_numpy(x).cuda(), 48, 6, init_mode=init_mode, seed=42)
+    oc, oa = oracle.kmeans_fit(x, 48, 6, init_mode=init_mode, seed=42)
+    assert np.array_equal(_bits(_host(cent)), _bits(oc))
+    assert np.array_equal(_host(assign), oa)
+
+
+# --------------------------------------------------------------------------- PQ (A15, A16)
+def test_pq_train_matches_reference_fixture():
+    _say("pq_train golden")
+    import os
+    g = np.load(os.path.join(os.path.dirname(__file__), "golden", "ref_pq.npz"))
+    _, x, cent, assign = golden_inputs()
+    cb = fg.pq_train(torch.from_numpy(x).cuda(), torch.from_numpy(assign).cuda(), torch.from_numpy(cent).cuda(),
+                     32, sample_size=500, iters=5)
+    assert np.array_equal(_bits(_host(cb)), _bits(g["codebook"]))
+
+
+@pytest.mark.parametrize("dim,m", [(128, 32), (128, 16), (96, 48)])
+def test_pq_train_and_encode_bit_exact(dim, m):
+    _say(f"pq dim={dim} m={m}")
+    rng = np.random.default_rng(dim + m)
+    nlist = 20
+    cent = rng.standard_normal((nlist, dim)).astype(np.float32)
+    a = rng.integers(0, nlist, 5000).astype(np.int32)
+    x = (cent[a] + 0.3 * rng.standard_normal((5000, dim))).astype(np.float32)
+    dx, da, dc = torch.from_numpy(x).cuda(), torch.from_numpy(a).cuda(), torch.from_numpy(cent).cuda()
+    cb = fg.pq_train(dx, da, dc, m, sample_size=3000, iters=4)
+    ocb = oracle.pq_train(x, a, cent, m, sample_size=3000, iters=4)
+    assert np.array_equal(_bits(_host(cb)), _bits(ocb))
+    codes = fg.pq_encode(dx, da, dc, cb)
+    assert np.array_equal(_host(codes), oracle.pq_encode(x, a, cent, ocb, fma_mode=1))
+
+
+def test_build_ivfpq_bit_exact():
+    _say("build_ivfpq")
+    x = oracle.gen_gmm(8000, 128, 16, seed=9, sig_lo=0.1)
+    got = fg.build_ivfpq(torch.from_numpy(x).cuda(), 32, 32, kmeans_iters=4, init_mode=1, seed=7, pq_iters=3,
+                         sample_size=3000)
+    want = oracle.build_ivfpq(x, 32, 32, kmeans_iters=4, init_mode=1, seed=7, pq_iters=3, sample_size=3000)
+    for g, w, name in zip(got, want, ["offsets", "ids", "codes", "centroids", "codebook"]):
+        assert np.array_equal(np.asarray(g).view(np.uint8), np.asarray(w).view(np.uint8)), name
