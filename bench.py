@@ -53,7 +53,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--cpu-queries", type=int, default=2000, help="query sample for the CPU baseline (0 = skip)")
+    ap.add_argument("--cpu-queries", type=int, default=10000, help="query sample for the CPU baseline (0 = skip)")
     ap.add_argument("--n", type=int, default=1_000_000)
     ap.add_argument("--nq", type=int, default=10_000)
     ap.add_argument("--copy-probe", action="store_true", help="also run a 1 GiB device copy (PMC calibration)")

@@ -79,6 +79,11 @@ class FgpuError(RuntimeError):
 def _load():
     if not os.path.exists(lib_path):
         raise ImportError(f"{lib_path} is not built; run __graft_entry__.build() (hipcc for gfx950)")
+    # torch ships its own libamdhip64.so.7.  Importing torch first makes this
+    # library bind to that already-loaded HIP runtime instead of loading a
+    # second one (/opt/rocm) into the process: two runtimes cannot share the
+    # device, and the second reports "no ROCm-capable device".
+    import torch  # noqa: F401,PLC0415
     l = ctypes.CDLL(lib_path)
     for name, (res, args) in _SIGS.items():
         f = getattr(l, name)
