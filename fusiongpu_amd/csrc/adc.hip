@@ -20,11 +20,12 @@
 //     (gpu_global.cu:196-253): one SDWA byte-to-address shift and one
 //     ds_read_b32 with an immediate row offset per term.
 //   * Each scanning wave keeps its own running top-64 (one (distance, id) per
-//     lane, sorted by the tie rule).  A vector is a candidate only if it beats
-//     the wave's k-th entry; after the first list almost nothing passes, so
-//     the selection costs one compare per vector.  Few passers are inserted
-//     one by one; many are bitonic-sorted and merged.  At the end the wave
-//     lists are merged in LDS.
+//     lane, sorted by the tie rule).  A vector is a candidate only if its
+//     (distance, id) beats the smallest k-th entry over all scanning waves,
+//     kept in LDS with a 64-bit atomic min; ids are loaded with the codes, so
+//     the test is one 64-bit compare with no dependent load.  After the first
+//     list almost nothing passes.  Few passers are inserted one by one; many
+//     are bitonic-sorted and merged.  At the end the wave lists are merged.
 //   * adc_spec_kernel (pq_m <= 32): 16 waves, 8 build LUT(p+1) into one LDS
 //     buffer while 8 scan list p out of the other; one barrier per list.
 //     adc_plain_kernel (pq_m 48, 64): 8 waves alternate build and scan.
@@ -94,51 +95,99 @@ __device__ __forceinline__ float adc_sum(const float* __restrict__ lut, const ui
   return d;
 }
 
-// Offer one distance per lane to the wave's running top-k.
-__device__ __forceinline__ void offer(float d, bool valid, int vid_index, const int32_t* __restrict__ ids, int k,
-                                      float& ld, int& li, float& thr_d, int& thr_i) {
-  const bool cand = valid && d <= thr_d;
-  if (__ballot(cand)) {
-    const int id = cand ? ids[vid_index] : kPadId;
-    const bool pass = cand && lt_pair(d, id, thr_d, thr_i);
-    uint64_t bm = __ballot(pass);
-    if (bm) {
-      if (__popcll(bm) > kSerialMax) {
-        float cd = pass ? d : FLT_MAX;
-        int ci = pass ? id : kPadId;
-        wave_sort64(cd, ci);
-        wave_merge_sorted64(ld, li, cd, ci);
-      } else {
-        while (bm) {
-          const int src = __ffsll((unsigned long long)bm) - 1;
-          bm &= bm - 1;
-          wave_insert64(ld, li, readlane_f(d, src), readlane_i(id, src));
-        }
+// Two ADC chains at once, interleaved so each wave keeps twice as many LDS
+// gathers in flight.  Each chain is still the sequential sum over ascending m.
+// Lanes past the end of a list run on stale codes: every byte value indexes
+// inside the LUT, and the caller masks those results.
+//
+// Early abandon: every term is a sum of squares (>= +0), and adding a
+// non-negative float never lowers a rounded sum, so a partial sum already above
+// thr_d bounds the final distance from below.  After each group of 8
+// subspaces, if no valid lane of either chain is still <= thr_d, the wave
+// stops: none of its vectors can enter the top-k (a vector equal to thr_d
+// could still win on its id, so equality keeps a lane alive).  Returns false
+// in that case; otherwise d0/d1 are the complete, exact distances.
+template <int M>
+__device__ __forceinline__ bool adc_sum2(const float* __restrict__ lut, const uint4 (&w0)[M / 16],
+                                         const uint4 (&w1)[M / 16], bool ok0, bool ok1, float thr_d, float& d0,
+                                         float& d1) {
+  float a = 0.0f, b = 0.0f;
+#pragma unroll
+  for (int i = 0; i < M / 16; ++i) {
+    const uint32_t x[4] = {w0[i].x, w0[i].y, w0[i].z, w0[i].w};
+    const uint32_t y[4] = {w1[i].x, w1[i].y, w1[i].z, w1[i].w};
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const uint32_t cx = (x[j >> 2] >> (8 * (j & 3))) & 0xFFu;
+      const uint32_t cy = (y[j >> 2] >> (8 * (j & 3))) & 0xFFu;
+      a += lut[(i * 16 + j) * kPQK + cx];
+      b += lut[(i * 16 + j) * kPQK + cy];
+      if ((j & 7) == 7 && i * 16 + j + 1 < M) {
+        if (!__ballot((ok0 && a <= thr_d) || (ok1 && b <= thr_d))) return false;
       }
-      thr_d = readlane_f(ld, k - 1);
-      thr_i = readlane_i(li, k - 1);
     }
   }
+  d0 = a;
+  d1 = b;
+  return true;
+}
+
+// (distance, id) packed so that unsigned order is the tie rule: distances are
+// sums of squares (never negative, never -0), so their bit patterns order like
+// the floats; ids are non-negative.
+__device__ __forceinline__ uint64_t pack_key(float d, int id) {
+  return ((uint64_t)__float_as_uint(d) << 32) | (uint32_t)id;
+}
+// "No threshold yet": the padding entry (FLT_MAX, kPadId); every real
+// candidate is below it and its distance part is a finite float.
+constexpr uint64_t kNoThr = ((uint64_t)0x7F7FFFFFu << 32) | (uint32_t)kPadId;
+
+// Offer one (distance, id) per lane to the wave's running top-64 list; only
+// pairs strictly below `thr` (the k-th best known to the workgroup) enter.
+// Returns true if the list changed.
+__device__ __forceinline__ bool offer(float d, int id, bool valid, uint64_t thr, float& ld, int& li) {
+  const bool pass = valid && pack_key(d, id) < thr;
+  uint64_t bm = __ballot(pass);
+  if (!bm) return false;
+  if (__popcll(bm) > kSerialMax) {
+    float cd = pass ? d : FLT_MAX;
+    int ci = pass ? id : kPadId;
+    wave_sort64(cd, ci);
+    wave_merge_sorted64(ld, li, cd, ci);
+  } else {
+    while (bm) {
+      const int src = __ffsll((unsigned long long)bm) - 1;
+      bm &= bm - 1;
+      wave_insert64(ld, li, readlane_f(d, src), readlane_i(id, src));
+    }
+  }
+  return true;
 }
 
 // Each scanning wave takes 128 consecutive vectors per round (two per lane).
 constexpr int kVecPerWaveRound = 2 * kWave;
 
+// Codes and vector ids of this lane's two vectors of a round (ids come along
+// so the top-k filter never waits on a dependent load).
 template <int M>
-__device__ __forceinline__ void load_pair(const uint8_t* __restrict__ codes, int start, int n, int v0,
-                                          uint4 (&w0)[M / 16], uint4 (&w1)[M / 16]) {
-  if (v0 < n) load_codes<M>(codes, (int64_t)start + v0, w0);
-  if (v0 + kWave < n) load_codes<M>(codes, (int64_t)start + v0 + kWave, w1);
+__device__ __forceinline__ void load_pair(const uint8_t* __restrict__ codes, const int32_t* __restrict__ ids, int start,
+                                          int n, int v0, uint4 (&w0)[M / 16], uint4 (&w1)[M / 16], int& i0, int& i1) {
+  if (v0 < n) { load_codes<M>(codes, (int64_t)start + v0, w0); i0 = ids[start + v0]; }
+  if (v0 + kWave < n) { load_codes<M>(codes, (int64_t)start + v0 + kWave, w1); i1 = ids[start + v0 + kWave]; }
 }
 
-// Scan one list with the LUT at a compile-time LDS position.  w0/w1 hold the
-// codes of this wave's first round (loaded by the caller ahead of time); with
-// PREFETCH later rounds are loaded one round ahead, otherwise at round start.
+// Scan one list with the LUT at a compile-time LDS position.  w0/w1 (i0/i1)
+// hold the codes (ids) of this wave's first round, loaded by the caller ahead
+// of time; with PREFETCH later rounds are loaded one round ahead, otherwise at
+// round start.  `own` is this wave's k-th best as a packed key; `s_thr` is the
+// workgroup-wide minimum of those keys, shared through LDS: a vector that does
+// not beat it cannot enter the query's top-k, because k vectors seen by some
+// wave already do.
 template <int D, int M, int BUF, int SCAN_WAVES, bool PREFETCH>
 __device__ __forceinline__ void scan_list(const float* smem, const uint8_t* __restrict__ codes,
                                           const int32_t* __restrict__ ids, int start, int n, int k, int swave,
-                                          uint4 (&w0)[M / 16], uint4 (&w1)[M / 16], float& ld, int& li,
-                                          float& thr_d, int& thr_i) {
+                                          uint4 (&w0)[M / 16], uint4 (&w1)[M / 16], int& i0, int& i1, float& ld,
+                                          int& li, uint64_t& own, unsigned long long* s_thr) {
   using C = Cfg<D, M>;
   constexpr int kRound = SCAN_WAVES * kVecPerWaveRound;
   const float* lut = smem + BUF * C::LUT;
@@ -146,19 +195,33 @@ __device__ __forceinline__ void scan_list(const float* smem, const uint8_t* __re
   for (int base = swave * kVecPerWaveRound; base < n; base += kRound) {
     const int v0 = base + lane, v1 = v0 + kWave;
     uint4 n0[C::NV4], n1[C::NV4];
+    int j0 = kPadId, j1 = kPadId;
     const bool more = base + kRound < n;
     if (PREFETCH) {
-      if (more) load_pair<M>(codes, start, n, v0 + kRound, n0, n1);
+      if (more) load_pair<M>(codes, ids, start, n, v0 + kRound, n0, n1, j0, j1);
     } else if (base != swave * kVecPerWaveRound) {
-      load_pair<M>(codes, start, n, v0, w0, w1);
+      load_pair<M>(codes, ids, start, n, v0, w0, w1, i0, i1);
     }
-    const float d0 = v0 < n ? adc_sum<M>(lut, w0) : FLT_MAX;
-    const float d1 = v1 < n ? adc_sum<M>(lut, w1) : FLT_MAX;
-    offer(d0, v0 < n, start + v0, ids, k, ld, li, thr_d, thr_i);
-    offer(d1, v1 < n, start + v1, ids, k, ld, li, thr_d, thr_i);
+    const uint64_t shared_thr = *s_thr;
+    uint64_t thr = own < shared_thr ? own : shared_thr;
+    float d0, d1;
+    if (adc_sum2<M>(lut, w0, w1, v0 < n, v1 < n, __uint_as_float((uint32_t)(thr >> 32)), d0, d1)) {
+      bool changed = offer(d0, i0, v0 < n, thr, ld, li);
+      if (changed) {
+        const uint64_t kth = pack_key(readlane_f(ld, k - 1), readlane_i(li, k - 1));
+        thr = kth < thr ? kth : thr;
+      }
+      changed |= offer(d1, i1, v1 < n, thr, ld, li);
+      if (changed) {
+        own = pack_key(readlane_f(ld, k - 1), readlane_i(li, k - 1));
+        if (lane == 0) atomicMin(s_thr, (unsigned long long)own);
+      }
+    }
     if (PREFETCH && more) {
 #pragma unroll
       for (int i = 0; i < C::NV4; ++i) { w0[i] = n0[i]; w1[i] = n1[i]; }
+      i0 = j0;
+      i1 = j1;
     }
   }
 }
@@ -190,10 +253,12 @@ __global__ __launch_bounds__(kNT) void adc_plain_kernel(AdcArgs a) {
   constexpr int MG = M / G;      // subspaces per thread
   static_assert(M % G == 0, "pq_m must split across the codeword threads");
   __shared__ __align__(16) float smem[C::SMEM];
+  __shared__ unsigned long long s_thr;
   float* rbuf = smem + C::R_OFF;
   float* qs = smem + C::Q_OFF;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int kc = tid & (kPQK - 1), g = tid / kPQK;
+  if (tid == 0) s_thr = kNoThr;
   const int q = blockIdx.x;
   const int P = a.nprobe, k = a.k;
   const uint32_t NL = (uint32_t)a.nlist;
@@ -214,10 +279,12 @@ __global__ __launch_bounds__(kNT) void adc_plain_kernel(AdcArgs a) {
   if (p < P && tid < D) rbuf[tid] = qs[tid] - a.centroids[(size_t)probes[p] * D + tid];
   __syncthreads();
 
-  float ld = FLT_MAX, thr_d = FLT_MAX;
-  int li = kPadId, thr_i = kPadId;
+  float ld = FLT_MAX;
+  int li = kPadId;
+  uint64_t own = kNoThr;
   int it = 0;
   uint4 w0[C::NV4], w1[C::NV4];
+  int i0 = kPadId, i1 = kPadId;
   while (p < P) {
     const uint32_t l = probes[p];
     int pn = p + 1;
@@ -225,7 +292,7 @@ __global__ __launch_bounds__(kNT) void adc_plain_kernel(AdcArgs a) {
     const int start = a.offsets[l];
     const int n = a.offsets[l + 1] - start;
     // First-round code loads go out before the LUT build, which hides their latency.
-    load_pair<M>(a.codes, start, n, wave * kVecPerWaveRound + lane, w0, w1);
+    load_pair<M>(a.codes, a.vec_ids, start, n, wave * kVecPerWaveRound + lane, w0, w1, i0, i1);
     const int buf = C::DBUF ? (it & 1) : 0;
     float* lut = smem + buf * C::LUT;
     const float* r = rbuf + (it & 1) * D;
@@ -240,10 +307,10 @@ __global__ __launch_bounds__(kNT) void adc_plain_kernel(AdcArgs a) {
     if (pn < P && tid < D) rbuf[((it + 1) & 1) * D + tid] = qs[tid] - a.centroids[(size_t)probes[pn] * D + tid];
     __syncthreads();
     if (buf == 0)
-      scan_list<D, M, 0, kNW, false>(smem, a.codes, a.vec_ids, start, n, k, wave, w0, w1, ld, li, thr_d, thr_i);
+      scan_list<D, M, 0, kNW, false>(smem, a.codes, a.vec_ids, start, n, k, wave, w0, w1, i0, i1, ld, li, own, &s_thr);
     else
-      scan_list<D, M, (C::DBUF ? 1 : 0), kNW, false>(smem, a.codes, a.vec_ids, start, n, k, wave, w0, w1, ld, li,
-                                                    thr_d, thr_i);
+      scan_list<D, M, (C::DBUF ? 1 : 0), kNW, false>(smem, a.codes, a.vec_ids, start, n, k, wave, w0, w1, i0, i1, ld,
+                                                    li, own, &s_thr);
     if (!C::DBUF) __syncthreads();
     p = pn;
     ++it;
@@ -275,6 +342,7 @@ __global__ __launch_bounds__(kSpecWaves * kWave, 4) void adc_spec_kernel(AdcArgs
   __shared__ __align__(16) float smem[C::SMEM];
   __shared__ int plist[64];
   __shared__ int pcount;
+  __shared__ unsigned long long s_thr;
   float* rbuf = smem + C::R_OFF;
   float* qs = smem + C::Q_OFF;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -293,6 +361,7 @@ __global__ __launch_bounds__(kSpecWaves * kWave, 4) void adc_spec_kernel(AdcArgs
       if (l < NL) plist[c++] = (int)l;  // pruned (0xFFFFFFFF) or out-of-range probes are skipped
     }
     pcount = c;
+    s_thr = kNoThr;
   }
   __syncthreads();
   const int nv = pcount;
@@ -330,27 +399,28 @@ __global__ __launch_bounds__(kSpecWaves * kWave, 4) void adc_spec_kernel(AdcArgs
       __syncthreads();
     }
   } else {
-    float thr_d = FLT_MAX;
-    int thr_i = kPadId;
+    uint64_t own = kNoThr;
     uint4 w0[C::NV4], w1[C::NV4];
+    int i0 = kPadId, i1 = kPadId;
     if (nv > 0) {
       const int l0 = plist[0];
-      load_pair<M>(a.codes, a.offsets[l0], a.offsets[l0 + 1] - a.offsets[l0], swave * kVecPerWaveRound + lane, w0, w1);
+      load_pair<M>(a.codes, a.vec_ids, a.offsets[l0], a.offsets[l0 + 1] - a.offsets[l0],
+                   swave * kVecPerWaveRound + lane, w0, w1, i0, i1);
     }
     for (int f = 0; f <= nv; ++f) {
       if (f >= 1) {
         const int l = plist[f - 1];
         const int start = a.offsets[l], n = a.offsets[l + 1] - start;
         if ((f - 1) & 1)
-          scan_list<D, M, 1, kScanWaves, true>(smem, a.codes, a.vec_ids, start, n, k, swave, w0, w1, ld, li, thr_d,
-                                               thr_i);
+          scan_list<D, M, 1, kScanWaves, false>(smem, a.codes, a.vec_ids, start, n, k, swave, w0, w1, i0, i1, ld, li,
+                                               own, &s_thr);
         else
-          scan_list<D, M, 0, kScanWaves, true>(smem, a.codes, a.vec_ids, start, n, k, swave, w0, w1, ld, li, thr_d,
-                                               thr_i);
+          scan_list<D, M, 0, kScanWaves, false>(smem, a.codes, a.vec_ids, start, n, k, swave, w0, w1, i0, i1, ld, li,
+                                               own, &s_thr);
         if (f < nv) {  // first-round codes of the next list land while this phase's barrier waits
           const int l2 = plist[f];
-          load_pair<M>(a.codes, a.offsets[l2], a.offsets[l2 + 1] - a.offsets[l2], swave * kVecPerWaveRound + lane,
-                       w0, w1);
+          load_pair<M>(a.codes, a.vec_ids, a.offsets[l2], a.offsets[l2 + 1] - a.offsets[l2],
+                       swave * kVecPerWaveRound + lane, w0, w1, i0, i1);
         }
       }
       __syncthreads();
