@@ -19,7 +19,7 @@
 // Tie rule used wherever an order is needed: ascending fp32 distance, then
 // ascending id (list id / codeword index / vector id).
 //
-// Parity pinning (what checks each function; see tests/test_oracle_*.py):
+// Parity pinning (what checks each function; see tests/test_oracle.py):
 //   orc_l2_fma            closed form vs float64 (tolerance) and tiny brute force
 //   orc_lut               fp64 closed form; special cases s=2,4,8 chains
 //   orc_adc               brute force decode-and-sum identity
