@@ -166,7 +166,7 @@ def main():
         "config": {"workload": "BASELINE config 2: 1M x 128 fp32, 1024 lists, PQ M=32 x 256 (8-bit), "
                                "10k queries in one batch, nprobe=32, k=10",
                    "n": args.n, "dim": dim, "nlist": nlist, "pq_m": m, "nq": args.nq, "nprobe": nprobe, "k": k},
-        "roofline": {"bound": "hbm", "kernel": "adc_spec_kernel<128,32>", "achieved": round(adc_gbs, 1),
+        "roofline": {"bound": "hbm", "kernel": "adc_flow_kernel<128,32>", "achieved": round(adc_gbs, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(adc_gbs / HBM_PEAK_GBS, 4),
                      "traffic": read_traffic(), "algorithmic_bytes_per_launch": adc_bytes,
                      "avg_launch_ms": round(adc_ms, 4)},

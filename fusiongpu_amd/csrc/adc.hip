@@ -26,8 +26,9 @@
 //     the test is one 64-bit compare with no dependent load.  After the first
 //     list almost nothing passes.  Few passers are inserted one by one; many
 //     are bitonic-sorted and merged.  At the end the wave lists are merged.
-//   * adc_spec_kernel (pq_m <= 32): 16 waves, 8 build LUT(p+1) into one LDS
-//     buffer while 8 scan list p out of the other; one barrier per list.
+//   * adc_flow_kernel (pq_m <= 32): 16 waves; 8 build the LUTs of the coming
+//     lists into two LDS buffers while 8 scan, handing buffers over through
+//     LDS counters instead of workgroup barriers.
 //     adc_plain_kernel (pq_m 48, 64): 8 waves alternate build and scan.
 #include "common.hpp"
 #include "kernels.hpp"
@@ -226,6 +227,63 @@ __device__ __forceinline__ void scan_list(const float* smem, const uint8_t* __re
   }
 }
 
+// One round of a scanning wave: this lane's two vectors v0 and v0 + 64 of a list
+// of n (codes in w0/w1, ids in i0/i1), LUT at LDS buffer BUF.  Same filter and
+// threshold sharing as scan_list.
+template <int D, int M, int BUF>
+__device__ __forceinline__ void scan_round(const float* smem, int v0, int n, int k, const uint4 (&w0)[M / 16],
+                                           const uint4 (&w1)[M / 16], int i0, int i1, float& ld, int& li,
+                                           uint64_t& own, unsigned long long* s_thr) {
+  using C = Cfg<D, M>;
+  const float* lut = smem + BUF * C::LUT;
+  const int v1 = v0 + kWave;
+  const uint64_t shared_thr = *s_thr;
+  uint64_t thr = own < shared_thr ? own : shared_thr;
+  float d0, d1;
+  if (adc_sum2<M>(lut, w0, w1, v0 < n, v1 < n, __uint_as_float((uint32_t)(thr >> 32)), d0, d1)) {
+    bool changed = offer(d0, i0, v0 < n, thr, ld, li);
+    if (changed) {
+      const uint64_t kth = pack_key(readlane_f(ld, k - 1), readlane_i(li, k - 1));
+      thr = kth < thr ? kth : thr;
+    }
+    changed |= offer(d1, i1, v1 < n, thr, ld, li);
+    if (changed) {
+      own = pack_key(readlane_f(ld, k - 1), readlane_i(li, k - 1));
+      if ((threadIdx.x & 63) == 0) atomicMin(s_thr, (unsigned long long)own);
+    }
+  }
+}
+
+// Inclusive prefix sum across the wave.
+__device__ __forceinline__ int wave_incl_scan(int v) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int o = 1; o < kWave; o <<= 1) {
+    const int t = __shfl_up(v, o, kWave);
+    if (lane >= o) v += t;
+  }
+  return v;
+}
+
+// Workgroup-local hand-off through LDS counters.  The waits are bounded: a
+// wave that spins kSpinLimit times gives up and carries on, so every wave
+// reaches the end of the kernel whatever the counters say (with correct
+// counting the longest legitimate wait is the scan of one list, microseconds).
+constexpr int kSpinLimit = 1 << 16;
+
+__device__ __forceinline__ void lds_wait_at_least(const int* p, int target) {
+  int spins = 0;
+  while (__hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < target && ++spins < kSpinLimit)
+    __builtin_amdgcn_s_sleep(1);
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+}
+
+// Publish this wave's earlier LDS reads and writes, then add `v` to *p.
+__device__ __forceinline__ void lds_signal_add(int* p, int v) {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  if ((threadIdx.x & 63) == 0) __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
 // Merge `nw` sorted wave lists held in LDS (md/mi, 64 entries each) into this
 // wave's registers and write the k best.
 __device__ __forceinline__ void merge_and_write(float ld, int li, const float* md, const int* mi, int nw, int q, int k,
@@ -326,54 +384,100 @@ __global__ __launch_bounds__(kNT) void adc_plain_kernel(AdcArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// Wave-specialised kernel (two LUTs within the 64 KiB DS-offset reach).
-// 16 waves: waves 0-7 build LUTs (the codebook lives in their registers),
-// waves 8-15 scan.  Phase f: builders write LUT(f) into buffer f&1 while
-// scanners scan list f-1 out of buffer (f-1)&1; one barrier ends the phase.
+// Wave-specialised kernels: 16 waves; waves 0-7 build LUTs (the codebook lives
+// in their registers), waves 8-15 scan.
 constexpr int kSpecWaves = 16;
 constexpr int kBuilderWaves = 8;
 constexpr int kScanWaves = kSpecWaves - kBuilderWaves;
 
+// ---------------------------------------------------------------------------
+// Decoupled wave-specialised kernel: no workgroup barrier between lists.
+//   * the probed, non-empty lists are cut into chunks of 128 vectors (one
+//     scanner round) and numbered in coarse order; scanner wave w takes chunks
+//     w, w + 8, w + 16, ..., so a wave that finishes its part of list f moves on
+//     to list f + 1 while slower waves are still in f;
+//   * builder waves write LUT(f) into buffer b = f & 1 once every chunk of
+//     list f - 2 (the buffer's previous user) has been scanned, then add 1 to
+//     built[b]; a scanner entering list f waits for built[b] >= 8 (f / 2 + 1);
+//   * scanners add the chunks they finish to done[b] when they leave a list;
+//     the builder of list f waits for done[b] to reach the chunk count of the
+//     earlier lists of buffer b.
+// Both counters are cumulative per buffer.  A count cannot run ahead of the
+// list it stands for: a builder wave contributes to list f + 2 only after all
+// of list f is scanned, and a scanner scans list f + 2 only after it is built,
+// so the first time a threshold is met every contribution comes from earlier
+// lists of that buffer.  Deadlock-free: builders wait only on chunks of lists
+// already built, scanners take chunks in increasing order and report a list
+// before waiting on the next.  Each builder wave computes its own half of the
+// residual, so builders never wait on each other.
 template <int D, int M>
-__global__ __launch_bounds__(kSpecWaves * kWave, 4) void adc_spec_kernel(AdcArgs a) {
+__global__ __launch_bounds__(kSpecWaves * kWave, 4) void adc_flow_kernel(AdcArgs a) {
   using C = Cfg<D, M>;
-  static_assert(C::DBUF, "wave-specialised kernel needs two LUTs within the DS offset reach");
-  constexpr int MB = M / 2;  // subspaces per builder thread (512 builder threads, 2 per codeword)
-  __shared__ __align__(16) float smem[C::SMEM];
-  __shared__ int plist[64];
-  __shared__ int pcount;
+  static_assert(C::DBUF, "decoupled kernel needs two LUTs within the DS offset reach");
+  constexpr int MB = M / 2;     // subspaces per builder thread
+  constexpr int HALF = D / 2;   // residual floats per builder half
+  static_assert(HALF <= kWave, "one residual float per builder lane");
+  constexpr int kChunk = kVecPerWaveRound;
+  __shared__ __align__(16) float smem[2 * C::LUT];
+  __shared__ float qs[D];
+  __shared__ float rws[kBuilderWaves][kWave];
+  __shared__ int f_list[64], f_start[64], f_n[64], f_cst[65], f_need[64];
+  __shared__ int s_nv;
+  __shared__ int s_built[2], s_done[2];
   __shared__ unsigned long long s_thr;
-  float* rbuf = smem + C::R_OFF;
-  float* qs = smem + C::Q_OFF;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const bool builder = wave < kBuilderWaves;
-  const int kc = tid & (kPQK - 1), g = (tid >> 8) & 1;
-  const int swave = wave - kBuilderWaves;
   const int q = blockIdx.x;
   const int P = a.nprobe, k = a.k;
   const uint32_t NL = (uint32_t)a.nlist;
 
   for (int i = tid; i < D; i += kSpecWaves * kWave) qs[i] = a.queries[(size_t)q * D + i];
-  if (tid == 0) {
-    int c = 0;
-    for (int p = 0; p < P; ++p) {
-      const uint32_t l = a.probes[(size_t)q * P + p];
-      if (l < NL) plist[c++] = (int)l;  // pruned (0xFFFFFFFF) or out-of-range probes are skipped
+  if (wave == 0) {
+    // Compact the usable probes (in range, non-empty) in coarse order and
+    // number their chunks: f_cst = first chunk of each list, f_need = chunks of
+    // the earlier lists that used the same LUT buffer.
+    int l = 0, st = 0, n = 0;
+    if (lane < P) {
+      const uint32_t pl = a.probes[(size_t)q * P + lane];
+      if (pl < NL) {
+        l = (int)pl;
+        st = a.offsets[pl];
+        n = a.offsets[pl + 1] - st;
+      }
     }
-    pcount = c;
-    s_thr = kNoThr;
+    const bool valid = n > 0;
+    const uint64_t bm = __ballot(valid);
+    const int pos = __popcll(bm & ((1ull << lane) - 1ull));
+    const int nch = valid ? (n + kChunk - 1) / kChunk : 0;
+    const int incl = wave_incl_scan(nch);
+    const int ev = (pos & 1) ? 0 : nch, od = (pos & 1) ? nch : 0;
+    const int incl_e = wave_incl_scan(ev), incl_o = wave_incl_scan(od);
+    if (valid) {
+      f_list[pos] = l;
+      f_start[pos] = st;
+      f_n[pos] = n;
+      f_cst[pos] = incl - nch;
+      f_need[pos] = (pos & 1) ? incl_o - od : incl_e - ev;
+    }
+    const int nv = __popcll(bm);
+    const int total = __shfl(incl, kWave - 1, kWave);
+    if (lane == 0) {
+      f_cst[nv] = total;
+      s_nv = nv;
+      s_built[0] = 0;
+      s_built[1] = 0;
+      s_done[0] = 0;
+      s_done[1] = 0;
+      s_thr = kNoThr;
+    }
   }
   __syncthreads();
-  const int nv = pcount;
-  if (nv > 0 && tid < D) rbuf[tid] = qs[tid] - a.centroids[(size_t)plist[0] * D + tid];
-  __syncthreads();
+  const int nv = s_nv;
 
   float ld = FLT_MAX;
   int li = kPadId;
-  // The two roles run separate loops with the same barrier count (nv + 1), so
-  // the register allocator can give the codebook and the scan state the same
-  // physical registers.
   if (builder) {
+    const int kc = tid & (kPQK - 1), g = tid >> 8;
     float cb[MB * C::S];
 #pragma unroll
     for (int mm = 0; mm < MB; ++mm) {
@@ -381,74 +485,105 @@ __global__ __launch_bounds__(kSpecWaves * kWave, 4) void adc_spec_kernel(AdcArgs
 #pragma unroll
       for (int j = 0; j < C::S; ++j) cb[mm * C::S + j] = src[j];
     }
-    for (int f = 0; f <= nv; ++f) {
-      if (f < nv) {
-        float* lut = smem + (f & 1) * C::LUT;
-        const float* r = rbuf + (f & 1) * D;
+    float* rw = rws[wave];
+    float cnext = 0.0f;
+    if (nv > 0 && lane < HALF) cnext = a.centroids[(size_t)f_list[0] * D + g * HALF + lane];
+    for (int f = 0; f < nv; ++f) {
+      const float cval = cnext;
+      if (f + 1 < nv && lane < HALF) cnext = a.centroids[(size_t)f_list[f + 1] * D + g * HALF + lane];
+      if (lane < HALF) rw[lane] = qs[g * HALF + lane] - cval;
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      lds_wait_at_least(&s_done[f & 1], f_need[f]);
+      float* lut = smem + (f & 1) * C::LUT;
 #pragma unroll
-        for (int mm = 0; mm < MB; ++mm) {
-          const int m = g * MB + mm;
-          float rr[C::S];
+      for (int mm = 0; mm < MB; ++mm) {
+        float rr[C::S];
 #pragma unroll
-          for (int j = 0; j < C::S; ++j) rr[j] = r[m * C::S + j];
-          lut[m * kPQK + kc] = lut_entry<C::S>(rr, cb + mm * C::S);
-        }
-        if (f + 1 < nv && tid < D)
-          rbuf[((f + 1) & 1) * D + tid] = qs[tid] - a.centroids[(size_t)plist[f + 1] * D + tid];
+        for (int j = 0; j < C::S; ++j) rr[j] = rw[mm * C::S + j];
+        lut[(g * MB + mm) * kPQK + kc] = lut_entry<C::S>(rr, cb + mm * C::S);
       }
-      __syncthreads();
+      lds_signal_add(&s_built[f & 1], 1);
     }
   } else {
+    const int swave = wave - kBuilderWaves;
+    const int total = f_cst[nv];
     uint64_t own = kNoThr;
     uint4 w0[C::NV4], w1[C::NV4];
     int i0 = kPadId, i1 = kPadId;
-    if (nv > 0) {
-      const int l0 = plist[0];
-      load_pair<M>(a.codes, a.vec_ids, a.offsets[l0], a.offsets[l0 + 1] - a.offsets[l0],
-                   swave * kVecPerWaveRound + lane, w0, w1, i0, i1);
+    int f = 0, fready = -1, mine = 0;
+    int c = swave;
+    int start = 0, n = 0, v0 = 0;
+    auto locate = [&](int cc, int& ff) {  // advance ff to the list holding chunk cc
+      while (f_cst[ff + 1] <= cc) ++ff;
+    };
+    if (c < total) {
+      locate(c, f);
+      start = f_start[f];
+      n = f_n[f];
+      v0 = (c - f_cst[f]) * kChunk + lane;
+      load_pair<M>(a.codes, a.vec_ids, start, n, v0, w0, w1, i0, i1);
     }
-    for (int f = 0; f <= nv; ++f) {
-      if (f >= 1) {
-        const int l = plist[f - 1];
-        const int start = a.offsets[l], n = a.offsets[l + 1] - start;
-        if ((f - 1) & 1)
-          scan_list<D, M, 1, kScanWaves, false>(smem, a.codes, a.vec_ids, start, n, k, swave, w0, w1, i0, i1, ld, li,
-                                               own, &s_thr);
-        else
-          scan_list<D, M, 0, kScanWaves, false>(smem, a.codes, a.vec_ids, start, n, k, swave, w0, w1, i0, i1, ld, li,
-                                               own, &s_thr);
-        if (f < nv) {  // first-round codes of the next list land while this phase's barrier waits
-          const int l2 = plist[f];
-          load_pair<M>(a.codes, a.vec_ids, a.offsets[l2], a.offsets[l2 + 1] - a.offsets[l2],
-                       swave * kVecPerWaveRound + lane, w0, w1, i0, i1);
-        }
+    while (c < total) {
+      if (fready < f) {
+        lds_wait_at_least(&s_built[f & 1], kBuilderWaves * (f / 2 + 1));
+        fready = f;
       }
-      __syncthreads();
+      // Where this wave's next chunk lies is worked out before the scan, so its
+      // code loads can go out as soon as the scan ends.  They are not issued
+      // before it: holding a second set of codes during the scan costs more in
+      // registers than it hides, since the other scanner waves cover the load
+      // latency.
+      const int cn = c + kScanWaves;
+      int fn = f, startn = start, nn = n, v0n = v0;
+      if (cn < total) {
+        locate(cn, fn);
+        startn = f_start[fn];
+        nn = f_n[fn];
+        v0n = (cn - f_cst[fn]) * kChunk + lane;
+      }
+      if (f & 1)
+        scan_round<D, M, 1>(smem, v0, n, k, w0, w1, i0, i1, ld, li, own, &s_thr);
+      else
+        scan_round<D, M, 0>(smem, v0, n, k, w0, w1, i0, i1, ld, li, own, &s_thr);
+      ++mine;
+      if (fn != f || cn >= total) {  // leaving list f: its LUT buffer may be reused once all its chunks are in
+        lds_signal_add(&s_done[f & 1], mine);
+        mine = 0;
+      }
+      c = cn;
+      f = fn;
+      start = startn;
+      n = nn;
+      v0 = v0n;
+      if (c < total) load_pair<M>(a.codes, a.vec_ids, start, n, v0, w0, w1, i0, i1);
     }
   }
+  __syncthreads();
 
   // Merge the scanner waves' lists.
   float* md = smem;
   int* mi = reinterpret_cast<int*>(smem + kScanWaves * kWave);
   if (!builder) {
-    md[swave * kWave + lane] = ld;
-    mi[swave * kWave + lane] = li;
+    md[(wave - kBuilderWaves) * kWave + lane] = ld;
+    mi[(wave - kBuilderWaves) * kWave + lane] = li;
   }
   __syncthreads();
   if (wave == kBuilderWaves) merge_and_write(ld, li, md, mi, kScanWaves, q, k, a);
 }
 
 template <int D, int M>
-fgpu_status launch_plain(const AdcArgs& a, hipStream_t s) {
-  hipLaunchKernelGGL((adc_plain_kernel<D, M>), dim3((unsigned)a.nq), dim3(kNT), 0, s, a);
+fgpu_status launch_flow(const AdcArgs& a, hipStream_t s) {
+  FGPU_CHECK(a.nprobe <= 64, FGPU_ERR_UNSUPPORTED, "adc: nprobe must be <= 64");
+  hipLaunchKernelGGL((adc_flow_kernel<D, M>), dim3((unsigned)a.nq), dim3(kSpecWaves * kWave), 0, s, a);
   FGPU_HIP(hipGetLastError());
   return FGPU_OK;
 }
 
 template <int D, int M>
-fgpu_status launch_spec(const AdcArgs& a, hipStream_t s) {
-  FGPU_CHECK(a.nprobe <= 64, FGPU_ERR_UNSUPPORTED, "adc: nprobe must be <= 64");
-  hipLaunchKernelGGL((adc_spec_kernel<D, M>), dim3((unsigned)a.nq), dim3(kSpecWaves * kWave), 0, s, a);
+fgpu_status launch_plain(const AdcArgs& a, hipStream_t s) {
+  hipLaunchKernelGGL((adc_plain_kernel<D, M>), dim3((unsigned)a.nq), dim3(kNT), 0, s, a);
   FGPU_HIP(hipGetLastError());
   return FGPU_OK;
 }
@@ -462,12 +597,12 @@ bool adc_supported(int dim, int m) {
 fgpu_status launch_adc_plain(int dim, int m, const AdcArgs& a, hipStream_t s) {
   FGPU_CHECK(a.k >= 1 && a.k <= 64, FGPU_ERR_UNSUPPORTED, "adc: k must be in [1, 64]");
   if (a.nq <= 0) return FGPU_OK;
-  if (dim == 128 && m == 32) return launch_spec<128, 32>(a, s);
-  if (dim == 128 && m == 16) return launch_spec<128, 16>(a, s);
+  if (dim == 128 && m == 32) return launch_flow<128, 32>(a, s);
+  if (dim == 128 && m == 16) return launch_flow<128, 16>(a, s);
   if (dim == 128 && m == 64) return launch_plain<128, 64>(a, s);
   if (dim == 96 && m == 48) return launch_plain<96, 48>(a, s);
-  if (dim == 96 && m == 32) return launch_spec<96, 32>(a, s);
-  if (dim == 96 && m == 16) return launch_spec<96, 16>(a, s);
+  if (dim == 96 && m == 32) return launch_flow<96, 32>(a, s);
+  if (dim == 96 && m == 16) return launch_flow<96, 16>(a, s);
   return set_error(FGPU_ERR_UNSUPPORTED, "adc: unsupported (dim, pq_m)");
 }
 
