@@ -227,20 +227,55 @@ __device__ __forceinline__ void scan_list(const float* smem, const uint8_t* __re
   }
 }
 
-// One round of a scanning wave: this lane's two vectors v0 and v0 + 64 of a list
-// of n (codes in w0/w1, ids in i0/i1), LUT at LDS buffer BUF.  Same filter and
-// threshold sharing as scan_list.
+// Lower-bounded early abandon.  T[g] >= 0 is a float sum of the per-subspace
+// LUT minima over subspaces 8g .. M-1.  With p the partial sum after 8g terms,
+// the final distance is the rounded chain p + t_8g + ... + t_(M-1) with
+// t_m >= min_m, so by monotonicity of rounded addition it is at least the same
+// chain over the minima, which is at least (p + S)(1 - u)^r for the exact sum
+// S of those minima (r <= 32 additions, u = 2^-24).  T[g] overestimates S by at
+// most (1 + u)^r and fl(p + T[g]) adds one more rounding, so
+//   final >= fl(p + T[g]) (1 - (2r + 1) u) > fl(p + T[g]) (1 - 2^-17).
+// A vector whose final distance is <= thr therefore has
+// fl(p + T[g]) <= thr_hi = fl(thr (1 + 2^-16)): testing against thr_hi never
+// drops a vector that could enter the top-k, ties on distance included.
+template <int M>
+__device__ __forceinline__ bool adc_sum2_lb(const float* __restrict__ lut, const uint4 (&w0)[M / 16],
+                                            const uint4 (&w1)[M / 16], bool ok0, bool ok1, float thr_hi,
+                                            const float (&T)[M / 8], float& d0, float& d1) {
+  float a = 0.0f, b = 0.0f;
+#pragma unroll
+  for (int i = 0; i < M / 16; ++i) {
+    const uint32_t x[4] = {w0[i].x, w0[i].y, w0[i].z, w0[i].w};
+    const uint32_t y[4] = {w1[i].x, w1[i].y, w1[i].z, w1[i].w};
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const uint32_t cx = (x[j >> 2] >> (8 * (j & 3))) & 0xFFu;
+      const uint32_t cy = (y[j >> 2] >> (8 * (j & 3))) & 0xFFu;
+      a += lut[(i * 16 + j) * kPQK + cx];
+      b += lut[(i * 16 + j) * kPQK + cy];
+      if ((j & 7) == 7 && i * 16 + j + 1 < M) {
+        const float t = T[(i * 16 + j + 1) / 8];
+        if (!__ballot((ok0 && a + t <= thr_hi) || (ok1 && b + t <= thr_hi))) return false;
+      }
+    }
+  }
+  d0 = a;
+  d1 = b;
+  return true;
+}
+
+// One scanner round with the lower-bounded filter: thr is the packed k-th key
+// this wave filters against (own or shared, whichever is smaller).
 template <int D, int M, int BUF>
-__device__ __forceinline__ void scan_round(const float* smem, int v0, int n, int k, const uint4 (&w0)[M / 16],
-                                           const uint4 (&w1)[M / 16], int i0, int i1, float& ld, int& li,
-                                           uint64_t& own, unsigned long long* s_thr) {
+__device__ __forceinline__ void scan_round_lb(const float* smem, int v0, int n, int k, const uint4 (&w0)[M / 16],
+                                              const uint4 (&w1)[M / 16], int i0, int i1, uint64_t thr,
+                                              float thr_hi, const float (&T)[M / 8], float& ld, int& li,
+                                              uint64_t& own, unsigned long long* s_thr) {
   using C = Cfg<D, M>;
   const float* lut = smem + BUF * C::LUT;
   const int v1 = v0 + kWave;
-  const uint64_t shared_thr = *s_thr;
-  uint64_t thr = own < shared_thr ? own : shared_thr;
   float d0, d1;
-  if (adc_sum2<M>(lut, w0, w1, v0 < n, v1 < n, __uint_as_float((uint32_t)(thr >> 32)), d0, d1)) {
+  if (adc_sum2_lb<M>(lut, w0, w1, v0 < n, v1 < n, thr_hi, T, d0, d1)) {
     bool changed = offer(d0, i0, v0 < n, thr, ld, li);
     if (changed) {
       const uint64_t kth = pack_key(readlane_f(ld, k - 1), readlane_i(li, k - 1));
@@ -414,13 +449,11 @@ template <int D, int M>
 __global__ __launch_bounds__(kSpecWaves * kWave, 4) void adc_flow_kernel(AdcArgs a) {
   using C = Cfg<D, M>;
   static_assert(C::DBUF, "decoupled kernel needs two LUTs within the DS offset reach");
-  constexpr int MB = M / 2;     // subspaces per builder thread
-  constexpr int HALF = D / 2;   // residual floats per builder half
-  static_assert(HALF <= kWave, "one residual float per builder lane");
   constexpr int kChunk = kVecPerWaveRound;
   __shared__ __align__(16) float smem[2 * C::LUT];
   __shared__ float qs[D];
-  __shared__ float rws[kBuilderWaves][kWave];
+  __shared__ float rws[kBuilderWaves][16];
+  __shared__ unsigned s_min[64][M];  // per probed list: min over codewords of each LUT row (float bits)
   __shared__ int f_list[64], f_start[64], f_n[64], f_cst[65], f_need[64];
   __shared__ int s_nv;
   __shared__ int s_built[2], s_done[2];
@@ -432,6 +465,7 @@ __global__ __launch_bounds__(kSpecWaves * kWave, 4) void adc_flow_kernel(AdcArgs
   const uint32_t NL = (uint32_t)a.nlist;
 
   for (int i = tid; i < D; i += kSpecWaves * kWave) qs[i] = a.queries[(size_t)q * D + i];
+  for (int i = tid; i < 64 * M; i += kSpecWaves * kWave) (&s_min[0][0])[i] = 0x7F800000u;  // +inf
   if (wave == 0) {
     // Compact the usable probes (in range, non-empty) in coarse order and
     // number their chunks: f_cst = first chunk of each list, f_need = chunks of
@@ -477,33 +511,65 @@ __global__ __launch_bounds__(kSpecWaves * kWave, 4) void adc_flow_kernel(AdcArgs
   float ld = FLT_MAX;
   int li = kPadId;
   if (builder) {
-    const int kc = tid & (kPQK - 1), g = tid >> 8;
-    float cb[MB * C::S];
+    // Builder wave w owns subspaces w*SPW .. w*SPW + SPW-1 whole: TPM lanes per
+    // subspace, each with E codewords k = 4t + 4 TPM u + j (u < E/4, j < 4), so
+    // every 4 entries are one 16-byte LDS write and consecutive lanes write
+    // consecutive 16 bytes.  The codebook rows of those codewords stay in
+    // registers for the whole query.
+    constexpr int SPW = M / kBuilderWaves;
+    constexpr int TPM = kWave / SPW;
+    constexpr int E = kPQK / TPM;
+    constexpr int RW = SPW * C::S;  // residual floats per builder wave
+    static_assert(M % kBuilderWaves == 0 && (TPM == 16 || TPM == 32) && E % 4 == 0, "builder layout");
+    const int ms = wave * SPW + lane / TPM, t = lane % TPM;
+    float cb[E * C::S];
 #pragma unroll
-    for (int mm = 0; mm < MB; ++mm) {
-      const float* src = a.codebook + ((size_t)(g * MB + mm) * kPQK + kc) * C::S;
+    for (int u = 0; u < E / 4; ++u) {
 #pragma unroll
-      for (int j = 0; j < C::S; ++j) cb[mm * C::S + j] = src[j];
+      for (int j = 0; j < 4; ++j) {
+        const float* src = a.codebook + ((size_t)ms * kPQK + 4 * t + 4 * TPM * u + j) * C::S;
+#pragma unroll
+        for (int d = 0; d < C::S; ++d) cb[(4 * u + j) * C::S + d] = src[d];
+      }
     }
     float* rw = rws[wave];
+    const float qv = lane < RW ? qs[wave * RW + lane] : 0.0f;
     float cnext = 0.0f;
-    if (nv > 0 && lane < HALF) cnext = a.centroids[(size_t)f_list[0] * D + g * HALF + lane];
+    if (nv > 0 && lane < RW) cnext = a.centroids[(size_t)f_list[0] * D + wave * RW + lane];
     for (int f = 0; f < nv; ++f) {
-      const float cval = cnext;
-      if (f + 1 < nv && lane < HALF) cnext = a.centroids[(size_t)f_list[f + 1] * D + g * HALF + lane];
-      if (lane < HALF) rw[lane] = qs[g * HALF + lane] - cval;
+      // Residual q - c of this wave's subspaces, shared through the wave's own
+      // LDS slot (a wave's LDS accesses complete in order).
+      if (lane < RW) rw[lane] = qv - cnext;
+      if (f + 1 < nv && lane < RW) cnext = a.centroids[(size_t)f_list[f + 1] * D + wave * RW + lane];
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      float r[C::S];
+#pragma unroll
+      for (int d = 0; d < C::S; ++d) r[d] = rw[(lane / TPM) * C::S + d];
       lds_wait_at_least(&s_done[f & 1], f_need[f]);
-      float* lut = smem + (f & 1) * C::LUT;
+      float* lut = smem + (f & 1) * C::LUT + ms * kPQK + 4 * t;
+      float mn = __builtin_inff();
 #pragma unroll
-      for (int mm = 0; mm < MB; ++mm) {
-        float rr[C::S];
-#pragma unroll
-        for (int j = 0; j < C::S; ++j) rr[j] = rw[mm * C::S + j];
-        lut[(g * MB + mm) * kPQK + kc] = lut_entry<C::S>(rr, cb + mm * C::S);
+      for (int u = 0; u < E / 4; ++u) {
+        float4 v;
+        v.x = lut_entry<C::S>(r, cb + (4 * u + 0) * C::S);
+        v.y = lut_entry<C::S>(r, cb + (4 * u + 1) * C::S);
+        v.z = lut_entry<C::S>(r, cb + (4 * u + 2) * C::S);
+        v.w = lut_entry<C::S>(r, cb + (4 * u + 3) * C::S);
+        mn = fminf(mn, fminf(fminf(v.x, v.y), fminf(v.z, v.w)));
+        *reinterpret_cast<float4*>(lut + 4 * TPM * u) = v;
       }
+      // Row minimum of subspace ms: over the TPM lanes that share it.
+      mn = fminf(mn, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(mn), 0x128, 0xF, 0xF, false)));  // row_ror:8
+      mn = fminf(mn, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(mn), 0x124, 0xF, 0xF, false)));  // row_ror:4
+      mn = fminf(mn, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(mn), 0x122, 0xF, 0xF, false)));  // row_ror:2
+      mn = fminf(mn, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(mn), 0x121, 0xF, 0xF, false)));  // row_ror:1
+      if constexpr (TPM == 32) {  // rows 2i and 2i+1 share a subspace
+        const auto rr = __builtin_amdgcn_permlane16_swap(__float_as_uint(mn), __float_as_uint(mn), false, false);
+        mn = fminf(__uint_as_float(rr[0]), __uint_as_float(rr[1]));
+      }
+      if (t == 0) s_min[f][ms] = __float_as_uint(mn);
       lds_signal_add(&s_built[f & 1], 1);
     }
   } else {
@@ -525,11 +591,24 @@ __global__ __launch_bounds__(kSpecWaves * kWave, 4) void adc_flow_kernel(AdcArgs
       v0 = (c - f_cst[f]) * kChunk + lane;
       load_pair<M>(a.codes, a.vec_ids, start, n, v0, w0, w1, i0, i1);
     }
+    float T[M / 8];  // T[g] = sum of list f's row minima over subspaces 8g .. M-1
+    bool skip = false;
     while (c < total) {
       if (fready < f) {
         lds_wait_at_least(&s_built[f & 1], kBuilderWaves * (f / 2 + 1));
         fready = f;
+        float acc = 0.0f;
+#pragma unroll
+        for (int m = M - 1; m >= 0; --m) {
+          acc += __uint_as_float(s_min[f][m]);
+          if (m % 8 == 0) T[m / 8] = acc;
+        }
       }
+      const uint64_t shared_thr = s_thr;
+      const uint64_t thr = own < shared_thr ? own : shared_thr;
+      const float thr_hi = __uint_as_float((uint32_t)(thr >> 32)) * (1.0f + 0x1p-16f);
+      // Whole chunk out of reach: every vector of list f is at least T[0].
+      skip = T[0] > thr_hi;
       // Where this wave's next chunk lies is worked out before the scan, so its
       // code loads can go out as soon as the scan ends.  They are not issued
       // before it: holding a second set of codes during the scan costs more in
@@ -543,21 +622,26 @@ __global__ __launch_bounds__(kSpecWaves * kWave, 4) void adc_flow_kernel(AdcArgs
         nn = f_n[fn];
         v0n = (cn - f_cst[fn]) * kChunk + lane;
       }
-      if (f & 1)
-        scan_round<D, M, 1>(smem, v0, n, k, w0, w1, i0, i1, ld, li, own, &s_thr);
-      else
-        scan_round<D, M, 0>(smem, v0, n, k, w0, w1, i0, i1, ld, li, own, &s_thr);
+      if (!skip) {
+        if (f & 1)
+          scan_round_lb<D, M, 1>(smem, v0, n, k, w0, w1, i0, i1, thr, thr_hi, T, ld, li, own, &s_thr);
+        else
+          scan_round_lb<D, M, 0>(smem, v0, n, k, w0, w1, i0, i1, thr, thr_hi, T, ld, li, own, &s_thr);
+      }
       ++mine;
       if (fn != f || cn >= total) {  // leaving list f: its LUT buffer may be reused once all its chunks are in
         lds_signal_add(&s_done[f & 1], mine);
         mine = 0;
       }
+      // The threshold never rises, so a skipped list stays skipped: its later
+      // chunks need no codes.
+      const bool same_skipped = skip && fn == f;
       c = cn;
       f = fn;
       start = startn;
       n = nn;
       v0 = v0n;
-      if (c < total) load_pair<M>(a.codes, a.vec_ids, start, n, v0, w0, w1, i0, i1);
+      if (c < total && !same_skipped) load_pair<M>(a.codes, a.vec_ids, start, n, v0, w0, w1, i0, i1);
     }
   }
   __syncthreads();
