@@ -427,34 +427,73 @@ constexpr int kScanWaves = kSpecWaves - kBuilderWaves;
 
 // ---------------------------------------------------------------------------
 // Decoupled wave-specialised kernel: no workgroup barrier between lists.
-//   * the probed, non-empty lists are cut into chunks of 128 vectors (one
+//   * The probed, non-empty lists are cut into chunks of 128 vectors (one
 //     scanner round) and numbered in coarse order; scanner wave w takes chunks
-//     w, w + 8, w + 16, ..., so a wave that finishes its part of list f moves on
-//     to list f + 1 while slower waves are still in f;
-//   * builder waves write LUT(f) into buffer b = f & 1 once every chunk of
-//     list f - 2 (the buffer's previous user) has been scanned, then add 1 to
-//     built[b]; a scanner entering list f waits for built[b] >= 8 (f / 2 + 1);
-//   * scanners add the chunks they finish to done[b] when they leave a list;
-//     the builder of list f waits for done[b] to reach the chunk count of the
-//     earlier lists of buffer b.
+//     w, w + 8, w + 16, ..., so a wave that finishes its part of a list moves
+//     on while slower waves are still in it.
+//   * Before building list f's LUT, a builder tests a lower bound on every
+//     ADC distance the list can produce against the current k-th distance
+//     (list_lower_bound).  A list that cannot contribute is skipped: no LUT,
+//     no LDS buffer, and the scanners pass over its chunks without loading
+//     codes.  The first builder wave to reach list f records the decision in
+//     dec[f] with an LDS compare-and-swap, so every wave follows the same one.
+//     Built lists are numbered j = 0, 1, ... in order and use LUT buffer j & 1.
+//   * Builder waves write LUT j once every chunk of built list j - 2 (the
+//     buffer's previous user) has been scanned, then add 1 to built[b]; a
+//     scanner entering built list j waits for built[b] >= 8 (j / 2 + 1).
+//   * Scanners add the chunks of a built list they finish to done[b] when they
+//     leave it; the builder of list j waits for done[b] to reach the chunk
+//     count of the earlier built lists of buffer b.
 // Both counters are cumulative per buffer.  A count cannot run ahead of the
-// list it stands for: a builder wave contributes to list f + 2 only after all
-// of list f is scanned, and a scanner scans list f + 2 only after it is built,
-// so the first time a threshold is met every contribution comes from earlier
-// lists of that buffer.  Deadlock-free: builders wait only on chunks of lists
-// already built, scanners take chunks in increasing order and report a list
-// before waiting on the next.  Each builder wave computes its own half of the
-// residual, so builders never wait on each other.
+// list it stands for: a builder wave contributes to built list j + 2 only
+// after all of list j is scanned, and a scanner scans list j + 2 only after it
+// is built, so the first time a threshold is met every contribution comes
+// from earlier lists of that buffer.  Deadlock-free: builders decide lists in
+// order and wait only on chunks of lists already built; scanners take chunks
+// in increasing order and report a list before waiting on the next.  Each
+// builder wave computes its own part of the residual, so builders never wait
+// on each other.
+constexpr int kUndecided = -1;
+constexpr int kSkipped = -2;
+
+__device__ __forceinline__ int lds_wait_decided(const int* p) {
+  int spins = 0, v;
+  while ((v = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)) == kUndecided &&
+         ++spins < kSpinLimit)
+    __builtin_amdgcn_s_sleep(1);
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+  return v;
+}
+
+// Lower bound on every ADC distance of a list, from s2 = a float sum of the
+// squared residual coordinates r = fl(q - c) (the residual the LUT is built
+// from) and rl >= the norm of any decoded residual of the list.
+//   * The LUT entries and their ascending sum are chains of at most
+//     D/M + 2 + M <= 42 correctly rounded steps on non-negative terms, so the
+//     computed ADC distance is at least (1 - 2^-18) ||r - p||^2 for the
+//     decoded residual p; and ||r - p|| >= ||r|| - ||p|| >= ||r|| - rl.
+//   * s2 is within 129 u of ||r||^2 (D <= 128), so
+//     fl(sqrt(fl(s2 (1 - 2^-14)))) <= ||r||.
+//   * The returned value carries one more factor (1 - 2^-14), which covers
+//     the roundings of the subtraction and the square, so it is strictly below
+//     the computed distance of every vector in the list whenever it is > 0.
+__device__ __forceinline__ float list_lower_bound(float s2, float rl) {
+  const float nr = sqrtf(s2 * (1.0f - 0x1p-14f));
+  const float gap = nr - rl;
+  return gap > 0.0f ? gap * gap * (1.0f - 0x1p-14f) : 0.0f;
+}
+
 template <int D, int M>
 __global__ __launch_bounds__(kSpecWaves * kWave, 4) void adc_flow_kernel(AdcArgs a) {
   using C = Cfg<D, M>;
   static_assert(C::DBUF, "decoupled kernel needs two LUTs within the DS offset reach");
+  static_assert(D <= 2 * kWave, "the list bound takes two residual coordinates per lane");
   constexpr int kChunk = kVecPerWaveRound;
   __shared__ __align__(16) float smem[2 * C::LUT];
   __shared__ float qs[D];
   __shared__ float rws[kBuilderWaves][16];
   __shared__ unsigned s_min[64][M];  // per probed list: min over codewords of each LUT row (float bits)
-  __shared__ int f_list[64], f_start[64], f_n[64], f_cst[65], f_need[64];
+  __shared__ int f_list[64], f_start[64], f_n[64], f_cst[65], s_dec[64];
   __shared__ int s_nv;
   __shared__ int s_built[2], s_done[2];
   __shared__ unsigned long long s_thr;
@@ -466,10 +505,10 @@ __global__ __launch_bounds__(kSpecWaves * kWave, 4) void adc_flow_kernel(AdcArgs
 
   for (int i = tid; i < D; i += kSpecWaves * kWave) qs[i] = a.queries[(size_t)q * D + i];
   for (int i = tid; i < 64 * M; i += kSpecWaves * kWave) (&s_min[0][0])[i] = 0x7F800000u;  // +inf
+  if (tid < 64) s_dec[tid] = kUndecided;
   if (wave == 0) {
     // Compact the usable probes (in range, non-empty) in coarse order and
-    // number their chunks: f_cst = first chunk of each list, f_need = chunks of
-    // the earlier lists that used the same LUT buffer.
+    // number their chunks: f_cst[f] = first chunk of list f.
     int l = 0, st = 0, n = 0;
     if (lane < P) {
       const uint32_t pl = a.probes[(size_t)q * P + lane];
@@ -484,14 +523,11 @@ __global__ __launch_bounds__(kSpecWaves * kWave, 4) void adc_flow_kernel(AdcArgs
     const int pos = __popcll(bm & ((1ull << lane) - 1ull));
     const int nch = valid ? (n + kChunk - 1) / kChunk : 0;
     const int incl = wave_incl_scan(nch);
-    const int ev = (pos & 1) ? 0 : nch, od = (pos & 1) ? nch : 0;
-    const int incl_e = wave_incl_scan(ev), incl_o = wave_incl_scan(od);
     if (valid) {
       f_list[pos] = l;
       f_start[pos] = st;
       f_n[pos] = n;
       f_cst[pos] = incl - nch;
-      f_need[pos] = (pos & 1) ? incl_o - od : incl_e - ev;
     }
     const int nv = __popcll(bm);
     const int total = __shfl(incl, kWave - 1, kWave);
@@ -534,21 +570,51 @@ __global__ __launch_bounds__(kSpecWaves * kWave, 4) void adc_flow_kernel(AdcArgs
     }
     float* rw = rws[wave];
     const float qv = lane < RW ? qs[wave * RW + lane] : 0.0f;
-    float cnext = 0.0f;
-    if (nv > 0 && lane < RW) cnext = a.centroids[(size_t)f_list[0] * D + wave * RW + lane];
+    const float qa = lane < D ? qs[lane] : 0.0f, qb = lane + kWave < D ? qs[lane + kWave] : 0.0f;
+    // Centroid coordinates and radius of the next list, loaded one list ahead.
+    float cnext = 0.0f, ca = 0.0f, cbb = 0.0f, rnext = 0.0f;
+    auto fetch = [&](int ff) {
+      const int l = f_list[ff];
+      const float* cr = a.centroids + (size_t)l * D;
+      if (lane < RW) cnext = cr[wave * RW + lane];
+      ca = lane < D ? cr[lane] : 0.0f;
+      cbb = lane + kWave < D ? cr[lane + kWave] : 0.0f;
+      rnext = a.rmax[l];
+    };
+    if (nv > 0) fetch(0);
+    int nbuilt = 0, need0 = 0, need1 = 0;
     for (int f = 0; f < nv; ++f) {
+      const float cs = cnext, c0 = ca, c1 = cbb, rl = rnext;
+      if (f + 1 < nv) fetch(f + 1);
+      int dec = __hip_atomic_load(&s_dec[f], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      if (dec == kUndecided) {
+        const float ra = qa - c0, rb = qb - c1;
+        float s2 = ra * ra + rb * rb;
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) s2 += shfl_xor_f(s2, o);  // same value in every lane
+        s2 = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(s2)));
+        const uint64_t thr = s_thr;
+        const float thr_hi = __uint_as_float((uint32_t)(thr >> 32)) * (1.0f + 0x1p-16f);
+        const int mine = list_lower_bound(s2, rl) > thr_hi ? kSkipped : nbuilt;
+        int old = kUndecided;
+        if (lane == 0) old = atomicCAS(&s_dec[f], kUndecided, mine);
+        old = __builtin_amdgcn_readfirstlane(old);
+        dec = old == kUndecided ? mine : old;
+      }
+      if (dec == kSkipped) continue;
+      const int b = dec & 1;
+      ++nbuilt;
       // Residual q - c of this wave's subspaces, shared through the wave's own
       // LDS slot (a wave's LDS accesses complete in order).
-      if (lane < RW) rw[lane] = qv - cnext;
-      if (f + 1 < nv && lane < RW) cnext = a.centroids[(size_t)f_list[f + 1] * D + wave * RW + lane];
+      if (lane < RW) rw[lane] = qv - cs;
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
       float r[C::S];
 #pragma unroll
       for (int d = 0; d < C::S; ++d) r[d] = rw[(lane / TPM) * C::S + d];
-      lds_wait_at_least(&s_done[f & 1], f_need[f]);
-      float* lut = smem + (f & 1) * C::LUT + ms * kPQK + 4 * t;
+      lds_wait_at_least(&s_done[b], b ? need1 : need0);
+      float* lut = smem + b * C::LUT + ms * kPQK + 4 * t;
       float mn = __builtin_inff();
 #pragma unroll
       for (int u = 0; u < E / 4; ++u) {
@@ -570,7 +636,9 @@ __global__ __launch_bounds__(kSpecWaves * kWave, 4) void adc_flow_kernel(AdcArgs
         mn = fminf(__uint_as_float(rr[0]), __uint_as_float(rr[1]));
       }
       if (t == 0) s_min[f][ms] = __float_as_uint(mn);
-      lds_signal_add(&s_built[f & 1], 1);
+      lds_signal_add(&s_built[b], 1);
+      const int nch = f_cst[f + 1] - f_cst[f];
+      if (b) need1 += nch; else need0 += nch;
     }
   } else {
     const int swave = wave - kBuilderWaves;
@@ -578,70 +646,65 @@ __global__ __launch_bounds__(kSpecWaves * kWave, 4) void adc_flow_kernel(AdcArgs
     uint64_t own = kNoThr;
     uint4 w0[C::NV4], w1[C::NV4];
     int i0 = kPadId, i1 = kPadId;
-    int f = 0, fready = -1, mine = 0;
+    int f = 0, fready = -1, mine = 0, dec = kSkipped;
+    bool have = false;  // w0/w1/i0/i1 hold chunk c
+    float T[M / 8];     // T[g] = sum of list f's row minima over subspaces 8g .. M-1
     int c = swave;
-    int start = 0, n = 0, v0 = 0;
     auto locate = [&](int cc, int& ff) {  // advance ff to the list holding chunk cc
       while (f_cst[ff + 1] <= cc) ++ff;
     };
-    if (c < total) {
-      locate(c, f);
-      start = f_start[f];
-      n = f_n[f];
-      v0 = (c - f_cst[f]) * kChunk + lane;
-      load_pair<M>(a.codes, a.vec_ids, start, n, v0, w0, w1, i0, i1);
-    }
-    float T[M / 8];  // T[g] = sum of list f's row minima over subspaces 8g .. M-1
-    bool skip = false;
+    if (c < total) locate(c, f);
     while (c < total) {
+      const int start = f_start[f], n = f_n[f];
+      const int v0 = (c - f_cst[f]) * kChunk + lane;
       if (fready < f) {
-        lds_wait_at_least(&s_built[f & 1], kBuilderWaves * (f / 2 + 1));
         fready = f;
-        float acc = 0.0f;
+        dec = lds_wait_decided(&s_dec[f]);
+        if (dec >= 0) {
+          lds_wait_at_least(&s_built[dec & 1], kBuilderWaves * (dec / 2 + 1));
+          float acc = 0.0f;
 #pragma unroll
-        for (int m = M - 1; m >= 0; --m) {
-          acc += __uint_as_float(s_min[f][m]);
-          if (m % 8 == 0) T[m / 8] = acc;
+          for (int m = M - 1; m >= 0; --m) {
+            acc += __uint_as_float(s_min[f][m]);
+            if (m % 8 == 0) T[m / 8] = acc;
+          }
         }
       }
       const uint64_t shared_thr = s_thr;
       const uint64_t thr = own < shared_thr ? own : shared_thr;
       const float thr_hi = __uint_as_float((uint32_t)(thr >> 32)) * (1.0f + 0x1p-16f);
-      // Whole chunk out of reach: every vector of list f is at least T[0].
-      skip = T[0] > thr_hi;
-      // Where this wave's next chunk lies is worked out before the scan, so its
-      // code loads can go out as soon as the scan ends.  They are not issued
-      // before it: holding a second set of codes during the scan costs more in
-      // registers than it hides, since the other scanner waves cover the load
-      // latency.
+      // Skipped list, or every vector of the list at least T[0] > threshold.
+      const bool skip = dec < 0 || T[0] > thr_hi;
+      if (!skip && !have) load_pair<M>(a.codes, a.vec_ids, start, n, v0, w0, w1, i0, i1);
       const int cn = c + kScanWaves;
-      int fn = f, startn = start, nn = n, v0n = v0;
-      if (cn < total) {
-        locate(cn, fn);
-        startn = f_start[fn];
-        nn = f_n[fn];
-        v0n = (cn - f_cst[fn]) * kChunk + lane;
-      }
+      int fn = f;
+      if (cn < total) locate(cn, fn);
       if (!skip) {
-        if (f & 1)
+        if (dec & 1)
           scan_round_lb<D, M, 1>(smem, v0, n, k, w0, w1, i0, i1, thr, thr_hi, T, ld, li, own, &s_thr);
         else
           scan_round_lb<D, M, 0>(smem, v0, n, k, w0, w1, i0, i1, thr, thr_hi, T, ld, li, own, &s_thr);
       }
-      ++mine;
-      if (fn != f || cn >= total) {  // leaving list f: its LUT buffer may be reused once all its chunks are in
-        lds_signal_add(&s_done[f & 1], mine);
-        mine = 0;
+      if (dec >= 0) {
+        ++mine;
+        if (fn != f || cn >= total) {  // leaving list f: its LUT buffer may be reused once all its chunks are in
+          lds_signal_add(&s_done[dec & 1], mine);
+          mine = 0;
+        }
       }
-      // The threshold never rises, so a skipped list stays skipped: its later
-      // chunks need no codes.
-      const bool same_skipped = skip && fn == f;
+      // The next chunk's codes go out now if its list is already known to be
+      // scanned (the threshold never rises, so a skipped list stays skipped).
+      have = false;
+      if (cn < total) {
+        const int dn = fn == f ? (skip ? kSkipped : dec)
+                               : __hip_atomic_load(&s_dec[fn], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        if (dn >= 0) {
+          load_pair<M>(a.codes, a.vec_ids, f_start[fn], f_n[fn], (cn - f_cst[fn]) * kChunk + lane, w0, w1, i0, i1);
+          have = true;
+        }
+      }
       c = cn;
       f = fn;
-      start = startn;
-      n = nn;
-      v0 = v0n;
-      if (c < total && !same_skipped) load_pair<M>(a.codes, a.vec_ids, start, n, v0, w0, w1, i0, i1);
     }
   }
   __syncthreads();

@@ -399,6 +399,45 @@ fgpu_status launch1d(K kern, int64_t n, int block, hipStream_t s, A... args) {
   return FGPU_OK;
 }
 
+// ---------------------------------------------------------------------------
+// Per-list radius of the decoded residuals: rmax[l] >= ||decode(x)|| for every
+// vector x of list l, where decode(x)_m = codebook[m][code_m].  Squared
+// codeword norms and their sums are formed in double (each product of two
+// floats is exact in double; the few roundings of the sums are far below the
+// final margin), and the float result is rounded up.  One block per list.
+__global__ __launch_bounds__(256) void list_radius_kernel(const float* __restrict__ cb, int m, int sub,
+                                                          const uint8_t* __restrict__ codes,
+                                                          const int32_t* __restrict__ offsets,
+                                                          float* __restrict__ rmax) {
+  extern __shared__ double cbn2[];  // [m][256]
+  for (int i = threadIdx.x; i < m * kPQK; i += blockDim.x) {
+    double t = 0.0;
+    for (int d = 0; d < sub; ++d) {
+      const double v = cb[(size_t)i * sub + d];
+      t += v * v;
+    }
+    cbn2[i] = t;
+  }
+  __syncthreads();
+  const int l = blockIdx.x;
+  const int start = offsets[l], end = offsets[l + 1];
+  double mx = 0.0;
+  for (int v = start + threadIdx.x; v < end; v += blockDim.x) {
+    const uint8_t* c = codes + (size_t)v * m;
+    double t = 0.0;
+    for (int j = 0; j < m; ++j) t += cbn2[j * kPQK + c[j]];
+    mx = fmax(mx, t);
+  }
+  __shared__ double red[256];
+  red[threadIdx.x] = mx;
+  __syncthreads();
+  for (int o = blockDim.x / 2; o > 0; o >>= 1) {
+    if ((int)threadIdx.x < o) red[threadIdx.x] = fmax(red[threadIdx.x], red[threadIdx.x + o]);
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) rmax[l] = __double2float_ru(sqrt(red[0]) * (1.0 + 0x1p-30));
+}
+
 }  // namespace
 
 fgpu_status launch_probe_counts(const uint32_t* probes, int nq, int nprobe, int nlist, const int32_t* offsets,
@@ -521,6 +560,19 @@ fgpu_status launch_kmeans_pp(const float* x, int64_t n, int dim, int k, uint64_t
       hipLaunchKernelGGL(pp_update_kernel, dim3(nb), dim3(kPPBlock), 0, s, x, n, dim, cent + (size_t)j * dim, 0, d2,
                          (const int*)shift, w, part);
   }
+  FGPU_HIP(hipGetLastError());
+  return FGPU_OK;
+}
+
+
+fgpu_status launch_list_radius(const float* codebook, int m, int sub, const uint8_t* codes, const int32_t* offsets,
+                               int nlist, float* rmax, hipStream_t s) {
+  if (nlist <= 0) return FGPU_OK;
+  const size_t lds = (size_t)m * kPQK * sizeof(double);
+  FGPU_CHECK(lds <= 128 * 1024, FGPU_ERR_UNSUPPORTED, "list_radius: pq_m too large");
+  FGPU_HIP(hipFuncSetAttribute((const void*)list_radius_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+  hipLaunchKernelGGL(list_radius_kernel, dim3((unsigned)nlist), dim3(256), lds, s, codebook, m, sub, codes, offsets,
+                     rmax);
   FGPU_HIP(hipGetLastError());
   return FGPU_OK;
 }

@@ -24,6 +24,7 @@ struct fgpu_index {
   float* d_centroids = nullptr;
   float* d_cnorm = nullptr;      // [nlist] ||c||^2
   float* d_cnorm_max = nullptr;  // [1]
+  float* d_rmax = nullptr;       // [nlist] decoded-residual radius per list
 };
 
 namespace fgpu {
@@ -58,7 +59,8 @@ struct DevBuf {
 void free_index(fgpu_index* ix) {
   if (!ix) return;
   for (void* p : {(void*)ix->d_codebook, (void*)ix->d_offsets, (void*)ix->d_codes, (void*)ix->d_ids,
-                  (void*)ix->d_centroids, (void*)ix->d_cnorm, (void*)ix->d_cnorm_max})
+                  (void*)ix->d_centroids, (void*)ix->d_cnorm, (void*)ix->d_cnorm_max,
+                  (void*)ix->d_rmax})
     if (p) (void)hipFree(p);
   delete ix;
 }
@@ -116,7 +118,8 @@ fgpu_status fgpu_index_create(int dim, int pq_m, int nlist, int64_t total, const
   if (!alloc((void**)&ix->d_codebook, cb_bytes) || !alloc((void**)&ix->d_offsets, sizeof(int32_t) * (nlist + 1)) ||
       !alloc((void**)&ix->d_codes, (size_t)total * pq_m + 256) || !alloc((void**)&ix->d_ids, sizeof(int32_t) * total) ||
       !alloc((void**)&ix->d_centroids, sizeof(float) * (size_t)nlist * dim) ||
-      !alloc((void**)&ix->d_cnorm, sizeof(float) * nlist) || !alloc((void**)&ix->d_cnorm_max, 256)) {
+      !alloc((void**)&ix->d_cnorm, sizeof(float) * nlist) || !alloc((void**)&ix->d_cnorm_max, 256) ||
+      !alloc((void**)&ix->d_rmax, sizeof(float) * nlist)) {
     (void)hipGetLastError();
     return fail(set_error(FGPU_ERR_NOMEM, "index_create: device allocation failed"));
   }
@@ -128,6 +131,8 @@ fgpu_status fgpu_index_create(int dim, int pq_m, int nlist, int64_t total, const
     return fail(set_error(FGPU_ERR_HIP, "index_create: copy to device failed"));
   fgpu_status st = launch_row_norms(ix->d_centroids, nlist, dim, ix->d_cnorm, nullptr);
   if (st == FGPU_OK) st = launch_max_reduce(ix->d_cnorm, nlist, ix->d_cnorm_max, nullptr);
+  if (st == FGPU_OK)
+    st = launch_list_radius(ix->d_codebook, pq_m, dim / pq_m, ix->d_codes, ix->d_offsets, nlist, ix->d_rmax, nullptr);
   if (st != FGPU_OK) return fail(st);
   if (hipStreamSynchronize(nullptr) != hipSuccess) return fail(set_error(FGPU_ERR_HIP, "index_create: sync failed"));
   *out = ix;
@@ -207,7 +212,7 @@ fgpu_status fgpu_adc_search(const fgpu_index* ix, const float* dq, int nq, const
   FGPU_CHECK(ix && dq && d_probe_ids && d_out_ids && d_out_dists, FGPU_ERR_ARG, "adc_search: null argument");
   FGPU_CHECK(nq >= 0 && nprobe >= 1 && k >= 1, FGPU_ERR_ARG, "adc_search: bad sizes");
   FGPU_CHECK(adc_supported(ix->dim, ix->m), FGPU_ERR_UNSUPPORTED, "adc_search: no kernel for this (dim, pq_m)");
-  AdcArgs a{dq, ix->d_centroids, ix->d_codebook, ix->d_offsets, ix->d_codes, ix->d_ids, d_probe_ids,
+  AdcArgs a{dq, ix->d_centroids, ix->d_codebook, ix->d_offsets, ix->d_codes, ix->d_ids, d_probe_ids, ix->d_rmax,
             nq, nprobe, k, ix->nlist, d_out_ids, d_out_dists};
   return launch_adc_plain(ix->dim, ix->m, a, as_stream(stream));
 }

@@ -37,11 +37,15 @@ struct AdcArgs {
   const uint8_t* codes;     // [total][m]
   const int32_t* vec_ids;   // [total]
   const uint32_t* probes;   // [nq][nprobe]
+  const float* rmax;        // [nlist] upper bound on the norm of any decoded residual of the list
   int nq, nprobe, k, nlist;  // probe ids >= nlist are skipped like pruned ones
   int32_t* out_ids;         // [nq][k]
   float* out_d;             // [nq][k]
 };
 bool adc_supported(int dim, int m);
+// rmax[l] >= max over vectors x of list l of ||decode(x)|| (exact, rounded up).
+fgpu_status launch_list_radius(const float* codebook, int m, int sub, const uint8_t* codes, const int32_t* offsets,
+                               int nlist, float* rmax, hipStream_t s);
 fgpu_status launch_adc_plain(int dim, int m, const AdcArgs& a, hipStream_t s);
 
 // ---- build.hip ----------------------------------------------------------------
