@@ -483,17 +483,40 @@ __device__ __forceinline__ float list_lower_bound(float s2, float rl) {
   return gap > 0.0f ? gap * gap * (1.0f - 0x1p-14f) : 0.0f;
 }
 
+// list := the 64 smallest of list U the sorted list held in LDS at (pd, pi).
+__device__ __forceinline__ void wave_merge_lds64(float& d, int& id, const float* pd, const int* pi) {
+  const int lane = threadIdx.x & 63;
+  const float rd = pd[kWave - 1 - lane];
+  const int ri = pi[kWave - 1 - lane];
+  if (lt_pair(rd, ri, d, id)) {
+    d = rd;
+    id = ri;
+  }
+  wave_bitonic_merge64(d, id);
+}
+
 template <int D, int M>
 __global__ __launch_bounds__(kSpecWaves * kWave, 4) void adc_flow_kernel(AdcArgs a) {
   using C = Cfg<D, M>;
   static_assert(C::DBUF, "decoupled kernel needs two LUTs within the DS offset reach");
   static_assert(D <= 2 * kWave, "the list bound takes two residual coordinates per lane");
   constexpr int kChunk = kVecPerWaveRound;
+  // Builder layout: builder wave w owns subspaces w*SPW .. w*SPW + SPW-1
+  // whole: TPM lanes per subspace, each with E codewords k = 4t + 4 TPM u + j
+  // (u < E/4, j < 4), so every 4 entries are one 16-byte LDS write and
+  // consecutive lanes write consecutive 16 bytes.  The codebook rows of those
+  // codewords stay in registers for the whole query.
+  constexpr int SPW = M / kBuilderWaves;
+  constexpr int TPM = kWave / SPW;
+  constexpr int E = kPQK / TPM;
+  constexpr int RW = SPW * C::S;  // residual floats per builder wave
+  static_assert(M % kBuilderWaves == 0 && (TPM == 16 || TPM == 32) && E % 4 == 0, "builder layout");
   __shared__ __align__(16) float smem[2 * C::LUT];
   __shared__ float qs[D];
   __shared__ float rws[kBuilderWaves][16];
   __shared__ unsigned s_min[64][M];  // per probed list: min over codewords of each LUT row (float bits)
   __shared__ int f_list[64], f_start[64], f_n[64], f_cst[65], s_dec[64];
+  __shared__ float f_lb[64];  // list_lower_bound of each probed list
   __shared__ int s_nv;
   __shared__ int s_built[2], s_done[2];
   __shared__ unsigned long long s_thr;
@@ -503,6 +526,20 @@ __global__ __launch_bounds__(kSpecWaves * kWave, 4) void adc_flow_kernel(AdcArgs
   const int P = a.nprobe, k = a.k;
   const uint32_t NL = (uint32_t)a.nlist;
 
+  // Builder codebook registers: loaded first, so the loads overlap the set-up.
+  const int ms = wave * SPW + lane / TPM, t = lane % TPM;
+  float cb[E * C::S];
+  if (builder) {
+#pragma unroll
+    for (int u = 0; u < E / 4; ++u) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float* src = a.codebook + ((size_t)ms * kPQK + 4 * t + 4 * TPM * u + j) * C::S;
+#pragma unroll
+        for (int d = 0; d < C::S; ++d) cb[(4 * u + j) * C::S + d] = src[d];
+      }
+    }
+  }
   for (int i = tid; i < D; i += kSpecWaves * kWave) qs[i] = a.queries[(size_t)q * D + i];
   for (int i = tid; i < 64 * M; i += kSpecWaves * kWave) (&s_min[0][0])[i] = 0x7F800000u;  // +inf
   if (tid < 64) s_dec[tid] = kUndecided;
@@ -543,67 +580,75 @@ __global__ __launch_bounds__(kSpecWaves * kWave, 4) void adc_flow_kernel(AdcArgs
   }
   __syncthreads();
   const int nv = s_nv;
+  // Lower bound of every probed list, one list per wave at a time.
+  for (int f = wave; f < nv; f += kSpecWaves) {
+    const int l = f_list[f];
+    const float* cr = a.centroids + (size_t)l * D;
+    const float ra = lane < D ? qs[lane] - cr[lane] : 0.0f;
+    const float rb = lane + kWave < D ? qs[lane + kWave] - cr[lane + kWave] : 0.0f;
+    float s2 = ra * ra + rb * rb;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) s2 += shfl_xor_f(s2, o);  // same value in every lane
+    if (lane == 0) f_lb[f] = list_lower_bound(s2, a.rmax[l]);
+  }
+  __syncthreads();
+
+  // First list >= from (below nv) whose decision is not "skipped" and for which
+  // `want` holds; nv if there is none.  One LDS round trip for up to 64 lists.
+  auto next_list = [&](int from, auto want) {
+    const int g = from + lane;
+    const bool cand = g < nv && want(g) && __hip_atomic_load(&s_dec[g], __ATOMIC_RELAXED,
+                                                             __HIP_MEMORY_SCOPE_WORKGROUP) != kSkipped;
+    const uint64_t bm = __ballot(cand);
+    return bm ? from + __ffsll((unsigned long long)bm) - 1 : nv;
+  };
 
   float ld = FLT_MAX;
   int li = kPadId;
   if (builder) {
-    // Builder wave w owns subspaces w*SPW .. w*SPW + SPW-1 whole: TPM lanes per
-    // subspace, each with E codewords k = 4t + 4 TPM u + j (u < E/4, j < 4), so
-    // every 4 entries are one 16-byte LDS write and consecutive lanes write
-    // consecutive 16 bytes.  The codebook rows of those codewords stay in
-    // registers for the whole query.
-    constexpr int SPW = M / kBuilderWaves;
-    constexpr int TPM = kWave / SPW;
-    constexpr int E = kPQK / TPM;
-    constexpr int RW = SPW * C::S;  // residual floats per builder wave
-    static_assert(M % kBuilderWaves == 0 && (TPM == 16 || TPM == 32) && E % 4 == 0, "builder layout");
-    const int ms = wave * SPW + lane / TPM, t = lane % TPM;
-    float cb[E * C::S];
-#pragma unroll
-    for (int u = 0; u < E / 4; ++u) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const float* src = a.codebook + ((size_t)ms * kPQK + 4 * t + 4 * TPM * u + j) * C::S;
-#pragma unroll
-        for (int d = 0; d < C::S; ++d) cb[(4 * u + j) * C::S + d] = src[d];
-      }
-    }
     float* rw = rws[wave];
     const float qv = lane < RW ? qs[wave * RW + lane] : 0.0f;
-    const float qa = lane < D ? qs[lane] : 0.0f, qb = lane + kWave < D ? qs[lane + kWave] : 0.0f;
-    // Centroid coordinates and radius of the next list, loaded one list ahead.
-    float cnext = 0.0f, ca = 0.0f, cbb = 0.0f, rnext = 0.0f;
-    auto fetch = [&](int ff) {
-      const int l = f_list[ff];
-      const float* cr = a.centroids + (size_t)l * D;
-      if (lane < RW) cnext = cr[wave * RW + lane];
-      ca = lane < D ? cr[lane] : 0.0f;
-      cbb = lane + kWave < D ? cr[lane + kWave] : 0.0f;
-      rnext = a.rmax[l];
-    };
-    if (nv > 0) fetch(0);
+    auto any_list = [](int) { return true; };
+    // This wave's centroid coordinates of the next list that may be built,
+    // loaded ahead (cnext belongs to list cnext_f).
+    int cnext_f = nv > 0 ? 0 : nv;
+    float cnext = 0.0f;
+    if (nv > 0 && lane < RW) cnext = a.centroids[(size_t)f_list[0] * D + wave * RW + lane];
     int nbuilt = 0, need0 = 0, need1 = 0;
-    for (int f = 0; f < nv; ++f) {
-      const float cs = cnext, c0 = ca, c1 = cbb, rl = rnext;
-      if (f + 1 < nv) fetch(f + 1);
-      int dec = __hip_atomic_load(&s_dec[f], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-      if (dec == kUndecided) {
-        const float ra = qa - c0, rb = qb - c1;
-        float s2 = ra * ra + rb * rb;
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) s2 += shfl_xor_f(s2, o);  // same value in every lane
-        s2 = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(s2)));
-        const uint64_t thr = s_thr;
-        const float thr_hi = __uint_as_float((uint32_t)(thr >> 32)) * (1.0f + 0x1p-16f);
-        const int mine = list_lower_bound(s2, rl) > thr_hi ? kSkipped : nbuilt;
-        int old = kUndecided;
-        if (lane == 0) old = atomicCAS(&s_dec[f], kUndecided, mine);
-        old = __builtin_amdgcn_readfirstlane(old);
-        dec = old == kUndecided ? mine : old;
+    int f = 0;
+    while (f < nv) {
+      int dec;
+      if (wave == 0) {
+        // Builder wave 0 decides, a run at a time: the lists from f on whose
+        // bound exceeds the current threshold are skipped, and the first one
+        // that does not is built as list number nbuilt.  Later lists wait for
+        // a later (tighter) threshold.
+        dec = s_dec[f];
+        if (dec == kUndecided) {
+          const uint64_t thr = s_thr;
+          const float thr_hi = __uint_as_float((uint32_t)(thr >> 32)) * (1.0f + 0x1p-16f);
+          const int g = f + lane;
+          const bool cand = g < nv && f_lb[g] > thr_hi;
+          const uint64_t run = ~__ballot(cand);  // bit i clear: list f + i is skippable
+          const int p = run ? __ffsll((unsigned long long)run) - 1 : kWave;
+          if (lane < p && g < nv) s_dec[g] = kSkipped;
+          if (lane == p && g < nv) s_dec[g] = nbuilt;
+          __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+          dec = p > 0 ? kSkipped : nbuilt;
+        }
+      } else {
+        dec = lds_wait_decided(&s_dec[f]);
       }
-      if (dec == kSkipped) continue;
+      if (dec < 0) {
+        f = next_list(f + 1, any_list);
+        continue;
+      }
       const int b = dec & 1;
       ++nbuilt;
+      float cs = cnext;
+      if (cnext_f != f && lane < RW) cs = a.centroids[(size_t)f_list[f] * D + wave * RW + lane];
+      cnext_f = next_list(f + 1, any_list);
+      if (cnext_f < nv && lane < RW) cnext = a.centroids[(size_t)f_list[cnext_f] * D + wave * RW + lane];
       // Residual q - c of this wave's subspaces, shared through the wave's own
       // LDS slot (a wave's LDS accesses complete in order).
       if (lane < RW) rw[lane] = qv - cs;
@@ -639,85 +684,95 @@ __global__ __launch_bounds__(kSpecWaves * kWave, 4) void adc_flow_kernel(AdcArgs
       lds_signal_add(&s_built[b], 1);
       const int nch = f_cst[f + 1] - f_cst[f];
       if (b) need1 += nch; else need0 += nch;
+      f = cnext_f;
     }
   } else {
     const int swave = wave - kBuilderWaves;
-    const int total = f_cst[nv];
+    // This wave's first chunk at or after chunk cc; whether it has one in list g.
+    auto first_own = [&](int cc) { return cc + (((swave - cc) % kScanWaves) + kScanWaves) % kScanWaves; };
+    auto has_chunk = [&](int g) { return first_own(f_cst[g]) < f_cst[g + 1]; };
     uint64_t own = kNoThr;
     uint4 w0[C::NV4], w1[C::NV4];
     int i0 = kPadId, i1 = kPadId;
-    int f = 0, fready = -1, mine = 0, dec = kSkipped;
-    bool have = false;  // w0/w1/i0/i1 hold chunk c
-    float T[M / 8];     // T[g] = sum of list f's row minima over subspaces 8g .. M-1
-    int c = swave;
-    auto locate = [&](int cc, int& ff) {  // advance ff to the list holding chunk cc
-      while (f_cst[ff + 1] <= cc) ++ff;
-    };
-    if (c < total) locate(c, f);
-    while (c < total) {
-      const int start = f_start[f], n = f_n[f];
-      const int v0 = (c - f_cst[f]) * kChunk + lane;
-      if (fready < f) {
-        fready = f;
-        dec = lds_wait_decided(&s_dec[f]);
-        if (dec >= 0) {
-          lds_wait_at_least(&s_built[dec & 1], kBuilderWaves * (dec / 2 + 1));
-          float acc = 0.0f;
-#pragma unroll
-          for (int m = M - 1; m >= 0; --m) {
-            acc += __uint_as_float(s_min[f][m]);
-            if (m % 8 == 0) T[m / 8] = acc;
-          }
-        }
+    int have_c = -1;  // chunk whose codes w0/w1/i0/i1 hold (or are being loaded)
+    float T[M / 8];   // T[g] = sum of list f's row minima over subspaces 8g .. M-1
+    int f = next_list(0, has_chunk);
+    while (f < nv) {
+      const int dec = lds_wait_decided(&s_dec[f]);
+      if (dec < 0) {
+        f = next_list(f + 1, has_chunk);
+        continue;
       }
-      const uint64_t shared_thr = s_thr;
-      const uint64_t thr = own < shared_thr ? own : shared_thr;
-      const float thr_hi = __uint_as_float((uint32_t)(thr >> 32)) * (1.0f + 0x1p-16f);
-      // Skipped list, or every vector of the list at least T[0] > threshold.
-      const bool skip = dec < 0 || T[0] > thr_hi;
-      if (!skip && !have) load_pair<M>(a.codes, a.vec_ids, start, n, v0, w0, w1, i0, i1);
-      const int cn = c + kScanWaves;
-      int fn = f;
-      if (cn < total) locate(cn, fn);
-      if (!skip) {
+      const int start = f_start[f], n = f_n[f], c_end = f_cst[f + 1];
+      int c = first_own(f_cst[f]);
+      if (have_c != c) load_pair<M>(a.codes, a.vec_ids, start, n, (c - f_cst[f]) * kChunk + lane, w0, w1, i0, i1);
+      lds_wait_at_least(&s_built[dec & 1], kBuilderWaves * (dec / 2 + 1));
+      float acc = 0.0f;
+#pragma unroll
+      for (int m = M - 1; m >= 0; --m) {
+        acc += __uint_as_float(s_min[f][m]);
+        if (m % 8 == 0) T[m / 8] = acc;
+      }
+      int mine = 0;
+      while (true) {
+        const uint64_t shared_thr = s_thr;
+        const uint64_t thr = own < shared_thr ? own : shared_thr;
+        const float thr_hi = __uint_as_float((uint32_t)(thr >> 32)) * (1.0f + 0x1p-16f);
+        if (T[0] > thr_hi) {
+          // Every vector of list f is at least T[0]: this wave's remaining
+          // chunks of it are done without loading codes (the threshold never
+          // rises).
+          mine += (c_end - c + kScanWaves - 1) / kScanWaves;
+          break;
+        }
+        const int v0 = (c - f_cst[f]) * kChunk + lane;
         if (dec & 1)
           scan_round_lb<D, M, 1>(smem, v0, n, k, w0, w1, i0, i1, thr, thr_hi, T, ld, li, own, &s_thr);
         else
           scan_round_lb<D, M, 0>(smem, v0, n, k, w0, w1, i0, i1, thr, thr_hi, T, ld, li, own, &s_thr);
-      }
-      if (dec >= 0) {
         ++mine;
-        if (fn != f || cn >= total) {  // leaving list f: its LUT buffer may be reused once all its chunks are in
-          lds_signal_add(&s_done[dec & 1], mine);
-          mine = 0;
-        }
+        c += kScanWaves;
+        if (c >= c_end) break;
+        load_pair<M>(a.codes, a.vec_ids, start, n, (c - f_cst[f]) * kChunk + lane, w0, w1, i0, i1);
       }
-      // The next chunk's codes go out now if its list is already known to be
-      // scanned (the threshold never rises, so a skipped list stays skipped).
-      have = false;
-      if (cn < total) {
-        const int dn = fn == f ? (skip ? kSkipped : dec)
-                               : __hip_atomic_load(&s_dec[fn], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-        if (dn >= 0) {
-          load_pair<M>(a.codes, a.vec_ids, f_start[fn], f_n[fn], (cn - f_cst[fn]) * kChunk + lane, w0, w1, i0, i1);
-          have = true;
-        }
+      // List f done by this wave: its LUT buffer may be reused once all its
+      // chunks are in.
+      lds_signal_add(&s_done[dec & 1], mine);
+      // Next list; its first codes go out now if it is already known to be built.
+      f = next_list(f + 1, has_chunk);
+      have_c = -1;
+      if (f < nv && __hip_atomic_load(&s_dec[f], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >= 0) {
+        have_c = first_own(f_cst[f]);
+        load_pair<M>(a.codes, a.vec_ids, f_start[f], f_n[f], (have_c - f_cst[f]) * kChunk + lane, w0, w1, i0, i1);
       }
-      c = cn;
-      f = fn;
     }
   }
-  __syncthreads();
 
-  // Merge the scanner waves' lists.
+  // Merge the scanner waves' lists: a 3-level tree, pairs merged in parallel.
   float* md = smem;
   int* mi = reinterpret_cast<int*>(smem + kScanWaves * kWave);
-  if (!builder) {
-    md[(wave - kBuilderWaves) * kWave + lane] = ld;
-    mi[(wave - kBuilderWaves) * kWave + lane] = li;
-  }
+  const int sw = wave - kBuilderWaves;
   __syncthreads();
-  if (wave == kBuilderWaves) merge_and_write(ld, li, md, mi, kScanWaves, q, k, a);
+  if (!builder) {
+    md[sw * kWave + lane] = ld;
+    mi[sw * kWave + lane] = li;
+  }
+#pragma unroll
+  for (int step = 1; step < kScanWaves; step <<= 1) {
+    __syncthreads();
+    const bool active = !builder && (sw % (2 * step)) == 0;
+    if (active) wave_merge_lds64(ld, li, md + (sw + step) * kWave, mi + (sw + step) * kWave);
+    __syncthreads();
+    if (active) {
+      md[sw * kWave + lane] = ld;
+      mi[sw * kWave + lane] = li;
+    }
+  }
+  if (sw == 0 && lane < k) {
+    const bool pad = li == kPadId;
+    a.out_ids[(size_t)q * k + lane] = pad ? -1 : li;
+    a.out_d[(size_t)q * k + lane] = pad ? FLT_MAX : ld;
+  }
 }
 
 template <int D, int M>
