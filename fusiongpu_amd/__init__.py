@@ -46,6 +46,7 @@ _SIGS = {
     "fgpu_coarse_search": (_i32, [_vp, _vp, _i32, _i32, _f32, _vp, _vp, _vp, _sz, _vp]),
     "fgpu_probe_counts": (_i32, [_vp, _vp, _i32, _i32, _vp, _vp, _vp]),
     "fgpu_adc_search": (_i32, [_vp, _vp, _i32, _vp, _i32, _i32, _vp, _vp, _vp]),
+    "fgpu_adc_search_stats": (_i32, [_vp, _vp, _i32, _vp, _i32, _i32, _vp, _vp, _vp, _vp]),
     "fgpu_search_workspace_bytes": (_sz, [_i32, _i32, _i32]),
     "fgpu_search": (_i32, [_vp, _vp, _i32, _i32, _i32, _f32, _vp, _vp, _vp, _sz, _vp]),
     "fgpu_l2_topk_workspace_bytes": (_sz, [_i64, _i32]),
@@ -264,6 +265,20 @@ class Index:
         _check(lib.fgpu_adc_search(self._h, _dev_ptr(q), nq, _dev_ptr(p), nprobe, k, _dev_ptr(ids), _dev_ptr(d),
                                    _stream(stream)))
         return ids, d
+
+    def adc_search_stats(self, queries, probe_ids, k: int, out=None, stream=None):
+        """adc_search plus counters: (ids, dists, {"vectors_loaded", "luts_built", "lists_skipped"})."""
+        torch = _torch()
+        q = _to_dev(queries)
+        p = _to_dev(probe_ids)
+        nq, nprobe = p.shape
+        ids, d = out if out is not None else (torch.empty((nq, k), dtype=torch.int32, device="cuda"),
+                                              torch.empty((nq, k), dtype=torch.float32, device="cuda"))
+        st = torch.zeros(4, dtype=torch.int64, device="cuda")
+        _check(lib.fgpu_adc_search_stats(self._h, _dev_ptr(q), nq, _dev_ptr(p), nprobe, k, _dev_ptr(ids),
+                                         _dev_ptr(d), _dev_ptr(st), _stream(stream)))
+        v = st.cpu().tolist()
+        return ids, d, {"vectors_loaded": v[0], "luts_built": v[1], "lists_skipped": v[2]}
 
     def search_workspace_bytes(self, nq: int, nprobe: int) -> int:
         return lib.fgpu_search_workspace_bytes(nq, self.nlist, nprobe)

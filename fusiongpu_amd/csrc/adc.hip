@@ -407,7 +407,9 @@ __global__ __launch_bounds__(kNT) void adc_plain_kernel(AdcArgs a) {
     if (!C::DBUF) __syncthreads();
     p = pn;
     ++it;
+    if (a.stats && tid == 0) atomicAdd(&a.stats[0], (unsigned long long)n);
   }
+  if (a.stats && tid == 0) atomicAdd(&a.stats[1], (unsigned long long)it);
 
   __syncthreads();
   float* md = smem;
@@ -614,7 +616,7 @@ __global__ __launch_bounds__(kSpecWaves * kWave, 4) void adc_flow_kernel(AdcArgs
     int cnext_f = nv > 0 ? 0 : nv;
     float cnext = 0.0f;
     if (nv > 0 && lane < RW) cnext = a.centroids[(size_t)f_list[0] * D + wave * RW + lane];
-    int nbuilt = 0, need0 = 0, need1 = 0;
+    int nbuilt = 0, need0 = 0, need1 = 0, nskip = 0;
     int f = 0;
     while (f < nv) {
       int dec;
@@ -635,6 +637,7 @@ __global__ __launch_bounds__(kSpecWaves * kWave, 4) void adc_flow_kernel(AdcArgs
           if (lane == p && g < nv) s_dec[g] = nbuilt;
           __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
           dec = p > 0 ? kSkipped : nbuilt;
+          nskip += min(p, nv - f);
         }
       } else {
         dec = lds_wait_decided(&s_dec[f]);
@@ -686,6 +689,10 @@ __global__ __launch_bounds__(kSpecWaves * kWave, 4) void adc_flow_kernel(AdcArgs
       if (b) need1 += nch; else need0 += nch;
       f = cnext_f;
     }
+    if (a.stats && wave == 0 && lane == 0) {
+      atomicAdd(&a.stats[1], (unsigned long long)nbuilt);
+      atomicAdd(&a.stats[2], (unsigned long long)nskip);
+    }
   } else {
     const int swave = wave - kBuilderWaves;
     // This wave's first chunk at or after chunk cc; whether it has one in list g.
@@ -696,6 +703,8 @@ __global__ __launch_bounds__(kSpecWaves * kWave, 4) void adc_flow_kernel(AdcArgs
     int i0 = kPadId, i1 = kPadId;
     int have_c = -1;  // chunk whose codes w0/w1/i0/i1 hold (or are being loaded)
     float T[M / 8];   // T[g] = sum of list f's row minima over subspaces 8g .. M-1
+    unsigned nload = 0;  // vectors whose codes this wave loaded
+    auto chunk_vecs = [&](int g, int cc) { return (unsigned)min(kChunk, f_n[g] - (cc - f_cst[g]) * kChunk); };
     int f = next_list(0, has_chunk);
     while (f < nv) {
       const int dec = lds_wait_decided(&s_dec[f]);
@@ -705,7 +714,10 @@ __global__ __launch_bounds__(kSpecWaves * kWave, 4) void adc_flow_kernel(AdcArgs
       }
       const int start = f_start[f], n = f_n[f], c_end = f_cst[f + 1];
       int c = first_own(f_cst[f]);
-      if (have_c != c) load_pair<M>(a.codes, a.vec_ids, start, n, (c - f_cst[f]) * kChunk + lane, w0, w1, i0, i1);
+      if (have_c != c) {
+        load_pair<M>(a.codes, a.vec_ids, start, n, (c - f_cst[f]) * kChunk + lane, w0, w1, i0, i1);
+        nload += chunk_vecs(f, c);
+      }
       lds_wait_at_least(&s_built[dec & 1], kBuilderWaves * (dec / 2 + 1));
       float acc = 0.0f;
 #pragma unroll
@@ -734,6 +746,7 @@ __global__ __launch_bounds__(kSpecWaves * kWave, 4) void adc_flow_kernel(AdcArgs
         c += kScanWaves;
         if (c >= c_end) break;
         load_pair<M>(a.codes, a.vec_ids, start, n, (c - f_cst[f]) * kChunk + lane, w0, w1, i0, i1);
+        nload += chunk_vecs(f, c);
       }
       // List f done by this wave: its LUT buffer may be reused once all its
       // chunks are in.
@@ -744,8 +757,10 @@ __global__ __launch_bounds__(kSpecWaves * kWave, 4) void adc_flow_kernel(AdcArgs
       if (f < nv && __hip_atomic_load(&s_dec[f], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >= 0) {
         have_c = first_own(f_cst[f]);
         load_pair<M>(a.codes, a.vec_ids, f_start[f], f_n[f], (have_c - f_cst[f]) * kChunk + lane, w0, w1, i0, i1);
+        nload += chunk_vecs(f, have_c);
       }
     }
+    if (a.stats && lane == 0) atomicAdd(&a.stats[0], (unsigned long long)nload);
   }
 
   // Merge the scanner waves' lists: a 3-level tree, pairs merged in parallel.

@@ -217,6 +217,18 @@ fgpu_status fgpu_adc_search(const fgpu_index* ix, const float* dq, int nq, const
   return launch_adc_plain(ix->dim, ix->m, a, as_stream(stream));
 }
 
+fgpu_status fgpu_adc_search_stats(const fgpu_index* ix, const float* dq, int nq, const uint32_t* d_probe_ids,
+                                  int nprobe, int k, int32_t* d_out_ids, float* d_out_dists,
+                                  unsigned long long* d_stats, void* stream) {
+  FGPU_CHECK(ix && dq && d_probe_ids && d_out_ids && d_out_dists && d_stats, FGPU_ERR_ARG,
+             "adc_search_stats: null argument");
+  FGPU_CHECK(nq >= 0 && nprobe >= 1 && k >= 1, FGPU_ERR_ARG, "adc_search_stats: bad sizes");
+  FGPU_CHECK(adc_supported(ix->dim, ix->m), FGPU_ERR_UNSUPPORTED, "adc_search_stats: no kernel for this (dim, pq_m)");
+  AdcArgs a{dq, ix->d_centroids, ix->d_codebook, ix->d_offsets, ix->d_codes, ix->d_ids, d_probe_ids, ix->d_rmax,
+            nq, nprobe, k, ix->nlist, d_out_ids, d_out_dists, d_stats};
+  return launch_adc_plain(ix->dim, ix->m, a, as_stream(stream));
+}
+
 size_t fgpu_search_workspace_bytes(int nq, int nlist, int nprobe) {
   return carve_bytes<uint32_t>((size_t)nq * nprobe) + carve_bytes<float>((size_t)nq * nprobe) +
          fgpu_coarse_workspace_bytes(nq, nlist);

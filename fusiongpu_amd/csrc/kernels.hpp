@@ -41,6 +41,10 @@ struct AdcArgs {
   int nq, nprobe, k, nlist;  // probe ids >= nlist are skipped like pruned ones
   int32_t* out_ids;         // [nq][k]
   float* out_d;             // [nq][k]
+  // Optional instrumentation (nullptr = off), summed over the launch:
+  // [0] vectors whose codes were loaded, [1] LUTs built, [2] probed lists
+  // skipped by the list lower bound.
+  unsigned long long* stats = nullptr;
 };
 bool adc_supported(int dim, int m);
 // rmax[l] >= max over vectors x of list l of ||decode(x)|| (exact, rounded up).
