@@ -37,6 +37,9 @@ _SIGS = {
     "orc_probe_counts": (None, [_vp, _i32, _i32, _vp, _vp]),
     "orc_search_plain": (None, [_vp, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _vp, _vp, _i32]),
     "orc_knn_exact": (None, [_vp, _i32, _vp, _i64, _i32, _i32, _vp, _vp, _i32]),
+    "orc_search_two_phase": (None, [_vp, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _i32, _vp, _i32, _i32, _i32,
+                                    _f32, _i32, _vp, _vp, _vp, _vp, _vp, _i32]),
+    "orc_rerank": (None, [_vp, _i32, _i32, _vp, _i64, _vp, _vp, _i32, _i32, _i32, _f32, _i32, _vp, _vp, _vp, _i32]),
     "orc_kmeans_assign": (None, [_vp, _i64, _vp, _i32, _i32, _vp, _i32]),
     "orc_fixed_shift": (_i32, [_f32, _i64]),
     "orc_kmeans_update": (None, [_vp, _i64, _vp, _i32, _i32, _i32, _i32, _vp, _vp]),
@@ -130,6 +133,38 @@ def search_plain(q, cent, codebook, offsets, ids, codes, probe_ids, k, nthreads=
     lib.orc_search_plain(_p(q), nq, dim, m, _p(cent), _p(codebook), _p(offsets), _p(ids), _p(codes), _p(probe_ids),
                          probe_ids.shape[1], k, _p(oid), _p(od), nthreads)
     return oid, od
+
+
+def search_two_phase(q, cent, codebook, offsets, ids, codes, probe_ids, p1_lists, limit_k, threshold_coeff, rerank_m,
+                     nthreads=0):
+    """run_gpu_batch_logic restated: (top_ids [nq][rerank_m], top_dists, counts [nq], cutoffs [nq][p1], thr [nq])."""
+    q, cent, codebook, offsets, ids, codes = f32(q), f32(cent), f32(codebook), i32(offsets), i32(ids), u8(codes)
+    probe_ids = np.ascontiguousarray(probe_ids, np.uint32)
+    nq, dim = q.shape
+    nprobe = probe_ids.shape[1]
+    p1 = max(0, min(nprobe, p1_lists))
+    oid = np.empty((nq, rerank_m), np.int32)
+    od = np.empty((nq, rerank_m), np.float32)
+    cnt = np.empty(nq, np.int32)
+    cut = np.empty((nq, max(p1, 1)), np.float32)
+    thr = np.empty(nq, np.float32)
+    lib.orc_search_two_phase(_p(q), nq, dim, codebook.shape[0], _p(cent), _p(codebook), _p(offsets), _p(ids),
+                             _p(codes), cent.shape[0], _p(probe_ids), nprobe, p1_lists, limit_k, threshold_coeff,
+                             rerank_m, _p(oid), _p(od), _p(cnt), _p(cut), _p(thr), nthreads)
+    return oid, od, cnt, cut[:, :p1], thr
+
+
+def rerank(q, base, cand_ids, counts, k, mb=128, eps=0.1, beta=2, nthreads=0):
+    """run_gpu_rerank restated: (ids [nq][k], dists [nq][k], visited [nq])."""
+    q, base, cand_ids, counts = f32(q), f32(base), i32(cand_ids), i32(counts)
+    nq, dim = q.shape
+    rm = cand_ids.shape[1]
+    oid = np.empty((nq, k), np.int32)
+    od = np.empty((nq, k), np.float32)
+    vis = np.empty(nq, np.int32)
+    lib.orc_rerank(_p(q), nq, dim, _p(base), base.shape[0], _p(cand_ids), _p(counts), rm, k, mb, eps, beta, _p(oid),
+                   _p(od), _p(vis), nthreads)
+    return oid, od, vis
 
 
 def knn_exact(q, base, k, nthreads=0):

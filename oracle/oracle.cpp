@@ -25,6 +25,13 @@
 //   orc_adc               brute force decode-and-sum identity
 //   orc_coarse            brute force over all lists + tie rule
 //   orc_search_plain      brute force over all candidates of the probed lists
+//   orc_search_two_phase  reductions to orc_search_plain (p1 = nprobe with
+//                         limit_k >= list length; p1 = 0; one list at a time
+//                         for the cutoffs) and the threshold identities
+//   orc_rerank            known answers: eps < 0 (never stable) is the exact
+//                         top-k of all candidates (brute force); eps >= 1,
+//                         beta = 1 stops after one batch; a hand-built stop
+//                         sequence
 //   orc_kmeans_*          Lloyd invariants, brute-force argmin, fixed-point sum
 //   orc_pq_kmeans_fast,
 //   orc_pq_train,
@@ -279,6 +286,145 @@ void orc_search_plain(const float* q, int nq, int dim, int m, const float* cent,
         out_ids[(size_t)i * k + j] = j < top.n ? top.id[j] : -1;
         out_dists[(size_t)i * k + j] = j < top.n ? top.d[j] : FLT_MAX;
       }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// A6-A10 in their general form: the two-phase pruned scan of
+// run_gpu_batch_logic (gpu_global.cu:679-874).
+//   * phase 1 (ivf_scan_phase1_kernel, gpu_global.cu:321-390): for each of the
+//     first p1 = min(nprobe, p1_lists) probes, ADC over the whole list, the
+//     w = min(n_l, limit_k) best (dist, id) become candidates and the w-th
+//     distance is the list's cutoff; a pruned or empty probe leaves cutoff 0;
+//   * threshold (compute_threshold_kernel, gpu_global.cu:394-426):
+//     thr = coeff * min(cutoff > 0), or FLT_MAX if no cutoff is > 0;
+//   * phase 2 (ivf_scan_phase2_kernel, gpu_global.cu:428-527): for the other
+//     probes every vector with dist <= thr is a candidate (the reference's
+//     direct-codebook distance is bit-identical to the LUT distance);
+//   * compaction + segmented sort + gather (gpu_global.cu:533-576, 852-867):
+//     the candidates sorted ascending, the first rerank_m kept, padded with
+//     id -1 / FLT_MAX, counts[q] = min(#candidates, rerank_m).
+// Deviations kept on purpose: whole lists are scanned in phase 1 (the
+// reference stops at 1024 items, gpu_global.cu:346), phase 2 emits each
+// passing vector exactly once (the reference's overflow path re-writes some,
+// gpu_global.cu:508-526), all rerank_m entries are gathered (the reference's
+// gather writes at most 128, gpu_global.cu:867), and order is the tie rule
+// (dist, then id) where the reference's depends on atomic slot races.
+// Probe ids >= nlist count as pruned.  cutoffs ([nq][p1]) and thr ([nq]) are
+// optional outputs.
+void orc_search_two_phase(const float* q, int nq, int dim, int m, const float* cent,
+                          const float* codebook, const int* offsets, const int* vec_ids,
+                          const uint8_t* codes, int nlist, const uint32_t* probe_ids, int nprobe,
+                          int p1_lists, int limit_k, float threshold_coeff, int rerank_m,
+                          int* out_ids, float* out_dists, int* out_counts, float* cutoffs,
+                          float* thr_out, int nthreads) {
+  set_threads(nthreads);
+  const int p1 = std::max(0, std::min(nprobe, p1_lists));
+#pragma omp parallel
+  {
+    std::vector<float> lut((size_t)m * kPQK);
+    std::vector<std::pair<float, int>> cand, list;
+#pragma omp for schedule(dynamic, 2)
+    for (int i = 0; i < nq; ++i) {
+      const float* qi = q + (size_t)i * dim;
+      cand.clear();
+      float min_cut = FLT_MAX;
+      for (int p = 0; p < p1; ++p) {
+        const uint32_t l = probe_ids[(size_t)i * nprobe + p];
+        float cut = 0.0f;
+        if (l < (uint32_t)nlist && offsets[l + 1] > offsets[l]) {
+          orc_lut(qi, cent + (size_t)l * dim, codebook, dim, m, lut.data());
+          list.clear();
+          for (int v = offsets[l]; v < offsets[l + 1]; ++v)
+            list.push_back({orc_adc(codes + (size_t)v * m, lut.data(), m), vec_ids[v]});
+          const int w = std::min((int)list.size(), limit_k);
+          std::partial_sort(list.begin(), list.begin() + w, list.end());
+          cand.insert(cand.end(), list.begin(), list.begin() + w);
+          cut = list[w - 1].first;
+        }
+        if (cutoffs) cutoffs[(size_t)i * p1 + p] = cut;
+        if (cut > 0.0f && cut < min_cut) min_cut = cut;
+      }
+      const float thr = min_cut < FLT_MAX ? min_cut * threshold_coeff : FLT_MAX;
+      if (thr_out) thr_out[i] = thr;
+      for (int p = p1; p < nprobe; ++p) {
+        const uint32_t l = probe_ids[(size_t)i * nprobe + p];
+        if (l >= (uint32_t)nlist) continue;
+        orc_lut(qi, cent + (size_t)l * dim, codebook, dim, m, lut.data());
+        for (int v = offsets[l]; v < offsets[l + 1]; ++v) {
+          const float d = orc_adc(codes + (size_t)v * m, lut.data(), m);
+          if (d <= thr) cand.push_back({d, vec_ids[v]});
+        }
+      }
+      const int cnt = std::min((int)cand.size(), rerank_m);
+      std::partial_sort(cand.begin(), cand.begin() + cnt, cand.end());
+      for (int j = 0; j < rerank_m; ++j) {
+        out_ids[(size_t)i * rerank_m + j] = j < cnt ? cand[j].second : -1;
+        out_dists[(size_t)i * rerank_m + j] = j < cnt ? cand[j].first : FLT_MAX;
+      }
+      out_counts[i] = cnt;
+    }
+  }
+}
+
+// A11: heuristic early-stopping exact rerank (run_gpu_rerank +
+// heuristic_rerank_kernel, gpu_global.cu:603-673).  Per query, walk the first
+// counts[q] candidates (of a row of rm) in mini-batches of mb: exact
+// device-form L2 (`local_d += diff*diff` contracted, gpu_global.cu:636), merge
+// with the running top-k, chg = number of real ids in the new top-k that were
+// not in the old one; stable += 1 if (float)chg/k <= eps else stable = 0; stop
+// after beta stable batches or when the candidates run out (gpu_global.cu:
+// 615, 653-662).  Order: ascending (distance, id) with the padding entry
+// (FLT_MAX, -1) after every real entry; the reference sorts only 128 of the
+// k+mb entries (gpu_global.cu:644-647) -- all are sorted here.  A candidate id
+// outside [0, n) is skipped (treated as padding).  visited ([nq], optional) =
+// candidates evaluated.
+void orc_rerank(const float* q, int nq, int dim, const float* base, long long n,
+                const int* cand_ids, const int* counts, int rm, int k, int mb, float eps, int beta,
+                int* out_ids, float* out_dists, int* visited, int nthreads) {
+  set_threads(nthreads);
+#pragma omp parallel
+  {
+    std::vector<std::pair<float, uint32_t>> top, merged;
+#pragma omp for schedule(dynamic, 4)
+    for (int i = 0; i < nq; ++i) {
+      const float* qi = q + (size_t)i * dim;
+      top.assign(k, {FLT_MAX, 0xFFFFFFFFu});
+      int stable = 0, seen = 0;
+      const int total = std::min(counts[i], rm);
+      for (int off = 0; off < rm; off += mb) {
+        if (off >= total) break;
+        const int eff = std::min(mb, total - off);
+        merged = top;
+        for (int j = 0; j < eff; ++j) {
+          const int vid = cand_ids[(size_t)i * rm + off + j];
+          if (vid >= 0 && (long long)vid < n)
+            merged.push_back({l2_fma(qi, base + (size_t)vid * dim, dim), (uint32_t)vid});
+          else
+            merged.push_back({FLT_MAX, 0xFFFFFFFFu});
+        }
+        seen += eff;
+        std::stable_sort(merged.begin(), merged.end());
+        int chg = 0;
+        for (int j = 0; j < k; ++j) {
+          const uint32_t nid = merged[j].second;
+          if (nid == 0xFFFFFFFFu) continue;
+          bool found = false;
+          for (int t = 0; t < k; ++t)
+            if (top[t].second == nid) { found = true; break; }
+          if (!found) ++chg;
+        }
+        std::copy(merged.begin(), merged.begin() + k, top.begin());
+        if ((float)chg / (float)k <= eps) ++stable; else stable = 0;
+        if (stable >= beta) break;
+      }
+      for (int j = 0; j < k; ++j) {
+        const bool pad = top[j].second == 0xFFFFFFFFu;
+        out_ids[(size_t)i * k + j] = pad ? -1 : (int)top[j].second;
+        out_dists[(size_t)i * k + j] = pad ? FLT_MAX : top[j].first;
+      }
+      if (visited) visited[i] = seen;
     }
   }
 }
