@@ -11,6 +11,9 @@ Reference interfaces mirrored (Hello-day/FusionGPU):
   * Index.coarse_search             -> cuVS CAGRA top_m call (search_pipeline.cu:341)
   * Index.adc_search                -> run_gpu_batch_logic with p1_lists = nprobe,
                                        limit_k = rerank_m = k (gpu_global.cu:679-874)
+  * Index.two_phase_search          -> run_gpu_batch_logic, general form (gpu_global.cu:679-874)
+  * rerank                          -> run_gpu_rerank (gpu_global.cu:603-673)
+  * Index.search_rerank             -> SearchPipeline::submit_batch's device path (search_pipeline.cu:341-361)
   * kmeans_fit / l2_topk            -> run_kmeans_gpu / batch_assign_clusters (kmeans_gpu.cuh:197-324)
   * pq_train                        -> train_residual_pq_codebooks (pq_utils.h:77-138)
   * pq_encode                       -> encode_residuals_to_pq_gpu (kmeans_gpu.cuh:450-508)
@@ -26,7 +29,7 @@ import numpy as np
 __all__ = [
     "FgpuError", "lib", "lib_path", "Index", "gen_gmm", "l2_topk", "kmeans_fit", "kmeans_update",
     "fixed_shift", "pq_train", "pq_encode", "build_ivfpq", "write_ivf_data", "read_ivf_data",
-    "write_fvecs", "read_fvecs", "read_ivecs", "probe_counts",
+    "write_fvecs", "read_fvecs", "read_ivecs", "probe_counts", "rerank",
 ]
 
 lib_path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib", "libfusiongpu.so")
@@ -49,6 +52,13 @@ _SIGS = {
     "fgpu_adc_search_stats": (_i32, [_vp, _vp, _i32, _vp, _i32, _i32, _vp, _vp, _vp, _vp]),
     "fgpu_search_workspace_bytes": (_sz, [_i32, _i32, _i32]),
     "fgpu_search": (_i32, [_vp, _vp, _i32, _i32, _i32, _f32, _vp, _vp, _vp, _sz, _vp]),
+    "fgpu_two_phase_workspace_bytes": (_sz, [_i32, _i32, _i32, _i32, _i32]),
+    "fgpu_two_phase_search": (_i32, [_vp, _vp, _i32, _vp, _i32, _i32, _i32, _f32, _i32, _vp, _vp, _vp, _vp, _vp,
+                                     _vp, _sz, _vp]),
+    "fgpu_rerank": (_i32, [_vp, _i32, _i32, _vp, _i64, _vp, _vp, _i32, _i32, _i32, _f32, _i32, _vp, _vp, _vp, _vp]),
+    "fgpu_search_rerank_workspace_bytes": (_sz, [_i32, _i32, _i32, _i32, _i32, _i32]),
+    "fgpu_search_rerank": (_i32, [_vp, _vp, _i32, _i32, _f32, _i32, _i32, _f32, _i32, _vp, _i64, _i32, _i32, _f32,
+                                  _i32, _vp, _vp, _vp, _sz, _vp]),
     "fgpu_l2_topk_workspace_bytes": (_sz, [_i64, _i32]),
     "fgpu_l2_topk": (_i32, [_vp, _i64, _vp, _i32, _i32, _i32, _vp, _vp, _vp, _sz, _vp]),
     "fgpu_kmeans_workspace_bytes": (_sz, [_i32, _i32]),
@@ -280,6 +290,49 @@ class Index:
         v = st.cpu().tolist()
         return ids, d, {"vectors_loaded": v[0], "luts_built": v[1], "lists_skipped": v[2]}
 
+    def two_phase_search(self, queries, probe_ids, p1_lists: int, limit_k: int, threshold_coeff: float,
+                         rerank_m: int, want_cutoffs: bool = False, workspace=None, stream=None):
+        """run_gpu_batch_logic after the coarse step: (top_ids [nq][rerank_m], top_dists, top_counts [nq],
+        cutoffs [nq][p1] or None, thresholds [nq] or None)."""
+        torch = _torch()
+        q = _to_dev(queries)
+        p = _to_dev(probe_ids)
+        nq, nprobe = p.shape
+        p1 = max(0, min(nprobe, p1_lists))
+        ws = workspace if workspace is not None else _workspace(
+            lib.fgpu_two_phase_workspace_bytes(nq, nprobe, p1_lists, limit_k, rerank_m))
+        tid = torch.empty((nq, rerank_m), dtype=torch.int32, device="cuda")
+        td = torch.empty((nq, rerank_m), dtype=torch.float32, device="cuda")
+        tc = torch.empty(nq, dtype=torch.int32, device="cuda")
+        cut = torch.empty((nq, max(p1, 1)), dtype=torch.float32, device="cuda") if want_cutoffs else None
+        thr = torch.empty(nq, dtype=torch.float32, device="cuda") if want_cutoffs else None
+        _check(lib.fgpu_two_phase_search(self._h, _dev_ptr(q), nq, _dev_ptr(p), nprobe, p1_lists, limit_k,
+                                         threshold_coeff, rerank_m, _dev_ptr(tid), _dev_ptr(td), _dev_ptr(tc),
+                                         _dev_ptr(cut) if want_cutoffs else None,
+                                         _dev_ptr(thr) if want_cutoffs else None, _dev_ptr(ws), ws.numel(),
+                                         _stream(stream)))
+        return tid, td, tc, (cut[:, :p1] if want_cutoffs else None), thr
+
+    def search_rerank_workspace_bytes(self, nq: int, nprobe: int, p1_lists: int, limit_k: int, rerank_m: int) -> int:
+        return lib.fgpu_search_rerank_workspace_bytes(nq, self.nlist, nprobe, p1_lists, limit_k, rerank_m)
+
+    def search_rerank(self, queries, base, nprobe: int, k: int, p1_lists: int = 12, limit_k: int = 50,
+                      threshold_coeff: float = 1.0, rerank_m: int = 1000, mini_batch: int = 128, eps: float = 0.1,
+                      beta: int = 2, prune_ratio: float = 100.0, workspace=None, out=None, stream=None):
+        """coarse + two-phase scan + exact rerank (SearchPipeline's per-batch path): (ids, dists) [nq][k]."""
+        torch = _torch()
+        q = _to_dev(queries)
+        b = _to_dev(base)
+        nq = q.shape[0]
+        ws = workspace if workspace is not None else _workspace(
+            self.search_rerank_workspace_bytes(nq, nprobe, p1_lists, limit_k, rerank_m))
+        ids, d = out if out is not None else (torch.empty((nq, k), dtype=torch.int32, device="cuda"),
+                                              torch.empty((nq, k), dtype=torch.float32, device="cuda"))
+        _check(lib.fgpu_search_rerank(self._h, _dev_ptr(q), nq, nprobe, prune_ratio, p1_lists, limit_k,
+                                      threshold_coeff, rerank_m, _dev_ptr(b), b.shape[0], k, mini_batch, eps, beta,
+                                      _dev_ptr(ids), _dev_ptr(d), _dev_ptr(ws), ws.numel(), _stream(stream)))
+        return ids, d
+
     def search_workspace_bytes(self, nq: int, nprobe: int) -> int:
         return lib.fgpu_search_workspace_bytes(nq, self.nlist, nprobe)
 
@@ -305,6 +358,21 @@ def probe_counts(index: Index, probe_ids, stream=None):
     _check(lib.fgpu_probe_counts(index._h, _dev_ptr(p), nq, nprobe, _dev_ptr(counts), _dev_ptr(offs),
                                  _stream(stream)))
     return counts, offs
+
+
+def rerank(queries, base, top_ids, top_counts, k: int, mini_batch: int = 128, eps: float = 0.1, beta: int = 2,
+           stream=None):
+    """run_gpu_rerank: exact L2 over the ADC-ordered candidates with the early stop: (ids, dists, visited)."""
+    torch = _torch()
+    q, b, t, c = _to_dev(queries), _to_dev(base), _to_dev(top_ids), _to_dev(top_counts)
+    nq, dim = q.shape
+    rm = t.shape[1]
+    ids = torch.empty((nq, k), dtype=torch.int32, device="cuda")
+    d = torch.empty((nq, k), dtype=torch.float32, device="cuda")
+    vis = torch.empty(nq, dtype=torch.int32, device="cuda")
+    _check(lib.fgpu_rerank(_dev_ptr(q), nq, dim, _dev_ptr(b), b.shape[0], _dev_ptr(t), _dev_ptr(c), rm, k,
+                           mini_batch, eps, beta, _dev_ptr(ids), _dev_ptr(d), _dev_ptr(vis), _stream(stream)))
+    return ids, d, vis
 
 
 # --------------------------------------------------------------------------- exact selection + build

@@ -246,6 +246,82 @@ fgpu_status fgpu_search(const fgpu_index* ix, const float* dq, int nq, int nprob
 }
 
 // ---------------------------------------------------------------------------
+size_t fgpu_two_phase_workspace_bytes(int nq, int nprobe, int p1_lists, int limit_k, int rerank_m) {
+  const int p1 = std::max(0, std::min(nprobe, p1_lists));
+  return carve_bytes<uint64_t>((size_t)std::max(nq, 1) * two_phase_pool_cap(p1, limit_k, rerank_m));
+}
+
+fgpu_status fgpu_two_phase_search(const fgpu_index* ix, const float* dq, int nq, const uint32_t* d_probe_ids,
+                                  int nprobe, int p1_lists, int limit_k, float threshold_coeff, int rerank_m,
+                                  int32_t* d_top_ids, float* d_top_dists, int32_t* d_top_counts,
+                                  float* d_list_cutoffs, float* d_thresholds, void* ws, size_t ws_bytes,
+                                  void* stream) {
+  FGPU_CHECK(ix && dq && d_probe_ids && d_top_ids && d_top_dists && d_top_counts && ws, FGPU_ERR_ARG,
+             "two_phase_search: null argument");
+  FGPU_CHECK(nq >= 0 && nprobe >= 1 && nprobe <= 64, FGPU_ERR_ARG, "two_phase_search: need 1 <= nprobe <= 64");
+  FGPU_CHECK(limit_k >= 1 && rerank_m >= 1, FGPU_ERR_ARG, "two_phase_search: limit_k and rerank_m must be >= 1");
+  FGPU_CHECK(adc_supported(ix->dim, ix->m), FGPU_ERR_UNSUPPORTED, "two_phase_search: no kernel for this (dim, pq_m)");
+  if (nq == 0) return FGPU_OK;
+  const int p1 = std::max(0, std::min(nprobe, p1_lists));
+  const int cap = two_phase_pool_cap(p1, limit_k, rerank_m);
+  const int64_t chunk = std::min<int64_t>(nq, (int64_t)(ws_bytes / ((size_t)cap * sizeof(uint64_t))));
+  FGPU_CHECK(chunk >= 1, FGPU_ERR_WORKSPACE, "two_phase_search: workspace smaller than one query's pool");
+  for (int64_t q0 = 0; q0 < nq; q0 += chunk) {
+    const int nb = (int)std::min<int64_t>(chunk, nq - q0);
+    TwoPhaseArgs a{dq + q0 * ix->dim, ix->d_centroids, ix->d_codebook, ix->d_offsets, ix->d_codes, ix->d_ids,
+                   d_probe_ids + q0 * nprobe, ix->d_rmax, nb, nprobe, ix->nlist, p1, limit_k, threshold_coeff,
+                   rerank_m, reinterpret_cast<uint64_t*>(ws), cap, d_top_ids + q0 * rerank_m,
+                   d_top_dists + q0 * rerank_m, d_top_counts + q0,
+                   d_list_cutoffs ? d_list_cutoffs + q0 * p1 : nullptr, d_thresholds ? d_thresholds + q0 : nullptr};
+    FGPU_TRY(launch_two_phase(ix->dim, ix->m, a, as_stream(stream)));
+  }
+  return FGPU_OK;
+}
+
+fgpu_status fgpu_rerank(const float* dq, int nq, int dim, const float* d_base, int64_t n, const int32_t* d_top_ids,
+                        const int32_t* d_top_counts, int rerank_m, int k, int mini_batch, float eps, int beta,
+                        int32_t* d_final_ids, float* d_final_dists, int32_t* d_visited, void* stream) {
+  FGPU_CHECK(dq && d_base && d_top_ids && d_top_counts && d_final_ids && d_final_dists, FGPU_ERR_ARG,
+             "rerank: null argument");
+  FGPU_CHECK(nq >= 0 && n >= 0 && rerank_m >= 1 && k >= 1 && mini_batch >= 1, FGPU_ERR_ARG, "rerank: bad sizes");
+  FGPU_CHECK(((uintptr_t)d_base & 15) == 0 && ((uintptr_t)dq & 15) == 0, FGPU_ERR_ARG,
+             "rerank: base vectors and queries must be 16-byte aligned");
+  RerankArgs a{dq, d_base, (long long)n, d_top_ids, d_top_counts, nq, rerank_m, k, mini_batch, eps, beta,
+               d_final_ids, d_final_dists, d_visited};
+  return launch_rerank(dim, a, as_stream(stream));
+}
+
+size_t fgpu_search_rerank_workspace_bytes(int nq, int nlist, int nprobe, int p1_lists, int limit_k, int rerank_m) {
+  return carve_bytes<uint32_t>((size_t)nq * nprobe) + carve_bytes<float>((size_t)nq * nprobe) +
+         carve_bytes<int32_t>((size_t)nq * rerank_m) + carve_bytes<float>((size_t)nq * rerank_m) +
+         carve_bytes<int32_t>((size_t)nq) +
+         std::max(fgpu_coarse_workspace_bytes(nq, nlist),
+                  fgpu_two_phase_workspace_bytes(nq, nprobe, p1_lists, limit_k, rerank_m));
+}
+
+fgpu_status fgpu_search_rerank(const fgpu_index* ix, const float* dq, int nq, int nprobe, float prune_ratio,
+                               int p1_lists, int limit_k, float threshold_coeff, int rerank_m, const float* d_base,
+                               int64_t n, int k, int mini_batch, float eps, int beta, int32_t* d_out_ids,
+                               float* d_out_dists, void* ws, size_t ws_bytes, void* stream) {
+  FGPU_CHECK(ix && ws, FGPU_ERR_ARG, "search_rerank: null argument");
+  if (nq == 0) return FGPU_OK;
+  Carve cv(ws, ws_bytes);
+  uint32_t* pid = cv.take<uint32_t>((size_t)nq * nprobe);
+  float* pd = cv.take<float>((size_t)nq * nprobe);
+  int32_t* tid = cv.take<int32_t>((size_t)nq * rerank_m);
+  float* tdist = cv.take<float>((size_t)nq * rerank_m);
+  int32_t* tcnt = cv.take<int32_t>((size_t)nq);
+  FGPU_CHECK(cv.ok(), FGPU_ERR_WORKSPACE, "search_rerank: workspace too small");
+  void* rest = cv.base + cv.used;
+  const size_t rest_bytes = ws_bytes - cv.used;
+  FGPU_TRY(fgpu_coarse_search(ix, dq, nq, nprobe, prune_ratio, pid, pd, rest, rest_bytes, stream));
+  FGPU_TRY(fgpu_two_phase_search(ix, dq, nq, pid, nprobe, p1_lists, limit_k, threshold_coeff, rerank_m, tid, tdist,
+                                 tcnt, nullptr, nullptr, rest, rest_bytes, stream));
+  return fgpu_rerank(dq, nq, ix->dim, d_base, n, tid, tcnt, rerank_m, k, mini_batch, eps, beta, d_out_ids,
+                     d_out_dists, nullptr, stream);
+}
+
+// ---------------------------------------------------------------------------
 size_t fgpu_l2_topk_workspace_bytes(int64_t n, int nc) {
   return carve_bytes<float>(n) + carve_bytes<float>(nc) + 256 + carve_bytes<float>((size_t)topk_batch_rows(n, nc) * nc);
 }

@@ -52,6 +52,47 @@ fgpu_status launch_list_radius(const float* codebook, int m, int sub, const uint
                                int nlist, float* rmax, hipStream_t s);
 fgpu_status launch_adc_plain(int dim, int m, const AdcArgs& a, hipStream_t s);
 
+// ---- twophase.hip --------------------------------------------------------------
+struct TwoPhaseArgs {
+  const float* queries;     // [nq][dim]
+  const float* centroids;   // [nlist][dim]
+  const float* codebook;    // [m][256][dim/m]
+  const int32_t* offsets;   // [nlist+1]
+  const uint8_t* codes;     // [total][m]
+  const int32_t* vec_ids;   // [total]
+  const uint32_t* probes;   // [nq][nprobe]; ids >= nlist are skipped
+  const float* rmax;        // [nlist] decoded-residual radius per list
+  int nq, nprobe, nlist;
+  int p1;                   // phase-1 probes = min(nprobe, p1_lists)
+  int limit_k;              // per-list candidates in phase 1 (<= 64)
+  float coeff;              // threshold coefficient
+  int rerank_m;             // candidates kept (<= 4096)
+  uint64_t* pool;           // [nq][pool_cap] candidate keys (workspace)
+  int pool_cap;             // >= two_phase_pool_cap(p1, limit_k, rerank_m)
+  int32_t* top_ids;         // [nq][rerank_m]
+  float* top_d;             // [nq][rerank_m]
+  int32_t* top_counts;      // [nq]
+  float* cutoffs;           // [nq][p1] or nullptr
+  float* thr;               // [nq] or nullptr
+};
+int two_phase_pool_cap(int p1, int limit_k, int rerank_m);
+fgpu_status launch_two_phase(int dim, int m, const TwoPhaseArgs& a, hipStream_t s);
+
+struct RerankArgs {
+  const float* queries;     // [nq][dim]
+  const float* base;        // [n][dim] raw vectors
+  long long n;
+  const int32_t* cand;      // [nq][rm] candidate ids in ADC order
+  const int32_t* counts;    // [nq] valid candidates per row
+  int nq, rm, k, mb;
+  float eps;
+  int beta;
+  int32_t* out_ids;         // [nq][k]
+  float* out_d;             // [nq][k]
+  int32_t* visited;         // [nq] or nullptr
+};
+fgpu_status launch_rerank(int dim, const RerankArgs& a, hipStream_t s);
+
 // ---- build.hip ----------------------------------------------------------------
 fgpu_status launch_probe_counts(const uint32_t* probes, int nq, int nprobe, int nlist, const int32_t* offsets,
                                 int32_t* counts, int32_t* offs, hipStream_t s);

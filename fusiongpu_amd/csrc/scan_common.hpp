@@ -1,0 +1,185 @@
+// scan_common.hpp -- device building blocks shared by the ADC scan kernels
+// (adc.hip, twophase.hip): per-(query, list) LUT entries in the reference's
+// exact op order, 128-bit code loads, the sequential ADC chain with exact
+// early abandon, and the wave-level top-k offer.
+#pragma once
+
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace fgpu {
+
+constexpr int kSerialMax = 12;  // passers up to this count are inserted one by one
+
+template <int D, int M>
+struct Cfg {
+  static constexpr int S = D / M;
+  static constexpr int LUT = M * kPQK;  // floats per LUT
+  static constexpr bool DBUF = 2 * LUT * 4 <= 65536;  // both LUTs within the DS immediate-offset reach
+  static constexpr int NBUF = DBUF ? 2 : 1;
+  static constexpr int R_OFF = NBUF * LUT;      // residual double buffer [2][D]
+  static constexpr int Q_OFF = R_OFF + 2 * D;   // query [D]
+  static constexpr int SMEM = Q_OFF + D;
+  static constexpr int NV4 = M / 16;            // 128-bit code loads per vector
+  static_assert(D % M == 0, "dim must be a multiple of pq_m");
+  static_assert(M % 16 == 0, "pq_m must be a multiple of 16");
+  static_assert(LUT >= 2 * 8 * kWave, "merge area must fit in the LUT area");
+};
+
+template <int S>
+__device__ __forceinline__ float lut_entry(const float* r, const float* p) {
+  if constexpr (S == 4) {
+    const float dx = r[0] - p[0], dy = r[1] - p[1], dz = r[2] - p[2], dw = r[3] - p[3];
+    return __builtin_fmaf(dx, dx, __builtin_fmaf(dy, dy, __builtin_fmaf(dz, dz, dw * dw)));
+  } else if constexpr (S == 8) {
+    const float x1 = r[0] - p[0], y1 = r[1] - p[1], z1 = r[2] - p[2], w1 = r[3] - p[3];
+    const float x2 = r[4] - p[4], y2 = r[5] - p[5], z2 = r[6] - p[6], w2 = r[7] - p[7];
+    const float d = __builtin_fmaf(x1, x1, __builtin_fmaf(y1, y1, __builtin_fmaf(z1, z1, w1 * w1)));
+    return __builtin_fmaf(x2, x2, __builtin_fmaf(y2, y2, __builtin_fmaf(z2, z2, __builtin_fmaf(w2, w2, d))));
+  } else {
+    float d = 0.0f;
+#pragma unroll
+    for (int j = 0; j < S; ++j) {
+      const float df = r[j] - p[j];
+      d = __builtin_fmaf(df, df, d);
+    }
+    return d;
+  }
+}
+
+template <int M>
+__device__ __forceinline__ void load_codes(const uint8_t* __restrict__ codes, int64_t vec, uint4 (&w)[M / 16]) {
+  const uint4* p = reinterpret_cast<const uint4*>(codes + vec * M);
+#pragma unroll
+  for (int i = 0; i < M / 16; ++i) w[i] = p[i];
+}
+
+template <int M>
+__device__ __forceinline__ float adc_sum(const float* __restrict__ lut, const uint4 (&w)[M / 16]) {
+  float d = 0.0f;
+#pragma unroll
+  for (int i = 0; i < M / 16; ++i) {
+    const uint32_t ws[4] = {w[i].x, w[i].y, w[i].z, w[i].w};
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const uint32_t code = (ws[j >> 2] >> (8 * (j & 3))) & 0xFFu;
+      d += lut[(i * 16 + j) * kPQK + code];
+    }
+  }
+  return d;
+}
+
+// Two ADC chains at once, interleaved so each wave keeps twice as many LDS
+// gathers in flight.  Each chain is still the sequential sum over ascending m.
+// Lanes past the end of a list run on stale codes: every byte value indexes
+// inside the LUT, and the caller masks those results.
+//
+// Early abandon: every term is a sum of squares (>= +0), and adding a
+// non-negative float never lowers a rounded sum, so a partial sum already above
+// thr_d bounds the final distance from below.  After each group of 8
+// subspaces, if no valid lane of either chain is still <= thr_d, the wave
+// stops: none of its vectors can enter the top-k (a vector equal to thr_d
+// could still win on its id, so equality keeps a lane alive).  Returns false
+// in that case; otherwise d0/d1 are the complete, exact distances.
+template <int M>
+__device__ __forceinline__ bool adc_sum2(const float* __restrict__ lut, const uint4 (&w0)[M / 16],
+                                         const uint4 (&w1)[M / 16], bool ok0, bool ok1, float thr_d, float& d0,
+                                         float& d1) {
+  float a = 0.0f, b = 0.0f;
+#pragma unroll
+  for (int i = 0; i < M / 16; ++i) {
+    const uint32_t x[4] = {w0[i].x, w0[i].y, w0[i].z, w0[i].w};
+    const uint32_t y[4] = {w1[i].x, w1[i].y, w1[i].z, w1[i].w};
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const uint32_t cx = (x[j >> 2] >> (8 * (j & 3))) & 0xFFu;
+      const uint32_t cy = (y[j >> 2] >> (8 * (j & 3))) & 0xFFu;
+      a += lut[(i * 16 + j) * kPQK + cx];
+      b += lut[(i * 16 + j) * kPQK + cy];
+      if ((j & 7) == 7 && i * 16 + j + 1 < M) {
+        if (!__ballot((ok0 && a <= thr_d) || (ok1 && b <= thr_d))) return false;
+      }
+    }
+  }
+  d0 = a;
+  d1 = b;
+  return true;
+}
+
+// (distance, id) packed so that unsigned order is the tie rule: distances are
+// sums of squares (never negative, never -0), so their bit patterns order like
+// the floats; ids are non-negative.
+__device__ __forceinline__ uint64_t pack_key(float d, int id) {
+  return ((uint64_t)__float_as_uint(d) << 32) | (uint32_t)id;
+}
+// "No threshold yet": the padding entry (FLT_MAX, kPadId); every real
+// candidate is below it and its distance part is a finite float.
+constexpr uint64_t kNoThr = ((uint64_t)0x7F7FFFFFu << 32) | (uint32_t)kPadId;
+
+// Offer one (distance, id) per lane to the wave's running top-64 list; only
+// pairs strictly below `thr` (the k-th best known to the workgroup) enter.
+// Returns true if the list changed.
+__device__ __forceinline__ bool offer(float d, int id, bool valid, uint64_t thr, float& ld, int& li) {
+  const bool pass = valid && pack_key(d, id) < thr;
+  uint64_t bm = __ballot(pass);
+  if (!bm) return false;
+  if (__popcll(bm) > kSerialMax) {
+    float cd = pass ? d : FLT_MAX;
+    int ci = pass ? id : kPadId;
+    wave_sort64(cd, ci);
+    wave_merge_sorted64(ld, li, cd, ci);
+  } else {
+    while (bm) {
+      const int src = __ffsll((unsigned long long)bm) - 1;
+      bm &= bm - 1;
+      wave_insert64(ld, li, readlane_f(d, src), readlane_i(id, src));
+    }
+  }
+  return true;
+}
+
+// Each scanning wave takes 128 consecutive vectors per round (two per lane).
+constexpr int kVecPerWaveRound = 2 * kWave;
+
+// Codes and vector ids of this lane's two vectors of a round (ids come along
+// so the top-k filter never waits on a dependent load).
+template <int M>
+__device__ __forceinline__ void load_pair(const uint8_t* __restrict__ codes, const int32_t* __restrict__ ids, int start,
+                                          int n, int v0, uint4 (&w0)[M / 16], uint4 (&w1)[M / 16], int& i0, int& i1) {
+  if (v0 < n) { load_codes<M>(codes, (int64_t)start + v0, w0); i0 = ids[start + v0]; }
+  if (v0 + kWave < n) { load_codes<M>(codes, (int64_t)start + v0 + kWave, w1); i1 = ids[start + v0 + kWave]; }
+}
+
+
+// Inclusive prefix sum across the wave.
+__device__ __forceinline__ int wave_incl_scan(int v) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int o = 1; o < kWave; o <<= 1) {
+    const int t = __shfl_up(v, o, kWave);
+    if (lane >= o) v += t;
+  }
+  return v;
+}
+
+// Lower bound on every ADC distance of a list, from s2 = a float sum of the
+// squared residual coordinates r = fl(q - c) (the residual the LUT is built
+// from) and rl >= the norm of any decoded residual of the list.
+//   * The LUT entries and their ascending sum are chains of at most
+//     D/M + 2 + M <= 68 correctly rounded steps on non-negative terms (M <= 64),
+//     so the computed ADC distance is at least (1 - 2^-17) ||r - p||^2 for the
+//     decoded residual p; and ||r - p|| >= ||r|| - ||p|| >= ||r|| - rl.
+//   * s2 is within 129 u of ||r||^2 (D <= 128), so
+//     fl(sqrt(fl(s2 (1 - 2^-14)))) <= ||r||.
+//   * The returned value carries one more factor (1 - 2^-14); with the four
+//     roundings of the subtraction, the square and that product it stays
+//     below (1 - 2^-14 + 4u) (||r|| - rl)^2 < (1 - 2^-17) (||r|| - rl)^2, so it
+//     is strictly below the computed distance of every vector in the list
+//     whenever it is > 0.
+__device__ __forceinline__ float list_lower_bound(float s2, float rl) {
+  const float nr = sqrtf(s2 * (1.0f - 0x1p-14f));
+  const float gap = nr - rl;
+  return gap > 0.0f ? gap * gap * (1.0f - 0x1p-14f) : 0.0f;
+}
+
+}  // namespace fgpu

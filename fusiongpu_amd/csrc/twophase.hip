@@ -1,0 +1,541 @@
+// twophase.hip -- the general form of the reference's per-batch search and its
+// exact rerank.
+//
+// Reference: run_gpu_batch_logic (gpu_global.cu:679-874) runs phase 1
+// (ivf_scan_phase1_kernel, :321-390: per-list top-limit_k + cutoff), the
+// threshold (compute_threshold_kernel, :394-426), phase 2
+// (ivf_scan_phase2_kernel, :428-527: every vector with dist <= thr), then
+// compaction, a segmented radix sort of every candidate and a gather of the
+// first rerank_m (:533-576, :798-867), with two blocking host round trips to
+// size the candidate pool (:739-763, :813-849).  run_gpu_rerank
+// (:603-673) then walks the top rerank_m in mini-batches of exact L2.
+//
+// Here one workgroup owns one query for the whole search:
+//   * phase-1 lists: LUT in LDS, all 8 waves scan with a per-list shared
+//     threshold, the wave lists are merged and the list's w best plus its
+//     cutoff are appended to the query's candidate pool;
+//   * phase-2 lists: a list whose lower bound (residual norm minus the list's
+//     decoded-residual radius) exceeds the threshold is skipped whole;
+//     otherwise passers are appended with wave ballot + mbcnt compaction;
+//   * the pool lives in the workspace.  When it would overflow, the workgroup
+//     radix-selects the rerank_m best, keeps only those and admits later
+//     candidates only below the rerank_m-th key: exact, bounded memory, no
+//     host round trip;
+//   * at the end a select and an LDS bitonic sort give the top rerank_m.
+// The rerank kernel gives each query one 128-thread workgroup: exact
+// distances one candidate per lane, wave bitonic sorts and a merge-path merge
+// with the running top-k in LDS.
+#include "common.hpp"
+#include "kernels.hpp"
+#include "scan_common.hpp"
+
+namespace fgpu {
+namespace {
+
+constexpr int kTW = 8;                               // waves per workgroup
+constexpr int kTT = kTW * kWave;                     // 512 threads
+constexpr int kTRound = kTW * kVecPerWaveRound;      // vectors per workgroup round
+constexpr int kSortMax = 4096;                       // rerank_m limit (final LDS sort)
+constexpr uint64_t kNoKey = ~0ull;                   // "no admission bound yet"
+
+template <int D, int M>
+struct TCfg {
+  static constexpr int S = D / M;
+  static constexpr int LUT = M * kPQK;
+  static constexpr int SMEM = LUT > 2 * kSortMax ? LUT : 2 * kSortMax;  // floats: LUT, later the sort area
+  static constexpr int NV4 = M / 16;
+};
+
+__device__ __forceinline__ float key_dist(uint64_t key) {
+  return key == kNoKey ? FLT_MAX : __uint_as_float((uint32_t)(key >> 32));
+}
+
+// Keeps the R smallest keys of pool[0..cnt) (cnt > R) in pool[0..R), in no
+// particular order, and returns the R-th smallest key K: every kept key is
+// <= K, so a later candidate can still enter the R best only if its key is
+// < K.  MSB-first radix select, 8 bits a pass, over the full 64-bit key, then
+// an in-place stream compaction: round r reads pool[r*512 + tid] before it
+// writes, and its writes land below (r+1)*512, where later rounds no longer
+// read.  Every thread of the workgroup calls it.
+__device__ uint64_t pool_select(uint64_t* pool, int cnt, int R, int* hist, int* misc) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  uint64_t prefix = 0, mask = 0;
+  int need = R;
+  for (int shift = 56; shift >= 0; shift -= 8) {
+    for (int i = tid; i < 256; i += kTT) hist[i] = 0;
+    __syncthreads();
+    for (int i = tid; i < cnt; i += kTT) {
+      const uint64_t key = pool[i];
+      if ((key & mask) == prefix) atomicAdd(&hist[(key >> shift) & 255], 1);
+    }
+    __syncthreads();
+    if (wave == 0) {
+      const int h0 = hist[4 * lane], h1 = hist[4 * lane + 1], h2 = hist[4 * lane + 2], h3 = hist[4 * lane + 3];
+      const int tot = h0 + h1 + h2 + h3;
+      const int incl = wave_incl_scan(tot), excl = incl - tot;
+      if (excl < need && need <= incl) {
+        int r = need - excl, b = 4 * lane;
+        if (r > h0) {
+          r -= h0; ++b;
+          if (r > h1) {
+            r -= h1; ++b;
+            if (r > h2) { r -= h2; ++b; }
+          }
+        }
+        misc[0] = b;
+        misc[1] = r;
+      }
+    }
+    __syncthreads();
+    prefix |= (uint64_t)misc[0] << shift;
+    mask |= (uint64_t)0xFF << shift;
+    need = misc[1];
+  }
+  const uint64_t K = prefix;  // exactly the R-th smallest; `need` copies of K complete the R
+  if (tid == 0) misc[2] = 0;
+  __syncthreads();
+  int out = 0;
+  for (int r0 = 0; r0 < cnt; r0 += kTT) {
+    const int i = r0 + tid;
+    const uint64_t key = i < cnt ? pool[i] : kNoKey;
+    const bool keep = i < cnt && (key < K || (key == K && atomicAdd(&misc[2], 1) < need));
+    const uint64_t bm = __ballot(keep);
+    if (lane == 0) hist[wave] = __popcll(bm);
+    __syncthreads();
+    int before = 0, total = 0;
+#pragma unroll
+    for (int w = 0; w < kTW; ++w) {
+      const int c = hist[w];
+      before += w < wave ? c : 0;
+      total += c;
+    }
+    if (keep) pool[out + before + __popcll(bm & ((1ull << lane) - 1ull))] = key;
+    out += total;
+    __syncthreads();
+  }
+  return K;
+}
+
+// Ascending bitonic sort of sk[0..np2) (np2 a power of two) by all threads.
+__device__ void lds_bitonic_sort(uint64_t* sk, int np2) {
+  for (int size = 2; size <= np2; size <<= 1) {
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      for (int i = threadIdx.x; i < (np2 >> 1); i += kTT) {
+        const int lo = 2 * i - (i & (stride - 1)), hi = lo + stride;
+        const bool up = (lo & size) == 0;
+        const uint64_t x = sk[lo], y = sk[hi];
+        if ((x > y) == up) {
+          sk[lo] = y;
+          sk[hi] = x;
+        }
+      }
+      __syncthreads();
+    }
+  }
+}
+
+template <int D, int M>
+__global__ __launch_bounds__(kTT) void two_phase_kernel(TwoPhaseArgs a) {
+  using C = TCfg<D, M>;
+  constexpr int G = kTT / kPQK;  // threads sharing one codeword
+  constexpr int MG = M / G;      // subspaces per thread in the LUT build
+  static_assert(M % G == 0 && M % 16 == 0 && D % M == 0, "geometry");
+  static_assert(D <= 2 * kWave, "the list bound takes two residual coordinates per lane");
+  __shared__ __align__(16) float smem[C::SMEM];
+  __shared__ float rbuf[2][D];
+  __shared__ float qs[D];
+  __shared__ float md[kTW * kWave];
+  __shared__ int mi[kTW * kWave];
+  __shared__ int hist[256];
+  __shared__ int misc[4];
+  __shared__ float s_cut[64];
+  __shared__ int s_cnt;
+  __shared__ unsigned long long s_lthr, s_adm;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int kc = tid & (kPQK - 1), g = tid / kPQK;
+  const int q = blockIdx.x;
+  const int P = a.nprobe, p1 = a.p1, R = a.rerank_m, cap = a.pool_cap, K1 = a.limit_k;
+  const uint32_t NL = (uint32_t)a.nlist;
+  const uint32_t* probes = a.probes + (size_t)q * P;
+  uint64_t* pool = a.pool + (size_t)q * cap;
+
+  float cb[MG * C::S];
+#pragma unroll
+  for (int mm = 0; mm < MG; ++mm) {
+    const float* src = a.codebook + ((size_t)(g * MG + mm) * kPQK + kc) * C::S;
+#pragma unroll
+    for (int j = 0; j < C::S; ++j) cb[mm * C::S + j] = src[j];
+  }
+  for (int i = tid; i < D; i += kTT) qs[i] = a.queries[(size_t)q * D + i];
+  if (tid < 64) s_cut[tid] = 0.0f;
+  if (tid == 0) {
+    s_cnt = 0;
+    s_lthr = kNoThr;
+    s_adm = kNoKey;
+  }
+  __syncthreads();
+
+  float* lut = smem;
+  auto build_lut = [&](const float* r) {
+#pragma unroll
+    for (int mm = 0; mm < MG; ++mm) {
+      const int m = g * MG + mm;
+      float rr[C::S];
+#pragma unroll
+      for (int j = 0; j < C::S; ++j) rr[j] = r[m * C::S + j];
+      lut[m * kPQK + kc] = lut_entry<C::S>(rr, cb + mm * C::S);
+    }
+  };
+
+  uint4 w0[C::NV4], w1[C::NV4];
+  int i0 = kPadId, i1 = kPadId;
+  int it = 0;  // non-empty lists seen so far: selects the residual buffer
+
+  // ---------------- phase 1: per-list top-limit_k and cutoffs
+  int cnt_w0 = 0;  // only wave 0 appends during phase 1
+  for (int p = 0; p < p1; ++p) {
+    const uint32_t l = probes[p];
+    int start = 0, n = 0;
+    if (l < NL) {
+      start = a.offsets[l];
+      n = a.offsets[l + 1] - start;
+    }
+    if (n == 0) continue;  // pruned, out of range or empty: cutoff stays 0
+    float* r = rbuf[it & 1];
+    if (tid < D) r[tid] = qs[tid] - a.centroids[(size_t)l * D + tid];
+    load_pair<M>(a.codes, a.vec_ids, start, n, wave * kVecPerWaveRound + lane, w0, w1, i0, i1);
+    __syncthreads();  // residual ready; the previous list's merge is done
+    build_lut(r);
+    __syncthreads();  // LUT ready
+    float ld = FLT_MAX;
+    int li = kPadId;
+    uint64_t own = kNoThr;
+    for (int base = wave * kVecPerWaveRound; base < n; base += kTRound) {
+      if (base != wave * kVecPerWaveRound) load_pair<M>(a.codes, a.vec_ids, start, n, base + lane, w0, w1, i0, i1);
+      const int v0 = base + lane, v1 = v0 + kWave;
+      const uint64_t shared_thr = s_lthr;
+      uint64_t thr = own < shared_thr ? own : shared_thr;
+      float d0, d1;
+      if (adc_sum2<M>(lut, w0, w1, v0 < n, v1 < n, __uint_as_float((uint32_t)(thr >> 32)), d0, d1)) {
+        bool changed = offer(d0, i0, v0 < n, thr, ld, li);
+        if (changed) {
+          const uint64_t kth = pack_key(readlane_f(ld, K1 - 1), readlane_i(li, K1 - 1));
+          thr = kth < thr ? kth : thr;
+        }
+        changed |= offer(d1, i1, v1 < n, thr, ld, li);
+        if (changed) {
+          own = pack_key(readlane_f(ld, K1 - 1), readlane_i(li, K1 - 1));
+          if (lane == 0) atomicMin(&s_lthr, (unsigned long long)own);
+        }
+      }
+    }
+    md[wave * kWave + lane] = ld;
+    mi[wave * kWave + lane] = li;
+    __syncthreads();  // every wave's list of this list is in LDS
+    if (wave == 0) {
+#pragma unroll 1
+      for (int w = 1; w < kTW; ++w) wave_merge_sorted64(ld, li, md[w * kWave + lane], mi[w * kWave + lane]);
+      const int w = n < K1 ? n : K1;
+      if (lane < w) pool[cnt_w0 + lane] = pack_key(ld, li);
+      const float cut = readlane_f(ld, w - 1);
+      if (lane == 0) {
+        s_cut[p] = cut;
+        s_lthr = kNoThr;
+      }
+      cnt_w0 += w;
+    }
+    ++it;
+  }
+  if (tid == 0) s_cnt = cnt_w0;
+  __syncthreads();
+
+  // ---------------- threshold (compute_threshold_kernel): coeff * min(cutoff > 0)
+  float min_cut = FLT_MAX;
+  for (int p = 0; p < p1; ++p) {
+    const float c = s_cut[p];
+    if (c > 0.0f && c < min_cut) min_cut = c;
+  }
+  const float thr = min_cut < FLT_MAX ? min_cut * a.coeff : FLT_MAX;
+  if (a.cutoffs && tid < p1) a.cutoffs[(size_t)q * p1 + tid] = s_cut[tid];
+  if (a.thr && tid == 0) a.thr[q] = thr;
+
+  // ---------------- phase 2: every vector with dist <= thr, bounded pool
+  const int seg = cap - R;  // vectors per segment: their passers always fit after a select
+  for (int p = p1; p < P; ++p) {
+    const uint32_t l = probes[p];
+    int start = 0, n = 0;
+    if (l < NL) {
+      start = a.offsets[l];
+      n = a.offsets[l + 1] - start;
+    }
+    if (n == 0) continue;
+    float* r = rbuf[it & 1];
+    ++it;
+    if (tid < D) r[tid] = qs[tid] - a.centroids[(size_t)l * D + tid];
+    __syncthreads();  // residual ready; every append of earlier lists is done
+    int cnt0 = s_cnt;
+    uint64_t adm = s_adm;
+    float thr_d = fminf(thr, key_dist(adm));
+    // Lower bound on every ADC distance of the list (same value in every wave).
+    {
+      const float ra = lane < D ? r[lane] : 0.0f;
+      const float rb = lane + kWave < D ? r[lane + kWave] : 0.0f;
+      float s2 = ra * ra + rb * rb;
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) s2 += shfl_xor_f(s2, o);
+      if (list_lower_bound(s2, a.rmax[l]) > thr_d * (1.0f + 0x1p-16f)) continue;
+    }
+    load_pair<M>(a.codes, a.vec_ids, start, n, wave * kVecPerWaveRound + lane, w0, w1, i0, i1);
+    build_lut(r);
+    __syncthreads();  // LUT ready; every thread has read cnt0
+    int s0 = 0;
+    while (true) {
+      const int s1 = n - s0 > seg ? s0 + seg : n;
+      if (cnt0 + (s1 - s0) > cap) {
+        adm = pool_select(pool, cnt0, R, hist, misc);
+        cnt0 = R;
+        if (tid == 0) {
+          s_cnt = R;
+          s_adm = adm;
+        }
+        __syncthreads();
+        thr_d = fminf(thr, key_dist(adm));
+      }
+      for (int base = s0 + wave * kVecPerWaveRound; base < s1; base += kTRound) {
+        if (base != wave * kVecPerWaveRound) load_pair<M>(a.codes, a.vec_ids, start, n, base + lane, w0, w1, i0, i1);
+        const int v0 = base + lane, v1 = v0 + kWave;
+        float d0, d1;
+        if (adc_sum2<M>(lut, w0, w1, v0 < s1, v1 < s1, thr_d, d0, d1)) {
+          const uint64_t k0 = pack_key(d0, i0), k1 = pack_key(d1, i1);
+          const bool pass0 = v0 < s1 && d0 <= thr && k0 < adm;
+          const bool pass1 = v1 < s1 && d1 <= thr && k1 < adm;
+          const uint64_t b0 = __ballot(pass0), b1 = __ballot(pass1);
+          const int c0 = __popcll(b0), c = c0 + __popcll(b1);
+          if (c) {
+            int at = 0;
+            if (lane == 0) at = atomicAdd(&s_cnt, c);
+            at = __shfl(at, 0, kWave);
+            const uint64_t below = (1ull << lane) - 1ull;
+            if (pass0) pool[at + __popcll(b0 & below)] = k0;
+            if (pass1) pool[at + c0 + __popcll(b1 & below)] = k1;
+          }
+        }
+      }
+      if (s1 >= n) break;
+      s0 = s1;
+      __syncthreads();  // the segment's appends are done
+      cnt0 = s_cnt;
+      __syncthreads();  // everyone has read the count before new appends
+    }
+  }
+
+  // ---------------- top rerank_m: select, LDS bitonic sort, gather
+  __syncthreads();
+  int cnt = s_cnt;
+  if (cnt > R) {
+    pool_select(pool, cnt, R, hist, misc);
+    cnt = R;
+  }
+  uint64_t* sk = reinterpret_cast<uint64_t*>(smem);
+  int np2 = 1;
+  while (np2 < cnt) np2 <<= 1;
+  for (int i = tid; i < np2; i += kTT) sk[i] = i < cnt ? pool[i] : kNoKey;
+  __syncthreads();
+  lds_bitonic_sort(sk, np2);
+  for (int j = tid; j < R; j += kTT) {
+    const bool real = j < cnt;
+    const uint64_t key = real ? sk[j] : 0;
+    a.top_ids[(size_t)q * R + j] = real ? (int32_t)(uint32_t)key : -1;
+    a.top_d[(size_t)q * R + j] = real ? __uint_as_float((uint32_t)(key >> 32)) : FLT_MAX;
+  }
+  if (tid == 0) a.top_counts[q] = cnt;
+}
+
+template <int D, int M>
+fgpu_status launch_tp(const TwoPhaseArgs& a, int nq, hipStream_t s) {
+  hipLaunchKernelGGL((two_phase_kernel<D, M>), dim3((unsigned)nq), dim3(kTT), 0, s, a);
+  FGPU_HIP(hipGetLastError());
+  return FGPU_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Exact rerank.  128 threads per query; thread t evaluates candidate t of a
+// mini-batch (mb <= 128) with the reference's exact distance (sequential
+// fused chain over the dimensions, gpu_global.cu:636).
+constexpr int kRT = 2 * kWave;
+
+template <int D>
+__global__ __launch_bounds__(kRT) void rerank_kernel(RerankArgs a) {
+  __shared__ float qs[D];
+  __shared__ float td[2][256];  // running top-k (double-buffered), ascending
+  __shared__ int ti[2][256];
+  __shared__ float nd[kRT];     // the batch, sorted
+  __shared__ int ni[kRT];
+  __shared__ int s_chg, s_stable, s_fin;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int q = blockIdx.x, k = a.k, mb = a.mb, rm = a.rm;
+  for (int i = tid; i < D; i += kRT) qs[i] = a.queries[(size_t)q * D + i];
+  for (int i = tid; i < k; i += kRT) {
+    td[0][i] = FLT_MAX;
+    ti[0][i] = kPadId;
+  }
+  if (tid == 0) {
+    s_stable = 0;
+    s_fin = 0;
+  }
+  const int total = min(a.counts[q], rm);
+  const int32_t* cand = a.cand + (size_t)q * rm;
+  __syncthreads();
+  int cur = 0, seen = 0;
+  for (int off = 0; off < rm && off < total; off += mb) {
+    const int eff = min(mb, total - off);
+    seen += eff;
+    // exact distances, one candidate per thread
+    float d = FLT_MAX;
+    int id = kPadId;
+    if (tid < eff) {
+      const int vid = cand[off + tid];
+      if (vid >= 0 && (long long)vid < a.n) {
+        const float4* row = reinterpret_cast<const float4*>(a.base + (size_t)vid * D);
+        float acc = 0.0f;
+#pragma unroll 8
+        for (int j = 0; j < D / 4; ++j) {
+          const float4 v = row[j];
+          float df = qs[4 * j] - v.x;
+          acc = __builtin_fmaf(df, df, acc);
+          df = qs[4 * j + 1] - v.y;
+          acc = __builtin_fmaf(df, df, acc);
+          df = qs[4 * j + 2] - v.z;
+          acc = __builtin_fmaf(df, df, acc);
+          df = qs[4 * j + 3] - v.w;
+          acc = __builtin_fmaf(df, df, acc);
+        }
+        d = acc;
+        id = vid;
+      }
+    }
+    // sort the batch: each wave its 64, then a merge by ranks into nd/ni
+    wave_sort64(d, id);
+    nd[tid] = d;
+    ni[tid] = id;
+    if (tid == 0) s_chg = 0;
+    __syncthreads();
+    {
+      const float* od = nd + (wave ^ 1) * kWave;
+      const int* oi = ni + (wave ^ 1) * kWave;
+      // rank in the other wave's sorted list: wave 0 counts strictly smaller
+      // entries, wave 1 counts smaller-or-equal ones, so equal pairs keep a
+      // fixed order and every position is taken once.
+      int lo = 0, hi = kWave;
+      while (lo < hi) {
+        const int mid = (lo + hi) >> 1;
+        const bool before = wave == 0 ? lt_pair(od[mid], oi[mid], d, id) : !lt_pair(d, id, od[mid], oi[mid]);
+        if (before) lo = mid + 1; else hi = mid;
+      }
+      __syncthreads();
+      nd[lane + lo] = d;
+      ni[lane + lo] = id;
+    }
+    __syncthreads();
+    // merge the sorted batch (nd/ni, kRT entries) with the top-k (td/ti[cur])
+    const float* ctd = td[cur];
+    const int* cti = ti[cur];
+    float* xtd = td[cur ^ 1];
+    int* xti = ti[cur ^ 1];
+    {
+      const float bd = nd[tid];
+      const int bi = ni[tid];
+      // old entries precede equal batch entries
+      int lo = 0, hi = k;
+      while (lo < hi) {
+        const int mid = (lo + hi) >> 1;
+        if (!lt_pair(bd, bi, ctd[mid], cti[mid])) lo = mid + 1; else hi = mid;
+      }
+      const int pos = tid + lo;
+      bool fresh = false;
+      if (pos < k) {
+        xtd[pos] = bd;
+        xti[pos] = bi;
+        if (bi != kPadId) {
+          fresh = true;
+          for (int j = 0; j < k; ++j)
+            if (cti[j] == bi) { fresh = false; break; }
+        }
+      }
+      const uint64_t bm = __ballot(fresh);
+      if (lane == 0 && bm) atomicAdd(&s_chg, (int)__popcll(bm));
+    }
+    for (int j = tid; j < k; j += kRT) {
+      const float od = ctd[j];
+      const int oi = cti[j];
+      int lo = 0, hi = kRT;
+      while (lo < hi) {
+        const int mid = (lo + hi) >> 1;
+        if (lt_pair(nd[mid], ni[mid], od, oi)) lo = mid + 1; else hi = mid;
+      }
+      const int pos = j + lo;
+      if (pos < k) {
+        xtd[pos] = od;
+        xti[pos] = oi;
+      }
+    }
+    __syncthreads();
+    if (tid == 0) {
+      const int st = ((float)s_chg / (float)k <= a.eps) ? s_stable + 1 : 0;
+      s_stable = st;
+      s_fin = st >= a.beta;
+    }
+    cur ^= 1;
+    __syncthreads();
+    if (s_fin) break;
+  }
+  for (int j = tid; j < k; j += kRT) {
+    const bool pad = ti[cur][j] == kPadId;
+    a.out_ids[(size_t)q * k + j] = pad ? -1 : ti[cur][j];
+    a.out_d[(size_t)q * k + j] = pad ? FLT_MAX : td[cur][j];
+  }
+  if (a.visited && tid == 0) a.visited[q] = seen;
+}
+
+template <int D>
+fgpu_status launch_rr(const RerankArgs& a, hipStream_t s) {
+  hipLaunchKernelGGL((rerank_kernel<D>), dim3((unsigned)a.nq), dim3(kRT), 0, s, a);
+  FGPU_HIP(hipGetLastError());
+  return FGPU_OK;
+}
+
+}  // namespace
+
+int two_phase_pool_cap(int p1, int limit_k, int rerank_m) {
+  const int extra = p1 * limit_k > 2048 ? p1 * limit_k : 2048;
+  return (rerank_m + extra + 63) / 64 * 64;
+}
+
+fgpu_status launch_two_phase(int dim, int m, const TwoPhaseArgs& a, hipStream_t s) {
+  FGPU_CHECK(a.limit_k >= 1 && a.limit_k <= 64, FGPU_ERR_UNSUPPORTED, "two_phase: limit_k must be in [1, 64]");
+  FGPU_CHECK(a.rerank_m >= 1 && a.rerank_m <= kSortMax, FGPU_ERR_UNSUPPORTED, "two_phase: rerank_m must be in [1, 4096]");
+  FGPU_CHECK(a.nprobe >= 1 && a.nprobe <= 64 && a.p1 >= 0 && a.p1 <= a.nprobe, FGPU_ERR_ARG,
+             "two_phase: need 1 <= nprobe <= 64 and 0 <= p1 <= nprobe");
+  FGPU_CHECK(a.pool_cap >= two_phase_pool_cap(a.p1, a.limit_k, a.rerank_m), FGPU_ERR_ARG, "two_phase: pool too small");
+  if (a.nq <= 0) return FGPU_OK;
+  const int nq = a.nq;
+  if (dim == 128 && m == 32) return launch_tp<128, 32>(a, nq, s);
+  if (dim == 128 && m == 16) return launch_tp<128, 16>(a, nq, s);
+  if (dim == 128 && m == 64) return launch_tp<128, 64>(a, nq, s);
+  if (dim == 96 && m == 48) return launch_tp<96, 48>(a, nq, s);
+  if (dim == 96 && m == 32) return launch_tp<96, 32>(a, nq, s);
+  if (dim == 96 && m == 16) return launch_tp<96, 16>(a, nq, s);
+  return set_error(FGPU_ERR_UNSUPPORTED, "two_phase: unsupported (dim, pq_m)");
+}
+
+fgpu_status launch_rerank(int dim, const RerankArgs& a, hipStream_t s) {
+  FGPU_CHECK(a.k >= 1 && a.k <= 256, FGPU_ERR_UNSUPPORTED, "rerank: k must be in [1, 256]");
+  FGPU_CHECK(a.mb >= 1 && a.mb <= kRT, FGPU_ERR_UNSUPPORTED, "rerank: mini_batch must be in [1, 128]");
+  if (a.nq <= 0) return FGPU_OK;
+  if (dim == 128) return launch_rr<128>(a, s);
+  if (dim == 96) return launch_rr<96>(a, s);
+  return set_error(FGPU_ERR_UNSUPPORTED, "rerank: dim must be 96 or 128");
+}
+
+}  // namespace fgpu

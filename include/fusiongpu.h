@@ -106,6 +106,60 @@ fgpu_status fgpu_search(const fgpu_index* idx, const float* d_queries, int nq, i
                         float prune_ratio, int32_t* d_out_ids, float* d_out_dists,
                         void* d_workspace, size_t workspace_bytes, void* stream);
 
+/* ---- search: two-phase pruned scan + top-rerank_m (A6-A10) ------------- */
+
+/* The general form of run_gpu_batch_logic (gpu_global.cu:679-874) after the
+ * coarse step.  Phase 1 (ivf_scan_phase1_kernel, :321-390): for the first
+ * p1 = min(nprobe, p1_lists) probes, the w = min(n_l, limit_k) best vectors of
+ * each list are candidates and the w-th distance is the list's cutoff (0 for a
+ * pruned or empty probe).  Threshold (compute_threshold_kernel, :394-426):
+ * thr = threshold_coeff * min(cutoff > 0), FLT_MAX if none.  Phase 2
+ * (ivf_scan_phase2_kernel, :428-527): every vector of the other probed lists
+ * with distance <= thr is a candidate.  Outputs (compaction + sort + gather,
+ * :533-576, 798-867): the rerank_m best candidates ascending by (distance, id)
+ * in d_top_ids/d_top_dists [nq][rerank_m] (pad -1 / FLT_MAX) and
+ * d_top_counts[nq] = min(#candidates, rerank_m).  d_list_cutoffs [nq][p1] and
+ * d_thresholds [nq] are optional (NULL).  Whole lists are scanned (the
+ * reference stops at 1024 items), every passing vector is emitted once and
+ * all rerank_m entries are gathered.  No host synchronisation and no pool
+ * reallocation: the candidate pool is a bounded workspace, kept exact by
+ * selecting the rerank_m best whenever it would overflow.  limit_k <= 64,
+ * rerank_m <= 4096, nprobe <= 64.  A workspace smaller than the returned size
+ * is used in query chunks (it must hold at least one query's pool). */
+size_t fgpu_two_phase_workspace_bytes(int nq, int nprobe, int p1_lists, int limit_k, int rerank_m);
+fgpu_status fgpu_two_phase_search(const fgpu_index* idx, const float* d_queries, int nq,
+                                  const uint32_t* d_probe_ids, int nprobe, int p1_lists, int limit_k,
+                                  float threshold_coeff, int rerank_m, int32_t* d_top_ids,
+                                  float* d_top_dists, int32_t* d_top_counts, float* d_list_cutoffs,
+                                  float* d_thresholds, void* d_workspace, size_t workspace_bytes,
+                                  void* stream);
+
+/* ---- search: exact rerank (A11) ---------------------------------------- */
+
+/* run_gpu_rerank (gpu_global.cu:603-673): per query, walk the first
+ * d_top_counts[q] ids of d_top_ids [nq][rerank_m] in mini-batches of
+ * mini_batch; exact squared L2 against d_base [n][dim] (sequential fused
+ * chain, gpu_global.cu:636); merge into the running top-k ascending by
+ * (distance, id); chg = ids new to the top-k; stable += 1 if chg/k <= eps else
+ * 0; stop after beta stable batches or when candidates run out.  Ids outside
+ * [0, n) are skipped.  All k + mini_batch entries are sorted (the reference
+ * sorts only 128 of them).  d_visited [nq] (optional) = candidates evaluated.
+ * dim 96 or 128, d_base 16-byte aligned, k <= 256, mini_batch <= 128. */
+fgpu_status fgpu_rerank(const float* d_queries, int nq, int dim, const float* d_base, int64_t n,
+                        const int32_t* d_top_ids, const int32_t* d_top_counts, int rerank_m, int k,
+                        int mini_batch, float eps, int beta, int32_t* d_final_ids, float* d_final_dists,
+                        int32_t* d_visited, void* stream);
+
+/* coarse + two-phase + rerank in one call: the SearchPipeline per-batch path
+ * (search_pipeline.cu:341-361) with final_k = k. */
+size_t fgpu_search_rerank_workspace_bytes(int nq, int nlist, int nprobe, int p1_lists, int limit_k,
+                                          int rerank_m);
+fgpu_status fgpu_search_rerank(const fgpu_index* idx, const float* d_queries, int nq, int nprobe,
+                               float prune_ratio, int p1_lists, int limit_k, float threshold_coeff,
+                               int rerank_m, const float* d_base, int64_t n, int k, int mini_batch,
+                               float eps, int beta, int32_t* d_out_ids, float* d_out_dists,
+                               void* d_workspace, size_t workspace_bytes, void* stream);
+
 /* ---- exact nearest centroids (A13 / A2 core) -------------------------- */
 
 /* For each row x of d_x [n][dim]: the p nearest rows of d_c [nc][dim] by

@@ -1,0 +1,159 @@
+"""GPU parity for the two-phase pruned scan (A6-A10) and the exact rerank
+(A11): the HIP path through the C ABI against the CPU oracle on the same
+seeded inputs.  Bar: bit-exact ids, counts, cutoffs, thresholds, visit counts
+and fp32 distances.
+"""
+import sys
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+if not torch.cuda.is_available():
+    pytest.skip("no HIP device", allow_module_level=True)
+
+import fusiongpu_amd as fg  # noqa: E402
+import oracle  # noqa: E402
+
+
+def _say(msg):
+    print(f"[gpu-case] {msg}", flush=True)
+    sys.stdout.flush()
+
+
+def _bits(a):
+    return np.asarray(a, np.float32).view(np.uint32)
+
+
+def _host(t):
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def _index(rng, n, dim, m, nlist, empty=(), big=None):
+    p = rng.random(nlist) + 0.05
+    for e in empty:
+        p[e] = 0.0
+    if big is not None:
+        p[big] *= 40.0
+    assign = rng.choice(nlist, size=n, p=p / p.sum()).astype(np.int32)
+    codes = rng.integers(0, 256, (n, m)).astype(np.uint8)
+    codes[100] = codes[101]
+    assign[101] = assign[100]
+    offs, ids, lc = oracle.build_lists(assign, nlist, codes)
+    cent = rng.standard_normal((nlist, dim)).astype(np.float32) * 0.7
+    cb = (rng.standard_normal((m, 256, dim // m)) * 0.4).astype(np.float32)
+    return offs, ids, lc, cent, cb
+
+
+# (dim, m, p1_lists, limit_k, coeff, rerank_m)
+CASES = [
+    (128, 32, 3, 5, 1.0, 60),      # reference-shaped, small
+    (96, 48, 12, 50, 1.0, 1000),   # config-3 shape
+    (128, 16, 0, 10, 1.0, 50),     # no phase 1: thr = FLT_MAX, every vector passes, pool selects repeatedly
+    (96, 32, 16, 64, 1.5, 300),    # every probe in phase 1
+    (128, 64, 4, 1, 0.0, 17),      # threshold 0: phase 2 adds nothing
+    (96, 16, 2, 7, 3.0, 4096),     # the largest rerank_m, loose threshold
+]
+
+
+@pytest.mark.parametrize("dim,m,p1,limit_k,coeff,rerank_m", CASES)
+def test_two_phase_bit_exact(dim, m, p1, limit_k, coeff, rerank_m):
+    _say(f"two_phase dim={dim} m={m} p1={p1} limit_k={limit_k} coeff={coeff} rerank_m={rerank_m}")
+    rng = np.random.default_rng(dim + m + p1 + limit_k + rerank_m)
+    nlist = 40
+    offs, ids, lc, cent, cb = _index(rng, 30000, dim, m, nlist, empty=(3, 17), big=8)
+    q = (rng.standard_normal((120, dim)) * 0.7).astype(np.float32)
+    probes, _ = oracle.coarse(q, cent, 16)
+    probes[5, 1] = 0xFFFFFFFF            # pruned probe (phase 1 when p1 > 1)
+    probes[6, :] = 0xFFFFFFFF            # nothing probed: zero candidates
+    probes[7, 0] = 3                     # an empty list first
+    probes[8, 9] = 999                   # out-of-range id counts as pruned
+    probes[9, 0] = 8                     # the long list (> 1024 vectors) in phase 1 ...
+    probes[9, 12] = 8                    # ... and again in phase 2
+    idx = fg.Index.from_arrays(dim, m, offs, ids, lc, cent, cb)
+    assert idx.max_list_len > 1024
+    gid, gd, gcnt, gcut, gthr = idx.two_phase_search(torch.from_numpy(q).cuda(),
+                                                     torch.from_numpy(probes.view(np.int32)).cuda(), p1, limit_k,
+                                                     coeff, rerank_m, want_cutoffs=True)
+    gid, gd, gcnt, gthr = _host(gid), _host(gd), _host(gcnt), _host(gthr)
+    oid, od, ocnt, ocut, othr = oracle.search_two_phase(q, cent, cb, offs, ids, lc, probes, p1, limit_k, coeff,
+                                                        rerank_m)
+    assert np.array_equal(gcnt, ocnt), np.nonzero(gcnt != ocnt)[0][:5]
+    bad = np.nonzero(~np.all(gid == oid, axis=1))[0]
+    assert bad.size == 0, f"first mismatching queries {bad[:5]}"
+    assert np.array_equal(_bits(gd), _bits(od))
+    assert np.array_equal(_bits(gthr), _bits(othr))
+    if p1 > 0:
+        assert np.array_equal(_bits(_host(gcut)), _bits(ocut))
+    assert gcnt[6] == 0 and np.all(gid[6] == -1)
+    idx.close()
+
+
+def test_two_phase_workspace_chunks_equal_one_launch():
+    _say("two_phase chunked workspace")
+    rng = np.random.default_rng(77)
+    offs, ids, lc, cent, cb = _index(rng, 20000, 128, 32, 30)
+    q = torch.from_numpy((rng.standard_normal((300, 128)) * 0.7).astype(np.float32)).cuda()
+    idx = fg.Index.from_arrays(128, 32, offs, ids, lc, cent, cb)
+    probes, _ = idx.coarse_search(q, 12)
+    full = idx.two_phase_search(q, probes, 4, 20, 1.0, 200)
+    one = fg.lib.fgpu_two_phase_workspace_bytes(1, 12, 4, 20, 200)
+    small = torch.empty(one * 7 + 100, dtype=torch.uint8, device="cuda")   # 7 queries per launch
+    part = idx.two_phase_search(q, probes, 4, 20, 1.0, 200, workspace=small)
+    for a, b in zip(full[:3], part[:3]):
+        assert torch.equal(a, b)
+    idx.close()
+
+
+# (dim, k, mb, eps, beta)
+RERANK = [(96, 100, 128, 0.1, 2), (128, 10, 128, 0.1, 2), (96, 256, 32, -1.0, 2), (128, 20, 7, 0.5, 3),
+          (128, 5, 16, 1.0, 1)]
+
+
+@pytest.mark.parametrize("dim,k,mb,eps,beta", RERANK)
+def test_rerank_bit_exact(dim, k, mb, eps, beta):
+    _say(f"rerank dim={dim} k={k} mb={mb} eps={eps} beta={beta}")
+    rng = np.random.default_rng(dim + k + mb)
+    n, nq, rm = 20000, 200, 600
+    base = rng.standard_normal((n, dim)).astype(np.float32)
+    q = rng.standard_normal((nq, dim)).astype(np.float32)
+    # candidates in a noisy "ADC" order: the exact ranking perturbed
+    cand = np.empty((nq, rm), np.int32)
+    for i in range(nq):
+        pool = rng.choice(n, 3 * rm, replace=False)
+        d = ((base[pool] - q[i]) ** 2).sum(1) * rng.uniform(0.7, 1.3, pool.size)
+        cand[i] = pool[np.argsort(d)[:rm]]
+    cand[3, 10] = -1                     # invalid ids are skipped
+    cand[3, 11] = n + 5
+    cand[4, 20] = cand[4, 2]             # a duplicate candidate
+    counts = rng.integers(0, rm + 1, nq).astype(np.int32)
+    counts[:6] = [rm, rm, 0, rm, rm, 1]
+    gid, gd, gvis = fg.rerank(torch.from_numpy(q).cuda(), torch.from_numpy(base).cuda(), torch.from_numpy(cand).cuda(),
+                              torch.from_numpy(counts).cuda(), k, mb, eps, beta)
+    oid, od, ovis = oracle.rerank(q, base, cand, counts, k, mb, eps, beta)
+    gid, gd, gvis = _host(gid), _host(gd), _host(gvis)
+    assert np.array_equal(gvis, ovis), np.nonzero(gvis != ovis)[0][:5]
+    bad = np.nonzero(~np.all(gid == oid, axis=1))[0]
+    assert bad.size == 0, f"first mismatching queries {bad[:5]}"
+    assert np.array_equal(_bits(gd), _bits(od))
+    assert np.all(gid[2] == -1)
+
+
+def test_search_rerank_end_to_end():
+    _say("search_rerank end to end")
+    x = oracle.gen_gmm(30000, 96, 48, seed=11, sig_lo=0.05, sig_hi=0.15)
+    q = oracle.gen_gmm(300, 96, 48, seed=11, set=1, sig_lo=0.05, sig_hi=0.15)
+    offs, ids, codes, cent, cb = fg.build_ivfpq(torch.from_numpy(x).cuda(), 64, 48, kmeans_iters=4, init_mode=1,
+                                                seed=3, pq_iters=3, sample_size=5000)
+    idx = fg.Index.from_arrays(96, 48, offs, ids, codes, cent, cb)
+    dq, dx = torch.from_numpy(q).cuda(), torch.from_numpy(x).cuda()
+    gid, gd = idx.search_rerank(dq, dx, 16, 20, p1_lists=4, limit_k=30, threshold_coeff=1.0, rerank_m=200)
+    probes, _ = oracle.coarse(q, cent, 16)
+    tid, td, tc, _, _ = oracle.search_two_phase(q, cent, cb, offs, ids, codes, probes, 4, 30, 1.0, 200)
+    oid, od, _ = oracle.rerank(q, x, tid, tc, 20, 128, 0.1, 2)
+    assert np.array_equal(_host(gid), oid)
+    assert np.array_equal(_bits(_host(gd)), _bits(od))
+    idx.close()
