@@ -69,6 +69,8 @@ _SIGS = {
     "fgpu_pq_encode": (_i32, [_vp, _i64, _i32, _i32, _vp, _vp, _vp, _vp, _vp]),
     "fgpu_build_ivfpq": (_i32, [_vp, _i64, _i32, _i32, _i32, _i32, _i32, _u64, _i32, _i32,
                                 _vp, _vp, _vp, _vp, _vp, _vp]),
+    "fgpu_build_ivfpq_sampled": (_i32, [_vp, _i64, _i32, _i32, _i32, _i64, _i32, _i32, _u64, _i32, _i32,
+                                        _vp, _vp, _vp, _vp, _vp, _vp]),
     "fgpu_write_ivf_data": (_i32, [_c.c_char_p, _i64, _i32, _i32, _i32, _vp, _vp, _vp, _vp]),
     "fgpu_read_ivf_header": (_i32, [_c.c_char_p, _c.POINTER(_i64), _c.POINTER(_i32)]),
     "fgpu_read_ivf_data": (_i32, [_c.c_char_p, _i32, _i32, _vp, _vp, _vp, _vp]),
@@ -440,8 +442,9 @@ def pq_encode(x, assign, centroids, codebook, stream=None):
 
 
 def build_ivfpq(x, nlist: int, pq_m: int, kmeans_iters: int = 20, init_mode: int = 0, seed: int = 42,
-                pq_iters: int = 8, sample_size: int = 50000, stream=None):
-    """build_global without rebalancing: host arrays (offsets, ids, codes, centroids, codebook)."""
+                pq_iters: int = 8, sample_size: int = 50000, train_rows: int = 0, stream=None):
+    """build_global without rebalancing: host arrays (offsets, ids, codes, centroids, codebook).
+    train_rows > 0 trains the k-means on the systematic sample of that many rows."""
     x = _to_dev(x)
     n, dim = x.shape
     offs = np.empty(nlist + 1, np.int32)
@@ -449,7 +452,7 @@ def build_ivfpq(x, nlist: int, pq_m: int, kmeans_iters: int = 20, init_mode: int
     codes = np.empty((n, pq_m), np.uint8)
     cent = np.empty((nlist, dim), np.float32)
     cb = np.empty((pq_m, 256, dim // pq_m), np.float32)
-    _check(lib.fgpu_build_ivfpq(_dev_ptr(x), n, dim, nlist, pq_m, kmeans_iters, init_mode, seed, pq_iters,
-                                sample_size, _np_ptr(offs), _np_ptr(ids), _np_ptr(codes), _np_ptr(cent), _np_ptr(cb),
-                                _stream(stream)))
+    _check(lib.fgpu_build_ivfpq_sampled(_dev_ptr(x), n, dim, nlist, pq_m, train_rows, kmeans_iters, init_mode, seed,
+                                        pq_iters, sample_size, _np_ptr(offs), _np_ptr(ids), _np_ptr(codes),
+                                        _np_ptr(cent), _np_ptr(cb), _stream(stream)))
     return offs, ids, codes, cent, cb

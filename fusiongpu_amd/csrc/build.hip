@@ -274,6 +274,77 @@ __global__ __launch_bounds__(kPPBlock) void pp_update_kernel(const float* __rest
   }
 }
 
+// The same update for a compile-time dim: each lane still owns one row and
+// keeps the sequential fused chain, but the row arrives as D/4 16-byte loads
+// that are all issued before the chain starts, instead of D dependent scalar
+// loads.
+template <int D>
+__global__ __launch_bounds__(kPPBlock) void pp_update_vec_kernel(const float* __restrict__ x, int64_t n,
+                                                                 const float* __restrict__ c, int init,
+                                                                 float* __restrict__ d2, const int* __restrict__ shift,
+                                                                 uint64_t* __restrict__ w, uint64_t* __restrict__ part) {
+  static_assert(D % 4 == 0, "16-byte row loads");
+  __shared__ float cs[D];
+  for (int d = threadIdx.x; d < D; d += kPPBlock) cs[d] = c[d];
+  __syncthreads();
+  const int64_t i = (int64_t)blockIdx.x * kPPBlock + threadIdx.x;
+  uint64_t wi = 0;
+  if (i < n) {
+    const float4* xi = reinterpret_cast<const float4*>(x + i * D);
+    float4 v[D / 4];
+#pragma unroll
+    for (int j = 0; j < D / 4; ++j) v[j] = xi[j];
+    float acc = 0.0f;
+#pragma unroll
+    for (int j = 0; j < D / 4; ++j) {
+      float df = v[j].x - cs[4 * j];
+      acc = __builtin_fmaf(df, df, acc);
+      df = v[j].y - cs[4 * j + 1];
+      acc = __builtin_fmaf(df, df, acc);
+      df = v[j].z - cs[4 * j + 2];
+      acc = __builtin_fmaf(df, df, acc);
+      df = v[j].w - cs[4 * j + 3];
+      acc = __builtin_fmaf(df, df, acc);
+    }
+    const float v2 = (init || acc < d2[i]) ? acc : d2[i];
+    d2[i] = v2;
+    if (shift) {
+      wi = (uint64_t)__double2ll_rn(ldexp((double)v2, *shift));
+      w[i] = wi;
+    }
+  }
+  if (shift) {
+    __shared__ uint64_t s[kPPBlock / kWave];
+    uint64_t t = wi;
+#pragma unroll
+    for (int m = 32; m > 0; m >>= 1) t += __shfl_xor(t, m, kWave);
+    if ((threadIdx.x & 63) == 0) s[threadIdx.x >> 6] = t;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      uint64_t tot = 0;
+      for (int j = 0; j < kPPBlock / kWave; ++j) tot += s[j];
+      part[blockIdx.x] = tot;
+    }
+  }
+}
+
+// One pass of the d2 update: the vectorised kernel for the common dims (rows
+// 16-byte aligned), the generic one otherwise.
+fgpu_status pp_update(const float* x, int64_t n, int dim, const float* c, int init, float* d2, const int* shift,
+                      uint64_t* w, uint64_t* part, int nb, hipStream_t s) {
+  const bool vec = ((uintptr_t)x & 15) == 0;
+  if (vec && dim == 128)
+    hipLaunchKernelGGL(pp_update_vec_kernel<128>, dim3(nb), dim3(kPPBlock), 0, s, x, n, c, init, d2, shift, w, part);
+  else if (vec && dim == 96)
+    hipLaunchKernelGGL(pp_update_vec_kernel<96>, dim3(nb), dim3(kPPBlock), 0, s, x, n, c, init, d2, shift, w, part);
+  else if (vec && dim == 64)
+    hipLaunchKernelGGL(pp_update_vec_kernel<64>, dim3(nb), dim3(kPPBlock), 0, s, x, n, c, init, d2, shift, w, part);
+  else
+    hipLaunchKernelGGL(pp_update_kernel, dim3(nb), dim3(kPPBlock), 0, s, x, n, dim, c, init, d2, shift, w, part);
+  FGPU_HIP(hipGetLastError());
+  return FGPU_OK;
+}
+
 // shift from the first round's max d2 (so n * max w < 2^62).
 __global__ __launch_bounds__(1024) void pp_shift_kernel(const float* __restrict__ d2, int64_t n, int* __restrict__ shift) {
   __shared__ float part[16];
@@ -546,19 +617,15 @@ fgpu_status launch_kmeans_pp(const float* x, int64_t n, int dim, int k, uint64_t
   FGPU_HIP(hipMemsetAsync(chosen, 0, n, s));
   hipLaunchKernelGGL(pp_first_kernel, dim3(1), dim3(1), 0, s, n, seed, rows, chosen);
   hipLaunchKernelGGL(pp_take_kernel, dim3(1), dim3(256), 0, s, x, dim, rows, 0, cent, chosen);
-  hipLaunchKernelGGL(pp_update_kernel, dim3(nb), dim3(kPPBlock), 0, s, x, n, dim, cent, 1, d2, (const int*)nullptr,
-                     w, part);
+  FGPU_TRY(pp_update(x, n, dim, cent, 1, d2, nullptr, w, part, nb, s));
   hipLaunchKernelGGL(pp_shift_kernel, dim3(1), dim3(1024), 0, s, d2, n, shift);
   FGPU_HIP(hipGetLastError());
   // weights for round 1 from the initial d2
-  hipLaunchKernelGGL(pp_update_kernel, dim3(nb), dim3(kPPBlock), 0, s, x, n, dim, cent, 0, d2, (const int*)shift,
-                     w, part);
+  FGPU_TRY(pp_update(x, n, dim, cent, 0, d2, shift, w, part, nb, s));
   for (int j = 1; j < k; ++j) {
     hipLaunchKernelGGL(pp_pick_kernel, dim3(1), dim3(kPPBlock), 0, s, w, part, nb, n, seed, j, chosen, rows);
     hipLaunchKernelGGL(pp_take_kernel, dim3(1), dim3(256), 0, s, x, dim, rows, j, cent, chosen);
-    if (j + 1 < k)
-      hipLaunchKernelGGL(pp_update_kernel, dim3(nb), dim3(kPPBlock), 0, s, x, n, dim, cent + (size_t)j * dim, 0, d2,
-                         (const int*)shift, w, part);
+    if (j + 1 < k) FGPU_TRY(pp_update(x, n, dim, cent + (size_t)j * dim, 0, d2, shift, w, part, nb, s));
   }
   FGPU_HIP(hipGetLastError());
   return FGPU_OK;

@@ -486,6 +486,14 @@ fgpu_status fgpu_pq_encode(const float* dx, int64_t n, int dim, int pq_m, const 
 fgpu_status fgpu_build_ivfpq(const float* dx, int64_t n, int dim, int nlist, int pq_m, int kmeans_iters, int init_mode,
                              uint64_t seed, int pq_iters, int sample_size, int32_t* h_offsets, int32_t* h_ids,
                              uint8_t* h_codes, float* h_centroids, float* h_codebook, void* stream) {
+  return fgpu_build_ivfpq_sampled(dx, n, dim, nlist, pq_m, 0, kmeans_iters, init_mode, seed, pq_iters, sample_size,
+                                  h_offsets, h_ids, h_codes, h_centroids, h_codebook, stream);
+}
+
+fgpu_status fgpu_build_ivfpq_sampled(const float* dx, int64_t n, int dim, int nlist, int pq_m, int64_t train_rows,
+                                     int kmeans_iters, int init_mode, uint64_t seed, int pq_iters, int sample_size,
+                                     int32_t* h_offsets, int32_t* h_ids, uint8_t* h_codes, float* h_centroids,
+                                     float* h_codebook, void* stream) {
   FGPU_CHECK(dx && h_offsets && h_ids && h_codes && h_centroids && h_codebook, FGPU_ERR_ARG, "build: null argument");
   FGPU_CHECK(n < INT32_MAX, FGPU_ERR_ARG, "build: more than 2^31-1 vectors");
   hipStream_t s = as_stream(stream);
@@ -496,7 +504,26 @@ fgpu_status fgpu_build_ivfpq(const float* dx, int64_t n, int dim, int nlist, int
   FGPU_TRY(cb.alloc((size_t)pq_m * kPQK * (dim / pq_m)));
   FGPU_TRY(assign.alloc(n));
   FGPU_TRY(codes.alloc((size_t)n * pq_m));
-  FGPU_TRY(fgpu_kmeans_fit(dx, n, dim, nlist, kmeans_iters, init_mode, seed, cent.p, assign.p, stream));
+  if (train_rows <= 0 || train_rows >= n) {
+    FGPU_TRY(fgpu_kmeans_fit(dx, n, dim, nlist, kmeans_iters, init_mode, seed, cent.p, assign.p, stream));
+  } else {
+    FGPU_CHECK(train_rows >= nlist, FGPU_ERR_ARG, "build: train_rows must be >= nlist");
+    std::vector<int32_t> rows(train_rows);
+    for (int64_t j = 0; j < train_rows; ++j) rows[j] = (int32_t)(j * n / train_rows);
+    DevBuf<int32_t> drows;
+    DevBuf<float> train, dist;
+    DevBuf<char> tws;
+    FGPU_TRY(drows.alloc(train_rows));
+    FGPU_TRY(train.alloc((size_t)train_rows * dim));
+    FGPU_HIP(hipMemcpyAsync(drows.p, rows.data(), sizeof(int32_t) * train_rows, hipMemcpyHostToDevice, s));
+    FGPU_TRY(launch_gather_rows(dx, dim, drows.p, (int)train_rows, train.p, s));
+    FGPU_TRY(fgpu_kmeans_fit(train.p, train_rows, dim, nlist, kmeans_iters, init_mode, seed, cent.p, nullptr, stream));
+    const size_t tb = fgpu_l2_topk_workspace_bytes(n, nlist);
+    FGPU_TRY(dist.alloc(n));
+    FGPU_TRY(tws.alloc(tb));
+    FGPU_TRY(fgpu_l2_topk(dx, n, cent.p, nlist, dim, 1, assign.p, dist.p, tws.p, tb, stream));
+    FGPU_HIP(hipStreamSynchronize(s));
+  }
   FGPU_TRY(fgpu_pq_train(dx, n, dim, pq_m, assign.p, cent.p, sample_size, pq_iters, cb.p, stream));
   FGPU_TRY(fgpu_pq_encode(dx, n, dim, pq_m, assign.p, cent.p, cb.p, codes.p, stream));
   std::vector<int32_t> ha(n);

@@ -211,6 +211,17 @@ fgpu_status fgpu_build_ivfpq(const float* d_x, int64_t n, int dim, int nlist, in
                              int sample_size, int32_t* h_offsets, int32_t* h_ids, uint8_t* h_codes,
                              float* h_centroids, float* h_codebook, void* stream);
 
+/* fgpu_build_ivfpq with the k-means trained on a sample: rows
+ * floor(j * n / train_rows), j < train_rows (a systematic sample; BASELINE
+ * config 4 trains on 1M of 10M rows), then every row is assigned to its
+ * nearest centroid and the PQ training, encoding and lists follow as in
+ * fgpu_build_ivfpq.  train_rows <= 0 or >= n trains on every row, as
+ * build_global does (build_global.cu:41). */
+fgpu_status fgpu_build_ivfpq_sampled(const float* d_x, int64_t n, int dim, int nlist, int pq_m,
+                                     int64_t train_rows, int kmeans_iters, int init_mode, uint64_t seed,
+                                     int pq_iters, int sample_size, int32_t* h_offsets, int32_t* h_ids,
+                                     uint8_t* h_codes, float* h_centroids, float* h_codebook, void* stream);
+
 /* ---- files (utils.h, build_global.cu:242-252) -------------------------- */
 
 fgpu_status fgpu_write_ivf_data(const char* path, int64_t total, int nlist, int pq_m, int dim,

@@ -264,9 +264,17 @@ def build_lists(assign, nlist, codes):
     return offs, ids, lc
 
 
-def build_ivfpq(x, nlist, pq_m, kmeans_iters=20, init_mode=0, seed=42, pq_iters=8, sample_size=50000, nthreads=0):
-    """build_global restated without rebalancing (build_global.cu:21-258)."""
-    cent, assign = kmeans_fit(x, nlist, kmeans_iters, init_mode, seed, nthreads)
+def build_ivfpq(x, nlist, pq_m, kmeans_iters=20, init_mode=0, seed=42, pq_iters=8, sample_size=50000, nthreads=0,
+                train_rows=0):
+    """build_global restated without rebalancing (build_global.cu:21-258).  train_rows > 0: k-means on the
+    systematic sample rows floor(j*n/train_rows), then every row assigned to its nearest centroid."""
+    n = x.shape[0]
+    if 0 < train_rows < n:
+        rows = (np.arange(train_rows, dtype=np.int64) * n) // train_rows
+        cent, _ = kmeans_fit(np.ascontiguousarray(x[rows]), nlist, kmeans_iters, init_mode, seed, nthreads)
+        assign = kmeans_assign(x, cent, nthreads)
+    else:
+        cent, assign = kmeans_fit(x, nlist, kmeans_iters, init_mode, seed, nthreads)
     cb = pq_train(x, assign, cent, pq_m, sample_size, pq_iters, nthreads)
     codes = pq_encode(x, assign, cent, cb, 1, nthreads)
     offs, ids, lc = build_lists(assign, nlist, codes)

@@ -157,3 +157,14 @@ def test_search_rerank_end_to_end():
     assert np.array_equal(_host(gid), oid)
     assert np.array_equal(_bits(_host(gd)), _bits(od))
     idx.close()
+
+
+def test_build_ivfpq_sampled_bit_exact():
+    _say("build_ivfpq sampled k-means training")
+    x = oracle.gen_gmm(9000, 96, 16, seed=4, sig_lo=0.05, sig_hi=0.15)
+    got = fg.build_ivfpq(torch.from_numpy(x).cuda(), 24, 48, kmeans_iters=3, init_mode=1, seed=5, pq_iters=2,
+                         sample_size=2000, train_rows=2500)
+    want = oracle.build_ivfpq(x, 24, 48, kmeans_iters=3, init_mode=1, seed=5, pq_iters=2, sample_size=2000,
+                              train_rows=2500)
+    for g, w, name in zip(got, want, ["offsets", "ids", "codes", "centroids", "codebook"]):
+        assert np.array_equal(np.asarray(g).view(np.uint8), np.asarray(w).view(np.uint8)), name
