@@ -251,6 +251,10 @@ def run_c3(args, torch, fg, dev):
     tp_ws = torch.empty(fg.lib.fgpu_two_phase_workspace_bytes(nq, nprobe, p1, limit_k, rerank_m), dtype=torch.uint8,
                         device=dev)
     tid, td, tc, _, _ = idx.two_phase_search(dq, probes, p1, limit_k, coeff, rerank_m, workspace=tp_ws)
+    sid, sd, sc, tstats = idx.two_phase_stats(dq, probes, p1, limit_k, coeff, rerank_m, workspace=tp_ws)
+    assert torch.equal(sid, tid) and torch.equal(sd, td) and torch.equal(sc, tc), "instrumented scan differs"
+    loaded_bytes = tstats["vectors_loaded"] * (m + 4)
+    log(f"two-phase counters: {tstats}; loads {loaded_bytes / 1e9:.2f} GB (codes + ids)")
     _, _, vis = fg.rerank(dq, dx, tid, tc, k, mb, eps, beta)
     visited = int(vis.to(torch.int64).sum().item())
     ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
@@ -311,7 +315,9 @@ def run_c3(args, torch, fg, dev):
                    "n": n, "dim": dim, "nlist": nlist, "pq_m": m, "nq": nq, "nprobe": nprobe, "k": k},
         "roofline": {"bound": "hbm", "kernel": "two_phase_kernel<96,48>", "achieved": round(adc_gbs, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(adc_gbs / HBM_PEAK_GBS, 4),
-                     "traffic": None, "algorithmic_bytes_per_launch": adc_bytes, "avg_launch_ms": round(tp_ms, 4)},
+                     "traffic": None, "algorithmic_bytes_per_launch": adc_bytes, "avg_launch_ms": round(tp_ms, 4),
+                     "loaded_bytes_per_launch": loaded_bytes,
+                     "achieved_loaded": round(loaded_bytes / (tp_ms * 1e-3) / 1e9, 1), **tstats},
         "stages_ms": {"coarse": round(coarse_ms, 4), "two_phase": round(tp_ms, 4), "rerank": round(rr_ms, 4),
                       "rerank_rows": visited, "rerank_gbs": round(rr_bytes / (rr_ms * 1e-3) / 1e9, 1),
                       "candidates_per_query": round(tc.float().mean().item(), 1)},

@@ -55,6 +55,8 @@ _SIGS = {
     "fgpu_two_phase_workspace_bytes": (_sz, [_i32, _i32, _i32, _i32, _i32]),
     "fgpu_two_phase_search": (_i32, [_vp, _vp, _i32, _vp, _i32, _i32, _i32, _f32, _i32, _vp, _vp, _vp, _vp, _vp,
                                      _vp, _sz, _vp]),
+    "fgpu_two_phase_search_stats": (_i32, [_vp, _vp, _i32, _vp, _i32, _i32, _i32, _f32, _i32, _vp, _vp, _vp, _vp,
+                                           _vp, _sz, _vp]),
     "fgpu_rerank": (_i32, [_vp, _i32, _i32, _vp, _i64, _vp, _vp, _i32, _i32, _i32, _f32, _i32, _vp, _vp, _vp, _vp]),
     "fgpu_search_rerank_workspace_bytes": (_sz, [_i32, _i32, _i32, _i32, _i32, _i32]),
     "fgpu_search_rerank": (_i32, [_vp, _vp, _i32, _i32, _f32, _i32, _i32, _f32, _i32, _vp, _i64, _i32, _i32, _f32,
@@ -314,6 +316,27 @@ class Index:
                                          _dev_ptr(thr) if want_cutoffs else None, _dev_ptr(ws), ws.numel(),
                                          _stream(stream)))
         return tid, td, tc, (cut[:, :p1] if want_cutoffs else None), thr
+
+    def two_phase_stats(self, queries, probe_ids, p1_lists: int, limit_k: int, threshold_coeff: float, rerank_m: int,
+                        workspace=None, stream=None):
+        """two_phase_search plus counters: (top_ids, top_dists, top_counts, {counter: value})."""
+        torch = _torch()
+        q = _to_dev(queries)
+        p = _to_dev(probe_ids)
+        nq, nprobe = p.shape
+        ws = workspace if workspace is not None else _workspace(
+            lib.fgpu_two_phase_workspace_bytes(nq, nprobe, p1_lists, limit_k, rerank_m))
+        tid = torch.empty((nq, rerank_m), dtype=torch.int32, device="cuda")
+        td = torch.empty((nq, rerank_m), dtype=torch.float32, device="cuda")
+        tc = torch.empty(nq, dtype=torch.int32, device="cuda")
+        st = torch.zeros(12, dtype=torch.int64, device="cuda")
+        _check(lib.fgpu_two_phase_search_stats(self._h, _dev_ptr(q), nq, _dev_ptr(p), nprobe, p1_lists, limit_k,
+                                               threshold_coeff, rerank_m, _dev_ptr(tid), _dev_ptr(td), _dev_ptr(tc),
+                                               _dev_ptr(st), _dev_ptr(ws), ws.numel(), _stream(stream)))
+        v = st.cpu().tolist()
+        return tid, td, tc, {"vectors_loaded": v[0], "luts_built": v[1], "lists_skipped": v[2],
+                             "phase2_appended": v[3], "clk_setup": v[4], "clk_phase1": v[5], "clk_phase2": v[6],
+                             "clk_final": v[7], "clk_p1_build": v[8], "clk_p1_scan": v[9], "clk_p1_merge": v[10]}
 
     def search_rerank_workspace_bytes(self, nq: int, nprobe: int, p1_lists: int, limit_k: int, rerank_m: int) -> int:
         return lib.fgpu_search_rerank_workspace_bytes(nq, self.nlist, nprobe, p1_lists, limit_k, rerank_m)

@@ -251,11 +251,13 @@ size_t fgpu_two_phase_workspace_bytes(int nq, int nprobe, int p1_lists, int limi
   return carve_bytes<uint64_t>((size_t)std::max(nq, 1) * two_phase_pool_cap(p1, limit_k, rerank_m));
 }
 
-fgpu_status fgpu_two_phase_search(const fgpu_index* ix, const float* dq, int nq, const uint32_t* d_probe_ids,
-                                  int nprobe, int p1_lists, int limit_k, float threshold_coeff, int rerank_m,
-                                  int32_t* d_top_ids, float* d_top_dists, int32_t* d_top_counts,
-                                  float* d_list_cutoffs, float* d_thresholds, void* ws, size_t ws_bytes,
-                                  void* stream) {
+}  // extern "C"
+
+namespace {
+fgpu_status two_phase(const fgpu_index* ix, const float* dq, int nq, const uint32_t* d_probe_ids, int nprobe,
+                      int p1_lists, int limit_k, float threshold_coeff, int rerank_m, int32_t* d_top_ids,
+                      float* d_top_dists, int32_t* d_top_counts, float* d_list_cutoffs, float* d_thresholds,
+                      unsigned long long* d_stats, void* ws, size_t ws_bytes, void* stream) {
   FGPU_CHECK(ix && dq && d_probe_ids && d_top_ids && d_top_dists && d_top_counts && ws, FGPU_ERR_ARG,
              "two_phase_search: null argument");
   FGPU_CHECK(nq >= 0 && nprobe >= 1 && nprobe <= 64, FGPU_ERR_ARG, "two_phase_search: need 1 <= nprobe <= 64");
@@ -272,10 +274,32 @@ fgpu_status fgpu_two_phase_search(const fgpu_index* ix, const float* dq, int nq,
                    d_probe_ids + q0 * nprobe, ix->d_rmax, nb, nprobe, ix->nlist, p1, limit_k, threshold_coeff,
                    rerank_m, reinterpret_cast<uint64_t*>(ws), cap, d_top_ids + q0 * rerank_m,
                    d_top_dists + q0 * rerank_m, d_top_counts + q0,
-                   d_list_cutoffs ? d_list_cutoffs + q0 * p1 : nullptr, d_thresholds ? d_thresholds + q0 : nullptr};
+                   d_list_cutoffs ? d_list_cutoffs + q0 * p1 : nullptr, d_thresholds ? d_thresholds + q0 : nullptr,
+                   d_stats};
     FGPU_TRY(launch_two_phase(ix->dim, ix->m, a, as_stream(stream)));
   }
   return FGPU_OK;
+}
+}  // namespace
+
+extern "C" {
+
+fgpu_status fgpu_two_phase_search(const fgpu_index* ix, const float* dq, int nq, const uint32_t* d_probe_ids,
+                                  int nprobe, int p1_lists, int limit_k, float threshold_coeff, int rerank_m,
+                                  int32_t* d_top_ids, float* d_top_dists, int32_t* d_top_counts,
+                                  float* d_list_cutoffs, float* d_thresholds, void* ws, size_t ws_bytes,
+                                  void* stream) {
+  return two_phase(ix, dq, nq, d_probe_ids, nprobe, p1_lists, limit_k, threshold_coeff, rerank_m, d_top_ids,
+                   d_top_dists, d_top_counts, d_list_cutoffs, d_thresholds, nullptr, ws, ws_bytes, stream);
+}
+
+fgpu_status fgpu_two_phase_search_stats(const fgpu_index* ix, const float* dq, int nq, const uint32_t* d_probe_ids,
+                                        int nprobe, int p1_lists, int limit_k, float threshold_coeff, int rerank_m,
+                                        int32_t* d_top_ids, float* d_top_dists, int32_t* d_top_counts,
+                                        unsigned long long* d_stats, void* ws, size_t ws_bytes, void* stream) {
+  FGPU_CHECK(d_stats, FGPU_ERR_ARG, "two_phase_search_stats: null stats");
+  return two_phase(ix, dq, nq, d_probe_ids, nprobe, p1_lists, limit_k, threshold_coeff, rerank_m, d_top_ids,
+                   d_top_dists, d_top_counts, nullptr, nullptr, d_stats, ws, ws_bytes, stream);
 }
 
 fgpu_status fgpu_rerank(const float* dq, int nq, int dim, const float* d_base, int64_t n, const int32_t* d_top_ids,

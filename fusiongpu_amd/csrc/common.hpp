@@ -82,43 +82,81 @@ __device__ __forceinline__ float key_float(uint32_t k) {
   return __uint_as_float(u);
 }
 
+// ---- cross-lane exchange on the VALU ----------------------------------------
+// x(lane ^ S) for one wave, without the LDS crossbar: DPP quad permutes for
+// S = 1, 2, row rotates for S = 4, 8 (rotating a 16-lane row by 8 is xor 8;
+// xor 4 picks the rotate by 4 or by 12 from bit 2 of the lane), and the gfx950
+// permlane16/32 swaps for S = 16, 32.  Every lane must be active.
+template <int C>
+__device__ __forceinline__ int dpp_mov(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, C, 0xF, 0xF, false);
+}
+template <int S>
+__device__ __forceinline__ int xchg(int v) {
+  if constexpr (S == 1) {
+    return dpp_mov<0xB1>(v);  // quad_perm [1,0,3,2]
+  } else if constexpr (S == 2) {
+    return dpp_mov<0x4E>(v);  // quad_perm [2,3,0,1]
+  } else if constexpr (S == 4) {
+    const int a = dpp_mov<0x124>(v), b = dpp_mov<0x12C>(v);  // row_ror:4, row_ror:12
+    return (lane_id() & 4) ? a : b;
+  } else if constexpr (S == 8) {
+    return dpp_mov<0x128>(v);  // row_ror:8
+  } else if constexpr (S == 16) {
+    const auto r = __builtin_amdgcn_permlane16_swap((unsigned)v, (unsigned)v, false, false);
+    return (lane_id() & 16) ? (int)r[0] : (int)r[1];
+  } else {
+    static_assert(S == 32, "xor exchange distance");
+    const auto r = __builtin_amdgcn_permlane32_swap((unsigned)v, (unsigned)v, false, false);
+    return (lane_id() & 32) ? (int)r[0] : (int)r[1];
+  }
+}
+template <int S>
+__device__ __forceinline__ float xchg_f(float v) { return __int_as_float(xchg<S>(__float_as_int(v))); }
+
+// One compare-exchange stage of a bitonic network at distance S: the lower
+// lane of each pair keeps the smaller pair when `up`, the larger otherwise.
+template <int S>
+__device__ __forceinline__ void bitonic_stage(float& d, int& id, bool up) {
+  const float od = xchg_f<S>(d);
+  const int oi = xchg<S>(id);
+  const bool lower = (lane_id() & S) == 0;
+  const bool other_less = lt_pair(od, oi, d, id);
+  const bool take = (lower == up) ? other_less : (!other_less && !(od == d && oi == id));
+  if (take) { d = od; id = oi; }
+}
+// Stages S = SIZE/2 .. 1 with the direction of bitonic sequences of length SIZE.
+template <int SIZE>
+__device__ __forceinline__ void bitonic_pass(float& d, int& id, bool up) {
+  if constexpr (SIZE > 32) bitonic_stage<32>(d, id, up);
+  if constexpr (SIZE > 16) bitonic_stage<16>(d, id, up);
+  if constexpr (SIZE > 8) bitonic_stage<8>(d, id, up);
+  if constexpr (SIZE > 4) bitonic_stage<4>(d, id, up);
+  if constexpr (SIZE > 2) bitonic_stage<2>(d, id, up);
+  bitonic_stage<1>(d, id, up);
+}
+
 // Bitonic sort of one (d, id) pair per lane across the wave, ascending by the tie rule.
 __device__ __forceinline__ void wave_sort64(float& d, int& id) {
   const int lane = lane_id();
-#pragma unroll
-  for (int size = 2; size <= kWave; size <<= 1) {
-#pragma unroll
-    for (int stride = size >> 1; stride > 0; stride >>= 1) {
-      float od = shfl_xor_f(d, stride);
-      int oi = shfl_xor_i(id, stride);
-      const bool up = (lane & size) == 0 || size == kWave;
-      const bool lower = (lane & stride) == 0;
-      const bool other_less = lt_pair(od, oi, d, id);
-      const bool take = (lower == up) ? other_less : (!other_less && !(od == d && oi == id));
-      if (take) { d = od; id = oi; }
-    }
-  }
+  bitonic_pass<2>(d, id, (lane & 2) == 0);
+  bitonic_pass<4>(d, id, (lane & 4) == 0);
+  bitonic_pass<8>(d, id, (lane & 8) == 0);
+  bitonic_pass<16>(d, id, (lane & 16) == 0);
+  bitonic_pass<32>(d, id, (lane & 32) == 0);
+  bitonic_pass<64>(d, id, true);
 }
 
 // Bitonic merge (ascending) of a bitonic sequence held one pair per lane.
-__device__ __forceinline__ void wave_bitonic_merge64(float& d, int& id) {
-  const int lane = lane_id();
-#pragma unroll
-  for (int stride = kWave >> 1; stride > 0; stride >>= 1) {
-    float od = shfl_xor_f(d, stride);
-    int oi = shfl_xor_i(id, stride);
-    const bool lower = (lane & stride) == 0;
-    const bool other_less = lt_pair(od, oi, d, id);
-    const bool take = lower ? other_less : (!other_less && !(od == d && oi == id));
-    if (take) { d = od; id = oi; }
-  }
-}
+__device__ __forceinline__ void wave_bitonic_merge64(float& d, int& id) { bitonic_pass<64>(d, id, true); }
+
+// x(63 - lane): mirror inside each 16-lane row, then swap rows 0<->3, 1<->2.
+__device__ __forceinline__ int wave_reverse(int v) { return xchg<32>(xchg<16>(dpp_mov<0x140>(v))); }
 
 // list (ascending) := the 64 smallest of list U cand, where cand is ascending too.
 __device__ __forceinline__ void wave_merge_sorted64(float& d, int& id, float cd, int ci) {
-  const int lane = lane_id();
-  const float rd = __shfl(cd, kWave - 1 - lane, kWave);
-  const int ri = __shfl(ci, kWave - 1 - lane, kWave);
+  const float rd = __int_as_float(wave_reverse(__float_as_int(cd)));
+  const int ri = wave_reverse(ci);
   if (lt_pair(rd, ri, d, id)) { d = rd; id = ri; }
   wave_bitonic_merge64(d, id);
 }
@@ -126,8 +164,8 @@ __device__ __forceinline__ void wave_merge_sorted64(float& d, int& id, float cd,
 // Insert one (nd, nid) into the ascending list (one pair per lane); the last entry drops off.
 __device__ __forceinline__ void wave_insert64(float& d, int& id, float nd, int nid) {
   const int lane = lane_id();
-  float pd = __shfl_up(d, 1, kWave);
-  int pi = __shfl_up(id, 1, kWave);
+  const float pd = __int_as_float(dpp_mov<0x138>(__float_as_int(d)));  // wave_shr:1: lane i gets lane i-1
+  const int pi = dpp_mov<0x138>(id);
   if (!lt_pair(d, id, nd, nid)) {
     if (lane == 0 || lt_pair(pd, pi, nd, nid)) { d = nd; id = nid; }
     else { d = pd; id = pi; }

@@ -74,6 +74,13 @@ struct TwoPhaseArgs {
   int32_t* top_counts;      // [nq]
   float* cutoffs;           // [nq][p1] or nullptr
   float* thr;               // [nq] or nullptr
+  // Optional instrumentation (nullptr = off), summed over the launch:
+  // [0] vectors whose codes were loaded, [1] LUTs built, [2] phase-2 lists
+  // skipped by the list lower bound, [3] phase-2 candidates appended,
+  // [4..7] shader clocks of workgroup thread 0 in set-up, phase 1, phase 2
+  // and the final select + sort; [8..10] of its phase-1 clocks, those spent
+  // up to the LUT barrier, in the scan loop, and in the merge barrier + merge.
+  unsigned long long* stats = nullptr;
 };
 int two_phase_pool_cap(int p1, int limit_k, int rerank_m);
 fgpu_status launch_two_phase(int dim, int m, const TwoPhaseArgs& a, hipStream_t s);

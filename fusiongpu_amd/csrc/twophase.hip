@@ -149,16 +149,24 @@ __global__ __launch_bounds__(kTT) void two_phase_kernel(TwoPhaseArgs a) {
   __shared__ int hist[256];
   __shared__ int misc[4];
   __shared__ float s_cut[64];
+  __shared__ int f_list[64], f_start[64], f_n[64], f_p[64];  // usable probes in probe order
+  __shared__ float f_lb[64];                                 // lower bound of each phase-2 list
+  __shared__ int s_nv, s_nv1;
   __shared__ int s_cnt;
   __shared__ unsigned long long s_lthr, s_adm;
+  __shared__ unsigned long long s_pub[kTW];  // phase 1: each wave's Q-th best key of the current list
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int kc = tid & (kPQK - 1), g = tid / kPQK;
   const int q = blockIdx.x;
   const int P = a.nprobe, p1 = a.p1, R = a.rerank_m, cap = a.pool_cap, K1 = a.limit_k;
+  // If every wave holds Q = ceil(K1 / 8) vectors at or below its published
+  // key, the list has >= 8 Q >= K1 vectors at or below the largest published
+  // key, so nothing above it can be among the list's K1 best.
+  const int Q = (K1 + kTW - 1) / kTW;
   const uint32_t NL = (uint32_t)a.nlist;
-  const uint32_t* probes = a.probes + (size_t)q * P;
   uint64_t* pool = a.pool + (size_t)q * cap;
+  const long long t_start = a.stats ? clock64() : 0;
 
   float cb[MG * C::S];
 #pragma unroll
@@ -169,12 +177,54 @@ __global__ __launch_bounds__(kTT) void two_phase_kernel(TwoPhaseArgs a) {
   }
   for (int i = tid; i < D; i += kTT) qs[i] = a.queries[(size_t)q * D + i];
   if (tid < 64) s_cut[tid] = 0.0f;
-  if (tid == 0) {
-    s_cnt = 0;
-    s_lthr = kNoThr;
-    s_adm = kNoKey;
+  if (tid < kTW) s_pub[tid] = kNoThr;
+  if (wave == 0) {
+    // Usable probes (in range, non-empty) in probe order; the first s_nv1 are phase 1.
+    int l = 0, st = 0, n = 0;
+    if (lane < P) {
+      const uint32_t pl = a.probes[(size_t)q * P + lane];
+      if (pl < NL) {
+        l = (int)pl;
+        st = a.offsets[pl];
+        n = a.offsets[pl + 1] - st;
+      }
+    }
+    const uint64_t bm = __ballot(n > 0);
+    const int pos = __popcll(bm & ((1ull << lane) - 1ull));
+    if (n > 0) {
+      f_list[pos] = l;
+      f_start[pos] = st;
+      f_n[pos] = n;
+      f_p[pos] = lane;
+    }
+    if (lane == 0) {
+      s_nv = __popcll(bm);
+      s_nv1 = __popcll(bm & (p1 >= 64 ? ~0ull : ((1ull << p1) - 1ull)));
+      s_cnt = 0;
+      s_lthr = kNoThr;
+      s_adm = kNoKey;
+    }
   }
   __syncthreads();
+  const int nv = s_nv, nv1 = s_nv1;
+
+  auto residual = [&](int f, float* r) {
+    if (tid < D) r[tid] = qs[tid] - a.centroids[(size_t)f_list[f] * D + tid];
+  };
+  // Lower bound of every phase-2 list, one wave per list: every later skip
+  // decision is an LDS read.
+  for (int f = nv1 + wave; f < nv; f += kTW) {
+    const float* cr = a.centroids + (size_t)f_list[f] * D;
+    const float ra = lane < D ? qs[lane] - cr[lane] : 0.0f;
+    const float rb = lane + kWave < D ? qs[lane + kWave] - cr[lane + kWave] : 0.0f;
+    float s2 = ra * ra + rb * rb;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) s2 += shfl_xor_f(s2, o);
+    if (lane == 0) f_lb[f] = list_lower_bound(s2, a.rmax[f_list[f]]);
+  }
+  if (nv > 0) residual(0, rbuf[0]);
+  __syncthreads();
+  const long long t_setup = a.stats ? clock64() : 0;
 
   float* lut = smem;
   auto build_lut = [&](const float* r) {
@@ -188,34 +238,52 @@ __global__ __launch_bounds__(kTT) void two_phase_kernel(TwoPhaseArgs a) {
     }
   };
 
-  uint4 w0[C::NV4], w1[C::NV4];
-  int i0 = kPadId, i1 = kPadId;
-  int it = 0;  // non-empty lists seen so far: selects the residual buffer
+  uint4 w0[C::NV4], w1[C::NV4], n0[C::NV4], n1[C::NV4];
+  int i0 = kPadId, i1 = kPadId, j0 = kPadId, j1 = kPadId;
+  int it = 0;       // lists processed: rbuf[it & 1] holds the residual of list pre_f
+  int pre_f = nv > 0 ? 0 : -1;
+  // instrumentation (per wave; summed at the end when a.stats is set)
+  unsigned st_load = 0, st_lut = 0, st_skip = 0, st_pass = 0;
+  auto count_load = [&](int base, int end) { st_load += (unsigned)max(0, min(kVecPerWaveRound, end - base)); };
 
   // ---------------- phase 1: per-list top-limit_k and cutoffs
   int cnt_w0 = 0;  // only wave 0 appends during phase 1
-  for (int p = 0; p < p1; ++p) {
-    const uint32_t l = probes[p];
-    int start = 0, n = 0;
-    if (l < NL) {
-      start = a.offsets[l];
-      n = a.offsets[l + 1] - start;
-    }
-    if (n == 0) continue;  // pruned, out of range or empty: cutoff stays 0
-    float* r = rbuf[it & 1];
-    if (tid < D) r[tid] = qs[tid] - a.centroids[(size_t)l * D + tid];
-    load_pair<M>(a.codes, a.vec_ids, start, n, wave * kVecPerWaveRound + lane, w0, w1, i0, i1);
-    __syncthreads();  // residual ready; the previous list's merge is done
-    build_lut(r);
-    __syncthreads();  // LUT ready
+  long long c_build = 0, c_scan = 0, c_merge = 0;
+  for (int f = 0; f < nv1; ++f) {
+    const long long c0 = a.stats ? clock64() : 0;
+    const int start = f_start[f], n = f_n[f];
+    const int first = wave * kVecPerWaveRound;
+    load_pair<M>(a.codes, a.vec_ids, start, n, first + lane, w0, w1, i0, i1);
+    count_load(first, n);
+    ++st_lut;
+    // All waves have finished scanning list f-1 (they passed its merge
+    // barrier), so the single LUT buffer is free; wave 0 may still be merging.
+    build_lut(rbuf[it & 1]);
+    const int nf = f + 1 < nv ? f + 1 : -1;
+    if (nf >= 0) residual(nf, rbuf[(it + 1) & 1]);
+    __syncthreads();  // LUT f and the next residual ready; s_lthr reset
+    const long long c1 = a.stats ? clock64() : 0;
     float ld = FLT_MAX;
     int li = kPadId;
     uint64_t own = kNoThr;
-    for (int base = wave * kVecPerWaveRound; base < n; base += kTRound) {
-      if (base != wave * kVecPerWaveRound) load_pair<M>(a.codes, a.vec_ids, start, n, base + lane, w0, w1, i0, i1);
+    for (int base = first; base < n; base += kTRound) {
+      const int nb = base + kTRound;
+      if (nb < n) {
+        load_pair<M>(a.codes, a.vec_ids, start, n, nb + lane, n0, n1, j0, j1);
+        count_load(nb, n);
+      }
       const int v0 = base + lane, v1 = v0 + kWave;
-      const uint64_t shared_thr = s_lthr;
-      uint64_t thr = own < shared_thr ? own : shared_thr;
+      uint64_t thr = s_lthr;
+      thr = own < thr ? own : thr;
+      {
+        uint64_t pub = s_pub[0];
+#pragma unroll
+        for (int w = 1; w < kTW; ++w) {
+          const uint64_t pw = s_pub[w];
+          pub = pw > pub ? pw : pub;
+        }
+        thr = pub < thr ? pub : thr;
+      }
       float d0, d1;
       if (adc_sum2<M>(lut, w0, w1, v0 < n, v1 < n, __uint_as_float((uint32_t)(thr >> 32)), d0, d1)) {
         bool changed = offer(d0, i0, v0 < n, thr, ld, li);
@@ -226,13 +294,27 @@ __global__ __launch_bounds__(kTT) void two_phase_kernel(TwoPhaseArgs a) {
         changed |= offer(d1, i1, v1 < n, thr, ld, li);
         if (changed) {
           own = pack_key(readlane_f(ld, K1 - 1), readlane_i(li, K1 - 1));
-          if (lane == 0) atomicMin(&s_lthr, (unsigned long long)own);
+          const uint64_t qth = pack_key(readlane_f(ld, Q - 1), readlane_i(li, Q - 1));
+          if (lane == 0) {
+            atomicMin(&s_lthr, (unsigned long long)own);
+            s_pub[wave] = qth;
+          }
         }
       }
+      if (nb < n) {
+#pragma unroll
+        for (int i = 0; i < C::NV4; ++i) {
+          w0[i] = n0[i];
+          w1[i] = n1[i];
+        }
+        i0 = j0;
+        i1 = j1;
+      }
     }
+    const long long c2 = a.stats ? clock64() : 0;
     md[wave * kWave + lane] = ld;
     mi[wave * kWave + lane] = li;
-    __syncthreads();  // every wave's list of this list is in LDS
+    __syncthreads();  // every wave's list for list f is in LDS
     if (wave == 0) {
 #pragma unroll 1
       for (int w = 1; w < kTW; ++w) wave_merge_sorted64(ld, li, md[w * kWave + lane], mi[w * kWave + lane]);
@@ -240,15 +322,24 @@ __global__ __launch_bounds__(kTT) void two_phase_kernel(TwoPhaseArgs a) {
       if (lane < w) pool[cnt_w0 + lane] = pack_key(ld, li);
       const float cut = readlane_f(ld, w - 1);
       if (lane == 0) {
-        s_cut[p] = cut;
+        s_cut[f_p[f]] = cut;
         s_lthr = kNoThr;
       }
+      if (lane < kTW) s_pub[lane] = kNoThr;
       cnt_w0 += w;
     }
+    if (a.stats) {
+      const long long c3 = clock64();
+      c_build += c1 - c0;
+      c_scan += c2 - c1;
+      c_merge += c3 - c2;
+    }
     ++it;
+    pre_f = nf;
   }
   if (tid == 0) s_cnt = cnt_w0;
   __syncthreads();
+  const long long t_phase1 = a.stats ? clock64() : 0;
 
   // ---------------- threshold (compute_threshold_kernel): coeff * min(cutoff > 0)
   float min_cut = FLT_MAX;
@@ -262,32 +353,28 @@ __global__ __launch_bounds__(kTT) void two_phase_kernel(TwoPhaseArgs a) {
 
   // ---------------- phase 2: every vector with dist <= thr, bounded pool
   const int seg = cap - R;  // vectors per segment: their passers always fit after a select
-  for (int p = p1; p < P; ++p) {
-    const uint32_t l = probes[p];
-    int start = 0, n = 0;
-    if (l < NL) {
-      start = a.offsets[l];
-      n = a.offsets[l + 1] - start;
+  uint64_t adm = kNoKey;
+  float thr_d = thr;
+  for (int f = nv1; f < nv; ++f) {
+    // thr_d only shrinks (selects lower adm), so a list skipped now stays skippable.
+    const float thr_hi = thr_d * (1.0f + 0x1p-16f);
+    if (f_lb[f] > thr_hi) {
+      ++st_skip;
+      continue;
     }
-    if (n == 0) continue;
+    const int start = f_start[f], n = f_n[f];
     float* r = rbuf[it & 1];
-    ++it;
-    if (tid < D) r[tid] = qs[tid] - a.centroids[(size_t)l * D + tid];
-    __syncthreads();  // residual ready; every append of earlier lists is done
+    if (pre_f != f) residual(f, r);
+    __syncthreads();  // residual ready; the previous list is scanned and its appends are done
     int cnt0 = s_cnt;
-    uint64_t adm = s_adm;
-    float thr_d = fminf(thr, key_dist(adm));
-    // Lower bound on every ADC distance of the list (same value in every wave).
-    {
-      const float ra = lane < D ? r[lane] : 0.0f;
-      const float rb = lane + kWave < D ? r[lane + kWave] : 0.0f;
-      float s2 = ra * ra + rb * rb;
-#pragma unroll
-      for (int o = 32; o > 0; o >>= 1) s2 += shfl_xor_f(s2, o);
-      if (list_lower_bound(s2, a.rmax[l]) > thr_d * (1.0f + 0x1p-16f)) continue;
-    }
-    load_pair<M>(a.codes, a.vec_ids, start, n, wave * kVecPerWaveRound + lane, w0, w1, i0, i1);
+    const int first = wave * kVecPerWaveRound;
+    load_pair<M>(a.codes, a.vec_ids, start, n, first + lane, w0, w1, i0, i1);
+    count_load(first, n);
+    ++st_lut;
     build_lut(r);
+    int nf = f + 1;
+    while (nf < nv && f_lb[nf] > thr_hi) ++nf;
+    if (nf < nv) residual(nf, rbuf[(it + 1) & 1]);
     __syncthreads();  // LUT ready; every thread has read cnt0
     int s0 = 0;
     while (true) {
@@ -302,8 +389,17 @@ __global__ __launch_bounds__(kTT) void two_phase_kernel(TwoPhaseArgs a) {
         __syncthreads();
         thr_d = fminf(thr, key_dist(adm));
       }
-      for (int base = s0 + wave * kVecPerWaveRound; base < s1; base += kTRound) {
-        if (base != wave * kVecPerWaveRound) load_pair<M>(a.codes, a.vec_ids, start, n, base + lane, w0, w1, i0, i1);
+      int base = s0 + first;
+      if (s0 != 0 && base < s1) {  // segment 0's first round was loaded before the LUT build
+        load_pair<M>(a.codes, a.vec_ids, start, n, base + lane, w0, w1, i0, i1);
+        count_load(base, n);
+      }
+      while (base < s1) {
+        const int nb = base + kTRound;
+        if (nb < s1) {
+          load_pair<M>(a.codes, a.vec_ids, start, n, nb + lane, n0, n1, j0, j1);
+          count_load(nb, n);
+        }
         const int v0 = base + lane, v1 = v0 + kWave;
         float d0, d1;
         if (adc_sum2<M>(lut, w0, w1, v0 < s1, v1 < s1, thr_d, d0, d1)) {
@@ -313,6 +409,7 @@ __global__ __launch_bounds__(kTT) void two_phase_kernel(TwoPhaseArgs a) {
           const uint64_t b0 = __ballot(pass0), b1 = __ballot(pass1);
           const int c0 = __popcll(b0), c = c0 + __popcll(b1);
           if (c) {
+            st_pass += c;
             int at = 0;
             if (lane == 0) at = atomicAdd(&s_cnt, c);
             at = __shfl(at, 0, kWave);
@@ -321,6 +418,16 @@ __global__ __launch_bounds__(kTT) void two_phase_kernel(TwoPhaseArgs a) {
             if (pass1) pool[at + c0 + __popcll(b1 & below)] = k1;
           }
         }
+        if (nb < s1) {
+#pragma unroll
+          for (int i = 0; i < C::NV4; ++i) {
+            w0[i] = n0[i];
+            w1[i] = n1[i];
+          }
+          i0 = j0;
+          i1 = j1;
+        }
+        base = nb;
       }
       if (s1 >= n) break;
       s0 = s1;
@@ -328,6 +435,17 @@ __global__ __launch_bounds__(kTT) void two_phase_kernel(TwoPhaseArgs a) {
       cnt0 = s_cnt;
       __syncthreads();  // everyone has read the count before new appends
     }
+    ++it;
+    pre_f = nf < nv ? nf : -1;
+  }
+  const long long t_phase2 = a.stats ? clock64() : 0;
+  if (a.stats && lane == 0) {
+    atomicAdd(&a.stats[0], (unsigned long long)st_load);
+    if (wave == 0) {
+      atomicAdd(&a.stats[1], (unsigned long long)st_lut);
+      atomicAdd(&a.stats[2], (unsigned long long)st_skip);
+    }
+    atomicAdd(&a.stats[3], (unsigned long long)st_pass);
   }
 
   // ---------------- top rerank_m: select, LDS bitonic sort, gather
@@ -350,6 +468,16 @@ __global__ __launch_bounds__(kTT) void two_phase_kernel(TwoPhaseArgs a) {
     a.top_d[(size_t)q * R + j] = real ? __uint_as_float((uint32_t)(key >> 32)) : FLT_MAX;
   }
   if (tid == 0) a.top_counts[q] = cnt;
+  if (a.stats && tid == 0) {
+    const long long t_end = clock64();
+    atomicAdd(&a.stats[4], (unsigned long long)(t_setup - t_start));
+    atomicAdd(&a.stats[5], (unsigned long long)(t_phase1 - t_setup));
+    atomicAdd(&a.stats[6], (unsigned long long)(t_phase2 - t_phase1));
+    atomicAdd(&a.stats[7], (unsigned long long)(t_end - t_phase2));
+    atomicAdd(&a.stats[8], (unsigned long long)c_build);
+    atomicAdd(&a.stats[9], (unsigned long long)c_scan);
+    atomicAdd(&a.stats[10], (unsigned long long)c_merge);
+  }
 }
 
 template <int D, int M>

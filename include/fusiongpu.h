@@ -134,6 +134,20 @@ fgpu_status fgpu_two_phase_search(const fgpu_index* idx, const float* d_queries,
                                   float* d_thresholds, void* d_workspace, size_t workspace_bytes,
                                   void* stream);
 
+/* fgpu_two_phase_search plus instrumentation (no reference counterpart): adds
+ * to d_stats[0..10] (device, caller-zeroed, uint64) the vectors whose codes
+ * were loaded, the LUTs built, the phase-2 lists skipped by the list lower
+ * bound, the phase-2 candidates appended, the shader clocks each workgroup
+ * spent in set-up, phase 1, phase 2 and the final select + sort, and the
+ * phase-1 clocks up to the LUT barrier, in the scan and in the merge.
+ * Results are unchanged. */
+fgpu_status fgpu_two_phase_search_stats(const fgpu_index* idx, const float* d_queries, int nq,
+                                        const uint32_t* d_probe_ids, int nprobe, int p1_lists, int limit_k,
+                                        float threshold_coeff, int rerank_m, int32_t* d_top_ids,
+                                        float* d_top_dists, int32_t* d_top_counts,
+                                        unsigned long long* d_stats, void* d_workspace,
+                                        size_t workspace_bytes, void* stream);
+
 /* ---- search: exact rerank (A11) ---------------------------------------- */
 
 /* run_gpu_rerank (gpu_global.cu:603-673): per query, walk the first
