@@ -15,6 +15,7 @@ Reference interfaces mirrored (Hello-day/FusionGPU):
   * rerank                          -> run_gpu_rerank (gpu_global.cu:603-673)
   * Index.search_rerank             -> SearchPipeline::submit_batch's device path (search_pipeline.cu:341-361)
   * kmeans_fit / l2_topk            -> run_kmeans_gpu / batch_assign_clusters (kmeans_gpu.cuh:197-324)
+  * knn_exact                       -> brute_force_search_kernel (tune_parameters.cu:49-96)
   * pq_train                        -> train_residual_pq_codebooks (pq_utils.h:77-138)
   * pq_encode                       -> encode_residuals_to_pq_gpu (kmeans_gpu.cuh:450-508)
   * build_ivfpq                     -> build_global main (build_global.cu:21-258), no rebalancing
@@ -29,7 +30,7 @@ import numpy as np
 __all__ = [
     "FgpuError", "lib", "lib_path", "Index", "gen_gmm", "l2_topk", "kmeans_fit", "kmeans_update",
     "fixed_shift", "pq_train", "pq_encode", "build_ivfpq", "write_ivf_data", "read_ivf_data",
-    "write_fvecs", "read_fvecs", "read_ivecs", "probe_counts", "rerank",
+    "write_fvecs", "read_fvecs", "read_ivecs", "probe_counts", "rerank", "knn_exact",
 ]
 
 lib_path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib", "libfusiongpu.so")
@@ -61,6 +62,8 @@ _SIGS = {
     "fgpu_search_rerank_workspace_bytes": (_sz, [_i32, _i32, _i32, _i32, _i32, _i32]),
     "fgpu_search_rerank": (_i32, [_vp, _vp, _i32, _i32, _f32, _i32, _i32, _f32, _i32, _vp, _i64, _i32, _i32, _f32,
                                   _i32, _vp, _vp, _vp, _sz, _vp]),
+    "fgpu_knn_exact_workspace_bytes": (_sz, [_i32, _i64]),
+    "fgpu_knn_exact": (_i32, [_vp, _i32, _vp, _i64, _i32, _i32, _vp, _vp, _vp, _sz, _vp]),
     "fgpu_l2_topk_workspace_bytes": (_sz, [_i64, _i32]),
     "fgpu_l2_topk": (_i32, [_vp, _i64, _vp, _i32, _i32, _i32, _vp, _vp, _vp, _sz, _vp]),
     "fgpu_kmeans_workspace_bytes": (_sz, [_i32, _i32]),
@@ -412,6 +415,20 @@ def l2_topk(x, c, p: int, stream=None):
     d = torch.empty((n, p), dtype=torch.float32, device="cuda")
     _check(lib.fgpu_l2_topk(_dev_ptr(x), n, _dev_ptr(c), nc, dim, p, _dev_ptr(ids), _dev_ptr(d), _dev_ptr(ws),
                             ws.numel(), _stream(stream)))
+    return ids, d
+
+
+def knn_exact(queries, base, k: int, workspace=None, stream=None):
+    """Exact kNN ground truth (brute_force_search_kernel): (ids int32 [nq][k], dists float32 [nq][k])."""
+    torch = _torch()
+    q, b = _to_dev(queries), _to_dev(base)
+    nq, dim = q.shape
+    n = b.shape[0]
+    ws = workspace if workspace is not None else _workspace(lib.fgpu_knn_exact_workspace_bytes(nq, n))
+    ids = torch.empty((nq, k), dtype=torch.int32, device="cuda")
+    d = torch.empty((nq, k), dtype=torch.float32, device="cuda")
+    _check(lib.fgpu_knn_exact(_dev_ptr(q), nq, _dev_ptr(b), n, dim, k, _dev_ptr(ids), _dev_ptr(d), _dev_ptr(ws),
+                              ws.numel(), _stream(stream)))
     return ids, d
 
 

@@ -378,6 +378,58 @@ fgpu_status fgpu_l2_topk(const float* dx, int64_t n, const float* dc, int nc, in
 }
 
 // ---------------------------------------------------------------------------
+}  // extern "C"
+
+namespace {
+constexpr int kKnnChunk = 4096;
+int64_t knn_rows(int nq) {
+  const int64_t budget = 256ll << 20;
+  const int64_t r = budget / ((int64_t)kKnnChunk * sizeof(float));
+  return std::min<int64_t>(r - r % 64, ((int64_t)nq + 63) / 64 * 64);
+}
+}  // namespace
+
+extern "C" {
+
+size_t fgpu_knn_exact_workspace_bytes(int nq, int64_t n) {
+  return carve_bytes<float>((size_t)std::max(nq, 1)) + carve_bytes<float>((size_t)std::max<int64_t>(n, 1)) +
+         carve_bytes<float>(64) + carve_bytes<float>((size_t)knn_rows(std::max(nq, 1)) * kKnnChunk);
+}
+
+fgpu_status fgpu_knn_exact(const float* dq, int nq, const float* d_base, int64_t n, int dim, int k, int32_t* d_ids,
+                           float* d_dists, void* ws, size_t ws_bytes, void* stream) {
+  FGPU_CHECK(dq && d_base && d_ids && d_dists && ws, FGPU_ERR_ARG, "knn_exact: null argument");
+  FGPU_CHECK(nq >= 0 && n >= 1 && n < INT32_MAX && k >= 1 && k <= 128, FGPU_ERR_ARG,
+             "knn_exact: need 1 <= k <= 128 and 1 <= n < 2^31");
+  FGPU_CHECK(dim >= 4 && dim <= 256 && dim % 4 == 0, FGPU_ERR_UNSUPPORTED,
+             "knn_exact: dim must be a multiple of 4 in [4, 256]");
+  if (nq == 0) return FGPU_OK;
+  hipStream_t s = as_stream(stream);
+  Carve cv(ws, ws_bytes);
+  float* qn = cv.take<float>(nq);
+  float* bn = cv.take<float>(n);
+  float* bmax = cv.take<float>(64);
+  FGPU_CHECK(cv.ok(), FGPU_ERR_WORKSPACE, "knn_exact: workspace too small");
+  const size_t rest = ws_bytes - cv.used;
+  const int64_t rows = std::min<int64_t>(est_rows_per_batch(rest, kKnnChunk), ((int64_t)nq + 63) / 64 * 64);
+  FGPU_CHECK(rows >= 64, FGPU_ERR_WORKSPACE, "knn_exact: workspace too small");
+  float* est = cv.take<float>((size_t)rows * kKnnChunk);
+  FGPU_TRY(launch_row_norms(dq, nq, dim, qn, s));
+  FGPU_TRY(launch_row_norms(d_base, n, dim, bn, s));
+  FGPU_TRY(launch_max_reduce(bn, n, bmax, s));
+  for (int64_t b0 = 0; b0 < nq; b0 += rows) {
+    const int64_t nb = std::min<int64_t>(rows, nq - b0);
+    for (int64_t c0 = 0; c0 < n; c0 += kKnnChunk) {
+      const int ncols = (int)std::min<int64_t>(kKnnChunk, n - c0);
+      FGPU_TRY(launch_gemm_est(dq + b0 * dim, nb, d_base + c0 * dim, ncols, dim, qn + b0, bn + c0, est, kKnnChunk, s));
+      FGPU_TRY(launch_knn_chunk(est, kKnnChunk, nb, ncols, dq + b0 * dim, d_base + c0 * dim, dim, qn + b0, bmax, k,
+                                (int)c0, c0 > 0, d_ids + b0 * k, d_dists + b0 * k, s));
+    }
+  }
+  return FGPU_OK;
+}
+
+// ---------------------------------------------------------------------------
 int fgpu_fixed_shift(float maxabs, int64_t n) {
   int e = 0;
   if (maxabs > 0.0f) std::frexp((double)maxabs, &e);

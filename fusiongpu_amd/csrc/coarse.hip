@@ -122,6 +122,79 @@ __global__ __launch_bounds__(256) void gemm_est_kernel(const float* __restrict__
 
 constexpr int kCandCap = 256;
 
+// The p-th smallest of the wave's estimates val[j] (column j*64 + lane, only
+// columns < ncols count): LDS radix select, 8 bits a pass, over the
+// order-preserving integer map of the floats.  p == 1 is a plain minimum.
+template <int VPL>
+__device__ float wave_kth_estimate(const float (&val)[VPL], int ncols, int p, uint32_t* hist) {
+  const int lane = threadIdx.x & 63;
+  if (p == 1) {
+    float m = val[0];
+#pragma unroll
+    for (int j = 1; j < VPL; ++j) m = fminf(m, val[j]);
+    return wave_min_f(m);
+  }
+  uint32_t key[VPL];
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) key[j] = (j * kWave + lane < ncols) ? float_key(val[j]) : 0xFFFFFFFFu;
+  uint32_t prefix = 0, mask = 0;
+  uint32_t rem = (uint32_t)p;
+  for (int shift = 24; shift >= 0; shift -= 8) {
+    for (int b = lane; b < 256; b += kWave) hist[b] = 0u;
+    wave_lds_sync();
+#pragma unroll
+    for (int j = 0; j < VPL; ++j)
+      if ((key[j] & mask) == prefix) atomicAdd(&hist[(key[j] >> shift) & 255u], 1u);
+    wave_lds_sync();
+    const uint32_t h0 = hist[4 * lane], h1 = hist[4 * lane + 1], h2 = hist[4 * lane + 2],
+                   h3 = hist[4 * lane + 3];
+    const uint32_t s = h0 + h1 + h2 + h3;
+    uint32_t inc = s;
+#pragma unroll
+    for (int o = 1; o < kWave; o <<= 1) {
+      uint32_t t = __shfl_up(inc, o, kWave);
+      if (lane >= o) inc += t;
+    }
+    const uint32_t exc = inc - s;
+    const uint64_t bm = __ballot(exc < rem && rem <= inc);
+    const int L = __ffsll((unsigned long long)bm) - 1;
+    int bin = 3;
+    uint32_t below = exc + h0 + h1 + h2;
+    if (rem <= exc + h0) { bin = 0; below = exc; }
+    else if (rem <= exc + h0 + h1) { bin = 1; below = exc + h0; }
+    else if (rem <= exc + h0 + h1 + h2) { bin = 2; below = exc + h0 + h1; }
+    bin = readlane_i(bin, L) + 4 * L;
+    below = (uint32_t)readlane_i((int)below, L);
+    rem -= below;
+    prefix |= (uint32_t)bin << shift;
+    mask |= 0xFFu << shift;
+    wave_lds_sync();
+  }
+  return key_float(prefix);
+}
+
+// Exact squared L2 of the wave's staged row xs against row cr of c, in the
+// reference's device form (sequential fused multiply-add over dimensions).
+__device__ __forceinline__ float exact_l2(const float* __restrict__ xs, const float* __restrict__ cr, int dim) {
+  float acc = 0.0f;
+  if ((dim & 3) == 0) {
+    for (int t = 0; t < dim; t += 4) {
+      const float4 cv = *reinterpret_cast<const float4*>(cr + t);
+      const float4 xv = *reinterpret_cast<const float4*>(xs + t);
+      float df = xv.x - cv.x; acc = __builtin_fmaf(df, df, acc);
+      df = xv.y - cv.y; acc = __builtin_fmaf(df, df, acc);
+      df = xv.z - cv.z; acc = __builtin_fmaf(df, df, acc);
+      df = xv.w - cv.w; acc = __builtin_fmaf(df, df, acc);
+    }
+  } else {
+    for (int t = 0; t < dim; ++t) {
+      const float df = xs[t] - cr[t];
+      acc = __builtin_fmaf(df, df, acc);
+    }
+  }
+  return acc;
+}
+
 // One wave per row: p-th smallest estimate by LDS radix select, margin
 // superset, exact re-score, bitonic sort by (distance, index).
 template <int VPL>
@@ -150,51 +223,7 @@ __global__ __launch_bounds__(256) void select_exact_kernel(
   }
 
   // Threshold T = p-th smallest estimate.
-  float T;
-  if (p == 1) {
-    float m = val[0];
-#pragma unroll
-    for (int j = 1; j < VPL; ++j) m = fminf(m, val[j]);
-    T = wave_min_f(m);
-  } else {
-    uint32_t key[VPL];
-#pragma unroll
-    for (int j = 0; j < VPL; ++j) key[j] = (j * kWave + lane < ncols) ? float_key(val[j]) : 0xFFFFFFFFu;
-    uint32_t prefix = 0, mask = 0;
-    uint32_t rem = (uint32_t)p;
-    for (int shift = 24; shift >= 0; shift -= 8) {
-      for (int b = lane; b < 256; b += kWave) hist[b] = 0u;
-      wave_lds_sync();
-#pragma unroll
-      for (int j = 0; j < VPL; ++j)
-        if ((key[j] & mask) == prefix) atomicAdd(&hist[(key[j] >> shift) & 255u], 1u);
-      wave_lds_sync();
-      const uint32_t h0 = hist[4 * lane], h1 = hist[4 * lane + 1], h2 = hist[4 * lane + 2],
-                     h3 = hist[4 * lane + 3];
-      const uint32_t s = h0 + h1 + h2 + h3;
-      uint32_t inc = s;
-#pragma unroll
-      for (int o = 1; o < kWave; o <<= 1) {
-        uint32_t t = __shfl_up(inc, o, kWave);
-        if (lane >= o) inc += t;
-      }
-      const uint32_t exc = inc - s;
-      const uint64_t bm = __ballot(exc < rem && rem <= inc);
-      const int L = __ffsll((unsigned long long)bm) - 1;
-      int bin = 3;
-      uint32_t below = exc + h0 + h1 + h2;
-      if (rem <= exc + h0) { bin = 0; below = exc; }
-      else if (rem <= exc + h0 + h1) { bin = 1; below = exc + h0; }
-      else if (rem <= exc + h0 + h1 + h2) { bin = 2; below = exc + h0 + h1; }
-      bin = readlane_i(bin, L) + 4 * L;
-      below = (uint32_t)readlane_i((int)below, L);
-      rem -= below;
-      prefix |= (uint32_t)bin << shift;
-      mask |= 0xFFu << shift;
-      wave_lds_sync();
-    }
-    T = key_float(prefix);
-  }
+  const float T = wave_kth_estimate<VPL>(val, ncols, p, hist);
   const double E = (double)kappa * ((double)xn[row] + (double)(*cn_max));
   const double thr = (double)T + 2.0 * E;
 
@@ -221,24 +250,7 @@ __global__ __launch_bounds__(256) void select_exact_kernel(
     int id = kPadId;
     if (base + lane < ncand) {
       id = all_cols ? base + lane : cand[base + lane];
-      const float* cr = c + (int64_t)id * dim;
-      float acc = 0.0f;
-      if ((dim & 3) == 0) {
-        for (int t = 0; t < dim; t += 4) {
-          const float4 cv = *reinterpret_cast<const float4*>(cr + t);
-          const float4 xv = *reinterpret_cast<const float4*>(xs + t);
-          float df = xv.x - cv.x; acc = __builtin_fmaf(df, df, acc);
-          df = xv.y - cv.y; acc = __builtin_fmaf(df, df, acc);
-          df = xv.z - cv.z; acc = __builtin_fmaf(df, df, acc);
-          df = xv.w - cv.w; acc = __builtin_fmaf(df, df, acc);
-        }
-      } else {
-        for (int t = 0; t < dim; ++t) {
-          const float df = xs[t] - cr[t];
-          acc = __builtin_fmaf(df, df, acc);
-        }
-      }
-      d = acc;
+      d = exact_l2(xs, c + (int64_t)id * dim, dim);
     }
     wave_sort64(d, id);
     if (first) { ld_ = d; li = id; first = false; }
@@ -253,6 +265,130 @@ __global__ __launch_bounds__(256) void select_exact_kernel(
     out_ids[row * p + lane] = oid;
     out_d[row * p + lane] = ld_;
   }
+}
+
+// Exact kNN (brute_force_search_kernel, tune_parameters.cu:49-96) over one
+// chunk of base rows, merged into each query's running top-k (k <= 128):
+// the running list sits in two sorted 64-lists per wave, A (ranks 1-64) and
+// B (ranks 65-128).  Chunk columns carry ids id_base + col, above every id
+// of earlier chunks, so the tie rule (distance, id) needs no extra care.
+// Candidate superset: est <= min(T + 2E, kth + E), T the min(k, ncols)-th
+// estimate of the chunk and kth the running k-th exact distance; the second
+// bound alone is tried first once the running list is full, which spares the
+// radix select in every chunk after the first.
+constexpr int kKnnCap = 512;
+
+template <int VPL>
+__global__ __launch_bounds__(256) void knn_chunk_kernel(
+    const float* __restrict__ est, int64_t ld, int64_t nrows, int ncols, const float* __restrict__ x,
+    const float* __restrict__ c, int dim, const float* __restrict__ xn, const float* __restrict__ cn_max,
+    float kappa, int k, int id_base, int accum, int32_t* __restrict__ out_ids, float* __restrict__ out_d) {
+  __shared__ uint32_t hist_s[4][256];
+  __shared__ int cand_s[4][kKnnCap];
+  __shared__ __align__(16) float x_s[4][256];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t row = (int64_t)blockIdx.x * 4 + wave;
+  if (row >= nrows) return;  // whole wave leaves; no workgroup barrier follows
+  uint32_t* hist = hist_s[wave];
+  int* cand = cand_s[wave];
+  float* xs = x_s[wave];
+  for (int d = lane; d < dim; d += kWave) xs[d] = x[row * dim + d];
+
+  // running top-k
+  float ad = FLT_MAX, bd = FLT_MAX;
+  int ai = kPadId, bi = kPadId;
+  if (accum) {
+    if (lane < k) {
+      const int id = out_ids[row * k + lane];
+      if (id >= 0) { ad = out_d[row * k + lane]; ai = id; }
+    }
+    if (lane + kWave < k) {
+      const int id = out_ids[row * k + lane + kWave];
+      if (id >= 0) { bd = out_d[row * k + lane + kWave]; bi = id; }
+    }
+  }
+  const float kth = k <= kWave ? readlane_f(ad, k - 1) : readlane_f(bd, k - kWave - 1);
+  const bool full = (k <= kWave ? readlane_i(ai, k - 1) : readlane_i(bi, k - kWave - 1)) != kPadId;
+
+  float val[VPL];
+  const float* er = est + row * ld;
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) {
+    const int col = j * kWave + lane;
+    val[j] = col < ncols ? er[col] : FLT_MAX;
+  }
+  const double E = (double)kappa * ((double)xn[row] + (double)(*cn_max));
+  const int p = k < ncols ? k : ncols;
+
+  // Ordered compaction of the columns with estimate <= thr; the count may exceed the cap.
+  auto gather = [&](double thr) {
+    int C = 0;
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) {
+      const int col = j * kWave + lane;
+      const bool f = col < ncols && (double)val[j] <= thr;
+      const uint64_t bm = __ballot(f);
+      const int pos = C + lanes_below(bm);
+      if (f && pos < kKnnCap) cand[pos] = col;
+      C += __popcll(bm);
+    }
+    wave_lds_sync();
+    return C;
+  };
+  double thr = full ? (double)kth + E : 0.0;
+  int C = full ? gather(thr) : kKnnCap + 1;
+  if (C > kKnnCap) {
+    const float T = wave_kth_estimate<VPL>(val, ncols, p, hist);
+    const double t2 = (double)T + 2.0 * E;
+    thr = full && thr < t2 ? thr : t2;
+    C = gather(thr);
+  }
+  const bool all_cols = C > kKnnCap;  // pathological ties: re-score everything
+  const int ncand = all_cols ? ncols : C;
+
+  for (int base = 0; base < ncand; base += kWave) {
+    float d = FLT_MAX;
+    int id = kPadId;
+    if (base + lane < ncand) {
+      const int col = all_cols ? base + lane : cand[base + lane];
+      d = exact_l2(xs, c + (int64_t)col * dim, dim);
+      id = id_base + col;
+    }
+    wave_sort64(d, id);
+    if (k <= kWave) {
+      wave_merge_sorted64(ad, ai, d, id);
+    } else {
+      // A U C splits into its 64 smallest (new A) and 64 largest (H); B := best 64 of B U H.
+      const float rd = __int_as_float(wave_reverse(__float_as_int(d)));
+      const int ri = wave_reverse(id);
+      const bool c_lo = lt_pair(rd, ri, ad, ai);
+      float hd = c_lo ? ad : rd;
+      int hi = c_lo ? ai : ri;
+      if (c_lo) { ad = rd; ai = ri; }
+      wave_bitonic_merge64(ad, ai);
+      wave_bitonic_merge64(hd, hi);
+      wave_merge_sorted64(bd, bi, hd, hi);
+    }
+  }
+  if (lane < k) {
+    out_ids[row * k + lane] = ai == kPadId ? -1 : ai;
+    out_d[row * k + lane] = ai == kPadId ? FLT_MAX : ad;
+  }
+  if (lane + kWave < k) {
+    out_ids[row * k + lane + kWave] = bi == kPadId ? -1 : bi;
+    out_d[row * k + lane + kWave] = bi == kPadId ? FLT_MAX : bd;
+  }
+}
+
+template <int VPL>
+fgpu_status launch_knn_t(const float* est, int64_t ld, int64_t nrows, int ncols, const float* x, const float* c,
+                         int dim, const float* xn, const float* cn_max, float kappa, int k, int id_base, int accum,
+                         int32_t* ids, float* d, hipStream_t s) {
+  const int64_t blocks = (nrows + 3) / 4;
+  hipLaunchKernelGGL(knn_chunk_kernel<VPL>, dim3((unsigned)blocks), dim3(256), 0, s, est, ld, nrows, ncols, x, c,
+                     dim, xn, cn_max, kappa, k, id_base, accum, ids, d);
+  FGPU_HIP(hipGetLastError());
+  return FGPU_OK;
 }
 
 template <int VPL>
@@ -317,6 +453,19 @@ fgpu_status launch_select_exact(const float* est, int64_t ld, int64_t nrows, int
   FGPU_SEL(64);
 #undef FGPU_SEL
   return set_error(FGPU_ERR_UNSUPPORTED, "select: more than 4096 columns");
+}
+
+fgpu_status launch_knn_chunk(const float* est, int64_t ld, int64_t nrows, int ncols, const float* x, const float* c,
+                             int dim, const float* xn, const float* cn_max, int k, int id_base, int accum,
+                             int32_t* ids, float* d, hipStream_t s) {
+  FGPU_CHECK(k >= 1 && k <= 2 * kWave, FGPU_ERR_UNSUPPORTED, "knn: k must be in [1, 128]");
+  FGPU_CHECK(dim <= 256, FGPU_ERR_UNSUPPORTED, "knn: dim must be <= 256");
+  FGPU_CHECK(ncols >= 1 && ncols <= 64 * kWave, FGPU_ERR_UNSUPPORTED, "knn: chunk must hold 1..4096 rows");
+  if (nrows <= 0) return FGPU_OK;
+  const float kappa = coarse_kappa(dim);
+  if (ncols <= 16 * kWave)
+    return launch_knn_t<16>(est, ld, nrows, ncols, x, c, dim, xn, cn_max, kappa, k, id_base, accum, ids, d, s);
+  return launch_knn_t<64>(est, ld, nrows, ncols, x, c, dim, xn, cn_max, kappa, k, id_base, accum, ids, d, s);
 }
 
 int64_t est_rows_per_batch(size_t bytes, int ncols) {

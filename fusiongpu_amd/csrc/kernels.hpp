@@ -25,6 +25,11 @@ fgpu_status launch_select_exact(const float* est, int64_t ld, int64_t nrows, int
                                 const float* x, const float* c, int dim, const float* xn,
                                 const float* cn_max, int p, int prune, float prune_ratio,
                                 int32_t* out_ids, float* out_d, hipStream_t s);
+// Exact kNN over one chunk of <= 4096 base rows c (ids id_base + col), merged
+// into the running top-k in ids/d (k <= 128) when accum != 0.
+fgpu_status launch_knn_chunk(const float* est, int64_t ld, int64_t nrows, int ncols, const float* x, const float* c,
+                             int dim, const float* xn, const float* cn_max, int k, int id_base, int accum,
+                             int32_t* ids, float* d, hipStream_t s);
 // Rows per batch of the estimate matrix that fit in `bytes`.
 int64_t est_rows_per_batch(size_t bytes, int ncols);
 

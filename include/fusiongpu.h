@@ -186,6 +186,21 @@ fgpu_status fgpu_l2_topk(const float* d_x, int64_t n, const float* d_c, int nc, 
                          int32_t* d_ids, float* d_dists, void* d_workspace, size_t workspace_bytes,
                          void* stream);
 
+/* ---- exact kNN ground truth (A18) -------------------------------------- */
+
+/* brute_force_search_kernel (tune_parameters.cu:49-96): for each query row of
+ * d_queries [nq][dim], the k nearest rows of d_base [n][dim] by exact squared
+ * L2 in the reference's device form, ascending (distance, row index) -- the
+ * reference's strict-< insertion keeps the earlier row on ties; padding -1 /
+ * FLT_MAX when n < k.  The base streams through in chunks of 4096 rows: an
+ * MFMA GEMM estimate per chunk, then an exact re-score of every row that the
+ * rigorous error margin cannot rule out, merged into each query's running
+ * top-k.  k <= 128, dim <= 256 and a multiple of 4, n < 2^31. */
+size_t fgpu_knn_exact_workspace_bytes(int nq, int64_t n);
+fgpu_status fgpu_knn_exact(const float* d_queries, int nq, const float* d_base, int64_t n, int dim, int k,
+                           int32_t* d_ids, float* d_dists, void* d_workspace, size_t workspace_bytes,
+                           void* stream);
+
 /* ---- index build (A13-A17) -------------------------------------------- */
 
 /* One Lloyd update (kmeans_gpu.cuh:81-116) with deterministic fixed-point

@@ -168,3 +168,23 @@ def test_build_ivfpq_sampled_bit_exact():
                               train_rows=2500)
     for g, w, name in zip(got, want, ["offsets", "ids", "codes", "centroids", "codebook"]):
         assert np.array_equal(np.asarray(g).view(np.uint8), np.asarray(w).view(np.uint8)), name
+
+
+@pytest.mark.parametrize("k,n,dim", [(10, 10000, 96), (100, 9000, 128), (128, 4097, 96), (1, 5000, 64),
+                                     (64, 50, 128)])
+def test_knn_exact_bit_exact(k, n, dim):
+    _say(f"knn_exact k={k} n={n} dim={dim}")
+    rng = np.random.default_rng(k + n + dim)
+    base = rng.standard_normal((n, dim)).astype(np.float32)
+    q = rng.standard_normal((150, dim)).astype(np.float32)
+    base[min(4099, n - 1)] = base[7]      # a duplicate row in a later chunk: the lower id wins the tie
+    q[0] = base[7]                        # distance exactly 0 to both
+    q[1] = base[n - 1] + np.float32(1e-3)
+    gid, gd = fg.knn_exact(torch.from_numpy(q).cuda(), torch.from_numpy(base).cuda(), k)
+    oid, od = oracle.knn_exact(q, base, k)
+    gid, gd = _host(gid), _host(gd)
+    bad = np.nonzero(~np.all(gid == oid, axis=1))[0]
+    assert bad.size == 0, f"first mismatching queries {bad[:5]}: gpu {gid[bad[0]][:8]} oracle {oid[bad[0]][:8]}"
+    assert np.array_equal(_bits(gd), _bits(od))
+    if n < k:
+        assert np.all(gid[:, n:] == -1)
