@@ -16,6 +16,7 @@ Reference interfaces mirrored (Hello-day/FusionGPU):
   * Index.search_rerank             -> SearchPipeline::submit_batch's device path (search_pipeline.cu:341-361)
   * kmeans_fit / l2_topk            -> run_kmeans_gpu / batch_assign_clusters (kmeans_gpu.cuh:197-324)
   * knn_exact                       -> brute_force_search_kernel (tune_parameters.cu:49-96)
+  * graph_search                    -> the cuVS CAGRA search role (cagra_adapter.cuh:38-68), own algorithm
   * pq_train                        -> train_residual_pq_codebooks (pq_utils.h:77-138)
   * pq_encode                       -> encode_residuals_to_pq_gpu (kmeans_gpu.cuh:450-508)
   * build_ivfpq                     -> build_global main (build_global.cu:21-258), no rebalancing
@@ -30,7 +31,7 @@ import numpy as np
 __all__ = [
     "FgpuError", "lib", "lib_path", "Index", "gen_gmm", "l2_topk", "kmeans_fit", "kmeans_update",
     "fixed_shift", "pq_train", "pq_encode", "build_ivfpq", "write_ivf_data", "read_ivf_data",
-    "write_fvecs", "read_fvecs", "read_ivecs", "probe_counts", "rerank", "knn_exact",
+    "write_fvecs", "read_fvecs", "read_ivecs", "probe_counts", "rerank", "knn_exact", "graph_search",
 ]
 
 lib_path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib", "libfusiongpu.so")
@@ -64,6 +65,8 @@ _SIGS = {
                                   _i32, _vp, _vp, _vp, _sz, _vp]),
     "fgpu_knn_exact_workspace_bytes": (_sz, [_i32, _i64]),
     "fgpu_knn_exact": (_i32, [_vp, _i32, _vp, _i64, _i32, _i32, _vp, _vp, _vp, _sz, _vp]),
+    "fgpu_graph_search": (_i32, [_vp, _i32, _vp, _i64, _i32, _vp, _i32, _i32, _i32, _i32, _i32, _u64, _vp, _vp, _vp,
+                                 _vp, _vp]),
     "fgpu_l2_topk_workspace_bytes": (_sz, [_i64, _i32]),
     "fgpu_l2_topk": (_i32, [_vp, _i64, _vp, _i32, _i32, _i32, _vp, _vp, _vp, _sz, _vp]),
     "fgpu_kmeans_workspace_bytes": (_sz, [_i32, _i32]),
@@ -430,6 +433,23 @@ def knn_exact(queries, base, k: int, workspace=None, stream=None):
     _check(lib.fgpu_knn_exact(_dev_ptr(q), nq, _dev_ptr(b), n, dim, k, _dev_ptr(ids), _dev_ptr(d), _dev_ptr(ws),
                               ws.numel(), _stream(stream)))
     return ids, d
+
+
+def graph_search(queries, base, graph, k: int, itopk: int = 64, width: int = 4, max_iter: int = 64, seed: int = 1,
+                 want_evals: bool = False, out=None, stream=None):
+    """Graph search over a fixed-degree adjacency (the CAGRA role): (ids [nq][k], dists [nq][k], steps [nq])
+    plus, with want_evals, the exact distances computed per query."""
+    torch = _torch()
+    q, b, g = _to_dev(queries), _to_dev(base), _to_dev(graph)
+    nq, dim = q.shape
+    ids, d = out if out is not None else (torch.empty((nq, k), dtype=torch.int32, device="cuda"),
+                                          torch.empty((nq, k), dtype=torch.float32, device="cuda"))
+    it = torch.empty(nq, dtype=torch.int32, device="cuda")
+    ev = torch.empty(nq, dtype=torch.int32, device="cuda") if want_evals else None
+    _check(lib.fgpu_graph_search(_dev_ptr(q), nq, _dev_ptr(b), b.shape[0], dim, _dev_ptr(g), g.shape[1], itopk,
+                                 width, max_iter, k, seed, _dev_ptr(ids), _dev_ptr(d), _dev_ptr(it),
+                                 _dev_ptr(ev) if want_evals else None, _stream(stream)))
+    return (ids, d, it, ev) if want_evals else (ids, d, it)
 
 
 def fixed_shift(maxabs: float, n: int) -> int:

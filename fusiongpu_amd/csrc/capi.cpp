@@ -429,6 +429,17 @@ fgpu_status fgpu_knn_exact(const float* dq, int nq, const float* d_base, int64_t
   return FGPU_OK;
 }
 
+fgpu_status fgpu_graph_search(const float* dq, int nq, const float* d_base, int64_t n, int dim, const int32_t* d_graph,
+                              int degree, int itopk, int width, int max_iter, int k, uint64_t seed, int32_t* d_out_ids,
+                              float* d_out_dists, int32_t* d_iters, int32_t* d_evals, void* stream) {
+  FGPU_CHECK(dq && d_base && d_graph && d_out_ids && d_out_dists, FGPU_ERR_ARG, "graph_search: null argument");
+  FGPU_CHECK(nq >= 0, FGPU_ERR_ARG, "graph_search: nq must be >= 0");
+  FGPU_CHECK(((uintptr_t)d_base & 15) == 0, FGPU_ERR_ARG, "graph_search: base vectors must be 16-byte aligned");
+  GraphArgs a{dq, d_base, (long long)n, d_graph, degree, itopk, width, max_iter, k, seed, 0, nq,
+              d_out_ids, d_out_dists, d_iters, d_evals};
+  return launch_graph_search(dim, a, as_stream(stream));
+}
+
 // ---------------------------------------------------------------------------
 int fgpu_fixed_shift(float maxabs, int64_t n) {
   int e = 0;

@@ -161,6 +161,32 @@ __device__ __forceinline__ void wave_merge_sorted64(float& d, int& id, float cd,
   wave_bitonic_merge64(d, id);
 }
 
+// The same networks carrying an int payload with each (d, id) pair.
+template <int S>
+__device__ __forceinline__ void bitonic_stage_p(float& d, int& id, int& pl, bool up) {
+  const float od = xchg_f<S>(d);
+  const int oi = xchg<S>(id);
+  const int op = xchg<S>(pl);
+  const bool lower = (lane_id() & S) == 0;
+  const bool other_less = lt_pair(od, oi, d, id);
+  const bool take = (lower == up) ? other_less : (!other_less && !(od == d && oi == id));
+  if (take) { d = od; id = oi; pl = op; }
+}
+// list (ascending, with payload) := the 64 smallest of list U cand; cand
+// (ascending) enters with payload cp.
+__device__ __forceinline__ void wave_merge_sorted64_p(float& d, int& id, int& pl, float cd, int ci, int cp) {
+  const float rd = __int_as_float(wave_reverse(__float_as_int(cd)));
+  const int ri = wave_reverse(ci);
+  const int rp = wave_reverse(cp);
+  if (lt_pair(rd, ri, d, id)) { d = rd; id = ri; pl = rp; }
+  bitonic_stage_p<32>(d, id, pl, true);
+  bitonic_stage_p<16>(d, id, pl, true);
+  bitonic_stage_p<8>(d, id, pl, true);
+  bitonic_stage_p<4>(d, id, pl, true);
+  bitonic_stage_p<2>(d, id, pl, true);
+  bitonic_stage_p<1>(d, id, pl, true);
+}
+
 // Insert one (nd, nid) into the ascending list (one pair per lane); the last entry drops off.
 __device__ __forceinline__ void wave_insert64(float& d, int& id, float nd, int nid) {
   const int lane = lane_id();

@@ -1,0 +1,192 @@
+// graph.hip -- graph (CAGRA-style) search over a fixed-degree adjacency array
+// (A19).
+//
+// Reference: search_cagra_index (cagra_adapter.cuh:38-68) calls cuVS CAGRA
+// with an internal top-k list of itopk entries, a search width and a maximum
+// iteration count.  cuVS is not in the repository, so the algorithm here is
+// stated on its own (the oracle restates the same definition):
+//   * 64 seed nodes, node_j = mix64(seed ^ mix64((q << 20) | j)) % n;
+//   * each step expands the `width` best not-yet-expanded entries of the
+//     itopk list and offers their `degree` neighbours;
+//   * a candidate is dropped if its id is outside [0, n) or its bit in the
+//     query's visited bitmap was set before the step (2^16 bits, bit =
+//     (uint32)(id * 2654435761) >> 16; a hash collision drops a node);
+//     duplicates within the step are kept once; then the kept candidates'
+//     bits are set;
+//   * kept candidates get the exact device-form L2 and merge into the list by
+//     (distance, id); the search stops when nothing is left to expand or after
+//     max_iter steps.
+// Reading the bitmap as it was before the step makes the result independent
+// of the order in which lanes set bits.
+//
+// One wave per query, 4 queries per workgroup: the itopk list is one entry per
+// lane (with its expanded flag), the bitmap (8 KB) sits in the wave's LDS, and
+// a step's <= 128 candidates are two per lane.  Every sort and merge is a
+// DPP/permlane bitonic network; there is no workgroup barrier.
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace fgpu {
+namespace {
+
+constexpr int kGW = 4;                  // queries (waves) per workgroup
+constexpr int kBitmapWords = 1 << 11;   // 2^16 bits per query
+constexpr int kMaxWidth = 8;
+
+__device__ __forceinline__ uint64_t gmix64(uint64_t z) {
+  z += 0x9E3779B97F4A7C15ull;
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}
+__device__ __forceinline__ uint32_t graph_bit(int id) { return ((uint32_t)id * 2654435761u) >> 16; }
+
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+template <int D>
+__device__ __forceinline__ float row_l2(const float* __restrict__ qs, const float* __restrict__ row) {
+  const float4* r = reinterpret_cast<const float4*>(row);
+  float acc = 0.0f;
+#pragma unroll 8
+  for (int j = 0; j < D / 4; ++j) {
+    const float4 v = r[j];
+    float df = qs[4 * j] - v.x;
+    acc = __builtin_fmaf(df, df, acc);
+    df = qs[4 * j + 1] - v.y;
+    acc = __builtin_fmaf(df, df, acc);
+    df = qs[4 * j + 2] - v.z;
+    acc = __builtin_fmaf(df, df, acc);
+    df = qs[4 * j + 3] - v.w;
+    acc = __builtin_fmaf(df, df, acc);
+  }
+  return acc;
+}
+
+template <int D>
+__global__ __launch_bounds__(kGW * kWave) void graph_search_kernel(GraphArgs a) {
+  __shared__ uint32_t bm_s[kGW][kBitmapWords];
+  __shared__ __align__(16) float qs_s[kGW][D];
+  __shared__ int par_s[kGW][kMaxWidth];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int qi = blockIdx.x * kGW + wave;
+  if (qi >= a.nq) return;  // the whole wave leaves; the kernel has no workgroup barrier
+  uint32_t* bm = bm_s[wave];
+  float* qs = qs_s[wave];
+  int* par = par_s[wave];
+  for (int i = lane; i < kBitmapWords; i += kWave) bm[i] = 0u;
+  for (int i = lane; i < D; i += kWave) qs[i] = a.queries[(size_t)qi * D + i];
+  wave_lds_sync();
+  const long long n = a.n;
+  const int deg = a.degree, itopk = a.itopk;
+
+  // the itopk list: one entry per lane, ascending; ex = expanded flag
+  float ld = FLT_MAX;
+  int li = kPadId, ex = 0;
+  int nev = 0;  // exact distances computed by this lane
+
+  // One step: candidates c0, c1 (-1 = none) -> visited filter, dedup, exact
+  // distances, merge into the list.
+  auto step = [&](int c0, int c1) {
+    const uint32_t b0 = graph_bit(c0), b1 = graph_bit(c1);
+    const bool v0 = c0 >= 0 && (long long)c0 < n && !((bm[b0 >> 5] >> (b0 & 31)) & 1u);
+    const bool v1 = c1 >= 0 && (long long)c1 < n && !((bm[b1 >> 5] >> (b1 & 31)) & 1u);
+    // sort the 128 candidates by id: keys (0, id), dropped ones (FLT_MAX, pad)
+    float k0 = v0 ? 0.0f : FLT_MAX, k1 = v1 ? 0.0f : FLT_MAX;
+    int i0 = v0 ? c0 : kPadId, i1 = v1 ? c1 : kPadId;
+    wave_sort64(k0, i0);
+    wave_sort64(k1, i1);
+    {  // split into the 64 smallest (i0) and 64 largest (i1), both ascending
+      const float rk = __int_as_float(wave_reverse(__float_as_int(k1)));
+      const int ri = wave_reverse(i1);
+      const bool c_lo = lt_pair(rk, ri, k0, i0);
+      k1 = c_lo ? k0 : rk;
+      i1 = c_lo ? i0 : ri;
+      if (c_lo) { k0 = rk; i0 = ri; }
+      wave_bitonic_merge64(k0, i0);
+      wave_bitonic_merge64(k1, i1);
+    }
+    // keep each id once: drop an entry equal to its predecessor in the 128-sequence
+    const int p0 = dpp_mov<0x138>(i0);  // wave_shr:1
+    int p1 = dpp_mov<0x138>(i1);
+    const int last0 = readlane_i(i0, kWave - 1);
+    if (lane == 0) p1 = last0;
+    if (i0 != kPadId && lane > 0 && i0 == p0) i0 = kPadId;
+    if (i1 != kPadId && i1 == p1) i1 = kPadId;
+    // mark the kept candidates visited (every bitmap read of this step is done)
+    if (i0 != kPadId) { const uint32_t b = graph_bit(i0); atomicOr(&bm[b >> 5], 1u << (b & 31)); }
+    if (i1 != kPadId) { const uint32_t b = graph_bit(i1); atomicOr(&bm[b >> 5], 1u << (b & 31)); }
+    // exact distances
+    float d0 = FLT_MAX, d1 = FLT_MAX;
+    if (i0 != kPadId) { d0 = row_l2<D>(qs, a.base + (size_t)i0 * D); ++nev; }
+    if (i1 != kPadId) { d1 = row_l2<D>(qs, a.base + (size_t)i1 * D); ++nev; }
+    wave_sort64(d0, i0);
+    wave_sort64(d1, i1);
+    wave_merge_sorted64_p(ld, li, ex, d0, i0, 0);
+    wave_merge_sorted64_p(ld, li, ex, d1, i1, 0);
+    if (lane >= itopk) {
+      ld = FLT_MAX;
+      li = kPadId;
+      ex = 0;
+    }
+    wave_lds_sync();
+  };
+
+  const uint64_t qg = (uint64_t)a.q0 + (uint64_t)qi;
+  step((int)(gmix64(a.seed ^ gmix64((qg << 20) | (uint64_t)lane)) % (uint64_t)n), -1);
+  int it = 0;
+  for (; it < a.max_iter; ++it) {
+    uint64_t open = __ballot(li != kPadId && !ex);
+    if (!open) break;
+    int np = 0;
+    for (; np < a.width && open; ++np) {
+      const int L = __ffsll((unsigned long long)open) - 1;
+      open &= open - 1;
+      if (lane == L) ex = 1;
+      const int pid = readlane_i(li, L);
+      if (lane == 0) par[np] = pid;
+    }
+    wave_lds_sync();
+    int c0 = -1, c1 = -1;
+    const int s0 = lane / deg, s1 = (lane + kWave) / deg;
+    if (s0 < np) c0 = a.graph[(size_t)par[s0] * deg + (lane - s0 * deg)];
+    if (s1 < np) c1 = a.graph[(size_t)par[s1] * deg + (lane + kWave - s1 * deg)];
+    wave_lds_sync();
+    step(c0, c1);
+  }
+  if (lane < a.k) {
+    a.out_ids[(size_t)qi * a.k + lane] = li == kPadId ? -1 : li;
+    a.out_d[(size_t)qi * a.k + lane] = li == kPadId ? FLT_MAX : ld;
+  }
+  if (a.iters && lane == 0) a.iters[qi] = it;
+  if (a.evals) {
+    const int tot = wave_sum_i(nev);
+    if (lane == 0) a.evals[qi] = tot;
+  }
+}
+
+template <int D>
+fgpu_status launch_graph_t(const GraphArgs& a, hipStream_t s) {
+  hipLaunchKernelGGL(graph_search_kernel<D>, dim3((unsigned)((a.nq + kGW - 1) / kGW)), dim3(kGW * kWave), 0, s, a);
+  FGPU_HIP(hipGetLastError());
+  return FGPU_OK;
+}
+
+}  // namespace
+
+fgpu_status launch_graph_search(int dim, const GraphArgs& a, hipStream_t s) {
+  FGPU_CHECK(a.n >= 1 && a.n < INT32_MAX, FGPU_ERR_ARG, "graph_search: need 1 <= n < 2^31");
+  FGPU_CHECK(a.degree >= 1 && a.width >= 1 && a.width <= kMaxWidth && a.width * a.degree <= 2 * kWave,
+             FGPU_ERR_UNSUPPORTED, "graph_search: need width <= 8 and width * degree <= 128");
+  FGPU_CHECK(a.itopk >= 1 && a.itopk <= kWave && a.k >= 1 && a.k <= a.itopk && a.max_iter >= 0, FGPU_ERR_UNSUPPORTED,
+             "graph_search: need 1 <= k <= itopk <= 64 and max_iter >= 0");
+  if (a.nq <= 0) return FGPU_OK;
+  if (dim == 128) return launch_graph_t<128>(a, s);
+  if (dim == 96) return launch_graph_t<96>(a, s);
+  return set_error(FGPU_ERR_UNSUPPORTED, "graph_search: dim must be 96 or 128");
+}
+
+}  // namespace fgpu

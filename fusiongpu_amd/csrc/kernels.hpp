@@ -105,6 +105,23 @@ struct RerankArgs {
 };
 fgpu_status launch_rerank(int dim, const RerankArgs& a, hipStream_t s);
 
+// ---- graph.hip -----------------------------------------------------------------
+struct GraphArgs {
+  const float* queries;     // [nq][dim]
+  const float* base;        // [n][dim], 16-byte aligned
+  long long n;
+  const int32_t* graph;     // [n][degree] neighbour ids (ids outside [0, n) are skipped)
+  int degree, itopk, width, max_iter, k;
+  uint64_t seed;
+  int q0;                   // index of the first query (seeds depend on it)
+  int nq;
+  int32_t* out_ids;         // [nq][k]
+  float* out_d;             // [nq][k]
+  int32_t* iters;           // [nq] or nullptr: steps taken
+  int32_t* evals;           // [nq] or nullptr: exact distances computed
+};
+fgpu_status launch_graph_search(int dim, const GraphArgs& a, hipStream_t s);
+
 // ---- build.hip ----------------------------------------------------------------
 fgpu_status launch_probe_counts(const uint32_t* probes, int nq, int nprobe, int nlist, const int32_t* offsets,
                                 int32_t* counts, int32_t* offs, hipStream_t s);

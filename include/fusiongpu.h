@@ -201,6 +201,26 @@ fgpu_status fgpu_knn_exact(const float* d_queries, int nq, const float* d_base, 
                            int32_t* d_ids, float* d_dists, void* d_workspace, size_t workspace_bytes,
                            void* stream);
 
+/* ---- graph search (A19) ------------------------------------------------- */
+
+/* The role of cuVS CAGRA search (cagra_adapter.cuh:38-68: itopk list,
+ * search width, maximum iterations) over a caller-supplied fixed-degree
+ * adjacency d_graph [n][degree] (ids outside [0, n) are skipped) of the base
+ * vectors d_base [n][dim].  cuVS is not in the reference, so the algorithm is
+ * this library's own, deterministic one: 64 seeded start nodes; each step
+ * expands the `width` best unexpanded entries of the itopk list; candidates
+ * whose bit in a per-query 2^16-bit visited bitmap (in LDS) was already set
+ * are dropped; exact squared L2 (sequential fused chain); merge by
+ * (distance, id); stop when nothing is left to expand or after max_iter steps.
+ * Outputs the k best ids/dists [nq][k] and, optionally, d_iters [nq] (steps)
+ * and d_evals [nq] (exact distances computed, i.e. base rows read).
+ * dim 96 or 128, d_base 16-byte aligned, k <= itopk <= 64, width <= 8,
+ * width * degree <= 128. */
+fgpu_status fgpu_graph_search(const float* d_queries, int nq, const float* d_base, int64_t n, int dim,
+                              const int32_t* d_graph, int degree, int itopk, int width, int max_iter, int k,
+                              uint64_t seed, int32_t* d_out_ids, float* d_out_dists, int32_t* d_iters,
+                              int32_t* d_evals, void* stream);
+
 /* ---- index build (A13-A17) -------------------------------------------- */
 
 /* One Lloyd update (kmeans_gpu.cuh:81-116) with deterministic fixed-point

@@ -40,6 +40,8 @@ _SIGS = {
     "orc_search_two_phase": (None, [_vp, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _i32, _vp, _i32, _i32, _i32,
                                     _f32, _i32, _vp, _vp, _vp, _vp, _vp, _i32]),
     "orc_rerank": (None, [_vp, _i32, _i32, _vp, _i64, _vp, _vp, _i32, _i32, _i32, _f32, _i32, _vp, _vp, _vp, _i32]),
+    "orc_graph_search": (None, [_vp, _i32, _vp, _i64, _i32, _vp, _i32, _i32, _i32, _i32, _i32, _u64, _vp, _vp, _vp,
+                                _i32]),
     "orc_kmeans_assign": (None, [_vp, _i64, _vp, _i32, _i32, _vp, _i32]),
     "orc_fixed_shift": (_i32, [_f32, _i64]),
     "orc_kmeans_update": (None, [_vp, _i64, _vp, _i32, _i32, _i32, _i32, _vp, _vp]),
@@ -173,6 +175,23 @@ def knn_exact(q, base, k, nthreads=0):
     od = np.empty((q.shape[0], k), np.float32)
     lib.orc_knn_exact(_p(q), q.shape[0], _p(base), base.shape[0], q.shape[1], k, _p(oid), _p(od), nthreads)
     return oid, od
+
+
+def graph_search(q, base, graph, k, itopk=64, width=4, max_iter=64, seed=1, nthreads=0):
+    """Graph search (own definition, see oracle.cpp): (ids [nq][k], dists [nq][k], steps [nq])."""
+    q, base, graph = f32(q), f32(base), i32(graph)
+    nq, dim = q.shape
+    oid = np.empty((nq, k), np.int32)
+    od = np.empty((nq, k), np.float32)
+    it = np.empty(nq, np.int32)
+    lib.orc_graph_search(_p(q), nq, _p(base), base.shape[0], dim, _p(graph), graph.shape[1], itopk, width, max_iter,
+                         k, seed, _p(oid), _p(od), _p(it), nthreads)
+    return oid, od, it
+
+
+def graph_bit(node):
+    """The visited-bitmap bit of a node id (2^16-bit bitmap, multiplicative hash)."""
+    return ((int(node) * 2654435761) & 0xFFFFFFFF) >> 16
 
 
 def kmeans_assign(x, cent, nthreads=0):

@@ -41,6 +41,9 @@
 //   orc_pq_encode(device) brute-force argmin of the fused chain
 //   orc_build_lists       round trip with the ivf_data.bin writer layout
 //   orc_knn_exact         brute force, tie rule
+//   orc_graph_search      own definition (cuVS absent): complete graphs reduce
+//                         it to exact kNN; a hand-built path graph fixes the
+//                         step count; a planted bitmap collision drops a node
 //   orc_gen_gmm           no reference counterpart: the synthetic workload
 //                         generator; pinned by moments and determinism
 #include <algorithm>
@@ -425,6 +428,82 @@ void orc_rerank(const float* q, int nq, int dim, const float* base, long long n,
         out_dists[(size_t)i * k + j] = pad ? FLT_MAX : top[j].first;
       }
       if (visited) visited[i] = seen;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// A19: graph (CAGRA-style) search.  The reference calls cuVS CAGRA
+// (cagra_adapter.cuh:38-68: itopk, search width, max iterations), whose
+// algorithm is not in the repository, so this is a stated definition, not a
+// restatement:
+//   * 64 seed nodes, node_j = mix64(seed ^ mix64((q << 20) | j)) % n, with q
+//     the query's index;
+//   * each step takes the `width` best entries of the itopk list not yet
+//     expanded (in list order), marks them expanded, and offers their
+//     `degree` neighbours graph[p][0..degree) as candidates;
+//   * a candidate is dropped if its id is outside [0, n) or if its bit in the
+//     query's visited bitmap (2^16 bits, bit = (uint32)(id * 2654435761) >> 16)
+//     was set before the step (hash collisions drop a node: the bitmap is
+//     approximate by design); duplicates within the step are kept once; then
+//     the bits of the kept candidates are set;
+//   * kept candidates get the exact device-form L2 and are merged into the
+//     itopk list by (distance, id), which keeps its itopk best;
+//   * the search stops when no entry is left to expand or after max_iter
+//     steps; the first k entries are the answer (pad -1 / FLT_MAX).
+// iters ([nq], optional) = steps taken.
+static inline uint32_t graph_bit(int id) { return (uint32_t)((uint32_t)id * 2654435761u) >> 16; }
+
+void orc_graph_search(const float* q, int nq, const float* base, long long n, int dim, const int* graph,
+                      int degree, int itopk, int width, int max_iter, int k, unsigned long long seed,
+                      int* out_ids, float* out_dists, int* iters, int nthreads) {
+  set_threads(nthreads);
+#pragma omp parallel
+  {
+    std::vector<uint8_t> bits(1 << 16);
+    struct E { float d; int id; bool ex; };
+    std::vector<E> list, add;
+    std::vector<int> cand, keep;
+#pragma omp for schedule(dynamic, 4)
+    for (int i = 0; i < nq; ++i) {
+      const float* qi = q + (size_t)i * dim;
+      std::fill(bits.begin(), bits.end(), 0);
+      list.clear();
+      auto step = [&]() {
+        keep.clear();
+        for (int c : cand)
+          if (c >= 0 && (long long)c < n && !bits[graph_bit(c)]) keep.push_back(c);
+        std::sort(keep.begin(), keep.end());
+        keep.erase(std::unique(keep.begin(), keep.end()), keep.end());
+        for (int c : keep) bits[graph_bit(c)] = 1;
+        for (int c : keep) list.push_back({l2_fma(qi, base + (size_t)c * dim, dim), c, false});
+        std::sort(list.begin(), list.end(), [](const E& x, const E& y) { return lt_pair(x.d, x.id, y.d, y.id); });
+        if ((int)list.size() > itopk) list.resize(itopk);
+      };
+      cand.clear();
+      for (int j = 0; j < 64; ++j)
+        cand.push_back((int)(mix64(seed ^ mix64(((uint64_t)i << 20) | (uint64_t)j)) % (uint64_t)n));
+      step();
+      int it = 0;
+      for (; it < max_iter; ++it) {
+        cand.clear();
+        int taken = 0;
+        for (auto& e : list) {
+          if (taken == width) break;
+          if (e.ex) continue;
+          e.ex = true;
+          ++taken;
+          for (int j = 0; j < degree; ++j) cand.push_back(graph[(size_t)e.id * degree + j]);
+        }
+        if (taken == 0) break;
+        step();
+      }
+      for (int j = 0; j < k; ++j) {
+        const bool real = j < (int)list.size();
+        out_ids[(size_t)i * k + j] = real ? list[j].id : -1;
+        out_dists[(size_t)i * k + j] = real ? list[j].d : FLT_MAX;
+      }
+      if (iters) iters[i] = it;
     }
   }
 }
