@@ -14,7 +14,7 @@ kernel, the ADC scan: algorithmic bytes = sum over (query, probe) of
 list_len * M code bytes, divided by the scan kernel's average duration from HIP
 events recorded on the stream it runs on.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--cpu-queries N] [--workload c2|c3]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--cpu-queries N] [--workload c2|c3|c5]
 
 --workload c3 prints a supplementary line for BASELINE config 3 instead: 10M x
 96 fp32 (1024-component mixture, per-component sigma U[0.05, 0.15]), 4096
@@ -23,6 +23,13 @@ limit_k 50, threshold_coeff 1.0) compacted to the top 1000 candidates, then the
 early-stopping exact rerank (mini-batch 128, eps 0.1, beta 2) to k=100.  Its
 index is built in-run too (k-means on a 1M-row sample, then every row
 assigned), not timed.
+
+--workload c5 prints a supplementary line for BASELINE config 5: graph search
+over 5M x 128 fp32 (256-component mixture) with a fixed out-degree-32 graph,
+10k queries, itopk 64, search width 4, at most 64 steps, k=10.  The graph is
+built in-run, untimed: each base vector's nearest other vectors by this
+framework's IVF-PQ search (2048 lists, M=32, nprobe 8, ADC top-64 reranked
+exactly), optionally with seeded random long-range edges.
 """
 import argparse
 import json
@@ -65,7 +72,10 @@ def main():
     ap.add_argument("--n", type=int, default=1_000_000)
     ap.add_argument("--nq", type=int, default=10_000)
     ap.add_argument("--copy-probe", action="store_true", help="also run a 1 GiB device copy (PMC calibration)")
-    ap.add_argument("--workload", choices=["c2", "c3"], default="c2")
+    ap.add_argument("--workload", choices=["c2", "c3", "c5"], default="c2")
+    ap.add_argument("--c5-components", type=int, default=256, help="mixture components of the C5 data")
+    ap.add_argument("--c5-random-edges", type=int, default=4,
+                    help="C5: out-edges per vector replaced by seeded random long-range edges")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build targets one GPU; --gpus {args.gpus} is not supported "
@@ -80,6 +90,8 @@ def main():
     torch.cuda.set_device(dev)
     if args.workload == "c3":
         return run_c3(args, torch, fg, dev)
+    if args.workload == "c5":
+        return run_c5(args, torch, fg, dev)
     dim, nlist, m, nprobe, k = 128, 1024, 32, 32, 10
     t0 = time.time()
     x = fg.gen_gmm(args.n, dim, 256, seed=2024, set=0, sig_lo=0.08)
@@ -335,6 +347,114 @@ def run_c3(args, torch, fg, dev):
                       "candidates_per_query": round(tc.float().mean().item(), 1)},
         "cpu_baseline": cpu, "parity": parity, "recall_at_k": recall,
         "ground_truth": {"seconds": round(gt_s, 3), "oracle_parity_50": gt_parity},
+    }
+    print(json.dumps(res), flush=True)
+
+
+def run_c5(args, torch, fg, dev):
+    """graph search, itopk 64, width 4, <= 64 steps, k=10."""
+    dim, degree, itopk, width, max_iter, k = 128, 32, 64, 4, 64, 10
+    n = args.n if args.n != 1_000_000 else 5_000_000
+    nq = args.nq
+    t0 = time.time()
+    ncomp, nrand = args.c5_components, args.c5_random_edges
+    x = fg.gen_gmm(n, dim, ncomp, seed=2026, set=0, sig_lo=0.05, sig_hi=0.15)
+    q = fg.gen_gmm(nq, dim, ncomp, seed=2026, set=1, sig_lo=0.05, sig_hi=0.15)
+    log(f"generated {n}x{dim} base + {nq} queries in {time.time() - t0:.1f}s")
+    t0 = time.time()
+    dx = torch.from_numpy(x).to(dev)
+    offs, ids, codes, cent, cb = fg.build_ivfpq(dx, 2048, 32, kmeans_iters=10, init_mode=1, seed=7, pq_iters=8,
+                                                sample_size=50000, train_rows=min(n, 1_000_000))
+    idx = fg.Index.from_arrays(dim, 32, offs, ids, codes, cent, cb)
+    graph = torch.empty((n, degree), dtype=torch.int32, device=dev)
+    B = 1 << 18
+    sws = torch.empty(idx.search_workspace_bytes(B, 8), dtype=torch.uint8, device=dev)
+    cnt64 = torch.full((B,), 64, dtype=torch.int32, device=dev)
+    for b0 in range(0, n, B):
+        nb = min(B, n - b0)
+        # ADC top-64, then the exact top-(degree+1) among them (eps < 0: every candidate is evaluated)
+        aid, _ = idx.search(dx[b0:b0 + nb], 8, 64, workspace=sws)
+        gid, _, _ = fg.rerank(dx[b0:b0 + nb], dx, aid, cnt64[:nb], degree + 1, 64, -1.0, 2)
+        rows = torch.arange(b0, b0 + nb, device=dev, dtype=torch.int32)[:, None]
+        drop = (gid == rows) | (gid < 0)
+        order = torch.argsort(drop.to(torch.int8), dim=1, stable=True)[:, :degree]
+        graph[b0:b0 + nb] = torch.gather(gid, 1, order)
+    if nrand > 0:
+        # seeded long-range edges in the last nrand slots (a counter-based hash of (row, slot))
+        r = torch.arange(n, device=dev, dtype=torch.int64)[:, None] * 1000003 + torch.arange(
+            nrand, device=dev, dtype=torch.int64)[None, :] * 7919 + 12345
+        r = (r * 6364136223846793005 + 1442695040888963407) & ((1 << 62) - 1)
+        graph[:, degree - nrand:] = ((r >> 17) % n).to(torch.int32)
+    idx.close()
+    torch.cuda.synchronize()
+    log(f"index + degree-{degree} graph built on GPU in {time.time() - t0:.1f}s")
+    dq = torch.from_numpy(q).to(dev)
+    out = (torch.empty((nq, k), dtype=torch.int32, device=dev), torch.empty((nq, k), dtype=torch.float32, device=dev))
+    stream = torch.cuda.current_stream()
+
+    def step():
+        fg.graph_search(dq, dx, graph, k, itopk, width, max_iter, seed=1, out=out)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_per_step = 1e3 * wall / args.steps
+    qps = nq / (wall / args.steps)
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+    ev[0].record(stream)
+    step()
+    ev[1].record(stream)
+    torch.cuda.synchronize()
+    kern_ms = ev[0].elapsed_time(ev[1])
+    gid_t, gd_t, it_t, evals = fg.graph_search(dq, dx, graph, k, itopk, width, max_iter, seed=1, want_evals=True)
+    assert torch.equal(gid_t, out[0]) and torch.equal(gd_t, out[1]), "instrumented search differs"
+    n_evals = int(evals.to(torch.int64).sum().item())
+    n_steps = int(it_t.to(torch.int64).sum().item())
+    gather_bytes = n_evals * dim * 4 + n_steps * width * degree * 4
+    gbs = gather_bytes / (kern_ms * 1e-3) / 1e9
+    log(f"graph search: {ms_per_step:.3f} ms/step, {qps:,.0f} QPS; kernel {kern_ms:.3f} ms; {n_steps / nq:.1f} steps "
+        f"and {n_evals / nq:.0f} distance evaluations per query -> {gather_bytes / 1e9:.2f} GB = {gbs:.0f} GB/s")
+    gid, gd = out[0].cpu().numpy(), out[1].cpu().numpy()
+    gt, _ = fg.knn_exact(dq, dx, k)
+    gt = gt.cpu().numpy()
+    recall = float(np.mean([len(set(gid[i]) & set(gt[i])) / k for i in range(nq)]))
+    log(f"recall@{k} {recall:.4f} against exact kNN")
+
+    cpu = parity = None
+    if args.cpu_queries > 0:
+        import oracle
+        ns = min(args.cpu_queries, nq, 1000)
+        threads = oracle.lib.orc_max_threads()
+        hgraph = graph.cpu().numpy()
+        t0 = time.perf_counter()
+        oid, od, _ = oracle.graph_search(q[:ns], x, hgraph, k, itopk, width, max_iter, seed=1)
+        cpu_s = time.perf_counter() - t0
+        cpu = {"value": round(ns / cpu_s, 1), "unit": "queries/s", "cores": threads, "kind": "port",
+               "sample": f"first {ns} of the {nq} queries, same graph, {cpu_s:.1f}s wall on {threads} OpenMP threads"}
+        parity = {"queries": ns, "ids_equal": bool(np.array_equal(gid[:ns], oid)),
+                  "dists_bit_equal": bool(np.array_equal(gd[:ns].view(np.uint32), od.view(np.uint32)))}
+        log(f"cpu baseline {cpu['value']} QPS on {threads} threads; parity {parity}")
+    res = {
+        "metric": "QPS, graph search over 5M x 128 (degree 32, itopk 64, width 4, <= 64 steps), k=10 (1 GPU)",
+        "value": round(qps, 1), "unit": "queries/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32",
+        "data": f"synthetic: seeded {ncomp}-component Gaussian mixture; graph = each vector's {degree - nrand} nearest "
+                f"by this framework's IVF-PQ search (ADC top-64, exact rerank) + {nrand} seeded random edges",
+        "config": {"workload": "BASELINE config 5: 5M x 128 fp32, out-degree-32 graph, 10k queries, itopk 64, "
+                               "width 4, max 64 steps, k=10",
+                   "n": n, "dim": dim, "degree": degree, "nq": nq, "itopk": itopk, "width": width,
+                   "max_iter": max_iter, "k": k},
+        "roofline": {"bound": "hbm", "kernel": "graph_search_kernel<128>", "achieved": round(gbs, 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "algorithmic_bytes_per_launch": gather_bytes, "avg_launch_ms": round(kern_ms, 4),
+                     "distance_evaluations": n_evals, "steps": n_steps},
+        "cpu_baseline": cpu, "parity": parity, "recall_at_k": recall,
     }
     print(json.dumps(res), flush=True)
 
