@@ -1,0 +1,248 @@
+// search_pipeline -- search command, drop-in for the reference's
+// search_pipeline (search_pipeline.cu:559-648):
+//   search_pipeline <base> <query> [gt] [-b batch] [-m top_m] [-r rerank_m]
+//     [-mb mini_batch] [-e epsilon] [--beta b] [-p prune_ratio] [-s streams]
+//     [-k topk] [--p1_lists n] [--limit_k n] [--threshold_coeff c]
+//     [--pq_m M] [--res DIR] [--out ids.ivecs]
+// It loads <res>/ivf_data.bin + global_pq_codebook.bin, keeps the base
+// vectors in HBM for the exact rerank, runs the query batches through S
+// streams round-robin (search_pipeline.cu:168-214, 311-377) and prints the
+// reference's "Total time ... QPS" and "Recall@1/@10" lines plus a per-stage
+// timing table.
+//
+// Per batch, on its stream: queries H2D from pinned memory, the exact coarse
+// step, the two-phase scan + top-rerank_m, the exact rerank, results D2H into
+// pinned memory.  The stream's contexts are reused round-robin; a context's
+// results and stage times are collected when it is reused or at the end
+// (the reference hands that to a worker thread, search_pipeline.cu:392-478).
+// No call inside a batch synchronises the host.
+#include <algorithm>
+#include <chrono>
+#include <cstring>
+#include <iomanip>
+#include <iostream>
+#include <unordered_set>
+
+#include "app_common.hpp"
+
+using app::hip_ok;
+using app::ok;
+
+namespace {
+
+struct Ctx {
+  hipStream_t s = nullptr;
+  hipEvent_t ev[6] = {};  // begin, after H2D, after coarse, after scan, after rerank, after D2H
+  float* h_q = nullptr;   // pinned
+  int32_t* h_ids = nullptr;
+  float* d_q = nullptr;
+  uint32_t* d_probes = nullptr;
+  float* d_pd = nullptr;
+  int32_t* d_tid = nullptr;
+  float* d_td = nullptr;
+  int32_t* d_tcnt = nullptr;
+  int32_t* d_ids = nullptr;
+  float* d_d = nullptr;
+  void* d_ws = nullptr;
+  size_t ws_bytes = 0;
+  int start = -1, size = 0;
+};
+
+// The reference's recall (search_pipeline.cu:531-557): the whole gt row is the
+// hit set, repeated predicted ids count once, hits / (nq * recall_k).
+float compute_recall(const std::vector<int32_t>& res, int k, const std::vector<int32_t>& gt, int gt_k, int nq,
+                     int recall_k) {
+  long long hits = 0;
+  for (int i = 0; i < nq; ++i) {
+    std::unordered_set<int> gset(gt.begin() + (size_t)i * gt_k, gt.begin() + (size_t)(i + 1) * gt_k);
+    std::unordered_set<int> seen;
+    const int check = std::min(recall_k, k);
+    for (int j = 0; j < check; ++j) {
+      const int p = res[(size_t)i * k + j];
+      if (seen.insert(p).second && gset.count(p)) ++hits;
+    }
+  }
+  return (float)hits / ((float)nq * recall_k);
+}
+
+}  // namespace
+
+int main(int argc, char** argv) {
+  std::string base_path, query_path, gt_path, res = "../res", out_path;
+  int batch = 128, top_m = 20, rerank_m = 10000, mb = 128, beta = 2, streams = 2, final_k = 10, p1_lists = 12,
+      limit_k = 50, pq_m = 32;
+  float eps = 0.1f, prune_ratio = 100.0f, coeff = 1.0f;
+  for (int i = 1; i < argc; ++i) {
+    const std::string a = argv[i];
+    auto next = [&]() -> const char* {
+      if (i + 1 >= argc) { std::cerr << "missing value for " << a << "\n"; std::exit(1); }
+      return argv[++i];
+    };
+    if (a == "-b" || a == "--batch_size") batch = std::atoi(next());
+    else if (a == "-m" || a == "--top_m") top_m = std::atoi(next());
+    else if (a == "-r" || a == "--rerank_m") rerank_m = std::atoi(next());
+    else if (a == "-mb" || a == "--mini_batch") mb = std::atoi(next());
+    else if (a == "-e" || a == "--epsilon") eps = (float)std::atof(next());
+    else if (a == "--beta") beta = std::atoi(next());
+    else if (a == "-p" || a == "--prune") prune_ratio = (float)std::atof(next());
+    else if (a == "-s" || a == "--streams") streams = std::atoi(next());
+    else if (a == "-k" || a == "--topk") final_k = std::atoi(next());
+    else if (a == "--p1_lists") p1_lists = std::atoi(next());
+    else if (a == "--limit_k") limit_k = std::atoi(next());
+    else if (a == "--threshold_coeff") coeff = (float)std::atof(next());
+    else if (a == "--pq_m") pq_m = std::atoi(next());
+    else if (a == "--res") res = next();
+    else if (a == "--out") out_path = next();
+    else if (!a.empty() && a[0] != '-') {
+      if (base_path.empty()) base_path = a;
+      else if (query_path.empty()) query_path = a;
+      else if (gt_path.empty()) gt_path = a;
+    } else { std::cerr << "unknown argument " << a << "\n"; return 1; }
+  }
+  if (base_path.empty() || query_path.empty()) {
+    std::cerr << "Usage: ./search_pipeline <base> <query> [gt] [Options]\n";
+    return 1;
+  }
+  if (rerank_m > 4096) {
+    std::cerr << "note: rerank_m " << rerank_m << " exceeds this library's 4096; using 4096\n";
+    rerank_m = 4096;
+  }
+  if (batch < 1 || streams < 1) { std::cerr << "batch and streams must be >= 1\n"; return 1; }
+  const int dim = app::fvecs_dim(base_path);
+  int64_t n = 0, nq64 = 0;
+  std::vector<float> raw = app::read_fvecs(base_path, dim, n);
+  std::vector<float> all_q = app::read_fvecs(query_path, dim, nq64);
+  const int nq = (int)nq64;
+  fgpu_index* idx = nullptr;
+  ok(fgpu_index_load((res + "/ivf_data.bin").c_str(), (res + "/global_pq_codebook.bin").c_str(), dim, pq_m, &idx),
+     "loading the index");
+  fgpu_index_info info;
+  ok(fgpu_index_get_info(idx, &info), "index info");
+  top_m = std::min(top_m, info.nlist);
+  float* d_base = nullptr;
+  hip_ok(hipMalloc(&d_base, sizeof(float) * raw.size()), "hipMalloc base");
+  hip_ok(hipMemcpy(d_base, raw.data(), sizeof(float) * raw.size(), hipMemcpyHostToDevice), "copy base");
+
+  std::vector<Ctx> ctx(streams);
+  const size_t ws = std::max(fgpu_coarse_workspace_bytes(batch, info.nlist),
+                             fgpu_two_phase_workspace_bytes(batch, top_m, p1_lists, limit_k, rerank_m));
+  for (auto& c : ctx) {
+    hip_ok(hipStreamCreate(&c.s), "stream");
+    for (auto& e : c.ev) hip_ok(hipEventCreate(&e), "event");
+    hip_ok(hipHostMalloc((void**)&c.h_q, sizeof(float) * batch * dim, hipHostMallocDefault), "pinned queries");
+    hip_ok(hipHostMalloc((void**)&c.h_ids, sizeof(int32_t) * batch * final_k, hipHostMallocDefault), "pinned ids");
+    hip_ok(hipMalloc(&c.d_q, sizeof(float) * batch * dim), "hipMalloc");
+    hip_ok(hipMalloc(&c.d_probes, sizeof(uint32_t) * batch * top_m), "hipMalloc");
+    hip_ok(hipMalloc(&c.d_pd, sizeof(float) * batch * top_m), "hipMalloc");
+    hip_ok(hipMalloc(&c.d_tid, sizeof(int32_t) * batch * rerank_m), "hipMalloc");
+    hip_ok(hipMalloc(&c.d_td, sizeof(float) * batch * rerank_m), "hipMalloc");
+    hip_ok(hipMalloc(&c.d_tcnt, sizeof(int32_t) * batch), "hipMalloc");
+    hip_ok(hipMalloc(&c.d_ids, sizeof(int32_t) * batch * final_k), "hipMalloc");
+    hip_ok(hipMalloc(&c.d_d, sizeof(float) * batch * final_k), "hipMalloc");
+    hip_ok(hipMalloc(&c.d_ws, ws), "hipMalloc workspace");
+    c.ws_bytes = ws;
+  }
+  std::vector<int32_t> results((size_t)nq * final_k, -1);
+  double t_stage[5] = {0, 0, 0, 0, 0};  // H2D, coarse, scan, rerank, D2H (ms summed over batches)
+  int batches_done = 0;
+  bool keep = false;
+
+  auto collect = [&](Ctx& c) {
+    if (c.start < 0) return;
+    hip_ok(hipEventSynchronize(c.ev[5]), "event sync");
+    if (keep) {
+      std::memcpy(results.data() + (size_t)c.start * final_k, c.h_ids, sizeof(int32_t) * c.size * final_k);
+      for (int j = 0; j < 5; ++j) {
+        float ms = 0.0f;
+        hip_ok(hipEventElapsedTime(&ms, c.ev[j], c.ev[j + 1]), "elapsed");
+        t_stage[j] += ms;
+      }
+      ++batches_done;
+    }
+    c.start = -1;
+  };
+  auto submit = [&](int b, int start, int size) {
+    Ctx& c = ctx[b % streams];
+    collect(c);
+    std::memcpy(c.h_q, all_q.data() + (size_t)start * dim, sizeof(float) * size * dim);
+    hip_ok(hipEventRecord(c.ev[0], c.s), "record");
+    hip_ok(hipMemcpyAsync(c.d_q, c.h_q, sizeof(float) * size * dim, hipMemcpyHostToDevice, c.s), "H2D");
+    hip_ok(hipEventRecord(c.ev[1], c.s), "record");
+    ok(fgpu_coarse_search(idx, c.d_q, size, top_m, prune_ratio, c.d_probes, c.d_pd, c.d_ws, c.ws_bytes, c.s),
+       "coarse search");
+    hip_ok(hipEventRecord(c.ev[2], c.s), "record");
+    ok(fgpu_two_phase_search(idx, c.d_q, size, c.d_probes, top_m, p1_lists, limit_k, coeff, rerank_m, c.d_tid, c.d_td,
+                             c.d_tcnt, nullptr, nullptr, c.d_ws, c.ws_bytes, c.s),
+       "two-phase scan");
+    hip_ok(hipEventRecord(c.ev[3], c.s), "record");
+    ok(fgpu_rerank(c.d_q, size, dim, d_base, n, c.d_tid, c.d_tcnt, rerank_m, final_k, mb, eps, beta, c.d_ids, c.d_d,
+                   nullptr, c.s),
+       "rerank");
+    hip_ok(hipEventRecord(c.ev[4], c.s), "record");
+    hip_ok(hipMemcpyAsync(c.h_ids, c.d_ids, sizeof(int32_t) * size * final_k, hipMemcpyDeviceToHost, c.s), "D2H");
+    hip_ok(hipEventRecord(c.ev[5], c.s), "record");
+    c.start = start;
+    c.size = size;
+  };
+  auto drain = [&]() {
+    for (auto& c : ctx) collect(c);
+  };
+
+  // warm-up: one batch per stream (search_pipeline.cu:611-617)
+  for (int i = 0; i < streams; ++i) submit(i, 0, std::min(nq, batch));
+  drain();
+  keep = true;
+  const auto t0 = std::chrono::high_resolution_clock::now();
+  const int nb = (nq + batch - 1) / batch;
+  for (int b = 0; b < nb; ++b) submit(b, b * batch, std::min(batch, nq - b * batch));
+  drain();
+  const auto t1 = std::chrono::high_resolution_clock::now();
+  const double ms = std::chrono::duration<double, std::milli>(t1 - t0).count();
+  std::cout << "\nTotal time: " << ms << " ms, QPS: " << nq / (ms / 1000.0) << std::endl;
+  std::cout << "\n============= Pipeline Timing Breakdown =============\n" << std::fixed << std::setprecision(3);
+  const char* names[5] = {"H2D:          ", "Coarse:       ", "Scan (PQ):    ", "Rerank (GPU): ", "D2H:          "};
+  double sum = 0;
+  for (int j = 0; j < 5; ++j) {
+    const double avg = batches_done ? t_stage[j] / batches_done : 0.0;
+    sum += avg;
+    std::cout << "  " << names[j] << std::setw(8) << avg << " ms\n";
+  }
+  std::cout << "  -----------------------------------------\n";
+  std::cout << "  Sum of stages:" << std::setw(8) << sum << " ms\n";
+  std::cout << "  batch count:  " << batches_done << "\n";
+  std::cout << "=====================================================\n";
+  std::cout.unsetf(std::ios::fixed);
+  std::cout << std::setprecision(6);
+  if (!out_path.empty()) {  // the result ids as ivecs (one row of final_k per query)
+    FILE* f = std::fopen(out_path.c_str(), "wb");
+    if (!f) { std::cerr << "cannot create " << out_path << "\n"; return 1; }
+    for (int i = 0; i < nq; ++i) {
+      std::fwrite(&final_k, 4, 1, f);
+      std::fwrite(results.data() + (size_t)i * final_k, 4, final_k, f);
+    }
+    std::fclose(f);
+  }
+  if (!gt_path.empty()) {
+    int gt_k = 0;
+    int64_t gn = 0;
+    ok(fgpu_read_ivecs(gt_path.c_str(), &gt_k, &gn, nullptr), "reading ground truth");
+    std::vector<int32_t> gt((size_t)gn * gt_k);
+    ok(fgpu_read_ivecs(gt_path.c_str(), &gt_k, &gn, gt.data()), "reading ground truth");
+    if (gn < nq) { std::cerr << "ground truth has fewer rows than queries\n"; return 1; }
+    const float r1 = compute_recall(results, final_k, gt, gt_k, nq, 1);
+    const float r10 = compute_recall(results, final_k, gt, gt_k, nq, 10);
+    std::cout << "Recall@1: " << r1 * 100 << "%, Recall@10: " << r10 * 100 << "%" << std::endl;
+  }
+  for (auto& c : ctx) {
+    (void)hipStreamDestroy(c.s);
+    for (auto& e : c.ev) (void)hipEventDestroy(e);
+    (void)hipHostFree(c.h_q);
+    (void)hipHostFree(c.h_ids);
+    for (void* p : {(void*)c.d_q, (void*)c.d_probes, (void*)c.d_pd, (void*)c.d_tid, (void*)c.d_td, (void*)c.d_tcnt,
+                    (void*)c.d_ids, (void*)c.d_d, c.d_ws})
+      (void)hipFree(p);
+  }
+  (void)hipFree(d_base);
+  fgpu_index_destroy(idx);
+  return 0;
+}

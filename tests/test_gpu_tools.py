@@ -1,0 +1,119 @@
+"""The command-line tools on the GPU: build_global writes the same index files
+as the library build, its rebalancing keeps the reference's split invariants
+(build_global.cu:62-169), and search_pipeline returns the library path's ids
+and the reference's recall figures (search_pipeline.cu:531-557, 636-645)."""
+import os
+import re
+import subprocess
+import sys
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+if not torch.cuda.is_available():
+    pytest.skip("no HIP device", allow_module_level=True)
+
+import fusiongpu_amd as fg  # noqa: E402
+import oracle  # noqa: E402
+
+BIN = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "fusiongpu_amd", "_lib", "bin")
+
+
+def _say(msg):
+    print(f"[gpu-case] {msg}", flush=True)
+    sys.stdout.flush()
+
+
+def _run(*args, cwd):
+    r = subprocess.run([os.path.join(BIN, args[0]), *map(str, args[1:])], capture_output=True, text=True,
+                       timeout=120, cwd=cwd)
+    assert r.returncode == 0, r.stdout[-2000:] + r.stderr[-2000:]
+    return r.stdout
+
+
+def _write_ivecs(path, ids):
+    ids = np.ascontiguousarray(ids, np.int32)
+    rows = np.concatenate([np.full((ids.shape[0], 1), ids.shape[1], np.int32), ids], 1)
+    rows.tofile(path)
+
+
+def _read_ivecs(path):
+    a = np.fromfile(path, np.int32)
+    k = a[0]
+    return a.reshape(-1, k + 1)[:, 1:]
+
+
+def _build(tmp_path, x, extra):
+    res = tmp_path / "res"
+    res.mkdir(exist_ok=True)
+    fg.write_fvecs(tmp_path / "base.fvecs", x)
+    out = _run("build_global", tmp_path / "base.fvecs", "--res", res, *extra, cwd=tmp_path)
+    return res, out
+
+
+def test_build_global_matches_library_build(tmp_path):
+    _say("build_global --no-rebalance vs library build")
+    x = oracle.gen_gmm(20000, 128, 32, seed=3, sig_lo=0.1)
+    res, _ = _build(tmp_path, x, ["--nlist", 64, "--iters", 5, "--pq_iters", 3, "--sample", 5000, "--no-rebalance"])
+    offs, ids, codes, cent = fg.read_ivf_data(res / "ivf_data.bin", 32, 128)
+    cb = np.fromfile(res / "global_pq_codebook.bin", np.float32).reshape(32, 256, 4)
+    want = fg.build_ivfpq(torch.from_numpy(x).cuda(), 64, 32, kmeans_iters=5, init_mode=0, seed=42, pq_iters=3,
+                          sample_size=5000)
+    for g, w, name in zip((offs, ids, codes, cent, cb), want, ["offsets", "ids", "codes", "centroids", "codebook"]):
+        assert np.array_equal(np.asarray(g).view(np.uint8), np.asarray(w).view(np.uint8)), name
+    csv = np.loadtxt(tmp_path / "cluster_distribution.csv", delimiter=",", skiprows=1, dtype=np.int64)
+    assert np.array_equal(csv[:, 1], np.diff(offs))
+
+
+def test_build_global_rebalances_oversized_lists(tmp_path):
+    _say("build_global rebalancing")
+    x = oracle.gen_gmm(30000, 128, 6, seed=4, sig_lo=0.05, sig_hi=0.3)
+    res, out = _build(tmp_path, x, ["--nlist", 64, "--iters", 4, "--pq_iters", 2, "--sample", 3000])
+    m = re.search(r"Cluster Count: 64 -> (\d+)", out)
+    assert m and "Split Ops" in out
+    offs, ids, codes, cent = fg.read_ivf_data(res / "ivf_data.bin", 32, 128)
+    L = int(m.group(1))
+    assert offs.shape[0] == L + 1 and offs[0] == 0 and offs[-1] == 30000 and np.all(np.diff(offs) > 0)
+    assert np.array_equal(np.sort(ids), np.arange(30000))
+    sizes = np.diff(offs)
+    thr = int(30000 / 64 * 2)
+    assert np.all((sizes <= thr) | (sizes < 32)), sizes.max()
+    # the codes are the device-form encoding of each vector against its list's centroid
+    cb = np.fromfile(res / "global_pq_codebook.bin", np.float32).reshape(32, 256, 4)
+    assign = np.empty(30000, np.int32)
+    assign[ids] = np.repeat(np.arange(L, dtype=np.int32), sizes)
+    assert np.array_equal(codes, oracle.pq_encode(x, assign, cent, cb, fma_mode=1)[ids])
+    idx = fg.Index.load(res / "ivf_data.bin", res / "global_pq_codebook.bin", 128, 32)
+    assert idx.nlist == L
+    idx.close()
+
+
+def test_search_pipeline_matches_library_path(tmp_path):
+    _say("search_pipeline vs library path")
+    x = oracle.gen_gmm(20000, 128, 32, seed=5, sig_lo=0.1)
+    q = oracle.gen_gmm(300, 128, 32, seed=5, set=1, sig_lo=0.1)
+    res, _ = _build(tmp_path, x, ["--nlist", 64, "--iters", 5, "--pq_iters", 3, "--sample", 5000, "--no-rebalance"])
+    fg.write_fvecs(tmp_path / "q.fvecs", q)
+    gt, _ = oracle.knn_exact(q, x, 20)
+    _write_ivecs(tmp_path / "gt.ivecs", gt)
+    out = _run("search_pipeline", tmp_path / "base.fvecs", tmp_path / "q.fvecs", tmp_path / "gt.ivecs", "-b", 128,
+               "-m", 16, "-r", 500, "-k", 10, "--p1_lists", 4, "--limit_k", 30, "-s", 3, "--res", res, "--out",
+               tmp_path / "out.ivecs", cwd=tmp_path)
+    assert re.search(r"Total time: [\d.]+ ms, QPS: [\d.e+]+", out)
+    got = _read_ivecs(tmp_path / "out.ivecs")
+    idx = fg.Index.load(res / "ivf_data.bin", res / "global_pq_codebook.bin", 128, 32)
+    dq, dx = torch.from_numpy(q).cuda(), torch.from_numpy(x).cuda()
+    pid, _ = idx.coarse_search(dq, 16, 100.0)
+    tid, td, tc, _, _ = idx.two_phase_search(dq, pid, 4, 30, 1.0, 500)
+    want, _, _ = fg.rerank(dq, dx, tid, tc, 10, 128, 0.1, 2)
+    assert np.array_equal(got, want.cpu().numpy())
+    idx.close()
+    # the reference's recall: whole gt row as the hit set, repeated ids once, hits / (nq * k)
+    m = re.search(r"Recall@1: ([\d.]+)%, Recall@10: ([\d.]+)%", out)
+    assert m
+    for k, printed in ((1, float(m.group(1))), (10, float(m.group(2)))):
+        hits = sum(len(set(got[i, :k]) & set(gt[i])) for i in range(q.shape[0]))
+        assert abs(100.0 * hits / (q.shape[0] * k) - printed) < 1e-3
