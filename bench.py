@@ -14,7 +14,7 @@ kernel, the ADC scan: algorithmic bytes = sum over (query, probe) of
 list_len * M code bytes, divided by the scan kernel's average duration from HIP
 events recorded on the stream it runs on.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--cpu-queries N] [--workload c2|c3|c5]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--cpu-queries N] [--workload c2|c3|c4|c5]
 
 --workload c3 prints a supplementary line for BASELINE config 3 instead: 10M x
 96 fp32 (1024-component mixture, per-component sigma U[0.05, 0.15]), 4096
@@ -23,6 +23,13 @@ limit_k 50, threshold_coeff 1.0) compacted to the top 1000 candidates, then the
 early-stopping exact rerank (mini-batch 128, eps 0.1, beta 2) to k=100.  Its
 index is built in-run too (k-means on a 1M-row sample, then every row
 assigned), not timed.
+
+--workload c4 prints a supplementary line for BASELINE config 4, the index
+build: 10M x 128 fp32 (1024-component mixture); k-means++ seeding and 20 Lloyd
+iterations of 4096 centroids on a 1M-row sample; assignment of all 10M rows;
+PQ M=32 training (15 iterations, 50k sample) and encoding of all rows; and an
+elbow sweep over 1024/2048/4096 lists (k-means SSE on the sample, Kneedle
+knee).  value = rows built per second over the whole build.
 
 --workload c5 prints a supplementary line for BASELINE config 5: graph search
 over 5M x 128 fp32 (256-component mixture) with a fixed out-degree-32 graph,
@@ -72,7 +79,7 @@ def main():
     ap.add_argument("--n", type=int, default=1_000_000)
     ap.add_argument("--nq", type=int, default=10_000)
     ap.add_argument("--copy-probe", action="store_true", help="also run a 1 GiB device copy (PMC calibration)")
-    ap.add_argument("--workload", choices=["c2", "c3", "c5"], default="c2")
+    ap.add_argument("--workload", choices=["c2", "c3", "c4", "c5"], default="c2")
     ap.add_argument("--c5-components", type=int, default=256, help="mixture components of the C5 data")
     ap.add_argument("--c5-random-edges", type=int, default=4,
                     help="C5: out-edges per vector replaced by seeded random long-range edges")
@@ -92,6 +99,8 @@ def main():
         return run_c3(args, torch, fg, dev)
     if args.workload == "c5":
         return run_c5(args, torch, fg, dev)
+    if args.workload == "c4":
+        return run_c4(args, torch, fg, dev)
     dim, nlist, m, nprobe, k = 128, 1024, 32, 32, 10
     t0 = time.time()
     x = fg.gen_gmm(args.n, dim, 256, seed=2024, set=0, sig_lo=0.08)
@@ -347,6 +356,94 @@ def run_c3(args, torch, fg, dev):
                       "candidates_per_query": round(tc.float().mean().item(), 1)},
         "cpu_baseline": cpu, "parity": parity, "recall_at_k": recall,
         "ground_truth": {"seconds": round(gt_s, 3), "oracle_parity_50": gt_parity},
+    }
+    print(json.dumps(res), flush=True)
+
+
+def knee(lists, sse):
+    """Kneedle on a decreasing curve: normalised (log2 L, SSE); largest gap below the chord; first on ties."""
+    x = np.log2(np.asarray(lists, np.float64))
+    y = np.asarray(sse, np.float64)
+    xn = (x - x[0]) / (x[-1] - x[0])
+    yn = (y - y[-1]) / (y[0] - y[-1]) if y[0] != y[-1] else np.zeros_like(y)
+    return int(lists[int(np.argmax((1.0 - xn) - yn))])
+
+
+def run_c4(args, torch, fg, dev):
+    """the index build, phase by phase, plus the elbow sweep."""
+    dim, nlist, m, train = 128, 4096, 32, 1_000_000
+    n = args.n if args.n != 1_000_000 else 10_000_000
+    t0 = time.time()
+    x = fg.gen_gmm(n, dim, 1024, seed=2027, set=0, sig_lo=0.05, sig_hi=0.15)
+    log(f"generated {n}x{dim} in {time.time() - t0:.1f}s")
+    dx = torch.from_numpy(x).to(dev)
+    rows = torch.from_numpy((np.arange(train, dtype=np.int64) * n) // train).to(dev)
+    dtr = dx[rows].contiguous()
+    torch.cuda.synchronize()
+
+    def timed(fn):
+        torch.cuda.synchronize()
+        t = time.perf_counter()
+        r = fn()
+        torch.cuda.synchronize()
+        return r, time.perf_counter() - t
+
+    (cent, _), t_km = timed(lambda: fg.kmeans_fit(dtr, nlist, 20, init_mode=1, seed=42, want_assign=False))
+    (asg, dist), t_as = timed(lambda: fg.l2_topk(dx, cent, 1))
+    asg = asg[:, 0].contiguous()
+    cb, t_pq = timed(lambda: fg.pq_train(dx, asg, cent, m, sample_size=50000, iters=15))
+    codes, t_en = timed(lambda: fg.pq_encode(dx, asg, cent, cb))
+    total = t_km + t_as + t_pq + t_en
+    # one Lloyd assignment pass on the sample: the MFMA GEMM + exact re-score
+    _, t_lloyd = timed(lambda: fg.l2_topk(dtr, cent, 1))
+    gemm_flop = 2.0 * n * nlist * dim
+    lloyd_flop = 2.0 * train * nlist * dim
+    log(f"build: k-means (k-means++ + 20 iterations on {train} rows) {t_km:.2f}s, assign {n} rows {t_as:.2f}s "
+        f"({gemm_flop / t_as / 1e12:.1f} TFLOP/s), PQ train {t_pq:.2f}s, encode {t_en:.2f}s; total {total:.2f}s; "
+        f"one Lloyd assignment {t_lloyd * 1e3:.1f} ms ({lloyd_flop / t_lloyd / 1e12:.1f} TFLOP/s)")
+    # elbow sweep
+    t0 = time.perf_counter()
+    sse = {}
+    for L in (1024, 2048, 4096):
+        c = cent if L == nlist else fg.kmeans_fit(dtr, L, 20, init_mode=1, seed=42, want_assign=False)[0]
+        _, d = fg.l2_topk(dtr, c, 1)
+        sse[L] = float(d.to(torch.float64).sum().item())
+    t_elbow = time.perf_counter() - t0
+    chosen = knee(list(sse), list(sse.values()))
+    log(f"elbow sweep {t_elbow:.2f}s: SSE {sse}; knee at {chosen} lists")
+    cpu = parity = None
+    if args.cpu_queries > 0:
+        import oracle
+        ns = min(args.cpu_queries, 20000)
+        threads = oracle.lib.orc_max_threads()
+        hcent = cent.cpu().numpy()
+        t0 = time.perf_counter()
+        oa = oracle.kmeans_assign(x[:ns], hcent)
+        cpu_s = time.perf_counter() - t0
+        cpu = {"value": round(ns / cpu_s, 1), "unit": "rows assigned/s", "cores": threads, "kind": "port",
+               "sample": f"exact assignment of the first {ns} rows to the 4096 centroids, {cpu_s:.1f}s wall on "
+                         f"{threads} OpenMP threads"}
+        parity = {"rows": ns, "assignment_equal": bool(np.array_equal(asg[:ns].cpu().numpy(), oa)),
+                  "codes_equal": bool(np.array_equal(codes[:2000].cpu().numpy(),
+                                                     oracle.pq_encode(x[:2000], oa[:2000], hcent, cb.cpu().numpy(),
+                                                                      fma_mode=1)))}
+        log(f"cpu baseline {cpu['value']} rows/s on {threads} threads; parity {parity}")
+    res = {
+        "metric": "index build rows/s: 10M x 128, 4096 lists (k-means on a 1M sample), PQ M=32 (1 GPU)",
+        "value": round(n / total, 1), "unit": "rows/s", "n_gpus": 1, "steps": 1, "warmup": 0,
+        "ms_per_step": round(total * 1e3, 1), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32", "data": "synthetic: seeded 1024-component Gaussian mixture",
+        "config": {"workload": "BASELINE config 4: 10M x 128, k-means++ + 20 Lloyd iterations of 4096 centroids on "
+                               "a 1M sample, PQ M=32 x 256 (15 iterations), encode 10M, elbow 1024/2048/4096",
+                   "n": n, "dim": dim, "nlist": nlist, "pq_m": m, "train_rows": train},
+        "roofline": {"bound": "mfma", "kernel": "gemm_est_kernel + select_exact_kernel (assignment of all rows)",
+                     "achieved": round(gemm_flop / t_as / 1e12, 2), "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(gemm_flop / t_as / 1e12 / FP32_MFMA_PEAK_TFLOPS, 4), "traffic": None},
+        "phases_s": {"kmeans": round(t_km, 3), "assign": round(t_as, 3), "pq_train": round(t_pq, 3),
+                     "encode": round(t_en, 3), "elbow_sweep": round(t_elbow, 3),
+                     "lloyd_assignment_ms": round(t_lloyd * 1e3, 2)},
+        "elbow": {"sse": sse, "knee": chosen},
+        "cpu_baseline": cpu, "parity": parity,
     }
     print(json.dumps(res), flush=True)
 

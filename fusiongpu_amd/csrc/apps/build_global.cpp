@@ -15,12 +15,21 @@
 //   --nlist N (2048)  --pq_m M (32)  --iters I (20)  --pq_iters I (8)
 //   --sample S (50000)  --init strided|pp (strided)  --seed S (42)
 //   --no-rebalance  --res DIR (../res)
+//   --train_rows T: train the k-means on the rows floor(j*n/T), j < T (all rows
+//     by default, as the reference does); every row is then assigned
+//   --elbow L1,L2,...: before the build, run the k-means for each list count,
+//     print its SSE (sum of exact squared distances of the training rows to
+//     their nearest centroid) and build with the knee: the list count whose
+//     normalised (log2 L, SSE) point lies farthest below the chord from the
+//     first to the last point (the Kneedle rule)
 #include <cmath>
 #include <cstring>
 #include <deque>
 #include <fstream>
 #include <iostream>
 #include <numeric>
+
+#include <sstream>
 
 #include "app_common.hpp"
 
@@ -47,6 +56,41 @@ std::vector<int32_t> assign(const float* d_x, int64_t n, const float* d_c, int k
   return h;
 }
 
+// Sum over rows of the exact squared distance to the nearest centroid.
+double kmeans_sse(const float* d_x, int64_t n, const float* d_c, int k, int dim) {
+  Dev<int32_t> a(n);
+  Dev<float> d(n);
+  const size_t wb = fgpu_l2_topk_workspace_bytes(n, k);
+  Dev<char> ws(wb);
+  ok(fgpu_l2_topk(d_x, n, d_c, k, dim, 1, a.p, d.p, ws.p, wb, nullptr), "SSE assignment");
+  std::vector<float> h(n);
+  hip_ok(hipMemcpy(h.data(), d.p, sizeof(float) * n, hipMemcpyDeviceToHost), "copy distances");
+  double s = 0.0;
+  for (float v : h) s += v;
+  return s;
+}
+
+// Kneedle on a decreasing curve: normalise x = log2 L and y = SSE to [0, 1] and
+// pick the point with the largest (chord - y); the first point on ties.
+int knee(const std::vector<int>& L, const std::vector<double>& sse) {
+  const size_t m = L.size();
+  if (m < 3) return L[0];
+  const double x0 = std::log2((double)L.front()), x1 = std::log2((double)L.back());
+  const double y0 = sse.front(), y1 = sse.back();
+  int best = L[0];
+  double best_gap = -1.0;
+  for (size_t i = 0; i < m; ++i) {
+    const double xn = (std::log2((double)L[i]) - x0) / (x1 - x0);
+    const double yn = (y0 == y1) ? 0.0 : (sse[i] - y1) / (y0 - y1);
+    const double gap = (1.0 - xn) - yn;  // the chord from (0, 1) to (1, 0)
+    if (gap > best_gap) {
+      best_gap = gap;
+      best = L[i];
+    }
+  }
+  return best;
+}
+
 }  // namespace
 
 int main(int argc, char** argv) {
@@ -54,6 +98,8 @@ int main(int argc, char** argv) {
   int nlist = 2048, pq_m = 32, iters = 20, pq_iters = 8, sample = 50000;
   uint64_t seed = 42;
   bool rebalance = true;
+  int64_t train_rows = 0;
+  std::vector<int> elbow;
   for (int i = 1; i < argc; ++i) {
     const std::string a = argv[i];
     auto next = [&]() -> const char* {
@@ -69,12 +115,19 @@ int main(int argc, char** argv) {
     else if (a == "--seed") seed = std::strtoull(next(), nullptr, 10);
     else if (a == "--res") res = next();
     else if (a == "--no-rebalance") rebalance = false;
+    else if (a == "--train_rows") train_rows = std::atoll(next());
+    else if (a == "--elbow") {
+      std::stringstream ss(next());
+      std::string tok;
+      while (std::getline(ss, tok, ',')) elbow.push_back(std::atoi(tok.c_str()));
+    }
     else if (!a.empty() && a[0] != '-' && base.empty()) base = a;
     else { std::cerr << "unknown argument " << a << "\n"; return 1; }
   }
   if (base.empty()) {
     std::cerr << "Usage: ./build_global <base.fvecs> [--nlist N] [--pq_m M] [--iters I] [--pq_iters I] "
-                 "[--sample S] [--init strided|pp] [--seed S] [--no-rebalance] [--res DIR]\n";
+                 "[--sample S] [--init strided|pp] [--seed S] [--no-rebalance] [--res DIR] [--train_rows T] "
+                 "[--elbow L1,L2,...]\n";
     return 1;
   }
   const int dim = app::fvecs_dim(base);
@@ -87,10 +140,37 @@ int main(int argc, char** argv) {
   Dev<float> d_x((size_t)n * dim);
   hip_ok(hipMemcpy(d_x.p, h_x.data(), sizeof(float) * h_x.size(), hipMemcpyHostToDevice), "copy base");
 
-  // k-means over every row (run_kmeans_gpu, kmeans_gpu.cuh:234-324)
+  // training rows: all (the reference) or the systematic sample
+  const float* d_train = d_x.p;
+  int64_t nt = n;
+  Dev<float> d_sample(train_rows > 0 && train_rows < n ? (size_t)train_rows * dim : 1);
+  if (train_rows > 0 && train_rows < n) {
+    std::vector<float> hs((size_t)train_rows * dim);
+    for (int64_t j = 0; j < train_rows; ++j)
+      std::memcpy(hs.data() + (size_t)j * dim, h_x.data() + (size_t)(j * n / train_rows) * dim, sizeof(float) * dim);
+    hip_ok(hipMemcpy(d_sample.p, hs.data(), sizeof(float) * hs.size(), hipMemcpyHostToDevice), "copy sample");
+    d_train = d_sample.p;
+    nt = train_rows;
+    std::cout << "Training on " << nt << " sampled rows." << std::endl;
+  }
+  const int initm = init == "pp" ? 1 : 0;
+  if (!elbow.empty()) {
+    std::vector<double> sse;
+    for (int L : elbow) {
+      if (L < 1 || L > nt) { std::cerr << "elbow list count " << L << " out of range\n"; return 1; }
+      Dev<float> d_e((size_t)L * dim);
+      ok(fgpu_kmeans_fit(d_train, nt, dim, L, iters, initm, seed, d_e.p, nullptr, nullptr), "elbow k-means");
+      sse.push_back(kmeans_sse(d_train, nt, d_e.p, L, dim));
+      std::cout << "Elbow: nlist " << L << " SSE " << sse.back() << std::endl;
+    }
+    nlist = knee(elbow, sse);
+    std::cout << "Elbow: chosen nlist " << nlist << std::endl;
+  }
+
+  // k-means (run_kmeans_gpu, kmeans_gpu.cuh:234-324)
   std::cout << "Training " << nlist << " initial centroids (GPU)..." << std::endl;
   Dev<float> d_c((size_t)nlist * dim);
-  ok(fgpu_kmeans_fit(d_x.p, n, dim, nlist, iters, init == "pp" ? 1 : 0, seed, d_c.p, nullptr, nullptr), "k-means");
+  ok(fgpu_kmeans_fit(d_train, nt, dim, nlist, iters, initm, seed, d_c.p, nullptr, nullptr), "k-means");
   std::cout << "Assigning vectors to initial clusters (GPU)..." << std::endl;
   std::vector<int32_t> a0 = assign(d_x.p, n, d_c.p, nlist, dim);
   std::vector<float> h_c((size_t)nlist * dim);
@@ -128,7 +208,7 @@ int main(int argc, char** argv) {
         std::memcpy(sub.data() + i * dim, h_x.data() + (size_t)t.rows[i] * dim, sizeof(float) * dim);
       Dev<float> d_sub(sub.size()), d_sc((size_t)sub_k * dim);
       hip_ok(hipMemcpy(d_sub.p, sub.data(), sizeof(float) * sub.size(), hipMemcpyHostToDevice), "copy subset");
-      ok(fgpu_kmeans_fit(d_sub.p, (int64_t)sz, dim, sub_k, 15, init == "pp" ? 1 : 0, seed, d_sc.p, nullptr, nullptr),
+      ok(fgpu_kmeans_fit(d_sub.p, (int64_t)sz, dim, sub_k, 15, initm, seed, d_sc.p, nullptr, nullptr),
          "local k-means");
       std::vector<int32_t> la = assign(d_sub.p, (int64_t)sz, d_sc.p, sub_k, dim);
       std::vector<float> sc((size_t)sub_k * dim);

@@ -117,3 +117,26 @@ def test_search_pipeline_matches_library_path(tmp_path):
     for k, printed in ((1, float(m.group(1))), (10, float(m.group(2)))):
         hits = sum(len(set(got[i, :k]) & set(gt[i])) for i in range(q.shape[0]))
         assert abs(100.0 * hits / (q.shape[0] * k) - printed) < 1e-3
+
+
+def test_build_global_elbow_sweep(tmp_path):
+    _say("build_global --elbow")
+    x = oracle.gen_gmm(12000, 128, 24, seed=6, sig_lo=0.1)
+    res, out = _build(tmp_path, x, ["--elbow", "16,32,64", "--train_rows", 6000, "--iters", 3, "--pq_iters", 2,
+                                    "--sample", 3000, "--no-rebalance", "--init", "pp"])
+    sse = [float(v) for v in re.findall(r"Elbow: nlist \d+ SSE ([\d.e+]+)", out)]
+    chosen = int(re.search(r"Elbow: chosen nlist (\d+)", out).group(1))
+    assert len(sse) == 3 and sse[0] > sse[1] > sse[2]
+    # the SSE of each list count: exact distances of the training sample to its k-means centroids
+    rows = (np.arange(6000, dtype=np.int64) * 12000) // 6000
+    tr = torch.from_numpy(np.ascontiguousarray(x[rows])).cuda()
+    for L, printed in zip((16, 32, 64), sse):
+        c, _ = fg.kmeans_fit(tr, L, 3, init_mode=1, seed=42, want_assign=False)
+        _, d = fg.l2_topk(tr, c, 1)
+        assert abs(float(d.to(torch.float64).sum().item()) - printed) <= 1e-5 * printed
+    xn = np.log2([16, 32, 64]) - 4.0
+    xn /= xn[-1]
+    yn = (np.array(sse) - sse[-1]) / (sse[0] - sse[-1])
+    assert chosen == [16, 32, 64][int(np.argmax((1 - xn) - yn))]
+    offs, _, _, _ = fg.read_ivf_data(res / "ivf_data.bin", 32, 128)
+    assert offs.shape[0] == chosen + 1
