@@ -159,6 +159,8 @@ def main():
     assert torch.equal(sid, out[0]) and torch.equal(sd, out[1]), "instrumented scan differs"
     loaded_bytes = st["vectors_loaded"] * (m + 4)  # code bytes + the 4-byte vector id loaded with them
     loaded_gbs = loaded_bytes / (adc_ms * 1e-3) / 1e9
+    log("adc clocks per query: " + ", ".join(f"{kk} {st[kk] / args.nq:.0f}" for kk in
+                                                ("clk_setup", "clk_builder", "clk_scanner", "clk_total")))
     log(f"adc loads {st['vectors_loaded'] * m / 1e9:.2f} GB of codes (+ids {st['vectors_loaded'] * 4 / 1e9:.2f} GB) "
         f"= {loaded_gbs:.0f} GB/s; LUTs built {st['luts_built']}, probed lists skipped {st['lists_skipped']} "
         f"of {int((probes.view(torch.int32) >= 0).sum().item())}")
@@ -216,7 +218,9 @@ def main():
                              "reach the top-k, so it loads only loaded_bytes_per_launch",
                      "loaded_bytes_per_launch": loaded_bytes, "achieved_loaded": round(loaded_gbs, 1),
                      "frac_loaded": round(loaded_gbs / HBM_PEAK_GBS, 4),
-                     "luts_built": st["luts_built"], "lists_skipped": st["lists_skipped"]},
+                     "luts_built": st["luts_built"], "lists_skipped": st["lists_skipped"],
+                     "clocks_per_query": {kk: round(st[kk] / args.nq) for kk in
+                                          ("clk_setup", "clk_builder", "clk_scanner", "clk_total")}},
         "stages_ms": {"coarse": round(coarse_ms, 4), "adc": round(adc_ms, 4),
                       "coarse_tflops_incl_select": round(gemm_flop / coarse_ms / 1e9, 2)},
         "cpu_baseline": cpu,

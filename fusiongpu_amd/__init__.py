@@ -294,11 +294,12 @@ class Index:
         nq, nprobe = p.shape
         ids, d = out if out is not None else (torch.empty((nq, k), dtype=torch.int32, device="cuda"),
                                               torch.empty((nq, k), dtype=torch.float32, device="cuda"))
-        st = torch.zeros(4, dtype=torch.int64, device="cuda")
+        st = torch.zeros(8, dtype=torch.int64, device="cuda")
         _check(lib.fgpu_adc_search_stats(self._h, _dev_ptr(q), nq, _dev_ptr(p), nprobe, k, _dev_ptr(ids),
                                          _dev_ptr(d), _dev_ptr(st), _stream(stream)))
         v = st.cpu().tolist()
-        return ids, d, {"vectors_loaded": v[0], "luts_built": v[1], "lists_skipped": v[2]}
+        return ids, d, {"vectors_loaded": v[0], "luts_built": v[1], "lists_skipped": v[2], "clk_setup": v[3],
+                        "clk_builder": v[4], "clk_scanner": v[5], "clk_total": v[6]}
 
     def two_phase_search(self, queries, probe_ids, p1_lists: int, limit_k: int, threshold_coeff: float,
                          rerank_m: int, want_cutoffs: bool = False, workspace=None, stream=None):

@@ -357,6 +357,7 @@ __global__ __launch_bounds__(kSpecWaves * kWave, 4) void adc_flow_kernel(AdcArgs
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const bool builder = wave < kBuilderWaves;
   const int q = blockIdx.x;
+  const long long t_start = a.stats ? clock64() : 0;
   const int P = a.nprobe, k = a.k;
   const uint32_t NL = (uint32_t)a.nlist;
 
@@ -427,6 +428,7 @@ __global__ __launch_bounds__(kSpecWaves * kWave, 4) void adc_flow_kernel(AdcArgs
   }
   __syncthreads();
 
+  const long long t_setup = a.stats ? clock64() : 0;
   // First list >= from (below nv) whose decision is not "skipped" and for which
   // `want` holds; nv if there is none.  One LDS round trip for up to 64 lists.
   auto next_list = [&](int from, auto want) {
@@ -524,6 +526,8 @@ __global__ __launch_bounds__(kSpecWaves * kWave, 4) void adc_flow_kernel(AdcArgs
     if (a.stats && wave == 0 && lane == 0) {
       atomicAdd(&a.stats[1], (unsigned long long)nbuilt);
       atomicAdd(&a.stats[2], (unsigned long long)nskip);
+      atomicAdd(&a.stats[3], (unsigned long long)(t_setup - t_start));
+      atomicAdd(&a.stats[4], (unsigned long long)(clock64() - t_setup));
     }
   } else {
     const int swave = wave - kBuilderWaves;
@@ -592,7 +596,10 @@ __global__ __launch_bounds__(kSpecWaves * kWave, 4) void adc_flow_kernel(AdcArgs
         nload += chunk_vecs(f, have_c);
       }
     }
-    if (a.stats && lane == 0) atomicAdd(&a.stats[0], (unsigned long long)nload);
+    if (a.stats && lane == 0) {
+      atomicAdd(&a.stats[0], (unsigned long long)nload);
+      if (wave == kBuilderWaves) atomicAdd(&a.stats[5], (unsigned long long)(clock64() - t_setup));
+    }
   }
 
   // Merge the scanner waves' lists: a 3-level tree, pairs merged in parallel.
@@ -620,6 +627,7 @@ __global__ __launch_bounds__(kSpecWaves * kWave, 4) void adc_flow_kernel(AdcArgs
     a.out_ids[(size_t)q * k + lane] = pad ? -1 : li;
     a.out_d[(size_t)q * k + lane] = pad ? FLT_MAX : ld;
   }
+  if (a.stats && tid == 0) atomicAdd(&a.stats[6], (unsigned long long)(clock64() - t_start));
 }
 
 template <int D, int M>

@@ -48,7 +48,9 @@ struct AdcArgs {
   float* out_d;             // [nq][k]
   // Optional instrumentation (nullptr = off), summed over the launch:
   // [0] vectors whose codes were loaded, [1] LUTs built, [2] probed lists
-  // skipped by the list lower bound.
+  // skipped by the list lower bound; shader clocks per workgroup: [3] set-up,
+  // [4] builder wave 0 after set-up, [5] scanner wave 8 after set-up, [6] the
+  // whole workgroup (thread 0, start to end).
   unsigned long long* stats = nullptr;
 };
 bool adc_supported(int dim, int m);

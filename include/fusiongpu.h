@@ -92,10 +92,12 @@ fgpu_status fgpu_adc_search(const fgpu_index* idx, const float* d_queries, int n
                             float* d_out_dists, void* stream);
 
 /* fgpu_adc_search plus instrumentation (no reference counterpart): adds to
- * d_stats[0..2] (device, caller-zeroed, uint64) the number of vectors whose
- * codes the scan loaded, the number of LUTs built and the number of probed
+ * d_stats[0..6] (device, caller-zeroed, uint64) the number of vectors whose
+ * codes the scan loaded, the number of LUTs built, the number of probed
  * lists the scan skipped because a lower bound on every distance in the list
- * exceeded the running k-th distance.  Results equal fgpu_adc_search's. */
+ * exceeded the running k-th distance, and per-workgroup shader clocks (set-up,
+ * a builder wave, a scanner wave, the whole workgroup).  Results equal
+ * fgpu_adc_search's. */
 fgpu_status fgpu_adc_search_stats(const fgpu_index* idx, const float* d_queries, int nq,
                                   const uint32_t* d_probe_ids, int nprobe, int k, int32_t* d_out_ids,
                                   float* d_out_dists, unsigned long long* d_stats, void* stream);

@@ -196,3 +196,24 @@ def test_build_ivfpq_bit_exact():
     want = oracle.build_ivfpq(x, 32, 32, kmeans_iters=4, init_mode=1, seed=7, pq_iters=3, sample_size=3000)
     for g, w, name in zip(got, want, ["offsets", "ids", "codes", "centroids", "codebook"]):
         assert np.array_equal(np.asarray(g).view(np.uint8), np.asarray(w).view(np.uint8)), name
+
+
+def test_config1_end_to_end_bit_exact():
+    """BASELINE config 1 at full size: 100k x 128 (64-component mixture, sigma 0.1), 256 lists, PQ M=16,
+    1000 queries, nprobe 16, k 10 -- index build and search, GPU against the oracle."""
+    _say("config 1 end to end")
+    x = oracle.gen_gmm(100000, 128, 64, seed=11, sig_lo=0.1)
+    q = oracle.gen_gmm(1000, 128, 64, seed=11, set=1, sig_lo=0.1)
+    got = fg.build_ivfpq(torch.from_numpy(x).cuda(), 256, 16, kmeans_iters=20, init_mode=1, seed=42, pq_iters=8,
+                         sample_size=50000)
+    want = oracle.build_ivfpq(x, 256, 16, kmeans_iters=20, init_mode=1, seed=42, pq_iters=8, sample_size=50000)
+    for g, w, name in zip(got, want, ["offsets", "ids", "codes", "centroids", "codebook"]):
+        assert np.array_equal(np.asarray(g).view(np.uint8), np.asarray(w).view(np.uint8)), name
+    offs, ids, codes, cent, cb = want
+    idx = fg.Index.from_arrays(128, 16, offs, ids, codes, cent, cb)
+    gid, gd = idx.search(torch.from_numpy(q).cuda(), 16, 10)
+    probes, _ = oracle.coarse(q, cent, 16)
+    oid, od = oracle.search_plain(q, cent, cb, offs, ids, codes, probes, 10)
+    assert np.array_equal(_host(gid), oid)
+    assert np.array_equal(_bits(_host(gd)), _bits(od))
+    idx.close()
