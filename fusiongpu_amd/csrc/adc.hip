@@ -47,8 +47,8 @@ namespace {
 template <int D, int M, int BUF, int SCAN_WAVES, bool PREFETCH>
 __device__ __forceinline__ void scan_list(const float* smem, const uint8_t* __restrict__ codes,
                                           const int32_t* __restrict__ ids, int start, int n, int k, int swave,
-                                          uint4 (&w0)[M / 16], uint4 (&w1)[M / 16], int& i0, int& i1, float& ld,
-                                          int& li, uint64_t& own, unsigned long long* s_thr) {
+                                          uint4 (&w0)[M / 16], uint4 (&w1)[M / 16], int& i0, int& i1, uint64_t& lk,
+                                          uint64_t& own, unsigned long long* s_thr) {
   using C = Cfg<D, M>;
   constexpr int kRound = SCAN_WAVES * kVecPerWaveRound;
   const float* lut = smem + BUF * C::LUT;
@@ -67,14 +67,14 @@ __device__ __forceinline__ void scan_list(const float* smem, const uint8_t* __re
     uint64_t thr = own < shared_thr ? own : shared_thr;
     float d0, d1;
     if (adc_sum2<M>(lut, w0, w1, v0 < n, v1 < n, __uint_as_float((uint32_t)(thr >> 32)), d0, d1)) {
-      bool changed = offer(d0, i0, v0 < n, thr, ld, li);
+      bool changed = offer_k(key_of(d0, i0), v0 < n, thr, lk);
       if (changed) {
-        const uint64_t kth = pack_key(readlane_f(ld, k - 1), readlane_i(li, k - 1));
+        const uint64_t kth = readlane64(lk, k - 1);
         thr = kth < thr ? kth : thr;
       }
-      changed |= offer(d1, i1, v1 < n, thr, ld, li);
+      changed |= offer_k(key_of(d1, i1), v1 < n, thr, lk);
       if (changed) {
-        own = pack_key(readlane_f(ld, k - 1), readlane_i(li, k - 1));
+        own = readlane64(lk, k - 1);
         if (lane == 0) atomicMin(s_thr, (unsigned long long)own);
       }
     }
@@ -129,21 +129,21 @@ __device__ __forceinline__ bool adc_sum2_lb(const float* __restrict__ lut, const
 template <int D, int M, int BUF>
 __device__ __forceinline__ void scan_round_lb(const float* smem, int v0, int n, int k, const uint4 (&w0)[M / 16],
                                               const uint4 (&w1)[M / 16], int i0, int i1, uint64_t thr,
-                                              float thr_hi, const float (&T)[M / 8], float& ld, int& li,
+                                              float thr_hi, const float (&T)[M / 8], uint64_t& lk,
                                               uint64_t& own, unsigned long long* s_thr) {
   using C = Cfg<D, M>;
   const float* lut = smem + BUF * C::LUT;
   const int v1 = v0 + kWave;
   float d0, d1;
   if (adc_sum2_lb<M>(lut, w0, w1, v0 < n, v1 < n, thr_hi, T, d0, d1)) {
-    bool changed = offer(d0, i0, v0 < n, thr, ld, li);
+    bool changed = offer_k(key_of(d0, i0), v0 < n, thr, lk);
     if (changed) {
-      const uint64_t kth = pack_key(readlane_f(ld, k - 1), readlane_i(li, k - 1));
+      const uint64_t kth = readlane64(lk, k - 1);
       thr = kth < thr ? kth : thr;
     }
-    changed |= offer(d1, i1, v1 < n, thr, ld, li);
+    changed |= offer_k(key_of(d1, i1), v1 < n, thr, lk);
     if (changed) {
-      own = pack_key(readlane_f(ld, k - 1), readlane_i(li, k - 1));
+      own = readlane64(lk, k - 1);
       if ((threadIdx.x & 63) == 0) atomicMin(s_thr, (unsigned long long)own);
     }
   }
@@ -168,18 +168,25 @@ __device__ __forceinline__ void lds_signal_add(int* p, int v) {
   if ((threadIdx.x & 63) == 0) __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
 
-// Merge `nw` sorted wave lists held in LDS (md/mi, 64 entries each) into this
-// wave's registers and write the k best.
-__device__ __forceinline__ void merge_and_write(float ld, int li, const float* md, const int* mi, int nw, int q, int k,
+// Write the k best of a sorted wave list (padding as id -1, distance FLT_MAX).
+__device__ __forceinline__ void write_topk(uint64_t lk, int q, int k, const AdcArgs& a) {
+  const int lane = threadIdx.x & 63;
+  if (lane < k) {
+    const int id = key_id(lk);
+    const bool pad = id == kPadId;
+    a.out_ids[(size_t)q * k + lane] = pad ? -1 : id;
+    a.out_d[(size_t)q * k + lane] = pad ? FLT_MAX : key_dist(lk);
+  }
+}
+
+// Merge `nw` sorted wave lists held in LDS (64 keys each) into this wave's
+// registers and write the k best.
+__device__ __forceinline__ void merge_and_write(uint64_t lk, const uint64_t* mk, int nw, int q, int k,
                                                 const AdcArgs& a) {
   const int lane = threadIdx.x & 63;
 #pragma unroll 1
-  for (int w = 1; w < nw; ++w) wave_merge_sorted64(ld, li, md[w * kWave + lane], mi[w * kWave + lane]);
-  if (lane < k) {
-    const bool pad = li == kPadId;
-    a.out_ids[(size_t)q * k + lane] = pad ? -1 : li;
-    a.out_d[(size_t)q * k + lane] = pad ? FLT_MAX : ld;
-  }
+  for (int w = 1; w < nw; ++w) wave_merge_sorted64_k(lk, mk[w * kWave + lane]);
+  write_topk(lk, q, k, a);
 }
 
 // ---------------------------------------------------------------------------
@@ -221,8 +228,7 @@ __global__ __launch_bounds__(kNT) void adc_plain_kernel(AdcArgs a) {
   if (p < P && tid < D) rbuf[tid] = qs[tid] - a.centroids[(size_t)probes[p] * D + tid];
   __syncthreads();
 
-  float ld = FLT_MAX;
-  int li = kPadId;
+  uint64_t lk = kPadKey;
   uint64_t own = kNoThr;
   int it = 0;
   uint4 w0[C::NV4], w1[C::NV4];
@@ -249,10 +255,10 @@ __global__ __launch_bounds__(kNT) void adc_plain_kernel(AdcArgs a) {
     if (pn < P && tid < D) rbuf[((it + 1) & 1) * D + tid] = qs[tid] - a.centroids[(size_t)probes[pn] * D + tid];
     __syncthreads();
     if (buf == 0)
-      scan_list<D, M, 0, kNW, false>(smem, a.codes, a.vec_ids, start, n, k, wave, w0, w1, i0, i1, ld, li, own, &s_thr);
+      scan_list<D, M, 0, kNW, false>(smem, a.codes, a.vec_ids, start, n, k, wave, w0, w1, i0, i1, lk, own, &s_thr);
     else
-      scan_list<D, M, (C::DBUF ? 1 : 0), kNW, false>(smem, a.codes, a.vec_ids, start, n, k, wave, w0, w1, i0, i1, ld,
-                                                    li, own, &s_thr);
+      scan_list<D, M, (C::DBUF ? 1 : 0), kNW, false>(smem, a.codes, a.vec_ids, start, n, k, wave, w0, w1, i0, i1, lk,
+                                                    own, &s_thr);
     if (!C::DBUF) __syncthreads();
     p = pn;
     ++it;
@@ -261,12 +267,10 @@ __global__ __launch_bounds__(kNT) void adc_plain_kernel(AdcArgs a) {
   if (a.stats && tid == 0) atomicAdd(&a.stats[1], (unsigned long long)it);
 
   __syncthreads();
-  float* md = smem;
-  int* mi = reinterpret_cast<int*>(smem + kNW * kWave);
-  md[wave * kWave + lane] = ld;
-  mi[wave * kWave + lane] = li;
+  uint64_t* mk = reinterpret_cast<uint64_t*>(smem);
+  mk[wave * kWave + lane] = lk;
   __syncthreads();
-  if (wave == 0) merge_and_write(ld, li, md, mi, kNW, q, k, a);
+  if (wave == 0) merge_and_write(lk, mk, kNW, q, k, a);
 }
 
 // ---------------------------------------------------------------------------
@@ -317,16 +321,11 @@ __device__ __forceinline__ int lds_wait_decided(const int* p) {
 }
 
 
-// list := the 64 smallest of list U the sorted list held in LDS at (pd, pi).
-__device__ __forceinline__ void wave_merge_lds64(float& d, int& id, const float* pd, const int* pi) {
-  const int lane = threadIdx.x & 63;
-  const float rd = pd[kWave - 1 - lane];
-  const int ri = pi[kWave - 1 - lane];
-  if (lt_pair(rd, ri, d, id)) {
-    d = rd;
-    id = ri;
-  }
-  wave_bitonic_merge64(d, id);
+// list := the 64 smallest of list U the sorted list of keys held in LDS at pk.
+__device__ __forceinline__ void wave_merge_lds64(uint64_t& k, const uint64_t* pk) {
+  const uint64_t r = pk[kWave - 1 - (threadIdx.x & 63)];
+  k = r < k ? r : k;
+  bitonic_pass_k<64>(k, true);
 }
 
 template <int D, int M>
@@ -439,8 +438,7 @@ __global__ __launch_bounds__(kSpecWaves * kWave, 4) void adc_flow_kernel(AdcArgs
     return bm ? from + __ffsll((unsigned long long)bm) - 1 : nv;
   };
 
-  float ld = FLT_MAX;
-  int li = kPadId;
+  uint64_t lk = kPadKey;
   if (builder) {
     float* rw = rws[wave];
     const float qv = lane < RW ? qs[wave * RW + lane] : 0.0f;
@@ -575,9 +573,9 @@ __global__ __launch_bounds__(kSpecWaves * kWave, 4) void adc_flow_kernel(AdcArgs
         }
         const int v0 = (c - f_cst[f]) * kChunk + lane;
         if (dec & 1)
-          scan_round_lb<D, M, 1>(smem, v0, n, k, w0, w1, i0, i1, thr, thr_hi, T, ld, li, own, &s_thr);
+          scan_round_lb<D, M, 1>(smem, v0, n, k, w0, w1, i0, i1, thr, thr_hi, T, lk, own, &s_thr);
         else
-          scan_round_lb<D, M, 0>(smem, v0, n, k, w0, w1, i0, i1, thr, thr_hi, T, ld, li, own, &s_thr);
+          scan_round_lb<D, M, 0>(smem, v0, n, k, w0, w1, i0, i1, thr, thr_hi, T, lk, own, &s_thr);
         ++mine;
         c += kScanWaves;
         if (c >= c_end) break;
@@ -603,30 +601,19 @@ __global__ __launch_bounds__(kSpecWaves * kWave, 4) void adc_flow_kernel(AdcArgs
   }
 
   // Merge the scanner waves' lists: a 3-level tree, pairs merged in parallel.
-  float* md = smem;
-  int* mi = reinterpret_cast<int*>(smem + kScanWaves * kWave);
+  uint64_t* mk = reinterpret_cast<uint64_t*>(smem);
   const int sw = wave - kBuilderWaves;
   __syncthreads();
-  if (!builder) {
-    md[sw * kWave + lane] = ld;
-    mi[sw * kWave + lane] = li;
-  }
+  if (!builder) mk[sw * kWave + lane] = lk;
 #pragma unroll
   for (int step = 1; step < kScanWaves; step <<= 1) {
     __syncthreads();
     const bool active = !builder && (sw % (2 * step)) == 0;
-    if (active) wave_merge_lds64(ld, li, md + (sw + step) * kWave, mi + (sw + step) * kWave);
+    if (active) wave_merge_lds64(lk, mk + (sw + step) * kWave);
     __syncthreads();
-    if (active) {
-      md[sw * kWave + lane] = ld;
-      mi[sw * kWave + lane] = li;
-    }
+    if (active) mk[sw * kWave + lane] = lk;
   }
-  if (sw == 0 && lane < k) {
-    const bool pad = li == kPadId;
-    a.out_ids[(size_t)q * k + lane] = pad ? -1 : li;
-    a.out_d[(size_t)q * k + lane] = pad ? FLT_MAX : ld;
-  }
+  if (sw == 0) write_topk(lk, q, k, a);
   if (a.stats && tid == 0) atomicAdd(&a.stats[6], (unsigned long long)(clock64() - t_start));
 }
 

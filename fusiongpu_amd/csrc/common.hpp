@@ -87,9 +87,10 @@ __device__ __forceinline__ float key_float(uint32_t k) {
 // S = 1, 2, row rotates for S = 4, 8 (rotating a 16-lane row by 8 is xor 8;
 // xor 4 picks the rotate by 4 or by 12 from bit 2 of the lane), and the gfx950
 // permlane16/32 swaps for S = 16, 32.  Every lane must be active.
+// A lane whose DPP source lies outside the wave (wave_shr:1 at lane 0) reads 0.
 template <int C>
 __device__ __forceinline__ int dpp_mov(int v) {
-  return __builtin_amdgcn_update_dpp(0, v, C, 0xF, 0xF, false);
+  return __builtin_amdgcn_mov_dpp(v, C, 0xF, 0xF, true);
 }
 template <int S>
 __device__ __forceinline__ int xchg(int v) {
@@ -202,6 +203,77 @@ __device__ __forceinline__ float readlane_f(float v, int l) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
 }
 __device__ __forceinline__ int readlane_i(int v, int l) { return __builtin_amdgcn_readlane(v, l); }
+
+// ---- the same networks on packed 64-bit keys ---------------------------------
+// A key is (float bits << 32) | id.  For distances >= 0 (sums of squares) and
+// ids >= 0, ascending key order is exactly the tie rule (distance, then id),
+// so a compare-exchange is one 64-bit compare and two selects, without the
+// branchy two-field compare of the (d, id) pair form.
+__device__ __forceinline__ uint64_t key_of(float d, int id) {
+  return ((uint64_t)__float_as_uint(d) << 32) | (uint32_t)id;
+}
+__device__ __forceinline__ float key_dist(uint64_t k) { return __uint_as_float((uint32_t)(k >> 32)); }
+__device__ __forceinline__ int key_id(uint64_t k) { return (int)(uint32_t)k; }
+constexpr uint64_t kPadKey = ((uint64_t)0x7F7FFFFFu << 32) | (uint32_t)kPadId;  // (FLT_MAX, kPadId)
+
+template <int S>
+__device__ __forceinline__ uint64_t xchg64(uint64_t v) {
+  const uint32_t lo = (uint32_t)xchg<S>((int)(uint32_t)v), hi = (uint32_t)xchg<S>((int)(uint32_t)(v >> 32));
+  return ((uint64_t)hi << 32) | lo;
+}
+template <int C>
+__device__ __forceinline__ uint64_t dpp_mov64(uint64_t v) {
+  const uint32_t lo = (uint32_t)dpp_mov<C>((int)(uint32_t)v), hi = (uint32_t)dpp_mov<C>((int)(uint32_t)(v >> 32));
+  return ((uint64_t)hi << 32) | lo;
+}
+__device__ __forceinline__ uint64_t readlane64(uint64_t v, int l) {
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, l);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), l);
+  return ((uint64_t)hi << 32) | lo;
+}
+
+// Compare-exchange at distance S: the lower lane of each pair keeps the
+// smaller key when `up`, the larger otherwise (equal keys are interchangeable).
+template <int S>
+__device__ __forceinline__ void bitonic_stage_k(uint64_t& k, bool up) {
+  const uint64_t o = xchg64<S>(k);
+  const bool lower = (lane_id() & S) == 0;
+  k = ((k < o) == (lower == up)) ? k : o;
+}
+template <int SIZE>
+__device__ __forceinline__ void bitonic_pass_k(uint64_t& k, bool up) {
+  if constexpr (SIZE > 32) bitonic_stage_k<32>(k, up);
+  if constexpr (SIZE > 16) bitonic_stage_k<16>(k, up);
+  if constexpr (SIZE > 8) bitonic_stage_k<8>(k, up);
+  if constexpr (SIZE > 4) bitonic_stage_k<4>(k, up);
+  if constexpr (SIZE > 2) bitonic_stage_k<2>(k, up);
+  bitonic_stage_k<1>(k, up);
+}
+// Ascending bitonic sort of one key per lane across the wave.
+__device__ __forceinline__ void wave_sort64_k(uint64_t& k) {
+  const int lane = lane_id();
+  bitonic_pass_k<2>(k, (lane & 2) == 0);
+  bitonic_pass_k<4>(k, (lane & 4) == 0);
+  bitonic_pass_k<8>(k, (lane & 8) == 0);
+  bitonic_pass_k<16>(k, (lane & 16) == 0);
+  bitonic_pass_k<32>(k, (lane & 32) == 0);
+  bitonic_pass_k<64>(k, true);
+}
+__device__ __forceinline__ uint64_t wave_reverse64(uint64_t v) {
+  const uint32_t lo = (uint32_t)wave_reverse((int)(uint32_t)v), hi = (uint32_t)wave_reverse((int)(uint32_t)(v >> 32));
+  return ((uint64_t)hi << 32) | lo;
+}
+// list (ascending) := the 64 smallest of list U cand (cand ascending too).
+__device__ __forceinline__ void wave_merge_sorted64_k(uint64_t& k, uint64_t cand) {
+  const uint64_t r = wave_reverse64(cand);
+  k = r < k ? r : k;
+  bitonic_pass_k<64>(k, true);
+}
+// Insert nk into the ascending list; the last entry drops off.
+__device__ __forceinline__ void wave_insert64_k(uint64_t& k, uint64_t nk) {
+  const uint64_t p = dpp_mov64<0x138>(k);  // wave_shr:1: lane i gets lane i-1
+  if (!(k < nk)) k = (lane_id() == 0 || p < nk) ? nk : p;
+}
 
 __device__ __forceinline__ float wave_min_f(float v) {
 #pragma unroll

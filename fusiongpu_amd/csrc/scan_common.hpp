@@ -138,6 +138,25 @@ __device__ __forceinline__ bool offer(float d, int id, bool valid, uint64_t thr,
   return true;
 }
 
+// The same on packed keys: lk holds the wave's ascending top-64 keys.
+__device__ __forceinline__ bool offer_k(uint64_t key, bool valid, uint64_t thr, uint64_t& lk) {
+  const bool pass = valid && key < thr;
+  uint64_t bm = __ballot(pass);
+  if (!bm) return false;
+  if (__popcll(bm) > kSerialMax) {
+    uint64_t c = pass ? key : kPadKey;
+    wave_sort64_k(c);
+    wave_merge_sorted64_k(lk, c);
+  } else {
+    while (bm) {
+      const int src = __ffsll((unsigned long long)bm) - 1;
+      bm &= bm - 1;
+      wave_insert64_k(lk, readlane64(key, src));
+    }
+  }
+  return true;
+}
+
 // Each scanning wave takes 128 consecutive vectors per round (two per lane).
 constexpr int kVecPerWaveRound = 2 * kWave;
 
