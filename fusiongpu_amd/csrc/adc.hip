@@ -30,6 +30,9 @@
 //     lists into two LDS buffers while 8 scan, handing buffers over through
 //     LDS counters instead of workgroup barriers.
 //     adc_plain_kernel (pq_m 48, 64): 8 waves alternate build and scan.
+#include <algorithm>
+#include <atomic>
+
 #include "common.hpp"
 #include "kernels.hpp"
 #include "scan_common.hpp"
@@ -281,33 +284,45 @@ constexpr int kBuilderWaves = 8;
 constexpr int kScanWaves = kSpecWaves - kBuilderWaves;
 
 // ---------------------------------------------------------------------------
-// Decoupled wave-specialised kernel: no workgroup barrier between lists.
+// Decoupled wave-specialised kernel, persistent over queries: no workgroup
+// barrier after the start.  Workgroup g takes queries g, g + G, g + 2G, ...
+// (G = grid size, at most one workgroup per CU); the per-query state lives in
+// two LDS slots used by alternate queries, so builder waves set up query i + 1
+// while scanner waves are still in query i.
 //   * The probed, non-empty lists are cut into chunks of 128 vectors (one
 //     scanner round) and numbered in coarse order; scanner wave w takes chunks
 //     w, w + 8, w + 16, ..., so a wave that finishes its part of a list moves
 //     on while slower waves are still in it.
-//   * Before building list f's LUT, a builder tests a lower bound on every
-//     ADC distance the list can produce against the current k-th distance
-//     (list_lower_bound).  A list that cannot contribute is skipped: no LUT,
-//     no LDS buffer, and the scanners pass over its chunks without loading
-//     codes.  The first builder wave to reach list f records the decision in
-//     dec[f] with an LDS compare-and-swap, so every wave follows the same one.
-//     Built lists are numbered j = 0, 1, ... in order and use LUT buffer j & 1.
+//   * Before building list f's LUT, builder wave 0 tests a lower bound on
+//     every ADC distance the list can produce against the current k-th
+//     distance (list_lower_bound).  A list that cannot contribute is skipped:
+//     no LUT, no LDS buffer, and the scanners pass over its chunks without
+//     loading codes.  Wave 0 records each decision in dec[f], and every wave
+//     follows it.  Built lists are numbered j = 0, 1, ... over the workgroup's
+//     whole run and use LUT buffer j & 1.
 //   * Builder waves write LUT j once every chunk of built list j - 2 (the
 //     buffer's previous user) has been scanned, then add 1 to built[b]; a
 //     scanner entering built list j waits for built[b] >= 8 (j / 2 + 1).
 //   * Scanners add the chunks of a built list they finish to done[b] when they
 //     leave it; the builder of list j waits for done[b] to reach the chunk
 //     count of the earlier built lists of buffer b.
-// Both counters are cumulative per buffer.  A count cannot run ahead of the
-// list it stands for: a builder wave contributes to built list j + 2 only
-// after all of list j is scanned, and a scanner scans list j + 2 only after it
-// is built, so the first time a threshold is met every contribution comes
-// from earlier lists of that buffer.  Deadlock-free: builders decide lists in
-// order and wait only on chunks of lists already built; scanners take chunks
-// in increasing order and report a list before waiting on the next.  Each
-// builder wave computes its own part of the residual, so builders never wait
-// on each other.
+//   * A scanner that is through query i takes a ticket t = 0..7; ticket t
+//     waits for ticket t - 1, merges its top-64 into the slot's running list,
+//     and ticket 7 writes the query's top-k and frees the slot.
+//   * Set-up of query i (builders, once the slot's previous query is freed):
+//     every builder wave computes the list bounds of its share of the probes
+//     (probe ids, then centroid rows and radii: two dependent HBM trips), wave
+//     0 adds offsets, compacts the usable lists and marks the slot ready.
+// All counters are cumulative.  A count cannot run ahead of the list it
+// stands for: a builder wave contributes to built list j + 2 only after all of
+// list j is scanned, and a scanner scans list j + 2 only after it is built, so
+// the first time a threshold is met every contribution comes from earlier
+// lists of that buffer.  Deadlock-free: builders decide lists in order and
+// wait only on chunks of lists already built, or on the end of query i - 1
+// when they set up query i + 1, whose lists were all built before query i's;
+// scanners take chunks in increasing order and report a list before waiting
+// on the next.  Each builder wave computes its own part of the residual, so
+// builders never wait on each other outside the set-up.
 constexpr int kUndecided = -1;
 constexpr int kSkipped = -2;
 
@@ -319,7 +334,6 @@ __device__ __forceinline__ int lds_wait_decided(const int* p) {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
   return v;
 }
-
 
 // list := the 64 smallest of list U the sorted list of keys held in LDS at pk.
 __device__ __forceinline__ void wave_merge_lds64(uint64_t& k, const uint64_t* pk) {
@@ -338,27 +352,42 @@ __global__ __launch_bounds__(kSpecWaves * kWave, 4) void adc_flow_kernel(AdcArgs
   // whole: TPM lanes per subspace, each with E codewords k = 4t + 4 TPM u + j
   // (u < E/4, j < 4), so every 4 entries are one 16-byte LDS write and
   // consecutive lanes write consecutive 16 bytes.  The codebook rows of those
-  // codewords stay in registers for the whole query.
+  // codewords stay in registers for the whole run.
   constexpr int SPW = M / kBuilderWaves;
   constexpr int TPM = kWave / SPW;
   constexpr int E = kPQK / TPM;
   constexpr int RW = SPW * C::S;  // residual floats per builder wave
+  constexpr int kMaxPerWave = 64 / kBuilderWaves;  // set-up: probes per builder wave (nprobe <= 64)
   static_assert(M % kBuilderWaves == 0 && (TPM == 16 || TPM == 32) && E % 4 == 0, "builder layout");
   __shared__ __align__(16) float smem[2 * C::LUT];
-  __shared__ float qs[D];
   __shared__ float rws[kBuilderWaves][16];
-  __shared__ unsigned s_min[64][M];  // per probed list: min over codewords of each LUT row (float bits)
-  __shared__ int f_list[64], f_start[64], f_n[64], f_cst[65], s_dec[64];
-  __shared__ float f_lb[64];  // list_lower_bound of each probed list
-  __shared__ int s_nv;
-  __shared__ int s_built[2], s_done[2];
-  __shared__ unsigned long long s_thr;
+  __shared__ unsigned s_min[2][M];  // per LUT buffer: min over codewords of each LUT row (float bits)
+  // Per query slot.  p_*: by probe index (set-up); f_*: compacted usable lists.
+  __shared__ float p_lb[2][64];
+  __shared__ int f_list[2][64], f_start[2][64], f_n[2][64], f_cst[2][65], s_dec[2][64];
+  __shared__ float f_lb[2][64];  // list_lower_bound of each usable list
+  __shared__ int s_nv[2];
+  __shared__ unsigned long long s_thr[2];
+  __shared__ uint64_t s_acc[2][kWave];  // running merge of the scanner lists
+  __shared__ int s_ready[2], s_free[2], s_lbdone[2], s_tick[2], s_mrg[2];
+  __shared__ int s_built[2], s_done[2];  // per LUT buffer
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const bool builder = wave < kBuilderWaves;
-  const int q = blockIdx.x;
   const long long t_start = a.stats ? clock64() : 0;
   const int P = a.nprobe, k = a.k;
   const uint32_t NL = (uint32_t)a.nlist;
+  const int G = (int)gridDim.x;
+  const int nqw = a.nq > (int)blockIdx.x ? (a.nq - (int)blockIdx.x + G - 1) / G : 0;  // this workgroup's queries
+
+  if (tid < 2) {
+    s_nv[tid] = 0;
+    s_ready[tid] = 0;
+    s_free[tid] = 0;
+    s_lbdone[tid] = 0;
+    s_built[tid] = 0;
+    s_done[tid] = 0;
+  }
+  __syncthreads();
 
   // Builder codebook registers: loaded first, so the loads overlap the set-up.
   const int ms = wave * SPW + lane / TPM, t = lane % TPM;
@@ -374,253 +403,315 @@ __global__ __launch_bounds__(kSpecWaves * kWave, 4) void adc_flow_kernel(AdcArgs
       }
     }
   }
-  for (int i = tid; i < D; i += kSpecWaves * kWave) qs[i] = a.queries[(size_t)q * D + i];
-  for (int i = tid; i < 64 * M; i += kSpecWaves * kWave) (&s_min[0][0])[i] = 0x7F800000u;  // +inf
-  if (tid < 64) s_dec[tid] = kUndecided;
-  if (wave == 0) {
-    // Compact the usable probes (in range, non-empty) in coarse order and
-    // number their chunks: f_cst[f] = first chunk of list f.
-    int l = 0, st = 0, n = 0;
-    if (lane < P) {
-      const uint32_t pl = a.probes[(size_t)q * P + lane];
-      if (pl < NL) {
-        l = (int)pl;
-        st = a.offsets[pl];
-        n = a.offsets[pl + 1] - st;
-      }
-    }
-    const bool valid = n > 0;
-    const uint64_t bm = __ballot(valid);
-    const int pos = __popcll(bm & ((1ull << lane) - 1ull));
-    const int nch = valid ? (n + kChunk - 1) / kChunk : 0;
-    const int incl = wave_incl_scan(nch);
-    if (valid) {
-      f_list[pos] = l;
-      f_start[pos] = st;
-      f_n[pos] = n;
-      f_cst[pos] = incl - nch;
-    }
-    const int nv = __popcll(bm);
-    const int total = __shfl(incl, kWave - 1, kWave);
-    if (lane == 0) {
-      f_cst[nv] = total;
-      s_nv = nv;
-      s_built[0] = 0;
-      s_built[1] = 0;
-      s_done[0] = 0;
-      s_done[1] = 0;
-      s_thr = kNoThr;
-    }
-  }
-  __syncthreads();
-  const int nv = s_nv;
-  // Lower bound of every probed list, one list per wave at a time.
-  for (int f = wave; f < nv; f += kSpecWaves) {
-    const int l = f_list[f];
-    const float* cr = a.centroids + (size_t)l * D;
-    const float ra = lane < D ? qs[lane] - cr[lane] : 0.0f;
-    const float rb = lane + kWave < D ? qs[lane + kWave] - cr[lane + kWave] : 0.0f;
-    float s2 = ra * ra + rb * rb;
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) s2 += shfl_xor_f(s2, o);  // same value in every lane
-    if (lane == 0) f_lb[f] = list_lower_bound(s2, a.rmax[l]);
-  }
-  __syncthreads();
 
-  const long long t_setup = a.stats ? clock64() : 0;
-  // First list >= from (below nv) whose decision is not "skipped" and for which
-  // `want` holds; nv if there is none.  One LDS round trip for up to 64 lists.
-  auto next_list = [&](int from, auto want) {
+  // First usable list >= from (below nv) of slot s whose decision is not
+  // "skipped" and for which `want` holds; nv if none.  One LDS round trip for
+  // up to 64 lists.
+  auto next_list = [&](int s, int nv, int from, auto want) {
     const int g = from + lane;
-    const bool cand = g < nv && want(g) && __hip_atomic_load(&s_dec[g], __ATOMIC_RELAXED,
+    const bool cand = g < nv && want(g) && __hip_atomic_load(&s_dec[s][g], __ATOMIC_RELAXED,
                                                              __HIP_MEMORY_SCOPE_WORKGROUP) != kSkipped;
     const uint64_t bm = __ballot(cand);
     return bm ? from + __ffsll((unsigned long long)bm) - 1 : nv;
   };
 
-  uint64_t lk = kPadKey;
   if (builder) {
     float* rw = rws[wave];
-    const float qv = lane < RW ? qs[wave * RW + lane] : 0.0f;
     auto any_list = [](int) { return true; };
-    // This wave's centroid coordinates of the next list that may be built,
-    // loaded ahead (cnext belongs to list cnext_f).
-    int cnext_f = nv > 0 ? 0 : nv;
-    float cnext = 0.0f;
-    if (nv > 0 && lane < RW) cnext = a.centroids[(size_t)f_list[0] * D + wave * RW + lane];
-    int nbuilt = 0, need0 = 0, need1 = 0, nskip = 0;
-    int f = 0;
-    while (f < nv) {
-      int dec;
-      if (wave == 0) {
-        // Builder wave 0 decides, a run at a time: the lists from f on whose
-        // bound exceeds the current threshold are skipped, and the first one
-        // that does not is built as list number nbuilt.  Later lists wait for
-        // a later (tighter) threshold.
-        dec = s_dec[f];
-        if (dec == kUndecided) {
-          const uint64_t thr = s_thr;
-          const float thr_hi = __uint_as_float((uint32_t)(thr >> 32)) * (1.0f + 0x1p-16f);
-          const int g = f + lane;
-          const bool cand = g < nv && f_lb[g] > thr_hi;
-          const uint64_t run = ~__ballot(cand);  // bit i clear: list f + i is skippable
-          const int p = run ? __ffsll((unsigned long long)run) - 1 : kWave;
-          if (lane < p && g < nv) s_dec[g] = kSkipped;
-          if (lane == p && g < nv) s_dec[g] = nbuilt;
-          __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-          dec = p > 0 ? kSkipped : nbuilt;
-          nskip += min(p, nv - f);
+    // Set-up of this workgroup's query i into slot i & 1 (all builder waves).
+    auto setup = [&](int i) {
+      const int s = i & 1, q = (int)blockIdx.x + i * G;
+      lds_wait_at_least(&s_free[s], i / 2);  // the slot's previous query is written out
+      const uint32_t* pr = a.probes + (size_t)q * P;
+      const uint32_t pl_lane = lane < P ? pr[lane] : kPruned;
+      const float qa = lane < D ? a.queries[(size_t)q * D + lane] : 0.0f;
+      const float qb = lane + kWave < D ? a.queries[(size_t)q * D + lane + kWave] : 0.0f;
+      // Centroid rows and radii of this wave's probes p = wave + 8 j, loaded
+      // four lists at a time.
+      constexpr int kBatch = 4;
+#pragma unroll 1
+      for (int j0 = 0; j0 < kMaxPerWave && wave + kBuilderWaves * j0 < P; j0 += kBatch) {
+        float ca[kBatch], cc[kBatch], rl[kBatch];
+#pragma unroll
+        for (int j = 0; j < kBatch; ++j) {
+          const int p = wave + kBuilderWaves * (j0 + j);
+          const uint32_t pl = (uint32_t)__builtin_amdgcn_readlane((int)pl_lane, p);
+          ca[j] = cc[j] = rl[j] = 0.0f;
+          if (p < P && pl < NL) {
+            const float* cr = a.centroids + (size_t)pl * D;
+            ca[j] = lane < D ? cr[lane] : 0.0f;
+            cc[j] = lane + kWave < D ? cr[lane + kWave] : 0.0f;
+            rl[j] = a.rmax[pl];
+          }
         }
-      } else {
-        dec = lds_wait_decided(&s_dec[f]);
-      }
-      if (dec < 0) {
-        f = next_list(f + 1, any_list);
-        continue;
-      }
-      const int b = dec & 1;
-      ++nbuilt;
-      float cs = cnext;
-      if (cnext_f != f && lane < RW) cs = a.centroids[(size_t)f_list[f] * D + wave * RW + lane];
-      cnext_f = next_list(f + 1, any_list);
-      if (cnext_f < nv && lane < RW) cnext = a.centroids[(size_t)f_list[cnext_f] * D + wave * RW + lane];
-      // Residual q - c of this wave's subspaces, shared through the wave's own
-      // LDS slot (a wave's LDS accesses complete in order).
-      if (lane < RW) rw[lane] = qv - cs;
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-      float r[C::S];
 #pragma unroll
-      for (int d = 0; d < C::S; ++d) r[d] = rw[(lane / TPM) * C::S + d];
-      lds_wait_at_least(&s_done[b], b ? need1 : need0);
-      float* lut = smem + b * C::LUT + ms * kPQK + 4 * t;
-      float mn = __builtin_inff();
+        for (int j = 0; j < kBatch; ++j) {
+          const int p = wave + kBuilderWaves * (j0 + j);
+          if (p < P) {
+            const float ra = lane < D ? qa - ca[j] : 0.0f;
+            const float rb = lane + kWave < D ? qb - cc[j] : 0.0f;
+            float s2 = ra * ra + rb * rb;
 #pragma unroll
-      for (int u = 0; u < E / 4; ++u) {
-        float4 v;
-        v.x = lut_entry<C::S>(r, cb + (4 * u + 0) * C::S);
-        v.y = lut_entry<C::S>(r, cb + (4 * u + 1) * C::S);
-        v.z = lut_entry<C::S>(r, cb + (4 * u + 2) * C::S);
-        v.w = lut_entry<C::S>(r, cb + (4 * u + 3) * C::S);
-        mn = fminf(mn, fminf(fminf(v.x, v.y), fminf(v.z, v.w)));
-        *reinterpret_cast<float4*>(lut + 4 * TPM * u) = v;
+            for (int o = 32; o > 0; o >>= 1) s2 += shfl_xor_f(s2, o);  // same value in every lane
+            if (lane == 0) p_lb[s][p] = list_lower_bound(s2, rl[j]);
+          }
+        }
       }
-      // Row minimum of subspace ms: over the TPM lanes that share it.
-      mn = fminf(mn, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(mn), 0x128, 0xF, 0xF, false)));  // row_ror:8
-      mn = fminf(mn, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(mn), 0x124, 0xF, 0xF, false)));  // row_ror:4
-      mn = fminf(mn, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(mn), 0x122, 0xF, 0xF, false)));  // row_ror:2
-      mn = fminf(mn, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(mn), 0x121, 0xF, 0xF, false)));  // row_ror:1
-      if constexpr (TPM == 32) {  // rows 2i and 2i+1 share a subspace
-        const auto rr = __builtin_amdgcn_permlane16_swap(__float_as_uint(mn), __float_as_uint(mn), false, false);
-        mn = fminf(__uint_as_float(rr[0]), __uint_as_float(rr[1]));
+      lds_signal_add(&s_lbdone[s], 1);
+      if (wave == 0) {
+        // Compact the usable probes (in range, non-empty) in coarse order and
+        // number their chunks: f_cst[f] = first chunk of list f.
+        int st = 0, n = 0;
+        if (pl_lane < NL) {
+          st = a.offsets[pl_lane];
+          n = a.offsets[pl_lane + 1] - st;
+        }
+        const bool valid = n > 0;
+        const uint64_t bm = __ballot(valid);
+        const int pos = __popcll(bm & ((1ull << lane) - 1ull));
+        const int nch = valid ? (n + kChunk - 1) / kChunk : 0;
+        const int incl = wave_incl_scan(nch);
+        // Every builder wave has signalled this set-up, so each has left the
+        // loop of query i - 1 and of query i - 2, the slot's previous user:
+        // no wave reads its decisions any more.
+        lds_wait_at_least(&s_lbdone[s], kBuilderWaves * (i / 2 + 1));
+        s_dec[s][lane] = kUndecided;
+        if (valid) {
+          f_list[s][pos] = (int)pl_lane;
+          f_start[s][pos] = st;
+          f_n[s][pos] = n;
+          f_cst[s][pos] = incl - nch;
+          f_lb[s][pos] = p_lb[s][lane];
+        }
+        const int nv = __popcll(bm);
+        const int total = __shfl(incl, kWave - 1, kWave);
+        if (lane == 0) {
+          f_cst[s][nv] = total;
+          s_nv[s] = nv;
+          s_thr[s] = kNoThr;
+          s_tick[s] = 0;
+          s_mrg[s] = 0;
+        }
+        lds_signal_add(&s_ready[s], 1);
       }
-      if (t == 0) s_min[f][ms] = __float_as_uint(mn);
-      lds_signal_add(&s_built[b], 1);
-      const int nch = f_cst[f + 1] - f_cst[f];
-      if (b) need1 += nch; else need0 += nch;
-      f = cnext_f;
+    };
+
+    int nbuilt = 0, need0 = 0, need1 = 0, nskip = 0;
+    long long t_su = 0;
+    if (nqw > 0) setup(0);
+    for (int i = 0; i < nqw; ++i) {
+      const int s = i & 1, q = (int)blockIdx.x + i * G;
+      lds_wait_at_least(&s_ready[s], i / 2 + 1);
+      const int nv = s_nv[s];
+      const float qv = lane < RW ? a.queries[(size_t)q * D + wave * RW + lane] : 0.0f;
+      // This wave's centroid coordinates of the next list that may be built,
+      // loaded ahead (cnext belongs to list cnext_f).
+      int cnext_f = nv > 0 ? 0 : nv;
+      float cnext = 0.0f;
+      if (nv > 0 && lane < RW) cnext = a.centroids[(size_t)f_list[s][0] * D + wave * RW + lane];
+      int f = 0;
+      while (f < nv) {
+        int dec;
+        if (wave == 0) {
+          // Builder wave 0 decides, a run at a time: the lists from f on whose
+          // bound exceeds the current threshold are skipped, and the first one
+          // that does not is built as list number nbuilt.  Later lists wait for
+          // a later (tighter) threshold.
+          dec = s_dec[s][f];
+          if (dec == kUndecided) {
+            const uint64_t thr = s_thr[s];
+            const float thr_hi = __uint_as_float((uint32_t)(thr >> 32)) * (1.0f + 0x1p-16f);
+            const int g = f + lane;
+            const bool cand = g < nv && f_lb[s][g] > thr_hi;
+            const uint64_t run = ~__ballot(cand);  // bit i clear: list f + i is skippable
+            const int p = run ? __ffsll((unsigned long long)run) - 1 : kWave;
+            if (lane < p && g < nv) s_dec[s][g] = kSkipped;
+            if (lane == p && g < nv) s_dec[s][g] = nbuilt;
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+            dec = p > 0 ? kSkipped : nbuilt;
+            nskip += min(p, nv - f);
+          }
+        } else {
+          dec = lds_wait_decided(&s_dec[s][f]);
+        }
+        if (dec < 0) {
+          f = next_list(s, nv, f + 1, any_list);
+          continue;
+        }
+        const int b = dec & 1;
+        ++nbuilt;
+        float cs = cnext;
+        if (cnext_f != f && lane < RW) cs = a.centroids[(size_t)f_list[s][f] * D + wave * RW + lane];
+        cnext_f = next_list(s, nv, f + 1, any_list);
+        if (cnext_f < nv && lane < RW) cnext = a.centroids[(size_t)f_list[s][cnext_f] * D + wave * RW + lane];
+        // Residual q - c of this wave's subspaces, shared through the wave's own
+        // LDS slot (a wave's LDS accesses complete in order).
+        if (lane < RW) rw[lane] = qv - cs;
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        float r[C::S];
+#pragma unroll
+        for (int d = 0; d < C::S; ++d) r[d] = rw[(lane / TPM) * C::S + d];
+        lds_wait_at_least(&s_done[b], b ? need1 : need0);
+        float* lut = smem + b * C::LUT + ms * kPQK + 4 * t;
+        float mn = __builtin_inff();
+#pragma unroll
+        for (int u = 0; u < E / 4; ++u) {
+          float4 v;
+          v.x = lut_entry<C::S>(r, cb + (4 * u + 0) * C::S);
+          v.y = lut_entry<C::S>(r, cb + (4 * u + 1) * C::S);
+          v.z = lut_entry<C::S>(r, cb + (4 * u + 2) * C::S);
+          v.w = lut_entry<C::S>(r, cb + (4 * u + 3) * C::S);
+          mn = fminf(mn, fminf(fminf(v.x, v.y), fminf(v.z, v.w)));
+          *reinterpret_cast<float4*>(lut + 4 * TPM * u) = v;
+        }
+        // Row minimum of subspace ms: over the TPM lanes that share it.
+        mn = fminf(mn, __int_as_float(dpp_mov<0x128>(__float_as_int(mn))));  // row_ror:8
+        mn = fminf(mn, __int_as_float(dpp_mov<0x124>(__float_as_int(mn))));  // row_ror:4
+        mn = fminf(mn, __int_as_float(dpp_mov<0x122>(__float_as_int(mn))));  // row_ror:2
+        mn = fminf(mn, __int_as_float(dpp_mov<0x121>(__float_as_int(mn))));  // row_ror:1
+        if constexpr (TPM == 32) {  // rows 2i and 2i+1 share a subspace
+          const auto rr = __builtin_amdgcn_permlane16_swap(__float_as_uint(mn), __float_as_uint(mn), false, false);
+          mn = fminf(__uint_as_float(rr[0]), __uint_as_float(rr[1]));
+        }
+        if (t == 0) s_min[b][ms] = __float_as_uint(mn);
+        lds_signal_add(&s_built[b], 1);
+        const int nch = f_cst[s][f + 1] - f_cst[s][f];
+        if (b) need1 += nch; else need0 += nch;
+        f = cnext_f;
+      }
+      if (i + 1 < nqw) {
+        const long long t0 = a.stats ? clock64() : 0;
+        setup(i + 1);
+        if (a.stats) t_su += clock64() - t0;
+      }
     }
     if (a.stats && wave == 0 && lane == 0) {
       atomicAdd(&a.stats[1], (unsigned long long)nbuilt);
       atomicAdd(&a.stats[2], (unsigned long long)nskip);
-      atomicAdd(&a.stats[3], (unsigned long long)(t_setup - t_start));
-      atomicAdd(&a.stats[4], (unsigned long long)(clock64() - t_setup));
+      atomicAdd(&a.stats[3], (unsigned long long)t_su);
+      atomicAdd(&a.stats[4], (unsigned long long)(clock64() - t_start));
     }
   } else {
     const int swave = wave - kBuilderWaves;
-    // This wave's first chunk at or after chunk cc; whether it has one in list g.
+    // This wave's first chunk at or after chunk cc.
     auto first_own = [&](int cc) { return cc + (((swave - cc) % kScanWaves) + kScanWaves) % kScanWaves; };
-    auto has_chunk = [&](int g) { return first_own(f_cst[g]) < f_cst[g + 1]; };
-    uint64_t own = kNoThr;
     uint4 w0[C::NV4], w1[C::NV4];
     int i0 = kPadId, i1 = kPadId;
-    int have_c = -1;  // chunk whose codes w0/w1/i0/i1 hold (or are being loaded)
     float T[M / 8];   // T[g] = sum of list f's row minima over subspaces 8g .. M-1
     unsigned nload = 0;  // vectors whose codes this wave loaded
-    auto chunk_vecs = [&](int g, int cc) { return (unsigned)min(kChunk, f_n[g] - (cc - f_cst[g]) * kChunk); };
-    int f = next_list(0, has_chunk);
-    while (f < nv) {
-      const int dec = lds_wait_decided(&s_dec[f]);
-      if (dec < 0) {
-        f = next_list(f + 1, has_chunk);
-        continue;
-      }
-      const int start = f_start[f], n = f_n[f], c_end = f_cst[f + 1];
-      int c = first_own(f_cst[f]);
-      if (have_c != c) {
-        load_pair<M>(a.codes, a.vec_ids, start, n, (c - f_cst[f]) * kChunk + lane, w0, w1, i0, i1);
-        nload += chunk_vecs(f, c);
-      }
-      lds_wait_at_least(&s_built[dec & 1], kBuilderWaves * (dec / 2 + 1));
-      float acc = 0.0f;
-#pragma unroll
-      for (int m = M - 1; m >= 0; --m) {
-        acc += __uint_as_float(s_min[f][m]);
-        if (m % 8 == 0) T[m / 8] = acc;
-      }
-      int mine = 0;
-      while (true) {
-        const uint64_t shared_thr = s_thr;
-        const uint64_t thr = own < shared_thr ? own : shared_thr;
-        const float thr_hi = __uint_as_float((uint32_t)(thr >> 32)) * (1.0f + 0x1p-16f);
-        if (T[0] > thr_hi) {
-          // Every vector of list f is at least T[0]: this wave's remaining
-          // chunks of it are done without loading codes (the threshold never
-          // rises).
-          mine += (c_end - c + kScanWaves - 1) / kScanWaves;
-          break;
+    for (int i = 0; i < nqw; ++i) {
+      const int s = i & 1, q = (int)blockIdx.x + i * G;
+      lds_wait_at_least(&s_ready[s], i / 2 + 1);
+      const int nv = s_nv[s];
+      const int* cst = f_cst[s];
+      auto has_chunk = [&](int g) { return first_own(cst[g]) < cst[g + 1]; };
+      auto chunk_vecs = [&](int g, int cc) { return (unsigned)min(kChunk, f_n[s][g] - (cc - cst[g]) * kChunk); };
+      uint64_t lk = kPadKey, own = kNoThr;
+      int have_c = -1;  // chunk whose codes w0/w1/i0/i1 hold (or are being loaded)
+      int f = next_list(s, nv, 0, has_chunk);
+      while (f < nv) {
+        const int dec = lds_wait_decided(&s_dec[s][f]);
+        if (dec < 0) {
+          f = next_list(s, nv, f + 1, has_chunk);
+          continue;
         }
-        const int v0 = (c - f_cst[f]) * kChunk + lane;
-        if (dec & 1)
-          scan_round_lb<D, M, 1>(smem, v0, n, k, w0, w1, i0, i1, thr, thr_hi, T, lk, own, &s_thr);
-        else
-          scan_round_lb<D, M, 0>(smem, v0, n, k, w0, w1, i0, i1, thr, thr_hi, T, lk, own, &s_thr);
-        ++mine;
-        c += kScanWaves;
-        if (c >= c_end) break;
-        load_pair<M>(a.codes, a.vec_ids, start, n, (c - f_cst[f]) * kChunk + lane, w0, w1, i0, i1);
-        nload += chunk_vecs(f, c);
+        const int start = f_start[s][f], n = f_n[s][f], c_end = cst[f + 1];
+        int c = first_own(cst[f]);
+        if (have_c != c) {
+          load_pair<M>(a.codes, a.vec_ids, start, n, (c - cst[f]) * kChunk + lane, w0, w1, i0, i1);
+          nload += chunk_vecs(f, c);
+        }
+        lds_wait_at_least(&s_built[dec & 1], kBuilderWaves * (dec / 2 + 1));
+        float acc = 0.0f;
+#pragma unroll
+        for (int m = M - 1; m >= 0; --m) {
+          acc += __uint_as_float(s_min[dec & 1][m]);
+          if (m % 8 == 0) T[m / 8] = acc;
+        }
+        int mine = 0;
+        while (true) {
+          const uint64_t shared_thr = s_thr[s];
+          const uint64_t thr = own < shared_thr ? own : shared_thr;
+          const float thr_hi = __uint_as_float((uint32_t)(thr >> 32)) * (1.0f + 0x1p-16f);
+          if (T[0] > thr_hi) {
+            // Every vector of list f is at least T[0]: this wave's remaining
+            // chunks of it are done without loading codes (the threshold never
+            // rises).
+            mine += (c_end - c + kScanWaves - 1) / kScanWaves;
+            break;
+          }
+          const int v0 = (c - cst[f]) * kChunk + lane;
+          if (dec & 1)
+            scan_round_lb<D, M, 1>(smem, v0, n, k, w0, w1, i0, i1, thr, thr_hi, T, lk, own, &s_thr[s]);
+          else
+            scan_round_lb<D, M, 0>(smem, v0, n, k, w0, w1, i0, i1, thr, thr_hi, T, lk, own, &s_thr[s]);
+          ++mine;
+          c += kScanWaves;
+          if (c >= c_end) break;
+          load_pair<M>(a.codes, a.vec_ids, start, n, (c - cst[f]) * kChunk + lane, w0, w1, i0, i1);
+          nload += chunk_vecs(f, c);
+        }
+        // List f done by this wave: its LUT buffer may be reused once all its
+        // chunks are in.
+        lds_signal_add(&s_done[dec & 1], mine);
+        // Next list; its first codes go out now if it is already known to be built.
+        f = next_list(s, nv, f + 1, has_chunk);
+        have_c = -1;
+        if (f < nv && __hip_atomic_load(&s_dec[s][f], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >= 0) {
+          have_c = first_own(cst[f]);
+          load_pair<M>(a.codes, a.vec_ids, f_start[s][f], f_n[s][f], (have_c - cst[f]) * kChunk + lane, w0, w1, i0,
+                       i1);
+          nload += chunk_vecs(f, have_c);
+        }
       }
-      // List f done by this wave: its LUT buffer may be reused once all its
-      // chunks are in.
-      lds_signal_add(&s_done[dec & 1], mine);
-      // Next list; its first codes go out now if it is already known to be built.
-      f = next_list(f + 1, has_chunk);
-      have_c = -1;
-      if (f < nv && __hip_atomic_load(&s_dec[f], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >= 0) {
-        have_c = first_own(f_cst[f]);
-        load_pair<M>(a.codes, a.vec_ids, f_start[f], f_n[f], (have_c - f_cst[f]) * kChunk + lane, w0, w1, i0, i1);
-        nload += chunk_vecs(f, have_c);
+      // Through query i: merge into the slot's running list in ticket order.
+      int tk = 0;
+      if (lane == 0) tk = __hip_atomic_fetch_add(&s_tick[s], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      tk = __builtin_amdgcn_readfirstlane(tk);
+      if (tk > 0) {
+        lds_wait_at_least(&s_mrg[s], tk);
+        wave_merge_lds64(lk, s_acc[s]);
+      }
+      if (tk == kScanWaves - 1) {
+        write_topk(lk, q, k, a);
+        lds_signal_add(&s_free[s], 1);
+        if (a.stats && lane == 0 && i == nqw - 1) atomicAdd(&a.stats[6], (unsigned long long)(clock64() - t_start));
+      } else {
+        s_acc[s][lane] = lk;
+        lds_signal_add(&s_mrg[s], 1);
       }
     }
     if (a.stats && lane == 0) {
       atomicAdd(&a.stats[0], (unsigned long long)nload);
-      if (wave == kBuilderWaves) atomicAdd(&a.stats[5], (unsigned long long)(clock64() - t_setup));
+      if (wave == kBuilderWaves) atomicAdd(&a.stats[5], (unsigned long long)(clock64() - t_start));
     }
   }
+}
 
-  // Merge the scanner waves' lists: a 3-level tree, pairs merged in parallel.
-  uint64_t* mk = reinterpret_cast<uint64_t*>(smem);
-  const int sw = wave - kBuilderWaves;
-  __syncthreads();
-  if (!builder) mk[sw * kWave + lane] = lk;
-#pragma unroll
-  for (int step = 1; step < kScanWaves; step <<= 1) {
-    __syncthreads();
-    const bool active = !builder && (sw % (2 * step)) == 0;
-    if (active) wave_merge_lds64(lk, mk + (sw + step) * kWave);
-    __syncthreads();
-    if (active) mk[sw * kWave + lane] = lk;
-  }
-  if (sw == 0) write_topk(lk, q, k, a);
-  if (a.stats && tid == 0) atomicAdd(&a.stats[6], (unsigned long long)(clock64() - t_start));
+// Workgroups resident at once for a kernel (one query each at a time): the
+// persistent flow kernel launches no more than that.
+template <class K>
+int resident_groups(K kernel, int threads, std::atomic<int> (&cached)[64]) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  int v = cached[dev].load(std::memory_order_relaxed);
+  if (v > 0) return v;
+  int cus = 0, per = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, kernel, threads, 0) != hipSuccess || per <= 0) per = 1;
+  v = cus * per;
+  cached[dev].store(v, std::memory_order_relaxed);
+  return v;
 }
 
 template <int D, int M>
 fgpu_status launch_flow(const AdcArgs& a, hipStream_t s) {
   FGPU_CHECK(a.nprobe <= 64, FGPU_ERR_UNSUPPORTED, "adc: nprobe must be <= 64");
-  hipLaunchKernelGGL((adc_flow_kernel<D, M>), dim3((unsigned)a.nq), dim3(kSpecWaves * kWave), 0, s, a);
+  static std::atomic<int> cached[64];
+  const int grid = std::min(a.nq, resident_groups(adc_flow_kernel<D, M>, kSpecWaves * kWave, cached));
+  hipLaunchKernelGGL((adc_flow_kernel<D, M>), dim3((unsigned)grid), dim3(kSpecWaves * kWave), 0, s, a);
   FGPU_HIP(hipGetLastError());
   return FGPU_OK;
 }

@@ -113,6 +113,32 @@ def test_adc_search_bit_exact(dim, m, k):
     idx.close()
 
 
+@pytest.mark.parametrize("dim,m,k", [(128, 32, 10), (96, 16, 33)])
+def test_adc_search_many_queries_per_workgroup(dim, m, k):
+    """More queries than resident workgroups: each workgroup runs a dozen
+    queries back to back through its two per-query state slots."""
+    _say(f"adc many queries dim={dim} m={m} k={k}")
+    rng = np.random.default_rng(dim + m + k + 5)
+    nlist = 64
+    offs, ids, lc, cent, cb = _random_index(rng, 40000, dim, m, nlist, empty=(5,), big=9)
+    nq = 3000
+    q = rng.standard_normal((nq, dim)).astype(np.float32) * 0.7
+    probes, _ = oracle.coarse(q, cent, 16)
+    probes[300:303, :] = 0xFFFFFFFF       # consecutive queries with nothing to scan
+    probes[700, 1:] = 0xFFFFFFFF          # one list only
+    probes[1500, :] = probes[1500, 0]     # one list, probed 16 times
+    probes[2999, 0] = 5                   # an empty list first, on the last query
+    idx = fg.Index.from_arrays(dim, m, offs, ids, lc, cent, cb)
+    gid, gd = idx.adc_search(torch.from_numpy(q).cuda(), torch.from_numpy(probes.view(np.int32)).cuda(), k)
+    gid, gd = _host(gid), _host(gd)
+    oid, od = oracle.search_plain(q, cent, cb, offs, ids, lc, probes, k)
+    bad = np.nonzero(~np.all(gid == oid, axis=1))[0]
+    assert bad.size == 0, f"first mismatching queries {bad[:5]}: gpu {gid[bad[0]]} oracle {oid[bad[0]]}"
+    assert np.array_equal(_bits(gd), _bits(od))
+    assert np.all(gid[300:303] == -1)
+    idx.close()
+
+
 def test_search_fused_equals_stages():
     _say("fused search")
     rng = np.random.default_rng(21)
