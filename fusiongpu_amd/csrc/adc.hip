@@ -156,12 +156,19 @@ __device__ __forceinline__ void scan_round_lb(const float* smem, int v0, int n, 
 // wave that spins kSpinLimit times gives up and carries on, so every wave
 // reaches the end of the kernel whatever the counters say (with correct
 // counting the longest legitimate wait is the scan of one list, microseconds).
+// Each poll is an LDS read and a few VALU instructions taken from the waves
+// that do the work, so waits off the critical path (builders waiting for
+// scanners) poll kLazySleep times less often: s_sleep N idles about 64 N
+// clocks.
 constexpr int kSpinLimit = 1 << 16;
+constexpr int kLazySleep = 8;
 
+template <int SLEEP = 1>
 __device__ __forceinline__ void lds_wait_at_least(const int* p, int target) {
   int spins = 0;
-  while (__hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < target && ++spins < kSpinLimit)
-    __builtin_amdgcn_s_sleep(1);
+  while (__hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < target &&
+         ++spins < kSpinLimit / SLEEP)
+    __builtin_amdgcn_s_sleep(SLEEP);
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
 }
 
@@ -326,11 +333,12 @@ constexpr int kScanWaves = kSpecWaves - kBuilderWaves;
 constexpr int kUndecided = -1;
 constexpr int kSkipped = -2;
 
+template <int SLEEP = 1>
 __device__ __forceinline__ int lds_wait_decided(const int* p) {
   int spins = 0, v;
   while ((v = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)) == kUndecided &&
-         ++spins < kSpinLimit)
-    __builtin_amdgcn_s_sleep(1);
+         ++spins < kSpinLimit / SLEEP)
+    __builtin_amdgcn_s_sleep(SLEEP);
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
   return v;
 }
@@ -421,7 +429,7 @@ __global__ __launch_bounds__(kSpecWaves * kWave, 4) void adc_flow_kernel(AdcArgs
     // Set-up of this workgroup's query i into slot i & 1 (all builder waves).
     auto setup = [&](int i) {
       const int s = i & 1, q = (int)blockIdx.x + i * G;
-      lds_wait_at_least(&s_free[s], i / 2);  // the slot's previous query is written out
+      lds_wait_at_least<kLazySleep>(&s_free[s], i / 2);  // the slot's previous query is written out
       const uint32_t* pr = a.probes + (size_t)q * P;
       const uint32_t pl_lane = lane < P ? pr[lane] : kPruned;
       const float qa = lane < D ? a.queries[(size_t)q * D + lane] : 0.0f;
@@ -474,7 +482,7 @@ __global__ __launch_bounds__(kSpecWaves * kWave, 4) void adc_flow_kernel(AdcArgs
         // Every builder wave has signalled this set-up, so each has left the
         // loop of query i - 1 and of query i - 2, the slot's previous user:
         // no wave reads its decisions any more.
-        lds_wait_at_least(&s_lbdone[s], kBuilderWaves * (i / 2 + 1));
+        lds_wait_at_least<kLazySleep>(&s_lbdone[s], kBuilderWaves * (i / 2 + 1));
         s_dec[s][lane] = kUndecided;
         if (valid) {
           f_list[s][pos] = (int)pl_lane;
@@ -532,7 +540,7 @@ __global__ __launch_bounds__(kSpecWaves * kWave, 4) void adc_flow_kernel(AdcArgs
             nskip += min(p, nv - f);
           }
         } else {
-          dec = lds_wait_decided(&s_dec[s][f]);
+          dec = lds_wait_decided<kLazySleep>(&s_dec[s][f]);
         }
         if (dec < 0) {
           f = next_list(s, nv, f + 1, any_list);
@@ -553,7 +561,7 @@ __global__ __launch_bounds__(kSpecWaves * kWave, 4) void adc_flow_kernel(AdcArgs
         float r[C::S];
 #pragma unroll
         for (int d = 0; d < C::S; ++d) r[d] = rw[(lane / TPM) * C::S + d];
-        lds_wait_at_least(&s_done[b], b ? need1 : need0);
+        lds_wait_at_least<kLazySleep>(&s_done[b], b ? need1 : need0);
         float* lut = smem + b * C::LUT + ms * kPQK + 4 * t;
         float mn = __builtin_inff();
 #pragma unroll
