@@ -313,9 +313,10 @@ constexpr int kScanWaves = kSpecWaves - kBuilderWaves;
 //   * Scanners add the chunks of a built list they finish to done[b] when they
 //     leave it; the builder of list j waits for done[b] to reach the chunk
 //     count of the earlier built lists of buffer b.
-//   * A scanner that is through query i takes a ticket t = 0..7; ticket t
-//     waits for ticket t - 1, merges its top-64 into the slot's running list,
-//     and ticket 7 writes the query's top-k and frees the slot.
+//   * A scanner that is through query i climbs a binary merge tree over the 8
+//     scanner lists: at each node the second of the two children to arrive
+//     merges both and climbs on, the first is done; nobody waits.  The
+//     second arrival at the root writes the query's top-k and frees the slot.
 //   * Set-up of query i (builders, once the slot's previous query is freed):
 //     every builder wave computes the list bounds of its share of the probes
 //     (probe ids, then centroid rows and radii: two dependent HBM trips), wave
@@ -376,8 +377,11 @@ __global__ __launch_bounds__(kSpecWaves * kWave, 4) void adc_flow_kernel(AdcArgs
   __shared__ float f_lb[2][64];  // list_lower_bound of each usable list
   __shared__ int s_nv[2];
   __shared__ unsigned long long s_thr[2];
-  __shared__ uint64_t s_acc[2][kWave];  // running merge of the scanner lists
-  __shared__ int s_ready[2], s_free[2], s_lbdone[2], s_tick[2], s_mrg[2];
+  // Merge tree of the scanner lists: node n has two child lists; level 0 is
+  // nodes 0-3 (waves 2j, 2j+1), level 1 nodes 4-5, the root node 6.
+  __shared__ uint64_t s_tree[2][kScanWaves - 1][2][kWave];
+  __shared__ int s_arr[2][kScanWaves - 1];  // arrivals per tree node
+  __shared__ int s_ready[2], s_free[2], s_lbdone[2];
   __shared__ int s_built[2], s_done[2];  // per LUT buffer
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const bool builder = wave < kBuilderWaves;
@@ -493,12 +497,12 @@ __global__ __launch_bounds__(kSpecWaves * kWave, 4) void adc_flow_kernel(AdcArgs
         }
         const int nv = __popcll(bm);
         const int total = __shfl(incl, kWave - 1, kWave);
+        if (lane < kScanWaves - 1) s_arr[s][lane] = 0;
         if (lane == 0) {
           f_cst[s][nv] = total;
           s_nv[s] = nv;
           s_thr[s] = kNoThr;
-          s_tick[s] = 0;
-          s_mrg[s] = 0;
+
         }
         lds_signal_add(&s_ready[s], 1);
       }
@@ -674,21 +678,32 @@ __global__ __launch_bounds__(kSpecWaves * kWave, 4) void adc_flow_kernel(AdcArgs
           nload += chunk_vecs(f, have_c);
         }
       }
-      // Through query i: merge into the slot's running list in ticket order.
-      int tk = 0;
-      if (lane == 0) tk = __hip_atomic_fetch_add(&s_tick[s], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-      tk = __builtin_amdgcn_readfirstlane(tk);
-      if (tk > 0) {
-        lds_wait_at_least(&s_mrg[s], tk);
-        wave_merge_lds64(lk, s_acc[s]);
+      // Through query i: climb the merge tree without waiting.  At each node
+      // the wave deposits its list, then counts itself in; the first of the
+      // two children to arrive is done with the query, the second merges its
+      // sibling's list and climbs on.  The second arrival at the root holds
+      // all eight lists merged: it writes the top-k and frees the slot.
+      bool root = true;
+      int base = 0;
+#pragma unroll
+      for (int lvl = 0, width = kScanWaves / 2; width >= 1; ++lvl, base += width, width >>= 1) {
+        const int nd = base + (swave >> (lvl + 1)), ch = (swave >> lvl) & 1;
+        s_tree[s][nd][ch][lane] = lk;
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+        int old = 0;
+        if (lane == 0) old = __hip_atomic_fetch_add(&s_arr[s][nd], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        old = __builtin_amdgcn_readfirstlane(old);
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+        if (old == 0) {
+          root = false;
+          break;
+        }
+        wave_merge_lds64(lk, s_tree[s][nd][ch ^ 1]);
       }
-      if (tk == kScanWaves - 1) {
+      if (root) {
         write_topk(lk, q, k, a);
         lds_signal_add(&s_free[s], 1);
         if (a.stats && lane == 0 && i == nqw - 1) atomicAdd(&a.stats[6], (unsigned long long)(clock64() - t_start));
-      } else {
-        s_acc[s][lane] = lk;
-        lds_signal_add(&s_mrg[s], 1);
       }
     }
     if (a.stats && lane == 0) {
