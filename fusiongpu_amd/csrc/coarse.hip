@@ -242,25 +242,26 @@ __global__ __launch_bounds__(256) void select_exact_kernel(
   const bool all_cols = C > kCandCap;  // pathological ties: re-score everything
   const int ncand = all_cols ? ncols : C;
 
-  float ld_ = FLT_MAX;
-  int li = kPadId;
+  // Running list of packed (distance, id) keys: squared L2 distances are >= 0,
+  // so key order is the tie rule.
+  uint64_t lk = kPadKey;
   bool first = true;
   for (int base = 0; base < ncand; base += kWave) {
-    float d = FLT_MAX;
-    int id = kPadId;
+    uint64_t key = kPadKey;
     if (base + lane < ncand) {
-      id = all_cols ? base + lane : cand[base + lane];
-      d = exact_l2(xs, c + (int64_t)id * dim, dim);
+      const int id = all_cols ? base + lane : cand[base + lane];
+      key = key_of(exact_l2(xs, c + (int64_t)id * dim, dim), id);
     }
-    wave_sort64(d, id);
-    if (first) { ld_ = d; li = id; first = false; }
-    else wave_merge_sorted64(ld_, li, d, id);
+    wave_sort64_k(key);
+    if (first) { lk = key; first = false; }
+    else wave_merge_sorted64_k(lk, key);
   }
 
-  const float best = readlane_f(ld_, 0);
+  const float best = key_dist(readlane64(lk, 0));
   const float pthr = best * prune_ratio;
   if (lane < p) {
-    int32_t oid = li;
+    const float ld_ = key_dist(lk);
+    int32_t oid = key_id(lk);
     if (prune && ld_ > pthr) oid = (int32_t)kPruned;
     out_ids[row * p + lane] = oid;
     out_d[row * p + lane] = ld_;
@@ -294,21 +295,22 @@ __global__ __launch_bounds__(256) void knn_chunk_kernel(
   float* xs = x_s[wave];
   for (int d = lane; d < dim; d += kWave) xs[d] = x[row * dim + d];
 
-  // running top-k
-  float ad = FLT_MAX, bd = FLT_MAX;
-  int ai = kPadId, bi = kPadId;
+  // running top-k as packed (distance, id) keys (squared L2 >= 0, so key
+  // order is the tie rule)
+  uint64_t ak = kPadKey, bk = kPadKey;
   if (accum) {
     if (lane < k) {
       const int id = out_ids[row * k + lane];
-      if (id >= 0) { ad = out_d[row * k + lane]; ai = id; }
+      if (id >= 0) ak = key_of(out_d[row * k + lane], id);
     }
     if (lane + kWave < k) {
       const int id = out_ids[row * k + lane + kWave];
-      if (id >= 0) { bd = out_d[row * k + lane + kWave]; bi = id; }
+      if (id >= 0) bk = key_of(out_d[row * k + lane + kWave], id);
     }
   }
-  const float kth = k <= kWave ? readlane_f(ad, k - 1) : readlane_f(bd, k - kWave - 1);
-  const bool full = (k <= kWave ? readlane_i(ai, k - 1) : readlane_i(bi, k - kWave - 1)) != kPadId;
+  const uint64_t kk = k <= kWave ? readlane64(ak, k - 1) : readlane64(bk, k - kWave - 1);
+  const float kth = key_dist(kk);
+  const bool full = key_id(kk) != kPadId;
 
   float val[VPL];
   const float* er = est + row * ld;
@@ -347,36 +349,35 @@ __global__ __launch_bounds__(256) void knn_chunk_kernel(
   const int ncand = all_cols ? ncols : C;
 
   for (int base = 0; base < ncand; base += kWave) {
-    float d = FLT_MAX;
-    int id = kPadId;
+    uint64_t key = kPadKey;
     if (base + lane < ncand) {
       const int col = all_cols ? base + lane : cand[base + lane];
-      d = exact_l2(xs, c + (int64_t)col * dim, dim);
-      id = id_base + col;
+      key = key_of(exact_l2(xs, c + (int64_t)col * dim, dim), id_base + col);
     }
-    wave_sort64(d, id);
+    wave_sort64_k(key);
     if (k <= kWave) {
-      wave_merge_sorted64(ad, ai, d, id);
+      wave_merge_sorted64_k(ak, key);
     } else {
       // A U C splits into its 64 smallest (new A) and 64 largest (H); B := best 64 of B U H.
-      const float rd = __int_as_float(wave_reverse(__float_as_int(d)));
-      const int ri = wave_reverse(id);
-      const bool c_lo = lt_pair(rd, ri, ad, ai);
-      float hd = c_lo ? ad : rd;
-      int hi = c_lo ? ai : ri;
-      if (c_lo) { ad = rd; ai = ri; }
-      wave_bitonic_merge64(ad, ai);
-      wave_bitonic_merge64(hd, hi);
-      wave_merge_sorted64(bd, bi, hd, hi);
+      const uint64_t r = wave_reverse64(key);
+      const bool c_lo = r < ak;
+      const uint64_t hk = c_lo ? ak : r;
+      ak = c_lo ? r : ak;
+      uint64_t h = hk;
+      bitonic_pass_k<64>(ak, true);
+      bitonic_pass_k<64>(h, true);
+      wave_merge_sorted64_k(bk, h);
     }
   }
   if (lane < k) {
+    const int ai = key_id(ak);
     out_ids[row * k + lane] = ai == kPadId ? -1 : ai;
-    out_d[row * k + lane] = ai == kPadId ? FLT_MAX : ad;
+    out_d[row * k + lane] = ai == kPadId ? FLT_MAX : key_dist(ak);
   }
   if (lane + kWave < k) {
+    const int bi = key_id(bk);
     out_ids[row * k + lane + kWave] = bi == kPadId ? -1 : bi;
-    out_d[row * k + lane + kWave] = bi == kPadId ? FLT_MAX : bd;
+    out_d[row * k + lane + kWave] = bi == kPadId ? FLT_MAX : key_dist(bk);
   }
 }
 

@@ -62,11 +62,6 @@ inline size_t carve_bytes(size_t count) { return align_up(count * sizeof(T), 256
 
 // ---- device helpers --------------------------------------------------------
 
-// Tie rule: ascending distance, then ascending id.
-__device__ __forceinline__ bool lt_pair(float da, int ia, float db, int ib) {
-  return da < db || (da == db && ia < ib);
-}
-
 __device__ __forceinline__ int lane_id() { return (int)__lane_id(); }
 
 __device__ __forceinline__ float shfl_xor_f(float v, int m) { return __shfl_xor(v, m, kWave); }
@@ -112,92 +107,9 @@ __device__ __forceinline__ int xchg(int v) {
     return (lane_id() & 32) ? (int)r[0] : (int)r[1];
   }
 }
-template <int S>
-__device__ __forceinline__ float xchg_f(float v) { return __int_as_float(xchg<S>(__float_as_int(v))); }
-
-// One compare-exchange stage of a bitonic network at distance S: the lower
-// lane of each pair keeps the smaller pair when `up`, the larger otherwise.
-template <int S>
-__device__ __forceinline__ void bitonic_stage(float& d, int& id, bool up) {
-  const float od = xchg_f<S>(d);
-  const int oi = xchg<S>(id);
-  const bool lower = (lane_id() & S) == 0;
-  const bool other_less = lt_pair(od, oi, d, id);
-  const bool take = (lower == up) ? other_less : (!other_less && !(od == d && oi == id));
-  if (take) { d = od; id = oi; }
-}
-// Stages S = SIZE/2 .. 1 with the direction of bitonic sequences of length SIZE.
-template <int SIZE>
-__device__ __forceinline__ void bitonic_pass(float& d, int& id, bool up) {
-  if constexpr (SIZE > 32) bitonic_stage<32>(d, id, up);
-  if constexpr (SIZE > 16) bitonic_stage<16>(d, id, up);
-  if constexpr (SIZE > 8) bitonic_stage<8>(d, id, up);
-  if constexpr (SIZE > 4) bitonic_stage<4>(d, id, up);
-  if constexpr (SIZE > 2) bitonic_stage<2>(d, id, up);
-  bitonic_stage<1>(d, id, up);
-}
-
-// Bitonic sort of one (d, id) pair per lane across the wave, ascending by the tie rule.
-__device__ __forceinline__ void wave_sort64(float& d, int& id) {
-  const int lane = lane_id();
-  bitonic_pass<2>(d, id, (lane & 2) == 0);
-  bitonic_pass<4>(d, id, (lane & 4) == 0);
-  bitonic_pass<8>(d, id, (lane & 8) == 0);
-  bitonic_pass<16>(d, id, (lane & 16) == 0);
-  bitonic_pass<32>(d, id, (lane & 32) == 0);
-  bitonic_pass<64>(d, id, true);
-}
-
-// Bitonic merge (ascending) of a bitonic sequence held one pair per lane.
-__device__ __forceinline__ void wave_bitonic_merge64(float& d, int& id) { bitonic_pass<64>(d, id, true); }
 
 // x(63 - lane): mirror inside each 16-lane row, then swap rows 0<->3, 1<->2.
 __device__ __forceinline__ int wave_reverse(int v) { return xchg<32>(xchg<16>(dpp_mov<0x140>(v))); }
-
-// list (ascending) := the 64 smallest of list U cand, where cand is ascending too.
-__device__ __forceinline__ void wave_merge_sorted64(float& d, int& id, float cd, int ci) {
-  const float rd = __int_as_float(wave_reverse(__float_as_int(cd)));
-  const int ri = wave_reverse(ci);
-  if (lt_pair(rd, ri, d, id)) { d = rd; id = ri; }
-  wave_bitonic_merge64(d, id);
-}
-
-// The same networks carrying an int payload with each (d, id) pair.
-template <int S>
-__device__ __forceinline__ void bitonic_stage_p(float& d, int& id, int& pl, bool up) {
-  const float od = xchg_f<S>(d);
-  const int oi = xchg<S>(id);
-  const int op = xchg<S>(pl);
-  const bool lower = (lane_id() & S) == 0;
-  const bool other_less = lt_pair(od, oi, d, id);
-  const bool take = (lower == up) ? other_less : (!other_less && !(od == d && oi == id));
-  if (take) { d = od; id = oi; pl = op; }
-}
-// list (ascending, with payload) := the 64 smallest of list U cand; cand
-// (ascending) enters with payload cp.
-__device__ __forceinline__ void wave_merge_sorted64_p(float& d, int& id, int& pl, float cd, int ci, int cp) {
-  const float rd = __int_as_float(wave_reverse(__float_as_int(cd)));
-  const int ri = wave_reverse(ci);
-  const int rp = wave_reverse(cp);
-  if (lt_pair(rd, ri, d, id)) { d = rd; id = ri; pl = rp; }
-  bitonic_stage_p<32>(d, id, pl, true);
-  bitonic_stage_p<16>(d, id, pl, true);
-  bitonic_stage_p<8>(d, id, pl, true);
-  bitonic_stage_p<4>(d, id, pl, true);
-  bitonic_stage_p<2>(d, id, pl, true);
-  bitonic_stage_p<1>(d, id, pl, true);
-}
-
-// Insert one (nd, nid) into the ascending list (one pair per lane); the last entry drops off.
-__device__ __forceinline__ void wave_insert64(float& d, int& id, float nd, int nid) {
-  const int lane = lane_id();
-  const float pd = __int_as_float(dpp_mov<0x138>(__float_as_int(d)));  // wave_shr:1: lane i gets lane i-1
-  const int pi = dpp_mov<0x138>(id);
-  if (!lt_pair(d, id, nd, nid)) {
-    if (lane == 0 || lt_pair(pd, pi, nd, nid)) { d = nd; id = nid; }
-    else { d = pd; id = pi; }
-  }
-}
 
 __device__ __forceinline__ float readlane_f(float v, int l) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
@@ -269,6 +181,34 @@ __device__ __forceinline__ void wave_merge_sorted64_k(uint64_t& k, uint64_t cand
   k = r < k ? r : k;
   bitonic_pass_k<64>(k, true);
 }
+// The same with an int payload travelling with each key.  A pair of equal
+// keys is left in place, so payloads are never duplicated.
+template <int S>
+__device__ __forceinline__ void bitonic_stage_kp(uint64_t& k, int& p, bool up) {
+  const uint64_t o = xchg64<S>(k);
+  const int op = xchg<S>(p);
+  const bool lower = (lane_id() & S) == 0;
+  const bool take = (lower == up) ? (o < k) : (k < o);
+  k = take ? o : k;
+  p = take ? op : p;
+}
+// list (ascending, with payload) := the 64 smallest of list U cand (cand
+// ascending, entering with payload cp).
+__device__ __forceinline__ void wave_merge_sorted64_kp(uint64_t& k, int& p, uint64_t cand, int cp) {
+  const uint64_t r = wave_reverse64(cand);
+  const int rp = wave_reverse(cp);
+  if (r < k) {
+    k = r;
+    p = rp;
+  }
+  bitonic_stage_kp<32>(k, p, true);
+  bitonic_stage_kp<16>(k, p, true);
+  bitonic_stage_kp<8>(k, p, true);
+  bitonic_stage_kp<4>(k, p, true);
+  bitonic_stage_kp<2>(k, p, true);
+  bitonic_stage_kp<1>(k, p, true);
+}
+
 // Insert nk into the ascending list; the last entry drops off.
 __device__ __forceinline__ void wave_insert64_k(uint64_t& k, uint64_t nk) {
   const uint64_t p = dpp_mov64<0x138>(k);  // wave_shr:1: lane i gets lane i-1

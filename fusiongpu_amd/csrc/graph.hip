@@ -83,9 +83,10 @@ __global__ __launch_bounds__(kGW * kWave) void graph_search_kernel(GraphArgs a) 
   const long long n = a.n;
   const int deg = a.degree, itopk = a.itopk;
 
-  // the itopk list: one entry per lane, ascending; ex = expanded flag
-  float ld = FLT_MAX;
-  int li = kPadId, ex = 0;
+  // the itopk list: one packed (distance, id) key per lane, ascending; ex =
+  // expanded flag
+  uint64_t lk = kPadKey;
+  int ex = 0;
   int nev = 0;  // exact distances computed by this lane
 
   // One step: candidates c0, c1 (-1 = none) -> visited filter, dedup, exact
@@ -94,21 +95,19 @@ __global__ __launch_bounds__(kGW * kWave) void graph_search_kernel(GraphArgs a) 
     const uint32_t b0 = graph_bit(c0), b1 = graph_bit(c1);
     const bool v0 = c0 >= 0 && (long long)c0 < n && !((bm[b0 >> 5] >> (b0 & 31)) & 1u);
     const bool v1 = c1 >= 0 && (long long)c1 < n && !((bm[b1 >> 5] >> (b1 & 31)) & 1u);
-    // sort the 128 candidates by id: keys (0, id), dropped ones (FLT_MAX, pad)
-    float k0 = v0 ? 0.0f : FLT_MAX, k1 = v1 ? 0.0f : FLT_MAX;
-    int i0 = v0 ? c0 : kPadId, i1 = v1 ? c1 : kPadId;
-    wave_sort64(k0, i0);
-    wave_sort64(k1, i1);
-    {  // split into the 64 smallest (i0) and 64 largest (i1), both ascending
-      const float rk = __int_as_float(wave_reverse(__float_as_int(k1)));
-      const int ri = wave_reverse(i1);
-      const bool c_lo = lt_pair(rk, ri, k0, i0);
-      k1 = c_lo ? k0 : rk;
-      i1 = c_lo ? i0 : ri;
-      if (c_lo) { k0 = rk; i0 = ri; }
-      wave_bitonic_merge64(k0, i0);
-      wave_bitonic_merge64(k1, i1);
+    // sort the 128 candidates by id: keys (0, id), dropped ones the padding key
+    uint64_t k0 = v0 ? (uint64_t)(uint32_t)c0 : kPadKey, k1 = v1 ? (uint64_t)(uint32_t)c1 : kPadKey;
+    wave_sort64_k(k0);
+    wave_sort64_k(k1);
+    {  // split into the 64 smallest (k0) and 64 largest (k1), both ascending
+      const uint64_t r = wave_reverse64(k1);
+      const bool c_lo = r < k0;
+      k1 = c_lo ? k0 : r;
+      k0 = c_lo ? r : k0;
+      bitonic_pass_k<64>(k0, true);
+      bitonic_pass_k<64>(k1, true);
     }
+    int i0 = key_id(k0), i1 = key_id(k1);
     // keep each id once: drop an entry equal to its predecessor in the 128-sequence
     const int p0 = dpp_mov<0x138>(i0);  // wave_shr:1
     int p1 = dpp_mov<0x138>(i1);
@@ -123,13 +122,13 @@ __global__ __launch_bounds__(kGW * kWave) void graph_search_kernel(GraphArgs a) 
     float d0 = FLT_MAX, d1 = FLT_MAX;
     if (i0 != kPadId) { d0 = row_l2<D>(qs, a.base + (size_t)i0 * D); ++nev; }
     if (i1 != kPadId) { d1 = row_l2<D>(qs, a.base + (size_t)i1 * D); ++nev; }
-    wave_sort64(d0, i0);
-    wave_sort64(d1, i1);
-    wave_merge_sorted64_p(ld, li, ex, d0, i0, 0);
-    wave_merge_sorted64_p(ld, li, ex, d1, i1, 0);
+    uint64_t e0 = key_of(d0, i0), e1 = key_of(d1, i1);  // padding ids give the padding key
+    wave_sort64_k(e0);
+    wave_sort64_k(e1);
+    wave_merge_sorted64_kp(lk, ex, e0, 0);
+    wave_merge_sorted64_kp(lk, ex, e1, 0);
     if (lane >= itopk) {
-      ld = FLT_MAX;
-      li = kPadId;
+      lk = kPadKey;
       ex = 0;
     }
     wave_lds_sync();
@@ -139,14 +138,14 @@ __global__ __launch_bounds__(kGW * kWave) void graph_search_kernel(GraphArgs a) 
   step((int)(gmix64(a.seed ^ gmix64((qg << 20) | (uint64_t)lane)) % (uint64_t)n), -1);
   int it = 0;
   for (; it < a.max_iter; ++it) {
-    uint64_t open = __ballot(li != kPadId && !ex);
+    uint64_t open = __ballot(key_id(lk) != kPadId && !ex);
     if (!open) break;
     int np = 0;
     for (; np < a.width && open; ++np) {
       const int L = __ffsll((unsigned long long)open) - 1;
       open &= open - 1;
       if (lane == L) ex = 1;
-      const int pid = readlane_i(li, L);
+      const int pid = readlane_i(key_id(lk), L);
       if (lane == 0) par[np] = pid;
     }
     wave_lds_sync();
@@ -158,8 +157,9 @@ __global__ __launch_bounds__(kGW * kWave) void graph_search_kernel(GraphArgs a) 
     step(c0, c1);
   }
   if (lane < a.k) {
+    const int li = key_id(lk);
     a.out_ids[(size_t)qi * a.k + lane] = li == kPadId ? -1 : li;
-    a.out_d[(size_t)qi * a.k + lane] = li == kPadId ? FLT_MAX : ld;
+    a.out_d[(size_t)qi * a.k + lane] = li == kPadId ? FLT_MAX : key_dist(lk);
   }
   if (a.iters && lane == 0) a.iters[qi] = it;
   if (a.evals) {

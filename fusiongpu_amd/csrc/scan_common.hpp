@@ -106,39 +106,14 @@ __device__ __forceinline__ bool adc_sum2(const float* __restrict__ lut, const ui
   return true;
 }
 
-// (distance, id) packed so that unsigned order is the tie rule: distances are
-// sums of squares (never negative, never -0), so their bit patterns order like
-// the floats; ids are non-negative.
-__device__ __forceinline__ uint64_t pack_key(float d, int id) {
-  return ((uint64_t)__float_as_uint(d) << 32) | (uint32_t)id;
-}
-// "No threshold yet": the padding entry (FLT_MAX, kPadId); every real
-// candidate is below it and its distance part is a finite float.
-constexpr uint64_t kNoThr = ((uint64_t)0x7F7FFFFFu << 32) | (uint32_t)kPadId;
+// "No threshold yet": the padding key (FLT_MAX, kPadId); every real
+// candidate key (key_of: distances are sums of squares, never negative) is
+// below it.
+constexpr uint64_t kNoThr = kPadKey;
 
-// Offer one (distance, id) per lane to the wave's running top-64 list; only
-// pairs strictly below `thr` (the k-th best known to the workgroup) enter.
-// Returns true if the list changed.
-__device__ __forceinline__ bool offer(float d, int id, bool valid, uint64_t thr, float& ld, int& li) {
-  const bool pass = valid && pack_key(d, id) < thr;
-  uint64_t bm = __ballot(pass);
-  if (!bm) return false;
-  if (__popcll(bm) > kSerialMax) {
-    float cd = pass ? d : FLT_MAX;
-    int ci = pass ? id : kPadId;
-    wave_sort64(cd, ci);
-    wave_merge_sorted64(ld, li, cd, ci);
-  } else {
-    while (bm) {
-      const int src = __ffsll((unsigned long long)bm) - 1;
-      bm &= bm - 1;
-      wave_insert64(ld, li, readlane_f(d, src), readlane_i(id, src));
-    }
-  }
-  return true;
-}
-
-// The same on packed keys: lk holds the wave's ascending top-64 keys.
+// Offer one packed (distance, id) key per lane to the wave's running top-64
+// list lk (ascending keys); only keys strictly below `thr` (the k-th best
+// known to the workgroup) enter.  Returns true if the list changed.
 __device__ __forceinline__ bool offer_k(uint64_t key, bool valid, uint64_t thr, uint64_t& lk) {
   const bool pass = valid && key < thr;
   uint64_t bm = __ballot(pass);

@@ -144,8 +144,7 @@ __global__ __launch_bounds__(kTT) void two_phase_kernel(TwoPhaseArgs a) {
   __shared__ __align__(16) float smem[C::SMEM];
   __shared__ float rbuf[2][D];
   __shared__ float qs[D];
-  __shared__ float md[kTW * kWave];
-  __shared__ int mi[kTW * kWave];
+  __shared__ uint64_t mk[kTW * kWave];  // the waves' sorted lists of the current list
   __shared__ int hist[256];
   __shared__ int misc[4];
   __shared__ float s_cut[64];
@@ -263,8 +262,7 @@ __global__ __launch_bounds__(kTT) void two_phase_kernel(TwoPhaseArgs a) {
     if (nf >= 0) residual(nf, rbuf[(it + 1) & 1]);
     __syncthreads();  // LUT f and the next residual ready; s_lthr reset
     const long long c1 = a.stats ? clock64() : 0;
-    float ld = FLT_MAX;
-    int li = kPadId;
+    uint64_t lk = kPadKey;
     uint64_t own = kNoThr;
     for (int base = first; base < n; base += kTRound) {
       const int nb = base + kTRound;
@@ -286,15 +284,15 @@ __global__ __launch_bounds__(kTT) void two_phase_kernel(TwoPhaseArgs a) {
       }
       float d0, d1;
       if (adc_sum2<M>(lut, w0, w1, v0 < n, v1 < n, __uint_as_float((uint32_t)(thr >> 32)), d0, d1)) {
-        bool changed = offer(d0, i0, v0 < n, thr, ld, li);
+        bool changed = offer_k(key_of(d0, i0), v0 < n, thr, lk);
         if (changed) {
-          const uint64_t kth = pack_key(readlane_f(ld, K1 - 1), readlane_i(li, K1 - 1));
+          const uint64_t kth = readlane64(lk, K1 - 1);
           thr = kth < thr ? kth : thr;
         }
-        changed |= offer(d1, i1, v1 < n, thr, ld, li);
+        changed |= offer_k(key_of(d1, i1), v1 < n, thr, lk);
         if (changed) {
-          own = pack_key(readlane_f(ld, K1 - 1), readlane_i(li, K1 - 1));
-          const uint64_t qth = pack_key(readlane_f(ld, Q - 1), readlane_i(li, Q - 1));
+          own = readlane64(lk, K1 - 1);
+          const uint64_t qth = readlane64(lk, Q - 1);
           if (lane == 0) {
             atomicMin(&s_lthr, (unsigned long long)own);
             s_pub[wave] = qth;
@@ -312,15 +310,14 @@ __global__ __launch_bounds__(kTT) void two_phase_kernel(TwoPhaseArgs a) {
       }
     }
     const long long c2 = a.stats ? clock64() : 0;
-    md[wave * kWave + lane] = ld;
-    mi[wave * kWave + lane] = li;
+    mk[wave * kWave + lane] = lk;
     __syncthreads();  // every wave's list for list f is in LDS
     if (wave == 0) {
 #pragma unroll 1
-      for (int w = 1; w < kTW; ++w) wave_merge_sorted64(ld, li, md[w * kWave + lane], mi[w * kWave + lane]);
+      for (int w = 1; w < kTW; ++w) wave_merge_sorted64_k(lk, mk[w * kWave + lane]);
       const int w = n < K1 ? n : K1;
-      if (lane < w) pool[cnt_w0 + lane] = pack_key(ld, li);
-      const float cut = readlane_f(ld, w - 1);
+      if (lane < w) pool[cnt_w0 + lane] = lk;
+      const float cut = key_dist(readlane64(lk, w - 1));
       if (lane == 0) {
         s_cut[f_p[f]] = cut;
         s_lthr = kNoThr;
@@ -403,7 +400,7 @@ __global__ __launch_bounds__(kTT) void two_phase_kernel(TwoPhaseArgs a) {
         const int v0 = base + lane, v1 = v0 + kWave;
         float d0, d1;
         if (adc_sum2<M>(lut, w0, w1, v0 < s1, v1 < s1, thr_d, d0, d1)) {
-          const uint64_t k0 = pack_key(d0, i0), k1 = pack_key(d1, i1);
+          const uint64_t k0 = key_of(d0, i0), k1 = key_of(d1, i1);
           const bool pass0 = v0 < s1 && d0 <= thr && k0 < adm;
           const bool pass1 = v1 < s1 && d1 <= thr && k1 < adm;
           const uint64_t b0 = __ballot(pass0), b1 = __ballot(pass1);
@@ -496,18 +493,13 @@ constexpr int kRT = 2 * kWave;
 template <int D>
 __global__ __launch_bounds__(kRT) void rerank_kernel(RerankArgs a) {
   __shared__ float qs[D];
-  __shared__ float td[2][256];  // running top-k (double-buffered), ascending
-  __shared__ int ti[2][256];
-  __shared__ float nd[kRT];     // the batch, sorted
-  __shared__ int ni[kRT];
+  __shared__ uint64_t tk[2][256];  // running top-k keys (double-buffered), ascending
+  __shared__ uint64_t nk[kRT];     // the batch, sorted
   __shared__ int s_chg, s_stable, s_fin;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int q = blockIdx.x, k = a.k, mb = a.mb, rm = a.rm;
   for (int i = tid; i < D; i += kRT) qs[i] = a.queries[(size_t)q * D + i];
-  for (int i = tid; i < k; i += kRT) {
-    td[0][i] = FLT_MAX;
-    ti[0][i] = kPadId;
-  }
+  for (int i = tid; i < k; i += kRT) tk[0][i] = kPadKey;
   if (tid == 0) {
     s_stable = 0;
     s_fin = 0;
@@ -543,70 +535,61 @@ __global__ __launch_bounds__(kRT) void rerank_kernel(RerankArgs a) {
         id = vid;
       }
     }
-    // sort the batch: each wave its 64, then a merge by ranks into nd/ni
-    wave_sort64(d, id);
-    nd[tid] = d;
-    ni[tid] = id;
+    // sort the batch: each wave its 64 keys, then a merge by ranks into nk
+    uint64_t key = key_of(d, id);
+    wave_sort64_k(key);
+    nk[tid] = key;
     if (tid == 0) s_chg = 0;
     __syncthreads();
     {
-      const float* od = nd + (wave ^ 1) * kWave;
-      const int* oi = ni + (wave ^ 1) * kWave;
+      const uint64_t* ok = nk + (wave ^ 1) * kWave;
       // rank in the other wave's sorted list: wave 0 counts strictly smaller
-      // entries, wave 1 counts smaller-or-equal ones, so equal pairs keep a
-      // fixed order and every position is taken once.
+      // keys, wave 1 counts smaller-or-equal ones, so equal keys keep a fixed
+      // order and every position is taken once.
       int lo = 0, hi = kWave;
       while (lo < hi) {
         const int mid = (lo + hi) >> 1;
-        const bool before = wave == 0 ? lt_pair(od[mid], oi[mid], d, id) : !lt_pair(d, id, od[mid], oi[mid]);
+        const bool before = wave == 0 ? ok[mid] < key : ok[mid] <= key;
         if (before) lo = mid + 1; else hi = mid;
       }
       __syncthreads();
-      nd[lane + lo] = d;
-      ni[lane + lo] = id;
+      nk[lane + lo] = key;
     }
     __syncthreads();
-    // merge the sorted batch (nd/ni, kRT entries) with the top-k (td/ti[cur])
-    const float* ctd = td[cur];
-    const int* cti = ti[cur];
-    float* xtd = td[cur ^ 1];
-    int* xti = ti[cur ^ 1];
+    // merge the sorted batch (nk, kRT keys) with the top-k (tk[cur])
+    const uint64_t* ck = tk[cur];
+    uint64_t* xk = tk[cur ^ 1];
     {
-      const float bd = nd[tid];
-      const int bi = ni[tid];
+      const uint64_t bk = nk[tid];
       // old entries precede equal batch entries
       int lo = 0, hi = k;
       while (lo < hi) {
         const int mid = (lo + hi) >> 1;
-        if (!lt_pair(bd, bi, ctd[mid], cti[mid])) lo = mid + 1; else hi = mid;
+        if (ck[mid] <= bk) lo = mid + 1; else hi = mid;
       }
       const int pos = tid + lo;
       bool fresh = false;
       if (pos < k) {
-        xtd[pos] = bd;
-        xti[pos] = bi;
+        xk[pos] = bk;
+        const int bi = key_id(bk);
         if (bi != kPadId) {
           fresh = true;
           for (int j = 0; j < k; ++j)
-            if (cti[j] == bi) { fresh = false; break; }
+            if (key_id(ck[j]) == bi) { fresh = false; break; }
         }
       }
       const uint64_t bm = __ballot(fresh);
       if (lane == 0 && bm) atomicAdd(&s_chg, (int)__popcll(bm));
     }
     for (int j = tid; j < k; j += kRT) {
-      const float od = ctd[j];
-      const int oi = cti[j];
+      const uint64_t okey = ck[j];
       int lo = 0, hi = kRT;
       while (lo < hi) {
         const int mid = (lo + hi) >> 1;
-        if (lt_pair(nd[mid], ni[mid], od, oi)) lo = mid + 1; else hi = mid;
+        if (nk[mid] < okey) lo = mid + 1; else hi = mid;
       }
       const int pos = j + lo;
-      if (pos < k) {
-        xtd[pos] = od;
-        xti[pos] = oi;
-      }
+      if (pos < k) xk[pos] = okey;
     }
     __syncthreads();
     if (tid == 0) {
@@ -619,9 +602,10 @@ __global__ __launch_bounds__(kRT) void rerank_kernel(RerankArgs a) {
     if (s_fin) break;
   }
   for (int j = tid; j < k; j += kRT) {
-    const bool pad = ti[cur][j] == kPadId;
-    a.out_ids[(size_t)q * k + j] = pad ? -1 : ti[cur][j];
-    a.out_d[(size_t)q * k + j] = pad ? FLT_MAX : td[cur][j];
+    const uint64_t kk = tk[cur][j];
+    const bool pad = key_id(kk) == kPadId;
+    a.out_ids[(size_t)q * k + j] = pad ? -1 : key_id(kk);
+    a.out_d[(size_t)q * k + j] = pad ? FLT_MAX : key_dist(kk);
   }
   if (a.visited && tid == 0) a.visited[q] = seen;
 }
