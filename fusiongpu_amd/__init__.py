@@ -72,6 +72,11 @@ _SIGS = {
     "fgpu_kmeans_workspace_bytes": (_sz, [_i32, _i32]),
     "fgpu_kmeans_update": (_i32, [_vp, _i64, _vp, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _sz, _vp]),
     "fgpu_fixed_shift": (_i32, [_f32, _i64]),
+    "fgpu_tune_list_stats": (_i32, [_vp, _vp, _i32, _vp, _i64, _vp, _vp, _vp, _vp, _i32, _vp, _vp, _vp, _vp, _vp,
+                                    _vp]),
+    "fgpu_tune_percentile_int": (_i32, [_vp, _i64, _f32]),
+    "fgpu_tune_percentile": (_f32, [_vp, _i64, _f32]),
+    "fgpu_tune_elbow": (_i32, [_vp, _i32, _i64, _c.POINTER(_f32)]),
     "fgpu_kmeans_fit": (_i32, [_vp, _i64, _i32, _i32, _i32, _i32, _u64, _vp, _vp, _vp]),
     "fgpu_pq_train": (_i32, [_vp, _i64, _i32, _i32, _vp, _vp, _i32, _i32, _vp, _vp]),
     "fgpu_pq_encode": (_i32, [_vp, _i64, _i32, _i32, _vp, _vp, _vp, _vp, _vp]),
@@ -380,6 +385,30 @@ class Index:
                                _dev_ptr(ws), ws.numel(), _stream(stream)))
         return ids, d
 
+    def tune_list_stats(self, queries, pair_query, pair_list, pair_target=None, pair_kth=None, base=None,
+                        stream=None):
+        """The tuner's per-(query, list) statistics (fgpu_tune_list_stats): (target_pq, target_exact, pq_rank,
+        exact_rank, kth_pq) as device tensors; the first four are None without pair_target, the last without
+        pair_kth."""
+        torch = _torch()
+        q = _to_dev(queries)
+        pq, pl = _to_dev(pair_query), _to_dev(pair_list)
+        n = pq.shape[0]
+        pt = _to_dev(pair_target) if pair_target is not None else None
+        pk = _to_dev(pair_kth) if pair_kth is not None else None
+        b = _to_dev(base) if base is not None else None
+        f = lambda: torch.empty(n, dtype=torch.float32, device="cuda")  # noqa: E731
+        i = lambda: torch.empty(n, dtype=torch.int32, device="cuda")  # noqa: E731
+        tp, te, pr, er = (f(), f(), i(), i()) if pt is not None else (None, None, None, None)
+        kp = f() if pk is not None else None
+        _check(lib.fgpu_tune_list_stats(self._h, _dev_ptr(q), q.shape[0], _dev_ptr(b) if b is not None else None,
+                                        b.shape[0] if b is not None else 0, _dev_ptr(pq), _dev_ptr(pl),
+                                        _dev_ptr(pt) if pt is not None else None,
+                                        _dev_ptr(pk) if pk is not None else None, n,
+                                        *(_dev_ptr(t) if t is not None else None for t in (tp, te, pr, er, kp)),
+                                        _stream(stream)))
+        return tp, te, pr, er, kp
+
 
 def probe_counts(index: Index, probe_ids, stream=None):
     torch = _torch()
@@ -420,6 +449,24 @@ def l2_topk(x, c, p: int, stream=None):
     _check(lib.fgpu_l2_topk(_dev_ptr(x), n, _dev_ptr(c), nc, dim, p, _dev_ptr(ids), _dev_ptr(d), _dev_ptr(ws),
                             ws.numel(), _stream(stream)))
     return ids, d
+
+
+def tune_percentile(values, pct: float):
+    """compute_percentile(_int) of the tuner (host): sorted[floor(n * pct)], clamped; 0 when empty."""
+    v = np.ascontiguousarray(values)
+    if v.dtype.kind in "iu":
+        v = np.ascontiguousarray(v, np.int32)
+        return int(lib.fgpu_tune_percentile_int(_np_ptr(v) if v.size else None, v.size, pct))
+    v = np.ascontiguousarray(v, np.float32)
+    return float(lib.fgpu_tune_percentile(_np_ptr(v) if v.size else None, v.size, pct))
+
+
+def tune_elbow(hits_per_rank, total_hits: int):
+    """find_elbow_point of the tuner (host): (recommended phase-1 list count, coverage there)."""
+    h = np.ascontiguousarray(hits_per_rank, np.int32)
+    cov = _c.c_float()
+    e = lib.fgpu_tune_elbow(_np_ptr(h) if h.size else None, h.size, int(total_hits), _c.byref(cov))
+    return int(e), float(cov.value)
 
 
 def knn_exact(queries, base, k: int, workspace=None, stream=None):

@@ -440,6 +440,24 @@ fgpu_status fgpu_graph_search(const float* dq, int nq, const float* d_base, int6
   return launch_graph_search(dim, a, as_stream(stream));
 }
 
+fgpu_status fgpu_tune_list_stats(const fgpu_index* idx, const float* d_queries, int nq, const float* d_base,
+                                 int64_t n_base, const int32_t* d_pair_query, const int32_t* d_pair_list,
+                                 const int32_t* d_pair_target, const int32_t* d_pair_kth, int npairs,
+                                 float* d_target_pq, float* d_target_exact, int32_t* d_pq_rank,
+                                 int32_t* d_exact_rank, float* d_kth_pq, void* stream) {
+  FGPU_CHECK(idx && d_queries && d_pair_query && d_pair_list && npairs >= 0 && nq >= 0, FGPU_ERR_ARG,
+             "tune_list_stats: bad argument");
+  FGPU_CHECK(!d_pair_target || (d_target_pq && d_target_exact && d_pq_rank && d_exact_rank), FGPU_ERR_ARG,
+             "tune_list_stats: target outputs missing");
+  FGPU_CHECK(!d_pair_kth || d_kth_pq, FGPU_ERR_ARG, "tune_list_stats: k-th output missing");
+  FGPU_CHECK(!d_base || n_base >= 0, FGPU_ERR_ARG, "tune_list_stats: bad n_base");
+  TuneStatsArgs a{d_queries, nq, idx->dim, idx->m, idx->nlist, idx->d_offsets, idx->d_ids, idx->d_codes,
+                  idx->d_centroids, idx->d_codebook, d_base, (long long)(d_base ? n_base : 0),
+                  d_pair_query, d_pair_list, d_pair_target, d_pair_kth,
+                  d_target_pq, d_target_exact, d_pq_rank, d_exact_rank, d_kth_pq};
+  return launch_tune_list_stats(a, npairs, as_stream(stream));
+}
+
 // ---------------------------------------------------------------------------
 int fgpu_fixed_shift(float maxabs, int64_t n) {
   int e = 0;

@@ -124,6 +124,30 @@ struct GraphArgs {
 };
 fgpu_status launch_graph_search(int dim, const GraphArgs& a, hipStream_t s);
 
+// ---- tune.hip -------------------------------------------------------------------
+constexpr int kMaxTuneLut = 64 * 256;  // pq_m <= 64
+struct TuneStatsArgs {
+  const float* queries;     // [nq][dim]
+  int nq, dim, pq_m, nlist;
+  const int32_t* offsets;   // [nlist+1]
+  const int32_t* ids;       // [total]
+  const uint8_t* codes;     // [total][pq_m]
+  const float* centroids;   // [nlist][dim]
+  const float* codebook;    // [pq_m][256][dim/pq_m]
+  const float* base;        // [n_base][dim] or nullptr (no exact distances)
+  long long n_base;
+  const int32_t* pair_query;   // [npairs] row of queries
+  const int32_t* pair_list;    // [npairs] list id
+  const int32_t* pair_target;  // [npairs] vector id, or -1; nullptr: none
+  const int32_t* pair_kth;     // [npairs] k for the k-th PQ distance, <= 0 none; nullptr: none
+  float* target_pq;         // [npairs]
+  float* target_exact;      // [npairs]
+  int32_t* pq_rank;         // [npairs]
+  int32_t* exact_rank;      // [npairs]
+  float* kth_pq;            // [npairs]
+};
+fgpu_status launch_tune_list_stats(const TuneStatsArgs& a, int npairs, hipStream_t s);
+
 // ---- build.hip ----------------------------------------------------------------
 fgpu_status launch_probe_counts(const uint32_t* probes, int nq, int nprobe, int nlist, const int32_t* offsets,
                                 int32_t* counts, int32_t* offs, hipStream_t s);

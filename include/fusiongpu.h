@@ -273,6 +273,40 @@ fgpu_status fgpu_build_ivfpq_sampled(const float* d_x, int64_t n, int dim, int n
                                      int pq_iters, int sample_size, int32_t* h_offsets, int32_t* h_ids,
                                      uint8_t* h_codes, float* h_centroids, float* h_codebook, void* stream);
 
+/* ---- offline parameter tuner (tune_parameters.cu:459-1053) ------------- */
+
+/* Per (query, list) statistics of the tuner, one pair per entry.  Replaces the
+ * per-item cudaMalloc + precompute_lut_kernel + compute_pq_dist_with_lut_kernel
+ * + compute_exact_distances_kernel + host ranking of tune_parameters.cu:690-784
+ * and the per-list cutoff of :843-900.  PQ distances use the tuner's own LUT
+ * (tune_parameters.cu:101-123: per entry, a sequential fused chain over the
+ * sub-vector of (q - c) - codeword; not the search LUT) summed in ascending
+ * subspace order (:127-145); exact distances are sequential fused chains over
+ * the dimensions (:148-166) against d_base rows (vector ids index d_base).
+ * For pair p (query row d_pair_query[p] of d_queries, list d_pair_list[p]):
+ *   with d_pair_target (vector id t, or -1): at the first list position
+ *     holding t, d_target_pq / d_target_exact get its distances and d_pq_rank /
+ *     d_exact_rank 1 + the list's vectors strictly below them (:766-778);
+ *     0 ranks and -1 distances when t is absent (d_base NULL: no exact part);
+ *   with d_pair_kth (k, or <= 0): d_kth_pq gets the min(k, n_l)-th smallest PQ
+ *     distance of the list (:893-899), 0 for an empty list.
+ * Pairs naming a query row outside [0, nq) or a list outside [0, nlist) get
+ * the "absent" values.  dim <= 128, pq_m <= 64. */
+fgpu_status fgpu_tune_list_stats(const fgpu_index* idx, const float* d_queries, int nq, const float* d_base,
+                                 int64_t n_base, const int32_t* d_pair_query, const int32_t* d_pair_list,
+                                 const int32_t* d_pair_target, const int32_t* d_pair_kth, int npairs,
+                                 float* d_target_pq, float* d_target_exact, int32_t* d_pq_rank,
+                                 int32_t* d_exact_rank, float* d_kth_pq, void* stream);
+/* compute_percentile_int / compute_percentile (tune_parameters.cu:170-183):
+ * the sorted sample's element at floor(n * pct) (product in single precision),
+ * clamped to the last element; 0 for an empty sample.  Host only. */
+int fgpu_tune_percentile_int(const int32_t* values, int64_t n, float pct);
+float fgpu_tune_percentile(const float* values, int64_t n, float pct);
+/* find_elbow_point (tune_parameters.cu:199-456) without its printed tables:
+ * the recommended phase-1 list count (1-based) from the ground-truth hits per
+ * coarse rank; *coverage gets the cumulative coverage there.  Host only. */
+int fgpu_tune_elbow(const int32_t* hits_per_rank, int n, int64_t total_hits, float* coverage);
+
 /* ---- files (utils.h, build_global.cu:242-252) -------------------------- */
 
 fgpu_status fgpu_write_ivf_data(const char* path, int64_t total, int nlist, int pq_m, int dim,

@@ -52,6 +52,9 @@ _SIGS = {
     "orc_pq_train": (_i32, [_vp, _i64, _i32, _i32, _vp, _vp, _i32, _i32, _vp, _i32]),
     "orc_pq_encode": (None, [_vp, _i64, _i32, _i32, _vp, _vp, _vp, _i32, _vp, _i32]),
     "orc_build_lists": (None, [_vp, _i64, _i32, _vp, _i32, _vp, _vp, _vp]),
+    "orc_tune_list_stats": (None, [_vp, _i32, _i32, _vp, _i32, _vp, _i32, _vp, _vp, _vp, _vp, _i64, _vp, _vp, _vp,
+                                   _vp, _i32, _vp, _vp, _vp, _vp, _vp, _i32]),
+    "orc_tune_coarse_order": (None, [_vp, _i32, _vp, _i32, _i32, _vp, _vp, _i32]),
 }
 
 
@@ -175,6 +178,159 @@ def knn_exact(q, base, k, nthreads=0):
     od = np.empty((q.shape[0], k), np.float32)
     lib.orc_knn_exact(_p(q), q.shape[0], _p(base), base.shape[0], q.shape[1], k, _p(oid), _p(od), nthreads)
     return oid, od
+
+
+# ---------------------------------------------------------------------------- tuner (tune_parameters.cu:459-1053)
+
+def tune_list_stats(q, cent, codebook, offsets, ids, codes, base, pair_q, pair_l, pair_t=None, pair_k=None,
+                    nthreads=0):
+    """Per (query, list) pair: target PQ/exact distance and ranks, and the k-th PQ distance (orc_tune_list_stats)."""
+    q, cent, codebook = f32(q), f32(cent), f32(codebook)
+    offsets, ids, codes = i32(offsets), i32(ids), u8(codes)
+    pair_q, pair_l = i32(pair_q), i32(pair_l)
+    npairs = pair_q.shape[0]
+    m = codebook.shape[0]
+    tp, te = np.empty(npairs, np.float32), np.empty(npairs, np.float32)
+    pr, er = np.empty(npairs, np.int32), np.empty(npairs, np.int32)
+    kp = np.empty(npairs, np.float32)
+    pt = i32(pair_t) if pair_t is not None else None
+    pk = i32(pair_k) if pair_k is not None else None
+    b = f32(base) if base is not None else None
+    lib.orc_tune_list_stats(_p(q), q.shape[0], q.shape[1], _p(cent), cent.shape[0], _p(codebook), m, _p(offsets),
+                            _p(ids), _p(codes), _p(b) if b is not None else None, b.shape[0] if b is not None else 0,
+                            _p(pair_q), _p(pair_l), _p(pt) if pt is not None else None,
+                            _p(pk) if pk is not None else None, npairs, _p(tp), _p(te), _p(pr), _p(er), _p(kp),
+                            nthreads)
+    return tp, te, pr, er, kp
+
+
+def tune_coarse_order(q, cent, nthreads=0):
+    """The tuner's host-form coarse order: (order [nq][nlist], rank_of [nq][nlist], 1-based)."""
+    q, cent = f32(q), f32(cent)
+    nq, nl = q.shape[0], cent.shape[0]
+    order = np.empty((nq, nl), np.int32)
+    rank_of = np.empty((nq, nl), np.int32)
+    lib.orc_tune_coarse_order(_p(q), nq, _p(cent), nl, q.shape[1], _p(order), _p(rank_of), nthreads)
+    return order, rank_of
+
+
+def tune_percentile(values, pct):
+    """compute_percentile(_int) (tune_parameters.cu:170-183): sorted[floor(n * pct)] with the product in float32,
+    clamped; 0 for an empty sample."""
+    v = np.sort(np.asarray(values))
+    if v.size == 0:
+        return 0
+    idx = int(np.float32(v.size) * np.float32(pct))
+    return v[min(idx, v.size - 1)]
+
+
+_libm = ctypes.CDLL("libm.so.6")
+_libm.logf.restype, _libm.logf.argtypes = _f32, [_f32]
+
+
+def _f(x):
+    return np.float32(x)
+
+
+def tune_elbow(hits, total_hits):
+    """find_elbow_point (tune_parameters.cu:199-456), float32 throughout as the reference's host code; log via the C
+    library's logf.  Returns (elbow list count, coverage there)."""
+    hits = [int(h) for h in hits]
+    n = len(hits)
+    if n == 0 or total_hits == 0:
+        return 1, _f(0.0)
+    cov, lg = [], []
+    cum = 0
+    for h in hits:
+        cum += h
+        cov.append(_f(_f(cum) / _f(total_hits)))
+        lg.append(_f(_libm.logf(float(_f(h) + _f(1.0)))))
+    sm = []
+    for i in range(n):
+        if i == 0 or i == n - 1:
+            sm.append(lg[i])
+        else:
+            sm.append(_f(_f(_f(_f(0.25) * lg[i - 1]) + _f(_f(0.5) * lg[i])) + _f(_f(0.25) * lg[i + 1])))
+    curv = [_f(0.0)] * n
+    for i in range(1, n - 1):
+        curv[i] = _f(_f(sm[i + 1] - _f(_f(2.0) * sm[i])) + sm[i - 1])
+    vol = [0.0] * n
+    for i in range(1, n - 1):
+        d1, d2 = _f(hits[i - 1] - hits[i]), _f(hits[i] - hits[i + 1])
+        if _f(d1 * d2) < 0:
+            vol[i] = 1.0
+    best, best_score = -1, _f(-1e9)
+    i = 2
+    while i + 1 < n and i < 30:
+        if cov[i] >= _f(0.60):
+            cs = _f(abs(curv[i]) * _f(10.0))
+            db = _f(_f(hits[i - 1] - hits[i]) / _f(_f(hits[i - 1]) + _f(1.0)))
+            da = _f(_f(hits[i] - hits[i + 1]) / _f(_f(hits[i]) + _f(1.0)))
+            ds = _f(_f(db - da) * _f(8.0)) if da < db else _f(0.0)
+            pen = _f(_f(vol[i]) * _f(5.0))
+            r = _f(_f(i) / _f(32.0))
+            bonus = _f(_f(4.0) * _f(_f(1.0) - _f(r * r)))
+            score = _f(_f(_f(cs + ds) + bonus) - pen)
+            if cov[i] >= _f(0.80) and score > best_score:
+                best_score, best = score, i
+        i += 1
+    if best >= 0:
+        return best + 1, cov[best]
+    for i in range(n):
+        if cov[i] >= _f(0.60):
+            return i + 1, cov[i]
+    return 1, _f(0.0)
+
+
+def tune_parameters(base, offsets, ids, codes, cent, codebook, samples, k):
+    """The tuner's recommendations (tune_search_parameters, tune_parameters.cu:459-1012) for the given sampled base
+    rows: (top_m, p1_lists, limit_k, threshold_coeff)."""
+    base = f32(base)
+    offsets, ids = i32(offsets), i32(ids)
+    nl = offsets.shape[0] - 1
+    q = np.ascontiguousarray(base[np.asarray(samples)])
+    nq = q.shape[0]
+    gt, _ = knn_exact(q, base, k)
+    list_of = {}
+    for c in range(nl):
+        for j in range(offsets[c], offsets[c + 1]):
+            list_of.setdefault(int(ids[j]), c)
+    order, rank_of = tune_coarse_order(q, cent)
+    ranks = [int(rank_of[i, list_of[int(t)]]) for i in range(nq) for t in gt[i] if int(t) in list_of]
+    top_m = int(tune_percentile(ranks, 0.995))
+    max_rank = max(ranks)
+    hits = np.bincount(np.asarray(ranks) - 1, minlength=max_rank)
+    p1, _ = tune_elbow(hits, len(ranks))
+    pq_, pl_, pt_, in_p1 = [], [], [], []
+    for i in range(nq):
+        for t in gt[i]:
+            c = list_of.get(int(t), -1)
+            if c < 0:
+                continue
+            pq_.append(i); pl_.append(c); pt_.append(int(t)); in_p1.append(rank_of[i, c] <= min(p1, nl))
+    _, _, pr, _, _ = tune_list_stats(q, cent, codebook, offsets, ids, codes, base, pq_, pl_, pt_)
+    all_pq = [int(r) for r in pr if r > 0]
+    p1_pq = [int(r) for r, f in zip(pr, in_p1) if r > 0 and f]
+    limit_k = max(p1_pq) if p1_pq else int(tune_percentile(all_pq, 0.98))
+    ratios = []
+    for i in range(nq):
+        lists = [int(order[i, r]) for r in range(min(p1, nl)) if offsets[order[i, r] + 1] > offsets[order[i, r]]]
+        if not lists:
+            continue
+        _, _, _, _, cut = tune_list_stats(q, cent, codebook, offsets, ids, codes, None, [i] * len(lists), lists,
+                                          None, [max(limit_k, 1)] * len(lists))
+        far = int(gt[i, k - 1])
+        c = list_of.get(far, -1)
+        if c < 0:
+            continue
+        fp, _, _, _, _ = tune_list_stats(q, cent, codebook, offsets, ids, codes, None, [i], [c], [far])
+        if fp[0] < 0:
+            continue
+        mc = np.float32(cut.min())
+        if mc > 0:
+            ratios.append(np.float32(fp[0] / mc))
+    coeff = max(ratios) if ratios else np.float32(2.0)
+    return top_m, p1, limit_k, np.float32(coeff)
 
 
 def graph_search(q, base, graph, k, itopk=64, width=4, max_iter=64, seed=1, nthreads=0):

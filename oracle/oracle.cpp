@@ -46,6 +46,13 @@
 //                         step count; a planted bitmap collision drops a node
 //   orc_gen_gmm           no reference counterpart: the synthetic workload
 //                         generator; pinned by moments and determinism
+//   orc_tune_list_stats   LUT entries against the fused chain evaluated in
+//                         exact rational arithmetic with one correct rounding
+//                         per step; on dyadic data (every operation exact)
+//                         distances and ranks against numpy brute force; the
+//                         k-th value and the ranks against sorted numpy arrays
+//   orc_tune_coarse_order brute force numpy sort with the tie rule, distances
+//                         as separately rounded float32 products and sums
 #include <algorithm>
 #include <cfloat>
 #include <climits>
@@ -802,6 +809,113 @@ void orc_build_lists(const int* assign, long long n, int nlist, const uint8_t* c
     int p = pos[assign[i]]++;
     ids[p] = (int)i;
     std::memcpy(list_codes + (size_t)p * m, codes + (size_t)i * m, m);
+  }
+}
+
+
+// ---------------------------------------------------------------------------
+// Offline tuner (tune_parameters.cu:459-1012), the per-(query, list) part.
+// For each pair: the tuner's own LUT (precompute_lut_kernel, :101-123; built
+// by nvcc, so `dist += diff*diff` is fused: dist = fmaf(diff, diff, dist) from
+// 0 over the sub-vector, with diff = (q - c) - codeword), the PQ distance as an
+// ascending sum of LUT entries (:127-145), the exact distance as the fused
+// chain over all dimensions (:148-166).  At the first list position holding
+// the target id: its distances and 1 + the count strictly below each
+// (:755-784); the min(kth, n)-th smallest PQ distance (:893-899).  Absent
+// target: ranks 0, distances -1.  base == nullptr: no exact part.
+void orc_tune_list_stats(const float* q, int nq, int dim, const float* cent, int nlist, const float* codebook,
+                         int m, const int* offsets, const int* ids, const uint8_t* codes, const float* base,
+                         long long n_base, const int* pair_q, const int* pair_l, const int* pair_t,
+                         const int* pair_k, int npairs, float* t_pq, float* t_ex, int* pq_rank, int* ex_rank,
+                         float* kth_pq, int nthreads) {
+  set_threads(nthreads);
+  const int S = dim / m;
+#pragma omp parallel for schedule(dynamic, 1)
+  for (int p = 0; p < npairs; ++p) {
+    const int qi = pair_q[p], l = pair_l[p];
+    const int target = pair_t ? pair_t[p] : -1, kk = pair_k ? pair_k[p] : 0;
+    if (qi < 0 || qi >= nq || l < 0 || l >= nlist) {
+      if (pair_t) { t_pq[p] = -1.0f; t_ex[p] = -1.0f; pq_rank[p] = 0; ex_rank[p] = 0; }
+      if (pair_k) kth_pq[p] = 0.0f;
+      continue;
+    }
+    const float* qv = q + (size_t)qi * dim;
+    const float* cv = cent + (size_t)l * dim;
+    std::vector<float> lut((size_t)m * kPQK);
+    for (int mm = 0; mm < m; ++mm)
+      for (int k = 0; k < kPQK; ++k) {
+        const float* cw = codebook + ((size_t)mm * kPQK + k) * S;
+        float dist = 0.0f;
+        for (int d = 0; d < S; ++d) {
+          const float r = qv[mm * S + d] - cv[mm * S + d];
+          const float diff = r - cw[d];
+          dist = std::fmaf(diff, diff, dist);
+        }
+        lut[(size_t)mm * kPQK + k] = dist;
+      }
+    const int st = offsets[l], n = offsets[l + 1] - st;
+    std::vector<float> pq(n), ex(n);
+    for (int j = 0; j < n; ++j) {
+      float sum = 0.0f;
+      for (int mm = 0; mm < m; ++mm) sum += lut[(size_t)mm * kPQK + codes[(size_t)(st + j) * m + mm]];
+      pq[j] = sum;
+      const int id = ids[st + j];
+      ex[j] = (base && id >= 0 && id < n_base) ? l2_fma(qv, base + (size_t)id * dim, dim) : INFINITY;
+    }
+    if (pair_t) {
+      int pos = -1;
+      for (int j = 0; j < n && pos < 0 && target >= 0; ++j)
+        if (ids[st + j] == target) pos = j;
+      if (pos < 0) {
+        t_pq[p] = -1.0f; t_ex[p] = -1.0f; pq_rank[p] = 0; ex_rank[p] = 0;
+      } else {
+        int bp = 0, be = 0;
+        for (int j = 0; j < n; ++j) {
+          bp += pq[j] < pq[pos];
+          be += ex[j] < ex[pos];
+        }
+        t_pq[p] = pq[pos];
+        pq_rank[p] = bp + 1;
+        t_ex[p] = base ? ex[pos] : -1.0f;
+        ex_rank[p] = base ? be + 1 : 0;
+      }
+    }
+    if (pair_k && kk > 0) {
+      if (n == 0) {
+        kth_pq[p] = 0.0f;
+      } else {
+        std::vector<float> srt(pq);
+        std::sort(srt.begin(), srt.end());
+        kth_pq[p] = srt[(size_t)std::min(kk, n) - 1];
+      }
+    }
+  }
+}
+
+// The tuner's coarse order (tune_parameters.cu:533-546): host-form squared
+// distances (g++ for x86-64 without FMA: `dist += diff*diff` rounds the
+// product and the sum separately) and std::sort over (distance, list id).
+// order[i][r] = list at 0-based position r; rank_of[i][c] = 1-based position.
+void orc_tune_coarse_order(const float* q, int nq, const float* cent, int nlist, int dim, int* order,
+                           int* rank_of, int nthreads) {
+  set_threads(nthreads);
+#pragma omp parallel for schedule(static)
+  for (int i = 0; i < nq; ++i) {
+    std::vector<std::pair<float, int>> v(nlist);
+    for (int c = 0; c < nlist; ++c) {
+      float dist = 0.0f;
+      for (int d = 0; d < dim; ++d) {
+        const float diff = q[(size_t)i * dim + d] - cent[(size_t)c * dim + d];
+        const float sq = diff * diff;
+        dist = dist + sq;
+      }
+      v[c] = {dist, c};
+    }
+    std::sort(v.begin(), v.end());
+    for (int r = 0; r < nlist; ++r) {
+      order[(size_t)i * nlist + r] = v[r].second;
+      rank_of[(size_t)i * nlist + v[r].second] = r + 1;
+    }
   }
 }
 
