@@ -70,13 +70,7 @@ __device__ __forceinline__ void scan_list(const float* smem, const uint8_t* __re
     uint64_t thr = own < shared_thr ? own : shared_thr;
     float d0, d1;
     if (adc_sum2<M>(lut, w0, w1, v0 < n, v1 < n, __uint_as_float((uint32_t)(thr >> 32)), d0, d1)) {
-      bool changed = offer_k(key_of(d0, i0), v0 < n, thr, lk);
-      if (changed) {
-        const uint64_t kth = readlane64(lk, k - 1);
-        thr = kth < thr ? kth : thr;
-      }
-      changed |= offer_k(key_of(d1, i1), v1 < n, thr, lk);
-      if (changed) {
+      if (offer2_k(v0 < n ? key_of(d0, i0) : kPadKey, v1 < n ? key_of(d1, i1) : kPadKey, thr, k, lk)) {
         own = readlane64(lk, k - 1);
         if (lane == 0) atomicMin(s_thr, (unsigned long long)own);
       }
@@ -139,13 +133,7 @@ __device__ __forceinline__ void scan_round_lb(const float* smem, int v0, int n, 
   const int v1 = v0 + kWave;
   float d0, d1;
   if (adc_sum2_lb<M>(lut, w0, w1, v0 < n, v1 < n, thr_hi, T, d0, d1)) {
-    bool changed = offer_k(key_of(d0, i0), v0 < n, thr, lk);
-    if (changed) {
-      const uint64_t kth = readlane64(lk, k - 1);
-      thr = kth < thr ? kth : thr;
-    }
-    changed |= offer_k(key_of(d1, i1), v1 < n, thr, lk);
-    if (changed) {
+    if (offer2_k(v0 < n ? key_of(d0, i0) : kPadKey, v1 < n ? key_of(d1, i1) : kPadKey, thr, k, lk)) {
       own = readlane64(lk, k - 1);
       if ((threadIdx.x & 63) == 0) atomicMin(s_thr, (unsigned long long)own);
     }

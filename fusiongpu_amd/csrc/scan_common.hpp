@@ -132,6 +132,45 @@ __device__ __forceinline__ bool offer_k(uint64_t key, bool valid, uint64_t thr, 
   return true;
 }
 
+// Offer a round's two keys per lane (kPadKey for an invalid vector) to the
+// running list lk; `kk` is the rank whose key bounds later candidates.  Few
+// passers are inserted one by one.  Many passers (the first round of a list
+// or query) are split per lane into the smaller and the larger key: the 64
+// smaller ones are sorted and merged in (taken as they are when lk is still
+// empty), and only the larger keys below the updated kk-th key follow.  For
+// kk much below 64 almost none do, so a first round costs one 64-lane sort.
+// Returns true if lk changed.
+__device__ __forceinline__ bool offer2_k(uint64_t k0, uint64_t k1, uint64_t thr, int kk, uint64_t& lk) {
+  const bool p0 = k0 < thr, p1 = k1 < thr;
+  uint64_t b0 = __ballot(p0), b1 = __ballot(p1);
+  const int c = __popcll(b0) + __popcll(b1);
+  if (c == 0) return false;
+  if (c <= kSerialMax) {
+    while (b0) {
+      const int src = __ffsll((unsigned long long)b0) - 1;
+      b0 &= b0 - 1;
+      wave_insert64_k(lk, readlane64(k0, src));
+    }
+    while (b1) {
+      const int src = __ffsll((unsigned long long)b1) - 1;
+      b1 &= b1 - 1;
+      wave_insert64_k(lk, readlane64(k1, src));
+    }
+    return true;
+  }
+  const uint64_t a = p0 ? k0 : kPadKey, b = p1 ? k1 : kPadKey;
+  uint64_t lo = a < b ? a : b;
+  const uint64_t hi = a < b ? b : a;
+  wave_sort64_k(lo);
+  if (readlane64(lk, 0) == kPadKey)
+    lk = lo;  // an empty list: the sorted keys are the list
+  else
+    wave_merge_sorted64_k(lk, lo);
+  const uint64_t kth = readlane64(lk, kk - 1);
+  offer_k(hi, true, kth < thr ? kth : thr, lk);
+  return true;
+}
+
 // Each scanning wave takes 128 consecutive vectors per round (two per lane).
 constexpr int kVecPerWaveRound = 2 * kWave;
 

@@ -156,7 +156,7 @@ __global__ __launch_bounds__(kTT) void two_phase_kernel(TwoPhaseArgs a) {
   __shared__ unsigned long long s_pub[kTW];  // phase 1: each wave's Q-th best key of the current list
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int kc = tid & (kPQK - 1), g = tid / kPQK;
+  const int kc = tid & (kPQK - 1), g = __builtin_amdgcn_readfirstlane(tid / kPQK);
   const int q = blockIdx.x;
   const int P = a.nprobe, p1 = a.p1, R = a.rerank_m, cap = a.pool_cap, K1 = a.limit_k;
   // If every wave holds Q = ceil(K1 / 8) vectors at or below its published
@@ -227,13 +227,16 @@ __global__ __launch_bounds__(kTT) void two_phase_kernel(TwoPhaseArgs a) {
 
   float* lut = smem;
   auto build_lut = [&](const float* r) {
+    int kcv = kc;
+    asm volatile("" : "+v"(kcv));
+    float* dst = lut + g * MG * kPQK + kcv;
+    const float* rg = r + g * MG * C::S;
 #pragma unroll
     for (int mm = 0; mm < MG; ++mm) {
-      const int m = g * MG + mm;
       float rr[C::S];
 #pragma unroll
-      for (int j = 0; j < C::S; ++j) rr[j] = r[m * C::S + j];
-      lut[m * kPQK + kc] = lut_entry<C::S>(rr, cb + mm * C::S);
+      for (int j = 0; j < C::S; ++j) rr[j] = rg[mm * C::S + j];
+      dst[mm * kPQK] = lut_entry<C::S>(rr, cb + mm * C::S);
     }
   };
 
@@ -284,13 +287,7 @@ __global__ __launch_bounds__(kTT) void two_phase_kernel(TwoPhaseArgs a) {
       }
       float d0, d1;
       if (adc_sum2<M>(lut, w0, w1, v0 < n, v1 < n, __uint_as_float((uint32_t)(thr >> 32)), d0, d1)) {
-        bool changed = offer_k(key_of(d0, i0), v0 < n, thr, lk);
-        if (changed) {
-          const uint64_t kth = readlane64(lk, K1 - 1);
-          thr = kth < thr ? kth : thr;
-        }
-        changed |= offer_k(key_of(d1, i1), v1 < n, thr, lk);
-        if (changed) {
+        if (offer2_k(v0 < n ? key_of(d0, i0) : kPadKey, v1 < n ? key_of(d1, i1) : kPadKey, thr, K1, lk)) {
           own = readlane64(lk, K1 - 1);
           const uint64_t qth = readlane64(lk, Q - 1);
           if (lane == 0) {
