@@ -37,6 +37,11 @@ constexpr int kTT = kTW * kWave;                     // 512 threads
 constexpr int kTRound = kTW * kVecPerWaveRound;      // vectors per workgroup round
 constexpr int kSortMax = 4096;                       // rerank_m limit (final LDS sort)
 constexpr uint64_t kNoKey = ~0ull;                   // "no admission bound yet"
+// Phase 1 stages the eight sorted wave lists of up to kStage lists; all waves
+// merge the staged lists in parallel when the stage is full and at the end of
+// phase 1, so no merge sits between two lists.
+constexpr int kStage = 16;
+constexpr int kStageFloats = kStage * kTW * kWave * 2;
 
 template <int D, int M>
 struct TCfg {
@@ -141,10 +146,13 @@ __global__ __launch_bounds__(kTT) void two_phase_kernel(TwoPhaseArgs a) {
   constexpr int MG = M / G;      // subspaces per thread in the LUT build
   static_assert(M % G == 0 && M % 16 == 0 && D % M == 0, "geometry");
   static_assert(D <= 2 * kWave, "the list bound takes two residual coordinates per lane");
-  __shared__ __align__(16) float smem[C::SMEM];
+  // The LUT (later the sort area) opens the array so that every LUT row is
+  // within the 16-bit immediate offset of a DS instruction; the phase-1 stage
+  // follows it.
+  __shared__ __align__(16) float smem[C::SMEM + kStageFloats];
   __shared__ float rbuf[2][D];
   __shared__ float qs[D];
-  __shared__ uint64_t mk[kTW * kWave];  // the waves' sorted lists of the current list
+  __shared__ int st_f[kStage], st_base[kStage];
   __shared__ int hist[256];
   __shared__ int misc[4];
   __shared__ float s_cut[64];
@@ -249,7 +257,25 @@ __global__ __launch_bounds__(kTT) void two_phase_kernel(TwoPhaseArgs a) {
   auto count_load = [&](int base, int end) { st_load += (unsigned)max(0, min(kVecPerWaveRound, end - base)); };
 
   // ---------------- phase 1: per-list top-limit_k and cutoffs
-  int cnt_w0 = 0;  // only wave 0 appends during phase 1
+  int cnt_p1 = 0;  // pool entries of the phase-1 lists so far (the same in every wave)
+  int nst = 0;     // lists staged
+  uint64_t(*stage)[kTW * kWave] = reinterpret_cast<uint64_t(*)[kTW * kWave]>(smem + C::SMEM);
+  // Merge round: wave w merges staged lists w, w + 8, ...; the list's w best
+  // keys go to its pool slots and the w-th distance is its cutoff.
+  auto flush = [&]() {
+    for (int t = wave; t < nst; t += kTW) {
+      uint64_t k = stage[t][lane];
+#pragma unroll 1
+      for (int v = 1; v < kTW; ++v) wave_merge_sorted64_k(k, stage[t][v * kWave + lane]);
+      const int lf = st_f[t], n = f_n[lf];
+      const int w = n < K1 ? n : K1;
+      if (lane < w) pool[st_base[t] + lane] = k;
+      const float cut = key_dist(readlane64(k, w - 1));
+      if (lane == 0) s_cut[f_p[lf]] = cut;
+    }
+    nst = 0;
+    __syncthreads();  // the stage is free again
+  };
   long long c_build = 0, c_scan = 0, c_merge = 0;
   for (int f = 0; f < nv1; ++f) {
     const long long c0 = a.stats ? clock64() : 0;
@@ -258,8 +284,8 @@ __global__ __launch_bounds__(kTT) void two_phase_kernel(TwoPhaseArgs a) {
     load_pair<M>(a.codes, a.vec_ids, start, n, first + lane, w0, w1, i0, i1);
     count_load(first, n);
     ++st_lut;
-    // All waves have finished scanning list f-1 (they passed its merge
-    // barrier), so the single LUT buffer is free; wave 0 may still be merging.
+    // All waves have finished scanning list f-1 (they passed the barrier
+    // after it), so the single LUT buffer is free.
     build_lut(rbuf[it & 1]);
     const int nf = f + 1 < nv ? f + 1 : -1;
     if (nf >= 0) residual(nf, rbuf[(it + 1) & 1]);
@@ -307,21 +333,19 @@ __global__ __launch_bounds__(kTT) void two_phase_kernel(TwoPhaseArgs a) {
       }
     }
     const long long c2 = a.stats ? clock64() : 0;
-    mk[wave * kWave + lane] = lk;
-    __syncthreads();  // every wave's list for list f is in LDS
-    if (wave == 0) {
-#pragma unroll 1
-      for (int w = 1; w < kTW; ++w) wave_merge_sorted64_k(lk, mk[w * kWave + lane]);
-      const int w = n < K1 ? n : K1;
-      if (lane < w) pool[cnt_w0 + lane] = lk;
-      const float cut = key_dist(readlane64(lk, w - 1));
-      if (lane == 0) {
-        s_cut[f_p[f]] = cut;
-        s_lthr = kNoThr;
-      }
-      if (lane < kTW) s_pub[lane] = kNoThr;
-      cnt_w0 += w;
+    stage[nst][wave * kWave + lane] = lk;
+    if (tid == 0) {
+      st_f[nst] = f;
+      st_base[nst] = cnt_p1;
     }
+    cnt_p1 += n < K1 ? n : K1;
+    ++nst;
+    __syncthreads();  // every wave is through list f: its list is staged, the LUT is free
+    if (wave == 0) {
+      if (lane == 0) s_lthr = kNoThr;
+      if (lane < kTW) s_pub[lane] = kNoThr;
+    }
+    if (nst == kStage || f == nv1 - 1) flush();
     if (a.stats) {
       const long long c3 = clock64();
       c_build += c1 - c0;
@@ -331,7 +355,7 @@ __global__ __launch_bounds__(kTT) void two_phase_kernel(TwoPhaseArgs a) {
     ++it;
     pre_f = nf;
   }
-  if (tid == 0) s_cnt = cnt_w0;
+  if (tid == 0) s_cnt = cnt_p1;
   __syncthreads();
   const long long t_phase1 = a.stats ? clock64() : 0;
 

@@ -92,6 +92,33 @@ def test_two_phase_bit_exact(dim, m, p1, limit_k, coeff, rerank_m):
     idx.close()
 
 
+def test_two_phase_many_phase1_lists():
+    """More phase-1 lists than the kernel stages at once (16): the staged
+    wave lists are merged in several rounds; unusable probes inside phase 1."""
+    _say("two_phase p1=37 of nprobe=40")
+    rng = np.random.default_rng(4040)
+    nlist = 64
+    offs, ids, lc, cent, cb = _index(rng, 40000, 96, 32, nlist, empty=(5, 9, 30), big=12)
+    q = (rng.standard_normal((90, 96)) * 0.7).astype(np.float32)
+    probes, _ = oracle.coarse(q, cent, 40)
+    probes[3, 7] = 0xFFFFFFFF
+    probes[4, 20] = 5                    # an empty list inside phase 1
+    probes[10, :17] = 0xFFFFFFFF         # exactly 20 usable phase-1 lists
+    p1, limit_k, coeff, rerank_m = 37, 24, 1.1, 700
+    idx = fg.Index.from_arrays(96, 32, offs, ids, lc, cent, cb)
+    gid, gd, gcnt, gcut, gthr = idx.two_phase_search(torch.from_numpy(q).cuda(),
+                                                     torch.from_numpy(probes.view(np.int32)).cuda(), p1, limit_k,
+                                                     coeff, rerank_m, want_cutoffs=True)
+    oid, od, ocnt, ocut, othr = oracle.search_two_phase(q, cent, cb, offs, ids, lc, probes, p1, limit_k, coeff,
+                                                        rerank_m)
+    assert np.array_equal(_host(gcnt), ocnt)
+    assert np.array_equal(_host(gid), oid)
+    assert np.array_equal(_bits(_host(gd)), _bits(od))
+    assert np.array_equal(_bits(_host(gcut)), _bits(ocut))
+    assert np.array_equal(_bits(_host(gthr)), _bits(othr))
+    idx.close()
+
+
 def test_two_phase_workspace_chunks_equal_one_launch():
     _say("two_phase chunked workspace")
     rng = np.random.default_rng(77)
