@@ -122,9 +122,39 @@ __global__ __launch_bounds__(256) void gemm_est_kernel(const float* __restrict__
 
 constexpr int kCandCap = 256;
 
+// Ascending bitonic sort of one 32-bit key per lane across the wave.
+template <int S>
+__device__ __forceinline__ void bitonic_stage_u32(uint32_t& k, bool up) {
+  const uint32_t o = (uint32_t)xchg<S>((int)k);
+  const bool lower = (lane_id() & S) == 0;
+  k = ((k < o) == (lower == up)) ? k : o;
+}
+template <int SIZE>
+__device__ __forceinline__ void bitonic_pass_u32(uint32_t& k, bool up) {
+  if constexpr (SIZE > 32) bitonic_stage_u32<32>(k, up);
+  if constexpr (SIZE > 16) bitonic_stage_u32<16>(k, up);
+  if constexpr (SIZE > 8) bitonic_stage_u32<8>(k, up);
+  if constexpr (SIZE > 4) bitonic_stage_u32<4>(k, up);
+  if constexpr (SIZE > 2) bitonic_stage_u32<2>(k, up);
+  bitonic_stage_u32<1>(k, up);
+}
+__device__ __forceinline__ void wave_sort_u32(uint32_t& k) {
+  const int lane = lane_id();
+  bitonic_pass_u32<2>(k, (lane & 2) == 0);
+  bitonic_pass_u32<4>(k, (lane & 4) == 0);
+  bitonic_pass_u32<8>(k, (lane & 8) == 0);
+  bitonic_pass_u32<16>(k, (lane & 16) == 0);
+  bitonic_pass_u32<32>(k, (lane & 32) == 0);
+  bitonic_pass_u32<64>(k, true);
+}
+
 // The p-th smallest of the wave's estimates val[j] (column j*64 + lane, only
 // columns < ncols count): LDS radix select, 8 bits a pass, over the
 // order-preserving integer map of the floats.  p == 1 is a plain minimum.
+// For p <= 64 the p-th smallest of the 64 per-lane minima bounds the answer
+// from above (those minima are p of the keys), and only keys at or below it
+// enter the histograms: the first passes otherwise pile most of the keys into
+// one or two bins, whose LDS atomics serialise.
 template <int VPL>
 __device__ float wave_kth_estimate(const float (&val)[VPL], int ncols, int p, uint32_t* hist) {
   const int lane = threadIdx.x & 63;
@@ -137,6 +167,14 @@ __device__ float wave_kth_estimate(const float (&val)[VPL], int ncols, int p, ui
   uint32_t key[VPL];
 #pragma unroll
   for (int j = 0; j < VPL; ++j) key[j] = (j * kWave + lane < ncols) ? float_key(val[j]) : 0xFFFFFFFFu;
+  uint32_t cap = 0xFFFFFFFFu;
+  if (p <= kWave) {
+    uint32_t mn = key[0];
+#pragma unroll
+    for (int j = 1; j < VPL; ++j) mn = key[j] < mn ? key[j] : mn;
+    wave_sort_u32(mn);
+    cap = (uint32_t)readlane_i((int)mn, p - 1);
+  }
   uint32_t prefix = 0, mask = 0;
   uint32_t rem = (uint32_t)p;
   for (int shift = 24; shift >= 0; shift -= 8) {
@@ -144,7 +182,7 @@ __device__ float wave_kth_estimate(const float (&val)[VPL], int ncols, int p, ui
     wave_lds_sync();
 #pragma unroll
     for (int j = 0; j < VPL; ++j)
-      if ((key[j] & mask) == prefix) atomicAdd(&hist[(key[j] >> shift) & 255u], 1u);
+      if ((key[j] & mask) == prefix && key[j] <= cap) atomicAdd(&hist[(key[j] >> shift) & 255u], 1u);
     wave_lds_sync();
     const uint32_t h0 = hist[4 * lane], h1 = hist[4 * lane + 1], h2 = hist[4 * lane + 2],
                    h3 = hist[4 * lane + 3];
