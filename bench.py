@@ -12,7 +12,11 @@ coarse quantizer (MFMA GEMM + exact re-score + top-32) and LUT + ADC scan +
 top-10.  value = 10k / step time.  The roofline entry is for the dominant
 kernel, the ADC scan: algorithmic bytes = sum over (query, probe) of
 list_len * M code bytes, divided by the scan kernel's average duration from HIP
-events recorded on the stream it runs on.
+events recorded on the stream it runs on.  The line also carries
+`graph_coarse`: the same coarse step done the reference's way (a graph walk over
+the centroids instead of the exact GEMM; not timed in `value`), with its time,
+the share of the exact top-32 lists it finds and how often the top-10 stays
+identical.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--cpu-queries N] [--workload c2|c3|c4|c5]
 
@@ -165,6 +169,34 @@ def main():
         f"= {loaded_gbs:.0f} GB/s; LUTs built {st['luts_built']}, probed lists skipped {st['lists_skipped']} "
         f"of {int((probes.view(torch.int32) >= 0).sum().item())}")
 
+    # ---- the graph coarse mode (the reference's CAGRA-over-centroids step): time and
+    # how many of the exact top-nprobe lists it finds, and the end-to-end top-10 it gives;
+    # the reference's graph degree (8) and a denser graph (32), its search parameters
+    graph_coarse = []
+    ep = probes.cpu().numpy().view(np.uint32)
+    for degree in (8, 32):
+        t0 = time.perf_counter()
+        cgraph = idx.coarse_graph_build(degree)
+        torch.cuda.synchronize()
+        graph_build_ms = 1e3 * (time.perf_counter() - t0)
+        gprobes, _ = idx.coarse_graph_search(dq, nprobe, cgraph)
+        ev[0].record(stream)
+        for _ in range(reps):
+            idx.coarse_graph_search(dq, nprobe, cgraph)
+        ev[1].record(stream)
+        torch.cuda.synchronize()
+        graph_ms = ev[0].elapsed_time(ev[1]) / reps
+        gp = gprobes.cpu().numpy().view(np.uint32)
+        probe_recall = float(np.mean([len(set(a_) & set(b_)) / nprobe for a_, b_ in zip(gp, ep)]))
+        gids, _ = idx.adc_search(dq, gprobes, k)
+        same_topk = float((gids == out[0]).all(dim=1).float().mean().item())
+        graph_coarse.append({"degree": degree, "itopk": 32, "width": 4, "max_iter": 200,
+                             "coarse_ms": round(graph_ms, 4), "graph_build_ms": round(graph_build_ms, 2),
+                             "probe_recall_vs_exact": round(probe_recall, 4),
+                             "queries_with_identical_top10": round(same_topk, 4)})
+        log(f"graph coarse mode, degree {degree}: {graph_ms:.3f} ms (build {graph_build_ms:.1f} ms), finds "
+            f"{probe_recall:.4f} of the exact top-{nprobe} lists; top-10 identical for {same_topk:.4f} of the queries")
+
     if args.copy_probe:
         a = torch.empty(1 << 28, dtype=torch.float32, device=dev)
         b = torch.empty_like(a)
@@ -225,6 +257,7 @@ def main():
                       "coarse_tflops_incl_select": round(gemm_flop / coarse_ms / 1e9, 2)},
         "cpu_baseline": cpu,
         "parity": parity,
+        "graph_coarse": graph_coarse,
     }
     print(json.dumps(res), flush=True)
 

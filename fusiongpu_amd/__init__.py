@@ -49,6 +49,10 @@ _SIGS = {
     "fgpu_index_get_info": (_i32, [_vp, _vp]),
     "fgpu_coarse_workspace_bytes": (_sz, [_i32, _i32]),
     "fgpu_coarse_search": (_i32, [_vp, _vp, _i32, _i32, _f32, _vp, _vp, _vp, _sz, _vp]),
+    "fgpu_coarse_graph_workspace_bytes": (_sz, [_i32, _i32]),
+    "fgpu_coarse_graph_build": (_i32, [_vp, _i32, _vp, _vp, _sz, _vp]),
+    "fgpu_coarse_graph_search": (_i32, [_vp, _vp, _i32, _i32, _i32, _vp, _i32, _i32, _i32, _i32, _u64, _f32, _vp,
+                                        _vp, _vp]),
     "fgpu_probe_counts": (_i32, [_vp, _vp, _i32, _i32, _vp, _vp, _vp]),
     "fgpu_adc_search": (_i32, [_vp, _vp, _i32, _vp, _i32, _i32, _vp, _vp, _vp]),
     "fgpu_adc_search_stats": (_i32, [_vp, _vp, _i32, _vp, _i32, _i32, _vp, _vp, _vp, _vp]),
@@ -277,6 +281,30 @@ class Index:
                                               torch.empty((nq, nprobe), dtype=torch.float32, device="cuda"))
         _check(lib.fgpu_coarse_search(self._h, _dev_ptr(q), nq, nprobe, prune_ratio, _dev_ptr(ids), _dev_ptr(d),
                                       _dev_ptr(ws), ws.numel(), _stream(stream)))
+        return ids, d
+
+    def coarse_graph_build(self, degree: int = 8, stream=None):
+        """Exact kNN graph of the centroids, self excluded (fgpu_coarse_graph_build): int32 [nlist][degree]."""
+        torch = _torch()
+        g = torch.empty((self.nlist, degree), dtype=torch.int32, device="cuda")
+        ws = _workspace(lib.fgpu_coarse_graph_workspace_bytes(self.nlist, degree))
+        _check(lib.fgpu_coarse_graph_build(self._h, degree, _dev_ptr(g), _dev_ptr(ws), ws.numel(), _stream(stream)))
+        return g
+
+    def coarse_graph_search(self, queries, nprobe: int, graph, itopk: int = 32, width: int = 4, max_iter: int = 200,
+                            seed: int = 1, prune_ratio: float = 100.0, first_query: int = 0, out=None,
+                            stream=None):
+        """Top-nprobe lists by the graph walk over the centroids (fgpu_coarse_graph_search): (probe_ids
+        uint32-as-int32 [nq][nprobe], dists [nq][nprobe])."""
+        torch = _torch()
+        q = _to_dev(queries)
+        g = _to_dev(graph)
+        nq = q.shape[0]
+        ids, d = out if out is not None else (torch.empty((nq, nprobe), dtype=torch.int32, device="cuda"),
+                                              torch.empty((nq, nprobe), dtype=torch.float32, device="cuda"))
+        _check(lib.fgpu_coarse_graph_search(self._h, _dev_ptr(q), nq, first_query, nprobe, _dev_ptr(g), g.shape[1],
+                                            itopk, width, max_iter, seed, prune_ratio, _dev_ptr(ids), _dev_ptr(d),
+                                            _stream(stream)))
         return ids, d
 
     def adc_search(self, queries, probe_ids, k: int, out=None, stream=None):

@@ -595,6 +595,10 @@ __global__ __launch_bounds__(kSpecWaves * kWave, 4) void adc_flow_kernel(AdcArgs
     }
   } else {
     const int swave = wave - kBuilderWaves;
+    // Scanner instructions issue ahead of the builders' on a shared SIMD: the
+    // builders run ahead of the scanners and have slack, the scanners set the
+    // pace (3% on C2).
+    __builtin_amdgcn_s_setprio(2);
     // This wave's first chunk at or after chunk cc.
     auto first_own = [&](int cc) { return cc + (((swave - cc) % kScanWaves) + kScanWaves) % kScanWaves; };
     uint4 w0[C::NV4], w1[C::NV4];

@@ -3,16 +3,20 @@
 //   search_pipeline <base> <query> [gt] [-b batch] [-m top_m] [-r rerank_m]
 //     [-mb mini_batch] [-e epsilon] [--beta b] [-p prune_ratio] [-s streams]
 //     [-k topk] [--p1_lists n] [--limit_k n] [--threshold_coeff c]
-//     [--pq_m M] [--res DIR] [--out ids.ivecs]
+//     [--pq_m M] [--res DIR] [--out ids.ivecs] [--coarse exact|graph]
+//     [--graph_degree 8]
 // It loads <res>/ivf_data.bin + global_pq_codebook.bin, keeps the base
 // vectors in HBM for the exact rerank, runs the query batches through S
 // streams round-robin (search_pipeline.cu:168-214, 311-377) and prints the
 // reference's "Total time ... QPS" and "Recall@1/@10" lines plus a per-stage
 // timing table.
 //
-// Per batch, on its stream: queries H2D from pinned memory, the exact coarse
-// step, the two-phase scan + top-rerank_m, the exact rerank, results D2H into
-// pinned memory.  The stream's contexts are reused round-robin; a context's
+// Per batch, on its stream: queries H2D from pinned memory, the coarse step,
+// the two-phase scan + top-rerank_m, the exact rerank, results D2H into
+// pinned memory.  The coarse step is exact by default; --coarse graph walks a
+// kNN graph of the centroids instead, with the reference's CAGRA search
+// parameters (itopk max(32, top_m), width 4, 200 iterations;
+// cagra_adapter.cuh:57-60) and graph degree 8 (cagra_adapter.cuh:15).  The stream's contexts are reused round-robin; a context's
 // results and stage times are collected when it is reused or at the end
 // (the reference hands that to a worker thread, search_pipeline.cu:392-478).
 // No call inside a batch synchronises the host.
@@ -68,9 +72,9 @@ float compute_recall(const std::vector<int32_t>& res, int k, const std::vector<i
 }  // namespace
 
 int main(int argc, char** argv) {
-  std::string base_path, query_path, gt_path, res = "../res", out_path;
+  std::string base_path, query_path, gt_path, res = "../res", out_path, coarse_mode = "exact";
   int batch = 128, top_m = 20, rerank_m = 10000, mb = 128, beta = 2, streams = 2, final_k = 10, p1_lists = 12,
-      limit_k = 50, pq_m = 32;
+      limit_k = 50, pq_m = 32, graph_degree = 8;
   float eps = 0.1f, prune_ratio = 100.0f, coeff = 1.0f;
   for (int i = 1; i < argc; ++i) {
     const std::string a = argv[i];
@@ -93,6 +97,8 @@ int main(int argc, char** argv) {
     else if (a == "--pq_m") pq_m = std::atoi(next());
     else if (a == "--res") res = next();
     else if (a == "--out") out_path = next();
+    else if (a == "--coarse") coarse_mode = next();
+    else if (a == "--graph_degree") graph_degree = std::atoi(next());
     else if (!a.empty() && a[0] != '-') {
       if (base_path.empty()) base_path = a;
       else if (query_path.empty()) query_path = a;
@@ -108,6 +114,8 @@ int main(int argc, char** argv) {
     rerank_m = 4096;
   }
   if (batch < 1 || streams < 1) { std::cerr << "batch and streams must be >= 1\n"; return 1; }
+  const bool graph_coarse = coarse_mode == "graph";
+  if (!graph_coarse && coarse_mode != "exact") { std::cerr << "--coarse must be exact or graph\n"; return 1; }
   const int dim = app::fvecs_dim(base_path);
   int64_t n = 0, nq64 = 0;
   std::vector<float> raw = app::read_fvecs(base_path, dim, n);
@@ -122,6 +130,23 @@ int main(int argc, char** argv) {
   float* d_base = nullptr;
   hip_ok(hipMalloc(&d_base, sizeof(float) * raw.size()), "hipMalloc base");
   hip_ok(hipMemcpy(d_base, raw.data(), sizeof(float) * raw.size(), hipMemcpyHostToDevice), "copy base");
+
+  // Graph coarse mode: the centroid graph is built once, here (the reference
+  // builds its CAGRA index in build_global and loads it, search_pipeline.cu:160).
+  int32_t* d_cgraph = nullptr;
+  const int itopk = std::min(64, std::max(32, top_m));
+  if (graph_coarse) {
+    if (top_m > 64) { std::cerr << "--coarse graph needs top_m <= 64\n"; return 1; }
+    hip_ok(hipMalloc(&d_cgraph, sizeof(int32_t) * (size_t)info.nlist * graph_degree), "hipMalloc graph");
+    void* gws = nullptr;
+    const size_t gws_bytes = fgpu_coarse_graph_workspace_bytes(info.nlist, graph_degree);
+    hip_ok(hipMalloc(&gws, gws_bytes), "hipMalloc graph workspace");
+    ok(fgpu_coarse_graph_build(idx, graph_degree, d_cgraph, gws, gws_bytes, nullptr), "centroid graph");
+    hip_ok(hipDeviceSynchronize(), "graph build");
+    hip_ok(hipFree(gws), "hipFree");
+    std::cout << "  centroid graph: " << info.nlist << " nodes, degree " << graph_degree << ", itopk " << itopk
+              << ", width 4, max 200 iterations\n";
+  }
 
   std::vector<Ctx> ctx(streams);
   const size_t ws = std::max(fgpu_coarse_workspace_bytes(batch, info.nlist),
@@ -168,8 +193,13 @@ int main(int argc, char** argv) {
     hip_ok(hipEventRecord(c.ev[0], c.s), "record");
     hip_ok(hipMemcpyAsync(c.d_q, c.h_q, sizeof(float) * size * dim, hipMemcpyHostToDevice, c.s), "H2D");
     hip_ok(hipEventRecord(c.ev[1], c.s), "record");
-    ok(fgpu_coarse_search(idx, c.d_q, size, top_m, prune_ratio, c.d_probes, c.d_pd, c.d_ws, c.ws_bytes, c.s),
-       "coarse search");
+    if (graph_coarse)
+      ok(fgpu_coarse_graph_search(idx, c.d_q, size, start, top_m, d_cgraph, graph_degree, itopk, 4, 200, 1,
+                                  prune_ratio, c.d_probes, c.d_pd, c.s),
+         "graph coarse search");
+    else
+      ok(fgpu_coarse_search(idx, c.d_q, size, top_m, prune_ratio, c.d_probes, c.d_pd, c.d_ws, c.ws_bytes, c.s),
+         "coarse search");
     hip_ok(hipEventRecord(c.ev[2], c.s), "record");
     ok(fgpu_two_phase_search(idx, c.d_q, size, c.d_probes, top_m, p1_lists, limit_k, coeff, rerank_m, c.d_tid, c.d_td,
                              c.d_tcnt, nullptr, nullptr, c.d_ws, c.ws_bytes, c.s),
@@ -243,6 +273,7 @@ int main(int argc, char** argv) {
       (void)hipFree(p);
   }
   (void)hipFree(d_base);
+  if (d_cgraph) (void)hipFree(d_cgraph);
   fgpu_index_destroy(idx);
   return 0;
 }

@@ -440,6 +440,69 @@ fgpu_status fgpu_graph_search(const float* dq, int nq, const float* d_base, int6
   return launch_graph_search(dim, a, as_stream(stream));
 }
 
+size_t fgpu_coarse_graph_workspace_bytes(int nlist, int degree) {
+  const size_t cells = (size_t)std::max(nlist, 1) * (size_t)(2 * std::max(degree, 1) + 1);
+  return 2 * carve_bytes<int32_t>(cells) + carve_bytes<float>(cells) + fgpu_knn_exact_workspace_bytes(nlist, nlist) +
+         256;
+}
+
+fgpu_status fgpu_coarse_graph_build(const fgpu_index* ix, int degree, int32_t* d_graph, void* ws, size_t ws_bytes,
+                                    void* stream) {
+  FGPU_CHECK(ix && d_graph && ws, FGPU_ERR_ARG, "coarse_graph_build: null argument");
+  FGPU_CHECK(degree >= 1 && degree <= 64 && 2 * degree < ix->nlist, FGPU_ERR_ARG,
+             "coarse_graph_build: need 1 <= degree <= 64 and 2 * degree < nlist");
+  hipStream_t s = as_stream(stream);
+  const int nl = ix->nlist, d2 = 2 * degree;
+  Carve cv(ws, ws_bytes);
+  int32_t* kid = cv.take<int32_t>((size_t)nl * (d2 + 1));
+  float* kd = cv.take<float>((size_t)nl * (d2 + 1));
+  int32_t* fwd = cv.take<int32_t>((size_t)nl * d2);
+  FGPU_CHECK(cv.ok(), FGPU_ERR_WORKSPACE, "coarse_graph_build: workspace too small");
+  // The 2 * degree nearest other centroids of each centroid (tie rule).
+  FGPU_TRY(fgpu_knn_exact(ix->d_centroids, nl, ix->d_centroids, nl, ix->dim, d2 + 1, kid, kd, cv.base + cv.used,
+                          ws_bytes - cv.used, stream));
+  FGPU_TRY(launch_drop_self(kid, nl, d2, fwd, s));
+  std::vector<int32_t> f((size_t)nl * d2), g((size_t)nl * degree);
+  FGPU_HIP(hipMemcpyAsync(f.data(), fwd, sizeof(int32_t) * f.size(), hipMemcpyDeviceToHost, s));
+  FGPU_HIP(hipStreamSynchronize(s));
+  // Reverse edges, as CAGRA adds them (Ootomo et al., 2023): u -> v of the
+  // degree-nearest lists, listed at v by (rank of v in u's list, u).
+  std::vector<std::vector<std::pair<int, int>>> rev(nl);
+  for (int u = 0; u < nl; ++u)
+    for (int r = 0; r < degree; ++r) rev[f[(size_t)u * d2 + r]].push_back({r, u});
+  const int nf = degree - degree / 2;
+  for (int v = 0; v < nl; ++v) {
+    std::sort(rev[v].begin(), rev[v].end());
+    int32_t* o = g.data() + (size_t)v * degree;
+    int cnt = 0;
+    auto add = [&](int id) {
+      if (cnt < degree && std::find(o, o + cnt, id) == o + cnt) o[cnt++] = id;
+    };
+    for (int r = 0; r < nf; ++r) add(f[(size_t)v * d2 + r]);
+    for (size_t j = 0; j < rev[v].size() && cnt < degree; ++j) add(rev[v][j].second);
+    for (int r = nf; r < d2 && cnt < degree; ++r) add(f[(size_t)v * d2 + r]);
+  }
+  FGPU_HIP(hipMemcpyAsync(d_graph, g.data(), sizeof(int32_t) * g.size(), hipMemcpyHostToDevice, s));
+  FGPU_HIP(hipStreamSynchronize(s));
+  return FGPU_OK;
+}
+
+fgpu_status fgpu_coarse_graph_search(const fgpu_index* ix, const float* dq, int nq, int first_query, int nprobe,
+                                     const int32_t* d_graph, int degree, int itopk, int width, int max_iter,
+                                     uint64_t seed, float prune_ratio, uint32_t* d_probe_ids, float* d_probe_dists,
+                                     void* stream) {
+  FGPU_CHECK(ix && dq && d_graph && d_probe_ids && d_probe_dists, FGPU_ERR_ARG, "coarse_graph_search: null argument");
+  FGPU_CHECK(nq >= 0 && first_query >= 0 && nprobe >= 1 && nprobe <= ix->nlist && nprobe <= itopk, FGPU_ERR_ARG,
+             "coarse_graph_search: need first_query >= 0 and 1 <= nprobe <= min(nlist, itopk)");
+  if (nq == 0) return FGPU_OK;
+  hipStream_t s = as_stream(stream);
+  int32_t* ids = reinterpret_cast<int32_t*>(d_probe_ids);
+  GraphArgs a{dq, ix->d_centroids, (long long)ix->nlist, d_graph, degree, itopk, width, max_iter, nprobe, seed,
+              first_query, nq, ids, d_probe_dists, nullptr, nullptr};
+  FGPU_TRY(launch_graph_search(ix->dim, a, s));
+  return launch_coarse_prune(ids, d_probe_dists, nq, nprobe, prune_ratio, s);
+}
+
 fgpu_status fgpu_tune_list_stats(const fgpu_index* idx, const float* d_queries, int nq, const float* d_base,
                                  int64_t n_base, const int32_t* d_pair_query, const int32_t* d_pair_list,
                                  const int32_t* d_pair_target, const int32_t* d_pair_kth, int npairs,

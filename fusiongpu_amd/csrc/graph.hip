@@ -175,7 +175,49 @@ fgpu_status launch_graph_t(const GraphArgs& a, hipStream_t s) {
   return FGPU_OK;
 }
 
+// Row i of an exact kNN list of the points themselves ([n][degree + 1],
+// ascending) without i: the first `degree` other ids.
+__global__ __launch_bounds__(256) void drop_self_kernel(const int32_t* __restrict__ knn, int n, int degree,
+                                                        int32_t* __restrict__ out) {
+  const int row = blockIdx.x * 256 + threadIdx.x;
+  if (row >= n) return;
+  const int32_t* r = knn + (size_t)row * (degree + 1);
+  int32_t* o = out + (size_t)row * degree;
+  int j = 0;
+  for (int t = 0; t <= degree && j < degree; ++t) {
+    const int v = r[t];
+    if (v != row) o[j++] = v;
+  }
+}
+
+// The coarse prune rule (prune_and_count_fused_kernel, gpu_global.cu:43-50)
+// on graph-walk results: a probe whose distance exceeds best * prune_ratio,
+// or a slot the walk left empty (id -1), becomes 0xFFFFFFFF.
+__global__ __launch_bounds__(256) void coarse_prune_kernel(int32_t* __restrict__ ids, const float* __restrict__ d,
+                                                           int nq, int p, float prune_ratio) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (int64_t)nq * p) return;
+  const float pthr = d[i - i % p] * prune_ratio;
+  if (ids[i] < 0 || d[i] > pthr) ids[i] = (int32_t)kPruned;
+}
+
 }  // namespace
+
+fgpu_status launch_drop_self(const int32_t* knn, int n, int degree, int32_t* out, hipStream_t s) {
+  if (n <= 0) return FGPU_OK;
+  hipLaunchKernelGGL(drop_self_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, knn, n, degree, out);
+  FGPU_HIP(hipGetLastError());
+  return FGPU_OK;
+}
+
+fgpu_status launch_coarse_prune(int32_t* ids, const float* d, int nq, int p, float prune_ratio, hipStream_t s) {
+  const int64_t total = (int64_t)nq * p;
+  if (total <= 0) return FGPU_OK;
+  hipLaunchKernelGGL(coarse_prune_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, ids, d, nq, p,
+                     prune_ratio);
+  FGPU_HIP(hipGetLastError());
+  return FGPU_OK;
+}
 
 fgpu_status launch_graph_search(int dim, const GraphArgs& a, hipStream_t s) {
   FGPU_CHECK(a.n >= 1 && a.n < INT32_MAX, FGPU_ERR_ARG, "graph_search: need 1 <= n < 2^31");

@@ -123,6 +123,8 @@ struct GraphArgs {
   int32_t* evals;           // [nq] or nullptr: exact distances computed
 };
 fgpu_status launch_graph_search(int dim, const GraphArgs& a, hipStream_t s);
+fgpu_status launch_drop_self(const int32_t* knn, int n, int degree, int32_t* out, hipStream_t s);
+fgpu_status launch_coarse_prune(int32_t* ids, const float* d, int nq, int p, float prune_ratio, hipStream_t s);
 
 // ---- tune.hip -------------------------------------------------------------------
 constexpr int kMaxTuneLut = 64 * 256;  // pq_m <= 64

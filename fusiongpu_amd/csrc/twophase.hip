@@ -160,7 +160,7 @@ __global__ __launch_bounds__(kTT) void two_phase_kernel(TwoPhaseArgs a) {
   __shared__ float f_lb[64];                                 // lower bound of each phase-2 list
   __shared__ int s_nv, s_nv1;
   __shared__ int s_cnt;
-  __shared__ unsigned long long s_lthr, s_adm;
+  __shared__ unsigned long long s_lthr;
   __shared__ unsigned long long s_pub[kTW];  // phase 1: each wave's Q-th best key of the current list
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -209,7 +209,6 @@ __global__ __launch_bounds__(kTT) void two_phase_kernel(TwoPhaseArgs a) {
       s_nv1 = __popcll(bm & (p1 >= 64 ? ~0ull : ((1ull << p1) - 1ull)));
       s_cnt = 0;
       s_lthr = kNoThr;
-      s_adm = kNoKey;
     }
   }
   __syncthreads();
@@ -400,10 +399,7 @@ __global__ __launch_bounds__(kTT) void two_phase_kernel(TwoPhaseArgs a) {
       if (cnt0 + (s1 - s0) > cap) {
         adm = pool_select(pool, cnt0, R, hist, misc);
         cnt0 = R;
-        if (tid == 0) {
-          s_cnt = R;
-          s_adm = adm;
-        }
+        if (tid == 0) s_cnt = R;
         __syncthreads();
         thr_d = fminf(thr, key_dist(adm));
       }

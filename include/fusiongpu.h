@@ -223,6 +223,41 @@ fgpu_status fgpu_graph_search(const float* d_queries, int nq, const float* d_bas
                               uint64_t seed, int32_t* d_out_ids, float* d_out_dists, int32_t* d_iters,
                               int32_t* d_evals, void* stream);
 
+/* ---- graph coarse quantizer (the reference's CAGRA-over-centroids mode) -- */
+
+/* The reference builds a cuVS CAGRA graph over the coarse centroids
+ * (build_cagra_index, cagra_adapter.cuh:10-27: graph_degree 8, intermediate
+ * degree 16, called from build_global) and walks it for every query batch
+ * (search_cagra_index, cagra_adapter.cuh:38-68, from search_pipeline.cu:341).
+ * Here, with F(v) the 2*degree nearest other centroids of v in tie-rule order
+ * (fgpu_knn_exact), row v of d_graph [nlist][degree] holds the first
+ * degree - degree/2 entries of F(v), then the reverse edges: every u whose
+ * first `degree` entries of F(u) include v, by (rank of v in F(u), u), then
+ * the rest of F(v), skipping ids already present, up to degree ids.  Reverse
+ * edges as in CAGRA (Ootomo et al., 2023) keep the graph navigable; CAGRA's
+ * NN-descent and rank-based pruning and its file (cagra_centroids.index) are
+ * not reproduced.  1 <= degree <= 64, 2 * degree < nlist.  The reverse-edge
+ * step runs on the host: the call synchronises `stream`.
+ * Workspace: fgpu_coarse_graph_workspace_bytes(nlist, degree). */
+size_t fgpu_coarse_graph_workspace_bytes(int nlist, int degree);
+fgpu_status fgpu_coarse_graph_build(const fgpu_index* idx, int degree, int32_t* d_graph, void* d_workspace,
+                                    size_t workspace_bytes, void* stream);
+
+/* Approximate top-nprobe lists per query by that walk (itopk, width,
+ * max_iter, seed as in fgpu_graph_search; nprobe <= itopk <= 64; the
+ * reference uses itopk = max(32, nprobe), width 4, max_iter 200).  A query's
+ * seed nodes depend on seed and on its index first_query + i, so a query set
+ * split into batches gets the same results as one call.  Ascending
+ * (distance, list id) with exact distances (the same chain as
+ * fgpu_coarse_search), then the same prune rule; slots the walk leaves empty
+ * are 0xFFFFFFFF.  When the walk evaluates every centroid (the visited bitmap
+ * holds every id below 16384 without a collision) the result equals
+ * fgpu_coarse_search's bit for bit. */
+fgpu_status fgpu_coarse_graph_search(const fgpu_index* idx, const float* d_queries, int nq, int first_query,
+                                     int nprobe, const int32_t* d_graph, int degree, int itopk, int width,
+                                     int max_iter, uint64_t seed, float prune_ratio, uint32_t* d_probe_ids,
+                                     float* d_probe_dists, void* stream);
+
 /* ---- index build (A13-A17) -------------------------------------------- */
 
 /* One Lloyd update (kmeans_gpu.cuh:81-116) with deterministic fixed-point

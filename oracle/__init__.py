@@ -345,6 +345,41 @@ def graph_search(q, base, graph, k, itopk=64, width=4, max_iter=64, seed=1, nthr
     return oid, od, it
 
 
+def coarse_graph_build(cent, degree, nthreads=0):
+    """The centroid graph of the graph coarse mode (fgpu_coarse_graph_build): with F(v) the 2*degree nearest
+    other centroids of v (knn_exact, tie rule (distance, id)), row v holds the first degree - degree//2 entries
+    of F(v), then the u whose first `degree` entries of F(u) include v, by (rank of v in F(u), u), then the rest
+    of F(v), skipping ids already present, up to `degree` ids: int32 [nlist][degree]."""
+    cent = f32(cent)
+    nl, d2 = cent.shape[0], 2 * degree
+    ids, _ = knn_exact(cent, cent, d2 + 1, nthreads)
+    fwd = [[int(j) for j in ids[i] if j != i][:d2] for i in range(nl)]
+    rev = [[] for _ in range(nl)]
+    for u in range(nl):
+        for r in range(degree):
+            rev[fwd[u][r]].append((r, u))
+    nf = degree - degree // 2
+    out = np.empty((nl, degree), np.int32)
+    for v in range(nl):
+        row = []
+        for c in fwd[v][:nf] + [u for _, u in sorted(rev[v])] + fwd[v][nf:]:
+            if len(row) < degree and c not in row:
+                row.append(c)
+        out[v] = row
+    return out
+
+
+def coarse_graph(q, cent, graph, nprobe, itopk=32, width=4, max_iter=200, seed=1, prune_ratio=100.0, nthreads=0):
+    """The graph coarse mode: graph_search over the centroids, then the prune rule of
+    prune_and_count_fused_kernel (gpu_global.cu:43-50) in float32, empty slots pruned:
+    (ids uint32 [nq][nprobe], dists float32 [nq][nprobe])."""
+    gid, gd, _ = graph_search(q, cent, graph, nprobe, itopk, width, max_iter, seed, nthreads)
+    thr = gd[:, :1] * np.float32(prune_ratio)
+    ids = gid.view(np.uint32).copy()
+    ids[(gid < 0) | (gd > thr)] = 0xFFFFFFFF
+    return ids, gd
+
+
 def graph_bit(node):
     """The visited-bitmap bit of a node id (2^16-bit bitmap, multiplicative hash)."""
     return ((int(node) * 2654435761) & 0xFFFFFFFF) >> 16

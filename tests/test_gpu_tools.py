@@ -119,6 +119,29 @@ def test_search_pipeline_matches_library_path(tmp_path):
         assert abs(100.0 * hits / (q.shape[0] * k) - printed) < 1e-3
 
 
+def test_search_pipeline_graph_coarse_matches_library_path(tmp_path):
+    """--coarse graph: the centroid kNN graph (degree 8) walked with the
+    reference's CAGRA parameters (itopk max(32, top_m), width 4, 200 steps)."""
+    _say("search_pipeline --coarse graph vs library path")
+    x = oracle.gen_gmm(20000, 128, 32, seed=6, sig_lo=0.1)
+    q = oracle.gen_gmm(300, 128, 32, seed=6, set=1, sig_lo=0.1)
+    res, _ = _build(tmp_path, x, ["--nlist", 256, "--iters", 5, "--pq_iters", 3, "--sample", 5000, "--no-rebalance"])
+    fg.write_fvecs(tmp_path / "q.fvecs", q)
+    out = _run("search_pipeline", tmp_path / "base.fvecs", tmp_path / "q.fvecs", "-b", 100, "-m", 24, "-r", 400,
+               "-k", 10, "--p1_lists", 6, "--limit_k", 20, "-s", 2, "--res", res, "--coarse", "graph", "--out",
+               tmp_path / "out.ivecs", cwd=tmp_path)
+    assert "centroid graph: 256 nodes, degree 8, itopk 32" in out
+    got = _read_ivecs(tmp_path / "out.ivecs")
+    idx = fg.Index.load(res / "ivf_data.bin", res / "global_pq_codebook.bin", 128, 32)
+    dq, dx = torch.from_numpy(q).cuda(), torch.from_numpy(x).cuda()
+    g = idx.coarse_graph_build(8)
+    pid, _ = idx.coarse_graph_search(dq, 24, g, itopk=32, width=4, max_iter=200, seed=1, prune_ratio=100.0)
+    tid, td, tc, _, _ = idx.two_phase_search(dq, pid, 6, 20, 1.0, 400)
+    want, _, _ = fg.rerank(dq, dx, tid, tc, 10, 128, 0.1, 2)
+    assert np.array_equal(got, want.cpu().numpy())
+    idx.close()
+
+
 def test_build_global_elbow_sweep(tmp_path):
     _say("build_global --elbow")
     x = oracle.gen_gmm(12000, 128, 24, seed=6, sig_lo=0.1)

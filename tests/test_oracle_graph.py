@@ -90,3 +90,46 @@ def test_visited_bitmap_collision_hides_a_node():
         graph[target] = target
         oid, od, it = oracle.graph_search(q, base, graph, 2, itopk=64, width=1, max_iter=200)
         assert (oid[0, 0] == target) == found and oid[0, int(found)] == a
+
+
+@pytest.mark.parametrize("nlist,nprobe,prune", [(33, 10, 100.0), (33, 32, 100.0), (20, 16, 1.3)])
+def test_coarse_graph_exhaustive_equals_exact_coarse(nlist, nprobe, prune):
+    """The graph coarse mode (the reference's CAGRA-over-centroids step,
+    cagra_adapter.cuh:38-68) restated as graph_search over the centroids plus
+    the prune rule.  On the complete graph (degree nlist - 1) with
+    itopk = 64 >= nlist the first expansion evaluates every centroid, so the
+    result must equal the exact coarse quantizer (orc_coarse, pinned by brute
+    force) bit for bit, pruned probes included."""
+    rng = np.random.default_rng(nlist + nprobe)
+    cent = (rng.standard_normal((nlist, 96)) * 0.6).astype(np.float32)
+    cent[7] = cent[3]                                   # equal distances: the lower list id first
+    graph = np.array([[j for j in range(nlist) if j != i] for i in range(nlist)], np.int32)
+    q = (rng.standard_normal((30, 96)) * 0.6).astype(np.float32)
+    gid, gd = oracle.coarse_graph(q, cent, graph, nprobe, itopk=64, width=4, max_iter=200, seed=5, prune_ratio=prune)
+    eid, ed = oracle.coarse(q, cent, nprobe, prune_ratio=prune)
+    assert np.array_equal(gid, eid)
+    assert np.array_equal(gd.view(np.uint32), ed.view(np.uint32))
+    if prune < 2.0:
+        assert np.any(gid == 0xFFFFFFFF)
+
+
+def test_coarse_graph_build_rule():
+    """The centroid graph by brute force: the nearest others in float64 (no
+    near-ties in this data) give F(v); forward part, reverse edges by (rank,
+    id), then the remaining forward entries."""
+    rng = np.random.default_rng(2)
+    cent = rng.standard_normal((200, 128)).astype(np.float32)
+    cent[50] = cent[10]                                 # a duplicate centroid: its twin comes first
+    deg = 6
+    g = oracle.coarse_graph_build(cent, deg)
+    d = ((cent[:, None, :].astype(np.float64) - cent[None, :, :]) ** 2).sum(-1)
+    fwd = [[j for j in np.lexsort((np.arange(200), d[i])) if j != i][:2 * deg] for i in range(200)]
+    for v in range(200):
+        want = list(fwd[v][:3])
+        rev = sorted((fwd[u].index(v), u) for u in range(200) if v in fwd[u][:deg])
+        for c in [u for _, u in rev] + fwd[v][3:]:
+            if len(want) < deg and c not in want:
+                want.append(c)
+        assert list(g[v]) == want, v
+        assert v not in g[v] and len(set(g[v])) == deg
+    assert g[10][0] == 50 and g[50][0] == 10

@@ -34,6 +34,8 @@ def test_missing_and_malformed_inputs(tmp_path):
     assert r.returncode == 1 and "unknown argument" in r.stderr
     r = _run("search_pipeline", str(tmp_path / "none.fvecs"), str(tmp_path / "q.fvecs"))
     assert r.returncode == 1 and "cannot open" in r.stderr
+    r = _run("search_pipeline", str(tmp_path / "none.fvecs"), str(tmp_path / "q.fvecs"), "--coarse", "cagra")
+    assert r.returncode == 1 and "--coarse must be exact or graph" in r.stderr
 
 
 def test_dimension_not_divisible_by_pq_m(tmp_path):
