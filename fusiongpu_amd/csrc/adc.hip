@@ -358,7 +358,8 @@ __global__ __launch_bounds__(kSpecWaves * kWave, 4) void adc_flow_kernel(AdcArgs
   static_assert(M % kBuilderWaves == 0 && (TPM == 16 || TPM == 32) && E % 4 == 0, "builder layout");
   __shared__ __align__(16) float smem[2 * C::LUT];
   __shared__ float rws[kBuilderWaves][16];
-  __shared__ unsigned s_min[2][M];  // per LUT buffer: min over codewords of each LUT row (float bits)
+  // Per LUT buffer: builder wave w's row minima summed over its SPW subspaces.
+  __shared__ __align__(16) float s_part[2][kBuilderWaves];
   // Per query slot.  p_*: by probe index (set-up); f_*: compacted usable lists.
   __shared__ float p_lb[2][64];
   __shared__ int f_list[2][64], f_start[2][64], f_n[2][64], f_cst[2][65], s_dec[2][64];
@@ -575,7 +576,13 @@ __global__ __launch_bounds__(kSpecWaves * kWave, 4) void adc_flow_kernel(AdcArgs
           const auto rr = __builtin_amdgcn_permlane16_swap(__float_as_uint(mn), __float_as_uint(mn), false, false);
           mn = fminf(__uint_as_float(rr[0]), __uint_as_float(rr[1]));
         }
-        if (t == 0) s_min[b][ms] = __float_as_uint(mn);
+        {
+          // This wave's subspaces in ascending order (lane TPM*i holds subspace wave*SPW + i).
+          float part = readlane_f(mn, 0);
+#pragma unroll
+          for (int i = 1; i < SPW; ++i) part += readlane_f(mn, TPM * i);
+          if (lane == 0) s_part[b][wave] = part;
+        }
         lds_signal_add(&s_built[b], 1);
         const int nch = f_cst[s][f + 1] - f_cst[s][f];
         if (b) need1 += nch; else need0 += nch;
@@ -628,11 +635,17 @@ __global__ __launch_bounds__(kSpecWaves * kWave, 4) void adc_flow_kernel(AdcArgs
           nload += chunk_vecs(f, c);
         }
         lds_wait_at_least(&s_built[dec & 1], kBuilderWaves * (dec / 2 + 1));
-        float acc = 0.0f;
+        {
+          // T[g]: the builder waves' partial sums from the top down; group g of
+          // 8 subspaces is waves g*8/SPW ..  (any order of the additions keeps
+          // the early-abandon bound valid).
+          constexpr int WPG = 8 / SPW;
+          float acc = 0.0f;
 #pragma unroll
-        for (int m = M - 1; m >= 0; --m) {
-          acc += __uint_as_float(s_min[dec & 1][m]);
-          if (m % 8 == 0) T[m / 8] = acc;
+          for (int w = kBuilderWaves - 1; w >= 0; --w) {
+            acc += s_part[dec & 1][w];
+            if (w % WPG == 0) T[w / WPG] = acc;
+          }
         }
         int mine = 0;
         while (true) {
