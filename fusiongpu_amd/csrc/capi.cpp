@@ -171,7 +171,10 @@ fgpu_status fgpu_index_load(const char* ivf_path, const char* cb_path, int dim, 
 
 // ---------------------------------------------------------------------------
 size_t fgpu_coarse_workspace_bytes(int nq, int nlist) {
-  return carve_bytes<float>((size_t)nq) + carve_bytes<float>((size_t)std::max(nq, 64) * nlist) + 256;
+  // The estimate block holds whole 64-row GEMM tiles: with room for every
+  // query row rounded up to 64, the coarse step is one GEMM + one select.
+  const size_t rows = ((size_t)std::max(nq, 64) + 63) / 64 * 64;
+  return carve_bytes<float>((size_t)nq) + carve_bytes<float>(rows * nlist) + 256;
 }
 
 fgpu_status fgpu_coarse_search(const fgpu_index* ix, const float* dq, int nq, int nprobe, float prune_ratio,
