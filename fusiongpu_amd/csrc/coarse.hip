@@ -120,6 +120,85 @@ __global__ __launch_bounds__(256) void gemm_est_kernel(const float* __restrict__
   }
 }
 
+// The same estimate for dim % 32 == 0, pipelined: each K stage of 32 is
+// staged with coalesced 16-byte loads (a thread loads rows t / 8 and
+// t / 8 + 32 at float4 t % 8: eight rows of 128 bytes an instruction), the
+// next stage's loads are in flight while the current stage's MFMAs run, and
+// the LDS tiles ([row][k], stride 36 floats: conflict-free 16-byte reads) are
+// double-buffered, so one barrier a stage.  Each wave reads its operands with
+// 16-byte LDS loads that feed four MFMAs: MFMA 4j + e of a stage contracts
+// k = 16 h + 4 j + e for lane half h, a permutation of the stage's 32 k's;
+// the error margin holds for any summation order.  Rows and columns past the
+// end are loaded clamped to the last one and never written.
+constexpr int kS2 = 36;
+__global__ __launch_bounds__(256) void gemm_est32_kernel(const float* __restrict__ x, int64_t nrows,
+                                                         const float* __restrict__ c, int ncols, int dim,
+                                                         const float* __restrict__ xn,
+                                                         const float* __restrict__ cn,
+                                                         float* __restrict__ est, int64_t ld) {
+  __shared__ __align__(16) float As[2][kTM * kS2];
+  __shared__ __align__(16) float Bs[2][kTN * kS2];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t row0 = (int64_t)blockIdx.x * kTM;
+  const int col0 = blockIdx.y * kTN;
+  const int wr = wave >> 1, wc = wave & 1;
+  const int li = lane & 31, lh = lane >> 5;
+  const int sr = tid >> 3, sf = tid & 7;
+  const float* ap0 = x + min(row0 + sr, nrows - 1) * dim + 4 * sf;
+  const float* ap1 = x + min(row0 + sr + 32, nrows - 1) * dim + 4 * sf;
+  const float* bp0 = c + (int64_t)min(col0 + sr, ncols - 1) * dim + 4 * sf;
+  const float* bp1 = c + (int64_t)min(col0 + sr + 32, ncols - 1) * dim + 4 * sf;
+  float4 ra0 = *reinterpret_cast<const float4*>(ap0), ra1 = *reinterpret_cast<const float4*>(ap1);
+  float4 rb0 = *reinterpret_cast<const float4*>(bp0), rb1 = *reinterpret_cast<const float4*>(bp1);
+  f32x16 acc;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
+  const int nst = dim / 32;
+  *reinterpret_cast<float4*>(&As[0][sr * kS2 + 4 * sf]) = ra0;
+  *reinterpret_cast<float4*>(&As[0][(sr + 32) * kS2 + 4 * sf]) = ra1;
+  *reinterpret_cast<float4*>(&Bs[0][sr * kS2 + 4 * sf]) = rb0;
+  *reinterpret_cast<float4*>(&Bs[0][(sr + 32) * kS2 + 4 * sf]) = rb1;
+  __syncthreads();
+  for (int st = 0; st < nst; ++st) {
+    const int buf = st & 1;
+    if (st + 1 < nst) {
+      const int ko = 32 * (st + 1);
+      ra0 = *reinterpret_cast<const float4*>(ap0 + ko);
+      ra1 = *reinterpret_cast<const float4*>(ap1 + ko);
+      rb0 = *reinterpret_cast<const float4*>(bp0 + ko);
+      rb1 = *reinterpret_cast<const float4*>(bp1 + ko);
+    }
+    const float* Ar = &As[buf][(wr * 32 + li) * kS2 + 16 * lh];
+    const float* Br = &Bs[buf][(wc * 32 + li) * kS2 + 16 * lh];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float4 av = *reinterpret_cast<const float4*>(Ar + 4 * j);
+      const float4 bv = *reinterpret_cast<const float4*>(Br + 4 * j);
+      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.x, bv.x, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.y, bv.y, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.z, bv.z, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.w, bv.w, acc, 0, 0, 0);
+    }
+    if (st + 1 < nst) {
+      const int nb = buf ^ 1;
+      *reinterpret_cast<float4*>(&As[nb][sr * kS2 + 4 * sf]) = ra0;
+      *reinterpret_cast<float4*>(&As[nb][(sr + 32) * kS2 + 4 * sf]) = ra1;
+      *reinterpret_cast<float4*>(&Bs[nb][sr * kS2 + 4 * sf]) = rb0;
+      *reinterpret_cast<float4*>(&Bs[nb][(sr + 32) * kS2 + 4 * sf]) = rb1;
+    }
+    __syncthreads();
+  }
+  // Output layout as in gemm_est_kernel.
+  const int j = col0 + wc * 32 + li;
+  if (j >= ncols) return;
+  const float cj = cn[j];
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int64_t i = row0 + wr * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
+    if (i < nrows) est[i * ld + j] = (xn[i] + cj) - 2.0f * acc[r];
+  }
+}
+
 constexpr int kCandCap = 256;
 
 // Ascending bitonic sort of one 32-bit key per lane across the wave.
@@ -462,7 +541,10 @@ fgpu_status launch_gemm_est(const float* x, int64_t nrows, const float* c, int n
   if (nrows <= 0 || ncols <= 0) return FGPU_OK;
   dim3 grid((unsigned)((nrows + kTM - 1) / kTM), (unsigned)((ncols + kTN - 1) / kTN));
   FGPU_CHECK(grid.y <= 65535u, FGPU_ERR_UNSUPPORTED, "gemm_est: too many columns");
-  hipLaunchKernelGGL(gemm_est_kernel, grid, dim3(256), 0, s, x, nrows, c, ncols, dim, xn, cn, est, ld);
+  if (dim % 32 == 0)
+    hipLaunchKernelGGL(gemm_est32_kernel, grid, dim3(256), 0, s, x, nrows, c, ncols, dim, xn, cn, est, ld);
+  else
+    hipLaunchKernelGGL(gemm_est_kernel, grid, dim3(256), 0, s, x, nrows, c, ncols, dim, xn, cn, est, ld);
   FGPU_HIP(hipGetLastError());
   return FGPU_OK;
 }

@@ -51,7 +51,8 @@ def _random_index(rng, n, dim, m, nlist, empty=(), big=None):
 
 
 # --------------------------------------------------------------------------- exact nearest centroids
-@pytest.mark.parametrize("dim,nc,p", [(128, 1024, 32), (96, 300, 1), (128, 4096, 64), (64, 50, 10), (128, 77, 1)])
+@pytest.mark.parametrize("dim,nc,p", [(128, 1024, 32), (96, 300, 1), (128, 4096, 64), (64, 50, 10), (128, 77, 1),
+                                      (36, 200, 8)])
 def test_l2_topk_bit_exact(dim, nc, p):
     _say(f"l2_topk dim={dim} nc={nc} p={p}")
     rng = np.random.default_rng(dim + nc + p)
