@@ -148,7 +148,7 @@ def main():
         idx.coarse_search(dq, nprobe, workspace=ws)
     ev[1].record(stream)
     for _ in range(reps):
-        idx.adc_search(dq, probes, k, out=out)
+        idx.adc_search(dq, probes, k, out=out, probe_dists=pd)
     ev[2].record(stream)
     torch.cuda.synchronize()
     coarse_ms = ev[0].elapsed_time(ev[1]) / reps
@@ -159,7 +159,7 @@ def main():
         f"adc {adc_ms:.3f} ms, algorithmic ADC bytes {adc_bytes / 1e9:.2f} GB -> {adc_gbs:.0f} GB/s")
     # What the scan really loads: the exact list / chunk bounds skip code loads
     # of lists and chunks that cannot reach the top-k (results unchanged).
-    sid, sd, st = idx.adc_search_stats(dq, probes, k)
+    sid, sd, st = idx.adc_search_stats(dq, probes, k, probe_dists=pd)
     assert torch.equal(sid, out[0]) and torch.equal(sd, out[1]), "instrumented scan differs"
     loaded_bytes = st["vectors_loaded"] * (m + 4)  # code bytes + the 4-byte vector id loaded with them
     loaded_gbs = loaded_bytes / (adc_ms * 1e-3) / 1e9

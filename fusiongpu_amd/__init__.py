@@ -54,8 +54,8 @@ _SIGS = {
     "fgpu_coarse_graph_search": (_i32, [_vp, _vp, _i32, _i32, _i32, _vp, _i32, _i32, _i32, _i32, _u64, _f32, _vp,
                                         _vp, _vp]),
     "fgpu_probe_counts": (_i32, [_vp, _vp, _i32, _i32, _vp, _vp, _vp]),
-    "fgpu_adc_search": (_i32, [_vp, _vp, _i32, _vp, _i32, _i32, _vp, _vp, _vp]),
-    "fgpu_adc_search_stats": (_i32, [_vp, _vp, _i32, _vp, _i32, _i32, _vp, _vp, _vp, _vp]),
+    "fgpu_adc_search": (_i32, [_vp, _vp, _i32, _vp, _vp, _i32, _i32, _vp, _vp, _vp]),
+    "fgpu_adc_search_stats": (_i32, [_vp, _vp, _i32, _vp, _vp, _i32, _i32, _vp, _vp, _vp, _vp]),
     "fgpu_search_workspace_bytes": (_sz, [_i32, _i32, _i32]),
     "fgpu_search": (_i32, [_vp, _vp, _i32, _i32, _i32, _f32, _vp, _vp, _vp, _sz, _vp]),
     "fgpu_two_phase_workspace_bytes": (_sz, [_i32, _i32, _i32, _i32, _i32]),
@@ -307,28 +307,32 @@ class Index:
                                             _stream(stream)))
         return ids, d
 
-    def adc_search(self, queries, probe_ids, k: int, out=None, stream=None):
-        """LUT + ADC scan + top-k over the probed lists: (ids int32 [nq][k], dists float32 [nq][k])."""
+    def adc_search(self, queries, probe_ids, k: int, out=None, stream=None, probe_dists=None):
+        """LUT + ADC scan + top-k over the probed lists: (ids int32 [nq][k], dists float32 [nq][k]).
+        probe_dists: coarse_search's distances for these probes (optional; the list bounds use them)."""
         torch = _torch()
         q = _to_dev(queries)
         p = _to_dev(probe_ids)
         nq, nprobe = p.shape
+        pd = _to_dev(probe_dists) if probe_dists is not None else None
         ids, d = out if out is not None else (torch.empty((nq, k), dtype=torch.int32, device="cuda"),
                                               torch.empty((nq, k), dtype=torch.float32, device="cuda"))
-        _check(lib.fgpu_adc_search(self._h, _dev_ptr(q), nq, _dev_ptr(p), nprobe, k, _dev_ptr(ids), _dev_ptr(d),
-                                   _stream(stream)))
+        _check(lib.fgpu_adc_search(self._h, _dev_ptr(q), nq, _dev_ptr(p), _dev_ptr(pd) if pd is not None else None,
+                                   nprobe, k, _dev_ptr(ids), _dev_ptr(d), _stream(stream)))
         return ids, d
 
-    def adc_search_stats(self, queries, probe_ids, k: int, out=None, stream=None):
+    def adc_search_stats(self, queries, probe_ids, k: int, out=None, stream=None, probe_dists=None):
         """adc_search plus counters: (ids, dists, {"vectors_loaded", "luts_built", "lists_skipped"})."""
         torch = _torch()
         q = _to_dev(queries)
         p = _to_dev(probe_ids)
         nq, nprobe = p.shape
+        pd = _to_dev(probe_dists) if probe_dists is not None else None
         ids, d = out if out is not None else (torch.empty((nq, k), dtype=torch.int32, device="cuda"),
                                               torch.empty((nq, k), dtype=torch.float32, device="cuda"))
         st = torch.zeros(8, dtype=torch.int64, device="cuda")
-        _check(lib.fgpu_adc_search_stats(self._h, _dev_ptr(q), nq, _dev_ptr(p), nprobe, k, _dev_ptr(ids),
+        _check(lib.fgpu_adc_search_stats(self._h, _dev_ptr(q), nq, _dev_ptr(p),
+                                         _dev_ptr(pd) if pd is not None else None, nprobe, k, _dev_ptr(ids),
                                          _dev_ptr(d), _dev_ptr(st), _stream(stream)))
         v = st.cpu().tolist()
         return ids, d, {"vectors_loaded": v[0], "luts_built": v[1], "lists_skipped": v[2], "clk_setup": v[3],

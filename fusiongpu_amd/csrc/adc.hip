@@ -425,13 +425,19 @@ __global__ __launch_bounds__(kSpecWaves * kWave, 4) void adc_flow_kernel(AdcArgs
       lds_wait_at_least<kLazySleep>(&s_free[s], i / 2);  // the slot's previous query is written out
       const uint32_t* pr = a.probes + (size_t)q * P;
       const uint32_t pl_lane = lane < P ? pr[lane] : kPruned;
-      const float qa = lane < D ? a.queries[(size_t)q * D + lane] : 0.0f;
-      const float qb = lane + kWave < D ? a.queries[(size_t)q * D + lane + kWave] : 0.0f;
-      // Centroid rows and radii of this wave's probes p = wave + 8 j, loaded
-      // four lists at a time.
+      // With the coarse distances at hand, wave 0 bounds every list from them
+      // (one lane a probe) and the other builder waves have nothing to do.
+      float lb_lane = 0.0f;
+      if (a.probe_dists) {
+        if (wave == 0 && pl_lane < NL) lb_lane = list_lower_bound(a.probe_dists[(size_t)q * P + lane], a.rmax[pl_lane]);
+      }
+      const float qa = !a.probe_dists && lane < D ? a.queries[(size_t)q * D + lane] : 0.0f;
+      const float qb = !a.probe_dists && lane + kWave < D ? a.queries[(size_t)q * D + lane + kWave] : 0.0f;
+      // Otherwise each builder wave computes the bounds of its probes
+      // p = wave + 8 j from the centroid rows, four lists at a time.
       constexpr int kBatch = 4;
 #pragma unroll 1
-      for (int j0 = 0; j0 < kMaxPerWave && wave + kBuilderWaves * j0 < P; j0 += kBatch) {
+      for (int j0 = 0; !a.probe_dists && j0 < kMaxPerWave && wave + kBuilderWaves * j0 < P; j0 += kBatch) {
         float ca[kBatch], cc[kBatch], rl[kBatch];
 #pragma unroll
         for (int j = 0; j < kBatch; ++j) {
@@ -482,7 +488,7 @@ __global__ __launch_bounds__(kSpecWaves * kWave, 4) void adc_flow_kernel(AdcArgs
           f_start[s][pos] = st;
           f_n[s][pos] = n;
           f_cst[s][pos] = incl - nch;
-          f_lb[s][pos] = p_lb[s][lane];
+          f_lb[s][pos] = a.probe_dists ? lb_lane : p_lb[s][lane];
         }
         const int nv = __popcll(bm);
         const int total = __shfl(incl, kWave - 1, kWave);

@@ -210,25 +210,29 @@ fgpu_status fgpu_probe_counts(const fgpu_index* ix, const uint32_t* d_probe_ids,
   return launch_probe_counts(d_probe_ids, nq, nprobe, ix->nlist, ix->d_offsets, d_counts, d_offsets, as_stream(stream));
 }
 
-fgpu_status fgpu_adc_search(const fgpu_index* ix, const float* dq, int nq, const uint32_t* d_probe_ids, int nprobe,
-                            int k, int32_t* d_out_ids, float* d_out_dists, void* stream) {
+fgpu_status fgpu_adc_search(const fgpu_index* ix, const float* dq, int nq, const uint32_t* d_probe_ids,
+                            const float* d_probe_dists, int nprobe, int k, int32_t* d_out_ids, float* d_out_dists,
+                            void* stream) {
   FGPU_CHECK(ix && dq && d_probe_ids && d_out_ids && d_out_dists, FGPU_ERR_ARG, "adc_search: null argument");
   FGPU_CHECK(nq >= 0 && nprobe >= 1 && k >= 1, FGPU_ERR_ARG, "adc_search: bad sizes");
   FGPU_CHECK(adc_supported(ix->dim, ix->m), FGPU_ERR_UNSUPPORTED, "adc_search: no kernel for this (dim, pq_m)");
   AdcArgs a{dq, ix->d_centroids, ix->d_codebook, ix->d_offsets, ix->d_codes, ix->d_ids, d_probe_ids, ix->d_rmax,
             nq, nprobe, k, ix->nlist, d_out_ids, d_out_dists};
+  a.probe_dists = d_probe_dists;
   return launch_adc_plain(ix->dim, ix->m, a, as_stream(stream));
 }
 
 fgpu_status fgpu_adc_search_stats(const fgpu_index* ix, const float* dq, int nq, const uint32_t* d_probe_ids,
-                                  int nprobe, int k, int32_t* d_out_ids, float* d_out_dists,
-                                  unsigned long long* d_stats, void* stream) {
+                                  const float* d_probe_dists, int nprobe, int k, int32_t* d_out_ids,
+                                  float* d_out_dists, unsigned long long* d_stats, void* stream) {
   FGPU_CHECK(ix && dq && d_probe_ids && d_out_ids && d_out_dists && d_stats, FGPU_ERR_ARG,
              "adc_search_stats: null argument");
   FGPU_CHECK(nq >= 0 && nprobe >= 1 && k >= 1, FGPU_ERR_ARG, "adc_search_stats: bad sizes");
   FGPU_CHECK(adc_supported(ix->dim, ix->m), FGPU_ERR_UNSUPPORTED, "adc_search_stats: no kernel for this (dim, pq_m)");
   AdcArgs a{dq, ix->d_centroids, ix->d_codebook, ix->d_offsets, ix->d_codes, ix->d_ids, d_probe_ids, ix->d_rmax,
-            nq, nprobe, k, ix->nlist, d_out_ids, d_out_dists, d_stats};
+            nq, nprobe, k, ix->nlist, d_out_ids, d_out_dists};
+  a.probe_dists = d_probe_dists;
+  a.stats = d_stats;
   return launch_adc_plain(ix->dim, ix->m, a, as_stream(stream));
 }
 
@@ -245,7 +249,7 @@ fgpu_status fgpu_search(const fgpu_index* ix, const float* dq, int nq, int nprob
   float* pd = cv.take<float>((size_t)nq * nprobe);
   FGPU_CHECK(cv.ok(), FGPU_ERR_WORKSPACE, "search: workspace too small");
   FGPU_TRY(fgpu_coarse_search(ix, dq, nq, nprobe, prune_ratio, pid, pd, cv.base + cv.used, ws_bytes - cv.used, stream));
-  return fgpu_adc_search(ix, dq, nq, pid, nprobe, k, d_out_ids, d_out_dists, stream);
+  return fgpu_adc_search(ix, dq, nq, pid, pd, nprobe, k, d_out_ids, d_out_dists, stream);
 }
 
 // ---------------------------------------------------------------------------

@@ -46,6 +46,10 @@ struct AdcArgs {
   int nq, nprobe, k, nlist;  // probe ids >= nlist are skipped like pruned ones
   int32_t* out_ids;         // [nq][k]
   float* out_d;             // [nq][k]
+  // Optional: [nq][nprobe] squared L2 of query and probed centroid in the
+  // coarse step's form (sequential fused chain over fl(q - c)), which the
+  // list lower bound accepts in place of its own sum (nullptr = compute).
+  const float* probe_dists = nullptr;
   // Optional instrumentation (nullptr = off), summed over the launch:
   // [0] vectors whose codes were loaded, [1] LUTs built, [2] probed lists
   // skipped by the list lower bound; shader clocks per workgroup: [3] set-up,

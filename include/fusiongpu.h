@@ -86,10 +86,14 @@ fgpu_status fgpu_probe_counts(const fgpu_index* idx, const uint32_t* d_probe_ids
 /* The k best (ADC distance, vector id) over every vector of every surviving
  * probed list; padding id -1 / distance FLT_MAX.  Equals run_gpu_batch_logic
  * (gpu_global.cu:679-874) with p1_lists = nprobe, limit_k = k, rerank_m = k.
- * k <= 64. */
+ * k <= 64.  d_probe_dists (may be NULL) takes the place of the reference's
+ * d_cagra_dists: fgpu_coarse_search's distances for these probes, which the
+ * scan then uses for its exact list bounds instead of recomputing them from
+ * the centroids.  Non-NULL, they must be those distances (the squared L2 in
+ * the coarse step's form); results are the same either way. */
 fgpu_status fgpu_adc_search(const fgpu_index* idx, const float* d_queries, int nq,
-                            const uint32_t* d_probe_ids, int nprobe, int k, int32_t* d_out_ids,
-                            float* d_out_dists, void* stream);
+                            const uint32_t* d_probe_ids, const float* d_probe_dists, int nprobe, int k,
+                            int32_t* d_out_ids, float* d_out_dists, void* stream);
 
 /* fgpu_adc_search plus instrumentation (no reference counterpart): adds to
  * d_stats[0..6] (device, caller-zeroed, uint64) the number of vectors whose
@@ -99,8 +103,9 @@ fgpu_status fgpu_adc_search(const fgpu_index* idx, const float* d_queries, int n
  * a builder wave, a scanner wave, the whole workgroup).  Results equal
  * fgpu_adc_search's. */
 fgpu_status fgpu_adc_search_stats(const fgpu_index* idx, const float* d_queries, int nq,
-                                  const uint32_t* d_probe_ids, int nprobe, int k, int32_t* d_out_ids,
-                                  float* d_out_dists, unsigned long long* d_stats, void* stream);
+                                  const uint32_t* d_probe_ids, const float* d_probe_dists, int nprobe, int k,
+                                  int32_t* d_out_ids, float* d_out_dists, unsigned long long* d_stats,
+                                  void* stream);
 
 /* coarse + ADC in one call. */
 size_t fgpu_search_workspace_bytes(int nq, int nlist, int nprobe);

@@ -97,20 +97,24 @@ def test_adc_search_bit_exact(dim, m, k):
     nlist = 40
     offs, ids, lc, cent, cb = _random_index(rng, 30000, dim, m, nlist, empty=(3, 17), big=8)
     q = rng.standard_normal((150, dim)).astype(np.float32) * 0.7
-    probes, _ = oracle.coarse(q, cent, 12)
+    probes, pdist = oracle.coarse(q, cent, 12)
     probes[5, 2] = 0xFFFFFFFF             # pruned probe mid-list
     probes[6, :] = 0xFFFFFFFF             # every probe pruned -> padding
     probes[7, 0] = 3                      # an empty list first
     probes[8, :] = probes[8, 0]           # the same list probed twice is scanned twice
+    pdist[8, :] = pdist[8, 0]
     idx = fg.Index.from_arrays(dim, m, offs, ids, lc, cent, cb)
     assert idx.max_list_len > 1024        # longer than the reference's 1024-item cut
-    gid, gd = idx.adc_search(torch.from_numpy(q).cuda(), torch.from_numpy(probes.view(np.int32)).cuda(), k)
-    gid, gd = _host(gid), _host(gd)
     oid, od = oracle.search_plain(q, cent, cb, offs, ids, lc, probes, k)
-    bad = np.nonzero(~np.all(gid == oid, axis=1))[0]
-    assert bad.size == 0, f"first mismatching queries {bad[:5]}: gpu {gid[bad[0]]} oracle {oid[bad[0]]}"
-    assert np.array_equal(_bits(gd), _bits(od))
-    assert np.all(gid[6] == -1)
+    # list bounds from the centroids, then from the coarse distances
+    for pd in (None, torch.from_numpy(pdist).cuda()):
+        gid, gd = idx.adc_search(torch.from_numpy(q).cuda(), torch.from_numpy(probes.view(np.int32)).cuda(), k,
+                                 probe_dists=pd)
+        gid, gd = _host(gid), _host(gd)
+        bad = np.nonzero(~np.all(gid == oid, axis=1))[0]
+        assert bad.size == 0, f"first mismatching queries {bad[:5]}: gpu {gid[bad[0]]} oracle {oid[bad[0]]}"
+        assert np.array_equal(_bits(gd), _bits(od))
+        assert np.all(gid[6] == -1)
     idx.close()
 
 
@@ -124,19 +128,22 @@ def test_adc_search_many_queries_per_workgroup(dim, m, k):
     offs, ids, lc, cent, cb = _random_index(rng, 40000, dim, m, nlist, empty=(5,), big=9)
     nq = 3000
     q = rng.standard_normal((nq, dim)).astype(np.float32) * 0.7
-    probes, _ = oracle.coarse(q, cent, 16)
+    probes, pdist = oracle.coarse(q, cent, 16)
     probes[300:303, :] = 0xFFFFFFFF       # consecutive queries with nothing to scan
     probes[700, 1:] = 0xFFFFFFFF          # one list only
     probes[1500, :] = probes[1500, 0]     # one list, probed 16 times
+    pdist[1500, :] = pdist[1500, 0]
     probes[2999, 0] = 5                   # an empty list first, on the last query
     idx = fg.Index.from_arrays(dim, m, offs, ids, lc, cent, cb)
-    gid, gd = idx.adc_search(torch.from_numpy(q).cuda(), torch.from_numpy(probes.view(np.int32)).cuda(), k)
-    gid, gd = _host(gid), _host(gd)
     oid, od = oracle.search_plain(q, cent, cb, offs, ids, lc, probes, k)
-    bad = np.nonzero(~np.all(gid == oid, axis=1))[0]
-    assert bad.size == 0, f"first mismatching queries {bad[:5]}: gpu {gid[bad[0]]} oracle {oid[bad[0]]}"
-    assert np.array_equal(_bits(gd), _bits(od))
-    assert np.all(gid[300:303] == -1)
+    for pd in (None, torch.from_numpy(pdist).cuda()):
+        gid, gd = idx.adc_search(torch.from_numpy(q).cuda(), torch.from_numpy(probes.view(np.int32)).cuda(), k,
+                                 probe_dists=pd)
+        gid, gd = _host(gid), _host(gd)
+        bad = np.nonzero(~np.all(gid == oid, axis=1))[0]
+        assert bad.size == 0, f"first mismatching queries {bad[:5]}: gpu {gid[bad[0]]} oracle {oid[bad[0]]}"
+        assert np.array_equal(_bits(gd), _bits(od))
+        assert np.all(gid[300:303] == -1)
     idx.close()
 
 
@@ -147,8 +154,10 @@ def test_search_fused_equals_stages():
     q = torch.from_numpy(rng.standard_normal((500, 128)).astype(np.float32) * 0.7).cuda()
     idx = fg.Index.from_arrays(128, 32, offs, ids, lc, cent, cb)
     fid, fd = idx.search(q, 16, 10)
-    pid, _ = idx.coarse_search(q, 16)
+    pid, pdist = idx.coarse_search(q, 16)
     sid, sd = idx.adc_search(q, pid, 10)
+    assert torch.equal(fid, sid) and torch.equal(fd, sd)
+    sid, sd = idx.adc_search(q, pid, 10, probe_dists=pdist)
     assert torch.equal(fid, sid) and torch.equal(fd, sd)
     qn = q.cpu().numpy()
     oprobe, _ = oracle.coarse(qn, cent, 16)
