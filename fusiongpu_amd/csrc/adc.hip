@@ -84,21 +84,17 @@ __device__ __forceinline__ void scan_list(const float* smem, const uint8_t* __re
   }
 }
 
-// Lower-bounded early abandon.  T[g] >= 0 is a float sum of the per-subspace
-// LUT minima over subspaces 8g .. M-1.  With p the partial sum after 8g terms,
-// the final distance is the rounded chain p + t_8g + ... + t_(M-1) with
-// t_m >= min_m, so by monotonicity of rounded addition it is at least the same
-// chain over the minima, which is at least (p + S)(1 - u)^r for the exact sum
-// S of those minima (r <= 32 additions, u = 2^-24).  T[g] overestimates S by at
-// most (1 + u)^r and fl(p + T[g]) adds one more rounding, so
-//   final >= fl(p + T[g]) (1 - (2r + 1) u) > fl(p + T[g]) (1 - 2^-17).
-// A vector whose final distance is <= thr therefore has
-// fl(p + T[g]) <= thr_hi = fl(thr (1 + 2^-16)): testing against thr_hi never
-// drops a vector that could enter the top-k, ties on distance included.
+// The ADC distances of the two vectors of a scanner round, every term: in
+// the flow kernel a wave-wide early abandon almost never fires (128 vectors a
+// round; on C2 fewer than 1 round in 1000 stops at any checkpoint), so the
+// round pays no per-lane bound tests.  Each group of 8 subspaces still ends in
+// a branch, on a uniform test that never holds (thr is a distance, >= 0): the
+// branches keep the code in the regions the register allocator fits into the
+// 128-VGPR budget of a 16-wave workgroup.  The first term starts each sum
+// (0 + t == t for the non-negative LUT entries).
 template <int M>
-__device__ __forceinline__ bool adc_sum2_lb(const float* __restrict__ lut, const uint4 (&w0)[M / 16],
-                                            const uint4 (&w1)[M / 16], bool ok0, bool ok1, float thr_hi,
-                                            const float (&T)[M / 8], float& d0, float& d1) {
+__device__ __forceinline__ bool adc_sum2_full(const float* __restrict__ lut, const uint4 (&w0)[M / 16],
+                                              const uint4 (&w1)[M / 16], float thr, float& d0, float& d1) {
   float a = 0.0f, b = 0.0f;
 #pragma unroll
   for (int i = 0; i < M / 16; ++i) {
@@ -108,12 +104,15 @@ __device__ __forceinline__ bool adc_sum2_lb(const float* __restrict__ lut, const
     for (int j = 0; j < 16; ++j) {
       const uint32_t cx = (x[j >> 2] >> (8 * (j & 3))) & 0xFFu;
       const uint32_t cy = (y[j >> 2] >> (8 * (j & 3))) & 0xFFu;
-      a += lut[(i * 16 + j) * kPQK + cx];
-      b += lut[(i * 16 + j) * kPQK + cy];
-      if ((j & 7) == 7 && i * 16 + j + 1 < M) {
-        const float t = T[(i * 16 + j + 1) / 8];
-        if (!__ballot((ok0 && a + t <= thr_hi) || (ok1 && b + t <= thr_hi))) return false;
+      const float ta = lut[(i * 16 + j) * kPQK + cx], tb = lut[(i * 16 + j) * kPQK + cy];
+      if (i == 0 && j == 0) {
+        a = ta;
+        b = tb;
+      } else {
+        a += ta;
+        b += tb;
       }
+      if ((j & 7) == 7 && i * 16 + j + 1 < M && thr < 0.0f) return false;
     }
   }
   d0 = a;
@@ -121,18 +120,17 @@ __device__ __forceinline__ bool adc_sum2_lb(const float* __restrict__ lut, const
   return true;
 }
 
-// One scanner round with the lower-bounded filter: thr is the packed k-th key
-// this wave filters against (own or shared, whichever is smaller).
+// One full scanner round: thr is the packed k-th key this wave filters
+// against (own or shared, whichever is smaller).
 template <int D, int M, int BUF>
-__device__ __forceinline__ void scan_round_lb(const float* smem, int v0, int n, int k, const uint4 (&w0)[M / 16],
-                                              const uint4 (&w1)[M / 16], int i0, int i1, uint64_t thr,
-                                              float thr_hi, const float (&T)[M / 8], uint64_t& lk,
-                                              uint64_t& own, unsigned long long* s_thr) {
+__device__ __forceinline__ void scan_round_full(const float* smem, int v0, int n, int k, const uint4 (&w0)[M / 16],
+                                                const uint4 (&w1)[M / 16], int i0, int i1, uint64_t thr,
+                                                uint64_t& lk, uint64_t& own, unsigned long long* s_thr) {
   using C = Cfg<D, M>;
   const float* lut = smem + BUF * C::LUT;
   const int v1 = v0 + kWave;
   float d0, d1;
-  if (adc_sum2_lb<M>(lut, w0, w1, v0 < n, v1 < n, thr_hi, T, d0, d1)) {
+  if (adc_sum2_full<M>(lut, w0, w1, __uint_as_float((uint32_t)(thr >> 32)), d0, d1)) {
     if (offer2_k(v0 < n ? key_of(d0, i0) : kPadKey, v1 < n ? key_of(d1, i1) : kPadKey, thr, k, lk)) {
       own = readlane64(lk, k - 1);
       if ((threadIdx.x & 63) == 0) atomicMin(s_thr, (unsigned long long)own);
@@ -306,9 +304,15 @@ constexpr int kScanWaves = kSpecWaves - kBuilderWaves;
 //     merges both and climbs on, the first is done; nobody waits.  The
 //     second arrival at the root writes the query's top-k and frees the slot.
 //   * Set-up of query i (builders, once the slot's previous query is freed):
-//     every builder wave computes the list bounds of its share of the probes
-//     (probe ids, then centroid rows and radii: two dependent HBM trips), wave
-//     0 adds offsets, compacts the usable lists and marks the slot ready.
+//     the list bounds come from the coarse step's probe distances when the
+//     caller passes them (wave 0: probe ids and distances, then radii and
+//     offsets), otherwise every builder wave computes those of its share of
+//     the probes from the centroid rows; wave 0 adds offsets, compacts the
+//     usable lists and marks the slot ready.
+//   * A scanner round computes both of its vectors' full ADC sums and offers
+//     them to the wave's top-k; on C2 a per-lane early abandon would almost
+//     never stop a 128-vector round, so the list bound above is the only
+//     pruning.
 // All counters are cumulative.  A count cannot run ahead of the list it
 // stands for: a builder wave contributes to built list j + 2 only after all of
 // list j is scanned, and a scanner scans list j + 2 only after it is built, so
@@ -358,8 +362,6 @@ __global__ __launch_bounds__(kSpecWaves * kWave, 4) void adc_flow_kernel(AdcArgs
   static_assert(M % kBuilderWaves == 0 && (TPM == 16 || TPM == 32) && E % 4 == 0, "builder layout");
   __shared__ __align__(16) float smem[2 * C::LUT];
   __shared__ float rws[kBuilderWaves][16];
-  // Per LUT buffer: builder wave w's row minima summed over its SPW subspaces.
-  __shared__ __align__(16) float s_part[2][kBuilderWaves];
   // Per query slot.  p_*: by probe index (set-up); f_*: compacted usable lists.
   __shared__ float p_lb[2][64];
   __shared__ int f_list[2][64], f_start[2][64], f_n[2][64], f_cst[2][65], s_dec[2][64];
@@ -562,7 +564,6 @@ __global__ __launch_bounds__(kSpecWaves * kWave, 4) void adc_flow_kernel(AdcArgs
         for (int d = 0; d < C::S; ++d) r[d] = rw[(lane / TPM) * C::S + d];
         lds_wait_at_least<kLazySleep>(&s_done[b], b ? need1 : need0);
         float* lut = smem + b * C::LUT + ms * kPQK + 4 * t;
-        float mn = __builtin_inff();
 #pragma unroll
         for (int u = 0; u < E / 4; ++u) {
           float4 v;
@@ -570,24 +571,7 @@ __global__ __launch_bounds__(kSpecWaves * kWave, 4) void adc_flow_kernel(AdcArgs
           v.y = lut_entry<C::S>(r, cb + (4 * u + 1) * C::S);
           v.z = lut_entry<C::S>(r, cb + (4 * u + 2) * C::S);
           v.w = lut_entry<C::S>(r, cb + (4 * u + 3) * C::S);
-          mn = fminf(mn, fminf(fminf(v.x, v.y), fminf(v.z, v.w)));
           *reinterpret_cast<float4*>(lut + 4 * TPM * u) = v;
-        }
-        // Row minimum of subspace ms: over the TPM lanes that share it.
-        mn = fminf(mn, __int_as_float(dpp_mov<0x128>(__float_as_int(mn))));  // row_ror:8
-        mn = fminf(mn, __int_as_float(dpp_mov<0x124>(__float_as_int(mn))));  // row_ror:4
-        mn = fminf(mn, __int_as_float(dpp_mov<0x122>(__float_as_int(mn))));  // row_ror:2
-        mn = fminf(mn, __int_as_float(dpp_mov<0x121>(__float_as_int(mn))));  // row_ror:1
-        if constexpr (TPM == 32) {  // rows 2i and 2i+1 share a subspace
-          const auto rr = __builtin_amdgcn_permlane16_swap(__float_as_uint(mn), __float_as_uint(mn), false, false);
-          mn = fminf(__uint_as_float(rr[0]), __uint_as_float(rr[1]));
-        }
-        {
-          // This wave's subspaces in ascending order (lane TPM*i holds subspace wave*SPW + i).
-          float part = readlane_f(mn, 0);
-#pragma unroll
-          for (int i = 1; i < SPW; ++i) part += readlane_f(mn, TPM * i);
-          if (lane == 0) s_part[b][wave] = part;
         }
         lds_signal_add(&s_built[b], 1);
         const int nch = f_cst[s][f + 1] - f_cst[s][f];
@@ -616,7 +600,6 @@ __global__ __launch_bounds__(kSpecWaves * kWave, 4) void adc_flow_kernel(AdcArgs
     auto first_own = [&](int cc) { return cc + (((swave - cc) % kScanWaves) + kScanWaves) % kScanWaves; };
     uint4 w0[C::NV4], w1[C::NV4];
     int i0 = kPadId, i1 = kPadId;
-    float T[M / 8];   // T[g] = sum of list f's row minima over subspaces 8g .. M-1
     unsigned nload = 0;  // vectors whose codes this wave loaded
     for (int i = 0; i < nqw; ++i) {
       const int s = i & 1, q = (int)blockIdx.x + i * G;
@@ -641,35 +624,15 @@ __global__ __launch_bounds__(kSpecWaves * kWave, 4) void adc_flow_kernel(AdcArgs
           nload += chunk_vecs(f, c);
         }
         lds_wait_at_least(&s_built[dec & 1], kBuilderWaves * (dec / 2 + 1));
-        {
-          // T[g]: the builder waves' partial sums from the top down; group g of
-          // 8 subspaces is waves g*8/SPW ..  (any order of the additions keeps
-          // the early-abandon bound valid).
-          constexpr int WPG = 8 / SPW;
-          float acc = 0.0f;
-#pragma unroll
-          for (int w = kBuilderWaves - 1; w >= 0; --w) {
-            acc += s_part[dec & 1][w];
-            if (w % WPG == 0) T[w / WPG] = acc;
-          }
-        }
         int mine = 0;
         while (true) {
           const uint64_t shared_thr = s_thr[s];
           const uint64_t thr = own < shared_thr ? own : shared_thr;
-          const float thr_hi = __uint_as_float((uint32_t)(thr >> 32)) * (1.0f + 0x1p-16f);
-          if (T[0] > thr_hi) {
-            // Every vector of list f is at least T[0]: this wave's remaining
-            // chunks of it are done without loading codes (the threshold never
-            // rises).
-            mine += (c_end - c + kScanWaves - 1) / kScanWaves;
-            break;
-          }
           const int v0 = (c - cst[f]) * kChunk + lane;
           if (dec & 1)
-            scan_round_lb<D, M, 1>(smem, v0, n, k, w0, w1, i0, i1, thr, thr_hi, T, lk, own, &s_thr[s]);
+            scan_round_full<D, M, 1>(smem, v0, n, k, w0, w1, i0, i1, thr, lk, own, &s_thr[s]);
           else
-            scan_round_lb<D, M, 0>(smem, v0, n, k, w0, w1, i0, i1, thr, thr_hi, T, lk, own, &s_thr[s]);
+            scan_round_full<D, M, 0>(smem, v0, n, k, w0, w1, i0, i1, thr, lk, own, &s_thr[s]);
           ++mine;
           c += kScanWaves;
           if (c >= c_end) break;
