@@ -311,7 +311,7 @@ __global__ __launch_bounds__(kTT) void two_phase_kernel(TwoPhaseArgs a) {
         thr = pub < thr ? pub : thr;
       }
       float d0, d1;
-      if (adc_sum2<M>(lut, w0, w1, v0 < n, v1 < n, __uint_as_float((uint32_t)(thr >> 32)), d0, d1)) {
+      if (adc_sum2_full<M>(lut, w0, w1, __uint_as_float((uint32_t)(thr >> 32)), d0, d1)) {
         if (offer2_k(v0 < n ? key_of(d0, i0) : kPadKey, v1 < n ? key_of(d1, i1) : kPadKey, thr, K1, lk)) {
           own = readlane64(lk, K1 - 1);
           const uint64_t qth = readlane64(lk, Q - 1);
