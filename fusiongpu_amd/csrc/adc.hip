@@ -570,29 +570,37 @@ __global__ __launch_bounds__(kSpecWaves * kWave, 4) void adc_flow_kernel(AdcArgs
       lds_wait_at_least(&s_ready[s], i / 2 + 1);
       const int nv = s_nv[s];
       const int* cst = f_cst[s];
-      auto has_chunk = [&](int g) { return first_own(cst[g]) < cst[g + 1]; };
-      auto chunk_vecs = [&](int g, int cc) { return (unsigned)min(kChunk, f_n[s][g] - (cc - cst[g]) * kChunk); };
       uint64_t lk = kPadKey, own = kNoThr;
-      int have_c = -1;  // chunk whose codes w0/w1/i0/i1 hold (or are being loaded)
-      int f = next_list(s, nv, 0, has_chunk);
-      while (f < nv) {
-        const int dec = lds_wait_decided(&s_dec[s][f]);
-        if (dec < 0) {
-          f = next_list(s, nv, f + 1, has_chunk);
-          continue;
-        }
-        const int start = f_start[s][f], n = f_n[s][f], c_end = cst[f + 1];
-        int c = first_own(cst[f]);
-        if (have_c != c) {
-          load_pair<M>(a.codes, a.vec_ids, start, n, (c - cst[f]) * kChunk + lane, w0, w1, i0, i1);
-          nload += chunk_vecs(f, c);
-        }
+      // List steps.  Each step reads every usable list's table entry and
+      // decision in one batch of LDS reads (one lane a list, nv <= 64), so a
+      // step costs one LDS round trip, not a chain of them: under the scan's
+      // gather load each LDS round trip waits hundreds of clocks.  A wave
+      // visits the lists holding one of its chunks in coarse order; the step
+      // index f only grows, so the loop ends.
+      int f = -1;
+      while (true) {
+        const int dec_l = lane < nv ? __hip_atomic_load(&s_dec[s][lane], __ATOMIC_RELAXED,
+                                                        __HIP_MEMORY_SCOPE_WORKGROUP)
+                                    : kSkipped;
+        const int cst_l = cst[lane], cst_n = cst[lane + 1];
+        const int st_l = f_start[s][lane], n_l = f_n[s][lane];
+        const uint64_t bm = __ballot(lane > f && dec_l != kSkipped && first_own(cst_l) < cst_n);
+        if (!bm) break;
+        f = __ffsll((unsigned long long)bm) - 1;
+        int dec = __builtin_amdgcn_readlane(dec_l, f);
+        if (dec == kUndecided) dec = lds_wait_decided(&s_dec[s][f]);
+        if (dec < 0) continue;
+        const int start = __builtin_amdgcn_readlane(st_l, f), n = __builtin_amdgcn_readlane(n_l, f);
+        const int c0 = __builtin_amdgcn_readlane(cst_l, f), c_end = __builtin_amdgcn_readlane(cst_n, f);
+        int c = first_own(c0);
+        load_pair<M>(a.codes, a.vec_ids, start, n, (c - c0) * kChunk + lane, w0, w1, i0, i1);
+        nload += (unsigned)min(kChunk, n - (c - c0) * kChunk);
         lds_wait_at_least(&s_built[dec & 1], kBuilderWaves * (dec / 2 + 1));
         int mine = 0;
         while (true) {
           const uint64_t shared_thr = s_thr[s];
           const uint64_t thr = own < shared_thr ? own : shared_thr;
-          const int v0 = (c - cst[f]) * kChunk + lane;
+          const int v0 = (c - c0) * kChunk + lane;
           if (dec & 1)
             scan_round_full<D, M, 1>(smem, v0, n, k, w0, w1, i0, i1, thr, lk, own, &s_thr[s]);
           else
@@ -600,21 +608,12 @@ __global__ __launch_bounds__(kSpecWaves * kWave, 4) void adc_flow_kernel(AdcArgs
           ++mine;
           c += kScanWaves;
           if (c >= c_end) break;
-          load_pair<M>(a.codes, a.vec_ids, start, n, (c - cst[f]) * kChunk + lane, w0, w1, i0, i1);
-          nload += chunk_vecs(f, c);
+          load_pair<M>(a.codes, a.vec_ids, start, n, (c - c0) * kChunk + lane, w0, w1, i0, i1);
+          nload += (unsigned)min(kChunk, n - (c - c0) * kChunk);
         }
         // List f done by this wave: its LUT buffer may be reused once all its
         // chunks are in.
         lds_signal_add(&s_done[dec & 1], mine);
-        // Next list; its first codes go out now if it is already known to be built.
-        f = next_list(s, nv, f + 1, has_chunk);
-        have_c = -1;
-        if (f < nv && __hip_atomic_load(&s_dec[s][f], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >= 0) {
-          have_c = first_own(cst[f]);
-          load_pair<M>(a.codes, a.vec_ids, f_start[s][f], f_n[s][f], (have_c - cst[f]) * kChunk + lane, w0, w1, i0,
-                       i1);
-          nload += chunk_vecs(f, have_c);
-        }
       }
       // Through query i: climb the merge tree without waiting.  At each node
       // the wave deposits its list, then counts itself in; the first of the
