@@ -256,10 +256,15 @@ constexpr int kScanWaves = kSpecWaves - kBuilderWaves;
 //     no LUT, no LDS buffer, and the scanners pass over its chunks without
 //     loading codes.  Wave 0 records each decision in dec[f], and every wave
 //     follows it.  Built lists are numbered j = 0, 1, ... over the workgroup's
-//     whole run and use LUT buffer j & 1.
-//   * Builder waves write LUT j once every chunk of built list j - 2 (the
+//     whole run and use LUT buffer b = j % 3, so the builders can be two
+//     lists ahead of the scanners.  Buffer 2 lies beyond the 64 KB reach of
+//     the DS immediate offset, so its gathers take a base register (one more
+//     VALU instruction each); the gathers are bound by LDS bank conflicts,
+//     not VALU issue, and three buffers beat two (C2 ADC 0.467 -> 0.447 ms)
+//     and four (0.462 ms, with staler list decisions).
+//   * Builder waves write LUT j once every chunk of built list j - 3 (the
 //     buffer's previous user) has been scanned, then add 1 to built[b]; a
-//     scanner entering built list j waits for built[b] >= 8 (j / 2 + 1).
+//     scanner entering built list j waits for built[b] >= 8 (j / 3 + 1).
 //   * Scanners add the chunks of a built list they finish to done[b] when they
 //     leave it; the builder of list j waits for done[b] to reach the chunk
 //     count of the earlier built lists of buffer b.
@@ -278,8 +283,8 @@ constexpr int kScanWaves = kSpecWaves - kBuilderWaves;
 //     never stop a 128-vector round, so the list bound above is the only
 //     pruning.
 // All counters are cumulative.  A count cannot run ahead of the list it
-// stands for: a builder wave contributes to built list j + 2 only after all of
-// list j is scanned, and a scanner scans list j + 2 only after it is built, so
+// stands for: a builder wave contributes to built list j + 3 only after all of
+// list j is scanned, and a scanner scans list j + 3 only after it is built, so
 // the first time a threshold is met every contribution comes from earlier
 // lists of that buffer.  Deadlock-free: builders decide lists in order and
 // wait only on chunks of lists already built, or on the end of query i - 1
@@ -287,6 +292,7 @@ constexpr int kScanWaves = kSpecWaves - kBuilderWaves;
 // scanners take chunks in increasing order and report a list before waiting
 // on the next.  Each builder wave computes its own part of the residual, so
 // builders never wait on each other outside the set-up.
+constexpr int kLutBufs = 3;  // LUT buffers of the flow kernel
 constexpr int kUndecided = -1;
 constexpr int kSkipped = -2;
 
@@ -324,7 +330,7 @@ __global__ __launch_bounds__(kSpecWaves * kWave, 4) void adc_flow_kernel(AdcArgs
   constexpr int RW = SPW * C::S;  // residual floats per builder wave
   constexpr int kMaxPerWave = 64 / kBuilderWaves;  // set-up: probes per builder wave (nprobe <= 64)
   static_assert(M % kBuilderWaves == 0 && (TPM == 16 || TPM == 32) && E % 4 == 0, "builder layout");
-  __shared__ __align__(16) float smem[2 * C::LUT];
+  __shared__ __align__(16) float smem[kLutBufs * C::LUT];
   __shared__ float rws[kBuilderWaves][16];
   // Per query slot.  p_*: by probe index (set-up); f_*: compacted usable lists.
   __shared__ float p_lb[2][64];
@@ -337,7 +343,7 @@ __global__ __launch_bounds__(kSpecWaves * kWave, 4) void adc_flow_kernel(AdcArgs
   __shared__ uint64_t s_tree[2][kScanWaves - 1][2][kWave];
   __shared__ int s_arr[2][kScanWaves - 1];  // arrivals per tree node
   __shared__ int s_ready[2], s_free[2], s_lbdone[2];
-  __shared__ int s_built[2], s_done[2];  // per LUT buffer
+  __shared__ int s_built[kLutBufs], s_done[kLutBufs];  // per LUT buffer
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const bool builder = wave < kBuilderWaves;
   const long long t_start = a.stats ? clock64() : 0;
@@ -351,6 +357,8 @@ __global__ __launch_bounds__(kSpecWaves * kWave, 4) void adc_flow_kernel(AdcArgs
     s_ready[tid] = 0;
     s_free[tid] = 0;
     s_lbdone[tid] = 0;
+  }
+  if (tid < kLutBufs) {
     s_built[tid] = 0;
     s_done[tid] = 0;
   }
@@ -469,7 +477,7 @@ __global__ __launch_bounds__(kSpecWaves * kWave, 4) void adc_flow_kernel(AdcArgs
       }
     };
 
-    int nbuilt = 0, need0 = 0, need1 = 0, nskip = 0;
+    int nbuilt = 0, need0 = 0, need1 = 0, need2 = 0, nskip = 0;
     long long t_su = 0;
     if (nqw > 0) setup(0);
     for (int i = 0; i < nqw; ++i) {
@@ -511,7 +519,7 @@ __global__ __launch_bounds__(kSpecWaves * kWave, 4) void adc_flow_kernel(AdcArgs
           f = next_list(s, nv, f + 1, any_list);
           continue;
         }
-        const int b = dec & 1;
+        const int b = dec % kLutBufs;
         ++nbuilt;
         float cs = cnext;
         if (cnext_f != f && lane < RW) cs = a.centroids[(size_t)f_list[s][f] * D + wave * RW + lane];
@@ -526,7 +534,7 @@ __global__ __launch_bounds__(kSpecWaves * kWave, 4) void adc_flow_kernel(AdcArgs
         float r[C::S];
 #pragma unroll
         for (int d = 0; d < C::S; ++d) r[d] = rw[(lane / TPM) * C::S + d];
-        lds_wait_at_least<kLazySleep>(&s_done[b], b ? need1 : need0);
+        lds_wait_at_least<kLazySleep>(&s_done[b], b == 0 ? need0 : b == 1 ? need1 : need2);
         float* lut = smem + b * C::LUT + ms * kPQK + 4 * t;
 #pragma unroll
         for (int u = 0; u < E / 4; ++u) {
@@ -539,7 +547,12 @@ __global__ __launch_bounds__(kSpecWaves * kWave, 4) void adc_flow_kernel(AdcArgs
         }
         lds_signal_add(&s_built[b], 1);
         const int nch = f_cst[s][f + 1] - f_cst[s][f];
-        if (b) need1 += nch; else need0 += nch;
+        if (b == 0)
+          need0 += nch;
+        else if (b == 1)
+          need1 += nch;
+        else
+          need2 += nch;
         f = cnext_f;
       }
       if (i + 1 < nqw) {
@@ -595,16 +608,19 @@ __global__ __launch_bounds__(kSpecWaves * kWave, 4) void adc_flow_kernel(AdcArgs
         int c = first_own(c0);
         load_pair<M>(a.codes, a.vec_ids, start, n, (c - c0) * kChunk + lane, w0, w1, i0, i1);
         nload += (unsigned)min(kChunk, n - (c - c0) * kChunk);
-        lds_wait_at_least(&s_built[dec & 1], kBuilderWaves * (dec / 2 + 1));
+        const int b = dec % kLutBufs;
+        lds_wait_at_least(&s_built[b], kBuilderWaves * (dec / kLutBufs + 1));
         int mine = 0;
         while (true) {
           const uint64_t shared_thr = s_thr[s];
           const uint64_t thr = own < shared_thr ? own : shared_thr;
           const int v0 = (c - c0) * kChunk + lane;
-          if (dec & 1)
-            scan_round_full<D, M, 1>(smem, v0, n, k, w0, w1, i0, i1, thr, lk, own, &s_thr[s]);
-          else
+          if (b == 0)
             scan_round_full<D, M, 0>(smem, v0, n, k, w0, w1, i0, i1, thr, lk, own, &s_thr[s]);
+          else if (b == 1)
+            scan_round_full<D, M, 1>(smem, v0, n, k, w0, w1, i0, i1, thr, lk, own, &s_thr[s]);
+          else  // beyond the 64 KB DS offset reach: addresses take a base register
+            scan_round_full<D, M, 2>(smem, v0, n, k, w0, w1, i0, i1, thr, lk, own, &s_thr[s]);
           ++mine;
           c += kScanWaves;
           if (c >= c_end) break;
@@ -613,7 +629,7 @@ __global__ __launch_bounds__(kSpecWaves * kWave, 4) void adc_flow_kernel(AdcArgs
         }
         // List f done by this wave: its LUT buffer may be reused once all its
         // chunks are in.
-        lds_signal_add(&s_done[dec & 1], mine);
+        lds_signal_add(&s_done[b], mine);
       }
       // Through query i: climb the merge tree without waiting.  At each node
       // the wave deposits its list, then counts itself in; the first of the
