@@ -23,6 +23,7 @@ Reference interfaces mirrored (Hello-day/FusionGPU):
 """
 from __future__ import annotations
 
+import contextlib
 import ctypes
 import os
 
@@ -32,6 +33,7 @@ __all__ = [
     "FgpuError", "lib", "lib_path", "Index", "gen_gmm", "l2_topk", "kmeans_fit", "kmeans_update",
     "fixed_shift", "pq_train", "pq_encode", "build_ivfpq", "write_ivf_data", "read_ivf_data",
     "write_fvecs", "read_fvecs", "read_ivecs", "probe_counts", "rerank", "knn_exact", "graph_search",
+    "debug_set_spin_limit", "FAULT_ID",
 ]
 
 lib_path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib", "libfusiongpu.so")
@@ -47,6 +49,9 @@ _SIGS = {
     "fgpu_index_load": (_i32, [_c.c_char_p, _c.c_char_p, _i32, _i32, _c.POINTER(_vp)]),
     "fgpu_index_destroy": (None, [_vp]),
     "fgpu_index_get_info": (_i32, [_vp, _vp]),
+    "fgpu_index_faults": (_i32, [_vp, _vp, _c.POINTER(_c.c_ulonglong), _i32]),
+    "fgpu_index_check": (_i32, [_vp, _vp]),
+    "fgpu_debug_set_spin_limit": (None, [_i32]),
     "fgpu_coarse_workspace_bytes": (_sz, [_i32, _i32]),
     "fgpu_coarse_search": (_i32, [_vp, _vp, _i32, _i32, _f32, _vp, _vp, _vp, _sz, _vp]),
     "fgpu_coarse_graph_workspace_bytes": (_sz, [_i32, _i32]),
@@ -141,15 +146,33 @@ def _torch():
     return torch
 
 
+FAULT_ID = -2  # FGPU_FAULT_ID: every slot of a query a bounded-wait give-up may have touched
+
+
 def _dev_ptr(t):
     assert t.is_cuda and t.is_contiguous(), "expected a contiguous device tensor"
     return _vp(t.data_ptr())
 
 
-def _stream(stream=None):
-    torch = _torch()
-    s = stream if stream is not None else torch.cuda.current_stream()
-    return _vp(s.cuda_stream)
+def _opt_ptr(t):
+    return _dev_ptr(t) if t is not None else None
+
+
+def _on(stream):
+    """Context for one library call: with an explicit stream, that stream is
+    torch's current stream while the call converts its inputs, allocates its
+    workspace, temporaries and outputs and enqueues its kernels.  The caching
+    allocator then ties every internal tensor to the stream the kernels run on,
+    so memory freed when the call returns is only handed to later work on that
+    same stream, never to other work while the kernels still read it."""
+    if stream is None:
+        return contextlib.nullcontext()
+    return _torch().cuda.stream(stream)
+
+
+def _stream():
+    """hipStream_t of torch's current stream (the one _on made current)."""
+    return _vp(_torch().cuda.current_stream().cuda_stream)
 
 
 def _workspace(nbytes: int):
@@ -157,11 +180,71 @@ def _workspace(nbytes: int):
     return torch.empty(max(int(nbytes), 256), dtype=torch.uint8, device="cuda")
 
 
-def _to_dev(a, dtype=None):
+def _ws_check(ws, name="workspace"):
+    torch = _torch()
+    if not (torch.is_tensor(ws) and ws.is_cuda and ws.is_contiguous()):
+        raise ValueError(f"{name}: expected a contiguous device tensor")
+    return ws.numel() * ws.element_size()
+
+
+# Implicit conversions the host mirror performs (the C ABI reads exactly these
+# element types): floating inputs become float32, integer ids int32 (an int64
+# probe id keeps its low 32 bits, so 0xFFFFFFFF stays the pruned sentinel).
+_FLOATS = ("float64", "float16", "bfloat16")
+_INTS = ("int64", "int16", "int8", "uint8", "uint16", "uint32")
+
+
+def _arg(a, dtype, name, shape=None):
+    """`a` (numpy array or torch tensor) as a torch tensor of `dtype` where it
+    lies, after checking its rank and the fixed entries of `shape` (None = any
+    size).  Raises TypeError / ValueError before anything is copied."""
     torch = _torch()
     if isinstance(a, np.ndarray):
-        return torch.from_numpy(np.ascontiguousarray(a)).to("cuda")
+        a = torch.from_numpy(np.ascontiguousarray(a))
+    elif not torch.is_tensor(a):
+        raise TypeError(f"{name}: expected a numpy array or a torch tensor, got {type(a).__name__}")
+    if a.dtype != dtype:
+        src = str(a.dtype).replace("torch.", "")
+        ok = (dtype == torch.float32 and src in _FLOATS) or (dtype == torch.int32 and src in _INTS)
+        if not ok:
+            raise TypeError(f"{name}: dtype {src} cannot be read as {str(dtype).replace('torch.', '')}")
+    if shape is not None:
+        if a.dim() != len(shape):
+            raise ValueError(f"{name}: expected {len(shape)} dimensions, got shape {tuple(a.shape)}")
+        for i, want in enumerate(shape):
+            if want is not None and a.shape[i] != want:
+                raise ValueError(f"{name}: dimension {i} is {a.shape[i]}, expected {want} "
+                                 f"(shape {tuple(a.shape)})")
+    return a.to(dtype) if a.dtype != dtype else a
+
+
+def _dev(a, dtype, name, shape=None):
+    """_arg, then a contiguous device tensor (copied to the device if needed)."""
+    a = _arg(a, dtype, name, shape)
+    if not a.is_cuda:
+        a = a.to("cuda")
     return a.contiguous()
+
+
+def _out(t, dtype, shape, name):
+    """Check a caller-supplied output tensor (dtype, exact shape, contiguous device memory)."""
+    torch = _torch()
+    if not torch.is_tensor(t):
+        raise TypeError(f"{name}: expected a torch tensor")
+    if t.dtype != dtype or tuple(t.shape) != tuple(shape) or not t.is_cuda or not t.is_contiguous():
+        raise ValueError(f"{name}: expected a contiguous device tensor {str(dtype).replace('torch.', '')}"
+                         f"{list(shape)}, got {t.dtype} {list(t.shape)} on {t.device}")
+    return t
+
+
+def _outs(out, nq, k, name="out"):
+    """(ids int32 [nq][k], dists float32 [nq][k]): the caller's, checked, or new."""
+    torch = _torch()
+    if out is None:
+        return (torch.empty((nq, k), dtype=torch.int32, device="cuda"),
+                torch.empty((nq, k), dtype=torch.float32, device="cuda"))
+    ids, d = out
+    return _out(ids, torch.int32, (nq, k), name + "[0]"), _out(d, torch.float32, (nq, k), name + "[1]")
 
 
 # --------------------------------------------------------------------------- synthetic data
@@ -218,6 +301,11 @@ def read_ivecs(path) -> np.ndarray:
     return out
 
 
+def debug_set_spin_limit(polls: int):
+    """Test hook (fgpu_debug_set_spin_limit): polls before a scan wait gives up; 0 = automatic."""
+    lib.fgpu_debug_set_spin_limit(int(polls))
+
+
 # --------------------------------------------------------------------------- index + search
 class _Info(ctypes.Structure):
     _fields_ = [("dim", _i32), ("pq_m", _i32), ("pq_k", _i32), ("nlist", _i32), ("total", _i64),
@@ -243,9 +331,14 @@ class Index:
         codes = np.ascontiguousarray(codes, np.uint8)
         centroids = np.ascontiguousarray(centroids, np.float32)
         codebook = np.ascontiguousarray(codebook, np.float32)
+        nlist, total = offsets.shape[0] - 1, ids.shape[0]
+        if codes.shape != (total, pq_m) or centroids.shape != (nlist, dim) or codebook.size != pq_m * 256 * (
+                dim // max(pq_m, 1)):
+            raise ValueError(f"from_arrays: inconsistent shapes: ids {ids.shape}, codes {codes.shape}, "
+                             f"centroids {centroids.shape}, codebook {codebook.shape} for dim {dim}, pq_m {pq_m}")
         h = _vp()
-        _check(lib.fgpu_index_create(dim, pq_m, offsets.shape[0] - 1, ids.shape[0], _np_ptr(offsets), _np_ptr(ids),
-                                     _np_ptr(codes), _np_ptr(centroids), _np_ptr(codebook), _c.byref(h)))
+        _check(lib.fgpu_index_create(dim, pq_m, nlist, total, _np_ptr(offsets), _np_ptr(ids), _np_ptr(codes),
+                                     _np_ptr(centroids), _np_ptr(codebook), _c.byref(h)))
         return cls(h.value)
 
     @classmethod
@@ -266,6 +359,30 @@ class Index:
         except Exception:
             pass
 
+    # -- bounded-wait give-ups of the scan kernel
+    def faults(self, reset: bool = False, stream=None) -> int:
+        """Give-ups of the scan kernel's bounded waits on this index (fgpu_index_faults; 0 in a correct run).
+        Waits for the stream."""
+        v = _c.c_ulonglong()
+        with _on(stream):
+            _check(lib.fgpu_index_faults(self._h, _stream(), _c.byref(v), int(bool(reset))))
+        return int(v.value)
+
+    def check(self, stream=None):
+        """Raise FgpuError (FGPU_ERR_WAIT) if any bounded wait of the scan kernel gave up (fgpu_index_check)."""
+        with _on(stream):
+            _check(lib.fgpu_index_check(self._h, _stream()))
+
+    # -- argument helpers
+    def _queries(self, queries):
+        return _dev(queries, _torch().float32, "queries", (None, self.dim))
+
+    def _probes(self, probe_ids, nq=None):
+        p = _dev(probe_ids, _torch().int32, "probe_ids", (nq, None))
+        if p.shape[1] < 1:
+            raise ValueError("probe_ids: need at least one probe per query")
+        return p
+
     # -- search
     def coarse_workspace_bytes(self, nq: int) -> int:
         return lib.fgpu_coarse_workspace_bytes(nq, self.nlist)
@@ -273,22 +390,22 @@ class Index:
     def coarse_search(self, queries, nprobe: int, prune_ratio: float = 100.0, workspace=None, out=None,
                       stream=None):
         """Exact top-nprobe lists: (probe_ids uint32-as-int32 [nq][nprobe], dists [nq][nprobe])."""
-        torch = _torch()
-        q = _to_dev(queries)
-        nq = q.shape[0]
-        ws = workspace if workspace is not None else _workspace(self.coarse_workspace_bytes(nq))
-        ids, d = out if out is not None else (torch.empty((nq, nprobe), dtype=torch.int32, device="cuda"),
-                                              torch.empty((nq, nprobe), dtype=torch.float32, device="cuda"))
-        _check(lib.fgpu_coarse_search(self._h, _dev_ptr(q), nq, nprobe, prune_ratio, _dev_ptr(ids), _dev_ptr(d),
-                                      _dev_ptr(ws), ws.numel(), _stream(stream)))
+        with _on(stream):
+            q = self._queries(queries)
+            nq = q.shape[0]
+            ws = workspace if workspace is not None else _workspace(self.coarse_workspace_bytes(nq))
+            ids, d = _outs(out, nq, nprobe)
+            _check(lib.fgpu_coarse_search(self._h, _dev_ptr(q), nq, nprobe, prune_ratio, _dev_ptr(ids), _dev_ptr(d),
+                                          _dev_ptr(ws), _ws_check(ws), _stream()))
         return ids, d
 
     def coarse_graph_build(self, degree: int = 8, stream=None):
         """Exact kNN graph of the centroids, self excluded (fgpu_coarse_graph_build): int32 [nlist][degree]."""
         torch = _torch()
-        g = torch.empty((self.nlist, degree), dtype=torch.int32, device="cuda")
-        ws = _workspace(lib.fgpu_coarse_graph_workspace_bytes(self.nlist, degree))
-        _check(lib.fgpu_coarse_graph_build(self._h, degree, _dev_ptr(g), _dev_ptr(ws), ws.numel(), _stream(stream)))
+        with _on(stream):
+            g = torch.empty((self.nlist, degree), dtype=torch.int32, device="cuda")
+            ws = _workspace(lib.fgpu_coarse_graph_workspace_bytes(self.nlist, degree))
+            _check(lib.fgpu_coarse_graph_build(self._h, degree, _dev_ptr(g), _dev_ptr(ws), _ws_check(ws), _stream()))
         return g
 
     def coarse_graph_search(self, queries, nprobe: int, graph, itopk: int = 32, width: int = 4, max_iter: int = 200,
@@ -297,44 +414,45 @@ class Index:
         """Top-nprobe lists by the graph walk over the centroids (fgpu_coarse_graph_search): (probe_ids
         uint32-as-int32 [nq][nprobe], dists [nq][nprobe])."""
         torch = _torch()
-        q = _to_dev(queries)
-        g = _to_dev(graph)
-        nq = q.shape[0]
-        ids, d = out if out is not None else (torch.empty((nq, nprobe), dtype=torch.int32, device="cuda"),
-                                              torch.empty((nq, nprobe), dtype=torch.float32, device="cuda"))
-        _check(lib.fgpu_coarse_graph_search(self._h, _dev_ptr(q), nq, first_query, nprobe, _dev_ptr(g), g.shape[1],
-                                            itopk, width, max_iter, seed, prune_ratio, _dev_ptr(ids), _dev_ptr(d),
-                                            _stream(stream)))
+        with _on(stream):
+            q = self._queries(queries)
+            g = _dev(graph, torch.int32, "graph", (self.nlist, None))
+            nq = q.shape[0]
+            ids, d = _outs(out, nq, nprobe)
+            _check(lib.fgpu_coarse_graph_search(self._h, _dev_ptr(q), nq, first_query, nprobe, _dev_ptr(g),
+                                                g.shape[1], itopk, width, max_iter, seed, prune_ratio, _dev_ptr(ids),
+                                                _dev_ptr(d), _stream()))
         return ids, d
 
     def adc_search(self, queries, probe_ids, k: int, out=None, stream=None, probe_dists=None):
         """LUT + ADC scan + top-k over the probed lists: (ids int32 [nq][k], dists float32 [nq][k]).
         probe_dists: coarse_search's distances for these probes (optional; the list bounds use them)."""
         torch = _torch()
-        q = _to_dev(queries)
-        p = _to_dev(probe_ids)
-        nq, nprobe = p.shape
-        pd = _to_dev(probe_dists) if probe_dists is not None else None
-        ids, d = out if out is not None else (torch.empty((nq, k), dtype=torch.int32, device="cuda"),
-                                              torch.empty((nq, k), dtype=torch.float32, device="cuda"))
-        _check(lib.fgpu_adc_search(self._h, _dev_ptr(q), nq, _dev_ptr(p), _dev_ptr(pd) if pd is not None else None,
-                                   nprobe, k, _dev_ptr(ids), _dev_ptr(d), _stream(stream)))
+        with _on(stream):
+            q = self._queries(queries)
+            nq = q.shape[0]
+            p = self._probes(probe_ids, nq)
+            nprobe = p.shape[1]
+            pd = _dev(probe_dists, torch.float32, "probe_dists", (nq, nprobe)) if probe_dists is not None else None
+            ids, d = _outs(out, nq, k)
+            _check(lib.fgpu_adc_search(self._h, _dev_ptr(q), nq, _dev_ptr(p), _opt_ptr(pd), nprobe, k, _dev_ptr(ids),
+                                       _dev_ptr(d), _stream()))
         return ids, d
 
     def adc_search_stats(self, queries, probe_ids, k: int, out=None, stream=None, probe_dists=None):
-        """adc_search plus counters: (ids, dists, {"vectors_loaded", "luts_built", "lists_skipped"})."""
+        """adc_search plus counters: (ids, dists, {"vectors_loaded", "luts_built", "lists_skipped", clocks})."""
         torch = _torch()
-        q = _to_dev(queries)
-        p = _to_dev(probe_ids)
-        nq, nprobe = p.shape
-        pd = _to_dev(probe_dists) if probe_dists is not None else None
-        ids, d = out if out is not None else (torch.empty((nq, k), dtype=torch.int32, device="cuda"),
-                                              torch.empty((nq, k), dtype=torch.float32, device="cuda"))
-        st = torch.zeros(8, dtype=torch.int64, device="cuda")
-        _check(lib.fgpu_adc_search_stats(self._h, _dev_ptr(q), nq, _dev_ptr(p),
-                                         _dev_ptr(pd) if pd is not None else None, nprobe, k, _dev_ptr(ids),
-                                         _dev_ptr(d), _dev_ptr(st), _stream(stream)))
-        v = st.cpu().tolist()
+        with _on(stream):
+            q = self._queries(queries)
+            nq = q.shape[0]
+            p = self._probes(probe_ids, nq)
+            nprobe = p.shape[1]
+            pd = _dev(probe_dists, torch.float32, "probe_dists", (nq, nprobe)) if probe_dists is not None else None
+            ids, d = _outs(out, nq, k)
+            st = torch.zeros(8, dtype=torch.int64, device="cuda")
+            _check(lib.fgpu_adc_search_stats(self._h, _dev_ptr(q), nq, _dev_ptr(p), _opt_ptr(pd), nprobe, k,
+                                             _dev_ptr(ids), _dev_ptr(d), _dev_ptr(st), _stream()))
+            v = st.cpu().tolist()
         return ids, d, {"vectors_loaded": v[0], "luts_built": v[1], "lists_skipped": v[2], "clk_setup": v[3],
                         "clk_builder": v[4], "clk_scanner": v[5], "clk_total": v[6]}
 
@@ -343,41 +461,44 @@ class Index:
         """run_gpu_batch_logic after the coarse step: (top_ids [nq][rerank_m], top_dists, top_counts [nq],
         cutoffs [nq][p1] or None, thresholds [nq] or None)."""
         torch = _torch()
-        q = _to_dev(queries)
-        p = _to_dev(probe_ids)
-        nq, nprobe = p.shape
-        p1 = max(0, min(nprobe, p1_lists))
-        ws = workspace if workspace is not None else _workspace(
-            lib.fgpu_two_phase_workspace_bytes(nq, nprobe, p1_lists, limit_k, rerank_m))
-        tid = torch.empty((nq, rerank_m), dtype=torch.int32, device="cuda")
-        td = torch.empty((nq, rerank_m), dtype=torch.float32, device="cuda")
-        tc = torch.empty(nq, dtype=torch.int32, device="cuda")
-        cut = torch.empty((nq, max(p1, 1)), dtype=torch.float32, device="cuda") if want_cutoffs else None
-        thr = torch.empty(nq, dtype=torch.float32, device="cuda") if want_cutoffs else None
-        _check(lib.fgpu_two_phase_search(self._h, _dev_ptr(q), nq, _dev_ptr(p), nprobe, p1_lists, limit_k,
-                                         threshold_coeff, rerank_m, _dev_ptr(tid), _dev_ptr(td), _dev_ptr(tc),
-                                         _dev_ptr(cut) if want_cutoffs else None,
-                                         _dev_ptr(thr) if want_cutoffs else None, _dev_ptr(ws), ws.numel(),
-                                         _stream(stream)))
+        with _on(stream):
+            q = self._queries(queries)
+            nq = q.shape[0]
+            p = self._probes(probe_ids, nq)
+            nprobe = p.shape[1]
+            p1 = max(0, min(nprobe, p1_lists))
+            ws = workspace if workspace is not None else _workspace(
+                lib.fgpu_two_phase_workspace_bytes(nq, nprobe, p1_lists, limit_k, rerank_m))
+            tid = torch.empty((nq, rerank_m), dtype=torch.int32, device="cuda")
+            td = torch.empty((nq, rerank_m), dtype=torch.float32, device="cuda")
+            tc = torch.empty(nq, dtype=torch.int32, device="cuda")
+            cut = torch.empty((nq, max(p1, 1)), dtype=torch.float32, device="cuda") if want_cutoffs else None
+            thr = torch.empty(nq, dtype=torch.float32, device="cuda") if want_cutoffs else None
+            _check(lib.fgpu_two_phase_search(self._h, _dev_ptr(q), nq, _dev_ptr(p), nprobe, p1_lists, limit_k,
+                                             threshold_coeff, rerank_m, _dev_ptr(tid), _dev_ptr(td), _dev_ptr(tc),
+                                             _opt_ptr(cut), _opt_ptr(thr), _dev_ptr(ws), _ws_check(ws), _stream()))
         return tid, td, tc, (cut[:, :p1] if want_cutoffs else None), thr
 
     def two_phase_stats(self, queries, probe_ids, p1_lists: int, limit_k: int, threshold_coeff: float, rerank_m: int,
                         workspace=None, stream=None):
         """two_phase_search plus counters: (top_ids, top_dists, top_counts, {counter: value})."""
         torch = _torch()
-        q = _to_dev(queries)
-        p = _to_dev(probe_ids)
-        nq, nprobe = p.shape
-        ws = workspace if workspace is not None else _workspace(
-            lib.fgpu_two_phase_workspace_bytes(nq, nprobe, p1_lists, limit_k, rerank_m))
-        tid = torch.empty((nq, rerank_m), dtype=torch.int32, device="cuda")
-        td = torch.empty((nq, rerank_m), dtype=torch.float32, device="cuda")
-        tc = torch.empty(nq, dtype=torch.int32, device="cuda")
-        st = torch.zeros(12, dtype=torch.int64, device="cuda")
-        _check(lib.fgpu_two_phase_search_stats(self._h, _dev_ptr(q), nq, _dev_ptr(p), nprobe, p1_lists, limit_k,
-                                               threshold_coeff, rerank_m, _dev_ptr(tid), _dev_ptr(td), _dev_ptr(tc),
-                                               _dev_ptr(st), _dev_ptr(ws), ws.numel(), _stream(stream)))
-        v = st.cpu().tolist()
+        with _on(stream):
+            q = self._queries(queries)
+            nq = q.shape[0]
+            p = self._probes(probe_ids, nq)
+            nprobe = p.shape[1]
+            ws = workspace if workspace is not None else _workspace(
+                lib.fgpu_two_phase_workspace_bytes(nq, nprobe, p1_lists, limit_k, rerank_m))
+            tid = torch.empty((nq, rerank_m), dtype=torch.int32, device="cuda")
+            td = torch.empty((nq, rerank_m), dtype=torch.float32, device="cuda")
+            tc = torch.empty(nq, dtype=torch.int32, device="cuda")
+            st = torch.zeros(12, dtype=torch.int64, device="cuda")
+            _check(lib.fgpu_two_phase_search_stats(self._h, _dev_ptr(q), nq, _dev_ptr(p), nprobe, p1_lists, limit_k,
+                                                   threshold_coeff, rerank_m, _dev_ptr(tid), _dev_ptr(td),
+                                                   _dev_ptr(tc), _dev_ptr(st), _dev_ptr(ws), _ws_check(ws),
+                                                   _stream()))
+            v = st.cpu().tolist()
         return tid, td, tc, {"vectors_loaded": v[0], "luts_built": v[1], "lists_skipped": v[2],
                              "phase2_appended": v[3], "clk_setup": v[4], "clk_phase1": v[5], "clk_phase2": v[6],
                              "clk_final": v[7], "clk_p1_build": v[8], "clk_p1_scan": v[9], "clk_p1_merge": v[10]}
@@ -390,16 +511,16 @@ class Index:
                       beta: int = 2, prune_ratio: float = 100.0, workspace=None, out=None, stream=None):
         """coarse + two-phase scan + exact rerank (SearchPipeline's per-batch path): (ids, dists) [nq][k]."""
         torch = _torch()
-        q = _to_dev(queries)
-        b = _to_dev(base)
-        nq = q.shape[0]
-        ws = workspace if workspace is not None else _workspace(
-            self.search_rerank_workspace_bytes(nq, nprobe, p1_lists, limit_k, rerank_m))
-        ids, d = out if out is not None else (torch.empty((nq, k), dtype=torch.int32, device="cuda"),
-                                              torch.empty((nq, k), dtype=torch.float32, device="cuda"))
-        _check(lib.fgpu_search_rerank(self._h, _dev_ptr(q), nq, nprobe, prune_ratio, p1_lists, limit_k,
-                                      threshold_coeff, rerank_m, _dev_ptr(b), b.shape[0], k, mini_batch, eps, beta,
-                                      _dev_ptr(ids), _dev_ptr(d), _dev_ptr(ws), ws.numel(), _stream(stream)))
+        with _on(stream):
+            q = self._queries(queries)
+            b = _dev(base, torch.float32, "base", (None, self.dim))
+            nq = q.shape[0]
+            ws = workspace if workspace is not None else _workspace(
+                self.search_rerank_workspace_bytes(nq, nprobe, p1_lists, limit_k, rerank_m))
+            ids, d = _outs(out, nq, k)
+            _check(lib.fgpu_search_rerank(self._h, _dev_ptr(q), nq, nprobe, prune_ratio, p1_lists, limit_k,
+                                          threshold_coeff, rerank_m, _dev_ptr(b), b.shape[0], k, mini_batch, eps, beta,
+                                          _dev_ptr(ids), _dev_ptr(d), _dev_ptr(ws), _ws_check(ws), _stream()))
         return ids, d
 
     def search_workspace_bytes(self, nq: int, nprobe: int) -> int:
@@ -407,14 +528,14 @@ class Index:
 
     def search(self, queries, nprobe: int, k: int, prune_ratio: float = 100.0, workspace=None, out=None,
                stream=None):
-        torch = _torch()
-        q = _to_dev(queries)
-        nq = q.shape[0]
-        ws = workspace if workspace is not None else _workspace(self.search_workspace_bytes(nq, nprobe))
-        ids, d = out if out is not None else (torch.empty((nq, k), dtype=torch.int32, device="cuda"),
-                                              torch.empty((nq, k), dtype=torch.float32, device="cuda"))
-        _check(lib.fgpu_search(self._h, _dev_ptr(q), nq, nprobe, k, prune_ratio, _dev_ptr(ids), _dev_ptr(d),
-                               _dev_ptr(ws), ws.numel(), _stream(stream)))
+        """coarse + LUT/ADC scan + top-k in one call (fgpu_search): (ids int32 [nq][k], dists float32 [nq][k])."""
+        with _on(stream):
+            q = self._queries(queries)
+            nq = q.shape[0]
+            ws = workspace if workspace is not None else _workspace(self.search_workspace_bytes(nq, nprobe))
+            ids, d = _outs(out, nq, k)
+            _check(lib.fgpu_search(self._h, _dev_ptr(q), nq, nprobe, k, prune_ratio, _dev_ptr(ids), _dev_ptr(d),
+                                   _dev_ptr(ws), _ws_check(ws), _stream()))
         return ids, d
 
     def tune_list_stats(self, queries, pair_query, pair_list, pair_target=None, pair_kth=None, base=None,
@@ -423,33 +544,33 @@ class Index:
         exact_rank, kth_pq) as device tensors; the first four are None without pair_target, the last without
         pair_kth."""
         torch = _torch()
-        q = _to_dev(queries)
-        pq, pl = _to_dev(pair_query), _to_dev(pair_list)
-        n = pq.shape[0]
-        pt = _to_dev(pair_target) if pair_target is not None else None
-        pk = _to_dev(pair_kth) if pair_kth is not None else None
-        b = _to_dev(base) if base is not None else None
-        f = lambda: torch.empty(n, dtype=torch.float32, device="cuda")  # noqa: E731
-        i = lambda: torch.empty(n, dtype=torch.int32, device="cuda")  # noqa: E731
-        tp, te, pr, er = (f(), f(), i(), i()) if pt is not None else (None, None, None, None)
-        kp = f() if pk is not None else None
-        _check(lib.fgpu_tune_list_stats(self._h, _dev_ptr(q), q.shape[0], _dev_ptr(b) if b is not None else None,
-                                        b.shape[0] if b is not None else 0, _dev_ptr(pq), _dev_ptr(pl),
-                                        _dev_ptr(pt) if pt is not None else None,
-                                        _dev_ptr(pk) if pk is not None else None, n,
-                                        *(_dev_ptr(t) if t is not None else None for t in (tp, te, pr, er, kp)),
-                                        _stream(stream)))
+        with _on(stream):
+            q = self._queries(queries)
+            pq = _dev(pair_query, torch.int32, "pair_query", (None,))
+            n = pq.shape[0]
+            pl = _dev(pair_list, torch.int32, "pair_list", (n,))
+            pt = _dev(pair_target, torch.int32, "pair_target", (n,)) if pair_target is not None else None
+            pk = _dev(pair_kth, torch.int32, "pair_kth", (n,)) if pair_kth is not None else None
+            b = _dev(base, torch.float32, "base", (None, self.dim)) if base is not None else None
+            f = lambda: torch.empty(n, dtype=torch.float32, device="cuda")  # noqa: E731
+            i = lambda: torch.empty(n, dtype=torch.int32, device="cuda")  # noqa: E731
+            tp, te, pr, er = (f(), f(), i(), i()) if pt is not None else (None, None, None, None)
+            kp = f() if pk is not None else None
+            _check(lib.fgpu_tune_list_stats(self._h, _dev_ptr(q), q.shape[0], _opt_ptr(b),
+                                            b.shape[0] if b is not None else 0, _dev_ptr(pq), _dev_ptr(pl),
+                                            _opt_ptr(pt), _opt_ptr(pk), n,
+                                            *(_opt_ptr(t) for t in (tp, te, pr, er, kp)), _stream()))
         return tp, te, pr, er, kp
 
 
 def probe_counts(index: Index, probe_ids, stream=None):
     torch = _torch()
-    p = _to_dev(probe_ids)
-    nq, nprobe = p.shape
-    counts = torch.empty(nq, dtype=torch.int32, device="cuda")
-    offs = torch.empty(nq + 1, dtype=torch.int32, device="cuda")
-    _check(lib.fgpu_probe_counts(index._h, _dev_ptr(p), nq, nprobe, _dev_ptr(counts), _dev_ptr(offs),
-                                 _stream(stream)))
+    with _on(stream):
+        p = index._probes(probe_ids)
+        nq, nprobe = p.shape
+        counts = torch.empty(nq, dtype=torch.int32, device="cuda")
+        offs = torch.empty(nq + 1, dtype=torch.int32, device="cuda")
+        _check(lib.fgpu_probe_counts(index._h, _dev_ptr(p), nq, nprobe, _dev_ptr(counts), _dev_ptr(offs), _stream()))
     return counts, offs
 
 
@@ -457,14 +578,18 @@ def rerank(queries, base, top_ids, top_counts, k: int, mini_batch: int = 128, ep
            stream=None):
     """run_gpu_rerank: exact L2 over the ADC-ordered candidates with the early stop: (ids, dists, visited)."""
     torch = _torch()
-    q, b, t, c = _to_dev(queries), _to_dev(base), _to_dev(top_ids), _to_dev(top_counts)
-    nq, dim = q.shape
-    rm = t.shape[1]
-    ids = torch.empty((nq, k), dtype=torch.int32, device="cuda")
-    d = torch.empty((nq, k), dtype=torch.float32, device="cuda")
-    vis = torch.empty(nq, dtype=torch.int32, device="cuda")
-    _check(lib.fgpu_rerank(_dev_ptr(q), nq, dim, _dev_ptr(b), b.shape[0], _dev_ptr(t), _dev_ptr(c), rm, k,
-                           mini_batch, eps, beta, _dev_ptr(ids), _dev_ptr(d), _dev_ptr(vis), _stream(stream)))
+    with _on(stream):
+        q = _dev(queries, torch.float32, "queries", (None, None))
+        nq, dim = q.shape
+        b = _dev(base, torch.float32, "base", (None, dim))
+        t = _dev(top_ids, torch.int32, "top_ids", (nq, None))
+        c = _dev(top_counts, torch.int32, "top_counts", (nq,))
+        rm = t.shape[1]
+        ids = torch.empty((nq, k), dtype=torch.int32, device="cuda")
+        d = torch.empty((nq, k), dtype=torch.float32, device="cuda")
+        vis = torch.empty(nq, dtype=torch.int32, device="cuda")
+        _check(lib.fgpu_rerank(_dev_ptr(q), nq, dim, _dev_ptr(b), b.shape[0], _dev_ptr(t), _dev_ptr(c), rm, k,
+                               mini_batch, eps, beta, _dev_ptr(ids), _dev_ptr(d), _dev_ptr(vis), _stream()))
     return ids, d, vis
 
 
@@ -472,14 +597,16 @@ def rerank(queries, base, top_ids, top_counts, k: int, mini_batch: int = 128, ep
 def l2_topk(x, c, p: int, stream=None):
     """p nearest rows of c for each row of x by exact device-form L2: (ids, dists)."""
     torch = _torch()
-    x, c = _to_dev(x), _to_dev(c)
-    n, dim = x.shape
-    nc = c.shape[0]
-    ws = _workspace(lib.fgpu_l2_topk_workspace_bytes(n, nc))
-    ids = torch.empty((n, p), dtype=torch.int32, device="cuda")
-    d = torch.empty((n, p), dtype=torch.float32, device="cuda")
-    _check(lib.fgpu_l2_topk(_dev_ptr(x), n, _dev_ptr(c), nc, dim, p, _dev_ptr(ids), _dev_ptr(d), _dev_ptr(ws),
-                            ws.numel(), _stream(stream)))
+    with _on(stream):
+        x = _dev(x, torch.float32, "x", (None, None))
+        n, dim = x.shape
+        c = _dev(c, torch.float32, "c", (None, dim))
+        nc = c.shape[0]
+        ws = _workspace(lib.fgpu_l2_topk_workspace_bytes(n, nc))
+        ids = torch.empty((n, p), dtype=torch.int32, device="cuda")
+        d = torch.empty((n, p), dtype=torch.float32, device="cuda")
+        _check(lib.fgpu_l2_topk(_dev_ptr(x), n, _dev_ptr(c), nc, dim, p, _dev_ptr(ids), _dev_ptr(d), _dev_ptr(ws),
+                                _ws_check(ws), _stream()))
     return ids, d
 
 
@@ -504,14 +631,16 @@ def tune_elbow(hits_per_rank, total_hits: int):
 def knn_exact(queries, base, k: int, workspace=None, stream=None):
     """Exact kNN ground truth (brute_force_search_kernel): (ids int32 [nq][k], dists float32 [nq][k])."""
     torch = _torch()
-    q, b = _to_dev(queries), _to_dev(base)
-    nq, dim = q.shape
-    n = b.shape[0]
-    ws = workspace if workspace is not None else _workspace(lib.fgpu_knn_exact_workspace_bytes(nq, n))
-    ids = torch.empty((nq, k), dtype=torch.int32, device="cuda")
-    d = torch.empty((nq, k), dtype=torch.float32, device="cuda")
-    _check(lib.fgpu_knn_exact(_dev_ptr(q), nq, _dev_ptr(b), n, dim, k, _dev_ptr(ids), _dev_ptr(d), _dev_ptr(ws),
-                              ws.numel(), _stream(stream)))
+    with _on(stream):
+        q = _dev(queries, torch.float32, "queries", (None, None))
+        nq, dim = q.shape
+        b = _dev(base, torch.float32, "base", (None, dim))
+        n = b.shape[0]
+        ws = workspace if workspace is not None else _workspace(lib.fgpu_knn_exact_workspace_bytes(nq, n))
+        ids = torch.empty((nq, k), dtype=torch.int32, device="cuda")
+        d = torch.empty((nq, k), dtype=torch.float32, device="cuda")
+        _check(lib.fgpu_knn_exact(_dev_ptr(q), nq, _dev_ptr(b), n, dim, k, _dev_ptr(ids), _dev_ptr(d), _dev_ptr(ws),
+                                  _ws_check(ws), _stream()))
     return ids, d
 
 
@@ -520,15 +649,17 @@ def graph_search(queries, base, graph, k: int, itopk: int = 64, width: int = 4, 
     """Graph search over a fixed-degree adjacency (the CAGRA role): (ids [nq][k], dists [nq][k], steps [nq])
     plus, with want_evals, the exact distances computed per query."""
     torch = _torch()
-    q, b, g = _to_dev(queries), _to_dev(base), _to_dev(graph)
-    nq, dim = q.shape
-    ids, d = out if out is not None else (torch.empty((nq, k), dtype=torch.int32, device="cuda"),
-                                          torch.empty((nq, k), dtype=torch.float32, device="cuda"))
-    it = torch.empty(nq, dtype=torch.int32, device="cuda")
-    ev = torch.empty(nq, dtype=torch.int32, device="cuda") if want_evals else None
-    _check(lib.fgpu_graph_search(_dev_ptr(q), nq, _dev_ptr(b), b.shape[0], dim, _dev_ptr(g), g.shape[1], itopk,
-                                 width, max_iter, k, seed, _dev_ptr(ids), _dev_ptr(d), _dev_ptr(it),
-                                 _dev_ptr(ev) if want_evals else None, _stream(stream)))
+    with _on(stream):
+        q = _dev(queries, torch.float32, "queries", (None, None))
+        nq, dim = q.shape
+        b = _dev(base, torch.float32, "base", (None, dim))
+        g = _dev(graph, torch.int32, "graph", (b.shape[0], None))
+        ids, d = _outs(out, nq, k)
+        it = torch.empty(nq, dtype=torch.int32, device="cuda")
+        ev = torch.empty(nq, dtype=torch.int32, device="cuda") if want_evals else None
+        _check(lib.fgpu_graph_search(_dev_ptr(q), nq, _dev_ptr(b), b.shape[0], dim, _dev_ptr(g), g.shape[1], itopk,
+                                     width, max_iter, k, seed, _dev_ptr(ids), _dev_ptr(d), _dev_ptr(it), _opt_ptr(ev),
+                                     _stream()))
     return (ids, d, it, ev) if want_evals else (ids, d, it)
 
 
@@ -539,45 +670,60 @@ def fixed_shift(maxabs: float, n: int) -> int:
 def kmeans_update(x, assign, centroids, shift: int, empty_rule: int = 0, stream=None):
     """One deterministic Lloyd update in place on `centroids` (device); returns counts."""
     torch = _torch()
-    x, a = _to_dev(x), _to_dev(assign)
-    n, dim = x.shape
-    k = centroids.shape[0]
-    ws = _workspace(lib.fgpu_kmeans_workspace_bytes(k, dim))
-    counts = torch.empty(k, dtype=torch.int32, device="cuda")
-    _check(lib.fgpu_kmeans_update(_dev_ptr(x), n, _dev_ptr(a), k, dim, shift, empty_rule, _dev_ptr(centroids),
-                                  _dev_ptr(counts), _dev_ptr(ws), ws.numel(), _stream(stream)))
+    with _on(stream):
+        x = _dev(x, torch.float32, "x", (None, None))
+        n, dim = x.shape
+        a = _dev(assign, torch.int32, "assign", (n,))
+        k = centroids.shape[0]
+        _out(centroids, torch.float32, (k, dim), "centroids")
+        ws = _workspace(lib.fgpu_kmeans_workspace_bytes(k, dim))
+        counts = torch.empty(k, dtype=torch.int32, device="cuda")
+        _check(lib.fgpu_kmeans_update(_dev_ptr(x), n, _dev_ptr(a), k, dim, shift, empty_rule, _dev_ptr(centroids),
+                                      _dev_ptr(counts), _dev_ptr(ws), _ws_check(ws), _stream()))
     return counts
 
 
 def kmeans_fit(x, k: int, iters: int, init_mode: int = 0, seed: int = 42, want_assign: bool = True, stream=None):
     torch = _torch()
-    x = _to_dev(x)
-    n, dim = x.shape
-    cent = torch.empty((k, dim), dtype=torch.float32, device="cuda")
-    assign = torch.empty(n, dtype=torch.int32, device="cuda") if want_assign else None
-    _check(lib.fgpu_kmeans_fit(_dev_ptr(x), n, dim, k, iters, init_mode, seed, _dev_ptr(cent),
-                               _dev_ptr(assign) if want_assign else None, _stream(stream)))
+    with _on(stream):
+        x = _dev(x, torch.float32, "x", (None, None))
+        n, dim = x.shape
+        cent = torch.empty((k, dim), dtype=torch.float32, device="cuda")
+        assign = torch.empty(n, dtype=torch.int32, device="cuda") if want_assign else None
+        _check(lib.fgpu_kmeans_fit(_dev_ptr(x), n, dim, k, iters, init_mode, seed, _dev_ptr(cent), _opt_ptr(assign),
+                                   _stream()))
     return cent, assign
 
 
 def pq_train(x, assign, centroids, pq_m: int, sample_size: int = 50000, iters: int = 8, stream=None):
     torch = _torch()
-    x, a, c = _to_dev(x), _to_dev(assign), _to_dev(centroids)
-    n, dim = x.shape
-    cb = torch.empty((pq_m, 256, dim // pq_m), dtype=torch.float32, device="cuda")
-    _check(lib.fgpu_pq_train(_dev_ptr(x), n, dim, pq_m, _dev_ptr(a), _dev_ptr(c), sample_size, iters,
-                             _dev_ptr(cb), _stream(stream)))
+    with _on(stream):
+        x = _dev(x, torch.float32, "x", (None, None))
+        n, dim = x.shape
+        a = _dev(assign, torch.int32, "assign", (n,))
+        c = _dev(centroids, torch.float32, "centroids", (None, dim))
+        if pq_m < 1 or dim % pq_m:
+            raise ValueError(f"pq_train: dim {dim} is not a multiple of pq_m {pq_m}")
+        cb = torch.empty((pq_m, 256, dim // pq_m), dtype=torch.float32, device="cuda")
+        _check(lib.fgpu_pq_train(_dev_ptr(x), n, dim, pq_m, _dev_ptr(a), _dev_ptr(c), sample_size, iters,
+                                 _dev_ptr(cb), _stream()))
     return cb
 
 
 def pq_encode(x, assign, centroids, codebook, stream=None):
     torch = _torch()
-    x, a, c, cb = _to_dev(x), _to_dev(assign), _to_dev(centroids), _to_dev(codebook)
-    n, dim = x.shape
-    pq_m = cb.shape[0]
-    codes = torch.empty((n, pq_m), dtype=torch.uint8, device="cuda")
-    _check(lib.fgpu_pq_encode(_dev_ptr(x), n, dim, pq_m, _dev_ptr(a), _dev_ptr(c), _dev_ptr(cb), _dev_ptr(codes),
-                              _stream(stream)))
+    with _on(stream):
+        x = _dev(x, torch.float32, "x", (None, None))
+        n, dim = x.shape
+        a = _dev(assign, torch.int32, "assign", (n,))
+        c = _dev(centroids, torch.float32, "centroids", (None, dim))
+        cb = _dev(codebook, torch.float32, "codebook", (None, 256, None))
+        pq_m = cb.shape[0]
+        if pq_m * cb.shape[2] != dim:
+            raise ValueError(f"pq_encode: codebook {tuple(cb.shape)} does not cover dim {dim}")
+        codes = torch.empty((n, pq_m), dtype=torch.uint8, device="cuda")
+        _check(lib.fgpu_pq_encode(_dev_ptr(x), n, dim, pq_m, _dev_ptr(a), _dev_ptr(c), _dev_ptr(cb), _dev_ptr(codes),
+                                  _stream()))
     return codes
 
 
@@ -585,14 +731,17 @@ def build_ivfpq(x, nlist: int, pq_m: int, kmeans_iters: int = 20, init_mode: int
                 pq_iters: int = 8, sample_size: int = 50000, train_rows: int = 0, stream=None):
     """build_global without rebalancing: host arrays (offsets, ids, codes, centroids, codebook).
     train_rows > 0 trains the k-means on the systematic sample of that many rows."""
-    x = _to_dev(x)
-    n, dim = x.shape
-    offs = np.empty(nlist + 1, np.int32)
-    ids = np.empty(n, np.int32)
-    codes = np.empty((n, pq_m), np.uint8)
-    cent = np.empty((nlist, dim), np.float32)
-    cb = np.empty((pq_m, 256, dim // pq_m), np.float32)
-    _check(lib.fgpu_build_ivfpq_sampled(_dev_ptr(x), n, dim, nlist, pq_m, train_rows, kmeans_iters, init_mode, seed,
-                                        pq_iters, sample_size, _np_ptr(offs), _np_ptr(ids), _np_ptr(codes),
-                                        _np_ptr(cent), _np_ptr(cb), _stream(stream)))
+    with _on(stream):
+        x = _dev(x, _torch().float32, "x", (None, None))
+        n, dim = x.shape
+        if pq_m < 1 or dim % pq_m:
+            raise ValueError(f"build_ivfpq: dim {dim} is not a multiple of pq_m {pq_m}")
+        offs = np.empty(nlist + 1, np.int32)
+        ids = np.empty(n, np.int32)
+        codes = np.empty((n, pq_m), np.uint8)
+        cent = np.empty((nlist, dim), np.float32)
+        cb = np.empty((pq_m, 256, dim // pq_m), np.float32)
+        _check(lib.fgpu_build_ivfpq_sampled(_dev_ptr(x), n, dim, nlist, pq_m, train_rows, kmeans_iters, init_mode,
+                                            seed, pq_iters, sample_size, _np_ptr(offs), _np_ptr(ids), _np_ptr(codes),
+                                            _np_ptr(cent), _np_ptr(cb), _stream()))
     return offs, ids, codes, cent, cb

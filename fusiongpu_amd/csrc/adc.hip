@@ -103,22 +103,44 @@ __device__ __forceinline__ void scan_round_full(const float* smem, int v0, int n
 }
 
 // Workgroup-local hand-off through LDS counters.  The waits are bounded: a
-// wave that spins kSpinLimit times gives up and carries on, so every wave
-// reaches the end of the kernel whatever the counters say (with correct
-// counting the longest legitimate wait is the scan of one list, microseconds).
+// wave that has polled `limit` times gives up and carries on, so every wave
+// reaches the end of the kernel whatever the counters say.  The limit
+// (flow_spin_limit) is far above the longest legitimate wait, the scan of
+// every probed list of a query.  A give-up is never silent: the wave adds 1 to
+// the device counter a.faults and sets the workgroup's LDS flag, and every
+// query whose top-k the workgroup writes after that gets kFaultId / NaN in all
+// its slots.  Queries written before the flag was set were complete, so no
+// later give-up can have touched them.
 // Each poll is an LDS read and a few VALU instructions taken from the waves
 // that do the work, so waits off the critical path (builders waiting for
 // scanners) poll kLazySleep times less often: s_sleep N idles about 64 N
 // clocks.
-constexpr int kSpinLimit = 1 << 16;
 constexpr int kLazySleep = 8;
 
+struct WaitCtl {
+  int limit;                   // polls of s_sleep 1 before a give-up
+  int* flag;                   // the workgroup's LDS give-up flag
+  unsigned long long* faults;  // device give-up counter
+};
+
+__device__ __forceinline__ void note_give_up(const WaitCtl& w) {
+  if ((threadIdx.x & 63) == 0) {
+    __hip_atomic_store(w.flag, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    atomicAdd(w.faults, 1ull);
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+}
+
 template <int SLEEP = 1>
-__device__ __forceinline__ void lds_wait_at_least(const int* p, int target) {
+__device__ __forceinline__ void lds_wait_at_least(const int* p, int target, const WaitCtl& w) {
   int spins = 0;
-  while (__hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < target &&
-         ++spins < kSpinLimit / SLEEP)
+  while (__hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < target) {
+    if (++spins >= w.limit / SLEEP) {
+      note_give_up(w);
+      break;
+    }
     __builtin_amdgcn_s_sleep(SLEEP);
+  }
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
 }
 
@@ -128,14 +150,15 @@ __device__ __forceinline__ void lds_signal_add(int* p, int v) {
   if ((threadIdx.x & 63) == 0) __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
 
-// Write the k best of a sorted wave list (padding as id -1, distance FLT_MAX).
-__device__ __forceinline__ void write_topk(uint64_t lk, int q, int k, const AdcArgs& a) {
+// Write the k best of a sorted wave list (padding as id -1, distance FLT_MAX;
+// with `fault`, every slot kFaultId / NaN).
+__device__ __forceinline__ void write_topk(uint64_t lk, int q, int k, const AdcArgs& a, bool fault = false) {
   const int lane = threadIdx.x & 63;
   if (lane < k) {
     const int id = key_id(lk);
     const bool pad = id == kPadId;
-    a.out_ids[(size_t)q * k + lane] = pad ? -1 : id;
-    a.out_d[(size_t)q * k + lane] = pad ? FLT_MAX : key_dist(lk);
+    a.out_ids[(size_t)q * k + lane] = fault ? kFaultId : pad ? -1 : id;
+    a.out_d[(size_t)q * k + lane] = fault ? __builtin_nanf("") : pad ? FLT_MAX : key_dist(lk);
   }
 }
 
@@ -297,11 +320,15 @@ constexpr int kUndecided = -1;
 constexpr int kSkipped = -2;
 
 template <int SLEEP = 1>
-__device__ __forceinline__ int lds_wait_decided(const int* p) {
+__device__ __forceinline__ int lds_wait_decided(const int* p, const WaitCtl& w) {
   int spins = 0, v;
-  while ((v = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)) == kUndecided &&
-         ++spins < kSpinLimit / SLEEP)
+  while ((v = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)) == kUndecided) {
+    if (++spins >= w.limit / SLEEP) {
+      note_give_up(w);
+      break;
+    }
     __builtin_amdgcn_s_sleep(SLEEP);
+  }
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
   return v;
 }
@@ -344,6 +371,7 @@ __global__ __launch_bounds__(kSpecWaves * kWave, 4) void adc_flow_kernel(AdcArgs
   __shared__ int s_arr[2][kScanWaves - 1];  // arrivals per tree node
   __shared__ int s_ready[2], s_free[2], s_lbdone[2];
   __shared__ int s_built[kLutBufs], s_done[kLutBufs];  // per LUT buffer
+  __shared__ int s_fault;                               // a wave of this workgroup gave up a wait
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const bool builder = wave < kBuilderWaves;
   const long long t_start = a.stats ? clock64() : 0;
@@ -362,6 +390,9 @@ __global__ __launch_bounds__(kSpecWaves * kWave, 4) void adc_flow_kernel(AdcArgs
     s_built[tid] = 0;
     s_done[tid] = 0;
   }
+  if (tid == 0) s_fault = 0;
+  const WaitCtl wc{a.spin_limit, &s_fault, a.faults};
+  const int total = (int)a.total;
   __syncthreads();
 
   // Builder codebook registers: loaded first, so the loads overlap the set-up.
@@ -396,7 +427,7 @@ __global__ __launch_bounds__(kSpecWaves * kWave, 4) void adc_flow_kernel(AdcArgs
     // Set-up of this workgroup's query i into slot i & 1 (all builder waves).
     auto setup = [&](int i) {
       const int s = i & 1, q = (int)blockIdx.x + i * G;
-      lds_wait_at_least<kLazySleep>(&s_free[s], i / 2);  // the slot's previous query is written out
+      lds_wait_at_least<kLazySleep>(&s_free[s], i / 2, wc);  // the slot's previous query is written out
       const uint32_t* pr = a.probes + (size_t)q * P;
       const uint32_t pl_lane = lane < P ? pr[lane] : kPruned;
       // With the coarse distances at hand, wave 0 bounds every list from them
@@ -455,7 +486,7 @@ __global__ __launch_bounds__(kSpecWaves * kWave, 4) void adc_flow_kernel(AdcArgs
         // Every builder wave has signalled this set-up, so each has left the
         // loop of query i - 1 and of query i - 2, the slot's previous user:
         // no wave reads its decisions any more.
-        lds_wait_at_least<kLazySleep>(&s_lbdone[s], kBuilderWaves * (i / 2 + 1));
+        lds_wait_at_least<kLazySleep>(&s_lbdone[s], kBuilderWaves * (i / 2 + 1), wc);
         s_dec[s][lane] = kUndecided;
         if (valid) {
           f_list[s][pos] = (int)pl_lane;
@@ -482,7 +513,7 @@ __global__ __launch_bounds__(kSpecWaves * kWave, 4) void adc_flow_kernel(AdcArgs
     if (nqw > 0) setup(0);
     for (int i = 0; i < nqw; ++i) {
       const int s = i & 1, q = (int)blockIdx.x + i * G;
-      lds_wait_at_least(&s_ready[s], i / 2 + 1);
+      lds_wait_at_least(&s_ready[s], i / 2 + 1, wc);
       const int nv = s_nv[s];
       const float qv = lane < RW ? a.queries[(size_t)q * D + wave * RW + lane] : 0.0f;
       // This wave's centroid coordinates of the next list that may be built,
@@ -513,7 +544,7 @@ __global__ __launch_bounds__(kSpecWaves * kWave, 4) void adc_flow_kernel(AdcArgs
             nskip += min(p, nv - f);
           }
         } else {
-          dec = lds_wait_decided<kLazySleep>(&s_dec[s][f]);
+          dec = lds_wait_decided<kLazySleep>(&s_dec[s][f], wc);
         }
         if (dec < 0) {
           f = next_list(s, nv, f + 1, any_list);
@@ -534,7 +565,7 @@ __global__ __launch_bounds__(kSpecWaves * kWave, 4) void adc_flow_kernel(AdcArgs
         float r[C::S];
 #pragma unroll
         for (int d = 0; d < C::S; ++d) r[d] = rw[(lane / TPM) * C::S + d];
-        lds_wait_at_least<kLazySleep>(&s_done[b], b == 0 ? need0 : b == 1 ? need1 : need2);
+        lds_wait_at_least<kLazySleep>(&s_done[b], b == 0 ? need0 : b == 1 ? need1 : need2, wc);
         float* lut = smem + b * C::LUT + ms * kPQK + 4 * t;
 #pragma unroll
         for (int u = 0; u < E / 4; ++u) {
@@ -580,7 +611,7 @@ __global__ __launch_bounds__(kSpecWaves * kWave, 4) void adc_flow_kernel(AdcArgs
     unsigned nload = 0;  // vectors whose codes this wave loaded
     for (int i = 0; i < nqw; ++i) {
       const int s = i & 1, q = (int)blockIdx.x + i * G;
-      lds_wait_at_least(&s_ready[s], i / 2 + 1);
+      lds_wait_at_least(&s_ready[s], i / 2 + 1, wc);
       const int nv = s_nv[s];
       const int* cst = f_cst[s];
       uint64_t lk = kPadKey, own = kNoThr;
@@ -601,15 +632,18 @@ __global__ __launch_bounds__(kSpecWaves * kWave, 4) void adc_flow_kernel(AdcArgs
         if (!bm) break;
         f = __ffsll((unsigned long long)bm) - 1;
         int dec = __builtin_amdgcn_readlane(dec_l, f);
-        if (dec == kUndecided) dec = lds_wait_decided(&s_dec[s][f]);
+        if (dec == kUndecided) dec = lds_wait_decided(&s_dec[s][f], wc);
         if (dec < 0) continue;
-        const int start = __builtin_amdgcn_readlane(st_l, f), n = __builtin_amdgcn_readlane(n_l, f);
+        // A list range as the set-up wrote it lies inside the index; the clamp
+        // keeps the loads inside it even after a give-up.
+        const int start = __builtin_amdgcn_readlane(st_l, f);
+        const int n = min(__builtin_amdgcn_readlane(n_l, f), total - start);
         const int c0 = __builtin_amdgcn_readlane(cst_l, f), c_end = __builtin_amdgcn_readlane(cst_n, f);
         int c = first_own(c0);
         load_pair<M>(a.codes, a.vec_ids, start, n, (c - c0) * kChunk + lane, w0, w1, i0, i1);
         nload += (unsigned)min(kChunk, n - (c - c0) * kChunk);
         const int b = dec % kLutBufs;
-        lds_wait_at_least(&s_built[b], kBuilderWaves * (dec / kLutBufs + 1));
+        lds_wait_at_least(&s_built[b], kBuilderWaves * (dec / kLutBufs + 1), wc);
         int mine = 0;
         while (true) {
           const uint64_t shared_thr = s_thr[s];
@@ -654,7 +688,7 @@ __global__ __launch_bounds__(kSpecWaves * kWave, 4) void adc_flow_kernel(AdcArgs
         wave_merge_lds64(lk, s_tree[s][nd][ch ^ 1]);
       }
       if (root) {
-        write_topk(lk, q, k, a);
+        write_topk(lk, q, k, a, __hip_atomic_load(&s_fault, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) != 0);
         lds_signal_add(&s_free[s], 1);
         if (a.stats && lane == 0 && i == nqw - 1) atomicAdd(&a.stats[6], (unsigned long long)(clock64() - t_start));
       }
@@ -683,8 +717,11 @@ int resident_groups(K kernel, int threads, std::atomic<int> (&cached)[64]) {
 }
 
 template <int D, int M>
-fgpu_status launch_flow(const AdcArgs& a, hipStream_t s) {
-  FGPU_CHECK(a.nprobe <= 64, FGPU_ERR_UNSUPPORTED, "adc: nprobe must be <= 64");
+fgpu_status launch_flow(const AdcArgs& args, hipStream_t s) {
+  FGPU_CHECK(args.nprobe <= 64, FGPU_ERR_UNSUPPORTED, "adc: nprobe must be <= 64");
+  FGPU_CHECK(args.faults, FGPU_ERR_ARG, "adc: the flow kernel needs a device give-up counter");
+  AdcArgs a = args;
+  if (a.spin_limit <= 0) a.spin_limit = (int)flow_spin_limit(a.nprobe, a.max_list_len);
   static std::atomic<int> cached[64];
   const int grid = std::min(a.nq, resident_groups(adc_flow_kernel<D, M>, kSpecWaves * kWave, cached));
   hipLaunchKernelGGL((adc_flow_kernel<D, M>), dim3((unsigned)grid), dim3(kSpecWaves * kWave), 0, s, a);
@@ -700,6 +737,15 @@ fgpu_status launch_plain(const AdcArgs& a, hipStream_t s) {
 }
 
 }  // namespace
+
+long long flow_spin_limit(int nprobe, int max_list_len) {
+  // Longest legitimate wait: a builder setting up query i + 1 waits for query
+  // i - 1 to be written, i.e. for up to nprobe lists of max_list_len vectors
+  // to be scanned.  At 32 clocks a vector and >= 64 clocks a poll that is
+  // nprobe * max_list_len / 2 polls; the limit allows 4x that, plus 2^16.
+  const long long v = (1ll << 16) + 2ll * (long long)std::max(nprobe, 1) * (long long)std::max(max_list_len, 0);
+  return std::min<long long>(v, 1ll << 30);
+}
 
 bool adc_supported(int dim, int m) {
   return (dim == 128 && (m == 16 || m == 32 || m == 64)) || (dim == 96 && (m == 16 || m == 32 || m == 48));

@@ -1,6 +1,7 @@
 // capi.cpp -- the extern "C" boundary (include/fusiongpu.h): index handle,
 // search and build orchestration, file formats and the synthetic generator.
 #include <algorithm>
+#include <atomic>
 #include <cmath>
 #include <cstdio>
 #include <cstring>
@@ -25,6 +26,7 @@ struct fgpu_index {
   float* d_cnorm = nullptr;      // [nlist] ||c||^2
   float* d_cnorm_max = nullptr;  // [1]
   float* d_rmax = nullptr;       // [nlist] decoded-residual radius per list
+  unsigned long long* d_faults = nullptr;  // [1] bounded-wait give-ups of the flow scan
 };
 
 namespace fgpu {
@@ -60,9 +62,25 @@ void free_index(fgpu_index* ix) {
   if (!ix) return;
   for (void* p : {(void*)ix->d_codebook, (void*)ix->d_offsets, (void*)ix->d_codes, (void*)ix->d_ids,
                   (void*)ix->d_centroids, (void*)ix->d_cnorm, (void*)ix->d_cnorm_max,
-                  (void*)ix->d_rmax})
+                  (void*)ix->d_rmax, (void*)ix->d_faults})
     if (p) (void)hipFree(p);
   delete ix;
+}
+
+// Poll limit of the flow kernel's bounded waits set by fgpu_debug_set_spin_limit
+// (0 = derived per launch from nprobe and the longest list).
+std::atomic<int> g_spin_override{0};
+
+AdcArgs adc_args(const fgpu_index* ix, const float* dq, int nq, const uint32_t* probes, const float* probe_dists,
+                 int nprobe, int k, int32_t* out_ids, float* out_d) {
+  AdcArgs a{dq, ix->d_centroids, ix->d_codebook, ix->d_offsets, ix->d_codes, ix->d_ids, probes, ix->d_rmax,
+            nq, nprobe, k, ix->nlist, out_ids, out_d};
+  a.probe_dists = probe_dists;
+  a.total = ix->total;
+  a.faults = ix->d_faults;
+  a.max_list_len = ix->max_list_len;
+  a.spin_limit = g_spin_override.load(std::memory_order_relaxed);
+  return a;
 }
 
 int64_t topk_batch_rows(int64_t n, int nc) {
@@ -119,7 +137,7 @@ fgpu_status fgpu_index_create(int dim, int pq_m, int nlist, int64_t total, const
       !alloc((void**)&ix->d_codes, (size_t)total * pq_m + 256) || !alloc((void**)&ix->d_ids, sizeof(int32_t) * total) ||
       !alloc((void**)&ix->d_centroids, sizeof(float) * (size_t)nlist * dim) ||
       !alloc((void**)&ix->d_cnorm, sizeof(float) * nlist) || !alloc((void**)&ix->d_cnorm_max, 256) ||
-      !alloc((void**)&ix->d_rmax, sizeof(float) * nlist)) {
+      !alloc((void**)&ix->d_rmax, sizeof(float) * nlist) || !alloc((void**)&ix->d_faults, 256)) {
     (void)hipGetLastError();
     return fail(set_error(FGPU_ERR_NOMEM, "index_create: device allocation failed"));
   }
@@ -127,7 +145,8 @@ fgpu_status fgpu_index_create(int dim, int pq_m, int nlist, int64_t total, const
       hipMemcpy(ix->d_offsets, h_offsets, sizeof(int32_t) * (nlist + 1), hipMemcpyHostToDevice) != hipSuccess ||
       (total && hipMemcpy(ix->d_codes, h_codes, (size_t)total * pq_m, hipMemcpyHostToDevice) != hipSuccess) ||
       (total && hipMemcpy(ix->d_ids, h_ids, sizeof(int32_t) * total, hipMemcpyHostToDevice) != hipSuccess) ||
-      hipMemcpy(ix->d_centroids, h_centroids, sizeof(float) * (size_t)nlist * dim, hipMemcpyHostToDevice) != hipSuccess)
+      hipMemcpy(ix->d_centroids, h_centroids, sizeof(float) * (size_t)nlist * dim, hipMemcpyHostToDevice) != hipSuccess ||
+      hipMemset(ix->d_faults, 0, 256) != hipSuccess)
     return fail(set_error(FGPU_ERR_HIP, "index_create: copy to device failed"));
   fgpu_status st = launch_row_norms(ix->d_centroids, nlist, dim, ix->d_cnorm, nullptr);
   if (st == FGPU_OK) st = launch_max_reduce(ix->d_cnorm, nlist, ix->d_cnorm_max, nullptr);
@@ -216,9 +235,7 @@ fgpu_status fgpu_adc_search(const fgpu_index* ix, const float* dq, int nq, const
   FGPU_CHECK(ix && dq && d_probe_ids && d_out_ids && d_out_dists, FGPU_ERR_ARG, "adc_search: null argument");
   FGPU_CHECK(nq >= 0 && nprobe >= 1 && k >= 1, FGPU_ERR_ARG, "adc_search: bad sizes");
   FGPU_CHECK(adc_supported(ix->dim, ix->m), FGPU_ERR_UNSUPPORTED, "adc_search: no kernel for this (dim, pq_m)");
-  AdcArgs a{dq, ix->d_centroids, ix->d_codebook, ix->d_offsets, ix->d_codes, ix->d_ids, d_probe_ids, ix->d_rmax,
-            nq, nprobe, k, ix->nlist, d_out_ids, d_out_dists};
-  a.probe_dists = d_probe_dists;
+  AdcArgs a = adc_args(ix, dq, nq, d_probe_ids, d_probe_dists, nprobe, k, d_out_ids, d_out_dists);
   return launch_adc_plain(ix->dim, ix->m, a, as_stream(stream));
 }
 
@@ -229,12 +246,31 @@ fgpu_status fgpu_adc_search_stats(const fgpu_index* ix, const float* dq, int nq,
              "adc_search_stats: null argument");
   FGPU_CHECK(nq >= 0 && nprobe >= 1 && k >= 1, FGPU_ERR_ARG, "adc_search_stats: bad sizes");
   FGPU_CHECK(adc_supported(ix->dim, ix->m), FGPU_ERR_UNSUPPORTED, "adc_search_stats: no kernel for this (dim, pq_m)");
-  AdcArgs a{dq, ix->d_centroids, ix->d_codebook, ix->d_offsets, ix->d_codes, ix->d_ids, d_probe_ids, ix->d_rmax,
-            nq, nprobe, k, ix->nlist, d_out_ids, d_out_dists};
-  a.probe_dists = d_probe_dists;
+  AdcArgs a = adc_args(ix, dq, nq, d_probe_ids, d_probe_dists, nprobe, k, d_out_ids, d_out_dists);
   a.stats = d_stats;
   return launch_adc_plain(ix->dim, ix->m, a, as_stream(stream));
 }
+
+fgpu_status fgpu_index_faults(const fgpu_index* ix, void* stream, unsigned long long* count, int reset) {
+  FGPU_CHECK(ix && count, FGPU_ERR_ARG, "index_faults: null argument");
+  hipStream_t s = as_stream(stream);
+  unsigned long long v = 0;
+  FGPU_HIP(hipMemcpyAsync(&v, ix->d_faults, sizeof(v), hipMemcpyDeviceToHost, s));
+  if (reset) FGPU_HIP(hipMemsetAsync(ix->d_faults, 0, sizeof(v), s));
+  FGPU_HIP(hipStreamSynchronize(s));
+  *count = v;
+  return FGPU_OK;
+}
+
+fgpu_status fgpu_index_check(const fgpu_index* ix, void* stream) {
+  unsigned long long v = 0;
+  FGPU_TRY(fgpu_index_faults(ix, stream, &v, 0));
+  FGPU_CHECK(v == 0, FGPU_ERR_WAIT,
+             std::to_string(v) + " bounded wait(s) of the scan kernel gave up; the affected queries carry id -2");
+  return FGPU_OK;
+}
+
+void fgpu_debug_set_spin_limit(int polls) { g_spin_override.store(polls > 0 ? polls : 0); }
 
 size_t fgpu_search_workspace_bytes(int nq, int nlist, int nprobe) {
   return carve_bytes<uint32_t>((size_t)nq * nprobe) + carve_bytes<float>((size_t)nq * nprobe) +

@@ -56,7 +56,25 @@ struct AdcArgs {
   // [4] builder wave 0 after set-up, [5] scanner wave 8 after set-up, [6] the
   // whole workgroup (thread 0, start to end).
   unsigned long long* stats = nullptr;
+  // Vectors in the index: list ranges read from LDS are clamped to it, so a
+  // scan stays inside the code and id arrays whatever the hand-off counters say.
+  long long total = 0;
+  // Bounded waits of the flow kernel: polls (of s_sleep 1) before a wave gives
+  // up; 0 = derive from nprobe and the longest list (flow_spin_limit).
+  int spin_limit = 0;
+  // Device counter (required by the flow kernel): every wait that gives up
+  // adds 1, and each query whose top-k is written after a give-up in its
+  // workgroup gets id kFaultId / distance NaN in every slot.
+  unsigned long long* faults = nullptr;
+  int max_list_len = 0;
 };
+// Id written to every slot of a query whose result a bounded-wait give-up may
+// have touched (the reference's padding id is -1; it never writes -2).
+constexpr int kFaultId = -2;
+// Polls a flow-kernel wave makes before it gives up: far above the longest
+// legitimate wait, the scan of every probed list of one query (a scanner CU
+// handles a vector in well under 32 clocks; a poll takes >= 64).
+long long flow_spin_limit(int nprobe, int max_list_len);
 bool adc_supported(int dim, int m);
 // rmax[l] >= max over vectors x of list l of ||decode(x)|| (exact, rounded up).
 fgpu_status launch_list_radius(const float* codebook, int m, int sub, const uint8_t* codes, const int32_t* offsets,

@@ -28,8 +28,14 @@ typedef enum {
   FGPU_ERR_HIP = 3,         /* a HIP runtime call failed */
   FGPU_ERR_IO = 4,          /* missing, short or inconsistent file */
   FGPU_ERR_NOMEM = 5,       /* device or host allocation failed */
-  FGPU_ERR_WORKSPACE = 6    /* workspace smaller than *_workspace_bytes() */
+  FGPU_ERR_WORKSPACE = 6,   /* workspace smaller than *_workspace_bytes() */
+  FGPU_ERR_WAIT = 7         /* a bounded device-side wait gave up (fgpu_index_check) */
 } fgpu_status;
+
+/* Id written in every result slot of a query that a bounded-wait give-up of
+ * the scan kernel may have touched (its distances are NaN).  The reference
+ * pads with -1 and never returns -2. */
+#define FGPU_FAULT_ID (-2)
 
 typedef struct fgpu_index fgpu_index; /* opaque device-resident IVF-PQ index */
 
@@ -63,6 +69,24 @@ fgpu_status fgpu_index_load(const char* ivf_data_path, const char* codebook_path
                             fgpu_index** out);
 void fgpu_index_destroy(fgpu_index* idx);
 fgpu_status fgpu_index_get_info(const fgpu_index* idx, fgpu_index_info* out);
+
+/* The plain scan (fgpu_adc_search, fgpu_search) hands LUT buffers and query
+ * slots between the waves of a workgroup through LDS counters.  Every wait on
+ * them is bounded, far above the longest legitimate wait (the scan of all
+ * probed lists of one query), so a counting error ends in a give-up rather
+ * than a hang.  A give-up is recorded: the index's device counter grows by 1,
+ * and every query whose results the workgroup writes afterwards gets
+ * FGPU_FAULT_ID / NaN in all k slots.  No reference counterpart: the
+ * reference's batch logic (gpu_global.cu:679-874) uses no such hand-offs.
+ * fgpu_index_faults waits for `stream`, then returns the count (and zeroes it
+ * when reset != 0); fgpu_index_check returns FGPU_ERR_WAIT when it is not 0.
+ * A correct run always reads 0. */
+fgpu_status fgpu_index_faults(const fgpu_index* idx, void* stream, unsigned long long* count, int reset);
+fgpu_status fgpu_index_check(const fgpu_index* idx, void* stream);
+/* Test hook: polls before a wait gives up, for every later scan launch in the
+ * process (0 = the automatic limit).  A tiny limit makes give-ups certain
+ * while every wave still runs to the end of the kernel. */
+void fgpu_debug_set_spin_limit(int polls);
 
 /* ---- search: coarse quantizer (A2 + A3) -------------------------------- */
 

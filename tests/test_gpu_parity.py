@@ -115,6 +115,7 @@ def test_adc_search_bit_exact(dim, m, k):
         assert bad.size == 0, f"first mismatching queries {bad[:5]}: gpu {gid[bad[0]]} oracle {oid[bad[0]]}"
         assert np.array_equal(_bits(gd), _bits(od))
         assert np.all(gid[6] == -1)
+    assert idx.faults() == 0
     idx.close()
 
 
@@ -144,6 +145,7 @@ def test_adc_search_many_queries_per_workgroup(dim, m, k):
         assert bad.size == 0, f"first mismatching queries {bad[:5]}: gpu {gid[bad[0]]} oracle {oid[bad[0]]}"
         assert np.array_equal(_bits(gd), _bits(od))
         assert np.all(gid[300:303] == -1)
+    assert idx.faults() == 0
     idx.close()
 
 
@@ -167,6 +169,7 @@ def test_search_fused_equals_stages():
     ocnt = oracle.probe_counts(oprobe, offs)
     assert np.array_equal(_host(cnt), ocnt)
     assert np.array_equal(_host(off), np.concatenate([[0], np.cumsum(ocnt)]).astype(np.int32))
+    assert idx.faults() == 0
     idx.close()
 
 
@@ -252,4 +255,26 @@ def test_config1_end_to_end_bit_exact():
     oid, od = oracle.search_plain(q, cent, cb, offs, ids, codes, probes, 10)
     assert np.array_equal(_host(gid), oid)
     assert np.array_equal(_bits(_host(gd)), _bits(od))
+    idx.close()
+
+
+def test_search_on_a_side_stream():
+    """stream= runs the whole call (conversions, workspace, outputs, kernels) on
+    that stream; results equal the default stream's."""
+    _say("search on a side stream")
+    rng = np.random.default_rng(23)
+    offs, ids, lc, cent, cb = _random_index(rng, 20000, 128, 32, 128)
+    q = rng.standard_normal((700, 128)).astype(np.float32) * 0.7
+    idx = fg.Index.from_arrays(128, 32, offs, ids, lc, cent, cb)
+    ref_id, ref_d = idx.search(torch.from_numpy(q).cuda(), 16, 10)
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    for _ in range(3):  # freed internal buffers are reused on the same stream only
+        gid, gd = idx.search(q, 16, 10, stream=s)
+        pid, pdist = idx.coarse_search(q, 16, stream=s)
+        aid, ad = idx.adc_search(q, pid, 10, probe_dists=pdist, stream=s)
+    s.synchronize()
+    assert torch.equal(gid, ref_id) and torch.equal(gd, ref_d)
+    assert torch.equal(aid, ref_id) and torch.equal(ad, ref_d)
+    assert idx.faults(stream=s) == 0
     idx.close()
