@@ -63,6 +63,9 @@ _SIGS = {
     "fgpu_adc_search_stats": (_i32, [_vp, _vp, _i32, _vp, _vp, _i32, _i32, _vp, _vp, _vp, _vp]),
     "fgpu_search_workspace_bytes": (_sz, [_i32, _i32, _i32]),
     "fgpu_search": (_i32, [_vp, _vp, _i32, _i32, _i32, _f32, _vp, _vp, _vp, _sz, _vp]),
+    "fgpu_search_noalloc_max_bytes": (_sz, []),
+    "fgpu_search_noalloc_max_rows": (_i32, [_i32, _i32]),
+    "fgpu_search_noalloc": (_i32, [_vp, _vp, _i32, _i32, _i32, _f32, _vp, _vp, _vp]),
     "fgpu_two_phase_workspace_bytes": (_sz, [_i32, _i32, _i32, _i32, _i32]),
     "fgpu_two_phase_search": (_i32, [_vp, _vp, _i32, _vp, _i32, _i32, _i32, _f32, _i32, _vp, _vp, _vp, _vp, _vp,
                                      _vp, _sz, _vp]),
@@ -536,6 +539,18 @@ class Index:
             ids, d = _outs(out, nq, k)
             _check(lib.fgpu_search(self._h, _dev_ptr(q), nq, nprobe, k, prune_ratio, _dev_ptr(ids), _dev_ptr(d),
                                    _dev_ptr(ws), _ws_check(ws), _stream()))
+        return ids, d
+
+    def search_noalloc(self, queries, nprobe: int, k: int, prune_ratio: float = 100.0, out=None, stream=None):
+        """fgpu_search without a workspace (fgpu_search_noalloc): its scratch is the library's fixed per-GPU
+        device array, so the call itself allocates nothing; with out= and device queries of the right dtype
+        neither does this method.  Calls overlapping on one GPU race on that array."""
+        with _on(stream):
+            q = self._queries(queries)
+            nq = q.shape[0]
+            ids, d = _outs(out, nq, k)
+            _check(lib.fgpu_search_noalloc(self._h, _dev_ptr(q), nq, nprobe, k, prune_ratio, _dev_ptr(ids),
+                                           _dev_ptr(d), _stream()))
         return ids, d
 
     def tune_list_stats(self, queries, pair_query, pair_list, pair_target=None, pair_kth=None, base=None,

@@ -137,6 +137,26 @@ fgpu_status fgpu_search(const fgpu_index* idx, const float* d_queries, int nq, i
                         float prune_ratio, int32_t* d_out_ids, float* d_out_dists,
                         void* d_workspace, size_t workspace_bytes, void* stream);
 
+/* ---- search without allocation ----------------------------------------- */
+
+/* No counterpart in the reference.  For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): fgpu_search with its scratch (probe ids and distances,
+ * query norms, the coarse estimate tile) in a file-scope device array of
+ * FGPU_NOALLOC_SCRATCH_BYTES that each GPU the library runs on holds until the
+ * process ends, instead of a caller workspace.  Queries run in chunks of
+ * fgpu_search_noalloc_max_rows(nlist, nprobe) rows; results equal
+ * fgpu_search's.  FGPU_ERR_WORKSPACE when not even 64 rows fit (nlist above
+ * about 120k at nprobe 32).  No hipMalloc, hipFree or allocating library call.
+ * Every call on one GPU shares that GPU's array: calls that overlap on one GPU
+ * (other streams, other host threads) race and must be serialised by the
+ * caller. */
+#define FGPU_NOALLOC_SCRATCH_BYTES (32u << 20)
+size_t fgpu_search_noalloc_max_bytes(void);
+int fgpu_search_noalloc_max_rows(int nlist, int nprobe);
+fgpu_status fgpu_search_noalloc(const fgpu_index* idx, const float* d_queries, int nq, int nprobe, int k,
+                                float prune_ratio, int32_t* d_out_ids, float* d_out_dists, void* stream);
+
 /* ---- search: two-phase pruned scan + top-rerank_m (A6-A10) ------------- */
 
 /* The general form of run_gpu_batch_logic (gpu_global.cu:679-874) after the
