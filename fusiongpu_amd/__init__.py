@@ -33,7 +33,7 @@ __all__ = [
     "FgpuError", "lib", "lib_path", "Index", "gen_gmm", "l2_topk", "kmeans_fit", "kmeans_update",
     "fixed_shift", "pq_train", "pq_encode", "build_ivfpq", "write_ivf_data", "read_ivf_data",
     "write_fvecs", "read_fvecs", "read_ivecs", "probe_counts", "rerank", "knn_exact", "graph_search",
-    "debug_set_spin_limit", "FAULT_ID",
+    "debug_set_spin_limit", "FAULT_ID", "prune_probes",
 ]
 
 lib_path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib", "libfusiongpu.so")
@@ -49,6 +49,7 @@ _SIGS = {
     "fgpu_index_load": (_i32, [_c.c_char_p, _c.c_char_p, _i32, _i32, _c.POINTER(_vp)]),
     "fgpu_index_destroy": (None, [_vp]),
     "fgpu_index_get_info": (_i32, [_vp, _vp]),
+    "fgpu_index_wrap": (_i32, [_i32, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _c.POINTER(_vp)]),
     "fgpu_index_faults": (_i32, [_vp, _vp, _c.POINTER(_c.c_ulonglong), _i32]),
     "fgpu_index_check": (_i32, [_vp, _vp]),
     "fgpu_debug_set_spin_limit": (None, [_i32]),
@@ -58,6 +59,7 @@ _SIGS = {
     "fgpu_coarse_graph_build": (_i32, [_vp, _i32, _vp, _vp, _sz, _vp]),
     "fgpu_coarse_graph_search": (_i32, [_vp, _vp, _i32, _i32, _i32, _vp, _i32, _i32, _i32, _i32, _u64, _f32, _vp,
                                         _vp, _vp]),
+    "fgpu_prune_probes": (_i32, [_vp, _vp, _i32, _i32, _f32, _vp]),
     "fgpu_probe_counts": (_i32, [_vp, _vp, _i32, _i32, _vp, _vp, _vp]),
     "fgpu_adc_search": (_i32, [_vp, _vp, _i32, _vp, _vp, _i32, _i32, _vp, _vp, _vp]),
     "fgpu_adc_search_stats": (_i32, [_vp, _vp, _i32, _vp, _vp, _i32, _i32, _vp, _vp, _vp, _vp]),
@@ -92,6 +94,7 @@ _SIGS = {
     "fgpu_kmeans_fit": (_i32, [_vp, _i64, _i32, _i32, _i32, _i32, _u64, _vp, _vp, _vp]),
     "fgpu_pq_train": (_i32, [_vp, _i64, _i32, _i32, _vp, _vp, _i32, _i32, _vp, _vp]),
     "fgpu_pq_encode": (_i32, [_vp, _i64, _i32, _i32, _vp, _vp, _vp, _vp, _vp]),
+    "fgpu_pq_encode_form": (_i32, [_vp, _i64, _i32, _i32, _vp, _vp, _vp, _i32, _vp, _vp]),
     "fgpu_build_ivfpq": (_i32, [_vp, _i64, _i32, _i32, _i32, _i32, _i32, _u64, _i32, _i32,
                                 _vp, _vp, _vp, _vp, _vp, _vp]),
     "fgpu_build_ivfpq_sampled": (_i32, [_vp, _i64, _i32, _i32, _i32, _i64, _i32, _i32, _u64, _i32, _i32,
@@ -345,6 +348,25 @@ class Index:
         return cls(h.value)
 
     @classmethod
+    def wrap(cls, dim, pq_m, offsets, ids, codes, centroids, codebook, stream=None) -> "Index":
+        """An index over device tensors the caller keeps (fgpu_index_wrap): no copy of the A1 arrays.  The
+        tensors are held by the returned object, so they outlive its handle."""
+        torch = _torch()
+        with _on(stream):
+            offsets = _dev(offsets, torch.int32, "offsets", (None,))
+            nlist = offsets.shape[0] - 1
+            ids = _dev(ids, torch.int32, "ids", (None,))
+            codes = _dev(codes, torch.uint8, "codes", (ids.shape[0], pq_m))
+            centroids = _dev(centroids, torch.float32, "centroids", (nlist, dim))
+            codebook = _dev(codebook, torch.float32, "codebook", (pq_m, 256, dim // max(pq_m, 1)))
+            h = _vp()
+            _check(lib.fgpu_index_wrap(dim, pq_m, nlist, _dev_ptr(offsets), _dev_ptr(ids), _dev_ptr(codes),
+                                       _dev_ptr(centroids), _dev_ptr(codebook), _stream(), _c.byref(h)))
+        ix = cls(h.value)
+        ix._arrays = (offsets, ids, codes, centroids, codebook)
+        return ix
+
+    @classmethod
     def load(cls, ivf_data_path, codebook_path, dim: int, pq_m: int) -> "Index":
         h = _vp()
         _check(lib.fgpu_index_load(str(ivf_data_path).encode(), str(codebook_path).encode(), dim, pq_m,
@@ -578,6 +600,18 @@ class Index:
         return tp, te, pr, er, kp
 
 
+def prune_probes(probe_ids, probe_dists, prune_ratio: float, stream=None):
+    """The reference's prune rule in place on a device int32 probe tensor (fgpu_prune_probes): a probe farther
+    than its query's first distance * prune_ratio becomes 0xFFFFFFFF (-1 as int32)."""
+    torch = _torch()
+    with _on(stream):
+        nq, nprobe = probe_ids.shape
+        _out(probe_ids, torch.int32, (nq, nprobe), "probe_ids")
+        d = _dev(probe_dists, torch.float32, "probe_dists", (nq, nprobe))
+        _check(lib.fgpu_prune_probes(_dev_ptr(probe_ids), _dev_ptr(d), nq, nprobe, prune_ratio, _stream()))
+    return probe_ids
+
+
 def probe_counts(index: Index, probe_ids, stream=None):
     torch = _torch()
     with _on(stream):
@@ -725,7 +759,9 @@ def pq_train(x, assign, centroids, pq_m: int, sample_size: int = 50000, iters: i
     return cb
 
 
-def pq_encode(x, assign, centroids, codebook, stream=None):
+def pq_encode(x, assign, centroids, codebook, fma_mode: int = 1, stream=None):
+    """Residual PQ codes (fgpu_pq_encode_form): fma_mode 1 = the device kernel's fused chain
+    (kmeans_gpu.cuh:403-445), 0 = the host twin's separately rounded form (pq_utils.h:141-175)."""
     torch = _torch()
     with _on(stream):
         x = _dev(x, torch.float32, "x", (None, None))
@@ -737,8 +773,8 @@ def pq_encode(x, assign, centroids, codebook, stream=None):
         if pq_m * cb.shape[2] != dim:
             raise ValueError(f"pq_encode: codebook {tuple(cb.shape)} does not cover dim {dim}")
         codes = torch.empty((n, pq_m), dtype=torch.uint8, device="cuda")
-        _check(lib.fgpu_pq_encode(_dev_ptr(x), n, dim, pq_m, _dev_ptr(a), _dev_ptr(c), _dev_ptr(cb), _dev_ptr(codes),
-                                  _stream()))
+        _check(lib.fgpu_pq_encode_form(_dev_ptr(x), n, dim, pq_m, _dev_ptr(a), _dev_ptr(c), _dev_ptr(cb), int(fma_mode),
+                                       _dev_ptr(codes), _stream()))
     return codes
 
 

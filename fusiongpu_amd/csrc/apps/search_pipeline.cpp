@@ -109,10 +109,6 @@ int main(int argc, char** argv) {
     std::cerr << "Usage: ./search_pipeline <base> <query> [gt] [Options]\n";
     return 1;
   }
-  if (rerank_m > 4096) {
-    std::cerr << "note: rerank_m " << rerank_m << " exceeds this library's 4096; using 4096\n";
-    rerank_m = 4096;
-  }
   if (batch < 1 || streams < 1) { std::cerr << "batch and streams must be >= 1\n"; return 1; }
   const bool graph_coarse = coarse_mode == "graph";
   if (!graph_coarse && coarse_mode != "exact") { std::cerr << "--coarse must be exact or graph\n"; return 1; }

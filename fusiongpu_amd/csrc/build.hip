@@ -116,8 +116,11 @@ __global__ void kmeans_finalize_kernel(const unsigned long long* __restrict__ su
 
 // ---- A16: residual PQ encoding (kmeans_gpu.cuh:403-445) ---------------------------
 // Codebook staged in LDS as [k][m][S] so lanes of one wave (consecutive
-// subspaces, same codeword) read consecutive 16-byte chunks.
-template <int S>
+// subspaces, same codeword) read consecutive 16-byte chunks.  FMA: the device
+// form, dist = fmaf(diff, diff, dist) as nvcc contracts encode_residuals_kernel
+// (kmeans_gpu.cuh:428-433); otherwise the host form of encode_residuals_to_pq
+// (pq_utils.h:160-166, built without FMA): the product and the sum each rounded.
+template <int S, bool FMA>
 __global__ __launch_bounds__(1024) void pq_encode_kernel(const float* __restrict__ x, int64_t n, int dim, int m,
                                                          const int32_t* __restrict__ assign,
                                                          const float* __restrict__ cent,
@@ -146,7 +149,7 @@ __global__ __launch_bounds__(1024) void pq_encode_kernel(const float* __restrict
 #pragma unroll
       for (int j = 0; j < S; ++j) {
         const float df = r[j] - p[j];
-        d = __builtin_fmaf(df, df, d);
+        d = FMA ? __builtin_fmaf(df, df, d) : __fadd_rn(d, __fmul_rn(df, df));
       }
       if (d < best) { best = d; bk = kk; }
     }
@@ -543,21 +546,26 @@ fgpu_status launch_gather_rows(const float* x, int dim, const int32_t* rows, int
 }
 
 fgpu_status launch_pq_encode(const float* x, int64_t n, int dim, int m, const int32_t* assign, const float* cent,
-                             const float* codebook, uint8_t* codes, hipStream_t s) {
+                             const float* codebook, uint8_t* codes, hipStream_t s, int fma_mode) {
   const int S = dim / m;
   const size_t lds = (size_t)kPQK * dim * sizeof(float);
   FGPU_CHECK(lds <= 160 * 1024, FGPU_ERR_UNSUPPORTED, "pq_encode: codebook exceeds LDS");
   if (n <= 0) return FGPU_OK;
   const int64_t pairs = n * m;
   const unsigned grid = (unsigned)std::min<int64_t>((pairs + 1023) / 1024, 256 * 8);
-#define FGPU_ENC(SS)                                                                                          \
-  if (S == SS) {                                                                                              \
-    FGPU_HIP(hipFuncSetAttribute((const void*)pq_encode_kernel<SS>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds)); \
-    hipLaunchKernelGGL(pq_encode_kernel<SS>, dim3(grid), dim3(1024), lds, s, x, n, dim, m, assign, cent, codebook, codes); \
+#define FGPU_ENC(SS, F)                                                                                       \
+  if (S == SS && (fma_mode != 0) == F) {                                                                      \
+    FGPU_HIP(hipFuncSetAttribute((const void*)pq_encode_kernel<SS, F>, hipFuncAttributeMaxDynamicSharedMemorySize, \
+                                 (int)lds));                                                                  \
+    hipLaunchKernelGGL((pq_encode_kernel<SS, F>), dim3(grid), dim3(1024), lds, s, x, n, dim, m, assign, cent, codebook, \
+                       codes);                                                                                \
     FGPU_HIP(hipGetLastError());                                                                              \
     return FGPU_OK;                                                                                           \
   }
-  FGPU_ENC(1) FGPU_ENC(2) FGPU_ENC(3) FGPU_ENC(4) FGPU_ENC(6) FGPU_ENC(8) FGPU_ENC(16)
+  FGPU_ENC(1, true) FGPU_ENC(2, true) FGPU_ENC(3, true) FGPU_ENC(4, true) FGPU_ENC(6, true) FGPU_ENC(8, true)
+  FGPU_ENC(16, true)
+  FGPU_ENC(1, false) FGPU_ENC(2, false) FGPU_ENC(3, false) FGPU_ENC(4, false) FGPU_ENC(6, false) FGPU_ENC(8, false)
+  FGPU_ENC(16, false)
 #undef FGPU_ENC
   return set_error(FGPU_ERR_UNSUPPORTED, "pq_encode: unsupported sub-dimension");
 }

@@ -27,6 +27,7 @@ struct fgpu_index {
   float* d_cnorm_max = nullptr;  // [1]
   float* d_rmax = nullptr;       // [nlist] decoded-residual radius per list
   unsigned long long* d_faults = nullptr;  // [1] bounded-wait give-ups of the flow scan
+  bool borrowed = false;  // the A1 arrays belong to the caller (fgpu_index_wrap)
 };
 
 namespace fgpu {
@@ -60,11 +61,32 @@ struct DevBuf {
 
 void free_index(fgpu_index* ix) {
   if (!ix) return;
-  for (void* p : {(void*)ix->d_codebook, (void*)ix->d_offsets, (void*)ix->d_codes, (void*)ix->d_ids,
-                  (void*)ix->d_centroids, (void*)ix->d_cnorm, (void*)ix->d_cnorm_max,
-                  (void*)ix->d_rmax, (void*)ix->d_faults})
+  if (!ix->borrowed)
+    for (void* p : {(void*)ix->d_codebook, (void*)ix->d_offsets, (void*)ix->d_codes, (void*)ix->d_ids,
+                    (void*)ix->d_centroids})
+      if (p) (void)hipFree(p);
+  for (void* p : {(void*)ix->d_cnorm, (void*)ix->d_cnorm_max, (void*)ix->d_rmax, (void*)ix->d_faults})
     if (p) (void)hipFree(p);
   delete ix;
+}
+
+// The derived arrays of an index whose A1 arrays are on the device: centroid
+// norms, their maximum, the per-list decoded-residual radius and the give-up
+// counter.
+fgpu_status finish_index(fgpu_index* ix, hipStream_t s) {
+  auto alloc = [&](void** p, size_t b) { return hipMalloc(p, b == 0 ? 256 : b) == hipSuccess; };
+  if (!alloc((void**)&ix->d_cnorm, sizeof(float) * ix->nlist) || !alloc((void**)&ix->d_cnorm_max, 256) ||
+      !alloc((void**)&ix->d_rmax, sizeof(float) * ix->nlist) || !alloc((void**)&ix->d_faults, 256)) {
+    (void)hipGetLastError();
+    return set_error(FGPU_ERR_NOMEM, "index: device allocation failed");
+  }
+  FGPU_HIP(hipMemsetAsync(ix->d_faults, 0, 256, s));
+  FGPU_TRY(launch_row_norms(ix->d_centroids, ix->nlist, ix->dim, ix->d_cnorm, s));
+  FGPU_TRY(launch_max_reduce(ix->d_cnorm, ix->nlist, ix->d_cnorm_max, s));
+  FGPU_TRY(launch_list_radius(ix->d_codebook, ix->m, ix->dim / ix->m, ix->d_codes, ix->d_offsets, ix->nlist, ix->d_rmax,
+                              s));
+  FGPU_HIP(hipStreamSynchronize(s));
+  return FGPU_OK;
 }
 
 // Poll limit of the flow kernel's bounded waits set by fgpu_debug_set_spin_limit
@@ -135,9 +157,7 @@ fgpu_status fgpu_index_create(int dim, int pq_m, int nlist, int64_t total, const
   const size_t cb_bytes = (size_t)pq_m * kPQK * (dim / pq_m) * sizeof(float);
   if (!alloc((void**)&ix->d_codebook, cb_bytes) || !alloc((void**)&ix->d_offsets, sizeof(int32_t) * (nlist + 1)) ||
       !alloc((void**)&ix->d_codes, (size_t)total * pq_m + 256) || !alloc((void**)&ix->d_ids, sizeof(int32_t) * total) ||
-      !alloc((void**)&ix->d_centroids, sizeof(float) * (size_t)nlist * dim) ||
-      !alloc((void**)&ix->d_cnorm, sizeof(float) * nlist) || !alloc((void**)&ix->d_cnorm_max, 256) ||
-      !alloc((void**)&ix->d_rmax, sizeof(float) * nlist) || !alloc((void**)&ix->d_faults, 256)) {
+      !alloc((void**)&ix->d_centroids, sizeof(float) * (size_t)nlist * dim)) {
     (void)hipGetLastError();
     return fail(set_error(FGPU_ERR_NOMEM, "index_create: device allocation failed"));
   }
@@ -145,15 +165,47 @@ fgpu_status fgpu_index_create(int dim, int pq_m, int nlist, int64_t total, const
       hipMemcpy(ix->d_offsets, h_offsets, sizeof(int32_t) * (nlist + 1), hipMemcpyHostToDevice) != hipSuccess ||
       (total && hipMemcpy(ix->d_codes, h_codes, (size_t)total * pq_m, hipMemcpyHostToDevice) != hipSuccess) ||
       (total && hipMemcpy(ix->d_ids, h_ids, sizeof(int32_t) * total, hipMemcpyHostToDevice) != hipSuccess) ||
-      hipMemcpy(ix->d_centroids, h_centroids, sizeof(float) * (size_t)nlist * dim, hipMemcpyHostToDevice) != hipSuccess ||
-      hipMemset(ix->d_faults, 0, 256) != hipSuccess)
+      hipMemcpy(ix->d_centroids, h_centroids, sizeof(float) * (size_t)nlist * dim, hipMemcpyHostToDevice) != hipSuccess)
     return fail(set_error(FGPU_ERR_HIP, "index_create: copy to device failed"));
-  fgpu_status st = launch_row_norms(ix->d_centroids, nlist, dim, ix->d_cnorm, nullptr);
-  if (st == FGPU_OK) st = launch_max_reduce(ix->d_cnorm, nlist, ix->d_cnorm_max, nullptr);
-  if (st == FGPU_OK)
-    st = launch_list_radius(ix->d_codebook, pq_m, dim / pq_m, ix->d_codes, ix->d_offsets, nlist, ix->d_rmax, nullptr);
+  const fgpu_status st = finish_index(ix, nullptr);
   if (st != FGPU_OK) return fail(st);
-  if (hipStreamSynchronize(nullptr) != hipSuccess) return fail(set_error(FGPU_ERR_HIP, "index_create: sync failed"));
+  *out = ix;
+  return FGPU_OK;
+}
+
+fgpu_status fgpu_index_wrap(int dim, int pq_m, int nlist, const int32_t* d_offsets, const int32_t* d_ids,
+                            const uint8_t* d_codes, const float* d_centroids, const float* d_codebook, void* stream,
+                            fgpu_index** out) {
+  FGPU_CHECK(out && d_offsets && d_centroids && d_codebook, FGPU_ERR_ARG, "index_wrap: null argument");
+  FGPU_CHECK(dim > 0 && pq_m > 0 && dim % pq_m == 0 && pq_m % 16 == 0 && nlist > 0, FGPU_ERR_ARG,
+             "index_wrap: bad geometry (pq_m must be a multiple of 16)");
+  FGPU_CHECK(((uintptr_t)d_codes & 15) == 0, FGPU_ERR_ARG, "index_wrap: codes must be 16-byte aligned");
+  hipStream_t s = as_stream(stream);
+  std::vector<int32_t> offs(nlist + 1);
+  FGPU_HIP(hipMemcpyAsync(offs.data(), d_offsets, sizeof(int32_t) * (nlist + 1), hipMemcpyDeviceToHost, s));
+  FGPU_HIP(hipStreamSynchronize(s));
+  FGPU_CHECK(offs[0] == 0 && offs[nlist] >= 0 && offs[nlist] < INT32_MAX, FGPU_ERR_ARG,
+             "index_wrap: offsets must start at 0 and end below 2^31");
+  FGPU_CHECK(offs[nlist] == 0 || (d_ids && d_codes), FGPU_ERR_ARG, "index_wrap: null ids/codes");
+  int maxlen = 0;
+  for (int l = 0; l < nlist; ++l) {
+    const int len = offs[l + 1] - offs[l];
+    FGPU_CHECK(len >= 0, FGPU_ERR_ARG, "index_wrap: offsets not monotone");
+    maxlen = std::max(maxlen, len);
+  }
+  fgpu_index* ix = new fgpu_index();
+  ix->dim = dim; ix->m = pq_m; ix->nlist = nlist; ix->total = offs[nlist]; ix->max_list_len = maxlen;
+  ix->borrowed = true;
+  ix->d_codebook = const_cast<float*>(d_codebook);
+  ix->d_offsets = const_cast<int32_t*>(d_offsets);
+  ix->d_codes = const_cast<uint8_t*>(d_codes);
+  ix->d_ids = const_cast<int32_t*>(d_ids);
+  ix->d_centroids = const_cast<float*>(d_centroids);
+  const fgpu_status st = finish_index(ix, s);
+  if (st != FGPU_OK) {
+    free_index(ix);
+    return st;
+  }
   *out = ix;
   return FGPU_OK;
 }
@@ -220,6 +272,14 @@ fgpu_status fgpu_coarse_search(const fgpu_index* ix, const float* dq, int nq, in
                                  reinterpret_cast<int32_t*>(d_ids) + b0 * nprobe, d_dists + b0 * nprobe, s));
   }
   return FGPU_OK;
+}
+
+fgpu_status fgpu_prune_probes(uint32_t* d_probe_ids, const float* d_probe_dists, int nq, int nprobe, float prune_ratio,
+                              void* stream) {
+  FGPU_CHECK(d_probe_ids && d_probe_dists && nq >= 0 && nprobe >= 1, FGPU_ERR_ARG, "prune_probes: bad argument");
+  if (nq == 0) return FGPU_OK;
+  return launch_coarse_prune(reinterpret_cast<int32_t*>(d_probe_ids), d_probe_dists, nq, nprobe, prune_ratio,
+                             as_stream(stream));
 }
 
 fgpu_status fgpu_probe_counts(const fgpu_index* ix, const uint32_t* d_probe_ids, int nq, int nprobe, int32_t* d_counts,
@@ -689,9 +749,15 @@ fgpu_status fgpu_pq_train(const float* dx, int64_t n, int dim, int pq_m, const i
 
 fgpu_status fgpu_pq_encode(const float* dx, int64_t n, int dim, int pq_m, const int32_t* d_assign,
                            const float* d_cent, const float* d_codebook, uint8_t* d_codes, void* stream) {
+  return fgpu_pq_encode_form(dx, n, dim, pq_m, d_assign, d_cent, d_codebook, 1, d_codes, stream);
+}
+
+fgpu_status fgpu_pq_encode_form(const float* dx, int64_t n, int dim, int pq_m, const int32_t* d_assign,
+                                const float* d_cent, const float* d_codebook, int fma_mode, uint8_t* d_codes,
+                                void* stream) {
   FGPU_CHECK(dx && d_assign && d_cent && d_codebook && d_codes && n >= 0 && pq_m >= 1 && dim % pq_m == 0,
              FGPU_ERR_ARG, "pq_encode: bad argument");
-  return launch_pq_encode(dx, n, dim, pq_m, d_assign, d_cent, d_codebook, d_codes, as_stream(stream));
+  return launch_pq_encode(dx, n, dim, pq_m, d_assign, d_cent, d_codebook, d_codes, as_stream(stream), fma_mode);
 }
 
 fgpu_status fgpu_build_ivfpq(const float* dx, int64_t n, int dim, int nlist, int pq_m, int kmeans_iters, int init_mode,

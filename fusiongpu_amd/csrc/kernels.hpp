@@ -95,7 +95,7 @@ struct TwoPhaseArgs {
   int p1;                   // phase-1 probes = min(nprobe, p1_lists)
   int limit_k;              // per-list candidates in phase 1 (<= 64)
   float coeff;              // threshold coefficient
-  int rerank_m;             // candidates kept (<= 4096)
+  int rerank_m;             // candidates kept (<= 2^17)
   uint64_t* pool;           // [nq][pool_cap] candidate keys (workspace)
   int pool_cap;             // >= two_phase_pool_cap(p1, limit_k, rerank_m)
   int32_t* top_ids;         // [nq][rerank_m]
@@ -183,8 +183,10 @@ fgpu_status launch_kmeans_finalize(const unsigned long long* sums, const int32_t
                                    int dim, int shift, int empty_rule, float* cent, hipStream_t s);
 fgpu_status launch_gather_rows(const float* x, int dim, const int32_t* rows, int nrows, float* out,
                                hipStream_t s);
+// fma_mode 1: the device form (fused chain); 0: the host form (separate roundings).
 fgpu_status launch_pq_encode(const float* x, int64_t n, int dim, int m, const int32_t* assign,
-                             const float* cent, const float* codebook, uint8_t* codes, hipStream_t s);
+                             const float* cent, const float* codebook, uint8_t* codes, hipStream_t s,
+                             int fma_mode = 1);
 fgpu_status launch_pq_residuals(const float* x, int dim, const int32_t* rows, int nrows,
                                 const int32_t* assign, const float* cent, float* res, hipStream_t s);
 fgpu_status launch_pq_init(const float* res, int nsample, int dim, int m, const int32_t* init_rows,

@@ -21,7 +21,9 @@
 //     radix-selects the rerank_m best, keeps only those and admits later
 //     candidates only below the rerank_m-th key: exact, bounded memory, no
 //     host round trip;
-//   * at the end a select and an LDS bitonic sort give the top rerank_m.
+//   * at the end a select and LDS bitonic sorts give the top rerank_m: one
+//     sort up to 4096 keys, otherwise sorted runs of 4096 placed by
+//     binary-search ranks against the other runs (rerank_m up to 2^17).
 // The rerank kernel gives each query one 128-thread workgroup: exact
 // distances one candidate per lane, wave bitonic sorts and a merge-path merge
 // with the running top-k in LDS.
@@ -35,7 +37,8 @@ namespace {
 constexpr int kTW = 8;                               // waves per workgroup
 constexpr int kTT = kTW * kWave;                     // 512 threads
 constexpr int kTRound = kTW * kVecPerWaveRound;      // vectors per workgroup round
-constexpr int kSortMax = 4096;                       // rerank_m limit (final LDS sort)
+constexpr int kSortMax = 4096;                       // keys of one final LDS sort (a run)
+constexpr int kRerankMax = 1 << 17;                  // rerank_m limit: at most 32 runs
 constexpr uint64_t kNoKey = ~0ull;                   // "no admission bound yet"
 // Phase 1 stages the eight sorted wave lists of up to kStage lists; all waves
 // merge the staged lists in parallel when the stage is full and at the end of
@@ -470,16 +473,60 @@ __global__ __launch_bounds__(kTT) void two_phase_kernel(TwoPhaseArgs a) {
     cnt = R;
   }
   uint64_t* sk = reinterpret_cast<uint64_t*>(smem);
-  int np2 = 1;
-  while (np2 < cnt) np2 <<= 1;
-  for (int i = tid; i < np2; i += kTT) sk[i] = i < cnt ? pool[i] : kNoKey;
-  __syncthreads();
-  lds_bitonic_sort(sk, np2);
-  for (int j = tid; j < R; j += kTT) {
-    const bool real = j < cnt;
-    const uint64_t key = real ? sk[j] : 0;
-    a.top_ids[(size_t)q * R + j] = real ? (int32_t)(uint32_t)key : -1;
-    a.top_d[(size_t)q * R + j] = real ? __uint_as_float((uint32_t)(key >> 32)) : FLT_MAX;
+  int32_t* out_id = a.top_ids + (size_t)q * R;
+  float* out_d = a.top_d + (size_t)q * R;
+  if (cnt <= kSortMax) {
+    int np2 = 1;
+    while (np2 < cnt) np2 <<= 1;
+    for (int i = tid; i < np2; i += kTT) sk[i] = i < cnt ? pool[i] : kNoKey;
+    __syncthreads();
+    lds_bitonic_sort(sk, np2);
+    for (int j = tid; j < cnt; j += kTT) {
+      const uint64_t key = sk[j];
+      out_id[j] = (int32_t)(uint32_t)key;
+      out_d[j] = __uint_as_float((uint32_t)(key >> 32));
+    }
+  } else {
+    // More keys than one LDS sort holds: sort runs of kSortMax keys in LDS and
+    // write each back in place, then put every key at its final position,
+    // its index in its run plus, for every other run, the keys there that
+    // precede it (binary search; on equal keys the earlier run goes first).
+    const int nruns = (cnt + kSortMax - 1) / kSortMax;
+    for (int r = 0; r < nruns; ++r) {
+      const int r0 = r * kSortMax, len = min(kSortMax, cnt - r0);
+      int np2 = 1;
+      while (np2 < len) np2 <<= 1;
+      for (int i = tid; i < np2; i += kTT) sk[i] = i < len ? pool[r0 + i] : kNoKey;
+      __syncthreads();
+      lds_bitonic_sort(sk, np2);
+      for (int i = tid; i < len; i += kTT) pool[r0 + i] = sk[i];
+      __syncthreads();  // the run is back in the pool before the sort area is reused / ranks are read
+    }
+    for (int j = tid; j < cnt; j += kTT) {
+      const int r = j / kSortMax;
+      const uint64_t key = pool[j];
+      int pos = j - r * kSortMax;
+      for (int o = 0; o < nruns; ++o) {
+        if (o == r) continue;
+        const uint64_t* run = pool + o * kSortMax;
+        int lo = 0, hi = min(kSortMax, cnt - o * kSortMax);  // count of run keys < key (o > r) or <= key (o < r)
+        while (lo < hi) {
+          const int mid = (lo + hi) >> 1;
+          const uint64_t v = run[mid];
+          if (o < r ? v <= key : v < key)
+            lo = mid + 1;
+          else
+            hi = mid;
+        }
+        pos += lo;
+      }
+      out_id[pos] = (int32_t)(uint32_t)key;
+      out_d[pos] = __uint_as_float((uint32_t)(key >> 32));
+    }
+  }
+  for (int j = cnt + tid; j < R; j += kTT) {
+    out_id[j] = -1;
+    out_d[j] = FLT_MAX;
   }
   if (tid == 0) a.top_counts[q] = cnt;
   if (a.stats && tid == 0) {
@@ -643,7 +690,8 @@ int two_phase_pool_cap(int p1, int limit_k, int rerank_m) {
 
 fgpu_status launch_two_phase(int dim, int m, const TwoPhaseArgs& a, hipStream_t s) {
   FGPU_CHECK(a.limit_k >= 1 && a.limit_k <= 64, FGPU_ERR_UNSUPPORTED, "two_phase: limit_k must be in [1, 64]");
-  FGPU_CHECK(a.rerank_m >= 1 && a.rerank_m <= kSortMax, FGPU_ERR_UNSUPPORTED, "two_phase: rerank_m must be in [1, 4096]");
+  FGPU_CHECK(a.rerank_m >= 1 && a.rerank_m <= kRerankMax, FGPU_ERR_UNSUPPORTED,
+             "two_phase: rerank_m must be in [1, 131072]");
   FGPU_CHECK(a.nprobe >= 1 && a.nprobe <= 64 && a.p1 >= 0 && a.p1 <= a.nprobe, FGPU_ERR_ARG,
              "two_phase: need 1 <= nprobe <= 64 and 0 <= p1 <= nprobe");
   FGPU_CHECK(a.pool_cap >= two_phase_pool_cap(a.p1, a.limit_k, a.rerank_m), FGPU_ERR_ARG, "two_phase: pool too small");

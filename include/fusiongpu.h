@@ -70,6 +70,17 @@ fgpu_status fgpu_index_load(const char* ivf_data_path, const char* codebook_path
 void fgpu_index_destroy(fgpu_index* idx);
 fgpu_status fgpu_index_get_info(const fgpu_index* idx, fgpu_index_info* out);
 
+/* An index over A1 arrays the caller already holds in HBM, laid out as the
+ * reference's IVFIndexGPU holds them (defs.h:51-58; filled by
+ * load_ivf_index_to_gpu, search_pipeline.cu:481-529): no copy.  The handle
+ * computes its own derived arrays (centroid norms, list radii) and reads the
+ * offsets once (it synchronises `stream`).  fgpu_index_destroy frees only what
+ * the handle allocated; the caller's arrays must outlive it.  d_codes must be
+ * 16-byte aligned and pq_m a multiple of 16. */
+fgpu_status fgpu_index_wrap(int dim, int pq_m, int nlist, const int32_t* d_offsets, const int32_t* d_ids,
+                            const uint8_t* d_codes, const float* d_centroids, const float* d_codebook,
+                            void* stream, fgpu_index** out);
+
 /* The plain scan (fgpu_adc_search, fgpu_search) hands LUT buffers and query
  * slots between the waves of a workgroup through LDS counters.  Every wait on
  * them is bounded, far above the longest legitimate wait (the scan of all
@@ -100,6 +111,12 @@ fgpu_status fgpu_coarse_search(const fgpu_index* idx, const float* d_queries, in
                                float prune_ratio, uint32_t* d_probe_ids, float* d_probe_dists,
                                void* d_workspace, size_t workspace_bytes, void* stream);
 
+/* The prune step of prune_and_count_fused_kernel (gpu_global.cu:43-50), in
+ * place: a probe whose distance exceeds (its query's first distance) *
+ * prune_ratio becomes 0xFFFFFFFF. */
+fgpu_status fgpu_prune_probes(uint32_t* d_probe_ids, const float* d_probe_dists, int nq, int nprobe,
+                              float prune_ratio, void* stream);
+
 /* counts[q] = sum of list sizes over surviving probes; offsets = exclusive
  * scan with offsets[nq] = total (gpu_global.cu:31-77, 704-723). */
 fgpu_status fgpu_probe_counts(const fgpu_index* idx, const uint32_t* d_probe_ids, int nq, int nprobe,
@@ -113,8 +130,12 @@ fgpu_status fgpu_probe_counts(const fgpu_index* idx, const uint32_t* d_probe_ids
  * k <= 64.  d_probe_dists (may be NULL) takes the place of the reference's
  * d_cagra_dists: fgpu_coarse_search's distances for these probes, which the
  * scan then uses for its exact list bounds instead of recomputing them from
- * the centroids.  Non-NULL, they must be those distances (the squared L2 in
- * the coarse step's form); results are the same either way. */
+ * the centroids.  Non-NULL, they must be exactly the distances
+ * fgpu_coarse_search or fgpu_coarse_graph_search returned for these probes:
+ * the bounds allow only the rounding of that form, so other distances (a
+ * GEMM's expanded ||q||^2 + ||c||^2 - 2 q.c, an approximation) can make the
+ * scan skip lists that hold top-k vectors; pass NULL for them.  With valid
+ * distances or NULL the results are the same. */
 fgpu_status fgpu_adc_search(const fgpu_index* idx, const float* d_queries, int nq,
                             const uint32_t* d_probe_ids, const float* d_probe_dists, int nprobe, int k,
                             int32_t* d_out_ids, float* d_out_dists, void* stream);
@@ -175,7 +196,7 @@ fgpu_status fgpu_search_noalloc(const fgpu_index* idx, const float* d_queries, i
  * all rerank_m entries are gathered.  No host synchronisation and no pool
  * reallocation: the candidate pool is a bounded workspace, kept exact by
  * selecting the rerank_m best whenever it would overflow.  limit_k <= 64,
- * rerank_m <= 4096, nprobe <= 64.  A workspace smaller than the returned size
+ * rerank_m <= 131072 (the reference's default is 10000), nprobe <= 64.  A workspace smaller than the returned size
  * is used in query chunks (it must hold at least one query's pool). */
 size_t fgpu_two_phase_workspace_bytes(int nq, int nprobe, int p1_lists, int limit_k, int rerank_m);
 fgpu_status fgpu_two_phase_search(const fgpu_index* idx, const float* d_queries, int nq,
@@ -335,6 +356,14 @@ fgpu_status fgpu_pq_train(const float* d_x, int64_t n, int dim, int pq_m, const 
 fgpu_status fgpu_pq_encode(const float* d_x, int64_t n, int dim, int pq_m, const int32_t* d_assign,
                            const float* d_centroids, const float* d_codebook, uint8_t* d_codes,
                            void* stream);
+/* The same with the distance form chosen: fma_mode 1 = the device kernel's
+ * fused chain (kmeans_gpu.cuh:428-433, as fgpu_pq_encode), 0 = the host twin
+ * encode_residuals_to_pq (pq_utils.h:141-175, built without FMA): every
+ * product and sum rounded separately.  The two can pick different codewords
+ * on near ties. */
+fgpu_status fgpu_pq_encode_form(const float* d_x, int64_t n, int dim, int pq_m, const int32_t* d_assign,
+                                const float* d_centroids, const float* d_codebook, int fma_mode,
+                                uint8_t* d_codes, void* stream);
 
 /* build_global (build_global.cu:21-258) without rebalancing and CAGRA: k-means
  * (nlist, kmeans_iters), assignment, PQ training (pq_iters, sample_size),

@@ -278,3 +278,27 @@ def test_search_on_a_side_stream():
     assert torch.equal(aid, ref_id) and torch.equal(ad, ref_d)
     assert idx.faults(stream=s) == 0
     idx.close()
+
+
+def test_wrapped_device_arrays_search_like_an_owned_index():
+    """fgpu_index_wrap over device arrays the caller holds (the reference's
+    IVFIndexGPU) gives the same search as an index that owns copies; the
+    in-place prune equals the oracle's prune rule."""
+    _say("index wrap + prune_probes")
+    rng = np.random.default_rng(31)
+    offs, ids, lc, cent, cb = _random_index(rng, 20000, 128, 32, 96)
+    q = torch.from_numpy(rng.standard_normal((400, 128)).astype(np.float32) * 0.7).cuda()
+    own = fg.Index.from_arrays(128, 32, offs, ids, lc, cent, cb)
+    dev = [torch.from_numpy(a).cuda() for a in (offs, ids, lc, cent, cb)]
+    wrapped = fg.Index.wrap(128, 32, *dev)
+    assert (wrapped.nlist, wrapped.total, wrapped.max_list_len) == (own.nlist, own.total, own.max_list_len)
+    a = own.search(q, 16, 10)
+    b = wrapped.search(q, 16, 10)
+    assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
+    pid, pd = own.coarse_search(q, 16, prune_ratio=np.inf)
+    fg.prune_probes(pid, pd, 1.2)
+    oid, _ = oracle.coarse(q.cpu().numpy(), cent, 16, prune_ratio=1.2)
+    assert np.array_equal(_host(pid).view(np.uint32), oid)
+    assert wrapped.faults() == 0
+    wrapped.close()
+    own.close()

@@ -55,7 +55,9 @@ CASES = [
     (128, 16, 0, 10, 1.0, 50),     # no phase 1: thr = FLT_MAX, every vector passes, pool selects repeatedly
     (96, 32, 16, 64, 1.5, 300),    # every probe in phase 1
     (128, 64, 4, 1, 0.0, 17),      # threshold 0: phase 2 adds nothing
-    (96, 16, 2, 7, 3.0, 4096),     # the largest rerank_m, loose threshold
+    (96, 16, 2, 7, 3.0, 4096),     # one full LDS sort, loose threshold
+    (128, 32, 2, 20, 5.0, 10000),  # the reference's default rerank_m: up to three sorted runs placed by rank
+    (96, 16, 0, 10, 1.0, 5000),    # every vector passes: two runs, repeated pool selects
 ]
 
 
@@ -215,3 +217,29 @@ def test_knn_exact_bit_exact(k, n, dim):
     assert np.array_equal(_bits(gd), _bits(od))
     if n < k:
         assert np.all(gid[:, n:] == -1)
+
+
+def test_reference_default_rerank_m_end_to_end():
+    """The reference's default rerank_m = 10000 (defs.h:18) through the
+    two-phase scan and the exact rerank, against the oracle."""
+    _say("two_phase + rerank with rerank_m 10000")
+    rng = np.random.default_rng(10000)
+    dim, m, nlist, k = 128, 32, 48, 10
+    offs, ids, lc, cent, cb = _index(rng, 40000, dim, m, nlist, big=4)
+    base = (rng.standard_normal((40000, dim)) * 0.7).astype(np.float32)
+    q = (rng.standard_normal((64, dim)) * 0.7).astype(np.float32)
+    probes, _ = oracle.coarse(q, cent, 20)
+    p1, limit_k, coeff, rerank_m = 12, 50, 2.5, 10000
+    idx = fg.Index.from_arrays(dim, m, offs, ids, lc, cent, cb)
+    dq = torch.from_numpy(q).cuda()
+    tid, td, tc, _, _ = idx.two_phase_search(dq, torch.from_numpy(probes.view(np.int32)).cuda(), p1, limit_k, coeff,
+                                             rerank_m)
+    oid, od, ocnt, _, _ = oracle.search_two_phase(q, cent, cb, offs, ids, lc, probes, p1, limit_k, coeff, rerank_m)
+    assert np.array_equal(_host(tc), ocnt)
+    assert (ocnt > 4096).any(), "the case must need more than one LDS sort"
+    assert np.array_equal(_host(tid), oid) and np.array_equal(_bits(_host(td)), _bits(od))
+    rid, rd, vis = fg.rerank(dq, torch.from_numpy(base).cuda(), tid, tc, k, 128, 0.1, 2)
+    fid, fd, fvis = oracle.rerank(q, base, oid, ocnt, k, 128, 0.1, 2)
+    assert np.array_equal(_host(rid), fid) and np.array_equal(_bits(_host(rd)), _bits(fd))
+    assert np.array_equal(_host(vis), fvis)
+    idx.close()
