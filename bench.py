@@ -10,13 +10,18 @@ not timed.
 One step = one full search of the 10k-query batch with queries already in HBM:
 coarse quantizer (MFMA GEMM + exact re-score + top-32) and LUT + ADC scan +
 top-10.  value = 10k / step time.  The roofline entry is for the dominant
-kernel, the ADC scan: algorithmic bytes = sum over (query, probe) of
-list_len * M code bytes, divided by the scan kernel's average duration from HIP
-events recorded on the stream it runs on.  The line also carries
-`graph_coarse`: the same coarse step done the reference's way (a graph walk over
-the centroids instead of the exact GEMM; not timed in `value`), with its time,
-the share of the exact top-32 lists it finds and how often the top-10 stays
-identical.
+kernel, the ADC scan: achieved = the code and id bytes of the lists it reads
+(its own load count), divided by its average duration from HIP events recorded
+on the stream it runs on; `traffic` is the copy-calibrated FETCH_SIZE +
+WRITE_SIZE from profiles/.  The scan's exact list bound skips most probed
+lists, so the work-equivalent figure (every probed list once) is
+reported apart as `effective`, and `no_skip` times the same kernel reading
+every probed list.  `measured_read_peak_gbs` is a streaming read of 4 GiB.
+`end_to_end` follows the reference's QPS definition (H2D + search + D2H).  The
+line also carries `graph_coarse`: the same coarse step done the reference's way
+(a graph walk over the centroids instead of the exact GEMM; not timed in
+`value`), with its time, the share of the exact top-32 lists it finds and how
+often the top-10 stays identical.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--cpu-queries N] [--workload c2|c3|c4|c5]
 
@@ -57,18 +62,60 @@ METRIC = "QPS at fixed nprobe, 1M×128 IVF-PQ k=10 (1 GPU); ADC-scan HBM GB/s vs
 HBM_PEAK_GBS = 8000.0
 FP32_MFMA_PEAK_TFLOPS = 157.3
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "adc_flow_c2_traffic.txt")
+TRAFFIC_FILE_C3 = os.path.join(ROOT, "profiles", "two_phase_c3_traffic.txt")
 
 
 def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def read_traffic():
-    """HBM bytes per ADC launch measured with rocprofv3 --pmc (FETCH_SIZE + WRITE_SIZE, copy-calibrated)."""
+def read_traffic(path=TRAFFIC_FILE, key="traffic_bytes_per_launch"):
+    """HBM bytes per launch measured with rocprofv3 --pmc (FETCH_SIZE + WRITE_SIZE, copy-calibrated)."""
     try:
-        for line in open(TRAFFIC_FILE):
-            if line.startswith("traffic_bytes_per_launch:"):
+        for line in open(path):
+            if line.startswith(key + ":"):
                 return float(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
+def timed_ms(torch, stream, reps, fn):
+    """Average time of fn() over reps launches, from HIP events recorded on the stream the work runs on."""
+    fn()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(reps):
+        fn()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / reps
+
+
+def stream_read_peak(torch, fg, dev, gib=4, reps=10):
+    """Measured HBM read rate: 16-byte streaming loads over a buffer far larger than the MALL."""
+    a = torch.empty(gib << 30, dtype=torch.uint8, device=dev)
+    ms = timed_ms(torch, torch.cuda.current_stream(), reps, lambda: fg.stream_read(a))
+    del a
+    return (gib << 30) / (ms * 1e-3) / 1e9
+
+
+def cpu_timed(fn, warm, runs=3):
+    """Median wall time of `runs` calls of fn after one warm-up call of warm; returns (seconds, last result)."""
+    warm()
+    ts, r = [], None
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        r = fn()
+        ts.append(time.perf_counter() - t0)
+    return float(np.median(ts)), r
+
+
+def cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
     except OSError:
         pass
     return None
@@ -140,34 +187,68 @@ def main():
     # ---- stage timing with HIP events on the launch stream
     probes, pd = idx.coarse_search(dq, nprobe)
     cnt, _ = fg.probe_counts(idx, probes)
-    adc_bytes = int(cnt.to(torch.int64).sum().item()) * m
-    ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+    n_probed_vecs = int(cnt.to(torch.int64).sum().item())
+    adc_bytes = n_probed_vecs * m  # code bytes of every probed list, once per (query, list)
+    pruned = int((probes == -1).sum().item())
     reps = max(args.steps, 5)
-    ev[0].record(stream)
-    for _ in range(reps):
-        idx.coarse_search(dq, nprobe, workspace=ws)
-    ev[1].record(stream)
-    for _ in range(reps):
-        idx.adc_search(dq, probes, k, out=out, probe_dists=pd)
-    ev[2].record(stream)
-    torch.cuda.synchronize()
-    coarse_ms = ev[0].elapsed_time(ev[1]) / reps
-    adc_ms = ev[1].elapsed_time(ev[2]) / reps
-    adc_gbs = adc_bytes / (adc_ms * 1e-3) / 1e9
+    coarse_ms = timed_ms(torch, stream, reps, lambda: idx.coarse_search(dq, nprobe, workspace=ws))
+    adc_ms = timed_ms(torch, stream, reps, lambda: idx.adc_search(dq, probes, k, out=out, probe_dists=pd))
     gemm_flop = 2.0 * args.nq * nlist * dim
-    log(f"coarse {coarse_ms:.3f} ms ({gemm_flop / coarse_ms / 1e9:.1f} TFLOP/s incl. select), "
-        f"adc {adc_ms:.3f} ms, algorithmic ADC bytes {adc_bytes / 1e9:.2f} GB -> {adc_gbs:.0f} GB/s")
-    # What the scan really loads: the exact list / chunk bounds skip code loads
-    # of lists and chunks that cannot reach the top-k (results unchanged).
+    log(f"coarse {coarse_ms:.3f} ms ({gemm_flop / coarse_ms / 1e9:.1f} TFLOP/s incl. select), adc {adc_ms:.3f} ms; "
+        f"{pruned} of {args.nq * nprobe} probes pruned (prune_ratio 100)")
+    # What the scan moves: the codes and ids of the lists it does not skip
+    # (the exact list bound skips lists that cannot reach the top-k).
     sid, sd, st = idx.adc_search_stats(dq, probes, k, probe_dists=pd)
     assert torch.equal(sid, out[0]) and torch.equal(sd, out[1]), "instrumented scan differs"
     loaded_bytes = st["vectors_loaded"] * (m + 4)  # code bytes + the 4-byte vector id loaded with them
     loaded_gbs = loaded_bytes / (adc_ms * 1e-3) / 1e9
+    eff_gbs = adc_bytes / (adc_ms * 1e-3) / 1e9
     log("adc clocks per query: " + ", ".join(f"{kk} {st[kk] / args.nq:.0f}" for kk in
                                                 ("clk_setup", "clk_builder", "clk_scanner", "clk_total")))
-    log(f"adc loads {st['vectors_loaded'] * m / 1e9:.2f} GB of codes (+ids {st['vectors_loaded'] * 4 / 1e9:.2f} GB) "
+    log(f"adc moves {st['vectors_loaded'] * m / 1e9:.2f} GB of codes (+ids {st['vectors_loaded'] * 4 / 1e9:.2f} GB) "
         f"= {loaded_gbs:.0f} GB/s; LUTs built {st['luts_built']}, probed lists skipped {st['lists_skipped']} "
-        f"of {int((probes.view(torch.int32) >= 0).sum().item())}")
+        f"of {int((probes != -1).sum().item())}; every probed list once would be {adc_bytes / 1e9:.2f} GB "
+        f"({eff_gbs:.0f} GB/s work-equivalent)")
+    # The same scan with the list bound off: it reads every probed list.
+    fg.debug_set_list_skip(False)
+    try:
+        nid, nd = idx.adc_search(dq, probes, k, probe_dists=pd)
+        ns_ms = timed_ms(torch, stream, reps, lambda: idx.adc_search(dq, probes, k, out=out, probe_dists=pd))
+    finally:
+        fg.debug_set_list_skip(True)
+    assert torch.equal(nid, sid) and torch.equal(nd, sd), "the scan without list skipping differs"
+    ns_bytes = n_probed_vecs * (m + 4)
+    ns_gbs = ns_bytes / (ns_ms * 1e-3) / 1e9
+    log(f"adc without list skipping: {ns_ms:.3f} ms, {ns_bytes / 1e9:.2f} GB (codes + ids of every probed list) "
+        f"= {ns_gbs:.0f} GB/s; ids identical")
+    assert idx.faults() == 0, "a bounded wait of the scan gave up"
+    peak_gbs = stream_read_peak(torch, fg, dev)
+    log(f"measured stream-read rate: {peak_gbs:.0f} GB/s (16-byte loads over 4 GiB)")
+
+    # ---- end to end, the reference's QPS definition (search_pipeline.cu:621-636): queries
+    # from pinned host memory, search, results back to pinned host memory, all steps enqueued
+    hq = torch.empty((args.nq, dim), dtype=torch.float32, pin_memory=True)
+    hq.copy_(torch.from_numpy(q))
+    hid = torch.empty((args.nq, k), dtype=torch.int32, pin_memory=True)
+    hdd = torch.empty((args.nq, k), dtype=torch.float32, pin_memory=True)
+    dq2 = torch.empty_like(dq)
+
+    def e2e_step():
+        dq2.copy_(hq, non_blocking=True)
+        idx.search(dq2, nprobe, k, workspace=ws, out=out)
+        hid.copy_(out[0], non_blocking=True)
+        hdd.copy_(out[1], non_blocking=True)
+
+    for _ in range(2):
+        e2e_step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        e2e_step()
+    torch.cuda.synchronize()
+    e2e_ms = 1e3 * (time.perf_counter() - t0) / args.steps
+    assert torch.equal(hid, out[0].cpu()), "end-to-end results differ"
+    log(f"end to end (H2D queries + search + D2H results): {e2e_ms:.3f} ms/step, {args.nq / e2e_ms * 1e3:,.0f} QPS")
 
     # ---- the graph coarse mode (the reference's CAGRA-over-centroids step): time and
     # how many of the exact top-nprobe lists it finds, and the end-to-end top-10 it gives;
@@ -180,12 +261,7 @@ def main():
         torch.cuda.synchronize()
         graph_build_ms = 1e3 * (time.perf_counter() - t0)
         gprobes, _ = idx.coarse_graph_search(dq, nprobe, cgraph)
-        ev[0].record(stream)
-        for _ in range(reps):
-            idx.coarse_graph_search(dq, nprobe, cgraph)
-        ev[1].record(stream)
-        torch.cuda.synchronize()
-        graph_ms = ev[0].elapsed_time(ev[1]) / reps
+        graph_ms = timed_ms(torch, stream, reps, lambda: idx.coarse_graph_search(dq, nprobe, cgraph))
         gp = gprobes.cpu().numpy().view(np.uint32)
         probe_recall = float(np.mean([len(set(a_) & set(b_)) / nprobe for a_, b_ in zip(gp, ep)]))
         gids, _ = idx.adc_search(dq, gprobes, k)
@@ -207,24 +283,29 @@ def main():
     gid = out[0].cpu().numpy()
     gd = out[1].cpu().numpy()
 
-    # ---- CPU baseline: the oracle (C++/OpenMP restatement) on a bounded query sample
+    # ---- CPU baseline: the oracle (C++/OpenMP restatement of the same search) on the same index
     cpu = None
     parity = None
     if args.cpu_queries > 0:
         import oracle
         ns = min(args.cpu_queries, args.nq)
+
+        def cpu_search(qq):
+            op, _ = oracle.coarse(qq, cent, nprobe)
+            return oracle.search_plain(qq, cent, cb, offs, ids, codes, op, k)
+
+        cpu_s, (oid, od) = cpu_timed(lambda: cpu_search(q[:ns]), warm=lambda: cpu_search(q[:min(ns, 500)]))
         threads = oracle.lib.orc_max_threads()
-        t0 = time.perf_counter()
-        oprobe, _ = oracle.coarse(q[:ns], cent, nprobe)
-        oid, od = oracle.search_plain(q[:ns], cent, cb, offs, ids, codes, oprobe, k)
-        cpu_s = time.perf_counter() - t0
         cpu = {"value": round(ns / cpu_s, 1), "unit": "queries/s", "cores": threads, "kind": "port",
-               "sample": f"first {ns} of the 10k queries, same index, coarse + LUT/ADC + top-10, "
-                         f"{cpu_s:.1f}s wall on {threads} OpenMP threads"}
+               "cpu_model": cpu_model(),
+               "sample": f"first {ns} of the 10k queries, same index: coarse + LUT/ADC + top-10 (the oracle's "
+                         f"exhaustive scan); median of 3 runs after a warm-up, {cpu_s:.2f}s each, "
+                         f"{threads} OpenMP threads"}
         parity = {"queries": ns, "ids_equal": bool(np.array_equal(gid[:ns], oid)),
                   "dists_bit_equal": bool(np.array_equal(gd[:ns].view(np.uint32), od.view(np.uint32)))}
-        log(f"cpu baseline {cpu['value']} QPS on {threads} threads; parity {parity}")
+        log(f"cpu baseline {cpu['value']} QPS on {threads} threads ({cpu['cpu_model']}); parity {parity}")
 
+    traffic = read_traffic()
     res = {
         "metric": METRIC,
         "value": round(qps, 1),
@@ -240,21 +321,35 @@ def main():
         "data": "synthetic: seeded Gaussian mixture; index built in-run by this framework's GPU build path",
         "config": {"workload": "BASELINE config 2: 1M x 128 fp32, 1024 lists, PQ M=32 x 256 (8-bit), "
                                "10k queries in one batch, nprobe=32, k=10",
-                   "n": args.n, "dim": dim, "nlist": nlist, "pq_m": m, "nq": args.nq, "nprobe": nprobe, "k": k},
-        "roofline": {"bound": "hbm", "kernel": "adc_flow_kernel<128,32>", "achieved": round(adc_gbs, 1),
-                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(adc_gbs / HBM_PEAK_GBS, 4),
-                     "traffic": read_traffic(), "algorithmic_bytes_per_launch": adc_bytes,
-                     "avg_launch_ms": round(adc_ms, 4),
-                     "note": "achieved = algorithmic code bytes (every probed list read once) / kernel time; "
-                             "exact lower bounds let the kernel skip loading lists and chunks that cannot "
-                             "reach the top-k, so it loads only loaded_bytes_per_launch",
-                     "loaded_bytes_per_launch": loaded_bytes, "achieved_loaded": round(loaded_gbs, 1),
-                     "frac_loaded": round(loaded_gbs / HBM_PEAK_GBS, 4),
-                     "luts_built": st["luts_built"], "lists_skipped": st["lists_skipped"],
+                   "n": args.n, "dim": dim, "nlist": nlist, "pq_m": m, "nq": args.nq, "nprobe": nprobe, "k": k,
+                   "prune_ratio": 100.0, "probes_pruned": pruned, "probes_total": args.nq * nprobe},
+        "roofline": {"bound": "hbm", "kernel": "adc_flow_kernel<128,32>", "achieved": round(loaded_gbs, 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(loaded_gbs / HBM_PEAK_GBS, 4),
+                     "traffic": traffic, "bytes_per_launch": loaded_bytes, "avg_launch_ms": round(adc_ms, 4),
+                     "note": "achieved = codes + ids of the lists the scan reads (its own load count in this run) / "
+                             "kernel time; traffic = copy-calibrated FETCH_SIZE + WRITE_SIZE per launch "
+                             "(profiles/adc_flow_c2_traffic.txt)",
+                     "traffic_rate_gbs": round(traffic / (adc_ms * 1e-3) / 1e9, 1) if traffic else None,
+                     "measured_read_peak_gbs": round(peak_gbs, 1),
+                     "frac_of_measured_peak": round(loaded_gbs / peak_gbs, 4),
+                     "effective": {"bytes_per_launch": adc_bytes, "gbs": round(eff_gbs, 1),
+                                   "lists_skipped": st["lists_skipped"], "luts_built": st["luts_built"],
+                                   "note": "work-equivalent rate: code bytes of every probed list once per (query, "
+                                           "list) over the kernel time; the exact list bound skips lists that "
+                                           "cannot reach the top-10, so this exceeds the HBM peak"},
+                     "no_skip": {"avg_launch_ms": round(ns_ms, 4), "bytes_per_launch": ns_bytes,
+                                 "achieved": round(ns_gbs, 1), "frac": round(ns_gbs / HBM_PEAK_GBS, 4),
+                                 "ids_identical": True,
+                                 "traffic": read_traffic(TRAFFIC_FILE, "traffic_bytes_per_launch_no_skip"),
+                                 "note": "the same kernel with the list bound off: it reads the codes and ids of "
+                                         "every probed list (32 MB of codes, so mostly from the MALL)"},
                      "clocks_per_query": {kk: round(st[kk] / args.nq) for kk in
                                           ("clk_setup", "clk_builder", "clk_scanner", "clk_total")}},
         "stages_ms": {"coarse": round(coarse_ms, 4), "adc": round(adc_ms, 4),
                       "coarse_tflops_incl_select": round(gemm_flop / coarse_ms / 1e9, 2)},
+        "end_to_end": {"ms_per_step": round(e2e_ms, 4), "qps": round(args.nq / e2e_ms * 1e3, 1),
+                       "note": "the reference's QPS definition: queries H2D from pinned memory + search + "
+                               "results D2H, every step enqueued, one wait at the end"},
         "cpu_baseline": cpu,
         "parity": parity,
         "graph_coarse": graph_coarse,
@@ -333,10 +428,18 @@ def run_c3(args, torch, fg, dev):
     tp_ms = ev[1].elapsed_time(ev[2]) / reps
     rr_ms = ev[2].elapsed_time(ev[3]) / reps
     adc_gbs = adc_bytes / (tp_ms * 1e-3) / 1e9
+    loaded_gbs = loaded_bytes / (tp_ms * 1e-3) / 1e9
     rr_bytes = visited * dim * 4
     log(f"coarse {coarse_ms:.3f} ms, two-phase {tp_ms:.3f} ms (algorithmic ADC bytes {adc_bytes / 1e9:.2f} GB -> "
         f"{adc_gbs:.0f} GB/s), rerank {rr_ms:.3f} ms ({visited} rows = {rr_bytes / 1e9:.2f} GB -> "
         f"{rr_bytes / (rr_ms * 1e-3) / 1e9:.0f} GB/s); candidates/query {tc.float().mean().item():.0f}")
+    if args.copy_probe:
+        a = torch.empty(1 << 28, dtype=torch.float32, device=dev)
+        b = torch.empty_like(a)
+        b.copy_(a)
+        torch.cuda.synchronize()
+        del a, b
+        log("copy probe: 1 GiB device-to-device copy done")
     gid, gd = out[0].cpu().numpy(), out[1].cpu().numpy()
 
     cpu = parity = recall = None
@@ -344,15 +447,18 @@ def run_c3(args, torch, fg, dev):
         import oracle
         ns = min(args.cpu_queries, nq, 2000)
         threads = oracle.lib.orc_max_threads()
-        t0 = time.perf_counter()
-        oprobe, _ = oracle.coarse(q[:ns], cent, nprobe)
-        otid, _, otc, _, _ = oracle.search_two_phase(q[:ns], cent, cb, offs, ids, codes, oprobe, p1, limit_k, coeff,
-                                                     rerank_m)
-        oid, od, _ = oracle.rerank(q[:ns], x, otid, otc, k, mb, eps, beta)
-        cpu_s = time.perf_counter() - t0
+
+        def cpu_search(qq):
+            oprobe, _ = oracle.coarse(qq, cent, nprobe)
+            otid, _, otc, _, _ = oracle.search_two_phase(qq, cent, cb, offs, ids, codes, oprobe, p1, limit_k, coeff,
+                                                         rerank_m)
+            return oracle.rerank(qq, x, otid, otc, k, mb, eps, beta)
+
+        cpu_s, (oid, od, _) = cpu_timed(lambda: cpu_search(q[:ns]), warm=lambda: cpu_search(q[:100]))
         cpu = {"value": round(ns / cpu_s, 1), "unit": "queries/s", "cores": threads, "kind": "port",
-               "sample": f"first {ns} of the {nq} queries, same index: coarse + two-phase scan + rerank, "
-                         f"{cpu_s:.1f}s wall on {threads} OpenMP threads"}
+               "cpu_model": cpu_model(),
+               "sample": f"first {ns} of the {nq} queries, same index: coarse + two-phase scan + rerank; median "
+                         f"of 3 runs after a warm-up, {cpu_s:.2f}s each, {threads} OpenMP threads"}
         parity = {"queries": ns, "ids_equal": bool(np.array_equal(gid[:ns], oid)),
                   "dists_bit_equal": bool(np.array_equal(gd[:ns].view(np.uint32), od.view(np.uint32)))}
         log(f"cpu baseline {cpu['value']} QPS on {threads} threads; parity {parity}")
@@ -383,11 +489,17 @@ def run_c3(args, torch, fg, dev):
         "config": {"workload": "BASELINE config 3: 10M x 96 fp32, 4096 lists, PQ M=48, 10k queries, nprobe=64, "
                                "p1_lists 12, limit_k 50, threshold_coeff 1.0, top-1000 -> exact rerank k=100",
                    "n": n, "dim": dim, "nlist": nlist, "pq_m": m, "nq": nq, "nprobe": nprobe, "k": k},
-        "roofline": {"bound": "hbm", "kernel": "two_phase_kernel<96,48>", "achieved": round(adc_gbs, 1),
-                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(adc_gbs / HBM_PEAK_GBS, 4),
-                     "traffic": None, "algorithmic_bytes_per_launch": adc_bytes, "avg_launch_ms": round(tp_ms, 4),
-                     "loaded_bytes_per_launch": loaded_bytes,
-                     "achieved_loaded": round(loaded_bytes / (tp_ms * 1e-3) / 1e9, 1), **tstats},
+        "roofline": {"bound": "hbm", "kernel": "two_phase_kernel<96,48>", "achieved": round(loaded_gbs, 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(loaded_gbs / HBM_PEAK_GBS, 4),
+                     "traffic": read_traffic(TRAFFIC_FILE_C3), "bytes_per_launch": loaded_bytes,
+                     "avg_launch_ms": round(tp_ms, 4),
+                     "note": "achieved = codes + ids of the lists the scan reads (its own load count in this run) / "
+                             "kernel time; traffic = copy-calibrated FETCH_SIZE + WRITE_SIZE per launch "
+                             "(profiles/two_phase_c3_traffic.txt)",
+                     "effective": {"bytes_per_launch": adc_bytes, "gbs": round(adc_gbs, 1),
+                                   "note": "work-equivalent: code bytes of every probed list once per (query, list); "
+                                           "phase 2 skips lists whose bound exceeds the threshold"},
+                     **tstats},
         "stages_ms": {"coarse": round(coarse_ms, 4), "two_phase": round(tp_ms, 4), "rerank": round(rr_ms, 4),
                       "rerank_rows": visited, "rerank_gbs": round(rr_bytes / (rr_ms * 1e-3) / 1e9, 1),
                       "candidates_per_query": round(tc.float().mean().item(), 1)},
@@ -454,12 +566,12 @@ def run_c4(args, torch, fg, dev):
         ns = min(args.cpu_queries, 20000)
         threads = oracle.lib.orc_max_threads()
         hcent = cent.cpu().numpy()
-        t0 = time.perf_counter()
-        oa = oracle.kmeans_assign(x[:ns], hcent)
-        cpu_s = time.perf_counter() - t0
+        cpu_s, oa = cpu_timed(lambda: oracle.kmeans_assign(x[:ns], hcent),
+                              warm=lambda: oracle.kmeans_assign(x[:1000], hcent))
         cpu = {"value": round(ns / cpu_s, 1), "unit": "rows assigned/s", "cores": threads, "kind": "port",
-               "sample": f"exact assignment of the first {ns} rows to the 4096 centroids, {cpu_s:.1f}s wall on "
-                         f"{threads} OpenMP threads"}
+               "cpu_model": cpu_model(),
+               "sample": f"exact assignment of the first {ns} rows to the 4096 centroids; median of 3 runs after a "
+                         f"warm-up, {cpu_s:.2f}s each, {threads} OpenMP threads"}
         parity = {"rows": ns, "assignment_equal": bool(np.array_equal(asg[:ns].cpu().numpy(), oa)),
                   "codes_equal": bool(np.array_equal(codes[:2000].cpu().numpy(),
                                                      oracle.pq_encode(x[:2000], oa[:2000], hcent, cb.cpu().numpy(),
@@ -565,11 +677,13 @@ def run_c5(args, torch, fg, dev):
         ns = min(args.cpu_queries, nq, 1000)
         threads = oracle.lib.orc_max_threads()
         hgraph = graph.cpu().numpy()
-        t0 = time.perf_counter()
-        oid, od, _ = oracle.graph_search(q[:ns], x, hgraph, k, itopk, width, max_iter, seed=1)
-        cpu_s = time.perf_counter() - t0
+        cpu_s, (oid, od, _) = cpu_timed(
+            lambda: oracle.graph_search(q[:ns], x, hgraph, k, itopk, width, max_iter, seed=1),
+            warm=lambda: oracle.graph_search(q[:50], x, hgraph, k, itopk, width, max_iter, seed=1))
         cpu = {"value": round(ns / cpu_s, 1), "unit": "queries/s", "cores": threads, "kind": "port",
-               "sample": f"first {ns} of the {nq} queries, same graph, {cpu_s:.1f}s wall on {threads} OpenMP threads"}
+               "cpu_model": cpu_model(),
+               "sample": f"first {ns} of the {nq} queries, same graph; median of 3 runs after a warm-up, "
+                         f"{cpu_s:.2f}s each, {threads} OpenMP threads"}
         parity = {"queries": ns, "ids_equal": bool(np.array_equal(gid[:ns], oid)),
                   "dists_bit_equal": bool(np.array_equal(gd[:ns].view(np.uint32), od.view(np.uint32)))}
         log(f"cpu baseline {cpu['value']} QPS on {threads} threads; parity {parity}")

@@ -33,7 +33,7 @@ __all__ = [
     "FgpuError", "lib", "lib_path", "Index", "gen_gmm", "l2_topk", "kmeans_fit", "kmeans_update",
     "fixed_shift", "pq_train", "pq_encode", "build_ivfpq", "write_ivf_data", "read_ivf_data",
     "write_fvecs", "read_fvecs", "read_ivecs", "probe_counts", "rerank", "knn_exact", "graph_search",
-    "debug_set_spin_limit", "FAULT_ID", "prune_probes",
+    "debug_set_spin_limit", "debug_set_list_skip", "stream_read", "FAULT_ID", "prune_probes",
 ]
 
 lib_path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib", "libfusiongpu.so")
@@ -53,6 +53,9 @@ _SIGS = {
     "fgpu_index_faults": (_i32, [_vp, _vp, _c.POINTER(_c.c_ulonglong), _i32]),
     "fgpu_index_check": (_i32, [_vp, _vp]),
     "fgpu_debug_set_spin_limit": (None, [_i32]),
+    "fgpu_debug_set_list_skip": (None, [_i32]),
+    "fgpu_stream_read_grid": (_i32, []),
+    "fgpu_stream_read": (_i32, [_vp, _sz, _vp, _vp]),
     "fgpu_coarse_workspace_bytes": (_sz, [_i32, _i32]),
     "fgpu_coarse_search": (_i32, [_vp, _vp, _i32, _i32, _f32, _vp, _vp, _vp, _sz, _vp]),
     "fgpu_coarse_graph_workspace_bytes": (_sz, [_i32, _i32]),
@@ -310,6 +313,21 @@ def read_ivecs(path) -> np.ndarray:
 def debug_set_spin_limit(polls: int):
     """Test hook (fgpu_debug_set_spin_limit): polls before a scan wait gives up; 0 = automatic."""
     lib.fgpu_debug_set_spin_limit(int(polls))
+
+
+def debug_set_list_skip(enabled: bool):
+    """Measurement hook (fgpu_debug_set_list_skip): False makes the plain scan read every probed list."""
+    lib.fgpu_debug_set_list_skip(int(bool(enabled)))
+
+
+def stream_read(data, stream=None):
+    """Stream a contiguous device tensor through 16-byte loads (fgpu_stream_read), for a measured read rate."""
+    torch = _torch()
+    with _on(stream):
+        if not (torch.is_tensor(data) and data.is_cuda and data.is_contiguous()):
+            raise ValueError("stream_read: expected a contiguous device tensor")
+        sink = torch.empty(lib.fgpu_stream_read_grid(), dtype=torch.int64, device="cuda")
+        _check(lib.fgpu_stream_read(_dev_ptr(data), data.numel() * data.element_size(), _dev_ptr(sink), _stream()))
 
 
 # --------------------------------------------------------------------------- index + search

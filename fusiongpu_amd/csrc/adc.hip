@@ -534,7 +534,7 @@ __global__ __launch_bounds__(kSpecWaves * kWave, 4) void adc_flow_kernel(AdcArgs
             const uint64_t thr = s_thr[s];
             const float thr_hi = __uint_as_float((uint32_t)(thr >> 32)) * (1.0f + 0x1p-16f);
             const int g = f + lane;
-            const bool cand = g < nv && f_lb[s][g] > thr_hi;
+            const bool cand = a.list_skip && g < nv && f_lb[s][g] > thr_hi;
             const uint64_t run = ~__ballot(cand);  // bit i clear: list f + i is skippable
             const int p = run ? __ffsll((unsigned long long)run) - 1 : kWave;
             if (lane < p && g < nv) s_dec[s][g] = kSkipped;

@@ -1,0 +1,44 @@
+// bandwidth.hip -- a streaming read of device memory, to measure the HBM read
+// rate the roofline figures are set against (no reference counterpart).
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace fgpu {
+namespace {
+
+// Grid-stride 16-byte loads, four independent ones in flight per lane; the
+// XOR of everything read goes to one sink slot per workgroup.
+__global__ __launch_bounds__(256) void stream_read_kernel(const uint4* __restrict__ d, size_t n16,
+                                                          unsigned long long* __restrict__ sink) {
+  const size_t stride = (size_t)gridDim.x * 256;
+  size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  uint32_t acc = 0;
+  for (; i + 3 * stride < n16; i += 4 * stride) {
+    const uint4 a = d[i], b = d[i + stride], c = d[i + 2 * stride], e = d[i + 3 * stride];
+    acc ^= a.x ^ a.y ^ a.z ^ a.w ^ b.x ^ b.y ^ b.z ^ b.w ^ c.x ^ c.y ^ c.z ^ c.w ^ e.x ^ e.y ^ e.z ^ e.w;
+  }
+  for (; i < n16; i += stride) {
+    const uint4 a = d[i];
+    acc ^= a.x ^ a.y ^ a.z ^ a.w;
+  }
+  __shared__ uint32_t red[256];
+  red[threadIdx.x] = acc;
+  __syncthreads();
+  for (int o = 128; o > 0; o >>= 1) {
+    if ((int)threadIdx.x < o) red[threadIdx.x] ^= red[threadIdx.x + o];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) sink[blockIdx.x] = red[0];
+}
+
+}  // namespace
+
+fgpu_status launch_stream_read(const void* d, size_t bytes, unsigned long long* sink, int grid, hipStream_t s) {
+  if (bytes == 0 || grid <= 0) return FGPU_OK;
+  hipLaunchKernelGGL(stream_read_kernel, dim3((unsigned)grid), dim3(256), 0, s, reinterpret_cast<const uint4*>(d),
+                     bytes / 16, sink);
+  FGPU_HIP(hipGetLastError());
+  return FGPU_OK;
+}
+
+}  // namespace fgpu

@@ -92,6 +92,8 @@ fgpu_status finish_index(fgpu_index* ix, hipStream_t s) {
 // Poll limit of the flow kernel's bounded waits set by fgpu_debug_set_spin_limit
 // (0 = derived per launch from nprobe and the longest list).
 std::atomic<int> g_spin_override{0};
+// fgpu_debug_set_list_skip: 0 turns the plain scan's list lower bound off.
+std::atomic<int> g_list_skip{1};
 
 AdcArgs adc_args(const fgpu_index* ix, const float* dq, int nq, const uint32_t* probes, const float* probe_dists,
                  int nprobe, int k, int32_t* out_ids, float* out_d) {
@@ -102,6 +104,7 @@ AdcArgs adc_args(const fgpu_index* ix, const float* dq, int nq, const uint32_t* 
   a.faults = ix->d_faults;
   a.max_list_len = ix->max_list_len;
   a.spin_limit = g_spin_override.load(std::memory_order_relaxed);
+  a.list_skip = g_list_skip.load(std::memory_order_relaxed);
   return a;
 }
 
@@ -331,6 +334,22 @@ fgpu_status fgpu_index_check(const fgpu_index* ix, void* stream) {
 }
 
 void fgpu_debug_set_spin_limit(int polls) { g_spin_override.store(polls > 0 ? polls : 0); }
+
+void fgpu_debug_set_list_skip(int enabled) { g_list_skip.store(enabled ? 1 : 0); }
+
+int fgpu_stream_read_grid(void) {
+  int dev = 0, cus = 256;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+    cus = 256;
+  return cus * 8;
+}
+
+fgpu_status fgpu_stream_read(const void* d, size_t bytes, unsigned long long* d_sink, void* stream) {
+  FGPU_CHECK(d && d_sink && bytes % 16 == 0 && ((uintptr_t)d & 15) == 0, FGPU_ERR_ARG,
+             "stream_read: need 16-byte aligned data, a size multiple of 16 and a sink");
+  return launch_stream_read(d, bytes, d_sink, fgpu_stream_read_grid(), as_stream(stream));
+}
 
 size_t fgpu_search_workspace_bytes(int nq, int nlist, int nprobe) {
   return carve_bytes<uint32_t>((size_t)nq * nprobe) + carve_bytes<float>((size_t)nq * nprobe) +

@@ -67,6 +67,9 @@ struct AdcArgs {
   // workgroup gets id kFaultId / distance NaN in every slot.
   unsigned long long* faults = nullptr;
   int max_list_len = 0;
+  // 0: never skip a list on its lower bound (timing of the scan reading every
+  // probed list; results are the same).
+  int list_skip = 1;
 };
 // Id written to every slot of a query whose result a bounded-wait give-up may
 // have touched (the reference's padding id is -1; it never writes -2).
@@ -171,6 +174,11 @@ struct TuneStatsArgs {
   float* kth_pq;            // [npairs]
 };
 fgpu_status launch_tune_list_stats(const TuneStatsArgs& a, int npairs, hipStream_t s);
+
+// ---- bandwidth.hip --------------------------------------------------------------
+// Reads `bytes` (a multiple of 16) from d with 16-byte loads; one XOR per
+// workgroup goes to sink[blockIdx.x] so the loads cannot be dropped.
+fgpu_status launch_stream_read(const void* d, size_t bytes, unsigned long long* sink, int grid, hipStream_t s);
 
 // ---- build.hip ----------------------------------------------------------------
 fgpu_status launch_probe_counts(const uint32_t* probes, int nq, int nprobe, int nlist, const int32_t* offsets,

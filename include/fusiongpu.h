@@ -98,6 +98,19 @@ fgpu_status fgpu_index_check(const fgpu_index* idx, void* stream);
  * process (0 = the automatic limit).  A tiny limit makes give-ups certain
  * while every wave still runs to the end of the kernel. */
 void fgpu_debug_set_spin_limit(int polls);
+/* Measurement hook: with enabled = 0 every later plain-scan launch in the
+ * process reads every probed list instead of skipping the lists whose lower
+ * bound exceeds the running k-th distance (results are the same; only the
+ * work differs).  1 restores the default. */
+void fgpu_debug_set_list_skip(int enabled);
+
+/* ---- measurement (no reference counterpart) ---------------------------- */
+
+/* Streams `bytes` (a multiple of 16, 16-byte aligned) of device memory
+ * through 16-byte loads, to measure the achievable HBM read rate next to the
+ * 8 TB/s figure.  d_sink: fgpu_stream_read_grid() uint64 values, overwritten. */
+int fgpu_stream_read_grid(void);
+fgpu_status fgpu_stream_read(const void* d_data, size_t bytes, unsigned long long* d_sink, void* stream);
 
 /* ---- search: coarse quantizer (A2 + A3) -------------------------------- */
 

@@ -8,7 +8,9 @@ package, and only as the checker or the timed CPU baseline.
 """
 from __future__ import annotations
 
+import collections
 import ctypes
+import math
 import os
 
 import numpy as np
@@ -489,6 +491,63 @@ def build_ivfpq(x, nlist, pq_m, kmeans_iters=20, init_mode=0, seed=42, pq_iters=
     codes = pq_encode(x, assign, cent, cb, 1, nthreads)
     offs, ids, lc = build_lists(assign, nlist, codes)
     return offs, ids, lc, cent, cb
+
+
+def rebalance_buckets(buckets, n_total, nlist, split):
+    """The queue-based recursive split of build_global (build_global.cu:62-169), restated.  buckets: the
+    initial (rows, centroid) pairs in cluster order; n_total: vectors over all buckets; nlist: the initial
+    cluster count (K_CLUSTERS).  avg = n_total / nlist in double; a bucket is final when its size is <= (size_t)
+    (2 avg) or < 32; otherwise sub_k = ceil(size / avg), at least 2, at most size / 2 (integer division), and
+    split(rows, sub_k) returns the sub_k children (rows, centroid) in child order, whose non-empty ones go to the
+    back of the queue.  Empty initial buckets are dropped.  Returns (final buckets in order, split count)."""
+    avg = float(n_total) / float(nlist)
+    thr = int(avg * 2)
+    queue = collections.deque((r, c) for r, c in buckets if len(r) > 0)
+    final, splits = [], 0
+    while queue:
+        rows, c = queue.popleft()
+        sz = len(rows)
+        if sz <= thr or sz < 32:
+            final.append((rows, c))
+            continue
+        splits += 1
+        sub_k = int(math.ceil(sz / avg))
+        sub_k = max(sub_k, 2)
+        sub_k = min(sub_k, sz // 2)
+        for ch_rows, ch_c in split(rows, sub_k):
+            if len(ch_rows) > 0:
+                queue.append((ch_rows, ch_c))
+    return final, splits
+
+
+def build_global(x, nlist, pq_m, kmeans_iters=20, pq_iters=8, sample_size=50000, init_mode=0, seed=42,
+                 rebalance=True, nthreads=0):
+    """build_global restated (build_global.cu:21-258): k-means over every row, assignment, the recursive split
+    (rebalance_buckets, each split a 15-iteration k-means of the bucket's rows with the same initialisation and
+    seed, then their exact assignment; build_global.cu:112-142), PQ training on the final lists, device-form
+    encoding, lists in final order with each list's rows ascending.  Without rebalancing every initial list stays,
+    empty ones included.  Returns (offsets, ids, codes, centroids, codebook, split count)."""
+    x = f32(x)
+    n = x.shape[0]
+    cent, a0 = kmeans_fit(x, nlist, kmeans_iters, init_mode, seed, nthreads)
+    buckets = [(np.nonzero(a0 == c)[0].astype(np.int32), cent[c]) for c in range(nlist)]
+
+    def split(rows, sub_k):
+        sub = np.ascontiguousarray(x[rows])
+        sc, _ = kmeans_fit(sub, sub_k, 15, init_mode, seed, nthreads)
+        la = kmeans_assign(sub, sc, nthreads)
+        return [(rows[la == j], sc[j]) for j in range(sub_k)]
+
+    final, splits = rebalance_buckets(buckets, n, nlist, split) if rebalance else (buckets, 0)
+    L = len(final)
+    assign = np.empty(n, np.int32)
+    for c, (rows, _) in enumerate(final):
+        assign[rows] = c
+    fc = np.ascontiguousarray(np.stack([c for _, c in final]).astype(np.float32))
+    cb = pq_train(x, assign, fc, pq_m, sample_size, pq_iters, nthreads)
+    codes = pq_encode(x, assign, fc, cb, 1, nthreads)
+    offs, ids, lc = build_lists(assign, L, codes)
+    return offs, ids, lc, fc, cb, splits
 
 
 # --------------------------------------------------------------------------- the reference's own code

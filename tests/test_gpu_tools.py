@@ -1,7 +1,8 @@
 """The command-line tools on the GPU: build_global writes the same index files
-as the library build, its rebalancing keeps the reference's split invariants
-(build_global.cu:62-169), and search_pipeline returns the library path's ids
-and the reference's recall figures (search_pipeline.cu:531-557, 636-645)."""
+as the library build and, with its recursive rebalancing (build_global.cu:62-169),
+the same bytes as the oracle's statement of it; search_pipeline returns the
+oracle's ids for its per-batch path and the reference's recall figures
+(search_pipeline.cu:531-557, 636-645)."""
 import os
 import re
 import subprocess
@@ -76,6 +77,12 @@ def test_build_global_rebalances_oversized_lists(tmp_path):
     assert m and "Split Ops" in out
     offs, ids, codes, cent = fg.read_ivf_data(res / "ivf_data.bin", 32, 128)
     L = int(m.group(1))
+    # byte for byte the oracle's statement of build_global with its queue (build_global.cu:21-258)
+    cb = np.fromfile(res / "global_pq_codebook.bin", np.float32).reshape(32, 256, 4)
+    want = oracle.build_global(x, 64, 32, kmeans_iters=4, pq_iters=2, sample_size=3000)
+    for g, w, name in zip((offs, ids, codes, cent, cb), want, ["offsets", "ids", "codes", "centroids", "codebook"]):
+        assert np.array_equal(np.asarray(g).view(np.uint8), np.asarray(w).view(np.uint8)), name
+    assert f"Split Ops: {want[5]}" in out
     assert offs.shape[0] == L + 1 and offs[0] == 0 and offs[-1] == 30000 and np.all(np.diff(offs) > 0)
     assert np.array_equal(np.sort(ids), np.arange(30000))
     sizes = np.diff(offs)
@@ -104,13 +111,13 @@ def test_search_pipeline_matches_library_path(tmp_path):
                tmp_path / "out.ivecs", cwd=tmp_path)
     assert re.search(r"Total time: [\d.]+ ms, QPS: [\d.e+]+", out)
     got = _read_ivecs(tmp_path / "out.ivecs")
-    idx = fg.Index.load(res / "ivf_data.bin", res / "global_pq_codebook.bin", 128, 32)
-    dq, dx = torch.from_numpy(q).cuda(), torch.from_numpy(x).cuda()
-    pid, _ = idx.coarse_search(dq, 16, 100.0)
-    tid, td, tc, _, _ = idx.two_phase_search(dq, pid, 4, 30, 1.0, 500)
-    want, _, _ = fg.rerank(dq, dx, tid, tc, 10, 128, 0.1, 2)
-    assert np.array_equal(got, want.cpu().numpy())
-    idx.close()
+    # the oracle's per-batch path: exact coarse, two-phase scan, early-stopping rerank
+    offs, ids, codes, cent = fg.read_ivf_data(res / "ivf_data.bin", 32, 128)
+    cb = np.fromfile(res / "global_pq_codebook.bin", np.float32).reshape(32, 256, 4)
+    probes, _ = oracle.coarse(q, cent, 16, 100.0)
+    tid, _, tcnt, _, _ = oracle.search_two_phase(q, cent, cb, offs, ids, codes, probes, 4, 30, 1.0, 500)
+    want, _, _ = oracle.rerank(q, x, tid, tcnt, 10, 128, 0.1, 2)
+    assert np.array_equal(got, want)
     # the reference's recall: whole gt row as the hit set, repeated ids once, hits / (nq * k)
     m = re.search(r"Recall@1: ([\d.]+)%, Recall@10: ([\d.]+)%", out)
     assert m
@@ -132,14 +139,14 @@ def test_search_pipeline_graph_coarse_matches_library_path(tmp_path):
                tmp_path / "out.ivecs", cwd=tmp_path)
     assert "centroid graph: 256 nodes, degree 8, itopk 32" in out
     got = _read_ivecs(tmp_path / "out.ivecs")
-    idx = fg.Index.load(res / "ivf_data.bin", res / "global_pq_codebook.bin", 128, 32)
-    dq, dx = torch.from_numpy(q).cuda(), torch.from_numpy(x).cuda()
-    g = idx.coarse_graph_build(8)
-    pid, _ = idx.coarse_graph_search(dq, 24, g, itopk=32, width=4, max_iter=200, seed=1, prune_ratio=100.0)
-    tid, td, tc, _, _ = idx.two_phase_search(dq, pid, 6, 20, 1.0, 400)
-    want, _, _ = fg.rerank(dq, dx, tid, tc, 10, 128, 0.1, 2)
-    assert np.array_equal(got, want.cpu().numpy())
-    idx.close()
+    # the oracle: its centroid graph and walk, then the same two-phase scan and rerank
+    offs, ids, codes, cent = fg.read_ivf_data(res / "ivf_data.bin", 32, 128)
+    cb = np.fromfile(res / "global_pq_codebook.bin", np.float32).reshape(32, 256, 4)
+    g = oracle.coarse_graph_build(cent, 8)
+    probes, _ = oracle.coarse_graph(q, cent, g, 24, itopk=32, width=4, max_iter=200, seed=1, prune_ratio=100.0)
+    tid, _, tcnt, _, _ = oracle.search_two_phase(q, cent, cb, offs, ids, codes, probes, 6, 20, 1.0, 400)
+    want, _, _ = oracle.rerank(q, x, tid, tcnt, 10, 128, 0.1, 2)
+    assert np.array_equal(got, want)
 
 
 def test_build_global_elbow_sweep(tmp_path):

@@ -343,3 +343,73 @@ def test_gen_gmm_moments_and_determinism():
     _, lab = kmeans2(a.astype(np.float64), 4, seed=0, minit="++")
     resid = np.concatenate([a[lab == j] - a[lab == j].mean(0) for j in range(4) if np.any(lab == j)])
     assert 0.08 < resid.std() < 0.2
+
+
+# --------------------------------------------------------------------------- build_global's rebalancing queue
+def _stub_split(rows, sub_k):
+    """Deterministic stand-in for the local k-means: rows cut into sub_k contiguous parts, the first part
+    carrying every row after a marker (to make a skewed child); centroid = the child's index."""
+    parts = np.array_split(rows, sub_k)
+    return [(p, np.float32(j)) for j, p in enumerate(parts)]
+
+
+def test_rebalance_queue_order_and_thresholds():
+    """build_global.cu:62-169 by hand: avg = 100 / 4 = 25, threshold (size_t)(2 avg) = 50, min 32.
+    Initial buckets of sizes 10, 0, 60, 30: the empty one is dropped, 10 and 30 are final at once (in
+    queue order), 60 splits into ceil(60 / 25) = 3 children of 20 appended behind them (FIFO)."""
+    rows = np.arange(100, dtype=np.int32)
+    buckets = [(rows[:10], 0), (rows[:0], 1), (rows[10:70], 2), (rows[70:], 3)]
+    final, splits = oracle.rebalance_buckets(buckets, 100, 4, _stub_split)
+    assert splits == 1
+    assert [len(r) for r, _ in final] == [10, 30, 20, 20, 20]
+    assert [c for _, c in final] == [0, 3, 0, 1, 2]
+    assert np.array_equal(np.concatenate([r for r, _ in final]), np.r_[rows[:10], rows[70:], rows[10:70]])
+
+
+def test_rebalance_resplits_oversized_children_at_the_back_of_the_queue():
+    """A child still above the threshold is split again after the buckets queued before it; sub_k is at
+    least 2 and at most size / 2; a bucket below 32 is final whatever its size against the threshold."""
+    calls = []
+
+    def split(rows, sub_k):
+        calls.append((len(rows), sub_k))
+        if len(rows) == 400:  # one heavy child of 300, the rest split evenly
+            return [(rows[:300], 0), (rows[300:350], 1), (rows[350:], 2)]
+        return [(p, j) for j, p in enumerate(np.array_split(rows, sub_k))]
+
+    rows = np.arange(420, dtype=np.int32)
+    # avg = 420 / 10 = 42, threshold 84
+    final, splits = oracle.rebalance_buckets([(rows[:400], "a"), (rows[400:], "b")], 420, 10, split)
+    # 400 -> sub_k ceil(400/42) = 10, then 300 -> ceil(300/42) = 8
+    assert calls == [(400, 10), (300, 8)]
+    assert splits == 2
+    assert [len(r) for r, _ in final] == [20, 50, 50] + [38] * 4 + [37] * 4
+    # the clamp: 33 rows with avg 1 (threshold 2) -> sub_k = min(33, 33 // 2) = 16
+    calls.clear()
+    oracle.rebalance_buckets([(np.arange(33, dtype=np.int32), 0)], 33, 33,
+                             lambda r, k: calls.append((len(r), k)) or [(r[:0], 0)] * k)
+    assert calls == [(33, 16)]
+    # 31 rows above a threshold of 2 stay whole (below the 32-row minimum)
+    final, splits = oracle.rebalance_buckets([(np.arange(31, dtype=np.int32), 0)], 31, 31, split)
+    assert splits == 0 and len(final) == 1
+
+
+def test_build_global_without_rebalancing_is_the_plain_build():
+    x = oracle.gen_gmm(3000, 32, 8, seed=12, sig_lo=0.1)
+    a = oracle.build_global(x, 16, 8, kmeans_iters=4, pq_iters=2, sample_size=1000, rebalance=False)
+    b = oracle.build_ivfpq(x, 16, 8, kmeans_iters=4, pq_iters=2, sample_size=1000)
+    for u, v in zip(a[:5], b):
+        assert np.array_equal(np.asarray(u).view(np.uint8), np.asarray(v).view(np.uint8))
+    assert a[5] == 0
+
+
+def test_build_global_rebalancing_keeps_every_row_once():
+    x = oracle.gen_gmm(6000, 32, 3, seed=13, sig_lo=0.05, sig_hi=0.3)
+    offs, ids, codes, cent, cb, splits = oracle.build_global(x, 16, 8, kmeans_iters=3, pq_iters=2, sample_size=1000)
+    L = offs.shape[0] - 1
+    assert splits > 0 and L > 16 and cent.shape == (L, 32)
+    assert np.array_equal(np.sort(ids), np.arange(6000))
+    sizes = np.diff(offs)
+    assert np.all((sizes <= int(6000 / 16 * 2)) | (sizes < 32)) and np.all(sizes > 0)
+    lid = np.repeat(np.arange(L), sizes)
+    assert np.all(np.diff(ids)[np.diff(lid) == 0] > 0)  # ascending inside each list
