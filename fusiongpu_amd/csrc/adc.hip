@@ -370,6 +370,8 @@ __global__ __launch_bounds__(kSpecWaves * kWave, 4) void adc_flow_kernel(AdcArgs
   __shared__ uint64_t s_tree[2][kScanWaves - 1][2][kWave];
   __shared__ int s_arr[2][kScanWaves - 1];  // arrivals per tree node
   __shared__ int s_ready[2], s_free[2], s_lbdone[2];
+  __shared__ int s_q[2];  // query of each slot; -1 once the workgroup's queries are done
+  __shared__ unsigned long long s_tend;  // instrumentation: the workgroup's end
   __shared__ int s_built[kLutBufs], s_done[kLutBufs];  // per LUT buffer
   __shared__ int s_fault;                               // a wave of this workgroup gave up a wait
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -379,9 +381,15 @@ __global__ __launch_bounds__(kSpecWaves * kWave, 4) void adc_flow_kernel(AdcArgs
   const uint32_t NL = (uint32_t)a.nlist;
   const int G = (int)gridDim.x;
   const int nqw = a.nq > (int)blockIdx.x ? (a.nq - (int)blockIdx.x + G - 1) / G : 0;  // this workgroup's queries
+  // Dynamic claims: after its first query (blockIdx.x) a workgroup takes the
+  // next unclaimed query from the counter a.qctr (reset to the grid size
+  // before the launch), so workgroups finish within about one query of each
+  // other.  Otherwise (no counter) workgroup g takes g, g + G, g + 2G, ...
+  const bool dyn = a.qctr != nullptr && a.probe_dists != nullptr;
 
   if (tid < 2) {
     s_nv[tid] = 0;
+    s_q[tid] = -1;
     s_ready[tid] = 0;
     s_free[tid] = 0;
     s_lbdone[tid] = 0;
@@ -390,7 +398,10 @@ __global__ __launch_bounds__(kSpecWaves * kWave, 4) void adc_flow_kernel(AdcArgs
     s_built[tid] = 0;
     s_done[tid] = 0;
   }
-  if (tid == 0) s_fault = 0;
+  if (tid == 0) {
+    s_fault = 0;
+    s_tend = 0;
+  }
   const WaitCtl wc{a.spin_limit, &s_fault, a.faults};
   const int total = (int)a.total;
   __syncthreads();
@@ -426,18 +437,29 @@ __global__ __launch_bounds__(kSpecWaves * kWave, 4) void adc_flow_kernel(AdcArgs
     auto any_list = [](int) { return true; };
     // Set-up of this workgroup's query i into slot i & 1 (all builder waves).
     auto setup = [&](int i) {
-      const int s = i & 1, q = (int)blockIdx.x + i * G;
+      const int s = i & 1;
       lds_wait_at_least<kLazySleep>(&s_free[s], i / 2, wc);  // the slot's previous query is written out
-      const uint32_t* pr = a.probes + (size_t)q * P;
-      const uint32_t pl_lane = lane < P ? pr[lane] : kPruned;
+      // The query of this slot: -1 past the workgroup's last one, which then
+      // sets up an empty slot that tells every wave to stop.  With dynamic
+      // claims only wave 0 knows it (the other builder waves have no set-up
+      // work when the coarse distances are given).
+      int q = (int)blockIdx.x + i * G;
+      if (dyn) {
+        int c = 0;
+        if (wave == 0 && lane == 0) c = i == 0 ? (int)blockIdx.x : atomicAdd(a.qctr, 1);
+        q = wave == 0 ? __builtin_amdgcn_readfirstlane(c) : -1;
+      }
+      if (q >= a.nq) q = -1;
+      const uint32_t* pr = a.probes + (size_t)(q >= 0 ? q : 0) * P;
+      const uint32_t pl_lane = q >= 0 && lane < P ? pr[lane] : kPruned;
       // With the coarse distances at hand, wave 0 bounds every list from them
       // (one lane a probe) and the other builder waves have nothing to do.
       float lb_lane = 0.0f;
       if (a.probe_dists) {
         if (wave == 0 && pl_lane < NL) lb_lane = list_lower_bound(a.probe_dists[(size_t)q * P + lane], a.rmax[pl_lane]);
       }
-      const float qa = !a.probe_dists && lane < D ? a.queries[(size_t)q * D + lane] : 0.0f;
-      const float qb = !a.probe_dists && lane + kWave < D ? a.queries[(size_t)q * D + lane + kWave] : 0.0f;
+      const float qa = !a.probe_dists && q >= 0 && lane < D ? a.queries[(size_t)q * D + lane] : 0.0f;
+      const float qb = !a.probe_dists && q >= 0 && lane + kWave < D ? a.queries[(size_t)q * D + lane + kWave] : 0.0f;
       // Otherwise each builder wave computes the bounds of its probes
       // p = wave + 8 j from the centroid rows, four lists at a time.
       constexpr int kBatch = 4;
@@ -471,6 +493,13 @@ __global__ __launch_bounds__(kSpecWaves * kWave, 4) void adc_flow_kernel(AdcArgs
       }
       lds_signal_add(&s_lbdone[s], 1);
       if (wave == 0) {
+        // The query's result row starts as the fault marker; its root write
+        // replaces it.  A row whose query a give-up kept from completing thus
+        // never holds silently wrong or stale values.
+        if (q >= 0 && lane < k) {
+          a.out_ids[(size_t)q * k + lane] = kFaultId;
+          a.out_d[(size_t)q * k + lane] = __builtin_nanf("");
+        }
         // Compact the usable probes (in range, non-empty) in coarse order and
         // number their chunks: f_cst[f] = first chunk of list f.
         int st = 0, n = 0;
@@ -501,6 +530,7 @@ __global__ __launch_bounds__(kSpecWaves * kWave, 4) void adc_flow_kernel(AdcArgs
         if (lane == 0) {
           f_cst[s][nv] = total;
           s_nv[s] = nv;
+          s_q[s] = q;
           s_thr[s] = kNoThr;
 
         }
@@ -511,9 +541,11 @@ __global__ __launch_bounds__(kSpecWaves * kWave, 4) void adc_flow_kernel(AdcArgs
     int nbuilt = 0, need0 = 0, need1 = 0, need2 = 0, nskip = 0;
     long long t_su = 0;
     if (nqw > 0) setup(0);
-    for (int i = 0; i < nqw; ++i) {
-      const int s = i & 1, q = (int)blockIdx.x + i * G;
+    for (int i = 0; dyn || i < nqw; ++i) {
+      const int s = i & 1;
       lds_wait_at_least(&s_ready[s], i / 2 + 1, wc);
+      const int q = dyn ? s_q[s] : (int)blockIdx.x + i * G;
+      if (q < 0 || q >= a.nq) break;
       const int nv = s_nv[s];
       const float qv = lane < RW ? a.queries[(size_t)q * D + wave * RW + lane] : 0.0f;
       // This wave's centroid coordinates of the next list that may be built,
@@ -586,7 +618,7 @@ __global__ __launch_bounds__(kSpecWaves * kWave, 4) void adc_flow_kernel(AdcArgs
           need2 += nch;
         f = cnext_f;
       }
-      if (i + 1 < nqw) {
+      if (dyn || i + 1 < nqw) {
         const long long t0 = a.stats ? clock64() : 0;
         setup(i + 1);
         if (a.stats) t_su += clock64() - t0;
@@ -609,9 +641,12 @@ __global__ __launch_bounds__(kSpecWaves * kWave, 4) void adc_flow_kernel(AdcArgs
     uint4 w0[C::NV4], w1[C::NV4];
     int i0 = kPadId, i1 = kPadId;
     unsigned nload = 0;  // vectors whose codes this wave loaded
-    for (int i = 0; i < nqw; ++i) {
-      const int s = i & 1, q = (int)blockIdx.x + i * G;
+    long long t_end = 0;
+    for (int i = 0; dyn || i < nqw; ++i) {
+      const int s = i & 1;
       lds_wait_at_least(&s_ready[s], i / 2 + 1, wc);
+      const int q = dyn ? s_q[s] : (int)blockIdx.x + i * G;
+      if (q < 0 || q >= a.nq) break;
       const int nv = s_nv[s];
       const int* cst = f_cst[s];
       uint64_t lk = kPadKey, own = kNoThr;
@@ -690,13 +725,19 @@ __global__ __launch_bounds__(kSpecWaves * kWave, 4) void adc_flow_kernel(AdcArgs
       if (root) {
         write_topk(lk, q, k, a, __hip_atomic_load(&s_fault, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) != 0);
         lds_signal_add(&s_free[s], 1);
-        if (a.stats && lane == 0 && i == nqw - 1) atomicAdd(&a.stats[6], (unsigned long long)(clock64() - t_start));
+        if (a.stats) t_end = clock64() - t_start;
       }
     }
+    // The workgroup's end: the latest of the scanner waves' last root writes.
+    if (a.stats && lane == 0 && t_end > 0) atomicMax(&s_tend, (unsigned long long)t_end);
     if (a.stats && lane == 0) {
       atomicAdd(&a.stats[0], (unsigned long long)nload);
       if (wave == kBuilderWaves) atomicAdd(&a.stats[5], (unsigned long long)(clock64() - t_start));
     }
+  }
+  if (a.stats) {  // every wave of the workgroup gets here (a.stats is uniform)
+    __syncthreads();
+    if (tid == 0) atomicAdd(&a.stats[6], s_tend);
   }
 }
 
@@ -716,6 +757,13 @@ int resident_groups(K kernel, int threads, std::atomic<int> (&cached)[64]) {
   return v;
 }
 
+// The claim counter of a launch starts at the grid size: the first G queries
+// are the workgroups' static first ones.  A kernel, not a memset, so that a
+// captured graph replays it correctly.
+__global__ void qctr_reset_kernel(int* qctr, int grid) {
+  if (threadIdx.x == 0) *qctr = grid;
+}
+
 template <int D, int M>
 fgpu_status launch_flow(const AdcArgs& args, hipStream_t s) {
   FGPU_CHECK(args.nprobe <= 64, FGPU_ERR_UNSUPPORTED, "adc: nprobe must be <= 64");
@@ -724,6 +772,7 @@ fgpu_status launch_flow(const AdcArgs& args, hipStream_t s) {
   if (a.spin_limit <= 0) a.spin_limit = (int)flow_spin_limit(a.nprobe, a.max_list_len);
   static std::atomic<int> cached[64];
   const int grid = std::min(a.nq, resident_groups(adc_flow_kernel<D, M>, kSpecWaves * kWave, cached));
+  if (a.qctr) hipLaunchKernelGGL(qctr_reset_kernel, dim3(1), dim3(64), 0, s, a.qctr, grid);
   hipLaunchKernelGGL((adc_flow_kernel<D, M>), dim3((unsigned)grid), dim3(kSpecWaves * kWave), 0, s, a);
   FGPU_HIP(hipGetLastError());
   return FGPU_OK;

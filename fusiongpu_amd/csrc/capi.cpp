@@ -353,7 +353,7 @@ fgpu_status fgpu_stream_read(const void* d, size_t bytes, unsigned long long* d_
 
 size_t fgpu_search_workspace_bytes(int nq, int nlist, int nprobe) {
   return carve_bytes<uint32_t>((size_t)nq * nprobe) + carve_bytes<float>((size_t)nq * nprobe) +
-         fgpu_coarse_workspace_bytes(nq, nlist);
+         carve_bytes<int>(1) + fgpu_coarse_workspace_bytes(nq, nlist);
 }
 
 fgpu_status fgpu_search(const fgpu_index* ix, const float* dq, int nq, int nprobe, int k, float prune_ratio,
@@ -362,9 +362,14 @@ fgpu_status fgpu_search(const fgpu_index* ix, const float* dq, int nq, int nprob
   Carve cv(ws, ws_bytes);
   uint32_t* pid = cv.take<uint32_t>((size_t)nq * nprobe);
   float* pd = cv.take<float>((size_t)nq * nprobe);
+  int* qctr = cv.take<int>(1);
   FGPU_CHECK(cv.ok(), FGPU_ERR_WORKSPACE, "search: workspace too small");
   FGPU_TRY(fgpu_coarse_search(ix, dq, nq, nprobe, prune_ratio, pid, pd, cv.base + cv.used, ws_bytes - cv.used, stream));
-  return fgpu_adc_search(ix, dq, nq, pid, pd, nprobe, k, d_out_ids, d_out_dists, stream);
+  FGPU_CHECK(nq >= 0 && k >= 1, FGPU_ERR_ARG, "search: bad sizes");
+  FGPU_CHECK(adc_supported(ix->dim, ix->m), FGPU_ERR_UNSUPPORTED, "search: no kernel for this (dim, pq_m)");
+  AdcArgs a = adc_args(ix, dq, nq, pid, pd, nprobe, k, d_out_ids, d_out_dists);
+  a.qctr = qctr;  // the scan claims queries dynamically
+  return launch_adc_plain(ix->dim, ix->m, a, as_stream(stream));
 }
 
 // ---------------------------------------------------------------------------

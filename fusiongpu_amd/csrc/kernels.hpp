@@ -70,6 +70,9 @@ struct AdcArgs {
   // 0: never skip a list on its lower bound (timing of the scan reading every
   // probed list; results are the same).
   int list_skip = 1;
+  // Optional device int (workspace) for dynamic query claims of the flow
+  // kernel, which resets it on the launch stream; needs probe_dists.
+  int* qctr = nullptr;
 };
 // Id written to every slot of a query whose result a bounded-wait give-up may
 // have touched (the reference's padding id is -1; it never writes -2).

@@ -77,6 +77,39 @@ def test_forced_give_ups_are_counted_and_mark_results():
     idx.close()
 
 
+def test_forced_give_ups_with_dynamic_query_claims():
+    """search (coarse, then the scan with queries claimed from a counter):
+    rows a give-up kept from completing keep the marker written at set-up."""
+    _say("faults: dynamic claims, spin limit 1")
+    rng = np.random.default_rng(73)
+    dim, m, nlist, nq, k = 128, 32, 48, 3000, 10
+    offs, ids, lc, cent, cb = _index(rng, 40000, dim, m, nlist)
+    q = rng.standard_normal((nq, dim)).astype(np.float32) * 0.7
+    probes, _ = oracle.coarse(q, cent, 12)
+    oid, od = oracle.search_plain(q, cent, cb, offs, ids, lc, probes, k)
+    idx = fg.Index.from_arrays(dim, m, offs, ids, lc, cent, cb)
+    dq = torch.from_numpy(q).cuda()
+    try:
+        fg.debug_set_spin_limit(1)
+        gid, gd = idx.search(dq, 12, k)
+        gid, gd = gid.cpu().numpy(), gd.cpu().numpy()
+        nf = idx.faults(reset=True)
+    finally:
+        fg.debug_set_spin_limit(0)
+    assert nf > 0
+    marked = np.all(gid == fg.FAULT_ID, axis=1)
+    assert marked.any()
+    assert np.isnan(gd[marked]).all()
+    rest = ~marked
+    assert np.array_equal(gid[rest], oid[rest])
+    assert np.array_equal(gd[rest].view(np.uint32), od[rest].view(np.uint32))
+    gid, gd = idx.search(dq, 12, k)
+    assert np.array_equal(gid.cpu().numpy(), oid)
+    assert np.array_equal(gd.cpu().numpy().view(np.uint32), od.view(np.uint32))
+    idx.check()
+    idx.close()
+
+
 def test_one_very_long_list_within_the_automatic_limit():
     """A list of 300k vectors (the flow kernel's waits then last a whole list
     scan) next to short ones: exact, and no wait gives up."""
