@@ -248,6 +248,45 @@ def test_kmeans_init_pp_definition():
     assert np.array_equal(cent, x[want])
 
 
+def test_kmeans_init_pp_never_picks_a_covered_point():
+    """D^2 seeding gives a point at distance 0 from a chosen centre weight 0:
+    with k equal to the number of distinct rows (each repeated many times) the
+    picks are exactly one row of each distinct value."""
+    rng = np.random.default_rng(13)
+    distinct = rng.standard_normal((12, 5)).astype(np.float32) * 3
+    x = distinct[rng.integers(0, 12, 600)]
+    x[:12] = distinct  # every value present
+    for seed in (1, 2, 3, 99):
+        cent, rows = oracle.kmeans_init_pp(x, 12, seed)
+        got = {tuple(r) for r in np.asarray(cent)}
+        assert len(got) == 12 and got == {tuple(r) for r in distinct}
+
+
+def test_kmeans_init_pp_second_pick_follows_d2():
+    """Across seeds, the second pick given the first is distributed as
+    d^2 / sum d^2 (a chi-square bound that d or d^4 weights fail)."""
+    x = np.array([[0.0], [1.0], [3.0], [7.0]], np.float32)
+    counts = np.zeros((4, 4))
+    for seed in range(4000):
+        _, rows = oracle.kmeans_init_pp(x, 2, seed)
+        counts[rows[0], rows[1]] += 1
+    for r0 in range(4):
+        n = counts[r0].sum()
+        assert n > 500
+        d2 = (x[:, 0] - x[r0, 0]) ** 2
+        p = d2 / d2.sum()
+        assert counts[r0, r0] == 0
+        exp = n * p
+        m = exp > 0
+        chi2 = float((((counts[r0][m] - exp[m]) ** 2) / exp[m]).sum())
+        assert chi2 < 16.3, (r0, counts[r0], exp)  # 3 cells, p < 0.001
+        for alt in (np.sqrt(d2), d2 ** 2):  # the bound separates neighbouring weightings
+            pa = alt / alt.sum()
+            ea = n * pa
+            ma = ea > 0
+            assert float((((counts[r0][ma] - ea[ma]) ** 2) / ea[ma]).sum()) > 16.3
+
+
 # ---------------------------------------------------------------- PQ (A15, A16) vs the reference's own code
 def test_pq_against_golden_fixture():
     g = np.load(GOLDEN)
