@@ -40,10 +40,11 @@ constexpr int kTRound = kTW * kVecPerWaveRound;      // vectors per workgroup ro
 constexpr int kSortMax = 4096;                       // keys of one final LDS sort (a run)
 constexpr int kRerankMax = 1 << 17;                  // rerank_m limit: at most 32 runs
 constexpr uint64_t kNoKey = ~0ull;                   // "no admission bound yet"
-// Phase 1 stages the eight sorted wave lists of up to kStage lists; all waves
+// Phase 1 stages the eight sorted wave lists of up to kStage lists; the waves
 // merge the staged lists in parallel when the stage is full and at the end of
-// phase 1, so no merge sits between two lists.
-constexpr int kStage = 16;
+// phase 1, so no merge sits between two lists.  Four lists (16 KB) keep the
+// workgroup's LDS within half a CU for pq_m <= 48.
+constexpr int kStage = 4;
 constexpr int kStageFloats = kStage * kTW * kWave * 2;
 
 template <int D, int M>
@@ -52,6 +53,9 @@ struct TCfg {
   static constexpr int LUT = M * kPQK;
   static constexpr int SMEM = LUT > 2 * kSortMax ? LUT : 2 * kSortMax;  // floats: LUT, later the sort area
   static constexpr int NV4 = M / 16;
+  // Two workgroups (queries) per CU where the LDS allows: 4 waves a SIMD,
+  // hence at most 128 VGPRs.
+  static constexpr int WPE = (SMEM + kStageFloats) * 4 <= 72 * 1024 ? 4 : 2;
 };
 
 __device__ __forceinline__ float key_dist(uint64_t key) {
@@ -143,7 +147,8 @@ __device__ void lds_bitonic_sort(uint64_t* sk, int np2) {
 }
 
 template <int D, int M>
-__global__ __launch_bounds__(kTT) void two_phase_kernel(TwoPhaseArgs a) {
+__global__ __launch_bounds__(kTT) __attribute__((amdgpu_waves_per_eu(TCfg<D, M>::WPE, TCfg<D, M>::WPE)))
+void two_phase_kernel(TwoPhaseArgs a) {
   using C = TCfg<D, M>;
   constexpr int G = kTT / kPQK;  // threads sharing one codeword
   constexpr int MG = M / G;      // subspaces per thread in the LUT build
@@ -178,13 +183,6 @@ __global__ __launch_bounds__(kTT) void two_phase_kernel(TwoPhaseArgs a) {
   uint64_t* pool = a.pool + (size_t)q * cap;
   const long long t_start = a.stats ? clock64() : 0;
 
-  float cb[MG * C::S];
-#pragma unroll
-  for (int mm = 0; mm < MG; ++mm) {
-    const float* src = a.codebook + ((size_t)(g * MG + mm) * kPQK + kc) * C::S;
-#pragma unroll
-    for (int j = 0; j < C::S; ++j) cb[mm * C::S + j] = src[j];
-  }
   for (int i = tid; i < D; i += kTT) qs[i] = a.queries[(size_t)q * D + i];
   if (tid < 64) s_cut[tid] = 0.0f;
   if (tid < kTW) s_pub[tid] = kNoThr;
@@ -240,13 +238,16 @@ __global__ __launch_bounds__(kTT) void two_phase_kernel(TwoPhaseArgs a) {
     int kcv = kc;
     asm volatile("" : "+v"(kcv));
     float* dst = lut + g * MG * kPQK + kcv;
+    // The codebook rows come from L2 at each build (the codebook is shared
+    // by every workgroup); holding them in registers would halve occupancy.
+    const float* cbp = a.codebook + ((size_t)g * MG * kPQK + kcv) * C::S;
     const float* rg = r + g * MG * C::S;
 #pragma unroll
     for (int mm = 0; mm < MG; ++mm) {
       float rr[C::S];
 #pragma unroll
       for (int j = 0; j < C::S; ++j) rr[j] = rg[mm * C::S + j];
-      dst[mm * kPQK] = lut_entry<C::S>(rr, cb + mm * C::S);
+      dst[mm * kPQK] = lut_entry<C::S>(rr, cbp + mm * kPQK * C::S);
     }
   };
 
