@@ -408,16 +408,17 @@ void two_phase_kernel(TwoPhaseArgs a) {
         thr_d = fminf(thr, key_dist(adm));
       }
       int base = s0 + first;
-      if (s0 != 0 && base < s1) {  // segment 0's first round was loaded before the LUT build
-        load_pair<M>(a.codes, a.vec_ids, start, n, base + lane, w0, w1, i0, i1);
-        count_load(base, n);
-      }
+      bool loaded = s0 == 0;  // segment 0's first round was loaded before the LUT build
+      // Phase 2 loads each round when it starts: most of its lists are
+      // skipped whole, and prefetch registers here would spill at the
+      // two-workgroup register budget.
       while (base < s1) {
         const int nb = base + kTRound;
-        if (nb < s1) {
-          load_pair<M>(a.codes, a.vec_ids, start, n, nb + lane, n0, n1, j0, j1);
-          count_load(nb, n);
+        if (!loaded) {
+          load_pair<M>(a.codes, a.vec_ids, start, n, base + lane, w0, w1, i0, i1);
+          count_load(base, n);
         }
+        loaded = false;
         const int v0 = base + lane, v1 = v0 + kWave;
         float d0, d1;
         if (adc_sum2<M>(lut, w0, w1, v0 < s1, v1 < s1, thr_d, d0, d1)) {
@@ -435,15 +436,6 @@ void two_phase_kernel(TwoPhaseArgs a) {
             if (pass0) pool[at + __popcll(b0 & below)] = k0;
             if (pass1) pool[at + c0 + __popcll(b1 & below)] = k1;
           }
-        }
-        if (nb < s1) {
-#pragma unroll
-          for (int i = 0; i < C::NV4; ++i) {
-            w0[i] = n0[i];
-            w1[i] = n1[i];
-          }
-          i0 = j0;
-          i1 = j1;
         }
         base = nb;
       }
