@@ -574,11 +574,18 @@ __global__ __launch_bounds__(kRT) void rerank_kernel(RerankArgs a) {
     if (tid < eff) {
       const int vid = cand[off + tid];
       if (vid >= 0 && (long long)vid < a.n) {
+        // The whole row is requested before the first multiply-add (the
+        // scheduling barrier keeps the loads together): one memory round
+        // trip a batch instead of one per eight float4.
         const float4* row = reinterpret_cast<const float4*>(a.base + (size_t)vid * D);
+        float4 rv[D / 4];
+#pragma unroll
+        for (int j = 0; j < D / 4; ++j) rv[j] = row[j];
+        __builtin_amdgcn_sched_barrier(0);
         float acc = 0.0f;
-#pragma unroll 8
+#pragma unroll
         for (int j = 0; j < D / 4; ++j) {
-          const float4 v = row[j];
+          const float4 v = rv[j];
           float df = qs[4 * j] - v.x;
           acc = __builtin_fmaf(df, df, acc);
           df = qs[4 * j + 1] - v.y;
