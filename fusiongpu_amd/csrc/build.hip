@@ -240,26 +240,53 @@ __device__ __forceinline__ uint64_t mix64(uint64_t z) {
 
 constexpr int kPPBlock = 1024;
 
+// The exact skip of the d2 update.  asg[i] is the centre whose distance d2[i]
+// holds, cc[a] = ||c_new - c_a||^2 for every earlier centre a.  By the
+// triangle inequality ||x - c_new|| >= ||c_new - c_a|| - ||x - c_a||, so with
+// cc >= 4 (1 + 1%) d2 the new distance exceeds d2 by about 2% even after the
+// roundings of the three fused chains (each within 1e-4 relative of its exact
+// value, D <= 256): the row cannot move, and its d2, weight and asg stay as
+// they are without reading the row.  d2 = 0 rows never move either.
+constexpr float kPPSkip = 4.04f;
+
+// Whether row i must compute its distance to the new centre (always, when
+// asg is null: the first passes).
+__device__ __forceinline__ bool pp_needs(const int32_t* asg, const float* cc, int64_t i, float old) {
+  return asg == nullptr || !(cc[asg[i]] >= kPPSkip * old);
+}
+
 // d2[i] = min(d2[i], ||x_i - c||^2) (init: d2 = dist); w[i] = round(d2 * 2^S);
-// part[b] = sum of w over block b.
+// part[b] = sum of w over block b.  With asg: rows the triangle bound clears
+// are skipped, and a row that moves records centre j.
 __global__ __launch_bounds__(kPPBlock) void pp_update_kernel(const float* __restrict__ x, int64_t n, int dim,
                                                              const float* __restrict__ c, int init,
                                                              float* __restrict__ d2, const int* __restrict__ shift,
-                                                             uint64_t* __restrict__ w, uint64_t* __restrict__ part) {
+                                                             uint64_t* __restrict__ w, uint64_t* __restrict__ part,
+                                                             int32_t* __restrict__ asg, const float* __restrict__ cc,
+                                                             int j) {
   const int64_t i = (int64_t)blockIdx.x * kPPBlock + threadIdx.x;
   uint64_t wi = 0;
   if (i < n) {
-    const float* xi = x + i * dim;
-    float acc = 0.0f;
-    for (int d = 0; d < dim; ++d) {
-      const float df = xi[d] - c[d];
-      acc = __builtin_fmaf(df, df, acc);
+    const float old = init ? 0.0f : d2[i];
+    float v = old;
+    bool moved = false;
+    if (init || pp_needs(init ? nullptr : asg, cc, i, old)) {
+      const float* xi = x + i * dim;
+      float acc = 0.0f;
+      for (int d = 0; d < dim; ++d) {
+        const float df = xi[d] - c[d];
+        acc = __builtin_fmaf(df, df, acc);
+      }
+      moved = init || acc < old;
+      v = moved ? acc : old;
     }
-    const float v = (init || acc < d2[i]) ? acc : d2[i];
-    d2[i] = v;
+    if (moved) {
+      d2[i] = v;
+      if (asg) asg[i] = j;
+    }
     if (shift) {
       wi = (uint64_t)__double2ll_rn(ldexp((double)v, *shift));
-      w[i] = wi;
+      if (moved || !asg) w[i] = wi;
     }
   }
   if (shift) {
@@ -285,7 +312,9 @@ template <int D>
 __global__ __launch_bounds__(kPPBlock) void pp_update_vec_kernel(const float* __restrict__ x, int64_t n,
                                                                  const float* __restrict__ c, int init,
                                                                  float* __restrict__ d2, const int* __restrict__ shift,
-                                                                 uint64_t* __restrict__ w, uint64_t* __restrict__ part) {
+                                                                 uint64_t* __restrict__ w, uint64_t* __restrict__ part,
+                                                                 int32_t* __restrict__ asg,
+                                                                 const float* __restrict__ cc, int jc) {
   static_assert(D % 4 == 0, "16-byte row loads");
   __shared__ float cs[D];
   for (int d = threadIdx.x; d < D; d += kPPBlock) cs[d] = c[d];
@@ -293,27 +322,36 @@ __global__ __launch_bounds__(kPPBlock) void pp_update_vec_kernel(const float* __
   const int64_t i = (int64_t)blockIdx.x * kPPBlock + threadIdx.x;
   uint64_t wi = 0;
   if (i < n) {
-    const float4* xi = reinterpret_cast<const float4*>(x + i * D);
-    float4 v[D / 4];
+    const float old = init ? 0.0f : d2[i];
+    float v2 = old;
+    bool moved = false;
+    if (init || pp_needs(init ? nullptr : asg, cc, i, old)) {
+      const float4* xi = reinterpret_cast<const float4*>(x + i * D);
+      float4 v[D / 4];
 #pragma unroll
-    for (int j = 0; j < D / 4; ++j) v[j] = xi[j];
-    float acc = 0.0f;
+      for (int j = 0; j < D / 4; ++j) v[j] = xi[j];
+      float acc = 0.0f;
 #pragma unroll
-    for (int j = 0; j < D / 4; ++j) {
-      float df = v[j].x - cs[4 * j];
-      acc = __builtin_fmaf(df, df, acc);
-      df = v[j].y - cs[4 * j + 1];
-      acc = __builtin_fmaf(df, df, acc);
-      df = v[j].z - cs[4 * j + 2];
-      acc = __builtin_fmaf(df, df, acc);
-      df = v[j].w - cs[4 * j + 3];
-      acc = __builtin_fmaf(df, df, acc);
+      for (int j = 0; j < D / 4; ++j) {
+        float df = v[j].x - cs[4 * j];
+        acc = __builtin_fmaf(df, df, acc);
+        df = v[j].y - cs[4 * j + 1];
+        acc = __builtin_fmaf(df, df, acc);
+        df = v[j].z - cs[4 * j + 2];
+        acc = __builtin_fmaf(df, df, acc);
+        df = v[j].w - cs[4 * j + 3];
+        acc = __builtin_fmaf(df, df, acc);
+      }
+      moved = init || acc < old;
+      v2 = moved ? acc : old;
     }
-    const float v2 = (init || acc < d2[i]) ? acc : d2[i];
-    d2[i] = v2;
+    if (moved) {
+      d2[i] = v2;
+      if (asg) asg[i] = jc;
+    }
     if (shift) {
       wi = (uint64_t)__double2ll_rn(ldexp((double)v2, *shift));
-      w[i] = wi;
+      if (moved || !asg) w[i] = wi;
     }
   }
   if (shift) {
@@ -333,19 +371,41 @@ __global__ __launch_bounds__(kPPBlock) void pp_update_vec_kernel(const float* __
 
 // One pass of the d2 update: the vectorised kernel for the common dims (rows
 // 16-byte aligned), the generic one otherwise.
+// asg == nullptr: every row computes (the first passes); otherwise the skip
+// above applies (cc filled for centre j).
 fgpu_status pp_update(const float* x, int64_t n, int dim, const float* c, int init, float* d2, const int* shift,
-                      uint64_t* w, uint64_t* part, int nb, hipStream_t s) {
+                      uint64_t* w, uint64_t* part, int nb, int32_t* asg, const float* cc, int j, hipStream_t s) {
   const bool vec = ((uintptr_t)x & 15) == 0;
   if (vec && dim == 128)
-    hipLaunchKernelGGL(pp_update_vec_kernel<128>, dim3(nb), dim3(kPPBlock), 0, s, x, n, c, init, d2, shift, w, part);
+    hipLaunchKernelGGL(pp_update_vec_kernel<128>, dim3(nb), dim3(kPPBlock), 0, s, x, n, c, init, d2, shift, w, part,
+                       asg, cc, j);
   else if (vec && dim == 96)
-    hipLaunchKernelGGL(pp_update_vec_kernel<96>, dim3(nb), dim3(kPPBlock), 0, s, x, n, c, init, d2, shift, w, part);
+    hipLaunchKernelGGL(pp_update_vec_kernel<96>, dim3(nb), dim3(kPPBlock), 0, s, x, n, c, init, d2, shift, w, part,
+                       asg, cc, j);
   else if (vec && dim == 64)
-    hipLaunchKernelGGL(pp_update_vec_kernel<64>, dim3(nb), dim3(kPPBlock), 0, s, x, n, c, init, d2, shift, w, part);
+    hipLaunchKernelGGL(pp_update_vec_kernel<64>, dim3(nb), dim3(kPPBlock), 0, s, x, n, c, init, d2, shift, w, part,
+                       asg, cc, j);
   else
-    hipLaunchKernelGGL(pp_update_kernel, dim3(nb), dim3(kPPBlock), 0, s, x, n, dim, c, init, d2, shift, w, part);
+    hipLaunchKernelGGL(pp_update_kernel, dim3(nb), dim3(kPPBlock), 0, s, x, n, dim, c, init, d2, shift, w, part, asg,
+                       cc, j);
   FGPU_HIP(hipGetLastError());
   return FGPU_OK;
+}
+
+// cc[a] = ||c_j - c_a||^2 for every earlier centre a < j (fused chain; only a
+// bound is needed from it).
+__global__ __launch_bounds__(256) void pp_cc_kernel(const float* __restrict__ cent, int dim, int j,
+                                                    float* __restrict__ cc) {
+  const int a = blockIdx.x * 256 + threadIdx.x;
+  if (a >= j) return;
+  const float* cj = cent + (size_t)j * dim;
+  const float* ca = cent + (size_t)a * dim;
+  float acc = 0.0f;
+  for (int d = 0; d < dim; ++d) {
+    const float df = cj[d] - ca[d];
+    acc = __builtin_fmaf(df, df, acc);
+  }
+  cc[a] = acc;
 }
 
 // shift from the first round's max d2 (so n * max w < 2^62).
@@ -606,10 +666,10 @@ fgpu_status launch_pq_mstep(const float* res, int ns, int dim, int m, const int3
   return FGPU_OK;
 }
 
-size_t kmeans_pp_ws_bytes(int64_t n) {
+size_t kmeans_pp_ws_bytes(int64_t n, int k) {
   const int64_t nb = (n + kPPBlock - 1) / kPPBlock;
   return carve_bytes<float>(n) + carve_bytes<uint64_t>(n) + carve_bytes<uint64_t>(nb) + carve_bytes<uint8_t>(n) +
-         carve_bytes<int>(1);
+         carve_bytes<int>(1) + carve_bytes<int32_t>(n) + carve_bytes<float>(k > 0 ? k : 1);
 }
 
 fgpu_status launch_kmeans_pp(const float* x, int64_t n, int dim, int k, uint64_t seed, float* cent, int32_t* rows,
@@ -621,19 +681,24 @@ fgpu_status launch_kmeans_pp(const float* x, int64_t n, int dim, int k, uint64_t
   uint64_t* part = cv.take<uint64_t>(nb);
   uint8_t* chosen = cv.take<uint8_t>(n);
   int* shift = cv.take<int>(1);
+  int32_t* asg = cv.take<int32_t>(n);
+  float* cc = cv.take<float>(k > 0 ? k : 1);
   FGPU_CHECK(cv.ok(), FGPU_ERR_WORKSPACE, "kmeans++: workspace too small");
   FGPU_HIP(hipMemsetAsync(chosen, 0, n, s));
   hipLaunchKernelGGL(pp_first_kernel, dim3(1), dim3(1), 0, s, n, seed, rows, chosen);
   hipLaunchKernelGGL(pp_take_kernel, dim3(1), dim3(256), 0, s, x, dim, rows, 0, cent, chosen);
-  FGPU_TRY(pp_update(x, n, dim, cent, 1, d2, nullptr, w, part, nb, s));
+  FGPU_TRY(pp_update(x, n, dim, cent, 1, d2, nullptr, w, part, nb, asg, cc, 0, s));  // asg := 0
   hipLaunchKernelGGL(pp_shift_kernel, dim3(1), dim3(1024), 0, s, d2, n, shift);
   FGPU_HIP(hipGetLastError());
-  // weights for round 1 from the initial d2
-  FGPU_TRY(pp_update(x, n, dim, cent, 0, d2, shift, w, part, nb, s));
+  // weights for round 1 from the initial d2 (every row: no skip yet)
+  FGPU_TRY(pp_update(x, n, dim, cent, 0, d2, shift, w, part, nb, nullptr, cc, 0, s));
   for (int j = 1; j < k; ++j) {
     hipLaunchKernelGGL(pp_pick_kernel, dim3(1), dim3(kPPBlock), 0, s, w, part, nb, n, seed, j, chosen, rows);
     hipLaunchKernelGGL(pp_take_kernel, dim3(1), dim3(256), 0, s, x, dim, rows, j, cent, chosen);
-    if (j + 1 < k) FGPU_TRY(pp_update(x, n, dim, cent + (size_t)j * dim, 0, d2, shift, w, part, nb, s));
+    if (j + 1 < k) {
+      hipLaunchKernelGGL(pp_cc_kernel, dim3((unsigned)((j + 255) / 256)), dim3(256), 0, s, cent, dim, j, cc);
+      FGPU_TRY(pp_update(x, n, dim, cent + (size_t)j * dim, 0, d2, shift, w, part, nb, asg, cc, j, s));
+    }
   }
   FGPU_HIP(hipGetLastError());
   return FGPU_OK;

@@ -705,7 +705,7 @@ fgpu_status fgpu_kmeans_fit(const float* dx, int64_t n, int dim, int k, int iter
     FGPU_HIP(hipStreamSynchronize(s));
   } else {
     DevBuf<char> pws;
-    const size_t b = kmeans_pp_ws_bytes(n);
+    const size_t b = kmeans_pp_ws_bytes(n, k);
     FGPU_TRY(pws.alloc(b));
     FGPU_TRY(launch_kmeans_pp(dx, n, dim, k, seed, d_cent, rows.p, pws.p, b, s));
     FGPU_HIP(hipStreamSynchronize(s));

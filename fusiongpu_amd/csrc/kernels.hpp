@@ -209,6 +209,6 @@ fgpu_status launch_pq_mstep(const float* res, int nsample, int dim, int m, const
 // k-means++ seeding on the device (definition in oracle.cpp orc_kmeans_init_pp).
 fgpu_status launch_kmeans_pp(const float* x, int64_t n, int dim, int k, uint64_t seed, float* cent,
                              int32_t* rows, void* ws, size_t ws_bytes, hipStream_t s);
-size_t kmeans_pp_ws_bytes(int64_t n);
+size_t kmeans_pp_ws_bytes(int64_t n, int k);
 
 }  // namespace fgpu

@@ -200,6 +200,21 @@ def test_kmeans_fit_bit_exact(init_mode):
     assert np.array_equal(_host(assign), oa)
 
 
+@pytest.mark.parametrize("n,dim,comp,k", [(40000, 128, 64, 300), (20000, 96, 40, 200), (8000, 40, 16, 120)])
+def test_kmeans_pp_seeding_bit_exact(n, dim, comp, k):
+    """k-means++ seeding (iters = 0) on tight clusters with duplicate rows, so
+    the update's exact triangle-inequality skip clears most rows after the
+    first picks: the centres equal the oracle's unpruned definition bit for
+    bit (dims 128 and 96 take the vectorised kernel, 40 the generic one)."""
+    _say(f"kmeans++ seeding n={n} dim={dim} k={k}")
+    x = oracle.gen_gmm(n, dim, comp, seed=17, sig_lo=0.05)
+    x[-200:] = x[:200]  # duplicates: rows at distance 0 from a picked centre
+    cent, _ = fg.kmeans_fit(torch.from_numpy(x).cuda(), k, 0, init_mode=1, seed=7, want_assign=False)
+    want, rows = oracle.kmeans_init_pp(x, k, 7)
+    assert len(set(rows.tolist())) == k
+    assert np.array_equal(_bits(_host(cent)), _bits(want))
+
+
 # --------------------------------------------------------------------------- PQ (A15, A16)
 def test_pq_train_matches_reference_fixture():
     _say("pq_train golden")
