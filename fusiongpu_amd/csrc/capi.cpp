@@ -254,8 +254,8 @@ size_t fgpu_coarse_workspace_bytes(int nq, int nlist) {
 fgpu_status fgpu_coarse_search(const fgpu_index* ix, const float* dq, int nq, int nprobe, float prune_ratio,
                                uint32_t* d_ids, float* d_dists, void* ws, size_t ws_bytes, void* stream) {
   FGPU_CHECK(ix && dq && d_ids && d_dists && ws, FGPU_ERR_ARG, "coarse_search: null argument");
-  FGPU_CHECK(nq >= 0 && nprobe >= 1 && nprobe <= ix->nlist && nprobe <= 64, FGPU_ERR_ARG,
-             "coarse_search: need 1 <= nprobe <= min(nlist, 64)");
+  FGPU_CHECK(nq >= 0 && nprobe >= 1 && nprobe <= ix->nlist && nprobe <= 256, FGPU_ERR_ARG,
+             "coarse_search: need 1 <= nprobe <= min(nlist, 256)");
   if (nq == 0) return FGPU_OK;
   hipStream_t s = as_stream(stream);
   Carve cv(ws, ws_bytes);
@@ -387,7 +387,7 @@ fgpu_status two_phase(const fgpu_index* ix, const float* dq, int nq, const uint3
                       unsigned long long* d_stats, void* ws, size_t ws_bytes, void* stream) {
   FGPU_CHECK(ix && dq && d_probe_ids && d_top_ids && d_top_dists && d_top_counts && ws, FGPU_ERR_ARG,
              "two_phase_search: null argument");
-  FGPU_CHECK(nq >= 0 && nprobe >= 1 && nprobe <= 64, FGPU_ERR_ARG, "two_phase_search: need 1 <= nprobe <= 64");
+  FGPU_CHECK(nq >= 0 && nprobe >= 1 && nprobe <= 256, FGPU_ERR_ARG, "two_phase_search: need 1 <= nprobe <= 256");
   FGPU_CHECK(limit_k >= 1 && rerank_m >= 1, FGPU_ERR_ARG, "two_phase_search: limit_k and rerank_m must be >= 1");
   FGPU_CHECK(adc_supported(ix->dim, ix->m), FGPU_ERR_UNSUPPORTED, "two_phase_search: no kernel for this (dim, pq_m)");
   if (nq == 0) return FGPU_OK;
@@ -480,7 +480,7 @@ size_t fgpu_l2_topk_workspace_bytes(int64_t n, int nc) {
 fgpu_status fgpu_l2_topk(const float* dx, int64_t n, const float* dc, int nc, int dim, int p, int32_t* d_ids,
                          float* d_dists, void* ws, size_t ws_bytes, void* stream) {
   FGPU_CHECK(dx && dc && d_ids && d_dists && ws, FGPU_ERR_ARG, "l2_topk: null argument");
-  FGPU_CHECK(n >= 0 && nc >= 1 && dim >= 1 && p >= 1 && p <= nc && p <= 64, FGPU_ERR_ARG, "l2_topk: bad sizes");
+  FGPU_CHECK(n >= 0 && nc >= 1 && dim >= 1 && p >= 1 && p <= nc && p <= 256, FGPU_ERR_ARG, "l2_topk: bad sizes");
   if (n == 0) return FGPU_OK;
   hipStream_t s = as_stream(stream);
   Carve cv(ws, ws_bytes);

@@ -199,7 +199,8 @@ __global__ __launch_bounds__(256) void gemm_est32_kernel(const float* __restrict
   }
 }
 
-constexpr int kCandCap = 256;
+constexpr int kCandCap = 512;
+constexpr int kSelectMax = 4 * kWave;  // p limit of the coarse select: four sorted 64-key lists
 
 // Ascending bitonic sort of one 32-bit key per lane across the wave.
 template <int S>
@@ -312,8 +313,40 @@ __device__ __forceinline__ float exact_l2(const float* __restrict__ xs, const fl
   return acc;
 }
 
+// Merge a sorted batch (ascending, one key a lane) into the running top-4*64
+// held as four sorted 64-lists a <= b <= c <= d (ranks 1-64, 65-128, ...):
+// each level keeps the 64 smallest of its list and what arrives, and passes
+// the 64 largest down; nl lists are live (nl = ceil(p / 64)).
+__device__ __forceinline__ void split_merge64(uint64_t& lo, uint64_t& inc) {
+  const uint64_t r = wave_reverse64(inc);
+  const bool take = r < lo;
+  const uint64_t hi = take ? lo : r;
+  lo = take ? r : lo;
+  inc = hi;
+  bitonic_pass_k<64>(lo, true);
+  bitonic_pass_k<64>(inc, true);
+}
+__device__ __forceinline__ void merge_top256(uint64_t (&l)[4], int nl, uint64_t key) {
+  if (nl == 1) {
+    wave_merge_sorted64_k(l[0], key);
+    return;
+  }
+  split_merge64(l[0], key);
+  if (nl == 2) {
+    wave_merge_sorted64_k(l[1], key);
+    return;
+  }
+  split_merge64(l[1], key);
+  if (nl == 3) {
+    wave_merge_sorted64_k(l[2], key);
+    return;
+  }
+  split_merge64(l[2], key);
+  wave_merge_sorted64_k(l[3], key);
+}
+
 // One wave per row: p-th smallest estimate by LDS radix select, margin
-// superset, exact re-score, bitonic sort by (distance, index).
+// superset, exact re-score, bitonic sort by (distance, index); p <= 256.
 template <int VPL>
 __global__ __launch_bounds__(256) void select_exact_kernel(
     const float* __restrict__ est, int64_t ld, int64_t nrows, int ncols,
@@ -359,9 +392,10 @@ __global__ __launch_bounds__(256) void select_exact_kernel(
   const bool all_cols = C > kCandCap;  // pathological ties: re-score everything
   const int ncand = all_cols ? ncols : C;
 
-  // Running list of packed (distance, id) keys: squared L2 distances are >= 0,
-  // so key order is the tie rule.
-  uint64_t lk = kPadKey;
+  // Running top-p of packed (distance, id) keys: squared L2 distances are
+  // >= 0, so key order is the tie rule.
+  const int nl = (p + kWave - 1) / kWave;
+  uint64_t lk[4] = {kPadKey, kPadKey, kPadKey, kPadKey};
   bool first = true;
   for (int base = 0; base < ncand; base += kWave) {
     uint64_t key = kPadKey;
@@ -370,18 +404,22 @@ __global__ __launch_bounds__(256) void select_exact_kernel(
       key = key_of(exact_l2(xs, c + (int64_t)id * dim, dim), id);
     }
     wave_sort64_k(key);
-    if (first) { lk = key; first = false; }
-    else wave_merge_sorted64_k(lk, key);
+    if (first) { lk[0] = key; first = false; }
+    else merge_top256(lk, nl, key);
   }
 
-  const float best = key_dist(readlane64(lk, 0));
+  const float best = key_dist(readlane64(lk[0], 0));
   const float pthr = best * prune_ratio;
-  if (lane < p) {
-    const float ld_ = key_dist(lk);
-    int32_t oid = key_id(lk);
-    if (prune && ld_ > pthr) oid = (int32_t)kPruned;
-    out_ids[row * p + lane] = oid;
-    out_d[row * p + lane] = ld_;
+#pragma unroll
+  for (int l = 0; l < 4; ++l) {
+    const int r = l * kWave + lane;
+    if (r < p) {
+      const float ld_ = key_dist(lk[l]);
+      int32_t oid = key_id(lk[l]);
+      if (prune && ld_ > pthr) oid = (int32_t)kPruned;
+      out_ids[row * p + r] = oid;
+      out_d[row * p + r] = ld_;
+    }
   }
 }
 
@@ -559,7 +597,7 @@ static float coarse_kappa(int dim) {
 fgpu_status launch_select_exact(const float* est, int64_t ld, int64_t nrows, int ncols, const float* x,
                                 const float* c, int dim, const float* xn, const float* cn_max, int p,
                                 int prune, float prune_ratio, int32_t* ids, float* d, hipStream_t s) {
-  FGPU_CHECK(p >= 1 && p <= 64 && p <= ncols, FGPU_ERR_UNSUPPORTED, "select: need 1 <= p <= min(64, ncols)");
+  FGPU_CHECK(p >= 1 && p <= kSelectMax && p <= ncols, FGPU_ERR_UNSUPPORTED, "select: need 1 <= p <= min(256, ncols)");
   FGPU_CHECK(dim <= 256, FGPU_ERR_UNSUPPORTED, "select: dim must be <= 256");
   if (nrows <= 0) return FGPU_OK;
   const float kappa = coarse_kappa(dim);

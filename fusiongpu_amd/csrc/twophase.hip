@@ -40,6 +40,7 @@ constexpr int kTRound = kTW * kVecPerWaveRound;      // vectors per workgroup ro
 constexpr int kSortMax = 4096;                       // keys of one final LDS sort (a run)
 constexpr int kRerankMax = 1 << 17;                  // rerank_m limit: at most 32 runs
 constexpr uint64_t kNoKey = ~0ull;                   // "no admission bound yet"
+constexpr int kMaxProbes = 4 * kWave;                // nprobe limit: four 64-probe chunks at set-up
 // Phase 1 stages the eight sorted wave lists of up to kStage lists; the waves
 // merge the staged lists in parallel when the stage is full and at the end of
 // phase 1, so no merge sits between two lists.  Four lists (16 KB) keep the
@@ -163,9 +164,9 @@ void two_phase_kernel(TwoPhaseArgs a) {
   __shared__ int st_f[kStage], st_base[kStage];
   __shared__ int hist[256];
   __shared__ int misc[4];
-  __shared__ float s_cut[64];
-  __shared__ int f_list[64], f_start[64], f_n[64], f_p[64];  // usable probes in probe order
-  __shared__ float f_lb[64];                                 // lower bound of each phase-2 list
+  __shared__ float s_cut[kMaxProbes];
+  __shared__ int f_list[kMaxProbes], f_start[kMaxProbes], f_n[kMaxProbes], f_p[kMaxProbes];  // usable probes, in order
+  __shared__ float f_lb[kMaxProbes];                                                          // phase-2 list bounds
   __shared__ int s_nv, s_nv1;
   __shared__ int s_cnt;
   __shared__ unsigned long long s_lthr;
@@ -184,30 +185,37 @@ void two_phase_kernel(TwoPhaseArgs a) {
   const long long t_start = a.stats ? clock64() : 0;
 
   for (int i = tid; i < D; i += kTT) qs[i] = a.queries[(size_t)q * D + i];
-  if (tid < 64) s_cut[tid] = 0.0f;
+  if (tid < kMaxProbes) s_cut[tid] = 0.0f;
   if (tid < kTW) s_pub[tid] = kNoThr;
   if (wave == 0) {
-    // Usable probes (in range, non-empty) in probe order; the first s_nv1 are phase 1.
-    int l = 0, st = 0, n = 0;
-    if (lane < P) {
-      const uint32_t pl = a.probes[(size_t)q * P + lane];
-      if (pl < NL) {
-        l = (int)pl;
-        st = a.offsets[pl];
-        n = a.offsets[pl + 1] - st;
+    // Usable probes (in range, non-empty) in probe order, 64 probes a step;
+    // the first s_nv1 are phase 1 (probe index < p1).
+    int nv_run = 0, nv1_run = 0;
+    for (int c0 = 0; c0 < P; c0 += kWave) {
+      const int pi = c0 + lane;
+      int l = 0, st = 0, n = 0;
+      if (pi < P) {
+        const uint32_t pl = a.probes[(size_t)q * P + pi];
+        if (pl < NL) {
+          l = (int)pl;
+          st = a.offsets[pl];
+          n = a.offsets[pl + 1] - st;
+        }
       }
-    }
-    const uint64_t bm = __ballot(n > 0);
-    const int pos = __popcll(bm & ((1ull << lane) - 1ull));
-    if (n > 0) {
-      f_list[pos] = l;
-      f_start[pos] = st;
-      f_n[pos] = n;
-      f_p[pos] = lane;
+      const uint64_t bm = __ballot(n > 0);
+      const int pos = nv_run + __popcll(bm & ((1ull << lane) - 1ull));
+      if (n > 0) {
+        f_list[pos] = l;
+        f_start[pos] = st;
+        f_n[pos] = n;
+        f_p[pos] = pi;
+      }
+      nv_run += __popcll(bm);
+      nv1_run += __popcll(__ballot(n > 0 && pi < p1));
     }
     if (lane == 0) {
-      s_nv = __popcll(bm);
-      s_nv1 = __popcll(bm & (p1 >= 64 ? ~0ull : ((1ull << p1) - 1ull)));
+      s_nv = nv_run;
+      s_nv1 = nv1_run;
       s_cnt = 0;
       s_lthr = kNoThr;
     }
@@ -692,8 +700,8 @@ fgpu_status launch_two_phase(int dim, int m, const TwoPhaseArgs& a, hipStream_t 
   FGPU_CHECK(a.limit_k >= 1 && a.limit_k <= 64, FGPU_ERR_UNSUPPORTED, "two_phase: limit_k must be in [1, 64]");
   FGPU_CHECK(a.rerank_m >= 1 && a.rerank_m <= kRerankMax, FGPU_ERR_UNSUPPORTED,
              "two_phase: rerank_m must be in [1, 131072]");
-  FGPU_CHECK(a.nprobe >= 1 && a.nprobe <= 64 && a.p1 >= 0 && a.p1 <= a.nprobe, FGPU_ERR_ARG,
-             "two_phase: need 1 <= nprobe <= 64 and 0 <= p1 <= nprobe");
+  FGPU_CHECK(a.nprobe >= 1 && a.nprobe <= kMaxProbes && a.p1 >= 0 && a.p1 <= a.nprobe, FGPU_ERR_ARG,
+             "two_phase: need 1 <= nprobe <= 256 and 0 <= p1 <= nprobe");
   FGPU_CHECK(a.pool_cap >= two_phase_pool_cap(a.p1, a.limit_k, a.rerank_m), FGPU_ERR_ARG, "two_phase: pool too small");
   if (a.nq <= 0) return FGPU_OK;
   const int nq = a.nq;

@@ -118,7 +118,7 @@ fgpu_status fgpu_stream_read(const void* d_data, size_t bytes, unsigned long lon
  * prune rule of prune_and_count_fused_kernel (gpu_global.cu:43-50): a probe
  * whose distance exceeds best*prune_ratio becomes 0xFFFFFFFF.  Replaces the
  * cuVS CAGRA call (search_pipeline.cu:341; cagra_adapter.cuh:38-68) with an
- * MFMA GEMM plus an exact re-score.  nprobe <= 64. */
+ * MFMA GEMM plus an exact re-score.  nprobe <= 256. */
 size_t fgpu_coarse_workspace_bytes(int nq, int nlist);
 fgpu_status fgpu_coarse_search(const fgpu_index* idx, const float* d_queries, int nq, int nprobe,
                                float prune_ratio, uint32_t* d_probe_ids, float* d_probe_dists,
@@ -140,7 +140,7 @@ fgpu_status fgpu_probe_counts(const fgpu_index* idx, const uint32_t* d_probe_ids
 /* The k best (ADC distance, vector id) over every vector of every surviving
  * probed list; padding id -1 / distance FLT_MAX.  Equals run_gpu_batch_logic
  * (gpu_global.cu:679-874) with p1_lists = nprobe, limit_k = k, rerank_m = k.
- * k <= 64.  d_probe_dists (may be NULL) takes the place of the reference's
+ * k <= 64, nprobe <= 64.  d_probe_dists (may be NULL) takes the place of the reference's
  * d_cagra_dists: fgpu_coarse_search's distances for these probes, which the
  * scan then uses for its exact list bounds instead of recomputing them from
  * the centroids.  Non-NULL, they must be exactly the distances
@@ -209,7 +209,7 @@ fgpu_status fgpu_search_noalloc(const fgpu_index* idx, const float* d_queries, i
  * all rerank_m entries are gathered.  No host synchronisation and no pool
  * reallocation: the candidate pool is a bounded workspace, kept exact by
  * selecting the rerank_m best whenever it would overflow.  limit_k <= 64,
- * rerank_m <= 131072 (the reference's default is 10000), nprobe <= 64.  A workspace smaller than the returned size
+ * rerank_m <= 131072 (the reference's default is 10000), nprobe <= 256.  A workspace smaller than the returned size
  * is used in query chunks (it must hold at least one query's pool). */
 size_t fgpu_two_phase_workspace_bytes(int nq, int nprobe, int p1_lists, int limit_k, int rerank_m);
 fgpu_status fgpu_two_phase_search(const fgpu_index* idx, const float* d_queries, int nq,
@@ -265,7 +265,7 @@ fgpu_status fgpu_search_rerank(const fgpu_index* idx, const float* d_queries, in
  * exact squared L2 in the reference's device form (sequential fused
  * multiply-add, tune_parameters.cu:39-46), ascending (distance, index).
  * p = 1 is the k-means assignment (kmeans_gpu.cuh:197-229, lowest index wins
- * ties).  MFMA GEMM + rigorous-margin re-score.  p <= 64. */
+ * ties).  MFMA GEMM + rigorous-margin re-score.  p <= 256. */
 size_t fgpu_l2_topk_workspace_bytes(int64_t n, int nc);
 fgpu_status fgpu_l2_topk(const float* d_x, int64_t n, const float* d_c, int nc, int dim, int p,
                          int32_t* d_ids, float* d_dists, void* d_workspace, size_t workspace_bytes,

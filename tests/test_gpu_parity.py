@@ -88,6 +88,26 @@ def test_coarse_search_bit_exact(prune_ratio):
     idx.close()
 
 
+@pytest.mark.parametrize("p,prune_ratio", [(100, 1.3), (256, float("inf")), (65, 100.0)])
+def test_coarse_search_many_probes(p, prune_ratio):
+    """Top-p above one 64-key list (up to four lists merged in cascade),
+    with duplicate centroids for ties and the prune rule past rank 64."""
+    _say(f"coarse p={p} prune_ratio={prune_ratio}")
+    rng = np.random.default_rng(p)
+    offs, ids, lc, cent, cb = _random_index(rng, 6000, 128, 32, 700)
+    cent[9] = cent[4]
+    cent[300] = cent[200]
+    q = rng.standard_normal((200, 128)).astype(np.float32) * 0.7
+    q[0] = cent[4]
+    idx = fg.Index.from_arrays(128, 32, offs, ids, lc, cent, cb)
+    pid, pd = idx.coarse_search(torch.from_numpy(q).cuda(), p, prune_ratio)
+    pid, pd = _host(pid).view(np.uint32), _host(pd)
+    oid, od = oracle.coarse(q, cent, p, prune_ratio)
+    assert np.array_equal(pid, oid)
+    assert np.array_equal(_bits(pd), _bits(od))
+    idx.close()
+
+
 # --------------------------------------------------------------------------- LUT + ADC + top-k (A4-A6, A10)
 @pytest.mark.parametrize("dim,m,k", [(128, 32, 10), (128, 16, 10), (96, 48, 20), (96, 32, 64), (128, 64, 1),
                                      (96, 16, 7)])

@@ -188,6 +188,56 @@ def test_search_rerank_end_to_end():
     idx.close()
 
 
+def test_two_phase_many_probes():
+    """nprobe 200 with 70 phase-1 lists (both above one 64-probe chunk): probe
+    compaction over four chunks, cutoffs past index 64, pruned and empty
+    probes in the later chunks."""
+    _say("two_phase nprobe=200 p1=70")
+    rng = np.random.default_rng(2200)
+    nlist = 300
+    offs, ids, lc, cent, cb = _index(rng, 60000, 96, 48, nlist, empty=(5, 77, 150), big=20)
+    q = (rng.standard_normal((80, 96)) * 0.7).astype(np.float32)
+    probes, _ = oracle.coarse(q, cent, 200)
+    probes[2, 66] = 0xFFFFFFFF           # pruned inside phase 1, second chunk
+    probes[3, 130] = 0xFFFFFFFF          # pruned in phase 2, third chunk
+    probes[4, 199] = 150                 # empty list in the last chunk
+    probes[5, 65] = 77                   # empty list in phase 1, second chunk
+    p1, limit_k, coeff, rerank_m = 70, 20, 1.2, 2000
+    idx = fg.Index.from_arrays(96, 48, offs, ids, lc, cent, cb)
+    gid, gd, gcnt, gcut, gthr = idx.two_phase_search(torch.from_numpy(q).cuda(),
+                                                     torch.from_numpy(probes.view(np.int32)).cuda(), p1, limit_k,
+                                                     coeff, rerank_m, want_cutoffs=True)
+    oid, od, ocnt, ocut, othr = oracle.search_two_phase(q, cent, cb, offs, ids, lc, probes, p1, limit_k, coeff,
+                                                        rerank_m)
+    assert np.array_equal(_host(gcnt), ocnt)
+    assert np.array_equal(_host(gid), oid)
+    assert np.array_equal(_bits(_host(gd)), _bits(od))
+    assert np.array_equal(_bits(_host(gcut)), _bits(ocut))
+    assert np.array_equal(_bits(_host(gthr)), _bits(othr))
+    assert np.all(_host(gcut)[:, 64:] >= 0) and (_host(gcut)[:, 64:] > 0).any()
+    idx.close()
+
+
+def test_search_rerank_many_probes():
+    """The whole general search at nprobe 128 (coarse top-128, two-phase,
+    rerank) against the oracle."""
+    _say("search_rerank nprobe=128")
+    x = oracle.gen_gmm(40000, 96, 64, seed=12, sig_lo=0.05, sig_hi=0.15)
+    q = oracle.gen_gmm(200, 96, 64, seed=12, set=1, sig_lo=0.05, sig_hi=0.15)
+    offs, ids, codes, cent, cb = fg.build_ivfpq(torch.from_numpy(x).cuda(), 256, 48, kmeans_iters=4, init_mode=1,
+                                                seed=3, pq_iters=3, sample_size=5000)
+    idx = fg.Index.from_arrays(96, 48, offs, ids, codes, cent, cb)
+    dq, dx = torch.from_numpy(q).cuda(), torch.from_numpy(x).cuda()
+    gid, gd = idx.search_rerank(dq, dx, 128, 20, p1_lists=80, limit_k=30, threshold_coeff=1.0, rerank_m=600)
+    probes, _ = oracle.coarse(q, cent, 128)
+    assert (probes[:, 64:] != 0xFFFFFFFF).any()
+    tid, td, tc, _, _ = oracle.search_two_phase(q, cent, cb, offs, ids, codes, probes, 80, 30, 1.0, 600)
+    oid, od, _ = oracle.rerank(q, x, tid, tc, 20, 128, 0.1, 2)
+    assert np.array_equal(_host(gid), oid)
+    assert np.array_equal(_bits(_host(gd)), _bits(od))
+    idx.close()
+
+
 def test_build_ivfpq_sampled_bit_exact():
     _say("build_ivfpq sampled k-means training")
     x = oracle.gen_gmm(9000, 96, 16, seed=4, sig_lo=0.05, sig_hi=0.15)
