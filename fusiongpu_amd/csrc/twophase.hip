@@ -41,6 +41,7 @@ constexpr int kSortMax = 4096;                       // keys of one final LDS so
 constexpr int kRerankMax = 1 << 17;                  // rerank_m limit: at most 32 runs
 constexpr uint64_t kNoKey = ~0ull;                   // "no admission bound yet"
 constexpr int kMaxProbes = 4 * kWave;                // nprobe limit: four 64-probe chunks at set-up
+constexpr int kMaxLimitK = 4096;                     // limit_k limit (above 64: the pool-select phase 1)
 // Phase 1 stages the eight sorted wave lists of up to kStage lists; the waves
 // merge the staged lists in parallel when the stage is full and at the end of
 // phase 1, so no merge sits between two lists.  Four lists (16 KB) keep the
@@ -288,7 +289,94 @@ void two_phase_kernel(TwoPhaseArgs a) {
     __syncthreads();  // the stage is free again
   };
   long long c_build = 0, c_scan = 0, c_merge = 0;
-  for (int f = 0; f < nv1; ++f) {
+  // limit_k > 64: every vector of a phase-1 list is a candidate.  The list's
+  // keys go to the pool above the earlier lists' entries; whenever the next
+  // segment could overflow the pool, pool_select cuts them to the limit_k
+  // best, and later keys enter only below the limit_k-th.  The pool leaves at
+  // least 2048 slots above limit_k for every list (two_phase_pool_cap).  The
+  // list's cutoff is then the largest of the w = min(n, limit_k) keys kept,
+  // its w-th smallest distance.
+  for (int f = 0; K1 > kWave && f < nv1; ++f) {
+    const int start = f_start[f], n = f_n[f];
+    const int first = wave * kVecPerWaveRound;
+    load_pair<M>(a.codes, a.vec_ids, start, n, first + lane, w0, w1, i0, i1);
+    count_load(first, n);
+    ++st_lut;
+    build_lut(rbuf[it & 1]);
+    const int nf = f + 1 < nv ? f + 1 : -1;
+    if (nf >= 0) residual(nf, rbuf[(it + 1) & 1]);
+    if (tid == 0) s_cnt = 0;
+    __syncthreads();  // LUT and next residual ready; the list's count is 0
+    uint64_t* lp = pool + cnt_p1;
+    const int room = cap - cnt_p1;
+    const int segl = room - K1;
+    uint64_t ladm = kNoKey;
+    int held = 0;
+    int s0 = 0;
+    bool loaded = true;
+    while (true) {
+      const int s1 = n - s0 > segl ? s0 + segl : n;
+      if (held + (s1 - s0) > room) {
+        ladm = pool_select(lp, held, K1, hist, misc);
+        held = K1;
+        if (tid == 0) s_cnt = K1;
+        __syncthreads();
+      }
+      for (int base = s0 + first; base < s1; base += kTRound) {
+        if (!loaded) {
+          load_pair<M>(a.codes, a.vec_ids, start, n, base + lane, w0, w1, i0, i1);
+          count_load(base, n);
+        }
+        loaded = false;
+        const int v0 = base + lane, v1 = v0 + kWave;
+        float d0, d1;
+        adc_sum2_full<M>(lut, w0, w1, 0.0f, d0, d1);
+        const uint64_t k0 = key_of(d0, i0), k1 = key_of(d1, i1);
+        const bool pass0 = v0 < s1 && k0 < ladm, pass1 = v1 < s1 && k1 < ladm;
+        const uint64_t b0 = __ballot(pass0), b1 = __ballot(pass1);
+        const int c0 = __popcll(b0), c = c0 + __popcll(b1);
+        if (c) {
+          int at = 0;
+          if (lane == 0) at = atomicAdd(&s_cnt, c);
+          at = __shfl(at, 0, kWave);
+          const uint64_t below = (1ull << lane) - 1ull;
+          if (pass0) lp[at + __popcll(b0 & below)] = k0;
+          if (pass1) lp[at + c0 + __popcll(b1 & below)] = k1;
+        }
+      }
+      loaded = false;
+      __syncthreads();  // the segment's appends are done
+      held = s_cnt;
+      __syncthreads();  // every thread has read the count
+      if (s1 >= n) break;
+      s0 = s1;
+    }
+    if (held > K1) {
+      pool_select(lp, held, K1, hist, misc);
+      held = K1;
+    }
+    // cutoff: the largest kept key (the w-th smallest of the list)
+    uint64_t mx = 0;
+    for (int i = tid; i < held; i += kTT) mx = lp[i] > mx ? lp[i] : mx;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      const uint64_t t = ((uint64_t)(uint32_t)__shfl_xor((int)(uint32_t)(mx >> 32), o, kWave) << 32) |
+                         (uint32_t)__shfl_xor((int)(uint32_t)mx, o, kWave);
+      mx = t > mx ? t : mx;
+    }
+    if (lane == 0) s_pub[wave] = mx;
+    __syncthreads();
+    if (tid == 0) {
+      uint64_t m = s_pub[0];
+      for (int w = 1; w < kTW; ++w) m = s_pub[w] > m ? s_pub[w] : m;
+      s_cut[f_p[f]] = held > 0 ? key_dist(m) : 0.0f;
+    }
+    cnt_p1 += held;
+    ++it;
+    pre_f = nf;
+    __syncthreads();  // every wave is through list f: the LUT and s_pub are free
+  }
+  for (int f = 0; K1 <= kWave && f < nv1; ++f) {
     const long long c0 = a.stats ? clock64() : 0;
     const int start = f_start[f], n = f_n[f];
     const int first = wave * kVecPerWaveRound;
@@ -692,12 +780,14 @@ fgpu_status launch_rr(const RerankArgs& a, hipStream_t s) {
 }  // namespace
 
 int two_phase_pool_cap(int p1, int limit_k, int rerank_m) {
-  const int extra = p1 * limit_k > 2048 ? p1 * limit_k : 2048;
+  // limit_k > 64 keeps each phase-1 list's keys in the pool while it is cut
+  // to its limit_k best, so every list needs 2048 free slots above them.
+  const int extra = limit_k > kWave ? p1 * limit_k + 2048 : (p1 * limit_k > 2048 ? p1 * limit_k : 2048);
   return (rerank_m + extra + 63) / 64 * 64;
 }
 
 fgpu_status launch_two_phase(int dim, int m, const TwoPhaseArgs& a, hipStream_t s) {
-  FGPU_CHECK(a.limit_k >= 1 && a.limit_k <= 64, FGPU_ERR_UNSUPPORTED, "two_phase: limit_k must be in [1, 64]");
+  FGPU_CHECK(a.limit_k >= 1 && a.limit_k <= kMaxLimitK, FGPU_ERR_UNSUPPORTED, "two_phase: limit_k must be in [1, 4096]");
   FGPU_CHECK(a.rerank_m >= 1 && a.rerank_m <= kRerankMax, FGPU_ERR_UNSUPPORTED,
              "two_phase: rerank_m must be in [1, 131072]");
   FGPU_CHECK(a.nprobe >= 1 && a.nprobe <= kMaxProbes && a.p1 >= 0 && a.p1 <= a.nprobe, FGPU_ERR_ARG,

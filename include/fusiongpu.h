@@ -208,7 +208,8 @@ fgpu_status fgpu_search_noalloc(const fgpu_index* idx, const float* d_queries, i
  * reference stops at 1024 items), every passing vector is emitted once and
  * all rerank_m entries are gathered.  No host synchronisation and no pool
  * reallocation: the candidate pool is a bounded workspace, kept exact by
- * selecting the rerank_m best whenever it would overflow.  limit_k <= 64,
+ * selecting the rerank_m best whenever it would overflow.  limit_k <= 4096 (above 64 a
+ * slower phase 1 that cuts each list's keys to its limit_k best in the pool),
  * rerank_m <= 131072 (the reference's default is 10000), nprobe <= 256.  A workspace smaller than the returned size
  * is used in query chunks (it must hold at least one query's pool). */
 size_t fgpu_two_phase_workspace_bytes(int nq, int nprobe, int p1_lists, int limit_k, int rerank_m);

@@ -188,6 +188,37 @@ def test_search_rerank_end_to_end():
     idx.close()
 
 
+@pytest.mark.parametrize("limit_k,p1,rerank_m", [(65, 12, 1000), (300, 6, 2500), (4096, 4, 20000)])
+def test_two_phase_large_limit_k(limit_k, p1, rerank_m):
+    """limit_k above 64 (the reference's tuner sets it to the largest rank of
+    a true neighbour in its list): each phase-1 list's keys are cut to its
+    limit_k best in the pool.  Lists longer than 2048 (several segments and
+    selects), lists shorter than limit_k (w = n), a list probed twice."""
+    _say(f"two_phase limit_k={limit_k} p1={p1} rerank_m={rerank_m}")
+    rng = np.random.default_rng(limit_k)
+    nlist = 30
+    offs, ids, lc, cent, cb = _index(rng, 45000, 96, 32, nlist, empty=(4,), big=7)
+    assert np.diff(offs).max() > 4096
+    q = (rng.standard_normal((60, 96)) * 0.7).astype(np.float32)
+    probes, _ = oracle.coarse(q, cent, 10)
+    probes[1, 0] = 7                     # the long list first ...
+    probes[1, 1] = 7                     # ... and again
+    probes[2, 0] = 4                     # an empty list in phase 1
+    probes[3, 2] = 0xFFFFFFFF
+    idx = fg.Index.from_arrays(96, 32, offs, ids, lc, cent, cb)
+    gid, gd, gcnt, gcut, gthr = idx.two_phase_search(torch.from_numpy(q).cuda(),
+                                                     torch.from_numpy(probes.view(np.int32)).cuda(), p1, limit_k,
+                                                     1.0, rerank_m, want_cutoffs=True)
+    oid, od, ocnt, ocut, othr = oracle.search_two_phase(q, cent, cb, offs, ids, lc, probes, p1, limit_k, 1.0,
+                                                        rerank_m)
+    assert np.array_equal(_host(gcnt), ocnt)
+    assert np.array_equal(_host(gid), oid)
+    assert np.array_equal(_bits(_host(gd)), _bits(od))
+    assert np.array_equal(_bits(_host(gcut)), _bits(ocut))
+    assert np.array_equal(_bits(_host(gthr)), _bits(othr))
+    idx.close()
+
+
 def test_two_phase_many_probes():
     """nprobe 200 with 70 phase-1 lists (both above one 64-probe chunk): probe
     compaction over four chunks, cutoffs past index 64, pruned and empty
