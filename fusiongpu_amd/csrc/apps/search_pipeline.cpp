@@ -16,15 +16,22 @@
 // pinned memory.  The coarse step is exact by default; --coarse graph walks a
 // kNN graph of the centroids instead, with the reference's CAGRA search
 // parameters (itopk max(32, top_m), width 4, 200 iterations;
-// cagra_adapter.cuh:57-60) and graph degree 8 (cagra_adapter.cuh:15).  The stream's contexts are reused round-robin; a context's
-// results and stage times are collected when it is reused or at the end
-// (the reference hands that to a worker thread, search_pipeline.cu:392-478).
-// No call inside a batch synchronises the host.
+// cagra_adapter.cuh:57-60) and graph degree 8 (cagra_adapter.cuh:15).  The
+// stream contexts are reused round-robin.  As in the reference
+// (search_pipeline.cu:217, 392-478), a collector thread waits for each
+// submitted batch in submission order, copies its ids and stage times out of
+// pinned memory and hands the context back, while the main thread goes on
+// submitting; it blocks only when every context is still in flight.  No call
+// inside a batch synchronises the host.
 #include <algorithm>
 #include <chrono>
+#include <condition_variable>
 #include <cstring>
+#include <deque>
 #include <iomanip>
 #include <iostream>
+#include <mutex>
+#include <thread>
 #include <unordered_set>
 
 #include "app_common.hpp"
@@ -50,6 +57,8 @@ struct Ctx {
   void* d_ws = nullptr;
   size_t ws_bytes = 0;
   int start = -1, size = 0;
+  bool busy = false;  // submitted and not yet collected
+  bool keep = false;  // its results and stage times count (not a warm-up batch)
 };
 
 // The reference's recall (search_pipeline.cu:531-557): the whole gt row is the
@@ -168,23 +177,51 @@ int main(int argc, char** argv) {
   int batches_done = 0;
   bool keep = false;
 
-  auto collect = [&](Ctx& c) {
-    if (c.start < 0) return;
-    hip_ok(hipEventSynchronize(c.ev[5]), "event sync");
-    if (keep) {
-      std::memcpy(results.data() + (size_t)c.start * final_k, c.h_ids, sizeof(int32_t) * c.size * final_k);
-      for (int j = 0; j < 5; ++j) {
-        float ms = 0.0f;
-        hip_ok(hipEventElapsedTime(&ms, c.ev[j], c.ev[j + 1]), "elapsed");
-        t_stage[j] += ms;
+  // The collector: contexts are queued in submission order; it waits for each
+  // one's last event, copies its results out and marks it free.
+  std::mutex mu;
+  std::condition_variable cv_work, cv_free;
+  std::deque<int> pending;
+  bool stop = false;
+  int dev = 0;
+  hip_ok(hipGetDevice(&dev), "device");
+  std::thread collector([&]() {
+    hip_ok(hipSetDevice(dev), "collector device");
+    for (;;) {
+      int slot;
+      {
+        std::unique_lock<std::mutex> lk(mu);
+        cv_work.wait(lk, [&] { return stop || !pending.empty(); });
+        if (pending.empty()) return;  // stop, nothing left
+        slot = pending.front();
       }
-      ++batches_done;
+      Ctx& c = ctx[slot];
+      hip_ok(hipEventSynchronize(c.ev[5]), "event sync");
+      if (c.keep) {
+        std::memcpy(results.data() + (size_t)c.start * final_k, c.h_ids, sizeof(int32_t) * c.size * final_k);
+        for (int j = 0; j < 5; ++j) {
+          float ms = 0.0f;
+          hip_ok(hipEventElapsedTime(&ms, c.ev[j], c.ev[j + 1]), "elapsed");
+          t_stage[j] += ms;
+        }
+        ++batches_done;
+      }
+      {
+        std::lock_guard<std::mutex> lk(mu);
+        pending.pop_front();
+        c.start = -1;
+        c.busy = false;
+      }
+      cv_free.notify_all();
     }
-    c.start = -1;
-  };
+  });
   auto submit = [&](int b, int start, int size) {
-    Ctx& c = ctx[b % streams];
-    collect(c);
+    const int slot = b % streams;
+    Ctx& c = ctx[slot];
+    {
+      std::unique_lock<std::mutex> lk(mu);
+      cv_free.wait(lk, [&] { return !c.busy; });
+    }
     std::memcpy(c.h_q, all_q.data() + (size_t)start * dim, sizeof(float) * size * dim);
     hip_ok(hipEventRecord(c.ev[0], c.s), "record");
     hip_ok(hipMemcpyAsync(c.d_q, c.h_q, sizeof(float) * size * dim, hipMemcpyHostToDevice, c.s), "H2D");
@@ -207,11 +244,19 @@ int main(int argc, char** argv) {
     hip_ok(hipEventRecord(c.ev[4], c.s), "record");
     hip_ok(hipMemcpyAsync(c.h_ids, c.d_ids, sizeof(int32_t) * size * final_k, hipMemcpyDeviceToHost, c.s), "D2H");
     hip_ok(hipEventRecord(c.ev[5], c.s), "record");
-    c.start = start;
-    c.size = size;
+    {
+      std::lock_guard<std::mutex> lk(mu);
+      c.start = start;
+      c.size = size;
+      c.keep = keep;
+      c.busy = true;
+      pending.push_back(slot);
+    }
+    cv_work.notify_one();
   };
   auto drain = [&]() {
-    for (auto& c : ctx) collect(c);
+    std::unique_lock<std::mutex> lk(mu);
+    cv_free.wait(lk, [&] { return pending.empty(); });
   };
 
   // warm-up: one batch per stream (search_pipeline.cu:611-617)
@@ -223,6 +268,12 @@ int main(int argc, char** argv) {
   for (int b = 0; b < nb; ++b) submit(b, b * batch, std::min(batch, nq - b * batch));
   drain();
   const auto t1 = std::chrono::high_resolution_clock::now();
+  {
+    std::lock_guard<std::mutex> lk(mu);
+    stop = true;
+  }
+  cv_work.notify_all();
+  collector.join();
   const double ms = std::chrono::duration<double, std::milli>(t1 - t0).count();
   std::cout << "\nTotal time: " << ms << " ms, QPS: " << nq / (ms / 1000.0) << std::endl;
   std::cout << "\n============= Pipeline Timing Breakdown =============\n" << std::fixed << std::setprecision(3);

@@ -106,10 +106,12 @@ def test_search_pipeline_matches_library_path(tmp_path):
     fg.write_fvecs(tmp_path / "q.fvecs", q)
     gt, _ = oracle.knn_exact(q, x, 20)
     _write_ivecs(tmp_path / "gt.ivecs", gt)
-    out = _run("search_pipeline", tmp_path / "base.fvecs", tmp_path / "q.fvecs", tmp_path / "gt.ivecs", "-b", 128,
+    # batches of 64 over 3 streams: five batches, so the collector thread hands contexts back for reuse
+    out = _run("search_pipeline", tmp_path / "base.fvecs", tmp_path / "q.fvecs", tmp_path / "gt.ivecs", "-b", 64,
                "-m", 16, "-r", 500, "-k", 10, "--p1_lists", 4, "--limit_k", 30, "-s", 3, "--res", res, "--out",
                tmp_path / "out.ivecs", cwd=tmp_path)
     assert re.search(r"Total time: [\d.]+ ms, QPS: [\d.e+]+", out)
+    assert re.search(r"batch count:\s+5\b", out), out
     got = _read_ivecs(tmp_path / "out.ivecs")
     # the oracle's per-batch path: exact coarse, two-phase scan, early-stopping rerank
     offs, ids, codes, cent = fg.read_ivf_data(res / "ivf_data.bin", 32, 128)
