@@ -251,12 +251,29 @@ void two_phase_kernel(TwoPhaseArgs a) {
     // by every workgroup); holding them in registers would halve occupancy.
     const float* cbp = a.codebook + ((size_t)g * MG * kPQK + kcv) * C::S;
     const float* rg = r + g * MG * C::S;
+    // Groups of about 16 codebook floats: a group's loads are all issued
+    // before its entries are computed (the scheduling barrier keeps them
+    // together), one L2 round trip a group instead of one a subspace.
+    constexpr int GR = 16 / C::S > 0 ? 16 / C::S : 1;
 #pragma unroll
-    for (int mm = 0; mm < MG; ++mm) {
-      float rr[C::S];
+    for (int m0 = 0; m0 < MG; m0 += GR) {
+      float cv[GR * C::S];
 #pragma unroll
-      for (int j = 0; j < C::S; ++j) rr[j] = rg[mm * C::S + j];
-      dst[mm * kPQK] = lut_entry<C::S>(rr, cbp + mm * kPQK * C::S);
+      for (int mm = 0; mm < GR; ++mm) {
+#pragma unroll
+        for (int j = 0; j < C::S; ++j)
+          cv[mm * C::S + j] = m0 + mm < MG ? cbp[(m0 + mm) * kPQK * C::S + j] : 0.0f;
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int mm = 0; mm < GR; ++mm) {
+        if (m0 + mm < MG) {
+          float rr[C::S];
+#pragma unroll
+          for (int j = 0; j < C::S; ++j) rr[j] = rg[(m0 + mm) * C::S + j];
+          dst[(m0 + mm) * kPQK] = lut_entry<C::S>(rr, cv + mm * C::S);
+        }
+      }
     }
   };
 
