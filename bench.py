@@ -100,6 +100,16 @@ def stream_read_peak(torch, fg, dev, gib=4, reps=10):
     return (gib << 30) / (ms * 1e-3) / 1e9
 
 
+def row_gather_peak(torch, fg, rows, nreads, reps=5, seed=5):
+    """Measured random-row read rate over a 2-D device tensor: nreads whole rows at seeded random ids, one lane a
+    row with all of its loads in flight (the rerank's and graph search's pattern)."""
+    g = torch.Generator(device=rows.device)
+    g.manual_seed(seed)
+    idx = torch.randint(0, rows.shape[0], (nreads,), generator=g, device=rows.device, dtype=torch.int32)
+    ms = timed_ms(torch, torch.cuda.current_stream(), reps, lambda: fg.row_gather(rows, idx))
+    return nreads * rows.shape[1] * rows.element_size() / (ms * 1e-3) / 1e9
+
+
 def cpu_timed(fn, warm, runs=3):
     """Median wall time of `runs` calls of fn after one warm-up call of warm; returns (seconds, last result)."""
     warm()
@@ -433,6 +443,10 @@ def run_c3(args, torch, fg, dev):
     log(f"coarse {coarse_ms:.3f} ms, two-phase {tp_ms:.3f} ms (algorithmic ADC bytes {adc_bytes / 1e9:.2f} GB -> "
         f"{adc_gbs:.0f} GB/s), rerank {rr_ms:.3f} ms ({visited} rows = {rr_bytes / 1e9:.2f} GB -> "
         f"{rr_bytes / (rr_ms * 1e-3) / 1e9:.0f} GB/s); candidates/query {tc.float().mean().item():.0f}")
+    rows_peak = row_gather_peak(torch, fg, dx, visited)
+    read_peak = stream_read_peak(torch, fg, dev)
+    log(f"measured read rates: {rows_peak:.0f} GB/s for random {dim * 4}-byte rows of the base "
+        f"({visited} rows, one lane a row), {read_peak:.0f} GB/s streaming")
     if args.copy_probe:
         a = torch.empty(1 << 28, dtype=torch.float32, device=dev)
         b = torch.empty_like(a)
@@ -502,7 +516,11 @@ def run_c3(args, torch, fg, dev):
                      **tstats},
         "stages_ms": {"coarse": round(coarse_ms, 4), "two_phase": round(tp_ms, 4), "rerank": round(rr_ms, 4),
                       "rerank_rows": visited, "rerank_gbs": round(rr_bytes / (rr_ms * 1e-3) / 1e9, 1),
+                      "rerank_frac_of_measured_row_rate": round(rr_bytes / (rr_ms * 1e-3) / 1e9 / rows_peak, 4),
                       "candidates_per_query": round(tc.float().mean().item(), 1)},
+        "measured_read_gbs": {"random_rows": round(rows_peak, 1), "streaming": round(read_peak, 1),
+                              "note": f"random rows: {visited} whole {dim * 4}-byte rows of the base at seeded random "
+                                      "ids, one lane a row (fgpu_row_gather); streaming: fgpu_stream_read over 4 GiB"},
         "cpu_baseline": cpu, "parity": parity, "recall_at_k": recall,
         "ground_truth": {"seconds": round(gt_s, 3), "oracle_parity_50": gt_parity},
     }
@@ -665,6 +683,8 @@ def run_c5(args, torch, fg, dev):
     gbs = gather_bytes / (kern_ms * 1e-3) / 1e9
     log(f"graph search: {ms_per_step:.3f} ms/step, {qps:,.0f} QPS; kernel {kern_ms:.3f} ms; {n_steps / nq:.1f} steps "
         f"and {n_evals / nq:.0f} distance evaluations per query -> {gather_bytes / 1e9:.2f} GB = {gbs:.0f} GB/s")
+    rows_peak = row_gather_peak(torch, fg, dx, n_evals)
+    log(f"measured read rate for random {dim * 4}-byte rows of the base: {rows_peak:.0f} GB/s ({n_evals} rows)")
     gid, gd = out[0].cpu().numpy(), out[1].cpu().numpy()
     gt, _ = fg.knn_exact(dq, dx, k)
     gt = gt.cpu().numpy()
@@ -701,7 +721,11 @@ def run_c5(args, torch, fg, dev):
         "roofline": {"bound": "hbm", "kernel": "graph_search_kernel<128>", "achieved": round(gbs, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
                      "algorithmic_bytes_per_launch": gather_bytes, "avg_launch_ms": round(kern_ms, 4),
-                     "distance_evaluations": n_evals, "steps": n_steps},
+                     "distance_evaluations": n_evals, "steps": n_steps,
+                     "measured_row_gather_gbs": round(rows_peak, 1),
+                     "frac_of_measured_row_rate": round(gbs / rows_peak, 4),
+                     "note": "achieved = distance rows + adjacency rows read / kernel time; the measured row rate is "
+                             "fgpu_row_gather over as many random whole rows of the base, one lane a row"},
         "cpu_baseline": cpu, "parity": parity, "recall_at_k": recall,
     }
     print(json.dumps(res), flush=True)

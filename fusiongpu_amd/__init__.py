@@ -33,7 +33,7 @@ __all__ = [
     "FgpuError", "lib", "lib_path", "Index", "gen_gmm", "l2_topk", "kmeans_fit", "kmeans_update",
     "fixed_shift", "pq_train", "pq_encode", "build_ivfpq", "write_ivf_data", "read_ivf_data",
     "write_fvecs", "read_fvecs", "read_ivecs", "probe_counts", "rerank", "knn_exact", "graph_search",
-    "debug_set_spin_limit", "debug_set_list_skip", "stream_read", "FAULT_ID", "prune_probes",
+    "debug_set_spin_limit", "debug_set_list_skip", "stream_read", "row_gather", "FAULT_ID", "prune_probes",
 ]
 
 lib_path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib", "libfusiongpu.so")
@@ -56,6 +56,7 @@ _SIGS = {
     "fgpu_debug_set_list_skip": (None, [_i32]),
     "fgpu_stream_read_grid": (_i32, []),
     "fgpu_stream_read": (_i32, [_vp, _sz, _vp, _vp]),
+    "fgpu_row_gather": (_i32, [_vp, _i64, _i32, _vp, _i64, _vp, _vp]),
     "fgpu_coarse_workspace_bytes": (_sz, [_i32, _i32]),
     "fgpu_coarse_search": (_i32, [_vp, _vp, _i32, _i32, _f32, _vp, _vp, _vp, _sz, _vp]),
     "fgpu_coarse_graph_workspace_bytes": (_sz, [_i32, _i32]),
@@ -328,6 +329,19 @@ def stream_read(data, stream=None):
             raise ValueError("stream_read: expected a contiguous device tensor")
         sink = torch.empty(lib.fgpu_stream_read_grid(), dtype=torch.int64, device="cuda")
         _check(lib.fgpu_stream_read(_dev_ptr(data), data.numel() * data.element_size(), _dev_ptr(sink), _stream()))
+
+
+def row_gather(rows, idx, stream=None):
+    """Read whole rows rows[idx[i]] (384- or 512-byte rows of a contiguous 2-D device tensor), one lane a row
+    (fgpu_row_gather), for a measured random-row read rate."""
+    torch = _torch()
+    with _on(stream):
+        if not (torch.is_tensor(rows) and rows.is_cuda and rows.is_contiguous() and rows.dim() == 2):
+            raise ValueError("row_gather: expected a contiguous 2-D device tensor")
+        ix = _dev(idx, torch.int32, "idx", (None,))
+        sink = torch.empty(lib.fgpu_stream_read_grid(), dtype=torch.int64, device="cuda")
+        _check(lib.fgpu_row_gather(_dev_ptr(rows), rows.shape[0], rows.shape[1] * rows.element_size(), _dev_ptr(ix),
+                                   ix.shape[0], _dev_ptr(sink), _stream()))
 
 
 # --------------------------------------------------------------------------- index + search

@@ -1,5 +1,6 @@
-// bandwidth.hip -- a streaming read of device memory, to measure the HBM read
-// rate the roofline figures are set against (no reference counterpart).
+// bandwidth.hip -- a streaming read and a random-row gather of device memory,
+// to measure the HBM read rates the roofline figures are set against (no
+// reference counterpart).
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -31,7 +32,49 @@ __global__ __launch_bounds__(256) void stream_read_kernel(const uint4* __restric
   if (threadIdx.x == 0) sink[blockIdx.x] = red[0];
 }
 
+// Random rows: each lane reads whole rows idx[i] (RB 16-byte loads, all
+// issued before any is used), the access pattern of the exact rerank and the
+// graph search (one lane a candidate row).
+template <int RB>
+__global__ __launch_bounds__(256) void row_gather_kernel(const uint4* __restrict__ d, int64_t nrows,
+                                                         const int32_t* __restrict__ idx, int64_t n,
+                                                         unsigned long long* __restrict__ sink) {
+  const int64_t stride = (int64_t)gridDim.x * 256;
+  uint32_t acc = 0;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += stride) {
+    const int64_t r = min(max((int64_t)idx[i], (int64_t)0), nrows - 1);  // out-of-range ids read a valid row
+    const uint4* row = d + r * RB;
+    uint4 v[RB];
+#pragma unroll
+    for (int j = 0; j < RB; ++j) v[j] = row[j];
+#pragma unroll
+    for (int j = 0; j < RB; ++j) acc ^= v[j].x ^ v[j].y ^ v[j].z ^ v[j].w;
+  }
+  __shared__ uint32_t red[256];
+  red[threadIdx.x] = acc;
+  __syncthreads();
+  for (int o = 128; o > 0; o >>= 1) {
+    if ((int)threadIdx.x < o) red[threadIdx.x] ^= red[threadIdx.x + o];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) sink[blockIdx.x] = red[0];
+}
+
 }  // namespace
+
+fgpu_status launch_row_gather(const void* d, int64_t nrows, int row_bytes, const int32_t* idx, int64_t n,
+                              unsigned long long* sink, int grid, hipStream_t s) {
+  if (n <= 0 || nrows <= 0 || grid <= 0) return FGPU_OK;
+  const uint4* p = reinterpret_cast<const uint4*>(d);
+  if (row_bytes == 384)
+    hipLaunchKernelGGL(row_gather_kernel<24>, dim3((unsigned)grid), dim3(256), 0, s, p, nrows, idx, n, sink);
+  else if (row_bytes == 512)
+    hipLaunchKernelGGL(row_gather_kernel<32>, dim3((unsigned)grid), dim3(256), 0, s, p, nrows, idx, n, sink);
+  else
+    return set_error(FGPU_ERR_UNSUPPORTED, "row_gather: row_bytes must be 384 or 512");
+  FGPU_HIP(hipGetLastError());
+  return FGPU_OK;
+}
 
 fgpu_status launch_stream_read(const void* d, size_t bytes, unsigned long long* sink, int grid, hipStream_t s) {
   if (bytes == 0 || grid <= 0) return FGPU_OK;

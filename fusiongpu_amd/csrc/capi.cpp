@@ -351,6 +351,13 @@ fgpu_status fgpu_stream_read(const void* d, size_t bytes, unsigned long long* d_
   return launch_stream_read(d, bytes, d_sink, fgpu_stream_read_grid(), as_stream(stream));
 }
 
+fgpu_status fgpu_row_gather(const void* d_rows, int64_t nrows, int row_bytes, const int32_t* d_idx, int64_t n,
+                            unsigned long long* d_sink, void* stream) {
+  FGPU_CHECK(d_rows && d_idx && d_sink && n >= 0 && nrows >= 1 && ((uintptr_t)d_rows & 15) == 0, FGPU_ERR_ARG,
+             "row_gather: need 16-byte aligned rows, indices and a sink");
+  return launch_row_gather(d_rows, nrows, row_bytes, d_idx, n, d_sink, fgpu_stream_read_grid(), as_stream(stream));
+}
+
 size_t fgpu_search_workspace_bytes(int nq, int nlist, int nprobe) {
   return carve_bytes<uint32_t>((size_t)nq * nprobe) + carve_bytes<float>((size_t)nq * nprobe) +
          carve_bytes<int>(1) + fgpu_coarse_workspace_bytes(nq, nlist);

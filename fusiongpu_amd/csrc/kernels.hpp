@@ -182,6 +182,8 @@ fgpu_status launch_tune_list_stats(const TuneStatsArgs& a, int npairs, hipStream
 // Reads `bytes` (a multiple of 16) from d with 16-byte loads; one XOR per
 // workgroup goes to sink[blockIdx.x] so the loads cannot be dropped.
 fgpu_status launch_stream_read(const void* d, size_t bytes, unsigned long long* sink, int grid, hipStream_t s);
+fgpu_status launch_row_gather(const void* d, int64_t nrows, int row_bytes, const int32_t* idx, int64_t n,
+                              unsigned long long* sink, int grid, hipStream_t s);
 
 // ---- build.hip ----------------------------------------------------------------
 fgpu_status launch_probe_counts(const uint32_t* probes, int nq, int nprobe, int nlist, const int32_t* offsets,

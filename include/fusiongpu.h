@@ -111,6 +111,13 @@ void fgpu_debug_set_list_skip(int enabled);
  * 8 TB/s figure.  d_sink: fgpu_stream_read_grid() uint64 values, overwritten. */
 int fgpu_stream_read_grid(void);
 fgpu_status fgpu_stream_read(const void* d_data, size_t bytes, unsigned long long* d_sink, void* stream);
+/* Reads n whole rows d_rows[d_idx[i]] of row_bytes (384 or 512) each, one
+ * lane a row with all of its 16-byte loads in flight: the access pattern of
+ * the exact rerank and the graph search, to measure the random-row read rate
+ * their rooflines are set against.  Ids outside [0, nrows) are clamped.
+ * d_sink as for fgpu_stream_read. */
+fgpu_status fgpu_row_gather(const void* d_rows, int64_t nrows, int row_bytes, const int32_t* d_idx, int64_t n,
+                            unsigned long long* d_sink, void* stream);
 
 /* ---- search: coarse quantizer (A2 + A3) -------------------------------- */
 
