@@ -392,22 +392,6 @@ fgpu_status pp_update(const float* x, int64_t n, int dim, const float* c, int in
   return FGPU_OK;
 }
 
-// cc[a] = ||c_j - c_a||^2 for every earlier centre a < j (fused chain; only a
-// bound is needed from it).
-__global__ __launch_bounds__(256) void pp_cc_kernel(const float* __restrict__ cent, int dim, int j,
-                                                    float* __restrict__ cc) {
-  const int a = blockIdx.x * 256 + threadIdx.x;
-  if (a >= j) return;
-  const float* cj = cent + (size_t)j * dim;
-  const float* ca = cent + (size_t)a * dim;
-  float acc = 0.0f;
-  for (int d = 0; d < dim; ++d) {
-    const float df = cj[d] - ca[d];
-    acc = __builtin_fmaf(df, df, acc);
-  }
-  cc[a] = acc;
-}
-
 // shift from the first round's max d2 (so n * max w < 2^62).
 __global__ __launch_bounds__(1024) void pp_shift_kernel(const float* __restrict__ d2, int64_t n, int* __restrict__ shift) {
   __shared__ float part[16];
@@ -431,9 +415,11 @@ __global__ __launch_bounds__(1024) void pp_shift_kernel(const float* __restrict_
 // Pick the next centre: smallest i with inclusive prefix(w) > u, u = r_j % total.
 // One workgroup; state[0] = chosen row.  chosen[] marks picked rows for the
 // all-zero fallback.
+// Then (cent != nullptr) take the picked row as centre j.
 __global__ __launch_bounds__(1024) void pp_pick_kernel(const uint64_t* __restrict__ w, const uint64_t* __restrict__ part,
                                                        int nblocks, int64_t n, uint64_t seed, int j,
-                                                       const uint8_t* __restrict__ chosen, int32_t* __restrict__ rows) {
+                                                       uint8_t* __restrict__ chosen, int32_t* __restrict__ rows,
+                                                       const float* __restrict__ x, int dim, float* __restrict__ cent) {
   __shared__ uint64_t s_tot;
   __shared__ uint64_t s_u;
   __shared__ int64_t s_pick;
@@ -489,27 +475,53 @@ __global__ __launch_bounds__(1024) void pp_pick_kernel(const uint64_t* __restric
       int64_t pick = 0;
       for (int64_t i = 0; i < n; ++i)
         if (!chosen[i]) { pick = i; break; }
-      rows[j] = (int32_t)pick;
+      s_pick = pick;
     }
-    return;
-  }
-  // Inside the block: inclusive scan of its 1024 weights.
-  const int64_t i = (int64_t)s_blk * kPPBlock + tid;
-  const uint64_t wi = i < n ? w[i] : 0;
-  sc[tid] = wi;
-  __syncthreads();
-  for (int o = 1; o < kPPBlock; o <<= 1) {
-    uint64_t t = tid >= o ? sc[tid - o] : 0;
+  } else {
+    // Inside the block: inclusive scan of its 1024 weights.
+    const int64_t i = (int64_t)s_blk * kPPBlock + tid;
+    const uint64_t wi = i < n ? w[i] : 0;
+    sc[tid] = wi;
     __syncthreads();
-    sc[tid] += t;
+    for (int o = 1; o < kPPBlock; o <<= 1) {
+      uint64_t t = tid >= o ? sc[tid - o] : 0;
+      __syncthreads();
+      sc[tid] += t;
+      __syncthreads();
+    }
+    const uint64_t incl = s_before + sc[tid];
+    const uint64_t excl = incl - wi;
+    if (i < n && excl <= s_u && s_u < incl) s_pick = i;
     __syncthreads();
+    // s_u lies inside block s_blk by construction; the fallback only keeps the row in range.
+    if (tid == 0 && s_pick < 0) s_pick = (int64_t)s_blk * kPPBlock;
   }
-  const uint64_t incl = s_before + sc[tid];
-  const uint64_t excl = incl - wi;
-  if (i < n && excl <= s_u && s_u < incl) s_pick = i;
   __syncthreads();
-  // s_u lies inside block s_blk by construction; the fallback only keeps the row in range.
-  if (tid == 0) rows[j] = (int32_t)(s_pick >= 0 ? s_pick : (int64_t)s_blk * kPPBlock);
+  const int64_t r = s_pick;
+  if (tid == 0) rows[j] = (int32_t)r;
+  if (!cent) return;
+  for (int d = tid; d < dim; d += kPPBlock) cent[(int64_t)j * dim + d] = x[r * dim + d];
+  if (tid == 0) chosen[r] = 1;
+}
+
+// cc[a] = ||c_j - c_a||^2 for every earlier centre a < j: one wave per centre,
+// lanes over dimensions.  Only the skip bound reads cc, and that bound holds
+// for any summation order.
+__global__ __launch_bounds__(256) void pp_cc_kernel(const float* __restrict__ cent, int dim, int j,
+                                                    float* __restrict__ cc) {
+  const int a = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (a >= j) return;
+  const float* cj = cent + (size_t)j * dim;
+  const float* ca = cent + (size_t)a * dim;
+  float acc = 0.0f;
+  for (int d = lane; d < dim; d += 64) {
+    const float df = cj[d] - ca[d];
+    acc = __builtin_fmaf(df, df, acc);
+  }
+#pragma unroll
+  for (int m = 32; m > 0; m >>= 1) acc += shfl_xor_f(acc, m);
+  if (lane == 0) cc[a] = acc;
 }
 
 __global__ void pp_take_kernel(const float* __restrict__ x, int dim, const int32_t* __restrict__ rows, int j,
@@ -693,10 +705,11 @@ fgpu_status launch_kmeans_pp(const float* x, int64_t n, int dim, int k, uint64_t
   // weights for round 1 from the initial d2 (every row: no skip yet)
   FGPU_TRY(pp_update(x, n, dim, cent, 0, d2, shift, w, part, nb, nullptr, cc, 0, s));
   for (int j = 1; j < k; ++j) {
-    hipLaunchKernelGGL(pp_pick_kernel, dim3(1), dim3(kPPBlock), 0, s, w, part, nb, n, seed, j, chosen, rows);
-    hipLaunchKernelGGL(pp_take_kernel, dim3(1), dim3(256), 0, s, x, dim, rows, j, cent, chosen);
+    // pick and take the row as centre j in one workgroup
+    hipLaunchKernelGGL(pp_pick_kernel, dim3(1), dim3(kPPBlock), 0, s, w, part, nb, n, seed, j, chosen, rows, x, dim,
+                       cent);
     if (j + 1 < k) {
-      hipLaunchKernelGGL(pp_cc_kernel, dim3((unsigned)((j + 255) / 256)), dim3(256), 0, s, cent, dim, j, cc);
+      hipLaunchKernelGGL(pp_cc_kernel, dim3((unsigned)((j + 3) / 4)), dim3(256), 0, s, cent, dim, j, cc);
       FGPU_TRY(pp_update(x, n, dim, cent + (size_t)j * dim, 0, d2, shift, w, part, nb, asg, cc, j, s));
     }
   }
