@@ -248,12 +248,13 @@ size_t fgpu_coarse_workspace_bytes(int nq, int nlist) {
   // The estimate block holds whole 64-row GEMM tiles: with room for every
   // query row rounded up to 64, the coarse step is one GEMM + one select.
   const size_t rows = ((size_t)std::max(nq, 64) + 63) / 64 * 64;
-  return carve_bytes<float>((size_t)nq) + carve_bytes<float>(rows * nlist) + 256;
+  return carve_bytes<float>((size_t)nq) + carve_bytes<float>(rows * (size_t)est_sel_ld(nlist)) + 256;
 }
 
 fgpu_status fgpu_coarse_search(const fgpu_index* ix, const float* dq, int nq, int nprobe, float prune_ratio,
                                uint32_t* d_ids, float* d_dists, void* ws, size_t ws_bytes, void* stream) {
   FGPU_CHECK(ix && dq && d_ids && d_dists && ws, FGPU_ERR_ARG, "coarse_search: null argument");
+  FGPU_CHECK(((uintptr_t)ws & 15) == 0, FGPU_ERR_ARG, "coarse_search: workspace must be 16-byte aligned");
   FGPU_CHECK(nq >= 0 && nprobe >= 1 && nprobe <= ix->nlist && nprobe <= 256, FGPU_ERR_ARG,
              "coarse_search: need 1 <= nprobe <= min(nlist, 256)");
   if (nq == 0) return FGPU_OK;
@@ -261,16 +262,18 @@ fgpu_status fgpu_coarse_search(const fgpu_index* ix, const float* dq, int nq, in
   Carve cv(ws, ws_bytes);
   float* xn = cv.take<float>(nq);
   const size_t rest = ws_bytes > cv.used ? ws_bytes - cv.used : 0;
-  int64_t rows = std::min<int64_t>(est_rows_per_batch(rest > 256 ? rest - 256 : 0, ix->nlist), ((nq + 63) / 64) * 64);
+  const int64_t ld = est_sel_ld(ix->nlist);
+  int64_t rows = std::min<int64_t>(est_rows_per_batch(rest > 256 ? rest - 256 : 0, (int)ld), ((nq + 63) / 64) * 64);
   FGPU_CHECK(xn && rows >= 64, FGPU_ERR_WORKSPACE, "coarse_search: workspace too small");
-  float* est = cv.take<float>((size_t)rows * ix->nlist);
+  void* est = cv.take<float>((size_t)rows * ld);
   FGPU_CHECK(est, FGPU_ERR_WORKSPACE, "coarse_search: workspace too small");
-  FGPU_TRY(launch_row_norms(dq, nq, ix->dim, xn, s));
+  // The estimates leave out each query's norm; the select computes it for
+  // its margin.
   for (int64_t b0 = 0; b0 < nq; b0 += rows) {
     const int64_t nb = std::min<int64_t>(rows, nq - b0);
-    FGPU_TRY(launch_gemm_est(dq + b0 * ix->dim, nb, ix->d_centroids, ix->nlist, ix->dim, xn + b0, ix->d_cnorm, est,
-                             ix->nlist, s));
-    FGPU_TRY(launch_select_exact(est, ix->nlist, nb, ix->nlist, dq + b0 * ix->dim, ix->d_centroids, ix->dim, xn + b0,
+    FGPU_TRY(launch_gemm_est_sel(dq + b0 * ix->dim, nb, ix->d_centroids, ix->nlist, ix->dim, ix->d_cnorm, est, ld,
+                                 s));
+    FGPU_TRY(launch_select_exact(est, ld, nb, ix->nlist, dq + b0 * ix->dim, ix->d_centroids, ix->dim,
                                  ix->d_cnorm_max, nprobe, 1, prune_ratio,
                                  reinterpret_cast<int32_t*>(d_ids) + b0 * nprobe, d_dists + b0 * nprobe, s));
   }
@@ -481,31 +484,33 @@ fgpu_status fgpu_search_rerank(const fgpu_index* ix, const float* dq, int nq, in
 
 // ---------------------------------------------------------------------------
 size_t fgpu_l2_topk_workspace_bytes(int64_t n, int nc) {
-  return carve_bytes<float>(n) + carve_bytes<float>(nc) + 256 + carve_bytes<float>((size_t)topk_batch_rows(n, nc) * nc);
+  return carve_bytes<float>(n) + carve_bytes<float>(nc) + 256 +
+         carve_bytes<float>((size_t)topk_batch_rows(n, nc) * (size_t)est_sel_ld(nc));
 }
 
 fgpu_status fgpu_l2_topk(const float* dx, int64_t n, const float* dc, int nc, int dim, int p, int32_t* d_ids,
                          float* d_dists, void* ws, size_t ws_bytes, void* stream) {
   FGPU_CHECK(dx && dc && d_ids && d_dists && ws, FGPU_ERR_ARG, "l2_topk: null argument");
+  FGPU_CHECK(((uintptr_t)ws & 15) == 0, FGPU_ERR_ARG, "l2_topk: workspace must be 16-byte aligned");
   FGPU_CHECK(n >= 0 && nc >= 1 && dim >= 1 && p >= 1 && p <= nc && p <= 256, FGPU_ERR_ARG, "l2_topk: bad sizes");
   if (n == 0) return FGPU_OK;
   hipStream_t s = as_stream(stream);
   Carve cv(ws, ws_bytes);
-  float* xn = cv.take<float>(n);
+  (void)cv.take<float>(n);  // the query-norm slot of the workspace layout, no longer written
   float* cn = cv.take<float>(nc);
   float* cmax = cv.take<float>(64);
   FGPU_CHECK(cv.ok(), FGPU_ERR_WORKSPACE, "l2_topk: workspace too small");
   const size_t rest = ws_bytes - cv.used;
-  const int64_t rows = std::min<int64_t>(est_rows_per_batch(rest, nc), ((n + 63) / 64) * 64);
+  const int64_t ld = est_sel_ld(nc);
+  const int64_t rows = std::min<int64_t>(est_rows_per_batch(rest, (int)ld), ((n + 63) / 64) * 64);
   FGPU_CHECK(rows >= 64, FGPU_ERR_WORKSPACE, "l2_topk: workspace too small");
-  float* est = cv.take<float>((size_t)rows * nc);
-  FGPU_TRY(launch_row_norms(dx, n, dim, xn, s));
+  void* est = cv.take<float>((size_t)rows * ld);
   FGPU_TRY(launch_row_norms(dc, nc, dim, cn, s));
   FGPU_TRY(launch_max_reduce(cn, nc, cmax, s));
   for (int64_t b0 = 0; b0 < n; b0 += rows) {
     const int64_t nb = std::min<int64_t>(rows, n - b0);
-    FGPU_TRY(launch_gemm_est(dx + b0 * dim, nb, dc, nc, dim, xn + b0, cn, est, nc, s));
-    FGPU_TRY(launch_select_exact(est, nc, nb, nc, dx + b0 * dim, dc, dim, xn + b0, cmax, p, 0, 0.0f, d_ids + b0 * p,
+    FGPU_TRY(launch_gemm_est_sel(dx + b0 * dim, nb, dc, nc, dim, cn, est, ld, s));
+    FGPU_TRY(launch_select_exact(est, ld, nb, nc, dx + b0 * dim, dc, dim, cmax, p, 0, 0.0f, d_ids + b0 * p,
                                  d_dists + b0 * p, s));
   }
   return FGPU_OK;

@@ -11,7 +11,14 @@
 //     |est - exact| <= E = kappa * (||x||^2 + max_c ||c||^2),
 //     kappa = 8 * gamma(2*dim + 8),  gamma(n) = n*u / (1 - n*u),  u = 2^-24
 // (standard forward error bounds for dot products in any summation order,
-// with a factor 2 of slack).  With T the p-th smallest estimate, every column
+// with a factor 2 of slack).  For dim % 32 == 0 the contraction runs on the
+// bf16 MFMA units instead, with each operand split as v = hi + lo + e, hi and
+// lo bf16 and |e| <= 2^-14 |v| (two faithful bf16 roundings), and
+// <x,c> ~ hi_x.hi_c + hi_x.lo_c + lo_x.hi_c: the three products of bf16
+// values are exact in fp32, and the dropped terms add at most
+// 3.1 * 2^-14 * sum|x_k c_k| <= 1.55 * 2^-14 (||x||^2 + ||c||^2) to the dot
+// product, so that kappa gains 4 * 2^-14 and the fp32 sum runs over 3*dim
+// products (kappa = 8 gamma(3 dim + 8) + 4 * 2^-14).  With T the p-th smallest estimate, every column
 // of the exact top-p has est <= T + 2E, so re-scoring exactly that superset
 // and sorting by (exact distance, index) yields the exact answer with the tie
 // rule, independent of the GEMM's summation order.
@@ -66,15 +73,50 @@ __global__ __launch_bounds__(1024) void max_reduce_kernel(const float* __restric
   }
 }
 
+// fp16 lower bounds of the estimates (the select's input): the largest fp16
+// value <= v (round to nearest, then one step toward -inf when that rounded
+// up; above the fp16 range this is 65504, below it -inf).
+__device__ __forceinline__ uint16_t half_at_or_below(float v) {
+  const _Float16 h = (_Float16)v;
+  uint16_t u = __builtin_bit_cast(uint16_t, h);
+  if ((float)h > v) u = (u & 0x8000u) ? (uint16_t)(u + 1u) : (uint16_t)(u - 1u);
+  return u;
+}
+__device__ __forceinline__ float half_bits_float(uint16_t u) { return (float)__builtin_bit_cast(_Float16, u); }
+// The smallest fp16 value above the fp16 value f (+inf and NaN stay).
+__device__ __forceinline__ float half_next_up(float f) {
+  uint16_t u = __builtin_bit_cast(uint16_t, (_Float16)f);
+  if ((u & 0x7C00u) == 0x7C00u && !(u & 0x8000u)) return f;  // +inf, NaN
+  if ((u & 0x7FFFu) == 0) u = 1u;                            // +-0 -> smallest subnormal
+  else u = (u & 0x8000u) ? (uint16_t)(u - 1u) : (uint16_t)(u + 1u);
+  return half_bits_float(u);
+}
+
+// Where an estimate tile goes (output mode OM).  kOutFull: fp32
+// xn[i] + cn[j] - 2 <x_i, c_j>.  kOutShift: fp32 cn[j] - 2 <x_i, c_j>, the row
+// shifted by its norm (xn unused).  kOutHalf: the fp16 lower bound (bit
+// pattern) of the shifted value.
+constexpr int kOutFull = 0, kOutShift = 1, kOutHalf = 2;
+template <int OM>
+__device__ __forceinline__ void put_est(void* est, int64_t off, const float* xn, int64_t i, float cj, float acc) {
+  if constexpr (OM == kOutHalf)
+    static_cast<uint16_t*>(est)[off] = half_at_or_below(cj - 2.0f * acc);
+  else if constexpr (OM == kOutShift)
+    static_cast<float*>(est)[off] = cj - 2.0f * acc;
+  else
+    static_cast<float*>(est)[off] = (xn[i] + cj) - 2.0f * acc;
+}
+
 // 64x64 output tile per workgroup, 4 waves each owning a 32x32 quadrant.
 // Operand tiles are staged k-major in LDS with a 96-float row stride, so the
 // MFMA operand reads (lanes 0-31: k, lanes 32-63: k+1) and the staging writes
 // (one row per lane) both hit distinct banks.
+template <int OM>
 __global__ __launch_bounds__(256) void gemm_est_kernel(const float* __restrict__ x, int64_t nrows,
                                                        const float* __restrict__ c, int ncols, int dim,
                                                        const float* __restrict__ xn,
                                                        const float* __restrict__ cn,
-                                                       float* __restrict__ est, int64_t ld) {
+                                                       void* __restrict__ est, int64_t ld) {
   __shared__ float As[kTK][kLdsStride];
   __shared__ float Bs[kTK][kLdsStride];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -116,28 +158,52 @@ __global__ __launch_bounds__(256) void gemm_est_kernel(const float* __restrict__
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
     const int64_t i = row0 + wr * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-    if (i < nrows) est[i * ld + j] = (xn[i] + cj) - 2.0f * acc[r];
+    if (i < nrows) put_est<OM>(est, i * ld + j, xn, i, cj, acc[r]);
   }
 }
 
-// The same estimate for dim % 32 == 0, pipelined: each K stage of 32 is
-// staged with coalesced 16-byte loads (a thread loads rows t / 8 and
-// t / 8 + 32 at float4 t % 8: eight rows of 128 bytes an instruction), the
-// next stage's loads are in flight while the current stage's MFMAs run, and
-// the LDS tiles ([row][k], stride 36 floats: conflict-free 16-byte reads) are
-// double-buffered, so one barrier a stage.  Each wave reads its operands with
-// 16-byte LDS loads that feed four MFMAs: MFMA 4j + e of a stage contracts
-// k = 16 h + 4 j + e for lane half h, a permutation of the stage's 32 k's;
-// the error margin holds for any summation order.  Rows and columns past the
-// end are loaded clamped to the last one and never written.
-constexpr int kS2 = 36;
-__global__ __launch_bounds__(256) void gemm_est32_kernel(const float* __restrict__ x, int64_t nrows,
-                                                         const float* __restrict__ c, int ncols, int dim,
-                                                         const float* __restrict__ xn,
-                                                         const float* __restrict__ cn,
-                                                         float* __restrict__ est, int64_t ld) {
-  __shared__ __align__(16) float As[2][kTM * kS2];
-  __shared__ __align__(16) float Bs[2][kTN * kS2];
+// The estimate for dim % 32 == 0 on v_mfma_f32_32x32x16_bf16 with the
+// hi/lo split above (three MFMAs a k-step: hi.hi, hi.lo, lo.hi).  Same grid
+// and 64x64 tile as gemm_est_kernel.  Each K stage of 32 is staged with
+// coalesced 16-byte loads (a thread loads rows t / 8 and t / 8 + 32 at float4
+// t % 8: eight rows of 128 bytes an instruction), the next stage's loads are
+// in flight while the current stage's MFMAs run, and the two LDS buffers take
+// turns, so one barrier a stage.  A stage is split into bf16 hi/lo while it
+// is written to LDS, one staged row = 32 hi, 32 lo and 8 pad bf16 (144 bytes,
+// an odd multiple of 16: the 16-byte operand reads of 16 consecutive rows hit
+// distinct banks).  MFMA s of a stage contracts k = 16 s + 8 h + e (lane half
+// h, element e) for A and B alike.  Rows and columns past the end are loaded
+// clamped to the last one and never written.  The tile leaves through LDS
+// (stride 72 floats: a store's two row segments hit distinct banks) so that
+// each thread writes four float4 rows of it instead of sixteen scattered
+// floats.
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+constexpr int kB3Row = 72;
+constexpr int kCStride = 72;
+// The select reads fp16 lower bounds of the shifted estimates (true) or the
+// fp32 values themselves (false).
+constexpr bool kEstHalf = true;  // 64 x 72 floats = 18 KB, inside the 36 KB of operand buffers
+
+__device__ __forceinline__ void split_put(__bf16* row, int sf, const float4 v) {
+  bf16x4 h, l;
+  h[0] = (__bf16)v.x; h[1] = (__bf16)v.y; h[2] = (__bf16)v.z; h[3] = (__bf16)v.w;
+  l[0] = (__bf16)(v.x - (float)h[0]);
+  l[1] = (__bf16)(v.y - (float)h[1]);
+  l[2] = (__bf16)(v.z - (float)h[2]);
+  l[3] = (__bf16)(v.w - (float)h[3]);
+  *reinterpret_cast<bf16x4*>(row + 4 * sf) = h;
+  *reinterpret_cast<bf16x4*>(row + 32 + 4 * sf) = l;
+}
+
+template <int OM>
+__global__ __launch_bounds__(256) void gemm_est_split_kernel(const float* __restrict__ x, int64_t nrows,
+                                                             const float* __restrict__ c, int ncols, int dim,
+                                                             const float* __restrict__ xn,
+                                                             const float* __restrict__ cn,
+                                                             void* __restrict__ est, int64_t ld) {
+  __shared__ __align__(16) __bf16 As[2][kTM * kB3Row];
+  __shared__ __align__(16) __bf16 Bs[2][kTN * kB3Row];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int64_t row0 = (int64_t)blockIdx.x * kTM;
   const int col0 = blockIdx.y * kTN;
@@ -154,10 +220,10 @@ __global__ __launch_bounds__(256) void gemm_est32_kernel(const float* __restrict
 #pragma unroll
   for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
   const int nst = dim / 32;
-  *reinterpret_cast<float4*>(&As[0][sr * kS2 + 4 * sf]) = ra0;
-  *reinterpret_cast<float4*>(&As[0][(sr + 32) * kS2 + 4 * sf]) = ra1;
-  *reinterpret_cast<float4*>(&Bs[0][sr * kS2 + 4 * sf]) = rb0;
-  *reinterpret_cast<float4*>(&Bs[0][(sr + 32) * kS2 + 4 * sf]) = rb1;
+  split_put(&As[0][sr * kB3Row], sf, ra0);
+  split_put(&As[0][(sr + 32) * kB3Row], sf, ra1);
+  split_put(&Bs[0][sr * kB3Row], sf, rb0);
+  split_put(&Bs[0][(sr + 32) * kB3Row], sf, rb1);
   __syncthreads();
   for (int st = 0; st < nst; ++st) {
     const int buf = st & 1;
@@ -168,35 +234,86 @@ __global__ __launch_bounds__(256) void gemm_est32_kernel(const float* __restrict
       rb0 = *reinterpret_cast<const float4*>(bp0 + ko);
       rb1 = *reinterpret_cast<const float4*>(bp1 + ko);
     }
-    const float* Ar = &As[buf][(wr * 32 + li) * kS2 + 16 * lh];
-    const float* Br = &Bs[buf][(wc * 32 + li) * kS2 + 16 * lh];
+    const __bf16* Ar = &As[buf][(wr * 32 + li) * kB3Row + 8 * lh];
+    const __bf16* Br = &Bs[buf][(wc * 32 + li) * kB3Row + 8 * lh];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const float4 av = *reinterpret_cast<const float4*>(Ar + 4 * j);
-      const float4 bv = *reinterpret_cast<const float4*>(Br + 4 * j);
-      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.x, bv.x, acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.y, bv.y, acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.z, bv.z, acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.w, bv.w, acc, 0, 0, 0);
+    for (int s2 = 0; s2 < 2; ++s2) {
+      const bf16x8 ah = *reinterpret_cast<const bf16x8*>(Ar + 16 * s2);
+      const bf16x8 al = *reinterpret_cast<const bf16x8*>(Ar + 32 + 16 * s2);
+      const bf16x8 bh = *reinterpret_cast<const bf16x8*>(Br + 16 * s2);
+      const bf16x8 bl = *reinterpret_cast<const bf16x8*>(Br + 32 + 16 * s2);
+      acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, bh, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, bl, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al, bh, acc, 0, 0, 0);
     }
     if (st + 1 < nst) {
       const int nb = buf ^ 1;
-      *reinterpret_cast<float4*>(&As[nb][sr * kS2 + 4 * sf]) = ra0;
-      *reinterpret_cast<float4*>(&As[nb][(sr + 32) * kS2 + 4 * sf]) = ra1;
-      *reinterpret_cast<float4*>(&Bs[nb][sr * kS2 + 4 * sf]) = rb0;
-      *reinterpret_cast<float4*>(&Bs[nb][(sr + 32) * kS2 + 4 * sf]) = rb1;
+      split_put(&As[nb][sr * kB3Row], sf, ra0);
+      split_put(&As[nb][(sr + 32) * kB3Row], sf, ra1);
+      split_put(&Bs[nb][sr * kB3Row], sf, rb0);
+      split_put(&Bs[nb][(sr + 32) * kB3Row], sf, rb1);
     }
     __syncthreads();
   }
-  // Output layout as in gemm_est_kernel.
-  const int j = col0 + wc * 32 + li;
-  if (j >= ncols) return;
-  const float cj = cn[j];
+  // acc layout as in gemm_est_kernel; the operand buffers are free after the
+  // last barrier.
+  float* Cs = reinterpret_cast<float*>(&As[0][0]);
 #pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    const int64_t i = row0 + wr * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
-    if (i < nrows) est[i * ld + j] = (xn[i] + cj) - 2.0f * acc[r];
+  for (int r = 0; r < 16; ++r) Cs[(wr * 32 + 8 * (r >> 2) + 4 * lh + (r & 3)) * kCStride + wc * 32 + li] = acc[r];
+  __syncthreads();
+  const int c4 = 4 * (tid & 15);
+  const int j = col0 + c4;
+  if (j >= ncols) return;
+  const bool full = j + 3 < ncols;
+  float4 cj;
+  if (full) {
+    cj = *reinterpret_cast<const float4*>(cn + j);
+  } else {
+    cj.x = cn[j];
+    cj.y = j + 1 < ncols ? cn[j + 1] : 0.0f;
+    cj.z = j + 2 < ncols ? cn[j + 2] : 0.0f;
+    cj.w = 0.0f;
   }
+  const bool vec = full && (ld & 3) == 0;
+#pragma unroll
+  for (int it = 0; it < 4; ++it) {
+    const int rr = 16 * it + (tid >> 4);
+    const int64_t i = row0 + rr;
+    if (i >= nrows) break;
+    const float4 a = *reinterpret_cast<const float4*>(&Cs[rr * kCStride + c4]);
+    const int64_t off = i * ld + j;
+    if (vec) {
+      if constexpr (OM == kOutHalf) {
+        const uint32_t lo = (uint32_t)half_at_or_below(cj.x - 2.0f * a.x) |
+                            ((uint32_t)half_at_or_below(cj.y - 2.0f * a.y) << 16);
+        const uint32_t hi = (uint32_t)half_at_or_below(cj.z - 2.0f * a.z) |
+                            ((uint32_t)half_at_or_below(cj.w - 2.0f * a.w) << 16);
+        *reinterpret_cast<uint2*>(static_cast<uint16_t*>(est) + off) = make_uint2(lo, hi);
+      } else if constexpr (OM == kOutShift) {
+        *reinterpret_cast<float4*>(static_cast<float*>(est) + off) =
+            make_float4(cj.x - 2.0f * a.x, cj.y - 2.0f * a.y, cj.z - 2.0f * a.z, cj.w - 2.0f * a.w);
+      } else {
+        const float xi = xn[i];
+        *reinterpret_cast<float4*>(static_cast<float*>(est) + off) =
+            make_float4((xi + cj.x) - 2.0f * a.x, (xi + cj.y) - 2.0f * a.y, (xi + cj.z) - 2.0f * a.z,
+                        (xi + cj.w) - 2.0f * a.w);
+      }
+    } else {
+      put_est<OM>(est, off, xn, i, cj.x, a.x);
+      if (j + 1 < ncols) put_est<OM>(est, off + 1, xn, i, cj.y, a.y);
+      if (j + 2 < ncols) put_est<OM>(est, off + 2, xn, i, cj.z, a.z);
+      if (j + 3 < ncols) put_est<OM>(est, off + 3, xn, i, cj.w, a.w);
+    }
+  }
+}
+
+// E for one row.  The absolute term covers products and operands below the
+// fp32 normal range, which the MFMA units may flush to zero: each such term
+// is under 2^-126 times an operand, so all of them together stay far below
+// 2^-100 (1 + ||x||^2 + ||c||^2) for any dim up to 2^20.
+__device__ __forceinline__ double est_margin(float kappa, float xn, float cn_max) {
+  const double nn = (double)xn + (double)cn_max;
+  return (double)kappa * nn + 0x1p-100 * (1.0 + nn);
 }
 
 constexpr int kCandCap = 512;
@@ -228,14 +345,23 @@ __device__ __forceinline__ void wave_sort_u32(uint32_t& k) {
   bitonic_pass_u32<64>(k, true);
 }
 
-// The p-th smallest of the wave's estimates val[j] (column j*64 + lane, only
-// columns < ncols count): LDS radix select, 8 bits a pass, over the
+// Which column a lane's value j holds: V = 1, column j*64 + lane; V = 4 or 8
+// (a row read as 16-byte vectors), runs of V consecutive columns a lane,
+// column (j / V) * 64 V + V lane + j % V.
+template <int V>
+__device__ __forceinline__ int col_of(int j, int lane) {
+  if constexpr (V == 1) return j * kWave + lane;
+  else return (j / V) * (kWave * V) + V * lane + (j % V);
+}
+
+// The p-th smallest of the wave's estimates val[j] (column col_of<V>(j, lane),
+// only columns < ncols count): LDS radix select, 8 bits a pass, over the
 // order-preserving integer map of the floats.  p == 1 is a plain minimum.
 // For p <= 64 the p-th smallest of the 64 per-lane minima bounds the answer
 // from above (those minima are p of the keys), and only keys at or below it
 // enter the histograms: the first passes otherwise pile most of the keys into
 // one or two bins, whose LDS atomics serialise.
-template <int VPL>
+template <int VPL, int V = 1>
 __device__ float wave_kth_estimate(const float (&val)[VPL], int ncols, int p, uint32_t* hist) {
   const int lane = threadIdx.x & 63;
   if (p == 1) {
@@ -246,7 +372,7 @@ __device__ float wave_kth_estimate(const float (&val)[VPL], int ncols, int p, ui
   }
   uint32_t key[VPL];
 #pragma unroll
-  for (int j = 0; j < VPL; ++j) key[j] = (j * kWave + lane < ncols) ? float_key(val[j]) : 0xFFFFFFFFu;
+  for (int j = 0; j < VPL; ++j) key[j] = (col_of<V>(j, lane) < ncols) ? float_key(val[j]) : 0xFFFFFFFFu;
   uint32_t cap = 0xFFFFFFFFu;
   if (p <= kWave) {
     uint32_t mn = key[0];
@@ -254,6 +380,26 @@ __device__ float wave_kth_estimate(const float (&val)[VPL], int ncols, int p, ui
     for (int j = 1; j < VPL; ++j) mn = key[j] < mn ? key[j] : mn;
     wave_sort_u32(mn);
     cap = (uint32_t)readlane_i((int)mn, p - 1);
+    // The keys at or below cap (at least p of them) usually number at most
+    // 64: gather them in column order and take the p-th of one sorted wave.
+    int n = 0;
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) {
+      const bool f = key[j] <= cap;
+      const uint64_t bm = __ballot(f);
+      const int pos = n + lanes_below(bm);
+      if (f && pos < kWave) hist[pos] = key[j];
+      n += __popcll(bm);
+    }
+    if (n <= kWave) {
+      wave_lds_sync();
+      uint32_t k = lane < n ? hist[lane] : 0xFFFFFFFFu;
+      wave_sort_u32(k);
+      const uint32_t t = (uint32_t)readlane_i((int)k, p - 1);
+      wave_lds_sync();
+      return key_float(t);
+    }
+    wave_lds_sync();
   }
   uint32_t prefix = 0, mask = 0;
   uint32_t rem = (uint32_t)p;
@@ -345,44 +491,44 @@ __device__ __forceinline__ void merge_top256(uint64_t (&l)[4], int nl, uint64_t 
   wave_merge_sorted64_k(l[3], key);
 }
 
-// One wave per row: p-th smallest estimate by LDS radix select, margin
-// superset, exact re-score, bitonic sort by (distance, index); p <= 256.
-template <int VPL>
-__global__ __launch_bounds__(256) void select_exact_kernel(
-    const float* __restrict__ est, int64_t ld, int64_t nrows, int ncols,
-    const float* __restrict__ x, const float* __restrict__ c, int dim,
-    const float* __restrict__ xn, const float* __restrict__ cn_max, float kappa, int p, int prune,
-    float prune_ratio, int32_t* __restrict__ out_ids, float* __restrict__ out_d) {
-  __shared__ uint32_t hist_s[4][256];
-  __shared__ int cand_s[4][kCandCap];
-  __shared__ __align__(16) float x_s[4][256];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int64_t row = (int64_t)blockIdx.x * 4 + wave;
-  if (row >= nrows) return;  // whole wave leaves; no workgroup barrier follows
-  uint32_t* hist = hist_s[wave];
-  int* cand = cand_s[wave];
-  float* xs = x_s[wave];
-  for (int d = lane; d < dim; d += kWave) xs[d] = x[row * dim + d];
-
-  float val[VPL];
-  const float* er = est + row * ld;
-#pragma unroll
-  for (int j = 0; j < VPL; ++j) {
-    const int col = j * kWave + lane;
-    val[j] = col < ncols ? er[col] : FLT_MAX;
+// The largest float <= t: for a float v, v <= t exactly when v <= this.
+__device__ __forceinline__ float float_at_or_below(double t) {
+  float f = (float)t;
+  if ((double)f > t) {
+    const uint32_t u = __float_as_uint(f);
+    f = __uint_as_float(f > 0.0f ? u - 1u : (f == 0.0f ? 0x80000001u : u + 1u));
   }
+  return f;
+}
 
-  // Threshold T = p-th smallest estimate.
-  const float T = wave_kth_estimate<VPL>(val, ncols, p, hist);
-  const double E = (double)kappa * ((double)xn[row] + (double)(*cn_max));
-  const double thr = (double)T + 2.0 * E;
+// The select for one row, given its estimates (val[j]: column
+// col_of<V>(j, lane), FLT_MAX past ncols; fp16 lower bounds when HALF) and
+// its query row xs in LDS: p-th smallest estimate, margin superset, exact
+// re-score, bitonic sort by (distance, index); p <= 256.  One wave; hist
+// (256 words) and cand (kCandCap ints) are the wave's own LDS.
+template <int VPL, int V, bool HALF>
+__device__ __forceinline__ void select_row(const float (&val)[VPL], int64_t row, int ncols, const float* xs,
+                                           uint32_t* hist, int* cand, const float* __restrict__ c, int dim,
+                                           float xnr, const float* __restrict__ cn_max,
+                                           float kappa, int p, int prune, float prune_ratio,
+                                           int32_t* __restrict__ out_ids, float* __restrict__ out_d) {
+  const int lane = threadIdx.x & 63;
+  // With fp16 lower bounds and T' their p-th smallest, the p smallest
+  // estimates lie below the next fp16 value above T' (each is below the next
+  // fp16 value above its own bound), so T = that value bounds the p-th
+  // smallest estimate from above, and every column whose estimate is
+  // <= (p-th smallest estimate) + 2E has val <= T + 2E.
+  const float Tv = wave_kth_estimate<VPL, V>(val, ncols, p, hist);
+  const float T = HALF ? half_next_up(Tv) : Tv;
+  const double E = est_margin(kappa, xnr, *cn_max);
+  const float thr = float_at_or_below((double)T + 2.0 * E);
 
-  // Ordered compaction of the candidate columns.
+  // Compaction of the candidate columns.
   int C = 0;
 #pragma unroll
   for (int j = 0; j < VPL; ++j) {
-    const int col = j * kWave + lane;
-    const bool f = col < ncols && (double)val[j] <= thr;
+    const int col = col_of<V>(j, lane);
+    const bool f = col < ncols && val[j] <= thr;
     const uint64_t bm = __ballot(f);
     const int pos = C + lanes_below(bm);
     if (f && pos < kCandCap) cand[pos] = col;
@@ -421,6 +567,68 @@ __global__ __launch_bounds__(256) void select_exact_kernel(
       out_d[row * p + r] = ld_;
     }
   }
+}
+
+// One wave per row over the estimate matrix est (row stride ld).  The
+// estimates may leave out the row's own norm (a shift of the whole row: the
+// p-th estimate and the candidate set move with it); the margin takes the
+// norm computed here, the same lane-strided chain and reduction as
+// row_norms_kernel.
+template <int VPL, typename E>
+__global__ __launch_bounds__(256) void select_exact_kernel(
+    const E* __restrict__ est, int64_t ld, int64_t nrows, int ncols,
+    const float* __restrict__ x, const float* __restrict__ c, int dim,
+    const float* __restrict__ cn_max, float kappa, int p, int prune,
+    float prune_ratio, int32_t* __restrict__ out_ids, float* __restrict__ out_d) {
+  __shared__ uint32_t hist_s[4][256];
+  __shared__ int cand_s[4][kCandCap];
+  __shared__ __align__(16) float x_s[4][256];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t row = (int64_t)blockIdx.x * 4 + wave;
+  if (row >= nrows) return;  // whole wave leaves; no workgroup barrier follows
+  float* xs = x_s[wave];
+  float xnr = 0.0f;
+  for (int d = lane; d < dim; d += kWave) {
+    const float v = x[row * dim + d];
+    xs[d] = v;
+    xnr = __builtin_fmaf(v, v, xnr);
+  }
+#pragma unroll
+  for (int m = 32; m > 0; m >>= 1) xnr += __shfl_xor(xnr, m, kWave);
+
+  // The row as 16-byte vectors (ld % 8 == 0): runs of V columns a lane.
+  constexpr bool HALF = sizeof(E) == 2;
+  constexpr int VEC = HALF ? 8 : 4;
+  constexpr int V = VPL >= VEC ? VEC : 1;
+  auto cvt = [](E e) -> float {
+    if constexpr (HALF) return half_bits_float(e);
+    else return e;
+  };
+  float val[VPL];
+  const E* er = est + row * ld;
+  if constexpr (V > 1) {
+#pragma unroll
+    for (int jj = 0; jj < VPL / V; ++jj) {
+      const int c0 = col_of<V>(jj * V, lane);
+      if (c0 + V <= ncols) {
+        const uint4 w = *reinterpret_cast<const uint4*>(er + c0);
+        const E* e = reinterpret_cast<const E*>(&w);
+#pragma unroll
+        for (int t = 0; t < V; ++t) val[jj * V + t] = cvt(e[t]);
+      } else {
+#pragma unroll
+        for (int t = 0; t < V; ++t) val[jj * V + t] = c0 + t < ncols ? cvt(er[c0 + t]) : FLT_MAX;
+      }
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) {
+      const int col = j * kWave + lane;
+      val[j] = col < ncols ? cvt(er[col]) : FLT_MAX;
+    }
+  }
+  select_row<VPL, V, HALF>(val, row, ncols, xs, hist_s[wave], cand_s[wave], c, dim, xnr, cn_max, kappa, p, prune,
+                           prune_ratio, out_ids, out_d);
 }
 
 // Exact kNN (brute_force_search_kernel, tune_parameters.cu:49-96) over one
@@ -474,7 +682,7 @@ __global__ __launch_bounds__(256) void knn_chunk_kernel(
     const int col = j * kWave + lane;
     val[j] = col < ncols ? er[col] : FLT_MAX;
   }
-  const double E = (double)kappa * ((double)xn[row] + (double)(*cn_max));
+  const double E = est_margin(kappa, xn[row], *cn_max);
   const int p = k < ncols ? k : ncols;
 
   // Ordered compaction of the columns with estimate <= thr; the count may exceed the cap.
@@ -548,12 +756,18 @@ fgpu_status launch_knn_t(const float* est, int64_t ld, int64_t nrows, int ncols,
 }
 
 template <int VPL>
-fgpu_status launch_select_t(const float* est, int64_t ld, int64_t nrows, int ncols, const float* x,
-                            const float* c, int dim, const float* xn, const float* cn_max, float kappa,
+fgpu_status launch_select_t(const void* est, int64_t ld, int64_t nrows, int ncols, const float* x,
+                            const float* c, int dim, const float* cn_max, float kappa,
                             int p, int prune, float prune_ratio, int32_t* ids, float* d, hipStream_t s) {
   const int64_t blocks = (nrows + 3) / 4;
-  hipLaunchKernelGGL(select_exact_kernel<VPL>, dim3((unsigned)blocks), dim3(256), 0, s, est, ld, nrows,
-                     ncols, x, c, dim, xn, cn_max, kappa, p, prune, prune_ratio, ids, d);
+  if (kEstHalf)
+    hipLaunchKernelGGL((select_exact_kernel<VPL, uint16_t>), dim3((unsigned)blocks), dim3(256), 0, s,
+                       static_cast<const uint16_t*>(est), ld, nrows, ncols, x, c, dim, cn_max, kappa, p, prune,
+                       prune_ratio, ids, d);
+  else
+    hipLaunchKernelGGL((select_exact_kernel<VPL, float>), dim3((unsigned)blocks), dim3(256), 0, s,
+                       static_cast<const float*>(est), ld, nrows, ncols, x, c, dim, cn_max, kappa, p, prune,
+                       prune_ratio, ids, d);
   FGPU_HIP(hipGetLastError());
   return FGPU_OK;
 }
@@ -573,36 +787,58 @@ fgpu_status launch_max_reduce(const float* v, int64_t n, float* out, hipStream_t
   return FGPU_OK;
 }
 
-fgpu_status launch_gemm_est(const float* x, int64_t nrows, const float* c, int ncols, int dim,
-                            const float* xn, const float* cn, float* est, int64_t ld, hipStream_t s) {
+template <int OM>
+fgpu_status launch_gemm_t(const float* x, int64_t nrows, const float* c, int ncols, int dim, const float* xn,
+                          const float* cn, void* est, int64_t ld, hipStream_t s) {
   FGPU_CHECK(dim % 4 == 0, FGPU_ERR_UNSUPPORTED, "gemm_est: dim must be a multiple of 4");
   if (nrows <= 0 || ncols <= 0) return FGPU_OK;
   dim3 grid((unsigned)((nrows + kTM - 1) / kTM), (unsigned)((ncols + kTN - 1) / kTN));
   FGPU_CHECK(grid.y <= 65535u, FGPU_ERR_UNSUPPORTED, "gemm_est: too many columns");
   if (dim % 32 == 0)
-    hipLaunchKernelGGL(gemm_est32_kernel, grid, dim3(256), 0, s, x, nrows, c, ncols, dim, xn, cn, est, ld);
+    hipLaunchKernelGGL(gemm_est_split_kernel<OM>, grid, dim3(256), 0, s, x, nrows, c, ncols, dim, xn, cn, est, ld);
   else
-    hipLaunchKernelGGL(gemm_est_kernel, grid, dim3(256), 0, s, x, nrows, c, ncols, dim, xn, cn, est, ld);
+    hipLaunchKernelGGL(gemm_est_kernel<OM>, grid, dim3(256), 0, s, x, nrows, c, ncols, dim, xn, cn, est, ld);
   FGPU_HIP(hipGetLastError());
   return FGPU_OK;
 }
 
+fgpu_status launch_gemm_est(const float* x, int64_t nrows, const float* c, int ncols, int dim,
+                            const float* xn, const float* cn, float* est, int64_t ld, hipStream_t s) {
+  return launch_gemm_t<kOutFull>(x, nrows, c, ncols, dim, xn, cn, est, ld, s);
+}
+
+fgpu_status launch_gemm_est_sel(const float* x, int64_t nrows, const float* c, int ncols, int dim, const float* cn,
+                                void* est, int64_t ld, hipStream_t s) {
+  FGPU_CHECK(ld % 8 == 0, FGPU_ERR_ARG, "gemm_est_sel: row stride must be a multiple of 8");
+  return kEstHalf ? launch_gemm_t<kOutHalf>(x, nrows, c, ncols, dim, nullptr, cn, est, ld, s)
+                  : launch_gemm_t<kOutShift>(x, nrows, c, ncols, dim, nullptr, cn, est, ld, s);
+}
+
+int64_t est_sel_ld(int ncols) { return ((int64_t)ncols + 7) / 8 * 8; }
+
+// The margin factor of the estimate launch_gemm_est computes for this dim.
 static float coarse_kappa(int dim) {
   const double u = std::ldexp(1.0, -24);
+  if (dim % 32 == 0) {  // gemm_est_split_kernel
+    const double n = 3.0 * dim + 8.0;
+    const double gamma = n * u / (1.0 - n * u);
+    return (float)(8.0 * gamma * 1.001 + 4.0 * std::ldexp(1.0, -14));
+  }
   const double n = 2.0 * dim + 8.0;
   const double gamma = n * u / (1.0 - n * u);
   return (float)(8.0 * gamma * 1.001);
 }
 
-fgpu_status launch_select_exact(const float* est, int64_t ld, int64_t nrows, int ncols, const float* x,
-                                const float* c, int dim, const float* xn, const float* cn_max, int p,
+fgpu_status launch_select_exact(const void* est, int64_t ld, int64_t nrows, int ncols, const float* x,
+                                const float* c, int dim, const float* cn_max, int p,
                                 int prune, float prune_ratio, int32_t* ids, float* d, hipStream_t s) {
+  FGPU_CHECK(ld % 8 == 0, FGPU_ERR_ARG, "select: row stride must be a multiple of 8");
   FGPU_CHECK(p >= 1 && p <= kSelectMax && p <= ncols, FGPU_ERR_UNSUPPORTED, "select: need 1 <= p <= min(256, ncols)");
   FGPU_CHECK(dim <= 256, FGPU_ERR_UNSUPPORTED, "select: dim must be <= 256");
   if (nrows <= 0) return FGPU_OK;
   const float kappa = coarse_kappa(dim);
 #define FGPU_SEL(V) \
-  if (ncols <= (V) * kWave) return launch_select_t<V>(est, ld, nrows, ncols, x, c, dim, xn, cn_max, kappa, p, prune, prune_ratio, ids, d, s)
+  if (ncols <= (V) * kWave) return launch_select_t<V>(est, ld, nrows, ncols, x, c, dim, cn_max, kappa, p, prune, prune_ratio, ids, d, s)
   FGPU_SEL(1);
   FGPU_SEL(2);
   FGPU_SEL(4);

@@ -15,14 +15,22 @@ fgpu_status launch_row_norms(const float* rows, int64_t n, int dim, float* norms
 // *out = max(norms[0..n)).
 fgpu_status launch_max_reduce(const float* v, int64_t n, float* out, hipStream_t s);
 // est[i][j] = xn[i] + cn[j] - 2 <x_i, c_j> for i in [0,nrows), j in [0,ncols);
-// est row stride is ld floats.  MFMA f32 32x32x2.
+// est row stride is ld floats.  dim % 32 == 0: bf16 MFMA on a hi/lo split of
+// both operands; otherwise MFMA f32 32x32x2.
 fgpu_status launch_gemm_est(const float* x, int64_t nrows, const float* c, int ncols, int dim,
                             const float* xn, const float* cn, float* est, int64_t ld, hipStream_t s);
+// The same contraction for launch_select_exact: cn[j] - 2 <x_i, c_j>, each
+// row shifted by its norm, in the select's element form (fp32, or the fp16
+// lower bound); ld % 8 == 0, at least est_sel_ld(ncols).  
+fgpu_status launch_gemm_est_sel(const float* x, int64_t nrows, const float* c, int ncols, int dim, const float* cn,
+                                void* est, int64_t ld, hipStream_t s);
+int64_t est_sel_ld(int ncols);
 // Per row: the p nearest columns by exact device-form L2, chosen from the
-// estimate with a rigorous error margin.  ids are int32 bit patterns; with
-// prune != 0 a column farther than best*prune_ratio gets 0xFFFFFFFF.
-fgpu_status launch_select_exact(const float* est, int64_t ld, int64_t nrows, int ncols,
-                                const float* x, const float* c, int dim, const float* xn,
+// estimates of launch_gemm_est_sel with a rigorous error margin.  ids
+// are int32 bit patterns; with prune != 0 a column farther than
+// best*prune_ratio gets 0xFFFFFFFF.
+fgpu_status launch_select_exact(const void* est, int64_t ld, int64_t nrows, int ncols,
+                                const float* x, const float* c, int dim,
                                 const float* cn_max, int p, int prune, float prune_ratio,
                                 int32_t* out_ids, float* out_d, hipStream_t s);
 // Exact kNN over one chunk of <= 4096 base rows c (ids id_base + col), merged

@@ -6,7 +6,8 @@
  * fgpu_last_error() returns a thread-local message for the last failure.
  * Calls that take a stream only enqueue work on it: no hidden host
  * synchronisation, no static scratch.  Scratch comes from a caller-owned
- * device workspace whose size the matching *_workspace_bytes() call returns.
+ * device workspace whose size the matching *_workspace_bytes() call returns,
+ * 16-byte aligned (hipMalloc and torch allocations are 256-byte aligned).
  *
  * Each entry point names the reference interface it replaces
  * (Hello-day/FusionGPU, file:line).

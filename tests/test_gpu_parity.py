@@ -70,6 +70,40 @@ def test_l2_topk_bit_exact(dim, nc, p):
         assert np.array_equal(ids[:, 0], oracle.kmeans_assign(x, c))
 
 
+@pytest.mark.parametrize("case", ["large", "tiny", "sphere", "offset"])
+@pytest.mark.parametrize("dim,p", [(128, 32), (128, 1), (36, 8)])
+def test_l2_topk_estimate_extremes(case, dim, p):
+    """The select reads fp16 lower bounds of the shifted estimates: values past
+    the fp16 range (saturated bounds, every column re-scored), values in its
+    subnormal range, many near-equal distances (a query at the centre of a
+    sphere of centroids) and a large common offset of both sets (estimates
+    far from zero against small differences) all stay exact."""
+    _say(f"l2_topk extremes case={case} dim={dim} p={p}")
+    rng = np.random.default_rng(["large", "tiny", "sphere", "offset"].index(case) * 1000 + dim * 10 + p)
+    n, nc = 129, 1024
+    x = rng.standard_normal((n, dim)).astype(np.float32)
+    c = rng.standard_normal((nc, dim)).astype(np.float32)
+    if case == "large":
+        x *= np.float32(300.0)
+        c *= np.float32(300.0)
+    elif case == "tiny":
+        x *= np.float32(2e-3)
+        c *= np.float32(2e-3)
+    elif case == "sphere":
+        u = c / np.linalg.norm(c, axis=1, keepdims=True)
+        c = (x[0] + np.float32(0.5) * u).astype(np.float32)
+        x[1:] = x[0] + np.float32(1e-4) * rng.standard_normal((n - 1, dim)).astype(np.float32)
+    else:
+        off = rng.standard_normal(dim).astype(np.float32) * np.float32(30.0)
+        x += off
+        c += off
+    ids, d = fg.l2_topk(torch.from_numpy(x).cuda(), torch.from_numpy(c).cuda(), p)
+    ids, d = _host(ids), _host(d)
+    oid, od = oracle.coarse(x, c, p, prune_ratio=np.inf)
+    assert np.array_equal(ids.view(np.uint32), oid)
+    assert np.array_equal(_bits(d), _bits(od))
+
+
 # --------------------------------------------------------------------------- coarse quantizer (A2, A3)
 @pytest.mark.parametrize("prune_ratio", [100.0, 1.3])
 def test_coarse_search_bit_exact(prune_ratio):
