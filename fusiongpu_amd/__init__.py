@@ -54,6 +54,7 @@ _SIGS = {
     "fgpu_index_check": (_i32, [_vp, _vp]),
     "fgpu_debug_set_spin_limit": (None, [_i32]),
     "fgpu_debug_set_list_skip": (None, [_i32]),
+    "fgpu_debug_pq_sample": (_i32, [_i64, _i32, _vp]),
     "fgpu_stream_read_grid": (_i32, []),
     "fgpu_stream_read": (_i32, [_vp, _sz, _vp, _vp]),
     "fgpu_row_gather": (_i32, [_vp, _i64, _i32, _vp, _i64, _vp, _vp]),
@@ -319,6 +320,15 @@ def debug_set_spin_limit(polls: int):
 def debug_set_list_skip(enabled: bool):
     """Measurement hook (fgpu_debug_set_list_skip): False makes the plain scan read every probed list."""
     lib.fgpu_debug_set_list_skip(int(bool(enabled)))
+
+
+def debug_pq_sample(n: int, sample_size: int) -> np.ndarray:
+    """Test hook (fgpu_debug_pq_sample, host only): fgpu_pq_train's sample rows."""
+    out = np.empty(max(0, min(int(sample_size), int(n))), dtype=np.int32)
+    got = lib.fgpu_debug_pq_sample(int(n), int(sample_size), out.ctypes.data)
+    if got < 0:
+        raise ValueError("debug_pq_sample: bad argument")
+    return out[:got]
 
 
 def stream_read(data, stream=None):

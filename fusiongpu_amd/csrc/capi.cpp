@@ -108,6 +108,40 @@ AdcArgs adc_args(const fgpu_index* ix, const float* dq, int nq, const uint32_t* 
   return a;
 }
 
+// The first k entries of what std::shuffle(iota(n), rng) leaves, drawing
+// exactly as std::shuffle does.  When rng's range is below n^2, libstdc++'s
+// std::shuffle swaps position i with position d(rng, [0, i]) for i = 1, 2, ...,
+// n - 1, one draw of a stateless uniform_int_distribution<size_t-like> each
+// (bits/stl_algo.h).  Position i still holds i when its turn comes, so the
+// prefix needs only the draws: a prefix slot j < k drawn at step i >= k takes
+// the value i.  Otherwise (small n: the paired-draw path) std::shuffle itself.
+// The oracle's full shuffle is the check (tests/test_capi.py).
+std::vector<int32_t> shuffled_prefix(int64_t n, int64_t k, std::mt19937& rng) {
+  using UD = std::make_unsigned<std::vector<int32_t>::difference_type>::type;
+  using UC = std::common_type<std::mt19937::result_type, UD>::type;
+  k = std::min(k, n);
+  const UC urng_range = rng.max() - rng.min();
+  if (n <= 1 || urng_range / (UC)n >= (UC)n) {
+    std::vector<int32_t> idx(n);
+    std::iota(idx.begin(), idx.end(), 0);
+    std::shuffle(idx.begin(), idx.end(), rng);
+    idx.resize(k);
+    return idx;
+  }
+  std::vector<int32_t> a(k);
+  std::iota(a.begin(), a.end(), 0);
+  std::uniform_int_distribution<UD> d;
+  using P = std::uniform_int_distribution<UD>::param_type;
+  for (int64_t i = 1; i < n; ++i) {
+    const UD j = d(rng, P(0, (UD)i));
+    if (i < k)
+      std::swap(a[i], a[j]);
+    else if ((int64_t)j < k)
+      a[j] = (int32_t)i;
+  }
+  return a;
+}
+
 int64_t topk_batch_rows(int64_t n, int nc) {
   const size_t budget = 256ull << 20;  // estimate tile budget per batch
   int64_t b = est_rows_per_batch(budget, nc);
@@ -339,6 +373,14 @@ fgpu_status fgpu_index_check(const fgpu_index* ix, void* stream) {
 void fgpu_debug_set_spin_limit(int polls) { g_spin_override.store(polls > 0 ? polls : 0); }
 
 void fgpu_debug_set_list_skip(int enabled) { g_list_skip.store(enabled ? 1 : 0); }
+
+int fgpu_debug_pq_sample(int64_t n, int sample_size, int32_t* h_rows) {
+  if (n < 1 || sample_size < 0 || !h_rows) return -1;
+  std::mt19937 rng(12345);
+  const std::vector<int32_t> r = shuffled_prefix(n, sample_size, rng);
+  std::memcpy(h_rows, r.data(), sizeof(int32_t) * r.size());
+  return (int)r.size();
+}
 
 int fgpu_stream_read_grid(void) {
   int dev = 0, cus = 256;
@@ -747,23 +789,28 @@ fgpu_status fgpu_pq_train(const float* dx, int64_t n, int dim, int pq_m, const i
   // sample rows (pq_utils.h:91-97)
   const int actual = (int)std::min<int64_t>(sample_size, n);
   FGPU_CHECK(actual >= kPQK, FGPU_ERR_ARG, "pq_train: need at least 256 sample rows");
-  std::vector<int32_t> idx(n);
-  std::iota(idx.begin(), idx.end(), 0);
+  std::vector<int32_t> idx;
   {
     std::mt19937 rng(12345);
-    std::shuffle(idx.begin(), idx.end(), rng);
+    idx = shuffled_prefix(n, actual, rng);
   }
-  idx.resize(actual);
   // per-subspace initial rows (pq_utils.h:20-31, seed 1234+m)
+  // Each subspace's shuffle has its own generator: a few host threads.
   std::vector<int32_t> init((size_t)pq_m * kPQK);
   {
-    std::vector<int> ind(actual);
-    for (int sub = 0; sub < pq_m; ++sub) {
-      std::iota(ind.begin(), ind.end(), 0);
-      std::mt19937 rng(1234 + sub);
-      std::shuffle(ind.begin(), ind.end(), rng);
-      std::copy(ind.begin(), ind.begin() + kPQK, init.begin() + (size_t)sub * kPQK);
-    }
+    const int nt = std::max(1, std::min(pq_m, 8));
+    std::vector<std::thread> th;
+    for (int t0 = 0; t0 < nt; ++t0)
+      th.emplace_back([&, t0] {
+        std::vector<int> ind(actual);
+        for (int sub = t0; sub < pq_m; sub += nt) {
+          std::iota(ind.begin(), ind.end(), 0);
+          std::mt19937 rng(1234 + sub);
+          std::shuffle(ind.begin(), ind.end(), rng);
+          std::copy(ind.begin(), ind.begin() + kPQK, init.begin() + (size_t)sub * kPQK);
+        }
+      });
+    for (auto& t : th) t.join();
   }
   DevBuf<int32_t> drows, dinit, dassign;
   DevBuf<float> res;

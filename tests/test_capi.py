@@ -36,6 +36,18 @@ def test_abi_version():
     assert fg.lib.fgpu_abi_version() == 1
 
 
+@pytest.mark.parametrize("n,k", [(1, 1), (300, 256), (65536, 50000), (65537, 50000), (70001, 256),
+                                 (1_000_000, 50000), (3_000_001, 50000)])
+def test_pq_sample_prefix_equals_full_shuffle(n, k):
+    """fgpu_pq_train draws its sample rows without the n-entry shuffle array
+    (only the first k positions are kept); they must equal the oracle's full
+    std::shuffle of 0 .. n-1 with mt19937(12345), on both of libstdc++'s
+    paths (n <= 65536 takes the paired-draw one)."""
+    got = fg.debug_pq_sample(n, k)
+    want = oracle.pq_sample(n, k)
+    assert np.array_equal(got, want)
+
+
 def test_generator_matches_oracle_definition():
     for (n, dim, nc, sig, sig2, seed, s) in [(3000, 128, 64, 0.1, None, 1, 0), (500, 96, 16, 0.05, 0.15, 9, 1)]:
         a = fg.gen_gmm(n, dim, nc, seed, set=s, sig_lo=sig, sig_hi=sig2, nthreads=4)
