@@ -679,7 +679,9 @@ def run_c4(args, torch, fg, dev):
         "config": {"workload": "BASELINE config 4: 10M x 128, k-means++ + 20 Lloyd iterations of 4096 centroids on "
                                "a 1M sample, PQ M=32 x 256 (15 iterations), encode 10M, elbow 1024/2048/4096",
                    "n": n, "dim": dim, "nlist": nlist, "pq_m": m, "train_rows": train},
-        "roofline": {"bound": "mfma", "kernel": "gemm_est_kernel + select_exact_kernel (assignment of all rows)",
+        "roofline": {"bound": "mfma", "kernel": "gemm_est_split_kernel + select_exact_kernel (assignment of all "
+                               "rows; FLOP counted as the fp32-equivalent 2 n k D, the split issues three bf16 "
+                               "products each)",
                      "achieved": round(gemm_flop / t_as / 1e12, 2), "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(gemm_flop / t_as / 1e12 / FP32_MFMA_PEAK_TFLOPS, 4), "traffic": None},
         "phases_s": {"kmeans": round(t_km, 3), "assign": round(t_as, 3), "pq_train": round(t_pq, 3),
