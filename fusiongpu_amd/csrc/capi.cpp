@@ -282,7 +282,7 @@ size_t fgpu_coarse_workspace_bytes(int nq, int nlist) {
   // The estimate block holds whole 64-row GEMM tiles: with room for every
   // query row rounded up to 64, the coarse step is one GEMM + one select.
   const size_t rows = ((size_t)std::max(nq, 64) + 63) / 64 * 64;
-  return carve_bytes<float>((size_t)nq) + carve_bytes<float>(rows * (size_t)est_sel_ld(nlist)) + 256;
+  return carve_bytes<float>(rows * (size_t)est_sel_ld(nlist)) + 256;
 }
 
 fgpu_status fgpu_coarse_search(const fgpu_index* ix, const float* dq, int nq, int nprobe, float prune_ratio,
@@ -294,11 +294,9 @@ fgpu_status fgpu_coarse_search(const fgpu_index* ix, const float* dq, int nq, in
   if (nq == 0) return FGPU_OK;
   hipStream_t s = as_stream(stream);
   Carve cv(ws, ws_bytes);
-  float* xn = cv.take<float>(nq);
-  const size_t rest = ws_bytes > cv.used ? ws_bytes - cv.used : 0;
   const int64_t ld = est_sel_ld(ix->nlist);
-  int64_t rows = std::min<int64_t>(est_rows_per_batch(rest > 256 ? rest - 256 : 0, (int)ld), ((nq + 63) / 64) * 64);
-  FGPU_CHECK(xn && rows >= 64, FGPU_ERR_WORKSPACE, "coarse_search: workspace too small");
+  int64_t rows = std::min<int64_t>(est_rows_per_batch(ws_bytes > 256 ? ws_bytes - 256 : 0, (int)ld), ((nq + 63) / 64) * 64);
+  FGPU_CHECK(rows >= 64, FGPU_ERR_WORKSPACE, "coarse_search: workspace too small");
   void* est = cv.take<float>((size_t)rows * ld);
   FGPU_CHECK(est, FGPU_ERR_WORKSPACE, "coarse_search: workspace too small");
   // The estimates leave out each query's norm; the select computes it for
@@ -526,8 +524,7 @@ fgpu_status fgpu_search_rerank(const fgpu_index* ix, const float* dq, int nq, in
 
 // ---------------------------------------------------------------------------
 size_t fgpu_l2_topk_workspace_bytes(int64_t n, int nc) {
-  return carve_bytes<float>(n) + carve_bytes<float>(nc) + 256 +
-         carve_bytes<float>((size_t)topk_batch_rows(n, nc) * (size_t)est_sel_ld(nc));
+  return carve_bytes<float>(nc) + 256 + carve_bytes<float>((size_t)topk_batch_rows(n, nc) * (size_t)est_sel_ld(nc));
 }
 
 fgpu_status fgpu_l2_topk(const float* dx, int64_t n, const float* dc, int nc, int dim, int p, int32_t* d_ids,
@@ -538,7 +535,6 @@ fgpu_status fgpu_l2_topk(const float* dx, int64_t n, const float* dc, int nc, in
   if (n == 0) return FGPU_OK;
   hipStream_t s = as_stream(stream);
   Carve cv(ws, ws_bytes);
-  (void)cv.take<float>(n);  // the query-norm slot of the workspace layout, no longer written
   float* cn = cv.take<float>(nc);
   float* cmax = cv.take<float>(64);
   FGPU_CHECK(cv.ok(), FGPU_ERR_WORKSPACE, "l2_topk: workspace too small");
