@@ -94,7 +94,12 @@ __device__ __forceinline__ void scan_round_full(const float* smem, int v0, int n
   const float* lut = smem + BUF * C::LUT;
   const int v1 = v0 + kWave;
   float d0, d1;
-  if (adc_sum2_full<M>(lut, w0, w1, __uint_as_float((uint32_t)(thr >> 32)), d0, d1)) {
+  bool go = true;
+  if (v0 - (int)(threadIdx.x & 63) + 2 * kWave <= n)  // a full chunk (uniform)
+    go = adc_sum2_full<M>(lut, w0, w1, __uint_as_float((uint32_t)(thr >> 32)), d0, d1);
+  else  // the list's partial last chunk: empty lanes send no gathers (C2: 0.444 -> 0.440 ms)
+    adc_sum2_part<M>(lut, w0, w1, v0 < n, v1 < n, d0, d1);
+  if (go) {
     if (offer2_k(v0 < n ? key_of(d0, i0) : kPadKey, v1 < n ? key_of(d1, i1) : kPadKey, thr, k, lk)) {
       own = readlane64(lk, k - 1);
       if ((threadIdx.x & 63) == 0) atomicMin(s_thr, (unsigned long long)own);

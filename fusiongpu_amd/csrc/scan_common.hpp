@@ -143,6 +143,41 @@ __device__ __forceinline__ bool adc_sum2_full(const float* __restrict__ lut, con
   return true;
 }
 
+// The same sums for a list's partial last chunk: each chain's gathers run
+// only in the lanes that hold a vector (ok0 / ok1), so the empty lanes send
+// no LDS requests; their results are FLT_MAX and the caller masks them.
+// Same order of terms as adc_sum2_full.
+template <int M>
+__device__ __forceinline__ void adc_sum2_part(const float* __restrict__ lut, const uint4 (&w0)[M / 16],
+                                              const uint4 (&w1)[M / 16], bool ok0, bool ok1, float& d0,
+                                              float& d1) {
+  float a = FLT_MAX, b = FLT_MAX;
+  if (ok0) {
+#pragma unroll
+    for (int i = 0; i < M / 16; ++i) {
+      const uint32_t x[4] = {w0[i].x, w0[i].y, w0[i].z, w0[i].w};
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const float t = lut[(i * 16 + j) * kPQK + ((x[j >> 2] >> (8 * (j & 3))) & 0xFFu)];
+        a = (i == 0 && j == 0) ? t : a + t;
+      }
+    }
+  }
+  if (ok1) {
+#pragma unroll
+    for (int i = 0; i < M / 16; ++i) {
+      const uint32_t y[4] = {w1[i].x, w1[i].y, w1[i].z, w1[i].w};
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const float t = lut[(i * 16 + j) * kPQK + ((y[j >> 2] >> (8 * (j & 3))) & 0xFFu)];
+        b = (i == 0 && j == 0) ? t : b + t;
+      }
+    }
+  }
+  d0 = a;
+  d1 = b;
+}
+
 // "No threshold yet": the padding key (FLT_MAX, kPadId); every real
 // candidate key (key_of: distances are sums of squares, never negative) is
 // below it.
