@@ -808,6 +808,15 @@ bool adc_supported(int dim, int m) {
 fgpu_status launch_adc_plain(int dim, int m, const AdcArgs& a, hipStream_t s) {
   FGPU_CHECK(a.k >= 1 && a.k <= 64, FGPU_ERR_UNSUPPORTED, "adc: k must be in [1, 64]");
   if (a.nq <= 0) return FGPU_OK;
+  // The flow kernel's per-query tables hold 64 lists; more probes go to the
+  // barrier-per-list kernel, which walks any number of them (every probed
+  // list scanned, no list bound).
+  if (a.nprobe > 64) {
+    if (dim == 128 && m == 32) return launch_plain<128, 32>(a, s);
+    if (dim == 128 && m == 16) return launch_plain<128, 16>(a, s);
+    if (dim == 96 && m == 32) return launch_plain<96, 32>(a, s);
+    if (dim == 96 && m == 16) return launch_plain<96, 16>(a, s);
+  }
   if (dim == 128 && m == 32) return launch_flow<128, 32>(a, s);
   if (dim == 128 && m == 16) return launch_flow<128, 16>(a, s);
   if (dim == 128 && m == 64) return launch_plain<128, 64>(a, s);

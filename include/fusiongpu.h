@@ -153,7 +153,8 @@ fgpu_status fgpu_probe_counts(const fgpu_index* idx, const uint32_t* d_probe_ids
 /* The k best (ADC distance, vector id) over every vector of every surviving
  * probed list; padding id -1 / distance FLT_MAX.  Equals run_gpu_batch_logic
  * (gpu_global.cu:679-874) with p1_lists = nprobe, limit_k = k, rerank_m = k.
- * k <= 64, nprobe <= 64.  d_probe_dists (may be NULL) takes the place of the reference's
+ * k <= 64; nprobe above 64 runs a kernel that scans every probed list (no
+ * list bound; same results).  d_probe_dists (may be NULL) takes the place of the reference's
  * d_cagra_dists: fgpu_coarse_search's distances for these probes, which the
  * scan then uses for its exact list bounds instead of recomputing them from
  * the centroids.  Non-NULL, they must be exactly the distances

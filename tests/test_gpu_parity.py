@@ -143,6 +143,29 @@ def test_coarse_search_many_probes(p, prune_ratio):
 
 
 # --------------------------------------------------------------------------- LUT + ADC + top-k (A4-A6, A10)
+@pytest.mark.parametrize("dim,m,p", [(128, 32, 65), (128, 16, 100), (96, 32, 256), (96, 16, 77)])
+def test_search_more_than_64_probes(dim, m, p):
+    """nprobe above the flow kernel's 64-list tables: fgpu_search (coarse +
+    scan) and fgpu_adc_search run the barrier-per-list kernel, which scans
+    every probed list, pruned probes included as skips."""
+    _say(f"search dim={dim} m={m} nprobe={p}")
+    rng = np.random.default_rng(dim + m + p)
+    offs, ids, lc, cent, cb = _random_index(rng, 9000, dim, m, 300)
+    q = rng.standard_normal((120, dim)).astype(np.float32) * 0.7
+    idx = fg.Index.from_arrays(dim, m, offs, ids, lc, cent, cb)
+    dq = torch.from_numpy(q).cuda()
+    gid, gd = idx.search(dq, p, 10, prune_ratio=1.5)
+    probes, _ = oracle.coarse(q, cent, p, 1.5)
+    oid, od = oracle.search_plain(q, cent, cb, offs, ids, lc, probes, 10)
+    assert np.array_equal(_host(gid), oid)
+    assert np.array_equal(_bits(_host(gd)), _bits(od))
+    gid, gd = idx.adc_search(dq, torch.from_numpy(probes.view(np.int32)).cuda(), 10)
+    assert np.array_equal(_host(gid), oid)
+    assert np.array_equal(_bits(_host(gd)), _bits(od))
+    idx.check()
+    idx.close()
+
+
 @pytest.mark.parametrize("dim,m,k", [(128, 32, 10), (128, 16, 10), (96, 48, 20), (96, 32, 64), (128, 64, 1),
                                      (96, 16, 7)])
 def test_adc_search_bit_exact(dim, m, k):
