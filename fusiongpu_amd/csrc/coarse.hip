@@ -632,6 +632,107 @@ __global__ __launch_bounds__(256) void select_exact_kernel(
                            prune_ratio, out_ids, out_d);
 }
 
+// p == 1 over many columns (the k-means assignment at k > 1024): the row is
+// read twice in pieces of 64 16-byte vectors (its minimum, then the
+// compaction) instead of being held whole in registers, so a wave stays
+// small and a CU holds many of them (the whole-row form needs 218 VGPRs at
+// 4096 columns).  Same margin, candidates and exact re-score as select_row;
+// the answer is the smallest (distance, id) key.
+__device__ __forceinline__ uint64_t wave_min64(uint64_t k) {
+#pragma unroll
+  for (int m = 32; m > 0; m >>= 1) {
+    const uint64_t o = ((uint64_t)(uint32_t)__shfl_xor((int)(uint32_t)(k >> 32), m, kWave) << 32) |
+                       (uint32_t)__shfl_xor((int)(uint32_t)k, m, kWave);
+    k = o < k ? o : k;
+  }
+  return k;
+}
+
+template <typename E>
+__global__ __launch_bounds__(256) void select_min_kernel(
+    const E* __restrict__ est, int64_t ld, int64_t nrows, int ncols,
+    const float* __restrict__ x, const float* __restrict__ c, int dim,
+    const float* __restrict__ cn_max, float kappa, int prune, float prune_ratio,
+    int32_t* __restrict__ out_ids, float* __restrict__ out_d) {
+  __shared__ int cand_s[4][kCandCap];
+  __shared__ __align__(16) float x_s[4][256];
+  constexpr bool HALF = sizeof(E) == 2;
+  constexpr int V = HALF ? 8 : 4;      // elements a 16-byte vector
+  constexpr int PIECE = V * kWave;     // columns a piece
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t row = (int64_t)blockIdx.x * 4 + wave;
+  if (row >= nrows) return;  // whole wave leaves; no workgroup barrier follows
+  float* xs = x_s[wave];
+  int* cand = cand_s[wave];
+  float xnr = 0.0f;
+  for (int d = lane; d < dim; d += kWave) {
+    const float v = x[row * dim + d];
+    xs[d] = v;
+    xnr = __builtin_fmaf(v, v, xnr);
+  }
+#pragma unroll
+  for (int m = 32; m > 0; m >>= 1) xnr += __shfl_xor(xnr, m, kWave);
+  auto cvt = [](E e) -> float {
+    if constexpr (HALF) return half_bits_float(e);
+    else return e;
+  };
+  const E* er = est + row * ld;
+  auto load = [&](int c0, float (&v)[V]) {  // columns c0 .. c0 + V - 1 (ld % 8 == 0)
+    if (c0 + V <= ncols) {
+      const uint4 w = *reinterpret_cast<const uint4*>(er + c0);
+      const E* e = reinterpret_cast<const E*>(&w);
+#pragma unroll
+      for (int t = 0; t < V; ++t) v[t] = cvt(e[t]);
+    } else {
+#pragma unroll
+      for (int t = 0; t < V; ++t) v[t] = c0 + t < ncols ? cvt(er[c0 + t]) : FLT_MAX;
+    }
+  };
+  float mn = FLT_MAX;
+  for (int base = 0; base < ncols; base += PIECE) {
+    float v[V];
+    load(base + V * lane, v);
+#pragma unroll
+    for (int t = 0; t < V; ++t) mn = fminf(mn, v[t]);
+  }
+  const float Tv = wave_min_f(mn);
+  const float T = HALF ? half_next_up(Tv) : Tv;
+  const float thr = float_at_or_below((double)T + 2.0 * est_margin(kappa, xnr, *cn_max));
+  int C = 0;
+  for (int base = 0; base < ncols; base += PIECE) {
+    float v[V];
+    load(base + V * lane, v);
+#pragma unroll
+    for (int t = 0; t < V; ++t) {
+      const int col = base + V * lane + t;
+      const bool f = col < ncols && v[t] <= thr;
+      const uint64_t bm = __ballot(f);
+      const int pos = C + lanes_below(bm);
+      if (f && pos < kCandCap) cand[pos] = col;
+      C += __popcll(bm);
+    }
+  }
+  wave_lds_sync();
+  const bool all_cols = C > kCandCap;  // pathological ties: re-score everything
+  const int ncand = all_cols ? ncols : C;
+  uint64_t best = kPadKey;
+  for (int b = 0; b < ncand; b += kWave) {
+    if (b + lane < ncand) {
+      const int id = all_cols ? b + lane : cand[b + lane];
+      const uint64_t key = key_of(exact_l2(xs, c + (int64_t)id * dim, dim), id);
+      best = key < best ? key : best;
+    }
+  }
+  best = wave_min64(best);
+  if (lane == 0) {
+    const float bd = key_dist(best);
+    int32_t oid = key_id(best);
+    if (prune && bd > bd * prune_ratio) oid = (int32_t)kPruned;
+    out_ids[row] = oid;
+    out_d[row] = bd;
+  }
+}
+
 // Exact kNN (brute_force_search_kernel, tune_parameters.cu:49-96) over one
 // chunk of base rows, merged into each query's running top-k (k <= 128):
 // the running list sits in two sorted 64-lists per wave, A (ranks 1-64) and
@@ -840,6 +941,17 @@ fgpu_status launch_select_exact(const void* est, int64_t ld, int64_t nrows, int 
   FGPU_CHECK(dim <= 256, FGPU_ERR_UNSUPPORTED, "select: dim must be <= 256");
   if (nrows <= 0) return FGPU_OK;
   const float kappa = coarse_kappa(dim);
+  if (p == 1 && ncols > 16 * kWave) {
+    const dim3 grid((unsigned)((nrows + 3) / 4));
+    if constexpr (kEstHalf)
+      hipLaunchKernelGGL(select_min_kernel<uint16_t>, grid, dim3(256), 0, s, static_cast<const uint16_t*>(est), ld,
+                         nrows, ncols, x, c, dim, cn_max, kappa, prune, prune_ratio, ids, d);
+    else
+      hipLaunchKernelGGL(select_min_kernel<float>, grid, dim3(256), 0, s, static_cast<const float*>(est), ld, nrows,
+                         ncols, x, c, dim, cn_max, kappa, prune, prune_ratio, ids, d);
+    FGPU_HIP(hipGetLastError());
+    return FGPU_OK;
+  }
 #define FGPU_SEL(V) \
   if (ncols <= (V) * kWave) return launch_select_t<V>(est, ld, nrows, ncols, x, c, dim, cn_max, kappa, p, prune, prune_ratio, ids, d, s)
   FGPU_SEL(1);

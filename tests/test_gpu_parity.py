@@ -52,7 +52,7 @@ def _random_index(rng, n, dim, m, nlist, empty=(), big=None):
 
 # --------------------------------------------------------------------------- exact nearest centroids
 @pytest.mark.parametrize("dim,nc,p", [(128, 1024, 32), (96, 300, 1), (128, 4096, 64), (64, 50, 10), (128, 77, 1),
-                                      (36, 200, 8)])
+                                      (36, 200, 8), (128, 4096, 1), (96, 2500, 1), (36, 1111, 1)])
 def test_l2_topk_bit_exact(dim, nc, p):
     _say(f"l2_topk dim={dim} nc={nc} p={p}")
     rng = np.random.default_rng(dim + nc + p)
@@ -71,16 +71,16 @@ def test_l2_topk_bit_exact(dim, nc, p):
 
 
 @pytest.mark.parametrize("case", ["large", "tiny", "sphere", "offset"])
-@pytest.mark.parametrize("dim,p", [(128, 32), (128, 1), (36, 8)])
-def test_l2_topk_estimate_extremes(case, dim, p):
+@pytest.mark.parametrize("dim,p,nc", [(128, 32, 1024), (128, 1, 1024), (36, 8, 1024), (128, 1, 3000)])
+def test_l2_topk_estimate_extremes(case, dim, p, nc):
     """The select reads fp16 lower bounds of the shifted estimates: values past
     the fp16 range (saturated bounds, every column re-scored), values in its
     subnormal range, many near-equal distances (a query at the centre of a
     sphere of centroids) and a large common offset of both sets (estimates
     far from zero against small differences) all stay exact."""
-    _say(f"l2_topk extremes case={case} dim={dim} p={p}")
-    rng = np.random.default_rng(["large", "tiny", "sphere", "offset"].index(case) * 1000 + dim * 10 + p)
-    n, nc = 129, 1024
+    _say(f"l2_topk extremes case={case} dim={dim} p={p} nc={nc}")
+    rng = np.random.default_rng(["large", "tiny", "sphere", "offset"].index(case) * 1000 + dim * 10 + p + nc)
+    n = 129
     x = rng.standard_normal((n, dim)).astype(np.float32)
     c = rng.standard_normal((nc, dim)).astype(np.float32)
     if case == "large":
