@@ -643,10 +643,64 @@ __global__ __launch_bounds__(kSpecWaves * kWave, 4) void adc_flow_kernel(AdcArgs
     __builtin_amdgcn_s_setprio(2);
     // This wave's first chunk at or after chunk cc.
     auto first_own = [&](int cc) { return cc + (((swave - cc) % kScanWaves) + kScanWaves) % kScanWaves; };
-    uint4 w0[C::NV4], w1[C::NV4];
-    int i0 = kPadId, i1 = kPadId;
     unsigned nload = 0;  // vectors whose codes this wave loaded
     long long t_end = 0;
+    // This wave's chunks of built list number dec (buffer dec % 3, vectors
+    // start .. start + n - 1, chunks c0 .. c_end - 1 of slot s's query):
+    // wait for its LUT, scan them into lk / own, and count them done.
+    auto scan_chunks = [&](int s, int dec, int start, int n, int c0, int c_end, uint64_t& lk, uint64_t& own) {
+      int c = first_own(c0);
+      uint4 w0[C::NV4], w1[C::NV4];
+      int i0 = kPadId, i1 = kPadId;
+      load_pair<M>(a.codes, a.vec_ids, start, n, (c - c0) * kChunk + lane, w0, w1, i0, i1);
+      nload += (unsigned)min(kChunk, n - (c - c0) * kChunk);
+      const int b = dec % kLutBufs;
+      lds_wait_at_least(&s_built[b], kBuilderWaves * (dec / kLutBufs + 1), wc);
+      int mine = 0;
+      while (true) {
+        const uint64_t shared_thr = s_thr[s];
+        const uint64_t thr = own < shared_thr ? own : shared_thr;
+        const int v0 = (c - c0) * kChunk + lane;
+        if (b == 0)
+          scan_round_full<D, M, 0>(smem, v0, n, k, w0, w1, i0, i1, thr, lk, own, &s_thr[s]);
+        else if (b == 1)
+          scan_round_full<D, M, 1>(smem, v0, n, k, w0, w1, i0, i1, thr, lk, own, &s_thr[s]);
+        else  // beyond the 64 KB DS offset reach: addresses take a base register
+          scan_round_full<D, M, 2>(smem, v0, n, k, w0, w1, i0, i1, thr, lk, own, &s_thr[s]);
+        ++mine;
+        c += kScanWaves;
+        if (c >= c_end) break;
+        load_pair<M>(a.codes, a.vec_ids, start, n, (c - c0) * kChunk + lane, w0, w1, i0, i1);
+        nload += (unsigned)min(kChunk, n - (c - c0) * kChunk);
+      }
+      // List done by this wave: its LUT buffer may be reused once all its
+      // chunks are in.
+      lds_signal_add(&s_done[b], mine);
+    };
+    // Through query q (slot s): climb the merge tree without waiting.  At each
+    // node the wave deposits its list, then counts itself in; the first of the
+    // two children to arrive is done with the query, the second merges its
+    // sibling's list and climbs on.  The second arrival at the root holds all
+    // eight lists merged: it writes the top-k and frees the slot.  Returns
+    // whether this wave was that root.
+    auto climb = [&](uint64_t lk, int s, int q) {
+      int base = 0;
+#pragma unroll
+      for (int lvl = 0, width = kScanWaves / 2; width >= 1; ++lvl, base += width, width >>= 1) {
+        const int nd = base + (swave >> (lvl + 1)), ch = (swave >> lvl) & 1;
+        s_tree[s][nd][ch][lane] = lk;
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+        int old = 0;
+        if (lane == 0) old = __hip_atomic_fetch_add(&s_arr[s][nd], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        old = __builtin_amdgcn_readfirstlane(old);
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+        if (old == 0) return false;
+        wave_merge_lds64(lk, s_tree[s][nd][ch ^ 1]);
+      }
+      write_topk(lk, q, k, a, __hip_atomic_load(&s_fault, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) != 0);
+      lds_signal_add(&s_free[s], 1);
+      return true;
+    };
     for (int i = 0; dyn || i < nqw; ++i) {
       const int s = i & 1;
       lds_wait_at_least(&s_ready[s], i / 2 + 1, wc);
@@ -678,60 +732,9 @@ __global__ __launch_bounds__(kSpecWaves * kWave, 4) void adc_flow_kernel(AdcArgs
         // keeps the loads inside it even after a give-up.
         const int start = __builtin_amdgcn_readlane(st_l, f);
         const int n = min(__builtin_amdgcn_readlane(n_l, f), total - start);
-        const int c0 = __builtin_amdgcn_readlane(cst_l, f), c_end = __builtin_amdgcn_readlane(cst_n, f);
-        int c = first_own(c0);
-        load_pair<M>(a.codes, a.vec_ids, start, n, (c - c0) * kChunk + lane, w0, w1, i0, i1);
-        nload += (unsigned)min(kChunk, n - (c - c0) * kChunk);
-        const int b = dec % kLutBufs;
-        lds_wait_at_least(&s_built[b], kBuilderWaves * (dec / kLutBufs + 1), wc);
-        int mine = 0;
-        while (true) {
-          const uint64_t shared_thr = s_thr[s];
-          const uint64_t thr = own < shared_thr ? own : shared_thr;
-          const int v0 = (c - c0) * kChunk + lane;
-          if (b == 0)
-            scan_round_full<D, M, 0>(smem, v0, n, k, w0, w1, i0, i1, thr, lk, own, &s_thr[s]);
-          else if (b == 1)
-            scan_round_full<D, M, 1>(smem, v0, n, k, w0, w1, i0, i1, thr, lk, own, &s_thr[s]);
-          else  // beyond the 64 KB DS offset reach: addresses take a base register
-            scan_round_full<D, M, 2>(smem, v0, n, k, w0, w1, i0, i1, thr, lk, own, &s_thr[s]);
-          ++mine;
-          c += kScanWaves;
-          if (c >= c_end) break;
-          load_pair<M>(a.codes, a.vec_ids, start, n, (c - c0) * kChunk + lane, w0, w1, i0, i1);
-          nload += (unsigned)min(kChunk, n - (c - c0) * kChunk);
-        }
-        // List f done by this wave: its LUT buffer may be reused once all its
-        // chunks are in.
-        lds_signal_add(&s_done[b], mine);
+        scan_chunks(s, dec, start, n, __builtin_amdgcn_readlane(cst_l, f), __builtin_amdgcn_readlane(cst_n, f), lk, own);
       }
-      // Through query i: climb the merge tree without waiting.  At each node
-      // the wave deposits its list, then counts itself in; the first of the
-      // two children to arrive is done with the query, the second merges its
-      // sibling's list and climbs on.  The second arrival at the root holds
-      // all eight lists merged: it writes the top-k and frees the slot.
-      bool root = true;
-      int base = 0;
-#pragma unroll
-      for (int lvl = 0, width = kScanWaves / 2; width >= 1; ++lvl, base += width, width >>= 1) {
-        const int nd = base + (swave >> (lvl + 1)), ch = (swave >> lvl) & 1;
-        s_tree[s][nd][ch][lane] = lk;
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-        int old = 0;
-        if (lane == 0) old = __hip_atomic_fetch_add(&s_arr[s][nd], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-        old = __builtin_amdgcn_readfirstlane(old);
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-        if (old == 0) {
-          root = false;
-          break;
-        }
-        wave_merge_lds64(lk, s_tree[s][nd][ch ^ 1]);
-      }
-      if (root) {
-        write_topk(lk, q, k, a, __hip_atomic_load(&s_fault, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) != 0);
-        lds_signal_add(&s_free[s], 1);
-        if (a.stats) t_end = clock64() - t_start;
-      }
+      if (climb(lk, s, q) && a.stats) t_end = clock64() - t_start;
     }
     // The workgroup's end: the latest of the scanner waves' last root writes.
     if (a.stats && lane == 0 && t_end > 0) atomicMax(&s_tend, (unsigned long long)t_end);
