@@ -772,15 +772,21 @@ __global__ void qctr_reset_kernel(int* qctr, int grid) {
   if (threadIdx.x == 0) *qctr = grid;
 }
 
+// Flow-kernel workgroups resident at once on the current device.
+template <int D, int M>
+int flow_resident() {
+  static std::atomic<int> cached[64];
+  return resident_groups(adc_flow_kernel<D, M>, kSpecWaves * kWave, cached);
+}
+
 template <int D, int M>
 fgpu_status launch_flow(const AdcArgs& args, hipStream_t s) {
   FGPU_CHECK(args.nprobe <= 64, FGPU_ERR_UNSUPPORTED, "adc: nprobe must be <= 64");
   FGPU_CHECK(args.faults, FGPU_ERR_ARG, "adc: the flow kernel needs a device give-up counter");
   AdcArgs a = args;
   if (a.spin_limit <= 0) a.spin_limit = (int)flow_spin_limit(a.nprobe, a.max_list_len);
-  static std::atomic<int> cached[64];
-  const int grid = std::min(a.nq, resident_groups(adc_flow_kernel<D, M>, kSpecWaves * kWave, cached));
-  if (a.qctr) hipLaunchKernelGGL(qctr_reset_kernel, dim3(1), dim3(64), 0, s, a.qctr, grid);
+  const int grid = std::min(a.nq, flow_resident<D, M>());
+  if (a.qctr && a.qctr_preset != grid) hipLaunchKernelGGL(qctr_reset_kernel, dim3(1), dim3(64), 0, s, a.qctr, grid);
   hipLaunchKernelGGL((adc_flow_kernel<D, M>), dim3((unsigned)grid), dim3(kSpecWaves * kWave), 0, s, a);
   FGPU_HIP(hipGetLastError());
   return FGPU_OK;
@@ -827,6 +833,16 @@ fgpu_status launch_adc_plain(int dim, int m, const AdcArgs& a, hipStream_t s) {
   if (dim == 96 && m == 32) return launch_flow<96, 32>(a, s);
   if (dim == 96 && m == 16) return launch_flow<96, 16>(a, s);
   return set_error(FGPU_ERR_UNSUPPORTED, "adc: unsupported (dim, pq_m)");
+}
+
+int flow_grid(int dim, int m, int nq, int nprobe) {
+  if (nq <= 0 || nprobe > 64) return 0;
+  int r = 0;
+  if (dim == 128 && m == 32) r = flow_resident<128, 32>();
+  else if (dim == 128 && m == 16) r = flow_resident<128, 16>();
+  else if (dim == 96 && m == 32) r = flow_resident<96, 32>();
+  else if (dim == 96 && m == 16) r = flow_resident<96, 16>();
+  return r > 0 ? std::min(nq, r) : 0;
 }
 
 }  // namespace fgpu

@@ -285,8 +285,15 @@ size_t fgpu_coarse_workspace_bytes(int nq, int nlist) {
   return carve_bytes<float>(rows * (size_t)est_sel_ld(nlist)) + 256;
 }
 
-fgpu_status fgpu_coarse_search(const fgpu_index* ix, const float* dq, int nq, int nprobe, float prune_ratio,
-                               uint32_t* d_ids, float* d_dists, void* ws, size_t ws_bytes, void* stream) {
+}  // extern "C"
+
+namespace {
+// fgpu_coarse_search; with side != nullptr its first select launch also
+// stores side_val at *side (the scan's query counter, so the scan needs no
+// reset kernel of its own).
+fgpu_status coarse_search(const fgpu_index* ix, const float* dq, int nq, int nprobe, float prune_ratio,
+                          uint32_t* d_ids, float* d_dists, void* ws, size_t ws_bytes, void* stream, int* side,
+                          int side_val) {
   FGPU_CHECK(ix && dq && d_ids && d_dists && ws, FGPU_ERR_ARG, "coarse_search: null argument");
   FGPU_CHECK(((uintptr_t)ws & 15) == 0, FGPU_ERR_ARG, "coarse_search: workspace must be 16-byte aligned");
   FGPU_CHECK(nq >= 0 && nprobe >= 1 && nprobe <= ix->nlist && nprobe <= 256, FGPU_ERR_ARG,
@@ -307,9 +314,18 @@ fgpu_status fgpu_coarse_search(const fgpu_index* ix, const float* dq, int nq, in
                                  s));
     FGPU_TRY(launch_select_exact(est, ld, nb, ix->nlist, dq + b0 * ix->dim, ix->d_centroids, ix->dim,
                                  ix->d_cnorm_max, nprobe, 1, prune_ratio,
-                                 reinterpret_cast<int32_t*>(d_ids) + b0 * nprobe, d_dists + b0 * nprobe, s));
+                                 reinterpret_cast<int32_t*>(d_ids) + b0 * nprobe, d_dists + b0 * nprobe, s,
+                                 b0 == 0 ? side : nullptr, side_val));
   }
   return FGPU_OK;
+}
+}  // namespace
+
+extern "C" {
+
+fgpu_status fgpu_coarse_search(const fgpu_index* ix, const float* dq, int nq, int nprobe, float prune_ratio,
+                               uint32_t* d_ids, float* d_dists, void* ws, size_t ws_bytes, void* stream) {
+  return coarse_search(ix, dq, nq, nprobe, prune_ratio, d_ids, d_dists, ws, ws_bytes, stream, nullptr, 0);
 }
 
 fgpu_status fgpu_prune_probes(uint32_t* d_probe_ids, const float* d_probe_dists, int nq, int nprobe, float prune_ratio,
@@ -414,11 +430,16 @@ fgpu_status fgpu_search(const fgpu_index* ix, const float* dq, int nq, int nprob
   float* pd = cv.take<float>((size_t)nq * nprobe);
   int* qctr = cv.take<int>(1);
   FGPU_CHECK(cv.ok(), FGPU_ERR_WORKSPACE, "search: workspace too small");
-  FGPU_TRY(fgpu_coarse_search(ix, dq, nq, nprobe, prune_ratio, pid, pd, cv.base + cv.used, ws_bytes - cv.used, stream));
   FGPU_CHECK(nq >= 0 && k >= 1, FGPU_ERR_ARG, "search: bad sizes");
   FGPU_CHECK(adc_supported(ix->dim, ix->m), FGPU_ERR_UNSUPPORTED, "search: no kernel for this (dim, pq_m)");
+  // The scan claims queries from a counter that starts at its grid size; the
+  // coarse step's select stores that value on the way.
+  const int grid = flow_grid(ix->dim, ix->m, nq, nprobe);
+  FGPU_TRY(coarse_search(ix, dq, nq, nprobe, prune_ratio, pid, pd, cv.base + cv.used, ws_bytes - cv.used, stream,
+                         grid > 0 ? qctr : nullptr, grid));
   AdcArgs a = adc_args(ix, dq, nq, pid, pd, nprobe, k, d_out_ids, d_out_dists);
-  a.qctr = qctr;  // the scan claims queries dynamically
+  a.qctr = qctr;
+  a.qctr_preset = grid;
   return launch_adc_plain(ix->dim, ix->m, a, as_stream(stream));
 }
 

@@ -580,12 +580,13 @@ __global__ __launch_bounds__(256) void select_exact_kernel(
     const E* __restrict__ est, int64_t ld, int64_t nrows, int ncols,
     const float* __restrict__ x, const float* __restrict__ c, int dim,
     const float* __restrict__ cn_max, float kappa, int p, int prune,
-    float prune_ratio, int32_t* __restrict__ out_ids, float* __restrict__ out_d) {
+    float prune_ratio, int32_t* __restrict__ out_ids, float* __restrict__ out_d, int* side, int side_val) {
   __shared__ uint32_t hist_s[4][256];
   __shared__ int cand_s[4][kCandCap];
   __shared__ __align__(16) float x_s[4][256];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int64_t row = (int64_t)blockIdx.x * 4 + wave;
+  if (side && blockIdx.x == 0 && threadIdx.x == 0) *side = side_val;  // the caller's one-word side write
   if (row >= nrows) return;  // whole wave leaves; no workgroup barrier follows
   float* xs = x_s[wave];
   float xnr = 0.0f;
@@ -653,7 +654,7 @@ __global__ __launch_bounds__(256) void select_min_kernel(
     const E* __restrict__ est, int64_t ld, int64_t nrows, int ncols,
     const float* __restrict__ x, const float* __restrict__ c, int dim,
     const float* __restrict__ cn_max, float kappa, int prune, float prune_ratio,
-    int32_t* __restrict__ out_ids, float* __restrict__ out_d) {
+    int32_t* __restrict__ out_ids, float* __restrict__ out_d, int* side, int side_val) {
   __shared__ int cand_s[4][kCandCap];
   __shared__ __align__(16) float x_s[4][256];
   constexpr bool HALF = sizeof(E) == 2;
@@ -661,6 +662,7 @@ __global__ __launch_bounds__(256) void select_min_kernel(
   constexpr int PIECE = V * kWave;     // columns a piece
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int64_t row = (int64_t)blockIdx.x * 4 + wave;
+  if (side && blockIdx.x == 0 && threadIdx.x == 0) *side = side_val;  // the caller's one-word side write
   if (row >= nrows) return;  // whole wave leaves; no workgroup barrier follows
   float* xs = x_s[wave];
   int* cand = cand_s[wave];
@@ -860,16 +862,17 @@ fgpu_status launch_knn_t(const float* est, int64_t ld, int64_t nrows, int ncols,
 template <int VPL>
 fgpu_status launch_select_t(const void* est, int64_t ld, int64_t nrows, int ncols, const float* x,
                             const float* c, int dim, const float* cn_max, float kappa,
-                            int p, int prune, float prune_ratio, int32_t* ids, float* d, hipStream_t s) {
+                            int p, int prune, float prune_ratio, int32_t* ids, float* d, int* side, int side_val,
+                            hipStream_t s) {
   const int64_t blocks = (nrows + 3) / 4;
   if constexpr (kEstHalf)
     hipLaunchKernelGGL((select_exact_kernel<VPL, uint16_t>), dim3((unsigned)blocks), dim3(256), 0, s,
                        static_cast<const uint16_t*>(est), ld, nrows, ncols, x, c, dim, cn_max, kappa, p, prune,
-                       prune_ratio, ids, d);
+                       prune_ratio, ids, d, side, side_val);
   else
     hipLaunchKernelGGL((select_exact_kernel<VPL, float>), dim3((unsigned)blocks), dim3(256), 0, s,
                        static_cast<const float*>(est), ld, nrows, ncols, x, c, dim, cn_max, kappa, p, prune,
-                       prune_ratio, ids, d);
+                       prune_ratio, ids, d, side, side_val);
   FGPU_HIP(hipGetLastError());
   return FGPU_OK;
 }
@@ -935,7 +938,8 @@ static float coarse_kappa(int dim) {
 
 fgpu_status launch_select_exact(const void* est, int64_t ld, int64_t nrows, int ncols, const float* x,
                                 const float* c, int dim, const float* cn_max, int p,
-                                int prune, float prune_ratio, int32_t* ids, float* d, hipStream_t s) {
+                                int prune, float prune_ratio, int32_t* ids, float* d, hipStream_t s, int* side,
+                                int side_val) {
   FGPU_CHECK(ld % 8 == 0, FGPU_ERR_ARG, "select: row stride must be a multiple of 8");
   FGPU_CHECK(p >= 1 && p <= kSelectMax && p <= ncols, FGPU_ERR_UNSUPPORTED, "select: need 1 <= p <= min(256, ncols)");
   FGPU_CHECK(dim <= 256, FGPU_ERR_UNSUPPORTED, "select: dim must be <= 256");
@@ -945,15 +949,17 @@ fgpu_status launch_select_exact(const void* est, int64_t ld, int64_t nrows, int 
     const dim3 grid((unsigned)((nrows + 3) / 4));
     if constexpr (kEstHalf)
       hipLaunchKernelGGL(select_min_kernel<uint16_t>, grid, dim3(256), 0, s, static_cast<const uint16_t*>(est), ld,
-                         nrows, ncols, x, c, dim, cn_max, kappa, prune, prune_ratio, ids, d);
+                         nrows, ncols, x, c, dim, cn_max, kappa, prune, prune_ratio, ids, d, side, side_val);
     else
       hipLaunchKernelGGL(select_min_kernel<float>, grid, dim3(256), 0, s, static_cast<const float*>(est), ld, nrows,
-                         ncols, x, c, dim, cn_max, kappa, prune, prune_ratio, ids, d);
+                         ncols, x, c, dim, cn_max, kappa, prune, prune_ratio, ids, d, side, side_val);
     FGPU_HIP(hipGetLastError());
     return FGPU_OK;
   }
 #define FGPU_SEL(V) \
-  if (ncols <= (V) * kWave) return launch_select_t<V>(est, ld, nrows, ncols, x, c, dim, cn_max, kappa, p, prune, prune_ratio, ids, d, s)
+  if (ncols <= (V) * kWave) \
+    return launch_select_t<V>(est, ld, nrows, ncols, x, c, dim, cn_max, kappa, p, prune, prune_ratio, ids, d, side, \
+                              side_val, s)
   FGPU_SEL(1);
   FGPU_SEL(2);
   FGPU_SEL(4);

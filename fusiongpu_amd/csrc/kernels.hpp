@@ -28,11 +28,13 @@ int64_t est_sel_ld(int ncols);
 // Per row: the p nearest columns by exact device-form L2, chosen from the
 // estimates of launch_gemm_est_sel with a rigorous error margin.  ids
 // are int32 bit patterns; with prune != 0 a column farther than
-// best*prune_ratio gets 0xFFFFFFFF.
+// best*prune_ratio gets 0xFFFFFFFF.  With side != nullptr the launch also
+// stores side_val at *side (one word, for the next kernel on the stream).
 fgpu_status launch_select_exact(const void* est, int64_t ld, int64_t nrows, int ncols,
                                 const float* x, const float* c, int dim,
                                 const float* cn_max, int p, int prune, float prune_ratio,
-                                int32_t* out_ids, float* out_d, hipStream_t s);
+                                int32_t* out_ids, float* out_d, hipStream_t s, int* side = nullptr,
+                                int side_val = 0);
 // Exact kNN over one chunk of <= 4096 base rows c (ids id_base + col), merged
 // into the running top-k in ids/d (k <= 128) when accum != 0.
 fgpu_status launch_knn_chunk(const float* est, int64_t ld, int64_t nrows, int ncols, const float* x, const float* c,
@@ -81,6 +83,10 @@ struct AdcArgs {
   // Optional device int (workspace) for dynamic query claims of the flow
   // kernel, which resets it on the launch stream; needs probe_dists.
   int* qctr = nullptr;
+  // A positive value: an earlier kernel on the stream has already stored it
+  // in *qctr (the select's side write).  The launch skips its own reset when
+  // it equals the grid it launches (flow_grid).
+  int qctr_preset = 0;
 };
 // Id written to every slot of a query whose result a bounded-wait give-up may
 // have touched (the reference's padding id is -1; it never writes -2).
@@ -94,6 +100,10 @@ bool adc_supported(int dim, int m);
 fgpu_status launch_list_radius(const float* codebook, int m, int sub, const uint8_t* codes, const int32_t* offsets,
                                int nlist, float* rmax, hipStream_t s);
 fgpu_status launch_adc_plain(int dim, int m, const AdcArgs& a, hipStream_t s);
+// The grid of the flow-kernel launch launch_adc_plain makes for these sizes
+// (the start value of its query counter), or 0 if that call takes another
+// kernel.
+int flow_grid(int dim, int m, int nq, int nprobe);
 
 // ---- twophase.hip --------------------------------------------------------------
 struct TwoPhaseArgs {
