@@ -54,6 +54,7 @@ _SIGS = {
     "fgpu_index_check": (_i32, [_vp, _vp]),
     "fgpu_debug_set_spin_limit": (None, [_i32]),
     "fgpu_debug_set_list_skip": (None, [_i32]),
+    "fgpu_debug_set_two_phase_split": (None, [_i32]),
     "fgpu_debug_pq_sample": (_i32, [_i64, _i32, _vp]),
     "fgpu_stream_read_grid": (_i32, []),
     "fgpu_stream_read": (_i32, [_vp, _sz, _vp, _vp]),
@@ -320,6 +321,11 @@ def debug_set_spin_limit(polls: int):
 def debug_set_list_skip(enabled: bool):
     """Measurement hook (fgpu_debug_set_list_skip): False makes the plain scan read every probed list."""
     lib.fgpu_debug_set_list_skip(int(bool(enabled)))
+
+
+def debug_set_two_phase_split(split: int):
+    """Test hook (fgpu_debug_set_two_phase_split): phase-1 workgroups a query (0 automatic, 1 never)."""
+    lib.fgpu_debug_set_two_phase_split(int(split))
 
 
 def debug_pq_sample(n: int, sample_size: int) -> np.ndarray:

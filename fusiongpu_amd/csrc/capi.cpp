@@ -387,6 +387,7 @@ fgpu_status fgpu_index_check(const fgpu_index* ix, void* stream) {
 void fgpu_debug_set_spin_limit(int polls) { g_spin_override.store(polls > 0 ? polls : 0); }
 
 void fgpu_debug_set_list_skip(int enabled) { g_list_skip.store(enabled ? 1 : 0); }
+void fgpu_debug_set_two_phase_split(int split) { set_two_phase_split_override(split); }
 
 int fgpu_debug_pq_sample(int64_t n, int sample_size, int32_t* h_rows) {
   if (n < 1 || sample_size < 0 || !h_rows) return -1;
@@ -446,7 +447,10 @@ fgpu_status fgpu_search(const fgpu_index* ix, const float* dq, int nq, int nprob
 // ---------------------------------------------------------------------------
 size_t fgpu_two_phase_workspace_bytes(int nq, int nprobe, int p1_lists, int limit_k, int rerank_m) {
   const int p1 = std::max(0, std::min(nprobe, p1_lists));
-  return carve_bytes<uint64_t>((size_t)std::max(nq, 1) * two_phase_pool_cap(p1, limit_k, rerank_m));
+  const size_t rows = (size_t)std::max(nq, 1);
+  // Each query's candidate pool, then its phase-1 cutoffs (split phase 1).
+  return carve_bytes<uint64_t>(rows * two_phase_pool_cap(p1, limit_k, rerank_m)) +
+         carve_bytes<float>(rows * (size_t)std::max(nprobe, 1));
 }
 
 }  // extern "C"
@@ -464,8 +468,14 @@ fgpu_status two_phase(const fgpu_index* ix, const float* dq, int nq, const uint3
   if (nq == 0) return FGPU_OK;
   const int p1 = std::max(0, std::min(nprobe, p1_lists));
   const int cap = two_phase_pool_cap(p1, limit_k, rerank_m);
-  const int64_t chunk = std::min<int64_t>(nq, (int64_t)(ws_bytes / ((size_t)cap * sizeof(uint64_t))));
+  // Queries a launch: their pools and cutoff rows fit the workspace.
+  auto need = [&](int64_t c) {
+    return carve_bytes<uint64_t>((size_t)c * cap) + carve_bytes<float>((size_t)c * nprobe);
+  };
+  int64_t chunk = std::min<int64_t>(nq, (int64_t)(ws_bytes / ((size_t)cap * sizeof(uint64_t) + nprobe * sizeof(float))));
+  while (chunk > 0 && need(chunk) > ws_bytes) --chunk;
   FGPU_CHECK(chunk >= 1, FGPU_ERR_WORKSPACE, "two_phase_search: workspace smaller than one query's pool");
+  float* cut_ws = reinterpret_cast<float*>(static_cast<char*>(ws) + carve_bytes<uint64_t>((size_t)chunk * cap));
   for (int64_t q0 = 0; q0 < nq; q0 += chunk) {
     const int nb = (int)std::min<int64_t>(chunk, nq - q0);
     TwoPhaseArgs a{dq + q0 * ix->dim, ix->d_centroids, ix->d_codebook, ix->d_offsets, ix->d_codes, ix->d_ids,
@@ -474,6 +484,10 @@ fgpu_status two_phase(const fgpu_index* ix, const float* dq, int nq, const uint3
                    d_top_dists + q0 * rerank_m, d_top_counts + q0,
                    d_list_cutoffs ? d_list_cutoffs + q0 * p1 : nullptr, d_thresholds ? d_thresholds + q0 : nullptr,
                    d_stats};
+    // A batch too small to fill the GPU (two workgroups a CU) spreads each
+    // query's phase-1 lists over several workgroups.
+    a.split = two_phase_split(nb, p1, limit_k);
+    a.cut_ws = cut_ws;
     FGPU_TRY(launch_two_phase(ix->dim, ix->m, a, as_stream(stream)));
   }
   return FGPU_OK;

@@ -134,8 +134,16 @@ struct TwoPhaseArgs {
   // and the final select + sort; [8..10] of its phase-1 clocks, those spent
   // up to the LUT barrier, in the scan loop, and in the merge barrier + merge.
   unsigned long long* stats = nullptr;
+  // Phase 1 over `split` workgroups a query (limit_k <= 64; small batches):
+  // cut_ws holds [nq][nprobe] phase-1 cutoffs between the two launches.
+  int split = 1;
+  float* cut_ws = nullptr;
 };
 int two_phase_pool_cap(int p1, int limit_k, int rerank_m);
+// Workgroups a query for phase 1 (TwoPhaseArgs::split) for a launch of nq
+// queries: 1 once nq fills every CU twice; a test override can force it.
+int two_phase_split(int nq, int p1, int limit_k);
+void set_two_phase_split_override(int v);
 fgpu_status launch_two_phase(int dim, int m, const TwoPhaseArgs& a, hipStream_t s);
 
 struct RerankArgs {

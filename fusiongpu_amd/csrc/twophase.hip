@@ -27,6 +27,9 @@
 // The rerank kernel gives each query one 128-thread workgroup: exact
 // distances one candidate per lane, wave bitonic sorts and a merge-path merge
 // with the running top-k in LDS.
+#include <algorithm>
+#include <atomic>
+
 #include "common.hpp"
 #include "kernels.hpp"
 #include "scan_common.hpp"
@@ -148,7 +151,7 @@ __device__ void lds_bitonic_sort(uint64_t* sk, int np2) {
   }
 }
 
-template <int D, int M>
+template <int D, int M, int MODE>
 __global__ __launch_bounds__(kTT) __attribute__((amdgpu_waves_per_eu(TCfg<D, M>::WPE, TCfg<D, M>::WPE)))
 void two_phase_kernel(TwoPhaseArgs a) {
   using C = TCfg<D, M>;
@@ -168,6 +171,7 @@ void two_phase_kernel(TwoPhaseArgs a) {
   __shared__ float s_cut[kMaxProbes];
   __shared__ int f_list[kMaxProbes], f_start[kMaxProbes], f_n[kMaxProbes], f_p[kMaxProbes];  // usable probes, in order
   __shared__ float f_lb[kMaxProbes];                                                          // phase-2 list bounds
+  __shared__ int f_base[kMaxProbes + 1];  // phase-1 list f's pool slots start at f_base[f] (limit_k <= 64)
   __shared__ int s_nv, s_nv1;
   __shared__ int s_cnt;
   __shared__ unsigned long long s_lthr;
@@ -175,7 +179,17 @@ void two_phase_kernel(TwoPhaseArgs a) {
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int kc = tid & (kPQK - 1), g = __builtin_amdgcn_readfirstlane(tid / kPQK);
-  const int q = blockIdx.x;
+  // Split phase 1 (small batches, limit_k <= 64): a launch with MODE 1 runs
+  // a.split workgroups a query, workgroup g scanning phase-1 lists g,
+  // g + split, ...; each list's pool slots and cutoff depend only on the list,
+  // so the workgroups write them independently (cutoffs to a.cut_ws).  A
+  // second launch with MODE 2 (one workgroup a query) reads the cutoffs back
+  // and runs the threshold, phase 2 and the final select.  MODE 0 does it
+  // all in one workgroup (separate instantiations keep its code as it is).
+  constexpr int mode = MODE;
+  const int q = mode == 1 ? (int)blockIdx.x / a.split : (int)blockIdx.x;
+  const int gsub = mode == 1 ? (int)blockIdx.x % a.split : 0;
+  const int gstep = mode == 1 ? a.split : 1;
   const int P = a.nprobe, p1 = a.p1, R = a.rerank_m, cap = a.pool_cap, K1 = a.limit_k;
   // If every wave holds Q = ceil(K1 / 8) vectors at or below its published
   // key, the list has >= 8 Q >= K1 vectors at or below the largest published
@@ -191,7 +205,7 @@ void two_phase_kernel(TwoPhaseArgs a) {
   if (wave == 0) {
     // Usable probes (in range, non-empty) in probe order, 64 probes a step;
     // the first s_nv1 are phase 1 (probe index < p1).
-    int nv_run = 0, nv1_run = 0;
+    int nv_run = 0, nv1_run = 0, base_run = 0;
     for (int c0 = 0; c0 < P; c0 += kWave) {
       const int pi = c0 + lane;
       int l = 0, st = 0, n = 0;
@@ -205,16 +219,22 @@ void two_phase_kernel(TwoPhaseArgs a) {
       }
       const uint64_t bm = __ballot(n > 0);
       const int pos = nv_run + __popcll(bm & ((1ull << lane) - 1ull));
+      // Pool slots of a phase-1 list: min(n, limit_k) (used with limit_k <= 64).
+      const int w1 = n > 0 && pi < p1 ? (n < K1 ? n : K1) : 0;
+      const int incl = wave_incl_scan(w1);
       if (n > 0) {
         f_list[pos] = l;
         f_start[pos] = st;
         f_n[pos] = n;
         f_p[pos] = pi;
+        if (pi < p1) f_base[pos] = base_run + incl - w1;
       }
       nv_run += __popcll(bm);
       nv1_run += __popcll(__ballot(n > 0 && pi < p1));
+      base_run += __shfl(incl, kWave - 1, kWave);
     }
     if (lane == 0) {
+      f_base[nv1_run] = base_run;
       s_nv = nv_run;
       s_nv1 = nv1_run;
       s_cnt = 0;
@@ -229,7 +249,7 @@ void two_phase_kernel(TwoPhaseArgs a) {
   };
   // Lower bound of every phase-2 list, one wave per list: every later skip
   // decision is an LDS read.
-  for (int f = nv1 + wave; f < nv; f += kTW) {
+  for (int f = nv1 + wave; mode != 1 && f < nv; f += kTW) {
     const float* cr = a.centroids + (size_t)f_list[f] * D;
     const float ra = lane < D ? qs[lane] - cr[lane] : 0.0f;
     const float rb = lane + kWave < D ? qs[lane + kWave] - cr[lane + kWave] : 0.0f;
@@ -238,7 +258,9 @@ void two_phase_kernel(TwoPhaseArgs a) {
     for (int o = 32; o > 0; o >>= 1) s2 += shfl_xor_f(s2, o);
     if (lane == 0) f_lb[f] = list_lower_bound(s2, a.rmax[f_list[f]]);
   }
-  if (nv > 0) residual(0, rbuf[0]);
+  // The first list this workgroup scans: gsub in phase 1, none ahead of
+  // phase 2 in mode 2 (phase 2 computes its residuals itself).
+  if (mode != 2 && gsub < nv) residual(gsub, rbuf[0]);
   __syncthreads();
   const long long t_setup = a.stats ? clock64() : 0;
 
@@ -280,7 +302,7 @@ void two_phase_kernel(TwoPhaseArgs a) {
   uint4 w0[C::NV4], w1[C::NV4], n0[C::NV4], n1[C::NV4];
   int i0 = kPadId, i1 = kPadId, j0 = kPadId, j1 = kPadId;
   int it = 0;       // lists processed: rbuf[it & 1] holds the residual of list pre_f
-  int pre_f = nv > 0 ? 0 : -1;
+  int pre_f = mode != 2 && gsub < nv ? gsub : -1;
   // instrumentation (per wave; summed at the end when a.stats is set)
   unsigned st_load = 0, st_lut = 0, st_skip = 0, st_pass = 0;
   auto count_load = [&](int base, int end) { st_load += (unsigned)max(0, min(kVecPerWaveRound, end - base)); };
@@ -300,7 +322,10 @@ void two_phase_kernel(TwoPhaseArgs a) {
       const int w = n < K1 ? n : K1;
       if (lane < w) pool[st_base[t] + lane] = k;
       const float cut = key_dist(readlane64(k, w - 1));
-      if (lane == 0) s_cut[f_p[lf]] = cut;
+      if (lane == 0) {
+        s_cut[f_p[lf]] = cut;
+        if (mode == 1) a.cut_ws[(size_t)q * P + f_p[lf]] = cut;
+      }
     }
     nst = 0;
     __syncthreads();  // the stage is free again
@@ -313,7 +338,7 @@ void two_phase_kernel(TwoPhaseArgs a) {
   // least 2048 slots above limit_k for every list (two_phase_pool_cap).  The
   // list's cutoff is then the largest of the w = min(n, limit_k) keys kept,
   // its w-th smallest distance.
-  for (int f = 0; K1 > kWave && f < nv1; ++f) {
+  for (int f = 0; K1 > kWave && mode == 0 && f < nv1; ++f) {
     const int start = f_start[f], n = f_n[f];
     const int first = wave * kVecPerWaveRound;
     load_pair<M>(a.codes, a.vec_ids, start, n, first + lane, w0, w1, i0, i1);
@@ -393,7 +418,7 @@ void two_phase_kernel(TwoPhaseArgs a) {
     pre_f = nf;
     __syncthreads();  // every wave is through list f: the LUT and s_pub are free
   }
-  for (int f = 0; K1 <= kWave && f < nv1; ++f) {
+  for (int f = gsub; K1 <= kWave && mode != 2 && f < nv1; f += gstep) {
     const long long c0 = a.stats ? clock64() : 0;
     const int start = f_start[f], n = f_n[f];
     const int first = wave * kVecPerWaveRound;
@@ -403,7 +428,9 @@ void two_phase_kernel(TwoPhaseArgs a) {
     // All waves have finished scanning list f-1 (they passed the barrier
     // after it), so the single LUT buffer is free.
     build_lut(rbuf[it & 1]);
-    const int nf = f + 1 < nv ? f + 1 : -1;
+    // The next list's residual: the next phase-1 list of this workgroup, or in
+    // mode 0 whatever list follows (the first phase-2 list after phase 1).
+    const int nf = mode == 1 ? (f + gstep < nv1 ? f + gstep : -1) : (f + 1 < nv ? f + 1 : -1);
     if (nf >= 0) residual(nf, rbuf[(it + 1) & 1]);
     __syncthreads();  // LUT f and the next residual ready; s_lthr reset
     const long long c1 = a.stats ? clock64() : 0;
@@ -452,7 +479,7 @@ void two_phase_kernel(TwoPhaseArgs a) {
     stage[nst][wave * kWave + lane] = lk;
     if (tid == 0) {
       st_f[nst] = f;
-      st_base[nst] = cnt_p1;
+      st_base[nst] = mode == 0 ? cnt_p1 : f_base[f];
     }
     cnt_p1 += n < K1 ? n : K1;
     ++nst;
@@ -461,7 +488,7 @@ void two_phase_kernel(TwoPhaseArgs a) {
       if (lane == 0) s_lthr = kNoThr;
       if (lane < kTW) s_pub[lane] = kNoThr;
     }
-    if (nst == kStage || f == nv1 - 1) flush();
+    if (nst == kStage || f + gstep >= nv1) flush();
     if (a.stats) {
       const long long c3 = clock64();
       c_build += c1 - c0;
@@ -470,6 +497,26 @@ void two_phase_kernel(TwoPhaseArgs a) {
     }
     ++it;
     pre_f = nf;
+  }
+  if constexpr (mode == 1) {  // this workgroup's phase-1 lists are in the pool, their cutoffs in a.cut_ws
+    if (a.stats) {
+      if (lane == 0) {
+        atomicAdd(&a.stats[0], (unsigned long long)st_load);
+        if (wave == 0) atomicAdd(&a.stats[1], (unsigned long long)st_lut);
+      }
+      if (tid == 0) {
+        atomicAdd(&a.stats[4], (unsigned long long)(t_setup - t_start));
+        atomicAdd(&a.stats[5], (unsigned long long)(clock64() - t_setup));
+        atomicAdd(&a.stats[8], (unsigned long long)c_build);
+        atomicAdd(&a.stats[9], (unsigned long long)c_scan);
+        atomicAdd(&a.stats[10], (unsigned long long)c_merge);
+      }
+    }
+    return;
+  }
+  if constexpr (mode == 2) {  // phase 1 ran in the mode-1 launch: its pool slots and cutoffs
+    if (K1 <= kWave) cnt_p1 = f_base[nv1];
+    for (int f = tid; f < nv1; f += kTT) s_cut[f_p[f]] = a.cut_ws[(size_t)q * P + f_p[f]];
   }
   if (tid == 0) s_cnt = cnt_p1;
   __syncthreads();
@@ -649,7 +696,14 @@ void two_phase_kernel(TwoPhaseArgs a) {
 
 template <int D, int M>
 fgpu_status launch_tp(const TwoPhaseArgs& a, int nq, hipStream_t s) {
-  hipLaunchKernelGGL((two_phase_kernel<D, M>), dim3((unsigned)nq), dim3(kTT), 0, s, a);
+  if (a.split > 1 && a.limit_k <= kWave && a.cut_ws) {
+    hipLaunchKernelGGL((two_phase_kernel<D, M, 1>), dim3((unsigned)(nq * a.split)), dim3(kTT), 0, s, a);
+    FGPU_HIP(hipGetLastError());
+    hipLaunchKernelGGL((two_phase_kernel<D, M, 2>), dim3((unsigned)nq), dim3(kTT), 0, s, a);
+    FGPU_HIP(hipGetLastError());
+    return FGPU_OK;
+  }
+  hipLaunchKernelGGL((two_phase_kernel<D, M, 0>), dim3((unsigned)nq), dim3(kTT), 0, s, a);
   FGPU_HIP(hipGetLastError());
   return FGPU_OK;
 }
@@ -801,6 +855,22 @@ int two_phase_pool_cap(int p1, int limit_k, int rerank_m) {
   // to its limit_k best, so every list needs 2048 free slots above them.
   const int extra = limit_k > kWave ? p1 * limit_k + 2048 : (p1 * limit_k > 2048 ? p1 * limit_k : 2048);
   return (rerank_m + extra + 63) / 64 * 64;
+}
+
+// 0: automatic; 1: never split; s >= 2: split phase 1 s ways (at most p1).
+static std::atomic<int> g_tp_split{0};
+void set_two_phase_split_override(int v) { g_tp_split.store(v < 0 ? 0 : v, std::memory_order_relaxed); }
+
+int two_phase_split(int nq, int p1, int limit_k) {
+  const int force = g_tp_split.load(std::memory_order_relaxed);
+  if (limit_k > kWave || p1 < 2 || nq <= 0 || force == 1) return 1;
+  if (force > 1) return std::min(p1, force);
+  int dev = 0, cus = 256;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+    cus = 256;
+  const int slots = 2 * cus;  // two_phase_kernel workgroups resident at once
+  return nq >= slots ? 1 : std::min(p1, std::max(1, slots / nq));
 }
 
 fgpu_status launch_two_phase(int dim, int m, const TwoPhaseArgs& a, hipStream_t s) {

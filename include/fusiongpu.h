@@ -104,6 +104,11 @@ void fgpu_debug_set_spin_limit(int polls);
  * bound exceeds the running k-th distance (results are the same; only the
  * work differs).  1 restores the default. */
 void fgpu_debug_set_list_skip(int enabled);
+/* Test hook: phase 1 of every later two-phase launch in the process runs on
+ * `split` workgroups a query (0 = automatic: split only batches too small to
+ * fill the GPU; 1 = never; s >= 2 = s, at most p1; limit_k <= 64 only).
+ * Results are the same whatever the split. */
+void fgpu_debug_set_two_phase_split(int split);
 /* Test hook (host only): the PQ training sample rows of fgpu_pq_train, the
  * first min(sample_size, n) entries of std::shuffle(0 .. n-1, mt19937(12345))
  * (pq_utils.h:91-97), into h_rows.  Returns their count, or -1 on a bad

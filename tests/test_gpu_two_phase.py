@@ -121,6 +121,49 @@ def test_two_phase_many_phase1_lists():
     idx.close()
 
 
+@pytest.mark.parametrize("dim,m,p1,limit_k,coeff,rerank_m", [
+    (128, 32, 12, 50, 1.0, 1000),  # the reference pipeline's defaults (p1 12, limit_k 50)
+    (96, 16, 5, 64, 1.2, 300),     # limit_k at the split's limit
+    (128, 16, 2, 1, 1.0, 40),      # two phase-1 lists, one candidate each
+])
+def test_two_phase_split_phase1_equals_one_workgroup(dim, m, p1, limit_k, coeff, rerank_m):
+    """Phase 1 spread over several workgroups a query (small batches) gives
+    the one-workgroup result bit for bit, also with more workgroups than
+    usable phase-1 lists; one split against the oracle."""
+    _say(f"two_phase split dim={dim} m={m} p1={p1} limit_k={limit_k}")
+    rng = np.random.default_rng(9000 + dim + m + p1)
+    nlist = 48
+    offs, ids, lc, cent, cb = _index(rng, 30000, dim, m, nlist, empty=(2, 11), big=6)
+    q = (rng.standard_normal((60, dim)) * 0.7).astype(np.float32)
+    probes, _ = oracle.coarse(q, cent, 16)
+    probes[1, 0] = 2                     # an empty list first
+    probes[2, :p1] = 0xFFFFFFFF          # no usable phase-1 list
+    probes[3, 1] = 0xFFFFFFFF            # a pruned probe inside phase 1
+    probes[4, 0] = 6                     # the long list in phase 1
+    idx = fg.Index.from_arrays(dim, m, offs, ids, lc, cent, cb)
+    dq, dp = torch.from_numpy(q).cuda(), torch.from_numpy(probes.view(np.int32)).cuda()
+    outs = {}
+    try:
+        for split in (1, 2, 3, 7, 64):
+            fg.debug_set_two_phase_split(split)
+            gid, gd, gcnt, gcut, gthr = idx.two_phase_search(dq, dp, p1, limit_k, coeff, rerank_m, want_cutoffs=True)
+            outs[split] = (_host(gid), _bits(_host(gd)), _host(gcnt), _bits(_host(gcut)), _bits(_host(gthr)))
+    finally:
+        fg.debug_set_two_phase_split(0)
+    for split in (2, 3, 7, 64):
+        for a, b in zip(outs[1], outs[split]):
+            assert np.array_equal(a, b), f"split {split} differs"
+    oid, od, ocnt, ocut, othr = oracle.search_two_phase(q, cent, cb, offs, ids, lc, probes, p1, limit_k, coeff,
+                                                        rerank_m)
+    gid, gd, gcnt, gcut, gthr = outs[7]
+    assert np.array_equal(gcnt, ocnt)
+    assert np.array_equal(gid, oid)
+    assert np.array_equal(gd, _bits(od))
+    assert np.array_equal(gcut, _bits(ocut))
+    assert np.array_equal(gthr, _bits(othr))
+    idx.close()
+
+
 def test_two_phase_workspace_chunks_equal_one_launch():
     _say("two_phase chunked workspace")
     rng = np.random.default_rng(77)
