@@ -55,6 +55,7 @@ _SIGS = {
     "fgpu_debug_set_spin_limit": (None, [_i32]),
     "fgpu_debug_set_list_skip": (None, [_i32]),
     "fgpu_debug_set_two_phase_split": (None, [_i32]),
+    "fgpu_debug_set_rerank_spec": (None, [_i32]),
     "fgpu_debug_pq_sample": (_i32, [_i64, _i32, _vp]),
     "fgpu_stream_read_grid": (_i32, []),
     "fgpu_stream_read": (_i32, [_vp, _sz, _vp, _vp]),
@@ -326,6 +327,11 @@ def debug_set_list_skip(enabled: bool):
 def debug_set_two_phase_split(split: int):
     """Test hook (fgpu_debug_set_two_phase_split): phase-1 workgroups a query (0 automatic, 1 never)."""
     lib.fgpu_debug_set_two_phase_split(int(split))
+
+
+def debug_set_rerank_spec(spec: int):
+    """Test hook (fgpu_debug_set_rerank_spec): rerank mini-batches computed at once (0 automatic, 1, or 4)."""
+    lib.fgpu_debug_set_rerank_spec(int(spec))
 
 
 def debug_pq_sample(n: int, sample_size: int) -> np.ndarray:

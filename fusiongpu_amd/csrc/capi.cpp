@@ -388,6 +388,7 @@ void fgpu_debug_set_spin_limit(int polls) { g_spin_override.store(polls > 0 ? po
 
 void fgpu_debug_set_list_skip(int enabled) { g_list_skip.store(enabled ? 1 : 0); }
 void fgpu_debug_set_two_phase_split(int split) { set_two_phase_split_override(split); }
+void fgpu_debug_set_rerank_spec(int spec) { set_rerank_spec_override(spec); }
 
 int fgpu_debug_pq_sample(int64_t n, int sample_size, int32_t* h_rows) {
   if (n < 1 || sample_size < 0 || !h_rows) return -1;

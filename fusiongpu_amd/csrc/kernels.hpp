@@ -160,6 +160,10 @@ struct RerankArgs {
   int32_t* visited;         // [nq] or nullptr
 };
 fgpu_status launch_rerank(int dim, const RerankArgs& a, hipStream_t s);
+// Mini-batches the rerank kernel computes at once for nq queries (1 or 4);
+// a test override can force either.
+int rerank_spec(int nq);
+void set_rerank_spec_override(int v);
 
 // ---- graph.hip -----------------------------------------------------------------
 struct GraphArgs {

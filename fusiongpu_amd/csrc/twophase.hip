@@ -714,16 +714,24 @@ fgpu_status launch_tp(const TwoPhaseArgs& a, int nq, hipStream_t s) {
 // fused chain over the dimensions, gpu_global.cu:636).
 constexpr int kRT = 2 * kWave;
 
-template <int D>
-__global__ __launch_bounds__(kRT) void rerank_kernel(RerankArgs a) {
+// SPEC mini-batches a step: the workgroup's SPEC groups of 128 threads
+// compute the exact distances of the next SPEC mini-batches at once (the row
+// loads of a small batch are latency-bound), then apply them one after
+// another in candidate order, each with the merge and the stop test of the
+// one-batch form; a stop discards the mini-batches after it, which count as
+// never visited.  SPEC = 1 is the one-batch form.
+template <int D, int SPEC>
+__global__ __launch_bounds__(kRT * SPEC) void rerank_kernel(RerankArgs a) {
+  constexpr int kT = kRT * SPEC;
   __shared__ float qs[D];
-  __shared__ uint64_t tk[2][256];  // running top-k keys (double-buffered), ascending
-  __shared__ uint64_t nk[kRT];     // the batch, sorted
+  __shared__ uint64_t tk[2][256];     // running top-k keys (double-buffered), ascending
+  __shared__ uint64_t nk[SPEC][kRT];  // each group's mini-batch, sorted
   __shared__ int s_chg, s_stable, s_fin;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int grp = tid / kRT, gt = tid % kRT, wave = gt >> 6;  // group, thread and wave within the group
   const int q = blockIdx.x, k = a.k, mb = a.mb, rm = a.rm;
-  for (int i = tid; i < D; i += kRT) qs[i] = a.queries[(size_t)q * D + i];
-  for (int i = tid; i < k; i += kRT) tk[0][i] = kPadKey;
+  for (int i = tid; i < D; i += kT) qs[i] = a.queries[(size_t)q * D + i];
+  for (int i = tid; i < k; i += kT) tk[0][i] = kPadKey;
   if (tid == 0) {
     s_stable = 0;
     s_fin = 0;
@@ -732,14 +740,14 @@ __global__ __launch_bounds__(kRT) void rerank_kernel(RerankArgs a) {
   const int32_t* cand = a.cand + (size_t)q * rm;
   __syncthreads();
   int cur = 0, seen = 0;
-  for (int off = 0; off < rm && off < total; off += mb) {
-    const int eff = min(mb, total - off);
-    seen += eff;
-    // exact distances, one candidate per thread
+  for (int off0 = 0; off0 < rm && off0 < total; off0 += SPEC * mb) {
+    // exact distances of this group's mini-batch, one candidate per thread
+    const int off = off0 + grp * mb;
+    const int eff = off < rm && off < total ? min(mb, total - off) : 0;
     float d = FLT_MAX;
     int id = kPadId;
-    if (tid < eff) {
-      const int vid = cand[off + tid];
+    if (gt < eff) {
+      const int vid = cand[off + gt];
       if (vid >= 0 && (long long)vid < a.n) {
         // The whole row is requested before the first multiply-add (the
         // scheduling barrier keeps the loads together): one memory round
@@ -766,14 +774,14 @@ __global__ __launch_bounds__(kRT) void rerank_kernel(RerankArgs a) {
         id = vid;
       }
     }
-    // sort the batch: each wave its 64 keys, then a merge by ranks into nk
+    // sort each mini-batch: each wave its 64 keys, then a merge by ranks
     uint64_t key = key_of(d, id);
     wave_sort64_k(key);
-    nk[tid] = key;
+    nk[grp][gt] = key;
     if (tid == 0) s_chg = 0;
     __syncthreads();
     {
-      const uint64_t* ok = nk + (wave ^ 1) * kWave;
+      const uint64_t* ok = nk[grp] + (wave ^ 1) * kWave;
       // rank in the other wave's sorted list: wave 0 counts strictly smaller
       // keys, wave 1 counts smaller-or-equal ones, so equal keys keep a fixed
       // order and every position is taken once.
@@ -784,55 +792,63 @@ __global__ __launch_bounds__(kRT) void rerank_kernel(RerankArgs a) {
         if (before) lo = mid + 1; else hi = mid;
       }
       __syncthreads();
-      nk[lane + lo] = key;
+      nk[grp][lane + lo] = key;
     }
     __syncthreads();
-    // merge the sorted batch (nk, kRT keys) with the top-k (tk[cur])
-    const uint64_t* ck = tk[cur];
-    uint64_t* xk = tk[cur ^ 1];
-    {
-      const uint64_t bk = nk[tid];
-      // old entries precede equal batch entries
-      int lo = 0, hi = k;
-      while (lo < hi) {
-        const int mid = (lo + hi) >> 1;
-        if (ck[mid] <= bk) lo = mid + 1; else hi = mid;
-      }
-      const int pos = tid + lo;
-      bool fresh = false;
-      if (pos < k) {
-        xk[pos] = bk;
-        const int bi = key_id(bk);
-        if (bi != kPadId) {
-          fresh = true;
-          for (int j = 0; j < k; ++j)
-            if (key_id(ck[j]) == bi) { fresh = false; break; }
+    // apply the mini-batches in order
+    for (int g = 0; g < SPEC; ++g) {
+      const int offg = off0 + g * mb;
+      if (offg >= rm || offg >= total) break;
+      seen += min(mb, total - offg);
+      // merge the sorted batch (nk[g], kRT keys) with the top-k (tk[cur])
+      const uint64_t* ck = tk[cur];
+      uint64_t* xk = tk[cur ^ 1];
+      if (tid < kRT) {
+        const uint64_t bk = nk[g][tid];
+        // old entries precede equal batch entries
+        int lo = 0, hi = k;
+        while (lo < hi) {
+          const int mid = (lo + hi) >> 1;
+          if (ck[mid] <= bk) lo = mid + 1; else hi = mid;
         }
+        const int pos = tid + lo;
+        bool fresh = false;
+        if (pos < k) {
+          xk[pos] = bk;
+          const int bi = key_id(bk);
+          if (bi != kPadId) {
+            fresh = true;
+            for (int j = 0; j < k; ++j)
+              if (key_id(ck[j]) == bi) { fresh = false; break; }
+          }
+        }
+        const uint64_t bm = __ballot(fresh);
+        if (lane == 0 && bm) atomicAdd(&s_chg, (int)__popcll(bm));
       }
-      const uint64_t bm = __ballot(fresh);
-      if (lane == 0 && bm) atomicAdd(&s_chg, (int)__popcll(bm));
-    }
-    for (int j = tid; j < k; j += kRT) {
-      const uint64_t okey = ck[j];
-      int lo = 0, hi = kRT;
-      while (lo < hi) {
-        const int mid = (lo + hi) >> 1;
-        if (nk[mid] < okey) lo = mid + 1; else hi = mid;
+      for (int j = tid; j < k; j += kT) {
+        const uint64_t okey = ck[j];
+        int lo = 0, hi = kRT;
+        while (lo < hi) {
+          const int mid = (lo + hi) >> 1;
+          if (nk[g][mid] < okey) lo = mid + 1; else hi = mid;
+        }
+        const int pos = j + lo;
+        if (pos < k) xk[pos] = okey;
       }
-      const int pos = j + lo;
-      if (pos < k) xk[pos] = okey;
+      __syncthreads();
+      if (tid == 0) {
+        const int st = ((float)s_chg / (float)k <= a.eps) ? s_stable + 1 : 0;
+        s_stable = st;
+        s_fin = st >= a.beta;
+        s_chg = 0;  // for the next mini-batch
+      }
+      cur ^= 1;
+      __syncthreads();
+      if (s_fin) break;
     }
-    __syncthreads();
-    if (tid == 0) {
-      const int st = ((float)s_chg / (float)k <= a.eps) ? s_stable + 1 : 0;
-      s_stable = st;
-      s_fin = st >= a.beta;
-    }
-    cur ^= 1;
-    __syncthreads();
     if (s_fin) break;
   }
-  for (int j = tid; j < k; j += kRT) {
+  for (int j = tid; j < k; j += kT) {
     const uint64_t kk = tk[cur][j];
     const bool pad = key_id(kk) == kPadId;
     a.out_ids[(size_t)q * k + j] = pad ? -1 : key_id(kk);
@@ -843,7 +859,12 @@ __global__ __launch_bounds__(kRT) void rerank_kernel(RerankArgs a) {
 
 template <int D>
 fgpu_status launch_rr(const RerankArgs& a, hipStream_t s) {
-  hipLaunchKernelGGL((rerank_kernel<D>), dim3((unsigned)a.nq), dim3(kRT), 0, s, a);
+  if (rerank_spec(a.nq) > 1) {
+    hipLaunchKernelGGL((rerank_kernel<D, 4>), dim3((unsigned)a.nq), dim3(kRT * 4), 0, s, a);
+    FGPU_HIP(hipGetLastError());
+    return FGPU_OK;
+  }
+  hipLaunchKernelGGL((rerank_kernel<D, 1>), dim3((unsigned)a.nq), dim3(kRT), 0, s, a);
   FGPU_HIP(hipGetLastError());
   return FGPU_OK;
 }
@@ -855,6 +876,24 @@ int two_phase_pool_cap(int p1, int limit_k, int rerank_m) {
   // to its limit_k best, so every list needs 2048 free slots above them.
   const int extra = limit_k > kWave ? p1 * limit_k + 2048 : (p1 * limit_k > 2048 ? p1 * limit_k : 2048);
   return (rerank_m + extra + 63) / 64 * 64;
+}
+
+// 0: automatic; 1: one mini-batch a step; anything else: four.
+static std::atomic<int> g_rr_spec{0};
+void set_rerank_spec_override(int v) { g_rr_spec.store(v < 0 ? 0 : v, std::memory_order_relaxed); }
+
+// Mini-batches the rerank computes a step: four while the batch leaves CUs
+// free (one 512-thread workgroup a query, latency-bound row loads), else one
+// (a large batch is bound by the row reads, and work past a stop is wasted).
+int rerank_spec(int nq) {
+  const int force = g_rr_spec.load(std::memory_order_relaxed);
+  if (force == 1) return 1;
+  if (force > 1) return 4;
+  int dev = 0, cus = 256;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+    cus = 256;
+  return nq <= cus ? 4 : 1;
 }
 
 // 0: automatic; 1: never split; s >= 2: split phase 1 s ways (at most p1).

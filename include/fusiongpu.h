@@ -109,6 +109,11 @@ void fgpu_debug_set_list_skip(int enabled);
  * fill the GPU; 1 = never; s >= 2 = s, at most p1; limit_k <= 64 only).
  * Results are the same whatever the split. */
 void fgpu_debug_set_two_phase_split(int split);
+/* Test hook: mini-batches every later rerank launch in the process computes
+ * at once before applying them in order (0 = automatic: 4 while the batch
+ * leaves CUs free, else 1; 1 = one; any other value = 4).  Results and visit
+ * counts are the same whatever the value. */
+void fgpu_debug_set_rerank_spec(int spec);
 /* Test hook (host only): the PQ training sample rows of fgpu_pq_train, the
  * first min(sample_size, n) entries of std::shuffle(0 .. n-1, mt19937(12345))
  * (pq_utils.h:91-97), into h_rows.  Returns their count, or -1 on a bad

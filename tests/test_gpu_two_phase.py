@@ -185,9 +185,12 @@ RERANK = [(96, 100, 128, 0.1, 2), (128, 10, 128, 0.1, 2), (96, 256, 32, -1.0, 2)
           (128, 5, 16, 1.0, 1)]
 
 
+@pytest.mark.parametrize("spec", [1, 4])
 @pytest.mark.parametrize("dim,k,mb,eps,beta", RERANK)
-def test_rerank_bit_exact(dim, k, mb, eps, beta):
-    _say(f"rerank dim={dim} k={k} mb={mb} eps={eps} beta={beta}")
+def test_rerank_bit_exact(dim, k, mb, eps, beta, spec):
+    """spec: mini-batches the kernel computes at once before applying them in
+    order (4 is the default for batches that leave CUs free)."""
+    _say(f"rerank dim={dim} k={k} mb={mb} eps={eps} beta={beta} spec={spec}")
     rng = np.random.default_rng(dim + k + mb)
     n, nq, rm = 20000, 200, 600
     base = rng.standard_normal((n, dim)).astype(np.float32)
@@ -203,8 +206,13 @@ def test_rerank_bit_exact(dim, k, mb, eps, beta):
     cand[4, 20] = cand[4, 2]             # a duplicate candidate
     counts = rng.integers(0, rm + 1, nq).astype(np.int32)
     counts[:6] = [rm, rm, 0, rm, rm, 1]
-    gid, gd, gvis = fg.rerank(torch.from_numpy(q).cuda(), torch.from_numpy(base).cuda(), torch.from_numpy(cand).cuda(),
-                              torch.from_numpy(counts).cuda(), k, mb, eps, beta)
+    fg.debug_set_rerank_spec(spec)
+    try:
+        gid, gd, gvis = fg.rerank(torch.from_numpy(q).cuda(), torch.from_numpy(base).cuda(),
+                                  torch.from_numpy(cand).cuda(), torch.from_numpy(counts).cuda(), k, mb, eps, beta)
+        torch.cuda.synchronize()
+    finally:
+        fg.debug_set_rerank_spec(0)
     oid, od, ovis = oracle.rerank(q, base, cand, counts, k, mb, eps, beta)
     gid, gd, gvis = _host(gid), _host(gd), _host(gvis)
     assert np.array_equal(gvis, ovis), np.nonzero(gvis != ovis)[0][:5]
