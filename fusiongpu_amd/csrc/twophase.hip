@@ -878,6 +878,18 @@ int two_phase_pool_cap(int p1, int limit_k, int rerank_m) {
   return (rerank_m + extra + 63) / 64 * 64;
 }
 
+// CUs of the current device (cached per device).
+static int cu_count() {
+  static std::atomic<int> cached[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  int v = cached[dev].load(std::memory_order_relaxed);
+  if (v > 0) return v;
+  if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0) v = 256;
+  cached[dev].store(v, std::memory_order_relaxed);
+  return v;
+}
+
 // 0: automatic; 1: one mini-batch a step; anything else: four.
 static std::atomic<int> g_rr_spec{0};
 void set_rerank_spec_override(int v) { g_rr_spec.store(v < 0 ? 0 : v, std::memory_order_relaxed); }
@@ -889,11 +901,7 @@ int rerank_spec(int nq) {
   const int force = g_rr_spec.load(std::memory_order_relaxed);
   if (force == 1) return 1;
   if (force > 1) return 4;
-  int dev = 0, cus = 256;
-  if (hipGetDevice(&dev) != hipSuccess ||
-      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
-    cus = 256;
-  return nq <= cus ? 4 : 1;
+  return nq <= cu_count() ? 4 : 1;
 }
 
 // 0: automatic; 1: never split; s >= 2: split phase 1 s ways (at most p1).
@@ -904,11 +912,7 @@ int two_phase_split(int nq, int p1, int limit_k) {
   const int force = g_tp_split.load(std::memory_order_relaxed);
   if (limit_k > kWave || p1 < 2 || nq <= 0 || force == 1) return 1;
   if (force > 1) return std::min(p1, force);
-  int dev = 0, cus = 256;
-  if (hipGetDevice(&dev) != hipSuccess ||
-      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
-    cus = 256;
-  const int slots = 2 * cus;  // two_phase_kernel workgroups resident at once
+  const int slots = 2 * cu_count();  // two_phase_kernel workgroups resident at once
   return nq >= slots ? 1 : std::min(p1, std::max(1, slots / nq));
 }
 
