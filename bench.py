@@ -14,9 +14,9 @@ kernel, the ADC scan: achieved = the code and id bytes of the lists it reads
 (its own load count), divided by its average duration from HIP events recorded
 on the stream it runs on; `traffic` is the copy-calibrated FETCH_SIZE +
 WRITE_SIZE from profiles/.  The scan's exact list bound skips most probed
-lists, so the work-equivalent figure (every probed list once) is
-reported apart as `effective`, and `no_skip` times the same kernel reading
-every probed list.  `measured_read_peak_gbs` is a streaming read of 4 GiB.
+lists, so the work-equivalent figure (the code bytes of every probed list, once
+per (query, list)) is reported apart as `effective`, and `no_skip` times the
+same kernel reading every probed list.  `measured_read_peak_gbs` is a streaming read of 4 GiB.
 `end_to_end` follows the reference's QPS definition (H2D + search + D2H).  The
 line also carries `graph_coarse`: the same coarse step done the reference's way
 (a graph walk over the centroids instead of the exact GEMM; not timed in
@@ -147,7 +147,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build targets one GPU; --gpus {args.gpus} is not supported "
-              "(the search shards by queries with no exchange; see DESIGN.md)", file=sys.stderr)
+              "(the search shards by queries, with no exchange between GPUs)", file=sys.stderr)
         sys.exit(2)
 
     import torch
@@ -200,7 +200,7 @@ def main():
     probes, pd = idx.coarse_search(dq, nprobe)
     cnt, _ = fg.probe_counts(idx, probes)
     n_probed_vecs = int(cnt.to(torch.int64).sum().item())
-    adc_bytes = n_probed_vecs * m  # SURVEY 8(d): code bytes of every probed list, once per (query, list)
+    adc_bytes = n_probed_vecs * m  # code bytes of every probed list, once per (query, list)
     pruned = int((probes == -1).sum().item())
     reps = max(args.steps, 5)
     coarse_ms = timed_ms(torch, stream, reps, lambda: idx.coarse_search(dq, nprobe, workspace=ws))
