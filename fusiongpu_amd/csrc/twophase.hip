@@ -628,7 +628,54 @@ void two_phase_kernel(TwoPhaseArgs a) {
   uint64_t* sk = reinterpret_cast<uint64_t*>(smem);
   int32_t* out_id = a.top_ids + (size_t)q * R;
   float* out_d = a.top_d + (size_t)q * R;
-  if (cnt <= kSortMax) {
+  if (cnt <= kSortMax / 2) {
+    // Runs of 64 keys sorted in registers (one wave a run, no barriers),
+    // then merged pairwise by ranks between two LDS buffers: a key's place
+    // in the merged pair is its index in its run plus the keys of the other
+    // run before it (on equal keys the left run goes first).  The last merge
+    // writes the output.  Padding keys (kNoKey) sort after every real key.
+    const int nk = (cnt + kWave - 1) / kWave * kWave;
+    uint64_t* src = sk;
+    uint64_t* dst = sk + kSortMax / 2;
+    for (int r = wave; r * kWave < nk; r += kTW) {
+      const int i = r * kWave + lane;
+      uint64_t key = i < cnt ? pool[i] : kNoKey;
+      wave_sort64_k(key);
+      src[i] = key;
+    }
+    __syncthreads();
+    for (int width = kWave;; width *= 2) {
+      const bool last = 2 * width >= nk;
+      for (int i = tid; i < nk; i += kTT) {
+        const int run = i / width, other = (run ^ 1) * width;
+        const uint64_t key = src[i];
+        int lo = 0, hi = other < nk ? min(width, nk - other) : 0;
+        if (run & 1) {  // right run: the left run's keys <= key come first
+          while (lo < hi) {
+            const int mid = (lo + hi) >> 1;
+            if (src[other + mid] <= key) lo = mid + 1; else hi = mid;
+          }
+        } else {  // left run: the right run's keys < key come first
+          while (lo < hi) {
+            const int mid = (lo + hi) >> 1;
+            if (src[other + mid] < key) lo = mid + 1; else hi = mid;
+          }
+        }
+        const int pos = (run & ~1) * width + (i - run * width) + lo;
+        if (!last) {
+          dst[pos] = key;
+        } else if (pos < cnt) {
+          out_id[pos] = (int32_t)(uint32_t)key;
+          out_d[pos] = __uint_as_float((uint32_t)(key >> 32));
+        }
+      }
+      if (last) break;
+      __syncthreads();
+      uint64_t* t = src;
+      src = dst;
+      dst = t;
+    }
+  } else if (cnt <= kSortMax) {
     int np2 = 1;
     while (np2 < cnt) np2 <<= 1;
     for (int i = tid; i < np2; i += kTT) sk[i] = i < cnt ? pool[i] : kNoKey;
