@@ -224,12 +224,10 @@ def main():
         f"of {int((probes != -1).sum().item())}; every probed list once would be {adc_bytes / 1e9:.2f} GB "
         f"({eff_gbs:.0f} GB/s work-equivalent)")
     # The same scan with the list bound off: it reads every probed list.
-    fg.debug_set_list_skip(False)
-    try:
-        nid, nd = idx.adc_search(dq, probes, k, probe_dists=pd)
-        ns_ms = timed_ms(torch, stream, reps, lambda: idx.adc_search(dq, probes, k, out=out, probe_dists=pd))
-    finally:
-        fg.debug_set_list_skip(True)
+    idx.set_option(fg.Index.OPT_LIST_SKIP, 0)
+    nid, nd = idx.adc_search(dq, probes, k, probe_dists=pd)
+    ns_ms = timed_ms(torch, stream, reps, lambda: idx.adc_search(dq, probes, k, out=out, probe_dists=pd))
+    idx.set_option(fg.Index.OPT_LIST_SKIP, 1)
     assert torch.equal(nid, sid) and torch.equal(nd, sd), "the scan without list skipping differs"
     ns_bytes = n_probed_vecs * (m + 4)
     ns_gbs = ns_bytes / (ns_ms * 1e-3) / 1e9
@@ -393,18 +391,14 @@ def run_batch128(args, torch, fg, dev):
     probes, _ = idx.coarse_search(dq, top_m)
     runs = {}
     for label, split, spec in (("small_batch_kernels", 0, 0), ("one_workgroup_a_query", 1, 1)):
-        fg.debug_set_two_phase_split(split)
-        fg.debug_set_rerank_spec(spec)
-        try:
-            tid, td, tc, _, _ = idx.two_phase_search(dq, probes, p1, limit_k, coeff, rm, workspace=tp_ws)
-            fid, fd, fvis = fg.rerank(dq, dx, tid, tc, k, mb, eps, beta)
-            t_coarse = timed_ms(torch, stream, 50, lambda: idx.coarse_search(dq, top_m))
-            t_tp = timed_ms(torch, stream, 50, lambda: idx.two_phase_search(dq, probes, p1, limit_k, coeff, rm,
-                                                                             workspace=tp_ws))
-            t_rr = timed_ms(torch, stream, 50, lambda: fg.rerank(dq, dx, tid, tc, k, mb, eps, beta))
-        finally:
-            fg.debug_set_two_phase_split(0)
-            fg.debug_set_rerank_spec(0)
+        idx.set_option(fg.Index.OPT_TWO_PHASE_SPLIT, split)
+        tid, td, tc, _, _ = idx.two_phase_search(dq, probes, p1, limit_k, coeff, rm, workspace=tp_ws)
+        fid, fd, fvis = fg.rerank(dq, dx, tid, tc, k, mb, eps, beta, spec=spec)
+        t_coarse = timed_ms(torch, stream, 50, lambda: idx.coarse_search(dq, top_m))
+        t_tp = timed_ms(torch, stream, 50, lambda: idx.two_phase_search(dq, probes, p1, limit_k, coeff, rm,
+                                                                         workspace=tp_ws))
+        t_rr = timed_ms(torch, stream, 50, lambda: fg.rerank(dq, dx, tid, tc, k, mb, eps, beta, spec=spec))
+        idx.set_option(fg.Index.OPT_TWO_PHASE_SPLIT, 0)
         runs[label] = {"coarse_ms": round(t_coarse, 4), "two_phase_ms": round(t_tp, 4), "rerank_ms": round(t_rr, 4),
                        "batch_ms": round(t_coarse + t_tp + t_rr, 4),
                        "qps": round(nb / (t_coarse + t_tp + t_rr) * 1e3, 1),

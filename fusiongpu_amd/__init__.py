@@ -33,7 +33,7 @@ __all__ = [
     "FgpuError", "lib", "lib_path", "Index", "gen_gmm", "l2_topk", "kmeans_fit", "kmeans_update",
     "fixed_shift", "pq_train", "pq_encode", "build_ivfpq", "write_ivf_data", "read_ivf_data",
     "write_fvecs", "read_fvecs", "read_ivecs", "probe_counts", "rerank", "knn_exact", "graph_search",
-    "debug_set_spin_limit", "debug_set_list_skip", "stream_read", "row_gather", "FAULT_ID", "prune_probes",
+    "stream_read", "row_gather", "FAULT_ID", "prune_probes",
 ]
 
 lib_path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib", "libfusiongpu.so")
@@ -52,10 +52,6 @@ _SIGS = {
     "fgpu_index_wrap": (_i32, [_i32, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _c.POINTER(_vp)]),
     "fgpu_index_faults": (_i32, [_vp, _vp, _c.POINTER(_c.c_ulonglong), _i32]),
     "fgpu_index_check": (_i32, [_vp, _vp]),
-    "fgpu_debug_set_spin_limit": (None, [_i32]),
-    "fgpu_debug_set_list_skip": (None, [_i32]),
-    "fgpu_debug_set_two_phase_split": (None, [_i32]),
-    "fgpu_debug_set_rerank_spec": (None, [_i32]),
     "fgpu_debug_pq_sample": (_i32, [_i64, _i32, _vp]),
     "fgpu_stream_read_grid": (_i32, []),
     "fgpu_stream_read": (_i32, [_vp, _sz, _vp, _vp]),
@@ -72,6 +68,9 @@ _SIGS = {
     "fgpu_adc_search_stats": (_i32, [_vp, _vp, _i32, _vp, _vp, _i32, _i32, _vp, _vp, _vp, _vp]),
     "fgpu_search_workspace_bytes": (_sz, [_i32, _i32, _i32]),
     "fgpu_search": (_i32, [_vp, _vp, _i32, _i32, _i32, _f32, _vp, _vp, _vp, _sz, _vp]),
+    "fgpu_search_screen_stats": (_i32, [_vp, _i32, _i32, _vp, _sz, _vp, _c.POINTER(_c.c_longlong), _i32]),
+    "fgpu_index_screen_ready": (_i32, [_vp]),
+    "fgpu_index_set_option": (_i32, [_vp, _i32, _i32]),
     "fgpu_search_noalloc_max_bytes": (_sz, []),
     "fgpu_search_noalloc_max_rows": (_i32, [_i32, _i32]),
     "fgpu_search_noalloc": (_i32, [_vp, _vp, _i32, _i32, _i32, _f32, _vp, _vp, _vp]),
@@ -81,6 +80,8 @@ _SIGS = {
     "fgpu_two_phase_search_stats": (_i32, [_vp, _vp, _i32, _vp, _i32, _i32, _i32, _f32, _i32, _vp, _vp, _vp, _vp,
                                            _vp, _sz, _vp]),
     "fgpu_rerank": (_i32, [_vp, _i32, _i32, _vp, _i64, _vp, _vp, _i32, _i32, _i32, _f32, _i32, _vp, _vp, _vp, _vp]),
+    "fgpu_rerank_spec": (_i32, [_vp, _i32, _i32, _vp, _i64, _vp, _vp, _i32, _i32, _i32, _f32, _i32, _vp, _vp, _vp,
+                                _i32, _vp]),
     "fgpu_search_rerank_workspace_bytes": (_sz, [_i32, _i32, _i32, _i32, _i32, _i32]),
     "fgpu_search_rerank": (_i32, [_vp, _vp, _i32, _i32, _f32, _i32, _i32, _f32, _i32, _vp, _i64, _i32, _i32, _f32,
                                   _i32, _vp, _vp, _vp, _sz, _vp]),
@@ -201,10 +202,24 @@ def _ws_check(ws, name="workspace"):
 
 
 # Implicit conversions the host mirror performs (the C ABI reads exactly these
-# element types): floating inputs become float32, integer ids int32 (an int64
-# probe id keeps its low 32 bits, so 0xFFFFFFFF stays the pruned sentinel).
+# element types): floating inputs become float32, integer ids int32.  An
+# integer value must fit in int32, except 0xFFFFFFFF (the pruned-probe
+# sentinel of a uint32 or int64 probe array), which becomes -1; any other
+# value outside int32 raises ValueError instead of wrapping.
 _FLOATS = ("float64", "float16", "bfloat16")
 _INTS = ("int64", "int16", "int8", "uint8", "uint16", "uint32")
+_INT32_MIN, _INT32_MAX, _PRUNED = -(1 << 31), (1 << 31) - 1, 0xFFFFFFFF
+
+
+def _check_int32_range(a, name):
+    torch = _torch()
+    if a.numel() == 0 or str(a.dtype).replace("torch.", "") in ("int16", "int8", "uint8", "uint16"):
+        return
+    v = a.to(torch.int64) if a.dtype == torch.uint32 else a
+    bad = ((v < _INT32_MIN) | (v > _INT32_MAX)) & (v != _PRUNED)
+    if bool(bad.any()):
+        first = int(v[bad].flatten()[0])
+        raise ValueError(f"{name}: value {first} does not fit in int32 (the C ABI reads int32 ids)")
 
 
 def _arg(a, dtype, name, shape=None):
@@ -221,6 +236,8 @@ def _arg(a, dtype, name, shape=None):
         ok = (dtype == torch.float32 and src in _FLOATS) or (dtype == torch.int32 and src in _INTS)
         if not ok:
             raise TypeError(f"{name}: dtype {src} cannot be read as {str(dtype).replace('torch.', '')}")
+        if dtype == torch.int32:
+            _check_int32_range(a, name)
     if shape is not None:
         if a.dim() != len(shape):
             raise ValueError(f"{name}: expected {len(shape)} dimensions, got shape {tuple(a.shape)}")
@@ -312,26 +329,6 @@ def read_ivecs(path) -> np.ndarray:
     out = np.empty((n.value, d.value), np.int32)
     _check(lib.fgpu_read_ivecs(str(path).encode(), _c.byref(d), _c.byref(n), _np_ptr(out)))
     return out
-
-
-def debug_set_spin_limit(polls: int):
-    """Test hook (fgpu_debug_set_spin_limit): polls before a scan wait gives up; 0 = automatic."""
-    lib.fgpu_debug_set_spin_limit(int(polls))
-
-
-def debug_set_list_skip(enabled: bool):
-    """Measurement hook (fgpu_debug_set_list_skip): False makes the plain scan read every probed list."""
-    lib.fgpu_debug_set_list_skip(int(bool(enabled)))
-
-
-def debug_set_two_phase_split(split: int):
-    """Test hook (fgpu_debug_set_two_phase_split): phase-1 workgroups a query (0 automatic, 1 never)."""
-    lib.fgpu_debug_set_two_phase_split(int(split))
-
-
-def debug_set_rerank_spec(spec: int):
-    """Test hook (fgpu_debug_set_rerank_spec): rerank mini-batches computed at once (0 automatic, 1, or 4)."""
-    lib.fgpu_debug_set_rerank_spec(int(spec))
 
 
 def debug_pq_sample(n: int, sample_size: int) -> np.ndarray:
@@ -607,7 +604,8 @@ class Index:
 
     def search(self, queries, nprobe: int, k: int, prune_ratio: float = 100.0, workspace=None, out=None,
                stream=None):
-        """coarse + LUT/ADC scan + top-k in one call (fgpu_search): (ids int32 [nq][k], dists float32 [nq][k])."""
+        """coarse + scan + top-k in one call (fgpu_search; the MFMA screen with an exact rescore where it
+        applies, the LUT kernels otherwise): (ids int32 [nq][k], dists float32 [nq][k])."""
         with _on(stream):
             q = self._queries(queries)
             nq = q.shape[0]
@@ -616,6 +614,34 @@ class Index:
             _check(lib.fgpu_search(self._h, _dev_ptr(q), nq, nprobe, k, prune_ratio, _dev_ptr(ids), _dev_ptr(d),
                                    _dev_ptr(ws), _ws_check(ws), _stream()))
         return ids, d
+
+    OPT_LIST_SKIP, OPT_SPIN_LIMIT, OPT_SCREEN, OPT_SCREEN_CLOCKS, OPT_TWO_PHASE_SPLIT = 1, 2, 3, 4, 5
+
+    def set_option(self, option: int, value: int):
+        """Per-index option (fgpu_index_set_option): OPT_LIST_SKIP (0 = the LUT scan reads every probed list),
+        OPT_SPIN_LIMIT (polls before a flow-kernel wait gives up, 0 = automatic), OPT_SCREEN (0 = fgpu_search
+        runs the LUT kernels), OPT_SCREEN_CLOCKS (1 = the screen records shader clocks),
+        OPT_TWO_PHASE_SPLIT (phase-1 workgroups a query: 0 automatic, 1 never, s >= 2).  Results never depend
+        on them; they change only this index's later calls."""
+        _check(lib.fgpu_index_set_option(self._h, int(option), int(value)))
+
+    @property
+    def screen_ready(self) -> bool:
+        """Whether the index carries the MFMA screen's arrays (fgpu_index_screen_ready)."""
+        return bool(lib.fgpu_index_screen_ready(self._h))
+
+    def search_screen_stats(self, nq: int, nprobe: int, workspace, stream=None) -> dict:
+        """Counters of the last search() on `workspace` that took the MFMA screen (fgpu_search_screen_stats;
+        waits for the stream)."""
+        st = (_c.c_longlong * 16)()
+        with _on(stream):
+            _check(lib.fgpu_search_screen_stats(self._h, nq, nprobe, _dev_ptr(workspace), _ws_check(workspace),
+                                                _stream(), st, 16))
+        keys = ("pairs_round1", "lists_round2", "pairs_round2", "candidates", "max_candidates",
+                "queries_to_lut_kernel", "queries_with_threshold", "_",
+                "clk1_pre", "clk1_setup", "clk1_tiles", "clk1_post", "clk2_pre", "clk2_setup", "clk2_tiles",
+                "clk2_post")
+        return {kk: int(st[i]) for i, kk in enumerate(keys)}
 
     def search_noalloc(self, queries, nprobe: int, k: int, prune_ratio: float = 100.0, out=None, stream=None):
         """fgpu_search without a workspace (fgpu_search_noalloc): its scratch is the library's fixed per-GPU
@@ -678,8 +704,9 @@ def probe_counts(index: Index, probe_ids, stream=None):
 
 
 def rerank(queries, base, top_ids, top_counts, k: int, mini_batch: int = 128, eps: float = 0.1, beta: int = 2,
-           stream=None):
-    """run_gpu_rerank: exact L2 over the ADC-ordered candidates with the early stop: (ids, dists, visited)."""
+           stream=None, spec: int = 0):
+    """run_gpu_rerank: exact L2 over the ADC-ordered candidates with the early stop: (ids, dists, visited).
+    spec: mini-batches computed at once (fgpu_rerank_spec: 0 automatic, 1, or 4); results do not depend on it."""
     torch = _torch()
     with _on(stream):
         q = _dev(queries, torch.float32, "queries", (None, None))
@@ -691,8 +718,9 @@ def rerank(queries, base, top_ids, top_counts, k: int, mini_batch: int = 128, ep
         ids = torch.empty((nq, k), dtype=torch.int32, device="cuda")
         d = torch.empty((nq, k), dtype=torch.float32, device="cuda")
         vis = torch.empty(nq, dtype=torch.int32, device="cuda")
-        _check(lib.fgpu_rerank(_dev_ptr(q), nq, dim, _dev_ptr(b), b.shape[0], _dev_ptr(t), _dev_ptr(c), rm, k,
-                               mini_batch, eps, beta, _dev_ptr(ids), _dev_ptr(d), _dev_ptr(vis), _stream()))
+        _check(lib.fgpu_rerank_spec(_dev_ptr(q), nq, dim, _dev_ptr(b), b.shape[0], _dev_ptr(t), _dev_ptr(c), rm,
+                                    k, mini_batch, eps, beta, _dev_ptr(ids), _dev_ptr(d), _dev_ptr(vis), int(spec),
+                                    _stream()))
     return ids, d, vis
 
 

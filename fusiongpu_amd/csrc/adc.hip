@@ -183,20 +183,18 @@ __device__ __forceinline__ void merge_and_write(uint64_t lk, const uint64_t* mk,
 constexpr int kNW = 8;
 constexpr int kNT = kNW * kWave;
 
+// One query of the generic kernel (the whole workgroup).
 template <int D, int M>
-__global__ __launch_bounds__(kNT) void adc_plain_kernel(AdcArgs a) {
+__device__ __forceinline__ void plain_query(const AdcArgs& a, int q, float* smem, unsigned long long& s_thr) {
   using C = Cfg<D, M>;
   constexpr int G = kNT / kPQK;  // threads sharing one codeword
   constexpr int MG = M / G;      // subspaces per thread
   static_assert(M % G == 0, "pq_m must split across the codeword threads");
-  __shared__ __align__(16) float smem[C::SMEM];
-  __shared__ unsigned long long s_thr;
   float* rbuf = smem + C::R_OFF;
   float* qs = smem + C::Q_OFF;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int kc = tid & (kPQK - 1), g = tid / kPQK;
   if (tid == 0) s_thr = kNoThr;
-  const int q = blockIdx.x;
   const int P = a.nprobe, k = a.k;
   const uint32_t NL = (uint32_t)a.nlist;
 
@@ -259,6 +257,28 @@ __global__ __launch_bounds__(kNT) void adc_plain_kernel(AdcArgs a) {
   mk[wave * kWave + lane] = lk;
   __syncthreads();
   if (wave == 0) merge_and_write(lk, mk, kNW, q, k, a);
+}
+
+template <int D, int M>
+__global__ __launch_bounds__(kNT) void adc_plain_kernel(AdcArgs a) {
+  __shared__ __align__(16) float smem[Cfg<D, M>::SMEM];
+  __shared__ unsigned long long s_thr;
+  plain_query<D, M>(a, (int)blockIdx.x, smem, s_thr);
+}
+
+// The generic kernel over the queries a.qlist[0 .. *a.qcount): the exact LUT
+// path for the queries the MFMA screen hands back.  A persistent grid; with
+// an empty list every workgroup ends at once.
+template <int D, int M>
+__global__ __launch_bounds__(kNT) void adc_plain_list_kernel(AdcArgs a) {
+  __shared__ __align__(16) float smem[Cfg<D, M>::SMEM];
+  __shared__ unsigned long long s_thr;
+  const int count = min(*a.qcount, a.nq);
+  for (int i = (int)blockIdx.x; i < count; i += (int)gridDim.x) {
+    const int q = a.qlist[i];
+    if (q >= 0 && q < a.nq) plain_query<D, M>(a, q, smem, s_thr);
+    __syncthreads();
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -799,6 +819,19 @@ fgpu_status launch_plain(const AdcArgs& a, hipStream_t s) {
   return FGPU_OK;
 }
 
+template <int D, int M>
+fgpu_status launch_plain_list(const AdcArgs& a, hipStream_t s) {
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+    cus = 256;
+  // Few workgroups: the list is usually empty, and then each ends at once.
+  const int grid = std::max(1, std::min(a.nq, cus / 4));
+  hipLaunchKernelGGL((adc_plain_list_kernel<D, M>), dim3((unsigned)grid), dim3(kNT), 0, s, a);
+  FGPU_HIP(hipGetLastError());
+  return FGPU_OK;
+}
+
 }  // namespace
 
 long long flow_spin_limit(int nprobe, int max_list_len) {
@@ -832,6 +865,18 @@ fgpu_status launch_adc_plain(int dim, int m, const AdcArgs& a, hipStream_t s) {
   if (dim == 96 && m == 48) return launch_plain<96, 48>(a, s);
   if (dim == 96 && m == 32) return launch_flow<96, 32>(a, s);
   if (dim == 96 && m == 16) return launch_flow<96, 16>(a, s);
+  return set_error(FGPU_ERR_UNSUPPORTED, "adc: unsupported (dim, pq_m)");
+}
+
+fgpu_status launch_adc_plain_list(int dim, int m, const AdcArgs& a, hipStream_t s) {
+  FGPU_CHECK(a.k >= 1 && a.k <= 64 && a.qlist && a.qcount, FGPU_ERR_ARG, "adc: bad query list launch");
+  if (a.nq <= 0) return FGPU_OK;
+  if (dim == 128 && m == 32) return launch_plain_list<128, 32>(a, s);
+  if (dim == 128 && m == 16) return launch_plain_list<128, 16>(a, s);
+  if (dim == 128 && m == 64) return launch_plain_list<128, 64>(a, s);
+  if (dim == 96 && m == 48) return launch_plain_list<96, 48>(a, s);
+  if (dim == 96 && m == 32) return launch_plain_list<96, 32>(a, s);
+  if (dim == 96 && m == 16) return launch_plain_list<96, 16>(a, s);
   return set_error(FGPU_ERR_UNSUPPORTED, "adc: unsupported (dim, pq_m)");
 }
 

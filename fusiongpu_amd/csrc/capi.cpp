@@ -28,6 +28,17 @@ struct fgpu_index {
   float* d_rmax = nullptr;       // [nlist] decoded-residual radius per list
   unsigned long long* d_faults = nullptr;  // [1] bounded-wait give-ups of the flow scan
   bool borrowed = false;  // the A1 arrays belong to the caller (fgpu_index_wrap)
+  // The MFMA screen of the plain search (screen.hip): bf16 codebook and the
+  // per-vector extra blocks, built at creation when the geometry allows it.
+  uint16_t* d_cb16 = nullptr;
+  uint4* d_vext = nullptr;
+  bool screen_ok = false;
+  // Per-index options (fgpu_index_set_option).
+  int opt_list_skip = 1;
+  int opt_spin_limit = 0;
+  int opt_screen = 1;
+  int opt_screen_clocks = 0;
+  int opt_two_phase_split = 0;
 };
 
 namespace fgpu {
@@ -65,7 +76,8 @@ void free_index(fgpu_index* ix) {
     for (void* p : {(void*)ix->d_codebook, (void*)ix->d_offsets, (void*)ix->d_codes, (void*)ix->d_ids,
                     (void*)ix->d_centroids})
       if (p) (void)hipFree(p);
-  for (void* p : {(void*)ix->d_cnorm, (void*)ix->d_cnorm_max, (void*)ix->d_rmax, (void*)ix->d_faults})
+  for (void* p : {(void*)ix->d_cnorm, (void*)ix->d_cnorm_max, (void*)ix->d_rmax, (void*)ix->d_faults,
+                  (void*)ix->d_cb16, (void*)ix->d_vext})
     if (p) (void)hipFree(p);
   delete ix;
 }
@@ -85,15 +97,38 @@ fgpu_status finish_index(fgpu_index* ix, hipStream_t s) {
   FGPU_TRY(launch_max_reduce(ix->d_cnorm, ix->nlist, ix->d_cnorm_max, s));
   FGPU_TRY(launch_list_radius(ix->d_codebook, ix->m, ix->dim / ix->m, ix->d_codes, ix->d_offsets, ix->nlist, ix->d_rmax,
                               s));
+  // The screen's arrays: only for its geometries, 16-byte aligned arrays,
+  // lists below 2^24 vectors, and (checked below) decoded norms below 2^40.
+  auto al16 = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
+  unsigned int* xmax = nullptr;
+  if (screen_supported(ix->dim, ix->m) && ix->max_list_len < (1 << 24) && al16(ix->d_codebook) &&
+      al16(ix->d_centroids) && al16(ix->d_codes)) {
+    if (alloc((void**)&ix->d_cb16, (size_t)ix->dim * kPQK * sizeof(uint16_t)) &&
+        alloc((void**)&ix->d_vext, sizeof(uint4) * (size_t)std::max<int64_t>(ix->total, 1)) &&
+        alloc((void**)&xmax, 256)) {
+      FGPU_TRY(launch_screen_prep(ix->d_codebook, ix->m, ix->dim / ix->m, ix->d_codes, ix->total, ix->d_cb16,
+                                  ix->d_vext, xmax, s));
+    } else {
+      (void)hipGetLastError();  // no room for the screen: the plain search keeps the LUT kernels
+    }
+  }
   FGPU_HIP(hipStreamSynchronize(s));
+  if (xmax) {
+    unsigned int bits = 0;
+    const bool got = hipMemcpy(&bits, xmax, sizeof(bits), hipMemcpyDeviceToHost) == hipSuccess;
+    (void)hipFree(xmax);
+    float xm = 0.0f;
+    std::memcpy(&xm, &bits, sizeof(xm));
+    ix->screen_ok = got && xm <= 0x1p40f;
+  }
+  if (!ix->screen_ok) {
+    for (void* p : {(void*)ix->d_cb16, (void*)ix->d_vext})
+      if (p) (void)hipFree(p);
+    ix->d_cb16 = nullptr;
+    ix->d_vext = nullptr;
+  }
   return FGPU_OK;
 }
-
-// Poll limit of the flow kernel's bounded waits set by fgpu_debug_set_spin_limit
-// (0 = derived per launch from nprobe and the longest list).
-std::atomic<int> g_spin_override{0};
-// fgpu_debug_set_list_skip: 0 turns the plain scan's list lower bound off.
-std::atomic<int> g_list_skip{1};
 
 AdcArgs adc_args(const fgpu_index* ix, const float* dq, int nq, const uint32_t* probes, const float* probe_dists,
                  int nprobe, int k, int32_t* out_ids, float* out_d) {
@@ -103,10 +138,43 @@ AdcArgs adc_args(const fgpu_index* ix, const float* dq, int nq, const uint32_t* 
   a.total = ix->total;
   a.faults = ix->d_faults;
   a.max_list_len = ix->max_list_len;
-  a.spin_limit = g_spin_override.load(std::memory_order_relaxed);
-  a.list_skip = g_list_skip.load(std::memory_order_relaxed);
+  a.spin_limit = ix->opt_spin_limit;
+  a.list_skip = ix->opt_list_skip;
   return a;
 }
+
+// The screen's workspace, carved from `base` (fgpu_search, after the probe
+// arrays).  The counters, per-list counts and per-query candidate counts are
+// one contiguous block that the first screen kernel zeroes.
+constexpr int kScreenCandCap = 512;  // candidates kept per query before it takes the LUT kernel
+struct ScreenWs {
+  int* zero = nullptr;  // [zero_words(nq, nlist)]
+  int* bucket = nullptr;
+  float* thr = nullptr;
+  uint2* cand = nullptr;
+  int* flist = nullptr;
+  int2* first = nullptr;
+  uint32_t* gminbuf = nullptr;
+  static size_t zero_words(int nq, int nlist) { return (size_t)kCtrCount + 2 * (size_t)nlist + (size_t)nq; }
+  static size_t gmin_words(int nq) { return (size_t)screen_gmin_words(nq); }
+  bool carve(void* base, size_t bytes, int nq, int nlist) {
+    Carve cv(base, bytes);
+    zero = cv.take<int>(zero_words(nq, nlist));
+    bucket = cv.take<int>((size_t)nlist * nq);
+    thr = cv.take<float>((size_t)nq);
+    cand = cv.take<uint2>((size_t)nq * kScreenCandCap);
+    flist = cv.take<int>((size_t)nq);
+    first = cv.take<int2>((size_t)nq);
+    gminbuf = cv.take<uint32_t>(gmin_words(nq));
+    return cv.ok();
+  }
+  static size_t bytes(int nq, int nlist) {
+    return carve_bytes<int>(zero_words(nq, nlist)) + carve_bytes<int>((size_t)nlist * nq) +
+           carve_bytes<float>((size_t)nq) + carve_bytes<uint2>((size_t)nq * kScreenCandCap) +
+           carve_bytes<int>((size_t)nq) + carve_bytes<int2>((size_t)nq) +
+           carve_bytes<uint32_t>(gmin_words(nq));
+  }
+};
 
 // The first k entries of what std::shuffle(iota(n), rng) leaves, drawing
 // exactly as std::shuffle does.  When rng's range is below n^2, libstdc++'s
@@ -384,11 +452,6 @@ fgpu_status fgpu_index_check(const fgpu_index* ix, void* stream) {
   return FGPU_OK;
 }
 
-void fgpu_debug_set_spin_limit(int polls) { g_spin_override.store(polls > 0 ? polls : 0); }
-
-void fgpu_debug_set_list_skip(int enabled) { g_list_skip.store(enabled ? 1 : 0); }
-void fgpu_debug_set_two_phase_split(int split) { set_two_phase_split_override(split); }
-void fgpu_debug_set_rerank_spec(int spec) { set_rerank_spec_override(spec); }
 
 int fgpu_debug_pq_sample(int64_t n, int sample_size, int32_t* h_rows) {
   if (n < 1 || sample_size < 0 || !h_rows) return -1;
@@ -419,9 +482,23 @@ fgpu_status fgpu_row_gather(const void* d_rows, int64_t nrows, int row_bytes, co
   return launch_row_gather(d_rows, nrows, row_bytes, d_idx, n, d_sink, fgpu_stream_read_grid(), as_stream(stream));
 }
 
-size_t fgpu_search_workspace_bytes(int nq, int nlist, int nprobe) {
+}  // extern "C"
+
+namespace fgpu {
+size_t search_lut_workspace_bytes(int nq, int nlist, int nprobe) {
   return carve_bytes<uint32_t>((size_t)nq * nprobe) + carve_bytes<float>((size_t)nq * nprobe) +
          carve_bytes<int>(1) + fgpu_coarse_workspace_bytes(nq, nlist);
+}
+}  // namespace fgpu
+
+extern "C" {
+
+size_t fgpu_search_workspace_bytes(int nq, int nlist, int nprobe) {
+  // The coarse step's estimate tile and the screen's buffers are never live
+  // at once, so they share one region (no screen beyond kScreenMaxLists lists).
+  const size_t screen = nlist <= kScreenMaxLists ? ScreenWs::bytes(nq, nlist) : 0;
+  return carve_bytes<uint32_t>((size_t)nq * nprobe) + carve_bytes<float>((size_t)nq * nprobe) +
+         carve_bytes<int>(1) + std::max(fgpu_coarse_workspace_bytes(nq, nlist), screen);
 }
 
 fgpu_status fgpu_search(const fgpu_index* ix, const float* dq, int nq, int nprobe, int k, float prune_ratio,
@@ -434,16 +511,101 @@ fgpu_status fgpu_search(const fgpu_index* ix, const float* dq, int nq, int nprob
   FGPU_CHECK(cv.ok(), FGPU_ERR_WORKSPACE, "search: workspace too small");
   FGPU_CHECK(nq >= 0 && k >= 1, FGPU_ERR_ARG, "search: bad sizes");
   FGPU_CHECK(adc_supported(ix->dim, ix->m), FGPU_ERR_UNSUPPORTED, "search: no kernel for this (dim, pq_m)");
+  void* rest = cv.base + cv.used;
+  const size_t rest_bytes = ws_bytes - cv.used;
+  // The MFMA screen + exact rescore (screen.hip), when the index has its
+  // arrays, k <= 32 and the workspace holds its buffers; the queries it hands
+  // back go through the generic LUT kernel.  Otherwise the LUT flow kernel.
+  ScreenWs sw;
+  if (ix->screen_ok && ix->opt_screen && k <= 32 && nq > 0 && ((uintptr_t)dq & 15) == 0 &&
+      ix->nlist <= kScreenMaxLists && sw.carve(rest, rest_bytes, nq, ix->nlist)) {
+    FGPU_TRY(coarse_search(ix, dq, nq, nprobe, prune_ratio, pid, pd, rest, rest_bytes, stream, nullptr, 0));
+    hipStream_t s = as_stream(stream);
+    ScreenArgs sa{dq, ix->d_centroids, ix->d_offsets, ix->d_codes, ix->d_ids, ix->d_codebook, ix->d_cb16,
+                  ix->d_vext, ix->d_rmax, pid, pd, nq, nprobe, k, ix->nlist};
+    sa.ctr = sw.zero;
+    sa.cnt1 = sw.zero + kCtrCount;
+    sa.cnt2 = sa.cnt1 + ix->nlist;
+    sa.cand_cnt = sa.cnt2 + ix->nlist;
+    sa.first = sw.first;
+    sa.gminbuf = sw.gminbuf;
+    sa.bucket = sw.bucket;
+    sa.thr = sw.thr;
+    sa.cand = sw.cand;
+    sa.cand_cap = kScreenCandCap;
+    sa.flist = sw.flist;
+    sa.out_ids = d_out_ids;
+    sa.out_d = d_out_dists;
+    if (ix->opt_screen_clocks) sa.stats = reinterpret_cast<unsigned long long*>(sw.zero + 16);
+    FGPU_TRY(launch_screen(ix->dim, ix->m, sa, s));
+    AdcArgs a = adc_args(ix, dq, nq, pid, pd, nprobe, k, d_out_ids, d_out_dists);
+    a.qlist = sw.flist;
+    a.qcount = sw.zero + kCtrFlag;
+    return launch_adc_plain_list(ix->dim, ix->m, a, s);
+  }
   // The scan claims queries from a counter that starts at its grid size; the
   // coarse step's select stores that value on the way.
   const int grid = flow_grid(ix->dim, ix->m, nq, nprobe);
-  FGPU_TRY(coarse_search(ix, dq, nq, nprobe, prune_ratio, pid, pd, cv.base + cv.used, ws_bytes - cv.used, stream,
+  FGPU_TRY(coarse_search(ix, dq, nq, nprobe, prune_ratio, pid, pd, rest, rest_bytes, stream,
                          grid > 0 ? qctr : nullptr, grid));
   AdcArgs a = adc_args(ix, dq, nq, pid, pd, nprobe, k, d_out_ids, d_out_dists);
   a.qctr = qctr;
   a.qctr_preset = grid;
   return launch_adc_plain(ix->dim, ix->m, a, as_stream(stream));
 }
+
+fgpu_status fgpu_search_screen_stats(const fgpu_index* ix, int nq, int nprobe, const void* ws, size_t ws_bytes,
+                                     void* stream, long long* h_stats, int n_stats) {
+  FGPU_CHECK(ix && ws && h_stats && n_stats >= 0 && nq >= 0 && nprobe >= 1, FGPU_ERR_ARG,
+             "search_screen_stats: bad argument");
+  Carve cv(const_cast<void*>(ws), ws_bytes);
+  cv.take<uint32_t>((size_t)nq * nprobe);
+  cv.take<float>((size_t)nq * nprobe);
+  cv.take<int>(1);
+  FGPU_CHECK(cv.ok(), FGPU_ERR_WORKSPACE, "search_screen_stats: workspace too small");
+  ScreenWs sw;
+  FGPU_CHECK(sw.carve(cv.base + cv.used, ws_bytes - cv.used, nq, ix->nlist), FGPU_ERR_WORKSPACE,
+             "search_screen_stats: workspace too small for the screen");
+  hipStream_t s = as_stream(stream);
+  std::vector<int> z(ScreenWs::zero_words(nq, ix->nlist));
+  std::vector<float> thr((size_t)nq);
+  FGPU_HIP(hipMemcpyAsync(z.data(), sw.zero, sizeof(int) * z.size(), hipMemcpyDeviceToHost, s));
+  FGPU_HIP(hipMemcpyAsync(thr.data(), sw.thr, sizeof(float) * thr.size(), hipMemcpyDeviceToHost, s));
+  FGPU_HIP(hipStreamSynchronize(s));
+  long long st[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  for (int l = 0; l < ix->nlist; ++l) {
+    st[0] += z[kCtrCount + l];
+    st[2] += z[kCtrCount + ix->nlist + l];
+    st[1] += z[kCtrCount + ix->nlist + l] > 0 ? 1 : 0;
+  }
+  for (int q = 0; q < nq; ++q) {
+    const int c = z[kCtrCount + 2 * ix->nlist + q];
+    st[3] += std::min(c, kScreenCandCap);
+    st[4] = std::max<long long>(st[4], c);
+    st[6] += std::isfinite(thr[q]) ? 1 : 0;
+  }
+  st[5] = z[kCtrFlag];
+  for (int i = 0; i < n_stats && i < 8; ++i) h_stats[i] = st[i];
+  // With FGPU_OPT_SCREEN_CLOCKS: the screen kernels' clock and tile counts.
+  unsigned long long ck[8];
+  std::memcpy(ck, z.data() + 16, sizeof(ck));
+  for (int i = 0; i < 8 && 8 + i < n_stats; ++i) h_stats[8 + i] = (long long)ck[i];
+  return FGPU_OK;
+}
+
+fgpu_status fgpu_index_set_option(fgpu_index* ix, int option, int value) {
+  FGPU_CHECK(ix, FGPU_ERR_ARG, "index_set_option: null index");
+  switch (option) {
+    case FGPU_OPT_LIST_SKIP: ix->opt_list_skip = value ? 1 : 0; return FGPU_OK;
+    case FGPU_OPT_SPIN_LIMIT: ix->opt_spin_limit = value > 0 ? value : 0; return FGPU_OK;
+    case FGPU_OPT_SCREEN: ix->opt_screen = value ? 1 : 0; return FGPU_OK;
+    case FGPU_OPT_SCREEN_CLOCKS: ix->opt_screen_clocks = value ? 1 : 0; return FGPU_OK;
+    case FGPU_OPT_TWO_PHASE_SPLIT: ix->opt_two_phase_split = value > 0 ? value : 0; return FGPU_OK;
+    default: return set_error(FGPU_ERR_ARG, "index_set_option: unknown option " + std::to_string(option));
+  }
+}
+
+int fgpu_index_screen_ready(const fgpu_index* ix) { return ix && ix->screen_ok ? 1 : 0; }
 
 // ---------------------------------------------------------------------------
 size_t fgpu_two_phase_workspace_bytes(int nq, int nprobe, int p1_lists, int limit_k, int rerank_m) {
@@ -487,7 +649,7 @@ fgpu_status two_phase(const fgpu_index* ix, const float* dq, int nq, const uint3
                    d_stats};
     // A batch too small to fill the GPU (two workgroups a CU) spreads each
     // query's phase-1 lists over several workgroups.
-    a.split = two_phase_split(nb, p1, limit_k);
+    a.split = two_phase_split(nb, p1, limit_k, ix->opt_two_phase_split);
     a.cut_ws = cut_ws;
     FGPU_TRY(launch_two_phase(ix->dim, ix->m, a, as_stream(stream)));
   }
@@ -518,6 +680,14 @@ fgpu_status fgpu_two_phase_search_stats(const fgpu_index* ix, const float* dq, i
 fgpu_status fgpu_rerank(const float* dq, int nq, int dim, const float* d_base, int64_t n, const int32_t* d_top_ids,
                         const int32_t* d_top_counts, int rerank_m, int k, int mini_batch, float eps, int beta,
                         int32_t* d_final_ids, float* d_final_dists, int32_t* d_visited, void* stream) {
+  return fgpu_rerank_spec(dq, nq, dim, d_base, n, d_top_ids, d_top_counts, rerank_m, k, mini_batch, eps, beta,
+                          d_final_ids, d_final_dists, d_visited, 0, stream);
+}
+
+fgpu_status fgpu_rerank_spec(const float* dq, int nq, int dim, const float* d_base, int64_t n,
+                             const int32_t* d_top_ids, const int32_t* d_top_counts, int rerank_m, int k,
+                             int mini_batch, float eps, int beta, int32_t* d_final_ids, float* d_final_dists,
+                             int32_t* d_visited, int spec, void* stream) {
   FGPU_CHECK(dq && d_base && d_top_ids && d_top_counts && d_final_ids && d_final_dists, FGPU_ERR_ARG,
              "rerank: null argument");
   FGPU_CHECK(nq >= 0 && n >= 0 && rerank_m >= 1 && k >= 1 && mini_batch >= 1, FGPU_ERR_ARG, "rerank: bad sizes");
@@ -525,6 +695,7 @@ fgpu_status fgpu_rerank(const float* dq, int nq, int dim, const float* d_base, i
              "rerank: base vectors and queries must be 16-byte aligned");
   RerankArgs a{dq, d_base, (long long)n, d_top_ids, d_top_counts, nq, rerank_m, k, mini_batch, eps, beta,
                d_final_ids, d_final_dists, d_visited};
+  a.spec = spec < 0 ? 0 : spec;
   return launch_rerank(dim, a, as_stream(stream));
 }
 

@@ -87,6 +87,10 @@ struct AdcArgs {
   // in *qctr (the select's side write).  The launch skips its own reset when
   // it equals the grid it launches (flow_grid).
   int qctr_preset = 0;
+  // launch_adc_plain_list only: the queries to search, qlist[0 .. *qcount)
+  // (device memory; the count is read on the device).
+  const int* qlist = nullptr;
+  const int* qcount = nullptr;
 };
 // Id written to every slot of a query whose result a bounded-wait give-up may
 // have touched (the reference's padding id is -1; it never writes -2).
@@ -100,10 +104,67 @@ bool adc_supported(int dim, int m);
 fgpu_status launch_list_radius(const float* codebook, int m, int sub, const uint8_t* codes, const int32_t* offsets,
                                int nlist, float* rmax, hipStream_t s);
 fgpu_status launch_adc_plain(int dim, int m, const AdcArgs& a, hipStream_t s);
+// The generic (one workgroup a query, every probed list) kernel over the
+// queries a.qlist[0 .. *a.qcount), on a persistent grid.
+fgpu_status launch_adc_plain_list(int dim, int m, const AdcArgs& a, hipStream_t s);
 // The grid of the flow-kernel launch launch_adc_plain makes for these sizes
 // (the start value of its query counter), or 0 if that call takes another
 // kernel.
 int flow_grid(int dim, int m, int nq, int nprobe);
+
+// ---- capi.cpp -----------------------------------------------------------------------
+// Workspace of fgpu_search on the LUT kernels alone (probe arrays + the coarse
+// step); fgpu_search_workspace_bytes adds room for the MFMA screen.
+size_t search_lut_workspace_bytes(int nq, int nlist, int nprobe);
+
+// ---- screen.hip -----------------------------------------------------------------
+// Counters at the head of the screen's zeroed region.
+constexpr int kCtrFlag = 0, kCtrCount = 32;
+// Lists an index may have for the screen (its work-item scan lives in LDS).
+constexpr int kScreenMaxLists = 8192;
+struct ScreenArgs {
+  const float* queries;     // [nq][dim]
+  const float* centroids;   // [nlist][dim]
+  const int32_t* offsets;   // [nlist+1]
+  const uint8_t* codes;     // [total][m]
+  const int32_t* vec_ids;   // [total]
+  const float* codebook;    // [m][256][dim/m] fp32
+  const uint16_t* cb16;     // [m][256][dim/m] bf16 (nearest)
+  const uint4* vext;        // [total] per-vector extra block (screen_prep)
+  const float* rmax;        // [nlist]
+  const uint32_t* probes;   // [nq][nprobe]; ids >= nlist are skipped
+  const float* probe_dists; // [nq][nprobe] the coarse step's squared distances
+  int nq, nprobe, k, nlist;
+  // One region, zeroed at the start of a launch: ctr[kCtrCount], cnt1[nlist],
+  // cnt2[nlist], cand_cnt[nq] (in this order, contiguous).
+  int* ctr;
+  int* cnt1;
+  int* cnt2;
+  int* cand_cnt;
+  int* bucket;              // [nlist][nq] queries of each list's pairs
+  int2* first;              // [nq] round 1: (list, bucket position) of the query's pair, or (-1, -1)
+  uint32_t* gminbuf;        // [nq][kMaxChunks][32] round 1: per query, first-list chunk and group, min U bits
+  float* thr;               // [nq] T(q)
+  uint2* cand;              // [nq][cand_cap] (vector position, list)
+  int cand_cap;
+  int* flist;               // [nq] queries handed to the LUT kernel
+  int32_t* out_ids;         // [nq][k]
+  float* out_d;             // [nq][k]
+  // Optional instrumentation (nullptr = off), summed over the waves: shader
+  // clocks [0] before the first item, [1] in item set-up, [2] in the tile
+  // loops, [3] after the tiles; [0..3] round 1, [4..7] round 2.
+  unsigned long long* stats = nullptr;
+};
+bool screen_supported(int dim, int m);
+// Words of ScreenArgs::gminbuf for nq queries.
+int64_t screen_gmin_words(int nq);
+// The bf16 codebook and the per-vector extra blocks of an index; *xmax_bits
+// gets the largest per-vector norm bound (float bits).
+fgpu_status launch_screen_prep(const float* codebook, int m, int sub, const uint8_t* codes, int64_t total,
+                               uint16_t* cb16, uint4* vext, unsigned int* xmax_bits, hipStream_t s);
+// Threshold, screen and rescore; the queries it cannot answer are listed in
+// flist[0 .. ctr[kCtrFlag]) for launch_adc_plain_list.
+fgpu_status launch_screen(int dim, int m, const ScreenArgs& a, hipStream_t s);
 
 // ---- twophase.hip --------------------------------------------------------------
 struct TwoPhaseArgs {
@@ -142,8 +203,8 @@ struct TwoPhaseArgs {
 int two_phase_pool_cap(int p1, int limit_k, int rerank_m);
 // Workgroups a query for phase 1 (TwoPhaseArgs::split) for a launch of nq
 // queries: 1 once nq fills every CU twice; a test override can force it.
-int two_phase_split(int nq, int p1, int limit_k);
-void set_two_phase_split_override(int v);
+// (force: 0 automatic, 1 never, s >= 2 s ways, at most p1.)
+int two_phase_split(int nq, int p1, int limit_k, int force = 0);
 fgpu_status launch_two_phase(int dim, int m, const TwoPhaseArgs& a, hipStream_t s);
 
 struct RerankArgs {
@@ -158,12 +219,13 @@ struct RerankArgs {
   int32_t* out_ids;         // [nq][k]
   float* out_d;             // [nq][k]
   int32_t* visited;         // [nq] or nullptr
+  int spec = 0;             // mini-batches computed a step: 0 automatic, 1, or 4 (any other value)
 };
 fgpu_status launch_rerank(int dim, const RerankArgs& a, hipStream_t s);
 // Mini-batches the rerank kernel computes at once for nq queries (1 or 4);
 // a test override can force either.
-int rerank_spec(int nq);
-void set_rerank_spec_override(int v);
+// (force: 0 automatic, 1 one, anything else four.)
+int rerank_spec(int nq, int force = 0);
 
 // ---- graph.hip -----------------------------------------------------------------
 struct GraphArgs {

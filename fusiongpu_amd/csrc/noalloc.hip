@@ -56,16 +56,23 @@ size_t fgpu_search_noalloc_max_bytes(void) { return kScratchBytes; }
 
 int fgpu_search_noalloc_max_rows(int nlist, int nprobe) {
   if (nlist < 1 || nprobe < 1) return 0;
-  // Largest multiple of 64 query rows whose fgpu_search workspace fits.
-  int lo = 0, hi = 1 << 20;
-  while (lo < hi) {
-    const int mid = (lo + hi + 1) / 2;
-    if (fgpu_search_workspace_bytes(mid * 64, nlist, nprobe) <= kScratchBytes)
-      lo = mid;
-    else
-      hi = mid - 1;
-  }
-  return lo * 64;
+  // Largest multiple of 64 query rows whose whole fgpu_search workspace fits
+  // (the screen path included); when not even 64 rows of that fit, the
+  // largest whose LUT-path workspace fits (fgpu_search then takes the LUT
+  // flow kernel, whose results are the same).
+  auto max_rows = [&](size_t (*need)(int, int, int)) {
+    int lo = 0, hi = 1 << 20;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) / 2;
+      if (need(mid * 64, nlist, nprobe) <= kScratchBytes)
+        lo = mid;
+      else
+        hi = mid - 1;
+    }
+    return lo * 64;
+  };
+  const int full = max_rows(fgpu_search_workspace_bytes);
+  return full >= 64 ? full : max_rows(search_lut_workspace_bytes);
 }
 
 fgpu_status fgpu_search_noalloc(const fgpu_index* ix, const float* dq, int nq, int nprobe, int k, float prune_ratio,
@@ -77,7 +84,7 @@ fgpu_status fgpu_search_noalloc(const fgpu_index* ix, const float* dq, int nq, i
   const int rows = fgpu_search_noalloc_max_rows(info.nlist, nprobe);
   FGPU_CHECK(rows >= 64, FGPU_ERR_WORKSPACE,
              "search_noalloc: 64 query rows of scratch for nlist " + std::to_string(info.nlist) + ", nprobe " +
-                 std::to_string(nprobe) + " need " + std::to_string(fgpu_search_workspace_bytes(64, info.nlist, nprobe)) +
+                 std::to_string(nprobe) + " need " + std::to_string(search_lut_workspace_bytes(64, info.nlist, nprobe)) +
                  " bytes, more than the " + std::to_string(kScratchBytes) + "-byte scratch array");
   if (nq == 0) return FGPU_OK;
   void* ws = nullptr;

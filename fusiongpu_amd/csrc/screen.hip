@@ -1,0 +1,786 @@
+// screen.hip -- the plain IVF-PQ search (A4, A5, A6 and A10 with p1 = nprobe,
+// limit_k = rerank_m = k) as an MFMA screen followed by an exact rescore.
+//
+// What is computed is unchanged.  The answer is the k smallest (ADC distance,
+// vector id) keys over the probed lists, where each ADC distance is the
+// sequential fp32 sum over ascending m of LUT[m][code_m] (gpu_global.cu:196-253)
+// and each LUT entry is the reference's fused chain over the residual
+// r = fl(q - c) minus the codeword (gpu_global.cu:79-166).  The reference
+// builds that LUT for every (query, probed list), scans every probed vector
+// with it (gpu_global.cu:321-390) and sorts (gpu_global.cu:852-867).
+//
+// Here no LUT is built.  Instead:
+//   1. Threshold.  For every query, its first usable probed list is screened
+//      with upper bounds U(v) >= d(q, v) of the exact distances.  The list's
+//      vectors fall into 32 groups by position; the k-th smallest of the 32
+//      group minima of U is T(q): k distinct vectors have d <= T(q), so the
+//      final k-th distance is <= T(q).
+//   2. Screen.  Every probed list whose lower bound (list_lower_bound, the
+//      flow kernel's rule) is <= T(q) is screened with lower bounds
+//      L(v) <= d(q, v) in the form V(v) = L(v) - T(q) <= 0: a vector with
+//      d <= T(q) always passes, so every member of the top-k is a candidate.
+//   3. Rescore.  The candidates' exact distances are recomputed with the
+//      reference's direct form (gpu_global.cu:259-319: the same fused chain per
+//      subspace and the same sequential sum, so each equals the LUT value bit
+//      for bit) and the k smallest keys are kept.  Queries without a threshold
+//      (a first list shorter than k, out-of-range values) or with more
+//      candidates than the buffer holds go to the LUT kernel instead.
+//
+// The bounds.  With p the decoded residual of v (codebook rows, fp32) and
+// D* = ||r - p||^2 exactly, d = D* (1 +- gamma_c), gamma_c = gamma(s + M + 1)
+// < 2^-16 (non-negative terms, s + M + 1 roundings; gamma(n) = n u/(1 - n u),
+// u = 2^-24).  The screen forms
+//     -2 <bf16(r), bf16(p)>  +  per-query and per-vector constants
+// on v_mfma_f32_32x32x16_bf16: the main K range holds -2 bf16(r) (an exact
+// scaling) against bf16(p); one extra K block of 16 carries the constants, each
+// split into three bf16 values with directed rounding, so the MFMA sum is the
+// whole test value.  Round-to-nearest bf16 is within 2^-8 relative (plus
+// 2^-134 absolute below the normal range), so
+//     |<bf16 r, bf16 p> - <r, p>| <= (2^-7 + 2^-16) R X + 2^-129 (R + X) + 2^-260
+// with R >= ||r||, X >= ||p||.  The MFMA adds at most 144 fp32 roundings over
+// terms whose magnitudes sum to <= 1.03 (T + (R + X)^2), and may flush terms
+// below 2^-126 (< 2^-118 in all).  With a = 2^-6 + 2^-12, g = 2^-13 and
+// t = 1 + 2^-12 the two tests are
+//     V = ||p||^2 - gX^2 - 2^-110 X  - 2<r',p'> - a R X
+//         - (t T - nr2 + g R^2 + 2^-110 (1 + R))          <= 0,
+//     U = ||p||^2 + gX^2 + 2^-110 X  - 2<r',p'> + a R X
+//         + (t nr2 + g R^2 + 2^-110 (1 + R))              >= D*,
+// nr2 the fp32 sum of squares of r (within gamma(129) of ||r||^2).  Collecting
+// terms, every coefficient of V - (d - T)-style slack is negative:
+// T (1/(1-gamma_c) - t + 1.8e-5) < 0, R X (2^-6 + 2^-15 + 3.6e-5 - a) < 0,
+// R^2 (gamma(129) + 1.8e-5 - g) < 0, X^2 (1.8e-5 - g) < 0 and the absolute
+// terms; so d <= T implies V <= 0, and U >= D* for the threshold, which is
+// then inflated by t.  The per-vector constants (X rounded up to bf16,
+// ||p||^2 -+ gX^2 in double, split) are built once per index; the per-query
+// ones per (query, list).  Values whose norms exceed 2^40 would leave the
+// fp32 range safety the bound assumes: such indexes and queries take the LUT
+// kernel.
+#include <cmath>
+
+#include "common.hpp"
+#include "kernels.hpp"
+#include "scan_common.hpp"
+
+namespace fgpu {
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+namespace {
+
+constexpr double kA = 0x1p-6 + 0x1p-12;  // coefficient of R X
+constexpr double kG = 0x1p-13;           // coefficient of R^2 and X^2
+constexpr double kTInfl = 1.0 + 0x1p-12;
+constexpr double kAbs = 0x1p-110;
+constexpr double kDbl = 0x1p-40;         // slack for the double-precision constant arithmetic
+constexpr float kMaxNorm2 = 0x1p80f;     // squared residual norms above this take the LUT kernel
+constexpr int kQB = 32;                  // queries per work item (MFMA rows)
+constexpr int kTV = 32;                  // vectors per tile (MFMA columns)
+constexpr int kSW = 16;                  // waves per screen workgroup
+constexpr int kCandBuf = 256;            // per-wave candidate staging entries (LDS)
+constexpr int kChunk = 256;              // list vectors per work item (at most kMaxChunks items a group)
+constexpr int kMaxChunks = 8;
+
+constexpr uint32_t kOneOne = 0x3F803F80u;  // two bf16 1.0
+
+__device__ __forceinline__ void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+__device__ __forceinline__ int lanes_below64(uint64_t m) {
+  return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+}
+
+// ---- bf16 with stated rounding ------------------------------------------------
+__device__ __forceinline__ uint16_t bf_rn(float f) { return __builtin_bit_cast(uint16_t, (__bf16)f); }
+__device__ __forceinline__ double bf_val(uint16_t b) { return (double)__uint_as_float((uint32_t)b << 16); }
+__device__ __forceinline__ float f_step_down(float f) {
+  if (f == 0.0f) return -0x1p-149f;
+  const uint32_t u = __float_as_uint(f);
+  return __uint_as_float(f > 0.0f ? u - 1u : u + 1u);
+}
+__device__ __forceinline__ float f_step_up(float f) {
+  if (f == 0.0f) return 0x1p-149f;
+  const uint32_t u = __float_as_uint(f);
+  return __uint_as_float(f > 0.0f ? u + 1u : u - 1u);
+}
+// The largest float <= v and the smallest float >= v (v finite).
+__device__ __forceinline__ float f_below(double v) {
+  const float f = (float)v;
+  return (double)f > v ? f_step_down(f) : f;
+}
+__device__ __forceinline__ float f_above(double v) {
+  const float f = (float)v;
+  return (double)f < v ? f_step_up(f) : f;
+}
+// The largest bf16 <= v and the smallest bf16 >= v.
+__device__ __forceinline__ uint16_t bf_down(double v) {
+  const float f = f_below(v);
+  const uint32_t u = __float_as_uint(f);
+  uint32_t hb = u >> 16;
+  if ((u & 0xFFFFu) && f < 0.0f) hb += 1u;  // truncation moved a negative value up
+  return (uint16_t)hb;
+}
+__device__ __forceinline__ uint16_t bf_up(double v) {
+  const float f = f_above(v);
+  const uint32_t u = __float_as_uint(f);
+  uint32_t hb = u >> 16;
+  if ((u & 0xFFFFu) && f > 0.0f) hb += 1u;  // truncation moved a positive value down
+  return (uint16_t)hb;
+}
+// Three bf16 whose sum is <= v (UP false) or >= v (UP true), within about
+// 2^-24 |v|.  The first two parts are nearest roundings, so each difference is
+// exact in double (Sterbenz); the last is rounded in the stated direction.
+template <bool UP>
+__device__ __forceinline__ void split3(double v, uint16_t& b1, uint16_t& b2, uint16_t& b3) {
+  b1 = bf_rn((float)v);
+  const double r1 = v - bf_val(b1);
+  b2 = bf_rn((float)r1);
+  const double r2 = r1 - bf_val(b2);
+  b3 = UP ? bf_up(r2) : bf_down(r2);
+}
+__device__ __forceinline__ uint32_t pack2(uint16_t lo, uint16_t hi) { return (uint32_t)lo | ((uint32_t)hi << 16); }
+
+// ---- index-time arrays -----------------------------------------------------------
+// vext[v]: the per-vector block of the extra K range, 8 bf16:
+//   [X, y'_1, y'_2, y'_3, y''_1, y''_2, y''_3, 1]
+// X >= ||p_v|| (bf16, rounded up), y' <= ||p||^2 - g X^2 - 2^-110 X,
+// y'' >= ||p||^2 + g X^2 + 2^-110 X (each a three-part split).  ||p||^2 is
+// summed in double (each square exact; 128 roundings of 2^-53 are covered by
+// the 2^-40 slack).  xmax_bits: the largest X as float bits (atomic max).
+__global__ __launch_bounds__(256) void screen_prep_kernel(const float* __restrict__ cb, int m, int s,
+                                                          const uint8_t* __restrict__ codes, int64_t total,
+                                                          uint4* __restrict__ vext,
+                                                          unsigned int* __restrict__ xmax_bits) {
+  const int64_t v = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  float xm = 0.0f;
+  if (v < total) {
+    const uint8_t* c = codes + v * m;
+    double p2 = 0.0;
+    for (int j = 0; j < m; ++j) {
+      const float* p = cb + ((size_t)j * kPQK + c[j]) * s;
+      for (int d = 0; d < s; ++d) p2 += (double)p[d] * (double)p[d];
+    }
+    const uint16_t xb = bf_up(sqrt(p2) * (1.0 + kDbl));
+    const double xu = bf_val(xb);
+    const double lo = p2 - kG * xu * xu - kAbs * xu - kDbl * p2;
+    const double hi = p2 + kG * xu * xu + kAbs * xu + kDbl * p2;
+    uint16_t l1, l2, l3, h1, h2, h3;
+    split3<false>(lo, l1, l2, l3);
+    split3<true>(hi, h1, h2, h3);
+    vext[v] = make_uint4(pack2(xb, l1), pack2(l2, l3), pack2(h1, h2), pack2(h3, 0x3F80u));
+    xm = (float)xu;
+  }
+  xm = wave_max_f(xm);
+  if ((threadIdx.x & 63) == 0 && xm > 0.0f) atomicMax(xmax_bits, __float_as_uint(xm));
+}
+
+__global__ __launch_bounds__(256) void cb_bf16_kernel(const float* __restrict__ cb, int64_t n,
+                                                      uint16_t* __restrict__ out) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) out[i] = bf_rn(cb[i]);
+}
+
+// ---- work lists ---------------------------------------------------------------------
+__global__ __launch_bounds__(256) void screen_zero_kernel(int* __restrict__ p, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+    p[i] = 0;
+}
+
+// Query q joins list l's bucket (the screen kernels derive their work
+// items from the final counts).
+__device__ __forceinline__ int bucket_add(const ScreenArgs& a, int* cnt, int l, int q) {
+  const int pos = atomicAdd(&cnt[l], 1);
+  if (pos >= a.nq) {  // a probe list repeating a list id: the query takes the LUT kernel
+    a.thr[q] = __builtin_nanf("");
+    return -1;
+  }
+  a.bucket[(size_t)l * a.nq + pos] = q;
+  return pos;
+}
+
+// Work items of list l: groups of kQB queries times chunks of the list of
+// kChunk vectors (longer chunks, multiples of kTV, past kMaxChunks of them).
+__device__ __forceinline__ int chunk_len(int n) {
+  return max(kChunk, (n + kMaxChunks * kTV - 1) / (kMaxChunks * kTV) * kTV);
+}
+__device__ __forceinline__ int list_items(int cnt, int nq, int n) {
+  if (cnt <= 0 || n <= 0) return 0;
+  const int ng = (min(cnt, nq) + kQB - 1) / kQB;
+  const int per = chunk_len(n);
+  return ng * ((n + per - 1) / per);
+}
+
+// Round 1 pairs: each query with its first usable probe (in range, non-empty)
+// when that list holds at least k vectors.
+__global__ __launch_bounds__(256) void screen_pairs1_kernel(ScreenArgs a) {
+  const int q = blockIdx.x * blockDim.x + threadIdx.x;
+  if (q >= a.nq) return;
+  const uint32_t* pr = a.probes + (size_t)q * a.nprobe;
+  int2 f = make_int2(-1, -1);
+  for (int p = 0; p < a.nprobe; ++p) {
+    const uint32_t l = pr[p];
+    if (l >= (uint32_t)a.nlist) continue;
+    const int n = a.offsets[l + 1] - a.offsets[l];
+    if (n <= 0) continue;
+    if (n >= a.k) {
+      const int pos = bucket_add(a, a.cnt1, (int)l, q);
+      if (pos >= 0) f = make_int2((int)l, pos);
+    }
+    break;
+  }
+  a.first[q] = f;
+}
+
+// Round 2 pairs, one wave a query.  First T(q): the k-th smallest of the 32
+// group minima of U over the query's first list (the minimum, over the list's
+// round-1 items, of each item's per-group minimum), inflated by 1 + 2^-12;
+// +inf without a round-1 pair or with fewer than k groups holding a value.
+// Then every usable probe whose list bound does not exceed T(q).
+__global__ __launch_bounds__(256) void screen_pairs2_kernel(ScreenArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int q = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  if (q >= a.nq) return;
+  const int2 f = a.first[q];
+  uint32_t gm = 0x7F800000u;
+  if (f.x >= 0 && lane < 32) {
+    const int n = a.offsets[f.x + 1] - a.offsets[f.x];
+    const int per = chunk_len(n), nch = (n + per - 1) / per;
+    const uint32_t* g = a.gminbuf + (size_t)q * kMaxChunks * 32 + lane;
+    for (int c = 0; c < nch; ++c) gm = min(gm, g[c * 32]);
+  }
+  uint64_t key = gm;
+  wave_sort64_k(key);
+  const float kth = __uint_as_float((uint32_t)readlane64(key, a.k - 1));
+  const float T = kth < INFINITY ? f_above((double)kth * kTInfl) : INFINITY;
+  if (lane == 0) a.thr[q] = T;
+  if (!(T < INFINITY)) return;
+  for (int p = lane; p < a.nprobe; p += kWave) {
+    const size_t t = (size_t)q * a.nprobe + p;
+    const uint32_t l = a.probes[t];
+    if (l >= (uint32_t)a.nlist) continue;
+    if (a.offsets[l + 1] - a.offsets[l] <= 0) continue;
+    if (list_lower_bound(a.probe_dists[t], a.rmax[l]) > T) continue;
+    bucket_add(a, a.cnt2, (int)l, q);
+  }
+}
+
+// ---- the screen ---------------------------------------------------------------------------
+// The 16 code bytes a lane half needs per 16-dim chunk group come from its
+// half of the code row.  Lane half h covers dims [h D/2, (h+1) D/2): chunk c
+// holds dims h D/2 + 8c + e (e < 8) for A and B alike.
+template <int M>
+__device__ __forceinline__ void load_half(const uint8_t* p, uint32_t (&w)[M / 8]) {
+  if constexpr (M % 32 == 0) {
+#pragma unroll
+    for (int i = 0; i < M / 32; ++i) {
+      const uint4 v = reinterpret_cast<const uint4*>(p)[i];
+      w[4 * i] = v.x; w[4 * i + 1] = v.y; w[4 * i + 2] = v.z; w[4 * i + 3] = v.w;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < M / 16; ++i) {
+      const uint2 v = reinterpret_cast<const uint2*>(p)[i];
+      w[2 * i] = v.x; w[2 * i + 1] = v.y;
+    }
+  }
+}
+
+// 16-bit words code | (h M/2) << 8 for code bytes b and b + 1 of w: times the
+// entry size this is the code's row in the lane half's part of the bf16
+// codebook, so every gather below takes one shift and an immediate offset.
+__device__ __forceinline__ uint32_t words2(uint32_t w, uint32_t hsel, int b) {
+  const uint32_t sel = (uint32_t)b | (4u << 8) | ((uint32_t)(b + 1) << 16) | (4u << 24);
+  return __builtin_amdgcn_perm(hsel, w, sel);
+}
+
+// The B fragment of chunk c: dims 8c .. 8c + 7 of the lane half's decoded row.
+template <int D, int M>
+__device__ __forceinline__ bf16x8 decode_chunk(const uint16_t* cbs, const uint32_t (&cw)[M / 8], uint32_t hsel,
+                                               int c) {
+  constexpr int S = D / M;
+  constexpr int SUB = 512 * S;  // bytes per subspace of the bf16 codebook
+  const char* base = reinterpret_cast<const char*>(cbs);
+  uint32_t f[4];
+  if constexpr (S == 4) {
+    const uint32_t wd = words2(cw[c >> 1], hsel, 2 * (c & 1));
+    const uint32_t a0 = (wd & 0xFFFFu) << 3, a1 = (wd >> 16) << 3;
+    const uint2 e0 = *reinterpret_cast<const uint2*>(base + a0 + (2 * c) * SUB);
+    const uint2 e1 = *reinterpret_cast<const uint2*>(base + a1 + (2 * c + 1) * SUB);
+    f[0] = e0.x; f[1] = e0.y; f[2] = e1.x; f[3] = e1.y;
+  } else if constexpr (S == 8) {
+    const uint32_t wd = words2(cw[c >> 2], hsel, c & 3);  // byte c & 3 (the second word is unused)
+    const uint32_t a0 = (wd & 0xFFFFu) << 4;
+    const uint4 e = *reinterpret_cast<const uint4*>(base + a0 + c * SUB);
+    f[0] = e.x; f[1] = e.y; f[2] = e.z; f[3] = e.w;
+  } else {
+    static_assert(S == 2, "screen: sub-dimension 2, 4 or 8");
+    const uint32_t w01 = words2(cw[c], hsel, 0), w23 = words2(cw[c], hsel, 2);
+    f[0] = *reinterpret_cast<const uint32_t*>(base + ((w01 & 0xFFFFu) << 2) + (4 * c) * SUB);
+    f[1] = *reinterpret_cast<const uint32_t*>(base + ((w01 >> 16) << 2) + (4 * c + 1) * SUB);
+    f[2] = *reinterpret_cast<const uint32_t*>(base + ((w23 & 0xFFFFu) << 2) + (4 * c + 2) * SUB);
+    f[3] = *reinterpret_cast<const uint32_t*>(base + ((w23 >> 16) << 2) + (4 * c + 3) * SUB);
+  }
+  return __builtin_bit_cast(bf16x8, f);
+}
+
+__device__ __forceinline__ bf16x8 frag_of(uint32_t x, uint32_t y, uint32_t z, uint32_t w) {
+  const uint32_t f[4] = {x, y, z, w};
+  return __builtin_bit_cast(bf16x8, f);
+}
+
+// k-th smallest (1 <= k <= 32) of 32 values: bitonic sort in registers.
+__device__ __forceinline__ uint32_t kth_of_32(uint32_t (&v)[32], int k) {
+#pragma unroll
+  for (int size = 2; size <= 32; size <<= 1) {
+#pragma unroll
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+#pragma unroll
+      for (int i = 0; i < 32; ++i) {
+        const int j = i ^ stride;
+        if (j > i) {
+          const bool up = (i & size) == 0;
+          const uint32_t lo = min(v[i], v[j]), hi = max(v[i], v[j]);
+          v[i] = up ? lo : hi;
+          v[j] = up ? hi : lo;
+        }
+      }
+    }
+  }
+  uint32_t r = v[0];
+#pragma unroll
+  for (int i = 1; i < 32; ++i) r = (i == k - 1) ? v[i] : r;
+  return r;
+}
+
+// One persistent workgroup per CU; each wave takes work items (list, group of
+// up to kQB queries, vector range) and screens the range in tiles of kTV
+// vectors.  A wave's first item is its global index; later ones come from a
+// counter.  ROUND 1 folds each (query, group) minimum of U into gmin;
+// ROUND 2 appends candidates.
+// LDS: the bf16 codebook first (offset 0, so every gather's subspace offset is
+// the instruction's immediate), then per-wave staging.
+template <int D, int M, int ROUND>
+__global__ __launch_bounds__(kSW * kWave) void screen_kernel(ScreenArgs a) {
+  constexpr int NC = D / 16;  // main K chunks
+  constexpr int HB = M / 2;   // code bytes per lane half
+  constexpr int HD = D / 2;   // dims per lane half
+  static_assert(D % 32 == 0 && D <= 128, "screen: dim a multiple of 32, at most 128");
+  constexpr int kCbBytes = D * kPQK * 2;
+  constexpr int kWaveWords = ROUND == 1 ? 0 : 2 * kCandBuf;  // staged (row, vector position) pairs
+  constexpr int kPreOff = kCbBytes + kSW * (kWaveWords + kQB) * 4;
+  __shared__ __align__(16) unsigned char lds[kPreOff + (kScreenMaxLists + 1 + kSW) * 4];
+  uint16_t* cbs = reinterpret_cast<uint16_t*>(lds);
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  uint2* wbuf = reinterpret_cast<uint2*>(lds + kCbBytes + wave * kWaveWords * 4);
+  int* rowq = reinterpret_cast<int*>(lds + kCbBytes + kSW * kWaveWords * 4) + wave * kQB;
+  int* pre = reinterpret_cast<int*>(lds + kPreOff);  // [nlist + 1] first item of each list
+  int* wsum = pre + kScreenMaxLists + 1;             // [kSW]
+  const int li = lane & 31, h = lane >> 5;
+  const long long t_begin = a.stats ? clock64() : 0;
+  const int* cnt = ROUND == 1 ? a.cnt1 : a.cnt2;
+  for (int i = tid; i < kCbBytes / 16; i += kSW * kWave)
+    reinterpret_cast<uint4*>(lds)[i] = reinterpret_cast<const uint4*>(a.cb16)[i];
+  // The work items: for each list, its groups of queries times its chunks,
+  // numbered by an exclusive scan over the lists (each thread 8 lists).
+  {
+    constexpr int kPer = kScreenMaxLists / (kSW * kWave);
+    int v[kPer], s = 0;
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int l = tid * kPer + i;
+      v[i] = l < a.nlist ? list_items(cnt[l], a.nq, a.offsets[l + 1] - a.offsets[l]) : 0;
+      s += v[i];
+    }
+    const int incl = wave_incl_scan(s);
+    if (lane == kWave - 1) wsum[wave] = incl;
+    __syncthreads();
+    if (wave == 0) {
+      int x = lane < kSW ? wsum[lane] : 0;
+      x = wave_incl_scan(x);
+      if (lane < kSW) wsum[lane] = x;
+    }
+    __syncthreads();
+    int base = (wave > 0 ? wsum[wave - 1] : 0) + incl - s;
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int l = tid * kPer + i;
+      if (l <= a.nlist) pre[l] = base;
+      base += v[i];
+    }
+    __syncthreads();
+  }
+  const int nitems = __builtin_amdgcn_readfirstlane(wsum[kSW - 1]);
+  long long ck = a.stats ? clock64() : 0;
+  long long ck_pre = ck - t_begin, ck_setup = 0, ck_tiles = 0, ck_post = 0, ntiles = 0, nit = 0;
+  const int nwaves = (int)gridDim.x * kSW;
+  const uint32_t hsel = h ? (uint32_t)HB * 0x01010101u : 0u;
+  // The extra block of a column past the end of the range: +1e30 in both
+  // rounds' terms (slots 1 and 4), so its value is never a candidate and
+  // never a group minimum; lane half 1 keeps the [1, 1, 0 ...] multipliers.
+  const uint16_t big = bf_rn(1e30f);
+  const uint4 bx_pad = h == 0 ? make_uint4(pack2(0u, big), 0u, pack2(big, 0u), pack2(0u, 0x3F80u))
+                              : make_uint4(kOneOne, 0u, 0u, 0u);
+
+  for (int w = (int)blockIdx.x * kSW + wave; w < nitems; w += nwaves) {
+    // Item w: the last list whose first item is <= w, then its group and chunk.
+    int lo = 0, hi = a.nlist - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (pre[mid] <= w) lo = mid; else hi = mid - 1;
+    }
+    const int l = __builtin_amdgcn_readfirstlane(lo);
+    const int start = a.offsets[l], n = a.offsets[l + 1] - start;
+    const int per = chunk_len(n), nch = (n + per - 1) / per;
+    const int local = w - __builtin_amdgcn_readfirstlane(pre[l]);
+    const int grp = local / nch, jb = (local % nch) * per, je = min(n, jb + per);
+    const int nrow = min(kQB, min(cnt[l], a.nq) - grp * kQB);
+    const int qi = li < nrow ? a.bucket[(size_t)l * a.nq + grp * kQB + li] : -1;
+
+    // Two tiles of codes in flight ahead of the one being screened.
+    auto load_tile = [&](int j0, uint32_t (&cw)[M / 8], uint4& bx) {
+      const int j = j0 + li;
+      const bool valid = j < je;
+      const int64_t v = (int64_t)start + (valid ? j : je - 1);
+      load_half<M>(a.codes + v * M + h * HB, cw);
+      bx = bx_pad;
+      if (valid && h == 0) bx = a.vext[v];
+    };
+    uint32_t cw0[M / 8], cw1[M / 8];
+    uint4 bx0, bx1;
+    load_tile(jb, cw0, bx0);
+    if (jb + kTV < je) load_tile(jb + kTV, cw1, bx1);
+
+    // A rows: -2 bf16(r) over this lane half's dims, and nr2 = ||r||^2 (fp32).
+    bf16x8 A[NC];
+    float nr2 = 0.0f;
+    {
+      const float4* qp = reinterpret_cast<const float4*>(a.queries + (size_t)(qi >= 0 ? qi : 0) * D + h * HD);
+      const float4* cp = reinterpret_cast<const float4*>(a.centroids + (size_t)l * D + h * HD);
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        const float4 q0 = qp[2 * c], q1 = qp[2 * c + 1], c0 = cp[2 * c], c1 = cp[2 * c + 1];
+        const float r[8] = {q0.x - c0.x, q0.y - c0.y, q0.z - c0.z, q0.w - c0.w,
+                            q1.x - c1.x, q1.y - c1.y, q1.z - c1.z, q1.w - c1.w};
+        uint32_t f[4];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) nr2 = __builtin_fmaf(r[e], r[e], nr2);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) f[e] = pack2(bf_rn(-2.0f * r[2 * e]), bf_rn(-2.0f * r[2 * e + 1]));
+        A[c] = __builtin_bit_cast(bf16x8, f);
+      }
+      nr2 += __shfl_xor(nr2, 32, kWave);
+    }
+    bool active = qi >= 0 && nr2 <= kMaxNorm2;  // false for NaN
+    float T = 0.0f;
+    if (ROUND == 2) {
+      T = active ? a.thr[qi] : 0.0f;
+      active = active && T < INFINITY;
+      T = fmaxf(T, 0.0f);
+    }
+    // The extra K block of this row (8 bf16 of this lane half).
+    uint32_t ex[4] = {0u, 0u, 0u, 0u};
+    if (active) {
+      const double n2 = (double)nr2;
+      const double R = sqrt(n2 * (1.0 + 0x1p-16)) * (1.0 + kDbl);
+      const uint16_t aR = bf_up(kA * R);
+      uint16_t p1, p2, p3;
+      if (ROUND == 2) {
+        const double rhs = (double)T * kTInfl - n2 + kG * R * R + kAbs * (1.0 + R);
+        split3<false>(-rhs - kDbl * ((double)T + n2 + kG * R * R), p1, p2, p3);
+        if (h == 0) {
+          ex[0] = pack2(aR ^ 0x8000u, 0x3F80u);
+          ex[1] = pack2(0x3F80u, 0x3F80u);
+          ex[2] = 0u;
+          ex[3] = pack2(0u, p1);
+        } else {
+          ex[0] = pack2(p2, p3);
+        }
+      } else {
+        const double c = n2 * kTInfl + kG * R * R + kAbs * (1.0 + R);
+        split3<true>(c * (1.0 + kDbl), p1, p2, p3);
+        if (h == 0) {
+          ex[0] = pack2(aR, 0u);
+          ex[1] = 0u;
+          ex[2] = pack2(0x3F80u, 0x3F80u);
+          ex[3] = pack2(0x3F80u, p1);
+        } else {
+          ex[0] = pack2(p2, p3);
+        }
+      }
+    } else {
+      // An inactive row never passes the round-2 test (V = 1e30) and
+      // contributes no group minimum in round 1.
+      if (ROUND == 2 && h == 0) ex[3] = pack2(0u, big);
+#pragma unroll
+      for (int c = 0; c < NC; ++c) A[c] = frag_of(0u, 0u, 0u, 0u);
+    }
+    const bf16x8 Aex = frag_of(ex[0], ex[1], ex[2], ex[3]);
+    // The query of each row, for the candidate flush and the round-1 fold
+    // (which skips inactive rows: their values bound nothing).
+    if (h == 0) rowq[li] = ROUND == 1 && !active ? -1 : qi;
+
+    // Per row and lane column, the smallest U bits seen (ROUND 1; every U is
+    // >= 0, where float order is unsigned order).
+    uint32_t mins[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) mins[r] = 0x7F800000u;
+    // ROUND 2 candidates: staged in wbuf as (row, vector position), then
+    // each takes a slot of its query's candidate array with an atomic.
+    int nb = 0;  // staged entries (wave-uniform)
+    auto flush = [&]() {
+      wave_sync();
+      for (int i0 = 0; i0 < nb; i0 += kWave) {
+        const int i = i0 + lane;
+        if (i < nb) {
+          const uint2 e = wbuf[i];
+          const int q = rowq[e.x];
+          const int slot = atomicAdd(&a.cand_cnt[q], 1);
+          if (slot < a.cand_cap) a.cand[(size_t)q * a.cand_cap + slot] = make_uint2((uint32_t)start + e.y, (uint32_t)l);
+        }
+      }
+      nb = 0;
+      wave_sync();
+    };
+    if (a.stats) {
+      const long long t = clock64();
+      ck_setup += t - ck;
+      ck = t;
+    }
+
+    for (int j0 = jb; j0 < je; j0 += kTV) {
+      // Every gather of the tile first, then the loads two tiles ahead, then
+      // the MFMA chain.
+      bf16x8 B[NC];
+#pragma unroll
+      for (int c = 0; c < NC; ++c) B[c] = decode_chunk<D, M>(cbs, cw0, hsel, c);
+      const bf16x8 Bx = frag_of(bx0.x, bx0.y, bx0.z, bx0.w);
+#pragma unroll
+      for (int i = 0; i < M / 8; ++i) cw0[i] = cw1[i];
+      bx0 = bx1;
+      if (j0 + 2 * kTV < je) load_tile(j0 + 2 * kTV, cw1, bx1);
+      f32x16 acc;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
+#pragma unroll
+      for (int c = 0; c < NC; ++c) acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A[c], B[c], acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(Aex, Bx, acc, 0, 0, 0);
+      // acc[r]: row 8 (r / 4) + 4 h + r % 4 of the work item, column li (vector j0 + li).
+      if constexpr (ROUND == 1) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mins[r] = min(mins[r], __float_as_uint(acc[r]));
+      } else {
+        // V <= 0: the bits as a signed int are <= 0 (+0, or the sign set).
+        int mn = __float_as_int(acc[0]);
+#pragma unroll
+        for (int r = 1; r < 16; ++r) mn = min(mn, __float_as_int(acc[r]));
+        if (__ballot(mn <= 0)) {
+          const int j = j0 + li;
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const bool pass = __float_as_int(acc[r]) <= 0;
+            const uint64_t bm = __ballot(pass);
+            if (bm) {
+              const int c = __popcll(bm);
+              if (nb + c > kCandBuf) flush();
+              const int row = 8 * (r >> 2) + 4 * h + (r & 3);
+              if (pass) wbuf[nb + lanes_below64(bm)] = make_uint2((uint32_t)row, (uint32_t)j);
+              nb += c;
+            }
+          }
+        }
+      }
+    }
+
+    if (a.stats) {
+      const long long t = clock64();
+      ck_tiles += t - ck;
+      ck = t;
+    }
+    if constexpr (ROUND == 2) {
+      if (nb > 0) flush();
+    } else {
+      // Groups are vector positions mod 32 (= the lane column): this item's
+      // per-row, per-group minima go to the row's query, at the item's chunk
+      // (each (query, chunk) slot has exactly one writer); the pair kernel
+      // of round 2 combines the chunks of a query's list.
+      wave_sync();
+      const int cidx = local % nch;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = 8 * (r >> 2) + 4 * h + (r & 3);
+        const int q = rowq[row];
+        if (q >= 0) a.gminbuf[((size_t)q * kMaxChunks + cidx) * 32 + li] = mins[r];
+      }
+    }
+    wave_sync();
+    if (a.stats) {
+      const long long t = clock64();
+      ck_post += t - ck;
+      ck = t;
+    }
+  }
+  if (a.stats && lane == 0) {
+    const int o = ROUND == 1 ? 0 : 4;
+    atomicAdd(&a.stats[o], (unsigned long long)ck_pre);
+    atomicAdd(&a.stats[o + 1], (unsigned long long)ck_setup);
+    atomicAdd(&a.stats[o + 2], (unsigned long long)ck_tiles);
+    atomicAdd(&a.stats[o + 3], (unsigned long long)ck_post);
+    (void)ntiles;
+    (void)nit;
+  }
+}
+
+// ---- exact rescore ------------------------------------------------------------------------
+template <int S>
+__device__ __forceinline__ void load_row(const float* p, float (&v)[S]) {
+  if constexpr (S % 4 == 0) {
+#pragma unroll
+    for (int i = 0; i < S / 4; ++i) {
+      const float4 t = reinterpret_cast<const float4*>(p)[i];
+      v[4 * i] = t.x; v[4 * i + 1] = t.y; v[4 * i + 2] = t.z; v[4 * i + 3] = t.w;
+    }
+  } else if constexpr (S % 2 == 0) {
+#pragma unroll
+    for (int i = 0; i < S / 2; ++i) {
+      const float2 t = reinterpret_cast<const float2*>(p)[i];
+      v[2 * i] = t.x; v[2 * i + 1] = t.y;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < S; ++i) v[i] = p[i];
+  }
+}
+
+// One wave a query: the exact ADC distance of every candidate in the
+// reference's direct form (the LUT entry's chain per subspace, summed in
+// ascending m), then the k smallest (distance, id) keys.  A persistent grid
+// of one workgroup per CU holding the fp32 codebook in LDS; wave g takes
+// queries g, g + G, ...
+constexpr int kRW = 16;  // waves per rescore workgroup
+template <int D, int M>
+__global__ __launch_bounds__(kRW * kWave) void rescore_kernel(ScreenArgs a) {
+  constexpr int S = D / M;
+  __shared__ __align__(16) float cbf[D * kPQK];
+  __shared__ float qs[kRW][D];
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  for (int i = threadIdx.x; i < D * kPQK / 4; i += kRW * kWave)
+    reinterpret_cast<float4*>(cbf)[i] = reinterpret_cast<const float4*>(a.codebook)[i];
+  __syncthreads();
+  for (int q = (int)blockIdx.x * kRW + wave; q < a.nq; q += (int)gridDim.x * kRW) {
+    const float T = a.thr[q];
+    const int cnt = __builtin_amdgcn_readfirstlane(a.cand_cnt[q]);
+    if (!(T < INFINITY) || cnt > a.cand_cap) {
+      if (lane == 0) {
+        const int f = atomicAdd(&a.ctr[kCtrFlag], 1);
+        a.flist[f] = q;
+      }
+      continue;
+    }
+    for (int d = lane; d < D; d += kWave) qs[wave][d] = a.queries[(size_t)q * D + d];
+    wave_sync();
+    const float* qv = qs[wave];
+    uint64_t lk = kPadKey;
+    for (int i0 = 0; i0 < cnt; i0 += kWave) {
+      const int i = i0 + lane;
+      uint64_t key = kPadKey;
+      if (i < cnt) {
+        const uint2 e = a.cand[(size_t)q * a.cand_cap + i];
+        const int64_t pos = e.x;
+        const float* cen = a.centroids + (size_t)e.y * D;
+        uint4 w[M / 16];
+        load_codes<M>(a.codes, pos, w);
+        const int id = a.vec_ids[pos];
+        float dist = 0.0f;
+#pragma unroll
+        for (int mm = 0; mm < M; ++mm) {
+          const uint32_t ww = mm % 16 < 4 ? w[mm / 16].x : mm % 16 < 8 ? w[mm / 16].y
+                                                       : mm % 16 < 12 ? w[mm / 16].z : w[mm / 16].w;
+          const uint32_t code = (ww >> (8 * (mm & 3))) & 0xFFu;
+          float cr[S], pr[S], r[S];
+          load_row<S>(cen + mm * S, cr);
+#pragma unroll
+          for (int e2 = 0; e2 < S; ++e2) pr[e2] = cbf[(mm * kPQK + code) * S + e2];
+#pragma unroll
+          for (int e2 = 0; e2 < S; ++e2) r[e2] = qv[mm * S + e2] - cr[e2];
+          const float t = lut_entry<S>(r, pr);
+          dist = mm == 0 ? t : dist + t;
+        }
+        key = key_of(dist, id);
+      }
+      wave_sort64_k(key);
+      if (i0 == 0)
+        lk = key;
+      else
+        wave_merge_sorted64_k(lk, key);
+    }
+    if (lane < a.k) {
+      const int id = key_id(lk);
+      const bool pad = id == kPadId;
+      a.out_ids[(size_t)q * a.k + lane] = pad ? -1 : id;
+      a.out_d[(size_t)q * a.k + lane] = pad ? FLT_MAX : key_dist(lk);
+    }
+    wave_sync();
+  }
+}
+
+int cu_count() {
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+    cus = 256;
+  return cus;
+}
+
+template <int D, int M>
+fgpu_status launch_screen_dm(const ScreenArgs& a, hipStream_t s) {
+  const int cus = cu_count();
+  const int64_t nz = kCtrCount + 2 * (int64_t)a.nlist + (int64_t)a.nq;
+  hipLaunchKernelGGL(screen_zero_kernel, dim3((unsigned)std::min<int64_t>((nz + 255) / 256, 2048)), dim3(256), 0, s,
+                     a.ctr, nz);
+  hipLaunchKernelGGL(screen_pairs1_kernel, dim3((unsigned)((a.nq + 255) / 256)), dim3(256), 0, s, a);
+  hipLaunchKernelGGL((screen_kernel<D, M, 1>), dim3((unsigned)cus), dim3(kSW * kWave), 0, s, a);
+  hipLaunchKernelGGL(screen_pairs2_kernel, dim3((unsigned)((a.nq + 3) / 4)), dim3(256), 0, s, a);
+  hipLaunchKernelGGL((screen_kernel<D, M, 2>), dim3((unsigned)cus), dim3(kSW * kWave), 0, s, a);
+  hipLaunchKernelGGL((rescore_kernel<D, M>), dim3((unsigned)cus), dim3(kRW * kWave), 0, s, a);
+  FGPU_HIP(hipGetLastError());
+  return FGPU_OK;
+}
+
+}  // namespace
+
+int64_t screen_gmin_words(int nq) {
+  // Round 1: per query, per chunk of its first list, 32 group minima.
+  return (int64_t)nq * kMaxChunks * 32;
+}
+
+bool screen_supported(int dim, int m) {
+  return (dim == 128 && (m == 16 || m == 32 || m == 64)) || (dim == 96 && m == 48);
+}
+
+
+fgpu_status launch_screen_prep(const float* codebook, int m, int sub, const uint8_t* codes, int64_t total,
+                               uint16_t* cb16, uint4* vext, unsigned int* xmax_bits, hipStream_t s) {
+  const int64_t ncb = (int64_t)m * kPQK * sub;
+  hipLaunchKernelGGL(cb_bf16_kernel, dim3((unsigned)((ncb + 255) / 256)), dim3(256), 0, s, codebook, ncb, cb16);
+  FGPU_HIP(hipMemsetAsync(xmax_bits, 0, sizeof(unsigned int), s));
+  if (total > 0)
+    hipLaunchKernelGGL(screen_prep_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, codebook, m, sub,
+                       codes, total, vext, xmax_bits);
+  FGPU_HIP(hipGetLastError());
+  return FGPU_OK;
+}
+
+fgpu_status launch_screen(int dim, int m, const ScreenArgs& a, hipStream_t s) {
+  FGPU_CHECK(a.k >= 1 && a.k <= 32, FGPU_ERR_UNSUPPORTED, "screen: k must be in [1, 32]");
+  if (a.nq <= 0) return FGPU_OK;
+  if (dim == 128 && m == 32) return launch_screen_dm<128, 32>(a, s);
+  if (dim == 128 && m == 16) return launch_screen_dm<128, 16>(a, s);
+  if (dim == 128 && m == 64) return launch_screen_dm<128, 64>(a, s);
+  if (dim == 96 && m == 48) return launch_screen_dm<96, 48>(a, s);
+  return set_error(FGPU_ERR_UNSUPPORTED, "screen: unsupported (dim, pq_m)");
+}
+
+}  // namespace fgpu

@@ -906,7 +906,7 @@ __global__ __launch_bounds__(kRT * SPEC) void rerank_kernel(RerankArgs a) {
 
 template <int D>
 fgpu_status launch_rr(const RerankArgs& a, hipStream_t s) {
-  if (rerank_spec(a.nq) > 1) {
+  if (rerank_spec(a.nq, a.spec) > 1) {
     hipLaunchKernelGGL((rerank_kernel<D, 4>), dim3((unsigned)a.nq), dim3(kRT * 4), 0, s, a);
     FGPU_HIP(hipGetLastError());
     return FGPU_OK;
@@ -937,26 +937,18 @@ static int cu_count() {
   return v;
 }
 
-// 0: automatic; 1: one mini-batch a step; anything else: four.
-static std::atomic<int> g_rr_spec{0};
-void set_rerank_spec_override(int v) { g_rr_spec.store(v < 0 ? 0 : v, std::memory_order_relaxed); }
-
 // Mini-batches the rerank computes a step: four while the batch leaves CUs
 // free (one 512-thread workgroup a query, latency-bound row loads), else one
 // (a large batch is bound by the row reads, and work past a stop is wasted).
-int rerank_spec(int nq) {
-  const int force = g_rr_spec.load(std::memory_order_relaxed);
+// force: 0 automatic, 1 one, anything else four.
+int rerank_spec(int nq, int force) {
   if (force == 1) return 1;
   if (force > 1) return 4;
   return nq <= cu_count() ? 4 : 1;
 }
 
-// 0: automatic; 1: never split; s >= 2: split phase 1 s ways (at most p1).
-static std::atomic<int> g_tp_split{0};
-void set_two_phase_split_override(int v) { g_tp_split.store(v < 0 ? 0 : v, std::memory_order_relaxed); }
-
-int two_phase_split(int nq, int p1, int limit_k) {
-  const int force = g_tp_split.load(std::memory_order_relaxed);
+// force: 0 automatic, 1 never split, s >= 2 split phase 1 s ways (at most p1).
+int two_phase_split(int nq, int p1, int limit_k, int force) {
   if (limit_k > kWave || p1 < 2 || nq <= 0 || force == 1) return 1;
   if (force > 1) return std::min(p1, force);
   const int slots = 2 * cu_count();  // two_phase_kernel workgroups resident at once

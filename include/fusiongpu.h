@@ -95,25 +95,6 @@ fgpu_status fgpu_index_wrap(int dim, int pq_m, int nlist, const int32_t* d_offse
  * A correct run always reads 0. */
 fgpu_status fgpu_index_faults(const fgpu_index* idx, void* stream, unsigned long long* count, int reset);
 fgpu_status fgpu_index_check(const fgpu_index* idx, void* stream);
-/* Test hook: polls before a wait gives up, for every later scan launch in the
- * process (0 = the automatic limit).  A tiny limit makes give-ups certain
- * while every wave still runs to the end of the kernel. */
-void fgpu_debug_set_spin_limit(int polls);
-/* Measurement hook: with enabled = 0 every later plain-scan launch in the
- * process reads every probed list instead of skipping the lists whose lower
- * bound exceeds the running k-th distance (results are the same; only the
- * work differs).  1 restores the default. */
-void fgpu_debug_set_list_skip(int enabled);
-/* Test hook: phase 1 of every later two-phase launch in the process runs on
- * `split` workgroups a query (0 = automatic: split only batches too small to
- * fill the GPU; 1 = never; s >= 2 = s, at most p1; limit_k <= 64 only).
- * Results are the same whatever the split. */
-void fgpu_debug_set_two_phase_split(int split);
-/* Test hook: mini-batches every later rerank launch in the process computes
- * at once before applying them in order (0 = automatic: 4 while the batch
- * leaves CUs free, else 1; 1 = one; any other value = 4).  Results and visit
- * counts are the same whatever the value. */
-void fgpu_debug_set_rerank_spec(int spec);
 /* Test hook (host only): the PQ training sample rows of fgpu_pq_train, the
  * first min(sample_size, n) entries of std::shuffle(0 .. n-1, mt19937(12345))
  * (pq_utils.h:91-97), into h_rows.  Returns their count, or -1 on a bad
@@ -189,22 +170,67 @@ fgpu_status fgpu_adc_search_stats(const fgpu_index* idx, const float* d_queries,
                                   int32_t* d_out_ids, float* d_out_dists, unsigned long long* d_stats,
                                   void* stream);
 
-/* coarse + ADC in one call. */
+/* coarse + ADC in one call: the same results as fgpu_coarse_search followed
+ * by fgpu_adc_search.  For k <= 32 on the geometries (dim, pq_m) = (128, 16),
+ * (128, 32), (128, 64), (96, 48) the scan part runs as an MFMA screen with an
+ * exact rescore (no per-(query, list) LUT): every query's first list gives an
+ * upper bound T on its k-th distance, every probed vector whose rigorous lower
+ * bound does not exceed T is rescored with the reference's direct ADC form
+ * (gpu_global.cu:259-319, bit-identical to the LUT sum), and the few queries
+ * it cannot settle (a first list shorter than k, more than 512 candidates)
+ * are scanned by the LUT kernel.  That needs fgpu_search_workspace_bytes; a
+ * smaller workspace that still holds the coarse step runs the LUT kernels. */
 size_t fgpu_search_workspace_bytes(int nq, int nlist, int nprobe);
 fgpu_status fgpu_search(const fgpu_index* idx, const float* d_queries, int nq, int nprobe, int k,
                         float prune_ratio, int32_t* d_out_ids, float* d_out_dists,
                         void* d_workspace, size_t workspace_bytes, void* stream);
+/* Instrumentation of the last fgpu_search on this workspace (waits for
+ * `stream`; no reference counterpart): h_stats[0..7] = (query, list) pairs
+ * screened for the thresholds, lists screened in the second round, (query,
+ * list) pairs screened there, candidates rescored, the largest candidate count
+ * of a query, queries handed to the LUT kernel, queries with a finite
+ * threshold, 0.  Only meaningful after a call that took the screen. */
+fgpu_status fgpu_search_screen_stats(const fgpu_index* idx, int nq, int nprobe, const void* d_workspace,
+                                     size_t workspace_bytes, void* stream, long long* h_stats, int n_stats);
+/* 1 when the index carries the screen's arrays (built at creation for the
+ * geometries above when decoded norms stay below 2^40). */
+int fgpu_index_screen_ready(const fgpu_index* idx);
+
+/* Per-index options (no reference counterpart).  They affect only later
+ * calls on this index, never another index:
+ *   FGPU_OPT_LIST_SKIP  0: the LUT scan reads every probed list (timing of the
+ *                       scan without its list bound; same results), 1 default;
+ *   FGPU_OPT_SPIN_LIMIT polls before a flow-kernel wait gives up (0 = automatic;
+ *                       a tiny limit makes give-ups certain while every wave
+ *                       still runs to the end of the kernel);
+ *   FGPU_OPT_TWO_PHASE_SPLIT phase 1 of fgpu_two_phase_search on `split`
+ *                       workgroups a query (0 = automatic: split only batches
+ *                       too small to fill the GPU; 1 = never; s >= 2 = s, at
+ *                       most p1; limit_k <= 64 only; same results);
+ *   FGPU_OPT_SCREEN     0: fgpu_search runs the LUT kernels, 1 default;
+ *   FGPU_OPT_SCREEN_CLOCKS 1: the screen kernels add their waves' shader
+ *                       clocks (before the first item, item set-up, tile
+ *                       loops, after the tiles; round 1 then round 2) to the
+ *                       counters fgpu_search_screen_stats returns in
+ *                       h_stats[8..15]; 0 default. */
+#define FGPU_OPT_LIST_SKIP 1
+#define FGPU_OPT_SPIN_LIMIT 2
+#define FGPU_OPT_SCREEN 3
+#define FGPU_OPT_SCREEN_CLOCKS 4
+#define FGPU_OPT_TWO_PHASE_SPLIT 5
+fgpu_status fgpu_index_set_option(fgpu_index* idx, int option, int value);
 
 /* ---- search without allocation ----------------------------------------- */
 
 /* No counterpart in the reference.  For callers that cannot allocate device
  * memory (code under HIP graph capture, tight serving loops, harnesses that
  * forbid hipMalloc): fgpu_search with its scratch (probe ids and distances,
- * query norms, the coarse estimate tile) in a file-scope device array of
- * FGPU_NOALLOC_SCRATCH_BYTES that each GPU the library runs on holds until the
- * process ends, instead of a caller workspace.  Queries run in chunks of
- * fgpu_search_noalloc_max_rows(nlist, nprobe) rows; results equal
- * fgpu_search's.  FGPU_ERR_WORKSPACE when not even 64 rows fit (nlist above
+ * query norms, the coarse estimate tile, the screen's buckets and candidates)
+ * in a file-scope device array of FGPU_NOALLOC_SCRATCH_BYTES that each GPU the
+ * library runs on holds until the process ends, instead of a caller workspace.
+ * Queries run in chunks of fgpu_search_noalloc_max_rows(nlist, nprobe) rows
+ * (sized so the screen path fits when 64 rows of it do, else for the LUT
+ * kernel); results equal fgpu_search's.  FGPU_ERR_WORKSPACE when not even 64 rows fit (nlist above
  * about 120k at nprobe 32).  No hipMalloc, hipFree or allocating library call.
  * Every call on one GPU shares that GPU's array: calls that overlap on one GPU
  * (other streams, other host threads) race and must be serialised by the
@@ -273,6 +299,14 @@ fgpu_status fgpu_rerank(const float* d_queries, int nq, int dim, const float* d_
                         const int32_t* d_top_ids, const int32_t* d_top_counts, int rerank_m, int k,
                         int mini_batch, float eps, int beta, int32_t* d_final_ids, float* d_final_dists,
                         int32_t* d_visited, void* stream);
+/* fgpu_rerank with the number of mini-batches computed at once stated per
+ * call (no reference counterpart): spec 0 automatic (four while the batch
+ * leaves CUs free, else one), 1 one, any other value four.  Results and
+ * visit counts are the same whatever spec. */
+fgpu_status fgpu_rerank_spec(const float* d_queries, int nq, int dim, const float* d_base, int64_t n,
+                             const int32_t* d_top_ids, const int32_t* d_top_counts, int rerank_m, int k,
+                             int mini_batch, float eps, int beta, int32_t* d_final_ids, float* d_final_dists,
+                             int32_t* d_visited, int spec, void* stream);
 
 /* coarse + two-phase + rerank in one call: the SearchPipeline per-batch path
  * (search_pipeline.cu:341-361) with final_k = k. */

@@ -14,12 +14,22 @@ import fusiongpu_amd as fg  # noqa: E402
 def test_arg_converts_the_dtypes_the_abi_reads():
     a = fg._arg(np.ones((3, 4), np.float64), torch.float32, "x", (None, 4))
     assert a.dtype == torch.float32 and tuple(a.shape) == (3, 4)
-    # int64 probe ids keep their low 32 bits: 0xFFFFFFFF stays the pruned sentinel
+    # int64 probe ids convert; 0xFFFFFFFF, the pruned sentinel, stays all-ones
     p = fg._arg(np.array([[0, 5, 0xFFFFFFFF]], np.int64), torch.int32, "probe_ids", (1, None))
     assert p.dtype == torch.int32
     assert p.numpy().view(np.uint32).tolist() == [[0, 5, 0xFFFFFFFF]]
     t = torch.arange(6, dtype=torch.int64).reshape(2, 3)
     assert fg._arg(t, torch.int32, "ids").dtype == torch.int32
+    assert fg._arg(np.array([-1, (1 << 31) - 1, -(1 << 31)], np.int64), torch.int32, "ids").tolist() \
+        == [-1, (1 << 31) - 1, -(1 << 31)]
+
+
+@pytest.mark.parametrize("v", [1 << 31, (1 << 32) + 3, -(1 << 31) - 1, 1 << 40])
+def test_arg_rejects_ids_that_do_not_fit_int32(v):
+    with pytest.raises(ValueError, match="does not fit in int32"):
+        fg._arg(np.array([[0, v]], np.int64), torch.int32, "ids")
+    with pytest.raises(ValueError, match="does not fit in int32"):
+        fg._arg(torch.tensor([7, v], dtype=torch.int64), torch.int32, "ids")
 
 
 @pytest.mark.parametrize("bad,dtype", [(np.ones((2, 4), np.int32), torch.float32),

@@ -1,7 +1,7 @@
 """The scan kernel's bounded waits: a give-up is counted on the index and marks
 the results it may have touched, never leaving silently wrong ids.
 
-Give-ups are forced from the host only (fgpu_debug_set_spin_limit): every
+Give-ups are forced from the host only (the index's FGPU_OPT_SPIN_LIMIT): every
 wave still runs to the end of the kernel, and the kernel clamps every list
 range it reads from LDS to the index, so its loads stay in bounds whatever
 the hand-off counters say.
@@ -48,13 +48,11 @@ def test_forced_give_ups_are_counted_and_mark_results():
     dq, dp, dpd = (torch.from_numpy(q).cuda(), torch.from_numpy(probes.view(np.int32)).cuda(),
                    torch.from_numpy(pdist).cuda())
     assert idx.faults() == 0
-    try:
-        fg.debug_set_spin_limit(1)
-        gid, gd = idx.adc_search(dq, dp, k, probe_dists=dpd)
-        gid, gd = gid.cpu().numpy(), gd.cpu().numpy()
-        nf = idx.faults()
-    finally:
-        fg.debug_set_spin_limit(0)
+    idx.set_option(fg.Index.OPT_SPIN_LIMIT, 1)
+    gid, gd = idx.adc_search(dq, dp, k, probe_dists=dpd)
+    gid, gd = gid.cpu().numpy(), gd.cpu().numpy()
+    nf = idx.faults()
+    idx.set_option(fg.Index.OPT_SPIN_LIMIT, 0)
     assert nf > 0, "a poll limit of 1 must make waits give up"
     with pytest.raises(fg.FgpuError) as e:
         idx.check()
@@ -78,8 +76,9 @@ def test_forced_give_ups_are_counted_and_mark_results():
 
 
 def test_forced_give_ups_with_dynamic_query_claims():
-    """search (coarse, then the scan with queries claimed from a counter):
-    rows a give-up kept from completing keep the marker written at set-up."""
+    """search on the LUT kernels (coarse, then the flow scan with queries
+    claimed from a counter): rows a give-up kept from completing keep the
+    marker written at set-up; another index is unaffected by the option."""
     _say("faults: dynamic claims, spin limit 1")
     rng = np.random.default_rng(73)
     dim, m, nlist, nq, k = 128, 32, 48, 3000, 10
@@ -88,14 +87,13 @@ def test_forced_give_ups_with_dynamic_query_claims():
     probes, _ = oracle.coarse(q, cent, 12)
     oid, od = oracle.search_plain(q, cent, cb, offs, ids, lc, probes, k)
     idx = fg.Index.from_arrays(dim, m, offs, ids, lc, cent, cb)
+    idx.set_option(fg.Index.OPT_SCREEN, 0)  # the LUT flow kernel, whose waits this test forces to give up
     dq = torch.from_numpy(q).cuda()
-    try:
-        fg.debug_set_spin_limit(1)
-        gid, gd = idx.search(dq, 12, k)
-        gid, gd = gid.cpu().numpy(), gd.cpu().numpy()
-        nf = idx.faults(reset=True)
-    finally:
-        fg.debug_set_spin_limit(0)
+    idx.set_option(fg.Index.OPT_SPIN_LIMIT, 1)
+    gid, gd = idx.search(dq, 12, k)
+    gid, gd = gid.cpu().numpy(), gd.cpu().numpy()
+    nf = idx.faults(reset=True)
+    idx.set_option(fg.Index.OPT_SPIN_LIMIT, 0)
     assert nf > 0
     marked = np.all(gid == fg.FAULT_ID, axis=1)
     assert marked.any()
@@ -107,6 +105,16 @@ def test_forced_give_ups_with_dynamic_query_claims():
     assert np.array_equal(gid.cpu().numpy(), oid)
     assert np.array_equal(gd.cpu().numpy().view(np.uint32), od.view(np.uint32))
     idx.check()
+    # The option belongs to its index: a second index over the same arrays
+    # keeps the automatic limit while the first one forces give-ups.
+    other = fg.Index.from_arrays(dim, m, offs, ids, lc, cent, cb)
+    other.set_option(fg.Index.OPT_SCREEN, 0)
+    idx.set_option(fg.Index.OPT_SPIN_LIMIT, 1)
+    gid, gd = other.search(dq, 12, k)
+    assert np.array_equal(gid.cpu().numpy(), oid)
+    assert np.array_equal(gd.cpu().numpy().view(np.uint32), od.view(np.uint32))
+    assert other.faults() == 0
+    other.close()
     idx.close()
 
 

@@ -143,13 +143,11 @@ def test_two_phase_split_phase1_equals_one_workgroup(dim, m, p1, limit_k, coeff,
     idx = fg.Index.from_arrays(dim, m, offs, ids, lc, cent, cb)
     dq, dp = torch.from_numpy(q).cuda(), torch.from_numpy(probes.view(np.int32)).cuda()
     outs = {}
-    try:
-        for split in (1, 2, 3, 7, 64):
-            fg.debug_set_two_phase_split(split)
-            gid, gd, gcnt, gcut, gthr = idx.two_phase_search(dq, dp, p1, limit_k, coeff, rerank_m, want_cutoffs=True)
-            outs[split] = (_host(gid), _bits(_host(gd)), _host(gcnt), _bits(_host(gcut)), _bits(_host(gthr)))
-    finally:
-        fg.debug_set_two_phase_split(0)
+    for split in (1, 2, 3, 7, 64):
+        idx.set_option(fg.Index.OPT_TWO_PHASE_SPLIT, split)
+        gid, gd, gcnt, gcut, gthr = idx.two_phase_search(dq, dp, p1, limit_k, coeff, rerank_m, want_cutoffs=True)
+        outs[split] = (_host(gid), _bits(_host(gd)), _host(gcnt), _bits(_host(gcut)), _bits(_host(gthr)))
+    idx.set_option(fg.Index.OPT_TWO_PHASE_SPLIT, 0)
     for split in (2, 3, 7, 64):
         for a, b in zip(outs[1], outs[split]):
             assert np.array_equal(a, b), f"split {split} differs"
@@ -206,13 +204,10 @@ def test_rerank_bit_exact(dim, k, mb, eps, beta, spec):
     cand[4, 20] = cand[4, 2]             # a duplicate candidate
     counts = rng.integers(0, rm + 1, nq).astype(np.int32)
     counts[:6] = [rm, rm, 0, rm, rm, 1]
-    fg.debug_set_rerank_spec(spec)
-    try:
-        gid, gd, gvis = fg.rerank(torch.from_numpy(q).cuda(), torch.from_numpy(base).cuda(),
-                                  torch.from_numpy(cand).cuda(), torch.from_numpy(counts).cuda(), k, mb, eps, beta)
-        torch.cuda.synchronize()
-    finally:
-        fg.debug_set_rerank_spec(0)
+    gid, gd, gvis = fg.rerank(torch.from_numpy(q).cuda(), torch.from_numpy(base).cuda(),
+                              torch.from_numpy(cand).cuda(), torch.from_numpy(counts).cuda(), k, mb, eps, beta,
+                              spec=spec)
+    torch.cuda.synchronize()
     oid, od, ovis = oracle.rerank(q, base, cand, counts, k, mb, eps, beta)
     gid, gd, gvis = _host(gid), _host(gd), _host(gvis)
     assert np.array_equal(gvis, ovis), np.nonzero(gvis != ovis)[0][:5]
