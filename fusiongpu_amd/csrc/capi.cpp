@@ -362,7 +362,8 @@ namespace {
 fgpu_status coarse_search(const fgpu_index* ix, const float* dq, int nq, int nprobe, float prune_ratio,
                           uint32_t* d_ids, float* d_dists, void* ws, size_t ws_bytes, void* stream, int* side,
                           int side_val) {
-  FGPU_CHECK(ix && dq && d_ids && d_dists && ws, FGPU_ERR_ARG, "coarse_search: null argument");
+  // An empty batch may come with empty (null) arrays.
+  FGPU_CHECK(ix && ws && (nq == 0 || (dq && d_ids && d_dists)), FGPU_ERR_ARG, "coarse_search: null argument");
   FGPU_CHECK(((uintptr_t)ws & 15) == 0, FGPU_ERR_ARG, "coarse_search: workspace must be 16-byte aligned");
   FGPU_CHECK(nq >= 0 && nprobe >= 1 && nprobe <= ix->nlist && nprobe <= 256, FGPU_ERR_ARG,
              "coarse_search: need 1 <= nprobe <= min(nlist, 256)");
@@ -414,7 +415,8 @@ fgpu_status fgpu_probe_counts(const fgpu_index* ix, const uint32_t* d_probe_ids,
 fgpu_status fgpu_adc_search(const fgpu_index* ix, const float* dq, int nq, const uint32_t* d_probe_ids,
                             const float* d_probe_dists, int nprobe, int k, int32_t* d_out_ids, float* d_out_dists,
                             void* stream) {
-  FGPU_CHECK(ix && dq && d_probe_ids && d_out_ids && d_out_dists, FGPU_ERR_ARG, "adc_search: null argument");
+  FGPU_CHECK(ix && (nq == 0 || (dq && d_probe_ids && d_out_ids && d_out_dists)), FGPU_ERR_ARG,
+             "adc_search: null argument");
   FGPU_CHECK(nq >= 0 && nprobe >= 1 && k >= 1, FGPU_ERR_ARG, "adc_search: bad sizes");
   FGPU_CHECK(adc_supported(ix->dim, ix->m), FGPU_ERR_UNSUPPORTED, "adc_search: no kernel for this (dim, pq_m)");
   AdcArgs a = adc_args(ix, dq, nq, d_probe_ids, d_probe_dists, nprobe, k, d_out_ids, d_out_dists);
@@ -424,7 +426,7 @@ fgpu_status fgpu_adc_search(const fgpu_index* ix, const float* dq, int nq, const
 fgpu_status fgpu_adc_search_stats(const fgpu_index* ix, const float* dq, int nq, const uint32_t* d_probe_ids,
                                   const float* d_probe_dists, int nprobe, int k, int32_t* d_out_ids,
                                   float* d_out_dists, unsigned long long* d_stats, void* stream) {
-  FGPU_CHECK(ix && dq && d_probe_ids && d_out_ids && d_out_dists && d_stats, FGPU_ERR_ARG,
+  FGPU_CHECK(ix && d_stats && (nq == 0 || (dq && d_probe_ids && d_out_ids && d_out_dists)), FGPU_ERR_ARG,
              "adc_search_stats: null argument");
   FGPU_CHECK(nq >= 0 && nprobe >= 1 && k >= 1, FGPU_ERR_ARG, "adc_search_stats: bad sizes");
   FGPU_CHECK(adc_supported(ix->dim, ix->m), FGPU_ERR_UNSUPPORTED, "adc_search_stats: no kernel for this (dim, pq_m)");
@@ -623,7 +625,7 @@ fgpu_status two_phase(const fgpu_index* ix, const float* dq, int nq, const uint3
                       int p1_lists, int limit_k, float threshold_coeff, int rerank_m, int32_t* d_top_ids,
                       float* d_top_dists, int32_t* d_top_counts, float* d_list_cutoffs, float* d_thresholds,
                       unsigned long long* d_stats, void* ws, size_t ws_bytes, void* stream) {
-  FGPU_CHECK(ix && dq && d_probe_ids && d_top_ids && d_top_dists && d_top_counts && ws, FGPU_ERR_ARG,
+  FGPU_CHECK(ix && ws && (nq == 0 || (dq && d_probe_ids && d_top_ids && d_top_dists && d_top_counts)), FGPU_ERR_ARG,
              "two_phase_search: null argument");
   FGPU_CHECK(nq >= 0 && nprobe >= 1 && nprobe <= 256, FGPU_ERR_ARG, "two_phase_search: need 1 <= nprobe <= 256");
   FGPU_CHECK(limit_k >= 1 && rerank_m >= 1, FGPU_ERR_ARG, "two_phase_search: limit_k and rerank_m must be >= 1");
@@ -688,7 +690,7 @@ fgpu_status fgpu_rerank_spec(const float* dq, int nq, int dim, const float* d_ba
                              const int32_t* d_top_ids, const int32_t* d_top_counts, int rerank_m, int k,
                              int mini_batch, float eps, int beta, int32_t* d_final_ids, float* d_final_dists,
                              int32_t* d_visited, int spec, void* stream) {
-  FGPU_CHECK(dq && d_base && d_top_ids && d_top_counts && d_final_ids && d_final_dists, FGPU_ERR_ARG,
+  FGPU_CHECK(d_base && (nq == 0 || (dq && d_top_ids && d_top_counts && d_final_ids && d_final_dists)), FGPU_ERR_ARG,
              "rerank: null argument");
   FGPU_CHECK(nq >= 0 && n >= 0 && rerank_m >= 1 && k >= 1 && mini_batch >= 1, FGPU_ERR_ARG, "rerank: bad sizes");
   FGPU_CHECK(((uintptr_t)d_base & 15) == 0 && ((uintptr_t)dq & 15) == 0, FGPU_ERR_ARG,
@@ -736,7 +738,7 @@ size_t fgpu_l2_topk_workspace_bytes(int64_t n, int nc) {
 
 fgpu_status fgpu_l2_topk(const float* dx, int64_t n, const float* dc, int nc, int dim, int p, int32_t* d_ids,
                          float* d_dists, void* ws, size_t ws_bytes, void* stream) {
-  FGPU_CHECK(dx && dc && d_ids && d_dists && ws, FGPU_ERR_ARG, "l2_topk: null argument");
+  FGPU_CHECK(dc && ws && (n == 0 || (dx && d_ids && d_dists)), FGPU_ERR_ARG, "l2_topk: null argument");
   FGPU_CHECK(((uintptr_t)ws & 15) == 0, FGPU_ERR_ARG, "l2_topk: workspace must be 16-byte aligned");
   FGPU_CHECK(n >= 0 && nc >= 1 && dim >= 1 && p >= 1 && p <= nc && p <= 256, FGPU_ERR_ARG, "l2_topk: bad sizes");
   if (n == 0) return FGPU_OK;
@@ -782,7 +784,7 @@ size_t fgpu_knn_exact_workspace_bytes(int nq, int64_t n) {
 
 fgpu_status fgpu_knn_exact(const float* dq, int nq, const float* d_base, int64_t n, int dim, int k, int32_t* d_ids,
                            float* d_dists, void* ws, size_t ws_bytes, void* stream) {
-  FGPU_CHECK(dq && d_base && d_ids && d_dists && ws, FGPU_ERR_ARG, "knn_exact: null argument");
+  FGPU_CHECK(d_base && ws && (nq == 0 || (dq && d_ids && d_dists)), FGPU_ERR_ARG, "knn_exact: null argument");
   FGPU_CHECK(nq >= 0 && n >= 1 && n < INT32_MAX && k >= 1 && k <= 128, FGPU_ERR_ARG,
              "knn_exact: need 1 <= k <= 128 and 1 <= n < 2^31");
   FGPU_CHECK(dim >= 4 && dim <= 256 && dim % 4 == 0, FGPU_ERR_UNSUPPORTED,
@@ -816,7 +818,8 @@ fgpu_status fgpu_knn_exact(const float* dq, int nq, const float* d_base, int64_t
 fgpu_status fgpu_graph_search(const float* dq, int nq, const float* d_base, int64_t n, int dim, const int32_t* d_graph,
                               int degree, int itopk, int width, int max_iter, int k, uint64_t seed, int32_t* d_out_ids,
                               float* d_out_dists, int32_t* d_iters, int32_t* d_evals, void* stream) {
-  FGPU_CHECK(dq && d_base && d_graph && d_out_ids && d_out_dists, FGPU_ERR_ARG, "graph_search: null argument");
+  FGPU_CHECK(d_base && d_graph && (nq == 0 || (dq && d_out_ids && d_out_dists)), FGPU_ERR_ARG,
+             "graph_search: null argument");
   FGPU_CHECK(nq >= 0, FGPU_ERR_ARG, "graph_search: nq must be >= 0");
   FGPU_CHECK(((uintptr_t)d_base & 15) == 0, FGPU_ERR_ARG, "graph_search: base vectors must be 16-byte aligned");
   GraphArgs a{dq, d_base, (long long)n, d_graph, degree, itopk, width, max_iter, k, seed, 0, nq,
@@ -875,7 +878,8 @@ fgpu_status fgpu_coarse_graph_search(const fgpu_index* ix, const float* dq, int 
                                      const int32_t* d_graph, int degree, int itopk, int width, int max_iter,
                                      uint64_t seed, float prune_ratio, uint32_t* d_probe_ids, float* d_probe_dists,
                                      void* stream) {
-  FGPU_CHECK(ix && dq && d_graph && d_probe_ids && d_probe_dists, FGPU_ERR_ARG, "coarse_graph_search: null argument");
+  FGPU_CHECK(ix && d_graph && (nq == 0 || (dq && d_probe_ids && d_probe_dists)), FGPU_ERR_ARG,
+             "coarse_graph_search: null argument");
   FGPU_CHECK(nq >= 0 && first_query >= 0 && nprobe >= 1 && nprobe <= ix->nlist && nprobe <= itopk, FGPU_ERR_ARG,
              "coarse_graph_search: need first_query >= 0 and 1 <= nprobe <= min(nlist, itopk)");
   if (nq == 0) return FGPU_OK;

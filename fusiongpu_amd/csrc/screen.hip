@@ -518,9 +518,10 @@ __global__ __launch_bounds__(kSW * kWave) void screen_kernel(ScreenArgs a) {
       for (int c = 0; c < NC; ++c) A[c] = frag_of(0u, 0u, 0u, 0u);
     }
     const bf16x8 Aex = frag_of(ex[0], ex[1], ex[2], ex[3]);
-    // The query of each row, for the candidate flush and the round-1 fold
-    // (which skips inactive rows: their values bound nothing).
-    if (h == 0) rowq[li] = ROUND == 1 && !active ? -1 : qi;
+    // The query of each row, for the candidate flush and the round-1 store:
+    // -1 for a row without a query; in round 1, -2 - q for an inactive row of
+    // query q (its values bound nothing: it stores +inf, so q gets no T).
+    if (h == 0) rowq[li] = ROUND == 1 && !active && qi >= 0 ? -2 - qi : qi;
 
     // Per row and lane column, the smallest U bits seen (ROUND 1; every U is
     // >= 0, where float order is unsigned order).
@@ -612,7 +613,8 @@ __global__ __launch_bounds__(kSW * kWave) void screen_kernel(ScreenArgs a) {
       for (int r = 0; r < 16; ++r) {
         const int row = 8 * (r >> 2) + 4 * h + (r & 3);
         const int q = rowq[row];
-        if (q >= 0) a.gminbuf[((size_t)q * kMaxChunks + cidx) * 32 + li] = mins[r];
+        if (q != -1)
+          a.gminbuf[((size_t)(q >= 0 ? q : -2 - q) * kMaxChunks + cidx) * 32 + li] = q >= 0 ? mins[r] : 0x7F800000u;
       }
     }
     wave_sync();
