@@ -7,21 +7,30 @@ k=10.  The index is built in-run by this framework's GPU build path (k-means++
 seeding, 20 Lloyd iterations, PQ 15 iterations on a 50k sample); that build is
 not timed.
 
-One step = one full search of the 10k-query batch with queries already in HBM:
-coarse quantizer (MFMA GEMM + exact re-score + top-32) and LUT + ADC scan +
-top-10.  value = 10k / step time.  The roofline entry is for the dominant
-kernel, the ADC scan: achieved = the code and id bytes of the lists it reads
-(its own load count), divided by its average duration from HIP events recorded
-on the stream it runs on; `traffic` is the copy-calibrated FETCH_SIZE +
-WRITE_SIZE from profiles/.  The scan's exact list bound skips most probed
-lists, so the work-equivalent figure (the code bytes of every probed list, once
-per (query, list)) is reported apart as `effective`, and `no_skip` times the
-same kernel reading every probed list.  `measured_read_peak_gbs` is a streaming read of 4 GiB.
-`end_to_end` follows the reference's QPS definition (H2D + search + D2H).  The
-line also carries `graph_coarse`: the same coarse step done the reference's way
-(a graph walk over the centroids instead of the exact GEMM; not timed in
-`value`), with its time, the share of the exact top-32 lists it finds and how
-often the top-10 stays identical.
+One step = one fgpu_search of the 10k-query batch with queries already in
+HBM: coarse quantizer (MFMA GEMM + exact re-score + top-32), then the MFMA
+screen (bf16 distance bounds: a threshold per query from its first list, then
+every probed list whose bound can reach it) and the exact rescore of the
+candidates with the reference's LUT arithmetic, top-10; queries the screen
+hands over run the LUT + ADC scan.  value = 10k / step time.  `stages_ms`
+holds HIP events fgpu_search records between its kernels on its own stream.
+
+The roofline entry is for the step's longest kernel, a screen round: achieved
+= its algorithmic flops (2 (dim + 16) per (query, vector) pair it screens) over
+its event-timed duration, against the dense bf16 MFMA peak; `traffic` is the
+copy-calibrated FETCH_SIZE + WRITE_SIZE from profiles/.  `adc_scan` is the
+metric's ADC-scan HBM GB/s: the LUT + ADC scan kernel timed on the same probes
+with HIP events on its stream, achieved = the code and id bytes of the lists
+it reads (its own load count); its exact list bound skips most probed lists,
+so the work-equivalent figure (the code bytes of every probed list, once per
+(query, list)) is reported apart as `effective`, and `no_skip` times the same
+kernel reading every probed list.  `measured_read_peak_gbs` is a streaming
+read of 4 GiB.  `end_to_end` follows the reference's QPS definition (H2D +
+search + D2H), on one stream and on two alternating streams.  The line also
+carries `graph_coarse`: the same coarse step done the reference's way (a graph
+walk over the centroids instead of the exact GEMM; not timed in `value`), with
+its time, the share of the exact top-32 lists it finds and how often the
+top-10 stays identical.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--cpu-queries N] [--workload c2|c3|c4|c5]
 
@@ -61,8 +70,10 @@ sys.path.insert(0, ROOT)
 METRIC = "QPS at fixed nprobe, 1M×128 IVF-PQ k=10 (1 GPU); ADC-scan HBM GB/s vs peak"
 HBM_PEAK_GBS = 8000.0
 FP32_MFMA_PEAK_TFLOPS = 157.3
+BF16_MFMA_PEAK_TFLOPS = 2500.0
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "adc_flow_c2_traffic.txt")
 TRAFFIC_FILE_C3 = os.path.join(ROOT, "profiles", "two_phase_c3_traffic.txt")
+SCREEN_TRAFFIC_FILE = os.path.join(ROOT, "profiles", "screen_c2_traffic.txt")
 
 
 def log(msg):
@@ -185,7 +196,7 @@ def main():
            torch.empty((args.nq, k), dtype=torch.float32, device=dev))
     stream = torch.cuda.current_stream()
 
-    # ---- whole-path timing (the metric)
+    # ---- whole-path timing (the metric): fgpu_search = coarse step, MFMA screen, exact rescore
     for _ in range(args.warmup):
         idx.search(dq, nprobe, k, workspace=ws, out=out)
     torch.cuda.synchronize()
@@ -196,71 +207,134 @@ def main():
     wall = time.perf_counter() - t0
     ms_per_step = 1e3 * wall / args.steps
     qps = args.nq / (wall / args.steps)
-    log(f"search: {ms_per_step:.3f} ms/step, {qps:,.0f} QPS")
+    log(f"search: {ms_per_step:.3f} ms/step, {qps:,.0f} QPS (screen path: {idx.screen_ready})")
 
-    # ---- stage timing with HIP events on the launch stream
+    # ---- per-stage times: HIP events fgpu_search records on its own stream between its kernels
+    reps = max(args.steps, 5)
+    idx.set_option(fg.Index.OPT_STAGE_EVENTS, 1)
+    stage_ms = {kk: 0.0 for kk in fg.Index.STAGES}
+    for _ in range(reps):
+        idx.search(dq, nprobe, k, workspace=ws, out=out)
+        for kk, v in idx.search_stage_times().items():
+            stage_ms[kk] += v / reps
+    idx.set_option(fg.Index.OPT_STAGE_EVENTS, 0)
+    sst = idx.search_screen_stats(args.nq, nprobe, ws)
+    log("stages (ms): " + ", ".join(f"{kk} {v:.4f}" for kk, v in stage_ms.items()))
+    log(f"screen: {sst['pairs_round2']} (query, list) pairs in round 2 over {sst['lists_round2']} lists, "
+        f"{sst['candidates'] / args.nq:.1f} candidates a query (max {sst['max_candidates']}), "
+        f"{sst['queries_to_lut_kernel']} queries to the LUT kernel")
+    # The roofline kernel: the larger screen round (both are screen_kernel<128,32,round>).  Its
+    # algorithmic work is the bound GEMM, 2 (dim + 16) flops per (query, vector) pair screened; the
+    # MFMA tiles it runs pad each list's queries to 32 rows.
+    rnd = 2 if stage_ms["screen_round2"] >= stage_ms["screen_round1"] else 1
+    scr_ms = stage_ms[f"screen_round{rnd}"]
+    scr_flop = 2.0 * (dim + 16) * sst[f"vector_pairs_round{rnd}"]
+    scr_exec_flop = 2.0 * (dim + 16) * 32 * 32 * sst[f"tiles_round{rnd}"]
+    scr_bytes = sst[f"tiles_round{rnd}"] * 32 * (m + 16)  # codes + 16-byte extra block of each vector row read
+    scr_tflops = scr_flop / (scr_ms * 1e-3) / 1e12
+    log(f"screen round {rnd}: {scr_ms:.4f} ms, {scr_flop / 1e9:.2f} GFLOP algorithmic ({scr_tflops:.1f} TFLOP/s), "
+        f"{scr_exec_flop / 1e9:.2f} GFLOP in MFMA tiles, {scr_bytes / 1e6:.1f} MB of codes + blocks read")
+
+    # ---- the LUT scan (the fallback kernel; what fgpu_adc_search runs), timed on its own
     probes, pd = idx.coarse_search(dq, nprobe)
     cnt, _ = fg.probe_counts(idx, probes)
     n_probed_vecs = int(cnt.to(torch.int64).sum().item())
     adc_bytes = n_probed_vecs * m  # code bytes of every probed list, once per (query, list)
     pruned = int((probes == -1).sum().item())
-    reps = max(args.steps, 5)
     coarse_ms = timed_ms(torch, stream, reps, lambda: idx.coarse_search(dq, nprobe, workspace=ws))
-    adc_ms = timed_ms(torch, stream, reps, lambda: idx.adc_search(dq, probes, k, out=out, probe_dists=pd))
+    lut_out = (torch.empty_like(out[0]), torch.empty_like(out[1]))
+    adc_ms = timed_ms(torch, stream, reps, lambda: idx.adc_search(dq, probes, k, out=lut_out, probe_dists=pd))
+    assert torch.equal(lut_out[0], out[0]) and torch.equal(lut_out[1], out[1]), "LUT scan and screen path differ"
     gemm_flop = 2.0 * args.nq * nlist * dim
-    log(f"coarse {coarse_ms:.3f} ms ({gemm_flop / coarse_ms / 1e9:.1f} TFLOP/s incl. select), adc {adc_ms:.3f} ms; "
-        f"{pruned} of {args.nq * nprobe} probes pruned (prune_ratio 100)")
-    # What the scan moves: the codes and ids of the lists it does not skip
-    # (the exact list bound skips lists that cannot reach the top-k).
+    log(f"coarse {coarse_ms:.3f} ms ({gemm_flop / coarse_ms / 1e9:.1f} TFLOP/s incl. select), LUT scan "
+        f"{adc_ms:.3f} ms; {pruned} of {args.nq * nprobe} probes pruned (prune_ratio 100)")
+    # What the LUT scan moves: the codes and ids of the lists it does not skip.
     sid, sd, st = idx.adc_search_stats(dq, probes, k, probe_dists=pd)
     assert torch.equal(sid, out[0]) and torch.equal(sd, out[1]), "instrumented scan differs"
     loaded_bytes = st["vectors_loaded"] * (m + 4)  # code bytes + the 4-byte vector id loaded with them
     loaded_gbs = loaded_bytes / (adc_ms * 1e-3) / 1e9
     eff_gbs = adc_bytes / (adc_ms * 1e-3) / 1e9
-    log("adc clocks per query: " + ", ".join(f"{kk} {st[kk] / args.nq:.0f}" for kk in
-                                                ("clk_setup", "clk_builder", "clk_scanner", "clk_total")))
-    log(f"adc moves {st['vectors_loaded'] * m / 1e9:.2f} GB of codes (+ids {st['vectors_loaded'] * 4 / 1e9:.2f} GB) "
-        f"= {loaded_gbs:.0f} GB/s; LUTs built {st['luts_built']}, probed lists skipped {st['lists_skipped']} "
+    log("LUT scan clocks per query: " + ", ".join(f"{kk} {st[kk] / args.nq:.0f}" for kk in
+                                                     ("clk_setup", "clk_builder", "clk_scanner", "clk_total")))
+    log(f"LUT scan moves {st['vectors_loaded'] * m / 1e9:.2f} GB of codes (+ids {st['vectors_loaded'] * 4 / 1e9:.2f}"
+        f" GB) = {loaded_gbs:.0f} GB/s; LUTs built {st['luts_built']}, probed lists skipped {st['lists_skipped']} "
         f"of {int((probes != -1).sum().item())}; every probed list once would be {adc_bytes / 1e9:.2f} GB "
         f"({eff_gbs:.0f} GB/s work-equivalent)")
     # The same scan with the list bound off: it reads every probed list.
     idx.set_option(fg.Index.OPT_LIST_SKIP, 0)
     nid, nd = idx.adc_search(dq, probes, k, probe_dists=pd)
-    ns_ms = timed_ms(torch, stream, reps, lambda: idx.adc_search(dq, probes, k, out=out, probe_dists=pd))
+    ns_ms = timed_ms(torch, stream, reps, lambda: idx.adc_search(dq, probes, k, out=lut_out, probe_dists=pd))
     idx.set_option(fg.Index.OPT_LIST_SKIP, 1)
     assert torch.equal(nid, sid) and torch.equal(nd, sd), "the scan without list skipping differs"
     ns_bytes = n_probed_vecs * (m + 4)
     ns_gbs = ns_bytes / (ns_ms * 1e-3) / 1e9
-    log(f"adc without list skipping: {ns_ms:.3f} ms, {ns_bytes / 1e9:.2f} GB (codes + ids of every probed list) "
-        f"= {ns_gbs:.0f} GB/s; ids identical")
+    log(f"LUT scan without list skipping: {ns_ms:.3f} ms, {ns_bytes / 1e9:.2f} GB (codes + ids of every probed "
+        f"list) = {ns_gbs:.0f} GB/s; ids identical")
     assert idx.faults() == 0, "a bounded wait of the scan gave up"
     peak_gbs = stream_read_peak(torch, fg, dev)
     log(f"measured stream-read rate: {peak_gbs:.0f} GB/s (16-byte loads over 4 GiB)")
 
     # ---- end to end, the reference's QPS definition (search_pipeline.cu:621-636): queries
-    # from pinned host memory, search, results back to pinned host memory, all steps enqueued
-    hq = torch.empty((args.nq, dim), dtype=torch.float32, pin_memory=True)
-    hq.copy_(torch.from_numpy(q))
-    hid = torch.empty((args.nq, k), dtype=torch.int32, pin_memory=True)
-    hdd = torch.empty((args.nq, k), dtype=torch.float32, pin_memory=True)
-    dq2 = torch.empty_like(dq)
+    # from pinned host memory, search, results back to pinned host memory, all steps enqueued.
+    # Serial: every step on one stream.  Two streams: steps alternate between two streams, each
+    # with its own buffers, so one step's copies can run beside the other's search (the
+    # reference's multi-stream pipeline, search_pipeline.cu:168-214, 311-377).
+    def e2e_bufs():
+        b = {"hq": torch.empty((args.nq, dim), dtype=torch.float32, pin_memory=True),
+             "hid": torch.empty((args.nq, k), dtype=torch.int32, pin_memory=True),
+             "hdd": torch.empty((args.nq, k), dtype=torch.float32, pin_memory=True),
+             "dq": torch.empty_like(dq), "ws": torch.empty_like(ws),
+             "out": (torch.empty_like(out[0]), torch.empty_like(out[1]))}
+        b["hq"].copy_(torch.from_numpy(q))
+        return b
 
-    def e2e_step():
-        dq2.copy_(hq, non_blocking=True)
-        idx.search(dq2, nprobe, k, workspace=ws, out=out)
-        hid.copy_(out[0], non_blocking=True)
-        hdd.copy_(out[1], non_blocking=True)
+    def e2e_step(b, ev=None):
+        if ev:
+            ev[0].record()
+        b["dq"].copy_(b["hq"], non_blocking=True)
+        if ev:
+            ev[1].record()
+        idx.search(b["dq"], nprobe, k, workspace=b["ws"], out=b["out"])
+        if ev:
+            ev[2].record()
+        b["hid"].copy_(b["out"][0], non_blocking=True)
+        b["hdd"].copy_(b["out"][1], non_blocking=True)
+        if ev:
+            ev[3].record()
 
+    bufs = [e2e_bufs(), e2e_bufs()]
     for _ in range(2):
-        e2e_step()
+        e2e_step(bufs[0])
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(args.steps):
-        e2e_step()
+        e2e_step(bufs[0])
     torch.cuda.synchronize()
     e2e_ms = 1e3 * (time.perf_counter() - t0) / args.steps
-    assert torch.equal(hid, out[0].cpu()), "end-to-end results differ"
-    log(f"end to end (H2D queries + search + D2H results): {e2e_ms:.3f} ms/step, {args.nq / e2e_ms * 1e3:,.0f} QPS")
+    assert torch.equal(bufs[0]["hid"], out[0].cpu()), "end-to-end results differ"
+    # where a serial step's time goes: events on its stream around the copies and the search
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+    part = [0.0, 0.0, 0.0]
+    for _ in range(reps):
+        e2e_step(bufs[0], evs)
+        evs[3].synchronize()
+        for t in range(3):
+            part[t] += evs[t].elapsed_time(evs[t + 1]) / reps
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        with torch.cuda.stream(streams[i % 2]):
+            e2e_step(bufs[i % 2])
+    torch.cuda.synchronize()
+    e2e2_ms = 1e3 * (time.perf_counter() - t0) / args.steps
+    for b in bufs:
+        assert torch.equal(b["hid"], out[0].cpu()) and torch.equal(b["hdd"], out[1].cpu()), \
+            "end-to-end results differ"
+    h2d_gbs = args.nq * dim * 4 / (part[0] * 1e-3) / 1e9
+    log(f"end to end (H2D queries + search + D2H results): {e2e_ms:.3f} ms/step serial "
+        f"(H2D {part[0]:.4f} ms = {h2d_gbs:.1f} GB/s, search {part[1]:.4f}, D2H {part[2]:.4f}); "
+        f"{e2e2_ms:.3f} ms/step on two streams, {args.nq / e2e2_ms * 1e3:,.0f} QPS")
 
     # ---- the graph coarse mode (the reference's CAGRA-over-centroids step): time and
     # how many of the exact top-nprobe lists it finds, and the end-to-end top-10 it gives;
@@ -335,12 +409,30 @@ def main():
                                "10k queries in one batch, nprobe=32, k=10",
                    "n": args.n, "dim": dim, "nlist": nlist, "pq_m": m, "nq": args.nq, "nprobe": nprobe, "k": k,
                    "prune_ratio": 100.0, "probes_pruned": pruned, "probes_total": args.nq * nprobe},
-        "roofline": {"bound": "hbm", "kernel": "adc_flow_kernel<128,32>", "achieved": round(loaded_gbs, 1),
+        "roofline": {"bound": "mfma", "kernel": f"screen_kernel<128,32,{rnd}> (screen round {rnd})",
+                     "achieved": round(scr_tflops, 2), "peak": BF16_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(scr_tflops / BF16_MFMA_PEAK_TFLOPS, 4),
+                     "traffic": read_traffic(SCREEN_TRAFFIC_FILE, f"traffic_bytes_per_launch_round{rnd}"),
+                     "avg_launch_ms": round(scr_ms, 4), "flop_per_launch": scr_flop,
+                     "mfma_tile_flop_per_launch": scr_exec_flop,
+                     "mfma_tile_frac": round(scr_exec_flop / (scr_ms * 1e-3) / 1e12 / BF16_MFMA_PEAK_TFLOPS, 4),
+                     "bytes_read_per_launch": scr_bytes,
+                     "hbm_gbs": round(scr_bytes / (scr_ms * 1e-3) / 1e9, 1),
+                     "note": "the step's longest kernel: bf16 MFMA distance bounds of (query, vector) pairs; "
+                             "achieved = 2 (dim + 16) flops per pair screened (the bound GEMM, K = dim plus a "
+                             "16-wide block of constants) / its event-timed duration, against the dense bf16 "
+                             "peak; mfma_tile_frac counts the 32 x 32 tiles it runs (a list's queries padded to "
+                             "32 rows); bytes_read = codes + 16-byte block of each vector row a tile reads; "
+                             "traffic = copy-calibrated FETCH_SIZE + WRITE_SIZE per launch "
+                             "(profiles/screen_c2_traffic.txt)"},
+        "adc_scan": {"bound": "hbm", "kernel": "adc_flow_kernel<128,32>", "achieved": round(loaded_gbs, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(loaded_gbs / HBM_PEAK_GBS, 4),
                      "traffic": traffic, "bytes_per_launch": loaded_bytes, "avg_launch_ms": round(adc_ms, 4),
-                     "note": "achieved = codes + ids of the lists the scan reads (its own load count in this run) / "
-                             "kernel time; traffic = copy-calibrated FETCH_SIZE + WRITE_SIZE per launch "
-                             "(profiles/adc_flow_c2_traffic.txt)",
+                     "note": "the LUT + ADC scan (fgpu_adc_search; fgpu_search's kernel for the queries the "
+                             "screen hands over, and its whole scan with the screen off), timed on the same "
+                             "probes; achieved = codes + ids of the lists the scan reads (its own load count "
+                             "in this run) / kernel time; traffic = copy-calibrated FETCH_SIZE + WRITE_SIZE per "
+                             "launch (profiles/adc_flow_c2_traffic.txt)",
                      "traffic_rate_gbs": round(traffic / (adc_ms * 1e-3) / 1e9, 1) if traffic else None,
                      "measured_read_peak_gbs": round(peak_gbs, 1),
                      "frac_of_measured_peak": round(loaded_gbs / peak_gbs, 4),
@@ -357,11 +449,26 @@ def main():
                                          "every probed list (32 MB of codes, so mostly from the MALL)"},
                      "clocks_per_query": {kk: round(st[kk] / args.nq) for kk in
                                           ("clk_setup", "clk_builder", "clk_scanner", "clk_total")}},
-        "stages_ms": {"coarse": round(coarse_ms, 4), "adc": round(adc_ms, 4),
-                      "coarse_tflops_incl_select": round(gemm_flop / coarse_ms / 1e9, 2)},
-        "end_to_end": {"ms_per_step": round(e2e_ms, 4), "qps": round(args.nq / e2e_ms * 1e3, 1),
+        "lut_path_ms": {"coarse": round(coarse_ms, 4), "adc_scan": round(adc_ms, 4),
+                        "coarse_tflops_incl_select": round(gemm_flop / coarse_ms / 1e9, 2)},
+        "stages_ms": dict({kk: round(v, 4) for kk, v in stage_ms.items()},
+                          note="HIP events fgpu_search records on its stream between its stages "
+                               "(FGPU_OPT_STAGE_EVENTS), averaged over the stage-timing launches; screen_pairs1 "
+                               "includes the zeroing kernel"),
+        "screen": {kk: sst[kk] for kk in ("pairs_round1", "pairs_round2", "lists_round2", "candidates",
+                                          "max_candidates", "queries_to_lut_kernel", "queries_with_threshold",
+                                          "vector_pairs_round1", "vector_pairs_round2", "tiles_round1",
+                                          "tiles_round2")},
+        "end_to_end": {"ms_per_step": round(min(e2e_ms, e2e2_ms), 4),
+                       "qps": round(args.nq / min(e2e_ms, e2e2_ms) * 1e3, 1),
+                       "serial_ms_per_step": round(e2e_ms, 4), "two_stream_ms_per_step": round(e2e2_ms, 4),
+                       "serial_parts_ms": {"h2d": round(part[0], 4), "search": round(part[1], 4),
+                                           "d2h": round(part[2], 4)},
+                       "h2d_gbs": round(h2d_gbs, 1),
                        "note": "the reference's QPS definition: queries H2D from pinned memory + search + "
-                               "results D2H, every step enqueued, one wait at the end"},
+                               "results D2H, every step enqueued, one wait at the end; ms_per_step is the faster "
+                               "of one stream and two alternating streams; the parts are events around a serial "
+                               "step's copies and search"},
         "cpu_baseline": cpu,
         "parity": parity,
         "graph_coarse": graph_coarse,

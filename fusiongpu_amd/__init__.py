@@ -71,6 +71,7 @@ _SIGS = {
     "fgpu_search_screen_stats": (_i32, [_vp, _i32, _i32, _vp, _sz, _vp, _c.POINTER(_c.c_longlong), _i32]),
     "fgpu_index_screen_ready": (_i32, [_vp]),
     "fgpu_index_set_option": (_i32, [_vp, _i32, _i32]),
+    "fgpu_search_stage_times": (_i32, [_vp, _c.POINTER(_c.c_float), _i32]),
     "fgpu_search_noalloc_max_bytes": (_sz, []),
     "fgpu_search_noalloc_max_rows": (_i32, [_i32, _i32]),
     "fgpu_search_noalloc": (_i32, [_vp, _vp, _i32, _i32, _i32, _f32, _vp, _vp, _vp]),
@@ -615,13 +616,16 @@ class Index:
                                    _dev_ptr(ws), _ws_check(ws), _stream()))
         return ids, d
 
-    OPT_LIST_SKIP, OPT_SPIN_LIMIT, OPT_SCREEN, OPT_SCREEN_CLOCKS, OPT_TWO_PHASE_SPLIT = 1, 2, 3, 4, 5
+    OPT_LIST_SKIP, OPT_SPIN_LIMIT, OPT_SCREEN, OPT_SCREEN_CLOCKS, OPT_TWO_PHASE_SPLIT, OPT_STAGE_EVENTS = \
+        1, 2, 3, 4, 5, 6
+    STAGES = ("coarse", "screen_pairs1", "screen_round1", "screen_pairs2", "screen_round2", "rescore", "lut_kernel")
 
     def set_option(self, option: int, value: int):
         """Per-index option (fgpu_index_set_option): OPT_LIST_SKIP (0 = the LUT scan reads every probed list),
         OPT_SPIN_LIMIT (polls before a flow-kernel wait gives up, 0 = automatic), OPT_SCREEN (0 = fgpu_search
         runs the LUT kernels), OPT_SCREEN_CLOCKS (1 = the screen records shader clocks),
-        OPT_TWO_PHASE_SPLIT (phase-1 workgroups a query: 0 automatic, 1 never, s >= 2).  Results never depend
+        OPT_TWO_PHASE_SPLIT (phase-1 workgroups a query: 0 automatic, 1 never, s >= 2), OPT_STAGE_EVENTS
+        (1 = search records HIP events between its stages, read by search_stage_times).  Results never depend
         on them; they change only this index's later calls."""
         _check(lib.fgpu_index_set_option(self._h, int(option), int(value)))
 
@@ -633,15 +637,22 @@ class Index:
     def search_screen_stats(self, nq: int, nprobe: int, workspace, stream=None) -> dict:
         """Counters of the last search() on `workspace` that took the MFMA screen (fgpu_search_screen_stats;
         waits for the stream)."""
-        st = (_c.c_longlong * 16)()
+        st = (_c.c_longlong * 20)()
         with _on(stream):
             _check(lib.fgpu_search_screen_stats(self._h, nq, nprobe, _dev_ptr(workspace), _ws_check(workspace),
-                                                _stream(), st, 16))
+                                                _stream(), st, 20))
         keys = ("pairs_round1", "lists_round2", "pairs_round2", "candidates", "max_candidates",
                 "queries_to_lut_kernel", "queries_with_threshold", "_",
                 "clk1_pre", "clk1_setup", "clk1_tiles", "clk1_post", "clk2_pre", "clk2_setup", "clk2_tiles",
-                "clk2_post")
+                "clk2_post", "vector_pairs_round1", "vector_pairs_round2", "tiles_round1", "tiles_round2")
         return {kk: int(st[i]) for i, kk in enumerate(keys)}
+
+    def search_stage_times(self) -> dict:
+        """Milliseconds of the last search()'s stages, from the events it recorded on its stream with
+        OPT_STAGE_EVENTS on (fgpu_search_stage_times; waits for them): keys Index.STAGES."""
+        ms = (_c.c_float * len(self.STAGES))()
+        _check(lib.fgpu_search_stage_times(self._h, ms, len(self.STAGES)))
+        return {kk: float(ms[i]) for i, kk in enumerate(self.STAGES)}
 
     def search_noalloc(self, queries, nprobe: int, k: int, prune_ratio: float = 100.0, out=None, stream=None):
         """fgpu_search without a workspace (fgpu_search_noalloc): its scratch is the library's fixed per-GPU

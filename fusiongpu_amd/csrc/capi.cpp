@@ -15,6 +15,10 @@
 #include "common.hpp"
 #include "kernels.hpp"
 
+// Events fgpu_search records with FGPU_OPT_STAGE_EVENTS: before the coarse
+// step, after it, after each of the screen's five stages, after the scan.
+constexpr int kStageEvents = 8;
+
 struct fgpu_index {
   int dim = 0, m = 0, nlist = 0, max_list_len = 0;
   int64_t total = 0;
@@ -39,6 +43,9 @@ struct fgpu_index {
   int opt_screen = 1;
   int opt_screen_clocks = 0;
   int opt_two_phase_split = 0;
+  // FGPU_OPT_STAGE_EVENTS: events fgpu_search records between its stages.
+  int opt_stage_events = 0;
+  hipEvent_t stage_ev[kStageEvents] = {};
 };
 
 namespace fgpu {
@@ -79,6 +86,8 @@ void free_index(fgpu_index* ix) {
   for (void* p : {(void*)ix->d_cnorm, (void*)ix->d_cnorm_max, (void*)ix->d_rmax, (void*)ix->d_faults,
                   (void*)ix->d_cb16, (void*)ix->d_vext})
     if (p) (void)hipFree(p);
+  for (hipEvent_t e : ix->stage_ev)
+    if (e) (void)hipEventDestroy(e);
   delete ix;
 }
 
@@ -150,6 +159,7 @@ constexpr int kScreenCandCap = 512;  // candidates kept per query before it take
 struct ScreenWs {
   int* zero = nullptr;  // [zero_words(nq, nlist)]
   int* bucket = nullptr;
+  uint4* arec = nullptr;
   float* thr = nullptr;
   uint2* cand = nullptr;
   int* flist = nullptr;
@@ -157,10 +167,12 @@ struct ScreenWs {
   uint32_t* gminbuf = nullptr;
   static size_t zero_words(int nq, int nlist) { return (size_t)kCtrCount + 2 * (size_t)nlist + (size_t)nq; }
   static size_t gmin_words(int nq) { return (size_t)screen_gmin_words(nq); }
-  bool carve(void* base, size_t bytes, int nq, int nlist) {
+  static size_t rec_count(int nq, int nprobe) { return (size_t)nq * nprobe * 18; }
+  bool carve(void* base, size_t bytes, int nq, int nlist, int nprobe) {
     Carve cv(base, bytes);
     zero = cv.take<int>(zero_words(nq, nlist));
     bucket = cv.take<int>((size_t)nlist * nq);
+    arec = cv.take<uint4>(rec_count(nq, nprobe));
     thr = cv.take<float>((size_t)nq);
     cand = cv.take<uint2>((size_t)nq * kScreenCandCap);
     flist = cv.take<int>((size_t)nq);
@@ -168,8 +180,9 @@ struct ScreenWs {
     gminbuf = cv.take<uint32_t>(gmin_words(nq));
     return cv.ok();
   }
-  static size_t bytes(int nq, int nlist) {
+  static size_t bytes(int nq, int nlist, int nprobe) {
     return carve_bytes<int>(zero_words(nq, nlist)) + carve_bytes<int>((size_t)nlist * nq) +
+           carve_bytes<uint4>(rec_count(nq, nprobe)) +
            carve_bytes<float>((size_t)nq) + carve_bytes<uint2>((size_t)nq * kScreenCandCap) +
            carve_bytes<int>((size_t)nq) + carve_bytes<int2>((size_t)nq) +
            carve_bytes<uint32_t>(gmin_words(nq));
@@ -498,7 +511,7 @@ extern "C" {
 size_t fgpu_search_workspace_bytes(int nq, int nlist, int nprobe) {
   // The coarse step's estimate tile and the screen's buffers are never live
   // at once, so they share one region (no screen beyond kScreenMaxLists lists).
-  const size_t screen = nlist <= kScreenMaxLists ? ScreenWs::bytes(nq, nlist) : 0;
+  const size_t screen = nlist <= kScreenMaxLists ? ScreenWs::bytes(nq, nlist, nprobe) : 0;
   return carve_bytes<uint32_t>((size_t)nq * nprobe) + carve_bytes<float>((size_t)nq * nprobe) +
          carve_bytes<int>(1) + std::max(fgpu_coarse_workspace_bytes(nq, nlist), screen);
 }
@@ -518,11 +531,17 @@ fgpu_status fgpu_search(const fgpu_index* ix, const float* dq, int nq, int nprob
   // The MFMA screen + exact rescore (screen.hip), when the index has its
   // arrays, k <= 32 and the workspace holds its buffers; the queries it hands
   // back go through the generic LUT kernel.  Otherwise the LUT flow kernel.
+  // With FGPU_OPT_STAGE_EVENTS, events between the stages (fgpu_search_stage_times).
+  hipStream_t s = as_stream(stream);
+  const hipEvent_t* ev = ix->opt_stage_events ? ix->stage_ev : nullptr;
+  auto mark = [&](int i) { return ev ? hipEventRecord(ev[i], s) : hipSuccess; };
+  FGPU_HIP(mark(0));
   ScreenWs sw;
   if (ix->screen_ok && ix->opt_screen && k <= 32 && nq > 0 && ((uintptr_t)dq & 15) == 0 &&
-      ix->nlist <= kScreenMaxLists && sw.carve(rest, rest_bytes, nq, ix->nlist)) {
+      ix->nlist <= kScreenMaxLists && (int64_t)nq * nprobe < INT32_MAX &&
+      sw.carve(rest, rest_bytes, nq, ix->nlist, nprobe)) {
     FGPU_TRY(coarse_search(ix, dq, nq, nprobe, prune_ratio, pid, pd, rest, rest_bytes, stream, nullptr, 0));
-    hipStream_t s = as_stream(stream);
+    FGPU_HIP(mark(1));
     ScreenArgs sa{dq, ix->d_centroids, ix->d_offsets, ix->d_codes, ix->d_ids, ix->d_codebook, ix->d_cb16,
                   ix->d_vext, ix->d_rmax, pid, pd, nq, nprobe, k, ix->nlist};
     sa.ctr = sw.zero;
@@ -532,6 +551,7 @@ fgpu_status fgpu_search(const fgpu_index* ix, const float* dq, int nq, int nprob
     sa.first = sw.first;
     sa.gminbuf = sw.gminbuf;
     sa.bucket = sw.bucket;
+    sa.arec = sw.arec;
     sa.thr = sw.thr;
     sa.cand = sw.cand;
     sa.cand_cap = kScreenCandCap;
@@ -539,21 +559,37 @@ fgpu_status fgpu_search(const fgpu_index* ix, const float* dq, int nq, int nprob
     sa.out_ids = d_out_ids;
     sa.out_d = d_out_dists;
     if (ix->opt_screen_clocks) sa.stats = reinterpret_cast<unsigned long long*>(sw.zero + 16);
+    sa.events = ev ? ev + 2 : nullptr;
     FGPU_TRY(launch_screen(ix->dim, ix->m, sa, s));
     AdcArgs a = adc_args(ix, dq, nq, pid, pd, nprobe, k, d_out_ids, d_out_dists);
     a.qlist = sw.flist;
     a.qcount = sw.zero + kCtrFlag;
-    return launch_adc_plain_list(ix->dim, ix->m, a, s);
+    FGPU_TRY(launch_adc_plain_list(ix->dim, ix->m, a, s));
+    FGPU_HIP(mark(kStageEvents - 1));
+    return FGPU_OK;
   }
   // The scan claims queries from a counter that starts at its grid size; the
   // coarse step's select stores that value on the way.
   const int grid = flow_grid(ix->dim, ix->m, nq, nprobe);
   FGPU_TRY(coarse_search(ix, dq, nq, nprobe, prune_ratio, pid, pd, rest, rest_bytes, stream,
                          grid > 0 ? qctr : nullptr, grid));
+  for (int i = 1; i < kStageEvents - 1; ++i) FGPU_HIP(mark(i));  // no screen stages
   AdcArgs a = adc_args(ix, dq, nq, pid, pd, nprobe, k, d_out_ids, d_out_dists);
   a.qctr = qctr;
   a.qctr_preset = grid;
-  return launch_adc_plain(ix->dim, ix->m, a, as_stream(stream));
+  FGPU_TRY(launch_adc_plain(ix->dim, ix->m, a, s));
+  FGPU_HIP(mark(kStageEvents - 1));
+  return FGPU_OK;
+}
+
+fgpu_status fgpu_search_stage_times(const fgpu_index* ix, float* h_ms, int n) {
+  FGPU_CHECK(ix && h_ms, FGPU_ERR_ARG, "search_stage_times: null argument");
+  FGPU_CHECK(ix->opt_stage_events && ix->stage_ev[0], FGPU_ERR_ARG,
+             "search_stage_times: FGPU_OPT_STAGE_EVENTS is off for this index");
+  FGPU_HIP(hipEventSynchronize(ix->stage_ev[kStageEvents - 1]));
+  for (int i = 0; i + 1 < kStageEvents && i < n; ++i)
+    FGPU_HIP(hipEventElapsedTime(&h_ms[i], ix->stage_ev[i], ix->stage_ev[i + 1]));
+  return FGPU_OK;
 }
 
 fgpu_status fgpu_search_screen_stats(const fgpu_index* ix, int nq, int nprobe, const void* ws, size_t ws_bytes,
@@ -566,7 +602,7 @@ fgpu_status fgpu_search_screen_stats(const fgpu_index* ix, int nq, int nprobe, c
   cv.take<int>(1);
   FGPU_CHECK(cv.ok(), FGPU_ERR_WORKSPACE, "search_screen_stats: workspace too small");
   ScreenWs sw;
-  FGPU_CHECK(sw.carve(cv.base + cv.used, ws_bytes - cv.used, nq, ix->nlist), FGPU_ERR_WORKSPACE,
+  FGPU_CHECK(sw.carve(cv.base + cv.used, ws_bytes - cv.used, nq, ix->nlist, nprobe), FGPU_ERR_WORKSPACE,
              "search_screen_stats: workspace too small for the screen");
   hipStream_t s = as_stream(stream);
   std::vector<int> z(ScreenWs::zero_words(nq, ix->nlist));
@@ -592,6 +628,22 @@ fgpu_status fgpu_search_screen_stats(const fgpu_index* ix, int nq, int nprobe, c
   unsigned long long ck[8];
   std::memcpy(ck, z.data() + 16, sizeof(ck));
   for (int i = 0; i < 8 && 8 + i < n_stats; ++i) h_stats[8 + i] = (long long)ck[i];
+  if (n_stats > 16) {
+    // The work of each round: (query, vector) pairs screened, and the MFMA
+    // tiles run (32-query groups of a list times its 32-vector tiles).
+    std::vector<int32_t> off((size_t)ix->nlist + 1);
+    FGPU_HIP(hipMemcpy(off.data(), ix->d_offsets, sizeof(int32_t) * off.size(), hipMemcpyDeviceToHost));
+    long long w[4] = {0, 0, 0, 0};
+    for (int l = 0; l < ix->nlist; ++l) {
+      const long long n = off[l + 1] - off[l];
+      for (int r = 0; r < 2; ++r) {
+        const long long c = std::min(z[kCtrCount + r * ix->nlist + l], nq);
+        w[r] += c * n;
+        w[2 + r] += (c + 31) / 32 * ((n + 31) / 32);
+      }
+    }
+    for (int i = 0; i < 4 && 16 + i < n_stats; ++i) h_stats[16 + i] = w[i];
+  }
   return FGPU_OK;
 }
 
@@ -603,6 +655,11 @@ fgpu_status fgpu_index_set_option(fgpu_index* ix, int option, int value) {
     case FGPU_OPT_SCREEN: ix->opt_screen = value ? 1 : 0; return FGPU_OK;
     case FGPU_OPT_SCREEN_CLOCKS: ix->opt_screen_clocks = value ? 1 : 0; return FGPU_OK;
     case FGPU_OPT_TWO_PHASE_SPLIT: ix->opt_two_phase_split = value > 0 ? value : 0; return FGPU_OK;
+    case FGPU_OPT_STAGE_EVENTS:
+      if (value && !ix->stage_ev[0])
+        for (hipEvent_t& e : ix->stage_ev) FGPU_HIP(hipEventCreate(&e));
+      ix->opt_stage_events = value ? 1 : 0;
+      return FGPU_OK;
     default: return set_error(FGPU_ERR_ARG, "index_set_option: unknown option " + std::to_string(option));
   }
 }

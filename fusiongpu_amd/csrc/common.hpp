@@ -225,6 +225,11 @@ __device__ __forceinline__ float wave_max_f(float v) {
   for (int m = 32; m > 0; m >>= 1) v = fmaxf(v, shfl_xor_f(v, m));
   return v;
 }
+__device__ __forceinline__ float wave_sum_f(float v) {
+#pragma unroll
+  for (int m = 32; m > 0; m >>= 1) v += shfl_xor_f(v, m);
+  return v;
+}
 __device__ __forceinline__ int wave_sum_i(int v) {
 #pragma unroll
   for (int m = 32; m > 0; m >>= 1) v += shfl_xor_i(v, m);

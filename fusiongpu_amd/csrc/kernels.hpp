@@ -141,7 +141,8 @@ struct ScreenArgs {
   int* cnt1;
   int* cnt2;
   int* cand_cnt;
-  int* bucket;              // [nlist][nq] queries of each list's pairs
+  int* bucket;              // [nlist][nq] pair entries (q nprobe + p) of each list
+  uint4* arec;              // [nq nprobe][2][9] pair records: per lane half 8 A fragments and the extra block
   int2* first;              // [nq] round 1: (list, bucket position) of the query's pair, or (-1, -1)
   uint32_t* gminbuf;        // [nq][kMaxChunks][32] round 1: per query, first-list chunk and group, min U bits
   float* thr;               // [nq] T(q)
@@ -154,6 +155,10 @@ struct ScreenArgs {
   // clocks [0] before the first item, [1] in item set-up, [2] in the tile
   // loops, [3] after the tiles; [0..3] round 1, [4..7] round 2.
   unsigned long long* stats = nullptr;
+  // Optional (nullptr = off): events recorded on the launch stream after the
+  // pair kernel of round 1 (with the zeroing), round 1, the pair kernel of
+  // round 2, round 2 and the rescore, in that order.
+  const hipEvent_t* events = nullptr;
 };
 bool screen_supported(int dim, int m);
 // Words of ScreenArgs::gminbuf for nq queries.

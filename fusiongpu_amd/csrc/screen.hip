@@ -82,6 +82,8 @@ constexpr int kChunk = 256;              // list vectors per work item (at most 
 constexpr int kMaxChunks = 8;
 
 constexpr uint32_t kOneOne = 0x3F803F80u;  // two bf16 1.0
+constexpr int kRecHalf = 9;              // uint4 per lane half of a pair record: 8 A fragments, the extra block
+constexpr int kRec = 2 * kRecHalf;
 
 __device__ __forceinline__ void wave_sync() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -189,15 +191,15 @@ __global__ __launch_bounds__(256) void screen_zero_kernel(int* __restrict__ p, i
     p[i] = 0;
 }
 
-// Query q joins list l's bucket (the screen kernels derive their work
-// items from the final counts).
-__device__ __forceinline__ int bucket_add(const ScreenArgs& a, int* cnt, int l, int q) {
+// Pair entry `ent` (= q nprobe + p) of query q joins list l's bucket (the
+// screen kernels derive their work items from the final counts).
+__device__ __forceinline__ int bucket_add(const ScreenArgs& a, int* cnt, int l, int q, int ent) {
   const int pos = atomicAdd(&cnt[l], 1);
   if (pos >= a.nq) {  // a probe list repeating a list id: the query takes the LUT kernel
     a.thr[q] = __builtin_nanf("");
     return -1;
   }
-  a.bucket[(size_t)l * a.nq + pos] = q;
+  a.bucket[(size_t)l * a.nq + pos] = ent;
   return pos;
 }
 
@@ -213,32 +215,107 @@ __device__ __forceinline__ int list_items(int cnt, int nq, int n) {
   return ng * ((n + per - 1) / per);
 }
 
-// Round 1 pairs: each query with its first usable probe (in range, non-empty)
-// when that list holds at least k vectors.
-__global__ __launch_bounds__(256) void screen_pairs1_kernel(ScreenArgs a) {
-  const int q = blockIdx.x * blockDim.x + threadIdx.x;
-  if (q >= a.nq) return;
-  const uint32_t* pr = a.probes + (size_t)q * a.nprobe;
-  int2 f = make_int2(-1, -1);
-  for (int p = 0; p < a.nprobe; ++p) {
-    const uint32_t l = pr[p];
-    if (l >= (uint32_t)a.nlist) continue;
-    const int n = a.offsets[l + 1] - a.offsets[l];
-    if (n <= 0) continue;
-    if (n >= a.k) {
-      const int pos = bucket_add(a, a.cnt1, (int)l, q);
-      if (pos >= 0) f = make_int2((int)l, pos);
-    }
-    break;
+// The pair record of entry ent = (query q, probe p of list l), written by a
+// whole wave: for each lane half h (dims [h D/2, (h+1) D/2)) the A fragments
+// -2 bf16(r), r = fl(q - c), in MFMA operand order (fragment c holds dims
+// h D/2 + 8c .. + 7), then the extra K block of the round's test:
+//   round 1 (U):  h0 [ aR, 0, 0, 0, 1, 1, 1, c1]   h1 [c2, c3, 0 ...]
+//   round 2 (V):  h0 [-aR, 1, 1, 1, 0, 0, 0, v1]   h1 [v2, v3, 0 ...]
+// against the vector's block [X, y'1..3, y''1..3, 1] (h0) and [1, 1, 0 ...]
+// (h1): aR = bf16 above a R, c1 + c2 + c3 >= (t nr2 + g R^2 + 2^-110 (1 + R)),
+// v1 + v2 + v3 <= -(t T - nr2 + g R^2 + 2^-110 (1 + R)), each with the 2^-40
+// slack of the double arithmetic.  qv: this lane's two query dims (2 lane,
+// 2 lane + 1).  Returns nr2; the record is unusable when nr2 is not <=
+// kMaxNorm2 (NaN included), and the caller then adds no pair.
+template <int D, int ROUND>
+__device__ float pair_record(const ScreenArgs& a, int64_t ent, float2 qv, int l, float T) {
+  const int lane = threadIdx.x & 63;
+  const bool has = 2 * lane < D;
+  float r0 = 0.0f, r1 = 0.0f;
+  if (has) {
+    const float2 cv = reinterpret_cast<const float2*>(a.centroids + (size_t)l * D)[lane];
+    r0 = qv.x - cv.x;
+    r1 = qv.y - cv.y;
   }
-  a.first[q] = f;
+  const float nr2 = wave_sum_f(__builtin_fmaf(r1, r1, r0 * r0));
+  uint32_t* rec = reinterpret_cast<uint32_t*>(a.arec + ent * kRec);
+  if (has) {
+    const int d = 2 * lane, h = d / (D / 2), w = d % (D / 2);
+    rec[(h * kRecHalf + w / 8) * 4 + (w % 8) / 2] = pack2(bf_rn(-2.0f * r0), bf_rn(-2.0f * r1));
+  }
+  if (lane < 2 && nr2 <= kMaxNorm2) {
+    const double n2 = (double)nr2;
+    const double R = sqrt(n2 * (1.0 + 0x1p-16)) * (1.0 + kDbl);
+    const uint16_t aR = bf_up(kA * R);
+    uint16_t p1, p2, p3;
+    uint4 ex = make_uint4(0u, 0u, 0u, 0u);
+    if (ROUND == 2) {
+      const double t = (double)fmaxf(T, 0.0f);
+      const double rhs = t * kTInfl - n2 + kG * R * R + kAbs * (1.0 + R);
+      split3<false>(-rhs - kDbl * (t + n2 + kG * R * R), p1, p2, p3);
+      ex = lane == 0 ? make_uint4(pack2(aR ^ 0x8000u, 0x3F80u), kOneOne, 0u, pack2(0u, p1))
+                     : make_uint4(pack2(p2, p3), 0u, 0u, 0u);
+    } else {
+      const double c = n2 * kTInfl + kG * R * R + kAbs * (1.0 + R);
+      split3<true>(c * (1.0 + kDbl), p1, p2, p3);
+      ex = lane == 0 ? make_uint4(pack2(aR, 0u), 0u, kOneOne, pack2(0x3F80u, p1))
+                     : make_uint4(pack2(p2, p3), 0u, 0u, 0u);
+    }
+    a.arec[ent * kRec + lane * kRecHalf + kRecHalf - 1] = ex;
+  }
+  return nr2;
+}
+
+__device__ __forceinline__ float2 query_dims(const ScreenArgs& a, int q, int dim) {
+  const int lane = threadIdx.x & 63;
+  return 2 * lane < dim ? reinterpret_cast<const float2*>(a.queries + (size_t)q * dim)[lane] : make_float2(0.0f, 0.0f);
+}
+
+// Round 1 pairs, one wave a query: the query with its first usable probe (in
+// range, non-empty) when that list holds at least k vectors and the residual
+// norm is in range; its pair record carries the U test.
+template <int D>
+__global__ __launch_bounds__(256) void screen_pairs1_kernel(ScreenArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int q = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  if (q >= a.nq) return;
+  int pf = -1, lf = 0;
+  for (int p0 = 0; p0 < a.nprobe; p0 += kWave) {
+    const int p = p0 + lane;
+    uint32_t l = 0xFFFFFFFFu;
+    bool use = false;
+    if (p < a.nprobe) {
+      l = a.probes[(size_t)q * a.nprobe + p];
+      use = l < (uint32_t)a.nlist && a.offsets[l + 1] - a.offsets[l] > 0;
+    }
+    const uint64_t m = __ballot(use);
+    if (m) {
+      const int b = __builtin_ctzll(m);
+      pf = p0 + b;
+      lf = __builtin_amdgcn_readlane((int)l, b);
+      break;
+    }
+  }
+  int2 f = make_int2(-1, -1);
+  if (pf >= 0 && a.offsets[lf + 1] - a.offsets[lf] >= a.k) {
+    const int64_t ent = (int64_t)q * a.nprobe + pf;
+    const float nr2 = pair_record<D, 1>(a, ent, query_dims(a, q, D), lf, 0.0f);
+    if (nr2 <= kMaxNorm2 && lane == 0) {
+      const int pos = bucket_add(a, a.cnt1, lf, q, (int)ent);
+      if (pos >= 0) f = make_int2(lf, pos);
+    }
+  }
+  if (lane == 0) a.first[q] = f;
 }
 
 // Round 2 pairs, one wave a query.  First T(q): the k-th smallest of the 32
 // group minima of U over the query's first list (the minimum, over the list's
-// round-1 items, of each item's per-group minimum), inflated by 1 + 2^-12;
-// +inf without a round-1 pair or with fewer than k groups holding a value.
-// Then every usable probe whose list bound does not exceed T(q).
+// chunks, of each chunk's per-group minimum), inflated by 1 + 2^-12; +inf
+// without a round-1 pair or with fewer than k groups holding a value.  Then
+// every usable probe whose list bound does not exceed T(q), with its pair
+// record carrying the V test.  A probe whose residual norm is out of range
+// sends the query to the LUT kernel (T = +inf).
+template <int D>
 __global__ __launch_bounds__(256) void screen_pairs2_kernel(ScreenArgs a) {
   const int lane = threadIdx.x & 63;
   const int q = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
@@ -257,14 +334,31 @@ __global__ __launch_bounds__(256) void screen_pairs2_kernel(ScreenArgs a) {
   const float T = kth < INFINITY ? f_above((double)kth * kTInfl) : INFINITY;
   if (lane == 0) a.thr[q] = T;
   if (!(T < INFINITY)) return;
-  for (int p = lane; p < a.nprobe; p += kWave) {
-    const size_t t = (size_t)q * a.nprobe + p;
-    const uint32_t l = a.probes[t];
-    if (l >= (uint32_t)a.nlist) continue;
-    if (a.offsets[l + 1] - a.offsets[l] <= 0) continue;
-    if (list_lower_bound(a.probe_dists[t], a.rmax[l]) > T) continue;
-    bucket_add(a, a.cnt2, (int)l, q);
+  const float2 qv = query_dims(a, q, D);
+  bool bad = false;
+  for (int p0 = 0; p0 < a.nprobe; p0 += kWave) {
+    const int p = p0 + lane;
+    uint32_t l = 0xFFFFFFFFu;
+    bool pass = false;
+    if (p < a.nprobe) {
+      const size_t t = (size_t)q * a.nprobe + p;
+      l = a.probes[t];
+      pass = l < (uint32_t)a.nlist && a.offsets[l + 1] - a.offsets[l] > 0 &&
+             list_lower_bound(a.probe_dists[t], a.rmax[l]) <= T;
+    }
+    for (uint64_t m = __ballot(pass); m; m &= m - 1) {
+      const int b = __builtin_ctzll(m);
+      const int lb = __builtin_amdgcn_readlane((int)l, b);
+      const int64_t ent = (int64_t)q * a.nprobe + p0 + b;
+      const float nr2 = pair_record<D, 2>(a, ent, qv, lb, T);
+      if (!(nr2 <= kMaxNorm2)) {
+        bad = true;
+        continue;
+      }
+      if (lane == 0) bucket_add(a, a.cnt2, lb, q, (int)ent);
+    }
   }
+  if (bad && lane == 0) a.thr[q] = INFINITY;
 }
 
 // ---- the screen ---------------------------------------------------------------------------
@@ -356,10 +450,11 @@ __device__ __forceinline__ uint32_t kth_of_32(uint32_t (&v)[32], int k) {
 }
 
 // One persistent workgroup per CU; each wave takes work items (list, group of
-// up to kQB queries, vector range) and screens the range in tiles of kTV
-// vectors.  A wave's first item is its global index; later ones come from a
-// counter.  ROUND 1 folds each (query, group) minimum of U into gmin;
-// ROUND 2 appends candidates.
+// up to kQB pairs of the list's bucket, range of the list's vectors) in turn:
+// items w, w + waves, ... where w is its global index.  Each item's rows come
+// from the pair records; the range is screened in tiles of kTV vectors.
+// ROUND 1 stores each row's per-group minima of U; ROUND 2 appends the
+// candidates (V <= 0) to their queries' arrays.
 // LDS: the bf16 codebook first (offset 0, so every gather's subspace offset is
 // the instruction's immediate), then per-wave staging.
 template <int D, int M, int ROUND>
@@ -437,91 +532,42 @@ __global__ __launch_bounds__(kSW * kWave) void screen_kernel(ScreenArgs a) {
     const int local = w - __builtin_amdgcn_readfirstlane(pre[l]);
     const int grp = local / nch, jb = (local % nch) * per, je = min(n, jb + per);
     const int nrow = min(kQB, min(cnt[l], a.nq) - grp * kQB);
-    const int qi = li < nrow ? a.bucket[(size_t)l * a.nq + grp * kQB + li] : -1;
+    const int ent = li < nrow ? a.bucket[(size_t)l * a.nq + grp * kQB + li] : -1;
 
-    // Two tiles of codes in flight ahead of the one being screened.
+    // A tile's codes and extra blocks.  Every lane loads on every call (a
+    // column past the range reloads the range's last vector; lane half 1
+    // loads a block it does not use), so each tile issues the same loads and
+    // the wait for a buffer never has to cover the loads issued after it;
+    // the padding block replaces the loaded one where the tile uses it.
     auto load_tile = [&](int j0, uint32_t (&cw)[M / 8], uint4& bx) {
-      const int j = j0 + li;
-      const bool valid = j < je;
-      const int64_t v = (int64_t)start + (valid ? j : je - 1);
+      const int j = min(j0 + li, je - 1);
+      const int64_t v = (int64_t)start + j;
       load_half<M>(a.codes + v * M + h * HB, cw);
-      bx = bx_pad;
-      if (valid && h == 0) bx = a.vext[v];
+      bx = a.vext[v];
     };
-    uint32_t cw0[M / 8], cw1[M / 8];
-    uint4 bx0, bx1;
-    load_tile(jb, cw0, bx0);
-    if (jb + kTV < je) load_tile(jb + kTV, cw1, bx1);
+    uint32_t cwA[M / 8], cwB[M / 8];
+    uint4 bxA, bxB;
+    load_tile(jb, cwA, bxA);
+    load_tile(jb + kTV, cwB, bxB);
 
-    // A rows: -2 bf16(r) over this lane half's dims, and nr2 = ||r||^2 (fp32).
+    // A rows and the extra block from the row's pair record.  A row without a
+    // pair: zeros, and in round 2 V = 1e30, so it never passes (in round 1
+    // its minima are not stored).
     bf16x8 A[NC];
-    float nr2 = 0.0f;
+    bf16x8 Aex;
     {
-      const float4* qp = reinterpret_cast<const float4*>(a.queries + (size_t)(qi >= 0 ? qi : 0) * D + h * HD);
-      const float4* cp = reinterpret_cast<const float4*>(a.centroids + (size_t)l * D + h * HD);
+      const uint4* rec = a.arec + (int64_t)(ent >= 0 ? ent : 0) * kRec + h * kRecHalf;
 #pragma unroll
       for (int c = 0; c < NC; ++c) {
-        const float4 q0 = qp[2 * c], q1 = qp[2 * c + 1], c0 = cp[2 * c], c1 = cp[2 * c + 1];
-        const float r[8] = {q0.x - c0.x, q0.y - c0.y, q0.z - c0.z, q0.w - c0.w,
-                            q1.x - c1.x, q1.y - c1.y, q1.z - c1.z, q1.w - c1.w};
-        uint32_t f[4];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) nr2 = __builtin_fmaf(r[e], r[e], nr2);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) f[e] = pack2(bf_rn(-2.0f * r[2 * e]), bf_rn(-2.0f * r[2 * e + 1]));
-        A[c] = __builtin_bit_cast(bf16x8, f);
+        const uint4 v = ent >= 0 ? rec[c] : make_uint4(0u, 0u, 0u, 0u);
+        A[c] = frag_of(v.x, v.y, v.z, v.w);
       }
-      nr2 += __shfl_xor(nr2, 32, kWave);
+      const uint4 e = ent >= 0 ? rec[kRecHalf - 1]
+                               : make_uint4(0u, 0u, 0u, ROUND == 2 && h == 0 ? pack2(0u, big) : 0u);
+      Aex = frag_of(e.x, e.y, e.z, e.w);
     }
-    bool active = qi >= 0 && nr2 <= kMaxNorm2;  // false for NaN
-    float T = 0.0f;
-    if (ROUND == 2) {
-      T = active ? a.thr[qi] : 0.0f;
-      active = active && T < INFINITY;
-      T = fmaxf(T, 0.0f);
-    }
-    // The extra K block of this row (8 bf16 of this lane half).
-    uint32_t ex[4] = {0u, 0u, 0u, 0u};
-    if (active) {
-      const double n2 = (double)nr2;
-      const double R = sqrt(n2 * (1.0 + 0x1p-16)) * (1.0 + kDbl);
-      const uint16_t aR = bf_up(kA * R);
-      uint16_t p1, p2, p3;
-      if (ROUND == 2) {
-        const double rhs = (double)T * kTInfl - n2 + kG * R * R + kAbs * (1.0 + R);
-        split3<false>(-rhs - kDbl * ((double)T + n2 + kG * R * R), p1, p2, p3);
-        if (h == 0) {
-          ex[0] = pack2(aR ^ 0x8000u, 0x3F80u);
-          ex[1] = pack2(0x3F80u, 0x3F80u);
-          ex[2] = 0u;
-          ex[3] = pack2(0u, p1);
-        } else {
-          ex[0] = pack2(p2, p3);
-        }
-      } else {
-        const double c = n2 * kTInfl + kG * R * R + kAbs * (1.0 + R);
-        split3<true>(c * (1.0 + kDbl), p1, p2, p3);
-        if (h == 0) {
-          ex[0] = pack2(aR, 0u);
-          ex[1] = 0u;
-          ex[2] = pack2(0x3F80u, 0x3F80u);
-          ex[3] = pack2(0x3F80u, p1);
-        } else {
-          ex[0] = pack2(p2, p3);
-        }
-      }
-    } else {
-      // An inactive row never passes the round-2 test (V = 1e30) and
-      // contributes no group minimum in round 1.
-      if (ROUND == 2 && h == 0) ex[3] = pack2(0u, big);
-#pragma unroll
-      for (int c = 0; c < NC; ++c) A[c] = frag_of(0u, 0u, 0u, 0u);
-    }
-    const bf16x8 Aex = frag_of(ex[0], ex[1], ex[2], ex[3]);
-    // The query of each row, for the candidate flush and the round-1 store:
-    // -1 for a row without a query; in round 1, -2 - q for an inactive row of
-    // query q (its values bound nothing: it stores +inf, so q gets no T).
-    if (h == 0) rowq[li] = ROUND == 1 && !active && qi >= 0 ? -2 - qi : qi;
+    // The query of each row, for the candidate flush and the round-1 store.
+    if (h == 0) rowq[li] = ent >= 0 ? ent / a.nprobe : -1;
 
     // Per row and lane column, the smallest U bits seen (ROUND 1; every U is
     // >= 0, where float order is unsigned order).
@@ -551,23 +597,22 @@ __global__ __launch_bounds__(kSW * kWave) void screen_kernel(ScreenArgs a) {
       ck = t;
     }
 
-    for (int j0 = jb; j0 < je; j0 += kTV) {
-      // Every gather of the tile first, then the loads two tiles ahead, then
-      // the MFMA chain.
-      bf16x8 B[NC];
-#pragma unroll
-      for (int c = 0; c < NC; ++c) B[c] = decode_chunk<D, M>(cbs, cw0, hsel, c);
-      const bf16x8 Bx = frag_of(bx0.x, bx0.y, bx0.z, bx0.w);
-#pragma unroll
-      for (int i = 0; i < M / 8; ++i) cw0[i] = cw1[i];
-      bx0 = bx1;
-      if (j0 + 2 * kTV < je) load_tile(j0 + 2 * kTV, cw1, bx1);
+    // One tile: the MFMA chain, each chunk's gathers just before its MFMA,
+    // then the reload of the same buffer two tiles ahead (two buffers
+    // alternate, so a tile never waits for the loads of the next one), then
+    // the tile's results.
+    auto tile = [&](int j0, uint32_t (&cw)[M / 8], uint4& bx) {
       f32x16 acc;
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
 #pragma unroll
-      for (int c = 0; c < NC; ++c) acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A[c], B[c], acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(Aex, Bx, acc, 0, 0, 0);
+      for (int c = 0; c < NC; ++c)
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A[c], decode_chunk<D, M>(cbs, cw, hsel, c), acc, 0, 0, 0);
+      const bool vcol = h == 0 && j0 + li < je;
+      acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+          Aex, frag_of(vcol ? bx.x : bx_pad.x, vcol ? bx.y : bx_pad.y, vcol ? bx.z : bx_pad.z, vcol ? bx.w : bx_pad.w),
+          acc, 0, 0, 0);
+      load_tile(j0 + 2 * kTV, cw, bx);
       // acc[r]: row 8 (r / 4) + 4 h + r % 4 of the work item, column li (vector j0 + li).
       if constexpr (ROUND == 1) {
 #pragma unroll
@@ -593,6 +638,10 @@ __global__ __launch_bounds__(kSW * kWave) void screen_kernel(ScreenArgs a) {
           }
         }
       }
+    };
+    for (int j0 = jb; j0 < je; j0 += 2 * kTV) {
+      tile(j0, cwA, bxA);
+      if (j0 + kTV < je) tile(j0 + kTV, cwB, bxB);
     }
 
     if (a.stats) {
@@ -613,8 +662,7 @@ __global__ __launch_bounds__(kSW * kWave) void screen_kernel(ScreenArgs a) {
       for (int r = 0; r < 16; ++r) {
         const int row = 8 * (r >> 2) + 4 * h + (r & 3);
         const int q = rowq[row];
-        if (q != -1)
-          a.gminbuf[((size_t)(q >= 0 ? q : -2 - q) * kMaxChunks + cidx) * 32 + li] = q >= 0 ? mins[r] : 0x7F800000u;
+        if (q >= 0) a.gminbuf[((size_t)q * kMaxChunks + cidx) * 32 + li] = mins[r];
       }
     }
     wave_sync();
@@ -742,11 +790,17 @@ fgpu_status launch_screen_dm(const ScreenArgs& a, hipStream_t s) {
   const int64_t nz = kCtrCount + 2 * (int64_t)a.nlist + (int64_t)a.nq;
   hipLaunchKernelGGL(screen_zero_kernel, dim3((unsigned)std::min<int64_t>((nz + 255) / 256, 2048)), dim3(256), 0, s,
                      a.ctr, nz);
-  hipLaunchKernelGGL(screen_pairs1_kernel, dim3((unsigned)((a.nq + 255) / 256)), dim3(256), 0, s, a);
+  auto mark = [&](int i) { return a.events ? hipEventRecord(a.events[i], s) : hipSuccess; };
+  hipLaunchKernelGGL(screen_pairs1_kernel<D>, dim3((unsigned)((a.nq + 3) / 4)), dim3(256), 0, s, a);
+  FGPU_HIP(mark(0));
   hipLaunchKernelGGL((screen_kernel<D, M, 1>), dim3((unsigned)cus), dim3(kSW * kWave), 0, s, a);
-  hipLaunchKernelGGL(screen_pairs2_kernel, dim3((unsigned)((a.nq + 3) / 4)), dim3(256), 0, s, a);
+  FGPU_HIP(mark(1));
+  hipLaunchKernelGGL(screen_pairs2_kernel<D>, dim3((unsigned)((a.nq + 3) / 4)), dim3(256), 0, s, a);
+  FGPU_HIP(mark(2));
   hipLaunchKernelGGL((screen_kernel<D, M, 2>), dim3((unsigned)cus), dim3(kSW * kWave), 0, s, a);
+  FGPU_HIP(mark(3));
   hipLaunchKernelGGL((rescore_kernel<D, M>), dim3((unsigned)cus), dim3(kRW * kWave), 0, s, a);
+  FGPU_HIP(mark(4));
   FGPU_HIP(hipGetLastError());
   return FGPU_OK;
 }

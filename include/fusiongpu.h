@@ -189,7 +189,10 @@ fgpu_status fgpu_search(const fgpu_index* idx, const float* d_queries, int nq, i
  * screened for the thresholds, lists screened in the second round, (query,
  * list) pairs screened there, candidates rescored, the largest candidate count
  * of a query, queries handed to the LUT kernel, queries with a finite
- * threshold, 0.  Only meaningful after a call that took the screen. */
+ * threshold, 0; h_stats[8..15] the clocks of FGPU_OPT_SCREEN_CLOCKS;
+ * h_stats[16..19] = (query, vector) pairs screened in round 1 and round 2,
+ * MFMA tiles (32 queries x 32 vectors) run in round 1 and round 2.  Only
+ * meaningful after a call that took the screen. */
 fgpu_status fgpu_search_screen_stats(const fgpu_index* idx, int nq, int nprobe, const void* d_workspace,
                                      size_t workspace_bytes, void* stream, long long* h_stats, int n_stats);
 /* 1 when the index carries the screen's arrays (built at creation for the
@@ -212,13 +215,24 @@ int fgpu_index_screen_ready(const fgpu_index* idx);
  *                       clocks (before the first item, item set-up, tile
  *                       loops, after the tiles; round 1 then round 2) to the
  *                       counters fgpu_search_screen_stats returns in
- *                       h_stats[8..15]; 0 default. */
+ *                       h_stats[8..15]; 0 default;
+ *   FGPU_OPT_STAGE_EVENTS 1: fgpu_search records HIP events on its stream
+ *                       between its stages (fgpu_search_stage_times); 0
+ *                       default.  The events belong to the index, so calls
+ *                       that overlap on one index overwrite each other's. */
 #define FGPU_OPT_LIST_SKIP 1
 #define FGPU_OPT_SPIN_LIMIT 2
 #define FGPU_OPT_SCREEN 3
 #define FGPU_OPT_SCREEN_CLOCKS 4
 #define FGPU_OPT_TWO_PHASE_SPLIT 5
+#define FGPU_OPT_STAGE_EVENTS 6
 fgpu_status fgpu_index_set_option(fgpu_index* idx, int option, int value);
+/* With FGPU_OPT_STAGE_EVENTS on: the milliseconds of the last fgpu_search's
+ * stages (waits for it), h_ms[0..6] = coarse step, the screen's zeroing and
+ * round-1 pairs, round 1, round-2 pairs, round 2, rescore, and the LUT kernel
+ * (the whole scan when the call did not take the screen; the screen stages
+ * are then 0).  No reference counterpart. */
+fgpu_status fgpu_search_stage_times(const fgpu_index* idx, float* h_ms, int n);
 
 /* ---- search without allocation ----------------------------------------- */
 
