@@ -125,9 +125,14 @@ def test_c4_full_size_build_properties():
     1M-row sample, every row assigned, PQ M=32 (15 iterations), every row
     encoded.  The lists are a permutation with ascending ids inside each list;
     for 20k seeded rows the list equals the oracle's exact argmin over the
-    GPU centroids and the codes equal the oracle's encoding; a Lloyd update of
-    the training sample's final assignment equals the oracle's fixed-point
-    update."""
+    GPU centroids and the codes equal the oracle's encoding; the codebook
+    equals the oracle's PQ training on the same assignment and 50k sample
+    (pq_utils.h:77-138); a Lloyd update of the training sample's final
+    assignment equals the oracle's fixed-point update.  Then the elbow sweep
+    over 1024/2048/4096 lists (tune_parameters.cu:199-456 scores the same
+    SSE): each SSE over the 1M-row sample equals the sum of the oracle's exact
+    distances from every sample row to its nearest GPU centroid, row by row
+    bit for bit, and the knee follows from those SSEs."""
     cfg = W.C4
     _say("c4: generate 10M x 128, build 4096 lists on the GPU")
     x = W.base(cfg)
@@ -151,6 +156,9 @@ def test_c4_full_size_build_properties():
     assert np.array_equal(row_list[s], oa)
     oc = oracle.pq_encode(x[s], oa, cent, cb, fma_mode=1)
     assert np.array_equal(row_code[s], oc)
+    _say("c4: oracle PQ training on the full assignment (50k sample, 15 iterations)")
+    ocb = oracle.pq_train(x, row_list, cent, cfg.pq_m, sample_size=50000, iters=cfg.pq_iters)
+    assert np.array_equal(_bits(cb), _bits(ocb))
     # the Lloyd update at the training sample's full size
     _say("c4: one fixed-point Lloyd update of the 1M-row sample against the oracle")
     rows = (np.arange(cfg.train_rows, dtype=np.int64) * n) // cfg.train_rows
@@ -164,7 +172,30 @@ def test_c4_full_size_build_properties():
     oc2, ocnt2 = oracle.kmeans_update(xs, _host(asg), cent, shift)
     assert np.array_equal(_host(cnt), ocnt2)
     assert np.array_equal(_bits(_host(gc)), _bits(oc2))
-    del dx, dxs
+    del dx
+    _free()
+    # the elbow sweep on the training sample
+    sse = {}
+    for L in (1024, 2048, 4096):
+        _say(f"c4: elbow sweep, k-means of {L} lists on the GPU, oracle exact distances of the 1M sample rows")
+        c, _ = fg.kmeans_fit(dxs, L, cfg.kmeans_iters, init_mode=1, seed=42, want_assign=False)
+        if L == cfg.nlist:
+            assert np.array_equal(_bits(_host(c)), _bits(cent)), "the sweep's 4096 lists differ from the build's"
+        _, d = fg.l2_topk(dxs, c, 1)
+        gsse = float(d.to(torch.float64).sum().item())
+        _, od = oracle.coarse(xs, _host(c), 1, prune_ratio=np.inf)
+        assert np.array_equal(_bits(_host(d)[:, 0]), _bits(od[:, 0]))
+        osse = float(od[:, 0].astype(np.float64).sum())
+        assert gsse == osse
+        sse[L] = osse
+    assert sse[1024] > sse[2048] > sse[4096]
+    xn = np.log2([1024, 2048, 4096]) - 10.0
+    xn /= xn[-1]
+    yv = np.array([sse[1024], sse[2048], sse[4096]])
+    yn = (yv - yv[-1]) / (yv[0] - yv[-1])
+    knee = [1024, 2048, 4096][int(np.argmax((1 - xn) - yn))]
+    _say(f"c4: elbow SSE {sse}, knee at {knee} lists")
+    del dxs
     _free()
 
 

@@ -159,13 +159,16 @@ def test_build_global_elbow_sweep(tmp_path):
     sse = [float(v) for v in re.findall(r"Elbow: nlist \d+ SSE ([\d.e+]+)", out)]
     chosen = int(re.search(r"Elbow: chosen nlist (\d+)", out).group(1))
     assert len(sse) == 3 and sse[0] > sse[1] > sse[2]
-    # the SSE of each list count: exact distances of the training sample to its k-means centroids
+    # the SSE of each list count: the oracle's k-means of the training sample
+    # (run_kmeans_gpu restated), then the oracle's exact distance of every
+    # sample row to its nearest centroid, summed
     rows = (np.arange(6000, dtype=np.int64) * 12000) // 6000
-    tr = torch.from_numpy(np.ascontiguousarray(x[rows])).cuda()
+    tr = np.ascontiguousarray(x[rows])
     for L, printed in zip((16, 32, 64), sse):
-        c, _ = fg.kmeans_fit(tr, L, 3, init_mode=1, seed=42, want_assign=False)
-        _, d = fg.l2_topk(tr, c, 1)
-        assert abs(float(d.to(torch.float64).sum().item()) - printed) <= 1e-5 * printed
+        oc, _ = oracle.kmeans_fit(tr, L, 3, init_mode=1, seed=42)
+        _, od = oracle.coarse(tr, oc, 1, prune_ratio=np.inf)
+        osse = float(od[:, 0].astype(np.float64).sum())
+        assert abs(osse - printed) <= 1e-5 * printed  # the tool prints six significant digits
     xn = np.log2([16, 32, 64]) - 4.0
     xn /= xn[-1]
     yn = (np.array(sse) - sse[-1]) / (sse[0] - sse[-1])
