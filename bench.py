@@ -153,8 +153,9 @@ def main():
     ap.add_argument("--copy-probe", action="store_true", help="also run a 1 GiB device copy (PMC calibration)")
     ap.add_argument("--workload", choices=["c1", "c2", "c3", "c4", "c5", "batch128"], default="c2")
     ap.add_argument("--c5-components", type=int, default=256, help="mixture components of the C5 data")
-    ap.add_argument("--c5-random-edges", type=int, default=4,
+    ap.add_argument("--c5-random-edges", type=int, default=8,
                     help="C5: out-edges per vector replaced by seeded random long-range edges")
+    ap.add_argument("--c5-no-reverse", action="store_true", help="C5: forward kNN edges only (no reverse edges)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build targets one GPU; --gpus {args.gpus} is not supported "
@@ -877,29 +878,9 @@ def run_c5(args, torch, fg, dev):
     log(f"generated {n}x{dim} base + {nq} queries in {time.time() - t0:.1f}s")
     t0 = time.time()
     dx = torch.from_numpy(x).to(dev)
-    offs, ids, codes, cent, cb = fg.build_ivfpq(dx, 2048, 32, kmeans_iters=10, init_mode=1, seed=7, pq_iters=8,
-                                                sample_size=50000, train_rows=min(n, 1_000_000))
-    idx = fg.Index.from_arrays(dim, 32, offs, ids, codes, cent, cb)
-    graph = torch.empty((n, degree), dtype=torch.int32, device=dev)
-    B = 1 << 18
-    sws = torch.empty(idx.search_workspace_bytes(B, 8), dtype=torch.uint8, device=dev)
-    cnt64 = torch.full((B,), 64, dtype=torch.int32, device=dev)
-    for b0 in range(0, n, B):
-        nb = min(B, n - b0)
-        # ADC top-64, then the exact top-(degree+1) among them (eps < 0: every candidate is evaluated)
-        aid, _ = idx.search(dx[b0:b0 + nb], 8, 64, workspace=sws)
-        gid, _, _ = fg.rerank(dx[b0:b0 + nb], dx, aid, cnt64[:nb], degree + 1, 64, -1.0, 2)
-        rows = torch.arange(b0, b0 + nb, device=dev, dtype=torch.int32)[:, None]
-        drop = (gid == rows) | (gid < 0)
-        order = torch.argsort(drop.to(torch.int8), dim=1, stable=True)[:, :degree]
-        graph[b0:b0 + nb] = torch.gather(gid, 1, order)
-    if nrand > 0:
-        # seeded long-range edges in the last nrand slots (a counter-based hash of (row, slot))
-        r = torch.arange(n, device=dev, dtype=torch.int64)[:, None] * 1000003 + torch.arange(
-            nrand, device=dev, dtype=torch.int64)[None, :] * 7919 + 12345
-        r = (r * 6364136223846793005 + 1442695040888963407) & ((1 << 62) - 1)
-        graph[:, degree - nrand:] = ((r >> 17) % n).to(torch.int32)
-    idx.close()
+    # forward candidates by IVF-PQ search + exact rerank, CAGRA's reverse-edge step, seeded long-range edges
+    from fusiongpu_amd import workloads as W
+    graph = W.knn_graph(dx, degree, nrand, reverse=not args.c5_no_reverse)
     torch.cuda.synchronize()
     log(f"index + degree-{degree} graph built on GPU in {time.time() - t0:.1f}s")
     dq = torch.from_numpy(q).to(dev)
@@ -938,8 +919,14 @@ def run_c5(args, torch, fg, dev):
     gid, gd = out[0].cpu().numpy(), out[1].cpu().numpy()
     gt, _ = fg.knn_exact(dq, dx, k)
     gt = gt.cpu().numpy()
-    recall = float(np.mean([len(set(gid[i]) & set(gt[i])) / k for i in range(nq)]))
-    log(f"recall@{k} {recall:.4f} against exact kNN")
+    rec = np.array([len(set(gid[i]) & set(gt[i])) / k for i in range(nq)])
+    recall = float(rec.mean())
+    # a walk that ends in the query's own mixture component finds a nearest distance within 2x of the
+    # true one (components lie about 9 apart, their points about 1.5 from each other)
+    gtd = fg.knn_exact(dq, dx, 1)[1][:, 0].cpu().numpy()
+    own = gd[:, 0] <= 2.0 * gtd
+    log(f"recall@{k} {recall:.4f} against exact kNN; {own.mean():.3f} of the walks end in the query's component, "
+        f"recall {rec[own].mean():.4f} there")
 
     cpu = parity = None
     if args.cpu_queries > 0:
@@ -962,8 +949,10 @@ def run_c5(args, torch, fg, dev):
         "value": round(qps, 1), "unit": "queries/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": round(ms_per_step, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "f32",
-        "data": f"synthetic: seeded {ncomp}-component Gaussian mixture; graph = each vector's {degree - nrand} nearest "
-                f"by this framework's IVF-PQ search (ADC top-64, exact rerank) + {nrand} seeded random edges",
+        "data": f"synthetic: seeded {ncomp}-component Gaussian mixture; graph = forward candidates by this "
+                f"framework's IVF-PQ search (ADC top-64, exact rerank)"
+                f"{'' if args.c5_no_reverse else ' with CAGRA reverse edges'}, last {nrand} slots seeded random "
+                f"long-range edges",
         "config": {"workload": "BASELINE config 5: 5M x 128 fp32, out-degree-32 graph, 10k queries, itopk 64, "
                                "width 4, max 64 steps, k=10",
                    "n": n, "dim": dim, "degree": degree, "nq": nq, "itopk": itopk, "width": width,
@@ -977,6 +966,8 @@ def run_c5(args, torch, fg, dev):
                      "note": "achieved = distance rows + adjacency rows read / kernel time; the measured row rate is "
                              "fgpu_row_gather over as many random whole rows of the base, one lane a row"},
         "cpu_baseline": cpu, "parity": parity, "recall_at_k": recall,
+        "walks_in_query_component": round(float(own.mean()), 4),
+        "recall_in_query_component": round(float(rec[own].mean()), 4),
     }
     print(json.dumps(res), flush=True)
 

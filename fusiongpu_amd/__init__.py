@@ -33,7 +33,7 @@ __all__ = [
     "FgpuError", "lib", "lib_path", "Index", "gen_gmm", "l2_topk", "kmeans_fit", "kmeans_update",
     "fixed_shift", "pq_train", "pq_encode", "build_ivfpq", "write_ivf_data", "read_ivf_data",
     "write_fvecs", "read_fvecs", "read_ivecs", "probe_counts", "rerank", "knn_exact", "graph_search",
-    "stream_read", "row_gather", "FAULT_ID", "prune_probes",
+    "stream_read", "row_gather", "FAULT_ID", "prune_probes", "graph_add_reverse",
 ]
 
 lib_path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib", "libfusiongpu.so")
@@ -71,6 +71,7 @@ _SIGS = {
     "fgpu_search_screen_stats": (_i32, [_vp, _i32, _i32, _vp, _sz, _vp, _c.POINTER(_c.c_longlong), _i32]),
     "fgpu_index_screen_ready": (_i32, [_vp]),
     "fgpu_index_set_option": (_i32, [_vp, _i32, _i32]),
+    "fgpu_graph_add_reverse": (_i32, [_vp, _i64, _i32, _i32, _vp, _i32]),
     "fgpu_search_stage_times": (_i32, [_vp, _c.POINTER(_c.c_float), _i32]),
     "fgpu_search_noalloc_max_bytes": (_sz, []),
     "fgpu_search_noalloc_max_rows": (_i32, [_i32, _i32]),
@@ -784,6 +785,16 @@ def knn_exact(queries, base, k: int, workspace=None, stream=None):
         _check(lib.fgpu_knn_exact(_dev_ptr(q), nq, _dev_ptr(b), n, dim, k, _dev_ptr(ids), _dev_ptr(d), _dev_ptr(ws),
                                   _ws_check(ws), _stream()))
     return ids, d
+
+
+def graph_add_reverse(fwd, degree: int, nthreads: int = 0) -> np.ndarray:
+    """CAGRA's reverse-edge step (fgpu_graph_add_reverse) on host arrays: fwd int32 [n][width], each row's
+    forward candidates nearest first; returns int32 [n][degree]."""
+    fwd = np.ascontiguousarray(fwd, np.int32)
+    n, width = fwd.shape
+    out = np.empty((n, degree), np.int32)
+    _check(lib.fgpu_graph_add_reverse(_np_ptr(fwd), n, width, degree, _np_ptr(out), nthreads))
+    return out
 
 
 def graph_search(queries, base, graph, k: int, itopk: int = 64, width: int = 4, max_iter: int = 64, seed: int = 1,

@@ -909,25 +909,55 @@ fgpu_status fgpu_coarse_graph_build(const fgpu_index* ix, int degree, int32_t* d
   std::vector<int32_t> f((size_t)nl * d2), g((size_t)nl * degree);
   FGPU_HIP(hipMemcpyAsync(f.data(), fwd, sizeof(int32_t) * f.size(), hipMemcpyDeviceToHost, s));
   FGPU_HIP(hipStreamSynchronize(s));
-  // Reverse edges, as CAGRA adds them (Ootomo et al., 2023): u -> v of the
-  // degree-nearest lists, listed at v by (rank of v in u's list, u).
-  std::vector<std::vector<std::pair<int, int>>> rev(nl);
-  for (int u = 0; u < nl; ++u)
-    for (int r = 0; r < degree; ++r) rev[f[(size_t)u * d2 + r]].push_back({r, u});
-  const int nf = degree - degree / 2;
-  for (int v = 0; v < nl; ++v) {
-    std::sort(rev[v].begin(), rev[v].end());
-    int32_t* o = g.data() + (size_t)v * degree;
-    int cnt = 0;
-    auto add = [&](int id) {
-      if (cnt < degree && std::find(o, o + cnt, id) == o + cnt) o[cnt++] = id;
-    };
-    for (int r = 0; r < nf; ++r) add(f[(size_t)v * d2 + r]);
-    for (size_t j = 0; j < rev[v].size() && cnt < degree; ++j) add(rev[v][j].second);
-    for (int r = nf; r < d2 && cnt < degree; ++r) add(f[(size_t)v * d2 + r]);
-  }
+  FGPU_TRY(fgpu_graph_add_reverse(f.data(), nl, d2, degree, g.data(), 1));
   FGPU_HIP(hipMemcpyAsync(d_graph, g.data(), sizeof(int32_t) * g.size(), hipMemcpyHostToDevice, s));
   FGPU_HIP(hipStreamSynchronize(s));
+  return FGPU_OK;
+}
+
+fgpu_status fgpu_graph_add_reverse(const int32_t* h_fwd, int64_t n, int width, int degree, int32_t* h_out,
+                                   int nthreads) {
+  FGPU_CHECK(h_fwd && h_out && n >= 0 && degree >= 1 && width >= degree && n < INT32_MAX, FGPU_ERR_ARG,
+             "graph_add_reverse: need n < 2^31 and 1 <= degree <= width");
+  // Reverse edges, as CAGRA adds them (Ootomo et al., 2023): each edge u -> v
+  // of the degree-nearest lists is listed at v, ordered by (rank of v in u's
+  // list, u).  Counting sort: in-degrees, offsets, then a fill by rank, then
+  // source, which leaves every node's list in that order.
+  std::vector<int64_t> off((size_t)n + 1, 0);
+  auto fwd = [&](int64_t u, int r) { return h_fwd[u * width + r]; };
+  for (int64_t u = 0; u < n; ++u)
+    for (int r = 0; r < degree; ++r) {
+      const int32_t v = fwd(u, r);
+      if (v >= 0 && v < n && v != u) ++off[(size_t)v + 1];
+    }
+  for (int64_t v = 0; v < n; ++v) off[(size_t)v + 1] += off[(size_t)v];
+  std::vector<int32_t> rev((size_t)off[(size_t)n]);
+  std::vector<int64_t> fill(off.begin(), off.end() - 1);
+  for (int r = 0; r < degree; ++r)
+    for (int64_t u = 0; u < n; ++u) {
+      const int32_t v = fwd(u, r);
+      if (v >= 0 && v < n && v != u) rev[(size_t)fill[(size_t)v]++] = (int32_t)u;
+    }
+  // Row v: its nearest degree - degree / 2 forward edges, then its reverse
+  // edges, then the rest of its forward list, without repeats; -1 pads.
+  const int nf = degree - degree / 2;
+  auto rows = [&](int64_t v0, int64_t v1) {
+    for (int64_t v = v0; v < v1; ++v) {
+      int32_t* o = h_out + v * degree;
+      int cnt = 0;
+      auto add = [&](int32_t id) {
+        if (id >= 0 && id < n && id != v && cnt < degree && std::find(o, o + cnt, id) == o + cnt) o[cnt++] = id;
+      };
+      for (int r = 0; r < nf; ++r) add(fwd(v, r));
+      for (int64_t j = off[(size_t)v]; j < off[(size_t)v + 1] && cnt < degree; ++j) add(rev[(size_t)j]);
+      for (int r = nf; r < width && cnt < degree; ++r) add(fwd(v, r));
+      for (; cnt < degree; ++cnt) o[cnt] = -1;
+    }
+  };
+  const int nt = (int)std::max<int64_t>(1, std::min<int64_t>(nthreads > 0 ? nthreads : 16, (n + 4095) / 4096));
+  std::vector<std::thread> th;
+  for (int t = 0; t < nt; ++t) th.emplace_back(rows, n * t / nt, n * (t + 1) / nt);
+  for (auto& t : th) t.join();
   return FGPU_OK;
 }
 

@@ -46,7 +46,7 @@ C5 = Config("c5", 5_000_000, 128, 256, 0.05, 0.15, 2026, 10_000, 2048, 32, 8, 10
 # with the config's compaction to the top 1000 and k = 100.
 C3_SEARCH = dict(p1_lists=12, limit_k=50, threshold_coeff=1.0, rerank_m=1000, mini_batch=128, eps=0.1, beta=2)
 # C5's graph search: fixed out-degree 32, itopk 64, width 4, at most 64 steps.
-C5_GRAPH = dict(degree=32, itopk=64, width=4, max_iter=64, random_edges=4)
+C5_GRAPH = dict(degree=32, itopk=64, width=4, max_iter=64, random_edges=8)
 
 
 def base(cfg: Config, n: int | None = None) -> np.ndarray:
@@ -71,39 +71,51 @@ def build_index(cfg: Config, dx, seed: int = 42):
                        train_rows=min(cfg.train_rows, dx.shape[0]) if cfg.train_rows else 0)
 
 
-def knn_graph(dx, degree: int = 32, random_edges: int = 4, nlist: int = 2048, pq_m: int = 32, batch: int = 1 << 18):
+def knn_graph(dx, degree: int = 32, random_edges: int = 4, nlist: int = 2048, pq_m: int = 32, batch: int = 1 << 18,
+              reverse: bool = True):
     """C5's fixed out-degree graph over the device rows dx, int32 [n][degree]
-    on the device.  Row v holds v's nearest other rows found by this library's
-    IVF-PQ search (nprobe 8, ADC top-64, then the exact top degree + 1 of those
-    64 by rerank with eps < 0, so every candidate is evaluated), self removed;
-    its last `random_edges` slots are replaced by seeded long-range edges
-    (a counter-based hash of (row, slot)).  A kNN graph over a well-separated
-    mixture has no edges between components; the long-range edges let a walk
-    from random seeds reach the query's component."""
+    on the device.  Each row's forward candidates are its nearest other rows
+    found by this library's IVF-PQ search (nprobe 8, ADC top-64, then the
+    exact top `width` + 1 of those 64 by rerank with eps < 0, so every
+    candidate is evaluated), self removed: width = degree, or with `reverse`
+    min(2 degree, 63), and then CAGRA's reverse-edge step
+    (graph_add_reverse: the nearest half of the forward edges, the reverse
+    edges by rank, the rest of the forward list).  The last `random_edges`
+    slots are then replaced by seeded long-range edges (a counter-based hash
+    of (row, slot)).  A kNN graph over a well-separated mixture has no edges
+    between components; the long-range edges let a walk from random seeds
+    reach the query's component, and the reverse edges reach the nodes that
+    no forward list names."""
     import torch  # noqa: PLC0415
 
-    from . import Index, rerank  # noqa: PLC0415
+    from . import Index, graph_add_reverse, rerank  # noqa: PLC0415
     n, dim = dx.shape
+    width = min(2 * degree, 63) if reverse else degree
     gcfg = Config("c5-graph", n, dim, 0, 0.0, 0.0, 0, 0, nlist, pq_m, 8, 64, train_rows=min(n, 1_000_000),
                   kmeans_iters=10, pq_iters=8)
     offs, ids, codes, cent, cb = build_index(gcfg, dx, seed=7)
     idx = Index.from_arrays(dim, pq_m, offs, ids, codes, cent, cb)
-    graph = torch.empty((n, degree), dtype=torch.int32, device=dx.device)
+    fwd = torch.empty((n, width), dtype=torch.int32, device=dx.device)
     sws = torch.empty(idx.search_workspace_bytes(min(batch, n), 8), dtype=torch.uint8, device=dx.device)
     cnt64 = torch.full((batch,), 64, dtype=torch.int32, device=dx.device)
     for b0 in range(0, n, batch):
         nb = min(batch, n - b0)
         aid, _ = idx.search(dx[b0:b0 + nb], 8, 64, workspace=sws)
-        gid, _, _ = rerank(dx[b0:b0 + nb], dx, aid, cnt64[:nb], degree + 1, 64, -1.0, 2)
+        gid, _, _ = rerank(dx[b0:b0 + nb], dx, aid, cnt64[:nb], width + 1, 64, -1.0, 2)
         rows = torch.arange(b0, b0 + nb, device=dx.device, dtype=torch.int32)[:, None]
         drop = (gid == rows) | (gid < 0)
-        order = torch.argsort(drop.to(torch.int8), dim=1, stable=True)[:, :degree]
-        graph[b0:b0 + nb] = torch.gather(gid, 1, order)
+        order = torch.argsort(drop.to(torch.int8), dim=1, stable=True)[:, :width]
+        fwd[b0:b0 + nb] = torch.where(torch.gather(drop, 1, order), -1, torch.gather(gid, 1, order))
     idx.check()
+    idx.close()
+    if reverse:
+        graph = torch.from_numpy(graph_add_reverse(fwd.cpu().numpy(), degree)).to(dx.device)
+    else:
+        graph = fwd
+    del fwd
     if random_edges > 0:
         r = torch.arange(n, device=dx.device, dtype=torch.int64)[:, None] * 1000003 + torch.arange(
             random_edges, device=dx.device, dtype=torch.int64)[None, :] * 7919 + 12345
         r = (r * 6364136223846793005 + 1442695040888963407) & ((1 << 62) - 1)
         graph[:, degree - random_edges:] = ((r >> 17) % n).to(torch.int32)
-    idx.close()
     return graph

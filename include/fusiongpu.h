@@ -398,6 +398,16 @@ fgpu_status fgpu_graph_search(const float* d_queries, int nq, const float* d_bas
 size_t fgpu_coarse_graph_workspace_bytes(int nlist, int degree);
 fgpu_status fgpu_coarse_graph_build(const fgpu_index* idx, int degree, int32_t* d_graph, void* d_workspace,
                                     size_t workspace_bytes, void* stream);
+/* CAGRA's reverse-edge step on host arrays (no reference counterpart: the
+ * reference gets its graphs from cuVS, cagra_adapter.cuh:10-26): h_fwd
+ * [n][width] holds each node's forward candidates nearest first (-1 and out-
+ * of-range ids are skipped); row v of h_out [n][degree] gets its nearest
+ * degree - degree / 2 forward edges, then the nodes u whose first `degree`
+ * forward edges include v, ordered by (rank of v there, u), then the rest of
+ * its forward list, without repeats or self edges, -1 padded.  nthreads <= 0:
+ * 16 host threads.  fgpu_coarse_graph_build uses it over the centroids. */
+fgpu_status fgpu_graph_add_reverse(const int32_t* h_fwd, int64_t n, int width, int degree, int32_t* h_out,
+                                   int nthreads);
 
 /* Approximate top-nprobe lists per query by that walk (itopk, width,
  * max_iter, seed as in fgpu_graph_search; nprobe <= itopk <= 64; the
