@@ -71,6 +71,10 @@ _SIGS = {
     "fgpu_search_screen_stats": (_i32, [_vp, _i32, _i32, _vp, _sz, _vp, _c.POINTER(_c.c_longlong), _i32]),
     "fgpu_index_screen_ready": (_i32, [_vp]),
     "fgpu_index_set_option": (_i32, [_vp, _i32, _i32]),
+    "fgpu_two_phase_search_precut": (_i32, [_vp, _vp, _i32, _vp, _i32, _i32, _i32, _f32, _i32, _vp, _vp, _vp, _vp,
+                                            _vp, _vp, _vp, _sz, _vp]),
+    "fgpu_rerank_state": (_i32, [_vp, _i32, _i32, _vp, _i64, _vp, _vp, _i32, _i32, _i32, _f32, _i32, _vp, _vp, _vp,
+                                 _vp, _vp, _i32, _vp]),
     "fgpu_graph_add_reverse": (_i32, [_vp, _i64, _i32, _i32, _vp, _i32]),
     "fgpu_search_stage_times": (_i32, [_vp, _c.POINTER(_c.c_float), _i32]),
     "fgpu_search_noalloc_max_bytes": (_sz, []),
@@ -535,9 +539,11 @@ class Index:
                         "clk_builder": v[4], "clk_scanner": v[5], "clk_total": v[6]}
 
     def two_phase_search(self, queries, probe_ids, p1_lists: int, limit_k: int, threshold_coeff: float,
-                         rerank_m: int, want_cutoffs: bool = False, workspace=None, stream=None):
+                         rerank_m: int, want_cutoffs: bool = False, workspace=None, stream=None,
+                         want_pre_cut: bool = False):
         """run_gpu_batch_logic after the coarse step: (top_ids [nq][rerank_m], top_dists, top_counts [nq],
-        cutoffs [nq][p1] or None, thresholds [nq] or None)."""
+        cutoffs [nq][p1] or None, thresholds [nq] or None) and, with want_pre_cut, each query's candidate count
+        before the rerank_m cut (fgpu_two_phase_search_precut; the reference's d_atomic)."""
         torch = _torch()
         with _on(stream):
             q = self._queries(queries)
@@ -552,6 +558,13 @@ class Index:
             tc = torch.empty(nq, dtype=torch.int32, device="cuda")
             cut = torch.empty((nq, max(p1, 1)), dtype=torch.float32, device="cuda") if want_cutoffs else None
             thr = torch.empty(nq, dtype=torch.float32, device="cuda") if want_cutoffs else None
+            if want_pre_cut:
+                pre = torch.empty(nq, dtype=torch.int32, device="cuda")
+                _check(lib.fgpu_two_phase_search_precut(self._h, _dev_ptr(q), nq, _dev_ptr(p), nprobe, p1_lists,
+                                                        limit_k, threshold_coeff, rerank_m, _dev_ptr(tid),
+                                                        _dev_ptr(td), _dev_ptr(tc), _opt_ptr(cut), _opt_ptr(thr),
+                                                        _dev_ptr(pre), _dev_ptr(ws), _ws_check(ws), _stream()))
+                return tid, td, tc, (cut[:, :p1] if want_cutoffs else None), thr, pre
             _check(lib.fgpu_two_phase_search(self._h, _dev_ptr(q), nq, _dev_ptr(p), nprobe, p1_lists, limit_k,
                                              threshold_coeff, rerank_m, _dev_ptr(tid), _dev_ptr(td), _dev_ptr(tc),
                                              _opt_ptr(cut), _opt_ptr(thr), _dev_ptr(ws), _ws_check(ws), _stream()))
@@ -716,9 +729,11 @@ def probe_counts(index: Index, probe_ids, stream=None):
 
 
 def rerank(queries, base, top_ids, top_counts, k: int, mini_batch: int = 128, eps: float = 0.1, beta: int = 2,
-           stream=None, spec: int = 0):
-    """run_gpu_rerank: exact L2 over the ADC-ordered candidates with the early stop: (ids, dists, visited).
-    spec: mini-batches computed at once (fgpu_rerank_spec: 0 automatic, 1, or 4); results do not depend on it."""
+           stream=None, spec: int = 0, want_state: bool = False):
+    """run_gpu_rerank: exact L2 over the ADC-ordered candidates with the early stop: (ids, dists, visited) and,
+    with want_state, the reference's stab[] (int32) and fin[] (uint8) as the walk leaves them
+    (fgpu_rerank_state).  spec: mini-batches computed at once (0 automatic, 1, or 4); results do not depend
+    on it."""
     torch = _torch()
     with _on(stream):
         q = _dev(queries, torch.float32, "queries", (None, None))
@@ -730,9 +745,13 @@ def rerank(queries, base, top_ids, top_counts, k: int, mini_batch: int = 128, ep
         ids = torch.empty((nq, k), dtype=torch.int32, device="cuda")
         d = torch.empty((nq, k), dtype=torch.float32, device="cuda")
         vis = torch.empty(nq, dtype=torch.int32, device="cuda")
-        _check(lib.fgpu_rerank_spec(_dev_ptr(q), nq, dim, _dev_ptr(b), b.shape[0], _dev_ptr(t), _dev_ptr(c), rm,
-                                    k, mini_batch, eps, beta, _dev_ptr(ids), _dev_ptr(d), _dev_ptr(vis), int(spec),
-                                    _stream()))
+        stab = torch.empty(nq, dtype=torch.int32, device="cuda") if want_state else None
+        fin = torch.empty(nq, dtype=torch.uint8, device="cuda") if want_state else None
+        _check(lib.fgpu_rerank_state(_dev_ptr(q), nq, dim, _dev_ptr(b), b.shape[0], _dev_ptr(t), _dev_ptr(c), rm,
+                                     k, mini_batch, eps, beta, _dev_ptr(ids), _dev_ptr(d), _dev_ptr(vis),
+                                     _opt_ptr(stab), _opt_ptr(fin), int(spec), _stream()))
+    if want_state:
+        return ids, d, vis, stab, fin
     return ids, d, vis
 
 

@@ -8,12 +8,15 @@
 // It loads <res>/ivf_data.bin + global_pq_codebook.bin, keeps the base
 // vectors in HBM for the exact rerank, runs the query batches through S
 // streams round-robin (search_pipeline.cu:168-214, 311-377) and prints the
-// reference's "Total time ... QPS" and "Recall@1/@10" lines plus a per-stage
-// timing table.
+// reference's "Total time ... QPS" and "Recall@1/@10" lines, a per-stage
+// timing table, and the GPU batch-logic breakdown with the candidate counts
+// and the pruning reduction rate (search_pipeline.cu:286-306).
 //
 // Per batch, on its stream: queries H2D from pinned memory, the coarse step,
-// the two-phase scan + top-rerank_m, the exact rerank, results D2H into
-// pinned memory.  The coarse step is exact by default; --coarse graph walks a
+// the probed lists' sizes (prune + count: the potential candidates), the
+// two-phase scan + top-rerank_m with each query's candidate count before the
+// cut (the reference's d_atomic), the exact rerank, results and counts D2H
+// into pinned memory.  The coarse step is exact by default; --coarse graph walks a
 // kNN graph of the centroids instead, with the reference's CAGRA search
 // parameters (itopk max(32, top_m), width 4, 200 iterations;
 // cagra_adapter.cuh:57-60) and graph degree 8 (cagra_adapter.cuh:15).  The
@@ -43,9 +46,16 @@ namespace {
 
 struct Ctx {
   hipStream_t s = nullptr;
-  hipEvent_t ev[6] = {};  // begin, after H2D, after coarse, after scan, after rerank, after D2H
+  // begin, after H2D, after coarse, after prune + count, after the two-phase
+  // scan, after rerank, after D2H
+  hipEvent_t ev[7] = {};
   float* h_q = nullptr;   // pinned
   int32_t* h_ids = nullptr;
+  int32_t* h_pre = nullptr;    // pinned: candidates before the rerank_m cut, per query
+  int32_t* h_total = nullptr;  // pinned: the batch's potential candidates (probed list sizes)
+  int32_t* d_cnt = nullptr;
+  int32_t* d_off = nullptr;
+  int32_t* d_pre = nullptr;
   float* d_q = nullptr;
   uint32_t* d_probes = nullptr;
   float* d_pd = nullptr;
@@ -161,6 +171,11 @@ int main(int argc, char** argv) {
     for (auto& e : c.ev) hip_ok(hipEventCreate(&e), "event");
     hip_ok(hipHostMalloc((void**)&c.h_q, sizeof(float) * batch * dim, hipHostMallocDefault), "pinned queries");
     hip_ok(hipHostMalloc((void**)&c.h_ids, sizeof(int32_t) * batch * final_k, hipHostMallocDefault), "pinned ids");
+    hip_ok(hipHostMalloc((void**)&c.h_pre, sizeof(int32_t) * batch, hipHostMallocDefault), "pinned counts");
+    hip_ok(hipHostMalloc((void**)&c.h_total, sizeof(int32_t), hipHostMallocDefault), "pinned total");
+    hip_ok(hipMalloc(&c.d_cnt, sizeof(int32_t) * batch), "hipMalloc");
+    hip_ok(hipMalloc(&c.d_off, sizeof(int32_t) * (batch + 1)), "hipMalloc");
+    hip_ok(hipMalloc(&c.d_pre, sizeof(int32_t) * batch), "hipMalloc");
     hip_ok(hipMalloc(&c.d_q, sizeof(float) * batch * dim), "hipMalloc");
     hip_ok(hipMalloc(&c.d_probes, sizeof(uint32_t) * batch * top_m), "hipMalloc");
     hip_ok(hipMalloc(&c.d_pd, sizeof(float) * batch * top_m), "hipMalloc");
@@ -173,7 +188,9 @@ int main(int argc, char** argv) {
     c.ws_bytes = ws;
   }
   std::vector<int32_t> results((size_t)nq * final_k, -1);
-  double t_stage[5] = {0, 0, 0, 0, 0};  // H2D, coarse, scan, rerank, D2H (ms summed over batches)
+  // H2D, coarse, prune + count, two-phase scan, rerank, D2H (ms summed over batches)
+  double t_stage[6] = {0, 0, 0, 0, 0, 0};
+  long long cand_total = 0, cand_max = 0;  // candidates before the cut, potential candidates (summed)
   int batches_done = 0;
   bool keep = false;
 
@@ -196,14 +213,16 @@ int main(int argc, char** argv) {
         slot = pending.front();
       }
       Ctx& c = ctx[slot];
-      hip_ok(hipEventSynchronize(c.ev[5]), "event sync");
+      hip_ok(hipEventSynchronize(c.ev[6]), "event sync");
       if (c.keep) {
         std::memcpy(results.data() + (size_t)c.start * final_k, c.h_ids, sizeof(int32_t) * c.size * final_k);
-        for (int j = 0; j < 5; ++j) {
+        for (int j = 0; j < 6; ++j) {
           float ms = 0.0f;
           hip_ok(hipEventElapsedTime(&ms, c.ev[j], c.ev[j + 1]), "elapsed");
           t_stage[j] += ms;
         }
+        for (int i = 0; i < c.size; ++i) cand_total += c.h_pre[i];
+        cand_max += *c.h_total;
         ++batches_done;
       }
       {
@@ -234,16 +253,21 @@ int main(int argc, char** argv) {
       ok(fgpu_coarse_search(idx, c.d_q, size, top_m, prune_ratio, c.d_probes, c.d_pd, c.d_ws, c.ws_bytes, c.s),
          "coarse search");
     hip_ok(hipEventRecord(c.ev[2], c.s), "record");
-    ok(fgpu_two_phase_search(idx, c.d_q, size, c.d_probes, top_m, p1_lists, limit_k, coeff, rerank_m, c.d_tid, c.d_td,
-                             c.d_tcnt, nullptr, nullptr, c.d_ws, c.ws_bytes, c.s),
-       "two-phase scan");
+    // the probed lists' sizes: each query's potential candidates and their total (d_off[size])
+    ok(fgpu_probe_counts(idx, c.d_probes, size, top_m, c.d_cnt, c.d_off, c.s), "probe counts");
     hip_ok(hipEventRecord(c.ev[3], c.s), "record");
+    ok(fgpu_two_phase_search_precut(idx, c.d_q, size, c.d_probes, top_m, p1_lists, limit_k, coeff, rerank_m, c.d_tid,
+                                    c.d_td, c.d_tcnt, nullptr, nullptr, c.d_pre, c.d_ws, c.ws_bytes, c.s),
+       "two-phase scan");
+    hip_ok(hipEventRecord(c.ev[4], c.s), "record");
     ok(fgpu_rerank(c.d_q, size, dim, d_base, n, c.d_tid, c.d_tcnt, rerank_m, final_k, mb, eps, beta, c.d_ids, c.d_d,
                    nullptr, c.s),
        "rerank");
-    hip_ok(hipEventRecord(c.ev[4], c.s), "record");
-    hip_ok(hipMemcpyAsync(c.h_ids, c.d_ids, sizeof(int32_t) * size * final_k, hipMemcpyDeviceToHost, c.s), "D2H");
     hip_ok(hipEventRecord(c.ev[5], c.s), "record");
+    hip_ok(hipMemcpyAsync(c.h_ids, c.d_ids, sizeof(int32_t) * size * final_k, hipMemcpyDeviceToHost, c.s), "D2H");
+    hip_ok(hipMemcpyAsync(c.h_pre, c.d_pre, sizeof(int32_t) * size, hipMemcpyDeviceToHost, c.s), "D2H");
+    hip_ok(hipMemcpyAsync(c.h_total, c.d_off + size, sizeof(int32_t), hipMemcpyDeviceToHost, c.s), "D2H");
+    hip_ok(hipEventRecord(c.ev[6], c.s), "record");
     {
       std::lock_guard<std::mutex> lk(mu);
       c.start = start;
@@ -277,17 +301,39 @@ int main(int argc, char** argv) {
   const double ms = std::chrono::duration<double, std::milli>(t1 - t0).count();
   std::cout << "\nTotal time: " << ms << " ms, QPS: " << nq / (ms / 1000.0) << std::endl;
   std::cout << "\n============= Pipeline Timing Breakdown =============\n" << std::fixed << std::setprecision(3);
+  const double nbd = batches_done ? (double)batches_done : 1.0;
+  const double avg[6] = {t_stage[0] / nbd, t_stage[1] / nbd, t_stage[2] / nbd,
+                         t_stage[3] / nbd, t_stage[4] / nbd, t_stage[5] / nbd};
   const char* names[5] = {"H2D:          ", "Coarse:       ", "Scan (PQ):    ", "Rerank (GPU): ", "D2H:          "};
+  const double stage[5] = {avg[0], avg[1], avg[2] + avg[3], avg[4], avg[5]};
   double sum = 0;
   for (int j = 0; j < 5; ++j) {
-    const double avg = batches_done ? t_stage[j] / batches_done : 0.0;
-    sum += avg;
-    std::cout << "  " << names[j] << std::setw(8) << avg << " ms\n";
+    sum += stage[j];
+    std::cout << "  " << names[j] << std::setw(8) << stage[j] << " ms\n";
   }
   std::cout << "  -----------------------------------------\n";
   std::cout << "  Sum of stages:" << std::setw(8) << sum << " ms\n";
   std::cout << "  batch count:  " << batches_done << "\n";
   std::cout << "=====================================================\n";
+  // The reference's fine-grained table (search_pipeline.cu:286-306).  Here the
+  // prune runs inside the coarse step's select and the offsets with the
+  // counts; steps 1-3 have no work (the LUTs are built on chip, the pool is
+  // bounded on the device, no host round trip) and steps 4a-7 are one kernel.
+  std::cout << "\n============= GPU Batch Logic Fine-grained Breakdown (Avg/Batch) =============\n";
+  std::cout << "  0. Prune+Count (Fused):     " << std::setw(8) << avg[2] << " ms\n";
+  std::cout << "  1. Scan Offsets (Prefix):   " << std::setw(8) << 0.0 << " ms  (with 0)\n";
+  std::cout << "  2. Precompute (Residual):   " << std::setw(8) << 0.0 << " ms  (LUTs built in the scan)\n";
+  std::cout << "  3. Resize Check & Sync:     " << std::setw(8) << 0.0 << " ms  (no host round trip)\n";
+  std::cout << "  4-7. Two-phase scan, select, sort (one kernel): " << std::setw(8) << avg[3] << " ms\n";
+  std::cout << "----------------------------------------------------------------\n";
+  std::cout << "  Total GPU Batch Kernel:     " << std::setw(8) << avg[2] + avg[3] << " ms\n";
+  const long long avg_max = batches_done ? cand_max / batches_done : 0;
+  const long long avg_real = batches_done ? cand_total / batches_done : 0;
+  std::cout << "  [Allocated] Max Potential Candidates: " << avg_max << "\n";
+  std::cout << "  [Actual]    Filtered Real Candidates: " << avg_real << " (Sorted Size)\n";
+  const double reduction = avg_max > 0 ? 100.0 * (1.0 - (double)avg_real / (double)avg_max) : 0.0;
+  std::cout << "  >> Pruning Reduction Rate: " << std::setprecision(1) << reduction << " %\n";
+  std::cout << "============================================================================\n";
   std::cout.unsetf(std::ios::fixed);
   std::cout << std::setprecision(6);
   if (!out_path.empty()) {  // the result ids as ivecs (one row of final_k per query)
@@ -315,8 +361,10 @@ int main(int argc, char** argv) {
     for (auto& e : c.ev) (void)hipEventDestroy(e);
     (void)hipHostFree(c.h_q);
     (void)hipHostFree(c.h_ids);
+    (void)hipHostFree(c.h_pre);
+    (void)hipHostFree(c.h_total);
     for (void* p : {(void*)c.d_q, (void*)c.d_probes, (void*)c.d_pd, (void*)c.d_tid, (void*)c.d_td, (void*)c.d_tcnt,
-                    (void*)c.d_ids, (void*)c.d_d, c.d_ws})
+                    (void*)c.d_ids, (void*)c.d_d, c.d_ws, (void*)c.d_cnt, (void*)c.d_off, (void*)c.d_pre})
       (void)hipFree(p);
   }
   (void)hipFree(d_base);

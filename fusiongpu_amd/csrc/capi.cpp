@@ -681,7 +681,8 @@ namespace {
 fgpu_status two_phase(const fgpu_index* ix, const float* dq, int nq, const uint32_t* d_probe_ids, int nprobe,
                       int p1_lists, int limit_k, float threshold_coeff, int rerank_m, int32_t* d_top_ids,
                       float* d_top_dists, int32_t* d_top_counts, float* d_list_cutoffs, float* d_thresholds,
-                      unsigned long long* d_stats, void* ws, size_t ws_bytes, void* stream) {
+                      unsigned long long* d_stats, void* ws, size_t ws_bytes, void* stream,
+                      int32_t* d_pre_cut = nullptr) {
   FGPU_CHECK(ix && ws && (nq == 0 || (dq && d_probe_ids && d_top_ids && d_top_dists && d_top_counts)), FGPU_ERR_ARG,
              "two_phase_search: null argument");
   FGPU_CHECK(nq >= 0 && nprobe >= 1 && nprobe <= 256, FGPU_ERR_ARG, "two_phase_search: need 1 <= nprobe <= 256");
@@ -710,6 +711,7 @@ fgpu_status two_phase(const fgpu_index* ix, const float* dq, int nq, const uint3
     // query's phase-1 lists over several workgroups.
     a.split = two_phase_split(nb, p1, limit_k, ix->opt_two_phase_split);
     a.cut_ws = cut_ws;
+    a.pre_cut = d_pre_cut ? d_pre_cut + q0 : nullptr;
     FGPU_TRY(launch_two_phase(ix->dim, ix->m, a, as_stream(stream)));
   }
   return FGPU_OK;
@@ -725,6 +727,16 @@ fgpu_status fgpu_two_phase_search(const fgpu_index* ix, const float* dq, int nq,
                                   void* stream) {
   return two_phase(ix, dq, nq, d_probe_ids, nprobe, p1_lists, limit_k, threshold_coeff, rerank_m, d_top_ids,
                    d_top_dists, d_top_counts, d_list_cutoffs, d_thresholds, nullptr, ws, ws_bytes, stream);
+}
+
+fgpu_status fgpu_two_phase_search_precut(const fgpu_index* ix, const float* dq, int nq,
+                                         const uint32_t* d_probe_ids, int nprobe, int p1_lists, int limit_k,
+                                         float threshold_coeff, int rerank_m, int32_t* d_top_ids, float* d_top_dists,
+                                         int32_t* d_top_counts, float* d_list_cutoffs, float* d_thresholds,
+                                         int32_t* d_pre_cut, void* ws, size_t ws_bytes, void* stream) {
+  FGPU_CHECK(d_pre_cut || nq == 0, FGPU_ERR_ARG, "two_phase_search_precut: null d_pre_cut");
+  return two_phase(ix, dq, nq, d_probe_ids, nprobe, p1_lists, limit_k, threshold_coeff, rerank_m, d_top_ids,
+                   d_top_dists, d_top_counts, d_list_cutoffs, d_thresholds, nullptr, ws, ws_bytes, stream, d_pre_cut);
 }
 
 fgpu_status fgpu_two_phase_search_stats(const fgpu_index* ix, const float* dq, int nq, const uint32_t* d_probe_ids,
@@ -747,6 +759,15 @@ fgpu_status fgpu_rerank_spec(const float* dq, int nq, int dim, const float* d_ba
                              const int32_t* d_top_ids, const int32_t* d_top_counts, int rerank_m, int k,
                              int mini_batch, float eps, int beta, int32_t* d_final_ids, float* d_final_dists,
                              int32_t* d_visited, int spec, void* stream) {
+  return fgpu_rerank_state(dq, nq, dim, d_base, n, d_top_ids, d_top_counts, rerank_m, k, mini_batch, eps, beta,
+                           d_final_ids, d_final_dists, d_visited, nullptr, nullptr, spec, stream);
+}
+
+fgpu_status fgpu_rerank_state(const float* dq, int nq, int dim, const float* d_base, int64_t n,
+                              const int32_t* d_top_ids, const int32_t* d_top_counts, int rerank_m, int k,
+                              int mini_batch, float eps, int beta, int32_t* d_final_ids, float* d_final_dists,
+                              int32_t* d_visited, int32_t* d_stable_cnt, uint8_t* d_finished, int spec,
+                              void* stream) {
   FGPU_CHECK(d_base && (nq == 0 || (dq && d_top_ids && d_top_counts && d_final_ids && d_final_dists)), FGPU_ERR_ARG,
              "rerank: null argument");
   FGPU_CHECK(nq >= 0 && n >= 0 && rerank_m >= 1 && k >= 1 && mini_batch >= 1, FGPU_ERR_ARG, "rerank: bad sizes");
@@ -755,6 +776,8 @@ fgpu_status fgpu_rerank_spec(const float* dq, int nq, int dim, const float* d_ba
   RerankArgs a{dq, d_base, (long long)n, d_top_ids, d_top_counts, nq, rerank_m, k, mini_batch, eps, beta,
                d_final_ids, d_final_dists, d_visited};
   a.spec = spec < 0 ? 0 : spec;
+  a.stable = d_stable_cnt;
+  a.finished = d_finished;
   return launch_rerank(dim, a, as_stream(stream));
 }
 

@@ -204,6 +204,11 @@ struct TwoPhaseArgs {
   // cut_ws holds [nq][nprobe] phase-1 cutoffs between the two launches.
   int split = 1;
   float* cut_ws = nullptr;
+  // [nq] or nullptr: candidates before the rerank_m cut (phase-1 slots plus
+  // every phase-2 vector with dist <= thr).  When set, phase 2 skips lists
+  // and ends sums against thr itself rather than the pool's admission bound,
+  // so that every such vector is seen.
+  int32_t* pre_cut = nullptr;
 };
 int two_phase_pool_cap(int p1, int limit_k, int rerank_m);
 // Workgroups a query for phase 1 (TwoPhaseArgs::split) for a launch of nq
@@ -225,6 +230,11 @@ struct RerankArgs {
   float* out_d;             // [nq][k]
   int32_t* visited;         // [nq] or nullptr
   int spec = 0;             // mini-batches computed a step: 0 automatic, 1, or 4 (any other value)
+  // [nq] or nullptr: the stable count after the last batch evaluated, and 1
+  // when the walk stopped on stability or reached an offset at or past the
+  // candidates before rm (the reference's stab[] and fin[]).
+  int32_t* stable = nullptr;
+  uint8_t* finished = nullptr;
 };
 fgpu_status launch_rerank(int dim, const RerankArgs& a, hipStream_t s);
 // Mini-batches the rerank kernel computes at once for nq queries (1 or 4);

@@ -174,6 +174,7 @@ void two_phase_kernel(TwoPhaseArgs a) {
   __shared__ int f_base[kMaxProbes + 1];  // phase-1 list f's pool slots start at f_base[f] (limit_k <= 64)
   __shared__ int s_nv, s_nv1;
   __shared__ int s_cnt;
+  __shared__ int s_pre;  // phase-2 vectors with dist <= thr (TwoPhaseArgs::pre_cut)
   __shared__ unsigned long long s_lthr;
   __shared__ unsigned long long s_pub[kTW];  // phase 1: each wave's Q-th best key of the current list
 
@@ -238,6 +239,7 @@ void two_phase_kernel(TwoPhaseArgs a) {
       s_nv = nv_run;
       s_nv1 = nv1_run;
       s_cnt = 0;
+      s_pre = 0;
       s_lthr = kNoThr;
     }
   }
@@ -536,9 +538,13 @@ void two_phase_kernel(TwoPhaseArgs a) {
   const int seg = cap - R;  // vectors per segment: their passers always fit after a select
   uint64_t adm = kNoKey;
   float thr_d = thr;
+  // Counting the candidates before the cut: every vector with dist <= thr is
+  // counted, so skips and early ends use thr, never the admission bound.
+  const bool count_all = a.pre_cut != nullptr;
+  int n_thr = 0;  // this wave's phase-2 vectors with dist <= thr (count_all)
   for (int f = nv1; f < nv; ++f) {
     // thr_d only shrinks (selects lower adm), so a list skipped now stays skippable.
-    const float thr_hi = thr_d * (1.0f + 0x1p-16f);
+    const float thr_hi = (count_all ? thr : thr_d) * (1.0f + 0x1p-16f);
     if (f_lb[f] > thr_hi) {
       ++st_skip;
       continue;
@@ -581,7 +587,9 @@ void two_phase_kernel(TwoPhaseArgs a) {
         loaded = false;
         const int v0 = base + lane, v1 = v0 + kWave;
         float d0, d1;
-        if (adc_sum2<M>(lut, w0, w1, v0 < s1, v1 < s1, thr_d, d0, d1)) {
+        if (adc_sum2<M>(lut, w0, w1, v0 < s1, v1 < s1, count_all ? thr : thr_d, d0, d1)) {
+          if (count_all)
+            n_thr += __popcll(__ballot(v0 < s1 && d0 <= thr)) + __popcll(__ballot(v1 < s1 && d1 <= thr));
           const uint64_t k0 = key_of(d0, i0), k1 = key_of(d1, i1);
           const bool pass0 = v0 < s1 && d0 <= thr && k0 < adm;
           const bool pass1 = v1 < s1 && d1 <= thr && k1 < adm;
@@ -619,8 +627,10 @@ void two_phase_kernel(TwoPhaseArgs a) {
   }
 
   // ---------------- top rerank_m: select, LDS bitonic sort, gather
+  if (count_all && lane == 0 && n_thr) atomicAdd(&s_pre, n_thr);
   __syncthreads();
   int cnt = s_cnt;
+  if (count_all && tid == 0) a.pre_cut[q] = f_base[nv1] + s_pre;
   if (cnt > R) {
     pool_select(pool, cnt, R, hist, misc);
     cnt = R;
@@ -902,6 +912,11 @@ __global__ __launch_bounds__(kRT * SPEC) void rerank_kernel(RerankArgs a) {
     a.out_d[(size_t)q * k + j] = pad ? FLT_MAX : key_dist(kk);
   }
   if (a.visited && tid == 0) a.visited[q] = seen;
+  if (tid == 0) {
+    if (a.stable) a.stable[q] = s_stable;
+    // finished: stopped on stability, or an offset below rm reached the end of the candidates
+    if (a.finished) a.finished[q] = (s_fin || (total + mb - 1) / mb * mb < rm) ? 1 : 0;
+  }
 }
 
 template <int D>

@@ -284,6 +284,21 @@ fgpu_status fgpu_two_phase_search(const fgpu_index* idx, const float* d_queries,
                                   float* d_thresholds, void* d_workspace, size_t workspace_bytes,
                                   void* stream);
 
+/* fgpu_two_phase_search that also writes d_pre_cut [nq]: each query's
+ * candidates before the rerank_m cut, the count the reference accumulates in
+ * d_atomic (query_atomic_counters, gpu_global.cu:349, 493-526; summed by
+ * search_pipeline.cu:455-457 for its pruning figures): the sum over the
+ * phase-1 lists of min(n_l, limit_k) plus every phase-2 vector with dist <=
+ * thr.  Results are those of fgpu_two_phase_search; phase 2 then skips lists
+ * against thr itself, not against the pool's admission bound, so a batch
+ * whose pools overflow may take longer. */
+fgpu_status fgpu_two_phase_search_precut(const fgpu_index* idx, const float* d_queries, int nq,
+                                         const uint32_t* d_probe_ids, int nprobe, int p1_lists, int limit_k,
+                                         float threshold_coeff, int rerank_m, int32_t* d_top_ids, float* d_top_dists,
+                                         int32_t* d_top_counts, float* d_list_cutoffs, float* d_thresholds,
+                                         int32_t* d_pre_cut, void* d_workspace, size_t workspace_bytes,
+                                         void* stream);
+
 /* fgpu_two_phase_search plus instrumentation (no reference counterpart): adds
  * to d_stats[0..10] (device, caller-zeroed, uint64) the vectors whose codes
  * were loaded, the LUTs built, the phase-2 lists skipped by the list lower
@@ -321,6 +336,17 @@ fgpu_status fgpu_rerank_spec(const float* d_queries, int nq, int dim, const floa
                              const int32_t* d_top_ids, const int32_t* d_top_counts, int rerank_m, int k,
                              int mini_batch, float eps, int beta, int32_t* d_final_ids, float* d_final_dists,
                              int32_t* d_visited, int spec, void* stream);
+/* fgpu_rerank_spec that also writes the state the reference's rerank leaves
+ * in stab[] and fin[] (gpu_global.cu:603-609, 615, 653-662; run_gpu_rerank's
+ * d_stable_cnt and d_finished): d_stable_cnt [nq] (optional) = the stable
+ * count after the last batch evaluated; d_finished [nq] (optional, one byte a
+ * query, 0 or 1) = 1 when the walk stopped on stability or reached an offset
+ * below rerank_m at or past the query's candidates. */
+fgpu_status fgpu_rerank_state(const float* d_queries, int nq, int dim, const float* d_base, int64_t n,
+                              const int32_t* d_top_ids, const int32_t* d_top_counts, int rerank_m, int k,
+                              int mini_batch, float eps, int beta, int32_t* d_final_ids, float* d_final_dists,
+                              int32_t* d_visited, int32_t* d_stable_cnt, uint8_t* d_finished, int spec,
+                              void* stream);
 
 /* coarse + two-phase + rerank in one call: the SearchPipeline per-batch path
  * (search_pipeline.cu:341-361) with final_k = k. */

@@ -287,7 +287,9 @@ inline void load_ivf_index_to_gpu(const std::string& res_dir, IVFIndexGPU& idx, 
  * d_top_ids / d_top_dists [batch_size][rerank_m] (pad -1 / FLT_MAX) and
  * d_top_counts; d_list_cutoffs [batch_size][min(top_m, p1_lists)] and
  * d_thresholds [batch_size] as the reference writes them; d_atomic gets each
- * query's kept count.  The candidate pool lives in d_flat_ids
+ * query's candidate count before the rerank_m cut (the reference's
+ * query_atomic_counters, gpu_global.cu:349, 493-526, which
+ * search_pipeline.cu:455-457 sums).  The candidate pool lives in d_flat_ids
  * (current_pool_cap ints); when that is too small for the batch the four pool
  * buffers are reallocated (the reference's growth rule: 1.5x what is needed)
  * after the stream is synchronised.  d_global_tables, d_compact_offsets and
@@ -327,17 +329,21 @@ inline void run_gpu_batch_logic(const IVFIndexGPU& idx, float* d_queries, uint32
     d::hip_check(hipMalloc(&d_flat_dists_alt, current_pool_cap * sizeof(float)), "hipMalloc");
   }
   if (events) d::record(events->evt_resize_sync, s);
-  d::check(fgpu_two_phase_search(ix, d_queries, batch_size, d_cagra_top_m, top_m, p1_lists, limit_k, threshold_coeff,
-                                 rerank_m, d_top_ids, d_top_dists, d_top_counts, d_list_cutoffs, d_thresholds,
-                                 d_flat_ids, current_pool_cap * sizeof(int), s),
-           "run_gpu_batch_logic");
+  if (d_atomic)
+    d::check(fgpu_two_phase_search_precut(ix, d_queries, batch_size, d_cagra_top_m, top_m, p1_lists, limit_k,
+                                          threshold_coeff, rerank_m, d_top_ids, d_top_dists, d_top_counts,
+                                          d_list_cutoffs, d_thresholds, d_atomic, d_flat_ids,
+                                          current_pool_cap * sizeof(int), s),
+             "run_gpu_batch_logic");
+  else
+    d::check(fgpu_two_phase_search(ix, d_queries, batch_size, d_cagra_top_m, top_m, p1_lists, limit_k,
+                                   threshold_coeff, rerank_m, d_top_ids, d_top_dists, d_top_counts, d_list_cutoffs,
+                                   d_thresholds, d_flat_ids, current_pool_cap * sizeof(int), s),
+             "run_gpu_batch_logic");
   if (events) {
     d::record(events->evt_scan_phase1_end, s);
     d::record(events->evt_scan_cand, s);
   }
-  if (d_atomic && batch_size > 0)
-    d::hip_check(hipMemcpyAsync(d_atomic, d_top_counts, sizeof(int) * batch_size, hipMemcpyDeviceToDevice, s),
-                 "hipMemcpyAsync");
   if (events) {
     d::record(events->evt_compact, s);
     d::record(events->evt_sort, s);
@@ -348,17 +354,19 @@ inline void run_gpu_batch_logic(const IVFIndexGPU& idx, float* d_queries, uint32
 /* run_gpu_rerank (gpu_global.cu:667-673): exact L2 over the first
  * d_top_counts[q] ids of d_top_ids [bs][rm] in mini-batches of mb, early stop
  * after b batches that change at most eps * k of the top k.  d_base_vecs
- * [tv][DIM].  The stable counters and finished flags live inside the kernel:
- * d_stable_cnt and d_finished are not written. */
+ * [tv][DIM].  d_stable_cnt and d_finished [batch_size] are left as the
+ * reference leaves them (gpu_global.cu:603-609, 653-662): the stable count
+ * after the last batch evaluated, and whether the walk stopped on stability
+ * or ran past its candidates before rerank_m. */
 inline void run_gpu_rerank(float* d_queries, int* d_top_ids, int* d_top_counts, float* d_base_vecs, int* d_final_ids,
                            float* d_final_dists, int* d_stable_cnt, bool* d_finished, int batch_size, int rerank_m,
                            int final_k, int total_vecs, int mini_batch_size, float epsilon, int beta,
                            hipStream_t stream) {
-  (void)d_stable_cnt;
-  (void)d_finished;
-  fgpu_compat_detail::check(fgpu_rerank(d_queries, batch_size, DIM, d_base_vecs, total_vecs, d_top_ids, d_top_counts,
-                                        rerank_m, final_k, mini_batch_size, epsilon, beta, d_final_ids, d_final_dists,
-                                        nullptr, stream),
+  static_assert(sizeof(bool) == 1, "d_finished is read as one byte a query");
+  fgpu_compat_detail::check(fgpu_rerank_state(d_queries, batch_size, DIM, d_base_vecs, total_vecs, d_top_ids,
+                                              d_top_counts, rerank_m, final_k, mini_batch_size, epsilon, beta,
+                                              d_final_ids, d_final_dists, nullptr, d_stable_cnt,
+                                              reinterpret_cast<uint8_t*>(d_finished), 0, stream),
                             "run_gpu_rerank");
 }
 

@@ -40,8 +40,9 @@ _SIGS = {
     "orc_search_plain": (None, [_vp, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _vp, _vp, _i32]),
     "orc_knn_exact": (None, [_vp, _i32, _vp, _i64, _i32, _i32, _vp, _vp, _i32]),
     "orc_search_two_phase": (None, [_vp, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _i32, _vp, _i32, _i32, _i32,
-                                    _f32, _i32, _vp, _vp, _vp, _vp, _vp, _i32]),
-    "orc_rerank": (None, [_vp, _i32, _i32, _vp, _i64, _vp, _vp, _i32, _i32, _i32, _f32, _i32, _vp, _vp, _vp, _i32]),
+                                    _f32, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _i32]),
+    "orc_rerank": (None, [_vp, _i32, _i32, _vp, _i64, _vp, _vp, _i32, _i32, _i32, _f32, _i32, _vp, _vp, _vp, _vp, _vp,
+                          _i32]),
     "orc_graph_search": (None, [_vp, _i32, _vp, _i64, _i32, _vp, _i32, _i32, _i32, _i32, _i32, _u64, _vp, _vp, _vp,
                                 _i32]),
     "orc_kmeans_assign": (None, [_vp, _i64, _vp, _i32, _i32, _vp, _i32]),
@@ -143,8 +144,9 @@ def search_plain(q, cent, codebook, offsets, ids, codes, probe_ids, k, nthreads=
 
 
 def search_two_phase(q, cent, codebook, offsets, ids, codes, probe_ids, p1_lists, limit_k, threshold_coeff, rerank_m,
-                     nthreads=0):
-    """run_gpu_batch_logic restated: (top_ids [nq][rerank_m], top_dists, counts [nq], cutoffs [nq][p1], thr [nq])."""
+                     nthreads=0, want_pre_cut=False):
+    """run_gpu_batch_logic restated: (top_ids [nq][rerank_m], top_dists, counts [nq], cutoffs [nq][p1], thr [nq])
+    and, with want_pre_cut, each query's candidate count before the rerank_m cut (the reference's d_atomic)."""
     q, cent, codebook, offsets, ids, codes = f32(q), f32(cent), f32(codebook), i32(offsets), i32(ids), u8(codes)
     probe_ids = np.ascontiguousarray(probe_ids, np.uint32)
     nq, dim = q.shape
@@ -155,22 +157,30 @@ def search_two_phase(q, cent, codebook, offsets, ids, codes, probe_ids, p1_lists
     cnt = np.empty(nq, np.int32)
     cut = np.empty((nq, max(p1, 1)), np.float32)
     thr = np.empty(nq, np.float32)
+    pre = np.empty(nq, np.int32)
     lib.orc_search_two_phase(_p(q), nq, dim, codebook.shape[0], _p(cent), _p(codebook), _p(offsets), _p(ids),
                              _p(codes), cent.shape[0], _p(probe_ids), nprobe, p1_lists, limit_k, threshold_coeff,
-                             rerank_m, _p(oid), _p(od), _p(cnt), _p(cut), _p(thr), nthreads)
+                             rerank_m, _p(oid), _p(od), _p(cnt), _p(cut), _p(thr), _p(pre), nthreads)
+    if want_pre_cut:
+        return oid, od, cnt, cut[:, :p1], thr, pre
     return oid, od, cnt, cut[:, :p1], thr
 
 
-def rerank(q, base, cand_ids, counts, k, mb=128, eps=0.1, beta=2, nthreads=0):
-    """run_gpu_rerank restated: (ids [nq][k], dists [nq][k], visited [nq])."""
+def rerank(q, base, cand_ids, counts, k, mb=128, eps=0.1, beta=2, nthreads=0, want_state=False):
+    """run_gpu_rerank restated: (ids [nq][k], dists [nq][k], visited [nq]) and, with want_state, the
+    reference's stab[] (int32) and fin[] (uint8) as it leaves them."""
     q, base, cand_ids, counts = f32(q), f32(base), i32(cand_ids), i32(counts)
     nq, dim = q.shape
     rm = cand_ids.shape[1]
     oid = np.empty((nq, k), np.int32)
     od = np.empty((nq, k), np.float32)
     vis = np.empty(nq, np.int32)
+    stab = np.empty(nq, np.int32)
+    fin = np.empty(nq, np.uint8)
     lib.orc_rerank(_p(q), nq, dim, _p(base), base.shape[0], _p(cand_ids), _p(counts), rm, k, mb, eps, beta, _p(oid),
-                   _p(od), _p(vis), nthreads)
+                   _p(od), _p(vis), _p(stab), _p(fin), nthreads)
+    if want_state:
+        return oid, od, vis, stab, fin
     return oid, od, vis
 
 

@@ -321,14 +321,17 @@ void orc_search_plain(const float* q, int nq, int dim, int m, const float* cent,
 // gpu_global.cu:508-526), all rerank_m entries are gathered (the reference's
 // gather writes at most 128, gpu_global.cu:867), and order is the tie rule
 // (dist, then id) where the reference's depends on atomic slot races.
-// Probe ids >= nlist count as pruned.  cutoffs ([nq][p1]) and thr ([nq]) are
-// optional outputs.
+// Probe ids >= nlist count as pruned.  cutoffs ([nq][p1]), thr ([nq]) and
+// pre_cut ([nq]) are optional outputs; pre_cut[q] is the number of candidates
+// before the rerank_m cut, the count the reference accumulates in
+// query_atomic_counters (gpu_global.cu:349, 493-526): sum over phase-1 lists
+// of min(n_l, limit_k) plus every phase-2 vector with dist <= thr.
 void orc_search_two_phase(const float* q, int nq, int dim, int m, const float* cent,
                           const float* codebook, const int* offsets, const int* vec_ids,
                           const uint8_t* codes, int nlist, const uint32_t* probe_ids, int nprobe,
                           int p1_lists, int limit_k, float threshold_coeff, int rerank_m,
                           int* out_ids, float* out_dists, int* out_counts, float* cutoffs,
-                          float* thr_out, int nthreads) {
+                          float* thr_out, int* pre_cut, int nthreads) {
   set_threads(nthreads);
   const int p1 = std::max(0, std::min(nprobe, p1_lists));
 #pragma omp parallel
@@ -367,6 +370,7 @@ void orc_search_two_phase(const float* q, int nq, int dim, int m, const float* c
           if (d <= thr) cand.push_back({d, vec_ids[v]});
         }
       }
+      if (pre_cut) pre_cut[i] = (int)cand.size();
       const int cnt = std::min((int)cand.size(), rerank_m);
       std::partial_sort(cand.begin(), cand.begin() + cnt, cand.end());
       for (int j = 0; j < rerank_m; ++j) {
@@ -389,10 +393,15 @@ void orc_search_two_phase(const float* q, int nq, int dim, int m, const float* c
 // (FLT_MAX, -1) after every real entry; the reference sorts only 128 of the
 // k+mb entries (gpu_global.cu:644-647) -- all are sorted here.  A candidate id
 // outside [0, n) is skipped (treated as padding).  visited ([nq], optional) =
-// candidates evaluated.
+// candidates evaluated; stable_out / finished_out ([nq], optional) = the
+// state the reference leaves in stab[] and fin[] (gpu_global.cu:603-609,
+// 615, 653-662): the stable count after the last batch evaluated, and
+// finished when the walk stopped on stability or reached an offset past the
+// candidates before rm.
 void orc_rerank(const float* q, int nq, int dim, const float* base, long long n,
                 const int* cand_ids, const int* counts, int rm, int k, int mb, float eps, int beta,
-                int* out_ids, float* out_dists, int* visited, int nthreads) {
+                int* out_ids, float* out_dists, int* visited, int* stable_out, uint8_t* finished_out,
+                int nthreads) {
   set_threads(nthreads);
 #pragma omp parallel
   {
@@ -402,9 +411,13 @@ void orc_rerank(const float* q, int nq, int dim, const float* base, long long n,
       const float* qi = q + (size_t)i * dim;
       top.assign(k, {FLT_MAX, 0xFFFFFFFFu});
       int stable = 0, seen = 0;
+      bool fin = false;
       const int total = std::min(counts[i], rm);
       for (int off = 0; off < rm; off += mb) {
-        if (off >= total) break;
+        if (off >= total) {
+          fin = true;
+          break;
+        }
         const int eff = std::min(mb, total - off);
         merged = top;
         for (int j = 0; j < eff; ++j) {
@@ -427,8 +440,13 @@ void orc_rerank(const float* q, int nq, int dim, const float* base, long long n,
         }
         std::copy(merged.begin(), merged.begin() + k, top.begin());
         if ((float)chg / (float)k <= eps) ++stable; else stable = 0;
-        if (stable >= beta) break;
+        if (stable >= beta) {
+          fin = true;
+          break;
+        }
       }
+      if (stable_out) stable_out[i] = stable;
+      if (finished_out) finished_out[i] = fin ? 1 : 0;
       for (int j = 0; j < k; ++j) {
         const bool pad = top[j].second == 0xFFFFFFFFu;
         out_ids[(size_t)i * k + j] = pad ? -1 : (int)top[j].second;

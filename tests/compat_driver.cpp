@@ -108,7 +108,8 @@ int search(char** a) {
                         &ev.evt_gather})
     hip(hipEventCreate(e));
   std::vector<uint32_t> pruned(probes.size());
-  std::vector<int> tid((size_t)nq * rerank_m), tcnt(nq), counts(nq), atomic(nq), fid((size_t)nq * final_k);
+  std::vector<int> tid((size_t)nq * rerank_m), tcnt(nq), counts(nq), atomic(nq), fid((size_t)nq * final_k), stab(nq);
+  std::vector<uint8_t> fin(nq);
   std::vector<float> td((size_t)nq * rerank_m), cut((size_t)nq * (p1e > 0 ? p1e : 1)), thr(nq),
       fd((size_t)nq * final_k);
   std::vector<int> offs_last;
@@ -136,6 +137,8 @@ int search(char** a) {
     hip(hipMemcpyAsync(thr.data() + b0, d_thr, sizeof(float) * bs, hipMemcpyDeviceToHost, s));
     hip(hipMemcpyAsync(fid.data() + b0 * final_k, d_fid, sizeof(int) * bs * final_k, hipMemcpyDeviceToHost, s));
     hip(hipMemcpyAsync(fd.data() + b0 * final_k, d_fd, sizeof(float) * bs * final_k, hipMemcpyDeviceToHost, s));
+    hip(hipMemcpyAsync(stab.data() + b0, d_st, sizeof(int) * bs, hipMemcpyDeviceToHost, s));
+    hip(hipMemcpyAsync(fin.data() + b0, d_fin, sizeof(bool) * bs, hipMemcpyDeviceToHost, s));
     offs_last.assign(bs + 1, 0);
     hip(hipMemcpyAsync(offs_last.data(), d_offsets, sizeof(int) * (bs + 1), hipMemcpyDeviceToHost, s));
     hip(hipStreamSynchronize(s));
@@ -159,6 +162,8 @@ int search(char** a) {
   write_raw(out + "/thresholds.f32", thr.data(), thr.size());
   write_raw(out + "/final_ids.i32", fid.data(), fid.size());
   write_raw(out + "/final_dists.f32", fd.data(), fd.size());
+  write_raw(out + "/stable.i32", stab.data(), stab.size());
+  write_raw(out + "/finished.u8", fin.data(), fin.size());
   std::printf("search ok: %lld queries, %d batches, pool grew %d time(s) to %zu ints, num_clusters %d\n",
               (long long)nq, (int)((nq + batch - 1) / batch), grows, cap, idx.num_clusters);
   fgpu_compat_release_index(idx);

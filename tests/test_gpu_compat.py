@@ -40,11 +40,16 @@ def _run(args):
     return r.stdout
 
 
-def test_batch_logic_and_rerank_with_reference_defaults(tmp_path):
-    _say("compat search: load_ivf_index_to_gpu, run_gpu_batch_logic, run_gpu_rerank")
+@pytest.mark.parametrize("rerank_m", [10000, 100])
+def test_batch_logic_and_rerank_with_reference_defaults(tmp_path, rerank_m):
+    """The reference's defaults (rerank_m 10000), and rerank_m 100, where
+    the cut drops candidates: d_atomic keeps each query's count before the cut
+    (query_atomic_counters, gpu_global.cu:349, 493-526), d_stable_cnt and
+    d_finished the rerank's final state (gpu_global.cu:603-609, 653-662)."""
+    _say(f"compat search: load_ivf_index_to_gpu, run_gpu_batch_logic, run_gpu_rerank (rerank_m {rerank_m})")
     rng = np.random.default_rng(5151)
     dim, m, nlist, n, nq = 128, 32, 64, 60000, 300
-    top_m, p1, limit_k, coeff, rerank_m, k, mb, eps, beta, prune = 20, 12, 50, 1.0, 10000, 10, 128, 0.1, 2, 1.3
+    top_m, p1, limit_k, coeff, k, mb, eps, beta, prune = 20, 12, 50, 1.0, 10, 128, 0.1, 2, 1.3
     assign = rng.integers(0, nlist, n).astype(np.int32)
     codes = rng.integers(0, 256, (n, m)).astype(np.uint8)
     offs, ids, lc = oracle.build_lists(assign, nlist, codes)
@@ -73,17 +78,21 @@ def test_batch_logic_and_rerank_with_reference_defaults(tmp_path):
     got = rd("pruned.u32", np.uint32).reshape(nq, top_m)
     assert np.array_equal(got, want)
     assert np.array_equal(rd("counts.i32", np.int32), oracle.probe_counts(want, offs))
-    oid, od, ocnt, ocut, othr = oracle.search_two_phase(q, cent, cb, offs, ids, lc, want, p1, limit_k, coeff,
-                                                        rerank_m)
+    oid, od, ocnt, ocut, othr, opre = oracle.search_two_phase(q, cent, cb, offs, ids, lc, want, p1, limit_k, coeff,
+                                                              rerank_m, want_pre_cut=True)
     assert np.array_equal(rd("top_counts.i32", np.int32), ocnt)
-    assert np.array_equal(rd("atomic.i32", np.int32), ocnt)
+    assert np.array_equal(rd("atomic.i32", np.int32), opre)
+    if rerank_m < 1000:
+        assert (opre > ocnt).any()          # the cut dropped candidates: d_atomic is not the kept count
     assert np.array_equal(rd("top_ids.i32", np.int32).reshape(nq, rerank_m), oid)
     assert np.array_equal(_bits(rd("top_dists.f32", np.float32).reshape(nq, rerank_m)), _bits(od))
     assert np.array_equal(_bits(rd("cutoffs.f32", np.float32).reshape(nq, p1)), _bits(ocut))
     assert np.array_equal(_bits(rd("thresholds.f32", np.float32)), _bits(othr))
-    fid, fdist, _ = oracle.rerank(q, base, oid, ocnt, k, mb, eps, beta)
+    fid, fdist, _, ostab, ofin = oracle.rerank(q, base, oid, ocnt, k, mb, eps, beta, want_state=True)
     assert np.array_equal(rd("final_ids.i32", np.int32).reshape(nq, k), fid)
     assert np.array_equal(_bits(rd("final_dists.f32", np.float32).reshape(nq, k)), _bits(fdist))
+    assert np.array_equal(rd("stable.i32", np.int32), ostab)
+    assert np.array_equal(rd("finished.u8", np.uint8), ofin)
 
 
 def test_build_functions_match_the_oracle(tmp_path):

@@ -117,9 +117,19 @@ def test_search_pipeline_matches_library_path(tmp_path):
     offs, ids, codes, cent = fg.read_ivf_data(res / "ivf_data.bin", 32, 128)
     cb = np.fromfile(res / "global_pq_codebook.bin", np.float32).reshape(32, 256, 4)
     probes, _ = oracle.coarse(q, cent, 16, 100.0)
-    tid, _, tcnt, _, _ = oracle.search_two_phase(q, cent, cb, offs, ids, codes, probes, 4, 30, 1.0, 500)
+    tid, _, tcnt, _, _, pre = oracle.search_two_phase(q, cent, cb, offs, ids, codes, probes, 4, 30, 1.0, 500,
+                                                      want_pre_cut=True)
     want, _, _ = oracle.rerank(q, x, tid, tcnt, 10, 128, 0.1, 2)
     assert np.array_equal(got, want)
+    # the batch-logic table (search_pipeline.cu:286-306): per-batch averages over the five batches of the
+    # probed lists' sizes and of the candidates before the rerank_m cut, and the reduction rate
+    assert "GPU Batch Logic Fine-grained Breakdown" in out
+    amax = int(oracle.probe_counts(probes, offs).astype(np.int64).sum()) // 5
+    areal = int(pre.astype(np.int64).sum()) // 5
+    assert int(re.search(r"\[Allocated\] Max Potential Candidates: (\d+)", out).group(1)) == amax
+    assert int(re.search(r"\[Actual\]\s+Filtered Real Candidates: (\d+)", out).group(1)) == areal
+    rate = float(re.search(r"Pruning Reduction Rate: ([\d.]+) %", out).group(1))
+    assert abs(rate - 100.0 * (1.0 - areal / amax)) <= 0.051 and areal < amax
     # the reference's recall: whole gt row as the hit set, repeated ids once, hits / (nq * k)
     m = re.search(r"Recall@1: ([\d.]+)%, Recall@10: ([\d.]+)%", out)
     assert m

@@ -91,6 +91,15 @@ def test_two_phase_bit_exact(dim, m, p1, limit_k, coeff, rerank_m):
     if p1 > 0:
         assert np.array_equal(_bits(_host(gcut)), _bits(ocut))
     assert gcnt[6] == 0 and np.all(gid[6] == -1)
+    # the count before the rerank_m cut (the reference's d_atomic); the results stay the same
+    pid, pd, pcnt, _, _, pre = idx.two_phase_search(torch.from_numpy(q).cuda(),
+                                                    torch.from_numpy(probes.view(np.int32)).cuda(), p1, limit_k,
+                                                    coeff, rerank_m, want_pre_cut=True)
+    *_, opre = oracle.search_two_phase(q, cent, cb, offs, ids, lc, probes, p1, limit_k, coeff, rerank_m,
+                                       want_pre_cut=True)
+    assert np.array_equal(_host(pre), opre), np.nonzero(_host(pre) != opre)[0][:5]
+    assert np.array_equal(_host(pid), oid) and np.array_equal(_bits(_host(pd)), _bits(od))
+    assert np.array_equal(_host(pcnt), ocnt)
     idx.close()
 
 
@@ -204,13 +213,14 @@ def test_rerank_bit_exact(dim, k, mb, eps, beta, spec):
     cand[4, 20] = cand[4, 2]             # a duplicate candidate
     counts = rng.integers(0, rm + 1, nq).astype(np.int32)
     counts[:6] = [rm, rm, 0, rm, rm, 1]
-    gid, gd, gvis = fg.rerank(torch.from_numpy(q).cuda(), torch.from_numpy(base).cuda(),
-                              torch.from_numpy(cand).cuda(), torch.from_numpy(counts).cuda(), k, mb, eps, beta,
-                              spec=spec)
+    gid, gd, gvis, gst, gfin = fg.rerank(torch.from_numpy(q).cuda(), torch.from_numpy(base).cuda(),
+                                         torch.from_numpy(cand).cuda(), torch.from_numpy(counts).cuda(), k, mb, eps,
+                                         beta, spec=spec, want_state=True)
     torch.cuda.synchronize()
-    oid, od, ovis = oracle.rerank(q, base, cand, counts, k, mb, eps, beta)
+    oid, od, ovis, ost, ofin = oracle.rerank(q, base, cand, counts, k, mb, eps, beta, want_state=True)
     gid, gd, gvis = _host(gid), _host(gd), _host(gvis)
     assert np.array_equal(gvis, ovis), np.nonzero(gvis != ovis)[0][:5]
+    assert np.array_equal(_host(gst), ost) and np.array_equal(_host(gfin), ofin)
     bad = np.nonzero(~np.all(gid == oid, axis=1))[0]
     assert bad.size == 0, f"first mismatching queries {bad[:5]}"
     assert np.array_equal(_bits(gd), _bits(od))

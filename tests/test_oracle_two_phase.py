@@ -220,3 +220,82 @@ def test_two_phase_threshold_is_inclusive():
     assert _bits(thr[0]) == _bits(d0[2]) and len(set(d0[:4].tolist())) == 4
     assert cnt[0] == 6                           # 3 from phase 1 + 3 at or below the cutoff in phase 2
     assert sorted(oid[0, :6].tolist()) == sorted(i0[:3].tolist() + (i0[:3] + n0).tolist())
+
+
+def _pre_cut(q, cent, cb, offs, ids, lc, probes, p1_lists, limit_k, coeff):
+    """Candidates before the rerank_m cut, rebuilt from single lists: every
+    phase-1 list's min(n, limit_k) plus every phase-2 vector with d <= thr."""
+    nlist = cent.shape[0]
+    _, _, _, thr = _expected(q, cent, cb, offs, ids, lc, probes, p1_lists, limit_k, coeff, 1)
+    p1 = max(0, min(probes.shape[0], p1_lists))
+    n = 0
+    for j, l in enumerate(int(v) for v in probes):
+        if l >= nlist or offs[l + 1] == offs[l]:
+            continue
+        if j < p1:
+            n += min(int(offs[l + 1] - offs[l]), limit_k)
+        else:
+            d, _ = _list_sorted(q, cent, cb, offs, ids, lc, l)
+            n += int((d <= thr).sum())
+    return n
+
+
+@pytest.mark.parametrize("p1_lists,limit_k,coeff", [(3, 5, 1.0), (4, 1, 1.5), (8, 10, 1.0), (0, 10, 1.0)])
+def test_two_phase_pre_cut_counts(p1_lists, limit_k, coeff):
+    """The count the reference accumulates per query before the rerank_m cut
+    (query_atomic_counters, gpu_global.cu:349, 493-526): rebuilt from single
+    lists, the same for every rerank_m, and equal to the kept count once
+    rerank_m holds them all."""
+    rng = np.random.default_rng(p1_lists * 10 + limit_k + 7)
+    offs, ids, lc, cent, cb = _index(rng)
+    q = rng.standard_normal((8, 32)).astype(np.float32) * 0.7
+    probes, _ = oracle.coarse(q, cent, 8)
+    probes[1, 2] = PRUNED
+    probes[2, 0] = 5                           # an empty list
+    pres = []
+    for rerank_m in (1, 17, 4000):
+        *_, pre = oracle.search_two_phase(q, cent, cb, offs, ids, lc, probes, p1_lists, limit_k, coeff, rerank_m,
+                                          want_pre_cut=True)
+        pres.append(pre)
+        if rerank_m == 4000:
+            cnt = oracle.search_two_phase(q, cent, cb, offs, ids, lc, probes, p1_lists, limit_k, coeff, rerank_m)[2]
+            assert np.array_equal(cnt, pre)
+    assert np.array_equal(pres[0], pres[1]) and np.array_equal(pres[0], pres[2])
+    for i in range(q.shape[0]):
+        assert pres[0][i] == _pre_cut(q[i], cent, cb, offs, ids, lc, probes[i], p1_lists, limit_k, coeff)
+
+
+def test_rerank_state_hand_worked():
+    """stab[] and fin[] as run_gpu_rerank leaves them (gpu_global.cu:603-609,
+    615, 653-662), on the hand-worked sequence above."""
+    a = np.array([2, 3, 1, 4, 5, 6, 0, 7], np.float32)
+    base = np.stack([a, np.zeros_like(a)], 1).astype(np.float32)
+    q = np.zeros((1, 2), np.float32)
+    cand = np.arange(8, dtype=np.int32)[None]
+
+    def state(count, eps, beta):
+        *_, stab, fin = oracle.rerank(q, base, cand, np.array([count], np.int32), 2, mb=2, eps=eps, beta=beta,
+                                      want_state=True)
+        return int(stab[0]), int(fin[0])
+
+    assert state(8, 0.5, 2) == (2, 1)    # stops on stability after batch {4,5}
+    assert state(8, 0.5, 3) == (3, 1)    # one batch later
+    # eps 0.4: the last batch {6,7} changes one of two -> stable 0; offsets 0..6 all run, none past the
+    # candidates before rm = 8, so fin stays false
+    assert state(8, 0.4, 2) == (0, 0)
+    # five candidates: {0,1} chg 2, {2,3} chg 1, {4} chg 0 -> stable 1; offset 6 >= 5 -> finished
+    assert state(5, 0.4, 2) == (1, 1)
+    assert state(0, 0.4, 2) == (0, 1)    # offset 0 >= 0 candidates
+
+
+def test_rerank_state_never_stable():
+    rng = np.random.default_rng(14)
+    base = rng.standard_normal((400, 8)).astype(np.float32)
+    q = rng.standard_normal((5, 8)).astype(np.float32)
+    rm, mb = 64, 16
+    cand = np.stack([rng.permutation(400)[:rm] for _ in range(5)]).astype(np.int32)
+    counts = np.array([64, 63, 48, 1, 0], np.int32)
+    *_, stab, fin = oracle.rerank(q, base, cand, counts, 4, mb=mb, eps=-1.0, beta=2, want_state=True)
+    assert np.all(stab == 0)
+    # finished exactly when an offset below rm lies at or past the candidates
+    assert list(fin) == [int(-(-c // mb) * mb < rm) for c in counts] == [0, 0, 1, 1, 1]
