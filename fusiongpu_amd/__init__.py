@@ -71,6 +71,7 @@ _SIGS = {
     "fgpu_search_screen_stats": (_i32, [_vp, _i32, _i32, _vp, _sz, _vp, _c.POINTER(_c.c_longlong), _i32]),
     "fgpu_index_screen_ready": (_i32, [_vp]),
     "fgpu_index_set_option": (_i32, [_vp, _i32, _i32]),
+    "fgpu_coarse_search_stats": (_i32, [_vp, _vp, _i32, _i32, _f32, _vp, _vp, _vp, _vp, _sz, _vp]),
     "fgpu_two_phase_search_precut": (_i32, [_vp, _vp, _i32, _vp, _i32, _i32, _i32, _f32, _i32, _vp, _vp, _vp, _vp,
                                             _vp, _vp, _vp, _sz, _vp]),
     "fgpu_rerank_state": (_i32, [_vp, _i32, _i32, _vp, _i64, _vp, _vp, _i32, _i32, _i32, _f32, _i32, _vp, _vp, _vp,
@@ -480,6 +481,21 @@ class Index:
             _check(lib.fgpu_coarse_search(self._h, _dev_ptr(q), nq, nprobe, prune_ratio, _dev_ptr(ids), _dev_ptr(d),
                                           _dev_ptr(ws), _ws_check(ws), _stream()))
         return ids, d
+
+    def coarse_search_stats(self, queries, nprobe: int, prune_ratio: float = 100.0, stream=None):
+        """coarse_search plus counters (fgpu_coarse_search_stats): (probe_ids, dists, {"rescored": centroids
+        re-scored exactly, summed over the queries, "full_rows": queries that re-scored every centroid})."""
+        torch = _torch()
+        with _on(stream):
+            q = self._queries(queries)
+            nq = q.shape[0]
+            ws = _workspace(self.coarse_workspace_bytes(nq))
+            ids, d = _outs(None, nq, nprobe)
+            st = torch.zeros(2, dtype=torch.int64, device="cuda")
+            _check(lib.fgpu_coarse_search_stats(self._h, _dev_ptr(q), nq, nprobe, prune_ratio, _dev_ptr(ids),
+                                                _dev_ptr(d), _dev_ptr(st), _dev_ptr(ws), _ws_check(ws), _stream()))
+            v = st.cpu().tolist()
+        return ids, d, {"rescored": v[0], "full_rows": v[1]}
 
     def coarse_graph_build(self, degree: int = 8, stream=None):
         """Exact kNN graph of the centroids, self excluded (fgpu_coarse_graph_build): int32 [nlist][degree]."""

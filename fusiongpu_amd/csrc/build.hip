@@ -246,13 +246,19 @@ constexpr int kPPBlock = 1024;
 // cc >= 4 (1 + 1%) d2 the new distance exceeds d2 by about 2% even after the
 // roundings of the three fused chains (each within 1e-4 relative of its exact
 // value, D <= 256): the row cannot move, and its d2, weight and asg stay as
-// they are without reading the row.  d2 = 0 rows never move either.
+// they are without reading the row.  d2 = 0 rows never move either.  The
+// 1e-4 bound is relative and needs values far above the fp32 subnormal range
+// (where a rounding step is absolute), so rows with 0 < d2 < 2^-100 always
+// compute; from d2 >= 2^-100 on, cc >= 4 d2 is as far above it.
 constexpr float kPPSkip = 4.04f;
+constexpr float kPPSkipMin = 0x1p-100f;
 
 // Whether row i must compute its distance to the new centre (always, when
 // asg is null: the first passes).
 __device__ __forceinline__ bool pp_needs(const int32_t* asg, const float* cc, int64_t i, float old) {
-  return asg == nullptr || !(cc[asg[i]] >= kPPSkip * old);
+  if (asg == nullptr) return true;
+  if (old == 0.0f) return false;
+  return !(old >= kPPSkipMin && cc[asg[i]] >= kPPSkip * old);
 }
 
 // d2[i] = min(d2[i], ||x_i - c||^2) (init: d2 = dist); w[i] = round(d2 * 2^S);

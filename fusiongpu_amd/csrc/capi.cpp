@@ -102,6 +102,11 @@ fgpu_status finish_index(fgpu_index* ix, hipStream_t s) {
     return set_error(FGPU_ERR_NOMEM, "index: device allocation failed");
   }
   FGPU_HIP(hipMemsetAsync(ix->d_faults, 0, 256, s));
+  // Per-device lookups that searches would otherwise make on their first
+  // call (which may be under graph capture): the no-allocation scratch
+  // address and the flow kernel's resident grid, both cached per device.
+  FGPU_TRY(noalloc_prepare());
+  (void)flow_grid(ix->dim, ix->m, 1, 1);
   FGPU_TRY(launch_row_norms(ix->d_centroids, ix->nlist, ix->dim, ix->d_cnorm, s));
   FGPU_TRY(launch_max_reduce(ix->d_cnorm, ix->nlist, ix->d_cnorm_max, s));
   FGPU_TRY(launch_list_radius(ix->d_codebook, ix->m, ix->dim / ix->m, ix->d_codes, ix->d_offsets, ix->nlist, ix->d_rmax,
@@ -374,7 +379,7 @@ namespace {
 // reset kernel of its own).
 fgpu_status coarse_search(const fgpu_index* ix, const float* dq, int nq, int nprobe, float prune_ratio,
                           uint32_t* d_ids, float* d_dists, void* ws, size_t ws_bytes, void* stream, int* side,
-                          int side_val) {
+                          int side_val, unsigned long long* stats = nullptr) {
   // An empty batch may come with empty (null) arrays.
   FGPU_CHECK(ix && ws && (nq == 0 || (dq && d_ids && d_dists)), FGPU_ERR_ARG, "coarse_search: null argument");
   FGPU_CHECK(((uintptr_t)ws & 15) == 0, FGPU_ERR_ARG, "coarse_search: workspace must be 16-byte aligned");
@@ -392,12 +397,12 @@ fgpu_status coarse_search(const fgpu_index* ix, const float* dq, int nq, int npr
   // its margin.
   for (int64_t b0 = 0; b0 < nq; b0 += rows) {
     const int64_t nb = std::min<int64_t>(rows, nq - b0);
-    FGPU_TRY(launch_gemm_est_sel(dq + b0 * ix->dim, nb, ix->d_centroids, ix->nlist, ix->dim, ix->d_cnorm, est, ld,
-                                 s));
+    FGPU_TRY(launch_gemm_est_sel(dq + b0 * ix->dim, nb, ix->d_centroids, ix->nlist, ix->dim, ix->d_cnorm,
+                                 ix->d_cnorm_max, est, ld, s));
     FGPU_TRY(launch_select_exact(est, ld, nb, ix->nlist, dq + b0 * ix->dim, ix->d_centroids, ix->dim,
                                  ix->d_cnorm_max, nprobe, 1, prune_ratio,
                                  reinterpret_cast<int32_t*>(d_ids) + b0 * nprobe, d_dists + b0 * nprobe, s,
-                                 b0 == 0 ? side : nullptr, side_val));
+                                 b0 == 0 ? side : nullptr, side_val, stats));
   }
   return FGPU_OK;
 }
@@ -408,6 +413,13 @@ extern "C" {
 fgpu_status fgpu_coarse_search(const fgpu_index* ix, const float* dq, int nq, int nprobe, float prune_ratio,
                                uint32_t* d_ids, float* d_dists, void* ws, size_t ws_bytes, void* stream) {
   return coarse_search(ix, dq, nq, nprobe, prune_ratio, d_ids, d_dists, ws, ws_bytes, stream, nullptr, 0);
+}
+
+fgpu_status fgpu_coarse_search_stats(const fgpu_index* ix, const float* dq, int nq, int nprobe, float prune_ratio,
+                                     uint32_t* d_ids, float* d_dists, unsigned long long* d_stats, void* ws,
+                                     size_t ws_bytes, void* stream) {
+  FGPU_CHECK(d_stats, FGPU_ERR_ARG, "coarse_search_stats: null stats");
+  return coarse_search(ix, dq, nq, nprobe, prune_ratio, d_ids, d_dists, ws, ws_bytes, stream, nullptr, 0, d_stats);
 }
 
 fgpu_status fgpu_prune_probes(uint32_t* d_probe_ids, const float* d_probe_dists, int nq, int nprobe, float prune_ratio,
@@ -836,7 +848,7 @@ fgpu_status fgpu_l2_topk(const float* dx, int64_t n, const float* dc, int nc, in
   FGPU_TRY(launch_max_reduce(cn, nc, cmax, s));
   for (int64_t b0 = 0; b0 < n; b0 += rows) {
     const int64_t nb = std::min<int64_t>(rows, n - b0);
-    FGPU_TRY(launch_gemm_est_sel(dx + b0 * dim, nb, dc, nc, dim, cn, est, ld, s));
+    FGPU_TRY(launch_gemm_est_sel(dx + b0 * dim, nb, dc, nc, dim, cn, cmax, est, ld, s));
     FGPU_TRY(launch_select_exact(est, ld, nb, nc, dx + b0 * dim, dc, dim, cmax, p, 0, 0.0f, d_ids + b0 * p,
                                  d_dists + b0 * p, s));
   }

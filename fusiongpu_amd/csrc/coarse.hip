@@ -92,15 +92,41 @@ __device__ __forceinline__ float half_next_up(float f) {
   return half_bits_float(u);
 }
 
+// The fp16 estimates of a row are scaled by 2^-s so that they stay inside the
+// fp16 range: |cn_j - 2 <x, c_j>| <= ||x||^2 + 2 max ||c||^2 = t/2 with
+// t = 2 (xn + cn_max) < 2^e, so 2^-s with s = max(0, e - 15) keeps every
+// shifted estimate (plus its small error) below 2^15.  A power-of-two scale is
+// exact in fp32 (a product that falls below the fp32 normal range rounds by
+// less than 2^-126, far inside the select's margin at any s > 0), so the
+// scaled fp16 values stay lower bounds of the scaled estimates; the select
+// scales its margin the same way.  xn is the row's fp32 sum of squares as
+// the GEMM forms it; every workgroup of a row forms it alike, so they agree on
+// s, and the select reads the s the row's first column tile stores.
+__device__ __forceinline__ int est_shift(float xn, float cn_max) {
+  const float t = 2.0f * (xn + cn_max);
+  if (!(t < 0x1p120f)) return 110;  // inf or NaN inputs: any scale
+  int e = 0;
+  (void)frexpf(t, &e);  // t = m 2^e, m in [0.5, 1) (e = 0 for t = 0)
+  return e > 15 ? e - 15 : 0;
+}
+__device__ __forceinline__ float pow2_neg(int s) { return __int_as_float((127 - s) << 23); }  // 2^-s, 0 <= s <= 126
+
+// The row shifts (one byte a row) of an fp16 estimate block of nrows rows:
+// stored after the estimates, inside the block's float-sized allocation.
+__host__ __device__ __forceinline__ uint8_t* est_row_shift(void* est, int64_t nrows, int64_t ld) {
+  return reinterpret_cast<uint8_t*>(static_cast<uint16_t*>(est) + nrows * ld);
+}
+
 // Where an estimate tile goes (output mode OM).  kOutFull: fp32
 // xn[i] + cn[j] - 2 <x_i, c_j>.  kOutShift: fp32 cn[j] - 2 <x_i, c_j>, the row
 // shifted by its norm (xn unused).  kOutHalf: the fp16 lower bound (bit
-// pattern) of the shifted value.
+// pattern) of the shifted value times the row's 2^-s (sc).
 constexpr int kOutFull = 0, kOutShift = 1, kOutHalf = 2;
 template <int OM>
-__device__ __forceinline__ void put_est(void* est, int64_t off, const float* xn, int64_t i, float cj, float acc) {
+__device__ __forceinline__ void put_est(void* est, int64_t off, const float* xn, int64_t i, float cj, float acc,
+                                        float sc = 1.0f) {
   if constexpr (OM == kOutHalf)
-    static_cast<uint16_t*>(est)[off] = half_at_or_below(cj - 2.0f * acc);
+    static_cast<uint16_t*>(est)[off] = half_at_or_below((cj - 2.0f * acc) * sc);
   else if constexpr (OM == kOutShift)
     static_cast<float*>(est)[off] = cj - 2.0f * acc;
   else
@@ -116,9 +142,14 @@ __global__ __launch_bounds__(256) void gemm_est_kernel(const float* __restrict__
                                                        const float* __restrict__ c, int ncols, int dim,
                                                        const float* __restrict__ xn,
                                                        const float* __restrict__ cn,
-                                                       void* __restrict__ est, int64_t ld) {
+                                                       void* __restrict__ est, int64_t ld,
+                                                       const float* __restrict__ cn_max,
+                                                       uint8_t* __restrict__ rsh) {
   __shared__ float As[kTK][kLdsStride];
   __shared__ float Bs[kTK][kLdsStride];
+  __shared__ float sq_s[4][64];  // kOutHalf: each wave's part of each tile row's sum of squares
+  __shared__ float sc_s[64];     // kOutHalf: each tile row's 2^-s
+  float sq = 0.0f;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int64_t row0 = (int64_t)blockIdx.x * kTM;
   const int col0 = blockIdx.y * kTN;
@@ -138,6 +169,7 @@ __global__ __launch_bounds__(256) void gemm_est_kernel(const float* __restrict__
         if (ar < nrows) va = *reinterpret_cast<const float4*>(x + ar * dim + k0 + kk);
         if (bc < ncols) vb = *reinterpret_cast<const float4*>(c + (int64_t)bc * dim + k0 + kk);
       }
+      if constexpr (OM == kOutHalf) sq += va.x * va.x + va.y * va.y + va.z * va.z + va.w * va.w;
       As[kk + 0][lane] = va.x; As[kk + 1][lane] = va.y; As[kk + 2][lane] = va.z; As[kk + 3][lane] = va.w;
       Bs[kk + 0][lane] = vb.x; Bs[kk + 1][lane] = vb.y; Bs[kk + 2][lane] = vb.z; Bs[kk + 3][lane] = vb.w;
     }
@@ -150,6 +182,16 @@ __global__ __launch_bounds__(256) void gemm_est_kernel(const float* __restrict__
     }
     __syncthreads();
   }
+  if constexpr (OM == kOutHalf) {
+    sq_s[wave][lane] = sq;
+    __syncthreads();
+    if (wave == 0) {
+      const int sh = est_shift(sq_s[0][lane] + sq_s[1][lane] + sq_s[2][lane] + sq_s[3][lane], *cn_max);
+      sc_s[lane] = pow2_neg(sh);
+      if (blockIdx.y == 0 && ar < nrows) rsh[ar] = (uint8_t)sh;
+    }
+    __syncthreads();
+  }
   // D layout of v_mfma_f32_32x32x2f32: lane l, accumulator r holds
   // row 8*(r/4) + 4*(l/32) + r%4, column l%32.
   const int j = col0 + wc * 32 + (lane & 31);
@@ -157,8 +199,9 @@ __global__ __launch_bounds__(256) void gemm_est_kernel(const float* __restrict__
   const float cj = cn[j];
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
-    const int64_t i = row0 + wr * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-    if (i < nrows) put_est<OM>(est, i * ld + j, xn, i, cj, acc[r]);
+    const int rr = wr * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+    const int64_t i = row0 + rr;
+    if (i < nrows) put_est<OM>(est, i * ld + j, xn, i, cj, acc[r], OM == kOutHalf ? sc_s[rr] : 1.0f);
   }
 }
 
@@ -202,9 +245,12 @@ __global__ __launch_bounds__(256) void gemm_est_split_kernel(const float* __rest
                                                              const float* __restrict__ c, int ncols, int dim,
                                                              const float* __restrict__ xn,
                                                              const float* __restrict__ cn,
-                                                             void* __restrict__ est, int64_t ld) {
+                                                             void* __restrict__ est, int64_t ld,
+                                                             const float* __restrict__ cn_max,
+                                                             uint8_t* __restrict__ rsh) {
   __shared__ __align__(16) __bf16 As[2][kTM * kB3Row];
   __shared__ __align__(16) __bf16 Bs[2][kTN * kB3Row];
+  __shared__ float sc_s[kTM];  // kOutHalf: each tile row's 2^-s
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int64_t row0 = (int64_t)blockIdx.x * kTM;
   const int col0 = blockIdx.y * kTN;
@@ -217,6 +263,15 @@ __global__ __launch_bounds__(256) void gemm_est_split_kernel(const float* __rest
   const float* bp1 = c + (int64_t)min(col0 + sr + 32, ncols - 1) * dim + 4 * sf;
   float4 ra0 = *reinterpret_cast<const float4*>(ap0), ra1 = *reinterpret_cast<const float4*>(ap1);
   float4 rb0 = *reinterpret_cast<const float4*>(bp0), rb1 = *reinterpret_cast<const float4*>(bp1);
+  // kOutHalf: this thread's part of the sums of squares of rows sr and sr + 32
+  float sq0 = 0.0f, sq1 = 0.0f;
+  auto add_sq = [&]() {
+    if constexpr (OM == kOutHalf) {
+      sq0 += ra0.x * ra0.x + ra0.y * ra0.y + ra0.z * ra0.z + ra0.w * ra0.w;
+      sq1 += ra1.x * ra1.x + ra1.y * ra1.y + ra1.z * ra1.z + ra1.w * ra1.w;
+    }
+  };
+  add_sq();
   f32x16 acc;
 #pragma unroll
   for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
@@ -234,6 +289,7 @@ __global__ __launch_bounds__(256) void gemm_est_split_kernel(const float* __rest
       ra1 = *reinterpret_cast<const float4*>(ap1 + ko);
       rb0 = *reinterpret_cast<const float4*>(bp0 + ko);
       rb1 = *reinterpret_cast<const float4*>(bp1 + ko);
+      add_sq();
     }
     const __bf16* Ar = &As[buf][(wr * 32 + li) * kB3Row + 8 * lh];
     const __bf16* Br = &Bs[buf][(wc * 32 + li) * kB3Row + 8 * lh];
@@ -255,6 +311,24 @@ __global__ __launch_bounds__(256) void gemm_est_split_kernel(const float* __rest
       split_put(&Bs[nb][(sr + 32) * kB3Row], sf, rb1);
     }
     __syncthreads();
+  }
+  if constexpr (OM == kOutHalf) {
+    // the eight threads of a row are consecutive lanes
+#pragma unroll
+    for (int m = 1; m < 8; m <<= 1) {
+      sq0 += __shfl_xor(sq0, m, kWave);
+      sq1 += __shfl_xor(sq1, m, kWave);
+    }
+    if (sf == 0) {
+      const float cm = *cn_max;
+      const int s0 = est_shift(sq0, cm), s1 = est_shift(sq1, cm);
+      sc_s[sr] = pow2_neg(s0);
+      sc_s[sr + 32] = pow2_neg(s1);
+      if (blockIdx.y == 0) {
+        if (row0 + sr < nrows) rsh[row0 + sr] = (uint8_t)s0;
+        if (row0 + sr + 32 < nrows) rsh[row0 + sr + 32] = (uint8_t)s1;
+      }
+    }
   }
   // acc layout as in gemm_est_kernel; the operand buffers are free after the
   // last barrier.
@@ -283,12 +357,13 @@ __global__ __launch_bounds__(256) void gemm_est_split_kernel(const float* __rest
     if (i >= nrows) break;
     const float4 a = *reinterpret_cast<const float4*>(&Cs[rr * kCStride + c4]);
     const int64_t off = i * ld + j;
+    const float sc = OM == kOutHalf ? sc_s[rr] : 1.0f;
     if (vec) {
       if constexpr (OM == kOutHalf) {
-        const uint32_t lo = (uint32_t)half_at_or_below(cj.x - 2.0f * a.x) |
-                            ((uint32_t)half_at_or_below(cj.y - 2.0f * a.y) << 16);
-        const uint32_t hi = (uint32_t)half_at_or_below(cj.z - 2.0f * a.z) |
-                            ((uint32_t)half_at_or_below(cj.w - 2.0f * a.w) << 16);
+        const uint32_t lo = (uint32_t)half_at_or_below((cj.x - 2.0f * a.x) * sc) |
+                            ((uint32_t)half_at_or_below((cj.y - 2.0f * a.y) * sc) << 16);
+        const uint32_t hi = (uint32_t)half_at_or_below((cj.z - 2.0f * a.z) * sc) |
+                            ((uint32_t)half_at_or_below((cj.w - 2.0f * a.w) * sc) << 16);
         *reinterpret_cast<uint2*>(static_cast<uint16_t*>(est) + off) = make_uint2(lo, hi);
       } else if constexpr (OM == kOutShift) {
         *reinterpret_cast<float4*>(static_cast<float*>(est) + off) =
@@ -300,10 +375,10 @@ __global__ __launch_bounds__(256) void gemm_est_split_kernel(const float* __rest
                         (xi + cj.w) - 2.0f * a.w);
       }
     } else {
-      put_est<OM>(est, off, xn, i, cj.x, a.x);
-      if (j + 1 < ncols) put_est<OM>(est, off + 1, xn, i, cj.y, a.y);
-      if (j + 2 < ncols) put_est<OM>(est, off + 2, xn, i, cj.z, a.z);
-      if (j + 3 < ncols) put_est<OM>(est, off + 3, xn, i, cj.w, a.w);
+      put_est<OM>(est, off, xn, i, cj.x, a.x, sc);
+      if (j + 1 < ncols) put_est<OM>(est, off + 1, xn, i, cj.y, a.y, sc);
+      if (j + 2 < ncols) put_est<OM>(est, off + 2, xn, i, cj.z, a.z, sc);
+      if (j + 3 < ncols) put_est<OM>(est, off + 3, xn, i, cj.w, a.w, sc);
     }
   }
 }
@@ -512,16 +587,18 @@ __device__ __forceinline__ void select_row(const float (&val)[VPL], int64_t row,
                                            uint32_t* hist, int* cand, const float* __restrict__ c, int dim,
                                            float xnr, const float* __restrict__ cn_max,
                                            float kappa, int p, int prune, float prune_ratio,
-                                           int32_t* __restrict__ out_ids, float* __restrict__ out_d) {
+                                           int32_t* __restrict__ out_ids, float* __restrict__ out_d, int shift,
+                                           unsigned long long* __restrict__ stats) {
   const int lane = threadIdx.x & 63;
   // With fp16 lower bounds and T' their p-th smallest, the p smallest
   // estimates lie below the next fp16 value above T' (each is below the next
   // fp16 value above its own bound), so T = that value bounds the p-th
   // smallest estimate from above, and every column whose estimate is
   // <= (p-th smallest estimate) + 2E has val <= T + 2E.
+  // The values are the row's estimates times 2^-shift, so is the margin.
   const float Tv = wave_kth_estimate<VPL, V>(val, ncols, p, hist);
   const float T = HALF ? half_next_up(Tv) : Tv;
-  const double E = est_margin(kappa, xnr, *cn_max);
+  const double E = std::ldexp(est_margin(kappa, xnr, *cn_max), -shift);
   const float thr = float_at_or_below((double)T + 2.0 * E);
 
   // Compaction of the candidate columns.
@@ -538,6 +615,10 @@ __device__ __forceinline__ void select_row(const float (&val)[VPL], int64_t row,
   wave_lds_sync();
   const bool all_cols = C > kCandCap;  // pathological ties: re-score everything
   const int ncand = all_cols ? ncols : C;
+  if (stats && lane == 0) {  // instrumentation: columns re-scored, rows re-scoring every column
+    atomicAdd(&stats[0], (unsigned long long)ncand);
+    if (all_cols) atomicAdd(&stats[1], 1ull);
+  }
 
   // Running top-p of packed (distance, id) keys: squared L2 distances are
   // >= 0, so key order is the tie rule.
@@ -580,7 +661,8 @@ __global__ __launch_bounds__(256) void select_exact_kernel(
     const E* __restrict__ est, int64_t ld, int64_t nrows, int ncols,
     const float* __restrict__ x, const float* __restrict__ c, int dim,
     const float* __restrict__ cn_max, float kappa, int p, int prune,
-    float prune_ratio, int32_t* __restrict__ out_ids, float* __restrict__ out_d, int* side, int side_val) {
+    float prune_ratio, int32_t* __restrict__ out_ids, float* __restrict__ out_d, int* side, int side_val,
+    const uint8_t* __restrict__ rsh, unsigned long long* __restrict__ stats) {
   __shared__ uint32_t hist_s[4][256];
   __shared__ int cand_s[4][kCandCap];
   __shared__ __align__(16) float x_s[4][256];
@@ -630,7 +712,7 @@ __global__ __launch_bounds__(256) void select_exact_kernel(
     }
   }
   select_row<VPL, V, HALF>(val, row, ncols, xs, hist_s[wave], cand_s[wave], c, dim, xnr, cn_max, kappa, p, prune,
-                           prune_ratio, out_ids, out_d);
+                           prune_ratio, out_ids, out_d, HALF ? (int)rsh[row] : 0, stats);
 }
 
 // p == 1 over many columns (the k-means assignment at k > 1024): the row is
@@ -654,7 +736,8 @@ __global__ __launch_bounds__(256) void select_min_kernel(
     const E* __restrict__ est, int64_t ld, int64_t nrows, int ncols,
     const float* __restrict__ x, const float* __restrict__ c, int dim,
     const float* __restrict__ cn_max, float kappa, int prune, float prune_ratio,
-    int32_t* __restrict__ out_ids, float* __restrict__ out_d, int* side, int side_val) {
+    int32_t* __restrict__ out_ids, float* __restrict__ out_d, int* side, int side_val,
+    const uint8_t* __restrict__ rsh, unsigned long long* __restrict__ stats) {
   __shared__ int cand_s[4][kCandCap];
   __shared__ __align__(16) float x_s[4][256];
   constexpr bool HALF = sizeof(E) == 2;
@@ -699,7 +782,9 @@ __global__ __launch_bounds__(256) void select_min_kernel(
   }
   const float Tv = wave_min_f(mn);
   const float T = HALF ? half_next_up(Tv) : Tv;
-  const float thr = float_at_or_below((double)T + 2.0 * est_margin(kappa, xnr, *cn_max));
+  // the values are the row's estimates times 2^-shift, so is the margin
+  const int shift = HALF ? (int)rsh[row] : 0;
+  const float thr = float_at_or_below((double)T + 2.0 * std::ldexp(est_margin(kappa, xnr, *cn_max), -shift));
   int C = 0;
   for (int base = 0; base < ncols; base += PIECE) {
     float v[V];
@@ -717,6 +802,10 @@ __global__ __launch_bounds__(256) void select_min_kernel(
   wave_lds_sync();
   const bool all_cols = C > kCandCap;  // pathological ties: re-score everything
   const int ncand = all_cols ? ncols : C;
+  if (stats && lane == 0) {  // instrumentation: columns re-scored, rows re-scoring every column
+    atomicAdd(&stats[0], (unsigned long long)ncand);
+    if (all_cols) atomicAdd(&stats[1], 1ull);
+  }
   uint64_t best = kPadKey;
   for (int b = 0; b < ncand; b += kWave) {
     if (b + lane < ncand) {
@@ -863,16 +952,16 @@ template <int VPL>
 fgpu_status launch_select_t(const void* est, int64_t ld, int64_t nrows, int ncols, const float* x,
                             const float* c, int dim, const float* cn_max, float kappa,
                             int p, int prune, float prune_ratio, int32_t* ids, float* d, int* side, int side_val,
-                            hipStream_t s) {
+                            hipStream_t s, unsigned long long* stats) {
   const int64_t blocks = (nrows + 3) / 4;
   if constexpr (kEstHalf)
     hipLaunchKernelGGL((select_exact_kernel<VPL, uint16_t>), dim3((unsigned)blocks), dim3(256), 0, s,
                        static_cast<const uint16_t*>(est), ld, nrows, ncols, x, c, dim, cn_max, kappa, p, prune,
-                       prune_ratio, ids, d, side, side_val);
+                       prune_ratio, ids, d, side, side_val, est_row_shift(const_cast<void*>(est), nrows, ld), stats);
   else
     hipLaunchKernelGGL((select_exact_kernel<VPL, float>), dim3((unsigned)blocks), dim3(256), 0, s,
                        static_cast<const float*>(est), ld, nrows, ncols, x, c, dim, cn_max, kappa, p, prune,
-                       prune_ratio, ids, d, side, side_val);
+                       prune_ratio, ids, d, side, side_val, nullptr, stats);
   FGPU_HIP(hipGetLastError());
   return FGPU_OK;
 }
@@ -894,15 +983,19 @@ fgpu_status launch_max_reduce(const float* v, int64_t n, float* out, hipStream_t
 
 template <int OM>
 fgpu_status launch_gemm_t(const float* x, int64_t nrows, const float* c, int ncols, int dim, const float* xn,
-                          const float* cn, void* est, int64_t ld, hipStream_t s) {
+                          const float* cn, void* est, int64_t ld, hipStream_t s, const float* cn_max = nullptr) {
   FGPU_CHECK(dim % 4 == 0, FGPU_ERR_UNSUPPORTED, "gemm_est: dim must be a multiple of 4");
+  FGPU_CHECK(OM != kOutHalf || cn_max, FGPU_ERR_ARG, "gemm_est: the fp16 form needs max ||c||^2");
   if (nrows <= 0 || ncols <= 0) return FGPU_OK;
   dim3 grid((unsigned)((nrows + kTM - 1) / kTM), (unsigned)((ncols + kTN - 1) / kTN));
   FGPU_CHECK(grid.y <= 65535u, FGPU_ERR_UNSUPPORTED, "gemm_est: too many columns");
+  uint8_t* rsh = OM == kOutHalf ? est_row_shift(est, nrows, ld) : nullptr;
   if (dim % 32 == 0)
-    hipLaunchKernelGGL(gemm_est_split_kernel<OM>, grid, dim3(256), 0, s, x, nrows, c, ncols, dim, xn, cn, est, ld);
+    hipLaunchKernelGGL(gemm_est_split_kernel<OM>, grid, dim3(256), 0, s, x, nrows, c, ncols, dim, xn, cn, est, ld,
+                       cn_max, rsh);
   else
-    hipLaunchKernelGGL(gemm_est_kernel<OM>, grid, dim3(256), 0, s, x, nrows, c, ncols, dim, xn, cn, est, ld);
+    hipLaunchKernelGGL(gemm_est_kernel<OM>, grid, dim3(256), 0, s, x, nrows, c, ncols, dim, xn, cn, est, ld, cn_max,
+                       rsh);
   FGPU_HIP(hipGetLastError());
   return FGPU_OK;
 }
@@ -913,10 +1006,10 @@ fgpu_status launch_gemm_est(const float* x, int64_t nrows, const float* c, int n
 }
 
 fgpu_status launch_gemm_est_sel(const float* x, int64_t nrows, const float* c, int ncols, int dim, const float* cn,
-                                void* est, int64_t ld, hipStream_t s) {
+                                const float* cn_max, void* est, int64_t ld, hipStream_t s) {
   FGPU_CHECK(ld % 8 == 0, FGPU_ERR_ARG, "gemm_est_sel: row stride must be a multiple of 8");
   if constexpr (kEstHalf)
-    return launch_gemm_t<kOutHalf>(x, nrows, c, ncols, dim, nullptr, cn, est, ld, s);
+    return launch_gemm_t<kOutHalf>(x, nrows, c, ncols, dim, nullptr, cn, est, ld, s, cn_max);
   else
     return launch_gemm_t<kOutShift>(x, nrows, c, ncols, dim, nullptr, cn, est, ld, s);
 }
@@ -939,7 +1032,7 @@ static float coarse_kappa(int dim) {
 fgpu_status launch_select_exact(const void* est, int64_t ld, int64_t nrows, int ncols, const float* x,
                                 const float* c, int dim, const float* cn_max, int p,
                                 int prune, float prune_ratio, int32_t* ids, float* d, hipStream_t s, int* side,
-                                int side_val) {
+                                int side_val, unsigned long long* stats) {
   FGPU_CHECK(ld % 8 == 0, FGPU_ERR_ARG, "select: row stride must be a multiple of 8");
   FGPU_CHECK(p >= 1 && p <= kSelectMax && p <= ncols, FGPU_ERR_UNSUPPORTED, "select: need 1 <= p <= min(256, ncols)");
   FGPU_CHECK(dim <= 256, FGPU_ERR_UNSUPPORTED, "select: dim must be <= 256");
@@ -949,17 +1042,19 @@ fgpu_status launch_select_exact(const void* est, int64_t ld, int64_t nrows, int 
     const dim3 grid((unsigned)((nrows + 3) / 4));
     if constexpr (kEstHalf)
       hipLaunchKernelGGL(select_min_kernel<uint16_t>, grid, dim3(256), 0, s, static_cast<const uint16_t*>(est), ld,
-                         nrows, ncols, x, c, dim, cn_max, kappa, prune, prune_ratio, ids, d, side, side_val);
+                         nrows, ncols, x, c, dim, cn_max, kappa, prune, prune_ratio, ids, d, side, side_val,
+                         est_row_shift(const_cast<void*>(est), nrows, ld), stats);
     else
       hipLaunchKernelGGL(select_min_kernel<float>, grid, dim3(256), 0, s, static_cast<const float*>(est), ld, nrows,
-                         ncols, x, c, dim, cn_max, kappa, prune, prune_ratio, ids, d, side, side_val);
+                         ncols, x, c, dim, cn_max, kappa, prune, prune_ratio, ids, d, side, side_val, nullptr,
+                         stats);
     FGPU_HIP(hipGetLastError());
     return FGPU_OK;
   }
 #define FGPU_SEL(V) \
   if (ncols <= (V) * kWave) \
     return launch_select_t<V>(est, ld, nrows, ncols, x, c, dim, cn_max, kappa, p, prune, prune_ratio, ids, d, side, \
-                              side_val, s)
+                              side_val, s, stats)
   FGPU_SEL(1);
   FGPU_SEL(2);
   FGPU_SEL(4);

@@ -21,20 +21,24 @@ fgpu_status launch_gemm_est(const float* x, int64_t nrows, const float* c, int n
                             const float* xn, const float* cn, float* est, int64_t ld, hipStream_t s);
 // The same contraction for launch_select_exact: cn[j] - 2 <x_i, c_j>, each
 // row shifted by its norm, in the select's element form (fp32, or the fp16
-// lower bound); ld % 8 == 0, at least est_sel_ld(ncols).  
+// lower bound of the row scaled by a power of two that keeps it inside the
+// fp16 range, the row's exponent stored after the block); ld % 8 == 0, at
+// least est_sel_ld(ncols); est holds nrows * ld floats; cn_max = max cn.
 fgpu_status launch_gemm_est_sel(const float* x, int64_t nrows, const float* c, int ncols, int dim, const float* cn,
-                                void* est, int64_t ld, hipStream_t s);
+                                const float* cn_max, void* est, int64_t ld, hipStream_t s);
 int64_t est_sel_ld(int ncols);
 // Per row: the p nearest columns by exact device-form L2, chosen from the
 // estimates of launch_gemm_est_sel with a rigorous error margin.  ids
 // are int32 bit patterns; with prune != 0 a column farther than
 // best*prune_ratio gets 0xFFFFFFFF.  With side != nullptr the launch also
 // stores side_val at *side (one word, for the next kernel on the stream).
+// stats (nullptr = off): adds the columns re-scored exactly to stats[0] and
+// the rows that re-scored every column to stats[1].
 fgpu_status launch_select_exact(const void* est, int64_t ld, int64_t nrows, int ncols,
                                 const float* x, const float* c, int dim,
                                 const float* cn_max, int p, int prune, float prune_ratio,
                                 int32_t* out_ids, float* out_d, hipStream_t s, int* side = nullptr,
-                                int side_val = 0);
+                                int side_val = 0, unsigned long long* stats = nullptr);
 // Exact kNN over one chunk of <= 4096 base rows c (ids id_base + col), merged
 // into the running top-k in ids/d (k <= 128) when accum != 0.
 fgpu_status launch_knn_chunk(const float* est, int64_t ld, int64_t nrows, int ncols, const float* x, const float* c,
@@ -111,6 +115,9 @@ fgpu_status launch_adc_plain_list(int dim, int m, const AdcArgs& a, hipStream_t 
 // (the start value of its query counter), or 0 if that call takes another
 // kernel.
 int flow_grid(int dim, int m, int nq, int nprobe);
+// noalloc.hip: resolve this device's scratch array address (index creation
+// calls it, so that fgpu_search_noalloc needs no first-call lookup).
+fgpu_status noalloc_prepare();
 
 // ---- capi.cpp -----------------------------------------------------------------------
 // Workspace of fgpu_search on the LUT kernels alone (probe arrays + the coarse

@@ -6,9 +6,10 @@
 //
 // Each GPU holds its own copy of the array from module load until the process
 // ends.  Host code never passes the array's name to a kernel or a copy: the
-// host-side symbol is only a stand-in.  The first call on a device (with that
-// device current) asks the runtime for the array's device address once and
-// keeps it per device; every later use goes through that address.
+// host-side symbol is only a stand-in.  Index creation (with the device
+// current) asks the runtime for the array's device address once per device
+// and keeps it; every use goes through that address, so a call made under
+// graph capture does no lookup of its own.
 //
 // Every call on one GPU shares that GPU's array: calls that overlap on one
 // GPU (different streams, or host threads) race on it.  Nothing in the array
@@ -46,6 +47,12 @@ fgpu_status scratch_address(void** out) {
 }
 
 }  // namespace
+
+fgpu_status noalloc_prepare() {
+  void* p = nullptr;
+  return scratch_address(&p);
+}
+
 }  // namespace fgpu
 
 using namespace fgpu;

@@ -127,6 +127,14 @@ size_t fgpu_coarse_workspace_bytes(int nq, int nlist);
 fgpu_status fgpu_coarse_search(const fgpu_index* idx, const float* d_queries, int nq, int nprobe,
                                float prune_ratio, uint32_t* d_probe_ids, float* d_probe_dists,
                                void* d_workspace, size_t workspace_bytes, void* stream);
+/* fgpu_coarse_search plus instrumentation (no reference counterpart): adds to
+ * d_stats[0..1] (device, caller-zeroed, uint64) the centroids re-scored
+ * exactly over all queries and the queries whose margin admitted more than
+ * 512 centroids (those re-score every centroid).  Results are unchanged. */
+fgpu_status fgpu_coarse_search_stats(const fgpu_index* idx, const float* d_queries, int nq, int nprobe,
+                                     float prune_ratio, uint32_t* d_probe_ids, float* d_probe_dists,
+                                     unsigned long long* d_stats, void* d_workspace, size_t workspace_bytes,
+                                     void* stream);
 
 /* The prune step of prune_and_count_fused_kernel (gpu_global.cu:43-50), in
  * place: a probe whose distance exceeds (its query's first distance) *
@@ -248,7 +256,8 @@ fgpu_status fgpu_search_stage_times(const fgpu_index* idx, float* h_ms, int n);
  * about 120k at nprobe 32).  No hipMalloc, hipFree or allocating library call.
  * Every call on one GPU shares that GPU's array: calls that overlap on one GPU
  * (other streams, other host threads) race and must be serialised by the
- * caller. */
+ * caller.  Index creation resolves the array's address on the current device,
+ * so the first call may itself be under graph capture. */
 #define FGPU_NOALLOC_SCRATCH_BYTES (32u << 20)
 size_t fgpu_search_noalloc_max_bytes(void);
 int fgpu_search_noalloc_max_rows(int nlist, int nprobe);

@@ -23,9 +23,11 @@ def _say(msg):
     sys.stdout.flush()
 
 
-@pytest.mark.parametrize("noalloc", [False, True])
-def test_search_replays_from_a_graph(noalloc):
-    _say(f"graph capture of the plain search (noalloc={noalloc})")
+@pytest.mark.parametrize("noalloc,captured_first", [(False, False), (True, False), (True, True), (False, True)])
+def test_search_replays_from_a_graph(noalloc, captured_first):
+    """captured_first: the index's first search is the captured one (index
+    creation has made every per-device lookup a search needs)."""
+    _say(f"graph capture of the plain search (noalloc={noalloc}, first call captured={captured_first})")
     rng = np.random.default_rng(99)
     dim, m, nlist, nq, nprobe, k = 128, 32, 200, 3000, 24, 10
     x = oracle.gen_gmm(60000, dim, 40, seed=9, sig_lo=0.08)
@@ -41,22 +43,28 @@ def test_search_replays_from_a_graph(noalloc):
     else:
         ws = torch.empty(idx.search_workspace_bytes(nq, nprobe), dtype=torch.uint8, device="cuda")
         step = lambda: idx.search(dq, nprobe, k, workspace=ws, out=(oi, od))  # noqa: E731
+    g = torch.cuda.CUDAGraph()
+    if captured_first:
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g):
+            step()
+        torch.cuda.synchronize()
     step()
     torch.cuda.synchronize()
     ref_i, ref_d = oi.clone(), od.clone()
     probes, _ = oracle.coarse(q[:200], cent, nprobe)
     wid, wd = oracle.search_plain(q[:200], cent, cb, offs, ids, codes, probes, k)
     assert np.array_equal(ref_i[:200].cpu().numpy(), wid)
-    s = torch.cuda.Stream()
-    s.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(s):
-        step()
-    torch.cuda.current_stream().wait_stream(s)
-    torch.cuda.synchronize()
-    g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g):
-        step()
-    torch.cuda.synchronize()
+    if not captured_first:
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            step()
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g):
+            step()
+        torch.cuda.synchronize()
     for _ in range(4):
         oi.fill_(-7)
         od.fill_(-1.0)

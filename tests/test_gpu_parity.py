@@ -73,11 +73,11 @@ def test_l2_topk_bit_exact(dim, nc, p):
 @pytest.mark.parametrize("case", ["large", "tiny", "sphere", "offset"])
 @pytest.mark.parametrize("dim,p,nc", [(128, 32, 1024), (128, 1, 1024), (36, 8, 1024), (128, 1, 3000)])
 def test_l2_topk_estimate_extremes(case, dim, p, nc):
-    """The select reads fp16 lower bounds of the shifted estimates: values past
-    the fp16 range (saturated bounds, every column re-scored), values in its
-    subnormal range, many near-equal distances (a query at the centre of a
-    sphere of centroids) and a large common offset of both sets (estimates
-    far from zero against small differences) all stay exact."""
+    """The select reads fp16 lower bounds of the shifted estimates, each row
+    scaled by a power of two into the fp16 range: large values (x 300), values
+    in the fp16 subnormal range, many near-equal distances (a query at the
+    centre of a sphere of centroids) and a large common offset of both sets
+    (estimates far from zero against small differences) all stay exact."""
     _say(f"l2_topk extremes case={case} dim={dim} p={p} nc={nc}")
     rng = np.random.default_rng(["large", "tiny", "sphere", "offset"].index(case) * 1000 + dim * 10 + p + nc)
     n = 129
@@ -105,6 +105,37 @@ def test_l2_topk_estimate_extremes(case, dim, p, nc):
 
 
 # --------------------------------------------------------------------------- coarse quantizer (A2, A3)
+@pytest.mark.parametrize("case", ["unit", "x300", "sift_like"])
+def test_coarse_margin_stays_tight_at_large_norms(case):
+    """Large norms do not turn the coarse step into a brute-force re-score:
+    the fp16 estimates of each row are scaled into range, so the margin still
+    admits few centroids per query (unit-scale mixture data, the same x 300,
+    and SIFT-like data with every coordinate in [0, 255] and squared norms
+    near 2e6); results bit-exact."""
+    _say(f"coarse margin case={case}")
+    rng = np.random.default_rng(["unit", "x300", "sift_like"].index(case) + 77)
+    if case == "sift_like":
+        x = fg.gen_gmm(20000, 128, 64, seed=8, lo=0.0, hi=200.0, sig_lo=12.0)
+        q = fg.gen_gmm(500, 128, 64, seed=8, set=1, lo=0.0, hi=200.0, sig_lo=12.0)
+        x, q = np.clip(x, 0, 255).round(), np.clip(q, 0, 255).round()
+    else:
+        sc = np.float32(300.0 if case == "x300" else 1.0)
+        x = fg.gen_gmm(20000, 128, 64, seed=8, sig_lo=0.1) * sc
+        q = fg.gen_gmm(500, 128, 64, seed=8, set=1, sig_lo=0.1) * sc
+    x, q = x.astype(np.float32), q.astype(np.float32)
+    cent = x[rng.choice(x.shape[0], 1024, replace=False)].copy()
+    offs, ids, lc, _, cb = _random_index(rng, 4000, 128, 32, 1024)
+    idx = fg.Index.from_arrays(128, 32, offs, ids, lc, cent, cb)
+    pid, pd, st = idx.coarse_search_stats(torch.from_numpy(q).cuda(), 32)
+    pid, pd = _host(pid).view(np.uint32), _host(pd)
+    oid, od = oracle.coarse(q, cent, 32)
+    assert np.array_equal(pid, oid) and np.array_equal(_bits(pd), _bits(od))
+    per_q = st["rescored"] / q.shape[0]
+    _say(f"  {per_q:.1f} centroids re-scored a query, {st['full_rows']} queries re-scored all 1024")
+    assert st["full_rows"] == 0 and per_q < 160, st
+    idx.close()
+
+
 @pytest.mark.parametrize("prune_ratio", [100.0, 1.3])
 def test_coarse_search_bit_exact(prune_ratio):
     _say(f"coarse prune_ratio={prune_ratio}")
