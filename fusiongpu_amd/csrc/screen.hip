@@ -227,23 +227,31 @@ __device__ __forceinline__ int list_items(int cnt, int nq, int n) {
 // slack of the double arithmetic.  qv: this lane's two query dims (2 lane,
 // 2 lane + 1).  Returns nr2; the record is unusable when nr2 is not <=
 // kMaxNorm2 (NaN included), and the caller then adds no pair.
+template <int D>
+__device__ __forceinline__ float2 centroid_dims(const ScreenArgs& a, int l) {
+  const int lane = threadIdx.x & 63;
+  return 2 * lane < D ? reinterpret_cast<const float2*>(a.centroids + (size_t)l * D)[lane] : make_float2(0.0f, 0.0f);
+}
+
+// cv: this lane's two dims of the list's centroid (centroid_dims).  A record
+// whose nr2 is out of range gets zero A fragments and the round's inactive
+// block (round 2: V = 1e30), so its row passes nothing and bounds nothing.
 template <int D, int ROUND>
-__device__ float pair_record(const ScreenArgs& a, int64_t ent, float2 qv, int l, float T) {
+__device__ float pair_record(const ScreenArgs& a, int64_t ent, float2 qv, float2 cv, float T) {
   const int lane = threadIdx.x & 63;
   const bool has = 2 * lane < D;
-  float r0 = 0.0f, r1 = 0.0f;
-  if (has) {
-    const float2 cv = reinterpret_cast<const float2*>(a.centroids + (size_t)l * D)[lane];
-    r0 = qv.x - cv.x;
-    r1 = qv.y - cv.y;
-  }
+  const float r0 = has ? qv.x - cv.x : 0.0f, r1 = has ? qv.y - cv.y : 0.0f;
   const float nr2 = wave_sum_f(__builtin_fmaf(r1, r1, r0 * r0));
+  const bool ok = nr2 <= kMaxNorm2;  // false for NaN
   uint32_t* rec = reinterpret_cast<uint32_t*>(a.arec + ent * kRec);
   if (has) {
     const int d = 2 * lane, h = d / (D / 2), w = d % (D / 2);
-    rec[(h * kRecHalf + w / 8) * 4 + (w % 8) / 2] = pack2(bf_rn(-2.0f * r0), bf_rn(-2.0f * r1));
+    rec[(h * kRecHalf + w / 8) * 4 + (w % 8) / 2] = ok ? pack2(bf_rn(-2.0f * r0), bf_rn(-2.0f * r1)) : 0u;
   }
-  if (lane < 2 && nr2 <= kMaxNorm2) {
+  if (lane < 2 && !ok)
+    a.arec[ent * kRec + lane * kRecHalf + kRecHalf - 1] =
+        make_uint4(0u, 0u, 0u, ROUND == 2 && lane == 0 ? pack2(0u, bf_rn(1e30f)) : 0u);
+  if (lane < 2 && ok) {
     const double n2 = (double)nr2;
     const double R = sqrt(n2 * (1.0 + 0x1p-16)) * (1.0 + kDbl);
     const uint16_t aR = bf_up(kA * R);
@@ -299,7 +307,7 @@ __global__ __launch_bounds__(256) void screen_pairs1_kernel(ScreenArgs a) {
   int2 f = make_int2(-1, -1);
   if (pf >= 0 && a.offsets[lf + 1] - a.offsets[lf] >= a.k) {
     const int64_t ent = (int64_t)q * a.nprobe + pf;
-    const float nr2 = pair_record<D, 1>(a, ent, query_dims(a, q, D), lf, 0.0f);
+    const float nr2 = pair_record<D, 1>(a, ent, query_dims(a, q, D), centroid_dims<D>(a, lf), 0.0f);
     if (nr2 <= kMaxNorm2 && lane == 0) {
       const int pos = bucket_add(a, a.cnt1, lf, q, (int)ent);
       if (pos >= 0) f = make_int2(lf, pos);
@@ -346,16 +354,26 @@ __global__ __launch_bounds__(256) void screen_pairs2_kernel(ScreenArgs a) {
       pass = l < (uint32_t)a.nlist && a.offsets[l + 1] - a.offsets[l] > 0 &&
              list_lower_bound(a.probe_dists[t], a.rmax[l]) <= T;
     }
-    for (uint64_t m = __ballot(pass); m; m &= m - 1) {
-      const int b = __builtin_ctzll(m);
-      const int lb = __builtin_amdgcn_readlane((int)l, b);
-      const int64_t ent = (int64_t)q * a.nprobe + p0 + b;
-      const float nr2 = pair_record<D, 2>(a, ent, qv, lb, T);
-      if (!(nr2 <= kMaxNorm2)) {
-        bad = true;
-        continue;
-      }
-      if (lane == 0) bucket_add(a, a.cnt2, lb, q, (int)ent);
+    // Every passing probe joins its list's bucket at once (one atomic a
+    // lane); a pair whose record turns out unusable sends the whole query to
+    // the LUT kernel, whose rescore then ignores its candidates.
+    if (pass) bucket_add(a, a.cnt2, (int)l, q, (int)((int64_t)q * a.nprobe + p));
+    // The records, one pair at a time with the next pair's centroid loads in
+    // flight.
+    uint64_t m = __ballot(pass);
+    if (!m) continue;
+    int b = __builtin_ctzll(m);
+    float2 cv = centroid_dims<D>(a, __builtin_amdgcn_readlane((int)l, b));
+    while (true) {
+      const uint64_t rest = m & (m - 1);
+      const int bn = rest ? __builtin_ctzll(rest) : b;
+      const float2 cn = rest ? centroid_dims<D>(a, __builtin_amdgcn_readlane((int)l, bn)) : cv;
+      const float nr2 = pair_record<D, 2>(a, (int64_t)q * a.nprobe + p0 + b, qv, cv, T);
+      bad = bad || !(nr2 <= kMaxNorm2);
+      if (!rest) break;
+      m = rest;
+      b = bn;
+      cv = cn;
     }
   }
   if (bad && lane == 0) a.thr[q] = INFINITY;
