@@ -395,32 +395,6 @@ __device__ __forceinline__ double est_margin(float kappa, float xn, float cn_max
 constexpr int kCandCap = 512;
 constexpr int kSelectMax = 4 * kWave;  // p limit of the coarse select: four sorted 64-key lists
 
-// Ascending bitonic sort of one 32-bit key per lane across the wave.
-template <int S>
-__device__ __forceinline__ void bitonic_stage_u32(uint32_t& k, bool up) {
-  const uint32_t o = (uint32_t)xchg<S>((int)k);
-  const bool lower = (lane_id() & S) == 0;
-  k = ((k < o) == (lower == up)) ? k : o;
-}
-template <int SIZE>
-__device__ __forceinline__ void bitonic_pass_u32(uint32_t& k, bool up) {
-  if constexpr (SIZE > 32) bitonic_stage_u32<32>(k, up);
-  if constexpr (SIZE > 16) bitonic_stage_u32<16>(k, up);
-  if constexpr (SIZE > 8) bitonic_stage_u32<8>(k, up);
-  if constexpr (SIZE > 4) bitonic_stage_u32<4>(k, up);
-  if constexpr (SIZE > 2) bitonic_stage_u32<2>(k, up);
-  bitonic_stage_u32<1>(k, up);
-}
-__device__ __forceinline__ void wave_sort_u32(uint32_t& k) {
-  const int lane = lane_id();
-  bitonic_pass_u32<2>(k, (lane & 2) == 0);
-  bitonic_pass_u32<4>(k, (lane & 4) == 0);
-  bitonic_pass_u32<8>(k, (lane & 8) == 0);
-  bitonic_pass_u32<16>(k, (lane & 16) == 0);
-  bitonic_pass_u32<32>(k, (lane & 32) == 0);
-  bitonic_pass_u32<64>(k, true);
-}
-
 // Which column a lane's value j holds: V = 1, column j*64 + lane; V = 4 or 8
 // (a row read as 16-byte vectors), runs of V consecutive columns a lane,
 // column (j / V) * 64 V + V lane + j % V.

@@ -171,6 +171,32 @@ __device__ __forceinline__ void wave_sort64_k(uint64_t& k) {
   bitonic_pass_k<32>(k, (lane & 32) == 0);
   bitonic_pass_k<64>(k, true);
 }
+// Ascending bitonic sort of one 32-bit key per lane across the wave.
+template <int S>
+__device__ __forceinline__ void bitonic_stage_u32(uint32_t& k, bool up) {
+  const uint32_t o = (uint32_t)xchg<S>((int)k);
+  const bool lower = (lane_id() & S) == 0;
+  k = ((k < o) == (lower == up)) ? k : o;
+}
+template <int SIZE>
+__device__ __forceinline__ void bitonic_pass_u32(uint32_t& k, bool up) {
+  if constexpr (SIZE > 32) bitonic_stage_u32<32>(k, up);
+  if constexpr (SIZE > 16) bitonic_stage_u32<16>(k, up);
+  if constexpr (SIZE > 8) bitonic_stage_u32<8>(k, up);
+  if constexpr (SIZE > 4) bitonic_stage_u32<4>(k, up);
+  if constexpr (SIZE > 2) bitonic_stage_u32<2>(k, up);
+  bitonic_stage_u32<1>(k, up);
+}
+__device__ __forceinline__ void wave_sort_u32(uint32_t& k) {
+  const int lane = lane_id();
+  bitonic_pass_u32<2>(k, (lane & 2) == 0);
+  bitonic_pass_u32<4>(k, (lane & 4) == 0);
+  bitonic_pass_u32<8>(k, (lane & 8) == 0);
+  bitonic_pass_u32<16>(k, (lane & 16) == 0);
+  bitonic_pass_u32<32>(k, (lane & 32) == 0);
+  bitonic_pass_u32<64>(k, true);
+}
+
 __device__ __forceinline__ uint64_t wave_reverse64(uint64_t v) {
   const uint32_t lo = (uint32_t)wave_reverse((int)(uint32_t)v), hi = (uint32_t)wave_reverse((int)(uint32_t)(v >> 32));
   return ((uint64_t)hi << 32) | lo;

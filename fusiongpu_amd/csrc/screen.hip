@@ -215,29 +215,29 @@ __device__ __forceinline__ int list_items(int cnt, int nq, int n) {
   return ng * ((n + per - 1) / per);
 }
 
-// The pair record of entry ent = (query q, probe p of list l), written by a
-// whole wave: for each lane half h (dims [h D/2, (h+1) D/2)) the A fragments
-// -2 bf16(r), r = fl(q - c), in MFMA operand order (fragment c holds dims
-// h D/2 + 8c .. + 7), then the extra K block of the round's test:
+// The pair record of entry ent = (query q, probe p of list l): for each lane
+// half h (dims [h D/2, (h+1) D/2)) the A fragments -2 bf16(r), r = fl(q - c),
+// in MFMA operand order (fragment c holds dims h D/2 + 8c .. + 7), then the
+// extra K block of the round's test:
 //   round 1 (U):  h0 [ aR, 0, 0, 0, 1, 1, 1, c1]   h1 [c2, c3, 0 ...]
 //   round 2 (V):  h0 [-aR, 1, 1, 1, 0, 0, 0, v1]   h1 [v2, v3, 0 ...]
 // against the vector's block [X, y'1..3, y''1..3, 1] (h0) and [1, 1, 0 ...]
 // (h1): aR = bf16 above a R, c1 + c2 + c3 >= (t nr2 + g R^2 + 2^-110 (1 + R)),
 // v1 + v2 + v3 <= -(t T - nr2 + g R^2 + 2^-110 (1 + R)), each with the 2^-40
-// slack of the double arithmetic.  qv: this lane's two query dims (2 lane,
-// 2 lane + 1).  Returns nr2; the record is unusable when nr2 is not <=
-// kMaxNorm2 (NaN included), and the caller then adds no pair.
+// slack of the double arithmetic.  The record is unusable when nr2 is not
+// <= kMaxNorm2 (NaN included): then its A fragments are zero and its block
+// the round's inactive one (round 2: V = 1e30), so its row passes nothing
+// and bounds nothing, and the caller adds no pair or drops the query.
+//
+// pair_a: the A fragments, by a whole wave (qv, cv: this lane's two dims of
+// the query and of the list's centroid); returns nr2 on every lane.
 template <int D>
 __device__ __forceinline__ float2 centroid_dims(const ScreenArgs& a, int l) {
   const int lane = threadIdx.x & 63;
   return 2 * lane < D ? reinterpret_cast<const float2*>(a.centroids + (size_t)l * D)[lane] : make_float2(0.0f, 0.0f);
 }
-
-// cv: this lane's two dims of the list's centroid (centroid_dims).  A record
-// whose nr2 is out of range gets zero A fragments and the round's inactive
-// block (round 2: V = 1e30), so its row passes nothing and bounds nothing.
-template <int D, int ROUND>
-__device__ float pair_record(const ScreenArgs& a, int64_t ent, float2 qv, float2 cv, float T) {
+template <int D>
+__device__ float pair_a(const ScreenArgs& a, int64_t ent, float2 qv, float2 cv) {
   const int lane = threadIdx.x & 63;
   const bool has = 2 * lane < D;
   const float r0 = has ? qv.x - cv.x : 0.0f, r1 = has ? qv.y - cv.y : 0.0f;
@@ -248,30 +248,32 @@ __device__ float pair_record(const ScreenArgs& a, int64_t ent, float2 qv, float2
     const int d = 2 * lane, h = d / (D / 2), w = d % (D / 2);
     rec[(h * kRecHalf + w / 8) * 4 + (w % 8) / 2] = ok ? pack2(bf_rn(-2.0f * r0), bf_rn(-2.0f * r1)) : 0u;
   }
-  if (lane < 2 && !ok)
-    a.arec[ent * kRec + lane * kRecHalf + kRecHalf - 1] =
-        make_uint4(0u, 0u, 0u, ROUND == 2 && lane == 0 ? pack2(0u, bf_rn(1e30f)) : 0u);
-  if (lane < 2 && ok) {
-    const double n2 = (double)nr2;
-    const double R = sqrt(n2 * (1.0 + 0x1p-16)) * (1.0 + kDbl);
-    const uint16_t aR = bf_up(kA * R);
-    uint16_t p1, p2, p3;
-    uint4 ex = make_uint4(0u, 0u, 0u, 0u);
-    if (ROUND == 2) {
-      const double t = (double)fmaxf(T, 0.0f);
-      const double rhs = t * kTInfl - n2 + kG * R * R + kAbs * (1.0 + R);
-      split3<false>(-rhs - kDbl * (t + n2 + kG * R * R), p1, p2, p3);
-      ex = lane == 0 ? make_uint4(pack2(aR ^ 0x8000u, 0x3F80u), kOneOne, 0u, pack2(0u, p1))
-                     : make_uint4(pack2(p2, p3), 0u, 0u, 0u);
-    } else {
-      const double c = n2 * kTInfl + kG * R * R + kAbs * (1.0 + R);
-      split3<true>(c * (1.0 + kDbl), p1, p2, p3);
-      ex = lane == 0 ? make_uint4(pack2(aR, 0u), 0u, kOneOne, pack2(0x3F80u, p1))
-                     : make_uint4(pack2(p2, p3), 0u, 0u, 0u);
-    }
-    a.arec[ent * kRec + lane * kRecHalf + kRecHalf - 1] = ex;
-  }
   return nr2;
+}
+// pair_ex: both lane halves' extra blocks of entry ent, by one lane.
+template <int ROUND>
+__device__ void pair_ex(const ScreenArgs& a, int64_t ent, float nr2, float T) {
+  uint4* rec = a.arec + ent * kRec;
+  if (!(nr2 <= kMaxNorm2)) {
+    rec[kRecHalf - 1] = make_uint4(0u, 0u, 0u, ROUND == 2 ? pack2(0u, bf_rn(1e30f)) : 0u);
+    rec[2 * kRecHalf - 1] = make_uint4(0u, 0u, 0u, 0u);
+    return;
+  }
+  const double n2 = (double)nr2;
+  const double R = sqrt(n2 * (1.0 + 0x1p-16)) * (1.0 + kDbl);
+  const uint16_t aR = bf_up(kA * R);
+  uint16_t p1, p2, p3;
+  if (ROUND == 2) {
+    const double t = (double)fmaxf(T, 0.0f);
+    const double rhs = t * kTInfl - n2 + kG * R * R + kAbs * (1.0 + R);
+    split3<false>(-rhs - kDbl * (t + n2 + kG * R * R), p1, p2, p3);
+    rec[kRecHalf - 1] = make_uint4(pack2(aR ^ 0x8000u, 0x3F80u), kOneOne, 0u, pack2(0u, p1));
+  } else {
+    const double c = n2 * kTInfl + kG * R * R + kAbs * (1.0 + R);
+    split3<true>(c * (1.0 + kDbl), p1, p2, p3);
+    rec[kRecHalf - 1] = make_uint4(pack2(aR, 0u), 0u, kOneOne, pack2(0x3F80u, p1));
+  }
+  rec[2 * kRecHalf - 1] = make_uint4(pack2(p2, p3), 0u, 0u, 0u);
 }
 
 __device__ __forceinline__ float2 query_dims(const ScreenArgs& a, int q, int dim) {
@@ -307,7 +309,8 @@ __global__ __launch_bounds__(256) void screen_pairs1_kernel(ScreenArgs a) {
   int2 f = make_int2(-1, -1);
   if (pf >= 0 && a.offsets[lf + 1] - a.offsets[lf] >= a.k) {
     const int64_t ent = (int64_t)q * a.nprobe + pf;
-    const float nr2 = pair_record<D, 1>(a, ent, query_dims(a, q, D), centroid_dims<D>(a, lf), 0.0f);
+    const float nr2 = pair_a<D>(a, ent, query_dims(a, q, D), centroid_dims<D>(a, lf));
+    if (lane == 0) pair_ex<1>(a, ent, nr2, 0.0f);
     if (nr2 <= kMaxNorm2 && lane == 0) {
       const int pos = bucket_add(a, a.cnt1, lf, q, (int)ent);
       if (pos >= 0) f = make_int2(lf, pos);
@@ -328,6 +331,17 @@ __global__ __launch_bounds__(256) void screen_pairs2_kernel(ScreenArgs a) {
   const int lane = threadIdx.x & 63;
   const int q = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   if (q >= a.nq) return;
+  // The first 64 probes' lists, sizes, bounds and the query's dims do not
+  // depend on T: their loads go out before the threshold's.
+  uint32_t l0 = 0xFFFFFFFFu;
+  float lb0 = INFINITY;
+  if (lane < a.nprobe) {
+    const size_t t = (size_t)q * a.nprobe + lane;
+    l0 = a.probes[t];
+    if (l0 < (uint32_t)a.nlist && a.offsets[l0 + 1] - a.offsets[l0] > 0)
+      lb0 = list_lower_bound(a.probe_dists[t], a.rmax[l0]);
+  }
+  const float2 qv = query_dims(a, q, D);
   const int2 f = a.first[q];
   uint32_t gm = 0x7F800000u;
   if (f.x >= 0 && lane < 32) {
@@ -336,19 +350,18 @@ __global__ __launch_bounds__(256) void screen_pairs2_kernel(ScreenArgs a) {
     const uint32_t* g = a.gminbuf + (size_t)q * kMaxChunks * 32 + lane;
     for (int c = 0; c < nch; ++c) gm = min(gm, g[c * 32]);
   }
-  uint64_t key = gm;
-  wave_sort64_k(key);
-  const float kth = __uint_as_float((uint32_t)readlane64(key, a.k - 1));
+  // U >= 0, so float order is unsigned order of the bits
+  wave_sort_u32(gm);
+  const float kth = __uint_as_float((uint32_t)__builtin_amdgcn_readlane((int)gm, a.k - 1));
   const float T = kth < INFINITY ? f_above((double)kth * kTInfl) : INFINITY;
   if (lane == 0) a.thr[q] = T;
   if (!(T < INFINITY)) return;
-  const float2 qv = query_dims(a, q, D);
   bool bad = false;
   for (int p0 = 0; p0 < a.nprobe; p0 += kWave) {
     const int p = p0 + lane;
-    uint32_t l = 0xFFFFFFFFu;
-    bool pass = false;
-    if (p < a.nprobe) {
+    uint32_t l = l0;
+    bool pass = p0 == 0 && lb0 <= T;
+    if (p0 > 0 && p < a.nprobe) {
       const size_t t = (size_t)q * a.nprobe + p;
       l = a.probes[t];
       pass = l < (uint32_t)a.nlist && a.offsets[l + 1] - a.offsets[l] > 0 &&
@@ -358,25 +371,31 @@ __global__ __launch_bounds__(256) void screen_pairs2_kernel(ScreenArgs a) {
     // lane); a pair whose record turns out unusable sends the whole query to
     // the LUT kernel, whose rescore then ignores its candidates.
     if (pass) bucket_add(a, a.cnt2, (int)l, q, (int)((int64_t)q * a.nprobe + p));
-    // The records, one pair at a time with the next pair's centroid loads in
-    // flight.
+    // The A fragments, one pair at a time with the next pair's centroid
+    // loads in flight; the lane of each probe keeps its pair's nr2, and the
+    // extra blocks follow lane-parallel (one lane a pair).
     uint64_t m = __ballot(pass);
     if (!m) continue;
+    float my_nr2 = 0.0f;
     int b = __builtin_ctzll(m);
     float2 cv = centroid_dims<D>(a, __builtin_amdgcn_readlane((int)l, b));
     while (true) {
       const uint64_t rest = m & (m - 1);
       const int bn = rest ? __builtin_ctzll(rest) : b;
       const float2 cn = rest ? centroid_dims<D>(a, __builtin_amdgcn_readlane((int)l, bn)) : cv;
-      const float nr2 = pair_record<D, 2>(a, (int64_t)q * a.nprobe + p0 + b, qv, cv, T);
-      bad = bad || !(nr2 <= kMaxNorm2);
+      const float nr2 = pair_a<D>(a, (int64_t)q * a.nprobe + p0 + b, qv, cv);
+      if (lane == b) my_nr2 = nr2;
       if (!rest) break;
       m = rest;
       b = bn;
       cv = cn;
     }
+    if (pass) {
+      pair_ex<2>(a, (int64_t)q * a.nprobe + p, my_nr2, T);
+      bad = bad || !(my_nr2 <= kMaxNorm2);
+    }
   }
-  if (bad && lane == 0) a.thr[q] = INFINITY;
+  if (__ballot(bad) && lane == 0) a.thr[q] = INFINITY;
 }
 
 // ---- the screen ---------------------------------------------------------------------------
