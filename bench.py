@@ -111,13 +111,13 @@ def stream_read_peak(torch, fg, dev, gib=4, reps=10):
     return (gib << 30) / (ms * 1e-3) / 1e9
 
 
-def row_gather_peak(torch, fg, rows, nreads, reps=5, seed=5):
-    """Measured random-row read rate over a 2-D device tensor: nreads whole rows at seeded random ids, one lane a
-    row with all of its loads in flight (the rerank's and graph search's pattern)."""
+def row_gather_peak(torch, fg, rows, nreads, lanes_per_row=8, reps=5, seed=5):
+    """Measured random-row read rate over a 2-D device tensor: nreads whole rows at seeded random ids, eight lanes a
+    row (the rerank's and graph search's pattern) or one lane a row, all loads in flight."""
     g = torch.Generator(device=rows.device)
     g.manual_seed(seed)
     idx = torch.randint(0, rows.shape[0], (nreads,), generator=g, device=rows.device, dtype=torch.int32)
-    ms = timed_ms(torch, torch.cuda.current_stream(), reps, lambda: fg.row_gather(rows, idx))
+    ms = timed_ms(torch, torch.cuda.current_stream(), reps, lambda: fg.row_gather(rows, idx, lanes_per_row))
     return nreads * rows.shape[1] * rows.element_size() / (ms * 1e-3) / 1e9
 
 
@@ -693,9 +693,10 @@ def run_c3(args, torch, fg, dev):
         f"{adc_gbs:.0f} GB/s), rerank {rr_ms:.3f} ms ({visited} rows = {rr_bytes / 1e9:.2f} GB -> "
         f"{rr_bytes / (rr_ms * 1e-3) / 1e9:.0f} GB/s); candidates/query {tc.float().mean().item():.0f}")
     rows_peak = row_gather_peak(torch, fg, dx, visited)
+    rows_one_lane = row_gather_peak(torch, fg, dx, visited, lanes_per_row=1)
     read_peak = stream_read_peak(torch, fg, dev)
     log(f"measured read rates: {rows_peak:.0f} GB/s for random {dim * 4}-byte rows of the base "
-        f"({visited} rows, one lane a row), {read_peak:.0f} GB/s streaming")
+        f"({visited} rows, eight lanes a row; {rows_one_lane:.0f} GB/s one lane a row), {read_peak:.0f} GB/s streaming")
     if args.copy_probe:
         a = torch.empty(1 << 28, dtype=torch.float32, device=dev)
         b = torch.empty_like(a)
@@ -767,9 +768,11 @@ def run_c3(args, torch, fg, dev):
                       "rerank_rows": visited, "rerank_gbs": round(rr_bytes / (rr_ms * 1e-3) / 1e9, 1),
                       "rerank_frac_of_measured_row_rate": round(rr_bytes / (rr_ms * 1e-3) / 1e9 / rows_peak, 4),
                       "candidates_per_query": round(tc.float().mean().item(), 1)},
-        "measured_read_gbs": {"random_rows": round(rows_peak, 1), "streaming": round(read_peak, 1),
+        "measured_read_gbs": {"random_rows": round(rows_peak, 1), "random_rows_one_lane": round(rows_one_lane, 1),
+                              "streaming": round(read_peak, 1),
                               "note": f"random rows: {visited} whole {dim * 4}-byte rows of the base at seeded random "
-                                      "ids, one lane a row (fgpu_row_gather); streaming: fgpu_stream_read over 4 GiB"},
+                                      "ids, eight lanes a row (fgpu_row_gather; the rerank's pattern) and one lane a "
+                                      "row (fgpu_row_gather_lanes 1); streaming: fgpu_stream_read over 4 GiB"},
         "cpu_baseline": cpu, "parity": parity, "recall_at_k": recall,
         "ground_truth": {"seconds": round(gt_s, 3), "oracle_parity_50": gt_parity},
     }
@@ -915,7 +918,9 @@ def run_c5(args, torch, fg, dev):
     log(f"graph search: {ms_per_step:.3f} ms/step, {qps:,.0f} QPS; kernel {kern_ms:.3f} ms; {n_steps / nq:.1f} steps "
         f"and {n_evals / nq:.0f} distance evaluations per query -> {gather_bytes / 1e9:.2f} GB = {gbs:.0f} GB/s")
     rows_peak = row_gather_peak(torch, fg, dx, n_evals)
-    log(f"measured read rate for random {dim * 4}-byte rows of the base: {rows_peak:.0f} GB/s ({n_evals} rows)")
+    rows_one_lane = row_gather_peak(torch, fg, dx, n_evals, lanes_per_row=1)
+    log(f"measured read rate for random {dim * 4}-byte rows of the base: {rows_peak:.0f} GB/s ({n_evals} rows, "
+        f"eight lanes a row; {rows_one_lane:.0f} GB/s one lane a row)")
     gid, gd = out[0].cpu().numpy(), out[1].cpu().numpy()
     gt, _ = fg.knn_exact(dq, dx, k)
     gt = gt.cpu().numpy()
@@ -962,9 +967,10 @@ def run_c5(args, torch, fg, dev):
                      "algorithmic_bytes_per_launch": gather_bytes, "avg_launch_ms": round(kern_ms, 4),
                      "distance_evaluations": n_evals, "steps": n_steps,
                      "measured_row_gather_gbs": round(rows_peak, 1),
+                     "measured_row_gather_one_lane_gbs": round(rows_one_lane, 1),
                      "frac_of_measured_row_rate": round(gbs / rows_peak, 4),
                      "note": "achieved = distance rows + adjacency rows read / kernel time; the measured row rate is "
-                             "fgpu_row_gather over as many random whole rows of the base, one lane a row"},
+                             "fgpu_row_gather over as many random whole rows of the base, eight lanes a row"},
         "cpu_baseline": cpu, "parity": parity, "recall_at_k": recall,
         "walks_in_query_component": round(float(own.mean()), 4),
         "recall_in_query_component": round(float(rec[own].mean()), 4),

@@ -56,6 +56,7 @@ _SIGS = {
     "fgpu_stream_read_grid": (_i32, []),
     "fgpu_stream_read": (_i32, [_vp, _sz, _vp, _vp]),
     "fgpu_row_gather": (_i32, [_vp, _i64, _i32, _vp, _i64, _vp, _vp]),
+    "fgpu_row_gather_lanes": (_i32, [_vp, _i64, _i32, _vp, _i64, _i32, _vp, _vp]),
     "fgpu_coarse_workspace_bytes": (_sz, [_i32, _i32]),
     "fgpu_coarse_search": (_i32, [_vp, _vp, _i32, _i32, _f32, _vp, _vp, _vp, _sz, _vp]),
     "fgpu_coarse_graph_workspace_bytes": (_sz, [_i32, _i32]),
@@ -357,17 +358,17 @@ def stream_read(data, stream=None):
         _check(lib.fgpu_stream_read(_dev_ptr(data), data.numel() * data.element_size(), _dev_ptr(sink), _stream()))
 
 
-def row_gather(rows, idx, stream=None):
-    """Read whole rows rows[idx[i]] (384- or 512-byte rows of a contiguous 2-D device tensor), one lane a row
-    (fgpu_row_gather), for a measured random-row read rate."""
+def row_gather(rows, idx, lanes_per_row=8, stream=None):
+    """Read whole rows rows[idx[i]] (384- or 512-byte rows of a contiguous 2-D device tensor), eight lanes a row
+    (the library's pattern) or one (fgpu_row_gather_lanes), for a measured random-row read rate."""
     torch = _torch()
     with _on(stream):
         if not (torch.is_tensor(rows) and rows.is_cuda and rows.is_contiguous() and rows.dim() == 2):
             raise ValueError("row_gather: expected a contiguous 2-D device tensor")
         ix = _dev(idx, torch.int32, "idx", (None,))
         sink = torch.empty(lib.fgpu_stream_read_grid(), dtype=torch.int64, device="cuda")
-        _check(lib.fgpu_row_gather(_dev_ptr(rows), rows.shape[0], rows.shape[1] * rows.element_size(), _dev_ptr(ix),
-                                   ix.shape[0], _dev_ptr(sink), _stream()))
+        _check(lib.fgpu_row_gather_lanes(_dev_ptr(rows), rows.shape[0], rows.shape[1] * rows.element_size(),
+                                         _dev_ptr(ix), ix.shape[0], int(lanes_per_row), _dev_ptr(sink), _stream()))
 
 
 # --------------------------------------------------------------------------- index + search

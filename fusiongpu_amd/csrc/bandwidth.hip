@@ -32,23 +32,29 @@ __global__ __launch_bounds__(256) void stream_read_kernel(const uint4* __restric
   if (threadIdx.x == 0) sink[blockIdx.x] = red[0];
 }
 
-// Random rows: each lane reads whole rows idx[i] (RB 16-byte loads, all
-// issued before any is used), the access pattern of the exact rerank and the
-// graph search (one lane a candidate row).
-template <int RB>
+// Random rows: n whole rows idx[i], LPR lanes a row.  With LPR = 1 each lane
+// reads its own row (RB 16-byte loads, all issued before any is used), so a
+// load instruction touches 64 rows; with LPR = 8 eight lanes share a row, each
+// 16 bytes of every 128-byte line, so an instruction touches 8 rows.  The
+// exact rerank and the graph search load their candidate rows the second way
+// (wave_rows_l2).
+template <int RB, int LPR>
 __global__ __launch_bounds__(256) void row_gather_kernel(const uint4* __restrict__ d, int64_t nrows,
                                                          const int32_t* __restrict__ idx, int64_t n,
                                                          unsigned long long* __restrict__ sink) {
-  const int64_t stride = (int64_t)gridDim.x * 256;
+  static_assert(RB % LPR == 0, "a row splits evenly over its lanes");
+  constexpr int kRowsPerGroup = 256 / LPR;
+  const int sub = (int)threadIdx.x % LPR;
   uint32_t acc = 0;
-  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += stride) {
+  for (int64_t i = (int64_t)blockIdx.x * kRowsPerGroup + threadIdx.x / LPR; i < n;
+       i += (int64_t)gridDim.x * kRowsPerGroup) {
     const int64_t r = min(max((int64_t)idx[i], (int64_t)0), nrows - 1);  // out-of-range ids read a valid row
-    const uint4* row = d + r * RB;
-    uint4 v[RB];
+    const uint4* row = d + r * RB + sub;
+    uint4 v[RB / LPR];
 #pragma unroll
-    for (int j = 0; j < RB; ++j) v[j] = row[j];
+    for (int j = 0; j < RB / LPR; ++j) v[j] = row[LPR * j];
 #pragma unroll
-    for (int j = 0; j < RB; ++j) acc ^= v[j].x ^ v[j].y ^ v[j].z ^ v[j].w;
+    for (int j = 0; j < RB / LPR; ++j) acc ^= v[j].x ^ v[j].y ^ v[j].z ^ v[j].w;
   }
   __shared__ uint32_t red[256];
   red[threadIdx.x] = acc;
@@ -60,18 +66,27 @@ __global__ __launch_bounds__(256) void row_gather_kernel(const uint4* __restrict
   if (threadIdx.x == 0) sink[blockIdx.x] = red[0];
 }
 
+template <int RB>
+void launch_gather_rb(int lanes, const uint4* p, int64_t nrows, const int32_t* idx, int64_t n,
+                      unsigned long long* sink, int grid, hipStream_t s) {
+  if (lanes == 1)
+    hipLaunchKernelGGL((row_gather_kernel<RB, 1>), dim3((unsigned)grid), dim3(256), 0, s, p, nrows, idx, n, sink);
+  else
+    hipLaunchKernelGGL((row_gather_kernel<RB, 8>), dim3((unsigned)grid), dim3(256), 0, s, p, nrows, idx, n, sink);
+}
+
 }  // namespace
 
 fgpu_status launch_row_gather(const void* d, int64_t nrows, int row_bytes, const int32_t* idx, int64_t n,
-                              unsigned long long* sink, int grid, hipStream_t s) {
+                              int lanes_per_row, unsigned long long* sink, int grid, hipStream_t s) {
+  FGPU_CHECK(lanes_per_row == 1 || lanes_per_row == 8, FGPU_ERR_UNSUPPORTED, "row_gather: lanes_per_row must be 1 or 8");
+  FGPU_CHECK(row_bytes == 384 || row_bytes == 512, FGPU_ERR_UNSUPPORTED, "row_gather: row_bytes must be 384 or 512");
   if (n <= 0 || nrows <= 0 || grid <= 0) return FGPU_OK;
   const uint4* p = reinterpret_cast<const uint4*>(d);
   if (row_bytes == 384)
-    hipLaunchKernelGGL(row_gather_kernel<24>, dim3((unsigned)grid), dim3(256), 0, s, p, nrows, idx, n, sink);
-  else if (row_bytes == 512)
-    hipLaunchKernelGGL(row_gather_kernel<32>, dim3((unsigned)grid), dim3(256), 0, s, p, nrows, idx, n, sink);
+    launch_gather_rb<24>(lanes_per_row, p, nrows, idx, n, sink, grid, s);
   else
-    return set_error(FGPU_ERR_UNSUPPORTED, "row_gather: row_bytes must be 384 or 512");
+    launch_gather_rb<32>(lanes_per_row, p, nrows, idx, n, sink, grid, s);
   FGPU_HIP(hipGetLastError());
   return FGPU_OK;
 }

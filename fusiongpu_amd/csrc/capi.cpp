@@ -502,11 +502,17 @@ fgpu_status fgpu_stream_read(const void* d, size_t bytes, unsigned long long* d_
   return launch_stream_read(d, bytes, d_sink, fgpu_stream_read_grid(), as_stream(stream));
 }
 
-fgpu_status fgpu_row_gather(const void* d_rows, int64_t nrows, int row_bytes, const int32_t* d_idx, int64_t n,
-                            unsigned long long* d_sink, void* stream) {
+fgpu_status fgpu_row_gather_lanes(const void* d_rows, int64_t nrows, int row_bytes, const int32_t* d_idx, int64_t n,
+                                  int lanes_per_row, unsigned long long* d_sink, void* stream) {
   FGPU_CHECK(d_rows && d_idx && d_sink && n >= 0 && nrows >= 1 && ((uintptr_t)d_rows & 15) == 0, FGPU_ERR_ARG,
              "row_gather: need 16-byte aligned rows, indices and a sink");
-  return launch_row_gather(d_rows, nrows, row_bytes, d_idx, n, d_sink, fgpu_stream_read_grid(), as_stream(stream));
+  return launch_row_gather(d_rows, nrows, row_bytes, d_idx, n, lanes_per_row, d_sink, fgpu_stream_read_grid(),
+                           as_stream(stream));
+}
+
+fgpu_status fgpu_row_gather(const void* d_rows, int64_t nrows, int row_bytes, const int32_t* d_idx, int64_t n,
+                            unsigned long long* d_sink, void* stream) {
+  return fgpu_row_gather_lanes(d_rows, nrows, row_bytes, d_idx, n, 8, d_sink, stream);
 }
 
 }  // extern "C"

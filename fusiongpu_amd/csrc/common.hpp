@@ -273,4 +273,112 @@ __device__ __forceinline__ float l2_fma(const float* __restrict__ a, const float
   return acc;
 }
 
+// Orders one wave's LDS writes before its later LDS reads (and the reads
+// before later writes) when lanes exchange data through LDS.
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// ---- exact L2 of random rows, one row per lane, loaded eight lanes a row ------
+// A load instruction in which every lane reads its own row touches 64 rows in
+// 64 places; over a 3.8 GB array (10 M rows of 384 bytes) such loads read
+// 1.66 TB/s, against 6.1 TB/s when eight lanes share a row (each lane 16 bytes
+// of one 128-byte line, 8 rows an instruction).  So the wave loads its 64 rows
+// the second way and hands each 128-byte line through its LDS buffer `tr` to
+// the lane that owns the row, which then runs the sequential chain
+// acc = fma(q[d] - x[d], q[d] - x[d], acc) over d = 0, 1, ..., D-1, the same
+// operations in the same order as a lane reading its row itself.
+// Keeps the compiler from moving the wave's LDS accesses across this point.
+// The LDS carries out one wave's accesses in issue order, so a read after it
+// sees what every lane wrote before it.  (A wavefront-scope fence would do the
+// same but also pins the caller's private arrays in scratch memory.)
+__device__ __forceinline__ void wave_lds_order() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_wave_barrier();
+}
+
+constexpr int kRowTrStride = 36;  // floats a row in `tr`: 32 + 4 pad, so b128 reads down the rows spread over the banks
+// Floats of a wave's `tr` buffer when RX rows (64 or 32) change hands a round.
+template <int RX = kWave>
+constexpr int row_tr_floats() { return RX * kRowTrStride; }
+
+// Called by the whole wave.  `row` is the lane's row index into base[][D];
+// every lane must pass one inside the array.  `qs` is the query (D floats) in
+// LDS; `tr` is the wave's buffer of row_tr_floats<RX>() floats, 16-byte
+// aligned.  RX = 32 halves the buffer: each line then changes hands in two
+// rounds, rows 0-31 and rows 32-63.  The loads go in batches of up to LB
+// lines (LB = D / 32: all of them in one memory round trip, 8 LB float4
+// registers a lane).
+template <int D, int RX = kWave, int LBATCH = D / 32>
+__device__ __forceinline__ float wave_rows_l2(const float* __restrict__ base, int row, const float* qs, float* tr) {
+  static_assert(D % 32 == 0, "rows must be whole 128-byte lines");
+  static_assert(RX == 64 || RX == 32, "64 or 32 rows a round");
+  static_assert(LBATCH >= 1, "at least a line a batch");
+  constexpr int L = D / 32;       // 128-byte lines a row
+  constexpr int LB = LBATCH < L ? LBATCH : L;
+  constexpr int NR = kWave / RX;  // rounds a line
+  constexpr int IR = 8 / NR;      // load registers a round (each 8 rows)
+  const int lane = lane_id(), sub = lane & 7, r8 = lane >> 3;
+  float acc = 0.0f;
+#pragma unroll
+  for (int b = 0; b < (L + LB - 1) / LB; ++b) {
+    // The row index passes through an empty asm so that these loads stay
+    // after the earlier LDS hand-overs (loads hoisted above them would hold
+    // twice the registers).
+    asm volatile("" : "+v"(row));
+    // v[8 p + i]: 16 bytes (sub) of line LB b + p of row 8 i + r8.
+    float4 v[LB * 8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int rv = __shfl(row, 8 * i + r8, kWave);
+      const float4* rp = reinterpret_cast<const float4*>(base + (size_t)rv * D) + 8 * LB * b + sub;
+#pragma unroll
+      for (int p = 0; p < LB; ++p)
+        if (LB * b + p < L) v[8 * p + i] = rp[8 * p];
+    }
+    // Every load of the batch issued before its first exchange: without these
+    // empty uses the compiler places each line's loads just before its
+    // exchange, one memory round trip a line.
+#pragma unroll
+    for (int k = 0; k < LB * 8; ++k)
+      if (LB * b + k / 8 < L) asm volatile("" ::"v"(v[k].x), "v"(v[k].y), "v"(v[k].z), "v"(v[k].w));
+#pragma unroll
+    for (int p = 0; p < LB; ++p) {
+      if (LB * b + p >= L) break;
+      float4 w[8];  // this line of the lane's row
+#pragma unroll
+      for (int h = 0; h < NR; ++h) {
+#pragma unroll
+        for (int i = 0; i < IR; ++i)
+          *reinterpret_cast<float4*>(tr + (8 * i + r8) * kRowTrStride + 4 * sub) = v[8 * p + IR * h + i];
+        wave_lds_order();
+        if (NR == 1 || (lane >> 5) == h) {
+#pragma unroll
+          for (int j = 0; j < 8; ++j)
+            w[j] = *reinterpret_cast<const float4*>(tr + (lane % RX) * kRowTrStride + 4 * j);
+        }
+        wave_lds_order();
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float* qd = qs + 32 * (LB * b + p) + 4 * j;
+        float df = qd[0] - w[j].x;
+        acc = __builtin_fmaf(df, df, acc);
+        df = qd[1] - w[j].y;
+        acc = __builtin_fmaf(df, df, acc);
+        df = qd[2] - w[j].z;
+        acc = __builtin_fmaf(df, df, acc);
+        df = qd[3] - w[j].w;
+        acc = __builtin_fmaf(df, df, acc);
+      }
+      // The line's chain done here: left to the scheduler, the chains sink
+      // below the later lines' hand-overs and every line stays live.
+      asm volatile("" : "+v"(acc));
+    }
+  }
+  return acc;
+}
+
 }  // namespace fgpu

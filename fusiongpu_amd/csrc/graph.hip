@@ -22,7 +22,10 @@
 // One wave per query, 4 queries per workgroup: the itopk list is one entry per
 // lane (with its expanded flag), the bitmap (8 KB) sits in the wave's LDS, and
 // a step's <= 128 candidates are two per lane.  Every sort and merge is a
-// DPP/permlane bitonic network; there is no workgroup barrier.
+// DPP/permlane bitonic network; there is no workgroup barrier.  The kept
+// candidates' rows are read eight lanes a row and handed to their lanes
+// through LDS (wave_rows_l2), so each distance is still one lane's sequential
+// chain.
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -32,6 +35,11 @@ namespace {
 constexpr int kGW = 4;                  // queries (waves) per workgroup
 constexpr int kBitmapWords = 1 << 11;   // 2^16 bits per query
 constexpr int kMaxWidth = 8;
+// Candidate rows change hands 32 rows a round (a 4.6 KB buffer a wave, so 3
+// workgroups fit a CU beside the bitmaps) and load 2 lines a batch: C5
+// measured 2.40 ms against 2.52-2.78 ms for the other choices of 64 / 32 rows
+// and 1, 2 or 4 lines, and 3.61 ms with one lane reading each row.
+constexpr int kGRX = 32, kGLB = 2;
 
 __device__ __forceinline__ uint64_t gmix64(uint64_t z) {
   z += 0x9E3779B97F4A7C15ull;
@@ -41,42 +49,19 @@ __device__ __forceinline__ uint64_t gmix64(uint64_t z) {
 }
 __device__ __forceinline__ uint32_t graph_bit(int id) { return ((uint32_t)id * 2654435761u) >> 16; }
 
-__device__ __forceinline__ void wave_lds_sync() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
-
-template <int D>
-__device__ __forceinline__ float row_l2(const float* __restrict__ qs, const float* __restrict__ row) {
-  const float4* r = reinterpret_cast<const float4*>(row);
-  float acc = 0.0f;
-#pragma unroll 8
-  for (int j = 0; j < D / 4; ++j) {
-    const float4 v = r[j];
-    float df = qs[4 * j] - v.x;
-    acc = __builtin_fmaf(df, df, acc);
-    df = qs[4 * j + 1] - v.y;
-    acc = __builtin_fmaf(df, df, acc);
-    df = qs[4 * j + 2] - v.z;
-    acc = __builtin_fmaf(df, df, acc);
-    df = qs[4 * j + 3] - v.w;
-    acc = __builtin_fmaf(df, df, acc);
-  }
-  return acc;
-}
-
 template <int D>
 __global__ __launch_bounds__(kGW * kWave) void graph_search_kernel(GraphArgs a) {
   __shared__ uint32_t bm_s[kGW][kBitmapWords];
   __shared__ __align__(16) float qs_s[kGW][D];
   __shared__ int par_s[kGW][kMaxWidth];
+  __shared__ __align__(16) float tr_s[kGW][row_tr_floats<kGRX>()];  // each wave's row hand-over buffer
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int qi = blockIdx.x * kGW + wave;
   if (qi >= a.nq) return;  // the whole wave leaves; the kernel has no workgroup barrier
   uint32_t* bm = bm_s[wave];
   float* qs = qs_s[wave];
   int* par = par_s[wave];
+  float* tr = tr_s[wave];
   for (int i = lane; i < kBitmapWords; i += kWave) bm[i] = 0u;
   for (int i = lane; i < D; i += kWave) qs[i] = a.queries[(size_t)qi * D + i];
   wave_lds_sync();
@@ -118,10 +103,20 @@ __global__ __launch_bounds__(kGW * kWave) void graph_search_kernel(GraphArgs a) 
     // mark the kept candidates visited (every bitmap read of this step is done)
     if (i0 != kPadId) { const uint32_t b = graph_bit(i0); atomicOr(&bm[b >> 5], 1u << (b & 31)); }
     if (i1 != kPadId) { const uint32_t b = graph_bit(i1); atomicOr(&bm[b >> 5], 1u << (b & 31)); }
-    // exact distances
+    // exact distances: the kept rows, eight lanes a row, one lane's chain each
     float d0 = FLT_MAX, d1 = FLT_MAX;
-    if (i0 != kPadId) { d0 = row_l2<D>(qs, a.base + (size_t)i0 * D); ++nev; }
-    if (i1 != kPadId) { d1 = row_l2<D>(qs, a.base + (size_t)i1 * D); ++nev; }
+#pragma unroll 1
+    for (int h = 0; h < 2; ++h) {
+      const int ih = h ? i1 : i0;
+      const uint64_t mh = __ballot(ih != kPadId);
+      if (!mh) break;  // the kept ids are sorted: an empty first half means an empty second
+      const int fill = readlane_i(ih, __ffsll((unsigned long long)mh) - 1);  // a kept row for the empty lanes
+      const float t = wave_rows_l2<D, kGRX, kGLB>(a.base, ih != kPadId ? ih : fill, qs, tr);
+      if (ih != kPadId) {
+        ++nev;
+        if (h) d1 = t; else d0 = t;
+      }
+    }
     uint64_t e0 = key_of(d0, i0), e1 = key_of(d1, i1);  // padding ids give the padding key
     wave_sort64_k(e0);
     wave_sort64_k(e1);

@@ -297,7 +297,7 @@ fgpu_status launch_tune_list_stats(const TuneStatsArgs& a, int npairs, hipStream
 // workgroup goes to sink[blockIdx.x] so the loads cannot be dropped.
 fgpu_status launch_stream_read(const void* d, size_t bytes, unsigned long long* sink, int grid, hipStream_t s);
 fgpu_status launch_row_gather(const void* d, int64_t nrows, int row_bytes, const int32_t* idx, int64_t n,
-                              unsigned long long* sink, int grid, hipStream_t s);
+                              int lanes_per_row, unsigned long long* sink, int grid, hipStream_t s);
 
 // ---- build.hip ----------------------------------------------------------------
 fgpu_status launch_probe_counts(const uint32_t* probes, int nq, int nprobe, int nlist, const int32_t* offsets,

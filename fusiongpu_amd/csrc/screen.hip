@@ -498,7 +498,6 @@ template <int D, int M, int ROUND>
 __global__ __launch_bounds__(kSW * kWave) void screen_kernel(ScreenArgs a) {
   constexpr int NC = D / 16;  // main K chunks
   constexpr int HB = M / 2;   // code bytes per lane half
-  constexpr int HD = D / 2;   // dims per lane half
   static_assert(D % 32 == 0 && D <= 128, "screen: dim a multiple of 32, at most 128");
   constexpr int kCbBytes = D * kPQK * 2;
   constexpr int kWaveWords = ROUND == 1 ? 0 : 2 * kCandBuf;  // staged (row, vector position) pairs

@@ -768,7 +768,8 @@ fgpu_status launch_tp(const TwoPhaseArgs& a, int nq, hipStream_t s) {
 // ---------------------------------------------------------------------------
 // Exact rerank.  128 threads per query; thread t evaluates candidate t of a
 // mini-batch (mb <= 128) with the reference's exact distance (sequential
-// fused chain over the dimensions, gpu_global.cu:636).
+// fused chain over the dimensions, gpu_global.cu:636).  The rows are loaded
+// eight lanes a row and handed to their lanes through LDS (wave_rows_l2).
 constexpr int kRT = 2 * kWave;
 
 // SPEC mini-batches a step: the workgroup's SPEC groups of 128 threads
@@ -781,6 +782,7 @@ template <int D, int SPEC>
 __global__ __launch_bounds__(kRT * SPEC) void rerank_kernel(RerankArgs a) {
   constexpr int kT = kRT * SPEC;
   __shared__ float qs[D];
+  __shared__ __align__(16) float trb[2 * SPEC][row_tr_floats()];  // each wave's row hand-over buffer
   __shared__ uint64_t tk[2][256];     // running top-k keys (double-buffered), ascending
   __shared__ uint64_t nk[SPEC][kRT];  // each group's mini-batch, sorted
   __shared__ int s_chg, s_stable, s_fin;
@@ -803,32 +805,17 @@ __global__ __launch_bounds__(kRT * SPEC) void rerank_kernel(RerankArgs a) {
     const int eff = off < rm && off < total ? min(mb, total - off) : 0;
     float d = FLT_MAX;
     int id = kPadId;
-    if (gt < eff) {
-      const int vid = cand[off + gt];
-      if (vid >= 0 && (long long)vid < a.n) {
-        // The whole row is requested before the first multiply-add (the
-        // scheduling barrier keeps the loads together): one memory round
-        // trip a batch instead of one per eight float4.
-        const float4* row = reinterpret_cast<const float4*>(a.base + (size_t)vid * D);
-        float4 rv[D / 4];
-#pragma unroll
-        for (int j = 0; j < D / 4; ++j) rv[j] = row[j];
-        __builtin_amdgcn_sched_barrier(0);
-        float acc = 0.0f;
-#pragma unroll
-        for (int j = 0; j < D / 4; ++j) {
-          const float4 v = rv[j];
-          float df = qs[4 * j] - v.x;
-          acc = __builtin_fmaf(df, df, acc);
-          df = qs[4 * j + 1] - v.y;
-          acc = __builtin_fmaf(df, df, acc);
-          df = qs[4 * j + 2] - v.z;
-          acc = __builtin_fmaf(df, df, acc);
-          df = qs[4 * j + 3] - v.w;
-          acc = __builtin_fmaf(df, df, acc);
+    {
+      const int vid = gt < eff ? cand[off + gt] : -1;
+      const bool ok = vid >= 0 && (long long)vid < a.n;
+      const uint64_t okm = __ballot(ok);
+      if (okm) {  // the wave's rows, all requested before the first multiply-add, eight lanes a row
+        const int fill = readlane_i(vid, __ffsll((unsigned long long)okm) - 1);  // a valid row for the other lanes
+        const float dd = wave_rows_l2<D>(a.base, ok ? vid : fill, qs, trb[tid >> 6]);
+        if (ok) {
+          d = dd;
+          id = vid;
         }
-        d = acc;
-        id = vid;
       }
     }
     // sort each mini-batch: each wave its 64 keys, then a merge by ranks

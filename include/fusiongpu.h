@@ -108,13 +108,18 @@ int fgpu_debug_pq_sample(int64_t n, int sample_size, int32_t* h_rows);
  * 8 TB/s figure.  d_sink: fgpu_stream_read_grid() uint64 values, overwritten. */
 int fgpu_stream_read_grid(void);
 fgpu_status fgpu_stream_read(const void* d_data, size_t bytes, unsigned long long* d_sink, void* stream);
-/* Reads n whole rows d_rows[d_idx[i]] of row_bytes (384 or 512) each, one
- * lane a row with all of its 16-byte loads in flight: the access pattern of
- * the exact rerank and the graph search, to measure the random-row read rate
- * their rooflines are set against.  Ids outside [0, nrows) are clamped.
- * d_sink as for fgpu_stream_read. */
+/* Reads n whole rows d_rows[d_idx[i]] of row_bytes (384 or 512) each, eight
+ * lanes a row (each lane 16 bytes of every 128-byte line), with all of a
+ * lane's loads in flight: the access pattern of the exact rerank and the graph
+ * search, to measure the random-row read rate their rooflines are set against.
+ * Ids outside [0, nrows) are clamped.  d_sink as for fgpu_stream_read. */
 fgpu_status fgpu_row_gather(const void* d_rows, int64_t nrows, int row_bytes, const int32_t* d_idx, int64_t n,
                             unsigned long long* d_sink, void* stream);
+/* The same with lanes_per_row 1 (each lane reads its own whole row, so one
+ * load instruction touches 64 rows) or 8 (fgpu_row_gather).  Over arrays of
+ * a few GB the first form reads far slower; it is kept to measure that. */
+fgpu_status fgpu_row_gather_lanes(const void* d_rows, int64_t nrows, int row_bytes, const int32_t* d_idx, int64_t n,
+                                  int lanes_per_row, unsigned long long* d_sink, void* stream);
 
 /* ---- search: coarse quantizer (A2 + A3) -------------------------------- */
 

@@ -36,18 +36,32 @@ def test_stream_read_reads_every_word():
     assert _fold(sink) == int(np.bitwise_xor.reduce(a))
 
 
+@pytest.mark.parametrize("lanes", [1, 8])
 @pytest.mark.parametrize("dim", [96, 128])
-def test_row_gather_reads_the_indexed_rows(dim):
-    _say(f"row_gather XOR check, {dim * 4}-byte rows")
+def test_row_gather_reads_the_indexed_rows(dim, lanes):
+    _say(f"row_gather XOR check, {dim * 4}-byte rows, {lanes} lanes a row")
     rng = np.random.default_rng(dim)
     rows = rng.integers(0, 2**32, size=(5000, dim), dtype=np.uint32)
-    idx = rng.integers(0, 5000, size=77777).astype(np.int32)
+    idx = rng.integers(0, 5000, size=77777).astype(np.int32)  # not a multiple of the rows a workgroup reads
     d = torch.from_numpy(rows.view(np.float32)).cuda()
     di = torch.from_numpy(idx).cuda()
     sink = torch.zeros(fg.lib.fgpu_stream_read_grid(), dtype=torch.int64, device="cuda")
-    fg._check(fg.lib.fgpu_row_gather(d.data_ptr(), 5000, dim * 4, di.data_ptr(), idx.size, sink.data_ptr(), None))
+    fg._check(fg.lib.fgpu_row_gather_lanes(d.data_ptr(), 5000, dim * 4, di.data_ptr(), idx.size, lanes,
+                                           sink.data_ptr(), None))
     torch.cuda.synchronize()
     per_row = np.bitwise_xor.reduce(rows, axis=1)
     assert _fold(sink) == int(np.bitwise_xor.reduce(per_row[idx]))
-    fg.row_gather(d, di)  # the Python wrapper runs the same call
+    if lanes == 8:  # fgpu_row_gather is the eight-lane form
+        sink.zero_()
+        fg._check(fg.lib.fgpu_row_gather(d.data_ptr(), 5000, dim * 4, di.data_ptr(), idx.size, sink.data_ptr(), None))
+        torch.cuda.synchronize()
+        assert _fold(sink) == int(np.bitwise_xor.reduce(per_row[idx]))
+    fg.row_gather(d, di, lanes_per_row=lanes)  # the Python wrapper runs the same call
     torch.cuda.synchronize()
+
+
+def test_row_gather_rejects_other_lane_counts():
+    d = torch.zeros(16, 96, device="cuda")
+    di = torch.zeros(4, dtype=torch.int32, device="cuda")
+    with pytest.raises(RuntimeError, match="lanes_per_row"):
+        fg.row_gather(d, di, lanes_per_row=4)
