@@ -4,7 +4,7 @@
 //     [-mb mini_batch] [-e epsilon] [--beta b] [-p prune_ratio] [-s streams]
 //     [-k topk] [--p1_lists n] [--limit_k n] [--threshold_coeff c]
 //     [--pq_m M] [--res DIR] [--out ids.ivecs] [--coarse exact|graph]
-//     [--graph_degree 8]
+//     [--graph_degree 8] [--graphs on|off]
 // It loads <res>/ivf_data.bin + global_pq_codebook.bin, keeps the base
 // vectors in HBM for the exact rerank, runs the query batches through S
 // streams round-robin (search_pipeline.cu:168-214, 311-377) and prints the
@@ -26,6 +26,14 @@
 // pinned memory and hands the context back, while the main thread goes on
 // submitting; it blocks only when every context is still in flight.  No call
 // inside a batch synchronises the host.
+//
+// With --graphs on (the default, exact coarse mode) each context captures its
+// full-size batch once into a HIP graph (every copy, kernel and stage event
+// above, on fixed buffers) and replays it for every later batch: one launch
+// call a batch instead of about twenty, so the host keeps up with small
+// batches.  A shorter last batch runs as separate launches.  The graph coarse
+// mode seeds its walk from the batch's first query index, so it always runs
+// as separate launches.
 #include <algorithm>
 #include <chrono>
 #include <condition_variable>
@@ -67,8 +75,10 @@ struct Ctx {
   void* d_ws = nullptr;
   size_t ws_bytes = 0;
   int start = -1, size = 0;
+  hipGraphExec_t exec = nullptr;  // the captured full-size batch (--graphs on)
   bool busy = false;  // submitted and not yet collected
   bool keep = false;  // its results and stage times count (not a warm-up batch)
+  bool staged = false;  // ran as separate launches with stage events (not a graph replay)
 };
 
 // The reference's recall (search_pipeline.cu:531-557): the whole gt row is the
@@ -95,6 +105,7 @@ int main(int argc, char** argv) {
   int batch = 128, top_m = 20, rerank_m = 10000, mb = 128, beta = 2, streams = 2, final_k = 10, p1_lists = 12,
       limit_k = 50, pq_m = 32, graph_degree = 8;
   float eps = 0.1f, prune_ratio = 100.0f, coeff = 1.0f;
+  bool graphs = true;
   for (int i = 1; i < argc; ++i) {
     const std::string a = argv[i];
     auto next = [&]() -> const char* {
@@ -118,6 +129,11 @@ int main(int argc, char** argv) {
     else if (a == "--out") out_path = next();
     else if (a == "--coarse") coarse_mode = next();
     else if (a == "--graph_degree") graph_degree = std::atoi(next());
+    else if (a == "--graphs") {
+      const std::string v = next();
+      if (v != "on" && v != "off") { std::cerr << "--graphs must be on or off\n"; return 1; }
+      graphs = v == "on";
+    }
     else if (!a.empty() && a[0] != '-') {
       if (base_path.empty()) base_path = a;
       else if (query_path.empty()) query_path = a;
@@ -131,6 +147,7 @@ int main(int argc, char** argv) {
   if (batch < 1 || streams < 1) { std::cerr << "batch and streams must be >= 1\n"; return 1; }
   const bool graph_coarse = coarse_mode == "graph";
   if (!graph_coarse && coarse_mode != "exact") { std::cerr << "--coarse must be exact or graph\n"; return 1; }
+  if (graph_coarse) graphs = false;
   const int dim = app::fvecs_dim(base_path);
   int64_t n = 0, nq64 = 0;
   std::vector<float> raw = app::read_fvecs(base_path, dim, n);
@@ -190,6 +207,8 @@ int main(int argc, char** argv) {
   std::vector<int32_t> results((size_t)nq * final_k, -1);
   // H2D, coarse, prune + count, two-phase scan, rerank, D2H (ms summed over batches)
   double t_stage[6] = {0, 0, 0, 0, 0, 0};
+  double t_replay = 0;  // graph replays: H2D to D2H, ms summed
+  int staged_done = 0, replays_done = 0;
   long long cand_total = 0, cand_max = 0;  // candidates before the cut, potential candidates (summed)
   int batches_done = 0;
   bool keep = false;
@@ -216,10 +235,18 @@ int main(int argc, char** argv) {
       hip_ok(hipEventSynchronize(c.ev[6]), "event sync");
       if (c.keep) {
         std::memcpy(results.data() + (size_t)c.start * final_k, c.h_ids, sizeof(int32_t) * c.size * final_k);
-        for (int j = 0; j < 6; ++j) {
+        if (c.staged) {
+          for (int j = 0; j < 6; ++j) {
+            float ms = 0.0f;
+            hip_ok(hipEventElapsedTime(&ms, c.ev[j], c.ev[j + 1]), "elapsed");
+            t_stage[j] += ms;
+          }
+          ++staged_done;
+        } else {
           float ms = 0.0f;
-          hip_ok(hipEventElapsedTime(&ms, c.ev[j], c.ev[j + 1]), "elapsed");
-          t_stage[j] += ms;
+          hip_ok(hipEventElapsedTime(&ms, c.ev[0], c.ev[6]), "elapsed");
+          t_replay += ms;
+          ++replays_done;
         }
         for (int i = 0; i < c.size; ++i) cand_total += c.h_pre[i];
         cand_max += *c.h_total;
@@ -234,6 +261,39 @@ int main(int argc, char** argv) {
       cv_free.notify_all();
     }
   });
+  // One batch's work on its context's stream, stage events included.
+  // One batch's work on its context's stream; with `stages` the stage events
+  // in between (a captured graph holds none: HIP reports no elapsed time for
+  // events recorded by graph nodes).
+  auto enqueue = [&](Ctx& c, int start, int size, bool stages) {
+    auto mark = [&](int j) {
+      if (stages) hip_ok(hipEventRecord(c.ev[j], c.s), "record");
+    };
+    hip_ok(hipMemcpyAsync(c.d_q, c.h_q, sizeof(float) * size * dim, hipMemcpyHostToDevice, c.s), "H2D");
+    mark(1);
+    if (graph_coarse)
+      ok(fgpu_coarse_graph_search(idx, c.d_q, size, start, top_m, d_cgraph, graph_degree, itopk, 4, 200, 1,
+                                  prune_ratio, c.d_probes, c.d_pd, c.s),
+         "graph coarse search");
+    else
+      ok(fgpu_coarse_search(idx, c.d_q, size, top_m, prune_ratio, c.d_probes, c.d_pd, c.d_ws, c.ws_bytes, c.s),
+         "coarse search");
+    mark(2);
+    // the probed lists' sizes: each query's potential candidates and their total (d_off[size])
+    ok(fgpu_probe_counts(idx, c.d_probes, size, top_m, c.d_cnt, c.d_off, c.s), "probe counts");
+    mark(3);
+    ok(fgpu_two_phase_search_precut(idx, c.d_q, size, c.d_probes, top_m, p1_lists, limit_k, coeff, rerank_m, c.d_tid,
+                                    c.d_td, c.d_tcnt, nullptr, nullptr, c.d_pre, c.d_ws, c.ws_bytes, c.s),
+       "two-phase scan");
+    mark(4);
+    ok(fgpu_rerank(c.d_q, size, dim, d_base, n, c.d_tid, c.d_tcnt, rerank_m, final_k, mb, eps, beta, c.d_ids, c.d_d,
+                   nullptr, c.s),
+       "rerank");
+    mark(5);
+    hip_ok(hipMemcpyAsync(c.h_ids, c.d_ids, sizeof(int32_t) * size * final_k, hipMemcpyDeviceToHost, c.s), "D2H");
+    hip_ok(hipMemcpyAsync(c.h_pre, c.d_pre, sizeof(int32_t) * size, hipMemcpyDeviceToHost, c.s), "D2H");
+    hip_ok(hipMemcpyAsync(c.h_total, c.d_off + size, sizeof(int32_t), hipMemcpyDeviceToHost, c.s), "D2H");
+  };
   auto submit = [&](int b, int start, int size) {
     const int slot = b % streams;
     Ctx& c = ctx[slot];
@@ -242,34 +302,25 @@ int main(int argc, char** argv) {
       cv_free.wait(lk, [&] { return !c.busy; });
     }
     std::memcpy(c.h_q, all_q.data() + (size_t)start * dim, sizeof(float) * size * dim);
+    const bool replay = graphs && size == batch;
     hip_ok(hipEventRecord(c.ev[0], c.s), "record");
-    hip_ok(hipMemcpyAsync(c.d_q, c.h_q, sizeof(float) * size * dim, hipMemcpyHostToDevice, c.s), "H2D");
-    hip_ok(hipEventRecord(c.ev[1], c.s), "record");
-    if (graph_coarse)
-      ok(fgpu_coarse_graph_search(idx, c.d_q, size, start, top_m, d_cgraph, graph_degree, itopk, 4, 200, 1,
-                                  prune_ratio, c.d_probes, c.d_pd, c.s),
-         "graph coarse search");
-    else
-      ok(fgpu_coarse_search(idx, c.d_q, size, top_m, prune_ratio, c.d_probes, c.d_pd, c.d_ws, c.ws_bytes, c.s),
-         "coarse search");
-    hip_ok(hipEventRecord(c.ev[2], c.s), "record");
-    // the probed lists' sizes: each query's potential candidates and their total (d_off[size])
-    ok(fgpu_probe_counts(idx, c.d_probes, size, top_m, c.d_cnt, c.d_off, c.s), "probe counts");
-    hip_ok(hipEventRecord(c.ev[3], c.s), "record");
-    ok(fgpu_two_phase_search_precut(idx, c.d_q, size, c.d_probes, top_m, p1_lists, limit_k, coeff, rerank_m, c.d_tid,
-                                    c.d_td, c.d_tcnt, nullptr, nullptr, c.d_pre, c.d_ws, c.ws_bytes, c.s),
-       "two-phase scan");
-    hip_ok(hipEventRecord(c.ev[4], c.s), "record");
-    ok(fgpu_rerank(c.d_q, size, dim, d_base, n, c.d_tid, c.d_tcnt, rerank_m, final_k, mb, eps, beta, c.d_ids, c.d_d,
-                   nullptr, c.s),
-       "rerank");
-    hip_ok(hipEventRecord(c.ev[5], c.s), "record");
-    hip_ok(hipMemcpyAsync(c.h_ids, c.d_ids, sizeof(int32_t) * size * final_k, hipMemcpyDeviceToHost, c.s), "D2H");
-    hip_ok(hipMemcpyAsync(c.h_pre, c.d_pre, sizeof(int32_t) * size, hipMemcpyDeviceToHost, c.s), "D2H");
-    hip_ok(hipMemcpyAsync(c.h_total, c.d_off + size, sizeof(int32_t), hipMemcpyDeviceToHost, c.s), "D2H");
+    if (replay) {
+      if (!c.exec) {
+        hipGraph_t g = nullptr;
+        hip_ok(hipStreamBeginCapture(c.s, hipStreamCaptureModeThreadLocal), "begin capture");
+        enqueue(c, start, size, false);
+        hip_ok(hipStreamEndCapture(c.s, &g), "end capture");
+        hip_ok(hipGraphInstantiate(&c.exec, g, nullptr, nullptr, 0), "instantiate graph");
+        hip_ok(hipGraphDestroy(g), "destroy graph");
+      }
+      hip_ok(hipGraphLaunch(c.exec, c.s), "graph launch");
+    } else {
+      enqueue(c, start, size, true);
+    }
     hip_ok(hipEventRecord(c.ev[6], c.s), "record");
     {
       std::lock_guard<std::mutex> lk(mu);
+      c.staged = !replay;
       c.start = start;
       c.size = size;
       c.keep = keep;
@@ -301,18 +352,33 @@ int main(int argc, char** argv) {
   const double ms = std::chrono::duration<double, std::milli>(t1 - t0).count();
   std::cout << "\nTotal time: " << ms << " ms, QPS: " << nq / (ms / 1000.0) << std::endl;
   std::cout << "\n============= Pipeline Timing Breakdown =============\n" << std::fixed << std::setprecision(3);
-  const double nbd = batches_done ? (double)batches_done : 1.0;
+  // Stage times come from runs of separate launches (--graphs off); a graph
+  // replay is timed as a whole (H2D to D2H), and a run with replays reports
+  // no stage table (its one shorter last batch would not be typical).
+  const bool stages = staged_done > 0 && replays_done == 0;
+  const double nbd = staged_done ? (double)staged_done : 1.0;
   const double avg[6] = {t_stage[0] / nbd, t_stage[1] / nbd, t_stage[2] / nbd,
                          t_stage[3] / nbd, t_stage[4] / nbd, t_stage[5] / nbd};
   const char* names[5] = {"H2D:          ", "Coarse:       ", "Scan (PQ):    ", "Rerank (GPU): ", "D2H:          "};
   const double stage[5] = {avg[0], avg[1], avg[2] + avg[3], avg[4], avg[5]};
+  auto put = [&](double v) {
+    if (stages) std::cout << std::setw(8) << v << " ms";
+    else std::cout << std::setw(8) << "n/a";
+  };
   double sum = 0;
   for (int j = 0; j < 5; ++j) {
     sum += stage[j];
-    std::cout << "  " << names[j] << std::setw(8) << stage[j] << " ms\n";
+    std::cout << "  " << names[j];
+    put(stage[j]);
+    std::cout << "\n";
   }
   std::cout << "  -----------------------------------------\n";
-  std::cout << "  Sum of stages:" << std::setw(8) << sum << " ms\n";
+  std::cout << "  Sum of stages:";
+  put(sum);
+  std::cout << "\n";
+  if (replays_done)
+    std::cout << "  Graph replay: " << std::setw(8) << t_replay / replays_done << " ms a batch, H2D to D2H (" << replays_done
+              << " batches)\n";
   std::cout << "  batch count:  " << batches_done << "\n";
   std::cout << "=====================================================\n";
   // The reference's fine-grained table (search_pipeline.cu:286-306).  Here the
@@ -320,13 +386,17 @@ int main(int argc, char** argv) {
   // counts; steps 1-3 have no work (the LUTs are built on chip, the pool is
   // bounded on the device, no host round trip) and steps 4a-7 are one kernel.
   std::cout << "\n============= GPU Batch Logic Fine-grained Breakdown (Avg/Batch) =============\n";
-  std::cout << "  0. Prune+Count (Fused):     " << std::setw(8) << avg[2] << " ms\n";
-  std::cout << "  1. Scan Offsets (Prefix):   " << std::setw(8) << 0.0 << " ms  (with 0)\n";
+  std::cout << "  0. Prune+Count (Fused):     ";
+  put(avg[2]);
+  std::cout << "\n  1. Scan Offsets (Prefix):   " << std::setw(8) << 0.0 << " ms  (with 0)\n";
   std::cout << "  2. Precompute (Residual):   " << std::setw(8) << 0.0 << " ms  (LUTs built in the scan)\n";
   std::cout << "  3. Resize Check & Sync:     " << std::setw(8) << 0.0 << " ms  (no host round trip)\n";
-  std::cout << "  4-7. Two-phase scan, select, sort (one kernel): " << std::setw(8) << avg[3] << " ms\n";
-  std::cout << "----------------------------------------------------------------\n";
-  std::cout << "  Total GPU Batch Kernel:     " << std::setw(8) << avg[2] + avg[3] << " ms\n";
+  std::cout << "  4-7. Two-phase scan, select, sort (one kernel): ";
+  put(avg[3]);
+  std::cout << "\n----------------------------------------------------------------\n";
+  std::cout << "  Total GPU Batch Kernel:     ";
+  put(avg[2] + avg[3]);
+  std::cout << "\n";
   const long long avg_max = batches_done ? cand_max / batches_done : 0;
   const long long avg_real = batches_done ? cand_total / batches_done : 0;
   std::cout << "  [Allocated] Max Potential Candidates: " << avg_max << "\n";
@@ -357,6 +427,7 @@ int main(int argc, char** argv) {
     std::cout << "Recall@1: " << r1 * 100 << "%, Recall@10: " << r10 * 100 << "%" << std::endl;
   }
   for (auto& c : ctx) {
+    if (c.exec) (void)hipGraphExecDestroy(c.exec);
     (void)hipStreamDestroy(c.s);
     for (auto& e : c.ev) (void)hipEventDestroy(e);
     (void)hipHostFree(c.h_q);

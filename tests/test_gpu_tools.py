@@ -136,6 +136,16 @@ def test_search_pipeline_matches_library_path(tmp_path):
     for k, printed in ((1, float(m.group(1))), (10, float(m.group(2)))):
         hits = sum(len(set(got[i, :k]) & set(gt[i])) for i in range(q.shape[0]))
         assert abs(100.0 * hits / (q.shape[0] * k) - printed) < 1e-3
+    # the full batches replayed HIP graphs (captured by each context's warm-up batch, then replayed for the
+    # timed batches: one context replays twice); the same run as separate launches gives the same ids and
+    # the per-stage table
+    assert re.search(r"Graph replay:\s+[\d.]+ ms a batch, H2D to D2H \(4 batches\)", out), out
+    out2 = _run("search_pipeline", tmp_path / "base.fvecs", tmp_path / "q.fvecs", "-b", 64, "-m", 16, "-r", 500, "-k",
+                10, "--p1_lists", 4, "--limit_k", 30, "-s", 3, "--res", res, "--graphs", "off", "--out",
+                tmp_path / "out2.ivecs", cwd=tmp_path)
+    assert np.array_equal(_read_ivecs(tmp_path / "out2.ivecs"), want)
+    assert "Graph replay" not in out2 and re.search(r"Sum of stages:\s+[\d.]+ ms", out2), out2
+    assert int(re.search(r"\[Actual\]\s+Filtered Real Candidates: (\d+)", out2).group(1)) == areal
 
 
 def test_search_pipeline_graph_coarse_matches_library_path(tmp_path):
