@@ -501,12 +501,14 @@ __global__ __launch_bounds__(kSW * kWave) void screen_kernel(ScreenArgs a) {
   static_assert(D % 32 == 0 && D <= 128, "screen: dim a multiple of 32, at most 128");
   constexpr int kCbBytes = D * kPQK * 2;
   constexpr int kWaveWords = ROUND == 1 ? 0 : 2 * kCandBuf;  // staged (row, vector position) pairs
-  constexpr int kPreOff = kCbBytes + kSW * (kWaveWords + kQB) * 4;
+  constexpr int kRowWords = ROUND == 1 ? kQB : 3 * kQB;        // each row's query (+ round 2: count, first slot)
+  constexpr int kPreOff = kCbBytes + kSW * (kWaveWords + kRowWords) * 4;
   __shared__ __align__(16) unsigned char lds[kPreOff + (kScreenMaxLists + 1 + kSW) * 4];
   uint16_t* cbs = reinterpret_cast<uint16_t*>(lds);
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   uint2* wbuf = reinterpret_cast<uint2*>(lds + kCbBytes + wave * kWaveWords * 4);
-  int* rowq = reinterpret_cast<int*>(lds + kCbBytes + kSW * kWaveWords * 4) + wave * kQB;
+  int* rowq = reinterpret_cast<int*>(lds + kCbBytes + kSW * kWaveWords * 4) + wave * kRowWords;
+  int* rcnt = rowq + kQB;  // round 2: each row's candidates in the staging buffer, then its first slot
   int* pre = reinterpret_cast<int*>(lds + kPreOff);  // [nlist + 1] first item of each list
   int* wsum = pre + kScreenMaxLists + 1;             // [kSW]
   const int li = lane & 31, h = lane >> 5;
@@ -610,10 +612,16 @@ __global__ __launch_bounds__(kSW * kWave) void screen_kernel(ScreenArgs a) {
     uint32_t mins[16];
 #pragma unroll
     for (int r = 0; r < 16; ++r) mins[r] = 0x7F800000u;
-    // ROUND 2 candidates: staged in wbuf as (row, vector position), then
-    // each takes a slot of its query's candidate array with an atomic.
+    // ROUND 2 candidates: staged in wbuf as (row, vector position).  A
+    // flush ranks each entry within its row (LDS atomics), reserves each
+    // row's slots of its query's candidate array with one global atomic a
+    // row, then writes the entries: one global round trip a flush instead of
+    // one atomic a candidate.  The order of a query's candidates is free (the
+    // rescore sorts them).
     int nb = 0;  // staged entries (wave-uniform)
-    auto flush = [&]() {
+    // A full buffer inside a tile (rare): one atomic a candidate, which keeps
+    // the tile loop's registers down.
+    auto flush_full = [&]() {
       wave_sync();
       for (int i0 = 0; i0 < nb; i0 += kWave) {
         const int i = i0 + lane;
@@ -621,6 +629,36 @@ __global__ __launch_bounds__(kSW * kWave) void screen_kernel(ScreenArgs a) {
           const uint2 e = wbuf[i];
           const int q = rowq[e.x];
           const int slot = atomicAdd(&a.cand_cnt[q], 1);
+          if (slot < a.cand_cap) a.cand[(size_t)q * a.cand_cap + slot] = make_uint2((uint32_t)start + e.y, (uint32_t)l);
+        }
+      }
+      nb = 0;
+      wave_sync();
+    };
+    auto flush = [&]() {
+      wave_sync();
+      if (lane < kQB) rcnt[lane] = 0;
+      wave_sync();
+      for (int i0 = 0; i0 < nb; i0 += kWave) {
+        const int i = i0 + lane;
+        if (i < nb) {
+          const uint32_t row = wbuf[i].x;
+          const int rank = atomicAdd(&rcnt[row], 1);
+          wbuf[i].x = row | ((uint32_t)rank << 8);  // row < 32, rank < kCandBuf
+        }
+      }
+      wave_sync();
+      if (lane < kQB) {
+        const int c = rcnt[lane];
+        rcnt[lane] = c > 0 ? atomicAdd(&a.cand_cnt[rowq[lane]], c) : 0;
+      }
+      wave_sync();
+      for (int i0 = 0; i0 < nb; i0 += kWave) {
+        const int i = i0 + lane;
+        if (i < nb) {
+          const uint2 e = wbuf[i];
+          const int row = (int)(e.x & 255u), q = rowq[row];
+          const int slot = rcnt[row] + (int)(e.x >> 8);
           if (slot < a.cand_cap) a.cand[(size_t)q * a.cand_cap + slot] = make_uint2((uint32_t)start + e.y, (uint32_t)l);
         }
       }
@@ -666,7 +704,7 @@ __global__ __launch_bounds__(kSW * kWave) void screen_kernel(ScreenArgs a) {
             const uint64_t bm = __ballot(pass);
             if (bm) {
               const int c = __popcll(bm);
-              if (nb + c > kCandBuf) flush();
+              if (nb + c > kCandBuf) flush_full();
               const int row = 8 * (r >> 2) + 4 * h + (r & 3);
               if (pass) wbuf[nb + lanes_below64(bm)] = make_uint2((uint32_t)row, (uint32_t)j);
               nb += c;
