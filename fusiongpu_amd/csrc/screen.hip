@@ -191,10 +191,10 @@ __global__ __launch_bounds__(256) void screen_zero_kernel(int* __restrict__ p, i
     p[i] = 0;
 }
 
-// Pair entry `ent` (= q nprobe + p) of query q joins list l's bucket (the
-// screen kernels derive their work items from the final counts).
-__device__ __forceinline__ int bucket_add(const ScreenArgs& a, int* cnt, int l, int q, int ent) {
-  const int pos = atomicAdd(&cnt[l], 1);
+// Pair entry `ent` (= q nprobe + p) of query q goes to slot `pos` of list
+// l's bucket, taken earlier with an atomic on the list's count (the screen
+// kernels derive their work items from the final counts).
+__device__ __forceinline__ int bucket_put(const ScreenArgs& a, int l, int q, int ent, int pos) {
   if (pos >= a.nq) {  // a probe list repeating a list id: the query takes the LUT kernel
     a.thr[q] = __builtin_nanf("");
     return -1;
@@ -312,7 +312,7 @@ __global__ __launch_bounds__(256) void screen_pairs1_kernel(ScreenArgs a) {
     const float nr2 = pair_a<D>(a, ent, query_dims(a, q, D), centroid_dims<D>(a, lf));
     if (lane == 0) pair_ex<1>(a, ent, nr2, 0.0f);
     if (nr2 <= kMaxNorm2 && lane == 0) {
-      const int pos = bucket_add(a, a.cnt1, lf, q, (int)ent);
+      const int pos = bucket_put(a, lf, q, (int)ent, atomicAdd(&a.cnt1[lf], 1));
       if (pos >= 0) f = make_int2(lf, pos);
     }
   }
@@ -367,10 +367,12 @@ __global__ __launch_bounds__(256) void screen_pairs2_kernel(ScreenArgs a) {
       pass = l < (uint32_t)a.nlist && a.offsets[l + 1] - a.offsets[l] > 0 &&
              list_lower_bound(a.probe_dists[t], a.rmax[l]) <= T;
     }
-    // Every passing probe joins its list's bucket at once (one atomic a
-    // lane); a pair whose record turns out unusable sends the whole query to
-    // the LUT kernel, whose rescore then ignores its candidates.
-    if (pass) bucket_add(a, a.cnt2, (int)l, q, (int)((int64_t)q * a.nprobe + p));
+    // Every passing probe takes its slot of its list's bucket at once (one
+    // atomic a lane) and writes it after the pair records, so the atomic's
+    // round trip overlaps the centroid loads; a pair whose record turns out
+    // unusable sends the whole query to the LUT kernel, whose rescore then
+    // ignores its candidates.
+    const int pos = pass ? atomicAdd(&a.cnt2[l], 1) : 0;
     // The A fragments, one pair at a time with the next pair's centroid
     // loads in flight; the lane of each probe keeps its pair's nr2, and the
     // extra blocks follow lane-parallel (one lane a pair).
@@ -393,6 +395,7 @@ __global__ __launch_bounds__(256) void screen_pairs2_kernel(ScreenArgs a) {
     if (pass) {
       pair_ex<2>(a, (int64_t)q * a.nprobe + p, my_nr2, T);
       bad = bad || !(my_nr2 <= kMaxNorm2);
+      bucket_put(a, (int)l, q, (int)((int64_t)q * a.nprobe + p), pos);
     }
   }
   if (__ballot(bad) && lane == 0) a.thr[q] = INFINITY;
