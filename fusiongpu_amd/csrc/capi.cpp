@@ -547,7 +547,7 @@ fgpu_status fgpu_search(const fgpu_index* ix, const float* dq, int nq, int nprob
   void* rest = cv.base + cv.used;
   const size_t rest_bytes = ws_bytes - cv.used;
   // The MFMA screen + exact rescore (screen.hip), when the index has its
-  // arrays, k <= 32 and the workspace holds its buffers; the queries it hands
+  // arrays, k <= 64 and the workspace holds its buffers; the queries it hands
   // back go through the generic LUT kernel.  Otherwise the LUT flow kernel.
   // With FGPU_OPT_STAGE_EVENTS, events between the stages (fgpu_search_stage_times).
   hipStream_t s = as_stream(stream);
@@ -555,7 +555,7 @@ fgpu_status fgpu_search(const fgpu_index* ix, const float* dq, int nq, int nprob
   auto mark = [&](int i) { return ev ? hipEventRecord(ev[i], s) : hipSuccess; };
   FGPU_HIP(mark(0));
   ScreenWs sw;
-  if (ix->screen_ok && ix->opt_screen && k <= 32 && nq > 0 && ((uintptr_t)dq & 15) == 0 &&
+  if (ix->screen_ok && ix->opt_screen && k <= 64 && nq > 0 && ((uintptr_t)dq & 15) == 0 &&
       ix->nlist <= kScreenMaxLists && (int64_t)nq * nprobe < INT32_MAX &&
       sw.carve(rest, rest_bytes, nq, ix->nlist, nprobe)) {
     FGPU_TRY(coarse_search(ix, dq, nq, nprobe, prune_ratio, pid, pd, rest, rest_bytes, stream, nullptr, 0));

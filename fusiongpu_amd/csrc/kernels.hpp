@@ -151,7 +151,7 @@ struct ScreenArgs {
   int* bucket;              // [nlist][nq] pair entries (q nprobe + p) of each list
   uint4* arec;              // [nq nprobe][2][9] pair records: per lane half 8 A fragments and the extra block
   int2* first;              // [nq] round 1: (list, bucket position) of the query's pair, or (-1, -1)
-  uint32_t* gminbuf;        // [nq][kMaxChunks][32] round 1: per query, first-list chunk and group, min U bits
+  uint32_t* gminbuf;        // [nq][kMaxChunks][64] round 1: per query, first-list chunk and group, min U bits
   float* thr;               // [nq] T(q)
   uint2* cand;              // [nq][cand_cap] (vector position, list)
   int cand_cap;

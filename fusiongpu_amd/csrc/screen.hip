@@ -80,6 +80,10 @@ constexpr int kSW = 16;                  // waves per screen workgroup
 constexpr int kCandBuf = 256;            // per-wave candidate staging entries (LDS)
 constexpr int kChunk = 256;              // list vectors per work item (at most kMaxChunks items a group)
 constexpr int kMaxChunks = 8;
+constexpr int kMaxGroups = 64;           // round-1 groups a query's first list splits into, at most
+// Groups of round 1: the k-th smallest group minimum bounds the k-th smallest
+// U from above only when k <= groups.
+__host__ __device__ constexpr int screen_groups(int k) { return k > 32 ? 64 : 32; }
 
 constexpr uint32_t kOneOne = 0x3F803F80u;  // two bf16 1.0
 constexpr int kRecHalf = 9;              // uint4 per lane half of a pair record: 8 A fragments, the extra block
@@ -344,11 +348,11 @@ __global__ __launch_bounds__(256) void screen_pairs2_kernel(ScreenArgs a) {
   const float2 qv = query_dims(a, q, D);
   const int2 f = a.first[q];
   uint32_t gm = 0x7F800000u;
-  if (f.x >= 0 && lane < 32) {
+  if (f.x >= 0 && lane < screen_groups(a.k)) {
     const int n = a.offsets[f.x + 1] - a.offsets[f.x];
     const int per = chunk_len(n), nch = (n + per - 1) / per;
-    const uint32_t* g = a.gminbuf + (size_t)q * kMaxChunks * 32 + lane;
-    for (int c = 0; c < nch; ++c) gm = min(gm, g[c * 32]);
+    const uint32_t* g = a.gminbuf + (size_t)q * kMaxChunks * kMaxGroups + lane;
+    for (int c = 0; c < nch; ++c) gm = min(gm, g[c * kMaxGroups]);
   }
   // U >= 0, so float order is unsigned order of the bits
   wave_sort_u32(gm);
@@ -497,8 +501,9 @@ __device__ __forceinline__ uint32_t kth_of_32(uint32_t (&v)[32], int k) {
 // candidates (V <= 0) to their queries' arrays.
 // LDS: the bf16 codebook first (offset 0, so every gather's subspace offset is
 // the instruction's immediate), then per-wave staging.
-template <int D, int M, int ROUND>
+template <int D, int M, int ROUND, int G = 32>
 __global__ __launch_bounds__(kSW * kWave) void screen_kernel(ScreenArgs a) {
+  static_assert(G == 32 || G == 64, "round-1 groups: 32 or 64");
   constexpr int NC = D / 16;  // main K chunks
   constexpr int HB = M / 2;   // code bytes per lane half
   static_assert(D % 32 == 0 && D <= 128, "screen: dim a multiple of 32, at most 128");
@@ -612,9 +617,11 @@ __global__ __launch_bounds__(kSW * kWave) void screen_kernel(ScreenArgs a) {
 
     // Per row and lane column, the smallest U bits seen (ROUND 1; every U is
     // >= 0, where float order is unsigned order).
-    uint32_t mins[16];
+    uint32_t mins[G / 32][16];
 #pragma unroll
-    for (int r = 0; r < 16; ++r) mins[r] = 0x7F800000u;
+    for (int gp = 0; gp < G / 32; ++gp)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) mins[gp][r] = 0x7F800000u;
     // ROUND 2 candidates: staged in wbuf as (row, vector position).  A
     // flush ranks each entry within its row (LDS atomics), reserves each
     // row's slots of its query's candidate array with one global atomic a
@@ -678,7 +685,9 @@ __global__ __launch_bounds__(kSW * kWave) void screen_kernel(ScreenArgs a) {
     // then the reload of the same buffer two tiles ahead (two buffers
     // alternate, so a tile never waits for the loads of the next one), then
     // the tile's results.
-    auto tile = [&](int j0, uint32_t (&cw)[M / 8], uint4& bx) {
+    // par: the tile's position within the chunk, mod 2 (its column group
+    // half when G = 64)
+    auto tile = [&](int j0, uint32_t (&cw)[M / 8], uint4& bx, int par) {
       f32x16 acc;
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
@@ -692,8 +701,13 @@ __global__ __launch_bounds__(kSW * kWave) void screen_kernel(ScreenArgs a) {
       load_tile(j0 + 2 * kTV, cw, bx);
       // acc[r]: row 8 (r / 4) + 4 h + r % 4 of the work item, column li (vector j0 + li).
       if constexpr (ROUND == 1) {
+        if (G == 64 && par) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) mins[r] = min(mins[r], __float_as_uint(acc[r]));
+          for (int r = 0; r < 16; ++r) mins[G / 32 - 1][r] = min(mins[G / 32 - 1][r], __float_as_uint(acc[r]));
+        } else {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) mins[0][r] = min(mins[0][r], __float_as_uint(acc[r]));
+        }
       } else {
         // V <= 0: the bits as a signed int are <= 0 (+0, or the sign set).
         int mn = __float_as_int(acc[0]);
@@ -717,8 +731,8 @@ __global__ __launch_bounds__(kSW * kWave) void screen_kernel(ScreenArgs a) {
       }
     };
     for (int j0 = jb; j0 < je; j0 += 2 * kTV) {
-      tile(j0, cwA, bxA);
-      if (j0 + kTV < je) tile(j0 + kTV, cwB, bxB);
+      tile(j0, cwA, bxA, 0);
+      if (j0 + kTV < je) tile(j0 + kTV, cwB, bxB, 1);
     }
 
     if (a.stats) {
@@ -729,18 +743,22 @@ __global__ __launch_bounds__(kSW * kWave) void screen_kernel(ScreenArgs a) {
     if constexpr (ROUND == 2) {
       if (nb > 0) flush();
     } else {
-      // Groups are vector positions mod 32 (= the lane column): this item's
-      // per-row, per-group minima go to the row's query, at the item's chunk
-      // (each (query, chunk) slot has exactly one writer); the pair kernel
-      // of round 2 combines the chunks of a query's list.
+      // Groups are vector positions within the chunk mod G (the lane column,
+      // plus 32 for odd tiles when G = 64): this item's per-row, per-group
+      // minima go to the row's query, at the item's chunk (each (query,
+      // chunk) slot has exactly one writer); the pair kernel of round 2
+      // combines the chunks of a query's list, group by group, which is again
+      // a partition of the list.
       wave_sync();
       const int cidx = local % nch;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int row = 8 * (r >> 2) + 4 * h + (r & 3);
-        const int q = rowq[row];
-        if (q >= 0) a.gminbuf[((size_t)q * kMaxChunks + cidx) * 32 + li] = mins[r];
-      }
+      for (int gp = 0; gp < G / 32; ++gp)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int row = 8 * (r >> 2) + 4 * h + (r & 3);
+          const int q = rowq[row];
+          if (q >= 0) a.gminbuf[((size_t)q * kMaxChunks + cidx) * kMaxGroups + 32 * gp + li] = mins[gp][r];
+        }
     }
     wave_sync();
     if (a.stats) {
@@ -870,7 +888,10 @@ fgpu_status launch_screen_dm(const ScreenArgs& a, hipStream_t s) {
   auto mark = [&](int i) { return a.events ? hipEventRecord(a.events[i], s) : hipSuccess; };
   hipLaunchKernelGGL(screen_pairs1_kernel<D>, dim3((unsigned)((a.nq + 3) / 4)), dim3(256), 0, s, a);
   FGPU_HIP(mark(0));
-  hipLaunchKernelGGL((screen_kernel<D, M, 1>), dim3((unsigned)cus), dim3(kSW * kWave), 0, s, a);
+  if (screen_groups(a.k) == 64)
+    hipLaunchKernelGGL((screen_kernel<D, M, 1, 64>), dim3((unsigned)cus), dim3(kSW * kWave), 0, s, a);
+  else
+    hipLaunchKernelGGL((screen_kernel<D, M, 1>), dim3((unsigned)cus), dim3(kSW * kWave), 0, s, a);
   FGPU_HIP(mark(1));
   hipLaunchKernelGGL(screen_pairs2_kernel<D>, dim3((unsigned)((a.nq + 3) / 4)), dim3(256), 0, s, a);
   FGPU_HIP(mark(2));
@@ -885,8 +906,8 @@ fgpu_status launch_screen_dm(const ScreenArgs& a, hipStream_t s) {
 }  // namespace
 
 int64_t screen_gmin_words(int nq) {
-  // Round 1: per query, per chunk of its first list, 32 group minima.
-  return (int64_t)nq * kMaxChunks * 32;
+  // Round 1: per query, per chunk of its first list, up to 64 group minima.
+  return (int64_t)nq * kMaxChunks * kMaxGroups;
 }
 
 bool screen_supported(int dim, int m) {
@@ -907,7 +928,7 @@ fgpu_status launch_screen_prep(const float* codebook, int m, int sub, const uint
 }
 
 fgpu_status launch_screen(int dim, int m, const ScreenArgs& a, hipStream_t s) {
-  FGPU_CHECK(a.k >= 1 && a.k <= 32, FGPU_ERR_UNSUPPORTED, "screen: k must be in [1, 32]");
+  FGPU_CHECK(a.k >= 1 && a.k <= 64, FGPU_ERR_UNSUPPORTED, "screen: k must be in [1, 64]");
   if (a.nq <= 0) return FGPU_OK;
   if (dim == 128 && m == 32) return launch_screen_dm<128, 32>(a, s);
   if (dim == 128 && m == 16) return launch_screen_dm<128, 16>(a, s);

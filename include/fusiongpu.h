@@ -184,7 +184,7 @@ fgpu_status fgpu_adc_search_stats(const fgpu_index* idx, const float* d_queries,
                                   void* stream);
 
 /* coarse + ADC in one call: the same results as fgpu_coarse_search followed
- * by fgpu_adc_search.  For k <= 32 on the geometries (dim, pq_m) = (128, 16),
+ * by fgpu_adc_search.  For k <= 64 on the geometries (dim, pq_m) = (128, 16),
  * (128, 32), (128, 64), (96, 48) the scan part runs as an MFMA screen with an
  * exact rescore (no per-(query, list) LUT): every query's first list gives an
  * upper bound T on its k-th distance, every probed vector whose rigorous lower

@@ -3,10 +3,10 @@ pick candidates, which are rescored with the reference's exact LUT arithmetic
 (gpu_global.cu:115-158 for the entries, :196-253 for the ascending-m sum).
 Bar: ids and fp32 distance bits equal to the oracle's exhaustive scan of the
 probed lists, and equal to the same index's LUT kernels (OPT_SCREEN 0), for
-every geometry the screen has, k from 1 to 32, and every hand-off to the LUT
-kernel: no threshold (the first usable list holds fewer than k vectors), too
-many candidates, norms beyond the bounds' range, a misaligned query array,
-k above 32.
+every geometry the screen has, k from 1 to 64 (64 round-1 groups above 32),
+and every hand-off to the LUT kernel: no threshold (the first usable list
+holds fewer than k vectors, or fewer than k of its groups hold a vector), too
+many candidates, norms beyond the bounds' range, a misaligned query array.
 The screen's counters show which path each case took."""
 import sys
 
@@ -68,7 +68,7 @@ def _check(idx, q, cent, cb, offs, ids, codes, nprobe, k, prune_ratio=100.0, dq=
 
 
 @pytest.mark.parametrize("dim,m,k", [(128, 32, 10), (128, 16, 32), (128, 64, 5), (96, 48, 1), (128, 32, 32),
-                                     (96, 48, 17)])
+                                     (96, 48, 17), (128, 32, 50), (96, 48, 64), (128, 16, 33)])
 def test_screen_geometries_bit_exact(dim, m, k):
     _say(f"screen dim={dim} m={m} k={k}")
     offs, ids, codes, cent, cb = _gmm_index(dim, m, 64, 24000, seed=dim + m + k)
@@ -76,12 +76,17 @@ def test_screen_geometries_bit_exact(dim, m, k):
     assert idx.screen_ready
     q = fg.gen_gmm(333, dim, 32, seed=dim + m + k, set=1, sig_lo=0.08)
     st = _check(idx, q, cent, cb, offs, ids, codes, 12, k)
-    # the screen ran: every query got a threshold from its first list; queries
-    # past 512 candidates (a few, at 16 subspaces and k 32) went to the LUT kernel
-    assert st["pairs_round1"] == 333 and st["queries_with_threshold"] == 333
-    assert st["candidates"] >= 333 * k
-    assert (st["queries_to_lut_kernel"] > 0) == (st["max_candidates"] > 512)
-    assert st["queries_to_lut_kernel"] <= 333 // 10
+    # the screen ran: every query whose first list holds k vectors got a
+    # threshold from it; queries past 512 candidates (a few, at 16 subspaces
+    # and k 32) went to the LUT kernel
+    lens = np.diff(offs)
+    probes, _ = oracle.coarse(q, cent, 12)
+    first = np.array([next((lens[l] for l in row if l < 64 and lens[l] > 0), 0) for row in probes])
+    assert st["queries_with_threshold"] == int((first >= k).sum()) >= 333 * 9 // 10
+    assert st["candidates"] >= st["queries_with_threshold"] * k
+    assert (st["queries_to_lut_kernel"] > int((first < k).sum())) == (st["max_candidates"] > 512)
+    # (at k 64, 12 probes of 375-vector lists often pass 512 candidates)
+    assert st["queries_to_lut_kernel"] <= 333 // (10 if k <= 32 else 3)
     idx.close()
 
 
@@ -215,10 +220,14 @@ def test_screen_misaligned_queries_take_the_lut_kernel():
     idx.close()
 
 
-def test_screen_k_above_32_takes_the_lut_kernel():
-    _say("screen k 33")
+@pytest.mark.parametrize("k", [33, 48, 64])
+def test_screen_k_above_32_uses_64_groups(k):
+    """k in (32, 64]: round 1 keeps 64 group minima a row; every query still gets a threshold from its first
+    list (lists of about 250 vectors, so all 64 groups hold one)."""
+    _say(f"screen k {k}")
     offs, ids, codes, cent, cb = _gmm_index(128, 32, 32, 8000, seed=17)
     idx = fg.Index.from_arrays(128, 32, offs, ids, codes, cent, cb)
     q = fg.gen_gmm(90, 128, 32, seed=17, set=1, sig_lo=0.08)
-    _check(idx, q, cent, cb, offs, ids, codes, 8, 33, screened=False)
+    st = _check(idx, q, cent, cb, offs, ids, codes, 8, k)
+    assert st["queries_with_threshold"] == 90 and st["pairs_round1"] == 90
     idx.close()
