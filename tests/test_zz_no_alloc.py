@@ -25,7 +25,7 @@ def test_noalloc_limits_on_the_host():
     assert rows % 64 == 0 and rows >= 64
     assert fg.lib.fgpu_search_workspace_bytes(rows, 4096, 32) <= 32 << 20
     assert fg.lib.fgpu_search_workspace_bytes(rows + 64, 4096, 32) > 32 << 20
-    assert fg.lib.fgpu_search_noalloc_max_rows(1024, 32) >= 1728   # C2 runs in six chunks
+    assert fg.lib.fgpu_search_noalloc_max_rows(1024, 32) >= 1664   # C2 runs in seven chunks
     assert fg.lib.fgpu_search_noalloc_max_rows(200000, 32) == 0     # beyond the array: rejected
 
 
