@@ -601,7 +601,7 @@ class Index:
             tid = torch.empty((nq, rerank_m), dtype=torch.int32, device="cuda")
             td = torch.empty((nq, rerank_m), dtype=torch.float32, device="cuda")
             tc = torch.empty(nq, dtype=torch.int32, device="cuda")
-            st = torch.zeros(12, dtype=torch.int64, device="cuda")
+            st = torch.zeros(16, dtype=torch.int64, device="cuda")
             _check(lib.fgpu_two_phase_search_stats(self._h, _dev_ptr(q), nq, _dev_ptr(p), nprobe, p1_lists, limit_k,
                                                    threshold_coeff, rerank_m, _dev_ptr(tid), _dev_ptr(td),
                                                    _dev_ptr(tc), _dev_ptr(st), _dev_ptr(ws), _ws_check(ws),
@@ -609,7 +609,9 @@ class Index:
             v = st.cpu().tolist()
         return tid, td, tc, {"vectors_loaded": v[0], "luts_built": v[1], "lists_skipped": v[2],
                              "phase2_appended": v[3], "clk_setup": v[4], "clk_phase1": v[5], "clk_phase2": v[6],
-                             "clk_final": v[7], "clk_p1_build": v[8], "clk_p1_scan": v[9], "clk_p1_merge": v[10]}
+                             "clk_final": v[7], "clk_p1_build": v[8], "clk_p1_scan": v[9], "clk_p1_merge": v[10],
+                             "screen_virtual_queries": v[11], "screen_candidates": v[12], "screen_to_lut": v[13],
+                             "screen_no_threshold": v[14], "screen_over_cap": v[15]}
 
     def search_rerank_workspace_bytes(self, nq: int, nprobe: int, p1_lists: int, limit_k: int, rerank_m: int) -> int:
         return lib.fgpu_search_rerank_workspace_bytes(nq, self.nlist, nprobe, p1_lists, limit_k, rerank_m)

@@ -2,6 +2,7 @@
 // search and build orchestration, file formats and the synthetic generator.
 #include <algorithm>
 #include <atomic>
+#include <cfloat>
 #include <cmath>
 #include <cstdio>
 #include <cstring>
@@ -173,10 +174,13 @@ struct ScreenWs {
   static size_t zero_words(int nq, int nlist) { return (size_t)kCtrCount + 2 * (size_t)nlist + (size_t)nq; }
   static size_t gmin_words(int nq) { return (size_t)screen_gmin_words(nq); }
   static size_t rec_count(int nq, int nprobe) { return (size_t)nq * nprobe * 18; }
-  bool carve(void* base, size_t bytes, int nq, int nlist, int nprobe) {
+  // Bucket entries: [nlist][nq], or with compact buckets (one probe a query,
+  // ScreenArgs::boff) one a query.
+  static size_t bucket_words(int nq, int nlist, bool compact) { return compact ? (size_t)nq : (size_t)nlist * nq; }
+  bool carve(void* base, size_t bytes, int nq, int nlist, int nprobe, bool compact = false) {
     Carve cv(base, bytes);
     zero = cv.take<int>(zero_words(nq, nlist));
-    bucket = cv.take<int>((size_t)nlist * nq);
+    bucket = cv.take<int>(bucket_words(nq, nlist, compact));
     arec = cv.take<uint4>(rec_count(nq, nprobe));
     thr = cv.take<float>((size_t)nq);
     cand = cv.take<uint2>((size_t)nq * kScreenCandCap);
@@ -185,12 +189,45 @@ struct ScreenWs {
     gminbuf = cv.take<uint32_t>(gmin_words(nq));
     return cv.ok();
   }
-  static size_t bytes(int nq, int nlist, int nprobe) {
-    return carve_bytes<int>(zero_words(nq, nlist)) + carve_bytes<int>((size_t)nlist * nq) +
+  static size_t bytes(int nq, int nlist, int nprobe, bool compact = false) {
+    return carve_bytes<int>(zero_words(nq, nlist)) + carve_bytes<int>(bucket_words(nq, nlist, compact)) +
            carve_bytes<uint4>(rec_count(nq, nprobe)) +
            carve_bytes<float>((size_t)nq) + carve_bytes<uint2>((size_t)nq * kScreenCandCap) +
            carve_bytes<int>((size_t)nq) + carve_bytes<int2>((size_t)nq) +
            carve_bytes<uint32_t>(gmin_words(nq));
+  }
+};
+
+// Phase 1 of fgpu_two_phase_search through the screen: the buffers of one
+// chunk of nvq virtual queries (one per (query, phase-1 probe)): their query
+// rows, probes and (zero) probe distances, their top-limit_k results, the
+// per-list counts and compact bucket offsets, and the screen's workspace.
+constexpr int kTpVqMax = 65536;  // virtual queries a chunk
+struct TpScreenWs {
+  float* vq = nullptr;
+  uint32_t* vprobe = nullptr;
+  float* vpd = nullptr;
+  int32_t* vids = nullptr;
+  float* vd = nullptr;
+  int* hist = nullptr;
+  int32_t* boff = nullptr;
+  ScreenWs sw;
+  bool carve(void* base, size_t bytes, int nvq, int nlist, int dim, int k) {
+    Carve cv(base, bytes);
+    vq = cv.take<float>((size_t)nvq * dim);
+    vprobe = cv.take<uint32_t>((size_t)nvq);
+    vpd = cv.take<float>((size_t)nvq);
+    vids = cv.take<int32_t>((size_t)nvq * k);
+    vd = cv.take<float>((size_t)nvq * k);
+    hist = cv.take<int>((size_t)nlist);
+    boff = cv.take<int32_t>((size_t)nlist + 1);
+    return cv.ok() && sw.carve(cv.base + cv.used, bytes - cv.used, nvq, nlist, 1, true);
+  }
+  static size_t bytes(int nvq, int nlist, int dim, int k) {
+    return carve_bytes<float>((size_t)nvq * dim) + carve_bytes<uint32_t>((size_t)nvq) +
+           carve_bytes<float>((size_t)nvq) + carve_bytes<int32_t>((size_t)nvq * k) +
+           carve_bytes<float>((size_t)nvq * k) + carve_bytes<int>((size_t)nlist) +
+           carve_bytes<int32_t>((size_t)nlist + 1) + ScreenWs::bytes(nvq, nlist, 1, true);
   }
 };
 
@@ -638,7 +675,7 @@ fgpu_status fgpu_search_screen_stats(const fgpu_index* ix, int nq, int nprobe, c
     const int c = z[kCtrCount + 2 * ix->nlist + q];
     st[3] += std::min(c, kScreenCandCap);
     st[4] = std::max<long long>(st[4], c);
-    st[6] += std::isfinite(thr[q]) ? 1 : 0;
+    st[6] += thr[q] < FLT_MAX ? 1 : 0;  // FLT_MAX: candidates set without a screen
   }
   st[5] = z[kCtrFlag];
   for (int i = 0; i < n_stats && i < 8; ++i) h_stats[i] = st[i];
@@ -688,9 +725,14 @@ int fgpu_index_screen_ready(const fgpu_index* ix) { return ix && ix->screen_ok ?
 size_t fgpu_two_phase_workspace_bytes(int nq, int nprobe, int p1_lists, int limit_k, int rerank_m) {
   const int p1 = std::max(0, std::min(nprobe, p1_lists));
   const size_t rows = (size_t)std::max(nq, 1);
-  // Each query's candidate pool, then its phase-1 cutoffs (split phase 1).
-  return carve_bytes<uint64_t>(rows * two_phase_pool_cap(p1, limit_k, rerank_m)) +
-         carve_bytes<float>(rows * (size_t)std::max(nprobe, 1));
+  // Each query's candidate pool, then its phase-1 cutoffs (split phase 1),
+  // then (limit_k <= 64) the buffers of phase 1 through the screen for up to
+  // kTpVqMax virtual queries, sized for the largest lists count and dim.
+  size_t b = carve_bytes<uint64_t>(rows * two_phase_pool_cap(p1, limit_k, rerank_m)) +
+             carve_bytes<float>(rows * (size_t)std::max(nprobe, 1));
+  if (limit_k >= 1 && limit_k <= 64 && p1 >= 1)
+    b += TpScreenWs::bytes((int)std::min<int64_t>((int64_t)rows * p1, kTpVqMax), kScreenMaxLists, 128, limit_k) + 1024;
+  return b;
 }
 
 }  // extern "C"
@@ -709,6 +751,83 @@ fgpu_status two_phase(const fgpu_index* ix, const float* dq, int nq, const uint3
   if (nq == 0) return FGPU_OK;
   const int p1 = std::max(0, std::min(nprobe, p1_lists));
   const int cap = two_phase_pool_cap(p1, limit_k, rerank_m);
+  hipStream_t s = as_stream(stream);
+  // Phase 1 through the MFMA screen (limit_k <= 64, an index with the
+  // screen's arrays, queries 16-byte aligned): every (query, phase-1 probe)
+  // is a virtual query of one probe whose exact top-limit_k the screen
+  // returns (its LUT kernel takes the virtual queries it cannot settle); they
+  // fill the pool slots and cutoffs a split phase 1 leaves, and the
+  // two-phase kernel's second half runs the threshold, phase 2 and the final
+  // select.  The virtual queries' buffers take the end of the workspace; the
+  // pools and cutoff rows the rest.
+  if (ix->screen_ok && ix->opt_screen && limit_k <= 64 && p1 >= 1 && screen_supported(ix->dim, ix->m) &&
+      ix->nlist <= kScreenMaxLists && ((uintptr_t)dq & 15) == 0) {
+    const int qv = std::max(1, kTpVqMax / p1);  // queries a virtual-query chunk
+    const int nvq_max = (int)std::min<int64_t>((int64_t)nq, qv) * p1;
+    const size_t tbytes = TpScreenWs::bytes(nvq_max, ix->nlist, ix->dim, limit_k);
+    const size_t per_q = (size_t)cap * sizeof(uint64_t) + nprobe * sizeof(float);
+    if (ws_bytes > tbytes + 2 * 256 + per_q) {
+      const size_t tofs = align_up(ws_bytes - tbytes, 256) - 256;  // 256-aligned, inside the workspace
+      char* tbase = static_cast<char*>(ws) + tofs;
+      auto need = [&](int64_t c) {
+        return carve_bytes<uint64_t>((size_t)c * cap) + carve_bytes<float>((size_t)c * nprobe);
+      };
+      int64_t chunk = std::min<int64_t>(nq, (int64_t)(tofs / per_q));
+      while (chunk > 0 && need(chunk) > tofs) --chunk;
+      if (chunk >= 1) {
+        float* cut_ws = reinterpret_cast<float*>(static_cast<char*>(ws) + carve_bytes<uint64_t>((size_t)chunk * cap));
+        uint64_t* pool = reinterpret_cast<uint64_t*>(ws);
+        for (int64_t q0 = 0; q0 < nq; q0 += chunk) {
+          const int nb = (int)std::min<int64_t>(chunk, nq - q0);
+          const float* qq = dq + q0 * ix->dim;
+          const uint32_t* pp = d_probe_ids + q0 * nprobe;
+          for (int s0 = 0; s0 < nb; s0 += qv) {
+            const int ns = std::min(qv, nb - s0), nvq = ns * p1;
+            TpScreenWs tw;
+            FGPU_CHECK(tw.carve(tbase, ws_bytes - tofs, nvq, ix->nlist, ix->dim, limit_k), FGPU_ERR_WORKSPACE,
+                       "two_phase_search: screen buffers do not fit");
+            FGPU_TRY(launch_tp_virtual(qq + (int64_t)s0 * ix->dim, ix->dim, pp + (int64_t)s0 * nprobe, nprobe, p1, ns,
+                                       ix->d_offsets, ix->nlist, tw.vq, tw.vprobe, tw.vpd, tw.hist, s));
+            FGPU_TRY(launch_tp_offsets(tw.hist, ix->nlist, tw.boff, s));
+            ScreenArgs sa{tw.vq, ix->d_centroids, ix->d_offsets, ix->d_codes, ix->d_ids, ix->d_codebook, ix->d_cb16,
+                          ix->d_vext, ix->d_rmax, tw.vprobe, tw.vpd, nvq, 1, limit_k, ix->nlist};
+            sa.ctr = tw.sw.zero;
+            sa.cnt1 = tw.sw.zero + kCtrCount;
+            sa.cnt2 = sa.cnt1 + ix->nlist;
+            sa.cand_cnt = sa.cnt2 + ix->nlist;
+            sa.first = tw.sw.first;
+            sa.gminbuf = tw.sw.gminbuf;
+            sa.bucket = tw.sw.bucket;
+            sa.boff = tw.boff;
+            sa.arec = tw.sw.arec;
+            sa.thr = tw.sw.thr;
+            sa.cand = tw.sw.cand;
+            sa.cand_cap = kScreenCandCap;
+            sa.flist = tw.sw.flist;
+            sa.out_ids = tw.vids;
+            sa.out_d = tw.vd;
+            FGPU_TRY(launch_screen(ix->dim, ix->m, sa, s));
+            AdcArgs la = adc_args(ix, tw.vq, nvq, tw.vprobe, tw.vpd, 1, limit_k, tw.vids, tw.vd);
+            la.qlist = tw.sw.flist;
+            la.qcount = tw.sw.zero + kCtrFlag;
+            FGPU_TRY(launch_adc_plain_list(ix->dim, ix->m, la, s));
+            FGPU_TRY(launch_tp_stats(sa.cand_cnt, sa.thr, nvq, kScreenCandCap, tw.sw.zero + kCtrFlag, d_stats, s));
+            FGPU_TRY(launch_tp_collect(pp + (int64_t)s0 * nprobe, nprobe, p1, ns, ix->d_offsets, ix->nlist, limit_k,
+                                       tw.vids, tw.vd, pool + (size_t)s0 * cap, cap, cut_ws + (size_t)s0 * nprobe, s));
+          }
+          TwoPhaseArgs a{qq, ix->d_centroids, ix->d_codebook, ix->d_offsets, ix->d_codes, ix->d_ids, pp, ix->d_rmax,
+                         nb, nprobe, ix->nlist, p1, limit_k, threshold_coeff, rerank_m, pool, cap,
+                         d_top_ids + q0 * rerank_m, d_top_dists + q0 * rerank_m, d_top_counts + q0,
+                         d_list_cutoffs ? d_list_cutoffs + q0 * p1 : nullptr,
+                         d_thresholds ? d_thresholds + q0 : nullptr, d_stats};
+          a.cut_ws = cut_ws;
+          a.pre_cut = d_pre_cut ? d_pre_cut + q0 : nullptr;
+          FGPU_TRY(launch_two_phase_after_phase1(ix->dim, ix->m, a, s));
+        }
+        return FGPU_OK;
+      }
+    }
+  }
   // Queries a launch: their pools and cutoff rows fit the workspace.
   auto need = [&](int64_t c) {
     return carve_bytes<uint64_t>((size_t)c * cap) + carve_bytes<float>((size_t)c * nprobe);

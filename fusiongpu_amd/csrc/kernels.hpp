@@ -148,7 +148,11 @@ struct ScreenArgs {
   int* cnt1;
   int* cnt2;
   int* cand_cnt;
-  int* bucket;              // [nlist][nq] pair entries (q nprobe + p) of each list
+  int* bucket;              // [nlist][nq] pair entries (q nprobe + p) of each list, or compact (boff)
+  // [nlist + 1] or nullptr: compact buckets for one probe a query, list l's
+  // entries at bucket[boff[l] .. boff[l + 1]) (boff[l + 1] - boff[l] = the
+  // queries whose probe is l); nullptr = bucket[l nq + pos].
+  const int32_t* boff = nullptr;
   uint4* arec;              // [nq nprobe][2][9] pair records: per lane half 8 A fragments and the extra block
   int2* first;              // [nq] round 1: (list, bucket position) of the query's pair, or (-1, -1)
   uint32_t* gminbuf;        // [nq][kMaxChunks][64] round 1: per query, first-list chunk and group, min U bits
@@ -218,6 +222,27 @@ struct TwoPhaseArgs {
   int32_t* pre_cut = nullptr;
 };
 int two_phase_pool_cap(int p1, int limit_k, int rerank_m);
+// Phase 1 through the screen: virtual query v = q p1 + p for the nqc queries
+// of a chunk (the query row copied to vq, probe p in vprobe, 0xFFFFFFFF when
+// unusable, a zero probe distance in vpd) and each usable list's count in
+// hist (zeroed first); boff = the exclusive scan of hist (nlist + 1 entries);
+// then each query's usable phase-1 lists get their w = min(n, limit_k) best
+// keys from (vids, vd) [nvq][limit_k] in their pool slots and their cutoffs
+// in cut_ws [nqc][nprobe]; launch_two_phase_after_phase1 runs the threshold,
+// phase 2 and the final select on them (limit_k <= 64).
+fgpu_status launch_tp_virtual(const float* queries, int dim, const uint32_t* probes, int nprobe, int p1, int nqc,
+                              const int32_t* offsets, int nlist, float* vq, uint32_t* vprobe, float* vpd, int* hist,
+                              hipStream_t s);
+fgpu_status launch_tp_offsets(const int* hist, int nlist, int32_t* boff, hipStream_t s);
+fgpu_status launch_tp_collect(const uint32_t* probes, int nprobe, int p1, int nqc, const int32_t* offsets, int nlist,
+                              int limit_k, const int32_t* vids, const float* vd, uint64_t* pool, int pool_cap,
+                              float* cut_ws, hipStream_t s);
+fgpu_status launch_two_phase_after_phase1(int dim, int m, const TwoPhaseArgs& a, hipStream_t s);
+// stats[11] += nvq, [12] += the sum of cand_cnt[0..nvq), [13] += *flag_cnt,
+// [14] += entries of thr[0..nvq) that are not below +inf, [15] += the others
+// whose cand_cnt exceeds cap.
+fgpu_status launch_tp_stats(const int* cand_cnt, const float* thr, int nvq, int cap, const int* flag_cnt,
+                            unsigned long long* stats, hipStream_t s);
 // Workgroups a query for phase 1 (TwoPhaseArgs::split) for a launch of nq
 // queries: 1 once nq fills every CU twice; a test override can force it.
 // (force: 0 automatic, 1 never, s >= 2 s ways, at most p1.)

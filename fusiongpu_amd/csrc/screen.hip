@@ -24,37 +24,44 @@
 //      subspace and the same sequential sum, so each equals the LUT value bit
 //      for bit) and the k smallest keys are kept.  Queries without a threshold
 //      (a first list shorter than k, out-of-range values) or with more
-//      candidates than the buffer holds go to the LUT kernel instead.
+//      candidates than the buffer holds go to the LUT kernel instead; a query
+//      without a usable probe, or whose only probe's list is shorter than k,
+//      has every vector there (none, or that list) as its candidates.
 //
 // The bounds.  With p the decoded residual of v (codebook rows, fp32) and
 // D* = ||r - p||^2 exactly, d = D* (1 +- gamma_c), gamma_c = gamma(s + M + 1)
 // < 2^-16 (non-negative terms, s + M + 1 roundings; gamma(n) = n u/(1 - n u),
 // u = 2^-24).  The screen forms
-//     -2 <bf16(r), bf16(p)>  +  per-query and per-vector constants
-// on v_mfma_f32_32x32x16_bf16: the main K range holds -2 bf16(r) (an exact
-// scaling) against bf16(p); one extra K block of 16 carries the constants, each
-// split into three bf16 values with directed rounding, so the MFMA sum is the
-// whole test value.  Round-to-nearest bf16 is within 2^-8 relative (plus
-// 2^-134 absolute below the normal range), so
-//     |<bf16 r, bf16 p> - <r, p>| <= (2^-7 + 2^-16) R X + 2^-129 (R + X) + 2^-260
-// with R >= ||r||, X >= ||p||.  The MFMA adds at most 144 fp32 roundings over
-// terms whose magnitudes sum to <= 1.03 (T + (R + X)^2), and may flush terms
-// below 2^-126 (< 2^-118 in all).  With a = 2^-6 + 2^-12, g = 2^-13 and
-// t = 1 + 2^-12 the two tests are
-//     V = ||p||^2 - gX^2 - 2^-110 X  - 2<r',p'> - a R X
+//     <a', p'>  +  per-query and per-vector constants,   a = -2 r (exact),
+// on v_mfma_f32_32x32x16_bf16, a' = bf16(a) and p' = bf16(p) (nearest): the
+// main K range holds a' against p'; one extra K block of 16 carries the
+// constants, each split into three bf16 values with directed rounding, so the
+// MFMA sum is the whole test value.  With the rounding errors' norms
+// E_a = ||a' - a|| (per query and list) and E_p = ||p' - p|| (per vector),
+//     |<a', p'> - <a, p>| <= E_a X + 2 R E_p + E_a E_p  (Cauchy-Schwarz)
+// for R >= ||r||, X >= ||p||: the norms are measured, not the worst case of
+// 2^-8 relative per element, which makes the bound about 2.6 times tighter
+// on typical data.  An input below the normal range the MFMA may flush
+// changes the product by < 2^-122 (R + X) more.  The MFMA adds at most 144
+// fp32 roundings over terms whose magnitudes sum to <= 1.03 (T + (R + X)^2),
+// and may flush terms below 2^-126 (< 2^-118 in all).  With B = (E_a + k R)
+// X' + 2 R E_p, X' >= X + E_p, k = 2^-14, g = 2^-13 and t = 1 + 2^-12 the two
+// tests are
+//     V = ||p||^2 - gX^2 - 2^-110 X + <a',p'> - B
 //         - (t T - nr2 + g R^2 + 2^-110 (1 + R))          <= 0,
-//     U = ||p||^2 + gX^2 + 2^-110 X  - 2<r',p'> + a R X
+//     U = ||p||^2 + gX^2 + 2^-110 X + <a',p'> + B
 //         + (t nr2 + g R^2 + 2^-110 (1 + R))              >= D*,
 // nr2 the fp32 sum of squares of r (within gamma(129) of ||r||^2).  Collecting
 // terms, every coefficient of V - (d - T)-style slack is negative:
-// T (1/(1-gamma_c) - t + 1.8e-5) < 0, R X (2^-6 + 2^-15 + 3.6e-5 - a) < 0,
+// T (1/(1-gamma_c) - t + 1.8e-5) < 0, R X (3.6e-5 - k) < 0,
 // R^2 (gamma(129) + 1.8e-5 - g) < 0, X^2 (1.8e-5 - g) < 0 and the absolute
 // terms; so d <= T implies V <= 0, and U >= D* for the threshold, which is
-// then inflated by t.  The per-vector constants (X rounded up to bf16,
-// ||p||^2 -+ gX^2 in double, split) are built once per index; the per-query
-// ones per (query, list).  Values whose norms exceed 2^40 would leave the
-// fp32 range safety the bound assumes: such indexes and queries take the LUT
-// kernel.
+// then inflated by t.  The per-vector constants (X' rounded up to bf16,
+// ||p||^2 -+ gX'^2 in double, split; E_p rounded up) are built once per
+// index; the per-query ones per (query, list), E_a from the fp32 sum of the
+// squared errors (relative error below 2^-16, plus 2^-100 absolute for
+// underflow).  Values whose norms exceed 2^40 would leave the fp32 range
+// safety the bound assumes: such indexes and queries take the LUT kernel.
 #include <cmath>
 
 #include "common.hpp"
@@ -68,7 +75,7 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
 namespace {
 
-constexpr double kA = 0x1p-6 + 0x1p-12;  // coefficient of R X
+constexpr double kRX = 0x1p-14;          // coefficient of R X (the MFMA's roundings)
 constexpr double kG = 0x1p-13;           // coefficient of R^2 and X^2
 constexpr double kTInfl = 1.0 + 0x1p-12;
 constexpr double kAbs = 0x1p-110;
@@ -151,11 +158,12 @@ __device__ __forceinline__ uint32_t pack2(uint16_t lo, uint16_t hi) { return (ui
 
 // ---- index-time arrays -----------------------------------------------------------
 // vext[v]: the per-vector block of the extra K range, 8 bf16:
-//   [X, y'_1, y'_2, y'_3, y''_1, y''_2, y''_3, 1]
-// X >= ||p_v|| (bf16, rounded up), y' <= ||p||^2 - g X^2 - 2^-110 X,
-// y'' >= ||p||^2 + g X^2 + 2^-110 X (each a three-part split).  ||p||^2 is
-// summed in double (each square exact; 128 roundings of 2^-53 are covered by
-// the 2^-40 slack).  xmax_bits: the largest X as float bits (atomic max).
+//   [X', y'_1, y'_2, y'_3, y''_1, y''_2, y''_3, E_p]
+// E_p >= ||bf16(p) - p|| and X' >= ||p_v|| + E_p (bf16, rounded up),
+// y' <= ||p||^2 - g X'^2 - 2^-110 X', y'' >= ||p||^2 + g X'^2 + 2^-110 X'
+// (each a three-part split).  ||p||^2 and the squared errors are summed in
+// double (each square exact; 128 roundings of 2^-53 are covered by the 2^-40
+// slack).  xmax_bits: the largest X' as float bits (atomic max).
 __global__ __launch_bounds__(256) void screen_prep_kernel(const float* __restrict__ cb, int m, int s,
                                                           const uint8_t* __restrict__ codes, int64_t total,
                                                           uint4* __restrict__ vext,
@@ -164,19 +172,24 @@ __global__ __launch_bounds__(256) void screen_prep_kernel(const float* __restric
   float xm = 0.0f;
   if (v < total) {
     const uint8_t* c = codes + v * m;
-    double p2 = 0.0;
+    double p2 = 0.0, e2 = 0.0;
     for (int j = 0; j < m; ++j) {
       const float* p = cb + ((size_t)j * kPQK + c[j]) * s;
-      for (int d = 0; d < s; ++d) p2 += (double)p[d] * (double)p[d];
+      for (int d = 0; d < s; ++d) {
+        const double e = (double)p[d] - bf_val(bf_rn(p[d]));
+        p2 += (double)p[d] * (double)p[d];
+        e2 += e * e;
+      }
     }
-    const uint16_t xb = bf_up(sqrt(p2) * (1.0 + kDbl));
+    const uint16_t eb = bf_up(sqrt(e2) * (1.0 + kDbl));
+    const uint16_t xb = bf_up((sqrt(p2) + bf_val(eb)) * (1.0 + kDbl));
     const double xu = bf_val(xb);
     const double lo = p2 - kG * xu * xu - kAbs * xu - kDbl * p2;
     const double hi = p2 + kG * xu * xu + kAbs * xu + kDbl * p2;
     uint16_t l1, l2, l3, h1, h2, h3;
     split3<false>(lo, l1, l2, l3);
     split3<true>(hi, h1, h2, h3);
-    vext[v] = make_uint4(pack2(xb, l1), pack2(l2, l3), pack2(h1, h2), pack2(h3, 0x3F80u));
+    vext[v] = make_uint4(pack2(xb, l1), pack2(l2, l3), pack2(h1, h2), pack2(h3, eb));
     xm = (float)xu;
   }
   xm = wave_max_f(xm);
@@ -198,12 +211,21 @@ __global__ __launch_bounds__(256) void screen_zero_kernel(int* __restrict__ p, i
 // Pair entry `ent` (= q nprobe + p) of query q goes to slot `pos` of list
 // l's bucket, taken earlier with an atomic on the list's count (the screen
 // kernels derive their work items from the final counts).
+__device__ __forceinline__ size_t bucket_base(const ScreenArgs& a, int l) {
+  return a.boff ? (size_t)a.boff[l] : (size_t)l * a.nq;
+}
+// Entries list l's bucket can hold.
+__device__ __forceinline__ int bucket_len(const ScreenArgs& a, int l) {
+  return a.boff ? a.boff[l + 1] - a.boff[l] : a.nq;
+}
 __device__ __forceinline__ int bucket_put(const ScreenArgs& a, int l, int q, int ent, int pos) {
-  if (pos >= a.nq) {  // a probe list repeating a list id: the query takes the LUT kernel
+  // A probe list repeating a list id (or more pairs than a compact bucket
+  // holds): the query takes the LUT kernel.
+  if (pos >= bucket_len(a, l)) {
     a.thr[q] = __builtin_nanf("");
     return -1;
   }
-  a.bucket[(size_t)l * a.nq + pos] = ent;
+  a.bucket[bucket_base(a, l) + pos] = ent;
   return pos;
 }
 
@@ -220,64 +242,75 @@ __device__ __forceinline__ int list_items(int cnt, int nq, int n) {
 }
 
 // The pair record of entry ent = (query q, probe p of list l): for each lane
-// half h (dims [h D/2, (h+1) D/2)) the A fragments -2 bf16(r), r = fl(q - c),
-// in MFMA operand order (fragment c holds dims h D/2 + 8c .. + 7), then the
-// extra K block of the round's test:
-//   round 1 (U):  h0 [ aR, 0, 0, 0, 1, 1, 1, c1]   h1 [c2, c3, 0 ...]
-//   round 2 (V):  h0 [-aR, 1, 1, 1, 0, 0, 0, v1]   h1 [v2, v3, 0 ...]
-// against the vector's block [X, y'1..3, y''1..3, 1] (h0) and [1, 1, 0 ...]
-// (h1): aR = bf16 above a R, c1 + c2 + c3 >= (t nr2 + g R^2 + 2^-110 (1 + R)),
+// half h (dims [h D/2, (h+1) D/2)) the A fragments a' = bf16(-2 r),
+// r = fl(q - c), in MFMA operand order (fragment c holds dims h D/2 + 8c ..
+// + 7), then the extra K block of the round's test:
+//   round 1 (U):  h0 [ e, 0, 0, 0, 1, 1, 1,  w]   h1 [c1, c2, c3, 0 ...]
+//   round 2 (V):  h0 [-e, 1, 1, 1, 0, 0, 0, -w]   h1 [v1, v2, v3, 0 ...]
+// against the vector's block [X', y'1..3, y''1..3, E_p] (h0) and
+// [1, 1, 1, 0 ...] (h1): e = bf16 above E_a + k R, w = bf16 above 2 R (so
+// e X' + w E_p >= B), c1 + c2 + c3 >= (t nr2 + g R^2 + 2^-110 (1 + R)),
 // v1 + v2 + v3 <= -(t T - nr2 + g R^2 + 2^-110 (1 + R)), each with the 2^-40
 // slack of the double arithmetic.  The record is unusable when nr2 is not
 // <= kMaxNorm2 (NaN included): then its A fragments are zero and its block
-// the round's inactive one (round 2: V = 1e30), so its row passes nothing
-// and bounds nothing, and the caller adds no pair or drops the query.
+// the round's inactive one (round 2: V = 1e30 through h1's first slot), so
+// its row passes nothing and bounds nothing, and the caller adds no pair or
+// drops the query.
 //
 // pair_a: the A fragments, by a whole wave (qv, cv: this lane's two dims of
-// the query and of the list's centroid); returns nr2 on every lane.
+// the query and of the list's centroid); returns (nr2, the fp32 sum of the
+// squared errors of a') on every lane.
 template <int D>
 __device__ __forceinline__ float2 centroid_dims(const ScreenArgs& a, int l) {
   const int lane = threadIdx.x & 63;
   return 2 * lane < D ? reinterpret_cast<const float2*>(a.centroids + (size_t)l * D)[lane] : make_float2(0.0f, 0.0f);
 }
+__device__ __forceinline__ float bf_float(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
 template <int D>
-__device__ float pair_a(const ScreenArgs& a, int64_t ent, float2 qv, float2 cv) {
+__device__ float2 pair_a(const ScreenArgs& a, int64_t ent, float2 qv, float2 cv) {
   const int lane = threadIdx.x & 63;
   const bool has = 2 * lane < D;
   const float r0 = has ? qv.x - cv.x : 0.0f, r1 = has ? qv.y - cv.y : 0.0f;
   const float nr2 = wave_sum_f(__builtin_fmaf(r1, r1, r0 * r0));
   const bool ok = nr2 <= kMaxNorm2;  // false for NaN
+  // -2 r is exact; its difference from the bf16 rounding is exact in fp32
+  const uint16_t b0 = bf_rn(-2.0f * r0), b1 = bf_rn(-2.0f * r1);
+  const float e0 = -2.0f * r0 - bf_float(b0), e1 = -2.0f * r1 - bf_float(b1);
+  const float ea2 = wave_sum_f(ok ? __builtin_fmaf(e1, e1, e0 * e0) : 0.0f);
   uint32_t* rec = reinterpret_cast<uint32_t*>(a.arec + ent * kRec);
   if (has) {
     const int d = 2 * lane, h = d / (D / 2), w = d % (D / 2);
-    rec[(h * kRecHalf + w / 8) * 4 + (w % 8) / 2] = ok ? pack2(bf_rn(-2.0f * r0), bf_rn(-2.0f * r1)) : 0u;
+    rec[(h * kRecHalf + w / 8) * 4 + (w % 8) / 2] = ok ? pack2(b0, b1) : 0u;
   }
-  return nr2;
+  return make_float2(nr2, ea2);
 }
-// pair_ex: both lane halves' extra blocks of entry ent, by one lane.
+// pair_ex: both lane halves' extra blocks of entry ent, by one lane (ne: the
+// (nr2, squared error sum) pair_a returned).
 template <int ROUND>
-__device__ void pair_ex(const ScreenArgs& a, int64_t ent, float nr2, float T) {
+__device__ void pair_ex(const ScreenArgs& a, int64_t ent, float2 ne, float T) {
   uint4* rec = a.arec + ent * kRec;
+  const float nr2 = ne.x;
   if (!(nr2 <= kMaxNorm2)) {
-    rec[kRecHalf - 1] = make_uint4(0u, 0u, 0u, ROUND == 2 ? pack2(0u, bf_rn(1e30f)) : 0u);
-    rec[2 * kRecHalf - 1] = make_uint4(0u, 0u, 0u, 0u);
+    rec[kRecHalf - 1] = make_uint4(0u, 0u, 0u, 0u);
+    rec[2 * kRecHalf - 1] = make_uint4(ROUND == 2 ? pack2(bf_rn(1e30f), 0u) : 0u, 0u, 0u, 0u);
     return;
   }
   const double n2 = (double)nr2;
   const double R = sqrt(n2 * (1.0 + 0x1p-16)) * (1.0 + kDbl);
-  const uint16_t aR = bf_up(kA * R);
+  const double Ea = sqrt((double)ne.y * (1.0 + 0x1p-16) + 0x1p-100) * (1.0 + kDbl);
+  const uint16_t e = bf_up(Ea + kRX * R), w = bf_up(2.0 * R);
   uint16_t p1, p2, p3;
   if (ROUND == 2) {
     const double t = (double)fmaxf(T, 0.0f);
     const double rhs = t * kTInfl - n2 + kG * R * R + kAbs * (1.0 + R);
     split3<false>(-rhs - kDbl * (t + n2 + kG * R * R), p1, p2, p3);
-    rec[kRecHalf - 1] = make_uint4(pack2(aR ^ 0x8000u, 0x3F80u), kOneOne, 0u, pack2(0u, p1));
+    rec[kRecHalf - 1] = make_uint4(pack2(e ^ 0x8000u, 0x3F80u), kOneOne, 0u, pack2(0u, w ^ 0x8000u));
   } else {
     const double c = n2 * kTInfl + kG * R * R + kAbs * (1.0 + R);
     split3<true>(c * (1.0 + kDbl), p1, p2, p3);
-    rec[kRecHalf - 1] = make_uint4(pack2(aR, 0u), 0u, kOneOne, pack2(0x3F80u, p1));
+    rec[kRecHalf - 1] = make_uint4(pack2(e, 0u), 0u, kOneOne, pack2(0x3F80u, w));
   }
-  rec[2 * kRecHalf - 1] = make_uint4(pack2(p2, p3), 0u, 0u, 0u);
+  rec[2 * kRecHalf - 1] = make_uint4(pack2(p1, p2), pack2(p3, 0u), 0u, 0u);
 }
 
 __device__ __forceinline__ float2 query_dims(const ScreenArgs& a, int q, int dim) {
@@ -287,7 +320,9 @@ __device__ __forceinline__ float2 query_dims(const ScreenArgs& a, int q, int dim
 
 // Round 1 pairs, one wave a query: the query with its first usable probe (in
 // range, non-empty) when that list holds at least k vectors and the residual
-// norm is in range; its pair record carries the U test.
+// norm is in range; its pair record carries the U test.  A query without a
+// usable probe, or with a single probe whose list is shorter than k, takes
+// that list's vectors as its candidates at once.
 template <int D>
 __global__ __launch_bounds__(256) void screen_pairs1_kernel(ScreenArgs a) {
   const int lane = threadIdx.x & 63;
@@ -311,11 +346,21 @@ __global__ __launch_bounds__(256) void screen_pairs1_kernel(ScreenArgs a) {
     }
   }
   int2 f = make_int2(-1, -1);
-  if (pf >= 0 && a.offsets[lf + 1] - a.offsets[lf] >= a.k) {
+  const int n = pf >= 0 ? a.offsets[lf + 1] - a.offsets[lf] : 0;
+  if (pf < 0 || (a.nprobe == 1 && n < a.k)) {
+    // No usable probe, or a single probe whose list holds fewer than k
+    // vectors: the answer is every vector there (then padding), so those are
+    // the candidates, with no screen (first = -2; the rescore sorts them).
+    const int start = pf >= 0 ? a.offsets[lf] : 0;
+    for (int i = lane; i < n; i += kWave)
+      a.cand[(size_t)q * a.cand_cap + i] = make_uint2((uint32_t)(start + i), (uint32_t)lf);
+    if (lane == 0) a.cand_cnt[q] = n;
+    f = make_int2(-2, 0);
+  } else if (n >= a.k) {
     const int64_t ent = (int64_t)q * a.nprobe + pf;
-    const float nr2 = pair_a<D>(a, ent, query_dims(a, q, D), centroid_dims<D>(a, lf));
-    if (lane == 0) pair_ex<1>(a, ent, nr2, 0.0f);
-    if (nr2 <= kMaxNorm2 && lane == 0) {
+    const float2 ne = pair_a<D>(a, ent, query_dims(a, q, D), centroid_dims<D>(a, lf));
+    if (lane == 0) pair_ex<1>(a, ent, ne, 0.0f);
+    if (ne.x <= kMaxNorm2 && lane == 0) {
       const int pos = bucket_put(a, lf, q, (int)ent, atomicAdd(&a.cnt1[lf], 1));
       if (pos >= 0) f = make_int2(lf, pos);
     }
@@ -326,7 +371,8 @@ __global__ __launch_bounds__(256) void screen_pairs1_kernel(ScreenArgs a) {
 // Round 2 pairs, one wave a query.  First T(q): the k-th smallest of the 32
 // group minima of U over the query's first list (the minimum, over the list's
 // chunks, of each chunk's per-group minimum), inflated by 1 + 2^-12; +inf
-// without a round-1 pair or with fewer than k groups holding a value.  Then
+// without a round-1 pair or with fewer than k groups holding a value
+// (FLT_MAX, and nothing more, for the queries whose candidates are set).  Then
 // every usable probe whose list bound does not exceed T(q), with its pair
 // record carrying the V test.  A probe whose residual norm is out of range
 // sends the query to the LUT kernel (T = +inf).
@@ -347,6 +393,12 @@ __global__ __launch_bounds__(256) void screen_pairs2_kernel(ScreenArgs a) {
   }
   const float2 qv = query_dims(a, q, D);
   const int2 f = a.first[q];
+  if (f.x == -2) {
+    // candidates set by the first pair kernel: the largest finite threshold
+    // sends them to the rescore
+    if (lane == 0) a.thr[q] = FLT_MAX;
+    return;
+  }
   uint32_t gm = 0x7F800000u;
   if (f.x >= 0 && lane < screen_groups(a.k)) {
     const int n = a.offsets[f.x + 1] - a.offsets[f.x];
@@ -378,27 +430,27 @@ __global__ __launch_bounds__(256) void screen_pairs2_kernel(ScreenArgs a) {
     // ignores its candidates.
     const int pos = pass ? atomicAdd(&a.cnt2[l], 1) : 0;
     // The A fragments, one pair at a time with the next pair's centroid
-    // loads in flight; the lane of each probe keeps its pair's nr2, and the
-    // extra blocks follow lane-parallel (one lane a pair).
+    // loads in flight; the lane of each probe keeps its pair's (nr2, error
+    // sum), and the extra blocks follow lane-parallel (one lane a pair).
     uint64_t m = __ballot(pass);
     if (!m) continue;
-    float my_nr2 = 0.0f;
+    float2 my_ne = make_float2(0.0f, 0.0f);
     int b = __builtin_ctzll(m);
     float2 cv = centroid_dims<D>(a, __builtin_amdgcn_readlane((int)l, b));
     while (true) {
       const uint64_t rest = m & (m - 1);
       const int bn = rest ? __builtin_ctzll(rest) : b;
       const float2 cn = rest ? centroid_dims<D>(a, __builtin_amdgcn_readlane((int)l, bn)) : cv;
-      const float nr2 = pair_a<D>(a, (int64_t)q * a.nprobe + p0 + b, qv, cv);
-      if (lane == b) my_nr2 = nr2;
+      const float2 ne = pair_a<D>(a, (int64_t)q * a.nprobe + p0 + b, qv, cv);
+      if (lane == b) my_ne = ne;
       if (!rest) break;
       m = rest;
       b = bn;
       cv = cn;
     }
     if (pass) {
-      pair_ex<2>(a, (int64_t)q * a.nprobe + p, my_nr2, T);
-      bad = bad || !(my_nr2 <= kMaxNorm2);
+      pair_ex<2>(a, (int64_t)q * a.nprobe + p, my_ne, T);
+      bad = bad || !(my_ne.x <= kMaxNorm2);
       bucket_put(a, (int)l, q, (int)((int64_t)q * a.nprobe + p), pos);
     }
   }
@@ -532,7 +584,7 @@ __global__ __launch_bounds__(kSW * kWave) void screen_kernel(ScreenArgs a) {
 #pragma unroll
     for (int i = 0; i < kPer; ++i) {
       const int l = tid * kPer + i;
-      v[i] = l < a.nlist ? list_items(cnt[l], a.nq, a.offsets[l + 1] - a.offsets[l]) : 0;
+      v[i] = l < a.nlist ? list_items(cnt[l], bucket_len(a, l), a.offsets[l + 1] - a.offsets[l]) : 0;
       s += v[i];
     }
     const int incl = wave_incl_scan(s);
@@ -560,10 +612,10 @@ __global__ __launch_bounds__(kSW * kWave) void screen_kernel(ScreenArgs a) {
   const uint32_t hsel = h ? (uint32_t)HB * 0x01010101u : 0u;
   // The extra block of a column past the end of the range: +1e30 in both
   // rounds' terms (slots 1 and 4), so its value is never a candidate and
-  // never a group minimum; lane half 1 keeps the [1, 1, 0 ...] multipliers.
+  // never a group minimum; lane half 1 keeps the [1, 1, 1, 0 ...] multipliers.
   const uint16_t big = bf_rn(1e30f);
-  const uint4 bx_pad = h == 0 ? make_uint4(pack2(0u, big), 0u, pack2(big, 0u), pack2(0u, 0x3F80u))
-                              : make_uint4(kOneOne, 0u, 0u, 0u);
+  const uint4 bx_pad = h == 0 ? make_uint4(pack2(0u, big), 0u, pack2(big, 0u), 0u)
+                              : make_uint4(kOneOne, 0x3F80u, 0u, 0u);
 
   for (int w = (int)blockIdx.x * kSW + wave; w < nitems; w += nwaves) {
     // Item w: the last list whose first item is <= w, then its group and chunk.
@@ -577,8 +629,8 @@ __global__ __launch_bounds__(kSW * kWave) void screen_kernel(ScreenArgs a) {
     const int per = chunk_len(n), nch = (n + per - 1) / per;
     const int local = w - __builtin_amdgcn_readfirstlane(pre[l]);
     const int grp = local / nch, jb = (local % nch) * per, je = min(n, jb + per);
-    const int nrow = min(kQB, min(cnt[l], a.nq) - grp * kQB);
-    const int ent = li < nrow ? a.bucket[(size_t)l * a.nq + grp * kQB + li] : -1;
+    const int nrow = min(kQB, min(cnt[l], bucket_len(a, l)) - grp * kQB);
+    const int ent = li < nrow ? a.bucket[bucket_base(a, l) + grp * kQB + li] : -1;
 
     // A tile's codes and extra blocks.  Every lane loads on every call (a
     // column past the range reloads the range's last vector; lane half 1
@@ -609,7 +661,7 @@ __global__ __launch_bounds__(kSW * kWave) void screen_kernel(ScreenArgs a) {
         A[c] = frag_of(v.x, v.y, v.z, v.w);
       }
       const uint4 e = ent >= 0 ? rec[kRecHalf - 1]
-                               : make_uint4(0u, 0u, 0u, ROUND == 2 && h == 0 ? pack2(0u, big) : 0u);
+                               : make_uint4(ROUND == 2 && h == 1 ? pack2(big, 0u) : 0u, 0u, 0u, 0u);
       Aex = frag_of(e.x, e.y, e.z, e.w);
     }
     // The query of each row, for the candidate flush and the round-1 store.

@@ -906,6 +906,140 @@ __global__ __launch_bounds__(kRT * SPEC) void rerank_kernel(RerankArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Phase 1 through the MFMA screen (fgpu_two_phase_search with limit_k <= 64):
+// every (query, phase-1 probe) becomes a virtual query of one probe, whose
+// exact top-limit_k over its list the screen (screen.hip) returns; these
+// kernels set the virtual queries up and put their results where phase 2
+// reads phase 1's (the pool slots and cutoffs of a split phase 1).
+
+__global__ __launch_bounds__(256) void tp_zero_kernel(int* __restrict__ p, int n) {
+  const int i = (int)blockIdx.x * 256 + (int)threadIdx.x;
+  if (i < n) p[i] = 0;
+}
+
+// Virtual query v = q p1 + p (q of the chunk): the query row (copied, 16
+// bytes a thread), its probe p (0xFFFFFFFF when out of range or empty), a zero
+// probe distance (the lower bound of its only list is then 0, so the list is
+// always screened), and its list's count in hist.
+__global__ __launch_bounds__(256) void tp_virtual_kernel(const float4* __restrict__ q, int d4,
+                                                         const uint32_t* __restrict__ probes, int P, int p1, int nvq,
+                                                         const int32_t* __restrict__ offsets, int nlist,
+                                                         float4* __restrict__ vq, uint32_t* __restrict__ vprobe,
+                                                         float* __restrict__ vpd, int* __restrict__ hist) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (int64_t)nvq * d4) return;
+  const int v = (int)(i / d4), c = (int)(i % d4);
+  const int qq = v / p1, p = v % p1;
+  vq[i] = q[(size_t)qq * d4 + c];
+  if (c == 0) {
+    const uint32_t l = probes[(size_t)qq * P + p];
+    const bool use = l < (uint32_t)nlist && offsets[l + 1] > offsets[l];
+    vprobe[v] = use ? l : 0xFFFFFFFFu;
+    vpd[v] = 0.0f;
+    if (use) atomicAdd(&hist[l], 1);
+  }
+}
+
+// boff[l] = hist[0] + ... + hist[l - 1] for l = 0 .. nlist (one workgroup,
+// nlist <= 8192: each thread sums 8 consecutive counts).
+__global__ __launch_bounds__(1024) void tp_offsets_kernel(const int* __restrict__ hist, int nlist,
+                                                          int32_t* __restrict__ boff) {
+  __shared__ int wsum[16];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  int v[8], sum = 0;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int l = tid * 8 + i;
+    v[i] = l < nlist ? hist[l] : 0;
+    sum += v[i];
+  }
+  const int incl = wave_incl_scan(sum);
+  if (lane == kWave - 1) wsum[wave] = incl;
+  __syncthreads();
+  if (wave == 0) {
+    int x = lane < 16 ? wsum[lane] : 0;
+    x = wave_incl_scan(x);
+    if (lane < 16) wsum[lane] = x;
+  }
+  __syncthreads();
+  int base = (wave > 0 ? wsum[wave - 1] : 0) + incl - sum;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int l = tid * 8 + i;
+    if (l <= nlist) boff[l] = base;
+    base += v[i];
+  }
+}
+
+// One wave a query of the chunk: the usable phase-1 probes in probe order
+// (in range, non-empty), each with w = min(n, limit_k) pool slots after the
+// earlier ones'; the w best keys of its virtual query (ascending) go to
+// them and its w-th distance to cut_ws[q][p], as the split phase 1 leaves
+// them (two_phase_kernel, mode 1).
+__global__ __launch_bounds__(256) void tp_collect_kernel(const uint32_t* __restrict__ probes, int P, int p1, int nqc,
+                                                         const int32_t* __restrict__ offsets, int nlist, int K1,
+                                                         const int32_t* __restrict__ vids, const float* __restrict__ vd,
+                                                         uint64_t* __restrict__ pool, int cap,
+                                                         float* __restrict__ cut_ws) {
+  const int lane = threadIdx.x & 63;
+  const int q = (int)blockIdx.x * 4 + (int)(threadIdx.x >> 6);
+  if (q >= nqc) return;
+  int base = 0;
+  for (int c0 = 0; c0 < p1; c0 += kWave) {
+    const int p = c0 + lane;
+    int w = 0;
+    if (p < p1) {
+      const uint32_t l = probes[(size_t)q * P + p];
+      if (l < (uint32_t)nlist) {
+        const int n = offsets[l + 1] - offsets[l];
+        w = n < K1 ? n : K1;
+      }
+    }
+    const int incl = wave_incl_scan(w);
+    const int mine = base + incl - w;
+    uint64_t m = __ballot(w > 0);
+    while (m) {
+      const int b = __ffsll((unsigned long long)m) - 1;
+      m &= m - 1;
+      const int wb = readlane_i(w, b), bb = readlane_i(mine, b);
+      const size_t v = ((size_t)q * p1 + c0 + b) * K1;
+      if (lane < wb) pool[(size_t)q * cap + bb + lane] = key_of(vd[v + lane], vids[v + lane]);
+      if (lane == 0) cut_ws[(size_t)q * P + c0 + b] = vd[v + wb - 1];
+    }
+    base += readlane_i(incl, kWave - 1);
+  }
+}
+
+// Instrumentation of phase 1 through the screen: stats[11] += virtual
+// queries, [12] += their candidates (every count, also past the cap), [13] +=
+// those handed to the LUT kernel, [14] += those without a threshold, [15] +=
+// those with more candidates than cap.
+__global__ __launch_bounds__(256) void tp_stats_kernel(const int* __restrict__ cand_cnt, const float* __restrict__ thr,
+                                                       int nvq, int cap, const int* __restrict__ flag_cnt,
+                                                       unsigned long long* __restrict__ stats) {
+  const int i = (int)blockIdx.x * 256 + (int)threadIdx.x;
+  const int c = i < nvq ? cand_cnt[i] : 0;
+  const bool no_t = i < nvq && !(thr[i] < INFINITY);
+  const int sc = wave_sum_i(c), sn = wave_sum_i(no_t ? 1 : 0), so = wave_sum_i(!no_t && c > cap ? 1 : 0);
+  if ((threadIdx.x & 63) == 0) {
+    if (sc) atomicAdd(&stats[12], (unsigned long long)sc);
+    if (sn) atomicAdd(&stats[14], (unsigned long long)sn);
+    if (so) atomicAdd(&stats[15], (unsigned long long)so);
+  }
+  if (i == 0) {
+    atomicAdd(&stats[11], (unsigned long long)nvq);
+    atomicAdd(&stats[13], (unsigned long long)*flag_cnt);
+  }
+}
+
+template <int D, int M>
+fgpu_status launch_tp_after(const TwoPhaseArgs& a, hipStream_t s) {
+  hipLaunchKernelGGL((two_phase_kernel<D, M, 2>), dim3((unsigned)a.nq), dim3(kTT), 0, s, a);
+  FGPU_HIP(hipGetLastError());
+  return FGPU_OK;
+}
+
 template <int D>
 fgpu_status launch_rr(const RerankArgs& a, hipStream_t s) {
   if (rerank_spec(a.nq, a.spec) > 1) {
@@ -972,6 +1106,65 @@ fgpu_status launch_two_phase(int dim, int m, const TwoPhaseArgs& a, hipStream_t 
   if (dim == 96 && m == 48) return launch_tp<96, 48>(a, nq, s);
   if (dim == 96 && m == 32) return launch_tp<96, 32>(a, nq, s);
   if (dim == 96 && m == 16) return launch_tp<96, 16>(a, nq, s);
+  return set_error(FGPU_ERR_UNSUPPORTED, "two_phase: unsupported (dim, pq_m)");
+}
+
+fgpu_status launch_tp_virtual(const float* queries, int dim, const uint32_t* probes, int nprobe, int p1, int nqc,
+                              const int32_t* offsets, int nlist, float* vq, uint32_t* vprobe, float* vpd, int* hist,
+                              hipStream_t s) {
+  FGPU_CHECK(dim % 4 == 0 && p1 >= 1 && nlist >= 1 && nlist <= 8192, FGPU_ERR_ARG, "two_phase: bad virtual queries");
+  if (nqc <= 0) return FGPU_OK;
+  hipLaunchKernelGGL(tp_zero_kernel, dim3((unsigned)((nlist + 255) / 256)), dim3(256), 0, s, hist, nlist);
+  const int64_t nvq = (int64_t)nqc * p1, nt = nvq * (dim / 4);
+  hipLaunchKernelGGL(tp_virtual_kernel, dim3((unsigned)((nt + 255) / 256)), dim3(256), 0, s,
+                     reinterpret_cast<const float4*>(queries), dim / 4, probes, nprobe, p1, (int)nvq, offsets, nlist,
+                     reinterpret_cast<float4*>(vq), vprobe, vpd, hist);
+  FGPU_HIP(hipGetLastError());
+  return FGPU_OK;
+}
+
+fgpu_status launch_tp_offsets(const int* hist, int nlist, int32_t* boff, hipStream_t s) {
+  FGPU_CHECK(nlist >= 1 && nlist <= 8192, FGPU_ERR_ARG, "two_phase: bad list count");
+  hipLaunchKernelGGL(tp_offsets_kernel, dim3(1), dim3(1024), 0, s, hist, nlist, boff);
+  FGPU_HIP(hipGetLastError());
+  return FGPU_OK;
+}
+
+fgpu_status launch_tp_collect(const uint32_t* probes, int nprobe, int p1, int nqc, const int32_t* offsets, int nlist,
+                              int limit_k, const int32_t* vids, const float* vd, uint64_t* pool, int pool_cap,
+                              float* cut_ws, hipStream_t s) {
+  FGPU_CHECK(limit_k >= 1 && limit_k <= kWave, FGPU_ERR_ARG, "two_phase: collect needs limit_k <= 64");
+  if (nqc <= 0) return FGPU_OK;
+  hipLaunchKernelGGL(tp_collect_kernel, dim3((unsigned)((nqc + 3) / 4)), dim3(256), 0, s, probes, nprobe, p1, nqc,
+                     offsets, nlist, limit_k, vids, vd, pool, pool_cap, cut_ws);
+  FGPU_HIP(hipGetLastError());
+  return FGPU_OK;
+}
+
+fgpu_status launch_tp_stats(const int* cand_cnt, const float* thr, int nvq, int cap, const int* flag_cnt,
+                            unsigned long long* stats, hipStream_t s) {
+  if (nvq <= 0 || !stats) return FGPU_OK;
+  hipLaunchKernelGGL(tp_stats_kernel, dim3((unsigned)((nvq + 255) / 256)), dim3(256), 0, s, cand_cnt, thr, nvq, cap,
+                     flag_cnt, stats);
+  FGPU_HIP(hipGetLastError());
+  return FGPU_OK;
+}
+
+fgpu_status launch_two_phase_after_phase1(int dim, int m, const TwoPhaseArgs& a, hipStream_t s) {
+  FGPU_CHECK(a.limit_k >= 1 && a.limit_k <= kWave && a.cut_ws, FGPU_ERR_ARG,
+             "two_phase: phase 2 after a separate phase 1 needs limit_k <= 64 and the cutoff rows");
+  FGPU_CHECK(a.rerank_m >= 1 && a.rerank_m <= kRerankMax, FGPU_ERR_UNSUPPORTED,
+             "two_phase: rerank_m must be in [1, 131072]");
+  FGPU_CHECK(a.nprobe >= 1 && a.nprobe <= kMaxProbes && a.p1 >= 0 && a.p1 <= a.nprobe, FGPU_ERR_ARG,
+             "two_phase: need 1 <= nprobe <= 256 and 0 <= p1 <= nprobe");
+  FGPU_CHECK(a.pool_cap >= two_phase_pool_cap(a.p1, a.limit_k, a.rerank_m), FGPU_ERR_ARG, "two_phase: pool too small");
+  if (a.nq <= 0) return FGPU_OK;
+  if (dim == 128 && m == 32) return launch_tp_after<128, 32>(a, s);
+  if (dim == 128 && m == 16) return launch_tp_after<128, 16>(a, s);
+  if (dim == 128 && m == 64) return launch_tp_after<128, 64>(a, s);
+  if (dim == 96 && m == 48) return launch_tp_after<96, 48>(a, s);
+  if (dim == 96 && m == 32) return launch_tp_after<96, 32>(a, s);
+  if (dim == 96 && m == 16) return launch_tp_after<96, 16>(a, s);
   return set_error(FGPU_ERR_UNSUPPORTED, "two_phase: unsupported (dim, pq_m)");
 }
 

@@ -201,8 +201,10 @@ fgpu_status fgpu_search(const fgpu_index* idx, const float* d_queries, int nq, i
  * `stream`; no reference counterpart): h_stats[0..7] = (query, list) pairs
  * screened for the thresholds, lists screened in the second round, (query,
  * list) pairs screened there, candidates rescored, the largest candidate count
- * of a query, queries handed to the LUT kernel, queries with a finite
- * threshold, 0; h_stats[8..15] the clocks of FGPU_OPT_SCREEN_CLOCKS;
+ * of a query, queries handed to the LUT kernel, queries with a threshold
+ * from the screen (not those whose candidates are every vector of their
+ * probes: no usable probe, or one probe holding fewer than k vectors), 0;
+ * h_stats[8..15] the clocks of FGPU_OPT_SCREEN_CLOCKS;
  * h_stats[16..19] = (query, vector) pairs screened in round 1 and round 2,
  * MFMA tiles (32 queries x 32 vectors) run in round 1 and round 2.  Only
  * meaningful after a call that took the screen. */
@@ -314,12 +316,16 @@ fgpu_status fgpu_two_phase_search_precut(const fgpu_index* idx, const float* d_q
                                          void* stream);
 
 /* fgpu_two_phase_search plus instrumentation (no reference counterpart): adds
- * to d_stats[0..10] (device, caller-zeroed, uint64) the vectors whose codes
+ * to d_stats[0..15] (device, caller-zeroed, uint64) the vectors whose codes
  * were loaded, the LUTs built, the phase-2 lists skipped by the list lower
  * bound, the phase-2 candidates appended, the shader clocks each workgroup
  * spent in set-up, phase 1, phase 2 and the final select + sort, and the
- * phase-1 clocks up to the LUT barrier, in the scan and in the merge.
- * Results are unchanged. */
+ * phase-1 clocks up to the LUT barrier, in the scan and in the merge; and
+ * when phase 1 runs through the MFMA screen (limit_k <= 64, see
+ * fgpu_two_phase_search), d_stats[11..15]: the virtual queries screened (one
+ * per query and phase-1 probe), their candidates, those handed to the LUT
+ * kernel, and of these the ones without a threshold and the ones with more
+ * candidates than the screen keeps.  Results are unchanged. */
 fgpu_status fgpu_two_phase_search_stats(const fgpu_index* idx, const float* d_queries, int nq,
                                         const uint32_t* d_probe_ids, int nprobe, int p1_lists, int limit_k,
                                         float threshold_coeff, int rerank_m, int32_t* d_top_ids,

@@ -144,7 +144,40 @@ def test_screen_hands_short_first_lists_to_the_lut_kernel():
     probes, _ = oracle.coarse(q, cent, 16)
     first = np.array([next((lens[l] for l in row if l < nlist and lens[l] > 0), 0) for row in probes])
     assert st["queries_with_threshold"] == int((first >= k).sum())
-    assert st["queries_to_lut_kernel"] >= int((first < k).sum()) > 0
+    assert st["queries_to_lut_kernel"] >= int(((first > 0) & (first < k)).sum()) > 0
+    idx.close()
+
+
+def test_screen_single_probe_short_and_empty_lists():
+    """nprobe 1: a query whose only list holds fewer than k vectors takes them
+    all as its candidates, one whose list is empty gets padding; neither runs
+    the LUT kernel.  Bit-exact with the oracle and the LUT kernels."""
+    _say("screen single probe, short and empty lists")
+    rng = np.random.default_rng(13)
+    dim, m, nlist, k = 128, 32, 300, 32
+    offs, ids, codes, cent, cb = _gmm_index(dim, m, nlist, 9000, seed=13)
+    lens = np.diff(offs)
+    empty = np.argsort(np.where(lens > 0, lens, 1 << 30))[:5]  # the five shortest lists, emptied
+    keep = np.ones(len(ids), bool)
+    for e in empty:
+        keep[offs[e]:offs[e + 1]] = False
+    lens2 = lens.copy()
+    lens2[empty] = 0
+    offs2 = np.concatenate([[0], np.cumsum(lens2)]).astype(offs.dtype)
+    ids2, codes2 = np.ascontiguousarray(ids[keep]), np.ascontiguousarray(codes[keep])
+    idx = fg.Index.from_arrays(dim, m, offs2, ids2, codes2, cent, cb)
+    assert idx.screen_ready
+    short = np.nonzero((lens2 > 0) & (lens2 < k))[0]
+    assert short.size >= 10
+    pick = np.concatenate([empty, short[:20]])
+    q = cent[np.repeat(pick, 3)] + rng.standard_normal((3 * pick.size, dim)).astype(np.float32) * 1e-3
+    q = np.concatenate([q, fg.gen_gmm(100, dim, 32, seed=13, set=1, sig_lo=0.08)]).astype(np.float32)
+    st = _check(idx, q, cent, cb, offs2, ids2, codes2, 1, k)
+    probes, _ = oracle.coarse(q, cent, 1)
+    n1 = lens2[probes[:, 0]]
+    assert (n1 == 0).sum() >= 10 and ((n1 > 0) & (n1 < k)).sum() >= 30
+    assert st["queries_with_threshold"] == int((n1 >= k).sum())
+    assert st["queries_to_lut_kernel"] == 0
     idx.close()
 
 

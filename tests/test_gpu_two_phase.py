@@ -130,6 +130,48 @@ def test_two_phase_many_phase1_lists():
     idx.close()
 
 
+def test_two_phase_screen_phase1_short_lists_and_pruned_probes():
+    """Phase 1 through the MFMA screen (limit_k <= 64): one single-probe
+    query per (query, phase-1 probe).  Lists shorter than limit_k and probes
+    without a list take their vectors directly, so nothing runs the LUT
+    kernel; bit-exact with the oracle and with the LUT path (OPT_SCREEN 0)."""
+    _say("two_phase screen phase 1: short lists, pruned probes")
+    rng = np.random.default_rng(5151)
+    dim, m, nlist = 96, 48, 64
+    offs, ids, lc, cent, cb = _index(rng, 8000, dim, m, nlist, empty=(2, 11))
+    lens = np.diff(offs)
+    p1, limit_k, coeff, rerank_m = 12, 50, 1.0, 600
+    short = np.nonzero((lens > 0) & (lens < limit_k))[0]
+    assert short.size >= 3
+    q = (rng.standard_normal((150, dim)) * 0.7).astype(np.float32)
+    probes, _ = oracle.coarse(q, cent, 16)
+    probes[4, :] = 0xFFFFFFFF            # nothing probed
+    probes[5, 0] = short[0]              # a short list first
+    probes[6, :3] = 0xFFFFFFFF           # pruned phase-1 probes
+    probes[7, 1] = 2                     # an empty list in phase 1
+    probes[8, 2] = 777                   # out of range: pruned
+    idx = fg.Index.from_arrays(dim, m, offs, ids, lc, cent, cb)
+    assert idx.screen_ready
+    dq, dp = torch.from_numpy(q).cuda(), torch.from_numpy(probes.view(np.int32)).cuda()
+    gid, gd, gcnt, st = idx.two_phase_stats(dq, dp, p1, limit_k, coeff, rerank_m)
+    oid, od, ocnt, _, _ = oracle.search_two_phase(q, cent, cb, offs, ids, lc, probes, p1, limit_k, coeff, rerank_m)
+    assert np.array_equal(_host(gcnt), ocnt)
+    assert np.array_equal(_host(gid), oid)
+    assert np.array_equal(_bits(_host(gd)), _bits(od))
+    assert st["screen_virtual_queries"] == 150 * p1
+    assert st["screen_no_threshold"] == 0
+    assert st["screen_to_lut"] == st["screen_over_cap"]
+    usable = (probes[:, :p1] < nlist) & (lens[np.minimum(probes[:, :p1], nlist - 1)] > 0)
+    assert st["screen_candidates"] >= int(np.minimum(lens[probes[:, :p1][usable]], limit_k).sum())
+    idx.set_option(fg.Index.OPT_SCREEN, 0)
+    lid, ld, lcnt, _, _ = idx.two_phase_search(dq, dp, p1, limit_k, coeff, rerank_m)
+    _, _, _, lst = idx.two_phase_stats(dq, dp, p1, limit_k, coeff, rerank_m)
+    assert lst["screen_virtual_queries"] == 0
+    assert np.array_equal(_host(lid), oid) and np.array_equal(_bits(_host(ld)), _bits(od))
+    assert np.array_equal(_host(lcnt), ocnt)
+    idx.close()
+
+
 @pytest.mark.parametrize("dim,m,p1,limit_k,coeff,rerank_m", [
     (128, 32, 12, 50, 1.0, 1000),  # the reference pipeline's defaults (p1 12, limit_k 50)
     (96, 16, 5, 64, 1.2, 300),     # limit_k at the split's limit
