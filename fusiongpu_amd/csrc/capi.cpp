@@ -202,7 +202,7 @@ struct ScreenWs {
 // chunk of nvq virtual queries (one per (query, phase-1 probe)): their query
 // rows, probes and (zero) probe distances, their top-limit_k results, the
 // per-list counts and compact bucket offsets, and the screen's workspace.
-constexpr int kTpVqMax = 65536;  // virtual queries a chunk
+constexpr int kTpVqMax = 131072;  // virtual queries a chunk (fuller 32-row MFMA groups per list)
 struct TpScreenWs {
   float* vq = nullptr;
   uint32_t* vprobe = nullptr;

@@ -855,9 +855,11 @@ __device__ __forceinline__ void load_row(const float* p, float (&v)[S]) {
 // reference's direct form (the LUT entry's chain per subspace, summed in
 // ascending m), then the k smallest (distance, id) keys.  A persistent grid
 // of one workgroup per CU holding the fp32 codebook in LDS; wave g takes
-// queries g, g + G, ...
+// queries g, g + G, ...  ONE (single-probe queries): every candidate lies in
+// the query's one list, so the residual r = fl(q - c) is formed once in LDS
+// (the same fp32 subtraction) instead of loading the centroid per candidate.
 constexpr int kRW = 16;  // waves per rescore workgroup
-template <int D, int M>
+template <int D, int M, bool ONE>
 __global__ __launch_bounds__(kRW * kWave) void rescore_kernel(ScreenArgs a) {
   constexpr int S = D / M;
   __shared__ __align__(16) float cbf[D * kPQK];
@@ -876,7 +878,13 @@ __global__ __launch_bounds__(kRW * kWave) void rescore_kernel(ScreenArgs a) {
       }
       continue;
     }
-    for (int d = lane; d < D; d += kWave) qs[wave][d] = a.queries[(size_t)q * D + d];
+    if constexpr (ONE) {
+      const uint32_t l1 = a.probes[q];  // cnt > 0 only when it is a usable list
+      for (int d = lane; d < D; d += kWave)
+        qs[wave][d] = cnt > 0 ? a.queries[(size_t)q * D + d] - a.centroids[(size_t)l1 * D + d] : 0.0f;
+    } else {
+      for (int d = lane; d < D; d += kWave) qs[wave][d] = a.queries[(size_t)q * D + d];
+    }
     wave_sync();
     const float* qv = qs[wave];
     uint64_t lk = kPadKey;
@@ -886,7 +894,7 @@ __global__ __launch_bounds__(kRW * kWave) void rescore_kernel(ScreenArgs a) {
       if (i < cnt) {
         const uint2 e = a.cand[(size_t)q * a.cand_cap + i];
         const int64_t pos = e.x;
-        const float* cen = a.centroids + (size_t)e.y * D;
+        const float* cen = a.centroids + (size_t)(ONE ? 0 : e.y) * D;
         uint4 w[M / 16];
         load_codes<M>(a.codes, pos, w);
         const int id = a.vec_ids[pos];
@@ -896,12 +904,18 @@ __global__ __launch_bounds__(kRW * kWave) void rescore_kernel(ScreenArgs a) {
           const uint32_t ww = mm % 16 < 4 ? w[mm / 16].x : mm % 16 < 8 ? w[mm / 16].y
                                                        : mm % 16 < 12 ? w[mm / 16].z : w[mm / 16].w;
           const uint32_t code = (ww >> (8 * (mm & 3))) & 0xFFu;
-          float cr[S], pr[S], r[S];
-          load_row<S>(cen + mm * S, cr);
+          float pr[S], r[S];
 #pragma unroll
           for (int e2 = 0; e2 < S; ++e2) pr[e2] = cbf[(mm * kPQK + code) * S + e2];
+          if constexpr (ONE) {
 #pragma unroll
-          for (int e2 = 0; e2 < S; ++e2) r[e2] = qv[mm * S + e2] - cr[e2];
+            for (int e2 = 0; e2 < S; ++e2) r[e2] = qv[mm * S + e2];
+          } else {
+            float cr[S];
+            load_row<S>(cen + mm * S, cr);
+#pragma unroll
+            for (int e2 = 0; e2 < S; ++e2) r[e2] = qv[mm * S + e2] - cr[e2];
+          }
           const float t = lut_entry<S>(r, pr);
           dist = mm == 0 ? t : dist + t;
         }
@@ -949,7 +963,10 @@ fgpu_status launch_screen_dm(const ScreenArgs& a, hipStream_t s) {
   FGPU_HIP(mark(2));
   hipLaunchKernelGGL((screen_kernel<D, M, 2>), dim3((unsigned)cus), dim3(kSW * kWave), 0, s, a);
   FGPU_HIP(mark(3));
-  hipLaunchKernelGGL((rescore_kernel<D, M>), dim3((unsigned)cus), dim3(kRW * kWave), 0, s, a);
+  if (a.nprobe == 1)
+    hipLaunchKernelGGL((rescore_kernel<D, M, true>), dim3((unsigned)cus), dim3(kRW * kWave), 0, s, a);
+  else
+    hipLaunchKernelGGL((rescore_kernel<D, M, false>), dim3((unsigned)cus), dim3(kRW * kWave), 0, s, a);
   FGPU_HIP(mark(4));
   FGPU_HIP(hipGetLastError());
   return FGPU_OK;
