@@ -40,7 +40,10 @@ lists, PQ M=48, 10k queries, nprobe=64, the two-phase pruned scan (p1_lists 12,
 limit_k 50, threshold_coeff 1.0) compacted to the top 1000 candidates, then the
 early-stopping exact rerank (mini-batch 128, eps 0.1, beta 2) to k=100.  Its
 index is built in-run too (k-means on a 1M-row sample, then every row
-assigned), not timed.
+assigned), not timed.  Phase 1 of the two-phase scan runs as the MFMA screen
+over one single-probe query per (query, phase-1 probe); the line's roofline is
+that screen's longer round, measured like config 2's, and `two_phase` holds
+the call's stage times and counters.
 
 --workload c4 prints a supplementary line for BASELINE config 4, the index
 build: 10M x 128 fp32 (1024-component mixture); k-means++ seeding and 20 Lloyd
@@ -666,7 +669,27 @@ def run_c3(args, torch, fg, dev):
     sid, sd, sc, tstats = idx.two_phase_stats(dq, probes, p1, limit_k, coeff, rerank_m, workspace=tp_ws)
     assert torch.equal(sid, tid) and torch.equal(sd, td) and torch.equal(sc, tc), "instrumented scan differs"
     loaded_bytes = tstats["vectors_loaded"] * (m + 4)
-    log(f"two-phase counters: {tstats}; loads {loaded_bytes / 1e9:.2f} GB (codes + ids)")
+    log(f"two-phase counters: {tstats}; phase-2 loads {loaded_bytes / 1e9:.4f} GB (codes + ids)")
+    # Phase 1 runs through the MFMA screen (one single-probe query per (query, phase-1 probe)); its
+    # stages, from the events the call records with OPT_STAGE_EVENTS on.
+    idx.set_option(fg.Index.OPT_STAGE_EVENTS, 1)
+    tp_stage = {kk: 0.0 for kk in fg.Index.TP_STAGES}
+    reps_st = max(args.steps, 3)
+    for _ in range(reps_st):
+        idx.two_phase_search(dq, probes, p1, limit_k, coeff, rerank_m, workspace=tp_ws)
+        for kk, v in idx.two_phase_stage_times().items():
+            tp_stage[kk] += v / reps_st
+    idx.set_option(fg.Index.OPT_STAGE_EVENTS, 0)
+    log("two-phase stages (ms): " + ", ".join(f"{kk} {v:.4f}" for kk, v in tp_stage.items()))
+    rnd = 2 if tp_stage["screen_round2"] >= tp_stage["screen_round1"] else 1
+    scr_ms = tp_stage[f"screen_round{rnd}"]
+    scr_flop = 2.0 * (dim + 16) * tstats[f"screen_vector_pairs_round{rnd}"]
+    scr_exec_flop = 2.0 * (dim + 16) * 32 * 32 * tstats[f"screen_tiles_round{rnd}"]
+    scr_bytes = tstats[f"screen_tiles_round{rnd}"] * 32 * (m + 16)
+    scr_tflops = scr_flop / (scr_ms * 1e-3) / 1e12
+    log(f"screen round {rnd} of phase 1: {scr_ms:.4f} ms, {scr_flop / 1e9:.2f} GFLOP algorithmic "
+        f"({scr_tflops:.1f} TFLOP/s), {scr_exec_flop / 1e9:.2f} GFLOP in MFMA tiles, {scr_bytes / 1e6:.1f} MB of "
+        f"codes + blocks read")
     _, _, vis = fg.rerank(dq, dx, tid, tc, k, mb, eps, beta)
     visited = int(vis.to(torch.int64).sum().item())
     ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
@@ -687,7 +710,6 @@ def run_c3(args, torch, fg, dev):
     tp_ms = ev[1].elapsed_time(ev[2]) / reps
     rr_ms = ev[2].elapsed_time(ev[3]) / reps
     adc_gbs = adc_bytes / (tp_ms * 1e-3) / 1e9
-    loaded_gbs = loaded_bytes / (tp_ms * 1e-3) / 1e9
     rr_bytes = visited * dim * 4
     log(f"coarse {coarse_ms:.3f} ms, two-phase {tp_ms:.3f} ms (algorithmic ADC bytes {adc_bytes / 1e9:.2f} GB -> "
         f"{adc_gbs:.0f} GB/s), rerank {rr_ms:.3f} ms ({visited} rows = {rr_bytes / 1e9:.2f} GB -> "
@@ -753,17 +775,24 @@ def run_c3(args, torch, fg, dev):
         "config": {"workload": "BASELINE config 3: 10M x 96 fp32, 4096 lists, PQ M=48, 10k queries, nprobe=64, "
                                "p1_lists 12, limit_k 50, threshold_coeff 1.0, top-1000 -> exact rerank k=100",
                    "n": n, "dim": dim, "nlist": nlist, "pq_m": m, "nq": nq, "nprobe": nprobe, "k": k},
-        "roofline": {"bound": "hbm", "kernel": "two_phase_kernel<96,48>", "achieved": round(loaded_gbs, 1),
-                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(loaded_gbs / HBM_PEAK_GBS, 4),
-                     "traffic": read_traffic(TRAFFIC_FILE_C3), "bytes_per_launch": loaded_bytes,
-                     "avg_launch_ms": round(tp_ms, 4),
-                     "note": "achieved = codes + ids of the lists the scan reads (its own load count in this run) / "
-                             "kernel time; traffic = copy-calibrated FETCH_SIZE + WRITE_SIZE per launch "
-                             "(profiles/two_phase_c3_traffic.txt)",
-                     "effective": {"bytes_per_launch": adc_bytes, "gbs": round(adc_gbs, 1),
-                                   "note": "work-equivalent: code bytes of every probed list once per (query, list); "
-                                           "phase 2 skips lists whose bound exceeds the threshold"},
-                     **tstats},
+        "roofline": {"bound": "mfma", "kernel": f"screen_kernel<96,48,{rnd}> (phase-1 screen round {rnd})",
+                     "achieved": round(scr_tflops, 2), "peak": BF16_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(scr_tflops / BF16_MFMA_PEAK_TFLOPS, 4),
+                     "traffic": read_traffic(TRAFFIC_FILE_C3, f"traffic_bytes_per_launch_round{rnd}"),
+                     "avg_launch_ms": round(scr_ms, 4), "flop_per_launch": scr_flop,
+                     "mfma_tile_flop_per_launch": scr_exec_flop,
+                     "mfma_tile_frac": round(scr_exec_flop / (scr_ms * 1e-3) / 1e12 / BF16_MFMA_PEAK_TFLOPS, 4),
+                     "bytes_read_per_launch": scr_bytes, "hbm_gbs": round(scr_bytes / (scr_ms * 1e-3) / 1e9, 1),
+                     "note": "the two-phase call's longest kernel: phase 1 (each phase-1 list's top-50 and cutoff) "
+                             "as one single-probe screen query per (query, phase-1 probe); achieved = 2 (dim + 16) "
+                             "flops per (query, vector) pair screened / its event-timed duration, against the "
+                             "dense bf16 peak; traffic = copy-calibrated FETCH_SIZE + WRITE_SIZE per launch "
+                             "(profiles/two_phase_c3_traffic.txt)"},
+        "two_phase": {"ms": round(tp_ms, 4), "stages_ms": {kk: round(v, 4) for kk, v in tp_stage.items()},
+                      "work_equivalent_adc_bytes": adc_bytes, "work_equivalent_gbs": round(adc_gbs, 1),
+                      "note": "work-equivalent: code bytes of every probed list once per (query, list), over the "
+                              "two-phase time; phase 2 skips lists whose bound exceeds the threshold",
+                      **tstats},
         "stages_ms": {"coarse": round(coarse_ms, 4), "two_phase": round(tp_ms, 4), "rerank": round(rr_ms, 4),
                       "rerank_rows": visited, "rerank_gbs": round(rr_bytes / (rr_ms * 1e-3) / 1e9, 1),
                       "rerank_frac_of_measured_row_rate": round(rr_bytes / (rr_ms * 1e-3) / 1e9 / rows_peak, 4),

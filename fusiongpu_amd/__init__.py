@@ -601,7 +601,7 @@ class Index:
             tid = torch.empty((nq, rerank_m), dtype=torch.int32, device="cuda")
             td = torch.empty((nq, rerank_m), dtype=torch.float32, device="cuda")
             tc = torch.empty(nq, dtype=torch.int32, device="cuda")
-            st = torch.zeros(16, dtype=torch.int64, device="cuda")
+            st = torch.zeros(20, dtype=torch.int64, device="cuda")
             _check(lib.fgpu_two_phase_search_stats(self._h, _dev_ptr(q), nq, _dev_ptr(p), nprobe, p1_lists, limit_k,
                                                    threshold_coeff, rerank_m, _dev_ptr(tid), _dev_ptr(td),
                                                    _dev_ptr(tc), _dev_ptr(st), _dev_ptr(ws), _ws_check(ws),
@@ -611,7 +611,9 @@ class Index:
                              "phase2_appended": v[3], "clk_setup": v[4], "clk_phase1": v[5], "clk_phase2": v[6],
                              "clk_final": v[7], "clk_p1_build": v[8], "clk_p1_scan": v[9], "clk_p1_merge": v[10],
                              "screen_virtual_queries": v[11], "screen_candidates": v[12], "screen_to_lut": v[13],
-                             "screen_no_threshold": v[14], "screen_over_cap": v[15]}
+                             "screen_no_threshold": v[14], "screen_over_cap": v[15],
+                             "screen_vector_pairs_round1": v[16], "screen_vector_pairs_round2": v[17],
+                             "screen_tiles_round1": v[18], "screen_tiles_round2": v[19]}
 
     def search_rerank_workspace_bytes(self, nq: int, nprobe: int, p1_lists: int, limit_k: int, rerank_m: int) -> int:
         return lib.fgpu_search_rerank_workspace_bytes(nq, self.nlist, nprobe, p1_lists, limit_k, rerank_m)
@@ -686,6 +688,16 @@ class Index:
         ms = (_c.c_float * len(self.STAGES))()
         _check(lib.fgpu_search_stage_times(self._h, ms, len(self.STAGES)))
         return {kk: float(ms[i]) for i, kk in enumerate(self.STAGES)}
+
+    TP_STAGES = ("virtual_queries", "screen_pairs1", "screen_round1", "screen_pairs2", "screen_round2", "rescore",
+                 "lut_collect_phase2_final")
+
+    def two_phase_stage_times(self) -> dict:
+        """Milliseconds of the stages of the last two_phase_search() whose phase 1 ran through the screen (the last
+        virtual-query chunk), from the events it recorded with OPT_STAGE_EVENTS on: keys Index.TP_STAGES."""
+        ms = (_c.c_float * len(self.TP_STAGES))()
+        _check(lib.fgpu_search_stage_times(self._h, ms, len(self.TP_STAGES)))
+        return {kk: float(ms[i]) for i, kk in enumerate(self.TP_STAGES)}
 
     def search_noalloc(self, queries, nprobe: int, k: int, prune_ratio: float = 100.0, out=None, stream=None):
         """fgpu_search without a workspace (fgpu_search_noalloc): its scratch is the library's fixed per-GPU

@@ -762,6 +762,11 @@ fgpu_status two_phase(const fgpu_index* ix, const float* dq, int nq, const uint3
   // pools and cutoff rows the rest.
   if (ix->screen_ok && ix->opt_screen && limit_k <= 64 && p1 >= 1 && screen_supported(ix->dim, ix->m) &&
       ix->nlist <= kScreenMaxLists && ((uintptr_t)dq & 15) == 0) {
+    // With FGPU_OPT_STAGE_EVENTS, the stage events of fgpu_search_stage_times
+    // around the last virtual-query chunk's set-up and screen stages; the
+    // last stage runs from its rescore to the end of the call.
+    const hipEvent_t* ev = ix->opt_stage_events ? ix->stage_ev : nullptr;
+    auto mark = [&](int i) { return ev ? hipEventRecord(ev[i], s) : hipSuccess; };
     const int qv = std::max(1, kTpVqMax / p1);  // queries a virtual-query chunk
     const int nvq_max = (int)std::min<int64_t>((int64_t)nq, qv) * p1;
     const size_t tbytes = TpScreenWs::bytes(nvq_max, ix->nlist, ix->dim, limit_k);
@@ -786,9 +791,11 @@ fgpu_status two_phase(const fgpu_index* ix, const float* dq, int nq, const uint3
             TpScreenWs tw;
             FGPU_CHECK(tw.carve(tbase, ws_bytes - tofs, nvq, ix->nlist, ix->dim, limit_k), FGPU_ERR_WORKSPACE,
                        "two_phase_search: screen buffers do not fit");
+            FGPU_HIP(mark(0));
             FGPU_TRY(launch_tp_virtual(qq + (int64_t)s0 * ix->dim, ix->dim, pp + (int64_t)s0 * nprobe, nprobe, p1, ns,
                                        ix->d_offsets, ix->nlist, tw.vq, tw.vprobe, tw.vpd, tw.hist, s));
             FGPU_TRY(launch_tp_offsets(tw.hist, ix->nlist, tw.boff, s));
+            FGPU_HIP(mark(1));
             ScreenArgs sa{tw.vq, ix->d_centroids, ix->d_offsets, ix->d_codes, ix->d_ids, ix->d_codebook, ix->d_cb16,
                           ix->d_vext, ix->d_rmax, tw.vprobe, tw.vpd, nvq, 1, limit_k, ix->nlist};
             sa.ctr = tw.sw.zero;
@@ -806,12 +813,14 @@ fgpu_status two_phase(const fgpu_index* ix, const float* dq, int nq, const uint3
             sa.flist = tw.sw.flist;
             sa.out_ids = tw.vids;
             sa.out_d = tw.vd;
+            sa.events = ev ? ev + 2 : nullptr;
             FGPU_TRY(launch_screen(ix->dim, ix->m, sa, s));
             AdcArgs la = adc_args(ix, tw.vq, nvq, tw.vprobe, tw.vpd, 1, limit_k, tw.vids, tw.vd);
             la.qlist = tw.sw.flist;
             la.qcount = tw.sw.zero + kCtrFlag;
             FGPU_TRY(launch_adc_plain_list(ix->dim, ix->m, la, s));
-            FGPU_TRY(launch_tp_stats(sa.cand_cnt, sa.thr, nvq, kScreenCandCap, tw.sw.zero + kCtrFlag, d_stats, s));
+            FGPU_TRY(launch_tp_stats(sa.cand_cnt, sa.thr, nvq, kScreenCandCap, tw.sw.zero + kCtrFlag, sa.cnt1,
+                                     sa.cnt2, tw.boff, ix->d_offsets, ix->nlist, d_stats, s));
             FGPU_TRY(launch_tp_collect(pp + (int64_t)s0 * nprobe, nprobe, p1, ns, ix->d_offsets, ix->nlist, limit_k,
                                        tw.vids, tw.vd, pool + (size_t)s0 * cap, cap, cut_ws + (size_t)s0 * nprobe, s));
           }
@@ -824,6 +833,7 @@ fgpu_status two_phase(const fgpu_index* ix, const float* dq, int nq, const uint3
           a.pre_cut = d_pre_cut ? d_pre_cut + q0 : nullptr;
           FGPU_TRY(launch_two_phase_after_phase1(ix->dim, ix->m, a, s));
         }
+        FGPU_HIP(mark(kStageEvents - 1));
         return FGPU_OK;
       }
     }

@@ -240,8 +240,11 @@ fgpu_status launch_tp_collect(const uint32_t* probes, int nprobe, int p1, int nq
 fgpu_status launch_two_phase_after_phase1(int dim, int m, const TwoPhaseArgs& a, hipStream_t s);
 // stats[11] += nvq, [12] += the sum of cand_cnt[0..nvq), [13] += *flag_cnt,
 // [14] += entries of thr[0..nvq) that are not below +inf, [15] += the others
-// whose cand_cnt exceeds cap.
+// whose cand_cnt exceeds cap; [16]/[17] += (query, vector) pairs screened in
+// round 1/2 and [18]/[19] += their 32 x 32 MFMA tiles (per list: the counts
+// cnt1/cnt2, capped at the compact bucket's length, against the list size).
 fgpu_status launch_tp_stats(const int* cand_cnt, const float* thr, int nvq, int cap, const int* flag_cnt,
+                            const int* cnt1, const int* cnt2, const int32_t* boff, const int32_t* offsets, int nlist,
                             unsigned long long* stats, hipStream_t s);
 // Workgroups a query for phase 1 (TwoPhaseArgs::split) for a launch of nq
 // queries: 1 once nq fills every CU twice; a test override can force it.

@@ -1014,9 +1014,15 @@ __global__ __launch_bounds__(256) void tp_collect_kernel(const uint32_t* __restr
 // Instrumentation of phase 1 through the screen: stats[11] += virtual
 // queries, [12] += their candidates (every count, also past the cap), [13] +=
 // those handed to the LUT kernel, [14] += those without a threshold, [15] +=
-// those with more candidates than cap.
+// those with more candidates than cap; per list l (cnt1/cnt2: its virtual
+// queries in rounds 1 and 2, at most its bucket's length), [16]/[17] +=
+// (query, vector) pairs screened in round 1/2 and [18]/[19] += 32 x 32 MFMA
+// tiles run.
 __global__ __launch_bounds__(256) void tp_stats_kernel(const int* __restrict__ cand_cnt, const float* __restrict__ thr,
                                                        int nvq, int cap, const int* __restrict__ flag_cnt,
+                                                       const int* __restrict__ cnt1, const int* __restrict__ cnt2,
+                                                       const int32_t* __restrict__ boff,
+                                                       const int32_t* __restrict__ offsets, int nlist,
                                                        unsigned long long* __restrict__ stats) {
   const int i = (int)blockIdx.x * 256 + (int)threadIdx.x;
   const int c = i < nvq ? cand_cnt[i] : 0;
@@ -1026,6 +1032,18 @@ __global__ __launch_bounds__(256) void tp_stats_kernel(const int* __restrict__ c
     if (sc) atomicAdd(&stats[12], (unsigned long long)sc);
     if (sn) atomicAdd(&stats[14], (unsigned long long)sn);
     if (so) atomicAdd(&stats[15], (unsigned long long)so);
+  }
+  if (i < nlist) {
+    const long long n = offsets[i + 1] - offsets[i], len = boff[i + 1] - boff[i];
+    const long long c1 = min((long long)cnt1[i], len), c2 = min((long long)cnt2[i], len);
+    if (c1 > 0) {
+      atomicAdd(&stats[16], (unsigned long long)(c1 * n));
+      atomicAdd(&stats[18], (unsigned long long)((c1 + 31) / 32 * ((n + 31) / 32)));
+    }
+    if (c2 > 0) {
+      atomicAdd(&stats[17], (unsigned long long)(c2 * n));
+      atomicAdd(&stats[19], (unsigned long long)((c2 + 31) / 32 * ((n + 31) / 32)));
+    }
   }
   if (i == 0) {
     atomicAdd(&stats[11], (unsigned long long)nvq);
@@ -1142,10 +1160,12 @@ fgpu_status launch_tp_collect(const uint32_t* probes, int nprobe, int p1, int nq
 }
 
 fgpu_status launch_tp_stats(const int* cand_cnt, const float* thr, int nvq, int cap, const int* flag_cnt,
+                            const int* cnt1, const int* cnt2, const int32_t* boff, const int32_t* offsets, int nlist,
                             unsigned long long* stats, hipStream_t s) {
   if (nvq <= 0 || !stats) return FGPU_OK;
-  hipLaunchKernelGGL(tp_stats_kernel, dim3((unsigned)((nvq + 255) / 256)), dim3(256), 0, s, cand_cnt, thr, nvq, cap,
-                     flag_cnt, stats);
+  const int nt = std::max(nvq, nlist);
+  hipLaunchKernelGGL(tp_stats_kernel, dim3((unsigned)((nt + 255) / 256)), dim3(256), 0, s, cand_cnt, thr, nvq, cap,
+                     flag_cnt, cnt1, cnt2, boff, offsets, nlist, stats);
   FGPU_HIP(hipGetLastError());
   return FGPU_OK;
 }

@@ -232,9 +232,11 @@ int fgpu_index_screen_ready(const fgpu_index* idx);
  *                       counters fgpu_search_screen_stats returns in
  *                       h_stats[8..15]; 0 default;
  *   FGPU_OPT_STAGE_EVENTS 1: fgpu_search records HIP events on its stream
- *                       between its stages (fgpu_search_stage_times); 0
- *                       default.  The events belong to the index, so calls
- *                       that overlap on one index overwrite each other's. */
+ *                       between its stages (fgpu_search_stage_times), and so
+ *                       does fgpu_two_phase_search when its phase 1 runs
+ *                       through the screen; 0 default.  The events belong to
+ *                       the index, so calls that overlap on one index
+ *                       overwrite each other's. */
 #define FGPU_OPT_LIST_SKIP 1
 #define FGPU_OPT_SPIN_LIMIT 2
 #define FGPU_OPT_SCREEN 3
@@ -246,7 +248,12 @@ fgpu_status fgpu_index_set_option(fgpu_index* idx, int option, int value);
  * stages (waits for it), h_ms[0..6] = coarse step, the screen's zeroing and
  * round-1 pairs, round 1, round-2 pairs, round 2, rescore, and the LUT kernel
  * (the whole scan when the call did not take the screen; the screen stages
- * are then 0).  No reference counterpart. */
+ * are then 0).  After an fgpu_two_phase_search whose phase 1 took the screen
+ * (the last call of the two on the index): h_ms[0] = the virtual queries'
+ * set-up, h_ms[1..5] the same screen stages, h_ms[6] the LUT hand-off, the
+ * pool fill and the second half of the two-phase kernel (threshold, phase 2,
+ * final select), for the last chunk of virtual queries.  No reference
+ * counterpart. */
 fgpu_status fgpu_search_stage_times(const fgpu_index* idx, float* h_ms, int n);
 
 /* ---- search without allocation ----------------------------------------- */
@@ -316,16 +323,18 @@ fgpu_status fgpu_two_phase_search_precut(const fgpu_index* idx, const float* d_q
                                          void* stream);
 
 /* fgpu_two_phase_search plus instrumentation (no reference counterpart): adds
- * to d_stats[0..15] (device, caller-zeroed, uint64) the vectors whose codes
+ * to d_stats[0..19] (device, caller-zeroed, uint64) the vectors whose codes
  * were loaded, the LUTs built, the phase-2 lists skipped by the list lower
  * bound, the phase-2 candidates appended, the shader clocks each workgroup
  * spent in set-up, phase 1, phase 2 and the final select + sort, and the
  * phase-1 clocks up to the LUT barrier, in the scan and in the merge; and
  * when phase 1 runs through the MFMA screen (limit_k <= 64, see
- * fgpu_two_phase_search), d_stats[11..15]: the virtual queries screened (one
+ * fgpu_two_phase_search), d_stats[11..19]: the virtual queries screened (one
  * per query and phase-1 probe), their candidates, those handed to the LUT
  * kernel, and of these the ones without a threshold and the ones with more
- * candidates than the screen keeps.  Results are unchanged. */
+ * candidates than the screen keeps; the (query, vector) pairs screened in
+ * rounds 1 and 2, and the 32 x 32 MFMA tiles run in rounds 1 and 2.  Results
+ * are unchanged. */
 fgpu_status fgpu_two_phase_search_stats(const fgpu_index* idx, const float* d_queries, int nq,
                                         const uint32_t* d_probe_ids, int nprobe, int p1_lists, int limit_k,
                                         float threshold_coeff, int rerank_m, int32_t* d_top_ids,
