@@ -209,8 +209,9 @@ struct TpScreenWs {
   float* vpd = nullptr;
   int32_t* vids = nullptr;
   float* vd = nullptr;
-  int* hist = nullptr;
+  int* hist = nullptr;  // [2 nlist + 1]: list counts, then launch_tp_order's fill counts
   int32_t* boff = nullptr;
+  int32_t* order = nullptr;
   ScreenWs sw;
   bool carve(void* base, size_t bytes, int nvq, int nlist, int dim, int k) {
     Carve cv(base, bytes);
@@ -219,15 +220,17 @@ struct TpScreenWs {
     vpd = cv.take<float>((size_t)nvq);
     vids = cv.take<int32_t>((size_t)nvq * k);
     vd = cv.take<float>((size_t)nvq * k);
-    hist = cv.take<int>((size_t)nlist);
+    hist = cv.take<int>(2 * (size_t)nlist + 1);
     boff = cv.take<int32_t>((size_t)nlist + 1);
+    order = cv.take<int32_t>((size_t)nvq);
     return cv.ok() && sw.carve(cv.base + cv.used, bytes - cv.used, nvq, nlist, 1, true);
   }
   static size_t bytes(int nvq, int nlist, int dim, int k) {
     return carve_bytes<float>((size_t)nvq * dim) + carve_bytes<uint32_t>((size_t)nvq) +
            carve_bytes<float>((size_t)nvq) + carve_bytes<int32_t>((size_t)nvq * k) +
-           carve_bytes<float>((size_t)nvq * k) + carve_bytes<int>((size_t)nlist) +
-           carve_bytes<int32_t>((size_t)nlist + 1) + ScreenWs::bytes(nvq, nlist, 1, true);
+           carve_bytes<float>((size_t)nvq * k) + carve_bytes<int>(2 * (size_t)nlist + 1) +
+           carve_bytes<int32_t>((size_t)nlist + 1) + carve_bytes<int32_t>((size_t)nvq) +
+           ScreenWs::bytes(nvq, nlist, 1, true);
   }
 };
 
@@ -795,6 +798,7 @@ fgpu_status two_phase(const fgpu_index* ix, const float* dq, int nq, const uint3
             FGPU_TRY(launch_tp_virtual(qq + (int64_t)s0 * ix->dim, ix->dim, pp + (int64_t)s0 * nprobe, nprobe, p1, ns,
                                        ix->d_offsets, ix->nlist, tw.vq, tw.vprobe, tw.vpd, tw.hist, s));
             FGPU_TRY(launch_tp_offsets(tw.hist, ix->nlist, tw.boff, s));
+            FGPU_TRY(launch_tp_order(tw.vprobe, nvq, ix->nlist, tw.boff, tw.hist + ix->nlist, tw.order, s));
             FGPU_HIP(mark(1));
             ScreenArgs sa{tw.vq, ix->d_centroids, ix->d_offsets, ix->d_codes, ix->d_ids, ix->d_codebook, ix->d_cb16,
                           ix->d_vext, ix->d_rmax, tw.vprobe, tw.vpd, nvq, 1, limit_k, ix->nlist};
@@ -806,6 +810,7 @@ fgpu_status two_phase(const fgpu_index* ix, const float* dq, int nq, const uint3
             sa.gminbuf = tw.sw.gminbuf;
             sa.bucket = tw.sw.bucket;
             sa.boff = tw.boff;
+            sa.order = tw.order;
             sa.arec = tw.sw.arec;
             sa.thr = tw.sw.thr;
             sa.cand = tw.sw.cand;

@@ -153,6 +153,10 @@ struct ScreenArgs {
   // entries at bucket[boff[l] .. boff[l + 1]) (boff[l + 1] - boff[l] = the
   // queries whose probe is l); nullptr = bucket[l nq + pos].
   const int32_t* boff = nullptr;
+  // The rescore's order of the queries (a permutation of 0 .. nq-1, e.g.
+  // single-probe queries grouped by list so a list's codes stay in L2);
+  // nullptr = ascending.
+  const int32_t* order = nullptr;
   uint4* arec;              // [nq nprobe][2][9] pair records: per lane half 8 A fragments and the extra block
   int2* first;              // [nq] round 1: (list, bucket position) of the query's pair, or (-1, -1)
   uint32_t* gminbuf;        // [nq][kMaxChunks][64] round 1: per query, first-list chunk and group, min U bits
@@ -238,6 +242,12 @@ fgpu_status launch_tp_collect(const uint32_t* probes, int nprobe, int p1, int nq
                               int limit_k, const int32_t* vids, const float* vd, uint64_t* pool, int pool_cap,
                               float* cut_ws, hipStream_t s);
 fgpu_status launch_two_phase_after_phase1(int dim, int m, const TwoPhaseArgs& a, hipStream_t s);
+// order[0 .. nvq): the virtual queries grouped by list (list l's at
+// boff[l] .. boff[l + 1), in no fixed order within it), those without a
+// usable list last; fill: 2 nlist + 1 ints of which the last nlist + 1 are
+// zero (launch_tp_virtual zeroes them).
+fgpu_status launch_tp_order(const uint32_t* vprobe, int nvq, int nlist, const int32_t* boff, int* fill,
+                            int32_t* order, hipStream_t s);
 // stats[11] += nvq, [12] += the sum of cand_cnt[0..nvq), [13] += *flag_cnt,
 // [14] += entries of thr[0..nvq) that are not below +inf, [15] += the others
 // whose cand_cnt exceeds cap; [16]/[17] += (query, vector) pairs screened in

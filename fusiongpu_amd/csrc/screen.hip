@@ -855,7 +855,7 @@ __device__ __forceinline__ void load_row(const float* p, float (&v)[S]) {
 // reference's direct form (the LUT entry's chain per subspace, summed in
 // ascending m), then the k smallest (distance, id) keys.  A persistent grid
 // of one workgroup per CU holding the fp32 codebook in LDS; wave g takes
-// queries g, g + G, ...  ONE (single-probe queries): every candidate lies in
+// queries g, g + G, ... (of a.order when set).  ONE (single-probe queries): every candidate lies in
 // the query's one list, so the residual r = fl(q - c) is formed once in LDS
 // (the same fp32 subtraction) instead of loading the centroid per candidate.
 constexpr int kRW = 16;  // waves per rescore workgroup
@@ -868,7 +868,12 @@ __global__ __launch_bounds__(kRW * kWave) void rescore_kernel(ScreenArgs a) {
   for (int i = threadIdx.x; i < D * kPQK / 4; i += kRW * kWave)
     reinterpret_cast<float4*>(cbf)[i] = reinterpret_cast<const float4*>(a.codebook)[i];
   __syncthreads();
-  for (int q = (int)blockIdx.x * kRW + wave; q < a.nq; q += (int)gridDim.x * kRW) {
+  const int stride = (int)gridDim.x * kRW;
+  int i = (int)blockIdx.x * kRW + wave;
+  int qn = i < a.nq ? (a.order ? a.order[i] : i) : 0;
+  for (; i < a.nq; i += stride) {
+    const int q = __builtin_amdgcn_readfirstlane(qn);
+    if (i + stride < a.nq) qn = a.order ? a.order[i + stride] : i + stride;  // the next query's index, early
     const float T = a.thr[q];
     const int cnt = __builtin_amdgcn_readfirstlane(a.cand_cnt[q]);
     if (!(T < INFINITY) || cnt > a.cand_cap) {

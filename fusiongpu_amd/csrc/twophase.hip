@@ -941,6 +941,29 @@ __global__ __launch_bounds__(256) void tp_virtual_kernel(const float4* __restric
   }
 }
 
+// The virtual queries grouped by list: list l's take order[boff[l] ..
+// boff[l + 1]) through its fill count, those without a usable list the slots
+// from boff[nlist] on.
+__global__ __launch_bounds__(256) void tp_order_kernel(const uint32_t* __restrict__ vprobe, int nvq, int nlist,
+                                                       const int32_t* __restrict__ boff, int* __restrict__ fill,
+                                                       int32_t* __restrict__ order) {
+  const int v = (int)blockIdx.x * 256 + (int)threadIdx.x;
+  const uint32_t l = v < nvq ? vprobe[v] : 0u;
+  const bool none = v < nvq && l >= (uint32_t)nlist;
+  // the queries without a list share one count: one atomic a wave for them
+  const uint64_t bm = __ballot(none);
+  int base = 0;
+  if (bm) {
+    if ((threadIdx.x & 63) == (unsigned)__builtin_ctzll(bm)) base = atomicAdd(&fill[nlist], __popcll(bm));
+    base = __shfl(base, __builtin_ctzll(bm), kWave);
+  }
+  if (v >= nvq) return;
+  if (none)
+    order[boff[nlist] + base + __popcll(bm & ((1ull << (threadIdx.x & 63)) - 1ull))] = v;
+  else
+    order[boff[l] + atomicAdd(&fill[l], 1)] = v;
+}
+
 // boff[l] = hist[0] + ... + hist[l - 1] for l = 0 .. nlist (one workgroup,
 // nlist <= 8192: each thread sums 8 consecutive counts).
 __global__ __launch_bounds__(1024) void tp_offsets_kernel(const int* __restrict__ hist, int nlist,
@@ -1132,7 +1155,9 @@ fgpu_status launch_tp_virtual(const float* queries, int dim, const uint32_t* pro
                               hipStream_t s) {
   FGPU_CHECK(dim % 4 == 0 && p1 >= 1 && nlist >= 1 && nlist <= 8192, FGPU_ERR_ARG, "two_phase: bad virtual queries");
   if (nqc <= 0) return FGPU_OK;
-  hipLaunchKernelGGL(tp_zero_kernel, dim3((unsigned)((nlist + 255) / 256)), dim3(256), 0, s, hist, nlist);
+  // hist, then the fill counts of launch_tp_order (2 nlist + 1 ints)
+  hipLaunchKernelGGL(tp_zero_kernel, dim3((unsigned)((2 * nlist + 1 + 255) / 256)), dim3(256), 0, s, hist,
+                     2 * nlist + 1);
   const int64_t nvq = (int64_t)nqc * p1, nt = nvq * (dim / 4);
   hipLaunchKernelGGL(tp_virtual_kernel, dim3((unsigned)((nt + 255) / 256)), dim3(256), 0, s,
                      reinterpret_cast<const float4*>(queries), dim / 4, probes, nprobe, p1, (int)nvq, offsets, nlist,
@@ -1144,6 +1169,15 @@ fgpu_status launch_tp_virtual(const float* queries, int dim, const uint32_t* pro
 fgpu_status launch_tp_offsets(const int* hist, int nlist, int32_t* boff, hipStream_t s) {
   FGPU_CHECK(nlist >= 1 && nlist <= 8192, FGPU_ERR_ARG, "two_phase: bad list count");
   hipLaunchKernelGGL(tp_offsets_kernel, dim3(1), dim3(1024), 0, s, hist, nlist, boff);
+  FGPU_HIP(hipGetLastError());
+  return FGPU_OK;
+}
+
+fgpu_status launch_tp_order(const uint32_t* vprobe, int nvq, int nlist, const int32_t* boff, int* fill,
+                            int32_t* order, hipStream_t s) {
+  if (nvq <= 0) return FGPU_OK;
+  hipLaunchKernelGGL(tp_order_kernel, dim3((unsigned)((nvq + 255) / 256)), dim3(256), 0, s, vprobe, nvq, nlist, boff,
+                     fill, order);
   FGPU_HIP(hipGetLastError());
   return FGPU_OK;
 }
