@@ -730,11 +730,13 @@ size_t fgpu_two_phase_workspace_bytes(int nq, int nprobe, int p1_lists, int limi
   const size_t rows = (size_t)std::max(nq, 1);
   // Each query's candidate pool, then its phase-1 cutoffs (split phase 1),
   // then (limit_k <= 64) the buffers of phase 1 through the screen for up to
-  // kTpVqMax virtual queries, sized for the largest lists count and dim.
+  // kTpVqMax virtual queries, sized for the largest lists count and dim, and
+  // the list of queries that take the general second half.
   size_t b = carve_bytes<uint64_t>(rows * two_phase_pool_cap(p1, limit_k, rerank_m)) +
              carve_bytes<float>(rows * (size_t)std::max(nprobe, 1));
   if (limit_k >= 1 && limit_k <= 64 && p1 >= 1)
-    b += TpScreenWs::bytes((int)std::min<int64_t>((int64_t)rows * p1, kTpVqMax), kScreenMaxLists, 128, limit_k) + 1024;
+    b += TpScreenWs::bytes((int)std::min<int64_t>((int64_t)rows * p1, kTpVqMax), kScreenMaxLists, 128, limit_k) +
+         carve_bytes<int32_t>(rows + 1) + 1024;
   return b;
 }
 
@@ -745,7 +747,7 @@ fgpu_status two_phase(const fgpu_index* ix, const float* dq, int nq, const uint3
                       int p1_lists, int limit_k, float threshold_coeff, int rerank_m, int32_t* d_top_ids,
                       float* d_top_dists, int32_t* d_top_counts, float* d_list_cutoffs, float* d_thresholds,
                       unsigned long long* d_stats, void* ws, size_t ws_bytes, void* stream,
-                      int32_t* d_pre_cut = nullptr) {
+                      int32_t* d_pre_cut = nullptr, const float* d_probe_dists = nullptr) {
   FGPU_CHECK(ix && ws && (nq == 0 || (dq && d_probe_ids && d_top_ids && d_top_dists && d_top_counts)), FGPU_ERR_ARG,
              "two_phase_search: null argument");
   FGPU_CHECK(nq >= 0 && nprobe >= 1 && nprobe <= 256, FGPU_ERR_ARG, "two_phase_search: need 1 <= nprobe <= 256");
@@ -773,22 +775,35 @@ fgpu_status two_phase(const fgpu_index* ix, const float* dq, int nq, const uint3
     const int qv = std::max(1, kTpVqMax / p1);  // queries a virtual-query chunk
     const int nvq_max = (int)std::min<int64_t>((int64_t)nq, qv) * p1;
     const size_t tbytes = TpScreenWs::bytes(nvq_max, ix->nlist, ix->dim, limit_k);
-    const size_t per_q = (size_t)cap * sizeof(uint64_t) + nprobe * sizeof(float);
-    if (ws_bytes > tbytes + 2 * 256 + per_q) {
+    const size_t per_q = (size_t)cap * sizeof(uint64_t) + nprobe * sizeof(float) + sizeof(int32_t);
+    if (ws_bytes > tbytes + 3 * 256 + per_q) {
       const size_t tofs = align_up(ws_bytes - tbytes, 256) - 256;  // 256-aligned, inside the workspace
       char* tbase = static_cast<char*>(ws) + tofs;
+      // per query chunk: pools, cutoff rows, and the list of queries that
+      // take the general second half (its count first)
       auto need = [&](int64_t c) {
-        return carve_bytes<uint64_t>((size_t)c * cap) + carve_bytes<float>((size_t)c * nprobe);
+        return carve_bytes<uint64_t>((size_t)c * cap) + carve_bytes<float>((size_t)c * nprobe) +
+               carve_bytes<int32_t>((size_t)c + 1);
       };
       int64_t chunk = std::min<int64_t>(nq, (int64_t)(tofs / per_q));
       while (chunk > 0 && need(chunk) > tofs) --chunk;
       if (chunk >= 1) {
-        float* cut_ws = reinterpret_cast<float*>(static_cast<char*>(ws) + carve_bytes<uint64_t>((size_t)chunk * cap));
-        uint64_t* pool = reinterpret_cast<uint64_t*>(ws);
+        Carve pc(ws, tofs);
+        uint64_t* pool = pc.take<uint64_t>((size_t)chunk * cap);
+        float* cut_ws = pc.take<float>((size_t)chunk * nprobe);
+        int32_t* slow = pc.take<int32_t>((size_t)chunk + 1);  // [0]: count, then the queries
         for (int64_t q0 = 0; q0 < nq; q0 += chunk) {
           const int nb = (int)std::min<int64_t>(chunk, nq - q0);
           const float* qq = dq + q0 * ix->dim;
           const uint32_t* pp = d_probe_ids + q0 * nprobe;
+          TwoPhaseArgs a{qq, ix->d_centroids, ix->d_codebook, ix->d_offsets, ix->d_codes, ix->d_ids, pp, ix->d_rmax,
+                         nb, nprobe, ix->nlist, p1, limit_k, threshold_coeff, rerank_m, pool, cap,
+                         d_top_ids + q0 * rerank_m, d_top_dists + q0 * rerank_m, d_top_counts + q0,
+                         d_list_cutoffs ? d_list_cutoffs + q0 * p1 : nullptr,
+                         d_thresholds ? d_thresholds + q0 : nullptr, d_stats};
+          a.cut_ws = cut_ws;
+          a.pre_cut = d_pre_cut ? d_pre_cut + q0 : nullptr;
+          FGPU_TRY(launch_tp_zero(slow, 1, s));
           for (int s0 = 0; s0 < nb; s0 += qv) {
             const int ns = std::min(qv, nb - s0), nvq = ns * p1;
             TpScreenWs tw;
@@ -826,16 +841,12 @@ fgpu_status two_phase(const fgpu_index* ix, const float* dq, int nq, const uint3
             FGPU_TRY(launch_adc_plain_list(ix->dim, ix->m, la, s));
             FGPU_TRY(launch_tp_stats(sa.cand_cnt, sa.thr, nvq, kScreenCandCap, tw.sw.zero + kCtrFlag, sa.cnt1,
                                      sa.cnt2, tw.boff, ix->d_offsets, ix->nlist, d_stats, s));
-            FGPU_TRY(launch_tp_collect(pp + (int64_t)s0 * nprobe, nprobe, p1, ns, ix->d_offsets, ix->nlist, limit_k,
-                                       tw.vids, tw.vd, pool + (size_t)s0 * cap, cap, cut_ws + (size_t)s0 * nprobe, s));
+            FGPU_TRY(launch_tp_finish(a, ix->dim, s0, ns, tw.vids, tw.vd,
+                                      d_probe_dists ? d_probe_dists + q0 * nprobe : nullptr, slow + 1, slow, s));
           }
-          TwoPhaseArgs a{qq, ix->d_centroids, ix->d_codebook, ix->d_offsets, ix->d_codes, ix->d_ids, pp, ix->d_rmax,
-                         nb, nprobe, ix->nlist, p1, limit_k, threshold_coeff, rerank_m, pool, cap,
-                         d_top_ids + q0 * rerank_m, d_top_dists + q0 * rerank_m, d_top_counts + q0,
-                         d_list_cutoffs ? d_list_cutoffs + q0 * p1 : nullptr,
-                         d_thresholds ? d_thresholds + q0 : nullptr, d_stats};
-          a.cut_ws = cut_ws;
-          a.pre_cut = d_pre_cut ? d_pre_cut + q0 : nullptr;
+          // the queries whose phase 2 may append, or whose keys need a select
+          a.qlist = slow + 1;
+          a.qcount = slow;
           FGPU_TRY(launch_two_phase_after_phase1(ix->dim, ix->m, a, s));
         }
         FGPU_HIP(mark(kStageEvents - 1));
@@ -957,8 +968,9 @@ fgpu_status fgpu_search_rerank(const fgpu_index* ix, const float* dq, int nq, in
   void* rest = cv.base + cv.used;
   const size_t rest_bytes = ws_bytes - cv.used;
   FGPU_TRY(fgpu_coarse_search(ix, dq, nq, nprobe, prune_ratio, pid, pd, rest, rest_bytes, stream));
-  FGPU_TRY(fgpu_two_phase_search(ix, dq, nq, pid, nprobe, p1_lists, limit_k, threshold_coeff, rerank_m, tid, tdist,
-                                 tcnt, nullptr, nullptr, rest, rest_bytes, stream));
+  // the coarse step's probe distances give the phase-2 list bounds
+  FGPU_TRY(two_phase(ix, dq, nq, pid, nprobe, p1_lists, limit_k, threshold_coeff, rerank_m, tid, tdist, tcnt, nullptr,
+                     nullptr, nullptr, rest, rest_bytes, stream, nullptr, pd));
   return fgpu_rerank(dq, nq, ix->dim, d_base, n, tid, tcnt, rerank_m, k, mini_batch, eps, beta, d_out_ids,
                      d_out_dists, nullptr, stream);
 }

@@ -224,23 +224,23 @@ struct TwoPhaseArgs {
   // and ends sums against thr itself rather than the pool's admission bound,
   // so that every such vector is seen.
   int32_t* pre_cut = nullptr;
+  // Mode 2 (after a separate phase 1) over the queries qlist[0 .. *qcount)
+  // only (workgroup i takes qlist[i]; nullptr = every query).
+  const int32_t* qlist = nullptr;
+  const int* qcount = nullptr;
 };
 int two_phase_pool_cap(int p1, int limit_k, int rerank_m);
 // Phase 1 through the screen: virtual query v = q p1 + p for the nqc queries
 // of a chunk (the query row copied to vq, probe p in vprobe, 0xFFFFFFFF when
 // unusable, a zero probe distance in vpd) and each usable list's count in
-// hist (zeroed first); boff = the exclusive scan of hist (nlist + 1 entries);
-// then each query's usable phase-1 lists get their w = min(n, limit_k) best
-// keys from (vids, vd) [nvq][limit_k] in their pool slots and their cutoffs
-// in cut_ws [nqc][nprobe]; launch_two_phase_after_phase1 runs the threshold,
-// phase 2 and the final select on them (limit_k <= 64).
+// hist (zeroed first); boff = the exclusive scan of hist (nlist + 1 entries).
+// After the screen, launch_tp_finish completes most queries and leaves the
+// others' pool slots and cutoffs to launch_two_phase_after_phase1, which
+// runs the threshold, phase 2 and the final select (limit_k <= 64).
 fgpu_status launch_tp_virtual(const float* queries, int dim, const uint32_t* probes, int nprobe, int p1, int nqc,
                               const int32_t* offsets, int nlist, float* vq, uint32_t* vprobe, float* vpd, int* hist,
                               hipStream_t s);
 fgpu_status launch_tp_offsets(const int* hist, int nlist, int32_t* boff, hipStream_t s);
-fgpu_status launch_tp_collect(const uint32_t* probes, int nprobe, int p1, int nqc, const int32_t* offsets, int nlist,
-                              int limit_k, const int32_t* vids, const float* vd, uint64_t* pool, int pool_cap,
-                              float* cut_ws, hipStream_t s);
 fgpu_status launch_two_phase_after_phase1(int dim, int m, const TwoPhaseArgs& a, hipStream_t s);
 // order[0 .. nvq): the virtual queries grouped by list (list l's at
 // boff[l] .. boff[l + 1), in no fixed order within it), those without a
@@ -248,6 +248,16 @@ fgpu_status launch_two_phase_after_phase1(int dim, int m, const TwoPhaseArgs& a,
 // zero (launch_tp_virtual zeroes them).
 fgpu_status launch_tp_order(const uint32_t* vprobe, int nvq, int nlist, const int32_t* boff, int* fill,
                             int32_t* order, hipStream_t s);
+// The second half of the two-phase scan for queries q_base .. q_base + nqc - 1
+// of a (phase 1 done by the screen: virtual query (q - q_base) p1 + p holds
+// probe p's top-limit_k in vids/vd): threshold, phase-2 list bounds (from
+// probe_dists[q][p] when given, else from the centroids) and, when no
+// phase-2 list can reach the threshold and the phase-1 keys fit rerank_m,
+// the final ranking; any other query gets its pool slots and cutoffs and
+// joins slow_list (slow_cnt counts them) for launch_two_phase_after_phase1.
+fgpu_status launch_tp_finish(const TwoPhaseArgs& a, int dim, int q_base, int nqc, const int32_t* vids, const float* vd,
+                             const float* probe_dists, int32_t* slow_list, int* slow_cnt, hipStream_t s);
+fgpu_status launch_tp_zero(int* p, int n, hipStream_t s);
 // stats[11] += nvq, [12] += the sum of cand_cnt[0..nvq), [13] += *flag_cnt,
 // [14] += entries of thr[0..nvq) that are not below +inf, [15] += the others
 // whose cand_cnt exceeds cap; [16]/[17] += (query, vector) pairs screened in

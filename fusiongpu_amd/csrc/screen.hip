@@ -404,7 +404,13 @@ __global__ __launch_bounds__(256) void screen_pairs2_kernel(ScreenArgs a) {
     const int n = a.offsets[f.x + 1] - a.offsets[f.x];
     const int per = chunk_len(n), nch = (n + per - 1) / per;
     const uint32_t* g = a.gminbuf + (size_t)q * kMaxChunks * kMaxGroups + lane;
-    for (int c = 0; c < nch; ++c) gm = min(gm, g[c * kMaxGroups]);
+    // every chunk's load issued at once (a chain of them is the kernel's
+    // longest latency)
+    uint32_t gc[kMaxChunks];
+#pragma unroll
+    for (int c = 0; c < kMaxChunks; ++c) gc[c] = c < nch ? g[c * kMaxGroups] : 0x7F800000u;
+#pragma unroll
+    for (int c = 0; c < kMaxChunks; ++c) gm = min(gm, gc[c]);
   }
   // U >= 0, so float order is unsigned order of the bits
   wave_sort_u32(gm);

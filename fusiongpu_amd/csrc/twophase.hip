@@ -188,7 +188,11 @@ void two_phase_kernel(TwoPhaseArgs a) {
   // and runs the threshold, phase 2 and the final select.  MODE 0 does it
   // all in one workgroup (separate instantiations keep its code as it is).
   constexpr int mode = MODE;
-  const int q = mode == 1 ? (int)blockIdx.x / a.split : (int)blockIdx.x;
+  int q = mode == 1 ? (int)blockIdx.x / a.split : (int)blockIdx.x;
+  if (mode == 2 && a.qlist) {  // uniform over the workgroup, before any barrier
+    if ((int)blockIdx.x >= *a.qcount) return;
+    q = a.qlist[blockIdx.x];
+  }
   const int gsub = mode == 1 ? (int)blockIdx.x % a.split : 0;
   const int gstep = mode == 1 ? a.split : 1;
   const int P = a.nprobe, p1 = a.p1, R = a.rerank_m, cap = a.pool_cap, K1 = a.limit_k;
@@ -995,42 +999,203 @@ __global__ __launch_bounds__(1024) void tp_offsets_kernel(const int* __restrict_
   }
 }
 
-// One wave a query of the chunk: the usable phase-1 probes in probe order
-// (in range, non-empty), each with w = min(n, limit_k) pool slots after the
-// earlier ones'; the w best keys of its virtual query (ascending) go to
-// them and its w-th distance to cut_ws[q][p], as the split phase 1 leaves
-// them (two_phase_kernel, mode 1).
-__global__ __launch_bounds__(256) void tp_collect_kernel(const uint32_t* __restrict__ probes, int P, int p1, int nqc,
-                                                         const int32_t* __restrict__ offsets, int nlist, int K1,
-                                                         const int32_t* __restrict__ vids, const float* __restrict__ vd,
-                                                         uint64_t* __restrict__ pool, int cap,
-                                                         float* __restrict__ cut_ws) {
+// The second half of the two-phase scan when phase 1 ran through the screen,
+// one wave a query (queries q_base + ql, ql < nqc; probe p's phase-1 result
+// is virtual query ql p1 + p's ascending top-limit_k in vids/vd).  As the
+// two-phase kernel's mode 2 does: each phase-1 cutoff is the w-th distance of
+// a usable phase-1 probe (w = min(n, limit_k); 0 for the others) and the
+// threshold is coeff times the smallest positive cutoff.  Then every usable
+// phase-2 list's lower bound (list_lower_bound; any valid one skips the same
+// lists' appends, since none of their vectors reaches the threshold): when
+// none is <= thr (1 + 2^-16) -- the mode-2 skip test -- phase 2 appends
+// nothing, and when the phase-1 keys also fit rerank_m they are the answer,
+// sorted: each usable phase-1 probe's keys are one 64-lane vector (padded
+// with kNoKey, odd vectors reversed), and a bitonic network over the vectors
+// (across vectors elementwise, within one by lane exchanges) sorts them, as
+// the mode-2 final sort does (equal keys are equal outputs); then padding to
+// rerank_m.  Other queries (a list that can reach the threshold, more keys
+// than rerank_m, more than kFinRuns phase-1 lists) get their pool slots and
+// cutoffs as the split phase 1 leaves them and go to slow_list.
+constexpr int kFinWaves = 4;
+constexpr int kFinRuns = 16;  // usable phase-1 probes the wave sorts (64-key vectors)
+
+// Ascending sort of the NV x 64 keys x[v] (lane j: flat position 64 v + j),
+// each vector already sorted, ascending for even v and descending for odd v.
+template <int NV>
+__device__ __forceinline__ void wave_sort_vectors(uint64_t (&x)[NV]) {
+#pragma unroll
+  for (int size = 128; size <= 64 * NV; size <<= 1) {
+#pragma unroll
+    for (int sv = size / 128; sv >= 1; sv >>= 1) {
+#pragma unroll
+      for (int v = 0; v < NV; ++v) {
+        if ((v & sv) == 0) {
+          const bool up = size == 64 * NV || ((64 * v) & size) == 0;
+          const uint64_t p = x[v], q = x[v + sv];
+          const bool sw = (p > q) == up;
+          x[v] = sw ? q : p;
+          x[v + sv] = sw ? p : q;
+        }
+      }
+    }
+#pragma unroll
+    for (int v = 0; v < NV; ++v) bitonic_pass_k<64>(x[v], size == 64 * NV || ((64 * v) & size) == 0);
+  }
+}
+
+template <int NV>
+__device__ __forceinline__ void fin_sort_write(const TwoPhaseArgs& a, int q, int ql, int nrun, int total,
+                                               const int* rp, const int* rw, const int32_t* __restrict__ vids,
+                                               const float* __restrict__ vd) {
   const int lane = threadIdx.x & 63;
-  const int q = (int)blockIdx.x * 4 + (int)(threadIdx.x >> 6);
-  if (q >= nqc) return;
-  int base = 0;
+  const int p1 = a.p1, K1 = a.limit_k;
+  uint64_t x[NV];
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+    x[v] = kNoKey;
+    if (v < nrun) {
+      const int w = rw[v];
+      // even vectors ascending (keys, then padding), odd ones descending
+      const int j = (v & 1) ? kWave - 1 - lane : lane;
+      if (j < w) {
+        const size_t e = ((size_t)ql * p1 + rp[v]) * K1 + j;
+        x[v] = key_of(vd[e], vids[e]);
+      }
+    }
+  }
+  wave_sort_vectors<NV>(x);
+  int32_t* out_id = a.top_ids + (size_t)q * a.rerank_m;
+  float* out_d = a.top_d + (size_t)q * a.rerank_m;
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+    const int i = v * kWave + lane;
+    if (i < total) {
+      out_id[i] = (int32_t)(uint32_t)x[v];
+      out_d[i] = __uint_as_float((uint32_t)(x[v] >> 32));
+    }
+  }
+}
+
+__global__ __launch_bounds__(kFinWaves * kWave) void tp_finish_kernel(TwoPhaseArgs a, int dim, int q_base, int nqc,
+                                                                      const int32_t* __restrict__ vids,
+                                                                      const float* __restrict__ vd,
+                                                                      const float* __restrict__ pd,
+                                                                      int32_t* __restrict__ slow_list,
+                                                                      int* __restrict__ slow_cnt) {
+  __shared__ int rp[kFinWaves][kFinRuns];  // vector (run) -> phase-1 probe index
+  __shared__ int rw[kFinWaves][kFinRuns];  // its key count
+  const int lane = threadIdx.x & 63, wv = (int)(threadIdx.x >> 6);
+  const int ql = (int)blockIdx.x * kFinWaves + wv;
+  if (ql >= nqc) return;  // no workgroup barrier below
+  const int q = q_base + ql;
+  const int P = a.nprobe, p1 = a.p1, K1 = a.limit_k, R = a.rerank_m;
+  const uint32_t NL = (uint32_t)a.nlist;
+  const uint32_t* pr = a.probes + (size_t)q * P;
+  float mcut = FLT_MAX;
+  int nrun = 0, total = 0;
   for (int c0 = 0; c0 < p1; c0 += kWave) {
     const int p = c0 + lane;
     int w = 0;
+    float cut = 0.0f;
     if (p < p1) {
-      const uint32_t l = probes[(size_t)q * P + p];
-      if (l < (uint32_t)nlist) {
-        const int n = offsets[l + 1] - offsets[l];
+      const uint32_t l = pr[p];
+      if (l < NL) {
+        const int n = a.offsets[l + 1] - a.offsets[l];
         w = n < K1 ? n : K1;
       }
+      if (w > 0) cut = vd[((size_t)ql * p1 + p) * K1 + w - 1];
+      if (a.cutoffs) a.cutoffs[(size_t)q * p1 + p] = cut;
     }
-    const int incl = wave_incl_scan(w);
-    const int mine = base + incl - w;
-    uint64_t m = __ballot(w > 0);
-    while (m) {
-      const int b = __ffsll((unsigned long long)m) - 1;
-      m &= m - 1;
-      const int wb = readlane_i(w, b), bb = readlane_i(mine, b);
-      const size_t v = ((size_t)q * p1 + c0 + b) * K1;
-      if (lane < wb) pool[(size_t)q * cap + bb + lane] = key_of(vd[v + lane], vids[v + lane]);
-      if (lane == 0) cut_ws[(size_t)q * P + c0 + b] = vd[v + wb - 1];
+    if (cut > 0.0f && cut < mcut) mcut = cut;
+    const uint64_t bm = __ballot(w > 0);
+    const int idx = nrun + __popcll(bm & ((1ull << lane) - 1ull));
+    if (w > 0 && idx < kFinRuns) {
+      rp[wv][idx] = p;
+      rw[wv][idx] = w;
     }
-    base += readlane_i(incl, kWave - 1);
+    nrun += __popcll(bm);
+    total += wave_sum_i(w);
+  }
+  mcut = wave_min_f(mcut);
+  const float thr = mcut < FLT_MAX ? mcut * a.coeff : FLT_MAX;
+  const float thr_hi = thr * (1.0f + 0x1p-16f);
+  bool slow = nrun > kFinRuns || total > R;
+  int skipped = 0;
+  for (int c0 = p1; !slow && c0 < P; c0 += kWave) {
+    const int p = c0 + lane;
+    bool use = false, reach = false;
+    if (p < P) {
+      const uint32_t l = pr[p];
+      if (l < NL && a.offsets[l + 1] > a.offsets[l]) {
+        use = true;
+        float s2 = 0.0f;
+        if (pd) {
+          s2 = pd[(size_t)q * P + p];
+        } else {
+          const float4* qv = reinterpret_cast<const float4*>(a.queries + (size_t)q * dim);
+          const float4* cv = reinterpret_cast<const float4*>(a.centroids + (size_t)l * dim);
+          for (int d = 0; d < dim / 4; ++d) {
+            const float4 x = qv[d], c = cv[d];
+            const float r0 = x.x - c.x, r1 = x.y - c.y, r2 = x.z - c.z, r3 = x.w - c.w;
+            s2 += r0 * r0 + r1 * r1 + r2 * r2 + r3 * r3;
+          }
+        }
+        reach = list_lower_bound(s2, a.rmax[l]) <= thr_hi;
+      }
+    }
+    slow = __ballot(reach) != 0;
+    skipped += __popcll(__ballot(use));
+  }
+  if (slow) {
+    int base = 0;
+    for (int c0 = 0; c0 < p1; c0 += kWave) {
+      const int p = c0 + lane;
+      int w = 0;
+      if (p < p1) {
+        const uint32_t l = pr[p];
+        if (l < NL) {
+          const int n = a.offsets[l + 1] - a.offsets[l];
+          w = n < K1 ? n : K1;
+        }
+      }
+      const int incl = wave_incl_scan(w);
+      const int mine = base + incl - w;
+      uint64_t m = __ballot(w > 0);
+      while (m) {
+        const int b = __ffsll((unsigned long long)m) - 1;
+        m &= m - 1;
+        const int wb = readlane_i(w, b), bb = readlane_i(mine, b);
+        const size_t v = ((size_t)ql * p1 + c0 + b) * K1;
+        if (lane < wb) a.pool[(size_t)q * a.pool_cap + bb + lane] = key_of(vd[v + lane], vids[v + lane]);
+        if (lane == 0) a.cut_ws[(size_t)q * P + c0 + b] = vd[v + wb - 1];
+      }
+      base += readlane_i(incl, kWave - 1);
+    }
+    if (lane == 0) slow_list[atomicAdd(slow_cnt, 1)] = q;
+    return;
+  }
+  if (lane == 0) {
+    if (a.thr) a.thr[q] = thr;
+    if (a.pre_cut) a.pre_cut[q] = total;
+    a.top_counts[q] = total;
+    if (a.stats && skipped) atomicAdd(&a.stats[2], (unsigned long long)skipped);
+  }
+  wave_lds_sync();  // rp, rw
+  if (nrun <= 1)
+    fin_sort_write<1>(a, q, ql, nrun, total, rp[wv], rw[wv], vids, vd);
+  else if (nrun <= 2)
+    fin_sort_write<2>(a, q, ql, nrun, total, rp[wv], rw[wv], vids, vd);
+  else if (nrun <= 4)
+    fin_sort_write<4>(a, q, ql, nrun, total, rp[wv], rw[wv], vids, vd);
+  else if (nrun <= 8)
+    fin_sort_write<8>(a, q, ql, nrun, total, rp[wv], rw[wv], vids, vd);
+  else
+    fin_sort_write<16>(a, q, ql, nrun, total, rp[wv], rw[wv], vids, vd);
+  int32_t* out_id = a.top_ids + (size_t)q * R;
+  float* out_d = a.top_d + (size_t)q * R;
+  for (int j = total + lane; j < R; j += kWave) {
+    out_id[j] = -1;
+    out_d[j] = FLT_MAX;
   }
 }
 
@@ -1173,22 +1338,29 @@ fgpu_status launch_tp_offsets(const int* hist, int nlist, int32_t* boff, hipStre
   return FGPU_OK;
 }
 
+fgpu_status launch_tp_finish(const TwoPhaseArgs& a, int dim, int q_base, int nqc, const int32_t* vids, const float* vd,
+                             const float* probe_dists, int32_t* slow_list, int* slow_cnt, hipStream_t s) {
+  FGPU_CHECK(dim % 4 == 0 && a.limit_k >= 1 && a.limit_k <= kWave && a.cut_ws && a.pool, FGPU_ERR_ARG,
+             "two_phase: bad finish arguments");
+  if (nqc <= 0) return FGPU_OK;
+  hipLaunchKernelGGL(tp_finish_kernel, dim3((unsigned)((nqc + kFinWaves - 1) / kFinWaves)), dim3(kFinWaves * kWave), 0,
+                     s, a, dim, q_base, nqc, vids, vd, probe_dists, slow_list, slow_cnt);
+  FGPU_HIP(hipGetLastError());
+  return FGPU_OK;
+}
+
+fgpu_status launch_tp_zero(int* p, int n, hipStream_t s) {
+  if (n <= 0) return FGPU_OK;
+  hipLaunchKernelGGL(tp_zero_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, p, n);
+  FGPU_HIP(hipGetLastError());
+  return FGPU_OK;
+}
+
 fgpu_status launch_tp_order(const uint32_t* vprobe, int nvq, int nlist, const int32_t* boff, int* fill,
                             int32_t* order, hipStream_t s) {
   if (nvq <= 0) return FGPU_OK;
   hipLaunchKernelGGL(tp_order_kernel, dim3((unsigned)((nvq + 255) / 256)), dim3(256), 0, s, vprobe, nvq, nlist, boff,
                      fill, order);
-  FGPU_HIP(hipGetLastError());
-  return FGPU_OK;
-}
-
-fgpu_status launch_tp_collect(const uint32_t* probes, int nprobe, int p1, int nqc, const int32_t* offsets, int nlist,
-                              int limit_k, const int32_t* vids, const float* vd, uint64_t* pool, int pool_cap,
-                              float* cut_ws, hipStream_t s) {
-  FGPU_CHECK(limit_k >= 1 && limit_k <= kWave, FGPU_ERR_ARG, "two_phase: collect needs limit_k <= 64");
-  if (nqc <= 0) return FGPU_OK;
-  hipLaunchKernelGGL(tp_collect_kernel, dim3((unsigned)((nqc + 3) / 4)), dim3(256), 0, s, probes, nprobe, p1, nqc,
-                     offsets, nlist, limit_k, vids, vd, pool, pool_cap, cut_ws);
   FGPU_HIP(hipGetLastError());
   return FGPU_OK;
 }
