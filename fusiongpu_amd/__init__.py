@@ -653,6 +653,7 @@ class Index:
 
     OPT_LIST_SKIP, OPT_SPIN_LIMIT, OPT_SCREEN, OPT_SCREEN_CLOCKS, OPT_TWO_PHASE_SPLIT, OPT_STAGE_EVENTS = \
         1, 2, 3, 4, 5, 6
+    OPT_TWO_PHASE_SCREEN = 7
     STAGES = ("coarse", "screen_pairs1", "screen_round1", "screen_pairs2", "screen_round2", "rescore", "lut_kernel")
 
     def set_option(self, option: int, value: int):
@@ -660,8 +661,9 @@ class Index:
         OPT_SPIN_LIMIT (polls before a flow-kernel wait gives up, 0 = automatic), OPT_SCREEN (0 = fgpu_search
         runs the LUT kernels), OPT_SCREEN_CLOCKS (1 = the screen records shader clocks),
         OPT_TWO_PHASE_SPLIT (phase-1 workgroups a query: 0 automatic, 1 never, s >= 2), OPT_STAGE_EVENTS
-        (1 = search records HIP events between its stages, read by search_stage_times).  Results never depend
-        on them; they change only this index's later calls."""
+        (1 = search records HIP events between its stages, read by search_stage_times), OPT_TWO_PHASE_SCREEN
+        (two-phase phase 1 through the MFMA screen: 0 automatic for batches >= 1024, 1 never, 2 always).
+        Results never depend on them; they change only this index's later calls."""
         _check(lib.fgpu_index_set_option(self._h, int(option), int(value)))
 
     @property

@@ -44,6 +44,7 @@ struct fgpu_index {
   int opt_screen = 1;
   int opt_screen_clocks = 0;
   int opt_two_phase_split = 0;
+  int opt_two_phase_screen = 0;  // FGPU_OPT_TWO_PHASE_SCREEN
   // FGPU_OPT_STAGE_EVENTS: events fgpu_search records between its stages.
   int opt_stage_events = 0;
   hipEvent_t stage_ev[kStageEvents] = {};
@@ -202,6 +203,9 @@ struct ScreenWs {
 // chunk of nvq virtual queries (one per (query, phase-1 probe)): their query
 // rows, probes and (zero) probe distances, their top-limit_k results, the
 // per-list counts and compact bucket offsets, and the screen's workspace.
+// Batches below this many queries keep phase 1 in the two-phase kernel (the
+// screen's fixed launches cost more than they save there).
+constexpr int kTpScreenMinQueries = 1024;
 constexpr int kTpVqMax = 131072;  // virtual queries a chunk (fuller 32-row MFMA groups per list)
 struct TpScreenWs {
   float* vq = nullptr;
@@ -713,6 +717,7 @@ fgpu_status fgpu_index_set_option(fgpu_index* ix, int option, int value) {
     case FGPU_OPT_SCREEN: ix->opt_screen = value ? 1 : 0; return FGPU_OK;
     case FGPU_OPT_SCREEN_CLOCKS: ix->opt_screen_clocks = value ? 1 : 0; return FGPU_OK;
     case FGPU_OPT_TWO_PHASE_SPLIT: ix->opt_two_phase_split = value > 0 ? value : 0; return FGPU_OK;
+    case FGPU_OPT_TWO_PHASE_SCREEN: ix->opt_two_phase_screen = value >= 0 && value <= 2 ? value : 0; return FGPU_OK;
     case FGPU_OPT_STAGE_EVENTS:
       if (value && !ix->stage_ev[0])
         for (hipEvent_t& e : ix->stage_ev) FGPU_HIP(hipEventCreate(&e));
@@ -765,7 +770,9 @@ fgpu_status two_phase(const fgpu_index* ix, const float* dq, int nq, const uint3
   // two-phase kernel's second half runs the threshold, phase 2 and the final
   // select.  The virtual queries' buffers take the end of the workspace; the
   // pools and cutoff rows the rest.
-  if (ix->screen_ok && ix->opt_screen && limit_k <= 64 && p1 >= 1 && screen_supported(ix->dim, ix->m) &&
+  const bool tp_screen = ix->opt_two_phase_screen == 2 ||
+                         (ix->opt_two_phase_screen == 0 && (int64_t)nq >= kTpScreenMinQueries);
+  if (tp_screen && ix->screen_ok && ix->opt_screen && limit_k <= 64 && p1 >= 1 && screen_supported(ix->dim, ix->m) &&
       ix->nlist <= kScreenMaxLists && ((uintptr_t)dq & 15) == 0) {
     // With FGPU_OPT_STAGE_EVENTS, the stage events of fgpu_search_stage_times
     // around the last virtual-query chunk's set-up and screen stages; the

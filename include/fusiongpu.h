@@ -225,7 +225,13 @@ int fgpu_index_screen_ready(const fgpu_index* idx);
  *                       workgroups a query (0 = automatic: split only batches
  *                       too small to fill the GPU; 1 = never; s >= 2 = s, at
  *                       most p1; limit_k <= 64 only; same results);
- *   FGPU_OPT_SCREEN     0: fgpu_search runs the LUT kernels, 1 default;
+ *   FGPU_OPT_SCREEN     0: fgpu_search runs the LUT kernels, and
+ *                       fgpu_two_phase_search phase 1 in its own kernel; 1
+ *                       default;
+ *   FGPU_OPT_TWO_PHASE_SCREEN phase 1 of fgpu_two_phase_search (limit_k <=
+ *                       64) through the MFMA screen: 0 automatic (batches of
+ *                       1024 queries or more), 1 never, 2 always; same
+ *                       results;
  *   FGPU_OPT_SCREEN_CLOCKS 1: the screen kernels add their waves' shader
  *                       clocks (before the first item, item set-up, tile
  *                       loops, after the tiles; round 1 then round 2) to the
@@ -243,6 +249,7 @@ int fgpu_index_screen_ready(const fgpu_index* idx);
 #define FGPU_OPT_SCREEN_CLOCKS 4
 #define FGPU_OPT_TWO_PHASE_SPLIT 5
 #define FGPU_OPT_STAGE_EVENTS 6
+#define FGPU_OPT_TWO_PHASE_SCREEN 7
 fgpu_status fgpu_index_set_option(fgpu_index* idx, int option, int value);
 /* With FGPU_OPT_STAGE_EVENTS on: the milliseconds of the last fgpu_search's
  * stages (waits for it), h_ms[0..6] = coarse step, the screen's zeroing and

@@ -61,9 +61,11 @@ CASES = [
 ]
 
 
+@pytest.mark.parametrize("tp_screen", [1, 2])  # phase 1 in the two-phase kernel / through the MFMA screen
 @pytest.mark.parametrize("dim,m,p1,limit_k,coeff,rerank_m", CASES)
-def test_two_phase_bit_exact(dim, m, p1, limit_k, coeff, rerank_m):
-    _say(f"two_phase dim={dim} m={m} p1={p1} limit_k={limit_k} coeff={coeff} rerank_m={rerank_m}")
+def test_two_phase_bit_exact(dim, m, p1, limit_k, coeff, rerank_m, tp_screen):
+    _say(f"two_phase dim={dim} m={m} p1={p1} limit_k={limit_k} coeff={coeff} rerank_m={rerank_m} "
+         f"tp_screen={tp_screen}")
     rng = np.random.default_rng(dim + m + p1 + limit_k + rerank_m)
     nlist = 40
     offs, ids, lc, cent, cb = _index(rng, 30000, dim, m, nlist, empty=(3, 17), big=8)
@@ -76,6 +78,7 @@ def test_two_phase_bit_exact(dim, m, p1, limit_k, coeff, rerank_m):
     probes[9, 0] = 8                     # the long list (> 1024 vectors) in phase 1 ...
     probes[9, 12] = 8                    # ... and again in phase 2
     idx = fg.Index.from_arrays(dim, m, offs, ids, lc, cent, cb)
+    idx.set_option(fg.Index.OPT_TWO_PHASE_SCREEN, tp_screen)
     assert idx.max_list_len > 1024
     gid, gd, gcnt, gcut, gthr = idx.two_phase_search(torch.from_numpy(q).cuda(),
                                                      torch.from_numpy(probes.view(np.int32)).cuda(), p1, limit_k,
@@ -103,10 +106,13 @@ def test_two_phase_bit_exact(dim, m, p1, limit_k, coeff, rerank_m):
     idx.close()
 
 
-def test_two_phase_many_phase1_lists():
+@pytest.mark.parametrize("tp_screen", [1, 2])
+def test_two_phase_many_phase1_lists(tp_screen):
     """More phase-1 lists than the kernel stages at once (16): the staged
-    wave lists are merged in several rounds; unusable probes inside phase 1."""
-    _say("two_phase p1=37 of nprobe=40")
+    wave lists are merged in several rounds; unusable probes inside phase 1.
+    Through the screen: more phase-1 lists than the one-wave final sorts, so
+    every query takes the two-phase kernel's second half."""
+    _say(f"two_phase p1=37 of nprobe=40 tp_screen={tp_screen}")
     rng = np.random.default_rng(4040)
     nlist = 64
     offs, ids, lc, cent, cb = _index(rng, 40000, 96, 32, nlist, empty=(5, 9, 30), big=12)
@@ -117,6 +123,7 @@ def test_two_phase_many_phase1_lists():
     probes[10, :17] = 0xFFFFFFFF         # exactly 20 usable phase-1 lists
     p1, limit_k, coeff, rerank_m = 37, 24, 1.1, 700
     idx = fg.Index.from_arrays(96, 32, offs, ids, lc, cent, cb)
+    idx.set_option(fg.Index.OPT_TWO_PHASE_SCREEN, tp_screen)
     gid, gd, gcnt, gcut, gthr = idx.two_phase_search(torch.from_numpy(q).cuda(),
                                                      torch.from_numpy(probes.view(np.int32)).cuda(), p1, limit_k,
                                                      coeff, rerank_m, want_cutoffs=True)
@@ -152,6 +159,7 @@ def test_two_phase_screen_phase1_short_lists_and_pruned_probes():
     probes[8, 2] = 777                   # out of range: pruned
     idx = fg.Index.from_arrays(dim, m, offs, ids, lc, cent, cb)
     assert idx.screen_ready
+    idx.set_option(fg.Index.OPT_TWO_PHASE_SCREEN, 2)  # 150 queries: below the automatic batch size
     dq, dp = torch.from_numpy(q).cuda(), torch.from_numpy(probes.view(np.int32)).cuda()
     gid, gd, gcnt, st = idx.two_phase_stats(dq, dp, p1, limit_k, coeff, rerank_m)
     oid, od, ocnt, _, _ = oracle.search_two_phase(q, cent, cb, offs, ids, lc, probes, p1, limit_k, coeff, rerank_m)
@@ -269,13 +277,17 @@ def test_rerank_bit_exact(dim, k, mb, eps, beta, spec):
     assert np.all(gid[2] == -1)
 
 
-def test_search_rerank_end_to_end():
-    _say("search_rerank end to end")
+@pytest.mark.parametrize("tp_screen", [1, 2])
+def test_search_rerank_end_to_end(tp_screen):
+    """Coarse + two-phase + rerank; through the screen the phase-2 list bounds
+    come from the coarse step's probe distances."""
+    _say(f"search_rerank end to end tp_screen={tp_screen}")
     x = oracle.gen_gmm(30000, 96, 48, seed=11, sig_lo=0.05, sig_hi=0.15)
     q = oracle.gen_gmm(300, 96, 48, seed=11, set=1, sig_lo=0.05, sig_hi=0.15)
     offs, ids, codes, cent, cb = fg.build_ivfpq(torch.from_numpy(x).cuda(), 64, 48, kmeans_iters=4, init_mode=1,
                                                 seed=3, pq_iters=3, sample_size=5000)
     idx = fg.Index.from_arrays(96, 48, offs, ids, codes, cent, cb)
+    idx.set_option(fg.Index.OPT_TWO_PHASE_SCREEN, tp_screen)
     dq, dx = torch.from_numpy(q).cuda(), torch.from_numpy(x).cuda()
     gid, gd = idx.search_rerank(dq, dx, 16, 20, p1_lists=4, limit_k=30, threshold_coeff=1.0, rerank_m=200)
     probes, _ = oracle.coarse(q, cent, 16)
