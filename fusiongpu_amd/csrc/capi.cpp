@@ -36,6 +36,7 @@ struct fgpu_index {
   // The MFMA screen of the plain search (screen.hip): bf16 codebook and the
   // per-vector extra blocks, built at creation when the geometry allows it.
   uint16_t* d_cb16 = nullptr;
+  int screen_scale_exp = 0;  // S: the screen works on the data times 2^S
   uint4* d_vext = nullptr;
   bool screen_ok = false;
   // Per-index options (fgpu_index_set_option).
@@ -114,15 +115,46 @@ fgpu_status finish_index(fgpu_index* ix, hipStream_t s) {
   FGPU_TRY(launch_list_radius(ix->d_codebook, ix->m, ix->dim / ix->m, ix->d_codes, ix->d_offsets, ix->nlist, ix->d_rmax,
                               s));
   // The screen's arrays: only for its geometries, 16-byte aligned arrays,
-  // lists below 2^24 vectors, and (checked below) decoded norms below 2^40.
+  // lists below 2^24 vectors, and decoded norms below 2^40.  The screen works
+  // on the data times 2^S, S the largest with every decoded norm at most 64
+  // after scaling; the bound sqrt(sum_j max_c ||codeword||^2) comes from the
+  // codebook alone.
   auto al16 = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
   unsigned int* xmax = nullptr;
+  double xcb = -1.0;
   if (screen_supported(ix->dim, ix->m) && ix->max_list_len < (1 << 24) && al16(ix->d_codebook) &&
       al16(ix->d_centroids) && al16(ix->d_codes)) {
+    const int sub = ix->dim / ix->m;
+    std::vector<float> hcb((size_t)ix->dim * kPQK);
+    FGPU_HIP(hipStreamSynchronize(s));
+    FGPU_HIP(hipMemcpy(hcb.data(), ix->d_codebook, hcb.size() * sizeof(float), hipMemcpyDeviceToHost));
+    double sum = 0.0;
+    for (int j = 0; j < ix->m; ++j) {
+      double mx = 0.0;
+      for (int c = 0; c < kPQK; ++c) {
+        double n2 = 0.0;
+        for (int d = 0; d < sub; ++d) {
+          const double v = hcb[((size_t)j * kPQK + c) * sub + d];
+          n2 += v * v;
+        }
+        mx = std::max(mx, n2);
+      }
+      sum += mx;
+    }
+    xcb = std::sqrt(sum);
+  }
+  if (xcb >= 0.0 && xcb <= 0x1p40) {
+    int se = 0;
+    if (xcb > 0.0) {
+      se = (int)std::floor(std::log2(64.0 / xcb));
+      while (std::ldexp(xcb, se) > 64.0) --se;
+      se = std::max(-60, std::min(60, se));
+    }
+    ix->screen_scale_exp = se;
     if (alloc((void**)&ix->d_cb16, (size_t)ix->dim * kPQK * sizeof(uint16_t)) &&
         alloc((void**)&ix->d_vext, sizeof(uint4) * (size_t)std::max<int64_t>(ix->total, 1)) &&
         alloc((void**)&xmax, 256)) {
-      FGPU_TRY(launch_screen_prep(ix->d_codebook, ix->m, ix->dim / ix->m, ix->d_codes, ix->total, ix->d_cb16,
+      FGPU_TRY(launch_screen_prep(ix->d_codebook, ix->m, ix->dim / ix->m, se, ix->d_codes, ix->total, ix->d_cb16,
                                   ix->d_vext, xmax, s));
     } else {
       (void)hipGetLastError();  // no room for the screen: the plain search keeps the LUT kernels
@@ -135,7 +167,7 @@ fgpu_status finish_index(fgpu_index* ix, hipStream_t s) {
     (void)hipFree(xmax);
     float xm = 0.0f;
     std::memcpy(&xm, &bits, sizeof(xm));
-    ix->screen_ok = got && xm <= 0x1p40f;
+    ix->screen_ok = got && xm <= 65.0f;  // every scaled norm bound X' (at most 64 plus its fp16 rounding)
   }
   if (!ix->screen_ok) {
     for (void* p : {(void*)ix->d_cb16, (void*)ix->d_vext})
@@ -606,6 +638,7 @@ fgpu_status fgpu_search(const fgpu_index* ix, const float* dq, int nq, int nprob
     FGPU_HIP(mark(1));
     ScreenArgs sa{dq, ix->d_centroids, ix->d_offsets, ix->d_codes, ix->d_ids, ix->d_codebook, ix->d_cb16,
                   ix->d_vext, ix->d_rmax, pid, pd, nq, nprobe, k, ix->nlist};
+    sa.scale_exp = ix->screen_scale_exp;
     sa.ctr = sw.zero;
     sa.cnt1 = sw.zero + kCtrCount;
     sa.cnt2 = sa.cnt1 + ix->nlist;
@@ -824,6 +857,7 @@ fgpu_status two_phase(const fgpu_index* ix, const float* dq, int nq, const uint3
             FGPU_HIP(mark(1));
             ScreenArgs sa{tw.vq, ix->d_centroids, ix->d_offsets, ix->d_codes, ix->d_ids, ix->d_codebook, ix->d_cb16,
                           ix->d_vext, ix->d_rmax, tw.vprobe, tw.vpd, nvq, 1, limit_k, ix->nlist};
+            sa.scale_exp = ix->screen_scale_exp;
             sa.ctr = tw.sw.zero;
             sa.cnt1 = tw.sw.zero + kCtrCount;
             sa.cnt2 = sa.cnt1 + ix->nlist;

@@ -136,12 +136,13 @@ struct ScreenArgs {
   const uint8_t* codes;     // [total][m]
   const int32_t* vec_ids;   // [total]
   const float* codebook;    // [m][256][dim/m] fp32
-  const uint16_t* cb16;     // [m][256][dim/m] bf16 (nearest)
+  const uint16_t* cb16;     // [m][256][dim/m] fp16 of the codebook times 2^scale_exp (nearest, flushed below 2^-14)
   const uint4* vext;        // [total] per-vector extra block (screen_prep)
   const float* rmax;        // [nlist]
   const uint32_t* probes;   // [nq][nprobe]; ids >= nlist are skipped
   const float* probe_dists; // [nq][nprobe] the coarse step's squared distances
   int nq, nprobe, k, nlist;
+  int scale_exp;            // S: the screen's operands are the data times 2^S (the index's choice)
   // One region, zeroed at the start of a launch: ctr[kCtrCount], cnt1[nlist],
   // cnt2[nlist], cand_cnt[nq] (in this order, contiguous).
   int* ctr;
@@ -158,7 +159,7 @@ struct ScreenArgs {
   // nullptr = ascending.
   const int32_t* order = nullptr;
   uint4* arec;              // [nq nprobe][2][9] pair records: per lane half 8 A fragments and the extra block
-  int2* first;              // [nq] round 1: (list, bucket position) of the query's pair, or (-1, -1)
+  int2* first;              // [nq] round 1: (list, row scale exponent t) of the query's pair, (-1, -1), or (-2, 0)
   uint32_t* gminbuf;        // [nq][kMaxChunks][64] round 1: per query, first-list chunk and group, min U bits
   float* thr;               // [nq] T(q)
   uint2* cand;              // [nq][cand_cap] (vector position, list)
@@ -178,10 +179,10 @@ struct ScreenArgs {
 bool screen_supported(int dim, int m);
 // Words of ScreenArgs::gminbuf for nq queries.
 int64_t screen_gmin_words(int nq);
-// The bf16 codebook and the per-vector extra blocks of an index; *xmax_bits
-// gets the largest per-vector norm bound (float bits).
-fgpu_status launch_screen_prep(const float* codebook, int m, int sub, const uint8_t* codes, int64_t total,
-                               uint16_t* cb16, uint4* vext, unsigned int* xmax_bits, hipStream_t s);
+// The fp16 codebook (times 2^scale_exp) and the per-vector extra blocks of an
+// index; *xmax_bits = the largest scaled decoded norm bound X' (float bits).
+fgpu_status launch_screen_prep(const float* codebook, int m, int sub, int scale_exp, const uint8_t* codes,
+                               int64_t total, uint16_t* cb16, uint4* vext, unsigned int* xmax_bits, hipStream_t s);
 // Threshold, screen and rescore; the queries it cannot answer are listed in
 // flist[0 .. ctr[kCtrFlag]) for launch_adc_plain_list.
 fgpu_status launch_screen(int dim, int m, const ScreenArgs& a, hipStream_t s);

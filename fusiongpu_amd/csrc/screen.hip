@@ -31,37 +31,46 @@
 // The bounds.  With p the decoded residual of v (codebook rows, fp32) and
 // D* = ||r - p||^2 exactly, d = D* (1 +- gamma_c), gamma_c = gamma(s + M + 1)
 // < 2^-16 (non-negative terms, s + M + 1 roundings; gamma(n) = n u/(1 - n u),
-// u = 2^-24).  The screen forms
-//     <a', p'>  +  per-query and per-vector constants,   a = -2 r (exact),
-// on v_mfma_f32_32x32x16_bf16, a' = bf16(a) and p' = bf16(p) (nearest): the
-// main K range holds a' against p'; one extra K block of 16 carries the
-// constants, each split into three bf16 values with directed rounding, so the
-// MFMA sum is the whole test value.  With the rounding errors' norms
-// E_a = ||a' - a|| (per query and list) and E_p = ||p' - p|| (per vector),
-//     |<a', p'> - <a, p>| <= E_a X + 2 R E_p + E_a E_p  (Cauchy-Schwarz)
-// for R >= ||r||, X >= ||p||: the norms are measured, not the worst case of
-// 2^-8 relative per element, which makes the bound about 2.6 times tighter
-// on typical data.  An input below the normal range the MFMA may flush
-// changes the product by < 2^-122 (R + X) more.  The MFMA adds at most 144
-// fp32 roundings over terms whose magnitudes sum to <= 1.03 (T + (R + X)^2),
-// and may flush terms below 2^-126 (< 2^-118 in all).  With B = (E_a + k R)
-// X' + 2 R E_p, X' >= X + E_p, k = 2^-14, g = 2^-13 and t = 1 + 2^-12 the two
-// tests are
-//     V = ||p||^2 - gX^2 - 2^-110 X + <a',p'> - B
-//         - (t T - nr2 + g R^2 + 2^-110 (1 + R))          <= 0,
-//     U = ||p||^2 + gX^2 + 2^-110 X + <a',p'> + B
-//         + (t nr2 + g R^2 + 2^-110 (1 + R))              >= D*,
-// nr2 the fp32 sum of squares of r (within gamma(129) of ||r||^2).  Collecting
-// terms, every coefficient of V - (d - T)-style slack is negative:
-// T (1/(1-gamma_c) - t + 1.8e-5) < 0, R X (3.6e-5 - k) < 0,
-// R^2 (gamma(129) + 1.8e-5 - g) < 0, X^2 (1.8e-5 - g) < 0 and the absolute
-// terms; so d <= T implies V <= 0, and U >= D* for the threshold, which is
-// then inflated by t.  The per-vector constants (X' rounded up to bf16,
-// ||p||^2 -+ gX'^2 in double, split; E_p rounded up) are built once per
+// u = 2^-24).  The screen works on the data times 2^S (S per index: every
+// decoded norm at most 64 after scaling), so it bounds D*' = 2^(2S) D*, and
+// each row (pair) runs at its own scale 2^-t (all its values times 2^-t,
+// which keeps every fp16 value below 2^15; see the pair record).  Powers of
+// two change neither the signs of the tests nor the order of one row's
+// values.  At the data's scale, with r' = 2^S r, p'' = 2^S p, the screen forms
+//     <a', p'>  +  per-query and per-vector constants,   a = -2 r' (exact),
+// on v_mfma_f32_32x32x16_f16, a' = fp16(a) and p' = fp16(p'') (nearest, zero
+// below 2^-14): the main K range holds a' against p'; one extra K block of 16
+// carries the constants, each split into three fp16 values with directed
+// rounding, so the MFMA sum is the whole test value.  With the rounding
+// errors' norms E_a = ||a' - a|| (per query and list) and E_p = ||p' - p''||
+// (per vector),
+//     |<a', p'> - <a, p''>| <= E_a X + 2 R E_p + E_a E_p  (Cauchy-Schwarz)
+// for R >= ||r'||, X >= ||p''||: the norms are measured, about 2^-12.4
+// relative per element (fp16 has 11 significant bits; bf16 would leave 8).
+// The fp16 values are normal or zero (the helpers below flush in the stated
+// direction), their products exact in fp32.  The MFMA adds at most 144 fp32
+// roundings over terms whose magnitudes sum to <= 1.03 (T + (R + X)^2), and
+// may flush partial sums below 2^-126 (< 2^-118 in all, at the row scale).
+// With B = (E_a + k R) X' + 2 R E_p, X' >= X + E_p, k = 2^-14, g = 2^-15 and
+// t = 1 + 2^-14 the two tests are (at the data's scale; each row's record
+// holds them times 2^-t)
+//     V = ||p''||^2 - gX'^2 + <a',p'> - B
+//         - (t T - nr2' + g R^2) - 2^-110 (1 + R)          <= 0,
+//     U = ||p''||^2 + gX'^2 + <a',p'> + B
+//         + (t nr2' + g R^2) + 2^-110 (1 + R)              >= D*',
+// nr2' = 2^(2S) times the fp32 sum of squares of r (within gamma(129) of
+// ||r'||^2).  Collecting terms, every coefficient of V - (d' - T)-style slack
+// is negative (1.8e-5 is twice the MFMA's 144 u 1.03): T (1/(1-gamma_c) - t
+// + 1.8e-5) < 0, R X (3.6e-5 - k) < 0, R^2 (gamma(129) + 1.8e-5 - g) < 0,
+// X^2 (1.8e-5 - g) < 0 (g = 3.05e-5, t - 1 = k = 6.1e-5) and the absolute
+// terms; so d' <= T implies V <= 0, and U >= D*' for the threshold, which is
+// then inflated by t.  The per-vector constants (X' rounded up to fp16,
+// ||p''||^2 -+ gX'^2 in double, split; E_p rounded up) are built once per
 // index; the per-query ones per (query, list), E_a from the fp32 sum of the
 // squared errors (relative error below 2^-16, plus 2^-100 absolute for
-// underflow).  Values whose norms exceed 2^40 would leave the fp32 range
-// safety the bound assumes: such indexes and queries take the LUT kernel.
+// underflow).  Indexes whose decoded norms exceed 2^40 take the LUT kernels;
+// a pair whose residual norm leaves the row scales (t > 14) or exceeds 2^40
+// sends its query to the LUT kernel.
 #include <cmath>
 
 #include "common.hpp"
@@ -71,13 +80,13 @@
 namespace fgpu {
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 
 namespace {
 
 constexpr double kRX = 0x1p-14;          // coefficient of R X (the MFMA's roundings)
-constexpr double kG = 0x1p-13;           // coefficient of R^2 and X^2
-constexpr double kTInfl = 1.0 + 0x1p-12;
+constexpr double kG = 0x1p-15;           // coefficient of R^2 and X^2
+constexpr double kTInfl = 1.0 + 0x1p-14;
 constexpr double kAbs = 0x1p-110;
 constexpr double kDbl = 0x1p-40;         // slack for the double-precision constant arithmetic
 constexpr float kMaxNorm2 = 0x1p80f;     // squared residual norms above this take the LUT kernel
@@ -92,7 +101,6 @@ constexpr int kMaxGroups = 64;           // round-1 groups a query's first list 
 // U from above only when k <= groups.
 __host__ __device__ constexpr int screen_groups(int k) { return k > 32 ? 64 : 32; }
 
-constexpr uint32_t kOneOne = 0x3F803F80u;  // two bf16 1.0
 constexpr int kRecHalf = 9;              // uint4 per lane half of a pair record: 8 A fragments, the extra block
 constexpr int kRec = 2 * kRecHalf;
 
@@ -106,9 +114,47 @@ __device__ __forceinline__ int lanes_below64(uint64_t m) {
   return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
 }
 
-// ---- bf16 with stated rounding ------------------------------------------------
-__device__ __forceinline__ uint16_t bf_rn(float f) { return __builtin_bit_cast(uint16_t, (__bf16)f); }
-__device__ __forceinline__ double bf_val(uint16_t b) { return (double)__uint_as_float((uint32_t)b << 16); }
+// ---- fp16 with stated rounding, normal values and zero only ----------------------
+// Every operand and constant the screen gives the MFMA is 0 or a normal fp16:
+// magnitudes below 2^-14 are flushed by these helpers (in the stated
+// direction), and the error norms are measured against the stored values, so
+// nothing depends on how the MFMA treats subnormal inputs.
+constexpr float kHMin = 0x1p-14f;            // smallest normal fp16
+constexpr uint16_t kHOne = 0x3C00u;          // 1.0
+constexpr uint16_t kHBig = 0x7BFFu;          // 65504, the largest finite fp16
+constexpr uint32_t kOneOne = 0x3C003C00u;    // two fp16 1.0
+__device__ __forceinline__ double h_val(uint16_t b) { return (double)(float)__builtin_bit_cast(_Float16, b); }
+__device__ __forceinline__ float h_float(uint16_t b) { return (float)__builtin_bit_cast(_Float16, b); }
+// Nearest (f finite, |f| < 65504), magnitudes below 2^-14 to zero.
+__device__ __forceinline__ uint16_t h_rn(float f) {
+  return fabsf(f) < kHMin ? (uint16_t)0 : __builtin_bit_cast(uint16_t, (_Float16)f);
+}
+// The neighbours of b among {0, normal fp16}.
+__device__ __forceinline__ uint16_t h_next_down(uint16_t b) {
+  const uint16_t mag = b & 0x7FFFu;
+  if (mag == 0) return 0x8400u;                                     // 0 -> -2^-14
+  if (b & 0x8000u) return (uint16_t)(b + 1u);                       // larger magnitude
+  return mag == 0x0400u ? (uint16_t)0 : (uint16_t)(b - 1u);         // 2^-14 -> 0
+}
+__device__ __forceinline__ uint16_t h_next_up(uint16_t b) {
+  const uint16_t mag = b & 0x7FFFu;
+  if (mag == 0) return 0x0400u;                                     // 0 -> 2^-14
+  if (b & 0x8000u) return mag == 0x0400u ? (uint16_t)0 : (uint16_t)(b - 1u);
+  return (uint16_t)(b + 1u);
+}
+// A value of {0, normal fp16} <= v, and one >= v (|v| < 65504): the nearest,
+// moved one step when it lies on the wrong side.
+__device__ __forceinline__ uint16_t h_down(double v) {
+  uint16_t b = h_rn((float)v);
+  while (h_val(b) > v) b = h_next_down(b);
+  return b;
+}
+__device__ __forceinline__ uint16_t h_up(double v) {
+  uint16_t b = h_rn((float)v);
+  while (h_val(b) < v) b = h_next_up(b);
+  return b;
+}
+// The largest float <= v and the smallest float >= v (v finite).
 __device__ __forceinline__ float f_step_down(float f) {
   if (f == 0.0f) return -0x1p-149f;
   const uint32_t u = __float_as_uint(f);
@@ -119,7 +165,6 @@ __device__ __forceinline__ float f_step_up(float f) {
   const uint32_t u = __float_as_uint(f);
   return __uint_as_float(f > 0.0f ? u + 1u : u - 1u);
 }
-// The largest float <= v and the smallest float >= v (v finite).
 __device__ __forceinline__ float f_below(double v) {
   const float f = (float)v;
   return (double)f > v ? f_step_down(f) : f;
@@ -128,47 +173,39 @@ __device__ __forceinline__ float f_above(double v) {
   const float f = (float)v;
   return (double)f < v ? f_step_up(f) : f;
 }
-// The largest bf16 <= v and the smallest bf16 >= v.
-__device__ __forceinline__ uint16_t bf_down(double v) {
-  const float f = f_below(v);
-  const uint32_t u = __float_as_uint(f);
-  uint32_t hb = u >> 16;
-  if ((u & 0xFFFFu) && f < 0.0f) hb += 1u;  // truncation moved a negative value up
-  return (uint16_t)hb;
-}
-__device__ __forceinline__ uint16_t bf_up(double v) {
-  const float f = f_above(v);
-  const uint32_t u = __float_as_uint(f);
-  uint32_t hb = u >> 16;
-  if ((u & 0xFFFFu) && f > 0.0f) hb += 1u;  // truncation moved a positive value down
-  return (uint16_t)hb;
-}
-// Three bf16 whose sum is <= v (UP false) or >= v (UP true), within about
-// 2^-24 |v|.  The first two parts are nearest roundings, so each difference is
-// exact in double (Sterbenz); the last is rounded in the stated direction.
+// Three fp16 whose sum is <= v (UP false) or >= v (UP true), within about
+// 2^-34 |v| + 2^-13 (|v| < 65504).  The first two parts are nearest roundings,
+// so each remainder is exact in double; the last is rounded in the stated
+// direction.
 template <bool UP>
 __device__ __forceinline__ void split3(double v, uint16_t& b1, uint16_t& b2, uint16_t& b3) {
-  b1 = bf_rn((float)v);
-  const double r1 = v - bf_val(b1);
-  b2 = bf_rn((float)r1);
-  const double r2 = r1 - bf_val(b2);
-  b3 = UP ? bf_up(r2) : bf_down(r2);
+  b1 = h_rn((float)v);
+  const double r1 = v - h_val(b1);
+  b2 = h_rn((float)r1);
+  const double r2 = r1 - h_val(b2);
+  b3 = UP ? h_up(r2) : h_down(r2);
 }
 __device__ __forceinline__ uint32_t pack2(uint16_t lo, uint16_t hi) { return (uint32_t)lo | ((uint32_t)hi << 16); }
 
 // ---- index-time arrays -----------------------------------------------------------
-// vext[v]: the per-vector block of the extra K range, 8 bf16:
+// The screen works on the data times 2^S (S per index, scale_exp: every
+// decoded residual norm at most 64 after scaling), so the squared distances
+// it bounds are 2^(2S) times the exact ones; the sign of every test, and the
+// order of values within one row, are unchanged.
+// vext[v]: the per-vector block of the extra K range, 8 fp16 (scaled data):
 //   [X', y'_1, y'_2, y'_3, y''_1, y''_2, y''_3, E_p]
-// E_p >= ||bf16(p) - p|| and X' >= ||p_v|| + E_p (bf16, rounded up),
-// y' <= ||p||^2 - g X'^2 - 2^-110 X', y'' >= ||p||^2 + g X'^2 + 2^-110 X'
-// (each a three-part split).  ||p||^2 and the squared errors are summed in
-// double (each square exact; 128 roundings of 2^-53 are covered by the 2^-40
-// slack).  xmax_bits: the largest X' as float bits (atomic max).
-__global__ __launch_bounds__(256) void screen_prep_kernel(const float* __restrict__ cb, int m, int s,
+// with p' = fp16(2^S p) (each element nearest, flushed below 2^-14, as
+// cb16 holds it), E_p >= ||p' - 2^S p|| and X' >= ||2^S p|| + E_p (rounded
+// up), y' <= P - g X'^2 - 2^-110 X', y'' >= P + g X'^2 + 2^-110 X',
+// P = ||2^S p||^2 (each a three-part split).  P and the squared errors are
+// summed in double (each square exact; 128 roundings of 2^-53 are covered by
+// the 2^-40 slack).  xmax_bits: the largest X' as float bits (atomic max).
+__global__ __launch_bounds__(256) void screen_prep_kernel(const float* __restrict__ cb, int m, int s, int scale_exp,
                                                           const uint8_t* __restrict__ codes, int64_t total,
                                                           uint4* __restrict__ vext,
                                                           unsigned int* __restrict__ xmax_bits) {
   const int64_t v = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const double sc = ldexp(1.0, scale_exp);
   float xm = 0.0f;
   if (v < total) {
     const uint8_t* c = codes + v * m;
@@ -176,14 +213,15 @@ __global__ __launch_bounds__(256) void screen_prep_kernel(const float* __restric
     for (int j = 0; j < m; ++j) {
       const float* p = cb + ((size_t)j * kPQK + c[j]) * s;
       for (int d = 0; d < s; ++d) {
-        const double e = (double)p[d] - bf_val(bf_rn(p[d]));
-        p2 += (double)p[d] * (double)p[d];
+        const double x = (double)p[d] * sc;
+        const double e = x - h_val(h_rn((float)x));
+        p2 += x * x;
         e2 += e * e;
       }
     }
-    const uint16_t eb = bf_up(sqrt(e2) * (1.0 + kDbl));
-    const uint16_t xb = bf_up((sqrt(p2) + bf_val(eb)) * (1.0 + kDbl));
-    const double xu = bf_val(xb);
+    const uint16_t eb = h_up(sqrt(e2) * (1.0 + kDbl));
+    const uint16_t xb = h_up((sqrt(p2) + h_val(eb)) * (1.0 + kDbl));
+    const double xu = h_val(xb);
     const double lo = p2 - kG * xu * xu - kAbs * xu - kDbl * p2;
     const double hi = p2 + kG * xu * xu + kAbs * xu + kDbl * p2;
     uint16_t l1, l2, l3, h1, h2, h3;
@@ -196,10 +234,12 @@ __global__ __launch_bounds__(256) void screen_prep_kernel(const float* __restric
   if ((threadIdx.x & 63) == 0 && xm > 0.0f) atomicMax(xmax_bits, __float_as_uint(xm));
 }
 
-__global__ __launch_bounds__(256) void cb_bf16_kernel(const float* __restrict__ cb, int64_t n,
-                                                      uint16_t* __restrict__ out) {
+// The codebook times 2^S in fp16 (nearest, flushed below 2^-14), as the
+// screen's B operand.  The scaling is exact in double.
+__global__ __launch_bounds__(256) void cb_f16_kernel(const float* __restrict__ cb, int64_t n, int scale_exp,
+                                                     uint16_t* __restrict__ out) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < n) out[i] = bf_rn(cb[i]);
+  if (i < n) out[i] = h_rn((float)((double)cb[i] * ldexp(1.0, scale_exp)));
 }
 
 // ---- work lists ---------------------------------------------------------------------
@@ -241,76 +281,102 @@ __device__ __forceinline__ int list_items(int cnt, int nq, int n) {
   return ng * ((n + per - 1) / per);
 }
 
-// The pair record of entry ent = (query q, probe p of list l): for each lane
-// half h (dims [h D/2, (h+1) D/2)) the A fragments a' = bf16(-2 r),
-// r = fl(q - c), in MFMA operand order (fragment c holds dims h D/2 + 8c ..
-// + 7), then the extra K block of the round's test:
-//   round 1 (U):  h0 [ e, 0, 0, 0, 1, 1, 1,  w]   h1 [c1, c2, c3, 0 ...]
-//   round 2 (V):  h0 [-e, 1, 1, 1, 0, 0, 0, -w]   h1 [v1, v2, v3, 0 ...]
+// The pair record of entry ent = (query q, probe p of list l), at the pair's
+// row scale 2^-t (t >= 0 the smallest with max(R'^2, t T') 2^-t <= 2^14, R'
+// and T' the scaled residual norm and threshold; t <= 14, else the pair is
+// unusable): for each lane half h (dims [h D/2, (h+1) D/2)) the A fragments
+// a' = fp16(-2 r 2^(S-t)), r = fl(q - c), in MFMA operand order (fragment c
+// holds dims h D/2 + 8c .. + 7), then the extra K block of the round's test:
+//   round 1 (U):  h0 [ e, 0, 0, 0, u, u, u,  w]   h1 [c1, c2, c3, 1, 0 ...]
+//   round 2 (V):  h0 [-e, u, u, u, 0, 0, 0, -w]   h1 [v1, v2, v3, 1, 0 ...]
 // against the vector's block [X', y'1..3, y''1..3, E_p] (h0) and
-// [1, 1, 1, 0 ...] (h1): e = bf16 above E_a + k R, w = bf16 above 2 R (so
-// e X' + w E_p >= B), c1 + c2 + c3 >= (t nr2 + g R^2 + 2^-110 (1 + R)),
-// v1 + v2 + v3 <= -(t T - nr2 + g R^2 + 2^-110 (1 + R)), each with the 2^-40
-// slack of the double arithmetic.  The record is unusable when nr2 is not
-// <= kMaxNorm2 (NaN included): then its A fragments are zero and its block
-// the round's inactive one (round 2: V = 1e30 through h1's first slot), so
-// its row passes nothing and bounds nothing, and the caller adds no pair or
+// [1, 1, 1, 0 ...] (h1; [1, 1, 1, 65504, 0 ...] for a column past the range,
+// which so exceeds every real value): u = 2^-t, e >= (E_a + k R') 2^-t with
+// E_a = ||a' - (-2 r 2^(S-t))|| 2^t, w >= 2 R' 2^-t (so e X' + w E_p >= B 2^-t),
+// c1 + c2 + c3 >= (t nr2' + g R'^2) 2^-t + 2^-110 (1 + R' 2^-t),
+// v1 + v2 + v3 <= -(t T' - nr2' + g R'^2) 2^-t - 2^-110 (1 + R' 2^-t), each
+// with the 2^-40 slack of the double arithmetic (nr2' = 2^(2S) nr2).  Every value
+// of a row is 2^-t times its value at the data's scale 2^S, so the row's
+// tests keep their signs and its U values their order, and every fp16 value
+// stays below 2^15.  The record is unusable when nr2 is not <= kMaxNorm2
+// (NaN included) or t > 14: then its A fragments are zero and its block the
+// round's inactive one (round 2: V = 65504 through h1's first slot), so its
+// row passes nothing and bounds nothing, and the caller adds no pair or
 // drops the query.
 //
 // pair_a: the A fragments, by a whole wave (qv, cv: this lane's two dims of
-// the query and of the list's centroid); returns (nr2, the fp32 sum of the
-// squared errors of a') on every lane.
+// the query and of the list's centroid; tt: t T' for round 2, else 0);
+// returns nr2, the fp32 sum of the squared errors of a' (at the row scale)
+// and t on every lane.
+struct PairA {
+  float nr2, ea2;
+  int t;  // > 14: unusable
+};
 template <int D>
 __device__ __forceinline__ float2 centroid_dims(const ScreenArgs& a, int l) {
   const int lane = threadIdx.x & 63;
   return 2 * lane < D ? reinterpret_cast<const float2*>(a.centroids + (size_t)l * D)[lane] : make_float2(0.0f, 0.0f);
 }
-__device__ __forceinline__ float bf_float(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
+// The row scale exponent of a pair: nr2 unscaled, tt scaled.
+__device__ __forceinline__ int row_scale_exp(float nr2, double tt, int scale_exp) {
+  const double m = fmax(fmax(ldexp((double)nr2, 2 * scale_exp), tt), 1.0) * (1.0 + 0x1p-10);
+  if (!(m <= 0x1p60)) return 99;  // NaN or far out of range
+  int t = 0;
+  while (ldexp(m, -t) > 0x1p14) ++t;
+  return t;
+}
 template <int D>
-__device__ float2 pair_a(const ScreenArgs& a, int64_t ent, float2 qv, float2 cv) {
+__device__ PairA pair_a(const ScreenArgs& a, int64_t ent, float2 qv, float2 cv, double tt) {
   const int lane = threadIdx.x & 63;
   const bool has = 2 * lane < D;
   const float r0 = has ? qv.x - cv.x : 0.0f, r1 = has ? qv.y - cv.y : 0.0f;
   const float nr2 = wave_sum_f(__builtin_fmaf(r1, r1, r0 * r0));
-  const bool ok = nr2 <= kMaxNorm2;  // false for NaN
-  // -2 r is exact; its difference from the bf16 rounding is exact in fp32
-  const uint16_t b0 = bf_rn(-2.0f * r0), b1 = bf_rn(-2.0f * r1);
-  const float e0 = -2.0f * r0 - bf_float(b0), e1 = -2.0f * r1 - bf_float(b1);
+  const int t = row_scale_exp(nr2, tt, a.scale_exp);
+  const bool ok = nr2 <= kMaxNorm2 && t <= 14;  // false for NaN
+  // -2 r 2^(S-t): a power-of-two scaling, exact in fp32 (up to underflow below
+  // 2^-126, covered by the absolute slack); its difference from the stored
+  // fp16 value is exact in fp32
+  const float f = ok ? ldexpf(-2.0f, a.scale_exp - t) : 0.0f;
+  const float x0 = r0 * f, x1 = r1 * f;
+  const uint16_t b0 = h_rn(x0), b1 = h_rn(x1);
+  const float e0 = x0 - h_float(b0), e1 = x1 - h_float(b1);
   const float ea2 = wave_sum_f(ok ? __builtin_fmaf(e1, e1, e0 * e0) : 0.0f);
   uint32_t* rec = reinterpret_cast<uint32_t*>(a.arec + ent * kRec);
   if (has) {
     const int d = 2 * lane, h = d / (D / 2), w = d % (D / 2);
     rec[(h * kRecHalf + w / 8) * 4 + (w % 8) / 2] = ok ? pack2(b0, b1) : 0u;
   }
-  return make_float2(nr2, ea2);
+  return PairA{nr2, ea2, ok ? t : 99};
 }
-// pair_ex: both lane halves' extra blocks of entry ent, by one lane (ne: the
-// (nr2, squared error sum) pair_a returned).
+// pair_ex: both lane halves' extra blocks of entry ent, by one lane (pa: what
+// pair_a returned; T: the scaled threshold, round 2).
 template <int ROUND>
-__device__ void pair_ex(const ScreenArgs& a, int64_t ent, float2 ne, float T) {
+__device__ void pair_ex(const ScreenArgs& a, int64_t ent, PairA pa, float T) {
   uint4* rec = a.arec + ent * kRec;
-  const float nr2 = ne.x;
-  if (!(nr2 <= kMaxNorm2)) {
+  if (pa.t > 14) {
     rec[kRecHalf - 1] = make_uint4(0u, 0u, 0u, 0u);
-    rec[2 * kRecHalf - 1] = make_uint4(ROUND == 2 ? pack2(bf_rn(1e30f), 0u) : 0u, 0u, 0u, 0u);
+    rec[2 * kRecHalf - 1] = make_uint4(ROUND == 2 ? pack2(kHBig, 0u) : 0u, 0u, 0u, 0u);
     return;
   }
-  const double n2 = (double)nr2;
+  const double n2 = ldexp((double)pa.nr2, 2 * a.scale_exp);
   const double R = sqrt(n2 * (1.0 + 0x1p-16)) * (1.0 + kDbl);
-  const double Ea = sqrt((double)ne.y * (1.0 + 0x1p-16) + 0x1p-100) * (1.0 + kDbl);
-  const uint16_t e = bf_up(Ea + kRX * R), w = bf_up(2.0 * R);
+  const double u = ldexp(1.0, -pa.t);
+  const double Ea = sqrt((double)pa.ea2 * (1.0 + 0x1p-16) + 0x1p-100) * (1.0 + kDbl);
+  const uint16_t e = h_up(Ea + kRX * R * u), w = h_up(2.0 * R * u);
+  const uint16_t ub = (uint16_t)((15 - pa.t) << 10);  // 2^-t
+  const uint32_t uu = pack2(ub, ub);
   uint16_t p1, p2, p3;
   if (ROUND == 2) {
     const double t = (double)fmaxf(T, 0.0f);
-    const double rhs = t * kTInfl - n2 + kG * R * R + kAbs * (1.0 + R);
-    split3<false>(-rhs - kDbl * (t + n2 + kG * R * R), p1, p2, p3);
-    rec[kRecHalf - 1] = make_uint4(pack2(e ^ 0x8000u, 0x3F80u), kOneOne, 0u, pack2(0u, w ^ 0x8000u));
+    const double rhs = (t * kTInfl - n2 + kG * R * R) * u + kAbs * (1.0 + R * u);
+    split3<false>(-rhs - kDbl * (t + n2 + kG * R * R) * u, p1, p2, p3);
+    rec[kRecHalf - 1] = make_uint4(pack2(e ^ 0x8000u, ub), uu, 0u, pack2(0u, w ^ 0x8000u));
   } else {
-    const double c = n2 * kTInfl + kG * R * R + kAbs * (1.0 + R);
+    const double c = (n2 * kTInfl + kG * R * R) * u + kAbs * (1.0 + R * u);
     split3<true>(c * (1.0 + kDbl), p1, p2, p3);
-    rec[kRecHalf - 1] = make_uint4(pack2(e, 0u), 0u, kOneOne, pack2(0x3F80u, w));
+    rec[kRecHalf - 1] = make_uint4(pack2(e, 0u), 0u, uu, pack2(ub, w));
   }
-  rec[2 * kRecHalf - 1] = make_uint4(pack2(p1, p2), pack2(p3, 0u), 0u, 0u);
+  rec[2 * kRecHalf - 1] = make_uint4(pack2(p1, p2), pack2(p3, kHOne), 0u, 0u);
 }
 
 __device__ __forceinline__ float2 query_dims(const ScreenArgs& a, int q, int dim) {
@@ -358,11 +424,11 @@ __global__ __launch_bounds__(256) void screen_pairs1_kernel(ScreenArgs a) {
     f = make_int2(-2, 0);
   } else if (n >= a.k) {
     const int64_t ent = (int64_t)q * a.nprobe + pf;
-    const float2 ne = pair_a<D>(a, ent, query_dims(a, q, D), centroid_dims<D>(a, lf));
-    if (lane == 0) pair_ex<1>(a, ent, ne, 0.0f);
-    if (ne.x <= kMaxNorm2 && lane == 0) {
+    const PairA pa = pair_a<D>(a, ent, query_dims(a, q, D), centroid_dims<D>(a, lf), 0.0);
+    if (lane == 0) pair_ex<1>(a, ent, pa, 0.0f);
+    if (pa.t <= 14 && lane == 0) {
       const int pos = bucket_put(a, lf, q, (int)ent, atomicAdd(&a.cnt1[lf], 1));
-      if (pos >= 0) f = make_int2(lf, pos);
+      if (pos >= 0) f = make_int2(lf, pa.t);
     }
   }
   if (lane == 0) a.first[q] = f;
@@ -370,12 +436,14 @@ __global__ __launch_bounds__(256) void screen_pairs1_kernel(ScreenArgs a) {
 
 // Round 2 pairs, one wave a query.  First T(q): the k-th smallest of the 32
 // group minima of U over the query's first list (the minimum, over the list's
-// chunks, of each chunk's per-group minimum), inflated by 1 + 2^-12; +inf
+// chunks, of each chunk's per-group minimum), taken back from the round-1
+// row's scale 2^-t to the data's scale 2^S and inflated by 1 + 2^-14; +inf
 // without a round-1 pair or with fewer than k groups holding a value
 // (FLT_MAX, and nothing more, for the queries whose candidates are set).  Then
-// every usable probe whose list bound does not exceed T(q), with its pair
-// record carrying the V test.  A probe whose residual norm is out of range
-// sends the query to the LUT kernel (T = +inf).
+// every usable probe whose list bound does not exceed T(q) 2^-2S (the
+// bounds are in the data's units), with its pair record carrying the V test.
+// A probe whose pair is out of range sends the query to the LUT kernel
+// (T = +inf).
 template <int D>
 __global__ __launch_bounds__(256) void screen_pairs2_kernel(ScreenArgs a) {
   const int lane = threadIdx.x & 63;
@@ -415,19 +483,22 @@ __global__ __launch_bounds__(256) void screen_pairs2_kernel(ScreenArgs a) {
   // U >= 0, so float order is unsigned order of the bits
   wave_sort_u32(gm);
   const float kth = __uint_as_float((uint32_t)__builtin_amdgcn_readlane((int)gm, a.k - 1));
-  const float T = kth < INFINITY ? f_above((double)kth * kTInfl) : INFINITY;
+  // the group minima are at the round-1 row's scale 2^-f.y
+  const float T = kth < INFINITY ? f_above(ldexp((double)kth, f.y) * kTInfl) : INFINITY;
   if (lane == 0) a.thr[q] = T;
   if (!(T < INFINITY)) return;
+  const double tt = (double)T * kTInfl;            // the V constants' largest term
+  const float Tu = ldexpf(T, -2 * a.scale_exp);    // in the data's units, for the list bounds
   bool bad = false;
   for (int p0 = 0; p0 < a.nprobe; p0 += kWave) {
     const int p = p0 + lane;
     uint32_t l = l0;
-    bool pass = p0 == 0 && lb0 <= T;
+    bool pass = p0 == 0 && lb0 <= Tu;
     if (p0 > 0 && p < a.nprobe) {
       const size_t t = (size_t)q * a.nprobe + p;
       l = a.probes[t];
       pass = l < (uint32_t)a.nlist && a.offsets[l + 1] - a.offsets[l] > 0 &&
-             list_lower_bound(a.probe_dists[t], a.rmax[l]) <= T;
+             list_lower_bound(a.probe_dists[t], a.rmax[l]) <= Tu;
     }
     // Every passing probe takes its slot of its list's bucket at once (one
     // atomic a lane) and writes it after the pair records, so the atomic's
@@ -440,23 +511,23 @@ __global__ __launch_bounds__(256) void screen_pairs2_kernel(ScreenArgs a) {
     // sum), and the extra blocks follow lane-parallel (one lane a pair).
     uint64_t m = __ballot(pass);
     if (!m) continue;
-    float2 my_ne = make_float2(0.0f, 0.0f);
+    PairA my_pa{0.0f, 0.0f, 99};
     int b = __builtin_ctzll(m);
     float2 cv = centroid_dims<D>(a, __builtin_amdgcn_readlane((int)l, b));
     while (true) {
       const uint64_t rest = m & (m - 1);
       const int bn = rest ? __builtin_ctzll(rest) : b;
       const float2 cn = rest ? centroid_dims<D>(a, __builtin_amdgcn_readlane((int)l, bn)) : cv;
-      const float2 ne = pair_a<D>(a, (int64_t)q * a.nprobe + p0 + b, qv, cv);
-      if (lane == b) my_ne = ne;
+      const PairA pa = pair_a<D>(a, (int64_t)q * a.nprobe + p0 + b, qv, cv, tt);
+      if (lane == b) my_pa = pa;
       if (!rest) break;
       m = rest;
       b = bn;
       cv = cn;
     }
     if (pass) {
-      pair_ex<2>(a, (int64_t)q * a.nprobe + p, my_ne, T);
-      bad = bad || !(my_ne.x <= kMaxNorm2);
+      pair_ex<2>(a, (int64_t)q * a.nprobe + p, my_pa, T);
+      bad = bad || my_pa.t > 14;
       bucket_put(a, (int)l, q, (int)((int64_t)q * a.nprobe + p), pos);
     }
   }
@@ -485,7 +556,7 @@ __device__ __forceinline__ void load_half(const uint8_t* p, uint32_t (&w)[M / 8]
 }
 
 // 16-bit words code | (h M/2) << 8 for code bytes b and b + 1 of w: times the
-// entry size this is the code's row in the lane half's part of the bf16
+// entry size this is the code's row in the lane half's part of the fp16
 // codebook, so every gather below takes one shift and an immediate offset.
 __device__ __forceinline__ uint32_t words2(uint32_t w, uint32_t hsel, int b) {
   const uint32_t sel = (uint32_t)b | (4u << 8) | ((uint32_t)(b + 1) << 16) | (4u << 24);
@@ -494,10 +565,10 @@ __device__ __forceinline__ uint32_t words2(uint32_t w, uint32_t hsel, int b) {
 
 // The B fragment of chunk c: dims 8c .. 8c + 7 of the lane half's decoded row.
 template <int D, int M>
-__device__ __forceinline__ bf16x8 decode_chunk(const uint16_t* cbs, const uint32_t (&cw)[M / 8], uint32_t hsel,
+__device__ __forceinline__ f16x8 decode_chunk(const uint16_t* cbs, const uint32_t (&cw)[M / 8], uint32_t hsel,
                                                int c) {
   constexpr int S = D / M;
-  constexpr int SUB = 512 * S;  // bytes per subspace of the bf16 codebook
+  constexpr int SUB = 512 * S;  // bytes per subspace of the fp16 codebook
   const char* base = reinterpret_cast<const char*>(cbs);
   uint32_t f[4];
   if constexpr (S == 4) {
@@ -519,12 +590,12 @@ __device__ __forceinline__ bf16x8 decode_chunk(const uint16_t* cbs, const uint32
     f[2] = *reinterpret_cast<const uint32_t*>(base + ((w23 & 0xFFFFu) << 2) + (4 * c + 2) * SUB);
     f[3] = *reinterpret_cast<const uint32_t*>(base + ((w23 >> 16) << 2) + (4 * c + 3) * SUB);
   }
-  return __builtin_bit_cast(bf16x8, f);
+  return __builtin_bit_cast(f16x8, f);
 }
 
-__device__ __forceinline__ bf16x8 frag_of(uint32_t x, uint32_t y, uint32_t z, uint32_t w) {
+__device__ __forceinline__ f16x8 frag_of(uint32_t x, uint32_t y, uint32_t z, uint32_t w) {
   const uint32_t f[4] = {x, y, z, w};
-  return __builtin_bit_cast(bf16x8, f);
+  return __builtin_bit_cast(f16x8, f);
 }
 
 // k-th smallest (1 <= k <= 32) of 32 values: bitonic sort in registers.
@@ -557,7 +628,7 @@ __device__ __forceinline__ uint32_t kth_of_32(uint32_t (&v)[32], int k) {
 // from the pair records; the range is screened in tiles of kTV vectors.
 // ROUND 1 stores each row's per-group minima of U; ROUND 2 appends the
 // candidates (V <= 0) to their queries' arrays.
-// LDS: the bf16 codebook first (offset 0, so every gather's subspace offset is
+// LDS: the fp16 codebook first (offset 0, so every gather's subspace offset is
 // the instruction's immediate), then per-wave staging.
 template <int D, int M, int ROUND, int G = 32>
 __global__ __launch_bounds__(kSW * kWave) void screen_kernel(ScreenArgs a) {
@@ -616,12 +687,13 @@ __global__ __launch_bounds__(kSW * kWave) void screen_kernel(ScreenArgs a) {
   long long ck_pre = ck - t_begin, ck_setup = 0, ck_tiles = 0, ck_post = 0, ntiles = 0, nit = 0;
   const int nwaves = (int)gridDim.x * kSW;
   const uint32_t hsel = h ? (uint32_t)HB * 0x01010101u : 0u;
-  // The extra block of a column past the end of the range: +1e30 in both
-  // rounds' terms (slots 1 and 4), so its value is never a candidate and
-  // never a group minimum; lane half 1 keeps the [1, 1, 1, 0 ...] multipliers.
-  const uint16_t big = bf_rn(1e30f);
-  const uint4 bx_pad = h == 0 ? make_uint4(pack2(0u, big), 0u, pack2(big, 0u), 0u)
-                              : make_uint4(kOneOne, 0x3F80u, 0u, 0u);
+  // The extra block of a column: lane half 0 its vector's block (zeros past
+  // the end of the range), lane half 1 the [1, 1, 1, 0 ...] multipliers, with
+  // 65504 in slot 3 past the end: every row's record has 1 there, so such a
+  // column's value (>= 65504 - 2^14 at every row scale) is never a candidate
+  // and never a group minimum over real vectors (their values stay below 2^15).
+  const uint4 h1_real = make_uint4(kOneOne, (uint32_t)kHOne, 0u, 0u);
+  const uint4 h1_pad = make_uint4(kOneOne, pack2(kHOne, kHBig), 0u, 0u);
 
   for (int w = (int)blockIdx.x * kSW + wave; w < nitems; w += nwaves) {
     // Item w: the last list whose first item is <= w, then its group and chunk.
@@ -655,10 +727,10 @@ __global__ __launch_bounds__(kSW * kWave) void screen_kernel(ScreenArgs a) {
     load_tile(jb + kTV, cwB, bxB);
 
     // A rows and the extra block from the row's pair record.  A row without a
-    // pair: zeros, and in round 2 V = 1e30, so it never passes (in round 1
+    // pair: zeros, and in round 2 V = 65504, so it never passes (in round 1
     // its minima are not stored).
-    bf16x8 A[NC];
-    bf16x8 Aex;
+    f16x8 A[NC];
+    f16x8 Aex;
     {
       const uint4* rec = a.arec + (int64_t)(ent >= 0 ? ent : 0) * kRec + h * kRecHalf;
 #pragma unroll
@@ -667,7 +739,7 @@ __global__ __launch_bounds__(kSW * kWave) void screen_kernel(ScreenArgs a) {
         A[c] = frag_of(v.x, v.y, v.z, v.w);
       }
       const uint4 e = ent >= 0 ? rec[kRecHalf - 1]
-                               : make_uint4(ROUND == 2 && h == 1 ? pack2(big, 0u) : 0u, 0u, 0u, 0u);
+                               : make_uint4(ROUND == 2 && h == 1 ? pack2(kHBig, 0u) : 0u, 0u, 0u, 0u);
       Aex = frag_of(e.x, e.y, e.z, e.w);
     }
     // The query of each row, for the candidate flush and the round-1 store.
@@ -751,11 +823,10 @@ __global__ __launch_bounds__(kSW * kWave) void screen_kernel(ScreenArgs a) {
       for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
 #pragma unroll
       for (int c = 0; c < NC; ++c)
-        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A[c], decode_chunk<D, M>(cbs, cw, hsel, c), acc, 0, 0, 0);
-      const bool vcol = h == 0 && j0 + li < je;
-      acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-          Aex, frag_of(vcol ? bx.x : bx_pad.x, vcol ? bx.y : bx_pad.y, vcol ? bx.z : bx_pad.z, vcol ? bx.w : bx_pad.w),
-          acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(A[c], decode_chunk<D, M>(cbs, cw, hsel, c), acc, 0, 0, 0);
+      const bool col = j0 + li < je;
+      const uint4 bh = h == 0 ? (col ? bx : make_uint4(0u, 0u, 0u, 0u)) : (col ? h1_real : h1_pad);
+      acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(Aex, frag_of(bh.x, bh.y, bh.z, bh.w), acc, 0, 0, 0);
       load_tile(j0 + 2 * kTV, cw, bx);
       // acc[r]: row 8 (r / 4) + 4 h + r % 4 of the work item, column li (vector j0 + li).
       if constexpr (ROUND == 1) {
@@ -995,14 +1066,15 @@ bool screen_supported(int dim, int m) {
 }
 
 
-fgpu_status launch_screen_prep(const float* codebook, int m, int sub, const uint8_t* codes, int64_t total,
-                               uint16_t* cb16, uint4* vext, unsigned int* xmax_bits, hipStream_t s) {
+fgpu_status launch_screen_prep(const float* codebook, int m, int sub, int scale_exp, const uint8_t* codes,
+                               int64_t total, uint16_t* cb16, uint4* vext, unsigned int* xmax_bits, hipStream_t s) {
   const int64_t ncb = (int64_t)m * kPQK * sub;
-  hipLaunchKernelGGL(cb_bf16_kernel, dim3((unsigned)((ncb + 255) / 256)), dim3(256), 0, s, codebook, ncb, cb16);
+  hipLaunchKernelGGL(cb_f16_kernel, dim3((unsigned)((ncb + 255) / 256)), dim3(256), 0, s, codebook, ncb, scale_exp,
+                     cb16);
   FGPU_HIP(hipMemsetAsync(xmax_bits, 0, sizeof(unsigned int), s));
   if (total > 0)
     hipLaunchKernelGGL(screen_prep_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, codebook, m, sub,
-                       codes, total, vext, xmax_bits);
+                       scale_exp, codes, total, vext, xmax_bits);
   FGPU_HIP(hipGetLastError());
   return FGPU_OK;
 }
