@@ -247,7 +247,9 @@ struct TpScreenWs {
   float* vd = nullptr;
   int* hist = nullptr;  // [2 nlist + 1]: list counts, then launch_tp_order's fill counts
   int32_t* boff = nullptr;
-  int32_t* order = nullptr;
+  int32_t* order = nullptr;   // the virtual queries by list: the rescore's order and the screen's buckets
+  int32_t* sp_cnt = nullptr;  // [nlist] the screen's single-probe counts
+  float2* pnorm = nullptr;    // [nvq]
   ScreenWs sw;
   bool carve(void* base, size_t bytes, int nvq, int nlist, int dim, int k) {
     Carve cv(base, bytes);
@@ -259,6 +261,8 @@ struct TpScreenWs {
     hist = cv.take<int>(2 * (size_t)nlist + 1);
     boff = cv.take<int32_t>((size_t)nlist + 1);
     order = cv.take<int32_t>((size_t)nvq);
+    sp_cnt = cv.take<int32_t>((size_t)nlist);
+    pnorm = cv.take<float2>((size_t)nvq);
     return cv.ok() && sw.carve(cv.base + cv.used, bytes - cv.used, nvq, nlist, 1, true);
   }
   static size_t bytes(int nvq, int nlist, int dim, int k) {
@@ -266,7 +270,7 @@ struct TpScreenWs {
            carve_bytes<float>((size_t)nvq) + carve_bytes<int32_t>((size_t)nvq * k) +
            carve_bytes<float>((size_t)nvq * k) + carve_bytes<int>(2 * (size_t)nlist + 1) +
            carve_bytes<int32_t>((size_t)nlist + 1) + carve_bytes<int32_t>((size_t)nvq) +
-           ScreenWs::bytes(nvq, nlist, 1, true);
+           carve_bytes<int32_t>((size_t)nlist) + carve_bytes<float2>((size_t)nvq) + ScreenWs::bytes(nvq, nlist, 1, true);
   }
 };
 
@@ -852,7 +856,7 @@ fgpu_status two_phase(const fgpu_index* ix, const float* dq, int nq, const uint3
             FGPU_HIP(mark(0));
             FGPU_TRY(launch_tp_virtual(qq + (int64_t)s0 * ix->dim, ix->dim, pp + (int64_t)s0 * nprobe, nprobe, p1, ns,
                                        ix->d_offsets, ix->nlist, tw.vq, tw.vprobe, tw.vpd, tw.hist, s));
-            FGPU_TRY(launch_tp_offsets(tw.hist, ix->nlist, tw.boff, s));
+            FGPU_TRY(launch_tp_offsets(tw.hist, ix->nlist, tw.boff, ix->d_offsets, limit_k, tw.sp_cnt, s));
             FGPU_TRY(launch_tp_order(tw.vprobe, nvq, ix->nlist, tw.boff, tw.hist + ix->nlist, tw.order, s));
             FGPU_HIP(mark(1));
             ScreenArgs sa{tw.vq, ix->d_centroids, ix->d_offsets, ix->d_codes, ix->d_ids, ix->d_codebook, ix->d_cb16,
@@ -864,9 +868,13 @@ fgpu_status two_phase(const fgpu_index* ix, const float* dq, int nq, const uint3
             sa.cand_cnt = sa.cnt2 + ix->nlist;
             sa.first = tw.sw.first;
             sa.gminbuf = tw.sw.gminbuf;
-            sa.bucket = tw.sw.bucket;
+            sa.bucket = tw.order;  // single-probe mode: each list's queries, as ordered
             sa.boff = tw.boff;
             sa.order = tw.order;
+            sa.sp_cnt = tw.sp_cnt;
+            sa.pnorm = tw.pnorm;
+            sa.r2_chunk = 128;  // one 32-query group a list: shorter chunks balance round 2
+            sa.r2_max_chunks = 16;
             sa.arec = tw.sw.arec;
             sa.thr = tw.sw.thr;
             sa.cand = tw.sw.cand;

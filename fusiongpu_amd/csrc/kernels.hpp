@@ -158,6 +158,16 @@ struct ScreenArgs {
   // single-probe queries grouped by list so a list's codes stay in L2);
   // nullptr = ascending.
   const int32_t* order = nullptr;
+  // Single-probe mode (nprobe 1, compact buckets): sp_cnt[l] = the queries
+  // screened against list l in both rounds, whose entries are
+  // bucket[boff[l] .. boff[l] + sp_cnt[l]) (filled by the caller); round 2
+  // keeps round 1's pairs and records, and pnorm[q] holds the round-1 pair's
+  // (nr2, squared error sum).  nullptr = the general buckets.
+  const int32_t* sp_cnt = nullptr;
+  float2* pnorm = nullptr;
+  // Round 2's work items: list chunks of at least r2_chunk vectors (a
+  // multiple of 32), at most r2_max_chunks of them.
+  int r2_chunk = 256, r2_max_chunks = 8;
   uint4* arec;              // [nq nprobe][2][9] pair records: per lane half 8 A fragments and the extra block
   int2* first;              // [nq] round 1: (list, row scale exponent t) of the query's pair, (-1, -1), or (-2, 0)
   uint32_t* gminbuf;        // [nq][kMaxChunks][64] round 1: per query, first-list chunk and group, min U bits
@@ -234,14 +244,16 @@ int two_phase_pool_cap(int p1, int limit_k, int rerank_m);
 // Phase 1 through the screen: virtual query v = q p1 + p for the nqc queries
 // of a chunk (the query row copied to vq, probe p in vprobe, 0xFFFFFFFF when
 // unusable, a zero probe distance in vpd) and each usable list's count in
-// hist (zeroed first); boff = the exclusive scan of hist (nlist + 1 entries).
+// hist (zeroed first); boff = the exclusive scan of hist (nlist + 1 entries)
+// and sp_cnt the screen's single-probe counts (ScreenArgs::sp_cnt).
 // After the screen, launch_tp_finish completes most queries and leaves the
 // others' pool slots and cutoffs to launch_two_phase_after_phase1, which
 // runs the threshold, phase 2 and the final select (limit_k <= 64).
 fgpu_status launch_tp_virtual(const float* queries, int dim, const uint32_t* probes, int nprobe, int p1, int nqc,
                               const int32_t* offsets, int nlist, float* vq, uint32_t* vprobe, float* vpd, int* hist,
                               hipStream_t s);
-fgpu_status launch_tp_offsets(const int* hist, int nlist, int32_t* boff, hipStream_t s);
+fgpu_status launch_tp_offsets(const int* hist, int nlist, int32_t* boff, const int32_t* offsets, int k,
+                              int32_t* sp_cnt, hipStream_t s);
 fgpu_status launch_two_phase_after_phase1(int dim, int m, const TwoPhaseArgs& a, hipStream_t s);
 // order[0 .. nvq): the virtual queries grouped by list (list l's at
 // boff[l] .. boff[l + 1), in no fixed order within it), those without a

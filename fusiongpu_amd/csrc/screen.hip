@@ -94,7 +94,7 @@ constexpr int kQB = 32;                  // queries per work item (MFMA rows)
 constexpr int kTV = 32;                  // vectors per tile (MFMA columns)
 constexpr int kSW = 16;                  // waves per screen workgroup
 constexpr int kCandBuf = 256;            // per-wave candidate staging entries (LDS)
-constexpr int kChunk = 256;              // list vectors per work item (at most kMaxChunks items a group)
+constexpr int kChunk = 256;              // list vectors per round-1 work item (at most kMaxChunks items a group)
 constexpr int kMaxChunks = 8;
 constexpr int kMaxGroups = 64;           // round-1 groups a query's first list splits into, at most
 // Groups of round 1: the k-th smallest group minimum bounds the k-th smallest
@@ -271,13 +271,17 @@ __device__ __forceinline__ int bucket_put(const ScreenArgs& a, int l, int q, int
 
 // Work items of list l: groups of kQB queries times chunks of the list of
 // kChunk vectors (longer chunks, multiples of kTV, past kMaxChunks of them).
-__device__ __forceinline__ int chunk_len(int n) {
-  return max(kChunk, (n + kMaxChunks * kTV - 1) / (kMaxChunks * kTV) * kTV);
+// Round 2 takes its chunk length and count from the launch (ScreenArgs).
+template <int ROUND = 1>
+__device__ __forceinline__ int chunk_len(const ScreenArgs& a, int n) {
+  const int kc = ROUND == 1 ? kChunk : a.r2_chunk, km = ROUND == 1 ? kMaxChunks : a.r2_max_chunks;
+  return max(kc, (n + km * kTV - 1) / (km * kTV) * kTV);
 }
-__device__ __forceinline__ int list_items(int cnt, int nq, int n) {
+template <int ROUND = 1>
+__device__ __forceinline__ int list_items(const ScreenArgs& a, int cnt, int nq, int n) {
   if (cnt <= 0 || n <= 0) return 0;
   const int ng = (min(cnt, nq) + kQB - 1) / kQB;
-  const int per = chunk_len(n);
+  const int per = chunk_len<ROUND>(a, n);
   return ng * ((n + per - 1) / per);
 }
 
@@ -317,21 +321,24 @@ __device__ __forceinline__ float2 centroid_dims(const ScreenArgs& a, int l) {
   const int lane = threadIdx.x & 63;
   return 2 * lane < D ? reinterpret_cast<const float2*>(a.centroids + (size_t)l * D)[lane] : make_float2(0.0f, 0.0f);
 }
-// The row scale exponent of a pair: nr2 unscaled, tt scaled.
-__device__ __forceinline__ int row_scale_exp(float nr2, double tt, int scale_exp) {
-  const double m = fmax(fmax(ldexp((double)nr2, 2 * scale_exp), tt), 1.0) * (1.0 + 0x1p-10);
+// The row scale exponent of a pair: nr2 unscaled, tt scaled; with `room`,
+// also room for any threshold the pair's own list can give, (R' + 64)^2.
+__device__ __forceinline__ int row_scale_exp(float nr2, double tt, int scale_exp, bool room = false) {
+  const double n2 = ldexp((double)nr2, 2 * scale_exp);
+  const double rt = sqrt(n2) + 64.0;
+  const double m = fmax(fmax(n2, room ? rt * rt * (1.0 + 0x1p-10) : tt), fmax(tt, 1.0)) * (1.0 + 0x1p-10);
   if (!(m <= 0x1p60)) return 99;  // NaN or far out of range
   int t = 0;
   while (ldexp(m, -t) > 0x1p14) ++t;
   return t;
 }
 template <int D>
-__device__ PairA pair_a(const ScreenArgs& a, int64_t ent, float2 qv, float2 cv, double tt) {
+__device__ PairA pair_a(const ScreenArgs& a, int64_t ent, float2 qv, float2 cv, double tt, bool room = false) {
   const int lane = threadIdx.x & 63;
   const bool has = 2 * lane < D;
   const float r0 = has ? qv.x - cv.x : 0.0f, r1 = has ? qv.y - cv.y : 0.0f;
   const float nr2 = wave_sum_f(__builtin_fmaf(r1, r1, r0 * r0));
-  const int t = row_scale_exp(nr2, tt, a.scale_exp);
+  const int t = row_scale_exp(nr2, tt, a.scale_exp, room);
   const bool ok = nr2 <= kMaxNorm2 && t <= 14;  // false for NaN
   // -2 r 2^(S-t): a power-of-two scaling, exact in fp32 (up to underflow below
   // 2^-126, covered by the absolute slack); its difference from the stored
@@ -424,9 +431,18 @@ __global__ __launch_bounds__(256) void screen_pairs1_kernel(ScreenArgs a) {
     f = make_int2(-2, 0);
   } else if (n >= a.k) {
     const int64_t ent = (int64_t)q * a.nprobe + pf;
-    const PairA pa = pair_a<D>(a, ent, query_dims(a, q, D), centroid_dims<D>(a, lf), 0.0);
+    // single-probe mode: the row scale leaves room for round 2's threshold
+    // (at most (R' + 64)^2 (1 + 2^-10) with 2^S-scaled decoded norms <= 64),
+    // so round 2 reuses this record's A fragments
+    const PairA pa = pair_a<D>(a, ent, query_dims(a, q, D), centroid_dims<D>(a, lf), 0.0, a.sp_cnt != nullptr);
     if (lane == 0) pair_ex<1>(a, ent, pa, 0.0f);
-    if (pa.t <= 14 && lane == 0) {
+    if (a.sp_cnt) {
+      // the caller placed the query in its list's bucket
+      if (lane == 0) {
+        a.pnorm[q] = make_float2(pa.nr2, pa.ea2);
+        if (pa.t <= 14) f = make_int2(lf, pa.t);
+      }
+    } else if (pa.t <= 14 && lane == 0) {
       const int pos = bucket_put(a, lf, q, (int)ent, atomicAdd(&a.cnt1[lf], 1));
       if (pos >= 0) f = make_int2(lf, pa.t);
     }
@@ -449,17 +465,19 @@ __global__ __launch_bounds__(256) void screen_pairs2_kernel(ScreenArgs a) {
   const int lane = threadIdx.x & 63;
   const int q = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   if (q >= a.nq) return;
+  const bool sp = a.sp_cnt != nullptr;
   // The first 64 probes' lists, sizes, bounds and the query's dims do not
-  // depend on T: their loads go out before the threshold's.
+  // depend on T: their loads go out before the threshold's (not needed in
+  // single-probe mode).
   uint32_t l0 = 0xFFFFFFFFu;
   float lb0 = INFINITY;
-  if (lane < a.nprobe) {
+  if (!sp && lane < a.nprobe) {
     const size_t t = (size_t)q * a.nprobe + lane;
     l0 = a.probes[t];
     if (l0 < (uint32_t)a.nlist && a.offsets[l0 + 1] - a.offsets[l0] > 0)
       lb0 = list_lower_bound(a.probe_dists[t], a.rmax[l0]);
   }
-  const float2 qv = query_dims(a, q, D);
+  const float2 qv = sp ? make_float2(0.0f, 0.0f) : query_dims(a, q, D);
   const int2 f = a.first[q];
   if (f.x == -2) {
     // candidates set by the first pair kernel: the largest finite threshold
@@ -470,7 +488,7 @@ __global__ __launch_bounds__(256) void screen_pairs2_kernel(ScreenArgs a) {
   uint32_t gm = 0x7F800000u;
   if (f.x >= 0 && lane < screen_groups(a.k)) {
     const int n = a.offsets[f.x + 1] - a.offsets[f.x];
-    const int per = chunk_len(n), nch = (n + per - 1) / per;
+    const int per = chunk_len<1>(a, n), nch = (n + per - 1) / per;
     const uint32_t* g = a.gminbuf + (size_t)q * kMaxChunks * kMaxGroups + lane;
     // every chunk's load issued at once (a chain of them is the kernel's
     // longest latency)
@@ -485,6 +503,25 @@ __global__ __launch_bounds__(256) void screen_pairs2_kernel(ScreenArgs a) {
   const float kth = __uint_as_float((uint32_t)__builtin_amdgcn_readlane((int)gm, a.k - 1));
   // the group minima are at the round-1 row's scale 2^-f.y
   const float T = kth < INFINITY ? f_above(ldexp((double)kth, f.y) * kTInfl) : INFINITY;
+  if (sp) {
+    // Single-probe mode: the round-2 pair is the round-1 pair (the only
+    // probe, whose list holds the threshold's own k vectors, so its bound
+    // never exceeds T), and only its constant block changes; its A fragments
+    // stay valid because round 1 chose the row scale with room for any
+    // threshold its list can give.  A row in a bucket without a threshold
+    // (an unusable round-1 pair) gets the unusable block, and its query the
+    // LUT kernel.
+    if (lane == 0) {
+      PairA pa{0.0f, 0.0f, 99};
+      if (f.x >= 0 && T < INFINITY) {
+        const float2 pn = a.pnorm[q];
+        pa = PairA{pn.x, pn.y, f.y};
+      }
+      pair_ex<2>(a, (int64_t)q * a.nprobe, pa, T);
+      a.thr[q] = pa.t <= 14 ? T : INFINITY;
+    }
+    return;
+  }
   if (lane == 0) a.thr[q] = T;
   if (!(T < INFINITY)) return;
   const double tt = (double)T * kTInfl;            // the V constants' largest term
@@ -650,7 +687,7 @@ __global__ __launch_bounds__(kSW * kWave) void screen_kernel(ScreenArgs a) {
   int* wsum = pre + kScreenMaxLists + 1;             // [kSW]
   const int li = lane & 31, h = lane >> 5;
   const long long t_begin = a.stats ? clock64() : 0;
-  const int* cnt = ROUND == 1 ? a.cnt1 : a.cnt2;
+  const int* cnt = a.sp_cnt ? a.sp_cnt : ROUND == 1 ? a.cnt1 : a.cnt2;
   for (int i = tid; i < kCbBytes / 16; i += kSW * kWave)
     reinterpret_cast<uint4*>(lds)[i] = reinterpret_cast<const uint4*>(a.cb16)[i];
   // The work items: for each list, its groups of queries times its chunks,
@@ -661,7 +698,7 @@ __global__ __launch_bounds__(kSW * kWave) void screen_kernel(ScreenArgs a) {
 #pragma unroll
     for (int i = 0; i < kPer; ++i) {
       const int l = tid * kPer + i;
-      v[i] = l < a.nlist ? list_items(cnt[l], bucket_len(a, l), a.offsets[l + 1] - a.offsets[l]) : 0;
+      v[i] = l < a.nlist ? list_items<ROUND>(a, cnt[l], bucket_len(a, l), a.offsets[l + 1] - a.offsets[l]) : 0;
       s += v[i];
     }
     const int incl = wave_incl_scan(s);
@@ -704,7 +741,7 @@ __global__ __launch_bounds__(kSW * kWave) void screen_kernel(ScreenArgs a) {
     }
     const int l = __builtin_amdgcn_readfirstlane(lo);
     const int start = a.offsets[l], n = a.offsets[l + 1] - start;
-    const int per = chunk_len(n), nch = (n + per - 1) / per;
+    const int per = chunk_len<ROUND>(a, n), nch = (n + per - 1) / per;
     const int local = w - __builtin_amdgcn_readfirstlane(pre[l]);
     const int grp = local / nch, jb = (local % nch) * per, je = min(n, jb + per);
     const int nrow = min(kQB, min(cnt[l], bucket_len(a, l)) - grp * kQB);
@@ -1081,6 +1118,8 @@ fgpu_status launch_screen_prep(const float* codebook, int m, int sub, int scale_
 
 fgpu_status launch_screen(int dim, int m, const ScreenArgs& a, hipStream_t s) {
   FGPU_CHECK(a.k >= 1 && a.k <= 64, FGPU_ERR_UNSUPPORTED, "screen: k must be in [1, 64]");
+  FGPU_CHECK(a.r2_chunk >= kTV && a.r2_chunk % kTV == 0 && a.r2_max_chunks >= 1, FGPU_ERR_ARG,
+             "screen: bad round-2 chunking");
   if (a.nq <= 0) return FGPU_OK;
   if (dim == 128 && m == 32) return launch_screen_dm<128, 32>(a, s);
   if (dim == 128 && m == 16) return launch_screen_dm<128, 16>(a, s);

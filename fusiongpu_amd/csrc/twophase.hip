@@ -969,9 +969,13 @@ __global__ __launch_bounds__(256) void tp_order_kernel(const uint32_t* __restric
 }
 
 // boff[l] = hist[0] + ... + hist[l - 1] for l = 0 .. nlist (one workgroup,
-// nlist <= 8192: each thread sums 8 consecutive counts).
+// nlist <= 8192: each thread sums 8 consecutive counts), and the screen's
+// single-probe counts sp_cnt[l] = hist[l] for lists of at least k vectors, 0
+// for the shorter ones (their queries take the list's vectors directly).
 __global__ __launch_bounds__(1024) void tp_offsets_kernel(const int* __restrict__ hist, int nlist,
-                                                          int32_t* __restrict__ boff) {
+                                                          int32_t* __restrict__ boff,
+                                                          const int32_t* __restrict__ offsets, int k,
+                                                          int32_t* __restrict__ sp_cnt) {
   __shared__ int wsum[16];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   int v[8], sum = 0;
@@ -980,6 +984,7 @@ __global__ __launch_bounds__(1024) void tp_offsets_kernel(const int* __restrict_
     const int l = tid * 8 + i;
     v[i] = l < nlist ? hist[l] : 0;
     sum += v[i];
+    if (l < nlist) sp_cnt[l] = offsets[l + 1] - offsets[l] >= k ? v[i] : 0;
   }
   const int incl = wave_incl_scan(sum);
   if (lane == kWave - 1) wsum[wave] = incl;
@@ -1331,9 +1336,10 @@ fgpu_status launch_tp_virtual(const float* queries, int dim, const uint32_t* pro
   return FGPU_OK;
 }
 
-fgpu_status launch_tp_offsets(const int* hist, int nlist, int32_t* boff, hipStream_t s) {
+fgpu_status launch_tp_offsets(const int* hist, int nlist, int32_t* boff, const int32_t* offsets, int k,
+                              int32_t* sp_cnt, hipStream_t s) {
   FGPU_CHECK(nlist >= 1 && nlist <= 8192, FGPU_ERR_ARG, "two_phase: bad list count");
-  hipLaunchKernelGGL(tp_offsets_kernel, dim3(1), dim3(1024), 0, s, hist, nlist, boff);
+  hipLaunchKernelGGL(tp_offsets_kernel, dim3(1), dim3(1024), 0, s, hist, nlist, boff, offsets, k, sp_cnt);
   FGPU_HIP(hipGetLastError());
   return FGPU_OK;
 }
