@@ -888,8 +888,9 @@ fgpu_status two_phase(const fgpu_index* ix, const float* dq, int nq, const uint3
             la.qlist = tw.sw.flist;
             la.qcount = tw.sw.zero + kCtrFlag;
             FGPU_TRY(launch_adc_plain_list(ix->dim, ix->m, la, s));
-            FGPU_TRY(launch_tp_stats(sa.cand_cnt, sa.thr, nvq, kScreenCandCap, tw.sw.zero + kCtrFlag, sa.cnt1,
-                                     sa.cnt2, tw.boff, ix->d_offsets, ix->nlist, d_stats, s));
+            // single-probe mode: both rounds screen the sp_cnt pairs
+            FGPU_TRY(launch_tp_stats(sa.cand_cnt, sa.thr, nvq, kScreenCandCap, tw.sw.zero + kCtrFlag, tw.sp_cnt,
+                                     tw.sp_cnt, tw.boff, ix->d_offsets, ix->nlist, d_stats, s));
             FGPU_TRY(launch_tp_finish(a, ix->dim, s0, ns, tw.vids, tw.vd,
                                       d_probe_dists ? d_probe_dists + q0 * nprobe : nullptr, slow + 1, slow, s));
           }
