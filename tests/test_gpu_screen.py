@@ -238,6 +238,29 @@ def test_screen_off_beyond_its_norm_range():
     idx.close()
 
 
+def test_screen_row_scales_for_far_queries():
+    """Queries far from the data: each pair row of the fp16 screen runs at its
+    own power-of-two scale (its residual norm squared over 2^14), so a query
+    tens of data radii away still takes the screen; one whose row would need
+    more than 2^14 takes the LUT kernel.  Bit-exact either way."""
+    _say("screen row scales, far queries")
+    rng = np.random.default_rng(21)
+    offs, ids, codes, cent, cb = _gmm_index(128, 32, 64, 20000, seed=21)
+    idx = fg.Index.from_arrays(128, 32, offs, ids, codes, cent, cb)
+    assert idx.screen_ready
+    q = fg.gen_gmm(200, 128, 32, seed=21, set=1, sig_lo=0.08)
+    spread = float(np.linalg.norm(cent - cent.mean(axis=0), axis=1).max())
+    d = rng.standard_normal(128).astype(np.float32)
+    d /= np.linalg.norm(d)
+    q[:60] += d * np.float32(30.0 * spread)      # far: larger row scales, still screened
+    q[60:70] += d * np.float32(3.0e5 * spread)   # beyond the row scales: the LUT kernel
+    q = q.astype(np.float32)
+    st = _check(idx, q, cent, cb, offs, ids, codes, 8, 10)
+    assert st["queries_with_threshold"] == 190
+    assert st["queries_to_lut_kernel"] >= 10
+    idx.close()
+
+
 def test_screen_misaligned_queries_take_the_lut_kernel():
     """A query array 4 bytes off 16-byte alignment: the screen's vector loads
     need 16, so search takes the LUT kernels, results unchanged."""
