@@ -1010,8 +1010,10 @@ __global__ __launch_bounds__(1024) void tp_offsets_kernel(const int* __restrict_
 // two-phase kernel's mode 2 does: each phase-1 cutoff is the w-th distance of
 // a usable phase-1 probe (w = min(n, limit_k); 0 for the others) and the
 // threshold is coeff times the smallest positive cutoff.  Then every usable
-// phase-2 list's lower bound (list_lower_bound; any valid one skips the same
-// lists' appends, since none of their vectors reaches the threshold): when
+// phase-2 list's lower bound (list_lower_bound of the coarse step's probe
+// distance, or of a wave-wide fp32 sum of the squared residual; any valid
+// bound skips the same lists' appends, since none of their vectors reaches
+// the threshold): when
 // none is <= thr (1 + 2^-16) -- the mode-2 skip test -- phase 2 appends
 // nothing, and when the phase-1 keys also fit rerank_m they are the answer,
 // sorted: each usable phase-1 probe's keys are one 64-lane vector (padded
@@ -1126,28 +1128,44 @@ __global__ __launch_bounds__(kFinWaves * kWave) void tp_finish_kernel(TwoPhaseAr
   const float thr_hi = thr * (1.0f + 0x1p-16f);
   bool slow = nrun > kFinRuns || total > R;
   int skipped = 0;
+  // this lane's two query dims (without probe distances, each list's residual
+  // norm is one wave-wide sum over a coalesced read of its centroid row)
+  const bool dl = 2 * lane < dim;
+  const float2 qd = !pd && dl ? reinterpret_cast<const float2*>(a.queries + (size_t)q * dim)[lane]
+                              : make_float2(0.0f, 0.0f);
   for (int c0 = p1; !slow && c0 < P; c0 += kWave) {
     const int p = c0 + lane;
-    bool use = false, reach = false;
+    uint32_t l = NL;
+    bool use = false;
     if (p < P) {
-      const uint32_t l = pr[p];
-      if (l < NL && a.offsets[l + 1] > a.offsets[l]) {
-        use = true;
-        float s2 = 0.0f;
-        if (pd) {
-          s2 = pd[(size_t)q * P + p];
-        } else {
-          const float4* qv = reinterpret_cast<const float4*>(a.queries + (size_t)q * dim);
-          const float4* cv = reinterpret_cast<const float4*>(a.centroids + (size_t)l * dim);
-          for (int d = 0; d < dim / 4; ++d) {
-            const float4 x = qv[d], c = cv[d];
-            const float r0 = x.x - c.x, r1 = x.y - c.y, r2 = x.z - c.z, r3 = x.w - c.w;
-            s2 += r0 * r0 + r1 * r1 + r2 * r2 + r3 * r3;
-          }
+      l = pr[p];
+      use = l < NL && a.offsets[l + 1] > a.offsets[l];
+    }
+    float s2 = 0.0f;
+    if (pd) {
+      if (use) s2 = pd[(size_t)q * P + p];
+    } else {
+      uint64_t m = __ballot(use);
+      while (m) {  // four lists at a time: their row loads in flight together
+        int b[4];
+        float2 cv[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          b[k] = m ? __builtin_ctzll(m) : -1;
+          if (m) m &= m - 1;
+          const uint32_t lk = b[k] >= 0 ? (uint32_t)__builtin_amdgcn_readlane((int)l, b[k]) : 0u;
+          cv[k] = b[k] >= 0 && dl ? reinterpret_cast<const float2*>(a.centroids + (size_t)lk * dim)[lane]
+                                  : make_float2(0.0f, 0.0f);
         }
-        reach = list_lower_bound(s2, a.rmax[l]) <= thr_hi;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const float r0 = dl ? qd.x - cv[k].x : 0.0f, r1 = dl ? qd.y - cv[k].y : 0.0f;
+          const float v = wave_sum_f(__builtin_fmaf(r1, r1, r0 * r0));
+          if (lane == b[k]) s2 = v;
+        }
       }
     }
+    const bool reach = use && list_lower_bound(s2, a.rmax[use ? l : 0]) <= thr_hi;
     slow = __ballot(reach) != 0;
     skipped += __popcll(__ballot(use));
   }
@@ -1346,8 +1364,8 @@ fgpu_status launch_tp_offsets(const int* hist, int nlist, int32_t* boff, const i
 
 fgpu_status launch_tp_finish(const TwoPhaseArgs& a, int dim, int q_base, int nqc, const int32_t* vids, const float* vd,
                              const float* probe_dists, int32_t* slow_list, int* slow_cnt, hipStream_t s) {
-  FGPU_CHECK(dim % 4 == 0 && a.limit_k >= 1 && a.limit_k <= kWave && a.cut_ws && a.pool, FGPU_ERR_ARG,
-             "two_phase: bad finish arguments");
+  FGPU_CHECK(dim % 4 == 0 && dim <= 2 * kWave && a.limit_k >= 1 && a.limit_k <= kWave && a.cut_ws && a.pool,
+             FGPU_ERR_ARG, "two_phase: bad finish arguments");
   if (nqc <= 0) return FGPU_OK;
   hipLaunchKernelGGL(tp_finish_kernel, dim3((unsigned)((nqc + kFinWaves - 1) / kFinWaves)), dim3(kFinWaves * kWave), 0,
                      s, a, dim, q_base, nqc, vids, vd, probe_dists, slow_list, slow_cnt);
