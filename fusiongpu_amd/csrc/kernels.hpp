@@ -169,7 +169,8 @@ struct ScreenArgs {
   // multiple of 32), at most r2_max_chunks of them.
   int r2_chunk = 256, r2_max_chunks = 8;
   uint4* arec;              // [nq nprobe][2][9] pair records: per lane half 8 A fragments and the extra block
-  int2* first;              // [nq] round 1: (list, row scale exponent t) of the query's pair, (-1, -1), or (-2, 0)
+  int2* first;              // [nq] round 1: (list, t | chunks << 8) of the query's pair (t its row scale
+                            // exponent, chunks its list's round-1 work items), (-1, -1), or (-2, 0)
   uint32_t* gminbuf;        // [nq][kMaxChunks][64] round 1: per query, first-list chunk and group, min U bits
   float* thr;               // [nq] T(q)
   uint2* cand;              // [nq][cand_cap] (vector position, list)

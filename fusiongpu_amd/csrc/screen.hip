@@ -97,6 +97,7 @@ constexpr int kCandBuf = 256;            // per-wave candidate staging entries (
 constexpr int kChunk = 256;              // list vectors per round-1 work item (at most kMaxChunks items a group)
 constexpr int kMaxChunks = 8;
 constexpr int kMaxGroups = 64;           // round-1 groups a query's first list splits into, at most
+constexpr int kPairBatch = 8;            // round-2 pairs whose centroid rows a wave loads together
 // Groups of round 1: the k-th smallest group minimum bounds the k-th smallest
 // U from above only when k <= groups.
 __host__ __device__ constexpr int screen_groups(int k) { return k > 32 ? 64 : 32; }
@@ -431,6 +432,8 @@ __global__ __launch_bounds__(256) void screen_pairs1_kernel(ScreenArgs a) {
     f = make_int2(-2, 0);
   } else if (n >= a.k) {
     const int64_t ent = (int64_t)q * a.nprobe + pf;
+    // first.y: the row scale exponent t and the list's round-1 chunk count
+    const int per = chunk_len<1>(a, n), fy = (((n + per - 1) / per) << 8);
     // single-probe mode: the row scale leaves room for round 2's threshold
     // (at most (R' + 64)^2 (1 + 2^-10) with 2^S-scaled decoded norms <= 64),
     // so round 2 reuses this record's A fragments
@@ -440,11 +443,11 @@ __global__ __launch_bounds__(256) void screen_pairs1_kernel(ScreenArgs a) {
       // the caller placed the query in its list's bucket
       if (lane == 0) {
         a.pnorm[q] = make_float2(pa.nr2, pa.ea2);
-        if (pa.t <= 14) f = make_int2(lf, pa.t);
+        if (pa.t <= 14) f = make_int2(lf, fy | pa.t);
       }
     } else if (pa.t <= 14 && lane == 0) {
       const int pos = bucket_put(a, lf, q, (int)ent, atomicAdd(&a.cnt1[lf], 1));
-      if (pos >= 0) f = make_int2(lf, pa.t);
+      if (pos >= 0) f = make_int2(lf, fy | pa.t);
     }
   }
   if (lane == 0) a.first[q] = f;
@@ -479,6 +482,7 @@ __global__ __launch_bounds__(256) void screen_pairs2_kernel(ScreenArgs a) {
   }
   const float2 qv = sp ? make_float2(0.0f, 0.0f) : query_dims(a, q, D);
   const int2 f = a.first[q];
+  const int ft = f.y & 0xFF;  // the round-1 row scale exponent
   if (f.x == -2) {
     // candidates set by the first pair kernel: the largest finite threshold
     // sends them to the rescore
@@ -487,8 +491,7 @@ __global__ __launch_bounds__(256) void screen_pairs2_kernel(ScreenArgs a) {
   }
   uint32_t gm = 0x7F800000u;
   if (f.x >= 0 && lane < screen_groups(a.k)) {
-    const int n = a.offsets[f.x + 1] - a.offsets[f.x];
-    const int per = chunk_len<1>(a, n), nch = (n + per - 1) / per;
+    const int nch = f.y >> 8;
     const uint32_t* g = a.gminbuf + (size_t)q * kMaxChunks * kMaxGroups + lane;
     // every chunk's load issued at once (a chain of them is the kernel's
     // longest latency)
@@ -501,8 +504,8 @@ __global__ __launch_bounds__(256) void screen_pairs2_kernel(ScreenArgs a) {
   // U >= 0, so float order is unsigned order of the bits
   wave_sort_u32(gm);
   const float kth = __uint_as_float((uint32_t)__builtin_amdgcn_readlane((int)gm, a.k - 1));
-  // the group minima are at the round-1 row's scale 2^-f.y
-  const float T = kth < INFINITY ? f_above(ldexp((double)kth, f.y) * kTInfl) : INFINITY;
+  // the group minima are at the round-1 row's scale 2^-t
+  const float T = kth < INFINITY ? f_above(ldexp((double)kth, ft) * kTInfl) : INFINITY;
   if (sp) {
     // Single-probe mode: the round-2 pair is the round-1 pair (the only
     // probe, whose list holds the threshold's own k vectors, so its bound
@@ -515,7 +518,7 @@ __global__ __launch_bounds__(256) void screen_pairs2_kernel(ScreenArgs a) {
       PairA pa{0.0f, 0.0f, 99};
       if (f.x >= 0 && T < INFINITY) {
         const float2 pn = a.pnorm[q];
-        pa = PairA{pn.x, pn.y, f.y};
+        pa = PairA{pn.x, pn.y, ft};
       }
       pair_ex<2>(a, (int64_t)q * a.nprobe, pa, T);
       a.thr[q] = pa.t <= 14 ? T : INFINITY;
@@ -543,24 +546,29 @@ __global__ __launch_bounds__(256) void screen_pairs2_kernel(ScreenArgs a) {
     // unusable sends the whole query to the LUT kernel, whose rescore then
     // ignores its candidates.
     const int pos = pass ? atomicAdd(&a.cnt2[l], 1) : 0;
-    // The A fragments, one pair at a time with the next pair's centroid
-    // loads in flight; the lane of each probe keeps its pair's (nr2, error
+    // The A fragments, one pair at a time, eight pairs' centroid rows loaded
+    // together ahead of them (a chain of single row loads is this loop's
+    // longest latency); the lane of each probe keeps its pair's (nr2, error
     // sum), and the extra blocks follow lane-parallel (one lane a pair).
     uint64_t m = __ballot(pass);
     if (!m) continue;
     PairA my_pa{0.0f, 0.0f, 99};
-    int b = __builtin_ctzll(m);
-    float2 cv = centroid_dims<D>(a, __builtin_amdgcn_readlane((int)l, b));
-    while (true) {
-      const uint64_t rest = m & (m - 1);
-      const int bn = rest ? __builtin_ctzll(rest) : b;
-      const float2 cn = rest ? centroid_dims<D>(a, __builtin_amdgcn_readlane((int)l, bn)) : cv;
-      const PairA pa = pair_a<D>(a, (int64_t)q * a.nprobe + p0 + b, qv, cv, tt);
-      if (lane == b) my_pa = pa;
-      if (!rest) break;
-      m = rest;
-      b = bn;
-      cv = cn;
+    while (m) {
+      int b[kPairBatch];
+      float2 cv[kPairBatch];
+#pragma unroll
+      for (int j = 0; j < kPairBatch; ++j) {
+        b[j] = m ? __builtin_ctzll(m) : -1;
+        if (m) m &= m - 1;
+        // list 0 stands in past the last pair (a row that exists; unused)
+        cv[j] = centroid_dims<D>(a, b[j] >= 0 ? __builtin_amdgcn_readlane((int)l, b[j]) : 0);
+      }
+#pragma unroll
+      for (int j = 0; j < kPairBatch; ++j) {
+        if (b[j] < 0) break;
+        const PairA pa = pair_a<D>(a, (int64_t)q * a.nprobe + p0 + b[j], qv, cv[j], tt);
+        if (lane == b[j]) my_pa = pa;
+      }
     }
     if (pass) {
       pair_ex<2>(a, (int64_t)q * a.nprobe + p, my_pa, T);
