@@ -481,6 +481,15 @@ __global__ __launch_bounds__(256) void screen_pairs2_kernel(ScreenArgs a) {
       lb0 = list_lower_bound(a.probe_dists[t], a.rmax[l0]);
   }
   const float2 qv = sp ? make_float2(0.0f, 0.0f) : query_dims(a, q, D);
+  // Every chunk's group minima load goes out with the first pair's record
+  // (a chain of the two is the kernel's longest latency); the query's block
+  // holds kMaxChunks x kMaxGroups words, those past its chunks are unused.
+  uint32_t gc[kMaxChunks];
+  {
+    const uint32_t* g = a.gminbuf + (size_t)q * kMaxChunks * kMaxGroups + lane;
+#pragma unroll
+    for (int c = 0; c < kMaxChunks; ++c) gc[c] = g[c * kMaxGroups];
+  }
   const int2 f = a.first[q];
   const int ft = f.y & 0xFF;  // the round-1 row scale exponent
   if (f.x == -2) {
@@ -492,14 +501,8 @@ __global__ __launch_bounds__(256) void screen_pairs2_kernel(ScreenArgs a) {
   uint32_t gm = 0x7F800000u;
   if (f.x >= 0 && lane < screen_groups(a.k)) {
     const int nch = f.y >> 8;
-    const uint32_t* g = a.gminbuf + (size_t)q * kMaxChunks * kMaxGroups + lane;
-    // every chunk's load issued at once (a chain of them is the kernel's
-    // longest latency)
-    uint32_t gc[kMaxChunks];
 #pragma unroll
-    for (int c = 0; c < kMaxChunks; ++c) gc[c] = c < nch ? g[c * kMaxGroups] : 0x7F800000u;
-#pragma unroll
-    for (int c = 0; c < kMaxChunks; ++c) gm = min(gm, gc[c]);
+    for (int c = 0; c < kMaxChunks; ++c) gm = min(gm, c < nch ? gc[c] : 0x7F800000u);
   }
   // U >= 0, so float order is unsigned order of the bits
   wave_sort_u32(gm);
