@@ -931,16 +931,21 @@ __global__ __launch_bounds__(256) void tp_virtual_kernel(const float4* __restric
                                                          const int32_t* __restrict__ offsets, int nlist,
                                                          float4* __restrict__ vq, uint32_t* __restrict__ vprobe,
                                                          float* __restrict__ vpd, int* __restrict__ hist) {
-  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (i >= (int64_t)nvq * d4) return;
-  const int v = (int)(i / d4), c = (int)(i % d4);
-  const int qq = v / p1, p = v % p1;
-  vq[i] = q[(size_t)qq * d4 + c];
-  if (c == 0) {
+  // thread i copies float4 i of the rows (nvq d4 < 2^31, checked at launch);
+  // the first nvq threads also take virtual query i's list, so only their
+  // waves wait for the probe and offset loads
+  const uint32_t i = blockIdx.x * 256u + threadIdx.x;
+  const uint32_t n = (uint32_t)nvq * (uint32_t)d4;
+  if (i < n) {
+    const uint32_t v = i / (uint32_t)d4, c = i - v * (uint32_t)d4;
+    vq[i] = q[(size_t)(v / (uint32_t)p1) * d4 + c];
+  }
+  if (i < (uint32_t)nvq) {
+    const uint32_t qq = i / (uint32_t)p1, p = i - qq * (uint32_t)p1;
     const uint32_t l = probes[(size_t)qq * P + p];
     const bool use = l < (uint32_t)nlist && offsets[l + 1] > offsets[l];
-    vprobe[v] = use ? l : 0xFFFFFFFFu;
-    vpd[v] = 0.0f;
+    vprobe[i] = use ? l : 0xFFFFFFFFu;
+    vpd[i] = 0.0f;
     if (use) atomicAdd(&hist[l], 1);
   }
 }
@@ -1347,6 +1352,7 @@ fgpu_status launch_tp_virtual(const float* queries, int dim, const uint32_t* pro
   hipLaunchKernelGGL(tp_zero_kernel, dim3((unsigned)((2 * nlist + 1 + 255) / 256)), dim3(256), 0, s, hist,
                      2 * nlist + 1);
   const int64_t nvq = (int64_t)nqc * p1, nt = nvq * (dim / 4);
+  FGPU_CHECK(dim >= 4 && nt < (int64_t(1) << 31), FGPU_ERR_ARG, "two_phase: too many virtual query values");
   hipLaunchKernelGGL(tp_virtual_kernel, dim3((unsigned)((nt + 255) / 256)), dim3(256), 0, s,
                      reinterpret_cast<const float4*>(queries), dim / 4, probes, nprobe, p1, (int)nvq, offsets, nlist,
                      reinterpret_cast<float4*>(vq), vprobe, vpd, hist);
