@@ -980,7 +980,11 @@ __device__ __forceinline__ void load_row(const float* p, float (&v)[S]) {
 // reference's direct form (the LUT entry's chain per subspace, summed in
 // ascending m), then the k smallest (distance, id) keys.  A persistent grid
 // of one workgroup per CU holding the fp32 codebook in LDS; wave g takes
-// queries g, g + G, ... (of a.order when set).  ONE (single-probe queries): every candidate lies in
+// queries g, g + G, ... (of a.order when set), where workgroup b counts as
+// b / 8 + (b % 8) G / (8 kRW) when the grid is a multiple of 8: workgroups go
+// round-robin over the 8 XCDs, so neighbouring positions of the order (one
+// list's queries, whose code rows they gather) share an XCD's L2.
+// ONE (single-probe queries): every candidate lies in
 // the query's one list, so the residual r = fl(q - c) is formed once in LDS
 // (the same fp32 subtraction) instead of loading the centroid per candidate.
 constexpr int kRW = 16;  // waves per rescore workgroup
@@ -994,7 +998,9 @@ __global__ __launch_bounds__(kRW * kWave) void rescore_kernel(ScreenArgs a) {
     reinterpret_cast<float4*>(cbf)[i] = reinterpret_cast<const float4*>(a.codebook)[i];
   __syncthreads();
   const int stride = (int)gridDim.x * kRW;
-  int i = (int)blockIdx.x * kRW + wave;
+  const int nb = (int)gridDim.x, b = (int)blockIdx.x;
+  const int lb = nb % 8 == 0 ? (b % 8) * (nb / 8) + b / 8 : b;
+  int i = lb * kRW + wave;
   int qn = i < a.nq ? (a.order ? a.order[i] : i) : 0;
   for (; i < a.nq; i += stride) {
     const int q = __builtin_amdgcn_readfirstlane(qn);
