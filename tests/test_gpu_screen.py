@@ -203,6 +203,25 @@ def test_screen_hands_candidate_overflow_to_the_lut_kernel():
     idx.close()
 
 
+@pytest.mark.parametrize("nprobe", [32, 27])
+def test_screen_every_probe_passes_round_2(nprobe):
+    """One Gaussian blob split into 32 lists: every list's bound is below each
+    query's threshold, so round 2 takes (almost) every probe, and the pair
+    kernel builds the A fragments of many probes a query, several batches of
+    centroid rows (the last one partial at 27 probes)."""
+    _say(f"screen all probes pass, nprobe={nprobe}")
+    dim, m, nlist, k = 128, 32, 32, 10
+    x = fg.gen_gmm(16000, dim, 1, seed=5, sig_lo=0.08)
+    offs, ids, codes, cent, cb = fg.build_ivfpq(torch.from_numpy(x).cuda(), nlist, m, kmeans_iters=4, init_mode=1,
+                                                seed=5, pq_iters=3, sample_size=4000)
+    idx = fg.Index.from_arrays(dim, m, offs, ids, codes, cent, cb)
+    q = fg.gen_gmm(200, dim, 1, seed=5, set=1, sig_lo=0.08)
+    st = _check(idx, q, cent, cb, offs, ids, codes, nprobe, k)
+    assert st["queries_with_threshold"] == 200
+    assert st["pairs_round2"] >= 200 * nprobe * 9 // 10
+    idx.close()
+
+
 @pytest.mark.parametrize("scale", [300.0, 1e-3])
 def test_screen_scaled_data(scale):
     """Large (x 300, norms^2 near 1e7) and small (x 1e-3) data: the bounds'
