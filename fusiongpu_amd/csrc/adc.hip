@@ -205,7 +205,7 @@ __device__ __forceinline__ void plain_query(const AdcArgs& a, int q, float* smem
 #pragma unroll
     for (int j = 0; j < C::S; ++j) cb[mm * C::S + j] = src[j];
   }
-  for (int i = tid; i < D; i += kNT) qs[i] = a.queries[(size_t)q * D + i];
+  for (int i = tid; i < D; i += kNT) qs[i] = a.queries[(size_t)(q / a.qdiv) * D + i];
   const uint32_t* probes = a.probes + (size_t)q * P;
   __syncthreads();
 
@@ -483,8 +483,9 @@ __global__ __launch_bounds__(kSpecWaves * kWave, 4) void adc_flow_kernel(AdcArgs
       if (a.probe_dists) {
         if (wave == 0 && pl_lane < NL) lb_lane = list_lower_bound(a.probe_dists[(size_t)q * P + lane], a.rmax[pl_lane]);
       }
-      const float qa = !a.probe_dists && q >= 0 && lane < D ? a.queries[(size_t)q * D + lane] : 0.0f;
-      const float qb = !a.probe_dists && q >= 0 && lane + kWave < D ? a.queries[(size_t)q * D + lane + kWave] : 0.0f;
+      const float qa = !a.probe_dists && q >= 0 && lane < D ? a.queries[(size_t)(q / a.qdiv) * D + lane] : 0.0f;
+      const float qb =
+          !a.probe_dists && q >= 0 && lane + kWave < D ? a.queries[(size_t)(q / a.qdiv) * D + lane + kWave] : 0.0f;
       // Otherwise each builder wave computes the bounds of its probes
       // p = wave + 8 j from the centroid rows, four lists at a time.
       constexpr int kBatch = 4;
@@ -572,7 +573,7 @@ __global__ __launch_bounds__(kSpecWaves * kWave, 4) void adc_flow_kernel(AdcArgs
       const int q = dyn ? s_q[s] : (int)blockIdx.x + i * G;
       if (q < 0 || q >= a.nq) break;
       const int nv = s_nv[s];
-      const float qv = lane < RW ? a.queries[(size_t)q * D + wave * RW + lane] : 0.0f;
+      const float qv = lane < RW ? a.queries[(size_t)(q / a.qdiv) * D + wave * RW + lane] : 0.0f;
       // This wave's centroid coordinates of the next list that may be built,
       // loaded ahead (cnext belongs to list cnext_f).
       int cnext_f = nv > 0 ? 0 : nv;

@@ -232,15 +232,14 @@ struct ScreenWs {
 };
 
 // Phase 1 of fgpu_two_phase_search through the screen: the buffers of one
-// chunk of nvq virtual queries (one per (query, phase-1 probe)): their query
-// rows, probes and (zero) probe distances, their top-limit_k results, the
+// chunk of nvq virtual queries (one per (query, phase-1 probe); virtual query
+// v reads query row v / p1 of the chunk): their probes and (zero) probe distances, their top-limit_k results, the
 // per-list counts and compact bucket offsets, and the screen's workspace.
 // Batches below this many queries keep phase 1 in the two-phase kernel (the
 // screen's fixed launches cost more than they save there).
 constexpr int kTpScreenMinQueries = 1024;
 constexpr int kTpVqMax = 131072;  // virtual queries a chunk (fuller 32-row MFMA groups per list)
 struct TpScreenWs {
-  float* vq = nullptr;
   uint32_t* vprobe = nullptr;
   float* vpd = nullptr;
   int32_t* vids = nullptr;
@@ -253,7 +252,7 @@ struct TpScreenWs {
   ScreenWs sw;
   bool carve(void* base, size_t bytes, int nvq, int nlist, int dim, int k) {
     Carve cv(base, bytes);
-    vq = cv.take<float>((size_t)nvq * dim);
+    (void)dim;
     vprobe = cv.take<uint32_t>((size_t)nvq);
     vpd = cv.take<float>((size_t)nvq);
     vids = cv.take<int32_t>((size_t)nvq * k);
@@ -266,7 +265,8 @@ struct TpScreenWs {
     return cv.ok() && sw.carve(cv.base + cv.used, bytes - cv.used, nvq, nlist, 1, true);
   }
   static size_t bytes(int nvq, int nlist, int dim, int k) {
-    return carve_bytes<float>((size_t)nvq * dim) + carve_bytes<uint32_t>((size_t)nvq) +
+    (void)dim;
+    return carve_bytes<uint32_t>((size_t)nvq) +
            carve_bytes<float>((size_t)nvq) + carve_bytes<int32_t>((size_t)nvq * k) +
            carve_bytes<float>((size_t)nvq * k) + carve_bytes<int>(2 * (size_t)nlist + 1) +
            carve_bytes<int32_t>((size_t)nlist + 1) + carve_bytes<int32_t>((size_t)nvq) +
@@ -854,14 +854,16 @@ fgpu_status two_phase(const fgpu_index* ix, const float* dq, int nq, const uint3
             FGPU_CHECK(tw.carve(tbase, ws_bytes - tofs, nvq, ix->nlist, ix->dim, limit_k), FGPU_ERR_WORKSPACE,
                        "two_phase_search: screen buffers do not fit");
             FGPU_HIP(mark(0));
-            FGPU_TRY(launch_tp_virtual(qq + (int64_t)s0 * ix->dim, ix->dim, pp + (int64_t)s0 * nprobe, nprobe, p1, ns,
-                                       ix->d_offsets, ix->nlist, tw.vq, tw.vprobe, tw.vpd, tw.hist, s));
+            const float* cq = qq + (int64_t)s0 * ix->dim;  // the chunk's query rows
+            FGPU_TRY(launch_tp_virtual(pp + (int64_t)s0 * nprobe, nprobe, p1, ns, ix->d_offsets, ix->nlist, tw.vprobe,
+                                       tw.vpd, tw.hist, s));
             FGPU_TRY(launch_tp_offsets(tw.hist, ix->nlist, tw.boff, ix->d_offsets, limit_k, tw.sp_cnt, s));
             FGPU_TRY(launch_tp_order(tw.vprobe, nvq, ix->nlist, tw.boff, tw.hist + ix->nlist, tw.order, s));
             FGPU_HIP(mark(1));
-            ScreenArgs sa{tw.vq, ix->d_centroids, ix->d_offsets, ix->d_codes, ix->d_ids, ix->d_codebook, ix->d_cb16,
+            ScreenArgs sa{cq, ix->d_centroids, ix->d_offsets, ix->d_codes, ix->d_ids, ix->d_codebook, ix->d_cb16,
                           ix->d_vext, ix->d_rmax, tw.vprobe, tw.vpd, nvq, 1, limit_k, ix->nlist};
             sa.scale_exp = ix->screen_scale_exp;
+            sa.qdiv = p1;
             sa.ctr = tw.sw.zero;
             sa.cnt1 = tw.sw.zero + kCtrCount;
             sa.cnt2 = sa.cnt1 + ix->nlist;
@@ -884,7 +886,8 @@ fgpu_status two_phase(const fgpu_index* ix, const float* dq, int nq, const uint3
             sa.out_d = tw.vd;
             sa.events = ev ? ev + 2 : nullptr;
             FGPU_TRY(launch_screen(ix->dim, ix->m, sa, s));
-            AdcArgs la = adc_args(ix, tw.vq, nvq, tw.vprobe, tw.vpd, 1, limit_k, tw.vids, tw.vd);
+            AdcArgs la = adc_args(ix, cq, nvq, tw.vprobe, tw.vpd, 1, limit_k, tw.vids, tw.vd);
+            la.qdiv = p1;
             la.qlist = tw.sw.flist;
             la.qcount = tw.sw.zero + kCtrFlag;
             FGPU_TRY(launch_adc_plain_list(ix->dim, ix->m, la, s));

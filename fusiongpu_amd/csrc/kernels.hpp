@@ -64,6 +64,9 @@ struct AdcArgs {
   // coarse step's form (sequential fused chain over fl(q - c)), which the
   // list lower bound accepts in place of its own sum (nullptr = compute).
   const float* probe_dists = nullptr;
+  // Queries per row of `queries`: query q reads row q / qdiv (several
+  // virtual queries of one query share its row).
+  int qdiv = 1;
   // Optional instrumentation (nullptr = off), summed over the launch:
   // [0] vectors whose codes were loaded, [1] LUTs built, [2] probed lists
   // skipped by the list lower bound; shader clocks per workgroup: [3] set-up,
@@ -168,6 +171,8 @@ struct ScreenArgs {
   // Round 2's work items: list chunks of at least r2_chunk vectors (a
   // multiple of 32), at most r2_max_chunks of them.
   int r2_chunk = 256, r2_max_chunks = 8;
+  // Queries per row of `queries`: query q reads row q / qdiv.
+  int qdiv = 1;
   uint4* arec;              // [nq nprobe][2][9] pair records: per lane half 8 A fragments and the extra block
   int2* first;              // [nq] round 1: (list, t | chunks << 8) of the query's pair (t its row scale
                             // exponent, chunks its list's round-1 work items), (-1, -1), or (-2, 0)
@@ -250,9 +255,8 @@ int two_phase_pool_cap(int p1, int limit_k, int rerank_m);
 // After the screen, launch_tp_finish completes most queries and leaves the
 // others' pool slots and cutoffs to launch_two_phase_after_phase1, which
 // runs the threshold, phase 2 and the final select (limit_k <= 64).
-fgpu_status launch_tp_virtual(const float* queries, int dim, const uint32_t* probes, int nprobe, int p1, int nqc,
-                              const int32_t* offsets, int nlist, float* vq, uint32_t* vprobe, float* vpd, int* hist,
-                              hipStream_t s);
+fgpu_status launch_tp_virtual(const uint32_t* probes, int nprobe, int p1, int nqc, const int32_t* offsets, int nlist,
+                              uint32_t* vprobe, float* vpd, int* hist, hipStream_t s);
 fgpu_status launch_tp_offsets(const int* hist, int nlist, int32_t* boff, const int32_t* offsets, int k,
                               int32_t* sp_cnt, hipStream_t s);
 fgpu_status launch_two_phase_after_phase1(int dim, int m, const TwoPhaseArgs& a, hipStream_t s);

@@ -389,7 +389,8 @@ __device__ void pair_ex(const ScreenArgs& a, int64_t ent, PairA pa, float T) {
 
 __device__ __forceinline__ float2 query_dims(const ScreenArgs& a, int q, int dim) {
   const int lane = threadIdx.x & 63;
-  return 2 * lane < dim ? reinterpret_cast<const float2*>(a.queries + (size_t)q * dim)[lane] : make_float2(0.0f, 0.0f);
+  return 2 * lane < dim ? reinterpret_cast<const float2*>(a.queries + (size_t)(q / a.qdiv) * dim)[lane]
+                        : make_float2(0.0f, 0.0f);
 }
 
 // Round 1 pairs, one wave a query: the query with its first usable probe (in
@@ -1017,9 +1018,9 @@ __global__ __launch_bounds__(kRW * kWave) void rescore_kernel(ScreenArgs a) {
     if constexpr (ONE) {
       const uint32_t l1 = a.probes[q];  // cnt > 0 only when it is a usable list
       for (int d = lane; d < D; d += kWave)
-        qs[wave][d] = cnt > 0 ? a.queries[(size_t)q * D + d] - a.centroids[(size_t)l1 * D + d] : 0.0f;
+        qs[wave][d] = cnt > 0 ? a.queries[(size_t)(q / a.qdiv) * D + d] - a.centroids[(size_t)l1 * D + d] : 0.0f;
     } else {
-      for (int d = lane; d < D; d += kWave) qs[wave][d] = a.queries[(size_t)q * D + d];
+      for (int d = lane; d < D; d += kWave) qs[wave][d] = a.queries[(size_t)(q / a.qdiv) * D + d];
     }
     wave_sync();
     const float* qv = qs[wave];

@@ -922,32 +922,23 @@ __global__ __launch_bounds__(256) void tp_zero_kernel(int* __restrict__ p, int n
   if (i < n) p[i] = 0;
 }
 
-// Virtual query v = q p1 + p (q of the chunk): the query row (copied, 16
-// bytes a thread), its probe p (0xFFFFFFFF when out of range or empty), a zero
+// Virtual query v = q p1 + p (q of the chunk; it reads query row q, as
+// v / p1, from the chunk's rows): its probe p (0xFFFFFFFF when out of range or
+// empty), a zero
 // probe distance (the lower bound of its only list is then 0, so the list is
 // always screened), and its list's count in hist.
-__global__ __launch_bounds__(256) void tp_virtual_kernel(const float4* __restrict__ q, int d4,
-                                                         const uint32_t* __restrict__ probes, int P, int p1, int nvq,
+__global__ __launch_bounds__(256) void tp_virtual_kernel(const uint32_t* __restrict__ probes, int P, int p1, int nvq,
                                                          const int32_t* __restrict__ offsets, int nlist,
-                                                         float4* __restrict__ vq, uint32_t* __restrict__ vprobe,
-                                                         float* __restrict__ vpd, int* __restrict__ hist) {
-  // thread i copies float4 i of the rows (nvq d4 < 2^31, checked at launch);
-  // the first nvq threads also take virtual query i's list, so only their
-  // waves wait for the probe and offset loads
-  const uint32_t i = blockIdx.x * 256u + threadIdx.x;
-  const uint32_t n = (uint32_t)nvq * (uint32_t)d4;
-  if (i < n) {
-    const uint32_t v = i / (uint32_t)d4, c = i - v * (uint32_t)d4;
-    vq[i] = q[(size_t)(v / (uint32_t)p1) * d4 + c];
-  }
-  if (i < (uint32_t)nvq) {
-    const uint32_t qq = i / (uint32_t)p1, p = i - qq * (uint32_t)p1;
-    const uint32_t l = probes[(size_t)qq * P + p];
-    const bool use = l < (uint32_t)nlist && offsets[l + 1] > offsets[l];
-    vprobe[i] = use ? l : 0xFFFFFFFFu;
-    vpd[i] = 0.0f;
-    if (use) atomicAdd(&hist[l], 1);
-  }
+                                                         uint32_t* __restrict__ vprobe, float* __restrict__ vpd,
+                                                         int* __restrict__ hist) {
+  const int i = (int)blockIdx.x * 256 + (int)threadIdx.x;
+  if (i >= nvq) return;
+  const int qq = i / p1, p = i - qq * p1;
+  const uint32_t l = probes[(size_t)qq * P + p];
+  const bool use = l < (uint32_t)nlist && offsets[l + 1] > offsets[l];
+  vprobe[i] = use ? l : 0xFFFFFFFFu;
+  vpd[i] = 0.0f;
+  if (use) atomicAdd(&hist[l], 1);
 }
 
 // The virtual queries grouped by list: list l's take order[boff[l] ..
@@ -1343,19 +1334,17 @@ fgpu_status launch_two_phase(int dim, int m, const TwoPhaseArgs& a, hipStream_t 
   return set_error(FGPU_ERR_UNSUPPORTED, "two_phase: unsupported (dim, pq_m)");
 }
 
-fgpu_status launch_tp_virtual(const float* queries, int dim, const uint32_t* probes, int nprobe, int p1, int nqc,
-                              const int32_t* offsets, int nlist, float* vq, uint32_t* vprobe, float* vpd, int* hist,
-                              hipStream_t s) {
-  FGPU_CHECK(dim % 4 == 0 && p1 >= 1 && nlist >= 1 && nlist <= 8192, FGPU_ERR_ARG, "two_phase: bad virtual queries");
+fgpu_status launch_tp_virtual(const uint32_t* probes, int nprobe, int p1, int nqc, const int32_t* offsets, int nlist,
+                              uint32_t* vprobe, float* vpd, int* hist, hipStream_t s) {
+  FGPU_CHECK(p1 >= 1 && nlist >= 1 && nlist <= 8192 && (int64_t)nqc * p1 < INT32_MAX, FGPU_ERR_ARG,
+             "two_phase: bad virtual queries");
   if (nqc <= 0) return FGPU_OK;
   // hist, then the fill counts of launch_tp_order (2 nlist + 1 ints)
   hipLaunchKernelGGL(tp_zero_kernel, dim3((unsigned)((2 * nlist + 1 + 255) / 256)), dim3(256), 0, s, hist,
                      2 * nlist + 1);
-  const int64_t nvq = (int64_t)nqc * p1, nt = nvq * (dim / 4);
-  FGPU_CHECK(dim >= 4 && nt < (int64_t(1) << 31), FGPU_ERR_ARG, "two_phase: too many virtual query values");
-  hipLaunchKernelGGL(tp_virtual_kernel, dim3((unsigned)((nt + 255) / 256)), dim3(256), 0, s,
-                     reinterpret_cast<const float4*>(queries), dim / 4, probes, nprobe, p1, (int)nvq, offsets, nlist,
-                     reinterpret_cast<float4*>(vq), vprobe, vpd, hist);
+  const int nvq = nqc * p1;
+  hipLaunchKernelGGL(tp_virtual_kernel, dim3((unsigned)((nvq + 255) / 256)), dim3(256), 0, s, probes, nprobe, p1, nvq,
+                     offsets, nlist, vprobe, vpd, hist);
   FGPU_HIP(hipGetLastError());
   return FGPU_OK;
 }
