@@ -244,7 +244,8 @@ struct TpScreenWs {
   float* vpd = nullptr;
   int32_t* vids = nullptr;
   float* vd = nullptr;
-  int* hist = nullptr;  // [2 nlist + 1]: list counts, then launch_tp_order's fill counts
+  int* hist = nullptr;  // [2 nlist + 1]: list counts, nlist unused, the count of those without a list
+  int32_t* rank = nullptr;  // [nvq] each virtual query's rank in its list
   int32_t* boff = nullptr;
   int32_t* order = nullptr;   // the virtual queries by list: the rescore's order and the screen's buckets
   int32_t* sp_cnt = nullptr;  // [nlist] the screen's single-probe counts
@@ -258,6 +259,7 @@ struct TpScreenWs {
     vids = cv.take<int32_t>((size_t)nvq * k);
     vd = cv.take<float>((size_t)nvq * k);
     hist = cv.take<int>(2 * (size_t)nlist + 1);
+    rank = cv.take<int32_t>((size_t)nvq);
     boff = cv.take<int32_t>((size_t)nlist + 1);
     order = cv.take<int32_t>((size_t)nvq);
     sp_cnt = cv.take<int32_t>((size_t)nlist);
@@ -268,7 +270,7 @@ struct TpScreenWs {
     (void)dim;
     return carve_bytes<uint32_t>((size_t)nvq) +
            carve_bytes<float>((size_t)nvq) + carve_bytes<int32_t>((size_t)nvq * k) +
-           carve_bytes<float>((size_t)nvq * k) + carve_bytes<int>(2 * (size_t)nlist + 1) +
+           carve_bytes<float>((size_t)nvq * k) + carve_bytes<int>(2 * (size_t)nlist + 1) + carve_bytes<int32_t>((size_t)nvq) +
            carve_bytes<int32_t>((size_t)nlist + 1) + carve_bytes<int32_t>((size_t)nvq) +
            carve_bytes<int32_t>((size_t)nlist) + carve_bytes<float2>((size_t)nvq) + ScreenWs::bytes(nvq, nlist, 1, true);
   }
@@ -856,9 +858,9 @@ fgpu_status two_phase(const fgpu_index* ix, const float* dq, int nq, const uint3
             FGPU_HIP(mark(0));
             const float* cq = qq + (int64_t)s0 * ix->dim;  // the chunk's query rows
             FGPU_TRY(launch_tp_virtual(pp + (int64_t)s0 * nprobe, nprobe, p1, ns, ix->d_offsets, ix->nlist, tw.vprobe,
-                                       tw.vpd, tw.hist, s));
+                                       tw.vpd, tw.hist, tw.rank, s));
             FGPU_TRY(launch_tp_offsets(tw.hist, ix->nlist, tw.boff, ix->d_offsets, limit_k, tw.sp_cnt, s));
-            FGPU_TRY(launch_tp_order(tw.vprobe, nvq, ix->nlist, tw.boff, tw.hist + ix->nlist, tw.order, s));
+            FGPU_TRY(launch_tp_order(tw.vprobe, tw.rank, nvq, ix->nlist, tw.boff, tw.order, s));
             FGPU_HIP(mark(1));
             ScreenArgs sa{cq, ix->d_centroids, ix->d_offsets, ix->d_codes, ix->d_ids, ix->d_codebook, ix->d_cb16,
                           ix->d_vext, ix->d_rmax, tw.vprobe, tw.vpd, nvq, 1, limit_k, ix->nlist};

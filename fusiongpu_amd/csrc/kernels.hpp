@@ -256,15 +256,14 @@ int two_phase_pool_cap(int p1, int limit_k, int rerank_m);
 // others' pool slots and cutoffs to launch_two_phase_after_phase1, which
 // runs the threshold, phase 2 and the final select (limit_k <= 64).
 fgpu_status launch_tp_virtual(const uint32_t* probes, int nprobe, int p1, int nqc, const int32_t* offsets, int nlist,
-                              uint32_t* vprobe, float* vpd, int* hist, hipStream_t s);
+                              uint32_t* vprobe, float* vpd, int* hist, int32_t* rank, hipStream_t s);
 fgpu_status launch_tp_offsets(const int* hist, int nlist, int32_t* boff, const int32_t* offsets, int k,
                               int32_t* sp_cnt, hipStream_t s);
 fgpu_status launch_two_phase_after_phase1(int dim, int m, const TwoPhaseArgs& a, hipStream_t s);
 // order[0 .. nvq): the virtual queries grouped by list (list l's at
 // boff[l] .. boff[l + 1), in no fixed order within it), those without a
-// usable list last; fill: 2 nlist + 1 ints of which the last nlist + 1 are
-// zero (launch_tp_virtual zeroes them).
-fgpu_status launch_tp_order(const uint32_t* vprobe, int nvq, int nlist, const int32_t* boff, int* fill,
+// usable list last, each at its rank from launch_tp_virtual.
+fgpu_status launch_tp_order(const uint32_t* vprobe, const int32_t* rank, int nvq, int nlist, const int32_t* boff,
                             int32_t* order, hipStream_t s);
 // The second half of the two-phase scan for queries q_base .. q_base + nqc - 1
 // of a (phase 1 done by the screen: virtual query (q - q_base) p1 + p holds

@@ -926,11 +926,13 @@ __global__ __launch_bounds__(256) void tp_zero_kernel(int* __restrict__ p, int n
 // v / p1, from the chunk's rows): its probe p (0xFFFFFFFF when out of range or
 // empty), a zero
 // probe distance (the lower bound of its only list is then 0, so the list is
-// always screened), and its list's count in hist.
+// always screened), its list's count in hist and its rank among the list's
+// virtual queries (the order of the list's atomics; those without a list
+// ranked by hist[2 nlist]).
 __global__ __launch_bounds__(256) void tp_virtual_kernel(const uint32_t* __restrict__ probes, int P, int p1, int nvq,
                                                          const int32_t* __restrict__ offsets, int nlist,
                                                          uint32_t* __restrict__ vprobe, float* __restrict__ vpd,
-                                                         int* __restrict__ hist) {
+                                                         int* __restrict__ hist, int32_t* __restrict__ rank) {
   const int i = (int)blockIdx.x * 256 + (int)threadIdx.x;
   if (i >= nvq) return;
   const int qq = i / p1, p = i - qq * p1;
@@ -938,30 +940,27 @@ __global__ __launch_bounds__(256) void tp_virtual_kernel(const uint32_t* __restr
   const bool use = l < (uint32_t)nlist && offsets[l + 1] > offsets[l];
   vprobe[i] = use ? l : 0xFFFFFFFFu;
   vpd[i] = 0.0f;
-  if (use) atomicAdd(&hist[l], 1);
+  // the queries without a list share one count (hist[2 nlist]): one atomic a wave
+  const uint64_t bm = __ballot(!use);
+  int base = 0;
+  if (bm) {
+    const int lead = __builtin_ctzll(bm);
+    if ((int)(threadIdx.x & 63) == lead) base = atomicAdd(&hist[2 * nlist], __popcll(bm));
+    base = __shfl(base, lead, kWave);
+  }
+  rank[i] = use ? atomicAdd(&hist[l], 1) : base + __popcll(bm & ((1ull << (threadIdx.x & 63)) - 1ull));
 }
 
 // The virtual queries grouped by list: list l's take order[boff[l] ..
-// boff[l + 1]) through its fill count, those without a usable list the slots
+// boff[l + 1]) by their rank in it, those without a usable list the slots
 // from boff[nlist] on.
-__global__ __launch_bounds__(256) void tp_order_kernel(const uint32_t* __restrict__ vprobe, int nvq, int nlist,
-                                                       const int32_t* __restrict__ boff, int* __restrict__ fill,
-                                                       int32_t* __restrict__ order) {
+__global__ __launch_bounds__(256) void tp_order_kernel(const uint32_t* __restrict__ vprobe,
+                                                       const int32_t* __restrict__ rank, int nvq, int nlist,
+                                                       const int32_t* __restrict__ boff, int32_t* __restrict__ order) {
   const int v = (int)blockIdx.x * 256 + (int)threadIdx.x;
-  const uint32_t l = v < nvq ? vprobe[v] : 0u;
-  const bool none = v < nvq && l >= (uint32_t)nlist;
-  // the queries without a list share one count: one atomic a wave for them
-  const uint64_t bm = __ballot(none);
-  int base = 0;
-  if (bm) {
-    if ((threadIdx.x & 63) == (unsigned)__builtin_ctzll(bm)) base = atomicAdd(&fill[nlist], __popcll(bm));
-    base = __shfl(base, __builtin_ctzll(bm), kWave);
-  }
   if (v >= nvq) return;
-  if (none)
-    order[boff[nlist] + base + __popcll(bm & ((1ull << (threadIdx.x & 63)) - 1ull))] = v;
-  else
-    order[boff[l] + atomicAdd(&fill[l], 1)] = v;
+  const uint32_t l = vprobe[v];
+  order[boff[l < (uint32_t)nlist ? l : (uint32_t)nlist] + rank[v]] = v;
 }
 
 // boff[l] = hist[0] + ... + hist[l - 1] for l = 0 .. nlist (one workgroup,
@@ -1335,16 +1334,16 @@ fgpu_status launch_two_phase(int dim, int m, const TwoPhaseArgs& a, hipStream_t 
 }
 
 fgpu_status launch_tp_virtual(const uint32_t* probes, int nprobe, int p1, int nqc, const int32_t* offsets, int nlist,
-                              uint32_t* vprobe, float* vpd, int* hist, hipStream_t s) {
+                              uint32_t* vprobe, float* vpd, int* hist, int32_t* rank, hipStream_t s) {
   FGPU_CHECK(p1 >= 1 && nlist >= 1 && nlist <= 8192 && (int64_t)nqc * p1 < INT32_MAX, FGPU_ERR_ARG,
              "two_phase: bad virtual queries");
   if (nqc <= 0) return FGPU_OK;
-  // hist, then the fill counts of launch_tp_order (2 nlist + 1 ints)
+  // hist: the list counts, nlist unused ints, the count of those without a list
   hipLaunchKernelGGL(tp_zero_kernel, dim3((unsigned)((2 * nlist + 1 + 255) / 256)), dim3(256), 0, s, hist,
                      2 * nlist + 1);
   const int nvq = nqc * p1;
   hipLaunchKernelGGL(tp_virtual_kernel, dim3((unsigned)((nvq + 255) / 256)), dim3(256), 0, s, probes, nprobe, p1, nvq,
-                     offsets, nlist, vprobe, vpd, hist);
+                     offsets, nlist, vprobe, vpd, hist, rank);
   FGPU_HIP(hipGetLastError());
   return FGPU_OK;
 }
@@ -1375,11 +1374,11 @@ fgpu_status launch_tp_zero(int* p, int n, hipStream_t s) {
   return FGPU_OK;
 }
 
-fgpu_status launch_tp_order(const uint32_t* vprobe, int nvq, int nlist, const int32_t* boff, int* fill,
+fgpu_status launch_tp_order(const uint32_t* vprobe, const int32_t* rank, int nvq, int nlist, const int32_t* boff,
                             int32_t* order, hipStream_t s) {
   if (nvq <= 0) return FGPU_OK;
-  hipLaunchKernelGGL(tp_order_kernel, dim3((unsigned)((nvq + 255) / 256)), dim3(256), 0, s, vprobe, nvq, nlist, boff,
-                     fill, order);
+  hipLaunchKernelGGL(tp_order_kernel, dim3((unsigned)((nvq + 255) / 256)), dim3(256), 0, s, vprobe, rank, nvq, nlist,
+                     boff, order);
   FGPU_HIP(hipGetLastError());
   return FGPU_OK;
 }
